@@ -1,0 +1,104 @@
+/* C ABI of libtace_hip.so -- MI355X (gfx950) kernels of the TACE/TECE
+ * energy-and-force path.
+ *
+ * Conventions
+ *   - Every pointer argument except `cell`/`pbc` (host arrays) is a device
+ *     pointer allocated by the caller (PyTorch on ROCm); the library never
+ *     allocates device memory and never holds a pointer after returning.
+ *   - `stream` is a hipStream_t; launches are asynchronous on it, nothing
+ *     synchronises the host.
+ *   - Return value: 0 on success, < 0 on error; tace_last_error() returns a
+ *     thread-local message for the last failure.
+ *   - dtype: TACE_F32 or TACE_F64; all float arrays of one call share it.
+ *   - Node features use e3nn's mul_ir layout: irrep blocks concatenated,
+ *     each block [channels, 2l+1] row-major.
+ *
+ * Reference interfaces replaced (xvzemin/tace, paths relative to its root):
+ *   tace_edge_tp_fwd / _bwd   O3ScatterTensorProduct.forward(x, y, w, edge_index)
+ *                             tace/models/_e3nn/fused.py:259-271 (the `fused_tp`
+ *                             plug-in slot filled at fused.py:218-257; same
+ *                             contract as oeq/_tp_scatter.py:53-93)
+ *   tace_uuu_fwd / _bwd       uuuTensorProduct.forward(x, y)  fused.py:90-95
+ *                             (plug-in slot fused.py:61-71)
+ *   tace_edge_basis_fwd/_bwd  RadialBasis.forward (radial.py:974-993: j0 Bessel
+ *                             43-84 x C2PolynomialCutoff 437-472) and
+ *                             SphericalHarmonics.forward (angular.py:288-315)
+ *                             as called at representation.py:305-324
+ *   tace_nl_*                 get_neighborhood (dataset/neighbour_list.py:195-298)
+ */
+#ifndef TACE_HIP_H
+#define TACE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TACE_HIP_ABI_VERSION 1
+#define TACE_F32 0
+#define TACE_F64 1
+
+const char* tace_last_error(void);
+int tace_abi_version(void);
+
+/* ---- tensor-product variants -------------------------------------------
+ * A variant is keyed by "kind|in1 ls|in2 ls|out ls", e.g.
+ * "uvu|0,1,2,3|0,1,2,3|0,1,2,3"; paths follow generate_paths
+ * (tace/models/_e3nn/paths.py:30-71).  d1/d2/dout are per-channel widths. */
+int tace_tp_num_variants(void);
+const char* tace_tp_variant_key(int vid);
+int tace_tp_find(const char* key);
+int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dout);
+
+/* out[n] = sum_{e: dst(e)=n} TP(x[src(e)], y[e], w[e])  -- uvu, mul2 = 1.
+ * Edges are visited in receiver-CSR order: rowptr[n_nodes+1] over the sorted
+ * edge list, eid[k] the edge id of sorted slot k (NULL = identity), src[e] the
+ * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout]. */
+int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
+                     const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                     void* out, void* stream);
+/* Gradients of sum(gout * out): gx [N, C*d1] (NULL to skip; zeroed then
+ * accumulated), gy [E, d2], gw [E, C*npath] (both fully overwritten). */
+int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
+                     int32_t channels, void* gx, void* gy, void* gw, void* stream);
+
+/* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout]. */
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels, void* out,
+                 void* stream);
+int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
+                 int32_t channels, void* g1, void* g2, void* stream);
+
+/* ---- edge featurisation --------------------------------------------------
+ * vec [E, 3] edge vectors; r = |vec| + 1e-9;
+ * radial[E, nb] = prefactor * sin(bessel_w[n] r) / r * f(r/cutoff) * [r < cutoff]
+ * sh[E, (lmax+1)^2] = component-normalised real SH of vec / r (e3nn order). */
+int tace_edge_basis_fwd(int dtype, const void* vec, int64_t n_edges, int32_t num_basis, const void* bessel_w,
+                        double prefactor, double cutoff, int32_t poly_p, int32_t lmax, void* radial, void* sh,
+                        void* stream);
+int tace_edge_basis_bwd(int dtype, const void* vec, const void* g_radial, const void* g_sh, int64_t n_edges,
+                        int32_t num_basis, const void* bessel_w, double prefactor, double cutoff, int32_t poly_p,
+                        int32_t lmax, void* g_vec, void* stream);
+
+/* ---- neighbour list (float64 positions, host cell[9] rows = lattice
+ * vectors, host pbc[3]).  Edge (src=i, dst=j, S) exists iff
+ * |r_j - r_i + S.cell|^2 < cutoff^2 and (i, S) != (j, 0); S = 0 on
+ * non-periodic axes.  Output is grouped by receiver j (CSR):
+ *   1. tace_nl_workspace_bytes -> allocate workspace
+ *   2. tace_nl_count  -> counts[n] (edges per receiver)
+ *   3. tace_scan_i32(counts) -> rowptr[n+1]; E = rowptr[n]
+ *   4. tace_nl_fill   -> src[E] (int32), shifts[E,3] (int32) in rowptr order. */
+int64_t tace_nl_workspace_bytes(int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff);
+int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
+                  void* workspace, int64_t workspace_bytes, int32_t* counts, void* stream);
+int tace_nl_fill(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
+                 const void* workspace, const int32_t* rowptr, int32_t* src, int32_t* shifts, void* stream);
+/* exclusive prefix sum: out[0] = 0, out[i+1] = out[i] + counts[i], i < n */
+int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TACE_HIP_H */

@@ -1,0 +1,554 @@
+"""CPU restatement of ``TensorModel(e3nnTACE(**cfg))`` (test infrastructure).
+
+Scope: the configurations of the MI355X build -- linear node embedding,
+identity edge embedding/update, ``cgtp`` atomic basis with ``sigmoid_gate``,
+``cgtp`` product basis (CgtpACE, correlation <= 3), BB element-aware resnet,
+scalar energy readout, ``rms_forces`` scale, one fidelity.  Module and
+parameter names equal the reference's so one ``state_dict`` drives both this
+oracle and the HIP model.
+
+Memory-bounded restatements (mathematically identical to the reference):
+* ``ElementLinear`` applies the per-species weight to each species group
+  instead of gathering a weight row per node (``tace/models/linear.py:470-473``).
+* ``ScatterTP`` evaluates the uvu tensor product + scatter in edge chunks
+  instead of materialising [E, d_out] (``tace/models/_e3nn/fused.py:269-271``).
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+from typing import Dict, List, Optional
+
+import torch
+
+from . import so3
+
+SILU_CST = None  # filled lazily by normalize2mom
+
+
+# ----------------------------------------------------------- activations ----
+_NORM2MOM = {}
+
+
+def normalize2mom_cst(name: str) -> float:
+    """e3nn ``normalize2mom``: c = E[f(z)^2]^(-1/2), z ~ N(0,1), 1e6 float64
+    samples from ``Generator.manual_seed(0)``; c := 1 if |c-1| < 1e-4.
+    (``tace/models/mlp.py:15-27``, pinned to e3nn by ``tests/test_o2.py:360-377``)."""
+    if name not in _NORM2MOM:
+        f = {"silu": torch.nn.functional.silu, "sigmoid": torch.sigmoid, "tanh": torch.tanh}[name]
+        g = torch.Generator(device="cpu").manual_seed(0)
+        z = torch.randn(1_000_000, generator=g, dtype=torch.float64)
+        c = f(z).square().mean().rsqrt().item()
+        _NORM2MOM[name] = 1.0 if abs(c - 1.0) < 1e-4 else c
+    return _NORM2MOM[name]
+
+
+def act(name: str, x: torch.Tensor) -> torch.Tensor:
+    f = {"silu": torch.nn.functional.silu, "sigmoid": torch.sigmoid, "tanh": torch.tanh}[name]
+    return f(x).mul(normalize2mom_cst(name))
+
+
+# --------------------------------------------------------------- linears ----
+class _LinearBase(torch.nn.Module):
+    """Shared bookkeeping of e3nn ``o3.Linear`` (instructions (i_in, i_out) with
+    equal irreps, ordered i_in-major; path weight 1/sqrt(sum mul_in into i_out);
+    flat weight = concatenation of row-major [mul_in, mul_out] blocks) plus the
+    reference's 0e-only bias (``tace/models/linear.py:282-374``)."""
+
+    def _setup(self, irreps_in, irreps_out):
+        self.irreps_in = so3.parse_irreps(irreps_in)
+        self.irreps_out = so3.parse_irreps(irreps_out)
+        ins = [(i, o) for i, (_, a) in enumerate(self.irreps_in)
+               for o, (_, b) in enumerate(self.irreps_out) if a == b]
+        fan = {}
+        for i, o in ins:
+            fan[o] = fan.get(o, 0) + self.irreps_in[i][0]
+        self.ins = []
+        off = 0
+        for i, o in ins:
+            mi, mo = self.irreps_in[i][0], self.irreps_out[o][0]
+            self.ins.append((i, o, off, mi, mo, fan[o] ** -0.5))
+            off += mi * mo
+        self.weight_numel = off
+        self.in_slices, acc = [], 0
+        for m, ir in self.irreps_in:
+            self.in_slices.append((acc, m, 2 * ir[0] + 1))
+            acc += m * (2 * ir[0] + 1)
+        self.out_slices, acc = [], 0
+        self.bias_slices, bacc = [], 0
+        for m, ir in self.irreps_out:
+            d = m * (2 * ir[0] + 1)
+            self.out_slices.append((acc, m, 2 * ir[0] + 1))
+            if ir == (0, 1):
+                self.bias_slices.append((acc, bacc, d))
+                bacc += d
+            acc += d
+        self.out_dim = acc
+        self.bias_numel = bacc
+
+    def _lin(self, x, w):
+        """x [Z, dim_in]; w [numel] -> [Z, dim_out]."""
+        outs = [None] * len(self.irreps_out)
+        for i, o, off, mi, mo, pw in self.ins:
+            s, m, d = self.in_slices[i]
+            xi = x[:, s:s + m * d].reshape(-1, m, d)
+            W = w[off:off + mi * mo].reshape(mi, mo)
+            y = pw * torch.einsum("zui,uw->zwi", xi, W)
+            outs[o] = y if outs[o] is None else outs[o] + y
+        cols = []
+        for o, (s, m, d) in enumerate(self.out_slices):
+            cols.append(outs[o].reshape(x.shape[0], m * d) if outs[o] is not None
+                        else x.new_zeros(x.shape[0], m * d))
+        return torch.cat(cols, dim=-1)
+
+
+class Linear(_LinearBase):
+    """``e3nnLinear`` (``tace/models/linear.py:282-374``)."""
+
+    def __init__(self, irreps_in, irreps_out, bias: bool = True):
+        super().__init__()
+        self._setup(irreps_in, irreps_out)
+        self.weight = torch.nn.Parameter(torch.randn(self.weight_numel))
+        if bias and self.bias_numel > 0:
+            self.bias = torch.nn.Parameter(torch.zeros(self.bias_numel))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x):
+        out = self._lin(x, self.weight)
+        if self.bias is not None:
+            add = torch.zeros_like(out)
+            for s, bs, d in self.bias_slices:
+                add[:, s:s + d] = self.bias[bs:bs + d]
+            out = out + add
+        return out
+
+
+class ElementLinear(_LinearBase):
+    """``e3nnElementLinear`` (``tace/models/linear.py:377-481``): weight row
+    picked by ``attrs.argmax`` -- applied per species group here; bias via
+    ``einsum('bz,zi->bi', attrs, bias)`` on 0e slices."""
+
+    def __init__(self, irreps_in, irreps_out, num_elements: int, bias: bool = True):
+        super().__init__()
+        self._setup(irreps_in, irreps_out)
+        self.num_elements = num_elements
+        self.weight = torch.nn.Parameter(torch.randn(num_elements, self.weight_numel))
+        if bias and self.bias_numel > 0:
+            self.bias = torch.nn.Parameter(torch.zeros(num_elements, self.bias_numel))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x, attrs):
+        species = attrs.argmax(dim=-1)
+        out = x.new_zeros(x.shape[0], self.out_dim)
+        for s in torch.unique(species).tolist():
+            idx = (species == s).nonzero().squeeze(1)
+            out = out.index_copy(0, idx, self._lin(x.index_select(0, idx), self.weight[s]))
+        if self.bias is not None:
+            b = torch.einsum("bz,zi->bi", attrs, self.bias)
+            add = torch.zeros_like(out)
+            for s, bs, d in self.bias_slices:
+                add[:, s:s + d] = b[:, bs:bs + d]
+            out = out + add
+        return out
+
+
+class MLPLinear(torch.nn.Module):
+    """``mlpLinear`` (``tace/models/linear.py:247-279``): x @ (W * alpha)."""
+
+    def __init__(self, i, o, alpha):
+        super().__init__()
+        self.alpha = alpha
+        self.weight = torch.nn.Parameter(torch.empty(i, o).uniform_(-math.sqrt(3), math.sqrt(3)))
+
+    def forward(self, x):
+        return torch.mm(x, self.weight * self.alpha)
+
+
+class MLP(torch.nn.Module):
+    """Radial ``MLP`` (``tace/models/mlp.py:136-191``): forward init
+    alpha = gain/sqrt(h_in), gain 1 on layer 0 else sqrt(2); plain SiLU."""
+
+    def __init__(self, dims):
+        super().__init__()
+        mods = []
+        n = len(dims) - 1
+        for layer, (a, b) in enumerate(zip(dims, dims[1:])):
+            gain = 1.0 if layer == 0 else math.sqrt(2.0)
+            mods.append(MLPLinear(a, b, gain / math.sqrt(a)))
+            if layer != n - 1:
+                mods.append(torch.nn.SiLU())
+        self.mlp = torch.nn.Sequential(*mods)
+
+    def forward(self, x):
+        return self.mlp(x)
+
+
+# --------------------------------------------------------- tensor products ----
+class ScatterTP(torch.nn.Module):
+    """``O3ScatterTensorProduct`` non-fused branch (``tace/models/_e3nn/fused.py:
+    172-271``): out = scatter_sum(tp(x[src], y, w), dst) with e3nn uvu
+    semantics -- path p contributes sqrt(2 l3 + 1) w[e,p,u] sum_ij x[u,i] y[j]
+    W3j_ijk into its own output block (mul2 = 1, element normalisation)."""
+
+    def __init__(self, irreps_in1, irreps_in2, irreps_out, chunk: int = 4096):
+        super().__init__()
+        self.in1 = so3.parse_irreps(irreps_in1)
+        self.in2 = so3.parse_irreps(irreps_in2)
+        self.paths, self.out = so3.generate_paths(so3.parse_irreps(irreps_out), self.in1, self.in2, "uvu")
+        self.weight_numel = sum(self.in1[i][0] * self.in2[j][0] for i, j, _ in self.paths)
+        self.irreps_out = self.out
+        self.chunk = chunk
+
+    def _tp(self, x1, x2, w):
+        s1 = _offsets(self.in1)
+        s2 = _offsets(self.in2)
+        outs = []
+        woff = 0
+        for i, j, k in self.paths:
+            m1, (l1, _) = self.in1[i]
+            m2, (l2, _) = self.in2[j]
+            l3 = self.out[k][1][0]
+            a = x1[:, s1[i]:s1[i] + m1 * (2 * l1 + 1)].reshape(-1, m1, 2 * l1 + 1)
+            b = x2[:, s2[j]:s2[j] + m2 * (2 * l2 + 1)].reshape(-1, m2, 2 * l2 + 1)
+            assert m2 == 1
+            C = so3.w3j_torch(l1, l2, l3, x1.dtype) * math.sqrt(2 * l3 + 1)
+            ww = w[:, woff:woff + m1].reshape(-1, m1, 1)
+            woff += m1
+            # M_e[i, k] = sum_j y[e, j] C_ijk ; t[e, u, k] = w[e, u] sum_i x[e, u, i] M_e[i, k]
+            M = (b[:, 0, :] @ C.permute(1, 0, 2).reshape(2 * l2 + 1, -1)).reshape(-1, 2 * l1 + 1, 2 * l3 + 1)
+            t = torch.bmm(a, M) * ww
+            outs.append(t.reshape(x1.shape[0], -1))
+        return torch.cat(outs, dim=-1)
+
+    def forward(self, x, y, w, edge_index):
+        src, dst = edge_index[0], edge_index[1]
+        out = x.new_zeros(x.shape[0], so3.irreps_dim(self.out))
+        for s in range(0, src.shape[0], self.chunk):
+            sl = slice(s, s + self.chunk)
+            out = out.index_add(0, dst[sl], self._tp(x[src[sl]], y[sl], w[sl]))
+        return out
+
+
+class UUUTP(torch.nn.Module):
+    """``uuuTensorProduct`` (``tace/models/_e3nn/fused.py:17-95``), e3nn uuu
+    without weights: path p -> sqrt(2 l3 + 1) sum_ij x1[u,i] x2[u,j] W3j_ijk."""
+
+    def __init__(self, in1, in2, irreps_out, identical_inputs: bool):
+        super().__init__()
+        self.in1, self.in2 = so3.parse_irreps(in1), so3.parse_irreps(in2)
+        self.paths, self.out = so3.generate_paths(so3.parse_irreps(irreps_out), self.in1, self.in2,
+                                                  "uuu", identical_inputs)
+        self.irreps_out = self.out
+
+    def forward(self, x1, x2):
+        s1, s2 = _offsets(self.in1), _offsets(self.in2)
+        outs = []
+        for i, j, k in self.paths:
+            m1, (l1, _) = self.in1[i]
+            m2, (l2, _) = self.in2[j]
+            assert m1 == m2
+            l3 = self.out[k][1][0]
+            a = x1[:, s1[i]:s1[i] + m1 * (2 * l1 + 1)].reshape(-1, m1, 2 * l1 + 1)
+            b = x2[:, s2[j]:s2[j] + m2 * (2 * l2 + 1)].reshape(-1, m2, 2 * l2 + 1)
+            C = so3.w3j_torch(l1, l2, l3, x1.dtype) * math.sqrt(2 * l3 + 1)
+            ab = (a.unsqueeze(-1) * b.unsqueeze(-2)).reshape(-1, (2 * l1 + 1) * (2 * l2 + 1))
+            outs.append((ab @ C.reshape(-1, 2 * l3 + 1)).reshape(x1.shape[0], -1))
+        return torch.cat(outs, dim=-1)
+
+
+def _offsets(irreps):
+    out, acc = [], 0
+    for m, ir in irreps:
+        out.append(acc)
+        acc += m * (2 * ir[0] + 1)
+    return out
+
+
+class Gate(torch.nn.Module):
+    """``O3Gate`` with gate_m0 (``tace/models/_e3nn/nonlinear.py:27-42, 93-143``):
+    input = [gates (one C-block of 0e per gated irrep) | gated irreps]; the gates
+    go through normalize2mom(sigmoid); e3nn's ElementwiseTensorProduct multiplies
+    gated[l] by its gate with coefficient sqrt(2l+1) W3j(l,0,l)."""
+
+    def __init__(self, gated_irreps):
+        super().__init__()
+        self.gated = gated_irreps  # [(mul, (l, p)), ...]
+        self.ngate = sum(m for m, _ in gated_irreps)
+
+    def forward(self, x):
+        g = act("sigmoid", x[:, :self.ngate])
+        outs, go, xo = [], 0, self.ngate
+        for m, (l, _) in self.gated:
+            d = 2 * l + 1
+            xi = x[:, xo:xo + m * d].reshape(-1, m, d)
+            gi = g[:, go:go + m].reshape(-1, m, 1)
+            C = so3.w3j_torch(l, 0, l, x.dtype)[:, 0, :] * math.sqrt(d)
+            outs.append(torch.einsum("zui,zuj,ik->zuk", xi, gi, C).reshape(x.shape[0], -1))
+            go += m
+            xo += m * d
+        return torch.cat(outs, dim=-1)
+
+
+# ------------------------------------------------------------------ blocks ----
+class RadialBasis(torch.nn.Module):
+    """``RadialBasis`` with j0 Bessel x C2 polynomial cutoff, apply_cutoff=True
+    (``tace/models/radial.py:43-84, 437-472, 877-993``)."""
+
+    def __init__(self, cutoff: float, num_basis: int, p: int):
+        super().__init__()
+        self.radial_fn = torch.nn.Module()
+        self.radial_fn.register_buffer(
+            "bessel_weights", math.pi / cutoff * torch.linspace(1.0, num_basis, num_basis))
+        self.radial_fn.register_buffer("cutoff", torch.tensor(cutoff))
+        self.radial_fn.register_buffer("prefactor", torch.tensor(math.sqrt(2.0 / cutoff)))
+        self.cutoff_fn = torch.nn.Module()
+        self.cutoff_fn.register_buffer("p", torch.tensor(p, dtype=torch.int))
+        self.cutoff_fn.register_buffer("cutoff", torch.tensor(cutoff))
+
+    def forward(self, r):
+        rf = self.radial_fn
+        radial = rf.prefactor * (torch.sin(rf.bessel_weights * r) / r)
+        p = self.cutoff_fn.p.to(torch.int)
+        x = r / self.cutoff_fn.cutoff
+        env = (1.0 - ((p + 1.0) * (p + 2.0) / 2.0) * torch.pow(x, p)
+               + p * (p + 2.0) * torch.pow(x, p + 1)
+               - (p * (p + 1.0) / 2) * torch.pow(x, p + 2))
+        env = env * (r < self.cutoff_fn.cutoff)
+        return radial * env
+
+
+class Interaction(torch.nn.Module):
+    """``O3CgtpInteraction`` (``tace/models/_e3nn/inter.py:28-285``), BB resnet."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements,
+                 avg_num_neighbors, radial_hidden, num_radial):
+        super().__init__()
+        self.layer = layer
+        self.avg = avg_num_neighbors
+        sh = so3.sh_irreps(lmax)
+        lm = Lmax if correlation == 1 else lmax
+        tp_out = so3.possible_tp_irreps(irreps_in, sh, False, lm)
+        self.irreps_out = so3.regroup(so3.times(tp_out, C))
+        if layer == num_layers - 1:
+            irreps_sc = so3.regroup(so3.times([(1, (0, 1))], C))
+        else:
+            irreps_sc = so3.regroup(so3.times(so3.possible_tp_irreps(irreps_in, sh, False, Lmax), C))
+        self.linear_up = Linear(irreps_in, irreps_in, bias=True)
+        self.rejector = ScatterTP(irreps_in, sh, self.irreps_out)
+        gated = [(C, ir) for _, ir in self.irreps_out]  # node_wise_hidden = C
+        gates = [(C, (0, 1)) for _ in gated]
+        self.nonlinearity = Gate(gated)
+        down_out = so3.simplify(gates + gated)
+        self.linear_nonlinearity = Linear(gated, self.irreps_out, bias=True)
+        self.linear_down = Linear(so3.simplify(self.rejector.irreps_out), down_out, bias=True)
+        self.edge_info = MLP([num_radial] + list(radial_hidden) + [self.rejector.weight_numel])
+        if layer > 0:
+            self.resnetBB = ElementLinear(irreps_in, irreps_sc, num_elements, bias=True)
+
+    def forward(self, x, attrs, edge_feats, edge_attrs, edge_index):
+        sc = self.resnetBB(x, attrs) if hasattr(self, "resnetBB") else None
+        x = self.linear_up(x)
+        w = self.edge_info(edge_feats)
+        m = self.linear_down(self.rejector(x, edge_attrs, w, edge_index))
+        m = m / self.avg
+        m = self.linear_nonlinearity(self.nonlinearity(m))
+        return m, sc
+
+
+class Product(torch.nn.Module):
+    """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``), element-aware coefs,
+    one expert, no bilinear gate."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements,
+                 agnostic: bool = False):
+        super().__init__()
+        last = layer == num_layers - 1
+        self.agnostic = agnostic
+        self.correlation = correlation
+        hidden = [(C, ir) for _, ir in irreps_in]
+        tp_out_list = []
+        for nu in range(2, correlation + 1):
+            if nu == correlation:
+                tp_out_list.append(so3.regroup(so3.times([(1, (0, 1))], C)) if last else
+                                   so3.regroup(so3.times(so3.possible_tp_irreps(hidden, hidden, False, Lmax), C)))
+            else:
+                tp_out_list.append(so3.possible_tp_irreps(hidden, hidden, False, lmax))
+        if correlation == 1:
+            coefs_out = [(C, ir) for _, ir in irreps_in if ir[0] <= Lmax]
+        else:
+            coefs_out = so3.regroup(so3.times(so3.possible_tp_irreps(irreps_in, irreps_in, False, Lmax), C))
+        if last:
+            coefs_out = so3.regroup(so3.times([(1, (0, 1))], C))
+        self.irreps_out = [(C, ir) for _, ir in coefs_out]
+
+        def mk(irr):
+            if agnostic:
+                return Linear(irr, coefs_out, bias=True)
+            return ElementLinear(irr, coefs_out, num_elements, bias=True)
+
+        self.coefs = torch.nn.ModuleList([mk(so3.simplify([(C, ir) for _, ir in hidden]))])
+        self.aces = torch.nn.ModuleList()
+        in1 = hidden
+        for nu in range(2, correlation + 1):
+            ace = UUUTP(in1, hidden, tp_out_list[nu - 2], identical_inputs=(nu == 2))
+            self.aces.append(ace)
+            self.coefs.append(mk(so3.simplify([(C, ir) for _, ir in ace.irreps_out])))
+            in1 = ace.irreps_out
+        self.linear = Linear([(C, ir) for _, ir in coefs_out], self.irreps_out, bias=True)
+
+    def forward(self, x, attrs, sc):
+        kw = (lambda f, t: f(t)) if self.agnostic else (lambda f, t: f(t, attrs))
+        outs = kw(self.coefs[0], x)
+        feats = x
+        for nu in range(2, self.correlation + 1):
+            feats = self.aces[nu - 2](feats, x)
+            outs = outs + kw(self.coefs[nu - 1], feats)
+        outs = self.linear(outs)
+        return outs + sc if sc is not None else outs
+
+
+class ScalarReadOut(torch.nn.Module):
+    """Last-layer ``ScalarReadOut`` (``tace/models/_e3nn/readout.py:36-84``)."""
+
+    def __init__(self, irreps_in, hidden=(16,)):
+        super().__init__()
+        dims = [irreps_in] + [[(h, (0, 1))] for h in hidden] + [[(1, (0, 1))]]
+        self.linear2 = torch.nn.ModuleList(Linear(a, b, bias=False) for a, b in zip(dims, dims[1:]))
+        self.nh = len(hidden)
+
+    def forward(self, x):
+        for k in range(self.nh):
+            x = act("silu", self.linear2[k](x))
+        return self.linear2[-1](x)
+
+
+class NodeEmbedding(torch.nn.Module):
+    def __init__(self, S, C):
+        super().__init__()
+        self.elem_emb1 = Linear([(S, (0, 1))], [(C, (0, 1))], bias=False)
+
+    def forward(self, attrs):
+        return self.elem_emb1(attrs)
+
+
+class Representation(torch.nn.Module):
+    """``Representation`` (``tace/models/_e3nn/representation.py:28-429``)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        S = len(cfg["atomic_numbers"])
+        C, L, Lmax = cfg["num_channel"], cfg["lmax"], cfg["Lmax"]
+        self.register_buffer("atomic_numbers", torch.tensor(cfg["atomic_numbers"], dtype=torch.int64))
+        rb = cfg["radial_basis"]
+        self.radial_basis = RadialBasis(cfg["cutoff"], rb["num_radial_basis"], rb["polynomial_cutoff"])
+        self.lmax = L
+        self.node_embedding = NodeEmbedding(S, C)
+        nl = cfg["num_layers"]
+        corr = cfg["product_basis"]["correlation"]
+        corr = corr if isinstance(corr, list) else [corr] * nl
+        self.interactions = torch.nn.ModuleList()
+        self.products = torch.nn.ModuleList()
+        irreps = [(C, (0, 1))]
+        for layer in range(nl):
+            inter = Interaction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
+                                rb["hidden"], rb["num_radial_basis"])
+            self.interactions.append(inter)
+            prod = Product(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S,
+                           cfg["product_basis"].get("agnostic", False))
+            self.products.append(prod)
+            irreps = prod.irreps_out
+
+    def forward(self, attrs, edge_index, edge_vector, edge_length):
+        R = self.radial_basis(edge_length)
+        Y = so3.spherical_harmonics(self.lmax, edge_vector / edge_length)
+        x = self.node_embedding(attrs)
+        for inter, prod in zip(self.interactions, self.products):
+            x, sc = inter(x, attrs, R, Y, edge_index)
+            x = prod(x, attrs, sc)
+        return x
+
+
+class TACE(torch.nn.Module):
+    """``e3nnTACE`` energy path (``tace/models/_e3nn/tace.py:28-790``)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        self.cfg = cfg
+        zs = cfg["atomic_numbers"]
+        self.register_buffer("cutoff", torch.tensor(cfg["cutoff"]))
+        self.register_buffer("atomic_numbers", torch.tensor(zs, dtype=torch.int64))
+        self.representation = Representation(cfg)
+        C = cfg["num_channel"]
+        self.energy_readouts = torch.nn.ModuleList([ScalarReadOut([(C, (0, 1))], cfg["readout_emlp"]["hidden"])])
+        stats = cfg["statistics"]
+        self.atomic_energy_layer = torch.nn.Module()
+        self.atomic_energy_layer.register_buffer("atomic_energy", torch.tensor(
+            [[float({int(k): v for k, v in s["atomic_energy"].items()}.get(z, 0.0)) for z in zs] for s in stats]))
+        self.scale_shift = torch.nn.Module()
+        self.scale_shift.register_buffer("atomic_numbers", torch.tensor(zs, dtype=torch.int64))
+        self.scale_shift.register_buffer("scale", torch.tensor(
+            [[float({int(k): v for k, v in s["rms_forces"].items()}.get(z, 1.0)) for z in zs] for s in stats]))
+        # shift_type None still builds a zero shift per fidelity (blocks.py:425-435)
+        self.scale_shift.register_buffer("shift", torch.zeros(len(stats), len(zs)))
+
+    def energy(self, attrs, edge_index, edge_vector, edge_length, batch, ptr, num_graphs):
+        """``readout_fn`` energy branch (``tace/models/_e3nn/tace.py:356-418``) and
+        ``ScaleShift`` (``tace/models/blocks.py:289-379``), fidelity 0."""
+        x = self.representation(attrs, edge_index, edge_vector, edge_length)
+        fid = 0
+        e_base_node = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, fid]
+        e_node = self.energy_readouts[0](x)[:, fid]
+        # scale (all_atoms=False: isolated single atoms get scale 0)
+        num_nodes = ptr[1:] - ptr[:-1]
+        if edge_index.numel() == 0:
+            num_edges = torch.zeros(num_graphs, dtype=torch.int64)
+        else:
+            num_edges = torch.zeros(num_graphs, dtype=torch.int64).index_add(
+                0, batch[edge_index[1]], torch.ones_like(edge_index[1]))
+        isolated = ((num_nodes == 1) & (num_edges == 0))[batch]
+        scale = (attrs * self.scale_shift.scale[fid]).sum(-1)
+        scale = torch.where(isolated, torch.zeros_like(scale), scale)
+        e_node = e_node * scale
+        shift = (attrs * self.scale_shift.shift[fid]).sum(-1)
+        e_node = e_node + torch.where(isolated, torch.zeros_like(shift), shift)
+        E = (torch.zeros(num_graphs, dtype=attrs.dtype).index_add(0, batch, e_base_node)
+             + torch.zeros(num_graphs, dtype=attrs.dtype).index_add(0, batch, e_node))
+        return E, e_base_node + e_node
+
+
+def compute(model: TACE, data: Dict[str, torch.Tensor], forces: bool = True, stress: bool = False):
+    """``TensorModel.forward`` restated (``tace/models/adapter.py:32-174, 278-384``):
+    edge vectors from (strained) positions, E, F = -dE/dr, S = -V/|det L| with
+    V = -dE/d(eps) (``compute_symmetric_displacement``, ``models/utils.py:50-79``)."""
+    dtype = data["node_attrs"].dtype
+    pos = data["positions"].detach().clone().requires_grad_(True)
+    lattice = data["lattice"]
+    batch, ptr = data["batch"], data["ptr"]
+    num_graphs = ptr.numel() - 1
+    inputs = [pos]
+    if stress:
+        disp = torch.zeros(num_graphs, 3, 3, dtype=dtype, requires_grad=True)
+        sym = 0.5 * (disp + disp.transpose(-1, -2))
+        pos_s = pos + torch.einsum("be,bec->bc", pos, sym[batch])
+        lat_s = lattice + torch.matmul(lattice, sym)
+        inputs.append(disp)
+    else:
+        pos_s, lat_s = pos, lattice
+    src, dst = data["edge_index"][0], data["edge_index"][1]
+    vec = pos_s[dst] - pos_s[src] + torch.einsum("ni,nij->nj", data["edge_shifts"], lat_s[batch[src]])
+    length = (vec ** 2).sum(dim=1, keepdim=True).sqrt() + 1e-9
+    E, e_node = model.energy(data["node_attrs"], data["edge_index"], vec, length, batch, ptr, num_graphs)
+    out = {"energy": E.detach(), "node_energy": e_node.detach()}
+    if forces or stress:
+        grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True)
+        out["forces"] = -grads[0] if grads[0] is not None else torch.zeros_like(pos)
+        if stress:
+            V = -grads[1] if grads[1] is not None else torch.zeros_like(lattice)
+            vol = torch.linalg.det(lattice).abs().view(-1, 1, 1)
+            S = -V / vol
+            out["virials"] = V
+            out["stress"] = torch.where(S.abs() < 1e10, S, torch.zeros_like(S))
+    return out

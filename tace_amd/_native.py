@@ -1,0 +1,95 @@
+"""ctypes binding of ``libtace_hip.so`` (the C ABI in ``include/tace_hip.h``).
+
+The library is loaded from the package tree (``tace_amd/_lib``).  There is no
+fallback: if it is missing or cannot be loaded, every operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Optional
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "libtace_hip.so")
+
+F32, F64 = 0, 1
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+_c_int, _c_i32, _c_i64, _c_dbl = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_double
+_vp, _cp = ctypes.c_void_p, ctypes.c_char_p
+
+_SIGS = {
+    "tace_last_error": (_cp, []),
+    "tace_abi_version": (_c_int, []),
+    "tace_tp_num_variants": (_c_int, []),
+    "tace_tp_variant_key": (_cp, [_c_int]),
+    "tace_tp_find": (_c_int, [_cp]),
+    "tace_tp_dims": (_c_int, [_c_int, _vp, _vp, _vp, _vp]),
+    "tace_edge_tp_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _vp, _vp]),
+    "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
+                                  _vp, _vp, _vp, _vp]),
+    "tace_uuu_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
+    "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp, _vp]),
+    "tace_edge_basis_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32, _vp, _vp, _vp]),
+    "tace_edge_basis_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32,
+                                     _vp, _vp]),
+    "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
+    "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
+    "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),
+    "tace_scan_i32": (_c_int, [_vp, _c_i64, _vp, _vp]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+class NativeError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once (raises if it is absent -- no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise NativeError(
+                        f"libtace_hip.so not found at {LIB_PATH}; build it with "
+                        "`python -m tace_amd.build` (hipcc, gfx950)")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGS.items():
+                    f = getattr(L, name)
+                    f.restype = res
+                    f.argtypes = args
+                _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().tace_last_error()
+        raise NativeError(f"{what or 'tace_hip'} failed ({rc}): {msg.decode() if msg else ''}")
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    if dtype == torch.float32:
+        return F32
+    if dtype == torch.float64:
+        return F64
+    raise NativeError(f"unsupported dtype {dtype}; TACE HIP kernels take float32 or float64")
+
+
+def ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,565 @@
+// MI355X (gfx950) kernels of the TACE energy/force path, exported through a
+// flat C ABI (include/tace_hip.h).  Host code (tace_amd/*.py) owns every
+// buffer; the library never allocates and never synchronises the stream.
+//
+// Contents
+//   * edge featurisation: Bessel j0 x C2-polynomial cutoff radial basis and
+//     component-normalised real spherical harmonics, forward and the backward
+//     to edge vectors (tace/models/radial.py:43-84, 437-472, 974-993;
+//     tace/models/angular.py:288-315);
+//   * CG tensor products: generated kernels (gen/tp_kernels.inc) dispatched by
+//     variant key (tace/models/_e3nn/fused.py:17-95, 172-271);
+//   * periodic cell-list neighbour search, float64, same edge set as
+//     tace/dataset/neighbour_list.py:195-298 (matscipy "ijSd").
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/tace_hip.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(const char* msg) {
+  snprintf(g_err, sizeof(g_err), "%s", msg);
+  return -1;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+    return -2;
+  }
+  return 0;
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace
+
+#include "gen/tp_kernels.inc"
+
+// ---------------------------------------------------------------- helpers --
+template <typename T>
+__global__ void k_fill(T* p, size_t n, T v) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) p[i] = v;
+}
+
+template <typename T>
+static void launch_fill(T* p, size_t n, T v, hipStream_t s) {
+  if (n == 0) return;
+  size_t blocks = (n + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+}
+
+// ------------------------------------------------------ edge featurisation --
+// R[e, n] = pref * sin(b_n r) / r * f(r / rc) * [r < rc],  r = |v| + 1e-9
+// f(x) = 1 - (p+1)(p+2)/2 x^p + p(p+2) x^(p+1) - p(p+1)/2 x^(p+2)
+// Y[e, :] = SH_lmax(v / r)
+template <typename T>
+__device__ __forceinline__ T ipow(T x, int p) {
+  T r = T(1);
+  for (int i = 0; i < p; ++i) r *= x;
+  return r;
+}
+
+template <typename T, int LMAX>
+__global__ __launch_bounds__(256) void k_edge_basis_fwd(const T* __restrict__ vec, int64_t E, int nb,
+                                                        const T* __restrict__ bw, T pref, T rc, int p,
+                                                        T* __restrict__ R, T* __restrict__ Y) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const T vx = vec[3 * e], vy = vec[3 * e + 1], vz = vec[3 * e + 2];
+  const T nrm = sqrt(vx * vx + vy * vy + vz * vz);
+  const T r = nrm + T(1e-9);
+  const T x = r / rc;
+  const T c1 = T((p + 1.0) * (p + 2.0) / 2.0), c2 = T(p * (p + 2.0)), c3 = T(p * (p + 1.0) / 2.0);
+  const T xp = ipow(x, p);
+  T env = T(1) - c1 * xp + c2 * (xp * x) - c3 * (xp * x * x);
+  env = (r < rc) ? env : T(0);
+  for (int n = 0; n < nb; ++n) R[e * nb + n] = pref * (sin(bw[n] * r) / r) * env;
+  constexpr int DY = (LMAX + 1) * (LMAX + 1);
+  T o[DY];
+  const T ux = vx / r, uy = vy / r, uz = vz / r;
+  if constexpr (LMAX == 0) sh_eval_0<T>(ux, uy, uz, o);
+  if constexpr (LMAX == 1) sh_eval_1<T>(ux, uy, uz, o);
+  if constexpr (LMAX == 2) sh_eval_2<T>(ux, uy, uz, o);
+  if constexpr (LMAX == 3) sh_eval_3<T>(ux, uy, uz, o);
+#pragma unroll
+  for (int i = 0; i < DY; ++i) Y[e * DY + i] = o[i];
+}
+
+template <typename T, int LMAX>
+__global__ __launch_bounds__(256) void k_edge_basis_bwd(const T* __restrict__ vec, const T* __restrict__ gR,
+                                                        const T* __restrict__ gY, int64_t E, int nb,
+                                                        const T* __restrict__ bw, T pref, T rc, int p,
+                                                        T* __restrict__ gvec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const T vx = vec[3 * e], vy = vec[3 * e + 1], vz = vec[3 * e + 2];
+  const T nrm = sqrt(vx * vx + vy * vy + vz * vz);
+  const T r = nrm + T(1e-9);
+  const T x = r / rc;
+  const T c1 = T((p + 1.0) * (p + 2.0) / 2.0), c2 = T(p * (p + 2.0)), c3 = T(p * (p + 1.0) / 2.0);
+  const T xp = ipow(x, p);
+  const T xpm1 = ipow(x, p - 1);
+  T env = T(1) - c1 * xp + c2 * (xp * x) - c3 * (xp * x * x);
+  T denv = (-c1 * T(p) * xpm1 + c2 * T(p + 1) * xp - c3 * T(p + 2) * (xp * x)) / rc;
+  const bool in = r < rc;
+  env = in ? env : T(0);
+  denv = in ? denv : T(0);
+  T gr = T(0);
+  for (int n = 0; n < nb; ++n) {
+    const T b = bw[n];
+    const T sn = sin(b * r), cs = cos(b * r);
+    const T dRdr = pref * (((b * cs) * r - sn) / (r * r) * env + (sn / r) * denv);
+    gr += gR[e * nb + n] * dRdr;
+  }
+  constexpr int DY = (LMAX + 1) * (LMAX + 1);
+  const T ux = vx / r, uy = vy / r, uz = vz / r;
+  T gux = T(0), guy = T(0), guz = T(0);
+  if constexpr (LMAX == 0) sh_grad_0<T>(ux, uy, uz, gY + e * DY, gux, guy, guz);
+  if constexpr (LMAX == 1) sh_grad_1<T>(ux, uy, uz, gY + e * DY, gux, guy, guz);
+  if constexpr (LMAX == 2) sh_grad_2<T>(ux, uy, uz, gY + e * DY, gux, guy, guz);
+  if constexpr (LMAX == 3) sh_grad_3<T>(ux, uy, uz, gY + e * DY, gux, guy, guz);
+  // u = v / r, r = |v| + eps:  du_a/dv_b = d_ab / r - v_a v_b / (|v| r^2)
+  const T gdot = gux * vx + guy * vy + guz * vz;
+  const T k = gdot / (nrm * r * r);
+  const T gl = gr / nrm;
+  gvec[3 * e] = gux / r - vx * k + gl * vx;
+  gvec[3 * e + 1] = guy / r - vy * k + gl * vy;
+  gvec[3 * e + 2] = guz / r - vz * k + gl * vz;
+}
+
+template <typename T>
+static int edge_basis_fwd_t(const T* vec, int64_t E, int nb, const T* bw, double pref, double rc, int p, int lmax,
+                            T* R, T* Y, hipStream_t s) {
+  if (E <= 0) return 0;
+  dim3 g((unsigned)((E + 255) / 256)), b(256);
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL((k_edge_basis_fwd<T, 0>), g, b, 0, s, vec, E, nb, bw, (T)pref, (T)rc, p, R, Y); break;
+    case 1: hipLaunchKernelGGL((k_edge_basis_fwd<T, 1>), g, b, 0, s, vec, E, nb, bw, (T)pref, (T)rc, p, R, Y); break;
+    case 2: hipLaunchKernelGGL((k_edge_basis_fwd<T, 2>), g, b, 0, s, vec, E, nb, bw, (T)pref, (T)rc, p, R, Y); break;
+    case 3: hipLaunchKernelGGL((k_edge_basis_fwd<T, 3>), g, b, 0, s, vec, E, nb, bw, (T)pref, (T)rc, p, R, Y); break;
+    default: return fail("tace_edge_basis_fwd: lmax must be 0..3");
+  }
+  return check_launch("tace_edge_basis_fwd");
+}
+
+template <typename T>
+static int edge_basis_bwd_t(const T* vec, const T* gR, const T* gY, int64_t E, int nb, const T* bw, double pref,
+                            double rc, int p, int lmax, T* gvec, hipStream_t s) {
+  if (E <= 0) return 0;
+  dim3 g((unsigned)((E + 255) / 256)), b(256);
+  switch (lmax) {
+    case 0: hipLaunchKernelGGL((k_edge_basis_bwd<T, 0>), g, b, 0, s, vec, gR, gY, E, nb, bw, (T)pref, (T)rc, p, gvec); break;
+    case 1: hipLaunchKernelGGL((k_edge_basis_bwd<T, 1>), g, b, 0, s, vec, gR, gY, E, nb, bw, (T)pref, (T)rc, p, gvec); break;
+    case 2: hipLaunchKernelGGL((k_edge_basis_bwd<T, 2>), g, b, 0, s, vec, gR, gY, E, nb, bw, (T)pref, (T)rc, p, gvec); break;
+    case 3: hipLaunchKernelGGL((k_edge_basis_bwd<T, 3>), g, b, 0, s, vec, gR, gY, E, nb, bw, (T)pref, (T)rc, p, gvec); break;
+    default: return fail("tace_edge_basis_bwd: lmax must be 0..3");
+  }
+  return check_launch("tace_edge_basis_bwd");
+}
+
+// ------------------------------------------------------------ neighbours --
+struct NlGeom {
+  double cell[9];  // rows are lattice vectors
+  double inv[9];   // inverse of cell (frac = pos @ inv)
+  int pbc[3];
+  int nb[3];       // bins per axis
+  int reach[3];    // bins searched on each side
+  double rc2;
+};
+
+static void inv3(const double* a, double* o) {
+  double det = a[0] * (a[4] * a[8] - a[5] * a[7]) - a[1] * (a[3] * a[8] - a[5] * a[6]) +
+               a[2] * (a[3] * a[7] - a[4] * a[6]);
+  o[0] = (a[4] * a[8] - a[5] * a[7]) / det;
+  o[1] = (a[2] * a[7] - a[1] * a[8]) / det;
+  o[2] = (a[1] * a[5] - a[2] * a[4]) / det;
+  o[3] = (a[5] * a[6] - a[3] * a[8]) / det;
+  o[4] = (a[0] * a[8] - a[2] * a[6]) / det;
+  o[5] = (a[2] * a[3] - a[0] * a[5]) / det;
+  o[6] = (a[3] * a[7] - a[4] * a[6]) / det;
+  o[7] = (a[1] * a[6] - a[0] * a[7]) / det;
+  o[8] = (a[0] * a[4] - a[1] * a[3]) / det;
+}
+
+static int nl_geometry(const double* cell, const int32_t* pbc, double cutoff, NlGeom* g) {
+  if (!(cutoff > 0.0)) return fail("tace_nl: cutoff must be > 0");
+  memcpy(g->cell, cell, 9 * sizeof(double));
+  double det = cell[0] * (cell[4] * cell[8] - cell[5] * cell[7]) - cell[1] * (cell[3] * cell[8] - cell[5] * cell[6]) +
+               cell[2] * (cell[3] * cell[7] - cell[4] * cell[6]);
+  if (fabs(det) < 1e-12) return fail("tace_nl: cell is singular (complete the cell for non-periodic axes)");
+  inv3(cell, g->inv);
+  for (int k = 0; k < 3; ++k) {
+    g->pbc[k] = pbc[k] ? 1 : 0;
+    const double c0 = g->inv[k], c1 = g->inv[3 + k], c2 = g->inv[6 + k];
+    const double h = 1.0 / sqrt(c0 * c0 + c1 * c1 + c2 * c2);  // plane spacing
+    int nb = (int)floor(h / cutoff);
+    if (nb < 1) nb = 1;
+    if (nb > 512) nb = 512;
+    g->nb[k] = nb;
+    g->reach[k] = (int)ceil(cutoff * nb / h + 1e-9);
+    if (!g->pbc[k] && g->reach[k] > nb) g->reach[k] = nb;
+  }
+  g->rc2 = cutoff * cutoff;
+  return 0;
+}
+
+__global__ void k_nl_bin(const double* __restrict__ pos, int n, NlGeom g, int* __restrict__ abin,
+                         int* __restrict__ aimg, int* __restrict__ bcount) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const double px = pos[3 * i], py = pos[3 * i + 1], pz = pos[3 * i + 2];
+  int b[3];
+  for (int k = 0; k < 3; ++k) {
+    const double f = px * g.inv[k] + py * g.inv[3 + k] + pz * g.inv[6 + k];
+    int o = 0;
+    double w = f;
+    if (g.pbc[k]) {
+      o = (int)floor(f);
+      w = f - (double)o;
+    }
+    int bi = (int)floor(w * g.nb[k]);
+    bi = bi < 0 ? 0 : (bi >= g.nb[k] ? g.nb[k] - 1 : bi);
+    b[k] = bi;
+    aimg[3 * i + k] = o;
+  }
+  const int lin = (b[0] * g.nb[1] + b[1]) * g.nb[2] + b[2];
+  abin[i] = lin;
+  atomicAdd(bcount + lin, 1);
+}
+
+// exclusive scan of cnt[0..m) into out[0..m]; single block of 1024 threads
+__global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ cnt, int m, int* __restrict__ out) {
+  __shared__ long long part[1024];
+  const int t = threadIdx.x;
+  const int chunk = (m + 1023) / 1024;
+  const int b = t * chunk, e = min(m, b + chunk);
+  long long s = 0;
+  for (int i = b; i < e; ++i) s += cnt[i];
+  part[t] = s;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    long long v = (t >= o) ? part[t - o] : 0;
+    __syncthreads();
+    part[t] += v;
+    __syncthreads();
+  }
+  long long run = part[t] - s;
+  for (int i = b; i < e; ++i) {
+    out[i] = (int)run;
+    run += cnt[i];
+  }
+  if (t == 1023) out[m] = (int)part[1023];
+}
+
+__global__ void k_nl_scatter(const int* __restrict__ abin, int n, const int* __restrict__ bstart,
+                             int* __restrict__ bfill, int* __restrict__ batoms) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int b = abin[i];
+  const int slot = atomicAdd(bfill + b, 1);
+  batoms[bstart[b] + slot] = i;
+}
+
+// deterministic order inside each bin: insertion sort of atom ids
+__global__ void k_nl_sortbins(const int* __restrict__ bstart, int nbins, int* __restrict__ batoms) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nbins) return;
+  const int s = bstart[b], e = bstart[b + 1];
+  for (int i = s + 1; i < e; ++i) {
+    const int v = batoms[i];
+    int j = i - 1;
+    while (j >= s && batoms[j] > v) {
+      batoms[j + 1] = batoms[j];
+      --j;
+    }
+    batoms[j + 1] = v;
+  }
+}
+
+// For receiver a: every source b and shift S with |r_a - r_b + S.cell|^2 < rc^2,
+// (b, S) != (a, 0).  The distance is evaluated exactly as the brute-force
+// oracle does for edge (i=b, j=a, S): d = r_a - r_b, v = d + S0 c0 + S1 c1 + S2 c2.
+template <bool FILL>
+__global__ __launch_bounds__(64) void k_nl_edges(const double* __restrict__ pos, int n, NlGeom g,
+                                                 const int* __restrict__ abin, const int* __restrict__ aimg,
+                                                 const int* __restrict__ bstart, const int* __restrict__ batoms,
+                                                 int* __restrict__ counts, const int* __restrict__ rowptr,
+                                                 int* __restrict__ src, int* __restrict__ shift) {
+#pragma clang fp contract(off)
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= n) return;
+  const double ax = pos[3 * a], ay = pos[3 * a + 1], az = pos[3 * a + 2];
+  const int lin = abin[a];
+  const int ba[3] = {lin / (g.nb[1] * g.nb[2]), (lin / g.nb[2]) % g.nb[1], lin % g.nb[2]};
+  const int oa[3] = {aimg[3 * a], aimg[3 * a + 1], aimg[3 * a + 2]};
+  int cnt = 0;
+  const int base = FILL ? rowptr[a] : 0;
+  int lo[3], hi[3];
+  for (int k = 0; k < 3; ++k) {
+    lo[k] = ba[k] - g.reach[k];
+    hi[k] = ba[k] + g.reach[k];
+    if (!g.pbc[k]) {
+      lo[k] = lo[k] < 0 ? 0 : lo[k];
+      hi[k] = hi[k] >= g.nb[k] ? g.nb[k] - 1 : hi[k];
+    }
+  }
+  for (int bx = lo[0]; bx <= hi[0]; ++bx) {
+    const int wx = ((bx % g.nb[0]) + g.nb[0]) % g.nb[0];
+    const int sx = (bx - wx) / g.nb[0];
+    for (int by = lo[1]; by <= hi[1]; ++by) {
+      const int wy = ((by % g.nb[1]) + g.nb[1]) % g.nb[1];
+      const int sy = (by - wy) / g.nb[1];
+      for (int bz = lo[2]; bz <= hi[2]; ++bz) {
+        const int wz = ((bz % g.nb[2]) + g.nb[2]) % g.nb[2];
+        const int sz = (bz - wz) / g.nb[2];
+        const int bl = (wx * g.nb[1] + wy) * g.nb[2] + wz;
+        for (int q = bstart[bl]; q < bstart[bl + 1]; ++q) {
+          const int b = batoms[q];
+          const int S0 = aimg[3 * b] - oa[0] - sx;
+          const int S1 = aimg[3 * b + 1] - oa[1] - sy;
+          const int S2 = aimg[3 * b + 2] - oa[2] - sz;
+          if (b == a && S0 == 0 && S1 == 0 && S2 == 0) continue;
+          const double d0 = ax - pos[3 * b], d1 = ay - pos[3 * b + 1], d2 = az - pos[3 * b + 2];
+          const double s0 = (double)S0, s1 = (double)S1, s2 = (double)S2;
+          const double v0 = d0 + s0 * g.cell[0] + s1 * g.cell[3] + s2 * g.cell[6];
+          const double v1 = d1 + s0 * g.cell[1] + s1 * g.cell[4] + s2 * g.cell[7];
+          const double v2 = d2 + s0 * g.cell[2] + s1 * g.cell[5] + s2 * g.cell[8];
+          const double r2 = v0 * v0 + v1 * v1 + v2 * v2;
+          if (r2 < g.rc2) {
+            if (FILL) {
+              const int slot = base + cnt;
+              src[slot] = b;
+              shift[3 * slot] = S0;
+              shift[3 * slot + 1] = S1;
+              shift[3 * slot + 2] = S2;
+            }
+            ++cnt;
+          }
+        }
+      }
+    }
+  }
+  if (!FILL) counts[a] = cnt;
+}
+
+// --------------------------------------------------------------- C ABI --
+extern "C" {
+
+const char* tace_last_error(void) { return g_err; }
+
+int tace_abi_version(void) { return TACE_HIP_ABI_VERSION; }
+
+int tace_tp_num_variants(void) { return kNumVariants; }
+
+const char* tace_tp_variant_key(int vid) {
+  if (vid < 0 || vid >= kNumVariants) return nullptr;
+  return kVariants[vid].key;
+}
+
+int tace_tp_find(const char* key) {
+  if (!key) return fail("tace_tp_find: null key");
+  for (int i = 0; i < kNumVariants; ++i)
+    if (strcmp(kVariants[i].key, key) == 0) return i;
+  snprintf(g_err, sizeof(g_err), "tace_tp_find: no compiled tensor-product variant for '%s'", key);
+  return -1;
+}
+
+int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dout) {
+  if (vid < 0 || vid >= kNumVariants) return fail("tace_tp_dims: bad variant id");
+  const TpVariant& v = kVariants[vid];
+  if (npath) *npath = v.npath;
+  if (d1) *d1 = v.d1;
+  if (d2) *d2 = v.d2;
+  if (dout) *dout = v.dout;
+  return 0;
+}
+
+int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
+                     const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                     void* out, void* stream) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_fwd: bad variant id");
+  if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_fwd: bad sizes");
+  if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_fwd: sizes exceed int32 indexing");
+  if ((!x && n_edges) || !out || !rowptr || (n_edges && (!y || !w || !src))) return fail("tace_edge_tp_fwd: null pointer");
+  const TpVariant& v = kVariants[vid];
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    v.fwd_f(x, y, w, rowptr, eid, src, out, (int)n_nodes, (int)n_edges, channels, s);
+  else if (dtype == TACE_F64)
+    v.fwd_d(x, y, w, rowptr, eid, src, out, (int)n_nodes, (int)n_edges, channels, s);
+  else
+    return fail("tace_edge_tp_fwd: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_edge_tp_fwd");
+}
+
+int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
+                     int32_t channels, void* gx, void* gy, void* gw, void* stream) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_bwd: bad variant id");
+  if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_bwd: bad sizes");
+  if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_bwd: sizes exceed int32 indexing");
+  if (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)) return fail("tace_edge_tp_bwd: null pointer");
+  const TpVariant& v = kVariants[vid];
+  hipStream_t s = (hipStream_t)stream;
+  const size_t nx = (size_t)n_nodes * channels * v.d1;
+  if (dtype == TACE_F32) {
+    if (gx) launch_fill<float>((float*)gx, nx, 0.f, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, gx, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+  } else if (dtype == TACE_F64) {
+    if (gx) launch_fill<double>((double*)gx, nx, 0.0, s);
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, gx, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+  } else {
+    return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
+  }
+  return check_launch("tace_edge_tp_bwd");
+}
+
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels, void* out,
+                 void* stream) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_fwd: bad variant id");
+  if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_fwd: bad sizes");
+  if (n_nodes && (!x1 || !x2 || !out)) return fail("tace_uuu_fwd: null pointer");
+  if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_fwd: too many nodes");
+  const TpVariant& v = kVariants[vid];
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    v.fwd_f(x1, x2, nullptr, nullptr, nullptr, nullptr, out, (int)n_nodes, 0, channels, s);
+  else if (dtype == TACE_F64)
+    v.fwd_d(x1, x2, nullptr, nullptr, nullptr, nullptr, out, (int)n_nodes, 0, channels, s);
+  else
+    return fail("tace_uuu_fwd: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_uuu_fwd");
+}
+
+int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
+                 int32_t channels, void* g1, void* g2, void* stream) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
+  if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
+  if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
+  const TpVariant& v = kVariants[vid];
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    v.bwd_f(x1, x2, nullptr, gout, nullptr, nullptr, nullptr, g1, g2, nullptr, (int)n_nodes, 0, channels, s);
+  else if (dtype == TACE_F64)
+    v.bwd_d(x1, x2, nullptr, gout, nullptr, nullptr, nullptr, g1, g2, nullptr, (int)n_nodes, 0, channels, s);
+  else
+    return fail("tace_uuu_bwd: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_uuu_bwd");
+}
+
+int tace_edge_basis_fwd(int dtype, const void* vec, int64_t n_edges, int32_t num_basis, const void* bessel_w,
+                        double prefactor, double cutoff, int32_t poly_p, int32_t lmax, void* radial, void* sh,
+                        void* stream) {
+  if (n_edges < 0 || num_basis <= 0 || poly_p < 1) return fail("tace_edge_basis_fwd: bad sizes");
+  if (n_edges && (!vec || !bessel_w || !radial || !sh)) return fail("tace_edge_basis_fwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    return edge_basis_fwd_t<float>((const float*)vec, n_edges, num_basis, (const float*)bessel_w, prefactor, cutoff,
+                                   poly_p, lmax, (float*)radial, (float*)sh, s);
+  if (dtype == TACE_F64)
+    return edge_basis_fwd_t<double>((const double*)vec, n_edges, num_basis, (const double*)bessel_w, prefactor, cutoff,
+                                    poly_p, lmax, (double*)radial, (double*)sh, s);
+  return fail("tace_edge_basis_fwd: dtype must be TACE_F32 or TACE_F64");
+}
+
+int tace_edge_basis_bwd(int dtype, const void* vec, const void* g_radial, const void* g_sh, int64_t n_edges,
+                        int32_t num_basis, const void* bessel_w, double prefactor, double cutoff, int32_t poly_p,
+                        int32_t lmax, void* g_vec, void* stream) {
+  if (n_edges < 0 || num_basis <= 0 || poly_p < 1) return fail("tace_edge_basis_bwd: bad sizes");
+  if (n_edges && (!vec || !g_radial || !g_sh || !bessel_w || !g_vec)) return fail("tace_edge_basis_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    return edge_basis_bwd_t<float>((const float*)vec, (const float*)g_radial, (const float*)g_sh, n_edges, num_basis,
+                                   (const float*)bessel_w, prefactor, cutoff, poly_p, lmax, (float*)g_vec, s);
+  if (dtype == TACE_F64)
+    return edge_basis_bwd_t<double>((const double*)vec, (const double*)g_radial, (const double*)g_sh, n_edges,
+                                    num_basis, (const double*)bessel_w, prefactor, cutoff, poly_p, lmax,
+                                    (double*)g_vec, s);
+  return fail("tace_edge_basis_bwd: dtype must be TACE_F32 or TACE_F64");
+}
+
+int64_t tace_nl_workspace_bytes(int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff) {
+  NlGeom g;
+  if (!cell || !pbc) return fail("tace_nl_workspace_bytes: null pointer");
+  if (nl_geometry(cell, pbc, cutoff, &g)) return -1;
+  const int64_t nbins = (int64_t)g.nb[0] * g.nb[1] * g.nb[2];
+  // abin[n], aimg[3n], bcount[nbins], bstart[nbins+1], bfill[nbins], batoms[n]
+  return (int64_t)sizeof(int32_t) * (n_atoms * 5 + nbins * 3 + 1);
+}
+
+int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
+                  void* workspace, int64_t workspace_bytes, int32_t* counts, void* stream) {
+  NlGeom g;
+  if (!cell || !pbc) return fail("tace_nl_count: null pointer");
+  if (nl_geometry(cell, pbc, cutoff, &g)) return -1;
+  if (n_atoms < 0 || n_atoms > INT32_MAX / 8) return fail("tace_nl_count: bad atom count");
+  if (n_atoms == 0) return 0;
+  if (!pos || !workspace || !counts) return fail("tace_nl_count: null pointer");
+  const int64_t nbins = (int64_t)g.nb[0] * g.nb[1] * g.nb[2];
+  if (workspace_bytes < (int64_t)sizeof(int32_t) * (n_atoms * 5 + nbins * 3 + 1))
+    return fail("tace_nl_count: workspace too small");
+  hipStream_t s = (hipStream_t)stream;
+  const int n = (int)n_atoms;
+  int* abin = (int*)workspace;
+  int* aimg = abin + n;
+  int* bcount = aimg + 3 * n;
+  int* bstart = bcount + nbins;
+  int* bfill = bstart + nbins + 1;
+  int* batoms = bfill + nbins;
+  launch_fill<int>(bcount, (size_t)nbins, 0, s);
+  launch_fill<int>(bfill, (size_t)nbins, 0, s);
+  const dim3 ga((n + 255) / 256), ba(256);
+  hipLaunchKernelGGL(k_nl_bin, ga, ba, 0, s, pos, n, g, abin, aimg, bcount);
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bcount, (int)nbins, bstart);
+  hipLaunchKernelGGL(k_nl_scatter, ga, ba, 0, s, abin, n, bstart, bfill, batoms);
+  hipLaunchKernelGGL(k_nl_sortbins, dim3((unsigned)((nbins + 255) / 256)), dim3(256), 0, s, bstart, (int)nbins, batoms);
+  hipLaunchKernelGGL((k_nl_edges<false>), dim3((n + 63) / 64), dim3(64), 0, s, pos, n, g, abin, aimg, bstart, batoms,
+                     counts, nullptr, nullptr, nullptr);
+  return check_launch("tace_nl_count");
+}
+
+int tace_nl_fill(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
+                 const void* workspace, const int32_t* rowptr, int32_t* src, int32_t* shifts, void* stream) {
+  NlGeom g;
+  if (!cell || !pbc) return fail("tace_nl_fill: null pointer");
+  if (nl_geometry(cell, pbc, cutoff, &g)) return -1;
+  if (n_atoms <= 0) return 0;
+  if (!pos || !workspace || !rowptr || !src || !shifts) return fail("tace_nl_fill: null pointer");
+  const int64_t nbins = (int64_t)g.nb[0] * g.nb[1] * g.nb[2];
+  hipStream_t s = (hipStream_t)stream;
+  const int n = (int)n_atoms;
+  const int* abin = (const int*)workspace;
+  const int* aimg = abin + n;
+  const int* bcount = aimg + 3 * n;
+  const int* bstart = bcount + nbins;
+  const int* bfill = bstart + nbins + 1;
+  const int* batoms = bfill + nbins;
+  hipLaunchKernelGGL((k_nl_edges<true>), dim3((n + 63) / 64), dim3(64), 0, s, pos, n, g, abin, aimg, bstart, batoms,
+                     nullptr, rowptr, src, shifts);
+  return check_launch("tace_nl_fill");
+}
+
+int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream) {
+  if (n < 0 || n > INT32_MAX - 1) return fail("tace_scan_i32: bad size");
+  if (!counts || !out) return fail("tace_scan_i32: null pointer");
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, (hipStream_t)stream, counts, (int)n, out);
+  return check_launch("tace_scan_i32");
+}
+
+}  // extern "C"

@@ -1,0 +1,103 @@
+"""Graph batches in the reference's data-dict format.
+
+``collate`` builds ``{positions, node_attrs, edge_index, edge_shifts, lattice,
+batch, ptr}`` as ``from_atoms`` + torch_geometric collation produce them
+(``tace/dataset/graph.py:36-161``; keys as used at
+``tace/interface/torchsim/torchsim.py:261-274``), from structures and their
+per-structure edge lists.  ``gpu_graph`` does the same on the GPU with the
+HIP neighbour list, keeping edges grouped by receiver.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, List, Sequence, Tuple
+
+import numpy as np
+import torch
+
+
+def one_hot(numbers: np.ndarray, atomic_numbers: Sequence[int], dtype) -> torch.Tensor:
+    """``TorchElement.z2onehot`` (``tace/dataset/element.py:40-64``)."""
+    zs = sorted(int(z) for z in atomic_numbers)
+    lut = np.full(max(zs) + 1, -1, dtype=np.int64)
+    lut[zs] = np.arange(len(zs))
+    idx = lut[np.asarray(numbers)]
+    if (idx < 0).any():
+        raise ValueError("structure contains an element outside the model's atomic_numbers")
+    out = torch.zeros(len(idx), len(zs), dtype=dtype)
+    out[torch.arange(len(idx)), torch.from_numpy(idx)] = 1
+    return out
+
+
+def collate(structs: List[Dict], edges: List[Tuple[np.ndarray, np.ndarray]], atomic_numbers: Sequence[int],
+            dtype=torch.float64, device="cpu") -> Dict[str, torch.Tensor]:
+    """``edges[k] = (edge_index [2,E_k], shifts [E_k,3])`` per structure, local indexing."""
+    pos, attrs, ei, sh, lat, batch, ptr = [], [], [], [], [], [], [0]
+    off = 0
+    for k, (s, (e, S)) in enumerate(zip(structs, edges)):
+        n = len(s["positions"])
+        pos.append(torch.as_tensor(np.asarray(s["positions"]), dtype=dtype))
+        attrs.append(one_hot(s["numbers"], atomic_numbers, dtype))
+        ei.append(torch.as_tensor(np.asarray(e), dtype=torch.int64) + off)
+        sh.append(torch.as_tensor(np.asarray(S), dtype=dtype))
+        lat.append(torch.as_tensor(np.asarray(s["cell"]), dtype=dtype).view(1, 3, 3))
+        batch.append(torch.full((n,), k, dtype=torch.int64))
+        off += n
+        ptr.append(off)
+    d = dict(positions=torch.cat(pos), node_attrs=torch.cat(attrs), edge_index=torch.cat(ei, 1),
+             edge_shifts=torch.cat(sh), lattice=torch.cat(lat), batch=torch.cat(batch),
+             ptr=torch.tensor(ptr, dtype=torch.int64))
+    return {k: v.to(device) for k, v in d.items()}
+
+
+def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float, dtype=torch.float32,
+              device="cuda") -> Dict[str, torch.Tensor]:
+    """Batch built on the GPU: HIP cell-list neighbour list per structure
+    (float64), edges grouped by receiver (``edge_index[1]`` non-decreasing)."""
+    from .ops import neighbour_list
+
+    pos, attrs, src, dst, sh, lat, batch, ptr = [], [], [], [], [], [], [], [0]
+    off = 0
+    for k, s in enumerate(structs):
+        n = len(s["positions"])
+        p64 = torch.as_tensor(np.asarray(s["positions"], dtype=np.float64), device=device)
+        rowptr, e_src, e_sh = neighbour_list(p64, s["cell"], s["pbc"], cutoff)
+        counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
+        e_dst = torch.repeat_interleave(torch.arange(n, device=device), counts)
+        pos.append(p64.to(dtype))
+        attrs.append(one_hot(s["numbers"], atomic_numbers, dtype).to(device))
+        src.append(e_src.to(torch.int64) + off)
+        dst.append(e_dst + off)
+        sh.append(e_sh.to(dtype))
+        lat.append(torch.as_tensor(np.asarray(s["cell"]), dtype=dtype, device=device).view(1, 3, 3))
+        batch.append(torch.full((n,), k, dtype=torch.int64, device=device))
+        off += n
+        ptr.append(off)
+    return dict(positions=torch.cat(pos), node_attrs=torch.cat(attrs),
+                edge_index=torch.stack([torch.cat(src), torch.cat(dst)]), edge_shifts=torch.cat(sh),
+                lattice=torch.cat(lat), batch=torch.cat(batch),
+                ptr=torch.tensor(ptr, dtype=torch.int64, device=device))
+
+
+def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cutoff: float,
+                   dtype=torch.float32) -> Dict[str, torch.Tensor]:
+    """One periodic structure already resident on the GPU (float64 positions)
+    -> model input dict, neighbour list rebuilt by the HIP cell list."""
+    from .ops import EdgePlan, neighbour_list
+
+    n = pos64.shape[0]
+    dev = pos64.device
+    rowptr, src, sh = neighbour_list(pos64, cell, pbc, cutoff)
+    counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
+    dst = torch.repeat_interleave(torch.arange(n, device=dev), counts, output_size=int(src.shape[0]))
+    d = dict(positions=pos64.to(dtype), node_attrs=node_attrs,
+             edge_index=torch.stack([src.to(torch.int64), dst]), edge_shifts=sh.to(dtype),
+             lattice=torch.as_tensor(np.asarray(cell), dtype=dtype, device=dev).view(1, 3, 3),
+             batch=torch.zeros(n, dtype=torch.int64, device=dev),
+             ptr=torch.tensor([0, n], dtype=torch.int64, device=dev))
+    d["_edge_plan"] = EdgePlan(n, int(src.shape[0]), rowptr, src, None)
+    return d
+
+
+def mean_in_degree(edge_index: np.ndarray, n: int) -> float:
+    return float(np.asarray(edge_index).shape[1]) / max(n, 1)

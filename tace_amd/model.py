@@ -1,0 +1,623 @@
+"""MI355X TACE model behind the reference model API.
+
+``TACE(**cfg)`` accepts the reference ``e3nnTACE`` configuration
+(``tace/models/_e3nn/tace.py:28-337``) and registers parameters and buffers
+under the reference's names and shapes, so a reference ``state_dict`` loads
+into it; ``TensorModel(TACE(**cfg))`` keeps ``TensorModel.forward(data)``
+(``tace/models/adapter.py:23-452``).  The hot path runs on hand-written HIP
+kernels (``tace_amd.ops``): edge featurisation, the fused edge tensor
+product + receiver scatter and the uuu product basis; the node-level channel
+mixing runs as species-grouped GEMMs.  There is no CPU execution path: the
+native library must be present and the tensors on the GPU.
+
+Supported configuration (the one the benchmark workloads use): linear node
+embedding, identity edge embedding/update, ``cgtp`` atomic basis with
+``sigmoid_gate`` (gate_m0), avg_num_neighbors scatter norm, BB element-aware
+resnet, ``cgtp`` product basis (correlation 1-3, one expert), energy readout
+with hidden [16], ``rms_forces`` scale, j0 Bessel x c2poly radial basis.
+Anything else raises ``NotImplementedError`` at construction.
+"""
+
+from __future__ import annotations
+
+import copy
+import math
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import torch
+
+from . import ops
+from .so3 import Irrep, Irreps, generate_paths, possible_tp_irreps, spherical_harmonics_irreps
+
+SIGMOID_CST = 1.8467055342154763  # e3nn normalize2mom(sigmoid)  (tace/models/mlp.py:43)
+SILU_CST = 1.6791767923989418     # e3nn normalize2mom(silu)     (tace/models/mlp.py:34)
+
+
+# ---------------------------------------------------------------- species ----
+class SpeciesPlan:
+    """Nodes grouped by species (``attrs.argmax``), for per-species GEMMs."""
+
+    def __init__(self, attrs: torch.Tensor):
+        self.attrs = attrs
+        species = attrs.argmax(dim=-1)
+        self.perm = torch.argsort(species, stable=True)
+        self.inv = torch.empty_like(self.perm)
+        self.inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
+        counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
+        self.ranges = []
+        acc = 0
+        for s, c in enumerate(counts):
+            if c:
+                self.ranges.append((s, acc, acc + c))
+            acc += c
+
+
+# ---------------------------------------------------------------- linears ----
+class _LinearLayout:
+    """e3nn ``o3.Linear`` bookkeeping: instructions (i_in, i_out) between equal
+    irreps in i_in-major order, path weight (sum of mul_in into i_out)^-1/2,
+    flat weight of row-major [mul_in, mul_out] blocks (``linear.py:282-374``)."""
+
+    def __init__(self, irreps_in, irreps_out):
+        self.irreps_in = Irreps(irreps_in)
+        self.irreps_out = Irreps(irreps_out)
+        ins = [(i, o) for i, (_, a) in enumerate(self.irreps_in) for o, (_, b) in enumerate(self.irreps_out) if a == b]
+        fan = {}
+        for i, o in ins:
+            fan[o] = fan.get(o, 0) + self.irreps_in[i][0]
+        self.ins, off = [], 0
+        for i, o in ins:
+            mi, mo = self.irreps_in[i][0], self.irreps_out[o][0]
+            self.ins.append((i, o, off, mi, mo, fan[o] ** -0.5))
+            off += mi * mo
+        self.weight_numel = off
+        self.sl_in = [(s.start, m, ir.dim) for s, (m, ir) in zip(self.irreps_in.slices(), self.irreps_in)]
+        self.sl_out = [(s.start, m, ir.dim) for s, (m, ir) in zip(self.irreps_out.slices(), self.irreps_out)]
+        self.bias_sl, b = [], 0
+        for (s, m, d), (_, ir) in zip(self.sl_out, self.irreps_out):
+            if ir.l == 0 and ir.p == 1:
+                self.bias_sl.append((s, b, m * d))
+                b += m * d
+        self.bias_numel = b
+        self.dim_in, self.dim_out = self.irreps_in.dim, self.irreps_out.dim
+
+    def apply(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        Z = x.shape[0]
+        outs: List[Optional[torch.Tensor]] = [None] * len(self.sl_out)
+        for i, o, off, mi, mo, pw in self.ins:
+            s, m, d = self.sl_in[i]
+            W = w[off:off + mi * mo].view(mi, mo) * pw
+            xi = x[:, s:s + m * d]
+            if d == 1:
+                y = xi @ W
+            else:
+                y = (xi.view(Z, m, d).transpose(1, 2).reshape(Z * d, m) @ W).view(Z, d, mo).transpose(1, 2)
+                y = y.reshape(Z, mo * d)
+            outs[o] = y if outs[o] is None else outs[o] + y
+        cols = [outs[o] if outs[o] is not None else x.new_zeros(Z, m * d) for o, (s, m, d) in enumerate(self.sl_out)]
+        return cols[0] if len(cols) == 1 else torch.cat(cols, dim=1)
+
+    def bias_full(self, b: torch.Tensor) -> torch.Tensor:
+        """[..., bias_numel] -> [..., dim_out] with zeros outside the 0e slices."""
+        parts, cur = [], 0
+        for s, bs, d in self.bias_sl:
+            if s > cur:
+                parts.append(b.new_zeros(*b.shape[:-1], s - cur))
+            parts.append(b[..., bs:bs + d])
+            cur = s + d
+        if cur < self.dim_out:
+            parts.append(b.new_zeros(*b.shape[:-1], self.dim_out - cur))
+        return torch.cat(parts, dim=-1)
+
+
+class e3nnLinear(torch.nn.Module):
+    """Parameters ``weight`` [numel] ~ N(0,1), ``bias`` [#0e] zeros (``linear.py:282-374``)."""
+
+    def __init__(self, irreps_in, irreps_out, bias: bool = True):
+        super().__init__()
+        self.lay = _LinearLayout(irreps_in, irreps_out)
+        self.irreps_in, self.irreps_out = self.lay.irreps_in, self.lay.irreps_out
+        self.weight = torch.nn.Parameter(torch.randn(self.lay.weight_numel))
+        self.bias = torch.nn.Parameter(torch.zeros(self.lay.bias_numel)) if bias and self.lay.bias_numel else None
+
+    def forward(self, x):
+        out = self.lay.apply(x, self.weight)
+        return out + self.lay.bias_full(self.bias) if self.bias is not None else out
+
+
+class e3nnElementLinear(torch.nn.Module):
+    """Per-species weights ``weight`` [S, numel], ``bias`` [S, #0e] (``linear.py:377-481``);
+    evaluated as one GEMM per (species, instruction) on species-contiguous rows."""
+
+    def __init__(self, irreps_in, irreps_out, num_elements: int, bias: bool = True):
+        super().__init__()
+        self.lay = _LinearLayout(irreps_in, irreps_out)
+        self.irreps_in, self.irreps_out = self.lay.irreps_in, self.lay.irreps_out
+        self.num_elements = num_elements
+        self.weight = torch.nn.Parameter(torch.randn(num_elements, self.lay.weight_numel))
+        self.bias = (torch.nn.Parameter(torch.zeros(num_elements, self.lay.bias_numel))
+                     if bias and self.lay.bias_numel else None)
+
+    def forward_sorted(self, xs: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor) -> torch.Tensor:
+        """``xs`` rows in species-sorted order; returns rows in the same order."""
+        parts = [self.lay.apply(xs[a:b], self.weight[s]) for (s, a, b) in sp.ranges]
+        out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)
+        if self.bias is not None:
+            out = out + self.lay.bias_full(attrs_sorted @ self.bias)
+        return out
+
+    def forward(self, x: torch.Tensor, sp: SpeciesPlan) -> torch.Tensor:
+        xs = x.index_select(0, sp.perm)
+        return self.forward_sorted(xs, sp, sp.attrs.index_select(0, sp.perm)).index_select(0, sp.inv)
+
+
+class mlpLinear(torch.nn.Module):
+    """``x @ (weight * alpha)``, weight [in, out] ~ U(-sqrt3, sqrt3) (``linear.py:247-279``)."""
+
+    def __init__(self, in_dim, out_dim, alpha):
+        super().__init__()
+        self.alpha = alpha
+        self.weight = torch.nn.Parameter(torch.empty(in_dim, out_dim).uniform_(-math.sqrt(3), math.sqrt(3)))
+
+    def forward(self, x):
+        return x @ (self.weight * self.alpha)
+
+
+class MLP(torch.nn.Module):
+    """Radial MLP (``mlp.py:136-191``): alpha = gain/sqrt(h_in), SiLU between layers."""
+
+    def __init__(self, dims):
+        super().__init__()
+        mods = []
+        for layer, (a, b) in enumerate(zip(dims, dims[1:])):
+            mods.append(mlpLinear(a, b, (1.0 if layer == 0 else math.sqrt(2.0)) / math.sqrt(a)))
+            if layer != len(dims) - 2:
+                mods.append(torch.nn.SiLU())
+        self.mlp = torch.nn.Sequential(*mods)
+
+    def forward(self, x):
+        return self.mlp(x)
+
+
+# ------------------------------------------------------------------ blocks ----
+def _ls(irreps: Irreps) -> List[int]:
+    return [ir.l for _, ir in irreps]
+
+
+class O3ScatterTensorProduct(torch.nn.Module):
+    """Edge uvu tensor product + scatter to receivers, on the HIP kernel
+    (replaces ``tace/models/_e3nn/fused.py:172-271``; no parameters)."""
+
+    def __init__(self, irreps_in1, irreps_in2, irreps_out):
+        super().__init__()
+        self.irreps_in1, self.irreps_in2 = Irreps(irreps_in1), Irreps(irreps_in2)
+        paths, self.irreps_out = generate_paths(Irreps(irreps_out), self.irreps_in1, self.irreps_in2, "uvu")
+        self.C = self.irreps_in1[0][0]
+        assert all(m == self.C for m, _ in self.irreps_in1) and all(m == 1 for m, _ in self.irreps_in2)
+        self.weight_numel = self.C * len(paths)
+        self.key = ops.variant_key("uvu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
+
+    def forward(self, x, y, w, plan: ops.EdgePlan):
+        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C)
+
+
+class uuuTensorProduct(torch.nn.Module):
+    """Node uuu product on the HIP kernel (replaces ``fused.py:17-95``)."""
+
+    def __init__(self, irreps_in1, irreps_in2, irreps_out, identical_inputs: bool):
+        super().__init__()
+        self.irreps_in1, self.irreps_in2 = Irreps(irreps_in1), Irreps(irreps_in2)
+        paths, self.irreps_out = generate_paths(Irreps(irreps_out), self.irreps_in1, self.irreps_in2, "uuu",
+                                                identical_inputs)
+        self.C = self.irreps_in1[0][0]
+        self.key = ops.variant_key("uuu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
+
+    def forward(self, x1, x2):
+        return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C)
+
+
+def _gate(x: torch.Tensor, gated: Irreps) -> torch.Tensor:
+    """``O3Gate`` with gate_m0 (``tace/models/_e3nn/nonlinear.py:27-42, 93-143``):
+    x = [one C-block of gates per gated irrep | gated irreps]; the gates go
+    through normalize2mom(sigmoid) and scale their irrep (e3nn's elementwise
+    product with sqrt(2l+1) W3j(l,0,l) is exactly that scaling)."""
+    Z = x.shape[0]
+    ng = sum(m for m, _ in gated)
+    g = torch.sigmoid(x[:, :ng]) * SIGMOID_CST
+    outs, go, xo = [], 0, ng
+    for m, ir in gated:
+        d = ir.dim
+        xi = x[:, xo:xo + m * d]
+        gi = g[:, go:go + m]
+        outs.append(xi * gi if d == 1 else (xi.view(Z, m, d) * gi.unsqueeze(-1)).reshape(Z, m * d))
+        go += m
+        xo += m * d
+    return torch.cat(outs, dim=1)
+
+
+class O3CgtpInteraction(torch.nn.Module):
+    """``O3CgtpInteraction`` (``tace/models/_e3nn/inter.py:28-285``), BB resnet."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements, avg_num_neighbors,
+                 radial_hidden, num_radial):
+        super().__init__()
+        self.layer = layer
+        self.avg_num_neighbors = float(avg_num_neighbors)
+        self.irreps_in = Irreps(irreps_in)
+        sh = spherical_harmonics_irreps(lmax)
+        tp_out = possible_tp_irreps(self.irreps_in, sh, False, Lmax if correlation == 1 else lmax)
+        self.irreps_out = (tp_out * C).regroup()
+        if layer == num_layers - 1:
+            irreps_sc = (Irreps("0e") * C).regroup()
+        else:
+            irreps_sc = (possible_tp_irreps(self.irreps_in, sh, False, Lmax) * C).regroup()
+        self.linear_up = e3nnLinear(self.irreps_in, self.irreps_in, bias=True)
+        self.rejector = O3ScatterTensorProduct(self.irreps_in, sh, self.irreps_out)
+        self.gated = Irreps([(C, ir) for _, ir in self.irreps_out])
+        gates = Irreps([(C, Irrep("0e")) for _ in self.gated])
+        self.linear_nonlinearity = e3nnLinear(self.gated, self.irreps_out, bias=True)
+        self.linear_down = e3nnLinear(self.rejector.irreps_out.simplify(), (gates + self.gated).simplify(), bias=True)
+        self.edge_info = MLP([num_radial] + list(radial_hidden) + [self.rejector.weight_numel])
+        if layer > 0:
+            self.resnetBB = e3nnElementLinear(self.irreps_in, irreps_sc, num_elements, bias=True)
+
+    def forward(self, x, sp: SpeciesPlan, R, Y, plan: ops.EdgePlan):
+        sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
+        x = self.linear_up(x)
+        w = self.edge_info(R)
+        m = self.linear_down(self.rejector(x, Y, w, plan))
+        m = m / self.avg_num_neighbors
+        m = self.linear_nonlinearity(_gate(m, self.gated))
+        return m, sc
+
+
+class CgtpACE(torch.nn.Module):
+    """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``): nu-chain of uuu products
+    and per-species coefficient linears, evaluated on species-sorted nodes."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements, agnostic=False):
+        super().__init__()
+        last = layer == num_layers - 1
+        self.correlation = correlation
+        self.agnostic = agnostic
+        irreps_in = Irreps(irreps_in)
+        hidden = Irreps([(C, ir) for _, ir in irreps_in])
+        tp_out = []
+        for nu in range(2, correlation + 1):
+            if nu == correlation:
+                tp_out.append((Irreps("0e") * C).regroup() if last else
+                              (possible_tp_irreps(hidden, hidden, False, Lmax) * C).regroup())
+            else:
+                tp_out.append(possible_tp_irreps(hidden, hidden, False, lmax))
+        if correlation == 1:
+            coefs_out = Irreps([(C, ir) for _, ir in irreps_in if ir.l <= Lmax])
+        else:
+            coefs_out = (possible_tp_irreps(irreps_in, irreps_in, False, Lmax) * C).regroup()
+        if last:
+            coefs_out = (Irreps("0e") * C).regroup()
+        self.irreps_out = Irreps([(C, ir) for _, ir in coefs_out])
+
+        def mk(irr):
+            if agnostic:
+                return e3nnLinear(irr, coefs_out, bias=True)
+            return e3nnElementLinear(irr, coefs_out, num_elements, bias=True)
+
+        self.coefs = torch.nn.ModuleList([mk(Irreps([(C, ir) for _, ir in hidden]).simplify())])
+        self.aces = torch.nn.ModuleList()
+        in1 = hidden
+        for nu in range(2, correlation + 1):
+            ace = uuuTensorProduct(in1, hidden, tp_out[nu - 2], identical_inputs=(nu == 2))
+            self.aces.append(ace)
+            self.coefs.append(mk(Irreps([(C, ir) for _, ir in ace.irreps_out]).simplify()))
+            in1 = ace.irreps_out
+        self.linear = e3nnLinear(Irreps([(C, ir) for _, ir in coefs_out]), self.irreps_out, bias=True)
+
+    def forward(self, x, sp: SpeciesPlan, sc):
+        if self.agnostic:
+            outs = self.coefs[0](x)
+            feats = x
+            for nu in range(2, self.correlation + 1):
+                feats = self.aces[nu - 2](feats, x)
+                outs = outs + self.coefs[nu - 1](feats)
+        else:
+            xs = x.index_select(0, sp.perm)
+            attrs_s = sp.attrs.index_select(0, sp.perm)
+            outs = self.coefs[0].forward_sorted(xs, sp, attrs_s)
+            feats = xs
+            for nu in range(2, self.correlation + 1):
+                feats = self.aces[nu - 2](feats, xs)
+                outs = outs + self.coefs[nu - 1].forward_sorted(feats, sp, attrs_s)
+            outs = outs.index_select(0, sp.inv)
+        outs = self.linear(outs)
+        return outs + sc if sc is not None else outs
+
+
+class ScalarReadOut(torch.nn.Module):
+    """Last-layer ``ScalarReadOut`` (``tace/models/_e3nn/readout.py:36-84``)."""
+
+    def __init__(self, irreps_in, hidden=(16,)):
+        super().__init__()
+        dims = [Irreps(irreps_in)] + [Irreps(f"{h}x0e") for h in hidden] + [Irreps("1x0e")]
+        self.linear2 = torch.nn.ModuleList(e3nnLinear(a, b, bias=False) for a, b in zip(dims, dims[1:]))
+
+    def forward(self, x):
+        for lin in self.linear2[:-1]:
+            x = torch.nn.functional.silu(lin(x)) * SILU_CST
+        return self.linear2[-1](x)
+
+
+class _Buffers(torch.nn.Module):
+    pass
+
+
+class LinearNodeEmbedding(torch.nn.Module):
+    def __init__(self, S, C):
+        super().__init__()
+        self.elem_emb1 = e3nnLinear(f"{S}x0e", f"{C}x0e", bias=False)
+
+    def forward(self, attrs):
+        return self.elem_emb1(attrs)
+
+
+class RadialBasis(torch.nn.Module):
+    """Buffers of ``RadialBasis`` (j0 + c2poly, ``radial.py:43-84, 437-472, 877-993``)."""
+
+    def __init__(self, cutoff, num_basis, p):
+        super().__init__()
+        self.cutoff_fn = _Buffers()
+        self.cutoff_fn.register_buffer("p", torch.tensor(p, dtype=torch.int))
+        self.cutoff_fn.register_buffer("cutoff", torch.tensor(cutoff, dtype=torch.get_default_dtype()))
+        self.radial_fn = _Buffers()
+        self.radial_fn.register_buffer("bessel_weights", math.pi / cutoff * torch.linspace(
+            1.0, num_basis, num_basis, dtype=torch.get_default_dtype()))
+        self.radial_fn.register_buffer("cutoff", torch.tensor(cutoff, dtype=torch.get_default_dtype()))
+        self.radial_fn.register_buffer("prefactor", torch.tensor(math.sqrt(2.0 / cutoff),
+                                                                 dtype=torch.get_default_dtype()))
+        self.num_basis = num_basis
+
+
+_SUPPORTED = dict(node_embedding="linear", edge_embedding="identity", edge_update="identity")
+
+
+def _check_supported(cfg):
+    for k, v in _SUPPORTED.items():
+        if cfg.get(k, {}).get("type", v) != v:
+            raise NotImplementedError(f"{k}.type={cfg[k]['type']!r} is not on the MI355X path")
+    ab = cfg.get("atomic_basis", {})
+    types = ab.get("type", "cgtp")
+    for t in (types if isinstance(types, list) else [types]):
+        if t != "cgtp":
+            raise NotImplementedError(f"atomic_basis.type={t!r} is not on the MI355X path")
+    nl = ab.get("nonlinear", "sigmoid_gate")
+    for t in (nl if isinstance(nl, list) else [nl]):
+        if t != "sigmoid_gate":
+            raise NotImplementedError(f"atomic_basis.nonlinear={t!r} is not on the MI355X path")
+    if not ab.get("gate_m0", True) or ab.get("scatter_norm", "avg_num_neighbors") != "avg_num_neighbors":
+        raise NotImplementedError("only gate_m0=True and scatter_norm=avg_num_neighbors are supported")
+    rb = cfg.get("radial_basis", {})
+    if rb.get("radial_basis", "j0") not in ("j0", "bessel") or rb.get("cutoff_fn", "c2poly") != "c2poly" \
+            or not rb.get("apply_cutoff", True) or rb.get("bias", False) or rb.get("distance_transform"):
+        raise NotImplementedError("only j0 Bessel x c2poly radial basis (apply_cutoff, no bias) is supported")
+    pb = cfg.get("product_basis", {})
+    if pb.get("type", "cgtp") not in ("cgtp",) and not isinstance(pb.get("type"), list):
+        raise NotImplementedError("only product_basis.type=cgtp is supported")
+    if pb.get("num_expert") not in (None, 1) or pb.get("nonlinear") is not None:
+        raise NotImplementedError("mixture-of-experts / bilinear product basis is not on the MI355X path")
+    rs = cfg.get("resnet", {})
+    if rs.get("type", "BB") != "BB" or rs.get("linear_type", "aware") != "aware" or rs.get("use_first_resnet"):
+        raise NotImplementedError("only resnet type BB, element-aware, no first resnet is supported")
+    if cfg.get("parity", False):
+        raise NotImplementedError("parity=True is not on the MI355X path")
+    if len(cfg.get("fidelity", [0])) != 1:
+        raise NotImplementedError("multi-fidelity heads are not on the MI355X path")
+
+
+class Representation(torch.nn.Module):
+    """``Representation`` (``tace/models/_e3nn/representation.py:28-429``)."""
+
+    def __init__(self, cfg):
+        super().__init__()
+        S = len(cfg["atomic_numbers"])
+        C, L, Lmax = cfg["num_channel"], cfg["lmax"], cfg["Lmax"]
+        self.register_buffer("atomic_numbers", torch.tensor(cfg["atomic_numbers"], dtype=torch.int64))
+        rb = cfg["radial_basis"]
+        self.radial_basis = RadialBasis(cfg["cutoff"], rb["num_radial_basis"], rb["polynomial_cutoff"])
+        self.lmax = L
+        self.node_embedding = LinearNodeEmbedding(S, C)
+        nl = cfg["num_layers"]
+        corr = cfg["product_basis"]["correlation"]
+        corr = corr if isinstance(corr, list) else [corr] * nl
+        self.interactions = torch.nn.ModuleList()
+        self.products = torch.nn.ModuleList()
+        irreps = Irreps(f"{C}x0e")
+        for layer in range(nl):
+            inter = O3CgtpInteraction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
+                                      rb["hidden"], rb["num_radial_basis"])
+            self.interactions.append(inter)
+            prod = CgtpACE(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S,
+                           cfg["product_basis"].get("agnostic", False))
+            self.products.append(prod)
+            irreps = prod.irreps_out
+
+    def edge_features(self, edge_vector: torch.Tensor):
+        rb = self.radial_basis
+        return ops.edge_basis(edge_vector, rb.radial_fn.bessel_weights.to(edge_vector.dtype),
+                              float(rb.radial_fn.prefactor), float(rb.cutoff_fn.cutoff), int(rb.cutoff_fn.p),
+                              self.lmax)
+
+    def forward(self, attrs, plan: ops.EdgePlan, edge_vector):
+        R, Y = self.edge_features(edge_vector)
+        sp = SpeciesPlan(attrs)
+        x = self.node_embedding(attrs)
+        for inter, prod in zip(self.interactions, self.products):
+            x, sc = inter(x, sp, R, Y, plan)
+            x = prod(x, sp, sc)
+        return x
+
+
+class TACE(torch.nn.Module):
+    """MI355X ``e3nnTACE`` (energy readout; ``tace/models/_e3nn/tace.py:28-790``)."""
+
+    def __init__(self, **cfg):
+        super().__init__()
+        cfg = copy.deepcopy(cfg)
+        if "atomic_numbers" not in cfg or cfg["atomic_numbers"] is None:
+            cfg["atomic_numbers"] = sorted({z for s in cfg["statistics"] for z in s["atomic_numbers"]})
+        if "avg_num_neighbors" not in cfg:
+            cfg["avg_num_neighbors"] = sum(s["avg_num_neighbors"] for s in cfg["statistics"]) / len(cfg["statistics"])
+        _check_supported(cfg)
+        self.model_config = cfg
+        self.target_property = list(cfg["target_property"])
+        self.embedding_property = list(cfg.get("embedding_property", []))
+        self.statistics = cfg["statistics"]
+        self.fidelity = cfg.get("fidelity", [dict(name="PBE", atomic_energy=None)])
+        self.max_neighbors = cfg.get("max_neighbors")
+        zs = cfg["atomic_numbers"]
+        self.register_buffer("cutoff", torch.tensor(cfg["cutoff"], dtype=torch.get_default_dtype()))
+        self.register_buffer("atomic_numbers", torch.tensor(zs, dtype=torch.int64))
+        self.representation = Representation(cfg)
+        C = cfg["num_channel"]
+        self.energy_readouts = torch.nn.ModuleList([ScalarReadOut(f"{C}x0e", cfg["readout_emlp"]["hidden"])])
+        stats = cfg["statistics"]
+        self.atomic_energy_layer = _Buffers()
+        self.atomic_energy_layer.register_buffer("atomic_energy", torch.tensor(
+            [[float({int(k): v for k, v in s["atomic_energy"].items()}.get(z, 0.0)) for z in zs] for s in stats],
+            dtype=torch.get_default_dtype()))
+        self.scale_shift = _Buffers()
+        self.scale_shift.register_buffer("atomic_numbers", torch.tensor(zs, dtype=torch.int64))
+        self.scale_shift.register_buffer("scale", torch.tensor(
+            [[float({int(k): v for k, v in s["rms_forces"].items()}.get(z, 1.0)) for z in zs] for s in stats],
+            dtype=torch.get_default_dtype()))
+        self.scale_shift.register_buffer("shift", torch.zeros(len(stats), len(zs), dtype=torch.get_default_dtype()))
+
+    def energy(self, data, plan: ops.EdgePlan, edge_vector):
+        """Energy branch of ``readout_fn`` (``tace.py:356-418``) + ``ScaleShift``
+        (``blocks.py:289-379``), fidelity 0."""
+        attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
+        num_graphs = ptr.numel() - 1
+        x = self.representation(attrs, plan, edge_vector)
+        e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
+        e_node = self.energy_readouts[0](x)[:, 0]
+        num_nodes = ptr[1:] - ptr[:-1]
+        ei = data["edge_index"]
+        num_edges = torch.zeros(num_graphs, dtype=torch.int64, device=attrs.device)
+        if ei.numel():
+            num_edges = num_edges.index_add(0, batch[ei[1]], torch.ones_like(ei[1]))
+        isolated = ((num_nodes == 1) & (num_edges == 0))[batch]
+        scale = (attrs * self.scale_shift.scale[0]).sum(-1)
+        e_node = e_node * torch.where(isolated, torch.zeros_like(scale), scale)
+        shift = (attrs * self.scale_shift.shift[0]).sum(-1)
+        e_node = e_node + torch.where(isolated, torch.zeros_like(shift), shift)
+        zeros = torch.zeros(num_graphs, dtype=attrs.dtype, device=attrs.device)
+        E = zeros.index_add(0, batch, e_base) + zeros.index_add(0, batch, e_node)
+        return E, e_base + e_node
+
+
+class TensorModel(torch.nn.Module):
+    """``TensorModel`` (``tace/models/adapter.py:23-452``) for energy, forces,
+    stress/virials: ``forward(data) -> {energy, node_energy, forces, stress, virials}``."""
+
+    def __init__(self, readout_fn: TACE):
+        super().__init__()
+        self.readout_fn = readout_fn
+        self.fidelity_idx = 0
+        self.lmp = False
+
+    # getters used by the ASE / TorchSim / LAMMPS callers (adapter.py:386-452)
+    def get_cutoff(self) -> float:
+        return float(self.readout_fn.cutoff.item())
+
+    def get_atomic_numbers(self):
+        return [int(z) for z in self.readout_fn.atomic_numbers.cpu().tolist()]
+
+    def get_model_dtype(self):
+        return self.readout_fn.cutoff.dtype
+
+    def get_target_property(self):
+        return list(set(self.readout_fn.target_property))
+
+    def get_embedding_property(self):
+        return list(self.readout_fn.embedding_property)
+
+    def get_max_neighbors(self):
+        return self.readout_fn.max_neighbors
+
+    def get_fidelity_idx(self) -> int:
+        return int(self.fidelity_idx)
+
+    def reset_fidelity_idx(self, fidelity_idx=0):
+        if fidelity_idx is not None:
+            self.fidelity_idx = fidelity_idx
+
+    def reset_target_property(self, target_property):
+        self.readout_fn.target_property = list(target_property)
+
+    def forward(self, data: Dict[str, torch.Tensor]) -> Dict[str, Optional[torch.Tensor]]:
+        tp = set(self.get_target_property())
+        want_f = "forces" in tp
+        want_s = bool({"stress", "virials"} & tp)
+        pos = data["positions"]
+        if not pos.is_cuda:
+            raise RuntimeError("tace_amd.TensorModel runs on the GPU only (positions are on %s)" % pos.device)
+        pos = pos.detach().requires_grad_(want_f or want_s)
+        lattice, batch = data["lattice"], data["batch"]
+        num_graphs = data["ptr"].numel() - 1
+        inputs = [pos] if want_f else []
+        if want_s:
+            # compute_symmetric_displacement (tace/models/utils.py:50-79)
+            disp = torch.zeros(num_graphs, 3, 3, dtype=pos.dtype, device=pos.device, requires_grad=True)
+            sym = 0.5 * (disp + disp.transpose(-1, -2))
+            pos_s = pos + torch.einsum("be,bec->bc", pos, sym[batch])
+            lat_s = lattice + torch.matmul(lattice, sym)
+            inputs.append(disp)
+        else:
+            pos_s, lat_s = pos, lattice
+        ei = data["edge_index"]
+        plan = data.get("_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
+        src, dst = ei[0], ei[1]
+        # prepare_graph (adapter.py:334-347); the +1e-9 of the length is applied in the kernel
+        vec = pos_s[dst] - pos_s[src] + torch.einsum("ni,nij->nj", data["edge_shifts"], lat_s[batch[src]])
+        E, e_node = self.readout_fn.energy(data, plan, vec)
+        out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, stress=None,
+                                                      virials=None)
+        if inputs:
+            grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True)
+            k = 0
+            if want_f:
+                out["forces"] = -grads[0] if grads[0] is not None else torch.zeros_like(pos)
+                k = 1
+            if want_s:
+                V = -grads[k] if grads[k] is not None else torch.zeros_like(lattice)
+                vol = torch.linalg.det(lattice).abs().view(-1, 1, 1)
+                S = -V / vol
+                out["virials"] = V
+                out["stress"] = torch.where(S.abs() < 1e10, S, torch.zeros_like(S))
+        out["energy"] = out["energy"].detach()
+        out["node_energy"] = out["node_energy"].detach()
+        return out
+
+
+# ------------------------------------------------------------- checkpoints ----
+_E3NN_INTERNAL = ("output_mask", "_compiled", ".tp.", ".sc.", ".act_gates.", ".mul.", "._bias_index",
+                  "._bias_mask", ".cut.")
+
+
+def load_reference_state_dict(model: torch.nn.Module, state_dict: Dict[str, torch.Tensor]):
+    """``load_state_dict(strict=True)`` semantics for every parameter and buffer
+    this model owns; keys that only e3nn's internal modules register in a
+    reference checkpoint (masks, compiled-graph constants) are ignored."""
+    own = model.state_dict()
+    extra = [k for k in state_dict if k not in own]
+    unknown = [k for k in extra if not any(t in k for t in _E3NN_INTERNAL)]
+    if unknown:
+        raise RuntimeError(f"unexpected keys in state_dict: {unknown[:8]}")
+    missing = [k for k in own if k not in state_dict]
+    if missing:
+        raise RuntimeError(f"missing keys in state_dict: {missing[:8]}")
+    model.load_state_dict({k: v for k, v in state_dict.items() if k in own}, strict=True)
+    return model
+
+
+def create_model(cfg: Dict) -> TensorModel:
+    """``create_model`` (``tace/lightning/torch_model.py:54-114``) for the MI355X path."""
+    return TensorModel(TACE(**cfg))

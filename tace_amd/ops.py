@@ -1,0 +1,282 @@
+"""Autograd operators over the HIP kernels of ``libtace_hip.so``.
+
+Each operator checks device, dtype, contiguity and shapes on the host before
+launching (the kernels trust these), launches on torch's current stream, and
+raises if the native library is missing -- there is no CPU path.
+
+* ``edge_basis``      radial basis x cutoff and SH of edge vectors
+                      (``tace/models/radial.py:974-993``, ``angular.py:288-315``)
+* ``edge_tp_scatter`` uvu tensor product fused with the receiver scatter
+                      (``tace/models/_e3nn/fused.py:259-271``)
+* ``uuu_tp``          node-level uuu product (``fused.py:90-95``)
+* ``neighbour_list``  cell-list neighbour search (``dataset/neighbour_list.py:195-298``)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _native as N
+
+
+class KernelTimer:
+    """Optional HIP-event bracketing of every native launch, on the stream the
+    kernel runs on (torch's current stream).  ``ops.TIMER = KernelTimer()``
+    enables it; ``summary()`` returns {name: (launches, total_ms)}."""
+
+    def __init__(self):
+        self.events = {}
+
+    def start(self, name):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        return name, e0
+
+    def stop(self, tok, info=None):
+        name, e0 = tok
+        e1 = torch.cuda.Event(enable_timing=True)
+        e1.record()
+        self.events.setdefault(name, []).append((e0, e1, info))
+
+    def summary(self):
+        torch.cuda.synchronize()
+        return {k: (len(v), sum(a.elapsed_time(b) for a, b, _ in v), [i for _, _, i in v]) for k, v in self.events.items()}
+
+
+TIMER = None
+
+
+def _t0(name):
+    return TIMER.start(name) if TIMER is not None else None
+
+
+def _t1(tok, info=None):
+    if tok is not None:
+        TIMER.stop(tok, info)
+
+
+def variant_key(kind: str, in1: Sequence[int], in2: Sequence[int], out: Sequence[int]) -> str:
+    j = lambda s: ",".join(str(int(v)) for v in s)
+    return f"{kind}|{j(in1)}|{j(in2)}|{j(out)}"
+
+
+@dataclass(frozen=True)
+class TpVariant:
+    vid: int
+    key: str
+    npath: int
+    d1: int
+    d2: int
+    dout: int
+
+
+_VCACHE = {}
+
+
+def find_variant(key: str) -> TpVariant:
+    if key not in _VCACHE:
+        L = N.lib()
+        vid = L.tace_tp_find(key.encode())
+        if vid < 0:
+            raise N.NativeError(L.tace_last_error().decode())
+        a, b, c, d = (np.zeros(1, np.int32) for _ in range(4))
+        N.check(L.tace_tp_dims(vid, a.ctypes.data, b.ctypes.data, c.ctypes.data, d.ctypes.data), "tace_tp_dims")
+        _VCACHE[key] = TpVariant(vid, key, int(a[0]), int(b[0]), int(c[0]), int(d[0]))
+    return _VCACHE[key]
+
+
+def _req(t: torch.Tensor, name: str, dtype, shape=None):
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+# ------------------------------------------------------------ edge plan ----
+@dataclass
+class EdgePlan:
+    """Receiver-CSR view of an edge list: edge ids sorted by ``dst``.
+
+    ``eid`` is None when the edges are already grouped by receiver (as the GPU
+    neighbour list emits them)."""
+
+    n_nodes: int
+    n_edges: int
+    rowptr: torch.Tensor           # int32 [N+1]
+    src: torch.Tensor              # int32 [E], sender of edge id
+    eid: Optional[torch.Tensor]    # int32 [E] or None
+
+    @staticmethod
+    def from_edge_index(edge_index: torch.Tensor, n_nodes: int) -> "EdgePlan":
+        src, dst = edge_index[0], edge_index[1]
+        E = int(src.shape[0])
+        if E and (int(torch.minimum(src.min(), dst.min())) < 0
+                  or int(torch.maximum(src.max(), dst.max())) >= n_nodes):
+            raise ValueError("edge_index refers to nodes outside [0, n_nodes)")
+        if E >= 2 ** 31 or n_nodes >= 2 ** 31:
+            raise ValueError("edge/node counts exceed the int32 CSR indexing of the kernels")
+        counts = torch.bincount(dst, minlength=n_nodes)
+        rowptr = torch.zeros(n_nodes + 1, dtype=torch.int64, device=dst.device)
+        rowptr[1:] = torch.cumsum(counts, 0)
+        if E > 0 and bool((dst[1:] >= dst[:-1]).all()):
+            eid = None
+        else:
+            eid = torch.argsort(dst, stable=True).to(torch.int32).contiguous()
+        return EdgePlan(n_nodes, E, rowptr.to(torch.int32).contiguous(), src.to(torch.int32).contiguous(), eid)
+
+
+# ------------------------------------------------------- edge featurisation ----
+class _EdgeBasis(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, vec, bessel_w, prefactor: float, cutoff: float, p: int, lmax: int):
+        E = vec.shape[0]
+        nb = bessel_w.shape[0]
+        _req(vec, "edge_vector", vec.dtype, (E, 3))
+        _req(bessel_w, "bessel_weights", vec.dtype, (nb,))
+        R = torch.empty(E, nb, dtype=vec.dtype, device=vec.device)
+        Y = torch.empty(E, (lmax + 1) ** 2, dtype=vec.dtype, device=vec.device)
+        tok = _t0("edge_basis_fwd")
+        N.check(N.lib().tace_edge_basis_fwd(N.dtype_code(vec.dtype), vec.data_ptr(), E, nb, bessel_w.data_ptr(),
+                                            prefactor, cutoff, p, lmax, R.data_ptr(), Y.data_ptr(),
+                                            N.stream_ptr(vec.device)), "tace_edge_basis_fwd")
+        _t1(tok, (E,))
+        ctx.save_for_backward(vec, bessel_w)
+        ctx.args = (prefactor, cutoff, p, lmax)
+        return R, Y
+
+    @staticmethod
+    def backward(ctx, gR, gY):
+        vec, bw = ctx.saved_tensors
+        prefactor, cutoff, p, lmax = ctx.args
+        E, nb = vec.shape[0], bw.shape[0]
+        gR = torch.zeros(E, nb, dtype=vec.dtype, device=vec.device) if gR is None else gR.contiguous()
+        gY = torch.zeros(E, (lmax + 1) ** 2, dtype=vec.dtype, device=vec.device) if gY is None else gY.contiguous()
+        gvec = torch.empty_like(vec)
+        tok = _t0("edge_basis_bwd")
+        N.check(N.lib().tace_edge_basis_bwd(N.dtype_code(vec.dtype), vec.data_ptr(), gR.data_ptr(), gY.data_ptr(), E,
+                                            nb, bw.data_ptr(), prefactor, cutoff, p, lmax, gvec.data_ptr(),
+                                            N.stream_ptr(vec.device)), "tace_edge_basis_bwd")
+        _t1(tok, (E,))
+        return gvec, None, None, None, None, None
+
+
+def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cutoff: float, p: int,
+               lmax: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    return _EdgeBasis.apply(vec.contiguous(), bessel_w.contiguous(), float(prefactor), float(cutoff), int(p),
+                            int(lmax))
+
+
+# ------------------------------------------------------ edge tensor product ----
+class _EdgeTP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int):
+        Nn, E = plan.n_nodes, plan.n_edges
+        dt = x.dtype
+        _req(x, "x", dt, (Nn, C * var.d1))
+        _req(y, "y", dt, (E, var.d2))
+        _req(w, "w", dt, (E, C * var.npath))
+        out = torch.empty(Nn, C * var.dout, dtype=dt, device=x.device)
+        tok = _t0("edge_tp_fwd:" + var.key)
+        N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                         plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), Nn, E, C,
+                                         out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
+        _t1(tok, (Nn, E, C))
+        ctx.save_for_backward(x, y, w)
+        ctx.plan, ctx.var, ctx.C = plan, var, C
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x, y, w = ctx.saved_tensors
+        plan, var, C = ctx.plan, ctx.var, ctx.C
+        gout = gout.contiguous()
+        need_x = ctx.needs_input_grad[0]
+        gx = torch.empty_like(x) if need_x else None
+        gy = torch.empty_like(y)
+        gw = torch.empty_like(w)
+        tok = _t0("edge_tp_bwd:" + var.key)
+        N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                         gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
+                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, N.ptr(gx),
+                                         gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
+        _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
+        return gx, gy, gw, None, None, None
+
+
+def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int) -> torch.Tensor:
+    return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C)
+
+
+# ---------------------------------------------------------------- uuu ----
+class _UUU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x1, x2, var: TpVariant, C: int):
+        Nn = x1.shape[0]
+        dt = x1.dtype
+        _req(x1, "x1", dt, (Nn, C * var.d1))
+        _req(x2, "x2", dt, (Nn, C * var.d2))
+        out = torch.empty(Nn, C * var.dout, dtype=dt, device=x1.device)
+        tok = _t0("uuu_fwd:" + var.key)
+        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), Nn, C, out.data_ptr(),
+                                     N.stream_ptr(x1.device)), "tace_uuu_fwd")
+        _t1(tok, (Nn, C))
+        ctx.save_for_backward(x1, x2)
+        ctx.var, ctx.C = var, C
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x1, x2 = ctx.saved_tensors
+        gout = gout.contiguous()
+        g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
+        tok = _t0("uuu_bwd:" + ctx.var.key)
+        N.check(N.lib().tace_uuu_bwd(ctx.var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(),
+                                     gout.data_ptr(), x1.shape[0], ctx.C, g1.data_ptr(), g2.data_ptr(),
+                                     N.stream_ptr(x1.device)), "tace_uuu_bwd")
+        _t1(tok, (x1.shape[0], ctx.C))
+        return g1, g2, None, None
+
+
+def uuu_tp(x1, x2, var: TpVariant, C: int) -> torch.Tensor:
+    return _UUU.apply(x1.contiguous(), x2.contiguous(), var, C)
+
+
+# ------------------------------------------------------------ neighbours ----
+def neighbour_list(positions: torch.Tensor, cell, pbc, cutoff: float):
+    """GPU cell-list neighbour search (float64).
+
+    Returns ``(rowptr int32 [N+1], src int32 [E], shifts int32 [E,3])`` with
+    edges grouped by receiver: receiver of slot k is the n with
+    rowptr[n] <= k < rowptr[n+1].  Edge vector = r[dst] - r[src] + S.cell."""
+    _req(positions, "positions", torch.float64)
+    n = positions.shape[0]
+    dev = positions.device
+    cell_np = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(3, 3))
+    pbc_np = np.ascontiguousarray(np.broadcast_to(np.asarray(pbc, dtype=np.int32), (3,)))
+    L = N.lib()
+    nbytes = L.tace_nl_workspace_bytes(n, cell_np.ctypes.data, pbc_np.ctypes.data, float(cutoff))
+    if nbytes < 0:
+        raise N.NativeError(L.tace_last_error().decode())
+    ws = torch.empty(max(int(nbytes), 4), dtype=torch.uint8, device=dev)
+    counts = torch.empty(n, dtype=torch.int32, device=dev)
+    s = N.stream_ptr(dev)
+    N.check(L.tace_nl_count(positions.data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data, float(cutoff),
+                            ws.data_ptr(), int(nbytes), counts.data_ptr(), s), "tace_nl_count")
+    rowptr = torch.empty(n + 1, dtype=torch.int32, device=dev)
+    N.check(L.tace_scan_i32(counts.data_ptr(), n, rowptr.data_ptr(), s), "tace_scan_i32")
+    E = int(rowptr[-1].item())
+    src = torch.empty(E, dtype=torch.int32, device=dev)
+    shifts = torch.empty(E, 3, dtype=torch.int32, device=dev)
+    if E > 0:
+        N.check(L.tace_nl_fill(positions.data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data, float(cutoff),
+                               ws.data_ptr(), rowptr.data_ptr(), src.data_ptr(), shifts.data_ptr(), s),
+                "tace_nl_fill")
+    return rowptr, src, shifts

@@ -1,0 +1,186 @@
+"""Operator-level parity of the HIP kernels against the CPU oracle (GPU).
+
+Tolerances: float64 to 1e-11 (relative to the largest magnitude), float32
+to 2e-5 relative -- the kernels and the oracle sum in different orders.
+"""
+
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from oracle import neighbours as onl
+from oracle import so3 as oso3
+from tace_amd import ops, structures
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-11, torch.float32: 2e-5}
+
+
+def close(got, want, dtype, what=""):
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    scale = max(want.abs().max().item(), 1e-30)
+    err = (got - want).abs().max().item() / scale
+    assert err < TOL[dtype], f"{what}: max rel err {err:.3e} (scale {scale:.3e})"
+
+
+def _irreps(ls, C):
+    return [(C, (l, (-1) ** l)) for l in ls]
+
+
+# ------------------------------------------------------------ edge basis ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax", [0, 1, 2, 3])
+def test_edge_basis_matches_oracle(cuda, dtype, lmax):
+    g = torch.Generator().manual_seed(lmax)
+    E, rc, nb, p = 3000, 5.0, 8, 5
+    d = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    d = d / d.norm(dim=1, keepdim=True) * (0.3 + 6.5 * torch.rand(E, 1, generator=g, dtype=torch.float64))
+    vec = d.to(dtype).double().requires_grad_(True)  # same values the GPU sees
+    rb = om.RadialBasis(rc, nb, p).double()
+    length = (vec ** 2).sum(1, keepdim=True).sqrt() + 1e-9
+    R_o = rb(length)
+    Y_o = oso3.spherical_harmonics(lmax, vec / length)
+    gR = torch.randn(E, nb, generator=g, dtype=torch.float64)
+    gY = torch.randn(E, (lmax + 1) ** 2, generator=g, dtype=torch.float64)
+    (gv_o,) = torch.autograd.grad((R_o * gR).sum() + (Y_o * gY).sum(), vec)
+
+    v = vec.detach().to(dtype).to(cuda).requires_grad_(True)
+    bw = (math.pi / rc * torch.linspace(1.0, nb, nb, dtype=torch.float64)).to(dtype).to(cuda)
+    R, Y = ops.edge_basis(v, bw, math.sqrt(2.0 / rc), rc, p, lmax)
+    close(R, R_o, dtype, "radial")
+    close(Y, Y_o, dtype, "sh")
+    (gv,) = torch.autograd.grad((R * gR.to(dtype).to(cuda)).sum() + (Y * gY.to(dtype).to(cuda)).sum(), v)
+    tol = {torch.float64: 1e-10, torch.float32: 1e-4}[dtype]
+    err = ((gv.double().cpu() - gv_o).abs().max() / gv_o.abs().max()).item()
+    assert err < tol, err
+
+
+# ------------------------------------------------- edge tensor product ----
+TP_CASES = [([0], 2, 64), ([0], 3, 128), ([0, 1, 2], 2, 64), ([0, 1, 2, 3], 3, 128), ([0, 1, 2], 3, 64),
+            ([0, 1], 1, 96)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("in1,lmax,C", TP_CASES)
+@pytest.mark.parametrize("sorted_edges", [True, False])
+def test_edge_tp_scatter_matches_oracle(cuda, dtype, in1, lmax, C, sorted_edges):
+    g = torch.Generator().manual_seed(C + lmax + len(in1))
+    Nn, E = 37, 260
+    src = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.randint(0, Nn - 3, (E,), generator=g)  # the last receivers get no edges
+    if sorted_edges:
+        order = torch.argsort(dst, stable=True)
+        src, dst = src[order], dst[order]
+    ei = torch.stack([src, dst])
+    tp = om.ScatterTP(_irreps(in1, C), oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)])
+    x = torch.randn(Nn, oso3.irreps_dim(_irreps(in1, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    y = torch.randn(E, (lmax + 1) ** 2, generator=g, dtype=torch.float64).to(dtype).double()
+    w = torch.randn(E, tp.weight_numel, generator=g, dtype=torch.float64).to(dtype).double()
+    x.requires_grad_(True), y.requires_grad_(True), w.requires_grad_(True)
+    out_o = tp(x, y, w, ei)
+    go = torch.randn(out_o.shape, generator=g, dtype=torch.float64).to(dtype).double()
+    gx_o, gy_o, gw_o = torch.autograd.grad((out_o * go).sum(), [x, y, w])
+
+    key = ops.variant_key("uvu", in1, list(range(lmax + 1)), list(range(lmax + 1)))
+    var = ops.find_variant(key)
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), Nn)
+    assert (plan.eid is None) == sorted_edges
+    xg, yg, wg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, y, w))
+    out = ops.edge_tp_scatter(xg, yg, wg, plan, var, C)
+    close(out, out_o, dtype, "out")
+    gx, gy, gw = torch.autograd.grad((out * go.to(dtype).to(cuda)).sum(), [xg, yg, wg])
+    close(gx, gx_o, dtype, "grad_x")
+    close(gy, gy_o, dtype, "grad_y")
+    close(gw, gw_o, dtype, "grad_w")
+
+
+def test_edge_tp_forward_is_deterministic(cuda):
+    g = torch.Generator().manual_seed(0)
+    Nn, E, C = 50, 900, 128
+    ei = torch.stack([torch.randint(0, Nn, (E,), generator=g), torch.randint(0, Nn, (E,), generator=g)]).to(cuda)
+    var = ops.find_variant(ops.variant_key("uvu", [0, 1, 2, 3], [0, 1, 2, 3], [0, 1, 2, 3]))
+    x = torch.randn(Nn, C * 16, generator=g).to(cuda)
+    y = torch.randn(E, 16, generator=g).to(cuda)
+    w = torch.randn(E, C * var.npath, generator=g).to(cuda)
+    plan = ops.EdgePlan.from_edge_index(ei, Nn)
+    a = ops.edge_tp_scatter(x, y, w, plan, var, C)
+    b = ops.edge_tp_scatter(x, y, w, plan, var, C)
+    assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ uuu ----
+def _uuu_cases():
+    out = []
+    for L in (1, 2, 3):
+        full = list(range(L + 1))
+        nu2 = om.UUUTP(_irreps(full, 1), _irreps(full, 1), [(1, (l, (-1) ** l)) for l in full], True)
+        nu2_ls = [ir[0] for _, ir in nu2.out]
+        out.append((full, full, full))
+        out.append((full, full, [0]))
+        out.append((nu2_ls, full, full))
+        out.append((nu2_ls, full, [0]))
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("in1,in2,outl", _uuu_cases())
+def test_uuu_matches_oracle(cuda, dtype, in1, in2, outl):
+    C = 64 if len(in1) > 8 else 96
+    g = torch.Generator().manual_seed(len(in1) * 7 + len(outl))
+    Nn = 29
+    ident = in1 == in2
+    tp = om.UUUTP(_irreps(in1, C), _irreps(in2, C), [(1, (l, (-1) ** l)) for l in outl], ident)
+    x1 = torch.randn(Nn, oso3.irreps_dim(_irreps(in1, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    x2 = torch.randn(Nn, oso3.irreps_dim(_irreps(in2, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    x1.requires_grad_(True), x2.requires_grad_(True)
+    o = tp(x1, x2)
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64).to(dtype).double()
+    g1o, g2o = torch.autograd.grad((o * go).sum(), [x1, x2])
+    var = ops.find_variant(ops.variant_key("uuu", in1, in2, outl))
+    a, b = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x1, x2))
+    out = ops.uuu_tp(a, b, var, C)
+    close(out, o, dtype, "out")
+    g1, g2 = torch.autograd.grad((out * go.to(dtype).to(cuda)).sum(), [a, b])
+    close(g1, g1o, dtype, "g1")
+    close(g2, g2o, dtype, "g2")
+
+
+# ------------------------------------------------------------ neighbours ----
+def _nl_cases():
+    rng = np.random.default_rng(11)
+    cases = [("si", structures.si_diamond(seed=1), 5.0),
+             ("si_perfect", structures.si_diamond(sigma=0.0), 5.0),
+             ("fcc", structures.fcc_alloy(reps=(4, 4, 3), seed=2), 5.0),
+             ("bcc", structures.bcc_fe(reps=(5, 5, 5), seed=3), 5.0),
+             ("water", structures.water_box(n_side=4, box=12.425, seed=4), 6.0)]
+    for k in range(4):
+        cases.append((f"tri{k}", structures.random_crystal(rng, int(rng.integers(4, 40)), [1, 8, 26]), 6.0))
+    s = structures.si_diamond(seed=5)
+    s = dict(s, positions=s["positions"] + np.array([7.0, -13.0, 30.0]))  # atoms far outside the cell
+    cases.append(("shifted", s, 5.0))
+    return cases
+
+
+@pytest.mark.parametrize("name,s,rc", _nl_cases(), ids=[c[0] for c in _nl_cases()])
+def test_neighbour_list_bit_exact_edge_set(cuda, name, s, rc):
+    ei_o, S_o = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)
+    pos = torch.as_tensor(np.asarray(s["positions"], dtype=np.float64), device=cuda)
+    rowptr, src, sh = ops.neighbour_list(pos, s["cell"], s["pbc"], rc)
+    n = len(s["positions"])
+    counts = (rowptr[1:] - rowptr[:-1]).cpu().numpy()
+    dst = np.repeat(np.arange(n), counts)
+    src = src.cpu().numpy().astype(np.int64)
+    sh = sh.cpu().numpy().astype(np.int64)
+    got = sorted(zip(src.tolist(), dst.tolist(), map(tuple, sh.tolist())))
+    want = sorted(zip(ei_o[0].tolist(), ei_o[1].tolist(), map(tuple, S_o.tolist())))
+    assert len(got) == len(want)
+    assert got == want
+    # deterministic output order
+    r2, s2, h2 = ops.neighbour_list(pos, s["cell"], s["pbc"], rc)
+    assert torch.equal(r2, rowptr) and np.array_equal(s2.cpu().numpy(), src) and np.array_equal(h2.cpu().numpy(), sh)

@@ -1,0 +1,106 @@
+"""End-to-end parity of the MI355X model against the CPU oracle (GPU).
+
+Same seeded structure and the same weights (the oracle's state_dict loaded
+into the HIP model).  Bars: float64 energies to 1e-10
+relative and forces to 1e-8 eV/A; float32 energies to 1e-5 relative and
+forces to 1e-4 eV/A (float32 GPU against the float64 oracle).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from oracle import neighbours as onl
+from tace_amd import configs, data, model as pm, structures
+
+pytestmark = pytest.mark.gpu
+
+BARS = {torch.float64: (1e-10, 1e-8, 1e-8), torch.float32: (1e-5, 1e-4, 1e-4)}
+
+
+def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, **over):
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS[preset]["cutoff"])
+             for s in structs]
+    zs = sorted({int(z) for s in structs for z in s["numbers"]})
+    nat = sum(len(s["positions"]) for s in structs)
+    avg = sum(e[0].shape[1] for e in edges) / nat
+    cfg = configs.model_cfg(preset, zs, avg, **over)
+    torch.manual_seed(seed)
+    ref = om.TACE(cfg).double()
+    d64 = data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float64)
+    want = om.compute(ref, d64, forces=True, stress=stress)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        gpu = pm.create_model(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    pm.load_reference_state_dict(gpu.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
+                                                  for k, v in ref.state_dict().items()})
+    gpu = gpu.to(cuda)
+    if not stress:
+        gpu.reset_target_property(["energy", "forces"])
+    dg = data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda)
+    got = gpu(dg)
+    return got, want
+
+
+def _check(got, want, dtype, stress=False):
+    e_rel, f_abs, s_abs = BARS[dtype]
+    E, E0 = got["energy"].double().cpu(), want["energy"]
+    assert ((E - E0).abs() / E0.abs()).max().item() < e_rel, (E, E0)
+    F, F0 = got["forces"].double().cpu(), want["forces"]
+    assert (F - F0).abs().max().item() < f_abs, (F - F0).abs().max().item()
+    # the model's forces are small at random init: also require relative agreement
+    assert (F - F0).abs().max().item() <= 1e-3 * F0.abs().max().item() + f_abs * 1e-2
+    if stress:
+        S, S0 = got["stress"].double().cpu(), want["stress"]
+        assert (S - S0).abs().max().item() < s_abs
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_si64_energy_forces_stress(cuda, dtype):
+    """Config 1 architecture: C=64, L=2, 2 layers, correlation 3, E/F/S."""
+    got, want = _run_pair([structures.si_diamond(seed=1)], "si64", cuda, dtype, stress=True)
+    _check(got, want, dtype, stress=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_fcc_alloy_slice(cuda, dtype):
+    """Config 2 architecture (C=128, L=3, 2 layers) on a 4x4x2 slice (128 atoms, 4 species)."""
+    got, want = _run_pair([structures.fcc_alloy(reps=(4, 4, 2), seed=2)], "fcc1024", cuda, dtype)
+    _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32])
+def test_water_slice(cuda, dtype):
+    """Config 3 architecture (C=128, L=3, 3 layers, r_c=6) on 64 molecules."""
+    got, want = _run_pair([structures.water_box(n_side=4, box=12.425, seed=3)], "water12k", cuda, dtype)
+    _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_ragged_batch_with_stress(cuda, dtype):
+    """Config 4 shape on a small ragged batch: triclinic cells, several species, E/F/S per crystal."""
+    rng = np.random.default_rng(5)
+    structs = [structures.random_crystal(rng, int(rng.integers(8, 30)), [3, 8, 14, 26, 29]) for _ in range(3)]
+    got, want = _run_pair(structs, "ragged128", cuda, dtype, stress=True, num_channel=32)
+    _check(got, want, dtype, stress=True)
+
+
+def test_gpu_neighbour_list_feeds_model(cuda):
+    """The GPU-built graph (receiver-grouped edges) gives the oracle-NL energies."""
+    s = structures.fcc_alloy(reps=(3, 3, 2), seed=6)
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], 5.0)]
+    cfg = configs.model_cfg("fcc1024", sorted(set(s["numbers"].tolist())), edges[0][0].shape[1] / len(s["numbers"]),
+                            num_channel=32)
+    torch.manual_seed(1)
+    gpu = pm.create_model(cfg).double().to(cuda)
+    gpu.reset_target_property(["energy", "forces"])
+    a = gpu(data.collate([s], edges, cfg["atomic_numbers"], dtype=torch.float64, device=cuda))
+    g = data.gpu_graph([s], cfg["atomic_numbers"], 5.0, dtype=torch.float64, device=cuda)
+    assert bool((g["edge_index"][1][1:] >= g["edge_index"][1][:-1]).all())
+    b = gpu(g)
+    assert abs(a["energy"] - b["energy"]).max().item() < 1e-10 * abs(a["energy"]).max().item()
+    assert (a["forces"] - b["forces"]).abs().max().item() < 1e-10

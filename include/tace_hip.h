@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 1
+#define TACE_HIP_ABI_VERSION 3
 #define TACE_F32 0
 #define TACE_F64 1
 
@@ -58,17 +58,30 @@ int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dou
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
                      const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
                      void* out, void* stream);
-/* Gradients of sum(gout * out): gx [N, C*d1] (NULL to skip; zeroed then
- * accumulated), gy [E, d2], gw [E, C*npath] (both fully overwritten). */
+/* Gradients of sum(gout * out): gy [E, d2], gw [E, C*npath]; gx [N, C*d1]
+ * (NULL to skip).  All outputs are fully overwritten, no atomics: the
+ * per-edge grad_x contributions go to `workspace` (>= E*C*d1 elements, one
+ * row per receiver-sorted slot) and are summed per sender through the sender
+ * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender. */
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, void* gx, void* gy, void* gw, void* stream);
+                     int32_t channels, const int32_t* s_rowptr, const int32_t* s_slot, void* workspace,
+                     int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
 
-/* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout]. */
-int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels, void* out,
-                 void* stream);
+/* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
+ * layout: TACE_LAYOUT_IN1_GROUPED / TACE_LAYOUT_OUT_GROUPED select, for x1
+ * (and g1) / out (and gout), the group-major layout instead of e3nn's: the
+ * runs of equal-l blocks that Irreps.simplify() merges form groups g, and
+ * group g of the whole batch is one row-major [N, 2l+1, count_g*C] matrix at
+ * element offset N*C*goff_g -- the operand layout of the per-species
+ * coefficient GEMMs that consume it.  x2 / g2 always use e3nn's layout.
+ * Accepted layouts: 0, OUT_GROUPED, IN1_GROUPED|OUT_GROUPED. */
+#define TACE_LAYOUT_IN1_GROUPED 1
+#define TACE_LAYOUT_OUT_GROUPED 2
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
+                 int32_t layout, void* out, void* stream);
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
-                 int32_t channels, void* g1, void* g2, void* stream);
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* stream);
 
 /* ---- edge featurisation --------------------------------------------------
  * vec [E, 3] edge vectors; r = |vec| + 1e-9;

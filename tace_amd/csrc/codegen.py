@@ -153,7 +153,7 @@ class Variant:
         L.append("    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,")
         L.append("    const T* __restrict__ gout,")
         L.append("    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,")
-        L.append("    T* __restrict__ gx, T* __restrict__ gy, T* __restrict__ gw, int n_nodes, int C) {")
+        L.append("    T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw, int n_nodes, int C) {")
         L.append("  const int n = blockIdx.x;")
         L.append("  if (n >= n_nodes) return;")
         L.append("  const int beg = rowptr[n], end = rowptr[n + 1];")
@@ -197,11 +197,13 @@ class Variant:
                 L.append(f"      if (NEED_GX) hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * a{k});")
                 L.append(f"      hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * a{k});")
             L.append("    }")
+        # grad_x contribution of this edge, one row per receiver-sorted slot;
+        # summed per sender by k_seg_rowsum (deterministic, no atomics)
         L.append("    if (NEED_GX && act) {")
-        L.append("      T* gxs = gx + (size_t)s * DX;")
+        L.append("      T* cb = cbuf + (size_t)e * DX;")
         for b, d in enumerate(self.d1):
             for m in range(d):
-                L.append(f"      unsafeAtomicAdd(gxs + (size_t)C * {self.off1[b]} + (size_t)u * {d} + {m}, hx{b}_{m});")
+                L.append(f"      cb[(size_t)C * {self.off1[b]} + (size_t)u * {d} + {m}] = hx{b}_{m};")
         L.append("    }")
         L.append(f"    T* gys = gy + (size_t)ed * {self.D2};")
         for b, d in enumerate(self.d2):
@@ -213,70 +215,105 @@ class Variant:
         return "\n".join(L)
 
     # ---------------------------------------------------------------- uuu ----
+    @staticmethod
+    def _groups(ls: Sequence[int]):
+        """Runs of equal l (what ``Irreps.simplify`` merges): per block
+        (group id, index inside the group); per group (l, count, per-channel offset)."""
+        blk, grp = [], []
+        for l in ls:
+            if grp and grp[-1][0] == l:
+                blk.append((len(grp) - 1, grp[-1][1]))
+                grp[-1][1] += 1
+            else:
+                blk.append((len(grp), 0))
+                grp.append([l, 1])
+        off, acc = [], 0
+        for l, c in grp:
+            off.append(acc)
+            acc += c * (2 * l + 1)
+        return blk, [(l, c, o) for (l, c), o in zip(grp, off)]
+
+    def _addr(self, which: str, b: int, m: int) -> Tuple[str, str]:
+        """(e3nn address, group-major address) of component m of block b of
+        operand ``which`` (in1 / in2 / out) for channel u of node n.
+        e3nn: n*C*D + C*off_b + u*d_b + m;  group-major: the whole batch's group
+        g is one [N, 2l+1, count*C] matrix at N*C*goff_g."""
+        ls = {"in1": self.in1, "in2": self.in2, "out": [l3 for (_, _, l3) in self.path_l]}[which]
+        D = {"in1": self.D1, "in2": self.D2, "out": self.DO}[which]
+        offs = {"in1": self.off1, "in2": self.off2, "out": self.offo}[which]
+        d = 2 * ls[b] + 1
+        e3 = f"n * C * {D} + (size_t)C * {offs[b]} + (size_t)u * {d} + {m}"
+        blk, grp = self._groups(ls)
+        g, j = blk[b]
+        l, cnt, goff = grp[g]
+        gm = f"(size_t)N * C * {goff} + (n * {2 * l + 1} + {m}) * ((size_t){cnt} * C) + (size_t){j} * C + u"
+        return e3, gm
+
+    def _ld(self, ptr: str, which: str, b: int, m: int, flag: str) -> str:
+        e3, gm = self._addr(which, b, m)
+        return f"({flag} ? {ptr}[{gm}] : {ptr}[{e3}])"
+
     def emit_uuu_fwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T>\n__global__ __launch_bounds__(256) void k_{self.name}_fwd(")
+        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_fwd(")
         L.append("    const T* __restrict__ x1, const T* __restrict__ x2, T* __restrict__ out, int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
-        L.append("  if (n >= (size_t)n_nodes) return;")
-        L.append(f"  const T* a = x1 + n * C * {self.D1};")
-        L.append(f"  const T* b = x2 + n * C * {self.D2};")
+        L.append("  const size_t N = (size_t)n_nodes;")
+        L.append("  if (n >= N) return;")
         for bb, d in enumerate(self.d1):
             for m in range(d):
-                L.append(f"  const T x{bb}_{m} = a[(size_t)C * {self.off1[bb]} + (size_t)u * {d} + {m}];")
+                L.append(f"  const T x{bb}_{m} = {self._ld('x1', 'in1', bb, m, 'IN1_GM')};")
         for bb, d in enumerate(self.d2):
             for m in range(d):
-                L.append(f"  const T y{bb}_{m} = b[(size_t)C * {self.off2[bb]} + (size_t)u * {d} + {m}];")
-        L.append(f"  T* o = out + n * C * {self.DO};")
+                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'false')};")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
             for k in range(d):
                 terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
-                L.append(f"  o[(size_t)C * {self.offo[p]} + (size_t)u * {d} + {k}] = {' + '.join(terms) if terms else 'T(0)'};")
+                e3, gm = self._addr("out", p, k)
+                L.append(f"  out[OUT_GM ? ({gm}) : ({e3})] = {' + '.join(terms) if terms else 'T(0)'};")
         L.append("}")
         return "\n".join(L)
 
     def emit_uuu_bwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
+        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
         L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ gout,")
         L.append("    T* __restrict__ g1, T* __restrict__ g2, int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
-        L.append("  if (n >= (size_t)n_nodes) return;")
-        L.append(f"  const T* a = x1 + n * C * {self.D1};")
-        L.append(f"  const T* b = x2 + n * C * {self.D2};")
-        L.append(f"  const T* go = gout + n * C * {self.DO};")
+        L.append("  const size_t N = (size_t)n_nodes;")
+        L.append("  if (n >= N) return;")
         for bb, d in enumerate(self.d1):
             for m in range(d):
-                L.append(f"  const T x{bb}_{m} = a[(size_t)C * {self.off1[bb]} + (size_t)u * {d} + {m}];")
+                L.append(f"  const T x{bb}_{m} = {self._ld('x1', 'in1', bb, m, 'IN1_GM')};")
                 L.append(f"  T hx{bb}_{m} = T(0);")
         for bb, d in enumerate(self.d2):
             for m in range(d):
-                L.append(f"  const T y{bb}_{m} = b[(size_t)C * {self.off2[bb]} + (size_t)u * {d} + {m}];")
+                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'false')};")
                 L.append(f"  T hy{bb}_{m} = T(0);")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
             L.append("  {")
             for k in range(d):
-                L.append(f"    const T g{k} = go[(size_t)C * {self.offo[p]} + (size_t)u * {d} + {k}];")
+                L.append(f"    const T g{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
             for (i, j, k, c) in self.cg[p]:
                 L.append(f"    hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * g{k});")
                 L.append(f"    hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * g{k});")
             L.append("  }")
-        L.append(f"  T* o1 = g1 + n * C * {self.D1};")
-        L.append(f"  T* o2 = g2 + n * C * {self.D2};")
         for bb, d in enumerate(self.d1):
             for m in range(d):
-                L.append(f"  o1[(size_t)C * {self.off1[bb]} + (size_t)u * {d} + {m}] = hx{bb}_{m};")
+                e3, gm = self._addr("in1", bb, m)
+                L.append(f"  g1[IN1_GM ? ({gm}) : ({e3})] = hx{bb}_{m};")
         for bb, d in enumerate(self.d2):
             for m in range(d):
-                L.append(f"  o2[(size_t)C * {self.off2[bb]} + (size_t)u * {d} + {m}] = hy{bb}_{m};")
+                e3, gm = self._addr("in2", bb, m)
+                L.append(f"  g2[{e3}] = hy{bb}_{m};")
         L.append("}")
         return "\n".join(L)
 
@@ -393,58 +430,91 @@ def emit_sh(lmax_all: int = 3) -> str:
 
 
 # -------------------------------------------------------------------- main ----
-def emit_all(path: str) -> None:
+_TYPEDEFS = [
+    "typedef void (*UvuFwd)(const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t);",
+    "typedef void (*UvuBwd)(const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t);",
+    "typedef void (*UuuFwd)(const void*, const void*, void*, int, int, int, hipStream_t);",
+    "typedef void (*UuuBwd)(const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t);",
+]
+
+
+def _launchers(v: Variant) -> List[str]:
+    out = []
+    for T, tag in (("float", "f"), ("double", "d")):
+        if v.kind == "uvu":
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int E, int C, hipStream_t s) {{")
+            out.append(f"  (void)E; if (n > 0) hipLaunchKernelGGL(k_{v.name}_fwd<{T}>, dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
+            out.append("}")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int E, int C, hipStream_t s) {{")
+            out.append("  (void)E; if (n <= 0) return;")
+            out.append(f"  if (gx) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, true>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
+            out.append(f"  else hipLaunchKernelGGL((k_{v.name}_bwd<{T}, false>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
+            out.append("}")
+        else:
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, void* o, int n, int C, int flags, hipStream_t s) {{")
+            out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
+            out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
+            for f in (0, 2, 3):  # in1 grouped implies out grouped (the product-basis chain)
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {'true' if f & 1 else 'false'}, {'true' if f & 2 else 'false'}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
+            out.append("}")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* go, void* g1, void* g2, int n, int C, int flags, hipStream_t s) {{")
+            out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
+            out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
+            for f in (0, 2, 3):
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {'true' if f & 1 else 'false'}, {'true' if f & 2 else 'false'}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
+            out.append("}")
+    return out
+
+
+def emit_all(gen_dir: str) -> List[str]:
+    """Writes gen/sh.inc, gen/registry.inc and one gen/v_<name>.hip per variant
+    (compiled as separate translation units).  Returns the .hip paths."""
+    os.makedirs(gen_dir, exist_ok=True)
+    hdr = "// GENERATED by tace_amd/csrc/codegen.py -- do not edit."
     vs = all_variants()
-    out = ["// GENERATED by tace_amd/csrc/codegen.py -- do not edit.", "#pragma once", ""]
-    out.append(emit_sh(3))
-    out.append("")
+    _write(os.path.join(gen_dir, "sh.inc"), [hdr, "#pragma once", emit_sh(3)])
+    srcs = []
     for v in vs:
-        out.append(f"// variant {v.key}: {len(v.paths)} paths, per-channel dims in1={v.D1} in2={v.D2} out={v.DO}")
-        out.append(v.emit())
-        out.append("")
-    # registry
-    out.append("struct TpVariant {")
-    out.append("  const char* key; int kind; int npath; int d1; int d2; int dout;")
-    out.append("  void (*fwd_f)(const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t);")
-    out.append("  void (*fwd_d)(const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t);")
-    out.append("  void (*bwd_f)(const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t);")
-    out.append("  void (*bwd_d)(const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t);")
-    out.append("};")
-    out.append("")
+        body = [hdr, f"// variant {v.key}: {len(v.paths)} paths, per-channel dims in1={v.D1} in2={v.D2} out={v.DO}",
+                '#include "../common.h"', *_TYPEDEFS, v.emit(), "", *_launchers(v)]
+        path = os.path.join(gen_dir, f"v_{v.name}.hip")
+        _write(path, body)
+        srcs.append(path)
+    reg = [hdr, "#pragma once", *_TYPEDEFS,
+           "struct TpVariant {", "  const char* key; int kind; int npath; int d1; int d2; int dout;",
+           "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d; UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;", "};"]
     for v in vs:
-        for T, tag in (("float", "f"), ("double", "d")):
-            if v.kind == "uvu":
-                out.append(f"static void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int E, int C, hipStream_t s) {{")
-                out.append(f"  (void)E; if (n > 0) hipLaunchKernelGGL(k_{v.name}_fwd<{T}>, dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
-                out.append("}")
-                out.append(f"static void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int E, int C, hipStream_t s) {{")
-                out.append("  (void)E; if (n <= 0) return;")
-                out.append(f"  if (gx) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, true>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
-                out.append(f"  else hipLaunchKernelGGL((k_{v.name}_bwd<{T}, false>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
-                out.append("}")
-            else:
-                out.append(f"static void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int E, int C, hipStream_t s) {{")
-                out.append("  (void)w; (void)rp; (void)eid; (void)src; (void)E;")
-                out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
-                out.append(f"  hipLaunchKernelGGL(k_{v.name}_fwd<{T}>, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, (const {T}*)x, (const {T}*)y, ({T}*)o, n, C);")
-                out.append("}")
-                out.append(f"static void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int E, int C, hipStream_t s) {{")
-                out.append("  (void)w; (void)rp; (void)eid; (void)src; (void)gw; (void)E;")
-                out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
-                out.append(f"  hipLaunchKernelGGL(k_{v.name}_bwd<{T}>, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)g, ({T}*)gx, ({T}*)gy, n, C);")
-                out.append("}")
-    out.append("static const TpVariant kVariants[] = {")
+        if v.kind == "uvu":
+            reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
+                    (("fwd", "const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t"),
+                     ("bwd", "const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t"))
+                    for t in ("f", "d")]
+        else:
+            reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
+                    (("fwd", "const void*, const void*, void*, int, int, int, hipStream_t"),
+                     ("bwd", "const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t"))
+                    for t in ("f", "d")]
+    reg.append("static const TpVariant kVariants[] = {")
     for v in vs:
-        kind = 0 if v.kind == "uvu" else 1
-        out.append(f"  {{\"{v.key}\", {kind}, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, L_{v.name}_fwd_f, L_{v.name}_fwd_d, L_{v.name}_bwd_f, L_{v.name}_bwd_d}},")
-    out.append("};")
-    out.append(f"static const int kNumVariants = {len(vs)};")
+        n = v.name
+        if v.kind == "uvu":
+            reg.append(f"  {{\"{v.key}\", 0, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")
+        else:
+            reg.append(f"  {{\"{v.key}\", 1, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, nullptr, nullptr, nullptr, nullptr, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d}},")
+    reg.append("};")
+    reg.append(f"static const int kNumVariants = {len(vs)};")
+    _write(os.path.join(gen_dir, "registry.inc"), reg)
+    return srcs
+
+
+def _write(path: str, lines: List[str]) -> None:
+    txt = "\n".join(lines) + "\n"
+    if os.path.exists(path) and open(path).read() == txt:
+        return  # unchanged: keep the mtime so the build can skip the object
     with open(path, "w") as f:
-        f.write("\n".join(out) + "\n")
+        f.write(txt)
 
 
 if __name__ == "__main__":
-    dst = sys.argv[1] if len(sys.argv) > 1 else os.path.join(_HERE, "gen", "tp_kernels.inc")
-    os.makedirs(os.path.dirname(dst), exist_ok=True)
-    emit_all(dst)
-    print(dst)
+    for p in emit_all(sys.argv[1] if len(sys.argv) > 1 else os.path.join(_HERE, "gen")):
+        print(p)

@@ -37,16 +37,11 @@ int check_launch(const char* what) {
   return 0;
 }
 
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
 }  // namespace
 
-#include "gen/tp_kernels.inc"
+#include "common.h"
+#include "gen/registry.inc"
+#include "gen/sh.inc"
 
 // ---------------------------------------------------------------- helpers --
 template <typename T>
@@ -62,6 +57,22 @@ static void launch_fill(T* p, size_t n, T v, hipStream_t s) {
   size_t blocks = (n + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(k_fill<T>, dim3((unsigned)blocks), dim3(256), 0, s, p, n, v);
+}
+
+// gx[s, :] = sum over the receiver-sorted slots k listed for sender s of
+// cbuf[k, :]; fixed summation order (sender CSR), no atomics.
+template <typename T>
+__global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, const int* __restrict__ s_rowptr,
+                                                    const int* __restrict__ s_slot, T* __restrict__ gx, int n,
+                                                    int64_t row) {
+  const int s = blockIdx.x;
+  if (s >= n) return;
+  const int b = s_rowptr[s], e = s_rowptr[s + 1];
+  for (int64_t j = threadIdx.x; j < row; j += 256) {
+    T acc = T(0);
+    for (int k = b; k < e; ++k) acc += cbuf[(size_t)s_slot[k] * row + j];
+    gx[(size_t)s * row + j] = acc;
+  }
 }
 
 // ------------------------------------------------------ edge featurisation --
@@ -410,54 +421,67 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
 
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, void* gx, void* gy, void* gw, void* stream) {
+                     int32_t channels, const int32_t* s_rowptr, const int32_t* s_slot, void* workspace,
+                     int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_bwd: bad sizes");
   if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_bwd: sizes exceed int32 indexing");
   if (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)) return fail("tace_edge_tp_bwd: null pointer");
   const TpVariant& v = kVariants[vid];
+  const int64_t row = (int64_t)channels * v.d1;
+  if (gx) {
+    if (!s_rowptr || (n_edges && (!s_slot || !workspace))) return fail("tace_edge_tp_bwd: grad_x needs sender CSR + workspace");
+    if (workspace_elems < n_edges * row) return fail("tace_edge_tp_bwd: workspace smaller than n_edges * channels * d1");
+  }
   hipStream_t s = (hipStream_t)stream;
-  const size_t nx = (size_t)n_nodes * channels * v.d1;
+  void* cbuf = gx ? workspace : nullptr;
   if (dtype == TACE_F32) {
-    if (gx) launch_fill<float>((float*)gx, nx, 0.f, s);
-    v.bwd_f(x, y, w, gout, rowptr, eid, src, gx, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    if (gx && n_nodes)
+      hipLaunchKernelGGL(k_seg_rowsum<float>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const float*)cbuf, s_rowptr,
+                         s_slot, (float*)gx, (int)n_nodes, row);
   } else if (dtype == TACE_F64) {
-    if (gx) launch_fill<double>((double*)gx, nx, 0.0, s);
-    v.bwd_d(x, y, w, gout, rowptr, eid, src, gx, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    if (gx && n_nodes)
+      hipLaunchKernelGGL(k_seg_rowsum<double>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const double*)cbuf,
+                         s_rowptr, s_slot, (double*)gx, (int)n_nodes, row);
   } else {
     return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
   }
   return check_launch("tace_edge_tp_bwd");
 }
 
-int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels, void* out,
-                 void* stream) {
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
+                 int32_t layout, void* out, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_fwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_fwd: bad sizes");
+  if (layout < 0 || layout > 3 || layout == 1) return fail("tace_uuu_fwd: layout must be 0, OUT_GROUPED or IN1|OUT_GROUPED");
   if (n_nodes && (!x1 || !x2 || !out)) return fail("tace_uuu_fwd: null pointer");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_fwd: too many nodes");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.fwd_f(x1, x2, nullptr, nullptr, nullptr, nullptr, out, (int)n_nodes, 0, channels, s);
+    v.ufwd_f(x1, x2, out, (int)n_nodes, channels, layout, s);
   else if (dtype == TACE_F64)
-    v.fwd_d(x1, x2, nullptr, nullptr, nullptr, nullptr, out, (int)n_nodes, 0, channels, s);
+    v.ufwd_d(x1, x2, out, (int)n_nodes, channels, layout, s);
   else
     return fail("tace_uuu_fwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_uuu_fwd");
 }
 
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
-                 int32_t channels, void* g1, void* g2, void* stream) {
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
+  if (layout < 0 || layout > 3 || layout == 1) return fail("tace_uuu_bwd: layout must be 0, OUT_GROUPED or IN1|OUT_GROUPED");
   if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
+  if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_bwd: too many nodes");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.bwd_f(x1, x2, nullptr, gout, nullptr, nullptr, nullptr, g1, g2, nullptr, (int)n_nodes, 0, channels, s);
+    v.ubwd_f(x1, x2, gout, g1, g2, (int)n_nodes, channels, layout, s);
   else if (dtype == TACE_F64)
-    v.bwd_d(x1, x2, nullptr, gout, nullptr, nullptr, nullptr, g1, g2, nullptr, (int)n_nodes, 0, channels, s);
+    v.ubwd_d(x1, x2, gout, g1, g2, (int)n_nodes, channels, layout, s);
   else
     return fail("tace_uuu_bwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_uuu_bwd");

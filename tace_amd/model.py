@@ -150,6 +150,69 @@ class e3nnElementLinear(torch.nn.Module):
         xs = x.index_select(0, sp.perm)
         return self.forward_sorted(xs, sp, sp.attrs.index_select(0, sp.perm)).index_select(0, sp.inv)
 
+    def forward_grouped(self, xg: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor) -> torch.Tensor:
+        """``xg``: species-sorted nodes in the group-major layout of ``irreps_in``."""
+        out = _GroupedSpeciesLinear.apply(xg, self.weight, self.lay, sp.ranges)
+        if self.bias is not None:
+            out = out + self.lay.bias_full(attrs_sorted @ self.bias)
+        return out
+
+
+class _GroupedSpeciesLinear(torch.autograd.Function):
+    """Per-species linear on a group-major input (``include/tace_hip.h``): the
+    input group of irrep l is one [N*(2l+1), K] matrix over species-sorted
+    nodes, so each (species, instruction) is a single GEMM with no transpose
+    of the large operand.  Output and its gradient are in e3nn layout."""
+
+    @staticmethod
+    def forward(ctx, xg, weight, lay: "_LinearLayout", ranges):
+        Nn = xg.shape[0]
+        flat = xg.view(-1)
+        out = xg.new_zeros(Nn, lay.dim_out)
+        for (i, o, off, mi, mo, pw) in lay.ins:
+            s_in, K, d = lay.sl_in[i]
+            X = flat[Nn * s_in:Nn * (s_in + K * d)].view(Nn * d, K)
+            so = lay.sl_out[o][0]
+            for (sp, a, b) in ranges:
+                Y = X[a * d:b * d] @ (weight[sp, off:off + mi * mo].view(mi, mo) * pw)
+                out[a:b, so:so + mo * d].view(b - a, mo, d).add_(Y.view(b - a, d, mo).transpose(1, 2))
+        ctx.save_for_backward(xg, weight)
+        ctx.lay, ctx.ranges = lay, ranges
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        xg, weight = ctx.saved_tensors
+        lay, ranges = ctx.lay, ctx.ranges
+        Nn = xg.shape[0]
+        flat = xg.view(-1)
+        gx = gw = None
+        if ctx.needs_input_grad[0]:
+            gx = torch.empty_like(xg)
+            gflat = gx.view(-1)
+            covered = set()
+            for (i, o, off, mi, mo, pw) in lay.ins:
+                covered.add(i)
+            for i, (s_in, K, d) in enumerate(lay.sl_in):
+                if i not in covered:
+                    gflat[Nn * s_in:Nn * (s_in + K * d)].zero_()
+        if ctx.needs_input_grad[1]:
+            gw = torch.zeros_like(weight)
+        for (i, o, off, mi, mo, pw) in lay.ins:
+            s_in, K, d = lay.sl_in[i]
+            so = lay.sl_out[o][0]
+            for (sp, a, b) in ranges:
+                G = gout[a:b, so:so + mo * d].reshape(b - a, mo, d).transpose(1, 2).reshape((b - a) * d, mo)
+                W = weight[sp, off:off + mi * mo].view(mi, mo)
+                if gx is not None:
+                    dst = gflat[Nn * s_in + a * d * K:Nn * s_in + b * d * K].view((b - a) * d, K)
+                    torch.mm(G, W.t(), out=dst)
+                    dst.mul_(pw)
+                if gw is not None:
+                    X = flat[Nn * s_in + a * d * K:Nn * s_in + b * d * K].view((b - a) * d, K)
+                    gw[sp, off:off + mi * mo] += (X.t() @ G).reshape(-1) * pw
+        return gx, gw, None, None
+
 
 class mlpLinear(torch.nn.Module):
     """``x @ (weight * alpha)``, weight [in, out] ~ U(-sqrt3, sqrt3) (``linear.py:247-279``)."""
@@ -212,8 +275,8 @@ class uuuTensorProduct(torch.nn.Module):
         self.C = self.irreps_in1[0][0]
         self.key = ops.variant_key("uuu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
 
-    def forward(self, x1, x2):
-        return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C)
+    def forward(self, x1, x2, layout: int = 0):
+        return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C, layout)
 
 
 def _gate(x: torch.Tensor, gated: Irreps) -> torch.Tensor:
@@ -320,13 +383,16 @@ class CgtpACE(torch.nn.Module):
                 feats = self.aces[nu - 2](feats, x)
                 outs = outs + self.coefs[nu - 1](feats)
         else:
+            # species-sorted nodes; the nu >= 2 products stay in the group-major
+            # layout that the coefficient GEMMs read without transposes
             xs = x.index_select(0, sp.perm)
             attrs_s = sp.attrs.index_select(0, sp.perm)
             outs = self.coefs[0].forward_sorted(xs, sp, attrs_s)
             feats = xs
             for nu in range(2, self.correlation + 1):
-                feats = self.aces[nu - 2](feats, xs)
-                outs = outs + self.coefs[nu - 1].forward_sorted(feats, sp, attrs_s)
+                lay = ops.LAYOUT_OUT_GROUPED | (ops.LAYOUT_IN1_GROUPED if nu > 2 else 0)
+                feats = self.aces[nu - 2](feats, xs, lay)
+                outs = outs + self.coefs[nu - 1].forward_grouped(feats, sp, attrs_s)
             outs = outs.index_select(0, sp.inv)
         outs = self.linear(outs)
         return outs + sc if sc is not None else outs

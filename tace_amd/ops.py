@@ -113,6 +113,19 @@ class EdgePlan:
     rowptr: torch.Tensor           # int32 [N+1]
     src: torch.Tensor              # int32 [E], sender of edge id
     eid: Optional[torch.Tensor]    # int32 [E] or None
+    _sender: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+
+    def sender_csr(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(s_rowptr int32 [N+1], s_slot int32 [E]): receiver-sorted slots grouped
+        by sender, stable -- the fixed order of the grad_x segmented sum."""
+        if self._sender is None:
+            slot_src = self.src.long() if self.eid is None else self.src.long()[self.eid.long()]
+            order = torch.argsort(slot_src, stable=True).to(torch.int32).contiguous()
+            counts = torch.bincount(slot_src, minlength=self.n_nodes)
+            rp = torch.zeros(self.n_nodes + 1, dtype=torch.int64, device=self.src.device)
+            rp[1:] = torch.cumsum(counts, 0)
+            self._sender = (rp.to(torch.int32).contiguous(), order)
+        return self._sender
 
     @staticmethod
     def from_edge_index(edge_index: torch.Tensor, n_nodes: int) -> "EdgePlan":
@@ -202,10 +215,16 @@ class _EdgeTP(torch.autograd.Function):
         gx = torch.empty_like(x) if need_x else None
         gy = torch.empty_like(y)
         gw = torch.empty_like(w)
+        if need_x:
+            s_rowptr, s_slot = plan.sender_csr()
+            ws = torch.empty(max(plan.n_edges, 1) * C * var.d1, dtype=x.dtype, device=x.device)
+        else:
+            s_rowptr = s_slot = ws = None
         tok = _t0("edge_tp_bwd:" + var.key)
         N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                          gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
-                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, N.ptr(gx),
+                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, N.ptr(s_rowptr),
+                                         N.ptr(s_slot), N.ptr(ws), 0 if ws is None else ws.numel(), N.ptr(gx),
                                          gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
         _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
         return gx, gy, gw, None, None, None
@@ -216,20 +235,23 @@ def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int) -> torch.Te
 
 
 # ---------------------------------------------------------------- uuu ----
+LAYOUT_IN1_GROUPED, LAYOUT_OUT_GROUPED = 1, 2
+
+
 class _UUU(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x1, x2, var: TpVariant, C: int):
+    def forward(ctx, x1, x2, var: TpVariant, C: int, layout: int):
         Nn = x1.shape[0]
         dt = x1.dtype
         _req(x1, "x1", dt, (Nn, C * var.d1))
         _req(x2, "x2", dt, (Nn, C * var.d2))
         out = torch.empty(Nn, C * var.dout, dtype=dt, device=x1.device)
         tok = _t0("uuu_fwd:" + var.key)
-        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), Nn, C, out.data_ptr(),
-                                     N.stream_ptr(x1.device)), "tace_uuu_fwd")
+        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), Nn, C, layout,
+                                     out.data_ptr(), N.stream_ptr(x1.device)), "tace_uuu_fwd")
         _t1(tok, (Nn, C))
         ctx.save_for_backward(x1, x2)
-        ctx.var, ctx.C = var, C
+        ctx.var, ctx.C, ctx.layout = var, C, layout
         return out
 
     @staticmethod
@@ -239,14 +261,53 @@ class _UUU(torch.autograd.Function):
         g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
         tok = _t0("uuu_bwd:" + ctx.var.key)
         N.check(N.lib().tace_uuu_bwd(ctx.var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(),
-                                     gout.data_ptr(), x1.shape[0], ctx.C, g1.data_ptr(), g2.data_ptr(),
+                                     gout.data_ptr(), x1.shape[0], ctx.C, ctx.layout, g1.data_ptr(), g2.data_ptr(),
                                      N.stream_ptr(x1.device)), "tace_uuu_bwd")
         _t1(tok, (x1.shape[0], ctx.C))
-        return g1, g2, None, None
+        return g1, g2, None, None, None
 
 
-def uuu_tp(x1, x2, var: TpVariant, C: int) -> torch.Tensor:
-    return _UUU.apply(x1.contiguous(), x2.contiguous(), var, C)
+def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
+    """``layout`` = 0 (e3nn operands), LAYOUT_OUT_GROUPED, or both flags: the
+    group-major layout of ``include/tace_hip.h`` for x1 / out."""
+    return _UUU.apply(x1.contiguous(), x2.contiguous(), var, C, int(layout))
+
+
+def to_grouped(x: torch.Tensor, ls: Sequence[int], C: int) -> torch.Tensor:
+    """e3nn layout [N, C*D] -> group-major layout (same shape; test helper)."""
+    Nn = x.shape[0]
+    cols, off = [], 0
+    groups = _runs(ls)
+    parts = []
+    for l, cnt in groups:
+        d = 2 * l + 1
+        blk = x[:, C * off:C * (off + cnt * d)].reshape(Nn, cnt, C, d)
+        parts.append(blk.permute(0, 3, 1, 2).reshape(-1))
+        off += cnt * d
+    return torch.cat(parts).view(Nn, -1)
+
+
+def from_grouped(x: torch.Tensor, ls: Sequence[int], C: int) -> torch.Tensor:
+    """group-major layout -> e3nn layout (test helper)."""
+    Nn = x.shape[0]
+    flat = x.reshape(-1)
+    cols, pos = [], 0
+    for l, cnt in _runs(ls):
+        d = 2 * l + 1
+        n = Nn * d * cnt * C
+        cols.append(flat[pos:pos + n].view(Nn, d, cnt, C).permute(0, 2, 3, 1).reshape(Nn, -1))
+        pos += n
+    return torch.cat(cols, dim=1)
+
+
+def _runs(ls: Sequence[int]):
+    out = []
+    for l in ls:
+        if out and out[-1][0] == l:
+            out[-1][1] += 1
+        else:
+            out.append([l, 1])
+    return [(l, c) for l, c in out]
 
 
 # ------------------------------------------------------------ neighbours ----

@@ -42,7 +42,11 @@ def test_edge_basis_matches_oracle(cuda, dtype, lmax):
     d = torch.randn(E, 3, generator=g, dtype=torch.float64)
     d = d / d.norm(dim=1, keepdim=True) * (0.3 + 6.5 * torch.rand(E, 1, generator=g, dtype=torch.float64))
     vec = d.to(dtype).double().requires_grad_(True)  # same values the GPU sees
-    rb = om.RadialBasis(rc, nb, p).double()
+    torch.set_default_dtype(dtype)
+    try:
+        rb = om.RadialBasis(rc, nb, p).double()  # buffers built in the model dtype, as the reference does
+    finally:
+        torch.set_default_dtype(torch.float32)
     length = (vec ** 2).sum(1, keepdim=True).sqrt() + 1e-9
     R_o = rb(length)
     Y_o = oso3.spherical_harmonics(lmax, vec / length)
@@ -51,7 +55,7 @@ def test_edge_basis_matches_oracle(cuda, dtype, lmax):
     (gv_o,) = torch.autograd.grad((R_o * gR).sum() + (Y_o * gY).sum(), vec)
 
     v = vec.detach().to(dtype).to(cuda).requires_grad_(True)
-    bw = (math.pi / rc * torch.linspace(1.0, nb, nb, dtype=torch.float64)).to(dtype).to(cuda)
+    bw = rb.radial_fn.bessel_weights.to(dtype).to(cuda)  # the oracle's own buffer
     R, Y = ops.edge_basis(v, bw, math.sqrt(2.0 / rc), rc, p, lmax)
     close(R, R_o, dtype, "radial")
     close(Y, Y_o, dtype, "sh")
@@ -184,3 +188,45 @@ def test_neighbour_list_bit_exact_edge_set(cuda, name, s, rc):
     # deterministic output order
     r2, s2, h2 = ops.neighbour_list(pos, s["cell"], s["pbc"], rc)
     assert torch.equal(r2, rowptr) and np.array_equal(s2.cpu().numpy(), src) and np.array_equal(h2.cpu().numpy(), sh)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("layout", [2, 3])
+@pytest.mark.parametrize("L", [2, 3])
+def test_uuu_grouped_layouts_match_oracle(cuda, dtype, layout, L):
+    """The group-major operand layouts (x1 and/or out) give the e3nn-layout results."""
+    C = 64
+    full = list(range(L + 1))
+    nu2 = om.UUUTP(_irreps(full, 1), _irreps(full, 1), [(1, (l, (-1) ** l)) for l in full], True)
+    nu2_ls = [ir[0] for _, ir in nu2.out]
+    in1 = nu2_ls if layout == 3 else full
+    tp = om.UUUTP(_irreps(in1, C), _irreps(full, C), [(1, (l, (-1) ** l)) for l in full], in1 == full)
+    out_ls = [ir[0] for _, ir in tp.out]
+    g = torch.Generator().manual_seed(L * 10 + layout)
+    Nn = 23
+    x1 = torch.randn(Nn, oso3.irreps_dim(_irreps(in1, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    x2 = torch.randn(Nn, oso3.irreps_dim(_irreps(full, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    x1.requires_grad_(True), x2.requires_grad_(True)
+    o = tp(x1, x2)
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64).to(dtype).double()
+    g1o, g2o = torch.autograd.grad((o * go).sum(), [x1, x2])
+    var = ops.find_variant(ops.variant_key("uuu", in1, full, full))
+    a = x1.detach().to(dtype).to(cuda)
+    if layout & ops.LAYOUT_IN1_GROUPED:
+        a = ops.to_grouped(a, in1, C)
+    a.requires_grad_(True)
+    b = x2.detach().to(dtype).to(cuda).requires_grad_(True)
+    out = ops.uuu_tp(a, b, var, C, layout)
+    close(ops.from_grouped(out, out_ls, C), o, dtype, "out")
+    gg = ops.to_grouped(go.to(dtype).to(cuda), out_ls, C)
+    g1, g2 = torch.autograd.grad((out * gg).sum(), [a, b])
+    if layout & ops.LAYOUT_IN1_GROUPED:
+        g1 = ops.from_grouped(g1, in1, C)
+    close(g1, g1o, dtype, "g1")
+    close(g2, g2o, dtype, "g2")
+
+
+def test_grouped_layout_helpers_roundtrip():
+    x = torch.randn(5, 8 * (1 + 3 + 3 + 5), dtype=torch.float64)
+    ls = [0, 1, 1, 2]
+    torch.testing.assert_close(ops.from_grouped(ops.to_grouped(x, ls, 8), ls, 8), x, rtol=0, atol=0)

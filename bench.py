@@ -79,6 +79,8 @@ def cpu_baseline(preset_cfg_fn, n_side=4, reps=2):
     cfg = preset_cfg_fn(ei.shape[1] / len(s["numbers"]))
     torch.manual_seed(0)
     m = om.TACE(cfg).float()
+    for prm in m.parameters():  # frozen, as in the reference calculators
+        prm.requires_grad_(False)
     d = data.collate([s], [(ei, S)], cfg["atomic_numbers"], dtype=torch.float32)
     om.compute(m, d, forces=True)  # warm-up
     t0 = time.perf_counter()
@@ -126,6 +128,11 @@ def main():
     torch.manual_seed(0)
     model = pm.create_model(cfg).to(dev)
     model.reset_target_property(["energy", "forces"])
+    # inference set-up of the reference calculators (ase/calculator.py:100-102,
+    # torchsim.py:142, lammps/mliap.py:38): eval mode, parameters frozen
+    model.eval()
+    for prm in model.parameters():
+        prm.requires_grad_(False)
     attrs = data.one_hot(s["numbers"], cfg["atomic_numbers"], torch.float32).to(dev)
 
     def step():

@@ -24,6 +24,8 @@
  *                             43-84 x C2PolynomialCutoff 437-472) and
  *                             SphericalHarmonics.forward (angular.py:288-315)
  *                             as called at representation.py:305-324
+ *   tace_edge_vec_fwd/_bwd    edge vectors of TensorModel.prepare_graph
+ *                             (models/adapter.py:334-340) and their position gradient
  *   tace_nl_*                 get_neighborhood (dataset/neighbour_list.py:195-298)
  */
 #ifndef TACE_HIP_H
@@ -35,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 3
+#define TACE_HIP_ABI_VERSION 4
 #define TACE_F32 0
 #define TACE_F64 1
 
@@ -51,13 +53,22 @@ const char* tace_tp_variant_key(int vid);
 int tace_tp_find(const char* key);
 int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dout);
 
+/* Operand layouts.  e3nn (0): node features in e3nn's mul_ir layout.
+ * Group-major: the runs of equal-l blocks that Irreps.simplify() merges form
+ * groups g; group g of the whole batch is one row-major [N, 2l+1, count_g*C]
+ * matrix at element offset N*C*goff_g (goff_g = per-channel offset of the
+ * group) -- the operand layout of the channel-mixing GEMMs that consume it. */
+#define TACE_LAYOUT_IN1_GROUPED 1
+#define TACE_LAYOUT_OUT_GROUPED 2
+
 /* out[n] = sum_{e: dst(e)=n} TP(x[src(e)], y[e], w[e])  -- uvu, mul2 = 1.
  * Edges are visited in receiver-CSR order: rowptr[n_nodes+1] over the sorted
  * edge list, eid[k] the edge id of sorted slot k (NULL = identity), src[e] the
- * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout]. */
+ * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout]
+ * (layout 0 or TACE_LAYOUT_OUT_GROUPED for out / gout). */
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
                      const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                     void* out, void* stream);
+                     int32_t layout, void* out, void* stream);
 /* Gradients of sum(gout * out): gy [E, d2], gw [E, C*npath]; gx [N, C*d1]
  * (NULL to skip).  All outputs are fully overwritten, no atomics: the
  * per-edge grad_x contributions go to `workspace` (>= E*C*d1 elements, one
@@ -65,19 +76,13 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
  * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender. */
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, const int32_t* s_rowptr, const int32_t* s_slot, void* workspace,
-                     int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
+                     int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
+                     void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
 
 /* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
- * layout: TACE_LAYOUT_IN1_GROUPED / TACE_LAYOUT_OUT_GROUPED select, for x1
- * (and g1) / out (and gout), the group-major layout instead of e3nn's: the
- * runs of equal-l blocks that Irreps.simplify() merges form groups g, and
- * group g of the whole batch is one row-major [N, 2l+1, count_g*C] matrix at
- * element offset N*C*goff_g -- the operand layout of the per-species
- * coefficient GEMMs that consume it.  x2 / g2 always use e3nn's layout.
- * Accepted layouts: 0, OUT_GROUPED, IN1_GROUPED|OUT_GROUPED. */
-#define TACE_LAYOUT_IN1_GROUPED 1
-#define TACE_LAYOUT_OUT_GROUPED 2
+ * layout flags select the group-major layout for x1 (and g1) / out (and
+ * gout); x2 / g2 always use e3nn's layout.  Accepted: 0, OUT_GROUPED,
+ * IN1_GROUPED|OUT_GROUPED. */
 int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream);
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
@@ -93,6 +98,17 @@ int tace_edge_basis_fwd(int dtype, const void* vec, int64_t n_edges, int32_t num
 int tace_edge_basis_bwd(int dtype, const void* vec, const void* g_radial, const void* g_sh, int64_t n_edges,
                         int32_t num_basis, const void* bessel_w, double prefactor, double cutoff, int32_t poly_p,
                         int32_t lmax, void* g_vec, void* stream);
+
+/* ---- edge vectors --------------------------------------------------------
+ * vec[e] = pos[dst[e]] - pos[src[e]] + shifts[e] . lattice[edge_graph[e]]
+ * (edge_graph NULL = graph 0).  The backward gives
+ * g_pos[n] = sum_{e: dst=n} g_vec[e] - sum_{e: src=n} g_vec[e] in the fixed
+ * order of the receiver CSR (rowptr, eid) and the sender CSR (s_rowptr,
+ * s_slot over receiver-sorted slots); no atomics. */
+int tace_edge_vec_fwd(int dtype, const void* pos, const void* lattice, const int32_t* src, const int32_t* dst,
+                      const void* shifts, const int32_t* edge_graph, int64_t n_edges, void* vec, void* stream);
+int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const int32_t* eid,
+                      const int32_t* s_rowptr, const int32_t* s_slot, int64_t n_nodes, void* g_pos, void* stream);
 
 /* ---- neighbour list (float64 positions, host cell[9] rows = lattice
  * vectors, host pbc[3]).  Edge (src=i, dst=j, S) exists iff

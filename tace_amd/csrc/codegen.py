@@ -108,7 +108,7 @@ class Variant:
     def emit_uvu_fwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T>\n__global__ __launch_bounds__(64) void k_{self.name}_fwd(")
+        L.append(f"template <typename T, bool OUT_GM>\n__global__ __launch_bounds__(64) void k_{self.name}_fwd(")
         L.append("    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,")
         L.append("    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,")
         L.append("    T* __restrict__ out, int n_nodes, int C) {")
@@ -136,11 +136,12 @@ class Variant:
                 L.append(f"    a{self.offo[p] + k} += w{p} * ({self._t_expr(p, k)});")
         L.append("    }")
         L.append("    if (act) {")
-        L.append(f"      T* o = out + (size_t)n * C * {self.DO};")
+        L.append("      const size_t N = (size_t)n_nodes;")
         for p in range(P):
             d = self.dout[p]
             for k in range(d):
-                L.append(f"      o[(size_t)C * {self.offo[p]} + (size_t)u * {d} + {k}] = a{self.offo[p] + k};")
+                e3, gm = self._addr("out", p, k)
+                L.append(f"      out[OUT_GM ? ({gm}) : ({e3})] = a{self.offo[p] + k};")
         L.append("    }")
         L.append("  }")
         L.append("}")
@@ -149,7 +150,7 @@ class Variant:
     def emit_uvu_bwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T, bool NEED_GX>\n__global__ __launch_bounds__(64) void k_{self.name}_bwd(")
+        L.append(f"template <typename T, bool NEED_GX, bool OUT_GM>\n__global__ __launch_bounds__(64) void k_{self.name}_bwd(")
         L.append("    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,")
         L.append("    const T* __restrict__ gout,")
         L.append("    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,")
@@ -161,11 +162,12 @@ class Variant:
         L.append("  for (int cb = 0; cb < C; cb += 64) {")
         L.append("    const int u = cb + (int)threadIdx.x;")
         L.append("    const bool act = u < C;")
-        L.append(f"    const T* go = gout + (size_t)n * C * {self.DO};")
+        L.append("    const size_t N = (size_t)n_nodes;")
         for p in range(P):
             d = self.dout[p]
             for k in range(d):
-                L.append(f"    const T g{self.offo[p] + k} = act ? go[(size_t)C * {self.offo[p]} + (size_t)u * {d} + {k}] : T(0);")
+                e3, gm = self._addr("out", p, k)
+                L.append(f"    const T g{self.offo[p] + k} = act ? gout[OUT_GM ? ({gm}) : ({e3})] : T(0);")
         L.append("    for (int e = beg; e < end; ++e) {")
         L.append("    const int ed = eid ? eid[e] : e;")
         L.append("    const int s = src[ed];")
@@ -242,11 +244,11 @@ class Variant:
         D = {"in1": self.D1, "in2": self.D2, "out": self.DO}[which]
         offs = {"in1": self.off1, "in2": self.off2, "out": self.offo}[which]
         d = 2 * ls[b] + 1
-        e3 = f"n * C * {D} + (size_t)C * {offs[b]} + (size_t)u * {d} + {m}"
+        e3 = f"(size_t)n * C * {D} + (size_t)C * {offs[b]} + (size_t)u * {d} + {m}"
         blk, grp = self._groups(ls)
         g, j = blk[b]
         l, cnt, goff = grp[g]
-        gm = f"(size_t)N * C * {goff} + (n * {2 * l + 1} + {m}) * ((size_t){cnt} * C) + (size_t){j} * C + u"
+        gm = f"(size_t)N * C * {goff} + ((size_t)n * {2 * l + 1} + {m}) * ((size_t){cnt} * C) + (size_t){j} * C + u"
         return e3, gm
 
     def _ld(self, ptr: str, which: str, b: int, m: int, flag: str) -> str:
@@ -442,13 +444,16 @@ def _launchers(v: Variant) -> List[str]:
     out = []
     for T, tag in (("float", "f"), ("double", "d")):
         if v.kind == "uvu":
-            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int E, int C, hipStream_t s) {{")
-            out.append(f"  (void)E; if (n > 0) hipLaunchKernelGGL(k_{v.name}_fwd<{T}>, dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int flags, int C, hipStream_t s) {{")
+            out.append("  if (n <= 0) return;")
+            for f in (0, 2):
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {'true' if f else 'false'}>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int E, int C, hipStream_t s) {{")
-            out.append("  (void)E; if (n <= 0) return;")
-            out.append(f"  if (gx) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, true>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
-            out.append(f"  else hipLaunchKernelGGL((k_{v.name}_bwd<{T}, false>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
+            out.append("  if (n <= 0) return;")
+            for f in (0, 2):
+                for gx in (True, False):
+                    out.append(f"  if (flags == {f} && {'gx' if gx else '!gx'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {'true' if gx else 'false'}, {'true' if f else 'false'}>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
             out.append("}")
         else:
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, void* o, int n, int C, int flags, hipStream_t s) {{")

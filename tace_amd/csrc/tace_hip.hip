@@ -75,6 +75,49 @@ __global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, 
   }
 }
 
+// ------------------------------------------------------------ edge vectors --
+// vec[e] = pos[dst] - pos[src] + S[e] . lat[eb[e]]   (adapter.py:334-340)
+template <typename T>
+__global__ __launch_bounds__(256) void k_edge_vec_fwd(const T* __restrict__ pos, const T* __restrict__ lat,
+                                                      const int* __restrict__ src, const int* __restrict__ dst,
+                                                      const T* __restrict__ shift, const int* __restrict__ eb,
+                                                      int64_t E, T* __restrict__ vec) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  const int i = src[e], j = dst[e];
+  const T* L = lat + (size_t)(eb ? eb[e] : 0) * 9;
+  const T s0 = shift[3 * e], s1 = shift[3 * e + 1], s2 = shift[3 * e + 2];
+#pragma unroll
+  for (int c = 0; c < 3; ++c)
+    vec[3 * e + c] = pos[3 * j + c] - pos[3 * i + c] + (s0 * L[c] + s1 * L[3 + c] + s2 * L[6 + c]);
+}
+
+// gpos[n] = sum_{e: dst(e)=n} g[e] - sum_{e: src(e)=n} g[e], both in CSR order
+template <typename T>
+__global__ __launch_bounds__(256) void k_edge_vec_bwd(const T* __restrict__ g, const int* __restrict__ rowptr,
+                                                      const int* __restrict__ eid, const int* __restrict__ s_rowptr,
+                                                      const int* __restrict__ s_slot, int n, T* __restrict__ gpos) {
+  const int a = blockIdx.x * blockDim.x + threadIdx.x;
+  if (a >= n) return;
+  T x = T(0), y = T(0), z = T(0);
+  for (int k = rowptr[a]; k < rowptr[a + 1]; ++k) {
+    const int e = eid ? eid[k] : k;
+    x += g[3 * e];
+    y += g[3 * e + 1];
+    z += g[3 * e + 2];
+  }
+  for (int k = s_rowptr[a]; k < s_rowptr[a + 1]; ++k) {
+    const int sl = s_slot[k];
+    const int e = eid ? eid[sl] : sl;
+    x -= g[3 * e];
+    y -= g[3 * e + 1];
+    z -= g[3 * e + 2];
+  }
+  gpos[3 * a] = x;
+  gpos[3 * a + 1] = y;
+  gpos[3 * a + 2] = z;
+}
+
 // ------------------------------------------------------ edge featurisation --
 // R[e, n] = pref * sin(b_n r) / r * f(r / rc) * [r < rc],  r = |v| + 1e-9
 // f(x) = 1 - (p+1)(p+2)/2 x^p + p(p+2) x^(p+1) - p(p+1)/2 x^(p+2)
@@ -403,7 +446,8 @@ int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dou
 
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
                      const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                     void* out, void* stream) {
+                     int32_t layout, void* out, void* stream) {
+  if (layout != 0 && layout != TACE_LAYOUT_OUT_GROUPED) return fail("tace_edge_tp_fwd: layout must be 0 or OUT_GROUPED");
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_fwd: bad variant id");
   if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_fwd: bad sizes");
   if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_fwd: sizes exceed int32 indexing");
@@ -411,9 +455,9 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.fwd_f(x, y, w, rowptr, eid, src, out, (int)n_nodes, (int)n_edges, channels, s);
+    v.fwd_f(x, y, w, rowptr, eid, src, out, (int)n_nodes, layout, channels, s);
   else if (dtype == TACE_F64)
-    v.fwd_d(x, y, w, rowptr, eid, src, out, (int)n_nodes, (int)n_edges, channels, s);
+    v.fwd_d(x, y, w, rowptr, eid, src, out, (int)n_nodes, layout, channels, s);
   else
     return fail("tace_edge_tp_fwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_edge_tp_fwd");
@@ -421,8 +465,9 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
 
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, const int32_t* s_rowptr, const int32_t* s_slot, void* workspace,
-                     int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
+                     int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
+                     void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
+  if (layout != 0 && layout != TACE_LAYOUT_OUT_GROUPED) return fail("tace_edge_tp_bwd: layout must be 0 or OUT_GROUPED");
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_bwd: bad sizes");
   if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_bwd: sizes exceed int32 indexing");
@@ -436,12 +481,12 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
   hipStream_t s = (hipStream_t)stream;
   void* cbuf = gx ? workspace : nullptr;
   if (dtype == TACE_F32) {
-    v.bwd_f(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
       hipLaunchKernelGGL(k_seg_rowsum<float>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const float*)cbuf, s_rowptr,
                          s_slot, (float*)gx, (int)n_nodes, row);
   } else if (dtype == TACE_F64) {
-    v.bwd_d(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, (int)n_edges, channels, s);
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
       hipLaunchKernelGGL(k_seg_rowsum<double>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const double*)cbuf,
                          s_rowptr, s_slot, (double*)gx, (int)n_nodes, row);
@@ -516,6 +561,42 @@ int tace_edge_basis_bwd(int dtype, const void* vec, const void* g_radial, const 
                                     num_basis, (const double*)bessel_w, prefactor, cutoff, poly_p, lmax,
                                     (double*)g_vec, s);
   return fail("tace_edge_basis_bwd: dtype must be TACE_F32 or TACE_F64");
+}
+
+int tace_edge_vec_fwd(int dtype, const void* pos, const void* lattice, const int32_t* src, const int32_t* dst,
+                      const void* shifts, const int32_t* edge_graph, int64_t n_edges, void* vec, void* stream) {
+  if (n_edges < 0) return fail("tace_edge_vec_fwd: bad sizes");
+  if (n_edges == 0) return 0;
+  if (!pos || !lattice || !src || !dst || !shifts || !vec) return fail("tace_edge_vec_fwd: null pointer");
+  const dim3 g((unsigned)((n_edges + 255) / 256)), b(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    hipLaunchKernelGGL(k_edge_vec_fwd<float>, g, b, 0, s, (const float*)pos, (const float*)lattice, src, dst,
+                       (const float*)shifts, edge_graph, n_edges, (float*)vec);
+  else if (dtype == TACE_F64)
+    hipLaunchKernelGGL(k_edge_vec_fwd<double>, g, b, 0, s, (const double*)pos, (const double*)lattice, src, dst,
+                       (const double*)shifts, edge_graph, n_edges, (double*)vec);
+  else
+    return fail("tace_edge_vec_fwd: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_edge_vec_fwd");
+}
+
+int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const int32_t* eid,
+                      const int32_t* s_rowptr, const int32_t* s_slot, int64_t n_nodes, void* g_pos, void* stream) {
+  if (n_nodes < 0 || n_nodes > INT32_MAX) return fail("tace_edge_vec_bwd: bad sizes");
+  if (n_nodes == 0) return 0;
+  if (!g_vec || !rowptr || !s_rowptr || !s_slot || !g_pos) return fail("tace_edge_vec_bwd: null pointer");
+  const dim3 g((unsigned)((n_nodes + 255) / 256)), b(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    hipLaunchKernelGGL(k_edge_vec_bwd<float>, g, b, 0, s, (const float*)g_vec, rowptr, eid, s_rowptr, s_slot,
+                       (int)n_nodes, (float*)g_pos);
+  else if (dtype == TACE_F64)
+    hipLaunchKernelGGL(k_edge_vec_bwd<double>, g, b, 0, s, (const double*)g_vec, rowptr, eid, s_rowptr, s_slot,
+                       (int)n_nodes, (double*)g_pos);
+  else
+    return fail("tace_edge_vec_bwd: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_edge_vec_bwd");
 }
 
 int64_t tace_nl_workspace_bytes(int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff) {

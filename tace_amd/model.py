@@ -120,8 +120,8 @@ class e3nnLinear(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.randn(self.lay.weight_numel))
         self.bias = torch.nn.Parameter(torch.zeros(self.lay.bias_numel)) if bias and self.lay.bias_numel else None
 
-    def forward(self, x):
-        out = self.lay.apply(x, self.weight)
+    def forward(self, x, grouped: bool = False):
+        out = _LinearFn.apply(x, self.weight, self.lay, None, grouped)
         return out + self.lay.bias_full(self.bias) if self.bias is not None else out
 
 
@@ -138,10 +138,11 @@ class e3nnElementLinear(torch.nn.Module):
         self.bias = (torch.nn.Parameter(torch.zeros(num_elements, self.lay.bias_numel))
                      if bias and self.lay.bias_numel else None)
 
-    def forward_sorted(self, xs: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor) -> torch.Tensor:
-        """``xs`` rows in species-sorted order; returns rows in the same order."""
-        parts = [self.lay.apply(xs[a:b], self.weight[s]) for (s, a, b) in sp.ranges]
-        out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=0)
+    def forward_sorted(self, xs: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor,
+                       grouped: bool = False) -> torch.Tensor:
+        """``xs`` rows in species-sorted order (e3nn or group-major layout);
+        returns e3nn-layout rows in the same order."""
+        out = _LinearFn.apply(xs, self.weight, self.lay, sp.ranges, grouped)
         if self.bias is not None:
             out = out + self.lay.bias_full(attrs_sorted @ self.bias)
         return out
@@ -152,66 +153,97 @@ class e3nnElementLinear(torch.nn.Module):
 
     def forward_grouped(self, xg: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor) -> torch.Tensor:
         """``xg``: species-sorted nodes in the group-major layout of ``irreps_in``."""
-        out = _GroupedSpeciesLinear.apply(xg, self.weight, self.lay, sp.ranges)
-        if self.bias is not None:
-            out = out + self.lay.bias_full(attrs_sorted @ self.bias)
-        return out
+        return self.forward_sorted(xg, sp, attrs_sorted, grouped=True)
 
 
-class _GroupedSpeciesLinear(torch.autograd.Function):
-    """Per-species linear on a group-major input (``include/tace_hip.h``): the
-    input group of irrep l is one [N*(2l+1), K] matrix over species-sorted
-    nodes, so each (species, instruction) is a single GEMM with no transpose
-    of the large operand.  Output and its gradient are in e3nn layout."""
+def _block_rows(x: torch.Tensor, lay_sl, a: int, b: int, grouped: bool) -> torch.Tensor:
+    """Rows a..b of input block (s, m, d) as a [(b-a)*d, m] matrix (a copy only
+    for an e3nn-layout block with d > 1)."""
+    s, m, d = lay_sl
+    Z = x.shape[0]
+    if grouped:
+        return x.view(-1)[Z * s + a * d * m:Z * s + b * d * m].view((b - a) * d, m)
+    if d == 1:
+        return x[a:b, s:s + m]
+    return x[a:b, s:s + m * d].reshape(b - a, m, d).transpose(1, 2).reshape((b - a) * d, m)
+
+
+def _put_rows(dst: torch.Tensor, y: torch.Tensor, lay_sl, a: int, b: int, grouped: bool, accumulate: bool):
+    """Inverse of ``_block_rows``: write / add the [(b-a)*d, m] matrix y."""
+    s, m, d = lay_sl
+    Z = dst.shape[0]
+    if grouped:
+        v = dst.view(-1)[Z * s + a * d * m:Z * s + b * d * m].view((b - a) * d, m)
+    elif d == 1:
+        v = dst[a:b, s:s + m]
+    else:
+        v = dst[a:b, s:s + m * d].view(b - a, m, d)
+        y = y.view(b - a, d, m).transpose(1, 2)
+    v.add_(y) if accumulate else v.copy_(y)
+
+
+class _LinearFn(torch.autograd.Function):
+    """e3nn ``o3.Linear`` as GEMMs, forward and backward written straight into
+    one output / one input-gradient buffer (no per-slice zero-filled gradients).
+
+    ``weight`` is [numel] (shared) or [S, numel] applied on the row ranges
+    ``ranges`` = [(species, a, b)] of species-sorted nodes.  ``grouped``: the
+    input is in the group-major layout (``include/tace_hip.h``); the output is
+    always e3nn layout."""
 
     @staticmethod
-    def forward(ctx, xg, weight, lay: "_LinearLayout", ranges):
-        Nn = xg.shape[0]
-        flat = xg.view(-1)
-        out = xg.new_zeros(Nn, lay.dim_out)
+    def forward(ctx, x, weight, lay: "_LinearLayout", ranges, grouped: bool):
+        Z = x.shape[0]
+        out = x.new_zeros(Z, lay.dim_out)
+        shared = weight.dim() == 1
+        rr = [(None, 0, Z)] if shared else ranges
         for (i, o, off, mi, mo, pw) in lay.ins:
-            s_in, K, d = lay.sl_in[i]
-            X = flat[Nn * s_in:Nn * (s_in + K * d)].view(Nn * d, K)
-            so = lay.sl_out[o][0]
-            for (sp, a, b) in ranges:
-                Y = X[a * d:b * d] @ (weight[sp, off:off + mi * mo].view(mi, mo) * pw)
-                out[a:b, so:so + mo * d].view(b - a, mo, d).add_(Y.view(b - a, d, mo).transpose(1, 2))
-        ctx.save_for_backward(xg, weight)
-        ctx.lay, ctx.ranges = lay, ranges
+            for (sp, a, b) in rr:
+                if b <= a:
+                    continue
+                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo) * pw
+                Y = _block_rows(x, lay.sl_in[i], a, b, grouped) @ W
+                _put_rows(out, Y, lay.sl_out[o], a, b, False, True)
+        ctx.save_for_backward(x, weight)
+        ctx.lay, ctx.ranges, ctx.grouped = lay, ranges, grouped
         return out
 
     @staticmethod
     def backward(ctx, gout):
-        xg, weight = ctx.saved_tensors
-        lay, ranges = ctx.lay, ctx.ranges
-        Nn = xg.shape[0]
-        flat = xg.view(-1)
-        gx = gw = None
-        if ctx.needs_input_grad[0]:
-            gx = torch.empty_like(xg)
-            gflat = gx.view(-1)
-            covered = set()
-            for (i, o, off, mi, mo, pw) in lay.ins:
-                covered.add(i)
-            for i, (s_in, K, d) in enumerate(lay.sl_in):
-                if i not in covered:
-                    gflat[Nn * s_in:Nn * (s_in + K * d)].zero_()
-        if ctx.needs_input_grad[1]:
-            gw = torch.zeros_like(weight)
+        x, weight = ctx.saved_tensors
+        lay, grouped = ctx.lay, ctx.grouped
+        Z = x.shape[0]
+        shared = weight.dim() == 1
+        rr = [(None, 0, Z)] if shared else ctx.ranges
+        gx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
+        readers = {}
+        for (i, o, *_r) in lay.ins:
+            readers[i] = readers.get(i, 0) + 1
+        if gx is not None:
+            for i, sl in enumerate(lay.sl_in):
+                if i not in readers:
+                    s, m, d = sl
+                    if grouped:
+                        gx.view(-1)[Z * s:Z * (s + m * d)].zero_()
+                    else:
+                        gx[:, s:s + m * d].zero_()
+        seen = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
-            s_in, K, d = lay.sl_in[i]
-            so = lay.sl_out[o][0]
-            for (sp, a, b) in ranges:
-                G = gout[a:b, so:so + mo * d].reshape(b - a, mo, d).transpose(1, 2).reshape((b - a) * d, mo)
-                W = weight[sp, off:off + mi * mo].view(mi, mo)
+            for (sp, a, b) in rr:
+                if b <= a:
+                    continue
+                G = _block_rows(gout, lay.sl_out[o], a, b, False)
+                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
                 if gx is not None:
-                    dst = gflat[Nn * s_in + a * d * K:Nn * s_in + b * d * K].view((b - a) * d, K)
-                    torch.mm(G, W.t(), out=dst)
-                    dst.mul_(pw)
+                    _put_rows(gx, (G @ W.t()) * pw, lay.sl_in[i], a, b, grouped, (i, sp) in seen)
                 if gw is not None:
-                    X = flat[Nn * s_in + a * d * K:Nn * s_in + b * d * K].view((b - a) * d, K)
-                    gw[sp, off:off + mi * mo] += (X.t() @ G).reshape(-1) * pw
-        return gx, gw, None, None
+                    X = _block_rows(x, lay.sl_in[i], a, b, grouped)
+                    tgt = gw if shared else gw[sp]
+                    tgt[off:off + mi * mo] += (X.t() @ G).reshape(-1) * pw
+            for (sp, a, b) in rr:
+                seen.add((i, sp))
+        return gx, gw, None, None, None
 
 
 class mlpLinear(torch.nn.Module):
@@ -260,8 +292,8 @@ class O3ScatterTensorProduct(torch.nn.Module):
         self.weight_numel = self.C * len(paths)
         self.key = ops.variant_key("uvu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
 
-    def forward(self, x, y, w, plan: ops.EdgePlan):
-        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C)
+    def forward(self, x, y, w, plan: ops.EdgePlan, layout: int = 0):
+        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C, layout)
 
 
 class uuuTensorProduct(torch.nn.Module):
@@ -328,7 +360,8 @@ class O3CgtpInteraction(torch.nn.Module):
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
         w = self.edge_info(R)
-        m = self.linear_down(self.rejector(x, Y, w, plan))
+        # the scatter writes group-major [N*(2l+1), paths*C] blocks = linear_down's GEMM operands
+        m = self.linear_down(self.rejector(x, Y, w, plan, ops.LAYOUT_OUT_GROUPED), grouped=True)
         m = m / self.avg_num_neighbors
         m = self.linear_nonlinearity(_gate(m, self.gated))
         return m, sc
@@ -640,9 +673,13 @@ class TensorModel(torch.nn.Module):
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
         plan = data.get("_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
-        src, dst = ei[0], ei[1]
-        # prepare_graph (adapter.py:334-347); the +1e-9 of the length is applied in the kernel
-        vec = pos_s[dst] - pos_s[src] + torch.einsum("ni,nij->nj", data["edge_shifts"], lat_s[batch[src]])
+        # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
+        # +1e-9 of the length is applied in the edge-basis kernel
+        dst32 = data.get("_dst32")
+        if dst32 is None:
+            dst32 = ei[1].to(torch.int32)
+        egraph = None if num_graphs == 1 else batch[ei[0]].to(torch.int32)
+        vec = ops.edge_vectors(pos_s, lat_s, data["edge_shifts"], plan, dst32, egraph)
         E, e_node = self.readout_fn.energy(data, plan, vec)
         out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, stress=None,
                                                       virials=None)

@@ -190,7 +190,7 @@ def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cuto
 # ------------------------------------------------------ edge tensor product ----
 class _EdgeTP(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int):
+    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int):
         Nn, E = plan.n_nodes, plan.n_edges
         dt = x.dtype
         _req(x, "x", dt, (Nn, C * var.d1))
@@ -200,10 +200,10 @@ class _EdgeTP(torch.autograd.Function):
         tok = _t0("edge_tp_fwd:" + var.key)
         N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                          plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), Nn, E, C,
-                                         out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
+                                         layout, out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
         _t1(tok, (Nn, E, C))
         ctx.save_for_backward(x, y, w)
-        ctx.plan, ctx.var, ctx.C = plan, var, C
+        ctx.plan, ctx.var, ctx.C, ctx.layout = plan, var, C, layout
         return out
 
     @staticmethod
@@ -223,15 +223,69 @@ class _EdgeTP(torch.autograd.Function):
         tok = _t0("edge_tp_bwd:" + var.key)
         N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                          gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
-                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, N.ptr(s_rowptr),
+                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, ctx.layout,
+                                         N.ptr(s_rowptr),
                                          N.ptr(s_slot), N.ptr(ws), 0 if ws is None else ws.numel(), N.ptr(gx),
                                          gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
         _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
-        return gx, gy, gw, None, None, None
+        return gx, gy, gw, None, None, None, None
 
 
-def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int) -> torch.Tensor:
-    return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C)
+def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
+    """``layout`` 0: e3nn output; LAYOUT_OUT_GROUPED: group-major output."""
+    return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout))
+
+
+# ------------------------------------------------------------ edge vectors ----
+class _EdgeVectors(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, pos, lattice, shifts, plan: EdgePlan, dst: torch.Tensor, edge_graph):
+        E = plan.n_edges
+        dt = pos.dtype
+        _req(pos, "positions", dt, (plan.n_nodes, 3))
+        _req(shifts, "edge_shifts", dt, (E, 3))
+        _req(lattice, "lattice", dt)
+        vec = torch.empty(E, 3, dtype=dt, device=pos.device)
+        N.check(N.lib().tace_edge_vec_fwd(N.dtype_code(dt), pos.data_ptr(), lattice.data_ptr(), plan.src.data_ptr(),
+                                          dst.data_ptr(), shifts.data_ptr(), N.ptr(edge_graph), E, vec.data_ptr(),
+                                          N.stream_ptr(pos.device)), "tace_edge_vec_fwd")
+        ctx.save_for_backward(shifts)
+        ctx.plan, ctx.edge_graph, ctx.nlat = plan, edge_graph, lattice.shape[0]
+        return vec
+
+    @staticmethod
+    def backward(ctx, g):
+        (shifts,) = ctx.saved_tensors
+        plan = ctx.plan
+        g = g.contiguous()
+        gpos = glat = None
+        if ctx.needs_input_grad[0]:
+            s_rowptr, s_slot = plan.sender_csr()
+            gpos = torch.empty(plan.n_nodes, 3, dtype=g.dtype, device=g.device)
+            N.check(N.lib().tace_edge_vec_bwd(N.dtype_code(g.dtype), g.data_ptr(), plan.rowptr.data_ptr(),
+                                              N.ptr(plan.eid), s_rowptr.data_ptr(), s_slot.data_ptr(),
+                                              plan.n_nodes, gpos.data_ptr(), N.stream_ptr(g.device)),
+                    "tace_edge_vec_bwd")
+        if ctx.needs_input_grad[1]:
+            outer = (shifts.unsqueeze(2) * g.unsqueeze(1)).reshape(-1, 9)
+            if ctx.edge_graph is None:
+                glat = outer.sum(0).view(1, 3, 3)
+            else:
+                glat = torch.zeros(ctx.nlat, 9, dtype=g.dtype, device=g.device).index_add_(
+                    0, ctx.edge_graph.long(), outer).view(-1, 3, 3)
+        return gpos, glat, None, None, None, None
+
+
+def edge_vectors(pos, lattice, shifts, plan: EdgePlan, dst: torch.Tensor, edge_graph=None) -> torch.Tensor:
+    """vec[e] = pos[dst] - pos[src] + shifts[e] . lattice[edge_graph[e]]
+    (``tace/models/adapter.py:334-340``) with a deterministic CSR backward.
+    ``dst`` int32 [E] in edge-id order; ``edge_graph`` int32 [E] or None (one graph)."""
+    if dst.dtype != torch.int32:
+        dst = dst.to(torch.int32)
+    if edge_graph is not None and edge_graph.dtype != torch.int32:
+        edge_graph = edge_graph.to(torch.int32)
+    return _EdgeVectors.apply(pos.contiguous(), lattice.contiguous(), shifts.contiguous(), plan, dst.contiguous(),
+                              None if edge_graph is None else edge_graph.contiguous())
 
 
 # ---------------------------------------------------------------- uuu ----

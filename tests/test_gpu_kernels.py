@@ -230,3 +230,61 @@ def test_grouped_layout_helpers_roundtrip():
     x = torch.randn(5, 8 * (1 + 3 + 3 + 5), dtype=torch.float64)
     ls = [0, 1, 1, 2]
     torch.testing.assert_close(ops.from_grouped(ops.to_grouped(x, ls, 8), ls, 8), x, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("in1,lmax,C", [([0], 3, 128), ([0, 1, 2, 3], 3, 128), ([0, 1, 2], 2, 64)])
+def test_edge_tp_grouped_output_matches_oracle(cuda, dtype, in1, lmax, C):
+    g = torch.Generator().manual_seed(7 + C)
+    Nn, E = 31, 200
+    ei = torch.stack([torch.randint(0, Nn, (E,), generator=g), torch.randint(0, Nn, (E,), generator=g)])
+    tp = om.ScatterTP(_irreps(in1, C), oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)])
+    out_ls = [ir[0] for _, ir in tp.out]
+    x = torch.randn(Nn, oso3.irreps_dim(_irreps(in1, C)), generator=g, dtype=torch.float64).to(dtype).double()
+    y = torch.randn(E, (lmax + 1) ** 2, generator=g, dtype=torch.float64).to(dtype).double()
+    w = torch.randn(E, tp.weight_numel, generator=g, dtype=torch.float64).to(dtype).double()
+    x.requires_grad_(True), y.requires_grad_(True), w.requires_grad_(True)
+    out_o = tp(x, y, w, ei)
+    go = torch.randn(out_o.shape, generator=g, dtype=torch.float64).to(dtype).double()
+    gx_o, gy_o, gw_o = torch.autograd.grad((out_o * go).sum(), [x, y, w])
+    var = ops.find_variant(ops.variant_key("uvu", in1, list(range(lmax + 1)), list(range(lmax + 1))))
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), Nn)
+    xg, yg, wg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, y, w))
+    out = ops.edge_tp_scatter(xg, yg, wg, plan, var, C, ops.LAYOUT_OUT_GROUPED)
+    close(ops.from_grouped(out, out_ls, C), out_o, dtype, "out")
+    gg = ops.to_grouped(go.to(dtype).to(cuda), out_ls, C)
+    gx, gy, gw = torch.autograd.grad((out * gg).sum(), [xg, yg, wg])
+    close(gx, gx_o, dtype, "grad_x")
+    close(gy, gy_o, dtype, "grad_y")
+    close(gw, gw_o, dtype, "grad_w")
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("two_graphs", [False, True])
+@pytest.mark.parametrize("sorted_edges", [True, False])
+def test_edge_vectors_and_position_gradient(cuda, dtype, two_graphs, sorted_edges):
+    g = torch.Generator().manual_seed(3)
+    Nn, E = 40, 500
+    src = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.randint(0, Nn, (E,), generator=g)
+    if sorted_edges:
+        o = torch.argsort(dst, stable=True)
+        src, dst = src[o], dst[o]
+    pos = torch.randn(Nn, 3, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    B = 2 if two_graphs else 1
+    lat = (torch.eye(3, dtype=torch.float64) * 7 + torch.randn(B, 3, 3, generator=g, dtype=torch.float64)).to(dtype).double()
+    lat.requires_grad_(True)
+    batch = (torch.arange(Nn) >= Nn // 2).long() if two_graphs else torch.zeros(Nn, dtype=torch.long)
+    sh = torch.randint(-1, 2, (E, 3), generator=g).double()
+    eg = batch[src]
+    ref = pos[dst] - pos[src] + torch.einsum("ni,nij->nj", sh, lat[eg])
+    gv = torch.randn(E, 3, generator=g, dtype=torch.float64).to(dtype).double()
+    gp_o, gl_o = torch.autograd.grad((ref * gv).sum(), [pos, lat])
+    plan = ops.EdgePlan.from_edge_index(torch.stack([src, dst]).to(cuda), Nn)
+    p = pos.detach().to(dtype).to(cuda).requires_grad_(True)
+    L = lat.detach().to(dtype).to(cuda).requires_grad_(True)
+    vec = ops.edge_vectors(p, L, sh.to(dtype).to(cuda), plan, dst.to(cuda), eg.to(cuda) if two_graphs else None)
+    close(vec, ref, dtype, "vec")
+    gp, gl = torch.autograd.grad((vec * gv.to(dtype).to(cuda)).sum(), [p, L])
+    close(gp, gp_o, dtype, "grad_pos")
+    close(gl, gl_o, dtype, "grad_lattice")

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED)
-    assert lib.tace_abi_version() == 3
+    assert lib.tace_abi_version() == 4
 
 
 def test_variant_registry_and_errors():
@@ -38,7 +38,7 @@ def test_variant_registry_and_errors():
     assert lib.tace_tp_find(b"uvu|9|9|9") == -1
     assert b"no compiled" in lib.tace_last_error()
     # argument checks fire before any device work
-    assert lib.tace_edge_tp_fwd(0, 0, None, None, None, None, None, None, 1, 1, 0, None, None) < 0
+    assert lib.tace_edge_tp_fwd(0, 0, None, None, None, None, None, None, 1, 1, 0, 0, None, None) < 0
     assert lib.tace_uuu_fwd(10 ** 6, 0, None, None, 1, 1, 0, None, None) < 0
     cell = np.zeros(9)
     pbc = np.ones(3, dtype=np.int32)

@@ -32,8 +32,8 @@ def cases():
     return {
         "si64_fp64": dict(structs=lambda: [structures.si_diamond(seed=1)], preset="si64", stress=True, over={}),
         "fcc1024": dict(structs=lambda: [structures.fcc_alloy(seed=1)], preset="fcc1024", stress=False, over={}),
-        "water1536": dict(structs=lambda: [structures.water_box(n_side=8, box=49.7 / 2, seed=2)], preset="water12k",
-                          stress=False, over={}),
+        "water375": dict(structs=lambda: [structures.water_box(n_side=5, box=49.7 / 16 * 5, seed=2)],
+                         preset="water12k", stress=False, over={}),
     }
 
 

@@ -1,0 +1,68 @@
+"""Golden fixtures (tests/golden/*.npz, written by tests/golden/make_golden.py).
+
+The CPU test re-derives the small fixture with the oracle (regression of the
+oracle itself); the GPU tests compare the HIP model, built with the same seeded
+weights, against the stored float64 oracle outputs at full configuration size.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tace_amd import model as pm
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    import sys
+
+    sys.path.insert(0, HERE)
+    import make_golden
+
+    spec = make_golden.cases()[name]
+    fix = np.load(os.path.join(HERE, f"{name}.npz"))
+    structs, edges, cfg, ref, d = make_golden.build(name, spec, int(fix["weight_seed"][0]))
+    np.testing.assert_allclose(make_golden.weight_checksum(ref), fix["weight_checksum"], rtol=1e-12)
+    assert d["edge_index"].shape[1] == int(fix["num_edges"][0])
+    return spec, fix, structs, edges, cfg, ref, d
+
+
+def test_oracle_reproduces_si64_golden():
+    from oracle import model as om
+
+    spec, fix, structs, edges, cfg, ref, d = _load("si64_fp64")
+    out = om.compute(ref, d, forces=True, stress=True)
+    np.testing.assert_allclose(out["energy"].numpy(), fix["energy"], rtol=1e-12)
+    np.testing.assert_allclose(out["forces"].numpy(), fix["forces"], atol=1e-12)
+    np.testing.assert_allclose(out["stress"].numpy(), fix["stress"], atol=1e-12)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,dtype", [("fcc1024", torch.float32), ("fcc1024", torch.float64),
+                                        ("water375", torch.float32)])
+def test_gpu_model_matches_golden(cuda, name, dtype):
+    from tace_amd import data
+
+    if not os.path.exists(os.path.join(HERE, f"{name}.npz")):
+        pytest.skip(f"fixture {name} not generated")
+    spec, fix, structs, edges, cfg, ref, d = _load(name)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        m = pm.create_model(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    pm.load_reference_state_dict(m.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
+                                                for k, v in ref.state_dict().items()})
+    m = m.to(cuda).eval()
+    for p in m.parameters():
+        p.requires_grad_(False)
+    m.reset_target_property(["energy", "forces"])
+    out = m(data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda))
+    E, F = out["energy"].double().cpu().numpy(), out["forces"].double().cpu().numpy()
+    e_rel, f_abs = (1e-10, 1e-8) if dtype == torch.float64 else (1e-5, 1e-4)
+    assert np.max(np.abs(E - fix["energy"]) / np.abs(fix["energy"])) < e_rel
+    assert np.max(np.abs(F - fix["forces"])) < f_abs

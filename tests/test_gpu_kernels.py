@@ -288,3 +288,21 @@ def test_edge_vectors_and_position_gradient(cuda, dtype, two_graphs, sorted_edge
     gp, gl = torch.autograd.grad((vec * gv.to(dtype).to(cuda)).sum(), [p, L])
     close(gp, gp_o, dtype, "grad_pos")
     close(gl, gl_o, dtype, "grad_lattice")
+
+
+def test_slot_adapter_matches_oracle_with_unsorted_edges(cuda):
+    """The plug-in-slot contract of fused.py:259-271 through tace_amd.slot."""
+    from tace_amd import slot
+
+    C, lmax = 64, 2
+    node = "+".join(f"{C}x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
+    sh = "+".join(f"1x{l}{'e' if l % 2 == 0 else 'o'}" for l in range(lmax + 1))
+    tp_h = slot.e3nnHipScatterTensorProduct(node, sh, node)
+    tp_o = om.ScatterTP(oso3.parse_irreps(node), oso3.sh_irreps(lmax), oso3.parse_irreps(node))
+    g = torch.Generator().manual_seed(9)
+    Nn, E = 25, 300
+    ei = torch.stack([torch.randint(0, Nn, (E,), generator=g), torch.randint(0, Nn, (E,), generator=g)])
+    x = torch.randn(Nn, oso3.irreps_dim(oso3.parse_irreps(node)), generator=g, dtype=torch.float64)
+    y = torch.randn(E, (lmax + 1) ** 2, generator=g, dtype=torch.float64)
+    w = torch.randn(E, tp_o.weight_numel, generator=g, dtype=torch.float64)
+    close(tp_h(x.to(cuda), y.to(cuda), w.to(cuda), ei.to(cuda)), tp_o(x, y, w, ei), torch.float64, "slot out")

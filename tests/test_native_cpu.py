@@ -80,3 +80,20 @@ def test_product_refuses_cpu_tensors():
              ptr=torch.tensor([0, 2]))
     with pytest.raises(RuntimeError, match="GPU"):
         m(d)
+
+
+def test_slot_adapters_validate_the_reference_contract():
+    from tace_amd import slot
+
+    sh = "1x0e+1x1o+1x2e+1x3o"
+    node = "128x0e+128x1o+128x2e+128x3o"
+    tp = slot.e3nnHipScatterTensorProduct(node, sh, node)
+    assert tp.weight_numel == 128 * 23
+    from tace_amd.so3 import Irreps, generate_paths
+    paths, actual = generate_paths(Irreps(node), Irreps(node), Irreps(sh), "uvu")
+    ins = [(i, j, k, "uvu", True) for i, j, k in paths]
+    slot.e3nnHipScatterTensorProduct(node, sh, actual, ins)
+    with pytest.raises(ValueError):
+        slot.e3nnHipScatterTensorProduct(node, sh, actual, ins[::-1])
+    u = slot.e3nnHipUuuTensorProduct(node, node, "1x0e+1x1o+1x2e+1x3o", identical_inputs=True)
+    assert u.C == 128

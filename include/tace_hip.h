@@ -37,7 +37,8 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 4
+#define TACE_HIP_ABI_VERSION 5
+#define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
 
@@ -64,8 +65,10 @@ int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dou
 /* out[n] = sum_{e: dst(e)=n} TP(x[src(e)], y[e], w[e])  -- uvu, mul2 = 1.
  * Edges are visited in receiver-CSR order: rowptr[n_nodes+1] over the sorted
  * edge list, eid[k] the edge id of sorted slot k (NULL = identity), src[e] the
- * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout]
- * (layout 0 or TACE_LAYOUT_OUT_GROUPED for out / gout). */
+ * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout];
+ * 1 <= C <= TACE_MAX_CHANNELS.  layout: any
+ * combination of TACE_LAYOUT_IN1_GROUPED (x, gx) and TACE_LAYOUT_OUT_GROUPED
+ * (out, gout). */
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
                      const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
                      int32_t layout, void* out, void* stream);
@@ -73,7 +76,8 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
  * (NULL to skip).  All outputs are fully overwritten, no atomics: the
  * per-edge grad_x contributions go to `workspace` (>= E*C*d1 elements, one
  * row per receiver-sorted slot) and are summed per sender through the sender
- * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender. */
+ * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender.
+ * gy is summed over channels in a fixed order. */
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
                      int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,

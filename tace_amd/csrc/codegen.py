@@ -82,139 +82,229 @@ class Variant:
             self.cg.append(nz)
 
     # ---------------------------------------------------------------- uvu ----
-    def _x_loads(self, ptr: str, guard: str) -> List[str]:
-        out = []
-        for b, d in enumerate(self.d1):
-            for m in range(d):
-                out.append(f"    const T x{b}_{m} = {guard} ? {ptr}[(size_t)C * {self.off1[b]} + (size_t)u * {d} + {m}] : T(0);")
+    def _ld_x(self, node: str, b: int, m: int) -> str:
+        e3, gm = self._addr("in1", b, m)
+        e3, gm = e3.replace("(size_t)n ", f"(size_t){node} "), gm.replace("(size_t)n ", f"(size_t){node} ")
+        return f"(IN1_GM ? x[{gm}] : x[{e3}])"
+
+    def parts(self, cap: int = 40) -> List[List[int]]:
+        """Input blocks split into consecutive parts whose paths hold at most
+        ``cap`` output components per channel: one kernel per part, so the
+        per-lane accumulators / output gradients of a part stay in registers
+        at an occupancy of several wavefronts per SIMD.  Parts touch disjoint
+        paths, x blocks, weights and outputs (grad_y is accumulated)."""
+        out, cur, acc = [], [], 0
+        for b in range(len(self.in1)):
+            d3 = sum(self.dout[p] for p in range(len(self.paths)) if self.path_blocks[p][0] == b)
+            if cur and acc + d3 > cap:
+                out.append(cur)
+                cur, acc = [], 0
+            cur.append(b)
+            acc += d3
+        if cur:
+            out.append(cur)
         return out
 
-    def _y_loads(self, ptr: str) -> List[str]:
-        return [f"    const T y{b}_{m} = {ptr}[{self.off2[b] + m}];" for b, d in enumerate(self.d2) for m in range(d)]
+    def _part_paths(self, blocks: Sequence[int]) -> List[int]:
+        return [p for p in range(len(self.paths)) if self.path_blocks[p][0] in blocks]
 
-    def _products(self) -> Tuple[List[str], Dict]:
-        used = set()
-        for p, (b1, b2) in enumerate(self.path_blocks):
-            for (i, j, k, c) in self.cg[p]:
-                used.add((b1, i, b2, j))
-        lines = [f"    const T q{b1}_{i}_{b2}_{j} = x{b1}_{i} * y{b2}_{j};" for (b1, i, b2, j) in sorted(used)]
-        return lines
+    def _block_pairs(self, paths: Sequence[int]):
+        """Paths grouped by their (in1 block, in2 block); per group the (i, j)
+        products x_i y_j that some path of the group couples."""
+        groups = {}
+        for p in paths:
+            groups.setdefault(self.path_blocks[p], []).append(p)
+        out = []
+        for (b1, b2), ps in groups.items():
+            pairs = sorted({(i, j) for p in ps for (i, j, k, c) in self.cg[p]})
+            out.append((b1, b2, ps, pairs))
+        return out
 
-    def _t_expr(self, p: int, k: int) -> str:
-        b1, b2 = self.path_blocks[p]
-        terms = [f"{_lit(c)} * q{b1}_{i}_{b2}_{j}" for (i, j, kk, c) in self.cg[p] if kk == k]
-        return " + ".join(terms) if terms else "T(0)"
-
-    def emit_uvu_fwd(self) -> str:
-        P = len(self.paths)
-        L = []
-        L.append(f"template <typename T, bool OUT_GM>\n__global__ __launch_bounds__(64) void k_{self.name}_fwd(")
-        L.append("    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,")
-        L.append("    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,")
-        L.append("    T* __restrict__ out, int n_nodes, int C) {")
-        L.append("  const int n = blockIdx.x;")
-        L.append("  if (n >= n_nodes) return;")
-        L.append("  const int beg = rowptr[n], end = rowptr[n + 1];")
-        L.append(f"  const size_t DX = (size_t)C * {self.D1}, WW = (size_t)C * {P};")
-        L.append("  for (int cb = 0; cb < C; cb += 64) {")
-        L.append("    const int u = cb + (int)threadIdx.x;")
-        L.append("    const bool act = u < C;")
-        for a in range(self.DO):
-            L.append(f"    T a{a} = T(0);")
-        L.append("    for (int e = beg; e < end; ++e) {")
-        L.append("    const int ed = eid ? eid[e] : e;")
-        L.append("    const T* xs = x + (size_t)src[ed] * DX;")
-        L.append(f"    const T* ys = y + (size_t)ed * {self.D2};")
-        L.append("    const T* ws = w + (size_t)ed * WW;")
-        L += self._x_loads("xs", "act")
-        L += self._y_loads("ys")
-        for p in range(P):
-            L.append(f"    const T w{p} = act ? ws[(size_t){p} * C + u] : T(0);")
-        L += self._products()
-        for p in range(P):
-            for k in range(self.dout[p]):
-                L.append(f"    a{self.offo[p] + k} += w{p} * ({self._t_expr(p, k)});")
-        L.append("    }")
-        L.append("    if (act) {")
-        L.append("      const size_t N = (size_t)n_nodes;")
-        for p in range(P):
-            d = self.dout[p]
-            for k in range(d):
-                e3, gm = self._addr("out", p, k)
-                L.append(f"      out[OUT_GM ? ({gm}) : ({e3})] = a{self.offo[p] + k};")
-        L.append("    }")
+    def _edge_pipeline(self, L: List[str], blocks: Sequence[int], paths: Sequence[int]) -> None:
+        """Head of the edge loop: the operands of the next edge are loaded
+        while the current one is computed (x*, w*, y* hold the current edge;
+        xn*, wn*, yn* the next one).  y is uniform over the workgroup."""
+        xs = [(b, m) for b in blocks for m in range(self.d1[b])]
+        L.append("  int e = beg;")
+        L.append("  int ed = e < end ? (eid ? eid[e] : e) : 0;")
+        L.append("  int s = e < end ? src[ed] : 0;")
+        for (b, m) in xs:
+            L.append(f"  T x{b}_{m} = T(0);")
+        L += [f"  T w{p} = T(0);" for p in paths]
+        L += [f"  T y{j} = T(0);" for j in range(self.D2)]
+        L.append("  if (e < end) {")
+        for (b, m) in xs:
+            L.append(f"    x{b}_{m} = {self._ld_x('s', b, m)};")
+        L += [f"    w{p} = w[(size_t)ed * WW + (size_t){p} * C + u];" for p in paths]
+        L += [f"    y{j} = y[(size_t)ed * {self.D2} + {j}];" for j in range(self.D2)]
         L.append("  }")
-        L.append("}")
-        return "\n".join(L)
+        L.append("  for (; e < end; ++e) {")
+        L.append("    const int en = e + 1 < end ? e + 1 : e;")
+        L.append("    const int edn = eid ? eid[en] : en;")
+        L.append("    const int sn = src[edn];")
+        for (b, m) in xs:
+            L.append(f"    const T xn{b}_{m} = {self._ld_x('sn', b, m)};")
+        L += [f"    const T wn{p} = w[(size_t)edn * WW + (size_t){p} * C + u];" for p in paths]
+        L += [f"    const T yn{j} = y[(size_t)edn * {self.D2} + {j}];" for j in range(self.D2)]
 
-    def emit_uvu_bwd(self) -> str:
+    def _edge_rotate(self, L: List[str], blocks: Sequence[int], paths: Sequence[int]) -> None:
+        for b in blocks:
+            for m in range(self.d1[b]):
+                L.append(f"    x{b}_{m} = xn{b}_{m};")
+        L += [f"    w{p} = wn{p};" for p in paths]
+        L += [f"    y{j} = yn{j};" for j in range(self.D2)]
+        L.append("    ed = edn;")
+        L.append("  }")
+
+    def emit_uvu_fwd(self, q: int) -> str:
+        """Part q of out[n] = sum over edges e -> n of w_e (.) CG(x[src e], y_e):
+        the paths of the part's input blocks.  The products x_i y_j are shared
+        by the paths of one (in1, in2) block pair."""
         P = len(self.paths)
-        L = []
-        L.append(f"template <typename T, bool NEED_GX, bool OUT_GM>\n__global__ __launch_bounds__(64) void k_{self.name}_bwd(")
-        L.append("    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,")
-        L.append("    const T* __restrict__ gout,")
-        L.append("    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,")
-        L.append("    T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw, int n_nodes, int C) {")
-        L.append("  const int n = blockIdx.x;")
-        L.append("  if (n >= n_nodes) return;")
-        L.append("  const int beg = rowptr[n], end = rowptr[n + 1];")
-        L.append(f"  const size_t DX = (size_t)C * {self.D1}, WW = (size_t)C * {P};")
-        L.append("  for (int cb = 0; cb < C; cb += 64) {")
-        L.append("    const int u = cb + (int)threadIdx.x;")
-        L.append("    const bool act = u < C;")
-        L.append("    const size_t N = (size_t)n_nodes;")
-        for p in range(P):
-            d = self.dout[p]
-            for k in range(d):
-                e3, gm = self._addr("out", p, k)
-                L.append(f"    const T g{self.offo[p] + k} = act ? gout[OUT_GM ? ({gm}) : ({e3})] : T(0);")
-        L.append("    for (int e = beg; e < end; ++e) {")
-        L.append("    const int ed = eid ? eid[e] : e;")
-        L.append("    const int s = src[ed];")
-        L.append("    const T* xs = x + (size_t)s * DX;")
-        L.append(f"    const T* ys = y + (size_t)ed * {self.D2};")
-        L.append("    const T* ws = w + (size_t)ed * WW;")
-        L += self._x_loads("xs", "act")
-        L += self._y_loads("ys")
-        for p in range(P):
-            L.append(f"    const T w{p} = act ? ws[(size_t){p} * C + u] : T(0);")
-        L += self._products()
-        for b, d in enumerate(self.d1):
-            for m in range(d):
-                L.append(f"    T hx{b}_{m} = T(0);")
-        for b, d in enumerate(self.d2):
-            for m in range(d):
-                L.append(f"    T hy{b}_{m} = T(0);")
-        for p in range(P):
-            b1, b2 = self.path_blocks[p]
-            d = self.dout[p]
+        blocks = self.parts()[q]
+        paths = self._part_paths(blocks)
+        L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd{q}(",
+             "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
+             "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+             "    T* __restrict__ out, int n_nodes, int C) {",
+             "  const int n = tp_node(n_nodes);",
+             "  const int u = (int)threadIdx.x;",
+             "  if (n < 0 || u >= C) return;",
+             "  const size_t N = (size_t)n_nodes;",
+             "  const int beg = rowptr[n], end = rowptr[n + 1];",
+             f"  const size_t WW = (size_t)C * {P};"]
+        for p in paths:
+            L += [f"  T a{self.offo[p] + k} = T(0);" for k in range(self.dout[p])]
+        self._edge_pipeline(L, blocks, paths)
+        for (b1, b2, ps, pairs) in self._block_pairs(paths):
+            o2 = self.off2[b2]
             L.append("    {")
-            for k in range(d):
-                L.append(f"      const T t{k} = {self._t_expr(p, k)};")
-            gsum = " + ".join(f"g{self.offo[p] + k} * t{k}" for k in range(d))
-            L.append(f"      if (act) gw[(size_t)ed * WW + (size_t){p} * C + u] = {gsum};")
-            for k in range(d):
-                L.append(f"      const T a{k} = w{p} * g{self.offo[p] + k};")
-            for (i, j, k, c) in self.cg[p]:
-                L.append(f"      if (NEED_GX) hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * a{k});")
-                L.append(f"      hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * a{k});")
+            for (i, j) in pairs:
+                L.append(f"      const T q{i}_{j} = x{b1}_{i} * y{o2 + j};")
+            for p in ps:
+                byk = {}
+                for (i, j, k, c) in self.cg[p]:
+                    byk.setdefault(k, []).append((i, j, c))
+                for k in range(self.dout[p]):
+                    if k in byk:
+                        t = " + ".join(f"{_lit(c)} * q{i}_{j}" for i, j, c in byk[k])
+                        L.append(f"      a{self.offo[p] + k} += w{p} * ({t});")
             L.append("    }")
-        # grad_x contribution of this edge, one row per receiver-sorted slot;
-        # summed per sender by k_seg_rowsum (deterministic, no atomics)
-        L.append("    if (NEED_GX && act) {")
-        L.append("      T* cb = cbuf + (size_t)e * DX;")
-        for b, d in enumerate(self.d1):
-            for m in range(d):
-                L.append(f"      cb[(size_t)C * {self.off1[b]} + (size_t)u * {d} + {m}] = hx{b}_{m};")
-        L.append("    }")
-        L.append(f"    T* gys = gy + (size_t)ed * {self.D2};")
-        for b, d in enumerate(self.d2):
-            for m in range(d):
-                L.append(f"    {{ const T v = wave_sum(hy{b}_{m}); if (threadIdx.x == 0) gys[{self.off2[b] + m}] = (cb == 0) ? v : gys[{self.off2[b] + m}] + v; }}")
-        L.append("    }")
-        L.append("  }")
+        self._edge_rotate(L, blocks, paths)
+        for p in paths:
+            for k in range(self.dout[p]):
+                e3, gm = self._addr("out", p, k)
+                L.append(f"  out[OUT_GM ? ({gm}) : ({e3})] = a{self.offo[p] + k};")
         L.append("}")
         return "\n".join(L)
+
+    def emit_uvu_bwd(self, q: int) -> str:
+        """Part q (paths of the part's input blocks).  Per edge e (slot of
+        receiver n, sender s), channel u, path p:
+          psi_i   = sum_{j,k} c^p_ijk y_j g_pk         (g = grad of out[n])
+          gw_p    = sum_i x_i psi_i
+          hx_i   += w_p psi_i                            -> cbuf row of slot e
+          hy_j   += sum_{i,k} c^p_ijk x_i (w_p g_pk)     -> summed over channels
+        grad_y is reduced over the 64 lanes of each wavefront (transposing
+        butterfly, 17 shuffles for 16 values) and over the workgroup's
+        wavefronts through LDS in a fixed order, then added to what earlier
+        parts wrote: deterministic, no atomics."""
+        P = len(self.paths)
+        blocks = self.parts()[q]
+        paths = self._part_paths(blocks)
+        assert self.D2 <= 16
+        L = [f"template <typename T, bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_bwd{q}(",
+             "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
+             "    const T* __restrict__ gout,",
+             "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+             "    T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw, int n_nodes, int C) {",
+             "  __shared__ T red[2][8][16];",
+             "  const int n = tp_node(n_nodes);",
+             "  if (n < 0) return;",
+             "  const int lane = (int)threadIdx.x & 63, wv = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;",
+             "  const bool act = (int)threadIdx.x < C;",
+             "  const int u = act ? (int)threadIdx.x : C - 1;",
+             "  const size_t N = (size_t)n_nodes;",
+             "  const int beg = rowptr[n], end = rowptr[n + 1];",
+             f"  const size_t WW = (size_t)C * {P}, DX = (size_t)C * {self.D1};"]
+        for p in paths:
+            for k in range(self.dout[p]):
+                e3, gm = self._addr("out", p, k)
+                # lanes past C contribute nothing: their grad_out is zero
+                L.append(f"  const T g{self.offo[p] + k} = act ? gout[OUT_GM ? ({gm}) : ({e3})] : T(0);")
+        self._edge_pipeline(L, blocks, paths)
+        for b in blocks:
+            for m in range(self.d1[b]):
+                L.append(f"    T hx{b}_{m} = T(0);")
+        L += [f"    T hy{j} = T(0);" for j in range(16)]
+        for p in paths:
+            b1, b2 = self.path_blocks[p]
+            o, o2 = self.offo[p], self.off2[b2]
+            L.append("    {")
+            byjk, byik = {}, {}
+            for (i, j, k, c) in self.cg[p]:
+                byjk.setdefault((j, k), []).append((i, c))
+                byik.setdefault((i, k), []).append((j, c))
+            used_i = sorted({i for (i, j, k, c) in self.cg[p]})
+            L += [f"      T psi{i} = T(0);" for i in used_i]
+            for (j, k), ic in sorted(byjk.items()):
+                L.append(f"      {{ const T r = y{o2 + j} * g{o + k};")
+                L += [f"        psi{i} += {_lit(c)} * r;" for i, c in ic]
+                L.append("      }")
+            L.append(f"      if (act) gw[(size_t)ed * WW + (size_t){p} * C + u] = "
+                     f"{' + '.join(f'x{b1}_{i} * psi{i}' for i in used_i)};")
+            L.append("      if (NEED_GX) {")
+            L += [f"        hx{b1}_{i} += w{p} * psi{i};" for i in used_i]
+            L.append("      }")
+            used_k = sorted({k for (i, j, k, c) in self.cg[p]})
+            L += [f"      const T a{k} = w{p} * g{o + k};" for k in used_k]
+            for (i, k), jc in sorted(byik.items()):
+                L.append(f"      {{ const T z = x{b1}_{i} * a{k};")
+                L += [f"        hy{o2 + j} += {_lit(c)} * z;" for j, c in jc]
+                L.append("      }")
+            L.append("    }")
+        L.append("    if (NEED_GX && act) {")
+        L.append("      T* __restrict__ cb = cbuf + (size_t)e * DX;")
+        for b in blocks:
+            for m in range(self.d1[b]):
+                e3, gm = self._row_addr(b, m)
+                L.append(f"      cb[IN1_GM ? ({gm}) : ({e3})] = hx{b}_{m};")
+        L.append("    }")
+        L.append("    const T v = reduce16_lanes(hy0, hy1, hy2, hy3, hy4, hy5, hy6, hy7, hy8, hy9, hy10, hy11, hy12, hy13, hy14, hy15);")
+        L.append("    const int jj = rev4(lane);")
+        prev = f"gy[(size_t)ed * {self.D2} + jj] + " if q > 0 else ""
+        L.append("    if (nw == 1) {")
+        L.append(f"      if (lane < 16 && jj < {self.D2}) gy[(size_t)ed * {self.D2} + jj] = {prev}v;")
+        L.append("    } else {")
+        L.append("      if (lane < 16) red[e & 1][wv][jj] = v;")
+        L.append("      __syncthreads();")
+        L.append(f"      if (wv == 0 && lane < 16 && jj < {self.D2}) {{")
+        L.append("        T acc = red[e & 1][0][jj];")
+        L.append("        for (int r = 1; r < nw; ++r) acc += red[e & 1][r][jj];")
+        L.append(f"        gy[(size_t)ed * {self.D2} + jj] = {prev}acc;")
+        L.append("      }")
+        L.append("    }")
+        self._edge_rotate(L, blocks, paths)
+        L.append("}")
+        return "\n".join(L)
+
+    def _row_addr(self, b: int, m: int) -> Tuple[str, str]:
+        """Position of (block b, component m, channel u) inside one grad-x row
+        of C*D1 values: e3nn order, or group-major order within the row (each
+        group g of count blocks is a [(2l+1), count*C] matrix at C*goff_g)."""
+        d = self.d1[b]
+        e3 = f"(size_t)C * {self.off1[b]} + (size_t)u * {d} + {m}"
+        blk, grp = self._groups(self.in1)
+        g, j = blk[b]
+        l, cnt, goff = grp[g]
+        gm = f"(size_t)C * {goff} + ((size_t){m} * {cnt} + {j}) * C + u"
+        return e3, gm
+
+    def row_segments(self):
+        """Group-major grad-x rows: per group (row offset / C, length / C) --
+        a node's group g lives at N*C*goff_g + node*len_g in the batch layout."""
+        _, grp = self._groups(self.in1)
+        return [(goff, (2 * l + 1) * cnt) for (l, cnt, goff) in grp]
 
     # ---------------------------------------------------------------- uuu ----
     @staticmethod
@@ -321,7 +411,8 @@ class Variant:
 
     def emit(self) -> str:
         if self.kind == "uvu":
-            return self.emit_uvu_fwd() + "\n\n" + self.emit_uvu_bwd()
+            nq = len(self.parts())
+            return "\n\n".join([self.emit_uvu_fwd(q) for q in range(nq)] + [self.emit_uvu_bwd(q) for q in range(nq)])
         return self.emit_uuu_fwd() + "\n\n" + self.emit_uuu_bwd()
 
 
@@ -432,41 +523,56 @@ def emit_sh(lmax_all: int = 3) -> str:
 
 
 # -------------------------------------------------------------------- main ----
+_UVU_FWD_SIG = "const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t"
+_UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, "
+                "void*, int, int, int, hipStream_t")
+_UUU_FWD_SIG = "const void*, const void*, void*, int, int, int, hipStream_t"
+_UUU_BWD_SIG = "const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t"
 _TYPEDEFS = [
-    "typedef void (*UvuFwd)(const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t);",
-    "typedef void (*UvuBwd)(const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t);",
-    "typedef void (*UuuFwd)(const void*, const void*, void*, int, int, int, hipStream_t);",
-    "typedef void (*UuuBwd)(const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t);",
+    f"typedef void (*UvuFwd)({_UVU_FWD_SIG});",
+    f"typedef void (*UvuBwd)({_UVU_BWD_SIG});",
+    f"typedef void (*UuuFwd)({_UUU_FWD_SIG});",
+    f"typedef void (*UuuBwd)({_UUU_BWD_SIG});",
 ]
+
+
+def _b(v) -> str:
+    return "true" if v else "false"
 
 
 def _launchers(v: Variant) -> List[str]:
     out = []
     for T, tag in (("float", "f"), ("double", "d")):
         if v.kind == "uvu":
+            # grid: receivers padded to a multiple of 8 (tp_node); block: one lane per channel
+            launch = "const dim3 g((unsigned)((n + 7) / 8 * 8)), b((unsigned)((C + 63) / 64 * 64));"
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
-            for f in (0, 2):
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {'true' if f else 'false'}>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
+            out.append("  " + launch)
+            for q in range(len(v.parts())):
+                for f in range(4):
+                    out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd{q}<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* g, const int* rp, const int* eid, const int* src, void* gx, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, void* cb, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
-            for f in (0, 2):
-                for gx in (True, False):
-                    out.append(f"  if (flags == {f} && {'gx' if gx else '!gx'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {'true' if gx else 'false'}, {'true' if f else 'false'}>), dim3(n), dim3(64), 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)g, rp, eid, src, ({T}*)gx, ({T}*)gy, ({T}*)gw, n, C);")
+            out.append("  " + launch)
+            for q in range(len(v.parts())):  # in order: part q > 0 adds to grad_y
+                for f in range(4):
+                    for gx in (True, False):
+                        out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd{q}<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, C);")
             out.append("}")
         else:
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, void* o, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
             for f in (0, 2, 3):  # in1 grouped implies out grouped (the product-basis chain)
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {'true' if f & 1 else 'false'}, {'true' if f & 2 else 'false'}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
             out.append("}")
             out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* go, void* g1, void* g2, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
             for f in (0, 2, 3):
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {'true' if f & 1 else 'false'}, {'true' if f & 2 else 'false'}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
             out.append("}")
     return out
 
@@ -486,26 +592,31 @@ def emit_all(gen_dir: str) -> List[str]:
         _write(path, body)
         srcs.append(path)
     reg = [hdr, "#pragma once", *_TYPEDEFS,
-           "struct TpVariant {", "  const char* key; int kind; int npath; int d1; int d2; int dout;",
-           "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d; UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;", "};"]
+           "struct TpVariant {",
+           "  const char* key; int kind; int npath; int d1; int d2; int dout;",
+           "  int nseg; int seg[8][2];        // group-major grad-x row segments (offset / C, length / C)",
+           "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
+           "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;", "};"]
     for v in vs:
         if v.kind == "uvu":
             reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
-                    (("fwd", "const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t"),
-                     ("bwd", "const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, void*, int, int, int, hipStream_t"))
-                    for t in ("f", "d")]
+                    (("fwd", _UVU_FWD_SIG), ("bwd", _UVU_BWD_SIG)) for t in ("f", "d")]
         else:
             reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
-                    (("fwd", "const void*, const void*, void*, int, int, int, hipStream_t"),
-                     ("bwd", "const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t"))
-                    for t in ("f", "d")]
+                    (("fwd", _UUU_FWD_SIG), ("bwd", _UUU_BWD_SIG)) for t in ("f", "d")]
     reg.append("static const TpVariant kVariants[] = {")
     for v in vs:
         n = v.name
+        segs = v.row_segments() if v.kind == "uvu" else []
+        assert len(segs) <= 8
+        seg = "{" + ", ".join(f"{{{a}, {b}}}" for a, b in segs + [(0, 0)] * (8 - len(segs))) + "}"
+        head = f"\"{v.key}\", {0 if v.kind == 'uvu' else 1}, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}"
         if v.kind == "uvu":
-            reg.append(f"  {{\"{v.key}\", 0, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")
+            reg.append(f"  {{{head}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
+                       f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")
         else:
-            reg.append(f"  {{\"{v.key}\", 1, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, nullptr, nullptr, nullptr, nullptr, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d}},")
+            reg.append(f"  {{{head}, 0, {seg}, nullptr, nullptr, nullptr, nullptr, "
+                       f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d}},")
     reg.append("};")
     reg.append(f"static const int kNumVariants = {len(vs)};")
     _write(os.path.join(gen_dir, "registry.inc"), reg)

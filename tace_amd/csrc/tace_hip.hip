@@ -60,19 +60,44 @@ static void launch_fill(T* p, size_t n, T v, hipStream_t s) {
 }
 
 // gx[s, :] = sum over the receiver-sorted slots k listed for sender s of
-// cbuf[k, :]; fixed summation order (sender CSR), no atomics.
-template <typename T>
+// cbuf[k, :]; fixed summation order (sender CSR), no atomics.  A cbuf row has
+// `row` values; with sg.n > 0 it is split into segments (offset, length) and
+// segment g of sender s goes to gx[n * off_g + s * len_g ...] (the
+// group-major batch layout), else the row goes to gx[s * row ...].
+// V values per thread (vector loads); row, offsets and lengths are multiples of V.
+struct RowSegs {
+  int n;
+  int64_t off[8], len[8];
+};
+
+template <typename T, int V>
 __global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, const int* __restrict__ s_rowptr,
                                                     const int* __restrict__ s_slot, T* __restrict__ gx, int n,
-                                                    int64_t row) {
+                                                    int64_t row, RowSegs sg) {
+  typedef T vec __attribute__((ext_vector_type(V)));
   const int s = blockIdx.x;
   if (s >= n) return;
   const int b = s_rowptr[s], e = s_rowptr[s + 1];
-  for (int64_t j = threadIdx.x; j < row; j += 256) {
-    T acc = T(0);
-    for (int k = b; k < e; ++k) acc += cbuf[(size_t)s_slot[k] * row + j];
-    gx[(size_t)s * row + j] = acc;
+  for (int64_t j = (int64_t)threadIdx.x * V; j < row; j += 256 * V) {
+    vec acc = (vec)(T(0));
+#pragma unroll 4
+    for (int k = b; k < e; ++k) acc += *(const vec*)(cbuf + (size_t)s_slot[k] * row + j);
+    int64_t dst = (int64_t)s * row + j;
+    for (int g = 0; g < sg.n; ++g)
+      if (j >= sg.off[g] && j < sg.off[g] + sg.len[g]) dst = (int64_t)n * sg.off[g] + (int64_t)s * sg.len[g] + (j - sg.off[g]);
+    *(vec*)(gx + dst) = acc;
   }
+}
+
+template <typename T>
+static void launch_seg_rowsum(const T* cbuf, const int* s_rowptr, const int* s_slot, T* gx, int n, int64_t row,
+                              const RowSegs& sg, int C, hipStream_t st) {
+  const int v = 16 / (int)sizeof(T);
+  if (C % v == 0)
+    hipLaunchKernelGGL((k_seg_rowsum<T, 16 / sizeof(T)>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, gx,
+                       n, row, sg);
+  else
+    hipLaunchKernelGGL((k_seg_rowsum<T, 1>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, gx, n, row, sg);
 }
 
 // ------------------------------------------------------------ edge vectors --
@@ -444,14 +469,34 @@ int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dou
   return 0;
 }
 
+static int tp_common_checks(const char* who, int vid, int64_t n_nodes, int64_t n_edges, int32_t channels,
+                            int32_t layout) {
+  char msg[160];
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) {
+    snprintf(msg, sizeof(msg), "%s: bad variant id", who);
+    return fail(msg);
+  }
+  if (layout < 0 || layout > 3) {
+    snprintf(msg, sizeof(msg), "%s: layout must be a combination of IN1_GROUPED and OUT_GROUPED", who);
+    return fail(msg);
+  }
+  if (channels <= 0 || channels > TACE_MAX_CHANNELS || n_nodes < 0 || n_edges < 0) {
+    snprintf(msg, sizeof(msg), "%s: bad sizes (channels must be in 1..%d)", who, TACE_MAX_CHANNELS);
+    return fail(msg);
+  }
+  if (n_nodes > INT32_MAX || n_edges > INT32_MAX) {
+    snprintf(msg, sizeof(msg), "%s: sizes exceed int32 indexing", who);
+    return fail(msg);
+  }
+  return 0;
+}
+
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
                      const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
                      int32_t layout, void* out, void* stream) {
-  if (layout != 0 && layout != TACE_LAYOUT_OUT_GROUPED) return fail("tace_edge_tp_fwd: layout must be 0 or OUT_GROUPED");
-  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_fwd: bad variant id");
-  if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_fwd: bad sizes");
-  if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_fwd: sizes exceed int32 indexing");
-  if ((!x && n_edges) || !out || !rowptr || (n_edges && (!y || !w || !src))) return fail("tace_edge_tp_fwd: null pointer");
+  if (tp_common_checks("tace_edge_tp_fwd", vid, n_nodes, n_edges, channels, layout)) return -1;
+  if ((!x && n_edges) || (!out && n_nodes) || !rowptr || (n_edges && (!y || !w || !src)))
+    return fail("tace_edge_tp_fwd: null pointer");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
@@ -467,29 +512,35 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
                      int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
-  if (layout != 0 && layout != TACE_LAYOUT_OUT_GROUPED) return fail("tace_edge_tp_bwd: layout must be 0 or OUT_GROUPED");
-  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_bwd: bad variant id");
-  if (channels <= 0 || n_nodes < 0 || n_edges < 0) return fail("tace_edge_tp_bwd: bad sizes");
-  if (n_nodes > INT32_MAX || n_edges > INT32_MAX) return fail("tace_edge_tp_bwd: sizes exceed int32 indexing");
-  if (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)) return fail("tace_edge_tp_bwd: null pointer");
+  if (tp_common_checks("tace_edge_tp_bwd", vid, n_nodes, n_edges, channels, layout)) return -1;
+  if (!rowptr || (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)))
+    return fail("tace_edge_tp_bwd: null pointer");
   const TpVariant& v = kVariants[vid];
   const int64_t row = (int64_t)channels * v.d1;
   if (gx) {
     if (!s_rowptr || (n_edges && (!s_slot || !workspace))) return fail("tace_edge_tp_bwd: grad_x needs sender CSR + workspace");
     if (workspace_elems < n_edges * row) return fail("tace_edge_tp_bwd: workspace smaller than n_edges * channels * d1");
   }
+  RowSegs sg;
+  memset(&sg, 0, sizeof(sg));
+  if (layout & TACE_LAYOUT_IN1_GROUPED) {
+    sg.n = v.nseg;
+    for (int g = 0; g < v.nseg; ++g) {
+      sg.off[g] = (int64_t)v.seg[g][0] * channels;
+      sg.len[g] = (int64_t)v.seg[g][1] * channels;
+    }
+  }
   hipStream_t s = (hipStream_t)stream;
-  void* cbuf = gx ? workspace : nullptr;
+  // cbuf == nullptr selects the kernels without grad_x
+  void* cbuf = gx && n_edges ? workspace : nullptr;
   if (dtype == TACE_F32) {
     v.bwd_f(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
-      hipLaunchKernelGGL(k_seg_rowsum<float>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const float*)cbuf, s_rowptr,
-                         s_slot, (float*)gx, (int)n_nodes, row);
+      launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, (float*)gx, (int)n_nodes, row, sg, channels, s);
   } else if (dtype == TACE_F64) {
     v.bwd_d(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
-      hipLaunchKernelGGL(k_seg_rowsum<double>, dim3((unsigned)n_nodes), dim3(256), 0, s, (const double*)cbuf,
-                         s_rowptr, s_slot, (double*)gx, (int)n_nodes, row);
+      launch_seg_rowsum<double>((const double*)cbuf, s_rowptr, s_slot, (double*)gx, (int)n_nodes, row, sg, channels, s);
   } else {
     return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
   }

@@ -232,7 +232,8 @@ class _EdgeTP(torch.autograd.Function):
 
 
 def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
-    """``layout`` 0: e3nn output; LAYOUT_OUT_GROUPED: group-major output."""
+    """Fused uvu tensor product + receiver scatter.  ``layout``: combination of
+    LAYOUT_IN1_GROUPED (x, grad x) and LAYOUT_OUT_GROUPED (output, grad output)."""
     return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout))
 
 

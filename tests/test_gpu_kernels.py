@@ -66,8 +66,10 @@ def test_edge_basis_matches_oracle(cuda, dtype, lmax):
 
 
 # ------------------------------------------------- edge tensor product ----
+# channel counts cover one partial wavefront (16), several wavefronts per
+# workgroup with a partial last one (96, 200) and the maximum (512)
 TP_CASES = [([0], 2, 64), ([0], 3, 128), ([0, 1, 2], 2, 64), ([0, 1, 2, 3], 3, 128), ([0, 1, 2], 3, 64),
-            ([0, 1], 1, 96)]
+            ([0, 1], 1, 96), ([0, 1, 2, 3], 3, 200), ([0, 1], 1, 16), ([0, 1, 2, 3], 3, 512)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -233,9 +235,13 @@ def test_grouped_layout_helpers_roundtrip():
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-@pytest.mark.parametrize("in1,lmax,C", [([0], 3, 128), ([0, 1, 2, 3], 3, 128), ([0, 1, 2], 2, 64)])
-def test_edge_tp_grouped_output_matches_oracle(cuda, dtype, in1, lmax, C):
-    g = torch.Generator().manual_seed(7 + C)
+@pytest.mark.parametrize("in1,lmax,C", [([0], 3, 128), ([0, 1, 2, 3], 3, 128), ([0, 1, 2], 2, 64),
+                                        ([0, 1, 2, 3], 3, 80)])
+@pytest.mark.parametrize("layout", [1, 2, 3])
+def test_edge_tp_grouped_layouts_match_oracle(cuda, dtype, in1, lmax, C, layout):
+    """Group-major x / grad_x (IN1_GROUPED) and out / grad_out (OUT_GROUPED)
+    give the e3nn-layout results."""
+    g = torch.Generator().manual_seed(7 + C + layout)
     Nn, E = 31, 200
     ei = torch.stack([torch.randint(0, Nn, (E,), generator=g), torch.randint(0, Nn, (E,), generator=g)])
     tp = om.ScatterTP(_irreps(in1, C), oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)])
@@ -249,12 +255,17 @@ def test_edge_tp_grouped_output_matches_oracle(cuda, dtype, in1, lmax, C):
     gx_o, gy_o, gw_o = torch.autograd.grad((out_o * go).sum(), [x, y, w])
     var = ops.find_variant(ops.variant_key("uvu", in1, list(range(lmax + 1)), list(range(lmax + 1))))
     plan = ops.EdgePlan.from_edge_index(ei.to(cuda), Nn)
-    xg, yg, wg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, y, w))
-    out = ops.edge_tp_scatter(xg, yg, wg, plan, var, C, ops.LAYOUT_OUT_GROUPED)
-    close(ops.from_grouped(out, out_ls, C), out_o, dtype, "out")
-    gg = ops.to_grouped(go.to(dtype).to(cuda), out_ls, C)
+    gin = bool(layout & ops.LAYOUT_IN1_GROUPED)
+    gout = bool(layout & ops.LAYOUT_OUT_GROUPED)
+    x_dev = x.detach().to(dtype).to(cuda)
+    xg = (ops.to_grouped(x_dev, in1, C) if gin else x_dev).requires_grad_(True)
+    yg, wg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (y, w))
+    out = ops.edge_tp_scatter(xg, yg, wg, plan, var, C, layout)
+    close(ops.from_grouped(out, out_ls, C) if gout else out, out_o, dtype, "out")
+    gg = go.to(dtype).to(cuda)
+    gg = ops.to_grouped(gg, out_ls, C) if gout else gg
     gx, gy, gw = torch.autograd.grad((out * gg).sum(), [xg, yg, wg])
-    close(gx, gx_o, dtype, "grad_x")
+    close(ops.from_grouped(gx, in1, C) if gin else gx, gx_o, dtype, "grad_x")
     close(gy, gy_o, dtype, "grad_y")
     close(gw, gw_o, dtype, "grad_w")
 

@@ -27,73 +27,67 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED)
-    assert lib.tace_abi_version() == 4
+    hdr = open(os.path.join(ROOT, "include", "tace_hip.h")).read()
+    assert lib.tace_abi_version() == int(re.search(r"TACE_HIP_ABI_VERSION (\d+)", hdr).group(1))
 
 
-def test_variant_registry_and_errors():
+def test_channel_limit_and_layout_checks():
+    """Channel counts beyond TACE_MAX_CHANNELS and unknown layout flags are
+    refused before any device work."""
     lib = _native.lib()
-    n = lib.tace_tp_num_variants()
-    keys = {lib.tace_tp_variant_key(i).decode() for i in range(n)}
-    assert {v.key for v in codegen.all_variants()} == keys
-    assert lib.tace_tp_find(b"uvu|9|9|9") == -1
-    assert b"no compiled" in lib.tace_last_error()
-    # argument checks fire before any device work
-    assert lib.tace_edge_tp_fwd(0, 0, None, None, None, None, None, None, 1, 1, 0, 0, None, None) < 0
-    assert lib.tace_uuu_fwd(10 ** 6, 0, None, None, 1, 1, 0, None, None) < 0
-    cell = np.zeros(9)
-    pbc = np.ones(3, dtype=np.int32)
-    assert lib.tace_nl_workspace_bytes(10, cell.ctypes.data, pbc.ctypes.data, 5.0) < 0
-    assert b"singular" in lib.tace_last_error()
+    vid = lib.tace_tp_find(b"uvu|0,1,2,3|0,1,2,3|0,1,2,3")
+    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, 4, 0, 513, 0, None, None)
+    assert rc < 0 and b"channels" in lib.tace_last_error()
+    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, 4, 0, 64, 4, None, None)
+    assert rc < 0 and b"layout" in lib.tace_last_error()
 
 
-@pytest.mark.parametrize("preset,zs,C", [("si64", [14], 64), ("fcc1024", [26, 27, 28, 29], 16),
-                                         ("water12k", [1, 8], 16)])
-def test_product_and_oracle_share_state_dict_layout(preset, zs, C):
-    cfg = configs.model_cfg(preset, zs, 30.0, num_channel=C)
-    torch.manual_seed(0)
-    o = om.TACE(cfg)
-    p = pm.TACE(**cfg)
-    so, sp = o.state_dict(), p.state_dict()
-    assert list(so) == list(sp) or set(so) == set(sp)
-    for k in so:
-        assert so[k].shape == sp[k].shape, k
-    pm.load_reference_state_dict(p, so)
-    # every tensor-product variant the model needs is compiled in
-    keys = {v.key for v in codegen.all_variants()}
-    for mod in p.modules():
-        if isinstance(mod, (pm.O3ScatterTensorProduct, pm.uuuTensorProduct)):
-            assert mod.key in keys, mod.key
+@pytest.mark.parametrize("in1,lmax", [([0], 2), ([0, 1, 2, 3], 3), ([0, 1, 2], 2)])
+def test_generated_contraction_order_matches_oracle(in1, lmax):
+    """CPU restatement of the contractions the generated edge kernels perform
+    (forward t = CG(x, y) per (in1, in2) block pair; backward
+    psi_i = sum_jk c y_j g_k, gw = x . psi, grad_x += w psi,
+    grad_y_j += sum_ik c x_i w g_k) agrees with the oracle."""
+    from oracle import so3 as oso3
 
+    v = codegen.Variant("uvu", in1, list(range(lmax + 1)), list(range(lmax + 1)))
+    g = torch.Generator().manual_seed(3)
+    Nn, E, C = 5, 14, 3
+    src = torch.randint(0, Nn, (E,), generator=g)
+    dst = torch.randint(0, Nn, (E,), generator=g)
+    irr = [(C, (l, (-1) ** l)) for l in in1]
+    tp = om.ScatterTP(irr, oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)]).double()
+    x = torch.randn(Nn, C * v.D1, generator=g, dtype=torch.float64, requires_grad=True)
+    y = torch.randn(E, v.D2, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(E, C * len(v.paths), generator=g, dtype=torch.float64, requires_grad=True)
+    out_o = tp(x, y, w, torch.stack([src, dst]))
+    go = torch.randn(out_o.shape, generator=g, dtype=torch.float64)
+    gx_o, gy_o, gw_o = torch.autograd.grad((out_o * go).sum(), [x, y, w])
 
-def test_unsupported_configuration_raises():
-    cfg = configs.model_cfg("si64", [14], 30.0, num_channel=8)
-    cfg["atomic_basis"]["type"] = "uv_so2"
-    with pytest.raises(NotImplementedError):
-        pm.TACE(**cfg)
+    X = x.detach().numpy()
+    Y, W, G = y.detach().numpy(), w.detach().numpy().reshape(E, -1, C), go.numpy()
 
+    def xi(node, b, i):  # e3nn layout: block b is [C, 2l+1]
+        return X[node, C * v.off1[b] + np.arange(C) * v.d1[b] + i]
 
-def test_product_refuses_cpu_tensors():
-    cfg = configs.model_cfg("si64", [14], 30.0, num_channel=8)
-    m = pm.create_model(cfg)
-    d = dict(positions=torch.zeros(2, 3), node_attrs=torch.ones(2, 1), edge_index=torch.zeros(2, 0, dtype=torch.long),
-             edge_shifts=torch.zeros(0, 3), lattice=torch.eye(3)[None], batch=torch.zeros(2, dtype=torch.long),
-             ptr=torch.tensor([0, 2]))
-    with pytest.raises(RuntimeError, match="GPU"):
-        m(d)
+    def oi(p, k):
+        return C * v.offo[p] + np.arange(C) * v.dout[p] + k
 
-
-def test_slot_adapters_validate_the_reference_contract():
-    from tace_amd import slot
-
-    sh = "1x0e+1x1o+1x2e+1x3o"
-    node = "128x0e+128x1o+128x2e+128x3o"
-    tp = slot.e3nnHipScatterTensorProduct(node, sh, node)
-    assert tp.weight_numel == 128 * 23
-    from tace_amd.so3 import Irreps, generate_paths
-    paths, actual = generate_paths(Irreps(node), Irreps(node), Irreps(sh), "uvu")
-    ins = [(i, j, k, "uvu", True) for i, j, k in paths]
-    slot.e3nnHipScatterTensorProduct(node, sh, actual, ins)
-    with pytest.raises(ValueError):
-        slot.e3nnHipScatterTensorProduct(node, sh, actual, ins[::-1])
-    u = slot.e3nnHipUuuTensorProduct(node, node, "1x0e+1x1o+1x2e+1x3o", identical_inputs=True)
-    assert u.C == 128
+    out = np.zeros((Nn, C * v.DO))
+    gx, gw, gy = np.zeros_like(X), np.zeros_like(W), np.zeros_like(Y)
+    for e in range(E):
+        s, n = int(src[e]), int(dst[e])
+        for p, (b1, b2) in enumerate(v.path_blocks):
+            o2 = v.off2[b2]
+            psi = {}
+            for (i, j, k, c) in v.cg[p]:
+                out[n, oi(p, k)] += W[e, p] * c * xi(s, b1, i) * Y[e, o2 + j]
+                psi[i] = psi.get(i, 0) + c * Y[e, o2 + j] * G[n, oi(p, k)]
+                gy[e, o2 + j] += (c * xi(s, b1, i) * W[e, p] * G[n, oi(p, k)]).sum()
+            for i, ps in psi.items():
+                gw[e, p] += xi(s, b1, i) * ps
+                gx[s, C * v.off1[b1] + np.arange(C) * v.d1[b1] + i] += W[e, p] * ps
+    np.testing.assert_allclose(out, out_o.detach().numpy(), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(gx, gx_o.numpy(), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(gw.reshape(E, -1), gw_o.numpy(), rtol=1e-11, atol=1e-11)
+    np.testing.assert_allclose(gy, gy_o.numpy(), rtol=1e-11, atol=1e-11)

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 5
+#define TACE_HIP_ABI_VERSION 6
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -61,17 +61,20 @@ int tace_tp_dims(int vid, int32_t* npath, int32_t* d1, int32_t* d2, int32_t* dou
  * group) -- the operand layout of the channel-mixing GEMMs that consume it. */
 #define TACE_LAYOUT_IN1_GROUPED 1
 #define TACE_LAYOUT_OUT_GROUPED 2
+#define TACE_LAYOUT_IN2_GROUPED 4 /* uuu only: x2 / g2 */
 
 /* out[n] = sum_{e: dst(e)=n} TP(x[src(e)], y[e], w[e])  -- uvu, mul2 = 1.
  * Edges are visited in receiver-CSR order: rowptr[n_nodes+1] over the sorted
  * edge list, eid[k] the edge id of sorted slot k (NULL = identity), src[e] the
  * sender of edge id e.  x [N, C*d1], y [E, d2], w [E, C*npath], out [N, C*dout];
- * 1 <= C <= TACE_MAX_CHANNELS.  layout: any
+ * 1 <= C <= TACE_MAX_CHANNELS.  node_map[N] (NULL = identity) gives the row
+ * of node n in x / out / gout / gx: the features may be stored in another node
+ * order (e.g. grouped by species) than the one the edges index.  layout: any
  * combination of TACE_LAYOUT_IN1_GROUPED (x, gx) and TACE_LAYOUT_OUT_GROUPED
  * (out, gout). */
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
-                     const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                     int32_t layout, void* out, void* stream);
+                     const int32_t* eid, const int32_t* src, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
+                     int32_t channels, int32_t layout, void* out, void* stream);
 /* Gradients of sum(gout * out): gy [E, d2], gw [E, C*npath]; gx [N, C*d1]
  * (NULL to skip).  All outputs are fully overwritten, no atomics: the
  * per-edge grad_x contributions go to `workspace` (>= E*C*d1 elements, one
@@ -79,14 +82,14 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
  * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender.
  * gy is summed over channels in a fixed order. */
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
-                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
+                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                     int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
 
 /* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
- * layout flags select the group-major layout for x1 (and g1) / out (and
- * gout); x2 / g2 always use e3nn's layout.  Accepted: 0, OUT_GROUPED,
- * IN1_GROUPED|OUT_GROUPED. */
+ * layout flags select the group-major layout for x1 (and g1), out (and
+ * gout) and x2 (and g2).  Accepted: 0, OUT_GROUPED, IN1_GROUPED|OUT_GROUPED,
+ * IN1_GROUPED|OUT_GROUPED|IN2_GROUPED. */
 int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream);
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,

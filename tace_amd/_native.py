@@ -29,9 +29,9 @@ _SIGS = {
     "tace_tp_variant_key": (_cp, [_c_int]),
     "tace_tp_find": (_c_int, [_cp]),
     "tace_tp_dims": (_c_int, [_c_int, _vp, _vp, _vp, _vp]),
-    "tace_edge_tp_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
-                                  _vp, _vp]),
-    "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
+    "tace_edge_tp_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
+                                  _c_i32, _vp, _vp]),
+    "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                   _c_i32, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp]),
     "tace_edge_vec_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_edge_vec_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),

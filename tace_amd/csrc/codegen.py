@@ -128,6 +128,7 @@ class Variant:
         L.append("  int e = beg;")
         L.append("  int ed = e < end ? (eid ? eid[e] : e) : 0;")
         L.append("  int s = e < end ? src[ed] : 0;")
+        L.append("  if (map) s = map[s];")
         for (b, m) in xs:
             L.append(f"  T x{b}_{m} = T(0);")
         L += [f"  T w{p} = T(0);" for p in paths]
@@ -141,7 +142,7 @@ class Variant:
         L.append("  for (; e < end; ++e) {")
         L.append("    const int en = e + 1 < end ? e + 1 : e;")
         L.append("    const int edn = eid ? eid[en] : en;")
-        L.append("    const int sn = src[edn];")
+        L.append("    const int sn = map ? map[src[edn]] : src[edn];")
         for (b, m) in xs:
             L.append(f"    const T xn{b}_{m} = {self._ld_x('sn', b, m)};")
         L += [f"    const T wn{p} = w[(size_t)edn * WW + (size_t){p} * C + u];" for p in paths]
@@ -166,12 +167,13 @@ class Variant:
         L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd{q}(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    T* __restrict__ out, int n_nodes, int C) {",
-             "  const int n = tp_node(n_nodes);",
+             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C) {",
+             "  const int n0 = tp_node(n_nodes);",
              "  const int u = (int)threadIdx.x;",
-             "  if (n < 0 || u >= C) return;",
+             "  if (n0 < 0 || u >= C) return;",
+             "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
              "  const size_t N = (size_t)n_nodes;",
-             "  const int beg = rowptr[n], end = rowptr[n + 1];",
+             "  const int beg = rowptr[n0], end = rowptr[n0 + 1];",
              f"  const size_t WW = (size_t)C * {P};"]
         for p in paths:
             L += [f"  T a{self.offo[p] + k} = T(0);" for k in range(self.dout[p])]
@@ -217,15 +219,17 @@ class Variant:
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const T* __restrict__ gout,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw, int n_nodes, int C) {",
+             "    const int* __restrict__ map, T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw,",
+             "    int n_nodes, int C) {",
              "  __shared__ T red[2][8][16];",
-             "  const int n = tp_node(n_nodes);",
-             "  if (n < 0) return;",
+             "  const int n0 = tp_node(n_nodes);",
+             "  if (n0 < 0) return;",
+             "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
              "  const int lane = (int)threadIdx.x & 63, wv = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;",
              "  const bool act = (int)threadIdx.x < C;",
              "  const int u = act ? (int)threadIdx.x : C - 1;",
              "  const size_t N = (size_t)n_nodes;",
-             "  const int beg = rowptr[n], end = rowptr[n + 1];",
+             "  const int beg = rowptr[n0], end = rowptr[n0 + 1];",
              f"  const size_t WW = (size_t)C * {P}, DX = (size_t)C * {self.D1};"]
         for p in paths:
             for k in range(self.dout[p]):
@@ -348,7 +352,7 @@ class Variant:
     def emit_uuu_fwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_fwd(")
+        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_fwd(")
         L.append("    const T* __restrict__ x1, const T* __restrict__ x2, T* __restrict__ out, int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
@@ -359,7 +363,7 @@ class Variant:
                 L.append(f"  const T x{bb}_{m} = {self._ld('x1', 'in1', bb, m, 'IN1_GM')};")
         for bb, d in enumerate(self.d2):
             for m in range(d):
-                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'false')};")
+                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
@@ -373,7 +377,7 @@ class Variant:
     def emit_uuu_bwd(self) -> str:
         P = len(self.paths)
         L = []
-        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
+        L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
         L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ gout,")
         L.append("    T* __restrict__ g1, T* __restrict__ g2, int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
@@ -386,7 +390,7 @@ class Variant:
                 L.append(f"  T hx{bb}_{m} = T(0);")
         for bb, d in enumerate(self.d2):
             for m in range(d):
-                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'false')};")
+                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
                 L.append(f"  T hy{bb}_{m} = T(0);")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
@@ -405,7 +409,7 @@ class Variant:
         for bb, d in enumerate(self.d2):
             for m in range(d):
                 e3, gm = self._addr("in2", bb, m)
-                L.append(f"  g2[{e3}] = hy{bb}_{m};")
+                L.append(f"  g2[IN2_GM ? ({gm}) : ({e3})] = hy{bb}_{m};")
         L.append("}")
         return "\n".join(L)
 
@@ -523,9 +527,10 @@ def emit_sh(lmax_all: int = 3) -> str:
 
 
 # -------------------------------------------------------------------- main ----
-_UVU_FWD_SIG = "const void*, const void*, const void*, const int*, const int*, const int*, void*, int, int, int, hipStream_t"
-_UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, void*, void*, "
-                "void*, int, int, int, hipStream_t")
+_UVU_FWD_SIG = ("const void*, const void*, const void*, const int*, const int*, const int*, const int*, void*, int, int, "
+                "int, hipStream_t")
+_UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, const int*, "
+                "void*, void*, void*, int, int, int, hipStream_t")
 _UUU_FWD_SIG = "const void*, const void*, void*, int, int, int, hipStream_t"
 _UUU_BWD_SIG = "const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t"
 _TYPEDEFS = [
@@ -534,6 +539,12 @@ _TYPEDEFS = [
     f"typedef void (*UuuFwd)({_UUU_FWD_SIG});",
     f"typedef void (*UuuBwd)({_UUU_BWD_SIG});",
 ]
+
+
+# uuu operand layouts compiled in (bit 1: x1 group-major, 2: out, 4: x2):
+# all-e3nn (the slot adapter), the product-basis chain with e3nn node
+# features (2, 3) and with group-major node features (7)
+UUU_LAYOUTS = (0, 2, 3, 7)
 
 
 def _b(v) -> str:
@@ -546,33 +557,33 @@ def _launchers(v: Variant) -> List[str]:
         if v.kind == "uvu":
             # grid: receivers padded to a multiple of 8 (tp_node); block: one lane per channel
             launch = "const dim3 g((unsigned)((n + 7) / 8 * 8)), b((unsigned)((C + 63) / 64 * 64));"
-            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, void* o, int n, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, const int* map, void* o, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
             for q in range(len(v.parts())):
                 for f in range(4):
-                    out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd{q}<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, ({T}*)o, n, C);")
+                    out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd{q}<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, map, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, void* cb, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, void* cb, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
             for q in range(len(v.parts())):  # in order: part q > 0 adds to grad_y
                 for f in range(4):
                     for gx in (True, False):
-                        out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd{q}<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, C);")
+                        out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd{q}<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, C);")
             out.append("}")
         else:
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, void* o, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
-            for f in (0, 2, 3):  # in1 grouped implies out grouped (the product-basis chain)
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
+            for f in UUU_LAYOUTS:
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
             out.append("}")
             out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* go, void* g1, void* g2, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
-            for f in (0, 2, 3):
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
+            for f in UUU_LAYOUTS:
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
             out.append("}")
     return out
 

@@ -72,12 +72,13 @@ struct RowSegs {
 
 template <typename T, int V>
 __global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, const int* __restrict__ s_rowptr,
-                                                    const int* __restrict__ s_slot, T* __restrict__ gx, int n,
-                                                    int64_t row, RowSegs sg) {
+                                                    const int* __restrict__ s_slot, const int* __restrict__ map,
+                                                    T* __restrict__ gx, int n, int64_t row, RowSegs sg) {
   typedef T vec __attribute__((ext_vector_type(V)));
-  const int s = blockIdx.x;
-  if (s >= n) return;
-  const int b = s_rowptr[s], e = s_rowptr[s + 1];
+  const int s0 = blockIdx.x;
+  if (s0 >= n) return;
+  const int b = s_rowptr[s0], e = s_rowptr[s0 + 1];
+  const int s = map ? map[s0] : s0;  // feature row of the sender
   for (int64_t j = (int64_t)threadIdx.x * V; j < row; j += 256 * V) {
     vec acc = (vec)(T(0));
 #pragma unroll 4
@@ -90,14 +91,15 @@ __global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, 
 }
 
 template <typename T>
-static void launch_seg_rowsum(const T* cbuf, const int* s_rowptr, const int* s_slot, T* gx, int n, int64_t row,
-                              const RowSegs& sg, int C, hipStream_t st) {
+static void launch_seg_rowsum(const T* cbuf, const int* s_rowptr, const int* s_slot, const int* map, T* gx, int n,
+                              int64_t row, const RowSegs& sg, int C, hipStream_t st) {
   const int v = 16 / (int)sizeof(T);
   if (C % v == 0)
-    hipLaunchKernelGGL((k_seg_rowsum<T, 16 / sizeof(T)>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, gx,
-                       n, row, sg);
+    hipLaunchKernelGGL((k_seg_rowsum<T, 16 / sizeof(T)>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot,
+                       map, gx, n, row, sg);
   else
-    hipLaunchKernelGGL((k_seg_rowsum<T, 1>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, gx, n, row, sg);
+    hipLaunchKernelGGL((k_seg_rowsum<T, 1>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, map, gx, n,
+                       row, sg);
 }
 
 // ------------------------------------------------------------ edge vectors --
@@ -492,24 +494,25 @@ static int tp_common_checks(const char* who, int vid, int64_t n_nodes, int64_t n
 }
 
 int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
-                     const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges, int32_t channels,
-                     int32_t layout, void* out, void* stream) {
+                     const int32_t* eid, const int32_t* src, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
+                     int32_t channels, int32_t layout, void* out, void* stream) {
   if (tp_common_checks("tace_edge_tp_fwd", vid, n_nodes, n_edges, channels, layout)) return -1;
   if ((!x && n_edges) || (!out && n_nodes) || !rowptr || (n_edges && (!y || !w || !src)))
     return fail("tace_edge_tp_fwd: null pointer");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.fwd_f(x, y, w, rowptr, eid, src, out, (int)n_nodes, layout, channels, s);
+    v.fwd_f(x, y, w, rowptr, eid, src, node_map, out, (int)n_nodes, layout, channels, s);
   else if (dtype == TACE_F64)
-    v.fwd_d(x, y, w, rowptr, eid, src, out, (int)n_nodes, layout, channels, s);
+    v.fwd_d(x, y, w, rowptr, eid, src, node_map, out, (int)n_nodes, layout, channels, s);
   else
     return fail("tace_edge_tp_fwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_edge_tp_fwd");
 }
 
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
-                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, int64_t n_nodes, int64_t n_edges,
+                     const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                     int64_t n_nodes, int64_t n_edges,
                      int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
   if (tp_common_checks("tace_edge_tp_bwd", vid, n_nodes, n_edges, channels, layout)) return -1;
@@ -534,24 +537,32 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
   // cbuf == nullptr selects the kernels without grad_x
   void* cbuf = gx && n_edges ? workspace : nullptr;
   if (dtype == TACE_F32) {
-    v.bwd_f(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
-      launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, (float*)gx, (int)n_nodes, row, sg, channels, s);
+      launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, node_map, (float*)gx, (int)n_nodes, row, sg,
+                               channels, s);
   } else if (dtype == TACE_F64) {
-    v.bwd_d(x, y, w, gout, rowptr, eid, src, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
     if (gx && n_nodes)
-      launch_seg_rowsum<double>((const double*)cbuf, s_rowptr, s_slot, (double*)gx, (int)n_nodes, row, sg, channels, s);
+      launch_seg_rowsum<double>((const double*)cbuf, s_rowptr, s_slot, node_map, (double*)gx, (int)n_nodes, row, sg,
+                                channels, s);
   } else {
     return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
   }
   return check_launch("tace_edge_tp_bwd");
 }
 
+static bool uuu_layout_ok(int32_t layout) {
+  return layout == 0 || layout == TACE_LAYOUT_OUT_GROUPED ||
+         layout == (TACE_LAYOUT_IN1_GROUPED | TACE_LAYOUT_OUT_GROUPED) ||
+         layout == (TACE_LAYOUT_IN1_GROUPED | TACE_LAYOUT_OUT_GROUPED | TACE_LAYOUT_IN2_GROUPED);
+}
+
 int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_fwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_fwd: bad sizes");
-  if (layout < 0 || layout > 3 || layout == 1) return fail("tace_uuu_fwd: layout must be 0, OUT_GROUPED or IN1|OUT_GROUPED");
+  if (!uuu_layout_ok(layout)) return fail("tace_uuu_fwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
   if (n_nodes && (!x1 || !x2 || !out)) return fail("tace_uuu_fwd: null pointer");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_fwd: too many nodes");
   const TpVariant& v = kVariants[vid];
@@ -569,7 +580,7 @@ int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void*
                  int32_t channels, int32_t layout, void* g1, void* g2, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
-  if (layout < 0 || layout > 3 || layout == 1) return fail("tace_uuu_bwd: layout must be 0, OUT_GROUPED or IN1|OUT_GROUPED");
+  if (!uuu_layout_ok(layout)) return fail("tace_uuu_bwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
   if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_bwd: too many nodes");
   const TpVariant& v = kVariants[vid];

@@ -35,14 +35,19 @@ SILU_CST = 1.6791767923989418     # e3nn normalize2mom(silu)     (tace/models/ml
 
 # ---------------------------------------------------------------- species ----
 class SpeciesPlan:
-    """Nodes grouped by species (``attrs.argmax``), for per-species GEMMs."""
+    """Node order of the model's feature tensors: nodes grouped by species
+    (``attrs.argmax``, stable), so that every per-species weight applies to
+    one contiguous row range.  ``perm[r]`` = node stored in row r,
+    ``node_map[n]`` (int32) = row of node n (what the edge kernels take)."""
 
     def __init__(self, attrs: torch.Tensor):
         self.attrs = attrs
         species = attrs.argmax(dim=-1)
         self.perm = torch.argsort(species, stable=True)
-        self.inv = torch.empty_like(self.perm)
-        self.inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
+        inv = torch.empty_like(self.perm)
+        inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
+        self.inv = inv
+        self.node_map = inv.to(torch.int32)
         counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
         self.ranges = []
         acc = 0
@@ -52,11 +57,59 @@ class SpeciesPlan:
             acc += c
 
 
+# ------------------------------------------------------------ feature layout ----
+class GMLayout:
+    """Group-major batch layout of features with (simplified) irreps: block b
+    of the whole batch is one row-major [Z, 2l+1, mul_b] matrix at element
+    offset Z * s_b (s_b = sum of mul*dim of the blocks before it).  A block's
+    rows for nodes a..b are then one contiguous [(b-a)(2l+1), mul] GEMM
+    operand, and a block of C-channel irreps is what the tensor-product
+    kernels read and write (``TACE_LAYOUT_*_GROUPED``)."""
+
+    def __init__(self, irreps):
+        self.irreps = Irreps(irreps)
+        if len(self.irreps.simplify()) != len(self.irreps):
+            raise ValueError(f"group-major layout needs simplified irreps, got {self.irreps}")
+        self.blocks, s = [], 0
+        for m, ir in self.irreps:
+            self.blocks.append((s, m, ir.dim))
+            s += m * ir.dim
+        self.dim = s
+
+    def block(self, x: torch.Tensor, b: int, a: int = 0, c: Optional[int] = None) -> torch.Tensor:
+        """Rows of nodes a..c of block b as a [(c-a)*(2l+1), mul] view."""
+        Z = x.shape[0]
+        s, m, d = self.blocks[b]
+        c = Z if c is None else c
+        return x.view(-1)[Z * s + a * d * m:Z * s + c * d * m].view((c - a) * d, m)
+
+
+def e3nn_to_gm(x: torch.Tensor, irreps) -> torch.Tensor:
+    """e3nn mul_ir layout -> group-major layout of the same irreps."""
+    lay = GMLayout(irreps)
+    Z = x.shape[0]
+    out = torch.empty_like(x)
+    col = 0
+    for b, (s, m, d) in enumerate(lay.blocks):
+        lay.block(out, b).view(Z, d, m).copy_(x[:, col:col + m * d].view(Z, m, d).transpose(1, 2))
+        col += m * d
+    return out
+
+
+def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
+    """group-major layout -> e3nn mul_ir layout."""
+    lay = GMLayout(irreps)
+    Z = x.shape[0]
+    cols = [lay.block(x, b).view(Z, d, m).transpose(1, 2).reshape(Z, m * d) for b, (s, m, d) in enumerate(lay.blocks)]
+    return torch.cat(cols, dim=1)
+
+
 # ---------------------------------------------------------------- linears ----
 class _LinearLayout:
     """e3nn ``o3.Linear`` bookkeeping: instructions (i_in, i_out) between equal
     irreps in i_in-major order, path weight (sum of mul_in into i_out)^-1/2,
-    flat weight of row-major [mul_in, mul_out] blocks (``linear.py:282-374``)."""
+    flat weight of row-major [mul_in, mul_out] blocks (``linear.py:282-374``);
+    bias on the 0e output blocks."""
 
     def __init__(self, irreps_in, irreps_out):
         self.irreps_in = Irreps(irreps_in)
@@ -71,47 +124,87 @@ class _LinearLayout:
             self.ins.append((i, o, off, mi, mo, fan[o] ** -0.5))
             off += mi * mo
         self.weight_numel = off
-        self.sl_in = [(s.start, m, ir.dim) for s, (m, ir) in zip(self.irreps_in.slices(), self.irreps_in)]
-        self.sl_out = [(s.start, m, ir.dim) for s, (m, ir) in zip(self.irreps_out.slices(), self.irreps_out)]
-        self.bias_sl, b = [], 0
-        for (s, m, d), (_, ir) in zip(self.sl_out, self.irreps_out):
+        self.bias_blocks, b = [], 0
+        for o, (m, ir) in enumerate(self.irreps_out):
             if ir.l == 0 and ir.p == 1:
-                self.bias_sl.append((s, b, m * d))
-                b += m * d
+                self.bias_blocks.append((o, b, m))
+                b += m
         self.bias_numel = b
-        self.dim_in, self.dim_out = self.irreps_in.dim, self.irreps_out.dim
+        self.gin, self.gout = GMLayout(self.irreps_in), GMLayout(self.irreps_out)
+        self.dim_in, self.dim_out = self.gin.dim, self.gout.dim
+        self.read = {i for (i, *_r) in self.ins}
+        self.written = {o for (_, o, *_r) in self.ins}
 
-    def apply(self, x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+
+class _LinearFn(torch.autograd.Function):
+    """e3nn ``o3.Linear`` on group-major features: per instruction and species
+    range one GEMM written in place into the output (``addmm_``, path weight
+    and ``alpha`` in the GEMM's scale), bias added to the 0e blocks.
+    ``weight`` [numel] (shared) or [S, numel] with ``ranges`` = [(species, a,
+    b)] over species-sorted rows.  out = alpha * (linear(x) + bias)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, lay: _LinearLayout, ranges, alpha: float):
         Z = x.shape[0]
-        outs: List[Optional[torch.Tensor]] = [None] * len(self.sl_out)
-        for i, o, off, mi, mo, pw in self.ins:
-            s, m, d = self.sl_in[i]
-            W = w[off:off + mi * mo].view(mi, mo) * pw
-            xi = x[:, s:s + m * d]
-            if d == 1:
-                y = xi @ W
-            else:
-                y = (xi.view(Z, m, d).transpose(1, 2).reshape(Z * d, m) @ W).view(Z, d, mo).transpose(1, 2)
-                y = y.reshape(Z, mo * d)
-            outs[o] = y if outs[o] is None else outs[o] + y
-        cols = [outs[o] if outs[o] is not None else x.new_zeros(Z, m * d) for o, (s, m, d) in enumerate(self.sl_out)]
-        return cols[0] if len(cols) == 1 else torch.cat(cols, dim=1)
+        out = x.new_empty(Z, lay.dim_out)
+        shared = weight.dim() == 1
+        rr = [(None, 0, Z)] if shared else ranges
+        rr = [r for r in rr if r[2] > r[1]]
+        done = set()
+        for (i, o, off, mi, mo, pw) in lay.ins:
+            for (sp, a, b) in rr:
+                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
+                lay.gout.block(out, o, a, b).addmm_(lay.gin.block(x, i, a, b), W,
+                                                    beta=1.0 if (o, sp) in done else 0.0, alpha=pw * alpha)
+                done.add((o, sp))
+        for o in range(len(lay.gout.blocks)):
+            if o not in lay.written:
+                lay.gout.block(out, o).zero_()
+        if bias is not None:
+            for (o, boff, m) in lay.bias_blocks:
+                for (sp, a, b) in rr:
+                    bv = (bias if shared else bias[sp])[boff:boff + m]
+                    lay.gout.block(out, o, a, b).add_(bv, alpha=alpha)
+        ctx.save_for_backward(x, weight, bias)
+        ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
+        return out
 
-    def bias_full(self, b: torch.Tensor) -> torch.Tensor:
-        """[..., bias_numel] -> [..., dim_out] with zeros outside the 0e slices."""
-        parts, cur = [], 0
-        for s, bs, d in self.bias_sl:
-            if s > cur:
-                parts.append(b.new_zeros(*b.shape[:-1], s - cur))
-            parts.append(b[..., bs:bs + d])
-            cur = s + d
-        if cur < self.dim_out:
-            parts.append(b.new_zeros(*b.shape[:-1], self.dim_out - cur))
-        return torch.cat(parts, dim=-1)
+    @staticmethod
+    def backward(ctx, gout):
+        x, weight, bias = ctx.saved_tensors
+        lay, rr, alpha = ctx.lay, ctx.rr, ctx.alpha
+        gout = gout.contiguous()
+        shared = weight.dim() == 1
+        gx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
+        gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
+        done = set()
+        for (i, o, off, mi, mo, pw) in lay.ins:
+            for (sp, a, b) in rr:
+                G = lay.gout.block(gout, o, a, b)
+                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
+                if gx is not None:
+                    lay.gin.block(gx, i, a, b).addmm_(G, W.t(), beta=1.0 if (i, sp) in done else 0.0,
+                                                      alpha=pw * alpha)
+                    done.add((i, sp))
+                if gw is not None:
+                    tgt = (gw if shared else gw[sp])[off:off + mi * mo].view(mi, mo)
+                    tgt.addmm_(lay.gin.block(x, i, a, b).t(), G, alpha=pw * alpha)
+        if gx is not None:
+            for i in range(len(lay.gin.blocks)):
+                if i not in lay.read:
+                    lay.gin.block(gx, i).zero_()
+        if gb is not None:
+            for (o, boff, m) in lay.bias_blocks:
+                for (sp, a, b) in rr:
+                    tgt = (gb if shared else gb[sp])[boff:boff + m]
+                    tgt += lay.gout.block(gout, o, a, b).sum(0) * alpha
+        return gx, gw, gb, None, None, None
 
 
 class e3nnLinear(torch.nn.Module):
-    """Parameters ``weight`` [numel] ~ N(0,1), ``bias`` [#0e] zeros (``linear.py:282-374``)."""
+    """Parameters ``weight`` [numel] ~ N(0,1), ``bias`` [#0e] zeros
+    (``linear.py:282-374``); group-major input and output."""
 
     def __init__(self, irreps_in, irreps_out, bias: bool = True):
         super().__init__()
@@ -120,14 +213,14 @@ class e3nnLinear(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.randn(self.lay.weight_numel))
         self.bias = torch.nn.Parameter(torch.zeros(self.lay.bias_numel)) if bias and self.lay.bias_numel else None
 
-    def forward(self, x, grouped: bool = False):
-        out = _LinearFn.apply(x, self.weight, self.lay, None, grouped)
-        return out + self.lay.bias_full(self.bias) if self.bias is not None else out
+    def forward(self, x, alpha: float = 1.0):
+        return _LinearFn.apply(x.contiguous(), self.weight, self.bias, self.lay, None, float(alpha))
 
 
 class e3nnElementLinear(torch.nn.Module):
-    """Per-species weights ``weight`` [S, numel], ``bias`` [S, #0e] (``linear.py:377-481``);
-    evaluated as one GEMM per (species, instruction) on species-contiguous rows."""
+    """Per-species weights ``weight`` [S, numel], ``bias`` [S, #0e]
+    (``linear.py:377-481``): one GEMM per (species, instruction) on the
+    species-sorted rows of group-major features."""
 
     def __init__(self, irreps_in, irreps_out, num_elements: int, bias: bool = True):
         super().__init__()
@@ -138,112 +231,8 @@ class e3nnElementLinear(torch.nn.Module):
         self.bias = (torch.nn.Parameter(torch.zeros(num_elements, self.lay.bias_numel))
                      if bias and self.lay.bias_numel else None)
 
-    def forward_sorted(self, xs: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor,
-                       grouped: bool = False) -> torch.Tensor:
-        """``xs`` rows in species-sorted order (e3nn or group-major layout);
-        returns e3nn-layout rows in the same order."""
-        out = _LinearFn.apply(xs, self.weight, self.lay, sp.ranges, grouped)
-        if self.bias is not None:
-            out = out + self.lay.bias_full(attrs_sorted @ self.bias)
-        return out
-
-    def forward(self, x: torch.Tensor, sp: SpeciesPlan) -> torch.Tensor:
-        xs = x.index_select(0, sp.perm)
-        return self.forward_sorted(xs, sp, sp.attrs.index_select(0, sp.perm)).index_select(0, sp.inv)
-
-    def forward_grouped(self, xg: torch.Tensor, sp: SpeciesPlan, attrs_sorted: torch.Tensor) -> torch.Tensor:
-        """``xg``: species-sorted nodes in the group-major layout of ``irreps_in``."""
-        return self.forward_sorted(xg, sp, attrs_sorted, grouped=True)
-
-
-def _block_rows(x: torch.Tensor, lay_sl, a: int, b: int, grouped: bool) -> torch.Tensor:
-    """Rows a..b of input block (s, m, d) as a [(b-a)*d, m] matrix (a copy only
-    for an e3nn-layout block with d > 1)."""
-    s, m, d = lay_sl
-    Z = x.shape[0]
-    if grouped:
-        return x.view(-1)[Z * s + a * d * m:Z * s + b * d * m].view((b - a) * d, m)
-    if d == 1:
-        return x[a:b, s:s + m]
-    return x[a:b, s:s + m * d].reshape(b - a, m, d).transpose(1, 2).reshape((b - a) * d, m)
-
-
-def _put_rows(dst: torch.Tensor, y: torch.Tensor, lay_sl, a: int, b: int, grouped: bool, accumulate: bool):
-    """Inverse of ``_block_rows``: write / add the [(b-a)*d, m] matrix y."""
-    s, m, d = lay_sl
-    Z = dst.shape[0]
-    if grouped:
-        v = dst.view(-1)[Z * s + a * d * m:Z * s + b * d * m].view((b - a) * d, m)
-    elif d == 1:
-        v = dst[a:b, s:s + m]
-    else:
-        v = dst[a:b, s:s + m * d].view(b - a, m, d)
-        y = y.view(b - a, d, m).transpose(1, 2)
-    v.add_(y) if accumulate else v.copy_(y)
-
-
-class _LinearFn(torch.autograd.Function):
-    """e3nn ``o3.Linear`` as GEMMs, forward and backward written straight into
-    one output / one input-gradient buffer (no per-slice zero-filled gradients).
-
-    ``weight`` is [numel] (shared) or [S, numel] applied on the row ranges
-    ``ranges`` = [(species, a, b)] of species-sorted nodes.  ``grouped``: the
-    input is in the group-major layout (``include/tace_hip.h``); the output is
-    always e3nn layout."""
-
-    @staticmethod
-    def forward(ctx, x, weight, lay: "_LinearLayout", ranges, grouped: bool):
-        Z = x.shape[0]
-        out = x.new_zeros(Z, lay.dim_out)
-        shared = weight.dim() == 1
-        rr = [(None, 0, Z)] if shared else ranges
-        for (i, o, off, mi, mo, pw) in lay.ins:
-            for (sp, a, b) in rr:
-                if b <= a:
-                    continue
-                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo) * pw
-                Y = _block_rows(x, lay.sl_in[i], a, b, grouped) @ W
-                _put_rows(out, Y, lay.sl_out[o], a, b, False, True)
-        ctx.save_for_backward(x, weight)
-        ctx.lay, ctx.ranges, ctx.grouped = lay, ranges, grouped
-        return out
-
-    @staticmethod
-    def backward(ctx, gout):
-        x, weight = ctx.saved_tensors
-        lay, grouped = ctx.lay, ctx.grouped
-        Z = x.shape[0]
-        shared = weight.dim() == 1
-        rr = [(None, 0, Z)] if shared else ctx.ranges
-        gx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
-        gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
-        readers = {}
-        for (i, o, *_r) in lay.ins:
-            readers[i] = readers.get(i, 0) + 1
-        if gx is not None:
-            for i, sl in enumerate(lay.sl_in):
-                if i not in readers:
-                    s, m, d = sl
-                    if grouped:
-                        gx.view(-1)[Z * s:Z * (s + m * d)].zero_()
-                    else:
-                        gx[:, s:s + m * d].zero_()
-        seen = set()
-        for (i, o, off, mi, mo, pw) in lay.ins:
-            for (sp, a, b) in rr:
-                if b <= a:
-                    continue
-                G = _block_rows(gout, lay.sl_out[o], a, b, False)
-                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
-                if gx is not None:
-                    _put_rows(gx, (G @ W.t()) * pw, lay.sl_in[i], a, b, grouped, (i, sp) in seen)
-                if gw is not None:
-                    X = _block_rows(x, lay.sl_in[i], a, b, grouped)
-                    tgt = gw if shared else gw[sp]
-                    tgt[off:off + mi * mo] += (X.t() @ G).reshape(-1) * pw
-            for (sp, a, b) in rr:
-                seen.add((i, sp))
-        return gx, gw, None, None, None
+    def forward(self, x: torch.Tensor, sp: SpeciesPlan, alpha: float = 1.0) -> torch.Tensor:
+        return _LinearFn.apply(x.contiguous(), self.weight, self.bias, self.lay, sp.ranges, float(alpha))
 
 
 class mlpLinear(torch.nn.Module):
@@ -255,7 +244,8 @@ class mlpLinear(torch.nn.Module):
         self.weight = torch.nn.Parameter(torch.empty(in_dim, out_dim).uniform_(-math.sqrt(3), math.sqrt(3)))
 
     def forward(self, x):
-        return x @ (self.weight * self.alpha)
+        # x @ (weight * alpha) with alpha in the GEMM's scale
+        return x.new_empty(x.shape[0], self.weight.shape[1]).addmm_(x, self.weight, beta=0.0, alpha=self.alpha)
 
 
 class MLP(torch.nn.Module):
@@ -292,8 +282,8 @@ class O3ScatterTensorProduct(torch.nn.Module):
         self.weight_numel = self.C * len(paths)
         self.key = ops.variant_key("uvu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
 
-    def forward(self, x, y, w, plan: ops.EdgePlan, layout: int = 0):
-        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C, layout)
+    def forward(self, x, y, w, plan: ops.EdgePlan, layout: int = 0, node_map=None):
+        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C, layout, node_map)
 
 
 class uuuTensorProduct(torch.nn.Module):
@@ -311,23 +301,62 @@ class uuuTensorProduct(torch.nn.Module):
         return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C, layout)
 
 
-def _gate(x: torch.Tensor, gated: Irreps) -> torch.Tensor:
-    """``O3Gate`` with gate_m0 (``tace/models/_e3nn/nonlinear.py:27-42, 93-143``):
-    x = [one C-block of gates per gated irrep | gated irreps]; the gates go
-    through normalize2mom(sigmoid) and scale their irrep (e3nn's elementwise
-    product with sqrt(2l+1) W3j(l,0,l) is exactly that scaling)."""
+class _GateFn(torch.autograd.Function):
+    """``O3Gate`` with gate_m0 (``tace/models/_e3nn/nonlinear.py:27-42, 93-143``)
+    on group-major features.  Input irreps (gates + gated).simplify(): the
+    first ng*C scalars of block 0 are the gates (one C-block per gated irrep),
+    then come the gated irreps (a gated 0e shares block 0).  Each gated block
+    [Z, 2l+1, C] is scaled by normalize2mom(sigmoid)(its gate) [Z, 1, C]
+    (e3nn's elementwise product with sqrt(2l+1) W3j(l,0,l) is exactly that)."""
+
+    @staticmethod
+    def forward(ctx, x, lin: GMLayout, lout: GMLayout, C: int):
+        Z = x.shape[0]
+        ng = len(lout.blocks)
+        X0 = lin.block(x, 0).view(Z, -1)
+        g = torch.sigmoid(X0[:, :ng * C]).mul_(SIGMOID_CST)
+        out = x.new_empty(Z, lout.dim)
+        for k, src in enumerate(_gated_blocks(x, lin, lout, C)):
+            torch.mul(src, g[:, k * C:(k + 1) * C].unsqueeze(1), out=lout.block(out, k).view(Z, -1, C))
+        ctx.save_for_backward(x, g)
+        ctx.lay = (lin, lout, C)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x, g = ctx.saved_tensors
+        lin, lout, C = ctx.lay
+        gout = gout.contiguous()
+        Z = x.shape[0]
+        ng = len(lout.blocks)
+        gx = torch.empty_like(x)
+        X0g = lin.block(gx, 0).view(Z, -1)
+        gg = x.new_empty(Z, ng * C)
+        srcs = _gated_blocks(x, lin, lout, C)
+        dsts = _gated_blocks(gx, lin, lout, C)
+        for k in range(ng):
+            go = lout.block(gout, k).view(Z, -1, C)
+            gk = g[:, k * C:(k + 1) * C]
+            torch.mul(go, gk.unsqueeze(1), out=dsts[k])
+            torch.sum(go * srcs[k], dim=1, out=gg[:, k * C:(k + 1) * C])
+        # d/dz [CST * sigmoid(z)] = g * (1 - g / CST)
+        X0g[:, :ng * C] = gg * g * (1.0 - g / SIGMOID_CST)
+        return gx, None, None, None
+
+
+def _gated_blocks(x: torch.Tensor, lin: GMLayout, lout: GMLayout, C: int) -> List[torch.Tensor]:
+    """[Z, 2l+1, C] views of the gated irreps inside the gate's input."""
     Z = x.shape[0]
-    ng = sum(m for m, _ in gated)
-    g = torch.sigmoid(x[:, :ng]) * SIGMOID_CST
-    outs, go, xo = [], 0, ng
-    for m, ir in gated:
-        d = ir.dim
-        xi = x[:, xo:xo + m * d]
-        gi = g[:, go:go + m]
-        outs.append(xi * gi if d == 1 else (xi.view(Z, m, d) * gi.unsqueeze(-1)).reshape(Z, m * d))
-        go += m
-        xo += m * d
-    return torch.cat(outs, dim=1)
+    ng = len(lout.blocks)
+    X0 = lin.block(x, 0).view(Z, -1)
+    out, b = [], 1
+    for k, (s, m, d) in enumerate(lout.blocks):
+        if k == 0 and d == 1:
+            out.append(X0[:, ng * C:ng * C + C].unsqueeze(1))
+        else:
+            out.append(lin.block(x, b).view(Z, d, C))
+            b += 1
+    return out
 
 
 class O3CgtpInteraction(torch.nn.Module):
@@ -352,18 +381,21 @@ class O3CgtpInteraction(torch.nn.Module):
         gates = Irreps([(C, Irrep("0e")) for _ in self.gated])
         self.linear_nonlinearity = e3nnLinear(self.gated, self.irreps_out, bias=True)
         self.linear_down = e3nnLinear(self.rejector.irreps_out.simplify(), (gates + self.gated).simplify(), bias=True)
+        self.C = C
+        self._gate_lay = (GMLayout(self.linear_down.irreps_out), GMLayout(self.gated))
         self.edge_info = MLP([num_radial] + list(radial_hidden) + [self.rejector.weight_numel])
         if layer > 0:
             self.resnetBB = e3nnElementLinear(self.irreps_in, irreps_sc, num_elements, bias=True)
 
     def forward(self, x, sp: SpeciesPlan, R, Y, plan: ops.EdgePlan):
+        """x: group-major node features in species-sorted row order."""
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
         w = self.edge_info(R)
-        # the scatter writes group-major [N*(2l+1), paths*C] blocks = linear_down's GEMM operands
-        m = self.linear_down(self.rejector(x, Y, w, plan, ops.LAYOUT_OUT_GROUPED), grouped=True)
-        m = m / self.avg_num_neighbors
-        m = self.linear_nonlinearity(_gate(m, self.gated))
+        m = self.rejector(x, Y, w, plan, ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED, sp.node_map)
+        # linear_down(m) / avg_num_neighbors, the division in the GEMM scale
+        m = self.linear_down(m, alpha=1.0 / self.avg_num_neighbors)
+        m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))
         return m, sc
 
 
@@ -409,24 +441,15 @@ class CgtpACE(torch.nn.Module):
         self.linear = e3nnLinear(Irreps([(C, ir) for _, ir in coefs_out]), self.irreps_out, bias=True)
 
     def forward(self, x, sp: SpeciesPlan, sc):
+        """x: group-major node features in species-sorted row order."""
         if self.agnostic:
             outs = self.coefs[0](x)
-            feats = x
-            for nu in range(2, self.correlation + 1):
-                feats = self.aces[nu - 2](feats, x)
-                outs = outs + self.coefs[nu - 1](feats)
         else:
-            # species-sorted nodes; the nu >= 2 products stay in the group-major
-            # layout that the coefficient GEMMs read without transposes
-            xs = x.index_select(0, sp.perm)
-            attrs_s = sp.attrs.index_select(0, sp.perm)
-            outs = self.coefs[0].forward_sorted(xs, sp, attrs_s)
-            feats = xs
-            for nu in range(2, self.correlation + 1):
-                lay = ops.LAYOUT_OUT_GROUPED | (ops.LAYOUT_IN1_GROUPED if nu > 2 else 0)
-                feats = self.aces[nu - 2](feats, xs, lay)
-                outs = outs + self.coefs[nu - 1].forward_grouped(feats, sp, attrs_s)
-            outs = outs.index_select(0, sp.inv)
+            outs = self.coefs[0](x, sp)
+        feats = x
+        for nu in range(2, self.correlation + 1):
+            feats = self.aces[nu - 2](feats, x, ops.LAYOUT_ALL_GROUPED)
+            outs = outs + (self.coefs[nu - 1](feats) if self.agnostic else self.coefs[nu - 1](feats, sp))
         outs = self.linear(outs)
         return outs + sc if sc is not None else outs
 
@@ -544,10 +567,10 @@ class Representation(torch.nn.Module):
                               float(rb.radial_fn.prefactor), float(rb.cutoff_fn.cutoff), int(rb.cutoff_fn.p),
                               self.lmax)
 
-    def forward(self, attrs, plan: ops.EdgePlan, edge_vector):
+    def forward(self, attrs, plan: ops.EdgePlan, edge_vector, sp: SpeciesPlan):
+        """Node features (group-major, rows in ``sp``'s species-sorted order)."""
         R, Y = self.edge_features(edge_vector)
-        sp = SpeciesPlan(attrs)
-        x = self.node_embedding(attrs)
+        x = self.node_embedding(attrs.index_select(0, sp.perm))
         for inter, prod in zip(self.interactions, self.products):
             x, sc = inter(x, sp, R, Y, plan)
             x = prod(x, sp, sc)
@@ -594,9 +617,10 @@ class TACE(torch.nn.Module):
         (``blocks.py:289-379``), fidelity 0."""
         attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
         num_graphs = ptr.numel() - 1
-        x = self.representation(attrs, plan, edge_vector)
+        sp = SpeciesPlan(attrs)
+        x = self.representation(attrs, plan, edge_vector, sp)
         e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
-        e_node = self.energy_readouts[0](x)[:, 0]
+        e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
         num_nodes = ptr[1:] - ptr[:-1]
         ei = data["edge_index"]
         num_edges = torch.zeros(num_graphs, dtype=torch.int64, device=attrs.device)

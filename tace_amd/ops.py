@@ -190,7 +190,7 @@ def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cuto
 # ------------------------------------------------------ edge tensor product ----
 class _EdgeTP(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int):
+    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int, node_map):
         Nn, E = plan.n_nodes, plan.n_edges
         dt = x.dtype
         _req(x, "x", dt, (Nn, C * var.d1))
@@ -199,11 +199,12 @@ class _EdgeTP(torch.autograd.Function):
         out = torch.empty(Nn, C * var.dout, dtype=dt, device=x.device)
         tok = _t0("edge_tp_fwd:" + var.key)
         N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
-                                         plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), Nn, E, C,
-                                         layout, out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
+                                         plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
+                                         N.ptr(node_map), Nn, E, C, layout, out.data_ptr(),
+                                         N.stream_ptr(x.device)), "tace_edge_tp_fwd")
         _t1(tok, (Nn, E, C))
         ctx.save_for_backward(x, y, w)
-        ctx.plan, ctx.var, ctx.C, ctx.layout = plan, var, C, layout
+        ctx.plan, ctx.var, ctx.C, ctx.layout, ctx.node_map = plan, var, C, layout, node_map
         return out
 
     @staticmethod
@@ -223,18 +224,24 @@ class _EdgeTP(torch.autograd.Function):
         tok = _t0("edge_tp_bwd:" + var.key)
         N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                          gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
-                                         plan.src.data_ptr(), plan.n_nodes, plan.n_edges, C, ctx.layout,
+                                         plan.src.data_ptr(), N.ptr(ctx.node_map), plan.n_nodes, plan.n_edges, C,
+                                         ctx.layout,
                                          N.ptr(s_rowptr),
                                          N.ptr(s_slot), N.ptr(ws), 0 if ws is None else ws.numel(), N.ptr(gx),
                                          gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
         _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
-        return gx, gy, gw, None, None, None, None
+        return gx, gy, gw, None, None, None, None, None
 
 
-def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
+def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0,
+                    node_map: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused uvu tensor product + receiver scatter.  ``layout``: combination of
-    LAYOUT_IN1_GROUPED (x, grad x) and LAYOUT_OUT_GROUPED (output, grad output)."""
-    return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout))
+    LAYOUT_IN1_GROUPED (x, grad x) and LAYOUT_OUT_GROUPED (output, grad output).
+    ``node_map`` (int32 [N]): row of node n in x and in the output when the
+    features are stored in another order than the edges index (None: same)."""
+    if node_map is not None:
+        _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout), node_map)
 
 
 # ------------------------------------------------------------ edge vectors ----
@@ -290,7 +297,8 @@ def edge_vectors(pos, lattice, shifts, plan: EdgePlan, dst: torch.Tensor, edge_g
 
 
 # ---------------------------------------------------------------- uuu ----
-LAYOUT_IN1_GROUPED, LAYOUT_OUT_GROUPED = 1, 2
+LAYOUT_IN1_GROUPED, LAYOUT_OUT_GROUPED, LAYOUT_IN2_GROUPED = 1, 2, 4
+LAYOUT_ALL_GROUPED = 7
 
 
 class _UUU(torch.autograd.Function):
@@ -323,8 +331,9 @@ class _UUU(torch.autograd.Function):
 
 
 def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
-    """``layout`` = 0 (e3nn operands), LAYOUT_OUT_GROUPED, or both flags: the
-    group-major layout of ``include/tace_hip.h`` for x1 / out."""
+    """``layout`` = 0 (e3nn operands), LAYOUT_OUT_GROUPED, IN1|OUT or
+    IN1|OUT|IN2 (LAYOUT_ALL_GROUPED): the group-major layout of
+    ``include/tace_hip.h`` for x1 / out / x2."""
     return _UUU.apply(x1.contiguous(), x2.contiguous(), var, C, int(layout))
 
 

@@ -193,15 +193,15 @@ def test_neighbour_list_bit_exact_edge_set(cuda, name, s, rc):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-@pytest.mark.parametrize("layout", [2, 3])
+@pytest.mark.parametrize("layout", [2, 3, 7])
 @pytest.mark.parametrize("L", [2, 3])
 def test_uuu_grouped_layouts_match_oracle(cuda, dtype, layout, L):
-    """The group-major operand layouts (x1 and/or out) give the e3nn-layout results."""
+    """The group-major operand layouts (x1, out, x2) give the e3nn-layout results."""
     C = 64
     full = list(range(L + 1))
     nu2 = om.UUUTP(_irreps(full, 1), _irreps(full, 1), [(1, (l, (-1) ** l)) for l in full], True)
     nu2_ls = [ir[0] for _, ir in nu2.out]
-    in1 = nu2_ls if layout == 3 else full
+    in1 = nu2_ls if layout & ops.LAYOUT_IN1_GROUPED else full
     tp = om.UUUTP(_irreps(in1, C), _irreps(full, C), [(1, (l, (-1) ** l)) for l in full], in1 == full)
     out_ls = [ir[0] for _, ir in tp.out]
     g = torch.Generator().manual_seed(L * 10 + layout)
@@ -217,13 +217,18 @@ def test_uuu_grouped_layouts_match_oracle(cuda, dtype, layout, L):
     if layout & ops.LAYOUT_IN1_GROUPED:
         a = ops.to_grouped(a, in1, C)
     a.requires_grad_(True)
-    b = x2.detach().to(dtype).to(cuda).requires_grad_(True)
+    b = x2.detach().to(dtype).to(cuda)
+    if layout & ops.LAYOUT_IN2_GROUPED:
+        b = ops.to_grouped(b, full, C)
+    b.requires_grad_(True)
     out = ops.uuu_tp(a, b, var, C, layout)
     close(ops.from_grouped(out, out_ls, C), o, dtype, "out")
     gg = ops.to_grouped(go.to(dtype).to(cuda), out_ls, C)
     g1, g2 = torch.autograd.grad((out * gg).sum(), [a, b])
     if layout & ops.LAYOUT_IN1_GROUPED:
         g1 = ops.from_grouped(g1, in1, C)
+    if layout & ops.LAYOUT_IN2_GROUPED:
+        g2 = ops.from_grouped(g2, full, C)
     close(g1, g1o, dtype, "g1")
     close(g2, g2o, dtype, "g2")
 
@@ -317,3 +322,48 @@ def test_slot_adapter_matches_oracle_with_unsorted_edges(cuda):
     y = torch.randn(E, (lmax + 1) ** 2, generator=g, dtype=torch.float64)
     w = torch.randn(E, tp_o.weight_numel, generator=g, dtype=torch.float64)
     close(tp_h(x.to(cuda), y.to(cuda), w.to(cuda), ei.to(cuda)), tp_o(x, y, w, ei), torch.float64, "slot out")
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("layout", [0, 3])
+def test_edge_tp_node_map_matches_identity_order(cuda, dtype, layout):
+    """Features stored in a permuted row order (node_map[n] = row of node n)
+    give the same per-node results and gradients as the identity order."""
+    g = torch.Generator().manual_seed(11 + layout)
+    Nn, E, C, in1, lmax = 41, 500, 96, [0, 1, 2, 3], 3
+    ei = torch.stack([torch.randint(0, Nn, (E,), generator=g), torch.randint(0, Nn, (E,), generator=g)]).to(cuda)
+    var = ops.find_variant(ops.variant_key("uvu", in1, list(range(lmax + 1)), list(range(lmax + 1))))
+    plan = ops.EdgePlan.from_edge_index(ei, Nn)
+    x = torch.randn(Nn, C * var.d1, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    y = torch.randn(E, var.d2, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    w = torch.randn(E, C * var.npath, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    go = torch.randn(Nn, C * var.dout, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    perm = torch.randperm(Nn, generator=g).to(cuda)          # row r holds node perm[r]
+    node_map = torch.empty_like(perm)
+    node_map[perm] = torch.arange(Nn, device=cuda)
+    node_map = node_map.to(torch.int32)
+
+    xa, ya, wa = (t.clone().requires_grad_(True) for t in (x, y, w))
+    out_a = ops.edge_tp_scatter(xa, ya, wa, plan, var, C, 0)
+    gxa, gya, gwa = torch.autograd.grad((out_a * go).sum(), [xa, ya, wa])
+
+    out_ls = var_out_ls(var, in1, lmax)
+    xs = x.index_select(0, perm)
+    gos = go.index_select(0, perm)
+    if layout:
+        xs, gos = ops.to_grouped(xs, in1, C), ops.to_grouped(gos, out_ls, C)
+    xb, yb, wb = (t.clone().requires_grad_(True) for t in (xs, y, w))
+    out_b = ops.edge_tp_scatter(xb, yb, wb, plan, var, C, layout, node_map)
+    gxb, gyb, gwb = torch.autograd.grad((out_b * gos).sum(), [xb, yb, wb])
+    if layout:
+        out_b, gxb = ops.from_grouped(out_b, out_ls, C), ops.from_grouped(gxb, in1, C)
+    inv = node_map.long()
+    close(out_b.index_select(0, inv), out_a, dtype, "out")
+    close(gxb.index_select(0, inv), gxa, dtype, "grad_x")
+    close(gyb, gya, dtype, "grad_y")
+    close(gwb, gwa, dtype, "grad_w")
+
+
+def var_out_ls(var, in1, lmax):
+    tp = om.ScatterTP(_irreps(in1, 1), oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)])
+    return [ir[0] for _, ir in tp.out]

@@ -36,9 +36,9 @@ def test_channel_limit_and_layout_checks():
     refused before any device work."""
     lib = _native.lib()
     vid = lib.tace_tp_find(b"uvu|0,1,2,3|0,1,2,3|0,1,2,3")
-    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, 4, 0, 513, 0, None, None)
+    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, None, 4, 0, 513, 0, None, None)
     assert rc < 0 and b"channels" in lib.tace_last_error()
-    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, 4, 0, 64, 4, None, None)
+    rc = lib.tace_edge_tp_fwd(vid, 0, None, None, None, None, None, None, None, 4, 0, 64, 4, None, None)
     assert rc < 0 and b"layout" in lib.tace_last_error()
 
 

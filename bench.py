@@ -66,8 +66,23 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     return float("nan")
 
 
-def cpu_baseline(preset_cfg_fn, n_side=4, reps=2):
-    """CPU oracle on a 64-molecule slice of the same water model (float32)."""
+def measured_traffic(entry: str):
+    """HBM bytes per call of ``entry`` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary committed under profiles/ (None when not measured)."""
+    path = os.path.join(ROOT, "profiles", "water12k_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        line = line.strip()
+        if line.startswith("traffic ") and "=" in line:
+            name, val = line[len("traffic "):].rsplit("=", 1)
+            if name.strip() == entry:
+                return float(val)
+    return None
+
+
+def cpu_baseline(preset_cfg_fn, n_side=5, reps=3):
+    """CPU oracle on a 125-molecule slice of the same water model (float32)."""
     from oracle import model as om
     from oracle import neighbours as onl
     from tace_amd import data, structures
@@ -104,7 +119,17 @@ def main():
     ap.add_argument("--n-side", type=int, default=16, help="water molecules per box edge (16 -> 12,288 atoms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="print the per-kernel breakdown to stderr")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a device copy of 1 GiB five times (reference for the HBM byte counters)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        a = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("[bench] copied 1 GiB x5")
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not part of it "
               "(see DESIGN.md for how the path would shard).", file=sys.stderr)
@@ -163,8 +188,10 @@ def main():
     var = ops.find_variant(key) if key else None
     byts = sum(algorithmic_bytes(name, i, var, 4) for i in infos)
     achieved = byts / (tot_ms * 1e-3) / 1e9
+    traffic = measured_traffic(name)
     roof = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=None,
+                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
+                algorithmic_bytes=round(byts / cnt),
                 avg_launch_us=round(tot_ms / cnt * 1e3, 1), share_of_step=round(tot_ms / (dt * 1e3), 3))
     if args.kernels:
         for k, (c, t, _) in sorted(summ.items(), key=lambda kv: -kv[1][1]):

@@ -243,10 +243,12 @@ class UUUTP(torch.nn.Module):
                                                   "uuu", identical_inputs)
         self.irreps_out = self.out
 
-    def forward(self, x1, x2):
+    def forward(self, x1, x2, ws=None):
+        """``ws`` [Z, paths * mul]: per-node weights of the trainable (bilinear
+        gate) form, one per path and channel (e3nn uuu, shared_weights=False)."""
         s1, s2 = _offsets(self.in1), _offsets(self.in2)
         outs = []
-        for i, j, k in self.paths:
+        for p, (i, j, k) in enumerate(self.paths):
             m1, (l1, _) = self.in1[i]
             m2, (l2, _) = self.in2[j]
             assert m1 == m2
@@ -255,7 +257,10 @@ class UUUTP(torch.nn.Module):
             b = x2[:, s2[j]:s2[j] + m2 * (2 * l2 + 1)].reshape(-1, m2, 2 * l2 + 1)
             C = so3.w3j_torch(l1, l2, l3, x1.dtype) * math.sqrt(2 * l3 + 1)
             ab = (a.unsqueeze(-1) * b.unsqueeze(-2)).reshape(-1, (2 * l1 + 1) * (2 * l2 + 1))
-            outs.append((ab @ C.reshape(-1, 2 * l3 + 1)).reshape(x1.shape[0], -1))
+            t = (ab @ C.reshape(-1, 2 * l3 + 1)).reshape(x1.shape[0], m1, 2 * l3 + 1)
+            if ws is not None:
+                t = t * ws[:, p * m1:(p + 1) * m1].unsqueeze(-1)
+            outs.append(t.reshape(x1.shape[0], -1))
         return torch.cat(outs, dim=-1)
 
 
@@ -358,16 +363,60 @@ class Interaction(torch.nn.Module):
         return m, sc
 
 
+class SO2Interaction(torch.nn.Module):
+    """``OAM20260705Interaction`` (``tace/models/_e3nn/inter.py:440-519``): the
+    cgtp interaction's linears and gate around the TECE convolution, with no
+    scatter normalisation (``_prepare_setup`` sets scatter_norm None)."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, mmax, num_elements, radial_hidden,
+                 num_radial, num_head, edge_ace_hidden):
+        super().__init__()
+        from . import tece
+        self.layer, self.lmax, self.C = layer, lmax, C
+        sh = so3.sh_irreps(lmax)
+        tp_out = so3.possible_tp_irreps(irreps_in, sh, False, lmax)
+        self.irreps_out = so3.regroup(so3.times(tp_out, C))
+        if [ir[0] for _, ir in self.irreps_out] != list(range(lmax + 1)):
+            raise NotImplementedError("TECE layer output must be one C block per l = 0..lmax")
+        if layer == num_layers - 1:
+            irreps_sc = so3.regroup(so3.times([(1, (0, 1))], C))
+        else:
+            irreps_sc = so3.regroup(so3.times(so3.possible_tp_irreps(irreps_in, sh, False, Lmax), C))
+        self.linear_up = Linear(irreps_in, irreps_in, bias=True)
+        self.rejector = tece.TeceConvolution(mmax, lmax, C, num_head, edge_ace_hidden, num_radial)
+        gated = [(C, ir) for _, ir in self.irreps_out]
+        gates = [(C, (0, 1)) for _ in gated]
+        self.nonlinearity = Gate(gated)
+        self.linear_nonlinearity = Linear(gated, self.irreps_out, bias=True)
+        self.linear_down = Linear([(C, ir) for _, ir in self.irreps_out], so3.simplify(gates + gated), bias=True)
+        self.edge_info = MLP([num_radial] + list(radial_hidden) + [self.rejector.weight_numel])
+        if layer > 0:
+            self.resnetBB = ElementLinear(irreps_in, irreps_sc, num_elements, bias=True)
+
+    def forward(self, x, attrs, edge_feats, edge_attrs, edge_index, wigner=None, wigner_inv=None):
+        from . import tece
+        sc = self.resnetBB(x, attrs) if hasattr(self, "resnetBB") else None
+        x = self.linear_up(x)
+        w = self.edge_info(edge_feats)
+        msg = self.rejector(tece.e3nn_to_lc(x, self.lmax, self.C), w, edge_index, wigner, wigner_inv, edge_feats)
+        m = self.linear_down(tece.lc_to_e3nn(msg, self.lmax))
+        m = self.linear_nonlinearity(self.nonlinearity(m))
+        return m, sc
+
+
 class Product(torch.nn.Module):
     """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``), element-aware coefs,
     one expert, no bilinear gate."""
 
     def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements,
-                 agnostic: bool = False):
+                 agnostic: bool = False, bilinear: bool = False):
         super().__init__()
         last = layer == num_layers - 1
         self.agnostic = agnostic
         self.correlation = correlation
+        self.bilinear = bilinear
+        if bilinear and correlation != 2:
+            raise ValueError("the bilinear-gate product basis needs correlation 2 (prod.py:83-84)")
         hidden = [(C, ir) for _, ir in irreps_in]
         tp_out_list = []
         for nu in range(2, correlation + 1):
@@ -391,20 +440,49 @@ class Product(torch.nn.Module):
 
         self.coefs = torch.nn.ModuleList([mk(so3.simplify([(C, ir) for _, ir in hidden]))])
         self.aces = torch.nn.ModuleList()
+        # bilinear gate (prod.py:83-87, 126-147): the second operand is the
+        # hidden irreps plus a C x 0e block of ones, and the products are
+        # weighted per node by silu of gate scalars from linear_up
+        base = hidden + [(C, (0, 1))] if bilinear else hidden
         in1 = hidden
         for nu in range(2, correlation + 1):
-            ace = UUUTP(in1, hidden, tp_out_list[nu - 2], identical_inputs=(nu == 2))
+            ace = UUUTP(in1, base, tp_out_list[nu - 2], identical_inputs=(nu == 2 and not bilinear))
             self.aces.append(ace)
             self.coefs.append(mk(so3.simplify([(C, ir) for _, ir in ace.irreps_out])))
             in1 = ace.irreps_out
+        if bilinear:
+            self.num_gate = sum(len(a.paths) * C for a in self.aces)
+            self.double = [(2 * C, ir) for _, ir in hidden]
+            self.linear_up = Linear(irreps_in, [(self.num_gate, (0, 1))] + self.double, bias=True)
         self.linear = Linear([(C, ir) for _, ir in coefs_out], self.irreps_out, bias=True)
+        self.C = C
+
+    def _split_up(self, x):
+        """linear_up output -> (node features, base features + ones, gate weights)."""
+        x = self.linear_up(x)
+        Z, C = x.shape[0], self.C
+        ws = torch.nn.functional.silu(x[:, :self.num_gate])
+        node, base, off = [], [], self.num_gate
+        for m, (l, _) in self.double:
+            d = 2 * l + 1
+            f = x[:, off:off + m * d].reshape(Z, m, d)
+            off += m * d
+            node.append(f[:, :C].reshape(Z, -1))
+            base.append(f[:, C:].reshape(Z, -1))
+        base.append(x.new_ones(Z, C))
+        return torch.cat(node, -1), torch.cat(base, -1), ws
 
     def forward(self, x, attrs, sc):
         kw = (lambda f, t: f(t)) if self.agnostic else (lambda f, t: f(t, attrs))
+        if self.bilinear:
+            x, base, ws = self._split_up(x)
         outs = kw(self.coefs[0], x)
         feats = x
         for nu in range(2, self.correlation + 1):
-            feats = self.aces[nu - 2](feats, x)
+            if self.bilinear:
+                feats = self.aces[nu - 2](feats, base, ws)
+            else:
+                feats = self.aces[nu - 2](feats, x)
             outs = outs + kw(self.coefs[nu - 1], feats)
         outs = self.linear(outs)
         return outs + sc if sc is not None else outs
@@ -451,22 +529,41 @@ class Representation(torch.nn.Module):
         corr = corr if isinstance(corr, list) else [corr] * nl
         self.interactions = torch.nn.ModuleList()
         self.products = torch.nn.ModuleList()
+        ab = cfg.get("atomic_basis", {})
+        types = ab.get("type", "cgtp")
+        types = types if isinstance(types, list) else [types] * nl
+        self.use_so2 = "uv_so2" in types
+        self.mmax = cfg.get("mmax", L)
+        pb = cfg["product_basis"]
+        bilinear = pb.get("nonlinear") == "silu_bilineargate"
         irreps = [(C, (0, 1))]
         for layer in range(nl):
-            inter = Interaction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
-                                rb["hidden"], rb["num_radial_basis"])
+            if types[layer] == "uv_so2":
+                inter = SO2Interaction(layer, nl, irreps, C, Lmax, L, self.mmax, S, rb["hidden"],
+                                       rb["num_radial_basis"], ab.get("num_head") or 1,
+                                       ab.get("edge_ace_hidden") or C)
+            else:
+                inter = Interaction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
+                                    rb["hidden"], rb["num_radial_basis"])
             self.interactions.append(inter)
-            prod = Product(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S,
-                           cfg["product_basis"].get("agnostic", False))
+            prod = Product(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S, pb.get("agnostic", False),
+                           bilinear)
             self.products.append(prod)
             irreps = prod.irreps_out
 
     def forward(self, attrs, edge_index, edge_vector, edge_length):
         R = self.radial_basis(edge_length)
         Y = so3.spherical_harmonics(self.lmax, edge_vector / edge_length)
+        wig = wig_inv = None
+        if self.use_so2:
+            from . import tece
+            wig, wig_inv = tece.edge_wigner(edge_vector, self.lmax, self.mmax)
         x = self.node_embedding(attrs)
         for inter, prod in zip(self.interactions, self.products):
-            x, sc = inter(x, attrs, R, Y, edge_index)
+            if isinstance(inter, SO2Interaction):
+                x, sc = inter(x, attrs, R, Y, edge_index, wig, wig_inv)
+            else:
+                x, sc = inter(x, attrs, R, Y, edge_index)
             x = prod(x, attrs, sc)
         return x
 

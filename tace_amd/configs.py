@@ -17,6 +17,12 @@ PRESETS = {
     "fcc1024": dict(num_channel=128, L=3, num_layers=2, cutoff=5.0, target=["energy", "forces"]),
     "water12k": dict(num_channel=128, L=3, num_layers=3, cutoff=6.0, target=["energy", "forces"]),
     "ragged128": dict(num_channel=256, L=3, num_layers=2, cutoff=6.0, target=["energy", "forces", "stress"]),
+    # config 5: TECE edge cluster expansion with radial rotary attention; layer 0
+    # cgtp (uv_so2 needs l > 0 inputs, inter.py:458-461), bilinear-gate product
+    # basis (correlation 2, prod.py:83-84), agnostic coefficients
+    "tece": dict(num_channel=128, L=2, mmax=2, num_layers=2, cutoff=5.0, target=["energy", "forces"],
+                 atomic_basis_type=["cgtp", "uv_so2"], num_head=4, edge_ace_hidden=32, correlation=2,
+                 product_nonlinear="silu_bilineargate", agnostic=True),
 }
 
 
@@ -48,13 +54,15 @@ def model_cfg(preset: str, atomic_numbers: Sequence[int], avg_num_neighbors: flo
                           polynomial_cutoff=5, order=0, trainable=False, apply_cutoff=True,
                           hidden=[64, 64, 64], gaussian_width=2.0, use_dydynamic_cutoff=False,
                           dydynamic_cutoff_mu=40),
-        atomic_basis=dict(type="cgtp", l1l2=None, scatter_norm="avg_num_neighbors",
-                          nonlinear="sigmoid_gate", gate_m0=True, num_head=None,
-                          edge_ace_hidden=None, scalar_act=None, tensor_act=None),
+        atomic_basis=dict(type=p.get("atomic_basis_type", "cgtp"), l1l2=None, scatter_norm="avg_num_neighbors",
+                          nonlinear="sigmoid_gate", edge_nonlinear="so2_sigmoid_gate", gate_m0=True,
+                          num_head=p.get("num_head"), edge_ace_hidden=p.get("edge_ace_hidden"),
+                          scalar_act=None, tensor_act=None),
         resnet=dict(type="BB", linear_type="aware", use_first_resnet=False),
         product_basis=dict(type="cgtp", l1l2=None, correlation=p.get("correlation", 3),
                            num_expert=None, num_channel_per_expert=None, use_shared_expert=False,
-                           nonlinear=None, agnostic=False, return_components=None),
+                           nonlinear=p.get("product_nonlinear"), agnostic=p.get("agnostic", False),
+                           return_components=None),
         readout_emlp=dict(bias=False, hidden=[16], use_alllayer=False, use_uie=False,
                           use_one_body_magmoms=True),
         scale_shift=dict(enable=True, scale_type="rms_forces", shift_type=None,

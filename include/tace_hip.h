@@ -27,6 +27,8 @@
  *   tace_edge_vec_fwd/_bwd    edge vectors of TensorModel.prepare_graph
  *                             (models/adapter.py:334-340) and their position gradient
  *   tace_nl_*                 get_neighborhood (dataset/neighbour_list.py:195-298)
+ *   tace_edge_wigner_*, tace_tece_*, tace_graph_softmax_*
+ *                             TECE convolution pieces, see their section below
  */
 #ifndef TACE_HIP_H
 #define TACE_HIP_H
@@ -37,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 6
+#define TACE_HIP_ABI_VERSION 7
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -77,23 +79,29 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
                      int32_t channels, int32_t layout, void* out, void* stream);
 /* Gradients of sum(gout * out): gy [E, d2], gw [E, C*npath]; gx [N, C*d1]
  * (NULL to skip).  All outputs are fully overwritten, no atomics: the
- * per-edge grad_x contributions go to `workspace` (>= E*C*d1 elements, one
- * row per receiver-sorted slot) and are summed per sender through the sender
- * CSR: s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender.
- * gy is summed over channels in a fixed order. */
+ * per-edge grad_x contributions go to `workspace` (one row per
+ * receiver-sorted slot) and are summed per sender through the sender CSR:
+ * s_rowptr[N+1], s_slot[E] = receiver-sorted slots grouped by sender.  gy is
+ * summed over channels and kernel parts in a fixed order.  `workspace` holds
+ * at least tace_edge_tp_workspace_elems(vid, E, C, gx != NULL) elements. */
+int64_t tace_edge_tp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx);
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
 
 /* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
+ * w [N, npath*C] (NULL = unweighted) scales path p of channel u by
+ * w[n, p*C + u] -- the trainable (bilinear-gate) product of
+ * _e3nn/prod.py:126-147 / fused.py:17-95; the backward then also writes
+ * gw [N, npath*C].
  * layout flags select the group-major layout for x1 (and g1), out (and
  * gout) and x2 (and g2).  Accepted: 0, OUT_GROUPED, IN1_GROUPED|OUT_GROUPED,
  * IN1_GROUPED|OUT_GROUPED|IN2_GROUPED. */
-int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void* w, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream);
-int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
-                 int32_t channels, int32_t layout, void* g1, void* g2, void* stream);
+int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* stream);
 
 /* ---- edge featurisation --------------------------------------------------
  * vec [E, 3] edge vectors; r = |vec| + 1e-9;
@@ -116,6 +124,51 @@ int tace_edge_vec_fwd(int dtype, const void* pos, const void* lattice, const int
                       const void* shifts, const int32_t* edge_graph, int64_t n_edges, void* vec, void* stream);
 int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const int32_t* eid,
                       const int32_t* s_rowptr, const int32_t* s_slot, int64_t n_nodes, void* g_pos, void* stream);
+
+/* ---- TECE radial-rotary edge attention (config 5)
+ * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"
+ * orders them m = 0 (l = 0..lmax), then per m = 1..lmax the +m rows and the
+ * -m rows (tace/models/o2/wigner.py:38-66).
+ *   tace_edge_wigner_fwd/_bwd   WignerD.get_wigner (o2/wigner.py:231-239) with
+ *                               init_edge_rot_mat_quaternion (o2/rotation_matrix.py:74-88):
+ *                               wigner [E, K, K] (row = m-layout component,
+ *                               column = e3nn component); its inverse is the
+ *                               transpose.  bwd: g_vec [E, 3] from g_wigner.
+ *   tace_tece_score_fwd/_bwd    OAM20260705Convolution._complex_qk_attention
+ *                               (_e3nn/archive/oam_2026_07_05.py:699-754): q, k
+ *                               [E, K, C] in the m layout with the default
+ *                               (lmax+1-m) components per m, radial_proj [E, 2H]
+ *                               (bias | phase logits), tscale[H] = attention
+ *                               scale x temperature -> score [E, H].
+ *   tace_graph_softmax_fwd/_bwd GraphSoftmax (softmax.py:80-114) over each
+ *                               receiver's in-edges (receiver CSR rowptr/eid),
+ *                               no rescale: alpha [E, H].
+ *   tace_tece_rotate_out_fwd/_bwd
+ *                               alpha-weighted wigner_inv product and
+ *                               scatter_sum to receivers
+ *                               (oam_2026_07_05.py:799-823): m [E, K, C] ->
+ *                               out in the group-major layout of C x (0..lmax)
+ *                               at rows node_map[n]; bwd gives g_m and g_alpha
+ *                               (the wigner gradient is g_m-independent:
+ *                               sum_c alpha m g_out, formed by the caller). */
+int tace_edge_wigner_fwd(int dtype, const void* vec, int64_t n_edges, int32_t lmax, void* wigner, void* stream);
+int tace_edge_wigner_bwd(int dtype, const void* vec, const void* g_wigner, int64_t n_edges, int32_t lmax,
+                         void* g_vec, void* stream);
+int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
+                        int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, void* score, void* stream);
+int tace_tece_score_bwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
+                        const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
+                        void* g_q, void* g_k, void* g_radial_proj, void* stream);
+int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, const int32_t* eid, int64_t n_nodes,
+                           int32_t heads, void* alpha, void* stream);
+int tace_graph_softmax_bwd(int dtype, const void* alpha, const void* g_alpha, const int32_t* rowptr,
+                           const int32_t* eid, int64_t n_nodes, int32_t heads, void* g_score, void* stream);
+int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const void* wigner, const int32_t* rowptr,
+                             const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int32_t lmax,
+                             int32_t channels, int32_t heads, void* out, void* stream);
+int tace_tece_rotate_out_bwd(int dtype, const void* m, const void* alpha, const void* wigner, const void* g_out,
+                             const int32_t* rowptr, const int32_t* eid, const int32_t* node_map, int64_t n_nodes,
+                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha, void* stream);
 
 /* ---- neighbour list (float64 positions, host cell[9] rows = lattice
  * vectors, host pbc[3]).  Edge (src=i, dst=j, S) exists iff

@@ -29,17 +29,29 @@ _SIGS = {
     "tace_tp_variant_key": (_cp, [_c_int]),
     "tace_tp_find": (_c_int, [_cp]),
     "tace_tp_dims": (_c_int, [_c_int, _vp, _vp, _vp, _vp]),
+    "tace_edge_tp_workspace_elems": (_c_i64, [_c_int, _c_i64, _c_i32, _c_i32]),
     "tace_edge_tp_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                   _c_i32, _vp, _vp]),
     "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                   _c_i32, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp]),
     "tace_edge_vec_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_edge_vec_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
-    "tace_uuu_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp]),
-    "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
+    "tace_uuu_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp]),
+    "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp]),
     "tace_edge_basis_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_edge_basis_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32,
                                      _vp, _vp]),
+    "tace_edge_wigner_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _vp]),
+    "tace_edge_wigner_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
+    "tace_tece_score_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp, _vp]),
+    "tace_tece_score_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32, _vp, _vp,
+                                     _vp, _vp]),
+    "tace_graph_softmax_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
+    "tace_graph_softmax_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
+    "tace_tece_rotate_out_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
+                                          _vp, _vp]),
+    "tace_tece_rotate_out_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,
+                                          _c_i32, _vp, _vp, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

@@ -164,13 +164,12 @@ class Variant:
         P = len(self.paths)
         blocks = self.parts()[q]
         paths = self._part_paths(blocks)
-        L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd{q}(",
+        L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__device__ __forceinline__ void f_{self.name}_fwd{q}(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C) {",
-             "  const int n0 = tp_node(n_nodes);",
+             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C, int n0) {",
              "  const int u = (int)threadIdx.x;",
-             "  if (n0 < 0 || u >= C) return;",
+             "  if (u >= C) return;",
              "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
              "  const size_t N = (size_t)n_nodes;",
              "  const int beg = rowptr[n0], end = rowptr[n0 + 1];",
@@ -209,21 +208,18 @@ class Variant:
           hy_j   += sum_{i,k} c^p_ijk x_i (w_p g_pk)     -> summed over channels
         grad_y is reduced over the 64 lanes of each wavefront (transposing
         butterfly, 17 shuffles for 16 values) and over the workgroup's
-        wavefronts through LDS in a fixed order, then added to what earlier
-        parts wrote: deterministic, no atomics."""
+        wavefronts through LDS in a fixed order into this part's partial
+        (``gy`` points at it): deterministic, no atomics."""
         P = len(self.paths)
         blocks = self.parts()[q]
         paths = self._part_paths(blocks)
         assert self.D2 <= 16
-        L = [f"template <typename T, bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_bwd{q}(",
+        L = [f"template <typename T, bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__device__ __forceinline__ void f_{self.name}_bwd{q}(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const T* __restrict__ gout,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
              "    const int* __restrict__ map, T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw,",
-             "    int n_nodes, int C) {",
-             "  __shared__ T red[2][8][16];",
-             "  const int n0 = tp_node(n_nodes);",
-             "  if (n0 < 0) return;",
+             "    int n_nodes, int C, int n0, T (*red)[8][16]) {",
              "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
              "  const int lane = (int)threadIdx.x & 63, wv = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;",
              "  const bool act = (int)threadIdx.x < C;",
@@ -276,7 +272,7 @@ class Variant:
         L.append("    }")
         L.append("    const T v = reduce16_lanes(hy0, hy1, hy2, hy3, hy4, hy5, hy6, hy7, hy8, hy9, hy10, hy11, hy12, hy13, hy14, hy15);")
         L.append("    const int jj = rev4(lane);")
-        prev = f"gy[(size_t)ed * {self.D2} + jj] + " if q > 0 else ""
+        prev = ""
         L.append("    if (nw == 1) {")
         L.append(f"      if (lane < 16 && jj < {self.D2}) gy[(size_t)ed * {self.D2} + jj] = {prev}v;")
         L.append("    } else {")
@@ -289,6 +285,39 @@ class Variant:
         L.append("      }")
         L.append("    }")
         self._edge_rotate(L, blocks, paths)
+        L.append("}")
+        return "\n".join(L)
+
+    def emit_uvu_wrappers(self) -> str:
+        """One launch runs every part: the workgroups of one receiver's parts
+        are neighbours on the same XCD (tp_part_node), so memory-heavy and
+        compute-heavy parts share the CUs instead of running one after the
+        other.  Part q of the backward writes grad_y partial q."""
+        nq = len(self.parts())
+        a_f = "x, y, w, rowptr, eid, src, map, out, n_nodes, C, n0"
+        a_b = "x, y, w, gout, rowptr, eid, src, map, cbuf, gy + (size_t)q * n_edges * %d, gw, n_nodes, C, n0, red" % self.D2
+        L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd(",
+             "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
+             "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C) {",
+             "  int q;",
+             f"  const int n0 = tp_part_node(n_nodes, {nq}, &q);",
+             "  if (n0 < 0) return;"]
+        for q in range(nq):
+            L.append(f"  {'if' if q == 0 else 'else if'} (q == {q}) f_{self.name}_fwd{q}<T, IN1_GM, OUT_GM>({a_f});")
+        L.append("}")
+        L += [f"template <typename T, bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_bwd(",
+              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
+              "    const T* __restrict__ gout,",
+              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+              "    const int* __restrict__ map, T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw,",
+              "    int n_nodes, int n_edges, int C) {",
+              "  __shared__ T red[2][8][16];",
+              "  int q;",
+              f"  const int n0 = tp_part_node(n_nodes, {nq}, &q);",
+              "  if (n0 < 0) return;"]
+        for q in range(nq):
+            L.append(f"  {'if' if q == 0 else 'else if'} (q == {q}) f_{self.name}_bwd{q}<T, NEED_GX, IN1_GM, OUT_GM>({a_b});")
         L.append("}")
         return "\n".join(L)
 
@@ -353,7 +382,8 @@ class Variant:
         P = len(self.paths)
         L = []
         L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_fwd(")
-        L.append("    const T* __restrict__ x1, const T* __restrict__ x2, T* __restrict__ out, int n_nodes, int C) {")
+        L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ w, T* __restrict__ out,")
+        L.append("    int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
         L.append("  const size_t N = (size_t)n_nodes;")
@@ -364,13 +394,17 @@ class Variant:
         for bb, d in enumerate(self.d2):
             for m in range(d):
                 L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
+        # per-node path weights w [N, P*C] (trainable / bilinear-gate form), or none
+        L.append(f"  const T* __restrict__ wn = w ? w + n * {P} * (size_t)C + u : nullptr;")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
+            L.append(f"  {{ const T wp = wn ? wn[(size_t){p} * C] : T(1);")
             for k in range(d):
                 terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
                 e3, gm = self._addr("out", p, k)
-                L.append(f"  out[OUT_GM ? ({gm}) : ({e3})] = {' + '.join(terms) if terms else 'T(0)'};")
+                L.append(f"    out[OUT_GM ? ({gm}) : ({e3})] = wp * ({' + '.join(terms) if terms else 'T(0)'});")
+            L.append("  }")
         L.append("}")
         return "\n".join(L)
 
@@ -378,8 +412,9 @@ class Variant:
         P = len(self.paths)
         L = []
         L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
-        L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ gout,")
-        L.append("    T* __restrict__ g1, T* __restrict__ g2, int n_nodes, int C) {")
+        L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ w,")
+        L.append("    const T* __restrict__ gout, T* __restrict__ g1, T* __restrict__ g2, T* __restrict__ gw,")
+        L.append("    int n_nodes, int C) {")
         L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
         L.append("  const size_t N = (size_t)n_nodes;")
@@ -392,12 +427,25 @@ class Variant:
             for m in range(d):
                 L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
                 L.append(f"  T hy{bb}_{m} = T(0);")
+        L.append(f"  const size_t wo = n * {P} * (size_t)C + u;")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
             L.append("  {")
             for k in range(d):
-                L.append(f"    const T g{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
+                L.append(f"    const T o{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
+            # grad of the weight: sum_k gout_k t_k with t the unweighted path output
+            L.append("    if (gw) {")
+            tsum = []
+            for k in range(d):
+                terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
+                if terms:
+                    tsum.append(f"o{k} * ({' + '.join(terms)})")
+            L.append(f"      gw[wo + (size_t){p} * C] = {' + '.join(tsum) if tsum else 'T(0)'};")
+            L.append("    }")
+            L.append(f"    const T wp = w ? w[wo + (size_t){p} * C] : T(1);")
+            for k in range(d):
+                L.append(f"    const T g{k} = wp * o{k};")
             for (i, j, k, c) in self.cg[p]:
                 L.append(f"    hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * g{k});")
                 L.append(f"    hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * g{k});")
@@ -416,20 +464,24 @@ class Variant:
     def emit(self) -> str:
         if self.kind == "uvu":
             nq = len(self.parts())
-            return "\n\n".join([self.emit_uvu_fwd(q) for q in range(nq)] + [self.emit_uvu_bwd(q) for q in range(nq)])
+            return "\n\n".join([self.emit_uvu_fwd(q) for q in range(nq)] + [self.emit_uvu_bwd(q) for q in range(nq)]
+                               + [self.emit_uvu_wrappers()])
         return self.emit_uuu_fwd() + "\n\n" + self.emit_uuu_bwd()
 
 
 # ------------------------------------------------------------ variant sets ----
-def model_variants(Lmax: int, lmax: int, correlation: int) -> List[Variant]:
+def model_variants(Lmax: int, lmax: int, correlation: int, bilinear: bool = False) -> List[Variant]:
     """All tensor-product variants one e3nnTACE model with these settings uses
     (cgtp interaction + CgtpACE product, natural parity, one fidelity,
-    energy target), mirroring ``base.py:113-360`` irreps bookkeeping."""
+    energy target), mirroring ``base.py:113-360`` irreps bookkeeping.  With
+    the bilinear-gate product basis (correlation 2) the second operand is the
+    hidden irreps plus one 0e block (``prod.py:83-87``)."""
     sh = list(range(lmax + 1))
     node_full = list(range(Lmax + 1))
     inter_out = list(range(lmax + 1)) if correlation != 1 else list(range(Lmax + 1))
     vs = [Variant("uvu", [0], sh, inter_out), Variant("uvu", node_full, sh, inter_out)]
     hidden = inter_out
+    base = hidden + [0] if bilinear else hidden
     for last in (False, True):
         in1 = hidden
         for nu in range(2, correlation + 1):
@@ -437,19 +489,20 @@ def model_variants(Lmax: int, lmax: int, correlation: int) -> List[Variant]:
                 out = [0] if last else list(range(Lmax + 1))
             else:
                 out = list(range(lmax + 1))
-            v = Variant("uuu", in1, hidden, out)
+            v = Variant("uuu", in1, base, out)
             vs.append(v)
             in1 = [l3 for (_, _, l3) in v.path_l]
     return vs
 
 
 SUPPORTED = [(1, 1, 2), (1, 1, 3), (2, 2, 2), (2, 2, 3), (3, 3, 2), (3, 3, 3), (2, 3, 3)]
+SUPPORTED_BILINEAR = [(1, 1, 2), (2, 2, 2), (3, 3, 2)]
 
 
 def all_variants() -> List[Variant]:
     seen, out = set(), []
-    for (Lm, lm, corr) in SUPPORTED:
-        for v in model_variants(Lm, lm, corr):
+    for (Lm, lm, corr, bil) in [s + (False,) for s in SUPPORTED] + [s + (True,) for s in SUPPORTED_BILINEAR]:
+        for v in model_variants(Lm, lm, corr, bil):
             if v.key not in seen:
                 seen.add(v.key)
                 out.append(v)
@@ -526,13 +579,29 @@ def emit_sh(lmax_all: int = 3) -> str:
     return "\n".join(L)
 
 
+# ------------------------------------------------------------ wigner-D cg ----
+def emit_wigner_cg(lmax_all: int = 3) -> str:
+    """W3j(1, l-1, l) tables for the edge-frame Wigner-D recursion
+    (``tace/models/o2/wigner.py:330-357``), flat [a][b][m]."""
+    L = ["// W3j(1, l-1, l) (e3nn real basis, unit Frobenius norm): the coupling of the",
+         "// Wigner-D recursion D^l = (2l+1) C^T (D^1 (x) D^(l-1)) C, flat [a][b][m].",
+         "template <int L> struct WigCG;"]
+    for l in range(2, lmax_all + 1):
+        cg = wigner_3j(1, l - 1, l)
+        vals = [repr(float(cg[a, b, m])) if abs(cg[a, b, m]) > 1e-14 else "0.0"
+                for a in range(3) for b in range(2 * l - 1) for m in range(2 * l + 1)]
+        L.append(f"template <> struct WigCG<{l}> {{ static constexpr double v[{3 * (2 * l - 1) * (2 * l + 1)}] = "
+                 f"{{{', '.join(vals)}}}; }};")
+    return "\n".join(L)
+
+
 # -------------------------------------------------------------------- main ----
 _UVU_FWD_SIG = ("const void*, const void*, const void*, const int*, const int*, const int*, const int*, void*, int, int, "
                 "int, hipStream_t")
 _UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, const int*, "
-                "void*, void*, void*, int, int, int, hipStream_t")
-_UUU_FWD_SIG = "const void*, const void*, void*, int, int, int, hipStream_t"
-_UUU_BWD_SIG = "const void*, const void*, const void*, void*, void*, int, int, int, hipStream_t"
+                "void*, void*, void*, int, int, int, int, hipStream_t")
+_UUU_FWD_SIG = "const void*, const void*, const void*, void*, int, int, int, hipStream_t"
+_UUU_BWD_SIG = "const void*, const void*, const void*, const void*, void*, void*, void*, int, int, int, hipStream_t"
 _TYPEDEFS = [
     f"typedef void (*UvuFwd)({_UVU_FWD_SIG});",
     f"typedef void (*UvuBwd)({_UVU_BWD_SIG});",
@@ -555,35 +624,34 @@ def _launchers(v: Variant) -> List[str]:
     out = []
     for T, tag in (("float", "f"), ("double", "d")):
         if v.kind == "uvu":
-            # grid: receivers padded to a multiple of 8 (tp_node); block: one lane per channel
-            launch = "const dim3 g((unsigned)((n + 7) / 8 * 8)), b((unsigned)((C + 63) / 64 * 64));"
+            # grid: parts x receivers padded to a multiple of 8 (tp_part_node); block: one lane per channel
+            nq = len(v.parts())
+            launch = f"const dim3 g((unsigned)((n + 7) / 8 * 8 * {nq})), b((unsigned)((C + 63) / 64 * 64));"
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, const int* map, void* o, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
-            for q in range(len(v.parts())):
-                for f in range(4):
-                    out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd{q}<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, map, ({T}*)o, n, C);")
+            for f in range(4):
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, map, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, void* cb, void* gy, void* gw, int n, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, void* cb, void* gy, void* gw, int n, int E, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
-            for q in range(len(v.parts())):  # in order: part q > 0 adds to grad_y
-                for f in range(4):
-                    for gx in (True, False):
-                        out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd{q}<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, C);")
+            for f in range(4):
+                for gx in (True, False):
+                    out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, E, C);")
             out.append("}")
         else:
-            out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, void* o, int n, int C, int flags, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, const void* w, void* o, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
             for f in UUU_LAYOUTS:
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, ({T}*)o, n, C);")
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)w, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* go, void* g1, void* g2, int n, int C, int flags, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* w, const void* go, void* g1, void* g2, void* gw, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
             out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
             for f in UUU_LAYOUTS:
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)go, ({T}*)g1, ({T}*)g2, n, C);")
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)w, (const {T}*)go, ({T}*)g1, ({T}*)g2, ({T}*)gw, n, C);")
             out.append("}")
     return out
 
@@ -595,6 +663,7 @@ def emit_all(gen_dir: str) -> List[str]:
     hdr = "// GENERATED by tace_amd/csrc/codegen.py -- do not edit."
     vs = all_variants()
     _write(os.path.join(gen_dir, "sh.inc"), [hdr, "#pragma once", emit_sh(3)])
+    _write(os.path.join(gen_dir, "wigner.inc"), [hdr, "#pragma once", emit_wigner_cg(3)])
     srcs = []
     for v in vs:
         body = [hdr, f"// variant {v.key}: {len(v.paths)} paths, per-channel dims in1={v.D1} in2={v.D2} out={v.DO}",
@@ -605,6 +674,7 @@ def emit_all(gen_dir: str) -> List[str]:
     reg = [hdr, "#pragma once", *_TYPEDEFS,
            "struct TpVariant {",
            "  const char* key; int kind; int npath; int d1; int d2; int dout;",
+           "  int nparts;                     // uvu: part kernels per launch = grad_y partials",
            "  int nseg; int seg[8][2];        // group-major grad-x row segments (offset / C, length / C)",
            "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
            "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;", "};"]
@@ -623,10 +693,10 @@ def emit_all(gen_dir: str) -> List[str]:
         seg = "{" + ", ".join(f"{{{a}, {b}}}" for a, b in segs + [(0, 0)] * (8 - len(segs))) + "}"
         head = f"\"{v.key}\", {0 if v.kind == 'uvu' else 1}, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}"
         if v.kind == "uvu":
-            reg.append(f"  {{{head}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
+            reg.append(f"  {{{head}, {len(v.parts())}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
                        f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")
         else:
-            reg.append(f"  {{{head}, 0, {seg}, nullptr, nullptr, nullptr, nullptr, "
+            reg.append(f"  {{{head}, 0, 0, {seg}, nullptr, nullptr, nullptr, nullptr, "
                        f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d}},")
     reg.append("};")
     reg.append(f"static const int kNumVariants = {len(vs)};")

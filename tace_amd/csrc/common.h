@@ -12,16 +12,6 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
-// Receiver of this workgroup.  Workgroups are dispatched round-robin over the
-// 8 XCDs; the grid is padded to a multiple of 8 and XCD k takes the k-th
-// contiguous range of receivers, so neighbouring receivers (which share most
-// senders) hit the same L2.  Returns -1 for padding workgroups.
-__device__ __forceinline__ int tp_node(int n_nodes) {
-  const int per = (int)(gridDim.x >> 3);
-  const int n = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
-  return n < n_nodes ? n : -1;
-}
-
 // bit-reversed low 4 bits of the lane: the component index that lane holds
 // after reduce16_lanes
 __device__ __forceinline__ int rev4(int lane) {
@@ -57,4 +47,18 @@ __device__ __forceinline__ T reduce16_lanes(T v0, T v1, T v2, T v3, T v4, T v5, 
   r += __shfl_xor(r, 16, 64);
   r += __shfl_xor(r, 32, 64);
   return r;
+}
+
+// Receiver and part of this workgroup when one launch runs `nparts` part
+// kernels.  Workgroups are dispatched round-robin over the 8 XCDs; the grid
+// is 8 * per * nparts workgroups (per = ceil(N / 8)) and XCD k takes the
+// contiguous receivers k*per .. k*per+per-1 (neighbouring receivers share
+// most senders, so they hit the same L2) and, for each, its parts in
+// consecutive workgroups of that XCD.  Returns -1 for padding workgroups.
+__device__ __forceinline__ int tp_part_node(int n_nodes, int nparts, int* q) {
+  const int per = (int)(gridDim.x >> 3) / nparts;
+  const int i = (int)(blockIdx.x >> 3);
+  *q = i % nparts;
+  const int n = (int)(blockIdx.x & 7) * per + i / nparts;
+  return n < n_nodes ? n : -1;
 }

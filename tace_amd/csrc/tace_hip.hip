@@ -39,6 +39,10 @@ int check_launch(const char* what) {
 
 }  // namespace
 
+// error helpers shared with the other translation units of the library
+int tace_fail_msg(const char* msg) { return fail(msg); }
+int tace_check_launch(const char* what) { return check_launch(what); }
+
 #include "common.h"
 #include "gen/registry.inc"
 #include "gen/sh.inc"
@@ -100,6 +104,17 @@ static void launch_seg_rowsum(const T* cbuf, const int* s_rowptr, const int* s_s
   else
     hipLaunchKernelGGL((k_seg_rowsum<T, 1>), dim3((unsigned)n), dim3(256), 0, st, cbuf, s_rowptr, s_slot, map, gx, n,
                        row, sg);
+}
+
+// gy = sum of the per-part grad_y partials, in part order
+template <typename T>
+__global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, int nparts, int64_t n,
+                                                   T* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  T acc = parts[i];
+  for (int q = 1; q < nparts; ++q) acc += parts[(size_t)q * n + i];
+  out[i] = acc;
 }
 
 // ------------------------------------------------------------ edge vectors --
@@ -510,6 +525,15 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
   return check_launch("tace_edge_tp_fwd");
 }
 
+int64_t tace_edge_tp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_workspace_elems: bad variant id");
+  if (n_edges < 0 || channels <= 0) return fail("tace_edge_tp_workspace_elems: bad sizes");
+  const TpVariant& v = kVariants[vid];
+  int64_t n = need_gx ? n_edges * (int64_t)channels * v.d1 : 0;
+  if (v.nparts > 1) n += (int64_t)v.nparts * n_edges * v.d2;
+  return n;
+}
+
 int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
                      int64_t n_nodes, int64_t n_edges,
@@ -520,10 +544,11 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
     return fail("tace_edge_tp_bwd: null pointer");
   const TpVariant& v = kVariants[vid];
   const int64_t row = (int64_t)channels * v.d1;
-  if (gx) {
-    if (!s_rowptr || (n_edges && (!s_slot || !workspace))) return fail("tace_edge_tp_bwd: grad_x needs sender CSR + workspace");
-    if (workspace_elems < n_edges * row) return fail("tace_edge_tp_bwd: workspace smaller than n_edges * channels * d1");
-  }
+  const int64_t cb_elems = gx ? n_edges * row : 0;
+  const int64_t need = cb_elems + (v.nparts > 1 ? (int64_t)v.nparts * n_edges * v.d2 : 0);
+  if (gx && !s_rowptr) return fail("tace_edge_tp_bwd: grad_x needs the sender CSR");
+  if (n_edges && ((gx && !s_slot) || (need && !workspace))) return fail("tace_edge_tp_bwd: null sender CSR or workspace");
+  if (workspace_elems < need) return fail("tace_edge_tp_bwd: workspace smaller than tace_edge_tp_workspace_elems()");
   RowSegs sg;
   memset(&sg, 0, sizeof(sg));
   if (layout & TACE_LAYOUT_IN1_GROUPED) {
@@ -534,20 +559,29 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
     }
   }
   hipStream_t s = (hipStream_t)stream;
+  if (dtype != TACE_F32 && dtype != TACE_F64) return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
+  const size_t es = dtype == TACE_F32 ? 4 : 8;
+  // workspace = [grad_x rows of every slot | grad_y partial of every part]
   // cbuf == nullptr selects the kernels without grad_x
   void* cbuf = gx && n_edges ? workspace : nullptr;
+  void* gyp = v.nparts > 1 ? (void*)((char*)workspace + cb_elems * es) : gy;
+  const int64_t ny = n_edges * v.d2;
+  const unsigned nb = (unsigned)((ny + 255) / 256);
   if (dtype == TACE_F32) {
-    v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout, channels, s);
+    if (v.nparts > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)gyp, v.nparts, ny, (float*)gy);
     if (gx && n_nodes)
       launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, node_map, (float*)gx, (int)n_nodes, row, sg,
                                channels, s);
-  } else if (dtype == TACE_F64) {
-    v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gy, gw, (int)n_nodes, layout, channels, s);
+  } else {
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout, channels, s);
+    if (v.nparts > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)gyp, v.nparts, ny,
+                         (double*)gy);
     if (gx && n_nodes)
       launch_seg_rowsum<double>((const double*)cbuf, s_rowptr, s_slot, node_map, (double*)gx, (int)n_nodes, row, sg,
                                 channels, s);
-  } else {
-    return fail("tace_edge_tp_bwd: dtype must be TACE_F32 or TACE_F64");
   }
   return check_launch("tace_edge_tp_bwd");
 }
@@ -558,7 +592,7 @@ static bool uuu_layout_ok(int32_t layout) {
          layout == (TACE_LAYOUT_IN1_GROUPED | TACE_LAYOUT_OUT_GROUPED | TACE_LAYOUT_IN2_GROUPED);
 }
 
-int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_nodes, int32_t channels,
+int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void* w, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_fwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_fwd: bad sizes");
@@ -568,27 +602,28 @@ int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, int64_t n_n
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.ufwd_f(x1, x2, out, (int)n_nodes, channels, layout, s);
+    v.ufwd_f(x1, x2, w, out, (int)n_nodes, channels, layout, s);
   else if (dtype == TACE_F64)
-    v.ufwd_d(x1, x2, out, (int)n_nodes, channels, layout, s);
+    v.ufwd_d(x1, x2, w, out, (int)n_nodes, channels, layout, s);
   else
     return fail("tace_uuu_fwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_uuu_fwd");
 }
 
-int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* gout, int64_t n_nodes,
-                 int32_t channels, int32_t layout, void* g1, void* g2, void* stream) {
+int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
   if (!uuu_layout_ok(layout)) return fail("tace_uuu_bwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
   if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
+  if (n_nodes && w && !gw) return fail("tace_uuu_bwd: weighted products need gw");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_bwd: too many nodes");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.ubwd_f(x1, x2, gout, g1, g2, (int)n_nodes, channels, layout, s);
+    v.ubwd_f(x1, x2, w, gout, g1, g2, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
   else if (dtype == TACE_F64)
-    v.ubwd_d(x1, x2, gout, g1, g2, (int)n_nodes, channels, layout, s);
+    v.ubwd_d(x1, x2, w, gout, g1, g2, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
   else
     return fail("tace_uuu_bwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_uuu_bwd");

@@ -14,7 +14,9 @@ Supported configuration (the one the benchmark workloads use): linear node
 embedding, identity edge embedding/update, ``cgtp`` atomic basis with
 ``sigmoid_gate`` (gate_m0), avg_num_neighbors scatter norm, BB element-aware
 resnet, ``cgtp`` product basis (correlation 1-3, one expert), energy readout
-with hidden [16], ``rms_forces`` scale, j0 Bessel x c2poly radial basis.
+with hidden [16], ``rms_forces`` scale, j0 Bessel x c2poly radial basis; and
+the TECE configuration: ``uv_so2`` layers (radial-rotary edge convolution,
+mmax = lmax) and the ``silu_bilineargate`` product basis (correlation 2).
 Anything else raises ``NotImplementedError`` at construction.
 """
 
@@ -67,9 +69,10 @@ class GMLayout:
     kernels read and write (``TACE_LAYOUT_*_GROUPED``)."""
 
     def __init__(self, irreps):
+        # one block per entry of ``irreps``: for simplified irreps this is the
+        # kernels' group-major layout; unsimplified irreps (adjacent equal
+        # entries) stay separate blocks, which only the model's own code reads
         self.irreps = Irreps(irreps)
-        if len(self.irreps.simplify()) != len(self.irreps):
-            raise ValueError(f"group-major layout needs simplified irreps, got {self.irreps}")
         self.blocks, s = [], 0
         for m, ir in self.irreps:
             self.blocks.append((s, m, ir.dim))
@@ -295,10 +298,11 @@ class uuuTensorProduct(torch.nn.Module):
         paths, self.irreps_out = generate_paths(Irreps(irreps_out), self.irreps_in1, self.irreps_in2, "uuu",
                                                 identical_inputs)
         self.C = self.irreps_in1[0][0]
+        self.weight_numel = self.C * len(paths)
         self.key = ops.variant_key("uuu", _ls(self.irreps_in1), _ls(self.irreps_in2), _ls(Irreps(irreps_out)))
 
-    def forward(self, x1, x2, layout: int = 0):
-        return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C, layout)
+    def forward(self, x1, x2, layout: int = 0, w=None):
+        return ops.uuu_tp(x1, x2, ops.find_variant(self.key), self.C, layout, w)
 
 
 class _GateFn(torch.autograd.Function):
@@ -399,15 +403,62 @@ class O3CgtpInteraction(torch.nn.Module):
         return m, sc
 
 
+class TeceInteraction(torch.nn.Module):
+    """``OAM20260705Interaction`` (``tace/models/_e3nn/inter.py:440-519``): the
+    cgtp interaction's linears, radial MLP and gate around the TECE
+    convolution (``tace_amd.tece``), without scatter normalisation."""
+
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, mmax, num_elements, radial_hidden, num_radial,
+                 num_head, edge_ace_hidden):
+        super().__init__()
+        from .tece import TeceConvolution
+        self.layer = layer
+        self.irreps_in = Irreps(irreps_in)
+        if self.irreps_in.lmax < 1:
+            raise ValueError("uv_so2 interactions need l > 0 inputs (inter.py:458-461)")
+        sh = spherical_harmonics_irreps(lmax)
+        self.irreps_out = (possible_tp_irreps(self.irreps_in, sh, False, lmax) * C).regroup()
+        if [ir.l for _, ir in self.irreps_out] != list(range(lmax + 1)):
+            raise NotImplementedError("TECE output must be one C block per l = 0..lmax")
+        if layer == num_layers - 1:
+            irreps_sc = (Irreps("0e") * C).regroup()
+        else:
+            irreps_sc = (possible_tp_irreps(self.irreps_in, sh, False, Lmax) * C).regroup()
+        self.linear_up = e3nnLinear(self.irreps_in, self.irreps_in, bias=True)
+        self.rejector = TeceConvolution(mmax, lmax, C, num_head, edge_ace_hidden, num_radial)
+        self.gated = Irreps([(C, ir) for _, ir in self.irreps_out])
+        gates = Irreps([(C, Irrep("0e")) for _ in self.gated])
+        self.linear_nonlinearity = e3nnLinear(self.gated, self.irreps_out, bias=True)
+        self.linear_down = e3nnLinear(Irreps([(C, ir) for _, ir in self.irreps_out]), (gates + self.gated).simplify(),
+                                      bias=True)
+        self.edge_info = MLP([num_radial] + list(radial_hidden) + [self.rejector.weight_numel])
+        if layer > 0:
+            self.resnetBB = e3nnElementLinear(self.irreps_in, irreps_sc, num_elements, bias=True)
+        self.C = C
+        self._gate_lay = (GMLayout(self.linear_down.irreps_out), GMLayout(self.gated))
+
+    def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
+        sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
+        x = self.linear_up(x)
+        msg = self.rejector(x, self.edge_info(R), plan, sp.node_map, src, dst, wigner, R)
+        m = self.linear_down(msg)
+        m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))
+        return m, sc
+
+
 class CgtpACE(torch.nn.Module):
     """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``): nu-chain of uuu products
     and per-species coefficient linears, evaluated on species-sorted nodes."""
 
-    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements, agnostic=False):
+    def __init__(self, layer, num_layers, irreps_in, C, Lmax, lmax, correlation, num_elements, agnostic=False,
+                 bilinear: bool = False):
         super().__init__()
         last = layer == num_layers - 1
         self.correlation = correlation
         self.agnostic = agnostic
+        self.bilinear = bilinear
+        if bilinear and correlation != 2:
+            raise ValueError("the bilinear-gate product basis needs correlation 2 (prod.py:83-84)")
         irreps_in = Irreps(irreps_in)
         hidden = Irreps([(C, ir) for _, ir in irreps_in])
         tp_out = []
@@ -432,23 +483,52 @@ class CgtpACE(torch.nn.Module):
 
         self.coefs = torch.nn.ModuleList([mk(Irreps([(C, ir) for _, ir in hidden]).simplify())])
         self.aces = torch.nn.ModuleList()
+        # bilinear gate (prod.py:83-87, 126-147, 178-214): second operand =
+        # hidden irreps + a C x 0e block of ones, per-node path weights
+        base = hidden + Irreps([(C, Irrep("0e"))]) if bilinear else hidden
         in1 = hidden
         for nu in range(2, correlation + 1):
-            ace = uuuTensorProduct(in1, hidden, tp_out[nu - 2], identical_inputs=(nu == 2))
+            ace = uuuTensorProduct(in1, base, tp_out[nu - 2], identical_inputs=(nu == 2 and not bilinear))
             self.aces.append(ace)
             self.coefs.append(mk(Irreps([(C, ir) for _, ir in ace.irreps_out]).simplify()))
             in1 = ace.irreps_out
         self.linear = e3nnLinear(Irreps([(C, ir) for _, ir in coefs_out]), self.irreps_out, bias=True)
+        self.C = C
+        if bilinear:
+            self.num_gate = sum(a.weight_numel for a in self.aces)
+            self.double = [(2 * C, ir) for _, ir in hidden]
+            self.linear_up = e3nnLinear(irreps_in, Irreps(f"{self.num_gate}x0e") + Irreps(self.double), bias=True)
+            self._up_lay = GMLayout(self.linear_up.irreps_out)
+
+    def _split_up(self, x):
+        """linear_up output -> (node features, base features + ones, path weights),
+        all group-major (``prod.py:178-214``)."""
+        u = self.linear_up(x)
+        Z, C = u.shape[0], self.C
+        ws = torch.nn.functional.silu(self._up_lay.block(u, 0))
+        node, base = [], []
+        for b, (mul, ir) in enumerate(self.double):
+            f = self._up_lay.block(u, b + 1).view(Z, ir.dim, mul)
+            node.append(f[:, :, :C].reshape(-1))
+            base.append(f[:, :, C:].reshape(-1))
+        base.append(u.new_ones(Z * C))
+        return torch.cat(node).view(Z, -1), torch.cat(base).view(Z, -1), ws
 
     def forward(self, x, sp: SpeciesPlan, sc):
         """x: group-major node features in species-sorted row order."""
+        ws = base = None
+        if self.bilinear:
+            x, base, ws = self._split_up(x)
         if self.agnostic:
             outs = self.coefs[0](x)
         else:
             outs = self.coefs[0](x, sp)
         feats = x
         for nu in range(2, self.correlation + 1):
-            feats = self.aces[nu - 2](feats, x, ops.LAYOUT_ALL_GROUPED)
+            if self.bilinear:
+                feats = self.aces[nu - 2](feats, base, ops.LAYOUT_ALL_GROUPED, ws)
+            else:
+                feats = self.aces[nu - 2](feats, x, ops.LAYOUT_ALL_GROUPED)
             outs = outs + (self.coefs[nu - 1](feats) if self.agnostic else self.coefs[nu - 1](feats, sp))
         outs = self.linear(outs)
         return outs + sc if sc is not None else outs
@@ -507,9 +587,15 @@ def _check_supported(cfg):
             raise NotImplementedError(f"{k}.type={cfg[k]['type']!r} is not on the MI355X path")
     ab = cfg.get("atomic_basis", {})
     types = ab.get("type", "cgtp")
-    for t in (types if isinstance(types, list) else [types]):
-        if t != "cgtp":
+    types = types if isinstance(types, list) else [types]
+    for t in types:
+        if t not in ("cgtp", "uv_so2"):
             raise NotImplementedError(f"atomic_basis.type={t!r} is not on the MI355X path")
+    if "uv_so2" in types:
+        if cfg.get("mmax", cfg["lmax"]) != cfg["lmax"]:
+            raise NotImplementedError("uv_so2 on the MI355X path needs mmax == lmax")
+        if ab.get("edge_nonlinear", "so2_sigmoid_gate") != "so2_sigmoid_gate":
+            raise NotImplementedError("uv_so2 needs edge_nonlinear=so2_sigmoid_gate")
     nl = ab.get("nonlinear", "sigmoid_gate")
     for t in (nl if isinstance(nl, list) else [nl]):
         if t != "sigmoid_gate":
@@ -523,8 +609,14 @@ def _check_supported(cfg):
     pb = cfg.get("product_basis", {})
     if pb.get("type", "cgtp") not in ("cgtp",) and not isinstance(pb.get("type"), list):
         raise NotImplementedError("only product_basis.type=cgtp is supported")
-    if pb.get("num_expert") not in (None, 1) or pb.get("nonlinear") is not None:
-        raise NotImplementedError("mixture-of-experts / bilinear product basis is not on the MI355X path")
+    if pb.get("num_expert") not in (None, 1):
+        raise NotImplementedError("mixture-of-experts product basis is not on the MI355X path")
+    if pb.get("nonlinear") not in (None, "silu_bilineargate"):
+        raise NotImplementedError(f"product_basis.nonlinear={pb.get('nonlinear')!r} is not on the MI355X path")
+    if pb.get("nonlinear") == "silu_bilineargate":
+        corr = pb.get("correlation", 3)
+        if any(c != 2 for c in (corr if isinstance(corr, list) else [corr])):
+            raise NotImplementedError("the bilinear-gate product basis needs correlation 2 (prod.py:83-84)")
     rs = cfg.get("resnet", {})
     if rs.get("type", "BB") != "BB" or rs.get("linear_type", "aware") != "aware" or rs.get("use_first_resnet"):
         raise NotImplementedError("only resnet type BB, element-aware, no first resnet is supported")
@@ -551,13 +643,24 @@ class Representation(torch.nn.Module):
         corr = corr if isinstance(corr, list) else [corr] * nl
         self.interactions = torch.nn.ModuleList()
         self.products = torch.nn.ModuleList()
+        ab = cfg.get("atomic_basis", {})
+        types = ab.get("type", "cgtp")
+        types = types if isinstance(types, list) else [types] * nl
+        self.use_so2 = "uv_so2" in types
+        pb = cfg["product_basis"]
+        bilinear = pb.get("nonlinear") == "silu_bilineargate"
         irreps = Irreps(f"{C}x0e")
         for layer in range(nl):
-            inter = O3CgtpInteraction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
-                                      rb["hidden"], rb["num_radial_basis"])
+            if types[layer] == "uv_so2":
+                inter = TeceInteraction(layer, nl, irreps, C, Lmax, L, cfg.get("mmax", L), S, rb["hidden"],
+                                        rb["num_radial_basis"], ab.get("num_head") or 1,
+                                        ab.get("edge_ace_hidden") or C)
+            else:
+                inter = O3CgtpInteraction(layer, nl, irreps, C, Lmax, L, corr[layer], S, cfg["avg_num_neighbors"],
+                                          rb["hidden"], rb["num_radial_basis"])
             self.interactions.append(inter)
-            prod = CgtpACE(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S,
-                           cfg["product_basis"].get("agnostic", False))
+            prod = CgtpACE(layer, nl, inter.irreps_out, C, Lmax, L, corr[layer], S, pb.get("agnostic", False),
+                           bilinear)
             self.products.append(prod)
             irreps = prod.irreps_out
 
@@ -567,12 +670,16 @@ class Representation(torch.nn.Module):
                               float(rb.radial_fn.prefactor), float(rb.cutoff_fn.cutoff), int(rb.cutoff_fn.p),
                               self.lmax)
 
-    def forward(self, attrs, plan: ops.EdgePlan, edge_vector, sp: SpeciesPlan):
+    def forward(self, attrs, plan: ops.EdgePlan, edge_vector, sp: SpeciesPlan, edge_index=None):
         """Node features (group-major, rows in ``sp``'s species-sorted order)."""
         R, Y = self.edge_features(edge_vector)
+        wigner = ops.edge_wigner(edge_vector, self.lmax) if self.use_so2 else None
         x = self.node_embedding(attrs.index_select(0, sp.perm))
         for inter, prod in zip(self.interactions, self.products):
-            x, sc = inter(x, sp, R, Y, plan)
+            if isinstance(inter, TeceInteraction):
+                x, sc = inter(x, sp, R, plan, edge_index[0], edge_index[1], wigner)
+            else:
+                x, sc = inter(x, sp, R, Y, plan)
             x = prod(x, sp, sc)
         return x
 
@@ -618,7 +725,7 @@ class TACE(torch.nn.Module):
         attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
         num_graphs = ptr.numel() - 1
         sp = SpeciesPlan(attrs)
-        x = self.representation(attrs, plan, edge_vector, sp)
+        x = self.representation(attrs, plan, edge_vector, sp, data["edge_index"])
         e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
         num_nodes = ptr[1:] - ptr[:-1]

@@ -216,18 +216,18 @@ class _EdgeTP(torch.autograd.Function):
         gx = torch.empty_like(x) if need_x else None
         gy = torch.empty_like(y)
         gw = torch.empty_like(w)
-        if need_x:
-            s_rowptr, s_slot = plan.sender_csr()
-            ws = torch.empty(max(plan.n_edges, 1) * C * var.d1, dtype=x.dtype, device=x.device)
-        else:
-            s_rowptr = s_slot = ws = None
+        s_rowptr, s_slot = plan.sender_csr() if need_x else (None, None)
+        n_ws = N.lib().tace_edge_tp_workspace_elems(var.vid, plan.n_edges, C, int(need_x))
+        if n_ws < 0:
+            N.check(int(n_ws), "tace_edge_tp_workspace_elems")
+        ws = torch.empty(max(n_ws, 1), dtype=x.dtype, device=x.device)
         tok = _t0("edge_tp_bwd:" + var.key)
         N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                          gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
                                          plan.src.data_ptr(), N.ptr(ctx.node_map), plan.n_nodes, plan.n_edges, C,
                                          ctx.layout,
                                          N.ptr(s_rowptr),
-                                         N.ptr(s_slot), N.ptr(ws), 0 if ws is None else ws.numel(), N.ptr(gx),
+                                         N.ptr(s_slot), ws.data_ptr(), ws.numel(), N.ptr(gx),
                                          gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
         _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
         return gx, gy, gw, None, None, None, None, None
@@ -303,38 +303,211 @@ LAYOUT_ALL_GROUPED = 7
 
 class _UUU(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x1, x2, var: TpVariant, C: int, layout: int):
+    def forward(ctx, x1, x2, w, var: TpVariant, C: int, layout: int):
         Nn = x1.shape[0]
         dt = x1.dtype
         _req(x1, "x1", dt, (Nn, C * var.d1))
         _req(x2, "x2", dt, (Nn, C * var.d2))
+        if w is not None:
+            _req(w, "w", dt, (Nn, C * var.npath))
         out = torch.empty(Nn, C * var.dout, dtype=dt, device=x1.device)
         tok = _t0("uuu_fwd:" + var.key)
-        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), Nn, C, layout,
-                                     out.data_ptr(), N.stream_ptr(x1.device)), "tace_uuu_fwd")
+        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), N.ptr(w), Nn, C,
+                                     layout, out.data_ptr(), N.stream_ptr(x1.device)), "tace_uuu_fwd")
         _t1(tok, (Nn, C))
-        ctx.save_for_backward(x1, x2)
+        ctx.save_for_backward(x1, x2, w)
         ctx.var, ctx.C, ctx.layout = var, C, layout
         return out
 
     @staticmethod
     def backward(ctx, gout):
-        x1, x2 = ctx.saved_tensors
+        x1, x2, w = ctx.saved_tensors
         gout = gout.contiguous()
         g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
+        gw = torch.empty_like(w) if w is not None else None
         tok = _t0("uuu_bwd:" + ctx.var.key)
-        N.check(N.lib().tace_uuu_bwd(ctx.var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(),
+        N.check(N.lib().tace_uuu_bwd(ctx.var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(), N.ptr(w),
                                      gout.data_ptr(), x1.shape[0], ctx.C, ctx.layout, g1.data_ptr(), g2.data_ptr(),
-                                     N.stream_ptr(x1.device)), "tace_uuu_bwd")
+                                     N.ptr(gw), N.stream_ptr(x1.device)), "tace_uuu_bwd")
         _t1(tok, (x1.shape[0], ctx.C))
-        return g1, g2, None, None, None
+        return g1, g2, gw, None, None, None
 
 
-def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0) -> torch.Tensor:
+def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0, w: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``layout`` = 0 (e3nn operands), LAYOUT_OUT_GROUPED, IN1|OUT or
     IN1|OUT|IN2 (LAYOUT_ALL_GROUPED): the group-major layout of
-    ``include/tace_hip.h`` for x1 / out / x2."""
-    return _UUU.apply(x1.contiguous(), x2.contiguous(), var, C, int(layout))
+    ``include/tace_hip.h`` for x1 / out / x2.  ``w`` [N, npath*C]: per-node
+    path weights (bilinear-gate product basis)."""
+    return _UUU.apply(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(), var, C, int(layout))
+
+
+# ---------------------------------------------------------------- TECE ops ----
+class _EdgeWigner(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, vec, lmax: int):
+        E = vec.shape[0]
+        K = (lmax + 1) ** 2
+        _req(vec, "edge_vector", vec.dtype, (E, 3))
+        W = torch.empty(E, K, K, dtype=vec.dtype, device=vec.device)
+        tok = _t0("edge_wigner_fwd")
+        N.check(N.lib().tace_edge_wigner_fwd(N.dtype_code(vec.dtype), vec.data_ptr(), E, lmax, W.data_ptr(),
+                                             N.stream_ptr(vec.device)), "tace_edge_wigner_fwd")
+        _t1(tok, (E,))
+        ctx.save_for_backward(vec)
+        ctx.lmax = lmax
+        return W
+
+    @staticmethod
+    def backward(ctx, gW):
+        (vec,) = ctx.saved_tensors
+        gW = gW.contiguous()
+        gv = torch.empty_like(vec)
+        tok = _t0("edge_wigner_bwd")
+        N.check(N.lib().tace_edge_wigner_bwd(N.dtype_code(vec.dtype), vec.data_ptr(), gW.data_ptr(), vec.shape[0],
+                                             ctx.lmax, gv.data_ptr(), N.stream_ptr(vec.device)), "tace_edge_wigner_bwd")
+        _t1(tok, (vec.shape[0],))
+        return gv, None
+
+
+def edge_wigner(vec: torch.Tensor, lmax: int) -> torch.Tensor:
+    """Edge-frame Wigner matrices [E, K, K] (rows in the SO(2) m layout,
+    columns e3nn components); the inverse rotation is the transpose."""
+    return _EdgeWigner.apply(vec.contiguous(), int(lmax))
+
+
+class _TeceScore(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, rp, tscale, lmax: int, H: int):
+        E, K, C = q.shape
+        dt = q.dtype
+        if K != (lmax + 1) ** 2:
+            raise ValueError(f"tece_score: {K} component rows, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
+        _req(q, "query", dt, (E, K, C))
+        _req(k, "key", dt, (E, K, C))
+        _req(rp, "radial_proj", dt, (E, 2 * H))
+        _req(tscale, "tscale", dt, (H,))
+        s = torch.empty(E, H, dtype=dt, device=q.device)
+        tok = _t0("tece_score_fwd")
+        N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), q.data_ptr(), k.data_ptr(), rp.data_ptr(),
+                                            tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(q.device)),
+                "tace_tece_score_fwd")
+        _t1(tok, (E,))
+        ctx.save_for_backward(q, k, rp, tscale)
+        ctx.lmax, ctx.H = lmax, H
+        return s
+
+    @staticmethod
+    def backward(ctx, gs):
+        q, k, rp, tscale = ctx.saved_tensors
+        E, K, C = q.shape
+        gs = gs.contiguous()
+        gq, gk, grp = torch.empty_like(q), torch.empty_like(k), torch.empty_like(rp)
+        tok = _t0("tece_score_bwd")
+        N.check(N.lib().tace_tece_score_bwd(N.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), rp.data_ptr(),
+                                            tscale.data_ptr(), gs.data_ptr(), E, ctx.lmax, C, ctx.H, gq.data_ptr(),
+                                            gk.data_ptr(), grp.data_ptr(), N.stream_ptr(q.device)),
+                "tace_tece_score_bwd")
+        _t1(tok, (E,))
+        # the attention temperature is a model parameter: no gradient on this
+        # (inference) path, as the calculators freeze parameters
+        return gq, gk, grp, None, None, None
+
+
+def tece_score(q, k, radial_proj, tscale, lmax: int, heads: int) -> torch.Tensor:
+    """Radial-rotary complex QK score [E, heads] (tscale = attention scale x temperature)."""
+    if tscale.requires_grad:
+        raise ValueError("tece_score: the temperature gradient is not computed (parameters must be frozen)")
+    return _TeceScore.apply(q.contiguous(), k.contiguous(), radial_proj.contiguous(), tscale.contiguous(),
+                            int(lmax), int(heads))
+
+
+class _GraphSoftmax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, s, plan: EdgePlan):
+        E, H = s.shape
+        _req(s, "score", s.dtype, (plan.n_edges, H))
+        a = torch.empty_like(s)
+        tok = _t0("graph_softmax_fwd")
+        N.check(N.lib().tace_graph_softmax_fwd(N.dtype_code(s.dtype), s.data_ptr(), plan.rowptr.data_ptr(),
+                                               N.ptr(plan.eid), plan.n_nodes, H, a.data_ptr(),
+                                               N.stream_ptr(s.device)), "tace_graph_softmax_fwd")
+        _t1(tok, (E,))
+        ctx.save_for_backward(a)
+        ctx.plan = plan
+        return a
+
+    @staticmethod
+    def backward(ctx, ga):
+        (a,) = ctx.saved_tensors
+        plan = ctx.plan
+        ga = ga.contiguous()
+        gs = torch.empty_like(a)
+        tok = _t0("graph_softmax_bwd")
+        N.check(N.lib().tace_graph_softmax_bwd(N.dtype_code(a.dtype), a.data_ptr(), ga.data_ptr(),
+                                               plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.n_nodes, a.shape[1],
+                                               gs.data_ptr(), N.stream_ptr(a.device)), "tace_graph_softmax_bwd")
+        _t1(tok, (a.shape[0],))
+        return gs, None
+
+
+def graph_softmax(score: torch.Tensor, plan: EdgePlan) -> torch.Tensor:
+    """Softmax of ``score`` [E, H] over each receiver's in-edges (receiver CSR)."""
+    return _GraphSoftmax.apply(score.contiguous(), plan)
+
+
+class _TeceRotateOut(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, H: int):
+        E, K, C = m.shape
+        dt = m.dtype
+        if K != (lmax + 1) ** 2:
+            raise ValueError(f"tece_rotate_out: {K} component rows, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
+        _req(m, "messages", dt, (plan.n_edges, K, C))
+        if node_map is not None:
+            _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+        _req(alpha, "alpha", dt, (E, H))
+        _req(W, "wigner", dt, (E, K, K))
+        out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=m.device)
+        tok = _t0("tece_rotate_out_fwd")
+        N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), m.data_ptr(), alpha.data_ptr(), W.data_ptr(),
+                                                 plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map),
+                                                 plan.n_nodes, lmax, C, H, out.data_ptr(),
+                                                 N.stream_ptr(m.device)), "tace_tece_rotate_out_fwd")
+        _t1(tok, (plan.n_nodes, E, C))
+        ctx.save_for_backward(m, alpha, W, node_map, dst)
+        ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        m, alpha, W, node_map, dst = ctx.saved_tensors
+        plan, lmax, H = ctx.plan, ctx.lmax, ctx.H
+        E, K, C = m.shape
+        gout = gout.contiguous()
+        gm, ga = torch.empty_like(m), torch.empty_like(alpha)
+        tok = _t0("tece_rotate_out_bwd")
+        N.check(N.lib().tace_tece_rotate_out_bwd(N.dtype_code(m.dtype), m.data_ptr(), alpha.data_ptr(), W.data_ptr(),
+                                                 gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
+                                                 N.ptr(node_map), plan.n_nodes, lmax, C, H, gm.data_ptr(),
+                                                 ga.data_ptr(), N.stream_ptr(m.device)), "tace_tece_rotate_out_bwd")
+        _t1(tok, (plan.n_nodes, E, C))
+        gW = None
+        if ctx.needs_input_grad[2]:
+            # gW[e] = (alpha m)[e] g_out[dst e]^T over the channels (batched GEMM)
+            rows = dst if node_map is None else node_map.long()[dst]
+            Nn = plan.n_nodes
+            g_lc = torch.cat([gout.view(-1)[Nn * C * l * l:Nn * C * (l + 1) ** 2].view(Nn, 2 * l + 1, C)
+                              for l in range(lmax + 1)], dim=1)
+            am = (m.view(E, K, H, C // H) * alpha.view(E, 1, H, 1)).view(E, K, C)
+            gW = torch.bmm(am, g_lc.index_select(0, rows).transpose(1, 2).contiguous())
+        return gm, ga, gW, None, None, None, None, None
+
+
+def tece_rotate_out(m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, heads: int) -> torch.Tensor:
+    """sum_{e -> n} W[e]^T (alpha[e] m[e]) per receiver n, in the group-major
+    layout of C x (0..lmax) at rows node_map[n] ([N, K*C])."""
+    return _TeceRotateOut.apply(m.contiguous(), alpha.contiguous(), W.contiguous(), plan, node_map, dst.long(),
+                                int(lmax), int(heads))
 
 
 def to_grouped(x: torch.Tensor, ls: Sequence[int], C: int) -> torch.Tensor:

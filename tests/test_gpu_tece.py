@@ -1,0 +1,337 @@
+"""TECE path parity against the CPU oracle (GPU): edge Wigner frames, the
+radial-rotary score, the graph softmax, the attention-weighted inverse
+rotation + receiver sum, the weighted (bilinear-gate) uuu product, the whole
+convolution and the config-5 model (energy + forces).
+
+Operator tolerances as in ``test_gpu_kernels``: float64 to 1e-11 relative to
+the largest magnitude, float32 to 2e-5.  Model bars:
+float64 energies to 1e-10 relative and forces to 1e-8 eV/A, float32 to 1e-5
+and 1e-4 eV/A.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model as om
+from oracle import neighbours as onl
+from oracle import tece as ot
+from tace_amd import configs, data, ops, structures
+from tace_amd import model as pm
+from tace_amd import tece as pt
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float64: 1e-11, torch.float32: 2e-5}
+
+
+def close(got, want, dtype, what="", tol=None):
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    scale = max(want.abs().max().item(), 1e-30)
+    err = (got - want).abs().max().item() / scale
+    assert err < (tol or TOL[dtype]), f"{what}: max rel err {err:.3e} (scale {scale:.3e})"
+
+
+def _vectors(E, g):
+    d = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    d = d / d.norm(dim=1, keepdim=True) * (0.5 + 4.5 * torch.rand(E, 1, generator=g, dtype=torch.float64))
+    # the chart boundaries of the frame blend: along +-y, in the x-z plane,
+    # at the smooth step's ends and on the axes
+    special = torch.tensor([[0, 1, 0], [0, -1, 0], [1, 0, 0], [0, 0, 1], [1, 0, 1], [0, 2.5, 1e-9],
+                            [0, -2.5, 1e-9], [1e-3, 1.0, 0], [1e-3, -1.0, 0], [-1, 0, -1]], dtype=torch.float64)
+    return torch.cat([d, special])
+
+
+def _random_graph(N, E, g):
+    src = torch.randint(0, N, (E,), generator=g)
+    dst = torch.randint(0, N - 2, (E,), generator=g)  # the last two nodes receive nothing
+    dst[0] = N - 3  # one receiver with a single in-edge
+    dst[dst == N - 3] = N - 4
+    dst[0] = N - 3
+    return torch.stack([src, dst])
+
+
+def _lc_to_gm(x, node_map, lmax):
+    """[N, (L+1)^2, C] l layout in node order -> group-major rows node_map[n]."""
+    N, _, C = x.shape
+    blocks = []
+    for l in range(lmax + 1):
+        b = torch.empty(N, 2 * l + 1, C, dtype=x.dtype)
+        b[node_map.long()] = x[:, l * l:(l + 1) ** 2]
+        blocks.append(b.reshape(-1))
+    return torch.cat(blocks).view(N, -1)
+
+
+def _gm_to_lc(x, node_map, lmax, C):
+    N = x.shape[0]
+    flat = x.reshape(-1)
+    parts = []
+    for l in range(lmax + 1):
+        b = flat[N * C * l * l:N * C * (l + 1) ** 2].view(N, 2 * l + 1, C)
+        parts.append(b[node_map.long()])
+    return torch.cat(parts, dim=1)
+
+
+# ----------------------------------------------------------- edge frames ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax", [1, 2, 3])
+def test_edge_wigner_matches_oracle(cuda, dtype, lmax):
+    g = torch.Generator().manual_seed(40 + lmax)
+    vec = _vectors(2000, g).to(dtype).double().requires_grad_(True)
+    W_o, _ = ot.edge_wigner(vec, lmax, lmax)
+    gW = torch.randn(W_o.shape, generator=g, dtype=torch.float64)
+    (gv_o,) = torch.autograd.grad((W_o * gW).sum(), vec)
+    v = vec.detach().to(dtype).to(cuda).requires_grad_(True)
+    W = ops.edge_wigner(v, lmax)
+    tol = None if dtype == torch.float64 else 1e-5
+    close(W, W_o, dtype, "wigner", tol)
+    (gv,) = torch.autograd.grad((W * gW.to(dtype).to(cuda)).sum(), v)
+    # the frame derivative is largest on the blend's steep part; compare per edge
+    # relative to that edge's gradient size
+    err = (gv.double().cpu() - gv_o).norm(dim=1) / (gv_o.norm(dim=1) + 1.0)
+    assert err.max().item() < (1e-10 if dtype == torch.float64 else 5e-4), err.max().item()
+
+
+# ---------------------------------------------------------------- score ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (2, 2, 32), (1, 1, 16), (3, 4, 64)])
+def test_tece_score_matches_oracle(cuda, dtype, lmax, H, C):
+    g = torch.Generator().manual_seed(lmax * 100 + H * 10 + C)
+    torch.manual_seed(0)
+    conv = ot.TeceConvolution(lmax, lmax, C, H, 8, 8).double()
+    with torch.no_grad():
+        conv.radial_proj.weight.copy_(torch.randn(conv.radial_proj.weight.shape, generator=g))
+        conv.radial_proj.bias.copy_(0.3 * torch.randn(conv.radial_proj.bias.shape, generator=g))
+        conv.temperature_logit.copy_(torch.randn(H, generator=g, dtype=torch.float64))
+    E, rows = 777, (lmax + 1) ** 2  # the projections' output rows (per m: n - m of them, twice for m > 0)
+    q = torch.randn(E, rows, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    k = torch.randn(E, rows, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    R = torch.randn(E, 8, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    s_o = conv.score(q, k, R)
+    gs = torch.randn(s_o.shape, generator=g, dtype=torch.float64)
+    gq_o, gk_o, gR_o = torch.autograd.grad((s_o * gs).sum(), [q, k, R])
+
+    a, b, r = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (q, k, R))
+    W = (conv.radial_proj.weight * conv.radial_proj.alpha).detach().to(dtype).to(cuda)
+    rp = torch.nn.functional.linear(r, W, conv.radial_proj.bias.detach().to(dtype).to(cuda))
+    T = conv.tmin + (conv.tmax - conv.tmin) * torch.sigmoid(conv.temperature_logit.detach())
+    s = ops.tece_score(a, b, rp, (T * conv.attention_scale).to(dtype).to(cuda), lmax, H)
+    close(s, s_o, dtype, "score")
+    gq, gk, gR = torch.autograd.grad((s * gs.to(dtype).to(cuda)).sum(), [a, b, r])
+    close(gq, gq_o, dtype, "grad q")
+    close(gk, gk_o, dtype, "grad k")
+    close(gR, gR_o, dtype, "grad R")
+
+
+# -------------------------------------------------------------- softmax ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("H", [1, 4])
+@pytest.mark.parametrize("sorted_edges", [True, False])
+def test_graph_softmax_matches_oracle(cuda, dtype, H, sorted_edges):
+    g = torch.Generator().manual_seed(H * 2 + sorted_edges)
+    N, E = 300, 5000
+    ei = _random_graph(N, E, g)
+    if sorted_edges:
+        ei = ei[:, torch.argsort(ei[1], stable=True)]
+    s = (3.0 * torch.randn(E, H, generator=g, dtype=torch.float64)).to(dtype).double().requires_grad_(True)
+    a_o = ot.graph_softmax(s, ei[1], N)
+    ga = torch.randn(a_o.shape, generator=g, dtype=torch.float64)
+    (gs_o,) = torch.autograd.grad((a_o * ga).sum(), s)
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
+    assert (plan.eid is None) == sorted_edges
+    x = s.detach().to(dtype).to(cuda).requires_grad_(True)
+    a = ops.graph_softmax(x, plan)
+    close(a, a_o, dtype, "alpha")
+    (gs,) = torch.autograd.grad((a * ga.to(dtype).to(cuda)).sum(), x)
+    close(gs, gs_o, dtype, "grad score")
+
+
+def test_graph_softmax_empty_graph(cuda):
+    plan = ops.EdgePlan.from_edge_index(torch.zeros(2, 0, dtype=torch.int64, device=cuda), 5)
+    s = torch.zeros(0, 4, dtype=torch.float64, device=cuda, requires_grad=True)
+    a = ops.graph_softmax(s, plan)
+    assert a.shape == (0, 4)
+
+
+# ---------------------------------------------------------- rotate out ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (2, 1, 64), (1, 2, 32), (2, 2, 256), (3, 4, 64)])
+def test_rotate_out_matches_oracle(cuda, dtype, lmax, H, C):
+    g = torch.Generator().manual_seed(lmax * 1000 + H * 100 + C)
+    N, E = 120, 1500
+    K = (lmax + 1) ** 2
+    ei = _random_graph(N, E, g)
+    node_map = torch.randperm(N, generator=g).to(torch.int32)
+    vec = _vectors(E - 10, g)
+    W_o, Winv_o = ot.edge_wigner(vec, lmax, lmax)
+    W_o = W_o.to(dtype).double().requires_grad_(True)
+    m = torch.randn(E, K, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    al = torch.rand(E, H, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    mm = (m.view(E, K, H, C // H) * al.view(E, 1, H, 1)).view(E, K, C)
+    o = torch.zeros(N, K, C, dtype=torch.float64).index_add(0, ei[1], torch.bmm(W_o.transpose(1, 2), mm))
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64)
+    gm_o, ga_o, gW_o = torch.autograd.grad((o * go).sum(), [m, al, W_o])
+
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
+    a, b, w = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (m, al, W_o))
+    nm = node_map.to(cuda)
+    out = ops.tece_rotate_out(a, b, w, plan, nm, ei[1].to(cuda), lmax, H)
+    close(out, _lc_to_gm(o, node_map, lmax), dtype, "out")
+    gout = _lc_to_gm(go, node_map, lmax).to(dtype).to(cuda)
+    gm, ga, gW = torch.autograd.grad((out * gout).sum(), [a, b, w])
+    close(gm, gm_o, dtype, "grad m")
+    close(ga, ga_o, dtype, "grad alpha")
+    close(gW, gW_o, dtype, "grad W")
+
+
+# ------------------------------------------------------- weighted uuu ----
+def _irreps(ls, C):
+    return [(C, (l, (-1) ** l)) for l in ls]
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("L,last", [(2, False), (2, True), (1, False), (3, False), (3, True)])
+def test_bilinear_uuu_matches_oracle(cuda, dtype, L, last):
+    """uuu with the ones-augmented second operand and per-node path weights
+    (bilinear-gate product basis), all operands group-major."""
+    C = 64
+    full = list(range(L + 1))
+    base = full + [0]
+    outl = [0] if last else full
+    tp = om.UUUTP(_irreps(full, C), _irreps(base, C), [(1, (l, (-1) ** l)) for l in outl], False)
+    out_ls = [ir[0] for _, ir in tp.out]
+    g = torch.Generator().manual_seed(L * 10 + last)
+    Nn = 37
+    x1 = torch.randn(Nn, sum(C * (2 * l + 1) for l in full), generator=g, dtype=torch.float64)
+    x2 = torch.randn(Nn, sum(C * (2 * l + 1) for l in base), generator=g, dtype=torch.float64)
+    x2[:, -C:] = 1.0
+    ws = torch.randn(Nn, len(tp.paths) * C, generator=g, dtype=torch.float64)
+    x1, x2, ws = (t.to(dtype).double().requires_grad_(True) for t in (x1, x2, ws))
+    o = tp(x1, x2, ws)
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64).to(dtype).double()
+    g1o, g2o, gwo = torch.autograd.grad((o * go).sum(), [x1, x2, ws])
+    var = ops.find_variant(ops.variant_key("uuu", full, base, outl))
+    assert var.npath == len(tp.paths)
+    a = ops.to_grouped(x1.detach().to(dtype).to(cuda), full, C).requires_grad_(True)
+    b = ops.to_grouped(x2.detach().to(dtype).to(cuda), base, C).requires_grad_(True)
+    w = ws.detach().to(dtype).to(cuda).requires_grad_(True)
+    out = ops.uuu_tp(a, b, var, C, ops.LAYOUT_ALL_GROUPED, w)
+    close(ops.from_grouped(out, out_ls, C), o, dtype, "out")
+    gg = ops.to_grouped(go.to(dtype).to(cuda), out_ls, C)
+    g1, g2, gw = torch.autograd.grad((out * gg).sum(), [a, b, w])
+    close(ops.from_grouped(g1, full, C), g1o, dtype, "g1")
+    close(ops.from_grouped(g2, base, C), g2o, dtype, "g2")
+    close(gw, gwo, dtype, "gw")
+
+
+# ------------------------------------------------------- convolution ----
+def _perturb_tece(module, g):
+    """Random radial phase / bias and temperatures (zero / fixed at init), so
+    that the rotary and temperature terms are exercised."""
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            if "radial_proj" in name:
+                p.copy_(0.7 * torch.randn(p.shape, generator=g, dtype=torch.float64))
+            elif "temperature_logit" in name:
+                p.copy_(torch.randn(p.shape, generator=g, dtype=torch.float64))
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("C,H,A", [(128, 4, 32), (32, 2, 16)])
+def test_tece_convolution_matches_oracle(cuda, dtype, C, H, A):
+    lmax, nr = 2, 8
+    g = torch.Generator().manual_seed(C + H + A)
+    N, E = 64, 900
+    ei = _random_graph(N, E, g)
+    torch.manual_seed(3)
+    conv_o = ot.TeceConvolution(lmax, lmax, C, H, A, nr).double()
+    _perturb_tece(conv_o, g)
+    K = (lmax + 1) ** 2
+    x = torch.randn(N, K, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    w = torch.randn(E, conv_o.weight_numel, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    R = torch.randn(E, nr, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    vec = _vectors(E - 10, g).to(dtype).double().requires_grad_(True)
+    W_o, Wi_o = ot.edge_wigner(vec, lmax, lmax)
+    o = conv_o(x, w, ei, W_o, Wi_o, R)
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64)
+    grads_o = torch.autograd.grad((o * go).sum(), [x, w, R, vec])
+
+    conv = pt.TeceConvolution(lmax, lmax, C, H, A, nr).to(dtype)
+    conv.load_state_dict({k: v.to(dtype) for k, v in conv_o.state_dict().items()})
+    conv = conv.to(cuda)
+    node_map = torch.randperm(N, generator=g).to(torch.int32)
+    nm = node_map.to(cuda)
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
+    xg = _lc_to_gm(x.detach(), node_map, lmax).to(dtype).to(cuda).requires_grad_(True)
+    wg, Rg, vg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (w, R, vec))
+    src, dst = ei[0].to(cuda), ei[1].to(cuda)
+    out = conv(xg, wg, plan, nm, src, dst, ops.edge_wigner(vg, lmax), Rg)
+    tol = None if dtype == torch.float64 else 2e-4
+    close(out, _lc_to_gm(o, node_map, lmax), dtype, "out", tol)
+    gx, gw, gR, gv = torch.autograd.grad((out * _lc_to_gm(go, node_map, lmax).to(dtype).to(cuda)).sum(),
+                                         [xg, wg, Rg, vg])
+    close(_gm_to_lc(gx.detach().cpu(), node_map, lmax, C), grads_o[0], dtype, "grad x", tol)
+    close(gw, grads_o[1], dtype, "grad w", tol)
+    close(gR, grads_o[2], dtype, "grad R", tol)
+    close(gv, grads_o[3], dtype, "grad vec", tol if tol is None else 1e-3)
+
+
+# ---------------------------------------------------------------- model ----
+BARS = {torch.float64: (1e-10, 1e-8), torch.float32: (1e-5, 1e-4)}
+
+
+def _model_pair(structs, cuda, dtype, seed=0, **over):
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS["tece"]["cutoff"])
+             for s in structs]
+    zs = sorted({int(z) for s in structs for z in s["numbers"]})
+    nat = sum(len(s["positions"]) for s in structs)
+    avg = sum(e[0].shape[1] for e in edges) / nat
+    cfg = configs.model_cfg("tece", zs, avg, **over)
+    torch.manual_seed(seed)
+    ref = om.TACE(cfg).double()
+    _perturb_tece(ref, torch.Generator().manual_seed(seed + 1))
+    d64 = data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float64)
+    want = om.compute(ref, d64, forces=True, stress=False)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        gpu = pm.create_model(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    pm.load_reference_state_dict(gpu.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
+                                                  for k, v in ref.state_dict().items()})
+    gpu = gpu.to(cuda)
+    gpu.reset_target_property(["energy", "forces"])
+    got = gpu(data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda))
+    return got, want
+
+
+def _check(got, want, dtype):
+    e_rel, f_abs = BARS[dtype]
+    E, E0 = got["energy"].double().cpu(), want["energy"]
+    assert ((E - E0).abs() / E0.abs()).max().item() < e_rel, (E, E0)
+    F, F0 = got["forces"].double().cpu(), want["forces"]
+    assert (F - F0).abs().max().item() < f_abs, (F - F0).abs().max().item()
+    assert (F - F0).abs().max().item() <= 1e-3 * F0.abs().max().item() + f_abs * 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_tece_bcc_fe_slice(cuda, dtype):
+    """Config 5 architecture (TECE, C=128, L=2, 4 heads, 2 layers, r_c=5) on a 3x3x3 bcc Fe slice."""
+    got, want = _model_pair([structures.bcc_fe(reps=(3, 3, 3), seed=7)], cuda, dtype)
+    _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_tece_two_species_batch(cuda, dtype):
+    """Two graphs, two species (species-sorted rows, per-species resnet), C=32."""
+    a = structures.bcc_fe(reps=(2, 2, 3), seed=8)
+    b = structures.bcc_fe(reps=(3, 2, 2), seed=9)
+    nb = np.array(b["numbers"]).copy()
+    nb[::3] = 28
+    b = dict(b, numbers=nb)
+    got, want = _model_pair([a, b], cuda, dtype, seed=4, num_channel=32, edge_ace_hidden=16, num_head=2)
+    _check(got, want, dtype)

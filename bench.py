@@ -1,13 +1,16 @@
 """Benchmark: TACE energy + conservative forces on the 12,288-atom water box.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                    [--workload water12k|fe101k]
 
 One step = one MD-step evaluation on one GPU: GPU cell-list neighbour list
 from positions resident in HBM, the model forward (edge featurisation, 3
 interaction + product layers, readout) and the backward for F = -dE/dr.
 Workload: 4,096 H2O, 49.7 A periodic cube, r_c = 6,
 Cartesian-TACE architecture C=128, L=3, nu=3, 3 layers, random-init weights
-(seed 0), float32.  Prints one JSON line on stdout.
+(seed 0), float32.  Prints one JSON line on stdout.  ``--workload fe101k``
+measures the TECE configuration instead (bcc Fe
+37^3 cells, 101,306 atoms, r_c = 5, C=128, L=2, 4 heads, 2 layers).
 
 ``roofline`` is for the kernel with the largest share of the timed region,
 bracketed with HIP events on the stream it runs on; its algorithmic bytes
@@ -57,6 +60,30 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     if name.startswith("uuu_bwd"):
         n, C = info
         return s * n * C * (2 * var.d1 + 2 * var.d2 + var.dout)
+    if name.startswith("edge_wigner_fwd"):
+        E, K = info
+        return s * E * (3 + K * K)
+    if name.startswith("edge_wigner_bwd"):
+        E, K = info
+        return s * E * (3 + K * K + 3)
+    if name.startswith("tece_score_fwd"):
+        E, K, C, H = info
+        return s * E * (2 * K * C + 2 * H + H) + s * H
+    if name.startswith("tece_score_bwd"):
+        E, K, C, H = info
+        return s * E * (4 * K * C + 4 * H + H) + s * H
+    if name.startswith("graph_softmax_fwd"):
+        E, H, n = info
+        return s * E * H * 2 + 4 * (E + n + 1)
+    if name.startswith("graph_softmax_bwd"):
+        E, H, n = info
+        return s * E * H * 3 + 4 * (E + n + 1)
+    if name.startswith("tece_rotate_out_fwd"):
+        n, E, C, K, H = info
+        return s * (E * (K * C + H + K * K) + n * K * C) + 4 * (E + 2 * n + 1)
+    if name.startswith("tece_rotate_out_bwd"):
+        n, E, C, K, H = info
+        return s * (E * (2 * K * C + 2 * H + K * K) + n * K * C) + 4 * (E + 2 * n + 1)
     if name.startswith("edge_basis_fwd"):
         (E,) = info
         return s * E * (3 + 8 + 16)
@@ -66,10 +93,10 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     return float("nan")
 
 
-def measured_traffic(entry: str):
+def measured_traffic(workload: str, entry: str):
     """HBM bytes per call of ``entry`` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-    summary committed under profiles/ (None when not measured)."""
-    path = os.path.join(ROOT, "profiles", "water12k_hbm_traffic.md")
+    summary committed under profiles/ for this workload (None when not measured)."""
+    path = os.path.join(ROOT, "profiles", f"{workload}_hbm_traffic.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -81,17 +108,18 @@ def measured_traffic(entry: str):
     return None
 
 
-def cpu_baseline(preset_cfg_fn, n_side=5, reps=3):
-    """CPU oracle on a 125-molecule slice of the same water model (float32)."""
+def cpu_baseline(wl, reps=3):
+    """CPU oracle on a bounded slice of the workload's structure (same model, float32)."""
     from oracle import model as om
     from oracle import neighbours as onl
-    from tace_amd import data, structures
+    from tace_amd import data
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    s = structures.water_box(n_side=n_side, box=49.7 / 16 * n_side, seed=1)
-    ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], 6.0)
-    cfg = preset_cfg_fn(ei.shape[1] / len(s["numbers"]))
+    s, what = wl["cpu_slice"]()
+    rc = wl["cutoff"]
+    ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)
+    cfg = wl["cfg"](ei.shape[1] / len(s["numbers"]))
     torch.manual_seed(0)
     m = om.TACE(cfg).float()
     for prm in m.parameters():  # frozen, as in the reference calculators
@@ -100,15 +128,40 @@ def cpu_baseline(preset_cfg_fn, n_side=5, reps=3):
     om.compute(m, d, forces=True)  # warm-up
     t0 = time.perf_counter()
     for _ in range(reps):
-        t_nl = time.perf_counter()
-        ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], 6.0)
+        ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)
         d = data.collate([s], [(ei, S)], cfg["atomic_numbers"], dtype=torch.float32)
         om.compute(m, d, forces=True)
     dt = time.perf_counter() - t0
     n = len(s["numbers"])
     return dict(value=n * reps / dt, unit="atom-steps/s", cores=threads, kind="port",
-                sample=f"{n}-atom water slice ({n_side}^3 H2O, same C=128/L=3/3-layer model, float32), "
+                sample=f"{n}-atom {what} (same model, float32), "
                        f"{reps} timed E+F steps incl. brute-force NL after 1 warm-up; {dt:.1f} s")
+
+
+def workloads(args):
+    """The bench workloads: the headline water box (configs[2], default) and the
+    TECE bcc Fe box."""
+    from tace_amd import configs, structures
+
+    box = 49.7 / 16 * args.n_side
+    water = dict(
+        metric=METRIC, cutoff=6.0, dt_fs=DT_FS, species=[1, 8],
+        structure=lambda: structures.water_box(n_side=args.n_side, box=box, seed=0),
+        cfg=lambda a: configs.model_cfg("water12k", [1, 8], a),
+        describe=lambda nat: f"water box {nat} atoms (configs[2]), E+F, NL rebuilt every step",
+        arch=dict(channels=128, L=3, correlation=3, layers=3, cutoff=6.0),
+        cpu_slice=lambda: (structures.water_box(n_side=5, box=49.7 / 16 * 5, seed=1), "water slice (5^3 H2O)"))
+    r = args.fe_reps
+    fe = dict(
+        metric=f"atom-steps/sec (E+F, fp32) at {2 * r ** 3} atoms bcc Fe, TECE (configs[4])", cutoff=5.0,
+        dt_fs=1.0, species=[26],
+        structure=lambda: structures.bcc_fe(reps=(r, r, r), seed=0),
+        cfg=lambda a: configs.model_cfg("tece", [26], a),
+        describe=lambda nat: f"bcc Fe {r}^3 box {nat} atoms (configs[4]), TECE E+F, NL rebuilt every step",
+        arch=dict(channels=128, L=2, mmax=2, heads=4, edge_ace_hidden=32, correlation=2, layers=2, cutoff=5.0,
+                  layer_types="cgtp, uv_so2", product="silu_bilineargate"),
+        cpu_slice=lambda: (structures.bcc_fe(reps=(4, 4, 4), seed=1), "bcc Fe slice (4^3 cells)"))
+    return dict(water12k=water, fe101k=fe)
 
 
 def main():
@@ -116,7 +169,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="water12k", choices=["water12k", "fe101k"],
+                    help="water12k: the headline water box (configs[2]); fe101k: TECE on bcc Fe (configs[4])")
     ap.add_argument("--n-side", type=int, default=16, help="water molecules per box edge (16 -> 12,288 atoms)")
+    ap.add_argument("--fe-reps", type=int, default=37, help="bcc cells per box edge (37 -> 101,306 atoms)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="print the per-kernel breakdown to stderr")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -135,21 +191,20 @@ def main():
               "(see DESIGN.md for how the path would shard).", file=sys.stderr)
         sys.exit(2)
 
-    from tace_amd import configs, data, model as pm, ops, structures
+    from tace_amd import data, model as pm, ops
 
+    wl = workloads(args)[args.workload]
     dev = torch.device("cuda:0")
-    box = 49.7 / 16 * args.n_side
-    s = structures.water_box(n_side=args.n_side, box=box, seed=0)
+    s = wl["structure"]()
+    rc = wl["cutoff"]
     nat = len(s["numbers"])
     pos64 = torch.as_tensor(s["positions"], dtype=torch.float64, device=dev)
-    g0 = data.resident_graph(pos64, s["cell"], s["pbc"], torch.zeros(nat, 2, device=dev), 6.0)
+    g0 = data.resident_graph(pos64, s["cell"], s["pbc"], torch.zeros(nat, len(wl["species"]), device=dev), rc)
     E0 = g0["edge_index"].shape[1]
     avg = E0 / nat
+    del g0
 
-    def cfg_fn(a):
-        return configs.model_cfg("water12k", [1, 8], a)
-
-    cfg = cfg_fn(avg)
+    cfg = wl["cfg"](avg)
     torch.manual_seed(0)
     model = pm.create_model(cfg).to(dev)
     model.reset_target_property(["energy", "forces"])
@@ -161,10 +216,10 @@ def main():
     attrs = data.one_hot(s["numbers"], cfg["atomic_numbers"], torch.float32).to(dev)
 
     def step():
-        g = data.resident_graph(pos64, s["cell"], s["pbc"], attrs, 6.0)
+        g = data.resident_graph(pos64, s["cell"], s["pbc"], attrs, rc)
         return model(g)
 
-    log(f"[bench] water box: {nat} atoms, {E0} edges (avg {avg:.1f}), warm-up {args.warmup}")
+    log(f"[bench] {args.workload}: {nat} atoms, {E0} edges (avg {avg:.1f}), warm-up {args.warmup}")
     for _ in range(args.warmup):
         out = step()
     torch.cuda.synchronize()
@@ -188,7 +243,7 @@ def main():
     var = ops.find_variant(key) if key else None
     byts = sum(algorithmic_bytes(name, i, var, 4) for i in infos)
     achieved = byts / (tot_ms * 1e-3) / 1e9
-    traffic = measured_traffic(name)
+    traffic = measured_traffic(args.workload, name)
     roof = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
                 algorithmic_bytes=round(byts / cnt),
@@ -197,16 +252,16 @@ def main():
         for k, (c, t, _) in sorted(summ.items(), key=lambda kv: -kv[1][1]):
             log(f"  {t / args.steps:8.3f} ms/step  {c // args.steps:3d} launches/step  {k}")
 
-    res = dict(metric=METRIC, value=round(nat * args.steps / dt, 1), unit="atom-steps/s", n_gpus=1,
+    res = dict(metric=wl["metric"], value=round(nat * args.steps / dt, 1), unit="atom-steps/s", n_gpus=1,
                steps=args.steps, warmup=args.warmup, ms_per_step=round(ms, 3), higher_is_better=True,
                scaling="weak", vs_baseline=None, dtype="fp32", data="synthetic",
-               config=dict(workload=f"water box {nat} atoms (configs[2]), E+F, NL rebuilt every step",
-                           atoms=nat, edges=int(E0), channels=128, L=3, correlation=3, layers=3, cutoff=6.0,
+               config=dict(workload=wl["describe"](nat), atoms=nat, edges=int(E0), **wl["arch"],
                            parallelism="single GPU"),
-               ns_per_day=round(1e3 / ms * 86400 * DT_FS * 1e-6, 4), roofline=roof)
+               ns_per_day=round(1e3 / ms * 86400 * wl["dt_fs"] * 1e-6, 4), dt_fs=wl["dt_fs"], roofline=roof,
+               peak_mem_gb=round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 1))
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
-        res["cpu_baseline"] = cpu_baseline(cfg_fn)
+        res["cpu_baseline"] = cpu_baseline(wl)
     print(json.dumps(res), flush=True)
 
 

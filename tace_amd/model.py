@@ -436,14 +436,53 @@ class TeceInteraction(torch.nn.Module):
             self.resnetBB = e3nnElementLinear(self.irreps_in, irreps_sc, num_elements, bias=True)
         self.C = C
         self._gate_lay = (GMLayout(self.linear_down.irreps_out), GMLayout(self.gated))
+        # edges per receiver chunk: above this the convolution runs chunk by
+        # chunk and recomputes its per-edge intermediates (~100 KB per edge at
+        # C=128) in the backward instead of keeping them
+        self.chunk_edges = 1 << 18
 
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
-        msg = self.rejector(x, self.edge_info(R), plan, sp.node_map, src, dst, wigner, R)
+        if plan.n_edges <= self.chunk_edges:
+            msg = self.rejector(x, self.edge_info(R), plan, sp.node_map, src, dst, wigner, R)
+        else:
+            msg = self._chunked(x, sp, R, plan, src, dst, wigner)
         m = self.linear_down(msg)
         m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))
         return m, sc
+
+
+    def _chunked(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
+        """The convolution over receiver chunks, each under activation
+        checkpointing; chunk outputs are assembled in node order and moved to
+        the group-major feature-row order."""
+        from torch.utils.checkpoint import checkpoint
+
+        from .tece import receiver_chunks, sub_plan
+        if plan.eid is not None:  # group the edges by receiver first
+            order = plan.eid.long()
+            R, wigner, src, dst = R[order], wigner[order], src[order], dst[order]
+            plan = ops.EdgePlan(plan.n_nodes, plan.n_edges, plan.rowptr, src.to(torch.int32).contiguous(), None)
+        conv, C, L = self.rejector, self.C, self.rejector.lmax
+        x_lc = conv.node_components(x)
+        rows = sp.node_map.long()
+        outs = []
+        for n0, n1, e0, e1 in receiver_chunks(plan, self.chunk_edges):
+            pc = sub_plan(plan, n0, n1, e0, e1)
+            rs, rd, dl = rows[src[e0:e1]], rows[dst[e0:e1]], dst[e0:e1] - n0
+
+            def run(x_lc, R_c, W_c, pc=pc, rs=rs, rd=rd, dl=dl):
+                return conv.edges(x_lc, self.edge_info(R_c), rs, rd, pc, None, dl, W_c, R_c)
+
+            outs.append(checkpoint(run, x_lc, R[e0:e1], wigner[e0:e1], use_reentrant=False))
+        blocks = []
+        for l in range(L + 1):
+            d = 2 * l + 1
+            node_order = torch.cat([o.view(-1)[o.shape[0] * C * l * l:o.shape[0] * C * (l + 1) ** 2]
+                                    .view(o.shape[0], d, C) for o in outs])
+            blocks.append(node_order.index_select(0, sp.perm).reshape(-1))
+        return torch.cat(blocks).view(x.shape[0], -1)
 
 
 class CgtpACE(torch.nn.Module):

@@ -352,7 +352,7 @@ class _EdgeWigner(torch.autograd.Function):
         tok = _t0("edge_wigner_fwd")
         N.check(N.lib().tace_edge_wigner_fwd(N.dtype_code(vec.dtype), vec.data_ptr(), E, lmax, W.data_ptr(),
                                              N.stream_ptr(vec.device)), "tace_edge_wigner_fwd")
-        _t1(tok, (E,))
+        _t1(tok, (E, K))
         ctx.save_for_backward(vec)
         ctx.lmax = lmax
         return W
@@ -365,7 +365,7 @@ class _EdgeWigner(torch.autograd.Function):
         tok = _t0("edge_wigner_bwd")
         N.check(N.lib().tace_edge_wigner_bwd(N.dtype_code(vec.dtype), vec.data_ptr(), gW.data_ptr(), vec.shape[0],
                                              ctx.lmax, gv.data_ptr(), N.stream_ptr(vec.device)), "tace_edge_wigner_bwd")
-        _t1(tok, (vec.shape[0],))
+        _t1(tok, (vec.shape[0], (ctx.lmax + 1) ** 2))
         return gv, None
 
 
@@ -391,7 +391,7 @@ class _TeceScore(torch.autograd.Function):
         N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), q.data_ptr(), k.data_ptr(), rp.data_ptr(),
                                             tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(q.device)),
                 "tace_tece_score_fwd")
-        _t1(tok, (E,))
+        _t1(tok, (E, K, C, H))
         ctx.save_for_backward(q, k, rp, tscale)
         ctx.lmax, ctx.H = lmax, H
         return s
@@ -407,7 +407,7 @@ class _TeceScore(torch.autograd.Function):
                                             tscale.data_ptr(), gs.data_ptr(), E, ctx.lmax, C, ctx.H, gq.data_ptr(),
                                             gk.data_ptr(), grp.data_ptr(), N.stream_ptr(q.device)),
                 "tace_tece_score_bwd")
-        _t1(tok, (E,))
+        _t1(tok, (E, K, C, ctx.H))
         # the attention temperature is a model parameter: no gradient on this
         # (inference) path, as the calculators freeze parameters
         return gq, gk, grp, None, None, None
@@ -431,7 +431,7 @@ class _GraphSoftmax(torch.autograd.Function):
         N.check(N.lib().tace_graph_softmax_fwd(N.dtype_code(s.dtype), s.data_ptr(), plan.rowptr.data_ptr(),
                                                N.ptr(plan.eid), plan.n_nodes, H, a.data_ptr(),
                                                N.stream_ptr(s.device)), "tace_graph_softmax_fwd")
-        _t1(tok, (E,))
+        _t1(tok, (E, H, plan.n_nodes))
         ctx.save_for_backward(a)
         ctx.plan = plan
         return a
@@ -446,7 +446,7 @@ class _GraphSoftmax(torch.autograd.Function):
         N.check(N.lib().tace_graph_softmax_bwd(N.dtype_code(a.dtype), a.data_ptr(), ga.data_ptr(),
                                                plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.n_nodes, a.shape[1],
                                                gs.data_ptr(), N.stream_ptr(a.device)), "tace_graph_softmax_bwd")
-        _t1(tok, (a.shape[0],))
+        _t1(tok, (a.shape[0], a.shape[1], plan.n_nodes))
         return gs, None
 
 
@@ -473,7 +473,7 @@ class _TeceRotateOut(torch.autograd.Function):
                                                  plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map),
                                                  plan.n_nodes, lmax, C, H, out.data_ptr(),
                                                  N.stream_ptr(m.device)), "tace_tece_rotate_out_fwd")
-        _t1(tok, (plan.n_nodes, E, C))
+        _t1(tok, (plan.n_nodes, E, C, K, H))
         ctx.save_for_backward(m, alpha, W, node_map, dst)
         ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
         return out
@@ -490,7 +490,7 @@ class _TeceRotateOut(torch.autograd.Function):
                                                  gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
                                                  N.ptr(node_map), plan.n_nodes, lmax, C, H, gm.data_ptr(),
                                                  ga.data_ptr(), N.stream_ptr(m.device)), "tace_tece_rotate_out_bwd")
-        _t1(tok, (plan.n_nodes, E, C))
+        _t1(tok, (plan.n_nodes, E, C, K, H))
         gW = None
         if ctx.needs_input_grad[2]:
             # gW[e] = (alpha m)[e] g_out[dst e]^T over the channels (batched GEMM)

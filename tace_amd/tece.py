@@ -169,18 +169,21 @@ class TeceConvolution(torch.nn.Module):
         self.temperature_logit = torch.nn.Parameter(
             torch.full((num_head,), math.log((1.0 - self.tmin) / (self.tmax - 1.0))))
 
-    def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):
-        """x_gm: node features, group-major C x (0..lmax) in feature-row order;
-        w: radial weights [E, weight_numel]; node_map[n] = feature row of node
-        n; src/dst: edge endpoints (node ids); wigner [E, K, K] from
-        ``ops.edge_wigner``; R: radial basis [E, num_radial].  Returns the
-        receiver sums, group-major, in feature-row order."""
-        Nn, C, K = x_gm.shape[0], self.C, self.K
-        E = w.shape[0]
-        x_lc = torch.cat([x_gm.view(-1)[Nn * C * l * l:Nn * C * (l + 1) ** 2].view(Nn, 2 * l + 1, C)
+    def node_components(self, x_gm):
+        """Group-major C x (0..lmax) node features -> [rows, (L+1)^2, C] (l layout)."""
+        Nn, C = x_gm.shape[0], self.C
+        return torch.cat([x_gm.view(-1)[Nn * C * l * l:Nn * C * (l + 1) ** 2].view(Nn, 2 * l + 1, C)
                           for l in range(self.lmax + 1)], dim=1)
-        rows = node_map.long()
-        m = torch.bmm(wigner, torch.cat((x_lc.index_select(0, rows[src]), x_lc.index_select(0, rows[dst])), dim=-1))
+
+    def edges(self, x_lc, w, rows_src, rows_dst, plan: ops.EdgePlan, out_map, dst_out, wigner, R):
+        """Messages of the edges of ``plan`` summed per receiver.  x_lc: node
+        features [rows, K, C]; rows_src / rows_dst (int64): feature rows of each
+        edge's sender / receiver; ``plan``: receiver CSR of these edges;
+        ``out_map`` (int32 or None) / ``dst_out``: output row of each receiver /
+        of each edge's receiver.  Returns [plan.n_nodes, K*C] group-major."""
+        C = self.C
+        E = w.shape[0]
+        m = torch.bmm(wigner, torch.cat((x_lc.index_select(0, rows_src), x_lc.index_select(0, rows_dst)), dim=-1))
         key = self.key_proj(m[:, :, :C])
         query = self.query_proj(m[:, :, C:])
         rp = self.radial_proj(R)
@@ -195,4 +198,34 @@ class TeceConvolution(torch.nn.Module):
         g = (torch.sigmoid(gate) * SIGMOID_CST).index_select(1, self.gate_index)
         m = m + g * m + self.ece(m, m2, coefs)
         m = self.linear_down(m)
-        return ops.tece_rotate_out(m, alpha, wigner, plan, node_map, dst, self.lmax, self.H)
+        return ops.tece_rotate_out(m, alpha, wigner, plan, out_map, dst_out, self.lmax, self.H)
+
+    def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):
+        """x_gm: node features, group-major C x (0..lmax) in feature-row order;
+        w: radial weights [E, weight_numel]; node_map[n] = feature row of node
+        n; src/dst: edge endpoints (node ids); wigner [E, K, K] from
+        ``ops.edge_wigner``; R: radial basis [E, num_radial].  Returns the
+        receiver sums, group-major, in feature-row order."""
+        rows = node_map.long()
+        return self.edges(self.node_components(x_gm), w, rows[src], rows[dst], plan, node_map, dst, wigner, R)
+
+
+def receiver_chunks(plan: ops.EdgePlan, max_edges: int):
+    """Receiver ranges [n0, n1) whose in-edges (contiguous in a receiver-grouped
+    edge list) number at most ``max_edges`` (or one receiver, if it alone has
+    more), with their edge ranges [e0, e1)."""
+    rp = plan.rowptr.cpu().tolist()
+    out, n0, N = [], 0, plan.n_nodes
+    while n0 < N:
+        n1 = n0 + 1
+        while n1 < N and rp[n1 + 1] - rp[n0] <= max_edges:
+            n1 += 1
+        out.append((n0, n1, rp[n0], rp[n1]))
+        n0 = n1
+    return out
+
+
+def sub_plan(plan: ops.EdgePlan, n0: int, n1: int, e0: int, e1: int) -> ops.EdgePlan:
+    """Receiver CSR of receivers n0..n1-1 and their edges e0..e1-1 (receiver-grouped edges)."""
+    return ops.EdgePlan(n1 - n0, e1 - e0, (plan.rowptr[n0:n1 + 1] - e0).contiguous(),
+                        plan.src[e0:e1].contiguous(), None)

@@ -283,7 +283,7 @@ def test_tece_convolution_matches_oracle(cuda, dtype, C, H, A):
 BARS = {torch.float64: (1e-10, 1e-8), torch.float32: (1e-5, 1e-4)}
 
 
-def _model_pair(structs, cuda, dtype, seed=0, **over):
+def _model_pair(structs, cuda, dtype, seed=0, chunk_edges=None, **over):
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS["tece"]["cutoff"])
              for s in structs]
     zs = sorted({int(z) for s in structs for z in s["numbers"]})
@@ -305,6 +305,13 @@ def _model_pair(structs, cuda, dtype, seed=0, **over):
                                                   for k, v in ref.state_dict().items()})
     gpu = gpu.to(cuda)
     gpu.reset_target_property(["energy", "forces"])
+    if chunk_edges is not None:
+        n = 0
+        for mod in gpu.modules():
+            if isinstance(mod, pm.TeceInteraction):
+                mod.chunk_edges = chunk_edges
+                n += 1
+        assert n > 0
     got = gpu(data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda))
     return got, want
 
@@ -335,3 +342,14 @@ def test_tece_two_species_batch(cuda, dtype):
     b = dict(b, numbers=nb)
     got, want = _model_pair([a, b], cuda, dtype, seed=4, num_channel=32, edge_ace_hidden=16, num_head=2)
     _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_tece_receiver_chunks(cuda, dtype):
+    """The receiver-chunked convolution (activation checkpointing per chunk, used
+    above 2^18 edges) on chunks of ~700 edges, with the oracle's sender-ordered
+    edge list (edges regrouped by receiver first)."""
+    got, want = _model_pair([structures.bcc_fe(reps=(3, 3, 2), seed=10)], cuda, dtype, seed=2, chunk_edges=700,
+                            num_channel=64, num_head=2)
+    _check(got, want, dtype)
+

@@ -1,0 +1,40 @@
+"""Host-side bookkeeping of the TECE path (CPU): receiver chunking of the
+edge list and the sub-CSR of a chunk."""
+
+import torch
+
+from tace_amd import ops
+from tace_amd.tece import receiver_chunks, sub_plan
+
+
+def _plan(deg):
+    dst = torch.repeat_interleave(torch.arange(len(deg)), deg)
+    src = torch.arange(len(dst)) % len(deg)
+    return ops.EdgePlan.from_edge_index(torch.stack([src, dst]), len(deg)), dst
+
+
+def test_chunks_tile_receivers_and_edges():
+    g = torch.Generator().manual_seed(5)
+    deg = torch.randint(0, 9, (200,), generator=g)
+    deg[17] = 40  # one receiver above the budget on its own
+    deg[100:110] = 0  # receivers without in-edges
+    plan, _ = _plan(deg)
+    ch = receiver_chunks(plan, 25)
+    assert ch[0][0] == 0 and ch[-1][1] == 200 and ch[0][2] == 0 and ch[-1][3] == int(deg.sum())
+    for (a, b, c, d), (a2, b2, c2, d2) in zip(ch, ch[1:]):
+        assert b == a2 and d == c2
+    for a, b, c, d in ch:
+        assert d - c <= 25 or b - a == 1
+        assert d - c == int(deg[a:b].sum())
+    assert any(b - a == 1 and a == 17 for a, b, _, _ in ch)
+
+
+def test_sub_plan_is_the_chunk_csr():
+    deg = torch.tensor([3, 0, 2, 5, 1, 0, 4])
+    plan, dst = _plan(deg)
+    for n0, n1, e0, e1 in receiver_chunks(plan, 6):
+        p = sub_plan(plan, n0, n1, e0, e1)
+        assert p.n_nodes == n1 - n0 and p.n_edges == e1 - e0 and p.eid is None
+        assert p.rowptr.tolist() == [0] + torch.cumsum(deg[n0:n1], 0).tolist()
+        assert torch.equal(p.src, plan.src[e0:e1])
+        assert torch.equal(dst[e0:e1] - n0, torch.repeat_interleave(torch.arange(n1 - n0), deg[n0:n1]))

@@ -83,7 +83,15 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         return s * (E * (K * C + H + K * K) + n * K * C) + 4 * (E + 2 * n + 1)
     if name.startswith("tece_rotate_out_bwd"):
         n, E, C, K, H = info
-        return s * (E * (2 * K * C + 2 * H + K * K) + n * K * C) + 4 * (E + 2 * n + 1)
+        return s * (E * (2 * K * C + 2 * H + 2 * K * K) + n * K * C) + 8 * E
+    if name.startswith("edge_rotate_in_fwd"):
+        E, K, C, has_w = info
+        nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
+        return s * E * (4 * K * C + K * K + (2 * nc * C + 2 * K * C if has_w else 0)) + 16 * E
+    if name.startswith("edge_rotate_in_bwd"):
+        E, K, C, has_w = info
+        nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
+        return s * E * (8 * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
     if name.startswith("edge_basis_fwd"):
         (E,) = info
         return s * E * (3 + 8 + 16)

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 7
+#define TACE_HIP_ABI_VERSION 8
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -134,12 +134,41 @@ int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const
  *                               wigner [E, K, K] (row = m-layout component,
  *                               column = e3nn component); its inverse is the
  *                               transpose.  bwd: g_vec [E, 3] from g_wigner.
+ *   tace_edge_rotate_in_fwd/_bwd
+ *                               gather of [x_src | x_dst], the wigner bmm and
+ *                               the radial weighting (oam_2026_07_05.py:769-780):
+ *                               x [n_rows, K, C] node features (l layout),
+ *                               rows_src / rows_dst (int64) the feature rows of
+ *                               each edge's ends; m = W [x_src | x_dst] is
+ *                               written as m_src = m[:, :, :C], m_dst =
+ *                               m[:, :, C:] ([E, K, C] each) and, given
+ *                               radial_w [E, ncomp, 2C] (ncomp = (lmax+1)
+ *                               (lmax+2)/2 components, shared by the +m and -m
+ *                               rows), m_w = radial_w[comp(r)] m [E, K, 2C].
+ *                               Rows outside [0, n_rows) read as zeros.  bwd
+ *                               (absent output gradients = zero): per-edge
+ *                               g_x_src, g_x_dst [E, K, C] (the caller sums
+ *                               them into the rows), g_wigner [E, K, K] and,
+ *                               if g_radial_w is given, g_radial_w.
  *   tace_tece_score_fwd/_bwd    OAM20260705Convolution._complex_qk_attention
  *                               (_e3nn/archive/oam_2026_07_05.py:699-754): q, k
  *                               [E, K, C] in the m layout with the default
  *                               (lmax+1-m) components per m, radial_proj [E, 2H]
  *                               (bias | phase logits), tscale[H] = attention
- *                               scale x temperature -> score [E, H].
+ *                               scale x temperature -> score [E, H]; the
+ *                               per-head width C/H divides 64 or is a
+ *                               multiple of 64.
+ *   tace_tece_edge_ace_fwd/_bwd gate + complex edge-ACE product
+ *                               (oam_2026_07_05.py:782-790; SO2Gate, and
+ *                               uuuSO2TensorProduct 312-516): out = u + g u +
+ *                               ece(u, v, c) on the stacked SO(2) GEMM
+ *                               outputs, n = lmax+1, A = hidden, P = number of
+ *                               edge-ACE paths: y0 [E, P n A (coef logits) |
+ *                               n A (v, m=0) | n (lmax+1) A (gate logits) |
+ *                               n A (u, m=0)], y_m [2E, n A (v) | n A (u)] for
+ *                               m = 1..lmax (row 2e = +m, 2e+1 = -m); out o0
+ *                               [E, n A], o_m [2E, n A].  Pointers past lmax
+ *                               are ignored.  bwd: g_y* from g_o*.
  *   tace_graph_softmax_fwd/_bwd GraphSoftmax (softmax.py:80-114) over each
  *                               receiver's in-edges (receiver CSR rowptr/eid),
  *                               no rescale: alpha [E, H].
@@ -148,17 +177,31 @@ int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const
  *                               scatter_sum to receivers
  *                               (oam_2026_07_05.py:799-823): m [E, K, C] ->
  *                               out in the group-major layout of C x (0..lmax)
- *                               at rows node_map[n]; bwd gives g_m and g_alpha
- *                               (the wigner gradient is g_m-independent:
- *                               sum_c alpha m g_out, formed by the caller). */
+ *                               at rows node_map[n]; bwd (per edge, dst[e] =
+ *                               receiver node id, int64) gives g_m, g_alpha
+ *                               and g_wigner. */
 int tace_edge_wigner_fwd(int dtype, const void* vec, int64_t n_edges, int32_t lmax, void* wigner, void* stream);
 int tace_edge_wigner_bwd(int dtype, const void* vec, const void* g_wigner, int64_t n_edges, int32_t lmax,
                          void* g_vec, void* stream);
+int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                            const int64_t* rows_dst, const void* radial_w, int64_t n_rows, int64_t n_edges,
+                            int32_t lmax, int32_t channels, void* m_src, void* m_dst, void* m_w, void* stream);
+int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                            const int64_t* rows_dst, const void* radial_w, const void* g_m_src, const void* g_m_dst,
+                            const void* g_m_w, int64_t n_rows, int64_t n_edges, int32_t lmax, int32_t channels,
+                            void* g_x_src, void* g_x_dst, void* g_wigner, void* g_radial_w, void* stream);
 int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
                         int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, void* score, void* stream);
 int tace_tece_score_bwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
                         const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
                         void* g_q, void* g_k, void* g_radial_proj, void* stream);
+int tace_tece_edge_ace_fwd(int dtype, const void* y0, const void* y1, const void* y2, const void* y3,
+                           int64_t n_edges, int32_t lmax, int32_t hidden, void* o0, void* o1, void* o2, void* o3,
+                           void* stream);
+int tace_tece_edge_ace_bwd(int dtype, const void* y0, const void* y1, const void* y2, const void* y3,
+                           const void* g_o0, const void* g_o1, const void* g_o2, const void* g_o3, int64_t n_edges,
+                           int32_t lmax, int32_t hidden, void* g_y0, void* g_y1, void* g_y2, void* g_y3,
+                           void* stream);
 int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, const int32_t* eid, int64_t n_nodes,
                            int32_t heads, void* alpha, void* stream);
 int tace_graph_softmax_bwd(int dtype, const void* alpha, const void* g_alpha, const int32_t* rowptr,
@@ -167,8 +210,9 @@ int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const 
                              const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int32_t lmax,
                              int32_t channels, int32_t heads, void* out, void* stream);
 int tace_tece_rotate_out_bwd(int dtype, const void* m, const void* alpha, const void* wigner, const void* g_out,
-                             const int32_t* rowptr, const int32_t* eid, const int32_t* node_map, int64_t n_nodes,
-                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha, void* stream);
+                             const int64_t* dst, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
+                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha,
+                             void* g_wigner, void* stream);
 
 /* ---- neighbour list (float64 positions, host cell[9] rows = lattice
  * vectors, host pbc[3]).  Edge (src=i, dst=j, S) exists iff

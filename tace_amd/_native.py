@@ -50,8 +50,16 @@ _SIGS = {
     "tace_graph_softmax_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
     "tace_tece_rotate_out_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
                                           _vp, _vp]),
-    "tace_tece_rotate_out_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,
-                                          _c_i32, _vp, _vp, _vp]),
+    "tace_tece_rotate_out_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
+                                          _c_i32, _vp, _vp, _vp, _vp]),
+    "tace_edge_rotate_in_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp, _vp,
+                                         _vp, _vp]),
+    "tace_edge_rotate_in_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
+                                         _c_i32, _vp, _vp, _vp, _vp, _vp]),
+    "tace_tece_edge_ace_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp,
+                                        _vp]),
+    "tace_tece_edge_ace_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,
+                                        _vp, _vp, _vp, _vp, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

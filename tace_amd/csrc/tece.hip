@@ -252,93 +252,535 @@ __global__ __launch_bounds__(64) void k_wigner_bwd(const T* __restrict__ vec, co
   gv[3 * e] = a0; gv[3 * e + 1] = a1; gv[3 * e + 2] = a2;
 }
 
+// ------------------------------------------------------- per-edge wavefronts --
+// The score, rotate-in and rotate-out backward kernels give each edge one
+// wavefront (4 edges per 256-thread workgroup): lane l holds channels
+// c = l + 64 j of slot j, so every feature row of an edge is one coalesced
+// 256-byte (fp32) access and the edge's Wigner matrix is wave-uniform.
+__device__ __forceinline__ int64_t wave_edge() {
+  return (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+
+// Channel slots per lane for `C` channels (a compile-time bound of the loops).
+#define TACE_SLOTS_DISPATCH(C, NS, ...)      \
+  if ((C) <= 64) { constexpr int NS = 1; __VA_ARGS__; }       \
+  else if ((C) <= 128) { constexpr int NS = 2; __VA_ARGS__; } \
+  else if ((C) <= 256) { constexpr int NS = 4; __VA_ARGS__; } \
+  else if ((C) <= 512) { constexpr int NS = 8; __VA_ARGS__; } \
+  else { constexpr int NS = 16; __VA_ARGS__; }
+
+// Sum over the lanes of one head of per-slot values v[0..V): heads of Ch < 64
+// channels (Ch divides 64) are lane groups of one slot; heads of Ch >= 64
+// (a multiple of 64) are whole slots, summed over the wave after their last
+// slot.  `run` carries the partial sums of a wide head across slots.
+// Returns true on the one lane (per head) that holds the total in v.
+template <typename T, int V>
+__device__ __forceinline__ bool head_sum(T* v, T* run, int j, int Ch, int lane) {
+  if (Ch < 64) {
+#pragma unroll
+    for (int i = 0; i < V; ++i)
+      for (int o = Ch >> 1; o > 0; o >>= 1) v[i] += __shfl_xor(v[i], o, 64);
+    return (lane & (Ch - 1)) == 0;
+  }
+#pragma unroll
+  for (int i = 0; i < V; ++i) run[i] += v[i];
+  if (((j + 1) * 64) % Ch) return false;
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    v[i] = wave_sum(run[i]);
+    run[i] = T(0);
+  }
+  return lane == 0;
+}
+
 // -------------------------------------------------------------- QK score --
 // score[e,h] = (S0 + sum_m cos(m phi) A_m + sin(m phi) B_m) * tscale[h] + rp[e,h],
 // phi = pi tanh(rp[e, H+h]);  S0 = sum over the m = 0 rows of q.k,
 // A_m = sum(q_re k_re + q_im k_im), B_m = sum(q_im k_re - q_re k_im) over the
-// +-m rows and the head's Ch channels.  One thread per (edge, head).
-template <typename T>
-__device__ __forceinline__ void rows_of_m(int L, int m, int* re, int* n) {
+// +-m rows (rows re..re+n-1 and re+n..re+2n-1, n = L+1-m) and the head's Ch
+// channels.  Rows of the m layout: m = 0 rows 0..L, then per m the +m and -m rows.
+template <int L>
+__device__ __forceinline__ int m_rows_start(int m) {
   int off = L + 1;
   for (int mm = 1; mm < m; ++mm) off += 2 * (L + 1 - mm);
-  *re = off;
-  *n = L + 1 - m;
+  return off;
 }
 
-template <typename T>
+template <typename T, int L, int NS>
 __global__ __launch_bounds__(256) void k_score_fwd(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ rp, const T* __restrict__ tscale,
-                                                   int64_t E, int L, int C, int H, T* __restrict__ score) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= E * H) return;
-  const int64_t e = t / H;
-  const int h = (int)(t - e * H);
-  const int Ch = C / H, K = (L + 1) * (L + 1);
-  const T* qe = q + e * K * C + h * Ch;
-  const T* ke = k + e * K * C + h * Ch;
-  T s = 0;
-  for (int r = 0; r <= L; ++r)
-    for (int c = 0; c < Ch; ++c) s += qe[r * C + c] * ke[r * C + c];
-  const T phi = T(M_PI) * tanh(rp[e * 2 * H + H + h]);
-  for (int m = 1; m <= L; ++m) {
-    int re, n;
-    rows_of_m<T>(L, m, &re, &n);
-    T A = 0, B = 0;
-    for (int j = 0; j < n; ++j)
-      for (int c = 0; c < Ch; ++c) {
-        const T qr = qe[(re + j) * C + c], qi = qe[(re + n + j) * C + c];
-        const T kr = ke[(re + j) * C + c], ki = ke[(re + n + j) * C + c];
-        A += qr * kr + qi * ki;
-        B += qi * kr - qr * ki;
+                                                   int64_t E, int C, int H, T* __restrict__ score) {
+  constexpr int K = (L + 1) * (L + 1), V = 1 + 2 * L;
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const int Ch = C / H;
+  const T* qe = q + e * K * C;
+  const T* ke = k + e * K * C;
+  T run[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) run[i] = T(0);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (64 * j >= C) break;
+    const int c = lane + 64 * j;
+    T v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = T(0);
+    if (c < C) {
+#pragma unroll
+      for (int r = 0; r <= L; ++r) v[0] += qe[r * C + c] * ke[r * C + c];
+#pragma unroll
+      for (int m = 1; m <= L; ++m) {
+        const int re = m_rows_start<L>(m), n = L + 1 - m;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+          const T qr = qe[(re + i) * C + c], qi = qe[(re + n + i) * C + c];
+          const T kr = ke[(re + i) * C + c], ki = ke[(re + n + i) * C + c];
+          v[2 * m - 1] += qr * kr + qi * ki;
+          v[2 * m] += qi * kr - qr * ki;
+        }
       }
-    s += cos(m * phi) * A + sin(m * phi) * B;
+    }
+    if (head_sum<T, V>(v, run, j, Ch, lane) && c < C) {
+      const int h = c / Ch;
+      const T phi = T(M_PI) * tanh(rp[e * 2 * H + H + h]);
+      T s = v[0];
+#pragma unroll
+      for (int m = 1; m <= L; ++m) s += cos(T(m) * phi) * v[2 * m - 1] + sin(T(m) * phi) * v[2 * m];
+      score[e * H + h] = s * tscale[h] + rp[e * 2 * H + h];
+    }
   }
-  score[t] = s * tscale[h] + rp[e * 2 * H + h];
 }
 
-template <typename T>
+template <typename T, int L, int NS>
 __global__ __launch_bounds__(256) void k_score_bwd(const T* __restrict__ q, const T* __restrict__ k,
                                                    const T* __restrict__ rp, const T* __restrict__ tscale,
-                                                   const T* __restrict__ gs, int64_t E, int L, int C, int H,
+                                                   const T* __restrict__ gs, int64_t E, int C, int H,
                                                    T* __restrict__ gq, T* __restrict__ gk, T* __restrict__ grp) {
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= E * H) return;
-  const int64_t e = t / H;
-  const int h = (int)(t - e * H);
-  const int Ch = C / H, K = (L + 1) * (L + 1);
-  const int64_t base = e * K * C + h * Ch;
-  const T g = gs[t];
-  const T G = g * tscale[h];
-  for (int r = 0; r <= L; ++r)
-    for (int c = 0; c < Ch; ++c) {
-      const int64_t i = base + r * C + c;
-      const T qv = q[i], kv = k[i];
-      gq[i] = G * kv;
-      gk[i] = G * qv;
-    }
-  const T th = tanh(rp[e * 2 * H + H + h]);
-  const T phi = T(M_PI) * th;
-  T dphi = 0;
-  for (int m = 1; m <= L; ++m) {
-    int re, n;
-    rows_of_m<T>(L, m, &re, &n);
-    const T cs = cos(m * phi), sn = sin(m * phi);
-    T A = 0, B = 0;
-    for (int j = 0; j < n; ++j)
-      for (int c = 0; c < Ch; ++c) {
-        const int64_t ir = base + (re + j) * C + c, ii = base + (re + n + j) * C + c;
-        const T qr = q[ir], qi = q[ii], kr = k[ir], ki = k[ii];
-        A += qr * kr + qi * ki;
-        B += qi * kr - qr * ki;
-        gq[ir] = G * (cs * kr - sn * ki);
-        gq[ii] = G * (cs * ki + sn * kr);
-        gk[ir] = G * (cs * qr + sn * qi);
-        gk[ii] = G * (cs * qi - sn * qr);
+  constexpr int K = (L + 1) * (L + 1);
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const int Ch = C / H;
+  const int64_t base = e * K * C;
+  T run[1] = {T(0)};
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (64 * j >= C) break;
+    const int c = lane + 64 * j;
+    const bool act = c < C;
+    const int h = act ? c / Ch : 0;
+    const T g = gs[e * H + h];
+    const T G = g * tscale[h];
+    const T th = tanh(rp[e * 2 * H + H + h]);
+    const T phi = T(M_PI) * th;
+    T d[1] = {T(0)};
+    if (act) {
+#pragma unroll
+      for (int r = 0; r <= L; ++r) {
+        const int64_t i = base + r * C + c;
+        const T qv = q[i], kv = k[i];
+        gq[i] = G * kv;
+        gk[i] = G * qv;
       }
-    dphi += T(m) * (cs * B - sn * A);
+#pragma unroll
+      for (int m = 1; m <= L; ++m) {
+        const int re = m_rows_start<L>(m), n = L + 1 - m;
+        const T cs = cos(T(m) * phi), sn = sin(T(m) * phi);
+        T A = 0, B = 0;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+          const int64_t ir = base + (re + i) * C + c, ii = base + (re + n + i) * C + c;
+          const T qr = q[ir], qi = q[ii], kr = k[ir], ki = k[ii];
+          A += qr * kr + qi * ki;
+          B += qi * kr - qr * ki;
+          gq[ir] = G * (cs * kr - sn * ki);
+          gq[ii] = G * (cs * ki + sn * kr);
+          gk[ir] = G * (cs * qr + sn * qi);
+          gk[ii] = G * (cs * qi - sn * qr);
+        }
+        d[0] += T(m) * (cs * B - sn * A);
+      }
+    }
+    if (head_sum<T, 1>(d, run, j, Ch, lane) && act) {
+      grp[e * 2 * H + h] = g;
+      grp[e * 2 * H + H + h] = G * d[0] * T(M_PI) * (T(1) - th * th);
+    }
   }
-  grp[e * 2 * H + h] = g;
-  grp[e * 2 * H + H + h] = G * dphi * T(M_PI) * (T(1) - th * th);
+}
+
+// ----------------------------------------------------- rotate into the frame --
+// m[e, r, c] = sum_k W[e, r, k] x[row(e, c), k, c mod C] over the 2C channels
+// of [x_src | x_dst]: row = rows_src[e] for c < C, rows_dst[e] otherwise
+// (the gather, concatenation and wigner bmm of oam_2026_07_05.py:769-771).
+// Outputs: ms = m[:, :, :C] and md = m[:, :, C:] (contiguous [E, K, C] each,
+// the key / query projection inputs) and, when radial weights w [E, ncomp, 2C]
+// are given, mw = w[e, comp(r), c] m[e, r, c] ([E, K, 2C], the radial
+// weighting of oam_2026_07_05.py:778-780: +m and -m rows share a component).
+// x: [n_rows, K, C] node features in the l layout; rows outside [0, n_rows)
+// read as zeros.
+template <int L>
+__device__ __forceinline__ int m_comp(int r) {
+  constexpr int n = L + 1;
+  if (r < n) return r;
+  int off = n, coff = n;
+#pragma unroll
+  for (int m = 1; m <= L; ++m) {
+    const int k = n - m;
+    if (r < off + 2 * k) return coff + (r - off < k ? r - off : r - off - k);
+    off += 2 * k;
+    coff += k;
+  }
+  return -1;
+}
+
+template <typename T, int L, int NS>
+__global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, const T* __restrict__ W,
+                                                   const int64_t* __restrict__ rows_src,
+                                                   const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
+                                                   int64_t n_rows, int64_t E, int C, T* __restrict__ ms,
+                                                   T* __restrict__ md, T* __restrict__ mw) {
+  constexpr int K = (L + 1) * (L + 1), NC = (L + 1) * (L + 2) / 2;
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const T* w = W + e * K * K;
+  const int64_t rs = rows_src[e], rd = rows_dst[e];
+  const int C2 = 2 * C;
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (64 * j >= C2) break;
+    const int c = lane + 64 * j;
+    if (c >= C2) continue;
+    const bool src = c < C;
+    const int64_t row = src ? rs : rd;
+    const int cc = src ? c : c - C;
+    T xk[K];
+    const bool ok = row >= 0 && row < n_rows;
+#pragma unroll
+    for (int kk = 0; kk < K; ++kk) xk[kk] = ok ? x[(row * K + kk) * C + cc] : T(0);
+    T* out = src ? ms : md;
+#pragma unroll
+    for (int r = 0; r < K; ++r) {
+      T a = 0;
+#pragma unroll
+      for (int kk = 0; kk < K; ++kk) a += w[r * K + kk] * xk[kk];
+      out[(e * K + r) * C + cc] = a;
+      if (wr) mw[(e * K + r) * C2 + c] = wr[(e * NC + m_comp<L>(r)) * C2 + c] * a;
+    }
+  }
+}
+
+// Sums p[0..P) over the 64 lanes in groups of 16 (reduce16_lanes) and stores
+// the totals at out[0..n).
+template <typename T, int P>
+__device__ __forceinline__ void store_lane_sums(const T* p, int n, T* out, int lane) {
+#pragma unroll
+  for (int g = 0; g < P / 16; ++g) {
+    const T t = reduce16_lanes(p[16 * g], p[16 * g + 1], p[16 * g + 2], p[16 * g + 3], p[16 * g + 4],
+                               p[16 * g + 5], p[16 * g + 6], p[16 * g + 7], p[16 * g + 8], p[16 * g + 9],
+                               p[16 * g + 10], p[16 * g + 11], p[16 * g + 12], p[16 * g + 13], p[16 * g + 14],
+                               p[16 * g + 15]);
+    const int i = 16 * g + rev4(lane);
+    if (lane < 16 && i < n) out[i] = t;
+  }
+}
+
+// backward: with g[e,r,c] = g_ms / g_md [e,r,c mod C] + w[e,comp(r),c] g_mw[e,r,c]
+// (absent gradients count as zero):
+//   g_x_src[e, k, c] = sum_r W[e,r,k] g[e,r,c] (c < C), g_x_dst the same for
+//   channels C..2C-1 (per edge; the caller sums them into the rows);
+//   g_W[e, r, k] = sum over the 2C channels of g[e,r,c] x[row(e,c), k, c];
+//   g_w[e, comp, c] = sum of g_mw[e,r,c] m[e,r,c] over the rows r of comp.
+template <typename T, int L, int NS>
+__global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, const T* __restrict__ W,
+                                                   const int64_t* __restrict__ rows_src,
+                                                   const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
+                                                   const T* __restrict__ gms, const T* __restrict__ gmd,
+                                                   const T* __restrict__ gmw, int64_t n_rows, int64_t E, int C,
+                                                   T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
+                                                   T* __restrict__ gwr) {
+  constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16, NC = (L + 1) * (L + 2) / 2;
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const T* w = W + e * K * K;
+  const int64_t rs = rows_src[e], rd = rows_dst[e];
+  const int C2 = 2 * C;
+  T p[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) p[i] = T(0);
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (64 * j >= C2) break;
+    const int c = lane + 64 * j;
+    if (c < C2) {
+      const bool src = c < C;
+      const int64_t row = src ? rs : rd;
+      const int cc = src ? c : c - C;
+      const bool ok = row >= 0 && row < n_rows;
+      const T* gsd = src ? gms : gmd;
+      T xk[K], g[K];
+#pragma unroll
+      for (int kk = 0; kk < K; ++kk) xk[kk] = ok ? x[(row * K + kk) * C + cc] : T(0);
+#pragma unroll
+      for (int r = 0; r < K; ++r) g[r] = gsd ? gsd[(e * K + r) * C + cc] : T(0);
+      if (gmw) {
+        T gc[NC];
+#pragma unroll
+        for (int q = 0; q < NC; ++q) gc[q] = T(0);
+#pragma unroll
+        for (int r = 0; r < K; ++r) {
+          const T gr = gmw[(e * K + r) * C2 + c];
+          const int q = m_comp<L>(r);
+          g[r] += wr[(e * NC + q) * C2 + c] * gr;
+          T mv = 0;
+#pragma unroll
+          for (int kk = 0; kk < K; ++kk) mv += w[r * K + kk] * xk[kk];
+          gc[q] += gr * mv;
+        }
+        if (gwr) {
+#pragma unroll
+          for (int q = 0; q < NC; ++q) gwr[(e * NC + q) * C2 + c] = gc[q];
+        }
+      }
+      T* gx = src ? gxs : gxd;
+#pragma unroll
+      for (int kk = 0; kk < K; ++kk) {
+        T a = 0;
+#pragma unroll
+        for (int r = 0; r < K; ++r) a += w[r * K + kk] * g[r];
+        gx[(e * K + kk) * C + cc] = a;
+      }
+#pragma unroll
+      for (int r = 0; r < K; ++r)
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) p[r * K + kk] += g[r] * xk[kk];
+    }
+  }
+  store_lane_sums<T, P>(p, K * K, gW + e * K * K, lane);
+}
+
+// ------------------------------------------------------------- edge ACE --
+// Gate + complex edge-ACE product of the SO(2) messages
+// (oam_2026_07_05.py:782-790, SO2Gate gate_m0 and uuuSO2TensorProduct
+// 312-516, mmax = lmax = L, n = L+1 rows per m and sign, A hidden channels):
+//   out = u + g u + ece(u, v, c)
+// u = linear_up features, v = linear_glu features, g = ScaledSigmoid of the
+// linear_up gate rows (row (m, i) of either sign takes gate m n + i), c =
+// ScaledSigmoid of the linear_coefs output (one weight per path, row and
+// channel).  ece: for every m3 the paths (m1 >= m2) with m1 + m2 = m3 ("sum",
+// z = a b) or |m1 - m2| = m3 ("diff", z = a conj(b)), a from u at m1, b from
+// v at m2 (m = 0 features are real), out re/im += z c, scaled by
+// 1/sqrt(#paths of m3); m3 = 0 keeps the real part.
+// Inputs are the stacked GEMM outputs: y0 [E, ncoef | n A (v, m=0) |
+// (n (L+1) + n) A (gates, then u, m=0)] with ncoef = #paths n A, and for
+// m > 0 y_m [2E, n A (v) | n A (u)] (row 2e = +m, 2e+1 = -m).  Outputs o0
+// [E, n A] and o_m [2E, n A].  One thread per (edge, channel).
+#define TACE_ACE_SCST 1.8467055342154763
+
+template <int L>
+struct AcePaths {
+  static constexpr int count(int m3) {
+    int c = 0;
+    for (int m1 = 0; m1 <= L; ++m1)
+      for (int m2 = 0; m2 <= m1; ++m2)
+        if (m1 + m2 == m3 || m1 - m2 == m3) ++c;
+    return c;
+  }
+  static constexpr int total() {
+    int c = 0;
+    for (int m3 = 0; m3 <= L; ++m3) c += count(m3);
+    return c;
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ T scaled_sigmoid(T z) { return T(TACE_ACE_SCST) / (T(1) + exp(-z)); }
+
+template <typename T, int L>
+__global__ __launch_bounds__(256) void k_edge_ace_fwd(const T* __restrict__ y0, const T* __restrict__ y1,
+                                                      const T* __restrict__ y2, const T* __restrict__ y3, int64_t E,
+                                                      int A, T* __restrict__ o0, T* __restrict__ o1,
+                                                      T* __restrict__ o2, T* __restrict__ o3) {
+  constexpr int n = L + 1, NG = n * (L + 1), NP = AcePaths<L>::total();
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= E * A) return;
+  const int64_t e = t / A;
+  const int a = (int)(t - e * A);
+  const T* ym[4] = {y0, y1, y2, y3};
+  T* om[4] = {o0, o1, o2, o3};
+  const int64_t r0 = e * (int64_t)(NP * n * A + n * A + (NG + n) * A);
+  const int cv0 = NP * n * A, cg = cv0 + n * A, cu0 = cg + NG * A;
+  // u, v [m][sign][i]
+  T u[L + 1][2][n], v[L + 1][2][n];
+#pragma unroll
+  for (int i = 0; i < n; ++i) {
+    u[0][0][i] = y0[r0 + cu0 + i * A + a];
+    v[0][0][i] = y0[r0 + cv0 + i * A + a];
+    u[0][1][i] = T(0);
+    v[0][1][i] = T(0);
+  }
+#pragma unroll
+  for (int m = 1; m <= L; ++m)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < n; ++i) {
+        const int64_t r = (2 * e + s) * (int64_t)(2 * n * A);
+        v[m][s][i] = ym[m][r + i * A + a];
+        u[m][s][i] = ym[m][r + n * A + i * A + a];
+      }
+  T re[L + 1][n], im[L + 1][n];
+#pragma unroll
+  for (int m = 0; m <= L; ++m)
+#pragma unroll
+    for (int i = 0; i < n; ++i) re[m][i] = im[m][i] = T(0);
+  int p = 0;
+#pragma unroll
+  for (int m3 = 0; m3 <= L; ++m3)
+#pragma unroll
+    for (int m1 = 0; m1 <= L; ++m1)
+#pragma unroll
+      for (int m2 = 0; m2 <= m1; ++m2) {
+        const bool sum = m1 + m2 == m3;
+        if (!sum && m1 - m2 != m3) continue;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+          const T w = scaled_sigmoid(y0[r0 + (p * n + i) * A + a]);
+          const T ar = u[m1][0][i], ai = u[m1][1][i], br = v[m2][0][i], bi = v[m2][1][i];
+          T zr, zi;
+          if (sum) { zr = ar * br - ai * bi; zi = ar * bi + ai * br; }
+          else { zr = ar * br + ai * bi; zi = ai * br - ar * bi; }
+          re[m3][i] += zr * w;
+          im[m3][i] += zi * w;
+        }
+        ++p;
+      }
+#pragma unroll
+  for (int m3 = 0; m3 <= L; ++m3) {
+    const T sc = T(1) / sqrt(T(AcePaths<L>::count(m3)));
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      const T g = scaled_sigmoid(y0[r0 + cg + (m3 * n + i) * A + a]);
+      if (m3 == 0) {
+        o0[e * (n * A) + i * A + a] = u[0][0][i] * (T(1) + g) + re[0][i] * sc;
+      } else {
+        om[m3][(2 * e) * (n * A) + i * A + a] = u[m3][0][i] * (T(1) + g) + re[m3][i] * sc;
+        om[m3][(2 * e + 1) * (n * A) + i * A + a] = u[m3][1][i] * (T(1) + g) + im[m3][i] * sc;
+      }
+    }
+  }
+}
+
+template <typename T, int L>
+__global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, const T* __restrict__ y1,
+                                                      const T* __restrict__ y2, const T* __restrict__ y3,
+                                                      const T* __restrict__ go0, const T* __restrict__ go1,
+                                                      const T* __restrict__ go2, const T* __restrict__ go3, int64_t E,
+                                                      int A, T* __restrict__ gy0, T* __restrict__ gy1,
+                                                      T* __restrict__ gy2, T* __restrict__ gy3) {
+  constexpr int n = L + 1, NG = n * (L + 1), NP = AcePaths<L>::total();
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= E * A) return;
+  const int64_t e = t / A;
+  const int a = (int)(t - e * A);
+  const T* ym[4] = {y0, y1, y2, y3};
+  const T* gom[4] = {go0, go1, go2, go3};
+  T* gym[4] = {gy0, gy1, gy2, gy3};
+  const int64_t r0 = e * (int64_t)(NP * n * A + n * A + (NG + n) * A);
+  const int cv0 = NP * n * A, cg = cv0 + n * A, cu0 = cg + NG * A;
+  T u[L + 1][2][n], v[L + 1][2][n], go[L + 1][2][n], gu[L + 1][2][n], gv[L + 1][2][n];
+#pragma unroll
+  for (int i = 0; i < n; ++i) {
+    u[0][0][i] = y0[r0 + cu0 + i * A + a];
+    v[0][0][i] = y0[r0 + cv0 + i * A + a];
+    go[0][0][i] = go0[e * (n * A) + i * A + a];
+    u[0][1][i] = v[0][1][i] = go[0][1][i] = T(0);
+  }
+#pragma unroll
+  for (int m = 1; m <= L; ++m)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < n; ++i) {
+        const int64_t r = (2 * e + s) * (int64_t)(2 * n * A);
+        v[m][s][i] = ym[m][r + i * A + a];
+        u[m][s][i] = ym[m][r + n * A + i * A + a];
+        go[m][s][i] = gom[m][(2 * e + s) * (n * A) + i * A + a];
+      }
+  // gate: out = u (1 + g) + ...
+#pragma unroll
+  for (int m = 0; m <= L; ++m)
+#pragma unroll
+    for (int i = 0; i < n; ++i) {
+      const T z = y0[r0 + cg + (m * n + i) * A + a];
+      const T sg = T(1) / (T(1) + exp(-z));
+      const T g = T(TACE_ACE_SCST) * sg;
+      T gz = go[m][0][i] * u[m][0][i];
+      gu[m][0][i] = go[m][0][i] * (T(1) + g);
+      gv[m][0][i] = gv[m][1][i] = T(0);
+      if (m > 0) {
+        gz += go[m][1][i] * u[m][1][i];
+        gu[m][1][i] = go[m][1][i] * (T(1) + g);
+      } else {
+        gu[m][1][i] = T(0);
+      }
+      gy0[r0 + cg + (m * n + i) * A + a] = gz * T(TACE_ACE_SCST) * sg * (T(1) - sg);
+    }
+  int p = 0;
+#pragma unroll
+  for (int m3 = 0; m3 <= L; ++m3) {
+    const T sc = T(1) / sqrt(T(AcePaths<L>::count(m3)));
+#pragma unroll
+    for (int m1 = 0; m1 <= L; ++m1)
+#pragma unroll
+      for (int m2 = 0; m2 <= m1; ++m2) {
+        const bool sum = m1 + m2 == m3;
+        if (!sum && m1 - m2 != m3) continue;
+#pragma unroll
+        for (int i = 0; i < n; ++i) {
+          const T zc = y0[r0 + (p * n + i) * A + a];
+          const T sg = T(1) / (T(1) + exp(-zc));
+          const T w = T(TACE_ACE_SCST) * sg;
+          const T ar = u[m1][0][i], ai = u[m1][1][i], br = v[m2][0][i], bi = v[m2][1][i];
+          T zr, zi;
+          if (sum) { zr = ar * br - ai * bi; zi = ar * bi + ai * br; }
+          else { zr = ar * br + ai * bi; zi = ai * br - ar * bi; }
+          const T Gre = go[m3][0][i] * sc, Gim = m3 > 0 ? go[m3][1][i] * sc : T(0);
+          gy0[r0 + (p * n + i) * A + a] = (Gre * zr + Gim * zi) * T(TACE_ACE_SCST) * sg * (T(1) - sg);
+          const T Gr = Gre * w, Gi = Gim * w;
+          if (sum) {
+            gu[m1][0][i] += Gr * br + Gi * bi;
+            gu[m1][1][i] += Gi * br - Gr * bi;
+            gv[m2][0][i] += Gr * ar + Gi * ai;
+            gv[m2][1][i] += Gi * ar - Gr * ai;
+          } else {
+            gu[m1][0][i] += Gr * br - Gi * bi;
+            gu[m1][1][i] += Gr * bi + Gi * br;
+            gv[m2][0][i] += Gr * ar + Gi * ai;
+            gv[m2][1][i] += Gr * ai - Gi * ar;
+          }
+        }
+        ++p;
+      }
+  }
+#pragma unroll
+  for (int i = 0; i < n; ++i) {
+    gy0[r0 + cu0 + i * A + a] = gu[0][0][i];
+    gy0[r0 + cv0 + i * A + a] = gv[0][0][i];
+  }
+#pragma unroll
+  for (int m = 1; m <= L; ++m)
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < n; ++i) {
+        const int64_t r = (2 * e + s) * (int64_t)(2 * n * A);
+        gym[m][r + i * A + a] = gv[m][s][i];
+        gym[m][r + n * A + i * A + a] = gu[m][s][i];
+      }
 }
 
 // ------------------------------------------------------------ graph softmax --
@@ -424,66 +866,63 @@ __global__ __launch_bounds__(512) void k_rotout_fwd(const T* __restrict__ m, con
   }
 }
 
-// backward: t[r] = sum_k W[e,r,k] g[dst,k,c];  g_m[e,r,c] = alpha t[r];
-// g_alpha[e,h] = sum over the head's channels and rows of m[e,r,c] t[r]
-// (lane reduction over Ch = 16/32/64 lanes, fixed order).
-template <typename T, int L>
-__global__ __launch_bounds__(512) void k_rotout_bwd(const T* __restrict__ m, const T* __restrict__ alpha,
+// backward, one wavefront per edge (n = map[dst[e]] or dst[e]):
+//   t[r] = sum_k W[e,r,k] g[n,k,c];  g_m[e,r,c] = alpha[e,h(c)] t[r];
+//   g_alpha[e,h] = sum over the head's channels and rows of m[e,r,c] t[r];
+//   g_W[e,r,k] = sum_c alpha[e,h(c)] m[e,r,c] g[n,k,c].
+template <typename T, int L, int NS>
+__global__ __launch_bounds__(256) void k_rotout_bwd(const T* __restrict__ m, const T* __restrict__ alpha,
                                                     const T* __restrict__ W, const T* __restrict__ gout,
-                                                    const int* __restrict__ rowptr, const int* __restrict__ eid,
-                                                    const int* __restrict__ map, int N, int C, int H,
-                                                    T* __restrict__ gm, T* __restrict__ galpha) {
-  constexpr int K = (L + 1) * (L + 1);
-  const int n0 = blockIdx.x;
-  const int c = threadIdx.x;
-  if (n0 >= N) return;
-  const bool act = c < C;
-  const int cc = act ? c : C - 1;
-  const int Ch = C / H, h = cc / Ch;
-  const int n = map ? map[n0] : n0;
+                                                    const int64_t* __restrict__ dst, const int* __restrict__ map,
+                                                    int N, int64_t E, int C, int H, T* __restrict__ gm,
+                                                    T* __restrict__ galpha, T* __restrict__ gW) {
+  constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16;
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const int Ch = C / H;
+  const int64_t n0 = dst[e];
+  const bool okn = n0 >= 0 && n0 < N;
+  const int64_t n = okn ? (map ? (int64_t)map[n0] : n0) : 0;
   const int64_t NN = N;
-  T g[K];
+  const T* w = W + e * K * K;
+  T p[P];
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    int l = 0;
-    while ((l + 1) * (l + 1) <= k) ++l;
-    const int j = k - l * l;
-    g[k] = act ? gout[NN * C * l * l + ((int64_t)n * (2 * l + 1) + j) * C + cc] : T(0);
-  }
-  for (int i = rowptr[n0]; i < rowptr[n0 + 1]; ++i) {
-    const int64_t e = eid ? eid[i] : i;
+  for (int i = 0; i < P; ++i) p[i] = T(0);
+  T run[1] = {T(0)};
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    if (64 * j >= C) break;
+    const int c = lane + 64 * j;
+    const bool act = c < C;
+    const int h = act ? c / Ch : 0;
     const T a = alpha[e * H + h];
-    const T* w = W + e * K * K;
-    const T* me = m + e * K * C + cc;
-    T p = 0;
+    T g[K];
 #pragma unroll
-    for (int r = 0; r < K; ++r) {
-      T t = 0;
-#pragma unroll
-      for (int k = 0; k < K; ++k) t += w[r * K + k] * g[k];
-      if (act) gm[e * K * C + (int64_t)r * C + c] = a * t;
-      p += me[(int64_t)r * C] * t;
+    for (int kk = 0; kk < K; ++kk) {
+      int l = 0;
+      while ((l + 1) * (l + 1) <= kk) ++l;
+      const int jj = kk - l * l;
+      g[kk] = act && okn ? gout[NN * C * l * l + (n * (2 * l + 1) + jj) * C + c] : T(0);
     }
-    // sum p over the Ch lanes of the head (Ch divides 64 or is a multiple of 64)
-    const int width = Ch < 64 ? Ch : 64;
-    for (int o = width >> 1; o > 0; o >>= 1) p += __shfl_xor(p, o, 64);
-    if (Ch <= 64) {
-      if ((c & (width - 1)) == 0 && act) galpha[e * H + h] = p;
-    } else {
-      // heads wider than a wavefront: partial sums of the head's wavefronts go
-      // through LDS in a fixed order
-      __shared__ T part[16];
-      const int wv = c >> 6, nw = (C + 63) >> 6;
-      __syncthreads();
-      if ((c & 63) == 0) part[wv] = p;
-      __syncthreads();
-      if (act && (c % Ch) == 0) {
-        T s = 0;
-        for (int q = c >> 6; q < ((c + Ch) >> 6) && q < nw; ++q) s += part[q];
-        galpha[e * H + h] = s;
+    T v[1] = {T(0)};
+    if (act) {
+#pragma unroll
+      for (int r = 0; r < K; ++r) {
+        T t = 0;
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) t += w[r * K + kk] * g[kk];
+        const T mv = m[(e * K + r) * C + c];
+        gm[(e * K + r) * C + c] = a * t;
+        v[0] += mv * t;
+        const T am = a * mv;
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) p[r * K + kk] += am * g[kk];
       }
     }
+    if (head_sum<T, 1>(v, run, j, Ch, lane) && act) galpha[e * H + h] = v[0];
   }
+  store_lane_sums<T, P>(p, K * K, gW + e * K * K, lane);
 }
 
 // ------------------------------------------------------------------ C ABI --
@@ -528,13 +967,17 @@ int tace_edge_wigner_bwd(int dtype, const void* vec, const void* g_wigner, int64
 }
 
 static int score_checks(const char* who, int64_t E, int32_t lmax, int32_t C, int32_t H) {
-  char msg[128];
-  if (E < 0 || lmax < 1 || lmax > 3 || C <= 0 || H <= 0 || C % H) {
-    snprintf(msg, sizeof(msg), "%s: bad sizes (lmax 1..3, channels divisible by heads)", who);
+  char msg[160];
+  if (E < 0 || lmax < 1 || lmax > 3 || C <= 0 || C > TACE_MAX_CHANNELS || H <= 0 || C % H ||
+      (C / H < 64 ? 64 % (C / H) : (C / H) % 64)) {
+    snprintf(msg, sizeof(msg), "%s: bad sizes (lmax 1..3, channels <= %d, divisible by heads; per-head width a "
+             "divisor or a multiple of 64)", who, TACE_MAX_CHANNELS);
     return tace_fail_msg(msg);
   }
   return 0;
 }
+
+static dim3 wave_grid(int64_t E) { return dim3((unsigned)((E + 3) / 4)); }
 
 int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
                         int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, void* score, void* stream) {
@@ -542,16 +985,19 @@ int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* rad
   if (n_edges == 0) return 0;
   if (!q || !k || !radial_proj || !tscale || !score) return tace_fail_msg("tace_tece_score_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 g((unsigned)((n_edges * heads + 255) / 256)), b(256);
-  if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_score_fwd<float>, g, b, 0, s, (const float*)q, (const float*)k, (const float*)radial_proj,
-                       (const float*)tscale, n_edges, lmax, channels, heads, (float*)score);
-  else if (dtype == TACE_F64)
-    hipLaunchKernelGGL(k_score_fwd<double>, g, b, 0, s, (const double*)q, (const double*)k,
-                       (const double*)radial_proj, (const double*)tscale, n_edges, lmax, channels, heads,
-                       (double*)score);
-  else
+  const dim3 g = wave_grid(n_edges), b(256);
+#define SC_F(TT, LL)                                                                                            \
+  TACE_SLOTS_DISPATCH(channels, NS,                                                                             \
+    hipLaunchKernelGGL((k_score_fwd<TT, LL, NS>), g, b, 0, s, (const TT*)q, (const TT*)k, (const TT*)radial_proj, \
+                       (const TT*)tscale, n_edges, channels, heads, (TT*)score))
+  if (dtype == TACE_F32) {
+    if (lmax == 1) { SC_F(float, 1) } else if (lmax == 2) { SC_F(float, 2) } else { SC_F(float, 3) }
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) { SC_F(double, 1) } else if (lmax == 2) { SC_F(double, 2) } else { SC_F(double, 3) }
+  } else {
     return tace_fail_msg("tace_tece_score_fwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef SC_F
   return tace_check_launch("tace_tece_score_fwd");
 }
 
@@ -563,18 +1009,82 @@ int tace_tece_score_bwd(int dtype, const void* q, const void* k, const void* rad
   if (!q || !k || !radial_proj || !tscale || !g_score || !g_q || !g_k || !g_radial_proj)
     return tace_fail_msg("tace_tece_score_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 g((unsigned)((n_edges * heads + 255) / 256)), b(256);
-  if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_score_bwd<float>, g, b, 0, s, (const float*)q, (const float*)k, (const float*)radial_proj,
-                       (const float*)tscale, (const float*)g_score, n_edges, lmax, channels, heads, (float*)g_q,
-                       (float*)g_k, (float*)g_radial_proj);
-  else if (dtype == TACE_F64)
-    hipLaunchKernelGGL(k_score_bwd<double>, g, b, 0, s, (const double*)q, (const double*)k,
-                       (const double*)radial_proj, (const double*)tscale, (const double*)g_score, n_edges, lmax,
-                       channels, heads, (double*)g_q, (double*)g_k, (double*)g_radial_proj);
-  else
+  const dim3 g = wave_grid(n_edges), b(256);
+#define SC_B(TT, LL)                                                                                            \
+  TACE_SLOTS_DISPATCH(channels, NS,                                                                             \
+    hipLaunchKernelGGL((k_score_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)q, (const TT*)k, (const TT*)radial_proj, \
+                       (const TT*)tscale, (const TT*)g_score, n_edges, channels, heads, (TT*)g_q, (TT*)g_k,      \
+                       (TT*)g_radial_proj))
+  if (dtype == TACE_F32) {
+    if (lmax == 1) { SC_B(float, 1) } else if (lmax == 2) { SC_B(float, 2) } else { SC_B(float, 3) }
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) { SC_B(double, 1) } else if (lmax == 2) { SC_B(double, 2) } else { SC_B(double, 3) }
+  } else {
     return tace_fail_msg("tace_tece_score_bwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef SC_B
   return tace_check_launch("tace_tece_score_bwd");
+}
+
+static int rotin_checks(const char* who, int64_t n_rows, int64_t E, int32_t lmax, int32_t C) {
+  char msg[128];
+  if (n_rows < 0 || E < 0 || lmax < 1 || lmax > 3 || C <= 0 || C > TACE_MAX_CHANNELS) {
+    snprintf(msg, sizeof(msg), "%s: bad sizes (lmax 1..3, channels 1..%d)", who, TACE_MAX_CHANNELS);
+    return tace_fail_msg(msg);
+  }
+  return 0;
+}
+
+int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                            const int64_t* rows_dst, const void* radial_w, int64_t n_rows, int64_t n_edges,
+                            int32_t lmax, int32_t channels, void* m_src, void* m_dst, void* m_w, void* stream) {
+  if (rotin_checks("tace_edge_rotate_in_fwd", n_rows, n_edges, lmax, channels)) return -1;
+  if (n_edges == 0) return 0;
+  if (!x || !wigner || !rows_src || !rows_dst || !m_src || !m_dst || (radial_w && !m_w))
+    return tace_fail_msg("tace_edge_rotate_in_fwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g = wave_grid(n_edges), b(256);
+#define RI_F(TT, LL)                                                                                        \
+  TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                     \
+    hipLaunchKernelGGL((k_rotin_fwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,   \
+                       rows_dst, (const TT*)radial_w, n_rows, n_edges, channels, (TT*)m_src, (TT*)m_dst,   \
+                       (TT*)m_w))
+  if (dtype == TACE_F32) {
+    if (lmax == 1) { RI_F(float, 1) } else if (lmax == 2) { RI_F(float, 2) } else { RI_F(float, 3) }
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) { RI_F(double, 1) } else if (lmax == 2) { RI_F(double, 2) } else { RI_F(double, 3) }
+  } else {
+    return tace_fail_msg("tace_edge_rotate_in_fwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef RI_F
+  return tace_check_launch("tace_edge_rotate_in_fwd");
+}
+
+int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                            const int64_t* rows_dst, const void* radial_w, const void* g_m_src, const void* g_m_dst,
+                            const void* g_m_w, int64_t n_rows, int64_t n_edges, int32_t lmax, int32_t channels,
+                            void* g_x_src, void* g_x_dst, void* g_wigner, void* g_radial_w, void* stream) {
+  if (rotin_checks("tace_edge_rotate_in_bwd", n_rows, n_edges, lmax, channels)) return -1;
+  if (n_edges == 0) return 0;
+  if (!x || !wigner || !rows_src || !rows_dst || !g_x_src || !g_x_dst || !g_wigner || (g_m_w && !radial_w))
+    return tace_fail_msg("tace_edge_rotate_in_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g = wave_grid(n_edges), b(256);
+#define RI_B(TT, LL)                                                                                          \
+  TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                       \
+    hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,     \
+                       rows_dst, (const TT*)radial_w, (const TT*)g_m_src, (const TT*)g_m_dst,                \
+                       (const TT*)g_m_w, n_rows, n_edges, channels, (TT*)g_x_src, (TT*)g_x_dst,              \
+                       (TT*)g_wigner, (TT*)g_radial_w))
+  if (dtype == TACE_F32) {
+    if (lmax == 1) { RI_B(float, 1) } else if (lmax == 2) { RI_B(float, 2) } else { RI_B(float, 3) }
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) { RI_B(double, 1) } else if (lmax == 2) { RI_B(double, 2) } else { RI_B(double, 3) }
+  } else {
+    return tace_fail_msg("tace_edge_rotate_in_bwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef RI_B
+  return tace_check_launch("tace_edge_rotate_in_bwd");
 }
 
 int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, const int32_t* eid, int64_t n_nodes,
@@ -647,25 +1157,85 @@ int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const 
 }
 
 int tace_tece_rotate_out_bwd(int dtype, const void* m, const void* alpha, const void* wigner, const void* g_out,
-                             const int32_t* rowptr, const int32_t* eid, const int32_t* node_map, int64_t n_nodes,
-                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha, void* stream) {
+                             const int64_t* dst, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
+                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha,
+                             void* g_wigner, void* stream) {
   if (rotout_checks("tace_tece_rotate_out_bwd", n_nodes, lmax, channels, heads)) return -1;
-  if (n_nodes == 0) return 0;
-  if (!rowptr || !g_out) return tace_fail_msg("tace_tece_rotate_out_bwd: null pointer");
+  if (n_edges < 0) return tace_fail_msg("tace_tece_rotate_out_bwd: negative edge count");
+  if (n_edges == 0) return 0;
+  if (!m || !alpha || !wigner || !g_out || !dst || !g_m || !g_alpha || !g_wigner)
+    return tace_fail_msg("tace_tece_rotate_out_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  const dim3 g((unsigned)n_nodes), b((unsigned)((channels + 63) / 64 * 64));
-#define ROT_B(TT, LL)                                                                                              \
-  hipLaunchKernelGGL((k_rotout_bwd<TT, LL>), g, b, 0, s, (const TT*)m, (const TT*)alpha, (const TT*)wigner,         \
-                     (const TT*)g_out, rowptr, eid, node_map, (int)n_nodes, channels, heads, (TT*)g_m, (TT*)g_alpha)
+  const dim3 g = wave_grid(n_edges), b(256);
+#define ROT_B(TT, LL)                                                                                          \
+  TACE_SLOTS_DISPATCH(channels, NS,                                                                            \
+    hipLaunchKernelGGL((k_rotout_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)m, (const TT*)alpha,                \
+                       (const TT*)wigner, (const TT*)g_out, dst, node_map, (int)n_nodes, n_edges, channels,   \
+                       heads, (TT*)g_m, (TT*)g_alpha, (TT*)g_wigner))
   if (dtype == TACE_F32) {
-    if (lmax == 1) ROT_B(float, 1); else if (lmax == 2) ROT_B(float, 2); else ROT_B(float, 3);
+    if (lmax == 1) { ROT_B(float, 1) } else if (lmax == 2) { ROT_B(float, 2) } else { ROT_B(float, 3) }
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) ROT_B(double, 1); else if (lmax == 2) ROT_B(double, 2); else ROT_B(double, 3);
+    if (lmax == 1) { ROT_B(double, 1) } else if (lmax == 2) { ROT_B(double, 2) } else { ROT_B(double, 3) }
   } else {
     return tace_fail_msg("tace_tece_rotate_out_bwd: dtype must be TACE_F32 or TACE_F64");
   }
 #undef ROT_B
   return tace_check_launch("tace_tece_rotate_out_bwd");
+}
+
+int tace_tece_edge_ace_fwd(int dtype, const void* y0, const void* y1, const void* y2, const void* y3,
+                           int64_t n_edges, int32_t lmax, int32_t hidden, void* o0, void* o1, void* o2, void* o3,
+                           void* stream) {
+  if (n_edges < 0 || lmax < 1 || lmax > 3 || hidden <= 0)
+    return tace_fail_msg("tace_tece_edge_ace_fwd: bad sizes (lmax 1..3)");
+  if (n_edges == 0) return 0;
+  const void* ys[4] = {y0, y1, y2, y3};
+  void* os[4] = {o0, o1, o2, o3};
+  for (int m = 0; m <= lmax; ++m)
+    if (!ys[m] || !os[m]) return tace_fail_msg("tace_tece_edge_ace_fwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g((unsigned)((n_edges * hidden + 255) / 256)), b(256);
+#define ACE_F(TT, LL)                                                                                           \
+  hipLaunchKernelGGL((k_edge_ace_fwd<TT, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,        \
+                     (const TT*)y3, n_edges, hidden, (TT*)o0, (TT*)o1, (TT*)o2, (TT*)o3)
+  if (dtype == TACE_F32) {
+    if (lmax == 1) ACE_F(float, 1); else if (lmax == 2) ACE_F(float, 2); else ACE_F(float, 3);
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) ACE_F(double, 1); else if (lmax == 2) ACE_F(double, 2); else ACE_F(double, 3);
+  } else {
+    return tace_fail_msg("tace_tece_edge_ace_fwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef ACE_F
+  return tace_check_launch("tace_tece_edge_ace_fwd");
+}
+
+int tace_tece_edge_ace_bwd(int dtype, const void* y0, const void* y1, const void* y2, const void* y3,
+                           const void* g_o0, const void* g_o1, const void* g_o2, const void* g_o3, int64_t n_edges,
+                           int32_t lmax, int32_t hidden, void* g_y0, void* g_y1, void* g_y2, void* g_y3,
+                           void* stream) {
+  if (n_edges < 0 || lmax < 1 || lmax > 3 || hidden <= 0)
+    return tace_fail_msg("tace_tece_edge_ace_bwd: bad sizes (lmax 1..3)");
+  if (n_edges == 0) return 0;
+  const void* ys[4] = {y0, y1, y2, y3};
+  const void* gos[4] = {g_o0, g_o1, g_o2, g_o3};
+  void* gys[4] = {g_y0, g_y1, g_y2, g_y3};
+  for (int m = 0; m <= lmax; ++m)
+    if (!ys[m] || !gos[m] || !gys[m]) return tace_fail_msg("tace_tece_edge_ace_bwd: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g((unsigned)((n_edges * hidden + 255) / 256)), b(256);
+#define ACE_B(TT, LL)                                                                                           \
+  hipLaunchKernelGGL((k_edge_ace_bwd<TT, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,        \
+                     (const TT*)y3, (const TT*)g_o0, (const TT*)g_o1, (const TT*)g_o2, (const TT*)g_o3, n_edges, \
+                     hidden, (TT*)g_y0, (TT*)g_y1, (TT*)g_y2, (TT*)g_y3)
+  if (dtype == TACE_F32) {
+    if (lmax == 1) ACE_B(float, 1); else if (lmax == 2) ACE_B(float, 2); else ACE_B(float, 3);
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) ACE_B(double, 1); else if (lmax == 2) ACE_B(double, 2); else ACE_B(double, 3);
+  } else {
+    return tace_fail_msg("tace_tece_edge_ace_bwd: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef ACE_B
+  return tace_check_launch("tace_tece_edge_ace_bwd");
 }
 
 }  // extern "C"

@@ -15,7 +15,7 @@ raises if the native library is missing -- there is no CPU path.
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Optional, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -484,30 +484,149 @@ class _TeceRotateOut(torch.autograd.Function):
         plan, lmax, H = ctx.plan, ctx.lmax, ctx.H
         E, K, C = m.shape
         gout = gout.contiguous()
-        gm, ga = torch.empty_like(m), torch.empty_like(alpha)
+        gm, ga, gW = torch.empty_like(m), torch.empty_like(alpha), torch.empty_like(W)
         tok = _t0("tece_rotate_out_bwd")
         N.check(N.lib().tace_tece_rotate_out_bwd(N.dtype_code(m.dtype), m.data_ptr(), alpha.data_ptr(), W.data_ptr(),
-                                                 gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
-                                                 N.ptr(node_map), plan.n_nodes, lmax, C, H, gm.data_ptr(),
-                                                 ga.data_ptr(), N.stream_ptr(m.device)), "tace_tece_rotate_out_bwd")
+                                                 gout.data_ptr(), dst.data_ptr(), N.ptr(node_map), plan.n_nodes, E,
+                                                 lmax, C, H, gm.data_ptr(), ga.data_ptr(), gW.data_ptr(),
+                                                 N.stream_ptr(m.device)), "tace_tece_rotate_out_bwd")
         _t1(tok, (plan.n_nodes, E, C, K, H))
-        gW = None
-        if ctx.needs_input_grad[2]:
-            # gW[e] = (alpha m)[e] g_out[dst e]^T over the channels (batched GEMM)
-            rows = dst if node_map is None else node_map.long()[dst]
-            Nn = plan.n_nodes
-            g_lc = torch.cat([gout.view(-1)[Nn * C * l * l:Nn * C * (l + 1) ** 2].view(Nn, 2 * l + 1, C)
-                              for l in range(lmax + 1)], dim=1)
-            am = (m.view(E, K, H, C // H) * alpha.view(E, 1, H, 1)).view(E, K, C)
-            gW = torch.bmm(am, g_lc.index_select(0, rows).transpose(1, 2).contiguous())
         return gm, ga, gW, None, None, None, None, None
 
 
 def tece_rotate_out(m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, heads: int) -> torch.Tensor:
     """sum_{e -> n} W[e]^T (alpha[e] m[e]) per receiver n, in the group-major
     layout of C x (0..lmax) at rows node_map[n] ([N, K*C])."""
-    return _TeceRotateOut.apply(m.contiguous(), alpha.contiguous(), W.contiguous(), plan, node_map, dst.long(),
+    dst = dst.long().contiguous()
+    if dst.shape != (plan.n_edges,):
+        raise ValueError(f"tece_rotate_out: dst has shape {tuple(dst.shape)}, expected ({plan.n_edges},)")
+    return _TeceRotateOut.apply(m.contiguous(), alpha.contiguous(), W.contiguous(), plan, node_map, dst,
                                 int(lmax), int(heads))
+
+
+class _EdgeRotateIn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W, wr, rows_src, rows_dst, lmax: int):
+        Nr, K, C = x.shape
+        E = W.shape[0]
+        dt = x.dtype
+        if K != (lmax + 1) ** 2:
+            raise ValueError(f"edge_rotate_in: {K} components, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
+        nc = (lmax + 1) * (lmax + 2) // 2
+        _req(x, "x", dt, (Nr, K, C))
+        _req(W, "wigner", dt, (E, K, K))
+        if wr is not None:
+            _req(wr, "radial_w", dt, (E, nc * 2 * C))
+        _req(rows_src, "rows_src", torch.int64, (E,))
+        _req(rows_dst, "rows_dst", torch.int64, (E,))
+        ms = torch.empty(E, K, C, dtype=dt, device=x.device)
+        md = torch.empty_like(ms)
+        mw = torch.empty(E, K, 2 * C, dtype=dt, device=x.device) if wr is not None else None
+        tok = _t0("edge_rotate_in_fwd")
+        N.check(N.lib().tace_edge_rotate_in_fwd(N.dtype_code(dt), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
+                                                rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C, ms.data_ptr(),
+                                                md.data_ptr(), N.ptr(mw), N.stream_ptr(x.device)),
+                "tace_edge_rotate_in_fwd")
+        _t1(tok, (E, K, C, wr is not None))
+        ctx.save_for_backward(x, W, wr, rows_src, rows_dst)
+        ctx.lmax = lmax
+        ctx.set_materialize_grads(False)
+        return (ms, md, mw) if wr is not None else (ms, md)
+
+    @staticmethod
+    def backward(ctx, gms, gmd, gmw=None):
+        x, W, wr, rows_src, rows_dst = ctx.saved_tensors
+        Nr, K, C = x.shape
+        E = W.shape[0]
+        gms = gms.contiguous() if gms is not None else None
+        gmd = gmd.contiguous() if gmd is not None else None
+        gmw = gmw.contiguous() if gmw is not None else None
+        gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
+        gxd = torch.empty_like(gxs)
+        gW = torch.empty_like(W)
+        gwr = torch.zeros_like(wr) if wr is not None and ctx.needs_input_grad[2] else None
+        if gwr is not None and gmw is not None:
+            gwr = torch.empty_like(wr)
+        tok = _t0("edge_rotate_in_bwd")
+        N.check(N.lib().tace_edge_rotate_in_bwd(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(),
+                                                rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr), N.ptr(gms),
+                                                N.ptr(gmd), N.ptr(gmw), Nr, E, ctx.lmax, C, gxs.data_ptr(),
+                                                gxd.data_ptr(), gW.data_ptr(),
+                                                N.ptr(gwr) if gmw is not None else 0,
+                                                N.stream_ptr(x.device)), "tace_edge_rotate_in_bwd")
+        _t1(tok, (E, K, C, gmw is not None))
+        gx = None
+        if ctx.needs_input_grad[0]:
+            gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
+        return gx, gW, gwr, None, None, None
+
+
+def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, rows_dst: torch.Tensor, lmax: int,
+                   radial_w: Optional[torch.Tensor] = None):
+    """Edge-frame messages m = W[e] @ [x[rows_src[e]] | x[rows_dst[e]]] for node
+    features x [rows, K, C] (l layout), returned as (m_src, m_dst) = (m[..., :C],
+    m[..., C:]) and, with radial weights [E, ncomp * 2C], also m_w = the
+    radially weighted m [E, K, 2C] (+m and -m rows share a weight component)."""
+    return _EdgeRotateIn.apply(x.contiguous(), W.contiguous(), None if radial_w is None else radial_w.contiguous(),
+                               rows_src.long().contiguous(), rows_dst.long().contiguous(), int(lmax))
+
+
+def edge_ace_paths(lmax: int) -> List[Tuple[int, int, int, bool]]:
+    """(m3, m1, m2, is_sum) of the complex edge-ACE product in weight order."""
+    out = []
+    for m3 in range(lmax + 1):
+        for m1 in range(lmax + 1):
+            for m2 in range(m1 + 1):
+                if m1 + m2 == m3:
+                    out.append((m3, m1, m2, True))
+                elif m1 - m2 == m3:
+                    out.append((m3, m1, m2, False))
+    return out
+
+
+class _EdgeAce(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, lmax: int, A: int, *ys):
+        n = lmax + 1
+        y0 = ys[0]
+        E = y0.shape[0]
+        dt = y0.dtype
+        P = len(edge_ace_paths(lmax))
+        _req(y0, "y0", dt, (E, P * n * A + n * A + (n * (lmax + 1) + n) * A))
+        for m in range(1, lmax + 1):
+            _req(ys[m], f"y{m}", dt, (2 * E, 2 * n * A))
+        outs = [torch.empty(E if m == 0 else 2 * E, n * A, dtype=dt, device=y0.device) for m in range(lmax + 1)]
+        pad = lambda lst: [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
+        tok = _t0("tece_edge_ace_fwd")
+        N.check(N.lib().tace_tece_edge_ace_fwd(N.dtype_code(dt), *pad(list(ys)), E, lmax, A, *pad(outs),
+                                               N.stream_ptr(y0.device)), "tace_tece_edge_ace_fwd")
+        _t1(tok, (E, A, lmax))
+        ctx.save_for_backward(*ys)
+        ctx.lmax, ctx.A = lmax, A
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *gos):
+        ys = ctx.saved_tensors
+        lmax, A = ctx.lmax, ctx.A
+        E = ys[0].shape[0]
+        gos = [g.contiguous() if g is not None else torch.zeros(E if m == 0 else 2 * E, (lmax + 1) * A,
+                                                                 dtype=ys[0].dtype, device=ys[0].device)
+               for m, g in enumerate(gos)]
+        gys = [torch.empty_like(y) for y in ys]
+        pad = lambda lst: [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
+        tok = _t0("tece_edge_ace_bwd")
+        N.check(N.lib().tace_tece_edge_ace_bwd(N.dtype_code(ys[0].dtype), *pad(list(ys)), *pad(gos), E, lmax, A,
+                                               *pad(gys), N.stream_ptr(ys[0].device)), "tace_tece_edge_ace_bwd")
+        _t1(tok, (E, A, lmax))
+        return (None, None) + tuple(gys)
+
+
+def tece_edge_ace(ys: Sequence[torch.Tensor], lmax: int, hidden: int) -> Tuple[torch.Tensor, ...]:
+    """Gate + complex edge-ACE product on the stacked SO(2) GEMM outputs (block
+    layouts of ``include/tace_hip.h``): returns the per-m blocks (o0 [E, n*A],
+    o_m [2E, n*A])."""
+    return _EdgeAce.apply(int(lmax), int(hidden), *[y.contiguous() for y in ys])
 
 
 def to_grouped(x: torch.Tensor, ls: Sequence[int], C: int) -> torch.Tensor:

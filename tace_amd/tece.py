@@ -5,10 +5,12 @@ reference's ``OAM20260705Convolution`` with the flags of
 ``OAM20260705Interaction`` (``tace/models/_e3nn/archive/oam_2026_07_05.py:547-823``,
 ``tace/models/_e3nn/inter.py:440-519``: SO(2) linears of type "w1",
 temperature, edge-ACE, graph softmax, radial phase, gate_m0).  The edge
-frames, the rotary QK score, the graph softmax and the attention-weighted
-inverse rotation + receiver sum run on the HIP kernels of ``csrc/tece.hip``;
-the SO(2) linears are dense GEMMs (hipBLASLt through torch).  Node features
-come and go in the model's group-major, species-sorted layout.
+frames, the gather + rotation into the edge frame with the radial weighting,
+the rotary QK score, the graph softmax, the gate + complex edge-ACE product
+and the attention-weighted inverse rotation + receiver sum run on the HIP
+kernels of ``csrc/tece.hip``; the SO(2) linears are dense GEMMs (hipBLASLt
+through torch), those sharing an input stacked into one GEMM per m.  Node
+features come and go in the model's group-major, species-sorted layout.
 """
 
 from __future__ import annotations
@@ -19,9 +21,6 @@ from typing import List, Optional
 import torch
 
 from . import ops
-
-SIGMOID_CST = 1.8467055342154763  # ScaledSigmoid (tace/models/mlp.py:40-46)
-
 
 class torchLinear(torch.nn.Module):
     """``torchLinear`` (``tace/models/linear.py:210-244``): y = x (W/sqrt(in))^T + b,
@@ -61,75 +60,17 @@ class uvSO2Linear(torch.nn.Module):
             uvSO2MLinear(cin, cout, self.nin[m], self.nout[m]) for m in range(1, mmax + 1))
 
     def forward(self, x):
+        # every block is one 2-D GEMM over (edge[, +-m]) rows: the row slices
+        # are made contiguous first (a strided 3-D operand would make torch
+        # fall back to one tiny GEMM per edge)
         E = x.shape[0]
         outs = [self.m0_rlinear(x[:, :self.nin[0]].reshape(E, -1)).view(E, self.nout[0], self.cout)]
         off = self.nin[0]
         for m in range(1, self.mmax + 1):
             n = self.nin[m]
-            y = self.ms_clinear[m - 1].fc(x[:, off:off + 2 * n].reshape(E, 2, n * self.cin))
+            xm = x[:, off:off + 2 * n].contiguous().view(E * 2, n * self.cin)
             off += 2 * n
-            outs.append(y.view(E, 2 * self.nout[m], self.cout))
-        return torch.cat(outs, dim=1)
-
-
-def _expand(mmax: int, lmax: int, full: bool) -> torch.Tensor:
-    idx, off = [], 0
-    for m in range(mmax + 1):
-        n = lmax + 1 if full else lmax + 1 - m
-        r = list(range(off, off + n))
-        idx += r + (r if m > 0 else [])
-        off += n
-    return torch.tensor(idx, dtype=torch.long)
-
-
-class ComplexProductBasis(torch.nn.Module):
-    """SO(2) edge-ACE complex product with per-edge weights, m1 >= m2
-    (``uuuSO2TensorProduct``, ``oam_2026_07_05.py:312-544``); no parameters."""
-
-    def __init__(self, mmax: int, lmax: int, C: int):
-        super().__init__()
-        self.mmax, self.n, self.C = mmax, lmax + 1, C
-        self.paths = []
-        for m3 in range(mmax + 1):
-            ps = []
-            for m1 in range(mmax + 1):
-                for m2 in range(mmax + 1):
-                    if m1 >= m2:
-                        if m1 + m2 == m3:
-                            ps.append((m1, m2, "sum"))
-                        elif abs(m1 - m2) == m3:
-                            ps.append((m1, m2, "diff"))
-            self.paths.append(ps)
-        self.weight_numel = sum(len(p) for p in self.paths) * self.n * C
-
-    def forward(self, x, y, ws):
-        E, n, C = x.shape[0], self.n, self.C
-        xs = [x[:, :n]] + [x[:, n + 2 * n * (m - 1):n + 2 * n * m].view(E, 2, n, C) for m in range(1, self.mmax + 1)]
-        ys = [y[:, :n]] + [y[:, n + 2 * n * (m - 1):n + 2 * n * m].view(E, 2, n, C) for m in range(1, self.mmax + 1)]
-        woff, outs = 0, []
-        for m3, ps in enumerate(self.paths):
-            re = im = None
-            for (m1, m2, mode) in ps:
-                w = ws[:, woff:woff + n * C].view(E, n, C)
-                woff += n * C
-                a, b = xs[m1], ys[m2]
-                if m1 == 0 and m2 == 0:
-                    zr, zi = a * b, None
-                elif m2 == 0:
-                    zr, zi = a[:, 0] * b, a[:, 1] * b
-                else:
-                    ar, ai, br, bi = a[:, 0], a[:, 1], b[:, 0], b[:, 1]
-                    if mode == "sum":
-                        zr, zi = ar * br - ai * bi, ar * bi + ai * br
-                    else:
-                        zr, zi = ar * br + ai * bi, ai * br - ar * bi
-                re = zr * w if re is None else re + zr * w
-                if m3 > 0:
-                    im = zi * w if im is None else im + zi * w
-            s = 1.0 / math.sqrt(len(ps))
-            outs.append(re * s)
-            if m3 > 0:
-                outs.append(im * s)
+            outs.append(self.ms_clinear[m - 1].fc(xm).view(E, 2 * self.nout[m], self.cout))
         return torch.cat(outs, dim=1)
 
 
@@ -142,22 +83,21 @@ class TeceConvolution(torch.nn.Module):
             raise NotImplementedError("TECE on the MI355X path needs mmax == lmax (the config-5 setting)")
         if C % num_head:
             raise ValueError("channels must be divisible by num_head")
-        self.mmax, self.lmax, self.C, self.H = mmax, lmax, C, num_head
+        self.mmax, self.lmax, self.C, self.H, self.A = mmax, lmax, C, num_head, edge_ace_hidden
         self.Ch = C // num_head
         n = lmax + 1
         A = edge_ace_hidden
         self.K = n * n
         self.num_components = sum(n - m for m in range(mmax + 1))
         self.weight_numel = self.num_components * C * 2
-        self.register_buffer("expand_index", _expand(mmax, lmax, False), persistent=False)
-        self.register_buffer("gate_index", _expand(mmax, lmax, True), persistent=False)
         self.num_gates = n * (mmax + 1)
         self.rows_full = n + 2 * n * mmax
         full = [n] * (mmax + 1)
         self.linear_up = uvSO2Linear(mmax, lmax, 2 * C, A, nout=[self.num_gates + n] + [n] * mmax)
         self.linear_glu = uvSO2Linear(mmax, lmax, 2 * C, A, nout=full)
-        self.ece = ComplexProductBasis(mmax, lmax, A)
-        self.linear_coefs = uvSO2Linear(0, lmax, 2 * C, 1, nout=[self.ece.weight_numel])
+        # one edge-ACE weight per path, row and hidden channel (uuuSO2TensorProduct)
+        self.ece_weight_numel = len(ops.edge_ace_paths(lmax)) * n * A
+        self.linear_coefs = uvSO2Linear(0, lmax, 2 * C, 1, nout=[self.ece_weight_numel])
         self.linear_down = uvSO2Linear(mmax, lmax, A, C, nin=full)
         self.query_proj = uvSO2Linear(mmax, lmax, C, C)
         self.key_proj = uvSO2Linear(mmax, lmax, C, C)
@@ -168,6 +108,38 @@ class TeceConvolution(torch.nn.Module):
         self.tmin, self.tmax = 0.25, 4.0
         self.temperature_logit = torch.nn.Parameter(
             torch.full((num_head,), math.log((1.0 - self.tmin) / (self.tmax - 1.0))))
+
+    def _shared_input_gemms(self, m):
+        """linear_coefs, linear_glu and linear_up of the radially weighted
+        messages m [E, K, 2C]: one GEMM per m block with the three weights
+        stacked.  Returns the block outputs y0 [E, coef | glu | up] and, per
+        m > 0, y_m [2E, glu | up] (the edge-ACE kernel's input layout)."""
+        E, n = m.shape[0], self.lmax + 1
+        lc, lg, lu = self.linear_coefs, self.linear_glu, self.linear_up
+        f0 = [lc.m0_rlinear, lg.m0_rlinear, lu.m0_rlinear]
+        W0 = torch.cat([f.weight * f.alpha for f in f0])
+        b0 = torch.cat([f.bias for f in f0])
+        ys = [torch.nn.functional.linear(m[:, :n].reshape(E, -1), W0, b0)]
+        off = n
+        for mm in range(1, self.mmax + 1):
+            k = n - mm
+            xm = m[:, off:off + 2 * k].contiguous().view(2 * E, -1)
+            off += 2 * k
+            fg, fu = lg.ms_clinear[mm - 1].fc, lu.ms_clinear[mm - 1].fc
+            ys.append(torch.nn.functional.linear(xm, torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha])))
+        return ys
+
+    def _linear_down_blocks(self, o):
+        """linear_down on the edge-ACE output blocks (o0 [E, n*A], o_m [2E, n*A])
+        -> [E, K, C] in the m layout."""
+        ld = self.linear_down
+        E = o[0].shape[0]
+        f = ld.m0_rlinear
+        outs = [torch.nn.functional.linear(o[0], f.weight * f.alpha, f.bias).view(E, ld.nout[0], ld.cout)]
+        for mm in range(1, self.mmax + 1):
+            fc = ld.ms_clinear[mm - 1].fc
+            outs.append(torch.nn.functional.linear(o[mm], fc.weight * fc.alpha).view(E, 2 * ld.nout[mm], ld.cout))
+        return torch.cat(outs, dim=1)
 
     def node_components(self, x_gm):
         """Group-major C x (0..lmax) node features -> [rows, (L+1)^2, C] (l layout)."""
@@ -181,23 +153,15 @@ class TeceConvolution(torch.nn.Module):
         edge's sender / receiver; ``plan``: receiver CSR of these edges;
         ``out_map`` (int32 or None) / ``dst_out``: output row of each receiver /
         of each edge's receiver.  Returns [plan.n_nodes, K*C] group-major."""
-        C = self.C
-        E = w.shape[0]
-        m = torch.bmm(wigner, torch.cat((x_lc.index_select(0, rows_src), x_lc.index_select(0, rows_dst)), dim=-1))
-        key = self.key_proj(m[:, :, :C])
-        query = self.query_proj(m[:, :, C:])
+        ms, md, m = ops.edge_rotate_in(x_lc, wigner, rows_src, rows_dst, self.lmax, w)
+        key = self.key_proj(ms)
+        query = self.query_proj(md)
         rp = self.radial_proj(R)
         T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
         score = ops.tece_score(query, key, rp, (T * self.attention_scale).detach(), self.lmax, self.H)
         alpha = ops.graph_softmax(score, plan)
-        m = w.view(E, self.num_components, 2 * C).index_select(1, self.expand_index) * m
-        coefs = torch.sigmoid(self.linear_coefs(m).squeeze(-1)) * SIGMOID_CST
-        m2 = self.linear_glu(m)
-        mu = self.linear_up(m)
-        gate, m = mu[:, :self.num_gates], mu[:, self.num_gates:self.num_gates + self.rows_full]
-        g = (torch.sigmoid(gate) * SIGMOID_CST).index_select(1, self.gate_index)
-        m = m + g * m + self.ece(m, m2, coefs)
-        m = self.linear_down(m)
+        o = ops.tece_edge_ace(self._shared_input_gemms(m), self.lmax, self.A)
+        m = self._linear_down_blocks(o)
         return ops.tece_rotate_out(m, alpha, wigner, plan, out_map, dst_out, self.lmax, self.H)
 
     def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):

@@ -97,7 +97,8 @@ def test_edge_wigner_matches_oracle(cuda, dtype, lmax):
 
 # ---------------------------------------------------------------- score ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (2, 2, 32), (1, 1, 16), (3, 4, 64)])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (2, 2, 32), (1, 1, 16), (3, 4, 64), (2, 1, 128), (2, 2, 512),
+                                      (2, 8, 256)])
 def test_tece_score_matches_oracle(cuda, dtype, lmax, H, C):
     g = torch.Generator().manual_seed(lmax * 100 + H * 10 + C)
     torch.manual_seed(0)
@@ -185,6 +186,109 @@ def test_rotate_out_matches_oracle(cuda, dtype, lmax, H, C):
     close(gm, gm_o, dtype, "grad m")
     close(ga, ga_o, dtype, "grad alpha")
     close(gW, gW_o, dtype, "grad W")
+
+
+# ----------------------------------------------------------- rotate in ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 32), (2, 48), (3, 64), (2, 512)])
+def test_rotate_in_matches_oracle(cuda, dtype, lmax, C):
+    """W[e] @ [x[src] | x[dst]] (the gather + wigner bmm of the convolution)."""
+    g = torch.Generator().manual_seed(lmax * 1000 + C)
+    N, E = 90, 700
+    K = (lmax + 1) ** 2
+    ei = _random_graph(N, E, g)
+    x = torch.randn(N, K, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    W_o, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W_o = W_o.to(dtype).double().requires_grad_(True)
+    rows = torch.randperm(N, generator=g)
+    m_o = torch.bmm(W_o, torch.cat((x[rows[ei[0]]], x[rows[ei[1]]]), dim=-1))
+    gm = torch.randn(m_o.shape, generator=g, dtype=torch.float64)
+    gx_o, gW_o = torch.autograd.grad((m_o * gm).sum(), [x, W_o])
+    a, w = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, W_o))
+    rs, rd = rows[ei[0]].to(cuda), rows[ei[1]].to(cuda)
+    ms, md = ops.edge_rotate_in(a, w, rs, rd, lmax)
+    m = torch.cat((ms, md), dim=-1)
+    close(m, m_o, dtype, "m")
+    gx, gW = torch.autograd.grad((m * gm.to(dtype).to(cuda)).sum(), [a, w])
+    close(gx, gx_o, dtype, "grad x")
+    close(gW, gW_o, dtype, "grad W")
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 32), (3, 64)])
+def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
+    """The three outputs (src half, dst half, radially weighted) and their gradients."""
+    g = torch.Generator().manual_seed(lmax * 100 + C + 7)
+    N, E = 70, 500
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    ei = _random_graph(N, E, g)
+    x = torch.randn(N, K, C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    wr = torch.randn(E, nc * 2 * C, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    W_o, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W_o = W_o.to(dtype).double().requires_grad_(True)
+    m = torch.bmm(W_o, torch.cat((x[ei[0]], x[ei[1]]), dim=-1))
+    mw_o = wr.view(E, nc, 2 * C).index_select(1, ot.so2_expand(lmax, lmax, False)) * m
+    gs, gd, gw = (torch.randn(t.shape, generator=g, dtype=torch.float64) for t in (m[..., :C], m[..., C:], mw_o))
+    loss = (m[..., :C] * gs).sum() + (m[..., C:] * gd).sum() + (mw_o * gw).sum()
+    gx_o, gW_o, gwr_o = torch.autograd.grad(loss, [x, W_o, wr])
+    a, w, r = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, W_o, wr))
+    ms, md, mw = ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda), lmax, r)
+    close(ms, m[..., :C], dtype, "m_src")
+    close(md, m[..., C:], dtype, "m_dst")
+    close(mw, mw_o, dtype, "m_w")
+    dv = lambda t: t.to(dtype).to(cuda)
+    loss = (ms * dv(gs)).sum() + (md * dv(gd)).sum() + (mw * dv(gw)).sum()
+    gx, gW, gwr = torch.autograd.grad(loss, [a, w, r])
+    close(gx, gx_o, dtype, "grad x")
+    close(gW, gW_o, dtype, "grad W")
+    close(gwr, gwr_o, dtype, "grad radial w")
+    # only the weighted output used: the src/dst gradients are absent
+    ms, md, mw = ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda), lmax, r)
+    gx2, = torch.autograd.grad((mw * dv(gw)).sum(), [a])
+    m = torch.bmm(W_o, torch.cat((x[ei[0]], x[ei[1]]), dim=-1))
+    mw_o = wr.view(E, nc, 2 * C).index_select(1, ot.so2_expand(lmax, lmax, False)) * m
+    gx2_o, = torch.autograd.grad((mw_o * gw).sum(), [x])
+    close(gx2, gx2_o, dtype, "grad x (weighted only)")
+
+
+# ------------------------------------------------------------- edge ACE ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,A", [(2, 32), (1, 16), (3, 8), (2, 20)])
+def test_edge_ace_matches_oracle(cuda, dtype, lmax, A):
+    """Gate + complex edge-ACE product on the stacked GEMM-output blocks."""
+    g = torch.Generator().manual_seed(lmax * 10 + A)
+    E, n = 300, lmax + 1
+    ng, P = n * (lmax + 1), len(ops.edge_ace_paths(lmax))
+    ece = ot.ComplexProduct(lmax, lmax, A)
+    assert ece.weight_numel == P * n * A
+    ys = [torch.randn(E, P * n * A + n * A + (ng + n) * A, generator=g, dtype=torch.float64)]
+    ys += [torch.randn(2 * E, 2 * n * A, generator=g, dtype=torch.float64) for _ in range(lmax)]
+    ys = [y.to(dtype).double().requires_grad_(True) for y in ys]
+    y0 = ys[0]
+    c0 = P * n * A
+    coefs = y0[:, :c0]
+    v = [y0[:, c0:c0 + n * A].reshape(E, n, A)]
+    gate = y0[:, c0 + n * A:c0 + n * A + ng * A].reshape(E, ng, A)
+    u = [y0[:, c0 + n * A + ng * A:].reshape(E, n, A)]
+    for m in range(1, lmax + 1):
+        b = ys[m].reshape(E, 2, 2, n, A)
+        v.append(b[:, :, 0].reshape(E, 2 * n, A))
+        u.append(b[:, :, 1].reshape(E, 2 * n, A))
+    u, v = torch.cat(u, 1), torch.cat(v, 1)
+    gt = ot.scaled_sigmoid(gate).index_select(1, ot.so2_expand(lmax, lmax, True))
+    out = u + gt * u + ece(u, v, ot.scaled_sigmoid(coefs))
+    want = [out[:, :n].reshape(E, n * A)]
+    for m in range(1, lmax + 1):
+        want.append(out[:, n + 2 * n * (m - 1):n + 2 * n * m].reshape(2 * E, n * A))
+    gos = [torch.randn(w.shape, generator=g, dtype=torch.float64) for w in want]
+    grads_o = torch.autograd.grad(sum((w * go).sum() for w, go in zip(want, gos)), ys)
+    yg = [y.detach().to(dtype).to(cuda).requires_grad_(True) for y in ys]
+    got = ops.tece_edge_ace(yg, lmax, A)
+    for m in range(lmax + 1):
+        close(got[m], want[m], dtype, f"o{m}")
+    grads = torch.autograd.grad(sum((o * go.to(dtype).to(cuda)).sum() for o, go in zip(got, gos)), yg)
+    for m in range(lmax + 1):
+        close(grads[m], grads_o[m], dtype, f"grad y{m}")
 
 
 # ------------------------------------------------------- weighted uuu ----

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 8
+#define TACE_HIP_ABI_VERSION 9
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -91,10 +91,11 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
 
 /* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
- * w [N, npath*C] (NULL = unweighted) scales path p of channel u by
- * w[n, p*C + u] -- the trainable (bilinear-gate) product of
- * _e3nn/prod.py:126-147 / fused.py:17-95; the backward then also writes
- * gw [N, npath*C].
+ * Weighted variants (the bilinear-gate products, second operand = hidden
+ * irreps + one 0e block) take w [N, npath*C], which scales path p of channel
+ * u by w[n, p*C + u] -- the trainable product of _e3nn/prod.py:126-147 /
+ * fused.py:17-95 -- and their backward also writes gw [N, npath*C]; all
+ * other variants take w = NULL.  A mismatch is an error.
  * layout flags select the group-major layout for x1 (and g1), out (and
  * gout) and x2 (and g2).  Accepted: 0, OUT_GROUPED, IN1_GROUPED|OUT_GROUPED,
  * IN1_GROUPED|OUT_GROUPED|IN2_GROUPED. */
@@ -124,6 +125,23 @@ int tace_edge_vec_fwd(int dtype, const void* pos, const void* lattice, const int
                       const void* shifts, const int32_t* edge_graph, int64_t n_edges, void* vec, void* stream);
 int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const int32_t* eid,
                       const int32_t* s_rowptr, const int32_t* s_slot, int64_t n_nodes, void* g_pos, void* stream);
+
+/* ---- radial MLP hidden layers (tace/models/mlp.py:136-191): h_0 = radial
+ * [E, n_in], h_l = silu(h_(l-1) W_l) for l = 1..n_layers, every hidden width
+ * TACE_MLP_WIDTH; the last (wide, linear) layer of the MLP is a GEMM left to
+ * the caller.  weights: the n_layers matrices packed row-major
+ * [n_in x 64 | 64 x 64 | ...] with their scale folded in.  Outputs are
+ * feature-major: h_t [64, E] (the last hidden activations) and the saved
+ * pre-activations z_t [n_layers, 64, E] that the backward reads.
+ *   tace_radial_mlp_bwd: g_radial [E, n_in] from g_h_t [64, E] (weights are
+ *   constants: no weight gradient). */
+#define TACE_MLP_WIDTH 64
+#define TACE_MLP_MAX_IN 32
+#define TACE_MLP_MAX_LAYERS 4
+int tace_radial_mlp_fwd(int dtype, const void* radial, int64_t n_edges, int32_t n_in, int32_t n_layers,
+                        const void* weights, void* h_t, void* z_t, void* stream);
+int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h_t, int64_t n_edges, int32_t n_in,
+                        int32_t n_layers, const void* weights, void* g_radial, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"

@@ -60,6 +60,8 @@ _SIGS = {
                                         _vp]),
     "tace_tece_edge_ace_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,
                                         _vp, _vp, _vp, _vp, _vp]),
+    "tace_radial_mlp_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp]),
+    "tace_radial_mlp_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

@@ -50,9 +50,12 @@ def variant_key(kind: str, in1: Sequence[int], in2: Sequence[int], out: Sequence
 
 
 class Variant:
-    def __init__(self, kind: str, in1: Sequence[int], in2: Sequence[int], out: Sequence[int]):
+    def __init__(self, kind: str, in1: Sequence[int], in2: Sequence[int], out: Sequence[int],
+                 weighted: bool = False):
         assert kind in ("uvu", "uuu")
+        assert not weighted or kind == "uuu"
         self.kind = kind
+        self.weighted = weighted  # uuu with per-node path weights (bilinear gate)
         self.in1, self.in2, self.out = list(in1), list(in2), list(out)
         self.key = variant_key(kind, in1, in2, out)
         i1 = _irreps_from_ls(in1, 2)
@@ -394,16 +397,18 @@ class Variant:
         for bb, d in enumerate(self.d2):
             for m in range(d):
                 L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
-        # per-node path weights w [N, P*C] (trainable / bilinear-gate form), or none
-        L.append(f"  const T* __restrict__ wn = w ? w + n * {P} * (size_t)C + u : nullptr;")
+        # weighted variants: per-node path weights w [N, P*C] (bilinear gate)
+        if self.weighted:
+            L.append(f"  const T* __restrict__ wn = w + n * {P} * (size_t)C + u;")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
-            L.append(f"  {{ const T wp = wn ? wn[(size_t){p} * C] : T(1);")
+            L.append(f"  {{ const T wp = {f'wn[(size_t){p} * C]' if self.weighted else 'T(1)'};")
             for k in range(d):
                 terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
                 e3, gm = self._addr("out", p, k)
-                L.append(f"    out[OUT_GM ? ({gm}) : ({e3})] = wp * ({' + '.join(terms) if terms else 'T(0)'});")
+                val = f"({' + '.join(terms) if terms else 'T(0)'})"
+                L.append(f"    out[OUT_GM ? ({gm}) : ({e3})] = {'wp * ' + val if self.weighted else val};")
             L.append("  }")
         L.append("}")
         return "\n".join(L)
@@ -427,25 +432,30 @@ class Variant:
             for m in range(d):
                 L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
                 L.append(f"  T hy{bb}_{m} = T(0);")
-        L.append(f"  const size_t wo = n * {P} * (size_t)C + u;")
+        if self.weighted:
+            L.append(f"  const size_t wo = n * {P} * (size_t)C + u;")
         for p in range(P):
             b1, b2 = self.path_blocks[p]
             d = self.dout[p]
             L.append("  {")
             for k in range(d):
                 L.append(f"    const T o{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
-            # grad of the weight: sum_k gout_k t_k with t the unweighted path output
-            L.append("    if (gw) {")
-            tsum = []
-            for k in range(d):
-                terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
-                if terms:
-                    tsum.append(f"o{k} * ({' + '.join(terms)})")
-            L.append(f"      gw[wo + (size_t){p} * C] = {' + '.join(tsum) if tsum else 'T(0)'};")
-            L.append("    }")
-            L.append(f"    const T wp = w ? w[wo + (size_t){p} * C] : T(1);")
-            for k in range(d):
-                L.append(f"    const T g{k} = wp * o{k};")
+            if self.weighted:
+                # grad of the weight: sum_k gout_k t_k with t the unweighted path output
+                L.append("    if (gw) {")
+                tsum = []
+                for k in range(d):
+                    terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
+                    if terms:
+                        tsum.append(f"o{k} * ({' + '.join(terms)})")
+                L.append(f"      gw[wo + (size_t){p} * C] = {' + '.join(tsum) if tsum else 'T(0)'};")
+                L.append("    }")
+                L.append(f"    const T wp = w[wo + (size_t){p} * C];")
+                for k in range(d):
+                    L.append(f"    const T g{k} = wp * o{k};")
+            else:
+                for k in range(d):
+                    L.append(f"    const T g{k} = o{k};")
             for (i, j, k, c) in self.cg[p]:
                 L.append(f"    hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * g{k});")
                 L.append(f"    hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * g{k});")
@@ -489,7 +499,7 @@ def model_variants(Lmax: int, lmax: int, correlation: int, bilinear: bool = Fals
                 out = [0] if last else list(range(Lmax + 1))
             else:
                 out = list(range(lmax + 1))
-            v = Variant("uuu", in1, base, out)
+            v = Variant("uuu", in1, base, out, weighted=bilinear)
             vs.append(v)
             in1 = [l3 for (_, _, l3) in v.path_l]
     return vs
@@ -674,6 +684,7 @@ def emit_all(gen_dir: str) -> List[str]:
     reg = [hdr, "#pragma once", *_TYPEDEFS,
            "struct TpVariant {",
            "  const char* key; int kind; int npath; int d1; int d2; int dout;",
+           "  int weighted;                   // uuu: per-node path weights required",
            "  int nparts;                     // uvu: part kernels per launch = grad_y partials",
            "  int nseg; int seg[8][2];        // group-major grad-x row segments (offset / C, length / C)",
            "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
@@ -691,7 +702,8 @@ def emit_all(gen_dir: str) -> List[str]:
         segs = v.row_segments() if v.kind == "uvu" else []
         assert len(segs) <= 8
         seg = "{" + ", ".join(f"{{{a}, {b}}}" for a, b in segs + [(0, 0)] * (8 - len(segs))) + "}"
-        head = f"\"{v.key}\", {0 if v.kind == 'uvu' else 1}, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}"
+        head = (f"\"{v.key}\", {0 if v.kind == 'uvu' else 1}, {len(v.paths)}, {v.D1}, {v.D2}, {v.DO}, "
+                f"{int(v.weighted)}")
         if v.kind == "uvu":
             reg.append(f"  {{{head}, {len(v.parts())}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
                        f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")

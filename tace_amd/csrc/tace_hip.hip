@@ -600,6 +600,9 @@ int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void*
   if (n_nodes && (!x1 || !x2 || !out)) return fail("tace_uuu_fwd: null pointer");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_fwd: too many nodes");
   const TpVariant& v = kVariants[vid];
+  if (n_nodes && v.weighted != (w != nullptr))
+    return fail(v.weighted ? "tace_uuu_fwd: this product is weighted: w is required"
+                           : "tace_uuu_fwd: this product has no path weights: w must be null");
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
     v.ufwd_f(x1, x2, w, out, (int)n_nodes, channels, layout, s);
@@ -616,9 +619,12 @@ int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void*
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
   if (!uuu_layout_ok(layout)) return fail("tace_uuu_bwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
   if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
-  if (n_nodes && w && !gw) return fail("tace_uuu_bwd: weighted products need gw");
   if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_bwd: too many nodes");
   const TpVariant& v = kVariants[vid];
+  if (n_nodes && v.weighted != (w != nullptr))
+    return fail(v.weighted ? "tace_uuu_bwd: this product is weighted: w is required"
+                           : "tace_uuu_bwd: this product has no path weights: w must be null");
+  if (n_nodes && w && !gw) return fail("tace_uuu_bwd: weighted products need gw");
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
     v.ubwd_f(x1, x2, w, gout, g1, g2, w ? gw : nullptr, (int)n_nodes, channels, layout, s);

@@ -252,7 +252,10 @@ class mlpLinear(torch.nn.Module):
 
 
 class MLP(torch.nn.Module):
-    """Radial MLP (``mlp.py:136-191``): alpha = gain/sqrt(h_in), SiLU between layers."""
+    """Radial MLP (``mlp.py:136-191``): alpha = gain/sqrt(h_in), SiLU between
+    layers.  Width-64 hidden layers run in one HIP kernel per direction
+    (``ops.radial_mlp_hidden``, the weights as constants: the inference path
+    freezes parameters); the wide last layer is a GEMM."""
 
     def __init__(self, dims):
         super().__init__()
@@ -262,9 +265,16 @@ class MLP(torch.nn.Module):
             if layer != len(dims) - 2:
                 mods.append(torch.nn.SiLU())
         self.mlp = torch.nn.Sequential(*mods)
+        self.fused = len(dims) >= 3 and all(h == 64 for h in dims[1:-1]) and dims[0] <= 32 and len(dims) - 2 <= 4
 
     def forward(self, x):
-        return self.mlp(x)
+        if not self.fused:
+            return self.mlp(x)
+        lins = [m for m in self.mlp if isinstance(m, mlpLinear)]
+        h_t = ops.radial_mlp_hidden(x, [m.weight * m.alpha for m in lins[:-1]])
+        last = lins[-1]
+        return x.new_empty(x.shape[0], last.weight.shape[1]).addmm_(h_t.t(), last.weight, beta=0.0,
+                                                                    alpha=last.alpha)
 
 
 # ------------------------------------------------------------------ blocks ----

@@ -571,6 +571,48 @@ def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, row
                                rows_src.long().contiguous(), rows_dst.long().contiguous(), int(lmax))
 
 
+class _RadialMlp(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, radial, weights, n_layers: int):
+        E, n_in = radial.shape
+        dt = radial.dtype
+        width = 64
+        _req(radial, "radial", dt, (E, n_in))
+        _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
+        h_t = torch.empty(width, E, dtype=dt, device=radial.device)
+        z_t = torch.empty(n_layers, width, E, dtype=dt, device=radial.device)
+        tok = _t0("radial_mlp_fwd")
+        N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers,
+                                            weights.data_ptr(), h_t.data_ptr(), z_t.data_ptr(),
+                                            N.stream_ptr(radial.device)), "tace_radial_mlp_fwd")
+        _t1(tok, (E, n_in, n_layers))
+        ctx.save_for_backward(z_t, weights)
+        ctx.n_in, ctx.n_layers = n_in, n_layers
+        return h_t
+
+    @staticmethod
+    def backward(ctx, gh_t):
+        z_t, weights = ctx.saved_tensors
+        E = z_t.shape[2]
+        gh_t = gh_t.contiguous()
+        g = torch.empty(E, ctx.n_in, dtype=z_t.dtype, device=z_t.device)
+        tok = _t0("radial_mlp_bwd")
+        N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh_t.data_ptr(), E, ctx.n_in,
+                                            ctx.n_layers, weights.data_ptr(), g.data_ptr(),
+                                            N.stream_ptr(z_t.device)), "tace_radial_mlp_bwd")
+        _t1(tok, (E, ctx.n_in, ctx.n_layers))
+        return g, None, None
+
+
+def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> torch.Tensor:
+    """silu(... silu(radial @ mats[0]) ... @ mats[-1]) for width-64 hidden
+    layers (scales folded into ``mats``), returned feature-major [64, E]
+    (``.t()`` is the [E, 64] activation).  The matrices are constants here:
+    gradients flow to ``radial`` only."""
+    flat = torch.cat([m.detach().reshape(-1) for m in mats]).to(radial.dtype).contiguous()
+    return _RadialMlp.apply(radial.contiguous(), flat, len(mats))
+
+
 def edge_ace_paths(lmax: int) -> List[Tuple[int, int, int, bool]]:
     """(m3, m1, m2, is_sum) of the complex edge-ACE product in weight order."""
     out = []

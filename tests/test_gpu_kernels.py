@@ -367,3 +367,33 @@ def test_edge_tp_node_map_matches_identity_order(cuda, dtype, layout):
 def var_out_ls(var, in1, lmax):
     tp = om.ScatterTP(_irreps(in1, 1), oso3.sh_irreps(lmax), [(1, (l, (-1) ** l)) for l in range(lmax + 1)])
     return [ir[0] for _, ir in tp.out]
+
+
+# ------------------------------------------------------------ radial MLP ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("dims", [[8, 64, 64, 64, 2944], [8, 64, 64, 64, 1536], [10, 64, 96], [8, 64, 64, 64, 64, 7]])
+def test_radial_mlp_matches_oracle(cuda, dtype, dims):
+    """Fused width-64 hidden layers + last-layer GEMM against the oracle MLP (same weights)."""
+    from tace_amd import model as pm
+    torch.manual_seed(len(dims) + dims[-1])
+    ref = om.MLP(dims).double()
+    g = torch.Generator().manual_seed(dims[-1])
+    E = 3001
+    R = torch.randn(E, dims[0], generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    out_o = ref(R)
+    go = torch.randn(out_o.shape, generator=g, dtype=torch.float64)
+    (gR_o,) = torch.autograd.grad((out_o * go).sum(), R)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        mlp = pm.MLP(dims)
+    finally:
+        torch.set_default_dtype(prev)
+    mlp.load_state_dict({k: v.to(dtype) for k, v in ref.state_dict().items()})
+    mlp = mlp.to(cuda)
+    assert mlp.fused
+    r = R.detach().to(dtype).to(cuda).requires_grad_(True)
+    out = mlp(r)
+    close(out, out_o, dtype, "mlp out")
+    (gR,) = torch.autograd.grad((out * go.to(dtype).to(cuda)).sum(), r)
+    close(gR, gR_o, dtype, "grad radial")

@@ -92,6 +92,9 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         E, K, C, has_w = info
         nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
         return s * E * (8 * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
+    if name.startswith("radial_mlp_out"):
+        E, n_out = info
+        return s * (E * (64 + n_out) + 64 * n_out)
     if name.startswith("edge_basis_fwd"):
         (E,) = info
         return s * E * (3 + 8 + 16)

@@ -9,9 +9,10 @@
 // activations out instead of a GEMM + activation launch pair per layer.
 //
 // Layouts: radial [E, n_in]; weights packed [n_in x 64 | 64 x 64 | ...]
-// (row-major, scale folded in); activations and saved pre-activations
-// feature-major: h_t [64, E], z_t [n_layers, 64, E] (consecutive edges =
-// consecutive addresses for every store and load).
+// (row-major, scale folded in); the last hidden activations h [E, 64]
+// row-major (the A operand of the last layer's GEMM); the saved
+// pre-activations feature-major, z_t [n_layers, 64, E] (consecutive edges =
+// consecutive addresses).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -31,12 +32,12 @@ __device__ __forceinline__ T sigm(T z) { return T(1) / (T(1) + exp(-z)); }
 
 template <typename T>
 __global__ __launch_bounds__(256) void k_mlp_fwd(const T* __restrict__ radial, int64_t E, int n_in, int n_layers,
-                                                 const T* __restrict__ wg, T* __restrict__ h_t,
+                                                 const T* __restrict__ wg, T* __restrict__ h,
                                                  T* __restrict__ z_t) {
   const T* __restrict__ w = wg;
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
-  T h[W], z[W];
+  T a_[W], z[W];
 #pragma unroll
   for (int j = 0; j < W; ++j) z[j] = T(0);
   for (int k = 0; k < n_in; ++k) {
@@ -49,26 +50,26 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(const T* __restrict__ radial, i
 #pragma unroll
     for (int j = 0; j < W; ++j) {
       z_t[((int64_t)l * W + j) * E + e] = z[j];
-      h[j] = z[j] * sigm(z[j]);
+      a_[j] = z[j] * sigm(z[j]);
     }
     if (l + 1 == n_layers) break;
 #pragma unroll
     for (int j = 0; j < W; ++j) z[j] = T(0);
 #pragma unroll
     for (int k = 0; k < W; ++k) {
-      const T a = h[k];
+      const T a = a_[k];
 #pragma unroll
       for (int j = 0; j < W; ++j) z[j] += a * w[off + k * W + j];
     }
     off += W * W;
   }
 #pragma unroll
-  for (int j = 0; j < W; ++j) h_t[(int64_t)j * E + e] = h[j];
+  for (int j = 0; j < W; ++j) h[e * W + j] = a_[j];
 }
 
 // backward to the radial basis: g_z = g_h silu'(z), g_h(prev) = W g_z
 template <typename T>
-__global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, const T* __restrict__ gh_t, int64_t E,
+__global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, const T* __restrict__ gh, int64_t E,
                                                  int n_in, int n_layers, const T* __restrict__ wg,
                                                  T* __restrict__ g_radial) {
   const T* __restrict__ w = wg;
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
   if (e >= E) return;
   T g[W];
 #pragma unroll
-  for (int j = 0; j < W; ++j) g[j] = gh_t[(int64_t)j * E + e];
+  for (int j = 0; j < W; ++j) g[j] = gh[e * W + j];
   for (int l = n_layers - 1; l >= 0; --l) {
 #pragma unroll
     for (int j = 0; j < W; ++j) {
@@ -105,6 +106,86 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
   }
 }
 
+// ------------------------------------------------------------- last layer --
+// out[e, n] = alpha sum_k h[e, k] W[k, n] with K = 64 (the wide, linear last
+// layer: E ~ 1e6 edges x N ~ 3e3 weights, output-write and fp32-MFMA bound).
+// Each wavefront owns 64 output columns and keeps their 64 x 64 slice of W in
+// registers as v_mfma_f32_16x16x4f32 B fragments for its whole life; it then
+// streams 16-edge blocks: A fragments from h (one 64-byte row segment per
+// lane), 16 k-steps x 4 column blocks of MFMA, and the 16 x 64 result tile
+// stored straight from the accumulators.  K is permuted inside each step
+// (lane group q of step s holds k = 16 q + s) so that a lane's A values are
+// one contiguous row segment.  Workgroups (4 waves = 256 columns) that share
+// an edge chunk are placed on one XCD (blockIdx round-robins over the 8
+// XCDs), so the chunk's h rows are read from HBM about once.
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void load_a_frag(const float* __restrict__ h, int64_t er, int64_t E, int q, float* a) {
+  if (er < E) {
+    const f4_t* hp = reinterpret_cast<const f4_t*>(h + er * 64 + 16 * q);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const f4_t t = hp[v];
+      a[4 * v] = t[0]; a[4 * v + 1] = t[1]; a[4 * v + 2] = t[2]; a[4 * v + 3] = t[3];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) a[s] = 0.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h, const float* __restrict__ Wm,
+                                                     int64_t E, int N, float alpha, int n_col_tiles,
+                                                     int64_t n_chunks, int edges_per_chunk, float* __restrict__ out) {
+  // per wave: the 16 x 64 result tile, transposed through LDS so that every
+  // store is one 256-byte row segment (row stride 65 floats: no bank conflicts)
+  __shared__ float tile[4][16][65];
+  const int b = (int)blockIdx.x;
+  const int64_t chunk = (int64_t)(b & 7) + 8 * (int64_t)((b >> 3) / n_col_tiles);
+  const int ct = (b >> 3) % n_col_tiles;
+  if (chunk >= n_chunks) return;
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
+  const int i = lane & 15, q = lane >> 4;
+  const int col0 = ct * 256 + wave * 64;
+  float bf[16][4];
+#pragma unroll
+  for (int s = 0; s < 16; ++s)
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int c = col0 + 16 * cb + i;
+      bf[s][cb] = c < N ? Wm[(int64_t)(16 * q + s) * N + c] : 0.0f;
+    }
+  const int64_t e_begin = chunk * edges_per_chunk;
+  const int64_t e_end = e_begin + edges_per_chunk < E ? e_begin + edges_per_chunk : E;
+  const bool col_ok = col0 + lane < N;
+  float a[16], an[16];
+  load_a_frag(h, e_begin + i, E, q, a);
+  for (int64_t e0 = e_begin; e0 < e_end; e0 += 16) {
+    // next block's A fragment in flight during this block's MFMAs
+    load_a_frag(h, e0 + 16 < e_end ? e0 + 16 + i : E, E, q, an);
+    f4_t acc[4];
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) acc[cb] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bf[s][cb], acc[cb], 0, 0, 0);
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) tile[wave][4 * q + r][16 * cb + i] = alpha * acc[cb][r];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = e0 + r;
+      if (row < E && col_ok) out[row * N + col0 + lane] = tile[wave][r][lane];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) a[s] = an[s];
+  }
+}
+
 int mlp_checks(const char* who, int64_t E, int32_t n_in, int32_t n_layers) {
   char msg[160];
   if (E < 0 || n_in < 1 || n_in > TACE_MLP_MAX_IN || n_layers < 1 || n_layers > TACE_MLP_MAX_LAYERS) {
@@ -120,39 +201,55 @@ int mlp_checks(const char* who, int64_t E, int32_t n_in, int32_t n_layers) {
 extern "C" {
 
 int tace_radial_mlp_fwd(int dtype, const void* radial, int64_t n_edges, int32_t n_in, int32_t n_layers,
-                        const void* weights, void* h_t, void* z_t, void* stream) {
+                        const void* weights, void* h, void* z_t, void* stream) {
   if (mlp_checks("tace_radial_mlp_fwd", n_edges, n_in, n_layers)) return -1;
   if (n_edges == 0) return 0;
-  if (!radial || !weights || !h_t || !z_t) return tace_fail_msg("tace_radial_mlp_fwd: null pointer");
+  if (!radial || !weights || !h || !z_t) return tace_fail_msg("tace_radial_mlp_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges + 255) / 256)), b(256);
   if (dtype == TACE_F32)
     hipLaunchKernelGGL(k_mlp_fwd<float>, g, b, 0, s, (const float*)radial, n_edges, n_in, n_layers,
-                       (const float*)weights, (float*)h_t, (float*)z_t);
+                       (const float*)weights, (float*)h, (float*)z_t);
   else if (dtype == TACE_F64)
     hipLaunchKernelGGL(k_mlp_fwd<double>, g, b, 0, s, (const double*)radial, n_edges, n_in, n_layers,
-                       (const double*)weights, (double*)h_t, (double*)z_t);
+                       (const double*)weights, (double*)h, (double*)z_t);
   else
     return tace_fail_msg("tace_radial_mlp_fwd: dtype must be TACE_F32 or TACE_F64");
   return tace_check_launch("tace_radial_mlp_fwd");
 }
 
-int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h_t, int64_t n_edges, int32_t n_in,
+int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h, int64_t n_edges, int32_t n_in,
                         int32_t n_layers, const void* weights, void* g_radial, void* stream) {
   if (mlp_checks("tace_radial_mlp_bwd", n_edges, n_in, n_layers)) return -1;
   if (n_edges == 0) return 0;
-  if (!z_t || !g_h_t || !weights || !g_radial) return tace_fail_msg("tace_radial_mlp_bwd: null pointer");
+  if (!z_t || !g_h || !weights || !g_radial) return tace_fail_msg("tace_radial_mlp_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges + 255) / 256)), b(256);
   if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_mlp_bwd<float>, g, b, 0, s, (const float*)z_t, (const float*)g_h_t, n_edges, n_in,
+    hipLaunchKernelGGL(k_mlp_bwd<float>, g, b, 0, s, (const float*)z_t, (const float*)g_h, n_edges, n_in,
                        n_layers, (const float*)weights, (float*)g_radial);
   else if (dtype == TACE_F64)
-    hipLaunchKernelGGL(k_mlp_bwd<double>, g, b, 0, s, (const double*)z_t, (const double*)g_h_t, n_edges,
+    hipLaunchKernelGGL(k_mlp_bwd<double>, g, b, 0, s, (const double*)z_t, (const double*)g_h, n_edges,
                        n_in, n_layers, (const double*)weights, (double*)g_radial);
   else
     return tace_fail_msg("tace_radial_mlp_bwd: dtype must be TACE_F32 or TACE_F64");
   return tace_check_launch("tace_radial_mlp_bwd");
+}
+
+int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
+                            float* out, void* stream) {
+  if (n_edges < 0 || n_out <= 0) return tace_fail_msg("tace_radial_mlp_out_f32: bad sizes");
+  if (n_edges == 0) return 0;
+  if (!h || !weight || !out) return tace_fail_msg("tace_radial_mlp_out_f32: null pointer");
+  if (((uintptr_t)h & 15) != 0) return tace_fail_msg("tace_radial_mlp_out_f32: h must be 16-byte aligned");
+  const int edges_per_chunk = 1024;
+  const int n_col_tiles = (n_out + 255) / 256;
+  const int64_t n_chunks = (n_edges + edges_per_chunk - 1) / edges_per_chunk;
+  const int64_t n_wg = n_col_tiles * ((n_chunks + 7) / 8) * 8;
+  if (n_wg > INT32_MAX) return tace_fail_msg("tace_radial_mlp_out_f32: too many edges");
+  hipLaunchKernelGGL(k_mlp_out_f32, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, h, weight, n_edges, n_out,
+                     alpha, n_col_tiles, n_chunks, edges_per_chunk, out);
+  return tace_check_launch("tace_radial_mlp_out_f32");
 }
 
 }  // extern "C"

@@ -254,8 +254,9 @@ class mlpLinear(torch.nn.Module):
 class MLP(torch.nn.Module):
     """Radial MLP (``mlp.py:136-191``): alpha = gain/sqrt(h_in), SiLU between
     layers.  Width-64 hidden layers run in one HIP kernel per direction
-    (``ops.radial_mlp_hidden``, the weights as constants: the inference path
-    freezes parameters); the wide last layer is a GEMM."""
+    (``ops.radial_mlp_hidden``) and the wide last layer on an fp32-MFMA kernel
+    (``ops.radial_mlp_out``), the weights as constants: the inference path
+    freezes parameters."""
 
     def __init__(self, dims):
         super().__init__()
@@ -271,10 +272,8 @@ class MLP(torch.nn.Module):
         if not self.fused:
             return self.mlp(x)
         lins = [m for m in self.mlp if isinstance(m, mlpLinear)]
-        h_t = ops.radial_mlp_hidden(x, [m.weight * m.alpha for m in lins[:-1]])
-        last = lins[-1]
-        return x.new_empty(x.shape[0], last.weight.shape[1]).addmm_(h_t.t(), last.weight, beta=0.0,
-                                                                    alpha=last.alpha)
+        h = ops.radial_mlp_hidden(x, [m.weight * m.alpha for m in lins[:-1]])
+        return ops.radial_mlp_out(h, lins[-1].weight, lins[-1].alpha)
 
 
 # ------------------------------------------------------------------ blocks ----

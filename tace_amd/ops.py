@@ -579,36 +579,65 @@ class _RadialMlp(torch.autograd.Function):
         width = 64
         _req(radial, "radial", dt, (E, n_in))
         _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
-        h_t = torch.empty(width, E, dtype=dt, device=radial.device)
+        h = torch.empty(E, width, dtype=dt, device=radial.device)
         z_t = torch.empty(n_layers, width, E, dtype=dt, device=radial.device)
         tok = _t0("radial_mlp_fwd")
         N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers,
-                                            weights.data_ptr(), h_t.data_ptr(), z_t.data_ptr(),
+                                            weights.data_ptr(), h.data_ptr(), z_t.data_ptr(),
                                             N.stream_ptr(radial.device)), "tace_radial_mlp_fwd")
         _t1(tok, (E, n_in, n_layers))
         ctx.save_for_backward(z_t, weights)
         ctx.n_in, ctx.n_layers = n_in, n_layers
-        return h_t
+        return h
 
     @staticmethod
-    def backward(ctx, gh_t):
+    def backward(ctx, gh):
         z_t, weights = ctx.saved_tensors
         E = z_t.shape[2]
-        gh_t = gh_t.contiguous()
+        gh = gh.contiguous()
         g = torch.empty(E, ctx.n_in, dtype=z_t.dtype, device=z_t.device)
         tok = _t0("radial_mlp_bwd")
-        N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh_t.data_ptr(), E, ctx.n_in,
+        N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh.data_ptr(), E, ctx.n_in,
                                             ctx.n_layers, weights.data_ptr(), g.data_ptr(),
                                             N.stream_ptr(z_t.device)), "tace_radial_mlp_bwd")
         _t1(tok, (E, ctx.n_in, ctx.n_layers))
         return g, None, None
 
 
+class _MlpOut(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, h, W, alpha: float):
+        E, K = h.shape
+        _req(h, "h", torch.float32, (E, 64))
+        _req(W, "weight", torch.float32, (64, W.shape[1]))
+        out = torch.empty(E, W.shape[1], dtype=torch.float32, device=h.device)
+        tok = _t0("radial_mlp_out")
+        N.check(N.lib().tace_radial_mlp_out_f32(h.data_ptr(), W.data_ptr(), E, W.shape[1], float(alpha),
+                                                out.data_ptr(), N.stream_ptr(h.device)), "tace_radial_mlp_out_f32")
+        _t1(tok, (E, W.shape[1]))
+        ctx.save_for_backward(W)
+        ctx.alpha = alpha
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (W,) = ctx.saved_tensors
+        return torch.mm(g, W.t()).mul_(ctx.alpha), None, None
+
+
+def radial_mlp_out(h: torch.Tensor, W: torch.Tensor, alpha: float) -> torch.Tensor:
+    """alpha h @ W for the width-64 last hidden activations: the fp32 MFMA
+    kernel for float32 (weights as constants: gradient to h only), a GEMM
+    otherwise."""
+    if h.dtype == torch.float32:
+        return _MlpOut.apply(h.contiguous(), W.detach().contiguous(), float(alpha))
+    return h.new_empty(h.shape[0], W.shape[1]).addmm_(h, W, beta=0.0, alpha=alpha)
+
+
 def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> torch.Tensor:
     """silu(... silu(radial @ mats[0]) ... @ mats[-1]) for width-64 hidden
-    layers (scales folded into ``mats``), returned feature-major [64, E]
-    (``.t()`` is the [E, 64] activation).  The matrices are constants here:
-    gradients flow to ``radial`` only."""
+    layers (scales folded into ``mats``): the last hidden activations [E, 64].
+    The matrices are constants here: gradients flow to ``radial`` only."""
     flat = torch.cat([m.detach().reshape(-1) for m in mats]).to(radial.dtype).contiguous()
     return _RadialMlp.apply(radial.contiguous(), flat, len(mats))
 

@@ -5,9 +5,10 @@ The reference fills ``self.fused_tp`` of ``O3ScatterTensorProduct``
 (``fused.py:61-71``) with an accelerated module when an acceleration flag is
 set (``tace/utils/env.py:9-64``).  These classes have the same constructor and
 ``forward`` contract as the OEQ adapter (``tace/models/oeq/_tp_scatter.py:53-93``)
-and run the MI355X HIP kernels; ``INTEGRATION.md`` shows the lines a
-maintainer adds to ``fused.py`` / ``env.py`` to select them with
-``TACE_USE_HIP=1``.
+and run the MI355X HIP kernels.  ``HipTeceConvolution`` replaces the TECE
+convolution module (``OAM20260705Convolution``) the same way.  A maintainer
+selects them with ``TACE_USE_HIP=1`` by adding a few lines to ``fused.py`` /
+``inter.py`` / ``env.py``.
 
 Contract (``fused.py:259-271``): ``forward(x [N, irreps_in1.dim], y [E,
 irreps_in2.dim], w [E, weight_numel], edge_index [2, E] int64)`` returns
@@ -22,7 +23,9 @@ from typing import Optional, Sequence
 import torch
 
 from . import ops
-from .so3 import Irreps, generate_paths
+from .model import e3nn_to_gm, gm_to_e3nn
+from .so3 import Irrep, Irreps, generate_paths
+from .tece import TeceConvolution
 
 ACCELERATION_ENV_NAME = "TACE_USE_HIP"
 
@@ -84,6 +87,43 @@ class e3nnHipUuuTensorProduct(torch.nn.Module):
         ops.find_variant(self.key)
 
     def forward(self, x: torch.Tensor, y: torch.Tensor, ws: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if ws is not None:
-            raise ValueError("the weighted (bilinear-gate) uuu product is not on the MI355X path")
-        return ops.uuu_tp(x, y, ops.find_variant(self.key), self.C)
+        # ws [N, paths*C]: the per-node weights of the trainable (bilinear-gate)
+        # product; only the variants compiled as weighted accept them (the ABI
+        # rejects a mismatch)
+        return ops.uuu_tp(x, y, ops.find_variant(self.key), self.C, 0, ws)
+
+
+class HipTeceConvolution(TeceConvolution):
+    """Drop-in for ``OAM20260705Convolution``
+    (``tace/models/_e3nn/archive/oam_2026_07_05.py:547-823``) as
+    ``OAM20260705Interaction._build_rejector`` (``inter.py:469-498``) builds
+    it: same constructor arguments, parameters (names, shapes) and
+    ``forward(x, w, edge_index, cutoff, wigner, wigner_inv, radial_basis)``,
+    x and the result in the e3nn ``mul_ir`` layout of C x (0..lmax).  Runs the
+    HIP kernels of ``tace_amd.tece``.  Supported: the interaction's flags
+    (``inter.py:450-454``), gate_m0, mmax == lmax, edge_wise_hidden == C and
+    ``cutoff`` None (radial basis with ``apply_cutoff``); anything else raises."""
+
+    def __init__(self, mmax: int, lmax: int, num_channel: int, num_head: int, use_temperature: bool,
+                 edge_ace_hidden: int, edge_wise_hidden: Optional[int], num_radial_basis: int, so2_linear_type: str,
+                 gate_m0: bool, use_so2_edge_ace: bool, use_graph_softmax: bool, reshape_in=None, reshape_out=None,
+                 scalar_act=None, tensor_act=None, use_radial_phase: bool = True):
+        flags = dict(use_temperature=use_temperature, use_so2_edge_ace=use_so2_edge_ace,
+                     use_graph_softmax=use_graph_softmax, use_radial_phase=use_radial_phase, gate_m0=gate_m0)
+        if so2_linear_type != "w1" or not all(flags.values()):
+            raise NotImplementedError(f"HipTeceConvolution covers so2_linear_type='w1' with {sorted(flags)} all True")
+        if edge_wise_hidden not in (None, num_channel):
+            raise NotImplementedError("HipTeceConvolution needs edge_wise_hidden == num_channel")
+        super().__init__(mmax, lmax, num_channel, num_head, edge_ace_hidden, num_radial_basis)
+
+    def forward(self, x, w, edge_index, cutoff, wigner, wigner_inv, radial_basis):
+        if cutoff is not None:
+            raise NotImplementedError("HipTeceConvolution: per-edge cutoff rescaling (apply_cutoff=False) is not "
+                                      "on the MI355X path")
+        Nn, C, L = x.shape[0], self.C, self.lmax
+        irreps = Irreps([(C, Irrep(l, (-1) ** l)) for l in range(L + 1)])
+        x_lc = self.node_components(e3nn_to_gm(x.contiguous(), irreps))
+        plan = ops.EdgePlan.from_edge_index(edge_index, Nn)
+        src, dst = edge_index[0], edge_index[1]
+        out = self.edges(x_lc, w, src, dst, plan, None, dst, wigner, radial_basis)
+        return gm_to_e3nn(out, irreps)

@@ -457,3 +457,61 @@ def test_tece_receiver_chunks(cuda, dtype):
                             num_channel=64, num_head=2)
     _check(got, want, dtype)
 
+
+
+# ----------------------------------------------------------- slot adapters ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_slot_tece_convolution_matches_oracle(cuda, dtype):
+    """HipTeceConvolution with the reference module's constructor and forward
+    (e3nn-layout x and result, the caller's wigner matrices, unsorted edges)."""
+    from tace_amd import slot
+    lmax, C, H, A, nr = 2, 32, 2, 16, 8
+    g = torch.Generator().manual_seed(77)
+    N, E = 50, 700
+    ei = _random_graph(N, E, g)
+    torch.manual_seed(5)
+    conv_o = ot.TeceConvolution(lmax, lmax, C, H, A, nr).double()
+    _perturb_tece(conv_o, g)
+    K = (lmax + 1) ** 2
+    x_lc = torch.randn(N, K, C, generator=g, dtype=torch.float64).to(dtype).double()
+    x = ot.lc_to_e3nn(x_lc, lmax).requires_grad_(True)
+    w = torch.randn(E, conv_o.weight_numel, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    R = torch.randn(E, nr, generator=g, dtype=torch.float64).to(dtype).double().requires_grad_(True)
+    W_o, Wi_o = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W_o = W_o.to(dtype).double()
+    o = ot.lc_to_e3nn(conv_o(ot.e3nn_to_lc(x, lmax, C), w, ei, W_o, W_o.transpose(1, 2), R), lmax)
+    go = torch.randn(o.shape, generator=g, dtype=torch.float64)
+    grads_o = torch.autograd.grad((o * go).sum(), [x, w, R])
+    m = slot.HipTeceConvolution(lmax, lmax, C, H, True, A, None, nr, "w1", True, True, True).to(dtype)
+    m.load_state_dict({k: v.to(dtype) for k, v in conv_o.state_dict().items()})
+    m = m.to(cuda)
+    xg, wg, Rg = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, w, R))
+    Wg = W_o.to(dtype).to(cuda)
+    out = m(xg, wg, ei.to(cuda), None, Wg, Wg.transpose(1, 2), Rg)
+    tol = None if dtype == torch.float64 else 2e-4
+    close(out, o, dtype, "out", tol)
+    grads = torch.autograd.grad((out * go.to(dtype).to(cuda)).sum(), [xg, wg, Rg])
+    for a_, b_, n_ in zip(grads, grads_o, ("x", "w", "R")):
+        close(a_, b_, dtype, "grad " + n_, tol)
+    with pytest.raises(NotImplementedError):
+        m(xg, wg, ei.to(cuda), torch.ones(E, 1, device=cuda, dtype=dtype), Wg, Wg.transpose(1, 2), Rg)
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_slot_uuu_weighted_matches_oracle(cuda, dtype):
+    """The uuu slot with per-node weights (bilinear gate), e3nn layout."""
+    from tace_amd import slot
+    C, full = 32, [0, 1, 2]
+    base = full + [0]
+    ir = lambda ls: [(C, (l, (-1) ** l)) for l in ls]
+    tp = om.UUUTP(ir(full), ir(base), [(1, (l, (-1) ** l)) for l in full], False)
+    g = torch.Generator().manual_seed(3)
+    Nn = 41
+    x1 = torch.randn(Nn, sum(C * (2 * l + 1) for l in full), generator=g, dtype=torch.float64).to(dtype).double()
+    x2 = torch.randn(Nn, sum(C * (2 * l + 1) for l in base), generator=g, dtype=torch.float64).to(dtype).double()
+    ws = torch.randn(Nn, len(tp.paths) * C, generator=g, dtype=torch.float64).to(dtype).double()
+    want = tp(x1, x2, ws)
+    irs = lambda ls: "+".join(f"{C}x{l}{'e' if l % 2 == 0 else 'o'}" for l in ls)
+    m = slot.e3nnHipUuuTensorProduct(irs(full), irs(base), irs(full), identical_inputs=False)
+    got = m(*(t.to(dtype).to(cuda) for t in (x1, x2, ws)))
+    close(got, want, dtype, "uuu weighted (slot)")

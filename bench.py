@@ -184,6 +184,8 @@ def main():
                     help="water12k: the headline water box (configs[2]); fe101k: TECE on bcc Fe (configs[4])")
     ap.add_argument("--n-side", type=int, default=16, help="water molecules per box edge (16 -> 12,288 atoms)")
     ap.add_argument("--fe-reps", type=int, default=37, help="bcc cells per box edge (37 -> 101,306 atoms)")
+    ap.add_argument("--fe-fp32-mixing", action="store_true",
+                    help="fe101k: SO(2) channel mixing in fp32 instead of the configuration's bf16")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernels", action="store_true", help="print the per-kernel breakdown to stderr")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -224,6 +226,10 @@ def main():
     model.eval()
     for prm in model.parameters():
         prm.requires_grad_(False)
+    mixing = None
+    if args.workload == "fe101k" and not args.fe_fp32_mixing:
+        mixing = torch.bfloat16  # "fp32 with bf16 channel mixing on MFMA"
+        pm.set_tece_channel_mixing(model, mixing)
     attrs = data.one_hot(s["numbers"], cfg["atomic_numbers"], torch.float32).to(dev)
 
     def step():
@@ -265,7 +271,8 @@ def main():
 
     res = dict(metric=wl["metric"], value=round(nat * args.steps / dt, 1), unit="atom-steps/s", n_gpus=1,
                steps=args.steps, warmup=args.warmup, ms_per_step=round(ms, 3), higher_is_better=True,
-               scaling="weak", vs_baseline=None, dtype="fp32", data="synthetic",
+               scaling="weak", vs_baseline=None, dtype="fp32" if mixing is None else "fp32, bf16 channel mixing",
+               data="synthetic",
                config=dict(workload=wl["describe"](nat), atoms=nat, edges=int(E0), **wl["arch"],
                            parallelism="single GPU"),
                ns_per_day=round(1e3 / ms * 86400 * wl["dt_fs"] * 1e-6, 4), dt_fs=wl["dt_fs"], roofline=roof,

@@ -791,6 +791,21 @@ class TACE(torch.nn.Module):
         return E, e_base + e_node
 
 
+def set_tece_channel_mixing(model: torch.nn.Module, dtype: Optional[torch.dtype]):
+    """Precision of the TECE SO(2) channel-mixing GEMMs: None (the model's
+    own, default) or torch.bfloat16 (bf16 operands, fp32 accumulation and
+    output; the configuration-5 option).  Returns the number of convolutions set."""
+    from .tece import TeceConvolution
+    if dtype not in (None, torch.bfloat16):
+        raise ValueError("channel mixing precision must be None or torch.bfloat16")
+    n = 0
+    for m in model.modules():
+        if isinstance(m, TeceConvolution):
+            m.mixing = dtype
+            n += 1
+    return n
+
+
 class TensorModel(torch.nn.Module):
     """``TensorModel`` (``tace/models/adapter.py:23-452``) for energy, forces,
     stress/virials: ``forward(data) -> {energy, node_energy, forces, stress, virials}``."""

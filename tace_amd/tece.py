@@ -22,6 +22,33 @@ import torch
 
 from . import ops
 
+class _MixedLinear(torch.autograd.Function):
+    """y = x W^T (+ b) with x and W rounded to bfloat16 and fp32 accumulation
+    and output (hipBLASLt); the input gradient likewise.  W is a constant."""
+
+    @staticmethod
+    def forward(ctx, x, wt, b):
+        y = torch.mm(x.to(torch.bfloat16), wt, out_dtype=torch.float32)
+        if b is not None:
+            y += b
+        ctx.save_for_backward(wt)
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        (wt,) = ctx.saved_tensors
+        return torch.mm(g.to(torch.bfloat16), wt.t(), out_dtype=torch.float32), None, None
+
+
+def mix_linear(x, W, b, mixing):
+    """``F.linear(x, W, b)`` for 2-D x; ``mixing`` = torch.bfloat16 runs the
+    product on bf16 MFMA with fp32 accumulation (the "bf16 channel mixing"
+    option of the TECE configuration), None in the input's precision."""
+    if mixing is None or x.dtype != torch.float32:
+        return torch.nn.functional.linear(x, W, b)
+    return _MixedLinear.apply(x, W.detach().t().to(mixing).contiguous(), None if b is None else b.detach())
+
+
 class torchLinear(torch.nn.Module):
     """``torchLinear`` (``tace/models/linear.py:210-244``): y = x (W/sqrt(in))^T + b,
     W ~ N(0,1) [out, in], b zeros."""
@@ -59,18 +86,21 @@ class uvSO2Linear(torch.nn.Module):
         self.ms_clinear = torch.nn.ModuleList(
             uvSO2MLinear(cin, cout, self.nin[m], self.nout[m]) for m in range(1, mmax + 1))
 
-    def forward(self, x):
+    def forward(self, x, mixing=None):
         # every block is one 2-D GEMM over (edge[, +-m]) rows: the row slices
         # are made contiguous first (a strided 3-D operand would make torch
         # fall back to one tiny GEMM per edge)
         E = x.shape[0]
-        outs = [self.m0_rlinear(x[:, :self.nin[0]].reshape(E, -1)).view(E, self.nout[0], self.cout)]
+        f = self.m0_rlinear
+        outs = [mix_linear(x[:, :self.nin[0]].reshape(E, -1), f.weight * f.alpha, f.bias, mixing)
+                .view(E, self.nout[0], self.cout)]
         off = self.nin[0]
         for m in range(1, self.mmax + 1):
             n = self.nin[m]
             xm = x[:, off:off + 2 * n].contiguous().view(E * 2, n * self.cin)
             off += 2 * n
-            outs.append(self.ms_clinear[m - 1].fc(xm).view(E, 2 * self.nout[m], self.cout))
+            fc = self.ms_clinear[m - 1].fc
+            outs.append(mix_linear(xm, fc.weight * fc.alpha, None, mixing).view(E, 2 * self.nout[m], self.cout))
         return torch.cat(outs, dim=1)
 
 
@@ -84,6 +114,9 @@ class TeceConvolution(torch.nn.Module):
         if C % num_head:
             raise ValueError("channels must be divisible by num_head")
         self.mmax, self.lmax, self.C, self.H, self.A = mmax, lmax, C, num_head, edge_ace_hidden
+        # precision of the SO(2) channel mixing GEMMs: None = the features'
+        # own, torch.bfloat16 = bf16 operands with fp32 accumulation
+        self.mixing = None
         self.Ch = C // num_head
         n = lmax + 1
         A = edge_ace_hidden
@@ -119,14 +152,14 @@ class TeceConvolution(torch.nn.Module):
         f0 = [lc.m0_rlinear, lg.m0_rlinear, lu.m0_rlinear]
         W0 = torch.cat([f.weight * f.alpha for f in f0])
         b0 = torch.cat([f.bias for f in f0])
-        ys = [torch.nn.functional.linear(m[:, :n].reshape(E, -1), W0, b0)]
+        ys = [mix_linear(m[:, :n].reshape(E, -1), W0, b0, self.mixing)]
         off = n
         for mm in range(1, self.mmax + 1):
             k = n - mm
             xm = m[:, off:off + 2 * k].contiguous().view(2 * E, -1)
             off += 2 * k
             fg, fu = lg.ms_clinear[mm - 1].fc, lu.ms_clinear[mm - 1].fc
-            ys.append(torch.nn.functional.linear(xm, torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha])))
+            ys.append(mix_linear(xm, torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha]), None, self.mixing))
         return ys
 
     def _linear_down_blocks(self, o):
@@ -135,10 +168,10 @@ class TeceConvolution(torch.nn.Module):
         ld = self.linear_down
         E = o[0].shape[0]
         f = ld.m0_rlinear
-        outs = [torch.nn.functional.linear(o[0], f.weight * f.alpha, f.bias).view(E, ld.nout[0], ld.cout)]
+        outs = [mix_linear(o[0], f.weight * f.alpha, f.bias, self.mixing).view(E, ld.nout[0], ld.cout)]
         for mm in range(1, self.mmax + 1):
             fc = ld.ms_clinear[mm - 1].fc
-            outs.append(torch.nn.functional.linear(o[mm], fc.weight * fc.alpha).view(E, 2 * ld.nout[mm], ld.cout))
+            outs.append(mix_linear(o[mm], fc.weight * fc.alpha, None, self.mixing).view(E, 2 * ld.nout[mm], ld.cout))
         return torch.cat(outs, dim=1)
 
     def node_components(self, x_gm):
@@ -154,8 +187,8 @@ class TeceConvolution(torch.nn.Module):
         ``out_map`` (int32 or None) / ``dst_out``: output row of each receiver /
         of each edge's receiver.  Returns [plan.n_nodes, K*C] group-major."""
         ms, md, m = ops.edge_rotate_in(x_lc, wigner, rows_src, rows_dst, self.lmax, w)
-        key = self.key_proj(ms)
-        query = self.query_proj(md)
+        key = self.key_proj(ms, self.mixing)
+        query = self.query_proj(md, self.mixing)
         rp = self.radial_proj(R)
         T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
         score = ops.tece_score(query, key, rp, (T * self.attention_scale).detach(), self.lmax, self.H)

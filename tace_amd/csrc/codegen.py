@@ -139,7 +139,7 @@ class Variant:
         L.append("  if (e < end) {")
         for (b, m) in xs:
             L.append(f"    x{b}_{m} = {self._ld_x('s', b, m)};")
-        L += [f"    w{p} = w[(size_t)ed * WW + (size_t){p} * C + u];" for p in paths]
+        L += [f"    w{p} = __builtin_nontemporal_load(&w[(size_t)ed * WW + (size_t){p} * C + u]);" for p in paths]
         L += [f"    y{j} = y[(size_t)ed * {self.D2} + {j}];" for j in range(self.D2)]
         L.append("  }")
         L.append("  for (; e < end; ++e) {")
@@ -148,7 +148,7 @@ class Variant:
         L.append("    const int sn = map ? map[src[edn]] : src[edn];")
         for (b, m) in xs:
             L.append(f"    const T xn{b}_{m} = {self._ld_x('sn', b, m)};")
-        L += [f"    const T wn{p} = w[(size_t)edn * WW + (size_t){p} * C + u];" for p in paths]
+        L += [f"    const T wn{p} = __builtin_nontemporal_load(&w[(size_t)edn * WW + (size_t){p} * C + u]);" for p in paths]
         L += [f"    const T yn{j} = y[(size_t)edn * {self.D2} + {j}];" for j in range(self.D2)]
 
     def _edge_rotate(self, L: List[str], blocks: Sequence[int], paths: Sequence[int]) -> None:
@@ -254,8 +254,8 @@ class Variant:
                 L.append(f"      {{ const T r = y{o2 + j} * g{o + k};")
                 L += [f"        psi{i} += {_lit(c)} * r;" for i, c in ic]
                 L.append("      }")
-            L.append(f"      if (act) gw[(size_t)ed * WW + (size_t){p} * C + u] = "
-                     f"{' + '.join(f'x{b1}_{i} * psi{i}' for i in used_i)};")
+            L.append(f"      if (act) __builtin_nontemporal_store("
+                     f"{' + '.join(f'x{b1}_{i} * psi{i}' for i in used_i)}, &gw[(size_t)ed * WW + (size_t){p} * C + u]);")
             L.append("      if (NEED_GX) {")
             L += [f"        hx{b1}_{i} += w{p} * psi{i};" for i in used_i]
             L.append("      }")
@@ -271,7 +271,7 @@ class Variant:
         for b in blocks:
             for m in range(self.d1[b]):
                 e3, gm = self._row_addr(b, m)
-                L.append(f"      cb[IN1_GM ? ({gm}) : ({e3})] = hx{b}_{m};")
+                L.append(f"      __builtin_nontemporal_store(hx{b}_{m}, &cb[IN1_GM ? ({gm}) : ({e3})]);")
         L.append("    }")
         L.append("    const T v = reduce16_lanes(hy0, hy1, hy2, hy3, hy4, hy5, hy6, hy7, hy8, hy9, hy10, hy11, hy12, hy13, hy14, hy15);")
         L.append("    const int jj = rev4(lane);")

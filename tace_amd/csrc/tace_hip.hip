@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void k_seg_rowsum(const T* __restrict__ cbuf, 
   for (int64_t j = (int64_t)threadIdx.x * V; j < row; j += 256 * V) {
     vec acc = (vec)(T(0));
 #pragma unroll 4
-    for (int k = b; k < e; ++k) acc += *(const vec*)(cbuf + (size_t)s_slot[k] * row + j);
+    for (int k = b; k < e; ++k) acc += __builtin_nontemporal_load((const vec*)(cbuf + (size_t)s_slot[k] * row + j));
     int64_t dst = (int64_t)s * row + j;
     for (int g = 0; g < sg.n; ++g)
       if (j >= sg.off[g] && j < sg.off[g] + sg.len[g]) dst = (int64_t)n * sg.off[g] + (int64_t)s * sg.len[g] + (j - sg.off[g]);

@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import copy
 import math
+from types import SimpleNamespace
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -815,6 +816,11 @@ class TensorModel(torch.nn.Module):
         self.readout_fn = readout_fn
         self.fidelity_idx = 0
         self.lmp = False
+        # switches the reference's callers set (adapter.py flags; the LAMMPS
+        # EdgeForcesWrapper, interface/lammps/mliap.py:25-34, turns on
+        # compute_edge_forces and sets lmp)
+        self.flags = SimpleNamespace(compute_forces=True, compute_stress=False, compute_virials=False,
+                                     compute_edge_forces=False)
 
     # getters used by the ASE / TorchSim / LAMMPS callers (adapter.py:386-452)
     def get_cutoff(self) -> float:
@@ -845,7 +851,64 @@ class TensorModel(torch.nn.Module):
     def reset_target_property(self, target_property):
         self.readout_fn.target_property = list(target_property)
 
+    @staticmethod
+    def _ghost_owners(lmp_data, nlocal: int, nghosts: int, like: torch.Tensor) -> torch.Tensor:
+        """Local atom that each of the nlocal + nghosts LAMMPS atoms stands for:
+        one width-1 ``forward_exchange`` of the local indices
+        (``models/lammps.py:82-102`` semantics: ghost rows are copied from
+        their owners)."""
+        ntotal = nlocal + nghosts
+        ids = torch.arange(ntotal, device=like.device)
+        if nghosts == 0:
+            return ids
+        if lmp_data is None or not hasattr(lmp_data, "forward_exchange"):
+            raise RuntimeError("LAMMPS mode with ghost atoms needs lmp_data with forward_exchange")
+        col = torch.zeros(ntotal, 1, dtype=like.dtype, device=like.device)
+        col[:nlocal, 0] = torch.arange(nlocal, device=like.device, dtype=like.dtype)
+        out = torch.empty_like(col)
+        lmp_data.forward_exchange(col, out, 1)
+        owner = out[:, 0].round().long()
+        owner[:nlocal] = ids[:nlocal]
+        if bool(((owner < 0) | (owner >= nlocal)).any()):
+            raise RuntimeError("ghost exchange returned owners outside the local atoms (a multi-domain run: the "
+                               "MI355X path covers one LAMMPS domain)")
+        return owner
+
+    def _forward_lammps(self, data: Dict[str, torch.Tensor]) -> Dict[str, Optional[torch.Tensor]]:
+        """LAMMPS ML-IAP mode (``adapter.py:286-312``, ``mliap.py:113-151``):
+        LAMMPS supplies pair vectors ``edge_vector`` [E, 3] for edges
+        ``edge_index`` = [neighbour j, local i] over nlocal + nghosts atoms
+        (``natoms``); returns the local energies and ``edge_forces`` =
+        dE/d(edge_vector).  A ghost atom's features equal its owner's in every
+        layer (the reference's per-layer ghost exchange), so each ghost sender
+        is replaced by its owner and the graph is the periodic one on the
+        local atoms; the gradients the exchange's reverse pass would sum into
+        the owners are summed there by the sender CSR."""
+        nlocal, nghosts = (int(v) for v in data["natoms"])
+        vec = data["edge_vector"]
+        if not vec.is_cuda:
+            raise RuntimeError("tace_amd.TensorModel runs on the GPU only (edge_vector is on %s)" % vec.device)
+        if not vec.requires_grad:
+            vec = vec.detach().requires_grad_(True)
+        ei = data["edge_index"]
+        if ei.numel() and int(ei[1].max()) >= nlocal:
+            raise ValueError("LAMMPS mode: every edge's receiver (edge_index[1]) must be a local atom")
+        owner = self._ghost_owners(data.get("lmp_data"), nlocal, nghosts, vec)
+        ei = torch.stack([owner[ei[0]], ei[1]])
+        attrs = data["node_attrs"][:nlocal]
+        d = dict(node_attrs=attrs, edge_index=ei, batch=data["batch"][:nlocal], ptr=data["ptr"])
+        plan = ops.EdgePlan.from_edge_index(ei, nlocal)
+        E, e_node = self.readout_fn.energy(d, plan, vec)
+        out: Dict[str, Optional[torch.Tensor]] = dict(energy=E.detach(), node_energy=e_node.detach(), forces=None,
+                                                      stress=None, virials=None, edge_forces=None)
+        if self.flags.compute_edge_forces:
+            (g,) = torch.autograd.grad(E, [vec], grad_outputs=torch.ones_like(E), allow_unused=True)
+            out["edge_forces"] = torch.zeros_like(vec) if g is None else g  # dE/dr_ij, as LAMMPS expects
+        return out
+
     def forward(self, data: Dict[str, torch.Tensor]) -> Dict[str, Optional[torch.Tensor]]:
+        if self.lmp or ("edge_vector" in data and "natoms" in data):
+            return self._forward_lammps(data)
         tp = set(self.get_target_property())
         want_f = "forces" in tp
         want_s = bool({"stress", "virials"} & tp)

@@ -807,6 +807,19 @@ def set_tece_channel_mixing(model: torch.nn.Module, dtype: Optional[torch.dtype]
     return n
 
 
+def _atomic_virials(vec, edge_forces, edge_index, lattice, batch, n_nodes):
+    """``compute_atomic_virials_stresses`` (``tace/models/utils.py:82-115``):
+    each edge's f (x) r split half to its sender and half to its receiver,
+    symmetrised and negated; stresses = -virials / cell volume."""
+    ev = edge_forces.unsqueeze(-1) * vec.unsqueeze(-2)  # [E, 3, 3], f_i r_j
+    av = torch.zeros(n_nodes, 3, 3, dtype=vec.dtype, device=vec.device)
+    av.index_add_(0, edge_index[0], ev).index_add_(0, edge_index[1], ev)
+    av = -0.5 * (av + av.transpose(-1, -2)) / 2
+    vol = torch.linalg.det(lattice).abs()
+    st = -av / vol[batch].view(-1, 1, 1)
+    return av, torch.where(st.abs() < 1e10, st, torch.zeros_like(st))
+
+
 class TensorModel(torch.nn.Module):
     """``TensorModel`` (``tace/models/adapter.py:23-452``) for energy, forces,
     stress/virials: ``forward(data) -> {energy, node_energy, forces, stress, virials}``."""
@@ -912,10 +925,11 @@ class TensorModel(torch.nn.Module):
         tp = set(self.get_target_property())
         want_f = "forces" in tp
         want_s = bool({"stress", "virials"} & tp)
+        want_e = bool({"edge_forces", "atomic_virials", "atomic_stresses"} & tp)
         pos = data["positions"]
         if not pos.is_cuda:
             raise RuntimeError("tace_amd.TensorModel runs on the GPU only (positions are on %s)" % pos.device)
-        pos = pos.detach().requires_grad_(want_f or want_s)
+        pos = pos.detach().requires_grad_(want_f or want_s or want_e)
         lattice, batch = data["lattice"], data["batch"]
         num_graphs = data["ptr"].numel() - 1
         inputs = [pos] if want_f else []
@@ -940,6 +954,8 @@ class TensorModel(torch.nn.Module):
         E, e_node = self.readout_fn.energy(data, plan, vec)
         out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, stress=None,
                                                       virials=None)
+        if want_e:
+            inputs.append(vec)
         if inputs:
             grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True)
             k = 0
@@ -952,6 +968,11 @@ class TensorModel(torch.nn.Module):
                 S = -V / vol
                 out["virials"] = V
                 out["stress"] = torch.where(S.abs() < 1e10, S, torch.zeros_like(S))
+            if want_e:
+                ef = grads[-1] if grads[-1] is not None else torch.zeros_like(vec)
+                out["edge_forces"] = ef
+                out["atomic_virials"], out["atomic_stresses"] = _atomic_virials(vec.detach(), ef, ei, lattice, batch,
+                                                                                pos.shape[0])
         out["energy"] = out["energy"].detach()
         out["node_energy"] = out["node_energy"].detach()
         return out

@@ -106,3 +106,45 @@ def test_lammps_mode_rejects_ghost_receivers(cuda):
     model.flags.compute_edge_forces = True
     with pytest.raises(ValueError):
         model(lmp)
+
+
+def test_atomic_virials_sum_to_the_virial(cuda):
+    """Per-atom virials (utils.py:82-115) from the edge forces add up to the
+    strain-derivative virial of each structure, and the edge forces are the
+    oracle's dE/d(edge vector)."""
+    rng = np.random.default_rng(21)
+    structs = [structures.random_crystal(rng, int(rng.integers(6, 14)), [3, 8, 26]) for _ in range(2)]
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], 5.0) for s in structs]
+    zs = sorted({int(z) for s in structs for z in s["numbers"]})
+    nat = sum(len(s["positions"]) for s in structs)
+    cfg = configs.model_cfg("si64", zs, sum(e[0].shape[1] for e in edges) / nat, num_channel=16)
+    torch.manual_seed(2)
+    ref = om.TACE(cfg).double()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    try:
+        model = pm.create_model(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    pm.load_reference_state_dict(model.readout_fn, ref.state_dict())
+    model = model.to(cuda)
+    model.reset_target_property(["energy", "forces", "virials", "atomic_virials", "atomic_stresses"])
+    d = data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float64, device=cuda)
+    out = model(d)
+    av = out["atomic_virials"].cpu()
+    V = out["virials"].cpu()
+    b = d["batch"].cpu()
+    for g in range(len(structs)):
+        Vg = av[b == g].sum(0)
+        assert (Vg - V[g]).abs().max().item() < 1e-9 * max(1.0, V[g].abs().max().item()), (Vg, V[g])
+    assert (av - av.transpose(-1, -2)).abs().max().item() == 0.0
+    # edge forces against the oracle
+    d64 = data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float64)
+    src, dst = d64["edge_index"]
+    vec = (d64["positions"][dst] - d64["positions"][src]
+           + torch.einsum("ni,nij->nj", d64["edge_shifts"], d64["lattice"][d64["batch"][src]])).requires_grad_(True)
+    n = d64["node_attrs"].shape[0]
+    E0, _ = ref.energy(d64["node_attrs"], d64["edge_index"], vec, (vec ** 2).sum(1, keepdim=True).sqrt() + 1e-9,
+                       d64["batch"], d64["ptr"], 2)
+    (gv,) = torch.autograd.grad(E0.sum(), vec)
+    assert (out["edge_forces"].cpu() - gv).abs().max().item() < 1e-8

@@ -34,6 +34,9 @@ def cases():
         "fcc1024": dict(structs=lambda: [structures.fcc_alloy(seed=1)], preset="fcc1024", stress=False, over={}),
         "water375": dict(structs=lambda: [structures.water_box(n_side=5, box=49.7 / 16 * 5, seed=2)],
                          preset="water12k", stress=False, over={}),
+        # config-5 architecture (TECE) on a 128-atom bcc Fe slice
+        "fe128_tece": dict(structs=lambda: [structures.bcc_fe(reps=(4, 4, 4), seed=3)], preset="tece", stress=False,
+                           over={}),
     }
 
 

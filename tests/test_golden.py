@@ -42,7 +42,8 @@ def test_oracle_reproduces_si64_golden():
 
 @pytest.mark.gpu
 @pytest.mark.parametrize("name,dtype", [("fcc1024", torch.float32), ("fcc1024", torch.float64),
-                                        ("water375", torch.float32)])
+                                        ("water375", torch.float32), ("fe128_tece", torch.float32),
+                                        ("fe128_tece", torch.float64)])
 def test_gpu_model_matches_golden(cuda, name, dtype):
     from tace_amd import data
 

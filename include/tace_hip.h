@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 9
+#define TACE_HIP_ABI_VERSION 10
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -152,6 +152,10 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"
  * orders them m = 0 (l = 0..lmax), then per m = 1..lmax the +m rows and the
  * -m rows (tace/models/o2/wigner.py:38-66).
+ * Edge features with ch channels are passed in the SO(2) block layout, as an
+ * array of lmax+1 block pointers: block 0 is [E, (lmax+1) ch] (the m = 0
+ * rows), block m is [2E, (lmax+1-m) ch] with row 2e the +m rows and row 2e+1
+ * the -m rows of edge e -- each block is one SO(2)-linear GEMM operand.
  *   tace_edge_wigner_fwd/_bwd   WignerD.get_wigner (o2/wigner.py:231-239) with
  *                               init_edge_rot_mat_quaternion (o2/rotation_matrix.py:74-88):
  *                               wigner [E, K, K] (row = m-layout component,
@@ -163,11 +167,12 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  *                               x [n_rows, K, C] node features (l layout),
  *                               rows_src / rows_dst (int64) the feature rows of
  *                               each edge's ends; m = W [x_src | x_dst] is
- *                               written as m_src = m[:, :, :C], m_dst =
- *                               m[:, :, C:] ([E, K, C] each) and, given
+ *                               written as the block arrays m_src (first C
+ *                               channels) and m_dst (last C) and, given
  *                               radial_w [E, ncomp, 2C] (ncomp = (lmax+1)
  *                               (lmax+2)/2 components, shared by the +m and -m
- *                               rows), m_w = radial_w[comp(r)] m [E, K, 2C].
+ *                               rows), m_w = radial_w[comp(r)] m with 2C
+ *                               channels.
  *                               Rows outside [0, n_rows) read as zeros.  bwd
  *                               (absent output gradients = zero): per-edge
  *                               g_x_src, g_x_dst [E, K, C] (the caller sums
@@ -175,8 +180,7 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  *                               if g_radial_w is given, g_radial_w.
  *   tace_tece_score_fwd/_bwd    OAM20260705Convolution._complex_qk_attention
  *                               (_e3nn/archive/oam_2026_07_05.py:699-754): q, k
- *                               [E, K, C] in the m layout with the default
- *                               (lmax+1-m) components per m, radial_proj [E, 2H]
+ *                               block arrays with C channels, radial_proj [E, 2H]
  *                               (bias | phase logits), tscale[H] = attention
  *                               scale x temperature -> score [E, H]; the
  *                               per-head width C/H divides 64 or is a
@@ -198,7 +202,8 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  *   tace_tece_rotate_out_fwd/_bwd
  *                               alpha-weighted wigner_inv product and
  *                               scatter_sum to receivers
- *                               (oam_2026_07_05.py:799-823): m [E, K, C] ->
+ *                               (oam_2026_07_05.py:799-823): m (block array,
+ *                               C channels) ->
  *                               out in the group-major layout of C x (0..lmax)
  *                               at rows node_map[n]; bwd (per edge, dst[e] =
  *                               receiver node id, int64) gives g_m, g_alpha
@@ -208,16 +213,20 @@ int tace_edge_wigner_bwd(int dtype, const void* vec, const void* g_wigner, int64
                          void* g_vec, void* stream);
 int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
                             const int64_t* rows_dst, const void* radial_w, int64_t n_rows, int64_t n_edges,
-                            int32_t lmax, int32_t channels, void* m_src, void* m_dst, void* m_w, void* stream);
+                            int32_t lmax, int32_t channels, const void* const* m_src, const void* const* m_dst,
+                            const void* const* m_w, void* stream);
 int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
-                            const int64_t* rows_dst, const void* radial_w, const void* g_m_src, const void* g_m_dst,
-                            const void* g_m_w, int64_t n_rows, int64_t n_edges, int32_t lmax, int32_t channels,
-                            void* g_x_src, void* g_x_dst, void* g_wigner, void* g_radial_w, void* stream);
-int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
-                        int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, void* score, void* stream);
-int tace_tece_score_bwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
-                        const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
-                        void* g_q, void* g_k, void* g_radial_proj, void* stream);
+                            const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
+                            const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows, int64_t n_edges,
+                            int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst, void* g_wigner,
+                            void* g_radial_w, void* stream);
+int tace_tece_score_fwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
+                        const void* tscale, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
+                        void* score, void* stream);
+int tace_tece_score_bwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
+                        const void* tscale, const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels,
+                        int32_t heads, const void* const* g_q, const void* const* g_k, void* g_radial_proj,
+                        void* stream);
 int tace_tece_edge_ace_fwd(int dtype, const void* y0, const void* y1, const void* y2, const void* y3,
                            int64_t n_edges, int32_t lmax, int32_t hidden, void* o0, void* o1, void* o2, void* o3,
                            void* stream);
@@ -229,13 +238,13 @@ int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, 
                            int32_t heads, void* alpha, void* stream);
 int tace_graph_softmax_bwd(int dtype, const void* alpha, const void* g_alpha, const int32_t* rowptr,
                            const int32_t* eid, int64_t n_nodes, int32_t heads, void* g_score, void* stream);
-int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const void* wigner, const int32_t* rowptr,
-                             const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int32_t lmax,
-                             int32_t channels, int32_t heads, void* out, void* stream);
-int tace_tece_rotate_out_bwd(int dtype, const void* m, const void* alpha, const void* wigner, const void* g_out,
-                             const int64_t* dst, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
-                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha,
-                             void* g_wigner, void* stream);
+int tace_tece_rotate_out_fwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
+                             const int32_t* rowptr, const int32_t* eid, const int32_t* node_map, int64_t n_nodes,
+                             int32_t lmax, int32_t channels, int32_t heads, void* out, void* stream);
+int tace_tece_rotate_out_bwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
+                             const void* g_out, const int64_t* dst, const int32_t* node_map, int64_t n_nodes,
+                             int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, const void* const* g_m,
+                             void* g_alpha, void* g_wigner, void* stream);
 
 /* ---- neighbour list (float64 positions, host cell[9] rows = lattice
  * vectors, host pbc[3]).  Edge (src=i, dst=j, S) exists iff

@@ -293,6 +293,46 @@ __device__ __forceinline__ bool head_sum(T* v, T* run, int j, int Ch, int lane) 
   return lane == 0;
 }
 
+// ------------------------------------------------------ SO(2) block layout --
+// Edge features of the convolution are kept as one 2-D GEMM operand per m
+// (the "block layout"): block 0 is [E, (L+1) ch] (rows l = 0..L of m = 0) and
+// block m > 0 is [2E, (L+1-m) ch], GEMM row 2e holding the +m rows of edge e
+// and row 2e+1 its -m rows.  Row r of an edge's m layout (m = 0 rows, then per
+// m the +m rows and the -m rows) is block mblk(r), local row mloc(r) of the
+// edge's mrows(b) rows.  Kernels take the L+1 block pointers by value.
+template <typename T>
+struct Blk {
+  T* p[4];
+};
+
+template <int L>
+__device__ __forceinline__ constexpr int mblk(int r) {
+  if (r <= L) return 0;
+  int off = L + 1;
+  for (int m = 1; m <= L; ++m) {
+    if (r < off + 2 * (L + 1 - m)) return m;
+    off += 2 * (L + 1 - m);
+  }
+  return -1;
+}
+
+template <int L>
+__device__ __forceinline__ constexpr int mstart(int b) {
+  int off = 0;
+  for (int m = 0; m < b; ++m) off += m == 0 ? L + 1 : 2 * (L + 1 - m);
+  return off;
+}
+
+template <int L>
+__device__ __forceinline__ constexpr int mrows(int b) { return b == 0 ? L + 1 : 2 * (L + 1 - b); }
+
+// pointer to row r of edge e (channel 0) in a block array with `ch` channels
+template <int L, typename T>
+__device__ __forceinline__ T* erow(const Blk<T>& B, int64_t e, int r, int ch) {
+  const int b = mblk<L>(r);
+  return B.p[b] + (e * mrows<L>(b) + (r - mstart<L>(b))) * (int64_t)ch;
+}
+
 // -------------------------------------------------------------- QK score --
 // score[e,h] = (S0 + sum_m cos(m phi) A_m + sin(m phi) B_m) * tscale[h] + rp[e,h],
 // phi = pi tanh(rp[e, H+h]);  S0 = sum over the m = 0 rows of q.k,
@@ -307,16 +347,14 @@ __device__ __forceinline__ int m_rows_start(int m) {
 }
 
 template <typename T, int L, int NS>
-__global__ __launch_bounds__(256) void k_score_fwd(const T* __restrict__ q, const T* __restrict__ k,
+__global__ __launch_bounds__(256) void k_score_fwd(const Blk<const T> q, const Blk<const T> k,
                                                    const T* __restrict__ rp, const T* __restrict__ tscale,
                                                    int64_t E, int C, int H, T* __restrict__ score) {
-  constexpr int K = (L + 1) * (L + 1), V = 1 + 2 * L;
+  constexpr int V = 1 + 2 * L;
   const int64_t e = wave_edge();
   if (e >= E) return;
   const int lane = (int)threadIdx.x & 63;
   const int Ch = C / H;
-  const T* qe = q + e * K * C;
-  const T* ke = k + e * K * C;
   T run[V];
 #pragma unroll
   for (int i = 0; i < V; ++i) run[i] = T(0);
@@ -329,14 +367,14 @@ __global__ __launch_bounds__(256) void k_score_fwd(const T* __restrict__ q, cons
     for (int i = 0; i < V; ++i) v[i] = T(0);
     if (c < C) {
 #pragma unroll
-      for (int r = 0; r <= L; ++r) v[0] += qe[r * C + c] * ke[r * C + c];
+      for (int r = 0; r <= L; ++r) v[0] += erow<L>(q, e, r, C)[c] * erow<L>(k, e, r, C)[c];
 #pragma unroll
       for (int m = 1; m <= L; ++m) {
         const int re = m_rows_start<L>(m), n = L + 1 - m;
 #pragma unroll
         for (int i = 0; i < n; ++i) {
-          const T qr = qe[(re + i) * C + c], qi = qe[(re + n + i) * C + c];
-          const T kr = ke[(re + i) * C + c], ki = ke[(re + n + i) * C + c];
+          const T qr = erow<L>(q, e, re + i, C)[c], qi = erow<L>(q, e, re + n + i, C)[c];
+          const T kr = erow<L>(k, e, re + i, C)[c], ki = erow<L>(k, e, re + n + i, C)[c];
           v[2 * m - 1] += qr * kr + qi * ki;
           v[2 * m] += qi * kr - qr * ki;
         }
@@ -354,16 +392,14 @@ __global__ __launch_bounds__(256) void k_score_fwd(const T* __restrict__ q, cons
 }
 
 template <typename T, int L, int NS>
-__global__ __launch_bounds__(256) void k_score_bwd(const T* __restrict__ q, const T* __restrict__ k,
+__global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const Blk<const T> k,
                                                    const T* __restrict__ rp, const T* __restrict__ tscale,
                                                    const T* __restrict__ gs, int64_t E, int C, int H,
-                                                   T* __restrict__ gq, T* __restrict__ gk, T* __restrict__ grp) {
-  constexpr int K = (L + 1) * (L + 1);
+                                                   const Blk<T> gq, const Blk<T> gk, T* __restrict__ grp) {
   const int64_t e = wave_edge();
   if (e >= E) return;
   const int lane = (int)threadIdx.x & 63;
   const int Ch = C / H;
-  const int64_t base = e * K * C;
   T run[1] = {T(0)};
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
@@ -379,10 +415,9 @@ __global__ __launch_bounds__(256) void k_score_bwd(const T* __restrict__ q, cons
     if (act) {
 #pragma unroll
       for (int r = 0; r <= L; ++r) {
-        const int64_t i = base + r * C + c;
-        const T qv = q[i], kv = k[i];
-        gq[i] = G * kv;
-        gk[i] = G * qv;
+        const T qv = erow<L>(q, e, r, C)[c], kv = erow<L>(k, e, r, C)[c];
+        erow<L>(gq, e, r, C)[c] = G * kv;
+        erow<L>(gk, e, r, C)[c] = G * qv;
       }
 #pragma unroll
       for (int m = 1; m <= L; ++m) {
@@ -391,14 +426,15 @@ __global__ __launch_bounds__(256) void k_score_bwd(const T* __restrict__ q, cons
         T A = 0, B = 0;
 #pragma unroll
         for (int i = 0; i < n; ++i) {
-          const int64_t ir = base + (re + i) * C + c, ii = base + (re + n + i) * C + c;
-          const T qr = q[ir], qi = q[ii], kr = k[ir], ki = k[ii];
+          const int ir = re + i, ii = re + n + i;
+          const T qr = erow<L>(q, e, ir, C)[c], qi = erow<L>(q, e, ii, C)[c];
+          const T kr = erow<L>(k, e, ir, C)[c], ki = erow<L>(k, e, ii, C)[c];
           A += qr * kr + qi * ki;
           B += qi * kr - qr * ki;
-          gq[ir] = G * (cs * kr - sn * ki);
-          gq[ii] = G * (cs * ki + sn * kr);
-          gk[ir] = G * (cs * qr + sn * qi);
-          gk[ii] = G * (cs * qi - sn * qr);
+          erow<L>(gq, e, ir, C)[c] = G * (cs * kr - sn * ki);
+          erow<L>(gq, e, ii, C)[c] = G * (cs * ki + sn * kr);
+          erow<L>(gk, e, ir, C)[c] = G * (cs * qr + sn * qi);
+          erow<L>(gk, e, ii, C)[c] = G * (cs * qi - sn * qr);
         }
         d[0] += T(m) * (cs * B - sn * A);
       }
@@ -439,8 +475,8 @@ template <typename T, int L, int NS>
 __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, const T* __restrict__ W,
                                                    const int64_t* __restrict__ rows_src,
                                                    const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
-                                                   int64_t n_rows, int64_t E, int C, T* __restrict__ ms,
-                                                   T* __restrict__ md, T* __restrict__ mw) {
+                                                   int64_t n_rows, int64_t E, int C, const Blk<T> ms,
+                                                   const Blk<T> md, const Blk<T> mw) {
   constexpr int K = (L + 1) * (L + 1), NC = (L + 1) * (L + 2) / 2;
   const int64_t e = wave_edge();
   if (e >= E) return;
@@ -460,14 +496,13 @@ __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, cons
     const bool ok = row >= 0 && row < n_rows;
 #pragma unroll
     for (int kk = 0; kk < K; ++kk) xk[kk] = ok ? x[(row * K + kk) * C + cc] : T(0);
-    T* out = src ? ms : md;
 #pragma unroll
     for (int r = 0; r < K; ++r) {
       T a = 0;
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) a += w[r * K + kk] * xk[kk];
-      out[(e * K + r) * C + cc] = a;
-      if (wr) mw[(e * K + r) * C2 + c] = wr[(e * NC + m_comp<L>(r)) * C2 + c] * a;
+      erow<L>(src ? ms : md, e, r, C)[cc] = a;
+      if (wr) erow<L>(mw, e, r, C2)[c] = wr[(e * NC + m_comp<L>(r)) * C2 + c] * a;
     }
   }
 }
@@ -497,8 +532,8 @@ template <typename T, int L, int NS>
 __global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, const T* __restrict__ W,
                                                    const int64_t* __restrict__ rows_src,
                                                    const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
-                                                   const T* __restrict__ gms, const T* __restrict__ gmd,
-                                                   const T* __restrict__ gmw, int64_t n_rows, int64_t E, int C,
+                                                   const Blk<const T> gms, const Blk<const T> gmd,
+                                                   const Blk<const T> gmw, int64_t n_rows, int64_t E, int C,
                                                    T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
                                                    T* __restrict__ gwr) {
   constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16, NC = (L + 1) * (L + 2) / 2;
@@ -520,19 +555,19 @@ __global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, cons
       const int64_t row = src ? rs : rd;
       const int cc = src ? c : c - C;
       const bool ok = row >= 0 && row < n_rows;
-      const T* gsd = src ? gms : gmd;
+      const Blk<const T>& gsd = src ? gms : gmd;
       T xk[K], g[K];
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) xk[kk] = ok ? x[(row * K + kk) * C + cc] : T(0);
 #pragma unroll
-      for (int r = 0; r < K; ++r) g[r] = gsd ? gsd[(e * K + r) * C + cc] : T(0);
-      if (gmw) {
+      for (int r = 0; r < K; ++r) g[r] = gsd.p[mblk<L>(r)] ? erow<L>(gsd, e, r, C)[cc] : T(0);
+      if (wr) {
         T gc[NC];
 #pragma unroll
         for (int q = 0; q < NC; ++q) gc[q] = T(0);
 #pragma unroll
         for (int r = 0; r < K; ++r) {
-          const T gr = gmw[(e * K + r) * C2 + c];
+          const T gr = gmw.p[mblk<L>(r)] ? erow<L>(gmw, e, r, C2)[c] : T(0);
           const int q = m_comp<L>(r);
           g[r] += wr[(e * NC + q) * C2 + c] * gr;
           T mv = 0;
@@ -830,7 +865,7 @@ __global__ __launch_bounds__(256) void k_softmax_bwd(const T* __restrict__ alpha
 // written group-major (block l of the batch = [N, 2l+1, C] at N*C*l^2) at
 // feature row map[n].  One workgroup per receiver, one lane per channel.
 template <typename T, int L>
-__global__ __launch_bounds__(512) void k_rotout_fwd(const T* __restrict__ m, const T* __restrict__ alpha,
+__global__ __launch_bounds__(512) void k_rotout_fwd(const Blk<const T> m, const T* __restrict__ alpha,
                                                     const T* __restrict__ W, const int* __restrict__ rowptr,
                                                     const int* __restrict__ eid, const int* __restrict__ map,
                                                     int N, int C, int H, T* __restrict__ out) {
@@ -846,10 +881,9 @@ __global__ __launch_bounds__(512) void k_rotout_fwd(const T* __restrict__ m, con
     const int64_t e = eid ? eid[i] : i;
     const T a = alpha[e * H + h];
     const T* w = W + e * K * K;
-    const T* me = m + e * K * C + c;
     T v[K];
 #pragma unroll
-    for (int r = 0; r < K; ++r) v[r] = a * me[(int64_t)r * C];
+    for (int r = 0; r < K; ++r) v[r] = a * erow<L>(m, e, r, C)[c];
 #pragma unroll
     for (int r = 0; r < K; ++r)
 #pragma unroll
@@ -871,10 +905,10 @@ __global__ __launch_bounds__(512) void k_rotout_fwd(const T* __restrict__ m, con
 //   g_alpha[e,h] = sum over the head's channels and rows of m[e,r,c] t[r];
 //   g_W[e,r,k] = sum_c alpha[e,h(c)] m[e,r,c] g[n,k,c].
 template <typename T, int L, int NS>
-__global__ __launch_bounds__(256) void k_rotout_bwd(const T* __restrict__ m, const T* __restrict__ alpha,
+__global__ __launch_bounds__(256) void k_rotout_bwd(const Blk<const T> m, const T* __restrict__ alpha,
                                                     const T* __restrict__ W, const T* __restrict__ gout,
                                                     const int64_t* __restrict__ dst, const int* __restrict__ map,
-                                                    int N, int64_t E, int C, int H, T* __restrict__ gm,
+                                                    int N, int64_t E, int C, int H, const Blk<T> gm,
                                                     T* __restrict__ galpha, T* __restrict__ gW) {
   constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16;
   const int64_t e = wave_edge();
@@ -912,8 +946,8 @@ __global__ __launch_bounds__(256) void k_rotout_bwd(const T* __restrict__ m, con
         T t = 0;
 #pragma unroll
         for (int kk = 0; kk < K; ++kk) t += w[r * K + kk] * g[kk];
-        const T mv = m[(e * K + r) * C + c];
-        gm[(e * K + r) * C + c] = a * t;
+        const T mv = erow<L>(m, e, r, C)[c];
+        erow<L>(gm, e, r, C)[c] = a * t;
         v[0] += mv * t;
         const T am = a * mv;
 #pragma unroll
@@ -926,6 +960,23 @@ __global__ __launch_bounds__(256) void k_rotout_bwd(const T* __restrict__ m, con
 }
 
 // ------------------------------------------------------------------ C ABI --
+// block arrays: lmax+1 pointers (block 0, then m = 1..lmax); entries past
+// lmax are ignored
+template <typename T>
+static Blk<T> blocks_of(const void* const* a, int lmax) {
+  Blk<T> b{{nullptr, nullptr, nullptr, nullptr}};
+  if (a)
+    for (int m = 0; m <= lmax && m < 4; ++m) b.p[m] = (T*)a[m];
+  return b;
+}
+
+static bool blocks_ok(const void* const* a, int lmax) {
+  if (!a) return false;
+  for (int m = 0; m <= lmax; ++m)
+    if (!a[m]) return false;
+  return true;
+}
+
 extern "C" {
 
 int tace_edge_wigner_fwd(int dtype, const void* vec, int64_t n_edges, int32_t lmax, void* wigner, void* stream) {
@@ -979,17 +1030,20 @@ static int score_checks(const char* who, int64_t E, int32_t lmax, int32_t C, int
 
 static dim3 wave_grid(int64_t E) { return dim3((unsigned)((E + 3) / 4)); }
 
-int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
-                        int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, void* score, void* stream) {
+int tace_tece_score_fwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
+                        const void* tscale, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
+                        void* score, void* stream) {
   if (score_checks("tace_tece_score_fwd", n_edges, lmax, channels, heads)) return -1;
   if (n_edges == 0) return 0;
-  if (!q || !k || !radial_proj || !tscale || !score) return tace_fail_msg("tace_tece_score_fwd: null pointer");
+  if (!blocks_ok(q, lmax) || !blocks_ok(k, lmax) || !radial_proj || !tscale || !score)
+    return tace_fail_msg("tace_tece_score_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
 #define SC_F(TT, LL)                                                                                            \
   TACE_SLOTS_DISPATCH(channels, NS,                                                                             \
-    hipLaunchKernelGGL((k_score_fwd<TT, LL, NS>), g, b, 0, s, (const TT*)q, (const TT*)k, (const TT*)radial_proj, \
-                       (const TT*)tscale, n_edges, channels, heads, (TT*)score))
+    hipLaunchKernelGGL((k_score_fwd<TT, LL, NS>), g, b, 0, s, blocks_of<const TT>(q, lmax),                 \
+                       blocks_of<const TT>(k, lmax), (const TT*)radial_proj, (const TT*)tscale, n_edges, channels, \
+                       heads, (TT*)score))
   if (dtype == TACE_F32) {
     if (lmax == 1) { SC_F(float, 1) } else if (lmax == 2) { SC_F(float, 2) } else { SC_F(float, 3) }
   } else if (dtype == TACE_F64) {
@@ -1001,20 +1055,23 @@ int tace_tece_score_fwd(int dtype, const void* q, const void* k, const void* rad
   return tace_check_launch("tace_tece_score_fwd");
 }
 
-int tace_tece_score_bwd(int dtype, const void* q, const void* k, const void* radial_proj, const void* tscale,
-                        const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
-                        void* g_q, void* g_k, void* g_radial_proj, void* stream) {
+int tace_tece_score_bwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
+                        const void* tscale, const void* g_score, int64_t n_edges, int32_t lmax, int32_t channels,
+                        int32_t heads, const void* const* g_q, const void* const* g_k, void* g_radial_proj,
+                        void* stream) {
   if (score_checks("tace_tece_score_bwd", n_edges, lmax, channels, heads)) return -1;
   if (n_edges == 0) return 0;
-  if (!q || !k || !radial_proj || !tscale || !g_score || !g_q || !g_k || !g_radial_proj)
+  if (!blocks_ok(q, lmax) || !blocks_ok(k, lmax) || !radial_proj || !tscale || !g_score || !blocks_ok(g_q, lmax) ||
+      !blocks_ok(g_k, lmax) || !g_radial_proj)
     return tace_fail_msg("tace_tece_score_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
 #define SC_B(TT, LL)                                                                                            \
   TACE_SLOTS_DISPATCH(channels, NS,                                                                             \
-    hipLaunchKernelGGL((k_score_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)q, (const TT*)k, (const TT*)radial_proj, \
-                       (const TT*)tscale, (const TT*)g_score, n_edges, channels, heads, (TT*)g_q, (TT*)g_k,      \
-                       (TT*)g_radial_proj))
+    hipLaunchKernelGGL((k_score_bwd<TT, LL, NS>), g, b, 0, s, blocks_of<const TT>(q, lmax),                 \
+                       blocks_of<const TT>(k, lmax), (const TT*)radial_proj, (const TT*)tscale,              \
+                       (const TT*)g_score, n_edges, channels, heads, blocks_of<TT>(g_q, lmax),               \
+                       blocks_of<TT>(g_k, lmax), (TT*)g_radial_proj))
   if (dtype == TACE_F32) {
     if (lmax == 1) { SC_B(float, 1) } else if (lmax == 2) { SC_B(float, 2) } else { SC_B(float, 3) }
   } else if (dtype == TACE_F64) {
@@ -1037,18 +1094,20 @@ static int rotin_checks(const char* who, int64_t n_rows, int64_t E, int32_t lmax
 
 int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
                             const int64_t* rows_dst, const void* radial_w, int64_t n_rows, int64_t n_edges,
-                            int32_t lmax, int32_t channels, void* m_src, void* m_dst, void* m_w, void* stream) {
+                            int32_t lmax, int32_t channels, const void* const* m_src, const void* const* m_dst,
+                            const void* const* m_w, void* stream) {
   if (rotin_checks("tace_edge_rotate_in_fwd", n_rows, n_edges, lmax, channels)) return -1;
   if (n_edges == 0) return 0;
-  if (!x || !wigner || !rows_src || !rows_dst || !m_src || !m_dst || (radial_w && !m_w))
+  if (!x || !wigner || !rows_src || !rows_dst || !blocks_ok(m_src, lmax) || !blocks_ok(m_dst, lmax) ||
+      (radial_w && !blocks_ok(m_w, lmax)))
     return tace_fail_msg("tace_edge_rotate_in_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
 #define RI_F(TT, LL)                                                                                        \
   TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                     \
     hipLaunchKernelGGL((k_rotin_fwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,   \
-                       rows_dst, (const TT*)radial_w, n_rows, n_edges, channels, (TT*)m_src, (TT*)m_dst,   \
-                       (TT*)m_w))
+                       rows_dst, (const TT*)radial_w, n_rows, n_edges, channels, blocks_of<TT>(m_src, lmax), \
+                       blocks_of<TT>(m_dst, lmax), blocks_of<TT>(radial_w ? m_w : nullptr, lmax)))
   if (dtype == TACE_F32) {
     if (lmax == 1) { RI_F(float, 1) } else if (lmax == 2) { RI_F(float, 2) } else { RI_F(float, 3) }
   } else if (dtype == TACE_F64) {
@@ -1061,9 +1120,10 @@ int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const 
 }
 
 int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
-                            const int64_t* rows_dst, const void* radial_w, const void* g_m_src, const void* g_m_dst,
-                            const void* g_m_w, int64_t n_rows, int64_t n_edges, int32_t lmax, int32_t channels,
-                            void* g_x_src, void* g_x_dst, void* g_wigner, void* g_radial_w, void* stream) {
+                            const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
+                            const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows, int64_t n_edges,
+                            int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst, void* g_wigner,
+                            void* g_radial_w, void* stream) {
   if (rotin_checks("tace_edge_rotate_in_bwd", n_rows, n_edges, lmax, channels)) return -1;
   if (n_edges == 0) return 0;
   if (!x || !wigner || !rows_src || !rows_dst || !g_x_src || !g_x_dst || !g_wigner || (g_m_w && !radial_w))
@@ -1073,9 +1133,9 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
 #define RI_B(TT, LL)                                                                                          \
   TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                       \
     hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,     \
-                       rows_dst, (const TT*)radial_w, (const TT*)g_m_src, (const TT*)g_m_dst,                \
-                       (const TT*)g_m_w, n_rows, n_edges, channels, (TT*)g_x_src, (TT*)g_x_dst,              \
-                       (TT*)g_wigner, (TT*)g_radial_w))
+                       rows_dst, (const TT*)radial_w, blocks_of<const TT>(g_m_src, lmax),                   \
+                       blocks_of<const TT>(g_m_dst, lmax), blocks_of<const TT>(g_m_w, lmax), n_rows, n_edges,  \
+                       channels, (TT*)g_x_src, (TT*)g_x_dst, (TT*)g_wigner, (TT*)g_radial_w))
   if (dtype == TACE_F32) {
     if (lmax == 1) { RI_B(float, 1) } else if (lmax == 2) { RI_B(float, 2) } else { RI_B(float, 3) }
   } else if (dtype == TACE_F64) {
@@ -1134,17 +1194,19 @@ static int rotout_checks(const char* who, int64_t N, int32_t lmax, int32_t C, in
   return 0;
 }
 
-int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const void* wigner, const int32_t* rowptr,
+int tace_tece_rotate_out_fwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
+                             const int32_t* rowptr,
                              const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int32_t lmax,
                              int32_t channels, int32_t heads, void* out, void* stream) {
   if (rotout_checks("tace_tece_rotate_out_fwd", n_nodes, lmax, channels, heads)) return -1;
   if (n_nodes == 0) return 0;
   if (!rowptr || !out) return tace_fail_msg("tace_tece_rotate_out_fwd: null pointer");
+  if (!m) return tace_fail_msg("tace_tece_rotate_out_fwd: null block array");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)n_nodes), b((unsigned)((channels + 63) / 64 * 64));
 #define ROT_F(TT, LL)                                                                                           \
-  hipLaunchKernelGGL((k_rotout_fwd<TT, LL>), g, b, 0, s, (const TT*)m, (const TT*)alpha, (const TT*)wigner, rowptr, \
-                     eid, node_map, (int)n_nodes, channels, heads, (TT*)out)
+  hipLaunchKernelGGL((k_rotout_fwd<TT, LL>), g, b, 0, s, blocks_of<const TT>(m, lmax), (const TT*)alpha,      \
+                     (const TT*)wigner, rowptr, eid, node_map, (int)n_nodes, channels, heads, (TT*)out)
   if (dtype == TACE_F32) {
     if (lmax == 1) ROT_F(float, 1); else if (lmax == 2) ROT_F(float, 2); else ROT_F(float, 3);
   } else if (dtype == TACE_F64) {
@@ -1156,22 +1218,22 @@ int tace_tece_rotate_out_fwd(int dtype, const void* m, const void* alpha, const 
   return tace_check_launch("tace_tece_rotate_out_fwd");
 }
 
-int tace_tece_rotate_out_bwd(int dtype, const void* m, const void* alpha, const void* wigner, const void* g_out,
-                             const int64_t* dst, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
-                             int32_t lmax, int32_t channels, int32_t heads, void* g_m, void* g_alpha,
-                             void* g_wigner, void* stream) {
+int tace_tece_rotate_out_bwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
+                             const void* g_out, const int64_t* dst, const int32_t* node_map, int64_t n_nodes,
+                             int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, const void* const* g_m,
+                             void* g_alpha, void* g_wigner, void* stream) {
   if (rotout_checks("tace_tece_rotate_out_bwd", n_nodes, lmax, channels, heads)) return -1;
   if (n_edges < 0) return tace_fail_msg("tace_tece_rotate_out_bwd: negative edge count");
   if (n_edges == 0) return 0;
-  if (!m || !alpha || !wigner || !g_out || !dst || !g_m || !g_alpha || !g_wigner)
+  if (!blocks_ok(m, lmax) || !alpha || !wigner || !g_out || !dst || !blocks_ok(g_m, lmax) || !g_alpha || !g_wigner)
     return tace_fail_msg("tace_tece_rotate_out_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
 #define ROT_B(TT, LL)                                                                                          \
   TACE_SLOTS_DISPATCH(channels, NS,                                                                            \
-    hipLaunchKernelGGL((k_rotout_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)m, (const TT*)alpha,                \
+    hipLaunchKernelGGL((k_rotout_bwd<TT, LL, NS>), g, b, 0, s, blocks_of<const TT>(m, lmax), (const TT*)alpha, \
                        (const TT*)wigner, (const TT*)g_out, dst, node_map, (int)n_nodes, n_edges, channels,   \
-                       heads, (TT*)g_m, (TT*)g_alpha, (TT*)g_wigner))
+                       heads, blocks_of<TT>(g_m, lmax), (TT*)g_alpha, (TT*)g_wigner))
   if (dtype == TACE_F32) {
     if (lmax == 1) { ROT_B(float, 1) } else if (lmax == 2) { ROT_B(float, 2) } else { ROT_B(float, 3) }
   } else if (dtype == TACE_F64) {

@@ -14,6 +14,7 @@ raises if the native library is missing -- there is no CPU path.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -375,50 +376,95 @@ def edge_wigner(vec: torch.Tensor, lmax: int) -> torch.Tensor:
     return _EdgeWigner.apply(vec.contiguous(), int(lmax))
 
 
+def so2_block_shapes(E: int, lmax: int, ch: int) -> List[Tuple[int, int]]:
+    """Shapes of the SO(2) block layout of edge features with ``ch`` channels:
+    block 0 [E, (lmax+1) ch], block m [2E, (lmax+1-m) ch] (row 2e = +m rows of
+    edge e, 2e+1 = its -m rows)."""
+    return [(E, (lmax + 1) * ch)] + [(2 * E, (lmax + 1 - m) * ch) for m in range(1, lmax + 1)]
+
+
+def so2_to_blocks(x: torch.Tensor, lmax: int) -> List[torch.Tensor]:
+    """[E, K, ch] in the m layout -> the SO(2) block layout (copies)."""
+    E, _, ch = x.shape
+    n = lmax + 1
+    out, off = [x[:, :n].reshape(E, n * ch)], n
+    for m in range(1, lmax + 1):
+        k = n - m
+        out.append(x[:, off:off + 2 * k].reshape(2 * E, k * ch))
+        off += 2 * k
+    return out
+
+
+def so2_from_blocks(blocks: Sequence[torch.Tensor], lmax: int) -> torch.Tensor:
+    """The SO(2) block layout -> [E, K, ch] in the m layout."""
+    E = blocks[0].shape[0]
+    n = lmax + 1
+    ch = blocks[0].shape[1] // n
+    return torch.cat([blocks[0].view(E, n, ch)] + [blocks[m].reshape(E, 2 * (n - m), ch)
+                                                   for m in range(1, lmax + 1)], dim=1)
+
+
+def _block_array(blocks) -> "ctypes.Array":
+    ptrs = [None if t is None else t.data_ptr() for t in blocks]
+    return (ctypes.c_void_p * 4)(*(ptrs + [None] * (4 - len(ptrs))))
+
+
+def _req_blocks(blocks, name: str, dt, E: int, lmax: int, ch: int):
+    if len(blocks) != lmax + 1:
+        raise ValueError(f"{name}: {len(blocks)} blocks, expected lmax+1 = {lmax + 1}")
+    for m, (t, shp) in enumerate(zip(blocks, so2_block_shapes(E, lmax, ch))):
+        _req(t, f"{name}[{m}]", dt, shp)
+
+
 class _TeceScore(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, rp, tscale, lmax: int, H: int):
-        E, K, C = q.shape
-        dt = q.dtype
-        if K != (lmax + 1) ** 2:
-            raise ValueError(f"tece_score: {K} component rows, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
-        _req(q, "query", dt, (E, K, C))
-        _req(k, "key", dt, (E, K, C))
+    def forward(ctx, rp, tscale, lmax: int, H: int, C: int, *qk):
+        n = lmax + 1
+        q, k = list(qk[:n]), list(qk[n:])
+        E, dt = rp.shape[0], rp.dtype
+        _req_blocks(q, "query", dt, E, lmax, C)
+        _req_blocks(k, "key", dt, E, lmax, C)
         _req(rp, "radial_proj", dt, (E, 2 * H))
         _req(tscale, "tscale", dt, (H,))
-        s = torch.empty(E, H, dtype=dt, device=q.device)
+        s = torch.empty(E, H, dtype=dt, device=rp.device)
         tok = _t0("tece_score_fwd")
-        N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), q.data_ptr(), k.data_ptr(), rp.data_ptr(),
-                                            tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(q.device)),
+        N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), _block_array(q), _block_array(k), rp.data_ptr(),
+                                            tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(rp.device)),
                 "tace_tece_score_fwd")
-        _t1(tok, (E, K, C, H))
-        ctx.save_for_backward(q, k, rp, tscale)
-        ctx.lmax, ctx.H = lmax, H
+        _t1(tok, (E, n * n, C, H))
+        ctx.save_for_backward(rp, tscale, *q, *k)
+        ctx.lmax, ctx.H, ctx.C = lmax, H, C
         return s
 
     @staticmethod
     def backward(ctx, gs):
-        q, k, rp, tscale = ctx.saved_tensors
-        E, K, C = q.shape
+        rp, tscale, *qk = ctx.saved_tensors
+        n = ctx.lmax + 1
+        q, k = qk[:n], qk[n:]
+        E = rp.shape[0]
         gs = gs.contiguous()
-        gq, gk, grp = torch.empty_like(q), torch.empty_like(k), torch.empty_like(rp)
+        gq, gk = [torch.empty_like(t) for t in q], [torch.empty_like(t) for t in k]
+        grp = torch.empty_like(rp)
         tok = _t0("tece_score_bwd")
-        N.check(N.lib().tace_tece_score_bwd(N.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), rp.data_ptr(),
-                                            tscale.data_ptr(), gs.data_ptr(), E, ctx.lmax, C, ctx.H, gq.data_ptr(),
-                                            gk.data_ptr(), grp.data_ptr(), N.stream_ptr(q.device)),
-                "tace_tece_score_bwd")
-        _t1(tok, (E, K, C, ctx.H))
+        N.check(N.lib().tace_tece_score_bwd(N.dtype_code(rp.dtype), _block_array(q), _block_array(k), rp.data_ptr(),
+                                            tscale.data_ptr(), gs.data_ptr(), E, ctx.lmax, ctx.C, ctx.H,
+                                            _block_array(gq), _block_array(gk), grp.data_ptr(),
+                                            N.stream_ptr(rp.device)), "tace_tece_score_bwd")
+        _t1(tok, (E, n * n, ctx.C, ctx.H))
         # the attention temperature is a model parameter: no gradient on this
         # (inference) path, as the calculators freeze parameters
-        return gq, gk, grp, None, None, None
+        return (grp, None, None, None, None) + tuple(gq) + tuple(gk)
 
 
-def tece_score(q, k, radial_proj, tscale, lmax: int, heads: int) -> torch.Tensor:
-    """Radial-rotary complex QK score [E, heads] (tscale = attention scale x temperature)."""
+def tece_score(q: Sequence[torch.Tensor], k: Sequence[torch.Tensor], radial_proj, tscale, lmax: int,
+               heads: int) -> torch.Tensor:
+    """Radial-rotary complex QK score [E, heads] of query / key in the SO(2)
+    block layout (tscale = attention scale x temperature)."""
     if tscale.requires_grad:
         raise ValueError("tece_score: the temperature gradient is not computed (parameters must be frozen)")
-    return _TeceScore.apply(q.contiguous(), k.contiguous(), radial_proj.contiguous(), tscale.contiguous(),
-                            int(lmax), int(heads))
+    C = q[0].shape[1] // (lmax + 1)
+    return _TeceScore.apply(radial_proj.contiguous(), tscale.contiguous(), int(lmax), int(heads), C,
+                            *[t.contiguous() for t in q], *[t.contiguous() for t in k])
 
 
 class _GraphSoftmax(torch.autograd.Function):
@@ -457,51 +503,53 @@ def graph_softmax(score: torch.Tensor, plan: EdgePlan) -> torch.Tensor:
 
 class _TeceRotateOut(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, H: int):
-        E, K, C = m.shape
-        dt = m.dtype
-        if K != (lmax + 1) ** 2:
-            raise ValueError(f"tece_rotate_out: {K} component rows, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
-        _req(m, "messages", dt, (plan.n_edges, K, C))
-        if node_map is not None:
-            _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    def forward(ctx, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, H: int, C: int, *m):
+        E, dt = W.shape[0], W.dtype
+        K = (lmax + 1) ** 2
+        _req_blocks(m, "messages", dt, plan.n_edges, lmax, C)
         _req(alpha, "alpha", dt, (E, H))
         _req(W, "wigner", dt, (E, K, K))
-        out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=m.device)
+        if node_map is not None:
+            _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+        out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=W.device)
         tok = _t0("tece_rotate_out_fwd")
-        N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), m.data_ptr(), alpha.data_ptr(), W.data_ptr(),
+        N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), _block_array(m), alpha.data_ptr(), W.data_ptr(),
                                                  plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map),
                                                  plan.n_nodes, lmax, C, H, out.data_ptr(),
-                                                 N.stream_ptr(m.device)), "tace_tece_rotate_out_fwd")
+                                                 N.stream_ptr(W.device)), "tace_tece_rotate_out_fwd")
         _t1(tok, (plan.n_nodes, E, C, K, H))
-        ctx.save_for_backward(m, alpha, W, node_map, dst)
-        ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
+        ctx.save_for_backward(alpha, W, node_map, dst, *m)
+        ctx.plan, ctx.lmax, ctx.H, ctx.C = plan, lmax, H, C
         return out
 
     @staticmethod
     def backward(ctx, gout):
-        m, alpha, W, node_map, dst = ctx.saved_tensors
-        plan, lmax, H = ctx.plan, ctx.lmax, ctx.H
-        E, K, C = m.shape
+        alpha, W, node_map, dst, *m = ctx.saved_tensors
+        plan, lmax, H, C = ctx.plan, ctx.lmax, ctx.H, ctx.C
+        E, K = W.shape[0], (lmax + 1) ** 2
         gout = gout.contiguous()
-        gm, ga, gW = torch.empty_like(m), torch.empty_like(alpha), torch.empty_like(W)
+        gm = [torch.empty_like(t) for t in m]
+        ga, gW = torch.empty_like(alpha), torch.empty_like(W)
         tok = _t0("tece_rotate_out_bwd")
-        N.check(N.lib().tace_tece_rotate_out_bwd(N.dtype_code(m.dtype), m.data_ptr(), alpha.data_ptr(), W.data_ptr(),
-                                                 gout.data_ptr(), dst.data_ptr(), N.ptr(node_map), plan.n_nodes, E,
-                                                 lmax, C, H, gm.data_ptr(), ga.data_ptr(), gW.data_ptr(),
-                                                 N.stream_ptr(m.device)), "tace_tece_rotate_out_bwd")
+        N.check(N.lib().tace_tece_rotate_out_bwd(N.dtype_code(W.dtype), _block_array(m), alpha.data_ptr(),
+                                                 W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
+                                                 plan.n_nodes, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
+                                                 gW.data_ptr(), N.stream_ptr(W.device)), "tace_tece_rotate_out_bwd")
         _t1(tok, (plan.n_nodes, E, C, K, H))
-        return gm, ga, gW, None, None, None, None, None
+        return (ga, gW, None, None, None, None, None, None) + tuple(gm)
 
 
-def tece_rotate_out(m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, heads: int) -> torch.Tensor:
-    """sum_{e -> n} W[e]^T (alpha[e] m[e]) per receiver n, in the group-major
-    layout of C x (0..lmax) at rows node_map[n] ([N, K*C])."""
+def tece_rotate_out(m: Sequence[torch.Tensor], alpha, W, plan: EdgePlan, node_map, dst, lmax: int,
+                    heads: int) -> torch.Tensor:
+    """sum_{e -> n} W[e]^T (alpha[e] m[e]) per receiver n for messages in the
+    SO(2) block layout, written in the group-major layout of C x (0..lmax) at
+    rows node_map[n] ([N, K*C])."""
     dst = dst.long().contiguous()
     if dst.shape != (plan.n_edges,):
         raise ValueError(f"tece_rotate_out: dst has shape {tuple(dst.shape)}, expected ({plan.n_edges},)")
-    return _TeceRotateOut.apply(m.contiguous(), alpha.contiguous(), W.contiguous(), plan, node_map, dst,
-                                int(lmax), int(heads))
+    C = m[0].shape[1] // (lmax + 1)
+    return _TeceRotateOut.apply(alpha.contiguous(), W.contiguous(), plan, node_map, dst, int(lmax), int(heads), C,
+                                *[t.contiguous() for t in m])
 
 
 class _EdgeRotateIn(torch.autograd.Function):
@@ -519,42 +567,43 @@ class _EdgeRotateIn(torch.autograd.Function):
             _req(wr, "radial_w", dt, (E, nc * 2 * C))
         _req(rows_src, "rows_src", torch.int64, (E,))
         _req(rows_dst, "rows_dst", torch.int64, (E,))
-        ms = torch.empty(E, K, C, dtype=dt, device=x.device)
-        md = torch.empty_like(ms)
-        mw = torch.empty(E, K, 2 * C, dtype=dt, device=x.device) if wr is not None else None
+        mk = lambda ch: [torch.empty(shp, dtype=dt, device=x.device) for shp in so2_block_shapes(E, lmax, ch)]
+        ms, md = mk(C), mk(C)
+        mw = mk(2 * C) if wr is not None else []
         tok = _t0("edge_rotate_in_fwd")
         N.check(N.lib().tace_edge_rotate_in_fwd(N.dtype_code(dt), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
-                                                rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C, ms.data_ptr(),
-                                                md.data_ptr(), N.ptr(mw), N.stream_ptr(x.device)),
-                "tace_edge_rotate_in_fwd")
+                                                rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C, _block_array(ms),
+                                                _block_array(md), _block_array(mw) if mw else None,
+                                                N.stream_ptr(x.device)), "tace_edge_rotate_in_fwd")
         _t1(tok, (E, K, C, wr is not None))
         ctx.save_for_backward(x, W, wr, rows_src, rows_dst)
-        ctx.lmax = lmax
+        ctx.lmax, ctx.n = lmax, lmax + 1
         ctx.set_materialize_grads(False)
-        return (ms, md, mw) if wr is not None else (ms, md)
+        return tuple(ms + md + mw)
 
     @staticmethod
-    def backward(ctx, gms, gmd, gmw=None):
+    def backward(ctx, *g):
         x, W, wr, rows_src, rows_dst = ctx.saved_tensors
         Nr, K, C = x.shape
-        E = W.shape[0]
-        gms = gms.contiguous() if gms is not None else None
-        gmd = gmd.contiguous() if gmd is not None else None
-        gmw = gmw.contiguous() if gmw is not None else None
+        E, n = W.shape[0], ctx.n
+        g = [t.contiguous() if t is not None else None for t in g]
+        gms, gmd, gmw = g[:n], g[n:2 * n], g[2 * n:]
         gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
         gxd = torch.empty_like(gxs)
         gW = torch.empty_like(W)
-        gwr = torch.zeros_like(wr) if wr is not None and ctx.needs_input_grad[2] else None
-        if gwr is not None and gmw is not None:
-            gwr = torch.empty_like(wr)
+        has_w = any(t is not None for t in gmw)
+        gwr = None
+        if wr is not None and ctx.needs_input_grad[2]:
+            gwr = torch.empty_like(wr) if has_w else torch.zeros_like(wr)
         tok = _t0("edge_rotate_in_bwd")
         N.check(N.lib().tace_edge_rotate_in_bwd(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(),
-                                                rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr), N.ptr(gms),
-                                                N.ptr(gmd), N.ptr(gmw), Nr, E, ctx.lmax, C, gxs.data_ptr(),
-                                                gxd.data_ptr(), gW.data_ptr(),
-                                                N.ptr(gwr) if gmw is not None else 0,
-                                                N.stream_ptr(x.device)), "tace_edge_rotate_in_bwd")
-        _t1(tok, (E, K, C, gmw is not None))
+                                                rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr),
+                                                _block_array(gms), _block_array(gmd),
+                                                _block_array(gmw) if has_w else None, Nr, E, ctx.lmax, C,
+                                                gxs.data_ptr(), gxd.data_ptr(), gW.data_ptr(),
+                                                N.ptr(gwr) if has_w else None, N.stream_ptr(x.device)),
+                "tace_edge_rotate_in_bwd")
+        _t1(tok, (E, K, C, has_w))
         gx = None
         if ctx.needs_input_grad[0]:
             gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
@@ -564,11 +613,15 @@ class _EdgeRotateIn(torch.autograd.Function):
 def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, rows_dst: torch.Tensor, lmax: int,
                    radial_w: Optional[torch.Tensor] = None):
     """Edge-frame messages m = W[e] @ [x[rows_src[e]] | x[rows_dst[e]]] for node
-    features x [rows, K, C] (l layout), returned as (m_src, m_dst) = (m[..., :C],
-    m[..., C:]) and, with radial weights [E, ncomp * 2C], also m_w = the
-    radially weighted m [E, K, 2C] (+m and -m rows share a weight component)."""
-    return _EdgeRotateIn.apply(x.contiguous(), W.contiguous(), None if radial_w is None else radial_w.contiguous(),
-                               rows_src.long().contiguous(), rows_dst.long().contiguous(), int(lmax))
+    features x [rows, K, C] (l layout), in the SO(2) block layout: returns
+    (m_src, m_dst) block lists (first / last C channels) and, with radial
+    weights [E, ncomp * 2C], also the radially weighted m_w block list (2C
+    channels; +m and -m rows share a weight component)."""
+    out = _EdgeRotateIn.apply(x.contiguous(), W.contiguous(), None if radial_w is None else radial_w.contiguous(),
+                              rows_src.long().contiguous(), rows_dst.long().contiguous(), int(lmax))
+    n = lmax + 1
+    blocks = [list(out[i * n:(i + 1) * n]) for i in range(len(out) // n)]
+    return tuple(blocks)
 
 
 class _RadialMlp(torch.autograd.Function):

@@ -103,6 +103,16 @@ class uvSO2Linear(torch.nn.Module):
             outs.append(mix_linear(xm, fc.weight * fc.alpha, None, mixing).view(E, 2 * self.nout[m], self.cout))
         return torch.cat(outs, dim=1)
 
+    def blocks(self, xb, mixing=None):
+        """The same map on the SO(2) block layout (``ops.so2_block_shapes``):
+        one GEMM per block, no copies."""
+        f = self.m0_rlinear
+        out = [mix_linear(xb[0], f.weight * f.alpha, f.bias, mixing)]
+        for m in range(1, self.mmax + 1):
+            fc = self.ms_clinear[m - 1].fc
+            out.append(mix_linear(xb[m], fc.weight * fc.alpha, None, mixing))
+        return out
+
 
 class TeceConvolution(torch.nn.Module):
     """``OAM20260705Convolution`` (see the module docstring)."""
@@ -142,37 +152,20 @@ class TeceConvolution(torch.nn.Module):
         self.temperature_logit = torch.nn.Parameter(
             torch.full((num_head,), math.log((1.0 - self.tmin) / (self.tmax - 1.0))))
 
-    def _shared_input_gemms(self, m):
+    def _shared_input_gemms(self, mw):
         """linear_coefs, linear_glu and linear_up of the radially weighted
-        messages m [E, K, 2C]: one GEMM per m block with the three weights
-        stacked.  Returns the block outputs y0 [E, coef | glu | up] and, per
-        m > 0, y_m [2E, glu | up] (the edge-ACE kernel's input layout)."""
-        E, n = m.shape[0], self.lmax + 1
+        messages (block layout, 2C channels): one GEMM per m block with the
+        three weights stacked.  Returns y0 [E, coef | glu | up] and, per m > 0,
+        y_m [2E, glu | up] (the edge-ACE kernel's input layout)."""
         lc, lg, lu = self.linear_coefs, self.linear_glu, self.linear_up
         f0 = [lc.m0_rlinear, lg.m0_rlinear, lu.m0_rlinear]
         W0 = torch.cat([f.weight * f.alpha for f in f0])
         b0 = torch.cat([f.bias for f in f0])
-        ys = [mix_linear(m[:, :n].reshape(E, -1), W0, b0, self.mixing)]
-        off = n
+        ys = [mix_linear(mw[0], W0, b0, self.mixing)]
         for mm in range(1, self.mmax + 1):
-            k = n - mm
-            xm = m[:, off:off + 2 * k].contiguous().view(2 * E, -1)
-            off += 2 * k
             fg, fu = lg.ms_clinear[mm - 1].fc, lu.ms_clinear[mm - 1].fc
-            ys.append(mix_linear(xm, torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha]), None, self.mixing))
+            ys.append(mix_linear(mw[mm], torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha]), None, self.mixing))
         return ys
-
-    def _linear_down_blocks(self, o):
-        """linear_down on the edge-ACE output blocks (o0 [E, n*A], o_m [2E, n*A])
-        -> [E, K, C] in the m layout."""
-        ld = self.linear_down
-        E = o[0].shape[0]
-        f = ld.m0_rlinear
-        outs = [mix_linear(o[0], f.weight * f.alpha, f.bias, self.mixing).view(E, ld.nout[0], ld.cout)]
-        for mm in range(1, self.mmax + 1):
-            fc = ld.ms_clinear[mm - 1].fc
-            outs.append(mix_linear(o[mm], fc.weight * fc.alpha, None, self.mixing).view(E, 2 * ld.nout[mm], ld.cout))
-        return torch.cat(outs, dim=1)
 
     def node_components(self, x_gm):
         """Group-major C x (0..lmax) node features -> [rows, (L+1)^2, C] (l layout)."""
@@ -186,15 +179,15 @@ class TeceConvolution(torch.nn.Module):
         edge's sender / receiver; ``plan``: receiver CSR of these edges;
         ``out_map`` (int32 or None) / ``dst_out``: output row of each receiver /
         of each edge's receiver.  Returns [plan.n_nodes, K*C] group-major."""
-        ms, md, m = ops.edge_rotate_in(x_lc, wigner, rows_src, rows_dst, self.lmax, w)
-        key = self.key_proj(ms, self.mixing)
-        query = self.query_proj(md, self.mixing)
+        ms, md, mw = ops.edge_rotate_in(x_lc, wigner, rows_src, rows_dst, self.lmax, w)
+        key = self.key_proj.blocks(ms, self.mixing)
+        query = self.query_proj.blocks(md, self.mixing)
         rp = self.radial_proj(R)
         T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
         score = ops.tece_score(query, key, rp, (T * self.attention_scale).detach(), self.lmax, self.H)
         alpha = ops.graph_softmax(score, plan)
-        o = ops.tece_edge_ace(self._shared_input_gemms(m), self.lmax, self.A)
-        m = self._linear_down_blocks(o)
+        o = ops.tece_edge_ace(self._shared_input_gemms(mw), self.lmax, self.A)
+        m = self.linear_down.blocks(o, self.mixing)
         return ops.tece_rotate_out(m, alpha, wigner, plan, out_map, dst_out, self.lmax, self.H)
 
     def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):

@@ -119,7 +119,8 @@ def test_tece_score_matches_oracle(cuda, dtype, lmax, H, C):
     W = (conv.radial_proj.weight * conv.radial_proj.alpha).detach().to(dtype).to(cuda)
     rp = torch.nn.functional.linear(r, W, conv.radial_proj.bias.detach().to(dtype).to(cuda))
     T = conv.tmin + (conv.tmax - conv.tmin) * torch.sigmoid(conv.temperature_logit.detach())
-    s = ops.tece_score(a, b, rp, (T * conv.attention_scale).to(dtype).to(cuda), lmax, H)
+    s = ops.tece_score(ops.so2_to_blocks(a, lmax), ops.so2_to_blocks(b, lmax), rp,
+                       (T * conv.attention_scale).to(dtype).to(cuda), lmax, H)
     close(s, s_o, dtype, "score")
     gq, gk, gR = torch.autograd.grad((s * gs.to(dtype).to(cuda)).sum(), [a, b, r])
     close(gq, gq_o, dtype, "grad q")
@@ -179,7 +180,7 @@ def test_rotate_out_matches_oracle(cuda, dtype, lmax, H, C):
     plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
     a, b, w = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (m, al, W_o))
     nm = node_map.to(cuda)
-    out = ops.tece_rotate_out(a, b, w, plan, nm, ei[1].to(cuda), lmax, H)
+    out = ops.tece_rotate_out(ops.so2_to_blocks(a, lmax), b, w, plan, nm, ei[1].to(cuda), lmax, H)
     close(out, _lc_to_gm(o, node_map, lmax), dtype, "out")
     gout = _lc_to_gm(go, node_map, lmax).to(dtype).to(cuda)
     gm, ga, gW = torch.autograd.grad((out * gout).sum(), [a, b, w])
@@ -207,7 +208,7 @@ def test_rotate_in_matches_oracle(cuda, dtype, lmax, C):
     a, w = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, W_o))
     rs, rd = rows[ei[0]].to(cuda), rows[ei[1]].to(cuda)
     ms, md = ops.edge_rotate_in(a, w, rs, rd, lmax)
-    m = torch.cat((ms, md), dim=-1)
+    m = torch.cat((ops.so2_from_blocks(ms, lmax), ops.so2_from_blocks(md, lmax)), dim=-1)
     close(m, m_o, dtype, "m")
     gx, gW = torch.autograd.grad((m * gm.to(dtype).to(cuda)).sum(), [a, w])
     close(gx, gx_o, dtype, "grad x")
@@ -232,7 +233,8 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
     loss = (m[..., :C] * gs).sum() + (m[..., C:] * gd).sum() + (mw_o * gw).sum()
     gx_o, gW_o, gwr_o = torch.autograd.grad(loss, [x, W_o, wr])
     a, w, r = (t.detach().to(dtype).to(cuda).requires_grad_(True) for t in (x, W_o, wr))
-    ms, md, mw = ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda), lmax, r)
+    ms, md, mw = (ops.so2_from_blocks(t, lmax) for t in ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda),
+                                                                             lmax, r))
     close(ms, m[..., :C], dtype, "m_src")
     close(md, m[..., C:], dtype, "m_dst")
     close(mw, mw_o, dtype, "m_w")
@@ -244,7 +246,7 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
     close(gwr, gwr_o, dtype, "grad radial w")
     # only the weighted output used: the src/dst gradients are absent
     ms, md, mw = ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda), lmax, r)
-    gx2, = torch.autograd.grad((mw * dv(gw)).sum(), [a])
+    gx2, = torch.autograd.grad((ops.so2_from_blocks(mw, lmax) * dv(gw)).sum(), [a])
     m = torch.bmm(W_o, torch.cat((x[ei[0]], x[ei[1]]), dim=-1))
     mw_o = wr.view(E, nc, 2 * C).index_select(1, ot.so2_expand(lmax, lmax, False)) * m
     gx2_o, = torch.autograd.grad((mw_o * gw).sum(), [x])

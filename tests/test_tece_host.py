@@ -38,3 +38,19 @@ def test_sub_plan_is_the_chunk_csr():
         assert p.rowptr.tolist() == [0] + torch.cumsum(deg[n0:n1], 0).tolist()
         assert torch.equal(p.src, plan.src[e0:e1])
         assert torch.equal(dst[e0:e1] - n0, torch.repeat_interleave(torch.arange(n1 - n0), deg[n0:n1]))
+
+
+def test_so2_block_layout_round_trip():
+    """m-layout rows <-> SO(2) blocks: block 0 holds the m = 0 rows, block m
+    the +m rows (GEMM row 2e) and -m rows (row 2e+1) of each edge."""
+    for lmax in (1, 2, 3):
+        E, ch, K = 5, 3, (lmax + 1) ** 2
+        x = torch.arange(E * K * ch, dtype=torch.float64).view(E, K, ch)
+        b = ops.so2_to_blocks(x, lmax)
+        assert [tuple(t.shape) for t in b] == ops.so2_block_shapes(E, lmax, ch)
+        assert torch.equal(ops.so2_from_blocks(b, lmax), x)
+        n = lmax + 1
+        # edge 2, m = 1: + rows start at row n, - rows at n + lmax
+        k = n - 1
+        assert torch.equal(b[1][2 * 2].view(k, ch), x[2, n:n + k])
+        assert torch.equal(b[1][2 * 2 + 1].view(k, ch), x[2, n + k:n + 2 * k])

@@ -127,52 +127,74 @@ def cpu_baseline(wl, reps=3):
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    s, what = wl["cpu_slice"]()
+    structs, what = wl["cpu_slice"]()
     rc = wl["cutoff"]
-    ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)
-    cfg = wl["cfg"](ei.shape[1] / len(s["numbers"]))
+    stress = "stress" in wl["targets"]
+
+    def graph():
+        edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc) for s in structs]
+        return edges, data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float32)
+
+    n = sum(len(s["numbers"]) for s in structs)
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc) for s in structs]
+    cfg = wl["cfg"](sum(e[0].shape[1] for e in edges) / n)
     torch.manual_seed(0)
     m = om.TACE(cfg).float()
     for prm in m.parameters():  # frozen, as in the reference calculators
         prm.requires_grad_(False)
-    d = data.collate([s], [(ei, S)], cfg["atomic_numbers"], dtype=torch.float32)
-    om.compute(m, d, forces=True)  # warm-up
+    om.compute(m, graph()[1], forces=True, stress=stress)  # warm-up
     t0 = time.perf_counter()
     for _ in range(reps):
-        ei, S = onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)
-        d = data.collate([s], [(ei, S)], cfg["atomic_numbers"], dtype=torch.float32)
-        om.compute(m, d, forces=True)
+        om.compute(m, graph()[1], forces=True, stress=stress)
     dt = time.perf_counter() - t0
-    n = len(s["numbers"])
     return dict(value=n * reps / dt, unit="atom-steps/s", cores=threads, kind="port",
                 sample=f"{n}-atom {what} (same model, float32), "
-                       f"{reps} timed E+F steps incl. brute-force NL after 1 warm-up; {dt:.1f} s")
+                       f"{reps} timed {'E+F+S' if stress else 'E+F'} steps incl. brute-force NL after 1 warm-up; "
+                       f"{dt:.1f} s")
 
 
 def workloads(args):
-    """The bench workloads: the headline water box (configs[2], default) and the
-    TECE bcc Fe box."""
+    """The bench workloads: the headline water box (configs[2], default), the
+    FCC alloy, the ragged crystal batch and the TECE
+    bcc Fe box."""
     from tace_amd import configs, structures
 
     box = 49.7 / 16 * args.n_side
     water = dict(
-        metric=METRIC, cutoff=6.0, dt_fs=DT_FS, species=[1, 8],
-        structure=lambda: structures.water_box(n_side=args.n_side, box=box, seed=0),
+        metric=METRIC, cutoff=6.0, dt_fs=DT_FS, species=[1, 8], targets=["energy", "forces"],
+        structs=lambda: [structures.water_box(n_side=args.n_side, box=box, seed=0)],
         cfg=lambda a: configs.model_cfg("water12k", [1, 8], a),
         describe=lambda nat: f"water box {nat} atoms (configs[2]), E+F, NL rebuilt every step",
         arch=dict(channels=128, L=3, correlation=3, layers=3, cutoff=6.0),
-        cpu_slice=lambda: (structures.water_box(n_side=5, box=49.7 / 16 * 5, seed=1), "water slice (5^3 H2O)"))
+        cpu_slice=lambda: ([structures.water_box(n_side=5, box=49.7 / 16 * 5, seed=1)], "water slice (5^3 H2O)"))
+    fcc = dict(
+        metric="atom-steps/sec (E+F, fp32) at 1,024 atoms FCC alloy (configs[1])", cutoff=5.0, dt_fs=1.0,
+        species=[26, 27, 28, 29], targets=["energy", "forces"],
+        structs=lambda: [structures.fcc_alloy(seed=0)],
+        cfg=lambda a: configs.model_cfg("fcc1024", [26, 27, 28, 29], a),
+        describe=lambda nat: f"4-species FCC alloy {nat} atoms (configs[1]), E+F, NL rebuilt every step",
+        arch=dict(channels=128, L=3, correlation=3, layers=2, cutoff=5.0),
+        cpu_slice=lambda: ([structures.fcc_alloy(reps=(4, 4, 2), seed=1)], "FCC alloy slice (4x4x2 cells)"))
+    ragged = dict(
+        metric="atom-steps/sec (E+F+S, fp32) on a 128-crystal ragged batch, 89 species (configs[3])", cutoff=6.0,
+        dt_fs=1.0, species=list(structures.MPTRJ_ELEMENTS), targets=["energy", "forces", "stress"],
+        structs=lambda: structures.ragged_batch(128, seed=0),
+        cfg=lambda a: configs.model_cfg("ragged128", list(structures.MPTRJ_ELEMENTS), a),
+        describe=lambda nat: f"128 random triclinic crystals, {nat} atoms (configs[3]), E+F+S, per-crystal GPU NL "
+                             f"every step",
+        arch=dict(channels=256, L=3, correlation=3, layers=2, cutoff=6.0, species=89),
+        cpu_slice=lambda: (structures.ragged_batch(3, nmin=8, nmax=40, seed=1), "3-crystal ragged slice"))
     r = args.fe_reps
     fe = dict(
         metric=f"atom-steps/sec (E+F, fp32) at {2 * r ** 3} atoms bcc Fe, TECE (configs[4])", cutoff=5.0,
-        dt_fs=1.0, species=[26],
-        structure=lambda: structures.bcc_fe(reps=(r, r, r), seed=0),
+        dt_fs=1.0, species=[26], targets=["energy", "forces"],
+        structs=lambda: [structures.bcc_fe(reps=(r, r, r), seed=0)],
         cfg=lambda a: configs.model_cfg("tece", [26], a),
         describe=lambda nat: f"bcc Fe {r}^3 box {nat} atoms (configs[4]), TECE E+F, NL rebuilt every step",
         arch=dict(channels=128, L=2, mmax=2, heads=4, edge_ace_hidden=32, correlation=2, layers=2, cutoff=5.0,
                   layer_types="cgtp, uv_so2", product="silu_bilineargate"),
-        cpu_slice=lambda: (structures.bcc_fe(reps=(4, 4, 4), seed=1), "bcc Fe slice (4^3 cells)"))
-    return dict(water12k=water, fe101k=fe)
+        cpu_slice=lambda: ([structures.bcc_fe(reps=(4, 4, 4), seed=1)], "bcc Fe slice (4^3 cells)"))
+    return dict(water12k=water, fcc1024=fcc, ragged128=ragged, fe101k=fe)
 
 
 def main():
@@ -180,8 +202,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="water12k", choices=["water12k", "fe101k"],
-                    help="water12k: the headline water box (configs[2]); fe101k: TECE on bcc Fe (configs[4])")
+    ap.add_argument("--workload", default="water12k", choices=["water12k", "fcc1024", "ragged128", "fe101k"],
+                    help="water12k: the headline water box (configs[2]); fcc1024: FCC alloy (configs[1]); "
+                         "ragged128: 128-crystal batch with stress (configs[3]); fe101k: TECE on bcc Fe (configs[4])")
     ap.add_argument("--n-side", type=int, default=16, help="water molecules per box edge (16 -> 12,288 atoms)")
     ap.add_argument("--fe-reps", type=int, default=37, help="bcc cells per box edge (37 -> 101,306 atoms)")
     ap.add_argument("--fe-fp32-mixing", action="store_true",
@@ -208,11 +231,16 @@ def main():
 
     wl = workloads(args)[args.workload]
     dev = torch.device("cuda:0")
-    s = wl["structure"]()
+    structs = wl["structs"]()
     rc = wl["cutoff"]
-    nat = len(s["numbers"])
-    pos64 = torch.as_tensor(s["positions"], dtype=torch.float64, device=dev)
-    g0 = data.resident_graph(pos64, s["cell"], s["pbc"], torch.zeros(nat, len(wl["species"]), device=dev), rc)
+    nat = sum(len(s["numbers"]) for s in structs)
+    single = len(structs) == 1
+    if single:
+        s = structs[0]
+        pos64 = torch.as_tensor(s["positions"], dtype=torch.float64, device=dev)
+        g0 = data.resident_graph(pos64, s["cell"], s["pbc"], torch.zeros(nat, len(wl["species"]), device=dev), rc)
+    else:
+        g0 = data.gpu_graph(structs, wl["species"], rc, dtype=torch.float32, device=dev)
     E0 = g0["edge_index"].shape[1]
     avg = E0 / nat
     del g0
@@ -220,7 +248,7 @@ def main():
     cfg = wl["cfg"](avg)
     torch.manual_seed(0)
     model = pm.create_model(cfg).to(dev)
-    model.reset_target_property(["energy", "forces"])
+    model.reset_target_property(wl["targets"])
     # inference set-up of the reference calculators (ase/calculator.py:100-102,
     # torchsim.py:142, lammps/mliap.py:38): eval mode, parameters frozen
     model.eval()
@@ -230,17 +258,20 @@ def main():
     if args.workload == "fe101k" and not args.fe_fp32_mixing:
         mixing = torch.bfloat16  # "fp32 with bf16 channel mixing on MFMA"
         pm.set_tece_channel_mixing(model, mixing)
-    attrs = data.one_hot(s["numbers"], cfg["atomic_numbers"], torch.float32).to(dev)
+    if single:
+        attrs = data.one_hot(s["numbers"], cfg["atomic_numbers"], torch.float32).to(dev)
 
-    def step():
-        g = data.resident_graph(pos64, s["cell"], s["pbc"], attrs, rc)
-        return model(g)
+        def step():
+            return model(data.resident_graph(pos64, s["cell"], s["pbc"], attrs, rc))
+    else:
+        def step():
+            return model(data.gpu_graph(structs, cfg["atomic_numbers"], rc, dtype=torch.float32, device=dev))
 
     log(f"[bench] {args.workload}: {nat} atoms, {E0} edges (avg {avg:.1f}), warm-up {args.warmup}")
     for _ in range(args.warmup):
         out = step()
     torch.cuda.synchronize()
-    log(f"[bench] warm-up done, E = {out['energy'].item():.6f}; timing {args.steps} steps")
+    log(f"[bench] warm-up done, E = {out['energy'].sum().item():.6f}; timing {args.steps} steps")
 
     ops.TIMER = ops.KernelTimer()
     torch.cuda.synchronize()

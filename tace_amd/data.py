@@ -52,31 +52,34 @@ def collate(structs: List[Dict], edges: List[Tuple[np.ndarray, np.ndarray]], ato
 
 def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float, dtype=torch.float32,
               device="cuda") -> Dict[str, torch.Tensor]:
-    """Batch built on the GPU: HIP cell-list neighbour list per structure
-    (float64), edges grouped by receiver (``edge_index[1]`` non-decreasing)."""
-    from .ops import neighbour_list
+    """Batch built on the GPU: one batched HIP cell-list neighbour search over
+    all structures (float64; ``ops.neighbour_list_batch``), edges grouped by
+    receiver (``edge_index[1]`` non-decreasing).  The result carries its
+    receiver CSR plan."""
+    from .ops import EdgePlan, neighbour_list_batch
 
-    pos, attrs, src, dst, sh, lat, batch, ptr = [], [], [], [], [], [], [], [0]
-    off = 0
-    for k, s in enumerate(structs):
-        n = len(s["positions"])
-        p64 = torch.as_tensor(np.asarray(s["positions"], dtype=np.float64), device=device)
-        rowptr, e_src, e_sh = neighbour_list(p64, s["cell"], s["pbc"], cutoff)
-        counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
-        e_dst = torch.repeat_interleave(torch.arange(n, device=device), counts)
-        pos.append(p64.to(dtype))
-        attrs.append(one_hot(s["numbers"], atomic_numbers, dtype).to(device))
-        src.append(e_src.to(torch.int64) + off)
-        dst.append(e_dst + off)
-        sh.append(e_sh.to(dtype))
-        lat.append(torch.as_tensor(np.asarray(s["cell"]), dtype=dtype, device=device).view(1, 3, 3))
-        batch.append(torch.full((n,), k, dtype=torch.int64, device=device))
-        off += n
-        ptr.append(off)
-    return dict(positions=torch.cat(pos), node_attrs=torch.cat(attrs),
-                edge_index=torch.stack([torch.cat(src), torch.cat(dst)]), edge_shifts=torch.cat(sh),
-                lattice=torch.cat(lat), batch=torch.cat(batch),
-                ptr=torch.tensor(ptr, dtype=torch.int64, device=device))
+    sizes = [len(s["positions"]) for s in structs]
+    n_tot = sum(sizes)
+    p64 = torch.as_tensor(np.concatenate([np.asarray(s["positions"], dtype=np.float64).reshape(-1, 3)
+                                          for s in structs]), device=device)
+    rowptr, src, shifts = neighbour_list_batch(p64, sizes, [s["cell"] for s in structs], [s["pbc"] for s in structs],
+                                               cutoff)
+    E = src.shape[0]
+    counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
+    dst = torch.repeat_interleave(torch.arange(n_tot, device=device), counts, output_size=E)
+    sizes_t = torch.tensor(sizes, dtype=torch.int64)
+    batch = torch.repeat_interleave(torch.arange(len(structs)), sizes_t).to(device)
+    ptr = torch.zeros(len(structs) + 1, dtype=torch.int64)
+    ptr[1:] = torch.cumsum(sizes_t, 0)
+    ptr = ptr.to(device)
+    src64 = src.to(torch.int64) + ptr[:-1][batch[dst]]
+    attrs = torch.cat([one_hot(s["numbers"], atomic_numbers, dtype) for s in structs]).to(device)
+    lat = torch.as_tensor(np.stack([np.asarray(s["cell"], dtype=np.float64).reshape(3, 3) for s in structs]),
+                          dtype=dtype, device=device)
+    ei = torch.stack([src64, dst])
+    plan = EdgePlan(n_tot, E, rowptr, (src64.to(torch.int32)).contiguous(), None)
+    return dict(positions=p64.to(dtype), node_attrs=attrs, edge_index=ei, edge_shifts=shifts.to(dtype),
+                lattice=lat, batch=batch, ptr=ptr, _edge_plan=plan, _dst32=dst.to(torch.int32))
 
 
 def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cutoff: float,

@@ -821,3 +821,56 @@ def neighbour_list(positions: torch.Tensor, cell, pbc, cutoff: float):
                                ws.data_ptr(), rowptr.data_ptr(), src.data_ptr(), shifts.data_ptr(), s),
                 "tace_nl_fill")
     return rowptr, src, shifts
+
+
+def neighbour_list_batch(positions: torch.Tensor, sizes: Sequence[int], cells, pbcs, cutoff: float):
+    """The cell-list neighbour search for a batch of structures in one pass:
+    every structure's count kernel, one scan over the whole batch, one host
+    synchronisation for the total edge count, then every fill kernel.
+    ``positions`` [sum(sizes), 3] float64 (structures back to back).
+
+    Returns ``(rowptr int32 [N+1], src int32 [E], shifts int32 [E,3])`` over
+    the batch: receiver n's edges are slots rowptr[n]..rowptr[n+1]; ``src``
+    holds the sender's index *within its structure*."""
+    _req(positions, "positions", torch.float64)
+    dev = positions.device
+    L = N.lib()
+    n_tot = int(sum(sizes))
+    if positions.shape[0] != n_tot:
+        raise ValueError(f"positions has {positions.shape[0]} rows, sizes sum to {n_tot}")
+    geo, ws_off, total = [], [], 0
+    for n, cell, pbc in zip(sizes, cells, pbcs):
+        cell_np = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(3, 3))
+        pbc_np = np.ascontiguousarray(np.broadcast_to(np.asarray(pbc, dtype=np.int32), (3,)))
+        nb = L.tace_nl_workspace_bytes(int(n), cell_np.ctypes.data, pbc_np.ctypes.data, float(cutoff))
+        if nb < 0:
+            raise N.NativeError(L.tace_last_error().decode())
+        geo.append((int(n), cell_np, pbc_np, int(nb)))
+        ws_off.append(total)
+        total += (max(int(nb), 4) + 255) // 256 * 256
+    ws = torch.empty(max(total, 256), dtype=torch.uint8, device=dev)
+    counts = torch.empty(n_tot, dtype=torch.int32, device=dev)
+    st = N.stream_ptr(dev)
+    a = 0
+    for (n, cell_np, pbc_np, nb), wo in zip(geo, ws_off):
+        if n:
+            N.check(L.tace_nl_count(positions[a:a + n].data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data,
+                                    float(cutoff), ws.data_ptr() + wo, nb, counts[a:a + n].data_ptr(), st),
+                    "tace_nl_count")
+        a += n
+    rowptr = torch.empty(n_tot + 1, dtype=torch.int32, device=dev)
+    N.check(L.tace_scan_i32(counts.data_ptr(), n_tot, rowptr.data_ptr(), st), "tace_scan_i32")
+    E = int(rowptr[-1].item())
+    src = torch.empty(E, dtype=torch.int32, device=dev)
+    shifts = torch.empty(E, 3, dtype=torch.int32, device=dev)
+    if E > 0:
+        a = 0
+        for (n, cell_np, pbc_np, nb), wo in zip(geo, ws_off):
+            if n:
+                # the structure's slice of the batch rowptr holds absolute slots
+                N.check(L.tace_nl_fill(positions[a:a + n].data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data,
+                                       float(cutoff), ws.data_ptr() + wo, rowptr[a:a + n + 1].data_ptr(),
+                                       src.data_ptr(), shifts.data_ptr(), st), "tace_nl_fill")
+            a += n
+    return rowptr, src, shifts
+

@@ -95,6 +95,9 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     if name.startswith("radial_mlp_out"):
         E, n_out = info
         return s * (E * (64 + n_out) + 64 * n_out)
+    if name.startswith("seg_linear"):
+        x_numel, y_numel, w_numel = info
+        return s * (x_numel + y_numel + w_numel)
     if name.startswith("edge_basis_fwd"):
         (E,) = info
         return s * E * (3 + 8 + 16)

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 10
+#define TACE_HIP_ABI_VERSION 11
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -147,6 +147,31 @@ int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h, int64_t n_e
  * weight [64, n_out] (row-major; h 16-byte aligned), on fp32 MFMA. */
 int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
                             float* out, void* stream);
+
+/* ---- per-species (element) linears
+ * tace_seg_linear replaces the per-element o3.Linear of e3nnElementLinear
+ * (tace/models/linear.py:377-482) on species-sorted, group-major node
+ * features: every output block, species and instruction of one linear (or of
+ * its input gradient) in one launch.  The work is a table of n_tiles output
+ * tiles of tile x tile elements (tile = 128: float32 on MFMA; 64: float32 or
+ * float64 on FMA), each inside one output block and one species' rows:
+ *   tiles    int64 [n_tiles, 8]: out_base (element offset of the tile's first
+ *            row in y), rows (1..tile), n (block width = row stride), c0 (first
+ *            column), bias_off (offset into bias, -1 none), cb, ce (its
+ *            contributions [cb, ce)), unused;
+ *   contribs int64 [*, 4]: x_base (offset of the tile's first row in x), k
+ *            (input block width = row stride), w_off (offset of the weight
+ *            matrix in w), trans (0: W is [k, n] row-major; 1: W is [n, k]
+ *            row-major and W^T is applied -- the input gradient);
+ *   scales   double [*]: the contribution's path weight.
+ * y[tile] = alpha (sum_c scale_c x_c[rows] @ W_c + bias[bias_off + cols]).
+ * Every tile element is written; tiles must not overlap.  The tables live in
+ * device memory and are trusted: the host builds them from the layout
+ * (tace_amd.ops.SegLinearPlan) and checks every offset against the array
+ * sizes before upload. */
+int tace_seg_linear(int dtype, int32_t tile, const void* x, void* y, const void* w, const void* bias,
+                    const int64_t* tiles, int64_t n_tiles, const int64_t* contribs, const double* scales,
+                    double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"
@@ -259,6 +284,32 @@ int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const 
                   void* workspace, int64_t workspace_bytes, int32_t* counts, void* stream);
 int tace_nl_fill(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
                  const void* workspace, const int32_t* rowptr, int32_t* src, int32_t* shifts, void* stream);
+/* The same search for a batch of structures (a collated batch of the
+ * reference's per-structure get_neighborhood calls,
+ * dataset/neighbour_list.py:195-298, one per structure from
+ * dataset/graph.py:53-60) in one launch per phase; structures are back to back in pos and
+ * node ids are batch-global (src too).  Each structure's edges are exactly
+ * what tace_nl_count/_fill give for it alone, in the same order.
+ *   1. tace_nl_batch_plan(plan = NULL) -> plan bytes; again with a host
+ *      buffer of that size -> the plan table (per-structure geometry, atom
+ *      and bin offsets), *n_atoms, *n_bins; copy it to device memory as is
+ *      (the kernels trust it);
+ *   2. tace_nl_batch_workspace_bytes(n_atoms, n_bins) -> allocate workspace;
+ *   3. tace_nl_batch_count -> counts[n_atoms];
+ *   4. tace_scan_i32(counts) -> rowptr[n_atoms+1];
+ *   5. tace_nl_batch_fill -> src[E], shifts[E,3] in rowptr order.
+ * sizes [n_structs] (int64), cells [n_structs, 3, 3] (rows = lattice
+ * vectors), pbcs [n_structs, 3].  mode: 0 = automatic, 1 = a thread per
+ * receiver, 2 = a wavefront per receiver (small structures); the result does
+ * not depend on it. */
+int64_t tace_nl_batch_plan(int32_t n_structs, const int64_t* sizes, const double* cells, const int32_t* pbcs,
+                           double cutoff, void* plan, int64_t plan_bytes, int64_t* n_atoms, int64_t* n_bins);
+int64_t tace_nl_batch_workspace_bytes(int64_t n_atoms, int64_t n_bins);
+int tace_nl_batch_count(const double* pos, int64_t n_atoms, int32_t n_structs, const void* plan, int64_t n_bins,
+                        void* workspace, int64_t workspace_bytes, int32_t mode, int32_t* counts, void* stream);
+int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, const void* plan, int64_t n_bins,
+                       const void* workspace, int64_t workspace_bytes, int32_t mode, const int32_t* rowptr,
+                       int32_t* src, int32_t* shifts, void* stream);
 /* exclusive prefix sum: out[0] = 0, out[i+1] = out[i] + counts[i], i < n */
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream);
 

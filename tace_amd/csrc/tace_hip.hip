@@ -454,6 +454,170 @@ __global__ __launch_bounds__(64) void k_nl_edges(const double* __restrict__ pos,
   if (!FILL) counts[a] = cnt;
 }
 
+// ------------------------------------------------- batched neighbours --
+// Many structures in one pass.  The host-built plan table holds per structure
+// its NlGeom, then struct_ptr[ns+1] (first atom of each structure) and
+// bin_off[ns+1] (first bin of each structure in the batch's bin arrays).
+// Atoms, bins and batoms entries are batch-global ids; the search per
+// receiver is the single-structure one (same candidate order, same distance
+// arithmetic), so each structure's edges come out exactly as
+// tace_nl_count/_fill produce them.
+struct NlBatch {
+  const NlGeom* geo;
+  const int* sptr;
+  const int* boff;
+  int ns;
+};
+
+static __device__ __forceinline__ int nlb_struct_of(const NlBatch& B, int a) {
+  int lo = 0, hi = B.ns - 1;   // last s with sptr[s] <= a
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (B.sptr[mid] <= a) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ void k_nlb_bin(const double* __restrict__ pos, int n, NlBatch B, int* __restrict__ abin,
+                          int* __restrict__ aimg, int* __restrict__ bcount) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int s = nlb_struct_of(B, i);
+  const NlGeom& g = B.geo[s];
+  const double px = pos[3 * i], py = pos[3 * i + 1], pz = pos[3 * i + 2];
+  int b[3];
+  for (int k = 0; k < 3; ++k) {
+    const double f = px * g.inv[k] + py * g.inv[3 + k] + pz * g.inv[6 + k];
+    int o = 0;
+    double w = f;
+    if (g.pbc[k]) {
+      o = (int)floor(f);
+      w = f - (double)o;
+    }
+    int bi = (int)floor(w * g.nb[k]);
+    bi = bi < 0 ? 0 : (bi >= g.nb[k] ? g.nb[k] - 1 : bi);
+    b[k] = bi;
+    aimg[3 * i + k] = o;
+  }
+  const int lin = B.boff[s] + (b[0] * g.nb[1] + b[1]) * g.nb[2] + b[2];
+  abin[i] = lin;
+  atomicAdd(bcount + lin, 1);
+}
+
+// Deterministic bin contents without a sort: atom i goes to the slot of its
+// rank (by id) among the atoms k_nl_scatter put into its bin in arbitrary
+// order -- batoms ends up ascending in every bin, as k_nl_sortbins leaves it,
+// with a thread per atom instead of a serial sort per bin.
+__global__ void k_nlb_rank(const int* __restrict__ abin, int n, const int* __restrict__ bstart,
+                           const int* __restrict__ unsorted, int* __restrict__ batoms) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int b = abin[i];
+  const int q0 = bstart[b], q1 = bstart[b + 1];
+  int r = 0;
+  for (int q = q0; q < q1; ++q) r += unsorted[q] < i;
+  batoms[q0 + r] = i;
+}
+
+// is source b (with periodic shift S) within the cutoff of receiver a?  The
+// same arithmetic as k_nl_edges (no contraction), the self image excluded.
+static __device__ __forceinline__ bool nl_pair(const double* __restrict__ pos, const int* __restrict__ aimg,
+                                               const NlGeom& g, int a, double ax, double ay, double az,
+                                               const int* oa, int sx, int sy, int sz, int b, int* S) {
+#pragma clang fp contract(off)
+  S[0] = aimg[3 * b] - oa[0] - sx;
+  S[1] = aimg[3 * b + 1] - oa[1] - sy;
+  S[2] = aimg[3 * b + 2] - oa[2] - sz;
+  if (b == a && S[0] == 0 && S[1] == 0 && S[2] == 0) return false;
+  const double d0 = ax - pos[3 * b], d1 = ay - pos[3 * b + 1], d2 = az - pos[3 * b + 2];
+  const double s0 = (double)S[0], s1 = (double)S[1], s2 = (double)S[2];
+  const double v0 = d0 + s0 * g.cell[0] + s1 * g.cell[3] + s2 * g.cell[6];
+  const double v1 = d1 + s0 * g.cell[1] + s1 * g.cell[4] + s2 * g.cell[7];
+  const double v2 = d2 + s0 * g.cell[2] + s1 * g.cell[5] + s2 * g.cell[8];
+  const double r2 = v0 * v0 + v1 * v1 + v2 * v2;
+  return r2 < g.rc2;
+}
+
+// WAVE = false: one thread per receiver (large structures: enough receivers
+// to fill the GPU).  WAVE = true: one wavefront per receiver, the 64 lanes
+// over each bin's candidates; counts by ballot, fill slots by the rank of the
+// lane's hit among the wave's hits -- the candidate order, and so the edge
+// order, is the serial one (small structures, where a thread per receiver
+// would leave the GPU idle behind a few long serial loops).
+template <bool FILL, bool WAVE>
+__global__ __launch_bounds__(256) void k_nlb_edges(const double* __restrict__ pos, int n, NlBatch B,
+                                                   const int* __restrict__ abin, const int* __restrict__ aimg,
+                                                   const int* __restrict__ bstart, const int* __restrict__ batoms,
+                                                   int* __restrict__ counts, const int* __restrict__ rowptr,
+                                                   int* __restrict__ src, int* __restrict__ shift) {
+  const int lane = WAVE ? (int)(threadIdx.x & 63) : 0;
+  const int a = WAVE ? (int)(blockIdx.x * 4 + (threadIdx.x >> 6)) : (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (a >= n) return;
+  const int s = nlb_struct_of(B, a);
+  const NlGeom& g = B.geo[s];
+  const int b0 = B.boff[s];
+  const double ax = pos[3 * a], ay = pos[3 * a + 1], az = pos[3 * a + 2];
+  const int lin = abin[a] - b0;
+  const int ba[3] = {lin / (g.nb[1] * g.nb[2]), (lin / g.nb[2]) % g.nb[1], lin % g.nb[2]};
+  const int oa[3] = {aimg[3 * a], aimg[3 * a + 1], aimg[3 * a + 2]};
+  int cnt = 0;
+  const int base = FILL ? rowptr[a] : 0;
+  int lo[3], hi[3];
+  for (int k = 0; k < 3; ++k) {
+    lo[k] = ba[k] - g.reach[k];
+    hi[k] = ba[k] + g.reach[k];
+    if (!g.pbc[k]) {
+      lo[k] = lo[k] < 0 ? 0 : lo[k];
+      hi[k] = hi[k] >= g.nb[k] ? g.nb[k] - 1 : hi[k];
+    }
+  }
+  for (int bx = lo[0]; bx <= hi[0]; ++bx) {
+    const int wx = ((bx % g.nb[0]) + g.nb[0]) % g.nb[0];
+    const int sx = (bx - wx) / g.nb[0];
+    for (int by = lo[1]; by <= hi[1]; ++by) {
+      const int wy = ((by % g.nb[1]) + g.nb[1]) % g.nb[1];
+      const int sy = (by - wy) / g.nb[1];
+      for (int bz = lo[2]; bz <= hi[2]; ++bz) {
+        const int wz = ((bz % g.nb[2]) + g.nb[2]) % g.nb[2];
+        const int sz = (bz - wz) / g.nb[2];
+        const int bl = b0 + (wx * g.nb[1] + wy) * g.nb[2] + wz;
+        const int q1 = bstart[bl + 1];
+        for (int q0 = bstart[bl]; q0 < q1; q0 += (WAVE ? 64 : 1)) {
+          const int q = q0 + lane;
+          int S[3] = {0, 0, 0};
+          int b = 0;
+          bool hit = false;
+          if (q < q1) {
+            b = batoms[q];
+            hit = nl_pair(pos, aimg, g, a, ax, ay, az, oa, sx, sy, sz, b, S);
+          }
+          if (WAVE) {
+            const unsigned long long m = __ballot(hit);
+            if (FILL && hit) {
+              const int slot = base + cnt + __popcll(m & ((1ull << lane) - 1ull));
+              src[slot] = b;
+              shift[3 * slot] = S[0];
+              shift[3 * slot + 1] = S[1];
+              shift[3 * slot + 2] = S[2];
+            }
+            cnt += __popcll(m);
+          } else if (hit) {
+            if (FILL) {
+              const int slot = base + cnt;
+              src[slot] = b;
+              shift[3 * slot] = S[0];
+              shift[3 * slot + 1] = S[1];
+              shift[3 * slot + 2] = S[2];
+            }
+            ++cnt;
+          }
+        }
+      }
+    }
+  }
+  if (!FILL && lane == 0) counts[a] = cnt;
+}
+
 // --------------------------------------------------------------- C ABI --
 extern "C" {
 
@@ -761,6 +925,129 @@ int tace_nl_fill(const double* pos, int64_t n_atoms, const double* cell, const i
   hipLaunchKernelGGL((k_nl_edges<true>), dim3((n + 63) / 64), dim3(64), 0, s, pos, n, g, abin, aimg, bstart, batoms,
                      nullptr, rowptr, src, shifts);
   return check_launch("tace_nl_fill");
+}
+
+// plan table: NlGeom[ns], then int32 struct_ptr[ns+1], int32 bin_off[ns+1]
+static int64_t nlb_plan_bytes(int64_t ns) {
+  return (int64_t)sizeof(NlGeom) * ns + (int64_t)sizeof(int32_t) * 2 * (ns + 1);
+}
+
+int64_t tace_nl_batch_plan(int32_t n_structs, const int64_t* sizes, const double* cells, const int32_t* pbcs,
+                           double cutoff, void* plan, int64_t plan_bytes, int64_t* n_atoms, int64_t* n_bins) {
+  if (n_structs < 1) return fail("tace_nl_batch_plan: need at least one structure");
+  if (!sizes || !cells || !pbcs || !n_atoms || !n_bins) return fail("tace_nl_batch_plan: null pointer");
+  const int64_t need = nlb_plan_bytes(n_structs);
+  if (!plan) return need;
+  if (plan_bytes < need) return fail("tace_nl_batch_plan: plan buffer too small");
+  NlGeom* geo = (NlGeom*)plan;
+  int32_t* sptr = (int32_t*)(geo + n_structs);
+  int32_t* boff = sptr + n_structs + 1;
+  int64_t na = 0, nb = 0;
+  for (int32_t i = 0; i < n_structs; ++i) {
+    if (sizes[i] < 0) return fail("tace_nl_batch_plan: negative structure size");
+    if (nl_geometry(cells + 9 * (int64_t)i, pbcs + 3 * (int64_t)i, cutoff, geo + i)) return -1;
+    sptr[i] = (int32_t)na;
+    boff[i] = (int32_t)nb;
+    na += sizes[i];
+    nb += (int64_t)geo[i].nb[0] * geo[i].nb[1] * geo[i].nb[2];
+    if (na > INT32_MAX / 8 || nb > INT32_MAX / 8) return fail("tace_nl_batch_plan: batch too large");
+  }
+  sptr[n_structs] = (int32_t)na;
+  boff[n_structs] = (int32_t)nb;
+  *n_atoms = na;
+  *n_bins = nb;
+  return need;
+}
+
+int64_t tace_nl_batch_workspace_bytes(int64_t n_atoms, int64_t n_bins) {
+  if (n_atoms < 0 || n_bins < 0 || n_atoms > INT32_MAX / 8 || n_bins > INT32_MAX / 8)
+    return fail("tace_nl_batch_workspace_bytes: bad sizes");
+  return (int64_t)sizeof(int32_t) * (n_atoms * 6 + n_bins * 3 + 1);
+}
+
+static int nlb_setup(const char* what, const void* plan, int32_t n_structs, int64_t n_atoms, int64_t n_bins,
+                     const void* workspace, int64_t workspace_bytes, NlBatch* B) {
+  if (n_structs < 1 || n_atoms < 0 || n_bins < 1 || n_atoms > INT32_MAX / 8 || n_bins > INT32_MAX / 8) {
+    char m[160];
+    snprintf(m, sizeof m, "%s: bad sizes", what);
+    return fail(m);
+  }
+  if (!plan || !workspace) {
+    char m[160];
+    snprintf(m, sizeof m, "%s: null pointer", what);
+    return fail(m);
+  }
+  if (workspace_bytes < (int64_t)sizeof(int32_t) * (n_atoms * 6 + n_bins * 3 + 1)) {
+    char m[160];
+    snprintf(m, sizeof m, "%s: workspace too small", what);
+    return fail(m);
+  }
+  B->geo = (const NlGeom*)plan;
+  B->sptr = (const int*)(B->geo + n_structs);
+  B->boff = B->sptr + n_structs + 1;
+  B->ns = n_structs;
+  return 0;
+}
+
+static bool nlb_wave_mode(int64_t n_atoms, int32_t mode) {
+  return mode == 2 || (mode == 0 && n_atoms < 32768);
+}
+
+int tace_nl_batch_count(const double* pos, int64_t n_atoms, int32_t n_structs, const void* plan, int64_t n_bins,
+                        void* workspace, int64_t workspace_bytes, int32_t mode, int32_t* counts, void* stream) {
+  NlBatch B;
+  if (nlb_setup("tace_nl_batch_count", plan, n_structs, n_atoms, n_bins, workspace, workspace_bytes, &B)) return -1;
+  if (mode < 0 || mode > 2) return fail("tace_nl_batch_count: mode must be 0 (auto), 1 (thread) or 2 (wave)");
+  if (n_atoms == 0) return 0;
+  if (!pos || !counts) return fail("tace_nl_batch_count: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int n = (int)n_atoms, nb = (int)n_bins;
+  int* abin = (int*)workspace;
+  int* aimg = abin + n;
+  int* bcount = aimg + 3 * n;
+  int* bstart = bcount + nb;
+  int* bfill = bstart + nb + 1;
+  int* batoms = bfill + nb;
+  int* unsorted = batoms + n;
+  launch_fill<int>(bcount, (size_t)nb, 0, s);
+  launch_fill<int>(bfill, (size_t)nb, 0, s);
+  const dim3 ga((n + 255) / 256), ba(256);
+  hipLaunchKernelGGL(k_nlb_bin, ga, ba, 0, s, pos, n, B, abin, aimg, bcount);
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bcount, nb, bstart);
+  hipLaunchKernelGGL(k_nl_scatter, ga, ba, 0, s, abin, n, bstart, bfill, unsorted);
+  hipLaunchKernelGGL(k_nlb_rank, ga, ba, 0, s, abin, n, bstart, unsorted, batoms);
+  if (nlb_wave_mode(n_atoms, mode))
+    hipLaunchKernelGGL((k_nlb_edges<false, true>), dim3((n + 3) / 4), dim3(256), 0, s, pos, n, B, abin, aimg,
+                       bstart, batoms, counts, nullptr, nullptr, nullptr);
+  else
+    hipLaunchKernelGGL((k_nlb_edges<false, false>), dim3((n + 255) / 256), dim3(256), 0, s, pos, n, B, abin, aimg,
+                       bstart, batoms, counts, nullptr, nullptr, nullptr);
+  return check_launch("tace_nl_batch_count");
+}
+
+int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, const void* plan, int64_t n_bins,
+                       const void* workspace, int64_t workspace_bytes, int32_t mode, const int32_t* rowptr,
+                       int32_t* src, int32_t* shifts, void* stream) {
+  NlBatch B;
+  if (nlb_setup("tace_nl_batch_fill", plan, n_structs, n_atoms, n_bins, workspace, workspace_bytes, &B)) return -1;
+  if (mode < 0 || mode > 2) return fail("tace_nl_batch_fill: mode must be 0 (auto), 1 (thread) or 2 (wave)");
+  if (n_atoms == 0) return 0;
+  if (!pos || !rowptr || !src || !shifts) return fail("tace_nl_batch_fill: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int n = (int)n_atoms, nb = (int)n_bins;
+  const int* abin = (const int*)workspace;
+  const int* aimg = abin + n;
+  const int* bcount = aimg + 3 * n;
+  const int* bstart = bcount + nb;
+  const int* bfill = bstart + nb + 1;
+  const int* batoms = bfill + nb;
+  if (nlb_wave_mode(n_atoms, mode))
+    hipLaunchKernelGGL((k_nlb_edges<true, true>), dim3((n + 3) / 4), dim3(256), 0, s, pos, n, B, abin, aimg,
+                       bstart, batoms, nullptr, rowptr, src, shifts);
+  else
+    hipLaunchKernelGGL((k_nlb_edges<true, false>), dim3((n + 255) / 256), dim3(256), 0, s, pos, n, B, abin, aimg,
+                       bstart, batoms, nullptr, rowptr, src, shifts);
+  return check_launch("tace_nl_batch_fill");
 }
 
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream) {

@@ -72,12 +72,12 @@ def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float,
     ptr = torch.zeros(len(structs) + 1, dtype=torch.int64)
     ptr[1:] = torch.cumsum(sizes_t, 0)
     ptr = ptr.to(device)
-    src64 = src.to(torch.int64) + ptr[:-1][batch[dst]]
+    src64 = src.to(torch.int64)
     attrs = torch.cat([one_hot(s["numbers"], atomic_numbers, dtype) for s in structs]).to(device)
     lat = torch.as_tensor(np.stack([np.asarray(s["cell"], dtype=np.float64).reshape(3, 3) for s in structs]),
                           dtype=dtype, device=device)
     ei = torch.stack([src64, dst])
-    plan = EdgePlan(n_tot, E, rowptr, (src64.to(torch.int32)).contiguous(), None)
+    plan = EdgePlan(n_tot, E, rowptr, src, None)
     return dict(positions=p64.to(dtype), node_attrs=attrs, edge_index=ei, edge_shifts=shifts.to(dtype),
                 lattice=lat, batch=batch, ptr=ptr, _edge_plan=plan, _dst32=dst.to(torch.int32))
 

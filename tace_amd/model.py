@@ -22,6 +22,7 @@ Anything else raises ``NotImplementedError`` at construction.
 
 from __future__ import annotations
 
+import collections
 import copy
 import math
 from types import SimpleNamespace
@@ -109,6 +110,14 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------- linears ----
+# per-species linears over at least this many species ranges run as one
+# segmented-GEMM launch (tace_seg_linear); fewer, larger ranges stay one
+# library GEMM per instruction and species
+SEG_LINEAR_MIN_RANGES = 3
+# tile edge of the float32 segmented GEMM: 128 = MFMA kernel, 64 = FMA kernel
+SEG_LINEAR_TILE_F32 = 128
+
+
 class _LinearLayout:
     """e3nn ``o3.Linear`` bookkeeping: instructions (i_in, i_out) between equal
     irreps in i_in-major order, path weight (sum of mul_in into i_out)^-1/2,
@@ -138,6 +147,34 @@ class _LinearLayout:
         self.dim_in, self.dim_out = self.gin.dim, self.gout.dim
         self.read = {i for (i, *_r) in self.ins}
         self.written = {o for (_, o, *_r) in self.ins}
+        self._seg = collections.OrderedDict()
+
+    def seg_plan(self, kind: str, rr, Z: int, x: torch.Tensor, weight: torch.Tensor,
+                 bias: Optional[torch.Tensor]) -> ops.SegLinearPlan:
+        """``tace_seg_linear`` tables of the forward ("fwd": x -> out, bias
+        added) or the input gradient ("bwd": g_out -> g_x, W^T) over species
+        ranges ``rr`` of Z rows; the last few are cached."""
+        tile = SEG_LINEAR_TILE_F32 if x.dtype == torch.float32 else 64
+        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile)
+        plan = self._seg.get(key)
+        if plan is not None:
+            self._seg.move_to_end(key)
+            return plan
+        if kind == "fwd":
+            boffs = {o: boff for (o, boff, m) in self.bias_blocks} if bias is not None else {}
+            outs = [(s, m, d, boffs.get(o)) for o, (s, m, d) in enumerate(self.gout.blocks)]
+            ins = [(o, self.gin.blocks[i][0], mi, off, False, pw) for (i, o, off, mi, mo, pw) in self.ins]
+            xn, yn = Z * self.dim_in, Z * self.dim_out
+        else:
+            outs = [(s, m, d, None) for (s, m, d) in self.gin.blocks]
+            ins = [(i, self.gout.blocks[o][0], mo, off, True, pw) for (i, o, off, mi, mo, pw) in self.ins]
+            xn, yn = Z * self.dim_out, Z * self.dim_in
+        plan = ops.SegLinearPlan(Z, outs, ins, rr, self.weight_numel, self.bias_numel, xn, yn, weight.numel(),
+                                 0 if bias is None else bias.numel(), x.device, tile)
+        self._seg[key] = plan
+        if len(self._seg) > 16:
+            self._seg.popitem(last=False)
+        return plan
 
 
 class _LinearFn(torch.autograd.Function):
@@ -154,6 +191,12 @@ class _LinearFn(torch.autograd.Function):
         shared = weight.dim() == 1
         rr = [(None, 0, Z)] if shared else ranges
         rr = [r for r in rr if r[2] > r[1]]
+        ctx.seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES
+        ctx.save_for_backward(x, weight, bias)
+        ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
+        if ctx.seg:
+            # all species and instructions in one segmented-GEMM launch
+            return ops.seg_linear(x, out, weight, bias, lay.seg_plan("fwd", rr, Z, x, weight, bias), alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
             for (sp, a, b) in rr:
@@ -169,8 +212,6 @@ class _LinearFn(torch.autograd.Function):
                 for (sp, a, b) in rr:
                     bv = (bias if shared else bias[sp])[boff:boff + m]
                     lay.gout.block(out, o, a, b).add_(bv, alpha=alpha)
-        ctx.save_for_backward(x, weight, bias)
-        ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
         return out
 
     @staticmethod
@@ -182,19 +223,21 @@ class _LinearFn(torch.autograd.Function):
         gx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
         gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
         gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
+        if ctx.seg and gx is not None:
+            ops.seg_linear(gout, gx, weight, None, lay.seg_plan("bwd", rr, x.shape[0], x, weight, None), alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
             for (sp, a, b) in rr:
                 G = lay.gout.block(gout, o, a, b)
                 W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
-                if gx is not None:
+                if gx is not None and not ctx.seg:
                     lay.gin.block(gx, i, a, b).addmm_(G, W.t(), beta=1.0 if (i, sp) in done else 0.0,
                                                       alpha=pw * alpha)
                     done.add((i, sp))
                 if gw is not None:
                     tgt = (gw if shared else gw[sp])[off:off + mi * mo].view(mi, mo)
                     tgt.addmm_(lay.gin.block(x, i, a, b).t(), G, alpha=pw * alpha)
-        if gx is not None:
+        if gx is not None and not ctx.seg:
             for i in range(len(lay.gin.blocks)):
                 if i not in lay.read:
                     lay.gin.block(gx, i).zero_()

@@ -695,6 +695,105 @@ def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> tor
     return _RadialMlp.apply(radial.contiguous(), flat, len(mats))
 
 
+# ------------------------------------------------------ per-species linears ----
+class SegLinearPlan:
+    """Device tables of ``tace_seg_linear`` for one direction of one
+    per-species linear over one set of species row ranges.
+
+    out_blocks: per output block (s, n, d, bias_off): element column offset s
+    of the block in the group-major feature row (the block starts at element
+    Z*s), width n, 2l+1 = d, bias offset within one species' bias (None = no
+    bias).  ins: (out_block, s_in, k, w_off, trans, scale) contributions (k =
+    input block width, w_off = weight offset within one species' weights).
+    ranges: [(species or None, a, b)] node ranges (species-sorted rows; None =
+    the shared weight).  w_stride / b_stride: elements per species of weight /
+    bias.  x_numel / y_numel / w_numel / b_numel: sizes every offset is
+    checked against before the tables go to the device.  tile: the tile edge
+    (128: float32 MFMA kernel, 64: FMA kernel)."""
+
+    def __init__(self, Z, out_blocks, ins, ranges, w_stride, b_stride, x_numel, y_numel, w_numel, b_numel, device,
+                 tile: int = 64):
+        TM = tile
+        self.tile = tile
+        tiles, contribs, scales = [], [], []
+        nc = 0
+        for ob, (s_o, n, d, boff) in enumerate(out_blocks):
+            mine = [c for c in ins if c[0] == ob]
+            c0s = np.arange(0, n, TM, dtype=np.int64)
+            for (sp, a, b) in ranges:
+                if b <= a:
+                    continue
+                r0 = np.arange(a * d, b * d, TM, dtype=np.int64)
+                rows = np.minimum(b * d - r0, TM)
+                R, Cc = np.meshgrid(r0, c0s, indexing="ij")
+                Rows = np.broadcast_to(rows[:, None], R.shape)
+                T = R.size
+                t = np.zeros((T, 8), dtype=np.int64)
+                t[:, 0] = Z * s_o + R.ravel() * n
+                t[:, 1] = Rows.ravel()
+                t[:, 2] = n
+                t[:, 3] = Cc.ravel()
+                t[:, 4] = -1 if boff is None else boff + (0 if sp is None else sp * b_stride)
+                k_each = len(mine)
+                t[:, 5] = nc + np.arange(T, dtype=np.int64) * k_each
+                t[:, 6] = t[:, 5] + k_each
+                nc += T * k_each
+                tiles.append(t)
+                if k_each:
+                    c = np.zeros((T, k_each, 4), dtype=np.int64)
+                    for j, (_, s_i, k, w_off, trans, sc) in enumerate(mine):
+                        c[:, j, 0] = Z * s_i + R.ravel() * k
+                        c[:, j, 1] = k
+                        c[:, j, 2] = w_off + (0 if sp is None else sp * w_stride)
+                        c[:, j, 3] = int(trans)
+                    contribs.append(c.reshape(-1, 4))
+                    scales.append(np.tile(np.array([m[5] for m in mine], dtype=np.float64), T))
+        t = np.concatenate(tiles) if tiles else np.zeros((0, 8), dtype=np.int64)
+        c = np.concatenate(contribs) if contribs else np.zeros((0, 4), dtype=np.int64)
+        s = np.concatenate(scales) if scales else np.zeros(0, dtype=np.float64)
+        # every access of every tile inside its array
+        if len(t):
+            last_col = np.minimum(t[:, 3] + TM, t[:, 2])
+            if (t[:, 0] + (t[:, 1] - 1) * t[:, 2] + last_col).max() > y_numel:
+                raise ValueError("seg linear plan: output tile out of range")
+            if (t[:, 4] >= 0).any() and (t[:, 4] + t[:, 2])[t[:, 4] >= 0].max() > b_numel:
+                raise ValueError("seg linear plan: bias out of range")
+        if len(c):
+            rows_c = np.repeat(t[:, 1], t[:, 6] - t[:, 5])
+            n_c = np.repeat(t[:, 2], t[:, 6] - t[:, 5])
+            if (c[:, 0] + rows_c * c[:, 1]).max() > x_numel:
+                raise ValueError("seg linear plan: input tile out of range")
+            if (c[:, 2] + c[:, 1] * n_c).max() > w_numel:
+                raise ValueError("seg linear plan: weight out of range")
+        self.n_tiles = len(t)
+        self.x_numel, self.y_numel, self.w_numel, self.b_numel = x_numel, y_numel, w_numel, b_numel
+        self.tiles = torch.from_numpy(np.ascontiguousarray(t)).to(device)
+        self.contribs = torch.from_numpy(np.ascontiguousarray(c) if len(c) else np.zeros((1, 4), np.int64)).to(device)
+        self.scales = torch.from_numpy(s if len(s) else np.zeros(1)).to(device)
+
+
+def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], plan: SegLinearPlan,
+               alpha: float) -> torch.Tensor:
+    """Runs ``plan`` (``tace_seg_linear``) from x into y (every element of y
+    that a tile covers is overwritten); returns y."""
+    dt = x.dtype
+    for t, nm, n in ((x, "x", plan.x_numel), (y, "y", plan.y_numel), (w, "weight", plan.w_numel)):
+        _req(t, nm, dt)
+        if t.numel() != n:
+            raise ValueError(f"seg linear: {nm} has {t.numel()} elements, the plan was built for {n}")
+    if bias is not None:
+        _req(bias, "bias", dt)
+        if bias.numel() != plan.b_numel:
+            raise ValueError("seg linear: bias size differs from the plan's")
+    tok = _t0("seg_linear")
+    N.check(N.lib().tace_seg_linear(N.dtype_code(dt), plan.tile, x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                    None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(), plan.n_tiles,
+                                    plan.contribs.data_ptr(), plan.scales.data_ptr(), float(alpha),
+                                    N.stream_ptr(x.device)), "tace_seg_linear")
+    _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel))
+    return y
+
+
 def edge_ace_paths(lmax: int) -> List[Tuple[int, int, int, bool]]:
     """(m3, m1, m2, is_sum) of the complex edge-ACE product in weight order."""
     out = []
@@ -823,54 +922,54 @@ def neighbour_list(positions: torch.Tensor, cell, pbc, cutoff: float):
     return rowptr, src, shifts
 
 
-def neighbour_list_batch(positions: torch.Tensor, sizes: Sequence[int], cells, pbcs, cutoff: float):
-    """The cell-list neighbour search for a batch of structures in one pass:
-    every structure's count kernel, one scan over the whole batch, one host
-    synchronisation for the total edge count, then every fill kernel.
-    ``positions`` [sum(sizes), 3] float64 (structures back to back).
+def neighbour_list_batch(positions: torch.Tensor, sizes: Sequence[int], cells, pbcs, cutoff: float,
+                         mode: int = 0):
+    """The cell-list neighbour search for a batch of structures in one pass
+    (``tace_nl_batch_*``): one launch per phase for all structures, one host
+    synchronisation for the total edge count.  ``positions`` [sum(sizes), 3]
+    float64 (structures back to back); ``mode`` 0 automatic, 1 a thread per
+    receiver, 2 a wavefront per receiver (same result).
 
     Returns ``(rowptr int32 [N+1], src int32 [E], shifts int32 [E,3])`` over
-    the batch: receiver n's edges are slots rowptr[n]..rowptr[n+1]; ``src``
-    holds the sender's index *within its structure*."""
+    the batch, node ids batch-global: receiver n's edges are slots
+    rowptr[n]..rowptr[n+1], each structure's in the order ``neighbour_list``
+    gives for it alone."""
     _req(positions, "positions", torch.float64)
     dev = positions.device
     L = N.lib()
+    ns = len(sizes)
     n_tot = int(sum(sizes))
     if positions.shape[0] != n_tot:
         raise ValueError(f"positions has {positions.shape[0]} rows, sizes sum to {n_tot}")
-    geo, ws_off, total = [], [], 0
-    for n, cell, pbc in zip(sizes, cells, pbcs):
-        cell_np = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(3, 3))
-        pbc_np = np.ascontiguousarray(np.broadcast_to(np.asarray(pbc, dtype=np.int32), (3,)))
-        nb = L.tace_nl_workspace_bytes(int(n), cell_np.ctypes.data, pbc_np.ctypes.data, float(cutoff))
-        if nb < 0:
-            raise N.NativeError(L.tace_last_error().decode())
-        geo.append((int(n), cell_np, pbc_np, int(nb)))
-        ws_off.append(total)
-        total += (max(int(nb), 4) + 255) // 256 * 256
-    ws = torch.empty(max(total, 256), dtype=torch.uint8, device=dev)
-    counts = torch.empty(n_tot, dtype=torch.int32, device=dev)
+    sizes_np = np.ascontiguousarray(np.asarray(sizes, dtype=np.int64))
+    cells_np = np.ascontiguousarray(np.stack([np.asarray(c, dtype=np.float64).reshape(3, 3) for c in cells]))
+    pbcs_np = np.ascontiguousarray(np.stack([np.broadcast_to(np.asarray(p, dtype=np.int32), (3,)) for p in pbcs]))
+    na, nb = ctypes.c_int64(0), ctypes.c_int64(0)
+    need = L.tace_nl_batch_plan(ns, sizes_np.ctypes.data, cells_np.ctypes.data, pbcs_np.ctypes.data, float(cutoff),
+                                None, 0, ctypes.byref(na), ctypes.byref(nb))
+    if need < 0:
+        raise N.NativeError(L.tace_last_error().decode())
+    host = np.zeros(need, dtype=np.uint8)
+    if L.tace_nl_batch_plan(ns, sizes_np.ctypes.data, cells_np.ctypes.data, pbcs_np.ctypes.data, float(cutoff),
+                            host.ctypes.data, need, ctypes.byref(na), ctypes.byref(nb)) < 0:
+        raise N.NativeError(L.tace_last_error().decode())
+    plan = torch.from_numpy(host).to(dev)
+    wsb = L.tace_nl_batch_workspace_bytes(na.value, nb.value)
+    if wsb < 0:
+        raise N.NativeError(L.tace_last_error().decode())
+    ws = torch.empty(max(wsb, 4), dtype=torch.uint8, device=dev)
+    counts = torch.empty(max(n_tot, 1), dtype=torch.int32, device=dev)
     st = N.stream_ptr(dev)
-    a = 0
-    for (n, cell_np, pbc_np, nb), wo in zip(geo, ws_off):
-        if n:
-            N.check(L.tace_nl_count(positions[a:a + n].data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data,
-                                    float(cutoff), ws.data_ptr() + wo, nb, counts[a:a + n].data_ptr(), st),
-                    "tace_nl_count")
-        a += n
+    N.check(L.tace_nl_batch_count(positions.data_ptr(), n_tot, ns, plan.data_ptr(), nb.value, ws.data_ptr(), wsb,
+                                  mode, counts.data_ptr(), st), "tace_nl_batch_count")
     rowptr = torch.empty(n_tot + 1, dtype=torch.int32, device=dev)
     N.check(L.tace_scan_i32(counts.data_ptr(), n_tot, rowptr.data_ptr(), st), "tace_scan_i32")
     E = int(rowptr[-1].item())
     src = torch.empty(E, dtype=torch.int32, device=dev)
     shifts = torch.empty(E, 3, dtype=torch.int32, device=dev)
     if E > 0:
-        a = 0
-        for (n, cell_np, pbc_np, nb), wo in zip(geo, ws_off):
-            if n:
-                # the structure's slice of the batch rowptr holds absolute slots
-                N.check(L.tace_nl_fill(positions[a:a + n].data_ptr(), n, cell_np.ctypes.data, pbc_np.ctypes.data,
-                                       float(cutoff), ws.data_ptr() + wo, rowptr[a:a + n + 1].data_ptr(),
-                                       src.data_ptr(), shifts.data_ptr(), st), "tace_nl_fill")
-            a += n
+        N.check(L.tace_nl_batch_fill(positions.data_ptr(), n_tot, ns, plan.data_ptr(), nb.value, ws.data_ptr(), wsb,
+                                     mode, rowptr.data_ptr(), src.data_ptr(), shifts.data_ptr(), st),
+                "tace_nl_batch_fill")
     return rowptr, src, shifts
 

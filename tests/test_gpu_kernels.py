@@ -192,6 +192,35 @@ def test_neighbour_list_bit_exact_edge_set(cuda, name, s, rc):
     assert torch.equal(r2, rowptr) and np.array_equal(s2.cpu().numpy(), src) and np.array_equal(h2.cpu().numpy(), sh)
 
 
+@pytest.mark.parametrize("mode", [1, 2])
+def test_neighbour_list_batch_equals_per_structure(cuda, mode):
+    """The batched search (a thread or a wavefront per receiver) gives every
+    structure's edges exactly as the single-structure search does, in the
+    same order, with batch-global node ids; the batch mixes all the
+    single-structure cases (skewed and shifted cells, a perfect lattice, tiny
+    triclinic crystals), a non-periodic molecule and a one-atom cell."""
+    structs = [s for _, s, _rc in _nl_cases()]
+    mol = structures.water_box(n_side=2, box=6.2, seed=9)
+    structs.append(dict(mol, pbc=[False, False, False], cell=np.eye(3) * 30.0))
+    structs.append(dict(positions=np.array([[0.3, 0.2, 0.1]]), numbers=np.array([26]),
+                        cell=np.eye(3) * 2.5, pbc=[True, True, True]))
+    rc = 5.5
+    sizes = [len(s["positions"]) for s in structs]
+    pos = torch.as_tensor(np.concatenate([np.asarray(s["positions"], dtype=np.float64) for s in structs]),
+                          device=cuda)
+    rowptr, src, sh = ops.neighbour_list_batch(pos, sizes, [s["cell"] for s in structs],
+                                               [s["pbc"] for s in structs], rc, mode=mode)
+    a = 0
+    for s, n in zip(structs, sizes):
+        r1, s1, h1 = ops.neighbour_list(pos[a:a + n].contiguous(), s["cell"], s["pbc"], rc)
+        e0, e1 = int(rowptr[a]), int(rowptr[a + n])
+        assert torch.equal((rowptr[a:a + n + 1] - e0).cpu(), r1.cpu())
+        assert torch.equal((src[e0:e1] - a).cpu(), s1.cpu())
+        assert torch.equal(sh[e0:e1].cpu(), h1.cpu())
+        a += n
+    assert int(rowptr[-1]) == src.shape[0]
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("layout", [2, 3, 7])
 @pytest.mark.parametrize("L", [2, 3])
@@ -397,3 +426,87 @@ def test_radial_mlp_matches_oracle(cuda, dtype, dims):
     close(out, out_o, dtype, "mlp out")
     (gR,) = torch.autograd.grad((out * go.to(dtype).to(cuda)).sum(), r)
     close(gR, gR_o, dtype, "grad radial")
+
+
+# --------------------------------------------------- per-species linears ----
+def _element_linear_reference(x, W, b, irreps_in, irreps_out, species, alpha):
+    """Per node: y_o = alpha (sum_{i -> o} pw x_i @ W[species](i, o) + bias[species]),
+    in e3nn's o3.Linear instruction order (every pair of equal irreps,
+    path weight (sum of mul_in into o)^-1/2), on [Z, 2l+1, mul] views."""
+    from tace_amd.so3 import Irreps
+    ii, io = Irreps(irreps_in), Irreps(irreps_out)
+    Z = x.shape[0]
+
+    # group-major: block of mul m, dim d starts at element Z * s
+    def blocks(t, irr):
+        out, s = [], 0
+        for m, ir in irr:
+            out.append(t.reshape(-1)[Z * s:Z * (s + m * ir.dim)].view(Z, ir.dim, m))
+            s += m * ir.dim
+        return out
+    xb = blocks(x, ii)
+    pairs = [(i, o) for i, (_, a) in enumerate(ii) for o, (_, q) in enumerate(io) if a == q]
+    fan = {}
+    for i, o in pairs:
+        fan[o] = fan.get(o, 0) + ii[i][0]
+    yb = [torch.zeros(Z, ir.dim, m, dtype=x.dtype) for m, ir in io]
+    off = 0
+    for i, o in pairs:
+        mi, mo = ii[i][0], io[o][0]
+        Ws = W[:, off:off + mi * mo].view(-1, mi, mo)[species]          # [Z, mi, mo]
+        yb[o] = yb[o] + fan[o] ** -0.5 * torch.einsum("zdi,zio->zdo", xb[i], Ws)
+        off += mi * mo
+    boff = 0
+    for o, (m, ir) in enumerate(io):
+        if ir.l == 0 and ir.p == 1:
+            yb[o] = yb[o] + b[:, boff:boff + m][species][:, None, :]
+            boff += m
+    return alpha * torch.cat([t.reshape(-1) for t in yb]).view(Z, -1)
+
+
+SEG_CASES = [("8x0e+5x0e+6x1o+4x1o+3x2e", "70x0e+6x1o+65x2e+2x3o", [0, 1, 17, 64, 65, 3, 130, 0]),
+             ("64x0e+36x0e+132x1o+20x2e", "260x0e+68x1o+40x2e", [140, 0, 3, 290, 1])]
+
+
+@pytest.mark.parametrize("dtype,tile", [(torch.float64, 64), (torch.float32, 128), (torch.float32, 64)])
+@pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
+def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts, monkeypatch):
+    """One-launch per-species linear (tace_seg_linear) against an independent
+    per-node restatement: several inputs into one output block (two 0e, two
+    1o), a 65-wide block (two column tiles, one partial), an output block no
+    instruction writes (3o: zeros), species with 0, 1, 17, 64, 65 and 130
+    nodes; then wide, 4-aligned blocks with k tails (36, 20) over several
+    128-row and 128-column tiles; forward with bias, then the input
+    gradient."""
+    from tace_amd import model as pm
+    monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", tile)
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).to(dtype)
+    g = torch.Generator().manual_seed(5)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S).to(dtype)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(lin.weight.shape, generator=g, dtype=dtype))
+        lin.bias.copy_(torch.randn(lin.bias.shape, generator=g, dtype=dtype))
+    x = torch.randn(Z, lin.lay.dim_in, generator=g, dtype=dtype)
+    go = torch.randn(Z, lin.lay.dim_out, generator=g, dtype=dtype)
+    alpha = 0.7
+    xr = x.clone().requires_grad_(True)
+    want = _element_linear_reference(xr, lin.weight.detach(), lin.bias.detach(), irr_in, irr_out, species, alpha)
+    (gx_want,) = torch.autograd.grad(want, xr, go)
+    lin = lin.to(cuda)
+    sp = pm.SpeciesPlan(attrs.to(cuda))
+    assert len(sp.ranges) >= pm.SEG_LINEAR_MIN_RANGES
+    for rep in range(2):   # second call: cached plan
+        xg = x.to(cuda).requires_grad_(True)
+        got = lin(xg, sp, alpha)
+        (gx,) = torch.autograd.grad(got, xg, go.to(cuda))
+        close(got, want, dtype, f"seg linear fwd (call {rep})")
+        close(gx, gx_want, dtype, f"seg linear grad x (call {rep})")
+    # the weight gradient (library GEMM path) next to the segmented forward
+    xg = x.to(cuda)
+    wr = lin.weight.detach().cpu().clone().requires_grad_(True)
+    ref = _element_linear_reference(x, wr, lin.bias.detach().cpu(), irr_in, irr_out, species, alpha)
+    (gw_want,) = torch.autograd.grad(ref, wr, go)
+    (gw,) = torch.autograd.grad(lin(xg, sp, alpha), lin.weight, go.to(cuda))
+    close(gw, gw_want, dtype, "seg linear grad w")

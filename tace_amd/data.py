@@ -50,36 +50,41 @@ def collate(structs: List[Dict], edges: List[Tuple[np.ndarray, np.ndarray]], ato
     return {k: v.to(device) for k, v in d.items()}
 
 
-def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float, dtype=torch.float32,
-              device="cuda") -> Dict[str, torch.Tensor]:
-    """Batch built on the GPU: one batched HIP cell-list neighbour search over
-    all structures (float64; ``ops.neighbour_list_batch``), edges grouped by
-    receiver (``edge_index[1]`` non-decreasing).  The result carries its
-    receiver CSR plan."""
+def device_graph(p64: torch.Tensor, sizes: Sequence[int], cells, pbcs, cutoff: float) -> Dict[str, torch.Tensor]:
+    """Edges of a batch whose float64 positions ``p64`` [sum(sizes), 3] are
+    already on the GPU: one batched HIP cell-list search
+    (``ops.neighbour_list_batch``), edges grouped by receiver
+    (``edge_index[1]`` non-decreasing), node ids batch-global.  Returns
+    edge_index (int64), integer edge_shifts (int32) and the receiver CSR plan
+    the model's kernels take (``_edge_plan``, ``_dst32``)."""
     from .ops import EdgePlan, neighbour_list_batch
 
-    sizes = [len(s["positions"]) for s in structs]
-    n_tot = sum(sizes)
-    p64 = torch.as_tensor(np.concatenate([np.asarray(s["positions"], dtype=np.float64).reshape(-1, 3)
-                                          for s in structs]), device=device)
-    rowptr, src, shifts = neighbour_list_batch(p64, sizes, [s["cell"] for s in structs], [s["pbc"] for s in structs],
-                                               cutoff)
+    n_tot = int(p64.shape[0])
+    rowptr, src, shifts = neighbour_list_batch(p64, sizes, cells, pbcs, cutoff)
     E = src.shape[0]
     counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
-    dst = torch.repeat_interleave(torch.arange(n_tot, device=device), counts, output_size=E)
+    dst = torch.repeat_interleave(torch.arange(n_tot, device=p64.device), counts, output_size=E)
+    return dict(edge_index=torch.stack([src.to(torch.int64), dst]), edge_shifts=shifts,
+                _edge_plan=EdgePlan(n_tot, E, rowptr, src, None), _dst32=dst.to(torch.int32))
+
+
+def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float, dtype=torch.float32,
+              device="cuda") -> Dict[str, torch.Tensor]:
+    """Batch built on the GPU (``device_graph``) from host structures; the
+    result carries its receiver CSR plan."""
+    sizes = [len(s["positions"]) for s in structs]
+    p64 = torch.as_tensor(np.concatenate([np.asarray(s["positions"], dtype=np.float64).reshape(-1, 3)
+                                          for s in structs]), device=device)
+    g = device_graph(p64, sizes, [s["cell"] for s in structs], [s["pbc"] for s in structs], cutoff)
     sizes_t = torch.tensor(sizes, dtype=torch.int64)
     batch = torch.repeat_interleave(torch.arange(len(structs)), sizes_t).to(device)
     ptr = torch.zeros(len(structs) + 1, dtype=torch.int64)
     ptr[1:] = torch.cumsum(sizes_t, 0)
-    ptr = ptr.to(device)
-    src64 = src.to(torch.int64)
     attrs = torch.cat([one_hot(s["numbers"], atomic_numbers, dtype) for s in structs]).to(device)
     lat = torch.as_tensor(np.stack([np.asarray(s["cell"], dtype=np.float64).reshape(3, 3) for s in structs]),
                           dtype=dtype, device=device)
-    ei = torch.stack([src64, dst])
-    plan = EdgePlan(n_tot, E, rowptr, src, None)
-    return dict(positions=p64.to(dtype), node_attrs=attrs, edge_index=ei, edge_shifts=shifts.to(dtype),
-                lattice=lat, batch=batch, ptr=ptr, _edge_plan=plan, _dst32=dst.to(torch.int32))
+    g["edge_shifts"] = g["edge_shifts"].to(dtype)
+    return dict(positions=p64.to(dtype), node_attrs=attrs, lattice=lat, batch=batch, ptr=ptr.to(device), **g)
 
 
 def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cutoff: float,

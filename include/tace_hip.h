@@ -9,7 +9,8 @@
  *     synchronises the host.
  *   - Return value: 0 on success, < 0 on error; tace_last_error() returns a
  *     thread-local message for the last failure.
- *   - dtype: TACE_F32 or TACE_F64; all float arrays of one call share it.
+ *   - dtype: TACE_F32 or TACE_F64; all float arrays of one call share it (five TECE
+ *     functions also take TACE_F32_BF16, see below).
  *   - Node features use e3nn's mul_ir layout: irrep blocks concatenated,
  *     each block [channels, 2l+1] row-major.
  *
@@ -39,10 +40,16 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 11
+#define TACE_HIP_ABI_VERSION 12
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
+/* float32 arithmetic and inputs; the outputs that feed the TECE SO(2)-linear
+ * GEMMs stored as bfloat16 (round to nearest even).  Accepted by
+ * tace_edge_rotate_in_fwd (m_src, m_dst, m_w), tace_tece_edge_ace_fwd (o*),
+ * tace_tece_edge_ace_bwd (g_y*), tace_tece_score_bwd (g_q, g_k) and
+ * tace_tece_rotate_out_bwd (g_m); every other output stays float32. */
+#define TACE_F32_BF16 2
 
 const char* tace_last_error(void);
 int tace_abi_version(void);

@@ -305,6 +305,20 @@ struct Blk {
   T* p[4];
 };
 
+// Outputs that feed the SO(2)-linear GEMMs may be stored as bfloat16 (the
+// bf16 channel-mixing option): round to nearest even, as torch's cast does,
+// so the GEMM sees the operand it would get from a float32 output + cast.
+typedef uint16_t bf16_t;
+template <typename TO, typename T>
+__device__ __forceinline__ TO out_cvt(T v) { return (TO)v; }
+template <>
+__device__ __forceinline__ bf16_t out_cvt<bf16_t, float>(float v) {
+  uint32_t u = __float_as_uint(v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
 template <int L>
 __device__ __forceinline__ constexpr int mblk(int r) {
   if (r <= L) return 0;
@@ -391,11 +405,11 @@ __global__ __launch_bounds__(256) void k_score_fwd(const Blk<const T> q, const B
   }
 }
 
-template <typename T, int L, int NS>
+template <typename T, typename TO, int L, int NS>
 __global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const Blk<const T> k,
                                                    const T* __restrict__ rp, const T* __restrict__ tscale,
                                                    const T* __restrict__ gs, int64_t E, int C, int H,
-                                                   const Blk<T> gq, const Blk<T> gk, T* __restrict__ grp) {
+                                                   const Blk<TO> gq, const Blk<TO> gk, T* __restrict__ grp) {
   const int64_t e = wave_edge();
   if (e >= E) return;
   const int lane = (int)threadIdx.x & 63;
@@ -416,8 +430,8 @@ __global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const B
 #pragma unroll
       for (int r = 0; r <= L; ++r) {
         const T qv = erow<L>(q, e, r, C)[c], kv = erow<L>(k, e, r, C)[c];
-        erow<L>(gq, e, r, C)[c] = G * kv;
-        erow<L>(gk, e, r, C)[c] = G * qv;
+        erow<L>(gq, e, r, C)[c] = out_cvt<TO>(G * kv);
+        erow<L>(gk, e, r, C)[c] = out_cvt<TO>(G * qv);
       }
 #pragma unroll
       for (int m = 1; m <= L; ++m) {
@@ -431,10 +445,10 @@ __global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const B
           const T kr = erow<L>(k, e, ir, C)[c], ki = erow<L>(k, e, ii, C)[c];
           A += qr * kr + qi * ki;
           B += qi * kr - qr * ki;
-          erow<L>(gq, e, ir, C)[c] = G * (cs * kr - sn * ki);
-          erow<L>(gq, e, ii, C)[c] = G * (cs * ki + sn * kr);
-          erow<L>(gk, e, ir, C)[c] = G * (cs * qr + sn * qi);
-          erow<L>(gk, e, ii, C)[c] = G * (cs * qi - sn * qr);
+          erow<L>(gq, e, ir, C)[c] = out_cvt<TO>(G * (cs * kr - sn * ki));
+          erow<L>(gq, e, ii, C)[c] = out_cvt<TO>(G * (cs * ki + sn * kr));
+          erow<L>(gk, e, ir, C)[c] = out_cvt<TO>(G * (cs * qr + sn * qi));
+          erow<L>(gk, e, ii, C)[c] = out_cvt<TO>(G * (cs * qi - sn * qr));
         }
         d[0] += T(m) * (cs * B - sn * A);
       }
@@ -471,12 +485,12 @@ __device__ __forceinline__ int m_comp(int r) {
   return -1;
 }
 
-template <typename T, int L, int NS>
+template <typename T, typename TO, int L, int NS>
 __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, const T* __restrict__ W,
                                                    const int64_t* __restrict__ rows_src,
                                                    const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
-                                                   int64_t n_rows, int64_t E, int C, const Blk<T> ms,
-                                                   const Blk<T> md, const Blk<T> mw) {
+                                                   int64_t n_rows, int64_t E, int C, const Blk<TO> ms,
+                                                   const Blk<TO> md, const Blk<TO> mw) {
   constexpr int K = (L + 1) * (L + 1), NC = (L + 1) * (L + 2) / 2;
   const int64_t e = wave_edge();
   if (e >= E) return;
@@ -501,8 +515,8 @@ __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, cons
       T a = 0;
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) a += w[r * K + kk] * xk[kk];
-      erow<L>(src ? ms : md, e, r, C)[cc] = a;
-      if (wr) erow<L>(mw, e, r, C2)[c] = wr[(e * NC + m_comp<L>(r)) * C2 + c] * a;
+      erow<L>(src ? ms : md, e, r, C)[cc] = out_cvt<TO>(a);
+      if (wr) erow<L>(mw, e, r, C2)[c] = out_cvt<TO>(wr[(e * NC + m_comp<L>(r)) * C2 + c] * a);
     }
   }
 }
@@ -634,18 +648,18 @@ struct AcePaths {
 template <typename T>
 __device__ __forceinline__ T scaled_sigmoid(T z) { return T(TACE_ACE_SCST) / (T(1) + exp(-z)); }
 
-template <typename T, int L>
+template <typename T, typename TO, int L>
 __global__ __launch_bounds__(256) void k_edge_ace_fwd(const T* __restrict__ y0, const T* __restrict__ y1,
                                                       const T* __restrict__ y2, const T* __restrict__ y3, int64_t E,
-                                                      int A, T* __restrict__ o0, T* __restrict__ o1,
-                                                      T* __restrict__ o2, T* __restrict__ o3) {
+                                                      int A, TO* __restrict__ o0, TO* __restrict__ o1,
+                                                      TO* __restrict__ o2, TO* __restrict__ o3) {
   constexpr int n = L + 1, NG = n * (L + 1), NP = AcePaths<L>::total();
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= E * A) return;
   const int64_t e = t / A;
   const int a = (int)(t - e * A);
   const T* ym[4] = {y0, y1, y2, y3};
-  T* om[4] = {o0, o1, o2, o3};
+  TO* om[4] = {o0, o1, o2, o3};
   const int64_t r0 = e * (int64_t)(NP * n * A + n * A + (NG + n) * A);
   const int cv0 = NP * n * A, cg = cv0 + n * A, cu0 = cg + NG * A;
   // u, v [m][sign][i]
@@ -700,22 +714,22 @@ __global__ __launch_bounds__(256) void k_edge_ace_fwd(const T* __restrict__ y0, 
     for (int i = 0; i < n; ++i) {
       const T g = scaled_sigmoid(y0[r0 + cg + (m3 * n + i) * A + a]);
       if (m3 == 0) {
-        o0[e * (n * A) + i * A + a] = u[0][0][i] * (T(1) + g) + re[0][i] * sc;
+        o0[e * (n * A) + i * A + a] = out_cvt<TO>(u[0][0][i] * (T(1) + g) + re[0][i] * sc);
       } else {
-        om[m3][(2 * e) * (n * A) + i * A + a] = u[m3][0][i] * (T(1) + g) + re[m3][i] * sc;
-        om[m3][(2 * e + 1) * (n * A) + i * A + a] = u[m3][1][i] * (T(1) + g) + im[m3][i] * sc;
+        om[m3][(2 * e) * (n * A) + i * A + a] = out_cvt<TO>(u[m3][0][i] * (T(1) + g) + re[m3][i] * sc);
+        om[m3][(2 * e + 1) * (n * A) + i * A + a] = out_cvt<TO>(u[m3][1][i] * (T(1) + g) + im[m3][i] * sc);
       }
     }
   }
 }
 
-template <typename T, int L>
+template <typename T, typename TO, int L>
 __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, const T* __restrict__ y1,
                                                       const T* __restrict__ y2, const T* __restrict__ y3,
                                                       const T* __restrict__ go0, const T* __restrict__ go1,
                                                       const T* __restrict__ go2, const T* __restrict__ go3, int64_t E,
-                                                      int A, T* __restrict__ gy0, T* __restrict__ gy1,
-                                                      T* __restrict__ gy2, T* __restrict__ gy3) {
+                                                      int A, TO* __restrict__ gy0, TO* __restrict__ gy1,
+                                                      TO* __restrict__ gy2, TO* __restrict__ gy3) {
   constexpr int n = L + 1, NG = n * (L + 1), NP = AcePaths<L>::total();
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (t >= E * A) return;
@@ -723,7 +737,7 @@ __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, 
   const int a = (int)(t - e * A);
   const T* ym[4] = {y0, y1, y2, y3};
   const T* gom[4] = {go0, go1, go2, go3};
-  T* gym[4] = {gy0, gy1, gy2, gy3};
+  TO* gym[4] = {gy0, gy1, gy2, gy3};
   const int64_t r0 = e * (int64_t)(NP * n * A + n * A + (NG + n) * A);
   const int cv0 = NP * n * A, cg = cv0 + n * A, cu0 = cg + NG * A;
   T u[L + 1][2][n], v[L + 1][2][n], go[L + 1][2][n], gu[L + 1][2][n], gv[L + 1][2][n];
@@ -762,7 +776,7 @@ __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, 
       } else {
         gu[m][1][i] = T(0);
       }
-      gy0[r0 + cg + (m * n + i) * A + a] = gz * T(TACE_ACE_SCST) * sg * (T(1) - sg);
+      gy0[r0 + cg + (m * n + i) * A + a] = out_cvt<TO>(gz * T(TACE_ACE_SCST) * sg * (T(1) - sg));
     }
   int p = 0;
 #pragma unroll
@@ -784,7 +798,7 @@ __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, 
           if (sum) { zr = ar * br - ai * bi; zi = ar * bi + ai * br; }
           else { zr = ar * br + ai * bi; zi = ai * br - ar * bi; }
           const T Gre = go[m3][0][i] * sc, Gim = m3 > 0 ? go[m3][1][i] * sc : T(0);
-          gy0[r0 + (p * n + i) * A + a] = (Gre * zr + Gim * zi) * T(TACE_ACE_SCST) * sg * (T(1) - sg);
+          gy0[r0 + (p * n + i) * A + a] = out_cvt<TO>((Gre * zr + Gim * zi) * T(TACE_ACE_SCST) * sg * (T(1) - sg));
           const T Gr = Gre * w, Gi = Gim * w;
           if (sum) {
             gu[m1][0][i] += Gr * br + Gi * bi;
@@ -803,8 +817,8 @@ __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, 
   }
 #pragma unroll
   for (int i = 0; i < n; ++i) {
-    gy0[r0 + cu0 + i * A + a] = gu[0][0][i];
-    gy0[r0 + cv0 + i * A + a] = gv[0][0][i];
+    gy0[r0 + cu0 + i * A + a] = out_cvt<TO>(gu[0][0][i]);
+    gy0[r0 + cv0 + i * A + a] = out_cvt<TO>(gv[0][0][i]);
   }
 #pragma unroll
   for (int m = 1; m <= L; ++m)
@@ -813,8 +827,8 @@ __global__ __launch_bounds__(256) void k_edge_ace_bwd(const T* __restrict__ y0, 
 #pragma unroll
       for (int i = 0; i < n; ++i) {
         const int64_t r = (2 * e + s) * (int64_t)(2 * n * A);
-        gym[m][r + i * A + a] = gv[m][s][i];
-        gym[m][r + n * A + i * A + a] = gu[m][s][i];
+        gym[m][r + i * A + a] = out_cvt<TO>(gv[m][s][i]);
+        gym[m][r + n * A + i * A + a] = out_cvt<TO>(gu[m][s][i]);
       }
 }
 
@@ -904,11 +918,11 @@ __global__ __launch_bounds__(512) void k_rotout_fwd(const Blk<const T> m, const 
 //   t[r] = sum_k W[e,r,k] g[n,k,c];  g_m[e,r,c] = alpha[e,h(c)] t[r];
 //   g_alpha[e,h] = sum over the head's channels and rows of m[e,r,c] t[r];
 //   g_W[e,r,k] = sum_c alpha[e,h(c)] m[e,r,c] g[n,k,c].
-template <typename T, int L, int NS>
+template <typename T, typename TO, int L, int NS>
 __global__ __launch_bounds__(256) void k_rotout_bwd(const Blk<const T> m, const T* __restrict__ alpha,
                                                     const T* __restrict__ W, const T* __restrict__ gout,
                                                     const int64_t* __restrict__ dst, const int* __restrict__ map,
-                                                    int N, int64_t E, int C, int H, const Blk<T> gm,
+                                                    int N, int64_t E, int C, int H, const Blk<TO> gm,
                                                     T* __restrict__ galpha, T* __restrict__ gW) {
   constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16;
   const int64_t e = wave_edge();
@@ -947,7 +961,7 @@ __global__ __launch_bounds__(256) void k_rotout_bwd(const Blk<const T> m, const 
 #pragma unroll
         for (int kk = 0; kk < K; ++kk) t += w[r * K + kk] * g[kk];
         const T mv = erow<L>(m, e, r, C)[c];
-        erow<L>(gm, e, r, C)[c] = a * t;
+        erow<L>(gm, e, r, C)[c] = out_cvt<TO>(a * t);
         v[0] += mv * t;
         const T am = a * mv;
 #pragma unroll
@@ -1066,18 +1080,20 @@ int tace_tece_score_bwd(int dtype, const void* const* q, const void* const* k, c
     return tace_fail_msg("tace_tece_score_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
-#define SC_B(TT, LL)                                                                                            \
+#define SC_B(TT, TO, LL)                                                                                        \
   TACE_SLOTS_DISPATCH(channels, NS,                                                                             \
-    hipLaunchKernelGGL((k_score_bwd<TT, LL, NS>), g, b, 0, s, blocks_of<const TT>(q, lmax),                 \
+    hipLaunchKernelGGL((k_score_bwd<TT, TO, LL, NS>), g, b, 0, s, blocks_of<const TT>(q, lmax),             \
                        blocks_of<const TT>(k, lmax), (const TT*)radial_proj, (const TT*)tscale,              \
-                       (const TT*)g_score, n_edges, channels, heads, blocks_of<TT>(g_q, lmax),               \
-                       blocks_of<TT>(g_k, lmax), (TT*)g_radial_proj))
+                       (const TT*)g_score, n_edges, channels, heads, blocks_of<TO>(g_q, lmax),               \
+                       blocks_of<TO>(g_k, lmax), (TT*)g_radial_proj))
   if (dtype == TACE_F32) {
-    if (lmax == 1) { SC_B(float, 1) } else if (lmax == 2) { SC_B(float, 2) } else { SC_B(float, 3) }
+    if (lmax == 1) { SC_B(float, float, 1) } else if (lmax == 2) { SC_B(float, float, 2) } else { SC_B(float, float, 3) }
+  } else if (dtype == TACE_F32_BF16) {
+    if (lmax == 1) { SC_B(float, bf16_t, 1) } else if (lmax == 2) { SC_B(float, bf16_t, 2) } else { SC_B(float, bf16_t, 3) }
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) { SC_B(double, 1) } else if (lmax == 2) { SC_B(double, 2) } else { SC_B(double, 3) }
+    if (lmax == 1) { SC_B(double, double, 1) } else if (lmax == 2) { SC_B(double, double, 2) } else { SC_B(double, double, 3) }
   } else {
-    return tace_fail_msg("tace_tece_score_bwd: dtype must be TACE_F32 or TACE_F64");
+    return tace_fail_msg("tace_tece_score_bwd: dtype must be TACE_F32, TACE_F32_BF16 or TACE_F64");
   }
 #undef SC_B
   return tace_check_launch("tace_tece_score_bwd");
@@ -1103,17 +1119,19 @@ int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const 
     return tace_fail_msg("tace_edge_rotate_in_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
-#define RI_F(TT, LL)                                                                                        \
+#define RI_F(TT, TO, LL)                                                                                    \
   TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                     \
-    hipLaunchKernelGGL((k_rotin_fwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,   \
-                       rows_dst, (const TT*)radial_w, n_rows, n_edges, channels, blocks_of<TT>(m_src, lmax), \
-                       blocks_of<TT>(m_dst, lmax), blocks_of<TT>(radial_w ? m_w : nullptr, lmax)))
+    hipLaunchKernelGGL((k_rotin_fwd<TT, TO, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src, \
+                       rows_dst, (const TT*)radial_w, n_rows, n_edges, channels, blocks_of<TO>(m_src, lmax), \
+                       blocks_of<TO>(m_dst, lmax), blocks_of<TO>(radial_w ? m_w : nullptr, lmax)))
   if (dtype == TACE_F32) {
-    if (lmax == 1) { RI_F(float, 1) } else if (lmax == 2) { RI_F(float, 2) } else { RI_F(float, 3) }
+    if (lmax == 1) { RI_F(float, float, 1) } else if (lmax == 2) { RI_F(float, float, 2) } else { RI_F(float, float, 3) }
+  } else if (dtype == TACE_F32_BF16) {
+    if (lmax == 1) { RI_F(float, bf16_t, 1) } else if (lmax == 2) { RI_F(float, bf16_t, 2) } else { RI_F(float, bf16_t, 3) }
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) { RI_F(double, 1) } else if (lmax == 2) { RI_F(double, 2) } else { RI_F(double, 3) }
+    if (lmax == 1) { RI_F(double, double, 1) } else if (lmax == 2) { RI_F(double, double, 2) } else { RI_F(double, double, 3) }
   } else {
-    return tace_fail_msg("tace_edge_rotate_in_fwd: dtype must be TACE_F32 or TACE_F64");
+    return tace_fail_msg("tace_edge_rotate_in_fwd: dtype must be TACE_F32, TACE_F32_BF16 or TACE_F64");
   }
 #undef RI_F
   return tace_check_launch("tace_edge_rotate_in_fwd");
@@ -1229,17 +1247,19 @@ int tace_tece_rotate_out_bwd(int dtype, const void* const* m, const void* alpha,
     return tace_fail_msg("tace_tece_rotate_out_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
-#define ROT_B(TT, LL)                                                                                          \
+#define ROT_B(TT, TO, LL)                                                                                      \
   TACE_SLOTS_DISPATCH(channels, NS,                                                                            \
-    hipLaunchKernelGGL((k_rotout_bwd<TT, LL, NS>), g, b, 0, s, blocks_of<const TT>(m, lmax), (const TT*)alpha, \
-                       (const TT*)wigner, (const TT*)g_out, dst, node_map, (int)n_nodes, n_edges, channels,   \
-                       heads, blocks_of<TT>(g_m, lmax), (TT*)g_alpha, (TT*)g_wigner))
+    hipLaunchKernelGGL((k_rotout_bwd<TT, TO, LL, NS>), g, b, 0, s, blocks_of<const TT>(m, lmax),             \
+                       (const TT*)alpha, (const TT*)wigner, (const TT*)g_out, dst, node_map, (int)n_nodes,    \
+                       n_edges, channels, heads, blocks_of<TO>(g_m, lmax), (TT*)g_alpha, (TT*)g_wigner))
   if (dtype == TACE_F32) {
-    if (lmax == 1) { ROT_B(float, 1) } else if (lmax == 2) { ROT_B(float, 2) } else { ROT_B(float, 3) }
+    if (lmax == 1) { ROT_B(float, float, 1) } else if (lmax == 2) { ROT_B(float, float, 2) } else { ROT_B(float, float, 3) }
+  } else if (dtype == TACE_F32_BF16) {
+    if (lmax == 1) { ROT_B(float, bf16_t, 1) } else if (lmax == 2) { ROT_B(float, bf16_t, 2) } else { ROT_B(float, bf16_t, 3) }
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) { ROT_B(double, 1) } else if (lmax == 2) { ROT_B(double, 2) } else { ROT_B(double, 3) }
+    if (lmax == 1) { ROT_B(double, double, 1) } else if (lmax == 2) { ROT_B(double, double, 2) } else { ROT_B(double, double, 3) }
   } else {
-    return tace_fail_msg("tace_tece_rotate_out_bwd: dtype must be TACE_F32 or TACE_F64");
+    return tace_fail_msg("tace_tece_rotate_out_bwd: dtype must be TACE_F32, TACE_F32_BF16 or TACE_F64");
   }
 #undef ROT_B
   return tace_check_launch("tace_tece_rotate_out_bwd");
@@ -1257,15 +1277,17 @@ int tace_tece_edge_ace_fwd(int dtype, const void* y0, const void* y1, const void
     if (!ys[m] || !os[m]) return tace_fail_msg("tace_tece_edge_ace_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges * hidden + 255) / 256)), b(256);
-#define ACE_F(TT, LL)                                                                                           \
-  hipLaunchKernelGGL((k_edge_ace_fwd<TT, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,        \
-                     (const TT*)y3, n_edges, hidden, (TT*)o0, (TT*)o1, (TT*)o2, (TT*)o3)
+#define ACE_F(TT, TO, LL)                                                                                       \
+  hipLaunchKernelGGL((k_edge_ace_fwd<TT, TO, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,    \
+                     (const TT*)y3, n_edges, hidden, (TO*)o0, (TO*)o1, (TO*)o2, (TO*)o3)
   if (dtype == TACE_F32) {
-    if (lmax == 1) ACE_F(float, 1); else if (lmax == 2) ACE_F(float, 2); else ACE_F(float, 3);
+    if (lmax == 1) ACE_F(float, float, 1); else if (lmax == 2) ACE_F(float, float, 2); else ACE_F(float, float, 3);
+  } else if (dtype == TACE_F32_BF16) {
+    if (lmax == 1) ACE_F(float, bf16_t, 1); else if (lmax == 2) ACE_F(float, bf16_t, 2); else ACE_F(float, bf16_t, 3);
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) ACE_F(double, 1); else if (lmax == 2) ACE_F(double, 2); else ACE_F(double, 3);
+    if (lmax == 1) ACE_F(double, double, 1); else if (lmax == 2) ACE_F(double, double, 2); else ACE_F(double, double, 3);
   } else {
-    return tace_fail_msg("tace_tece_edge_ace_fwd: dtype must be TACE_F32 or TACE_F64");
+    return tace_fail_msg("tace_tece_edge_ace_fwd: dtype must be TACE_F32, TACE_F32_BF16 or TACE_F64");
   }
 #undef ACE_F
   return tace_check_launch("tace_tece_edge_ace_fwd");
@@ -1285,16 +1307,18 @@ int tace_tece_edge_ace_bwd(int dtype, const void* y0, const void* y1, const void
     if (!ys[m] || !gos[m] || !gys[m]) return tace_fail_msg("tace_tece_edge_ace_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges * hidden + 255) / 256)), b(256);
-#define ACE_B(TT, LL)                                                                                           \
-  hipLaunchKernelGGL((k_edge_ace_bwd<TT, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,        \
+#define ACE_B(TT, TO, LL)                                                                                       \
+  hipLaunchKernelGGL((k_edge_ace_bwd<TT, TO, LL>), g, b, 0, s, (const TT*)y0, (const TT*)y1, (const TT*)y2,    \
                      (const TT*)y3, (const TT*)g_o0, (const TT*)g_o1, (const TT*)g_o2, (const TT*)g_o3, n_edges, \
-                     hidden, (TT*)g_y0, (TT*)g_y1, (TT*)g_y2, (TT*)g_y3)
+                     hidden, (TO*)g_y0, (TO*)g_y1, (TO*)g_y2, (TO*)g_y3)
   if (dtype == TACE_F32) {
-    if (lmax == 1) ACE_B(float, 1); else if (lmax == 2) ACE_B(float, 2); else ACE_B(float, 3);
+    if (lmax == 1) ACE_B(float, float, 1); else if (lmax == 2) ACE_B(float, float, 2); else ACE_B(float, float, 3);
+  } else if (dtype == TACE_F32_BF16) {
+    if (lmax == 1) ACE_B(float, bf16_t, 1); else if (lmax == 2) ACE_B(float, bf16_t, 2); else ACE_B(float, bf16_t, 3);
   } else if (dtype == TACE_F64) {
-    if (lmax == 1) ACE_B(double, 1); else if (lmax == 2) ACE_B(double, 2); else ACE_B(double, 3);
+    if (lmax == 1) ACE_B(double, double, 1); else if (lmax == 2) ACE_B(double, double, 2); else ACE_B(double, double, 3);
   } else {
-    return tace_fail_msg("tace_tece_edge_ace_bwd: dtype must be TACE_F32 or TACE_F64");
+    return tace_fail_msg("tace_tece_edge_ace_bwd: dtype must be TACE_F32, TACE_F32_BF16 or TACE_F64");
   }
 #undef ACE_B
   return tace_check_launch("tace_tece_edge_ace_bwd");

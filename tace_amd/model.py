@@ -495,9 +495,13 @@ class TeceInteraction(torch.nn.Module):
         self.chunk_edges = 1 << 18
 
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
+        from . import tece
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
-        if plan.n_edges <= self.chunk_edges:
+        if tece.FUSED and tece.fused_supported(self.rejector, self.edge_info):
+            msg = tece.tece_fused(self.rejector, self.edge_info, x, sp.node_map, R, plan, src, dst, wigner,
+                                  self.chunk_edges)
+        elif plan.n_edges <= self.chunk_edges:
             msg = self.rejector(x, self.edge_info(R), plan, sp.node_map, src, dst, wigner, R)
         else:
             msg = self._chunked(x, sp, R, plan, src, dst, wigner)

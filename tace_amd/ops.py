@@ -15,6 +15,7 @@ raises if the native library is missing -- there is no CPU path.
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -416,41 +417,210 @@ def _req_blocks(blocks, name: str, dt, E: int, lmax: int, ch: int):
         _req(t, f"{name}[{m}]", dt, shp)
 
 
+# Raw launches of the TECE kernels, shared by the autograd operators below and
+# the fused chunk operator of tece.py.  bf16_out=True stores the outputs that
+# feed SO(2)-linear GEMMs as bfloat16 (TACE_F32_BF16, float32 arithmetic).
+TACE_F32_BF16 = 2
+
+
+def _tece_code(dt, bf16_out: bool) -> int:
+    if bf16_out:
+        if dt != torch.float32:
+            raise ValueError("bfloat16 GEMM operands need float32 arithmetic")
+        return TACE_F32_BF16
+    return N.dtype_code(dt)
+
+
+def launch_score_fwd(q, k, rp, tscale, lmax: int, H: int) -> torch.Tensor:
+    E, dt = rp.shape[0], rp.dtype
+    C = q[0].shape[1] // (lmax + 1)
+    _req_blocks(q, "query", dt, E, lmax, C)
+    _req_blocks(k, "key", dt, E, lmax, C)
+    _req(rp, "radial_proj", dt, (E, 2 * H))
+    _req(tscale, "tscale", dt, (H,))
+    s = torch.empty(E, H, dtype=dt, device=rp.device)
+    tok = _t0("tece_score_fwd")
+    N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), _block_array(q), _block_array(k), rp.data_ptr(),
+                                        tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(rp.device)),
+            "tace_tece_score_fwd")
+    _t1(tok, (E, (lmax + 1) ** 2, C, H))
+    return s
+
+
+def launch_score_bwd(q, k, rp, tscale, gs, lmax: int, H: int, bf16_out: bool = False):
+    E, dt = rp.shape[0], rp.dtype
+    C = q[0].shape[1] // (lmax + 1)
+    _req(gs, "g_score", dt, (E, H))
+    odt = torch.bfloat16 if bf16_out else dt
+    gq = [torch.empty(t.shape, dtype=odt, device=t.device) for t in q]
+    gk = [torch.empty(t.shape, dtype=odt, device=t.device) for t in k]
+    grp = torch.empty_like(rp)
+    tok = _t0("tece_score_bwd")
+    N.check(N.lib().tace_tece_score_bwd(_tece_code(dt, bf16_out), _block_array(q), _block_array(k), rp.data_ptr(),
+                                        tscale.data_ptr(), gs.data_ptr(), E, lmax, C, H, _block_array(gq),
+                                        _block_array(gk), grp.data_ptr(), N.stream_ptr(rp.device)),
+            "tace_tece_score_bwd")
+    _t1(tok, (E, (lmax + 1) ** 2, C, H))
+    return gq, gk, grp
+
+
+def launch_softmax_fwd(s, plan: EdgePlan) -> torch.Tensor:
+    E, H = s.shape
+    _req(s, "score", s.dtype, (plan.n_edges, H))
+    a = torch.empty_like(s)
+    tok = _t0("graph_softmax_fwd")
+    N.check(N.lib().tace_graph_softmax_fwd(N.dtype_code(s.dtype), s.data_ptr(), plan.rowptr.data_ptr(),
+                                           N.ptr(plan.eid), plan.n_nodes, H, a.data_ptr(), N.stream_ptr(s.device)),
+            "tace_graph_softmax_fwd")
+    _t1(tok, (E, H, plan.n_nodes))
+    return a
+
+
+def launch_softmax_bwd(a, ga, plan: EdgePlan) -> torch.Tensor:
+    _req(ga, "g_alpha", a.dtype, tuple(a.shape))
+    gs = torch.empty_like(a)
+    tok = _t0("graph_softmax_bwd")
+    N.check(N.lib().tace_graph_softmax_bwd(N.dtype_code(a.dtype), a.data_ptr(), ga.data_ptr(), plan.rowptr.data_ptr(),
+                                           N.ptr(plan.eid), plan.n_nodes, a.shape[1], gs.data_ptr(),
+                                           N.stream_ptr(a.device)), "tace_graph_softmax_bwd")
+    _t1(tok, (a.shape[0], a.shape[1], plan.n_nodes))
+    return gs
+
+
+def launch_rotate_out_fwd(m, alpha, W, plan: EdgePlan, node_map, lmax: int, H: int) -> torch.Tensor:
+    E, dt = W.shape[0], W.dtype
+    K = (lmax + 1) ** 2
+    C = m[0].shape[1] // (lmax + 1)
+    _req_blocks(m, "messages", dt, plan.n_edges, lmax, C)
+    _req(alpha, "alpha", dt, (E, H))
+    _req(W, "wigner", dt, (E, K, K))
+    if node_map is not None:
+        _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=W.device)
+    tok = _t0("tece_rotate_out_fwd")
+    N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), _block_array(m), alpha.data_ptr(), W.data_ptr(),
+                                             plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map), plan.n_nodes,
+                                             lmax, C, H, out.data_ptr(), N.stream_ptr(W.device)),
+            "tace_tece_rotate_out_fwd")
+    _t1(tok, (plan.n_nodes, E, C, K, H))
+    return out
+
+
+def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax: int, H: int,
+                          bf16_out: bool = False):
+    E, dt = W.shape[0], W.dtype
+    K = (lmax + 1) ** 2
+    C = m[0].shape[1] // (lmax + 1)
+    _req(gout, "g_out", dt, (plan.n_nodes, K * C))
+    _req(dst, "dst", torch.int64, (E,))
+    odt = torch.bfloat16 if bf16_out else dt
+    gm = [torch.empty(t.shape, dtype=odt, device=t.device) for t in m]
+    ga, gW = torch.empty_like(alpha), torch.empty_like(W)
+    tok = _t0("tece_rotate_out_bwd")
+    N.check(N.lib().tace_tece_rotate_out_bwd(_tece_code(dt, bf16_out), _block_array(m), alpha.data_ptr(),
+                                             W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
+                                             plan.n_nodes, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
+                                             gW.data_ptr(), N.stream_ptr(W.device)), "tace_tece_rotate_out_bwd")
+    _t1(tok, (plan.n_nodes, E, C, K, H))
+    return gm, ga, gW
+
+
+def launch_rotate_in_fwd(x, W, rows_src, rows_dst, wr, lmax: int, bf16_out: bool = False):
+    Nr, K, C = x.shape
+    E, dt = W.shape[0], x.dtype
+    if K != (lmax + 1) ** 2:
+        raise ValueError(f"edge_rotate_in: {K} components, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
+    nc = (lmax + 1) * (lmax + 2) // 2
+    _req(x, "x", dt, (Nr, K, C))
+    _req(W, "wigner", dt, (E, K, K))
+    if wr is not None:
+        _req(wr, "radial_w", dt, (E, nc * 2 * C))
+    _req(rows_src, "rows_src", torch.int64, (E,))
+    _req(rows_dst, "rows_dst", torch.int64, (E,))
+    odt = torch.bfloat16 if bf16_out else dt
+    mk = lambda ch: [torch.empty(shp, dtype=odt, device=x.device) for shp in so2_block_shapes(E, lmax, ch)]
+    ms, md = mk(C), mk(C)
+    mw = mk(2 * C) if wr is not None else []
+    tok = _t0("edge_rotate_in_fwd")
+    N.check(N.lib().tace_edge_rotate_in_fwd(_tece_code(dt, bf16_out), x.data_ptr(), W.data_ptr(),
+                                            rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C,
+                                            _block_array(ms), _block_array(md), _block_array(mw) if mw else None,
+                                            N.stream_ptr(x.device)), "tace_edge_rotate_in_fwd")
+    _t1(tok, (E, K, C, wr is not None))
+    return ms, md, mw
+
+
+def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: bool):
+    """Per-edge grad_x rows of the senders / receivers [E, K, C] each, g_wigner
+    and (need_gwr) g_radial_w; gmw None = no gradient reaches m_w."""
+    Nr, K, C = x.shape
+    E = W.shape[0]
+    gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
+    gxd = torch.empty_like(gxs)
+    gW = torch.empty_like(W)
+    gwr = None
+    if wr is not None and need_gwr:
+        gwr = torch.empty_like(wr) if gmw is not None else torch.zeros_like(wr)
+    tok = _t0("edge_rotate_in_bwd")
+    N.check(N.lib().tace_edge_rotate_in_bwd(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
+                                            rows_dst.data_ptr(), N.ptr(wr), _block_array(gms), _block_array(gmd),
+                                            _block_array(gmw) if gmw is not None else None, Nr, E,
+                                            (int(math.isqrt(K)) - 1), C, gxs.data_ptr(), gxd.data_ptr(),
+                                            gW.data_ptr(), N.ptr(gwr) if gmw is not None else None,
+                                            N.stream_ptr(x.device)), "tace_edge_rotate_in_bwd")
+    _t1(tok, (E, K, C, gmw is not None))
+    return gxs, gxd, gW, gwr
+
+
+def _pad4(lst):
+    return [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
+
+
+def launch_edge_ace_fwd(ys, lmax: int, A: int, bf16_out: bool = False):
+    n = lmax + 1
+    y0 = ys[0]
+    E, dt = y0.shape[0], y0.dtype
+    P = len(edge_ace_paths(lmax))
+    _req(y0, "y0", dt, (E, P * n * A + n * A + (n * (lmax + 1) + n) * A))
+    for m in range(1, lmax + 1):
+        _req(ys[m], f"y{m}", dt, (2 * E, 2 * n * A))
+    odt = torch.bfloat16 if bf16_out else dt
+    outs = [torch.empty(E if m == 0 else 2 * E, n * A, dtype=odt, device=y0.device) for m in range(lmax + 1)]
+    tok = _t0("tece_edge_ace_fwd")
+    N.check(N.lib().tace_tece_edge_ace_fwd(_tece_code(dt, bf16_out), *_pad4(list(ys)), E, lmax, A, *_pad4(outs),
+                                           N.stream_ptr(y0.device)), "tace_tece_edge_ace_fwd")
+    _t1(tok, (E, A, lmax))
+    return outs
+
+
+def launch_edge_ace_bwd(ys, gos, lmax: int, A: int, bf16_out: bool = False):
+    E, dt = ys[0].shape[0], ys[0].dtype
+    for m, g in enumerate(gos):
+        _req(g, f"g_o{m}", dt, (E if m == 0 else 2 * E, (lmax + 1) * A))
+    odt = torch.bfloat16 if bf16_out else dt
+    gys = [torch.empty(y.shape, dtype=odt, device=y.device) for y in ys]
+    tok = _t0("tece_edge_ace_bwd")
+    N.check(N.lib().tace_tece_edge_ace_bwd(_tece_code(dt, bf16_out), *_pad4(list(ys)), *_pad4(list(gos)), E, lmax, A,
+                                           *_pad4(gys), N.stream_ptr(ys[0].device)), "tace_tece_edge_ace_bwd")
+    _t1(tok, (E, A, lmax))
+    return gys
+
+
 class _TeceScore(torch.autograd.Function):
     @staticmethod
     def forward(ctx, rp, tscale, lmax: int, H: int, C: int, *qk):
         n = lmax + 1
         q, k = list(qk[:n]), list(qk[n:])
-        E, dt = rp.shape[0], rp.dtype
-        _req_blocks(q, "query", dt, E, lmax, C)
-        _req_blocks(k, "key", dt, E, lmax, C)
-        _req(rp, "radial_proj", dt, (E, 2 * H))
-        _req(tscale, "tscale", dt, (H,))
-        s = torch.empty(E, H, dtype=dt, device=rp.device)
-        tok = _t0("tece_score_fwd")
-        N.check(N.lib().tace_tece_score_fwd(N.dtype_code(dt), _block_array(q), _block_array(k), rp.data_ptr(),
-                                            tscale.data_ptr(), E, lmax, C, H, s.data_ptr(), N.stream_ptr(rp.device)),
-                "tace_tece_score_fwd")
-        _t1(tok, (E, n * n, C, H))
+        s = launch_score_fwd(q, k, rp, tscale, lmax, H)
         ctx.save_for_backward(rp, tscale, *q, *k)
-        ctx.lmax, ctx.H, ctx.C = lmax, H, C
+        ctx.lmax, ctx.H = lmax, H
         return s
 
     @staticmethod
     def backward(ctx, gs):
         rp, tscale, *qk = ctx.saved_tensors
         n = ctx.lmax + 1
-        q, k = qk[:n], qk[n:]
-        E = rp.shape[0]
-        gs = gs.contiguous()
-        gq, gk = [torch.empty_like(t) for t in q], [torch.empty_like(t) for t in k]
-        grp = torch.empty_like(rp)
-        tok = _t0("tece_score_bwd")
-        N.check(N.lib().tace_tece_score_bwd(N.dtype_code(rp.dtype), _block_array(q), _block_array(k), rp.data_ptr(),
-                                            tscale.data_ptr(), gs.data_ptr(), E, ctx.lmax, ctx.C, ctx.H,
-                                            _block_array(gq), _block_array(gk), grp.data_ptr(),
-                                            N.stream_ptr(rp.device)), "tace_tece_score_bwd")
-        _t1(tok, (E, n * n, ctx.C, ctx.H))
+        gq, gk, grp = launch_score_bwd(qk[:n], qk[n:], rp, tscale, gs.contiguous(), ctx.lmax, ctx.H)
         # the attention temperature is a model parameter: no gradient on this
         # (inference) path, as the calculators freeze parameters
         return (grp, None, None, None, None) + tuple(gq) + tuple(gk)
@@ -470,14 +640,7 @@ def tece_score(q: Sequence[torch.Tensor], k: Sequence[torch.Tensor], radial_proj
 class _GraphSoftmax(torch.autograd.Function):
     @staticmethod
     def forward(ctx, s, plan: EdgePlan):
-        E, H = s.shape
-        _req(s, "score", s.dtype, (plan.n_edges, H))
-        a = torch.empty_like(s)
-        tok = _t0("graph_softmax_fwd")
-        N.check(N.lib().tace_graph_softmax_fwd(N.dtype_code(s.dtype), s.data_ptr(), plan.rowptr.data_ptr(),
-                                               N.ptr(plan.eid), plan.n_nodes, H, a.data_ptr(),
-                                               N.stream_ptr(s.device)), "tace_graph_softmax_fwd")
-        _t1(tok, (E, H, plan.n_nodes))
+        a = launch_softmax_fwd(s, plan)
         ctx.save_for_backward(a)
         ctx.plan = plan
         return a
@@ -485,15 +648,7 @@ class _GraphSoftmax(torch.autograd.Function):
     @staticmethod
     def backward(ctx, ga):
         (a,) = ctx.saved_tensors
-        plan = ctx.plan
-        ga = ga.contiguous()
-        gs = torch.empty_like(a)
-        tok = _t0("graph_softmax_bwd")
-        N.check(N.lib().tace_graph_softmax_bwd(N.dtype_code(a.dtype), a.data_ptr(), ga.data_ptr(),
-                                               plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.n_nodes, a.shape[1],
-                                               gs.data_ptr(), N.stream_ptr(a.device)), "tace_graph_softmax_bwd")
-        _t1(tok, (a.shape[0], a.shape[1], plan.n_nodes))
-        return gs, None
+        return launch_softmax_bwd(a, ga.contiguous(), ctx.plan), None
 
 
 def graph_softmax(score: torch.Tensor, plan: EdgePlan) -> torch.Tensor:
@@ -504,38 +659,15 @@ def graph_softmax(score: torch.Tensor, plan: EdgePlan) -> torch.Tensor:
 class _TeceRotateOut(torch.autograd.Function):
     @staticmethod
     def forward(ctx, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, H: int, C: int, *m):
-        E, dt = W.shape[0], W.dtype
-        K = (lmax + 1) ** 2
-        _req_blocks(m, "messages", dt, plan.n_edges, lmax, C)
-        _req(alpha, "alpha", dt, (E, H))
-        _req(W, "wigner", dt, (E, K, K))
-        if node_map is not None:
-            _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
-        out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=W.device)
-        tok = _t0("tece_rotate_out_fwd")
-        N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), _block_array(m), alpha.data_ptr(), W.data_ptr(),
-                                                 plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map),
-                                                 plan.n_nodes, lmax, C, H, out.data_ptr(),
-                                                 N.stream_ptr(W.device)), "tace_tece_rotate_out_fwd")
-        _t1(tok, (plan.n_nodes, E, C, K, H))
+        out = launch_rotate_out_fwd(list(m), alpha, W, plan, node_map, lmax, H)
         ctx.save_for_backward(alpha, W, node_map, dst, *m)
-        ctx.plan, ctx.lmax, ctx.H, ctx.C = plan, lmax, H, C
+        ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
         return out
 
     @staticmethod
     def backward(ctx, gout):
         alpha, W, node_map, dst, *m = ctx.saved_tensors
-        plan, lmax, H, C = ctx.plan, ctx.lmax, ctx.H, ctx.C
-        E, K = W.shape[0], (lmax + 1) ** 2
-        gout = gout.contiguous()
-        gm = [torch.empty_like(t) for t in m]
-        ga, gW = torch.empty_like(alpha), torch.empty_like(W)
-        tok = _t0("tece_rotate_out_bwd")
-        N.check(N.lib().tace_tece_rotate_out_bwd(N.dtype_code(W.dtype), _block_array(m), alpha.data_ptr(),
-                                                 W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
-                                                 plan.n_nodes, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
-                                                 gW.data_ptr(), N.stream_ptr(W.device)), "tace_tece_rotate_out_bwd")
-        _t1(tok, (plan.n_nodes, E, C, K, H))
+        gm, ga, gW = launch_rotate_out_bwd(m, alpha, W, gout.contiguous(), dst, node_map, ctx.plan, ctx.lmax, ctx.H)
         return (ga, gW, None, None, None, None, None, None) + tuple(gm)
 
 
@@ -555,27 +687,7 @@ def tece_rotate_out(m: Sequence[torch.Tensor], alpha, W, plan: EdgePlan, node_ma
 class _EdgeRotateIn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, W, wr, rows_src, rows_dst, lmax: int):
-        Nr, K, C = x.shape
-        E = W.shape[0]
-        dt = x.dtype
-        if K != (lmax + 1) ** 2:
-            raise ValueError(f"edge_rotate_in: {K} components, expected (lmax+1)^2 = {(lmax + 1) ** 2}")
-        nc = (lmax + 1) * (lmax + 2) // 2
-        _req(x, "x", dt, (Nr, K, C))
-        _req(W, "wigner", dt, (E, K, K))
-        if wr is not None:
-            _req(wr, "radial_w", dt, (E, nc * 2 * C))
-        _req(rows_src, "rows_src", torch.int64, (E,))
-        _req(rows_dst, "rows_dst", torch.int64, (E,))
-        mk = lambda ch: [torch.empty(shp, dtype=dt, device=x.device) for shp in so2_block_shapes(E, lmax, ch)]
-        ms, md = mk(C), mk(C)
-        mw = mk(2 * C) if wr is not None else []
-        tok = _t0("edge_rotate_in_fwd")
-        N.check(N.lib().tace_edge_rotate_in_fwd(N.dtype_code(dt), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
-                                                rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C, _block_array(ms),
-                                                _block_array(md), _block_array(mw) if mw else None,
-                                                N.stream_ptr(x.device)), "tace_edge_rotate_in_fwd")
-        _t1(tok, (E, K, C, wr is not None))
+        ms, md, mw = launch_rotate_in_fwd(x, W, rows_src, rows_dst, wr, lmax)
         ctx.save_for_backward(x, W, wr, rows_src, rows_dst)
         ctx.lmax, ctx.n = lmax, lmax + 1
         ctx.set_materialize_grads(False)
@@ -584,26 +696,12 @@ class _EdgeRotateIn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *g):
         x, W, wr, rows_src, rows_dst = ctx.saved_tensors
-        Nr, K, C = x.shape
-        E, n = W.shape[0], ctx.n
+        n = ctx.n
         g = [t.contiguous() if t is not None else None for t in g]
         gms, gmd, gmw = g[:n], g[n:2 * n], g[2 * n:]
-        gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
-        gxd = torch.empty_like(gxs)
-        gW = torch.empty_like(W)
         has_w = any(t is not None for t in gmw)
-        gwr = None
-        if wr is not None and ctx.needs_input_grad[2]:
-            gwr = torch.empty_like(wr) if has_w else torch.zeros_like(wr)
-        tok = _t0("edge_rotate_in_bwd")
-        N.check(N.lib().tace_edge_rotate_in_bwd(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(),
-                                                rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr),
-                                                _block_array(gms), _block_array(gmd),
-                                                _block_array(gmw) if has_w else None, Nr, E, ctx.lmax, C,
-                                                gxs.data_ptr(), gxd.data_ptr(), gW.data_ptr(),
-                                                N.ptr(gwr) if has_w else None, N.stream_ptr(x.device)),
-                "tace_edge_rotate_in_bwd")
-        _t1(tok, (E, K, C, has_w))
+        gxs, gxd, gW, gwr = launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw if has_w else None,
+                                                 ctx.needs_input_grad[2])
         gx = None
         if ctx.needs_input_grad[0]:
             gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
@@ -624,50 +722,66 @@ def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, row
     return tuple(blocks)
 
 
+def launch_mlp_hidden_fwd(radial, weights, n_layers: int):
+    """Hidden layers of the radial MLP: (h [E, 64], saved pre-activations z_t)."""
+    E, n_in = radial.shape
+    dt = radial.dtype
+    width = 64
+    _req(radial, "radial", dt, (E, n_in))
+    _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
+    h = torch.empty(E, width, dtype=dt, device=radial.device)
+    z_t = torch.empty(n_layers, width, E, dtype=dt, device=radial.device)
+    tok = _t0("radial_mlp_fwd")
+    N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers, weights.data_ptr(),
+                                        h.data_ptr(), z_t.data_ptr(), N.stream_ptr(radial.device)),
+            "tace_radial_mlp_fwd")
+    _t1(tok, (E, n_in, n_layers))
+    return h, z_t
+
+
+def launch_mlp_hidden_bwd(z_t, gh, weights, n_in: int) -> torch.Tensor:
+    n_layers, _, E = z_t.shape
+    _req(gh, "g_h", z_t.dtype, (E, 64))
+    g = torch.empty(E, n_in, dtype=z_t.dtype, device=z_t.device)
+    tok = _t0("radial_mlp_bwd")
+    N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh.data_ptr(), E, n_in, n_layers,
+                                        weights.data_ptr(), g.data_ptr(), N.stream_ptr(z_t.device)),
+            "tace_radial_mlp_bwd")
+    _t1(tok, (E, n_in, n_layers))
+    return g
+
+
 class _RadialMlp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, radial, weights, n_layers: int):
-        E, n_in = radial.shape
-        dt = radial.dtype
-        width = 64
-        _req(radial, "radial", dt, (E, n_in))
-        _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
-        h = torch.empty(E, width, dtype=dt, device=radial.device)
-        z_t = torch.empty(n_layers, width, E, dtype=dt, device=radial.device)
-        tok = _t0("radial_mlp_fwd")
-        N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers,
-                                            weights.data_ptr(), h.data_ptr(), z_t.data_ptr(),
-                                            N.stream_ptr(radial.device)), "tace_radial_mlp_fwd")
-        _t1(tok, (E, n_in, n_layers))
+        h, z_t = launch_mlp_hidden_fwd(radial, weights, n_layers)
         ctx.save_for_backward(z_t, weights)
-        ctx.n_in, ctx.n_layers = n_in, n_layers
+        ctx.n_in = radial.shape[1]
         return h
 
     @staticmethod
     def backward(ctx, gh):
         z_t, weights = ctx.saved_tensors
-        E = z_t.shape[2]
-        gh = gh.contiguous()
-        g = torch.empty(E, ctx.n_in, dtype=z_t.dtype, device=z_t.device)
-        tok = _t0("radial_mlp_bwd")
-        N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh.data_ptr(), E, ctx.n_in,
-                                            ctx.n_layers, weights.data_ptr(), g.data_ptr(),
-                                            N.stream_ptr(z_t.device)), "tace_radial_mlp_bwd")
-        _t1(tok, (E, ctx.n_in, ctx.n_layers))
-        return g, None, None
+        return launch_mlp_hidden_bwd(z_t, gh.contiguous(), weights, ctx.n_in), None, None
+
+
+def launch_mlp_out_f32(h, W, alpha: float) -> torch.Tensor:
+    """alpha h @ W on the fp32-MFMA kernel (h [E, 64], W [64, n_out])."""
+    E = h.shape[0]
+    _req(h, "h", torch.float32, (E, 64))
+    _req(W, "weight", torch.float32, (64, W.shape[1]))
+    out = torch.empty(E, W.shape[1], dtype=torch.float32, device=h.device)
+    tok = _t0("radial_mlp_out")
+    N.check(N.lib().tace_radial_mlp_out_f32(h.data_ptr(), W.data_ptr(), E, W.shape[1], float(alpha), out.data_ptr(),
+                                            N.stream_ptr(h.device)), "tace_radial_mlp_out_f32")
+    _t1(tok, (E, W.shape[1]))
+    return out
 
 
 class _MlpOut(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, W, alpha: float):
-        E, K = h.shape
-        _req(h, "h", torch.float32, (E, 64))
-        _req(W, "weight", torch.float32, (64, W.shape[1]))
-        out = torch.empty(E, W.shape[1], dtype=torch.float32, device=h.device)
-        tok = _t0("radial_mlp_out")
-        N.check(N.lib().tace_radial_mlp_out_f32(h.data_ptr(), W.data_ptr(), E, W.shape[1], float(alpha),
-                                                out.data_ptr(), N.stream_ptr(h.device)), "tace_radial_mlp_out_f32")
-        _t1(tok, (E, W.shape[1]))
+        out = launch_mlp_out_f32(h, W, alpha)
         ctx.save_for_backward(W)
         ctx.alpha = alpha
         return out
@@ -810,20 +924,7 @@ def edge_ace_paths(lmax: int) -> List[Tuple[int, int, int, bool]]:
 class _EdgeAce(torch.autograd.Function):
     @staticmethod
     def forward(ctx, lmax: int, A: int, *ys):
-        n = lmax + 1
-        y0 = ys[0]
-        E = y0.shape[0]
-        dt = y0.dtype
-        P = len(edge_ace_paths(lmax))
-        _req(y0, "y0", dt, (E, P * n * A + n * A + (n * (lmax + 1) + n) * A))
-        for m in range(1, lmax + 1):
-            _req(ys[m], f"y{m}", dt, (2 * E, 2 * n * A))
-        outs = [torch.empty(E if m == 0 else 2 * E, n * A, dtype=dt, device=y0.device) for m in range(lmax + 1)]
-        pad = lambda lst: [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
-        tok = _t0("tece_edge_ace_fwd")
-        N.check(N.lib().tace_tece_edge_ace_fwd(N.dtype_code(dt), *pad(list(ys)), E, lmax, A, *pad(outs),
-                                               N.stream_ptr(y0.device)), "tace_tece_edge_ace_fwd")
-        _t1(tok, (E, A, lmax))
+        outs = launch_edge_ace_fwd(list(ys), lmax, A)
         ctx.save_for_backward(*ys)
         ctx.lmax, ctx.A = lmax, A
         return tuple(outs)
@@ -836,13 +937,7 @@ class _EdgeAce(torch.autograd.Function):
         gos = [g.contiguous() if g is not None else torch.zeros(E if m == 0 else 2 * E, (lmax + 1) * A,
                                                                  dtype=ys[0].dtype, device=ys[0].device)
                for m, g in enumerate(gos)]
-        gys = [torch.empty_like(y) for y in ys]
-        pad = lambda lst: [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
-        tok = _t0("tece_edge_ace_bwd")
-        N.check(N.lib().tace_tece_edge_ace_bwd(N.dtype_code(ys[0].dtype), *pad(list(ys)), *pad(gos), E, lmax, A,
-                                               *pad(gys), N.stream_ptr(ys[0].device)), "tace_tece_edge_ace_bwd")
-        _t1(tok, (E, A, lmax))
-        return (None, None) + tuple(gys)
+        return (None, None) + tuple(launch_edge_ace_bwd(list(ys), gos, lmax, A))
 
 
 def tece_edge_ace(ys: Sequence[torch.Tensor], lmax: int, hidden: int) -> Tuple[torch.Tensor, ...]:

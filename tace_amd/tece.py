@@ -22,6 +22,10 @@ import torch
 
 from . import ops
 
+# frozen parameters run the convolution on the fused operator (_TeceFused);
+# False keeps the per-operator autograd path (the reference for its tests)
+FUSED = True
+
 class _MixedLinear(torch.autograd.Function):
     """y = x W^T (+ b) with x and W rounded to bfloat16 and fp32 accumulation
     and output (hipBLASLt); the input gradient likewise.  W is a constant."""
@@ -219,3 +223,202 @@ def sub_plan(plan: ops.EdgePlan, n0: int, n1: int, e0: int, e1: int) -> ops.Edge
     """Receiver CSR of receivers n0..n1-1 and their edges e0..e1-1 (receiver-grouped edges)."""
     return ops.EdgePlan(n1 - n0, e1 - e0, (plan.rowptr[n0:n1 + 1] - e0).contiguous(),
                         plan.src[e0:e1].contiguous(), None)
+
+
+# ----------------------------------------------------------- fused operator --
+class _FusedParams:
+    """Everything the fused TECE operator needs from the frozen modules,
+    prepared once per forward: the SO(2) linears as W^T (forward GEMM
+    operand) and W (input-gradient operand) in the mixing precision, the
+    biases, the radial projection, the attention scale and the radial MLP."""
+
+    def __init__(self, conv: "TeceConvolution", mlp, dtype):
+        self.lmax, self.H, self.A, self.C = conv.lmax, conv.H, conv.A, conv.C
+        self.mixing = conv.mixing if dtype == torch.float32 else None
+        self.bf16 = self.mixing is not None
+        op = self.mixing or dtype
+        L = self.lmax
+
+        def pair(W):
+            W = W.detach().to(dtype)
+            return W.t().to(op).contiguous(), W.to(op).contiguous()
+
+        def so2(lin):
+            f0 = lin.m0_rlinear
+            mats = [pair(f0.weight * f0.alpha)] + [pair(lin.ms_clinear[m - 1].fc.weight * lin.ms_clinear[m - 1].fc.alpha)
+                                                   for m in range(1, L + 1)]
+            return [a for a, _ in mats], [b for _, b in mats], f0.bias.detach().to(dtype).contiguous()
+
+        self.k_T, self.k_N, self.k_b = so2(conv.key_proj)
+        self.q_T, self.q_N, self.q_b = so2(conv.query_proj)
+        self.d_T, self.d_N, self.d_b = so2(conv.linear_down)
+        lc, lg, lu = conv.linear_coefs, conv.linear_glu, conv.linear_up
+        f0 = [lc.m0_rlinear, lg.m0_rlinear, lu.m0_rlinear]
+        sh = [pair(torch.cat([f.weight * f.alpha for f in f0]))]
+        for m in range(1, L + 1):
+            fg, fu = lg.ms_clinear[m - 1].fc, lu.ms_clinear[m - 1].fc
+            sh.append(pair(torch.cat([fg.weight * fg.alpha, fu.weight * fu.alpha])))
+        self.s_T, self.s_N = [a for a, _ in sh], [b for _, b in sh]
+        self.s_b = torch.cat([f.bias for f in f0]).detach().to(dtype).contiguous()
+        rp = conv.radial_proj
+        Wrp = (rp.weight * rp.alpha).detach().to(dtype)
+        self.rp_T, self.rp_N, self.rp_b = Wrp.t().contiguous(), Wrp.contiguous(), rp.bias.detach().to(dtype)
+        T = conv.tmin + (conv.tmax - conv.tmin) * torch.sigmoid(conv.temperature_logit.detach())
+        self.tscale = (T * conv.attention_scale).to(dtype).contiguous()
+        lins = [m for m in mlp.mlp if hasattr(m, "alpha")]
+        self.mlp_flat = torch.cat([(m.weight * m.alpha).detach().reshape(-1) for m in lins[:-1]]).to(dtype).contiguous()
+        self.mlp_layers = len(lins) - 1
+        self.mlp_W = lins[-1].weight.detach().to(dtype).contiguous()
+        self.mlp_alpha = float(lins[-1].alpha)
+        self.mlp_WT_scaled = (lins[-1].weight * lins[-1].alpha).detach().to(dtype).t().contiguous()
+
+    def mm(self, x, WT, b=None):
+        """x @ WT (+ b): bf16 operands with float32 accumulation and output
+        under bf16 mixing, else in the features' precision."""
+        if self.bf16:
+            if b is None:
+                return torch.mm(x, WT, out_dtype=torch.float32)
+            return torch.addmm(b, x, WT, out_dtype=torch.float32)
+        return torch.mm(x, WT) if b is None else torch.addmm(b, x, WT)
+
+    def mm_grad(self, g, WN):
+        return torch.mm(g, WN, out_dtype=torch.float32) if self.bf16 else torch.mm(g, WN)
+
+
+def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, save: bool):
+    """One receiver chunk of the convolution (the sequence of
+    ``TeceConvolution.edges`` with the radial MLP in front).  Returns the
+    receiver sums and, with ``save``, what the backward needs."""
+    L, H, A = P.lmax, P.H, P.A
+    h, z_t = ops.launch_mlp_hidden_fwd(R, P.mlp_flat, P.mlp_layers)
+    if h.dtype == torch.float32:
+        w = ops.launch_mlp_out_f32(h, P.mlp_W, P.mlp_alpha)
+    else:
+        w = torch.mm(h, P.mlp_W).mul_(P.mlp_alpha)
+    del h
+    ms, md, mw = ops.launch_rotate_in_fwd(x_lc, W, rs, rd, w, L, P.bf16)
+    key = [P.mm(ms[m], P.k_T[m], P.k_b if m == 0 else None) for m in range(L + 1)]
+    query = [P.mm(md[m], P.q_T[m], P.q_b if m == 0 else None) for m in range(L + 1)]
+    del ms, md
+    rp = torch.addmm(P.rp_b, R, P.rp_T)
+    alpha = ops.launch_softmax_fwd(ops.launch_score_fwd(query, key, rp, P.tscale, L, H), plan)
+    ys = [P.mm(mw[m], P.s_T[m], P.s_b if m == 0 else None) for m in range(L + 1)]
+    del mw
+    o = ops.launch_edge_ace_fwd(ys, L, A, P.bf16)
+    mb = [P.mm(o[m], P.d_T[m], P.d_b if m == 0 else None) for m in range(L + 1)]
+    del o
+    out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H)
+    return out, ((z_t, w, query, key, rp, alpha, ys, mb) if save else None)
+
+
+def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, dst_out, saved, g_out, gx):
+    """Backward of one chunk: adds its grad_x into ``gx`` (index_add over the
+    sender and receiver rows) and returns (grad_R, grad_W) of its edges."""
+    L, H, A = P.lmax, P.H, P.A
+    if saved is None:
+        _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True)
+    z_t, w, q, k, rp, alpha, ys, mb = saved
+    gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16)
+    go = [P.mm_grad(gm[m], P.d_N[m]) for m in range(L + 1)]
+    del gm
+    gys = ops.launch_edge_ace_bwd(ys, go, L, A, P.bf16)
+    del go
+    gmw = [P.mm_grad(gys[m], P.s_N[m]) for m in range(L + 1)]
+    del gys
+    g_score = ops.launch_softmax_bwd(alpha, g_alpha, plan)
+    gq, gk, grp = ops.launch_score_bwd(q, k, rp, P.tscale, g_score, L, H, P.bf16)
+    gms = [P.mm_grad(gk[m], P.k_N[m]) for m in range(L + 1)]
+    gmd = [P.mm_grad(gq[m], P.q_N[m]) for m in range(L + 1)]
+    del gq, gk
+    gR = torch.mm(grp, P.rp_N)
+    gxs, gxd, gW_in, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True)
+    gx.index_add_(0, rs, gxs).index_add_(0, rd, gxd)
+    del gxs, gxd
+    gh = torch.mm(gw, P.mlp_WT_scaled)
+    gR += ops.launch_mlp_hidden_bwd(z_t, gh, P.mlp_flat, R.shape[1])
+    return gR, gW.add_(gW_in)
+
+
+def _gm_blocks(t, n: int, L: int, C: int):
+    """[n, (L+1)^2 C] group-major rows -> per-l views [n, 2l+1, C]."""
+    flat = t.view(-1)
+    return [flat[n * C * l * l:n * C * (l + 1) ** 2].view(n, 2 * l + 1, C) for l in range(L + 1)]
+
+
+class _TeceFused(torch.autograd.Function):
+    """The whole TECE convolution with the radial MLP as one operator, for
+    frozen parameters: inputs x_lc [rows, K, C] (node features, l layout,
+    feature-row order), R [E, n_radial], wigner [E, K, K]; output the
+    receiver sums [N, K C], group-major, in feature-row order.  The backward
+    is written out (recomputing each chunk's forward when there is more than
+    one), so GEMM operands go between kernels and GEMMs in the mixing
+    precision without casts, and all chunks add their grad_x into one buffer."""
+
+    @staticmethod
+    def forward(ctx, x_lc, R, W, P: _FusedParams, plan: ops.EdgePlan, rs, rd, dst, node_map, chunks):
+        ctx.P, ctx.plan, ctx.chunks = P, plan, chunks
+        L, C = P.lmax, P.C
+        if chunks is None:
+            out, ctx.saved_chunk = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, node_map, True)
+        else:
+            Nn = plan.n_nodes
+            out = torch.empty(Nn, (L + 1) ** 2 * C, dtype=x_lc.dtype, device=x_lc.device)
+            full = _gm_blocks(out, Nn, L, C)
+            for n0, n1, e0, e1 in chunks:
+                oc, _ = _fused_chunk_fwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
+                                         sub_plan(plan, n0, n1, e0, e1), None, False)
+                rows_c = node_map[n0:n1].long()
+                for l, blk in enumerate(_gm_blocks(oc, n1 - n0, L, C)):
+                    full[l].index_copy_(0, rows_c, blk)
+            ctx.saved_chunk = None
+        ctx.save_for_backward(x_lc, R, W, rs, rd, dst, node_map)
+        return out
+
+    @staticmethod
+    def backward(ctx, g_out):
+        x_lc, R, W, rs, rd, dst, node_map = ctx.saved_tensors
+        P, plan, chunks = ctx.P, ctx.plan, ctx.chunks
+        L, C = P.lmax, P.C
+        g_out = g_out.contiguous()
+        gx = torch.zeros_like(x_lc)
+        if chunks is None:
+            gR, gW = _fused_chunk_bwd(P, x_lc, R, W, rs, rd, plan, node_map, dst, ctx.saved_chunk, g_out, gx)
+            ctx.saved_chunk = None
+            return gx, gR, gW, None, None, None, None, None, None, None
+        gR, gW = torch.empty_like(R), torch.empty_like(W)
+        full = _gm_blocks(g_out, plan.n_nodes, L, C)
+        for n0, n1, e0, e1 in chunks:
+            rows_c = node_map[n0:n1].long()
+            g_c = torch.cat([f.index_select(0, rows_c).reshape(-1) for f in full]).view(n1 - n0, -1)
+            gR_c, gW_c = _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
+                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0, None, g_c, gx)
+            gR[e0:e1] = gR_c
+            gW[e0:e1] = gW_c
+        return gx, gR, gW, None, None, None, None, None, None, None
+
+
+def fused_supported(conv: "TeceConvolution", mlp) -> bool:
+    """The fused operator covers frozen parameters and the fused radial MLP."""
+    mods = [conv, mlp]
+    return (getattr(mlp, "fused", False)
+            and not any(p.requires_grad for m in mods for p in m.parameters()))
+
+
+def tece_fused(conv: "TeceConvolution", mlp, x_gm, node_map, R, plan: ops.EdgePlan, src, dst, wigner,
+               chunk_edges: int):
+    """TECE convolution + radial MLP (``OAM20260705Convolution.forward`` with
+    ``edge_info``) on the fused operator; receiver chunks of at most
+    ``chunk_edges`` edges when the graph has more."""
+    P = _FusedParams(conv, mlp, x_gm.dtype)
+    x_lc = conv.node_components(x_gm)
+    rows = node_map.long()
+    src, dst = src.long(), dst.long()
+    if plan.n_edges <= chunk_edges:
+        return _TeceFused.apply(x_lc, R, wigner, P, plan, rows[src].contiguous(), rows[dst].contiguous(),
+                                dst.contiguous(), node_map, None)
+    if plan.eid is not None:   # chunks need receiver-grouped edges
+        order = plan.eid.long()
+        R, wigner, src, dst = R[order], wigner[order], src[order], dst[order]
+        plan = ops.EdgePlan(plan.n_nodes, plan.n_edges, plan.rowptr, src.to(torch.int32).contiguous(), None)
+    return _TeceFused.apply(x_lc, R.contiguous(), wigner.contiguous(), P, plan, rows[src].contiguous(),
+                            rows[dst].contiguous(), dst.contiguous(), node_map, receiver_chunks(plan, chunk_edges))

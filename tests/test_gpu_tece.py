@@ -18,7 +18,7 @@ import torch
 from oracle import model as om
 from oracle import neighbours as onl
 from oracle import tece as ot
-from tace_amd import configs, data, ops, structures
+from tace_amd import configs, data, ops, structures, tece
 from tace_amd import model as pm
 from tace_amd import tece as pt
 
@@ -389,7 +389,7 @@ def test_tece_convolution_matches_oracle(cuda, dtype, C, H, A):
 BARS = {torch.float64: (1e-10, 1e-8), torch.float32: (1e-5, 1e-4)}
 
 
-def _model_pair(structs, cuda, dtype, seed=0, chunk_edges=None, mixing=None, **over):
+def _model_pair(structs, cuda, dtype, seed=0, chunk_edges=None, mixing=None, frozen=False, fused=True, **over):
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS["tece"]["cutoff"])
              for s in structs]
     zs = sorted({int(z) for s in structs for z in s["numbers"]})
@@ -420,7 +420,16 @@ def _model_pair(structs, cuda, dtype, seed=0, chunk_edges=None, mixing=None, **o
                 mod.chunk_edges = chunk_edges
                 n += 1
         assert n > 0
-    got = gpu(data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda))
+    if frozen:   # the calculators' set-up: the TECE layers run on the fused operator
+        gpu.eval()
+        for prm in gpu.parameters():
+            prm.requires_grad_(False)
+    prev_fused = tece.FUSED
+    tece.FUSED = fused
+    try:
+        got = gpu(data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda))
+    finally:
+        tece.FUSED = prev_fused
     return got, want
 
 
@@ -461,6 +470,61 @@ def test_tece_receiver_chunks(cuda, dtype):
                             num_channel=64, num_head=2)
     _check(got, want, dtype)
 
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("chunk_edges", [None, 700])
+def test_tece_fused_operator_matches_oracle(cuda, dtype, chunk_edges):
+    """Frozen parameters (as every calculator sets them) run the TECE layers
+    on the fused operator (_TeceFused: hand-written backward, one grad_x
+    buffer), in one piece and in receiver chunks of ~700 edges."""
+    got, want = _model_pair([structures.bcc_fe(reps=(3, 3, 2), seed=10)], cuda, dtype, seed=2,
+                            chunk_edges=chunk_edges, num_channel=64, num_head=2, frozen=True)
+    _check(got, want, dtype)
+
+
+@pytest.mark.parametrize("chunk_edges", [None, 700])
+def test_tece_fused_bf16_mixing_equals_operator_path(cuda, chunk_edges):
+    """bf16 channel mixing: the fused operator (bf16 GEMM operands stored by
+    the kernels, biases in the GEMM epilogue) gives the per-operator path's
+    result (float32 outputs cast by torch, separate bias adds) up to float32
+    summation order."""
+    st = [structures.bcc_fe(reps=(3, 3, 2), seed=10)]
+    kw = dict(seed=2, chunk_edges=chunk_edges, num_channel=64, num_head=2, mixing=torch.bfloat16, frozen=True)
+    a, _ = _model_pair(st, cuda, torch.float32, fused=True, **kw)
+    b, _ = _model_pair(st, cuda, torch.float32, fused=False, **kw)
+    Ea, Eb = a["energy"].double(), b["energy"].double()
+    assert ((Ea - Eb).abs() / Eb.abs()).max().item() < 1e-6
+    Fa, Fb = a["forces"].double(), b["forces"].double()
+    assert (Fa - Fb).abs().max().item() < 1e-4 * Fb.abs().max().item()
+
+
+def test_bf16_gemm_operands_round_like_torch(cuda):
+    """TACE_F32_BF16 outputs are the float32 outputs rounded to bfloat16 the
+    way torch's cast rounds (nearest even), bit for bit."""
+    g = torch.Generator().manual_seed(12)
+    lmax, C, N, E = 2, 64, 40, 300
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    x = torch.randn(N, K, C, generator=g).to(cuda)
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = W.float().to(cuda).contiguous()
+    wr = torch.randn(E, nc * 2 * C, generator=g).to(cuda)
+    rs = torch.randint(0, N, (E,), generator=g).to(cuda)
+    rd = torch.randint(0, N, (E,), generator=g).to(cuda)
+    f32 = ops.launch_rotate_in_fwd(x, W, rs, rd, wr, lmax, False)
+    b16 = ops.launch_rotate_in_fwd(x, W, rs, rd, wr, lmax, True)
+    for a, b in zip(sum(f32, []), sum(b16, [])):
+        assert b.dtype == torch.bfloat16 and torch.equal(a.to(torch.bfloat16), b)
+    A = 16
+    P = len(ops.edge_ace_paths(lmax))
+    n = lmax + 1
+    ys = [torch.randn(E, P * n * A + n * A + (n * (lmax + 1) + n) * A, generator=g).to(cuda)]
+    ys += [torch.randn(2 * E, 2 * n * A, generator=g).to(cuda) for _ in range(lmax)]
+    for a, b in zip(ops.launch_edge_ace_fwd(ys, lmax, A, False), ops.launch_edge_ace_fwd(ys, lmax, A, True)):
+        assert torch.equal(a.to(torch.bfloat16), b)
+    gos = [torch.randn(E if m == 0 else 2 * E, n * A, generator=g).to(cuda) for m in range(lmax + 1)]
+    for a, b in zip(ops.launch_edge_ace_bwd(ys, gos, lmax, A, False), ops.launch_edge_ace_bwd(ys, gos, lmax, A, True)):
+        assert torch.equal(a.to(torch.bfloat16), b)
 
 
 # ----------------------------------------------------------- slot adapters ----

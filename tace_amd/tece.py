@@ -285,10 +285,12 @@ class _FusedParams:
         return torch.mm(g, WN, out_dtype=torch.float32) if self.bf16 else torch.mm(g, WN)
 
 
-def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, save: bool):
+def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, save: bool,
+                     need_out: bool = True):
     """One receiver chunk of the convolution (the sequence of
     ``TeceConvolution.edges`` with the radial MLP in front).  Returns the
-    receiver sums and, with ``save``, what the backward needs."""
+    receiver sums (None without ``need_out``: a recompute for the backward)
+    and, with ``save``, what the backward needs."""
     L, H, A = P.lmax, P.H, P.A
     h, z_t = ops.launch_mlp_hidden_fwd(R, P.mlp_flat, P.mlp_layers)
     if h.dtype == torch.float32:
@@ -307,7 +309,7 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     o = ops.launch_edge_ace_fwd(ys, L, A, P.bf16)
     mb = [P.mm(o[m], P.d_T[m], P.d_b if m == 0 else None) for m in range(L + 1)]
     del o
-    out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H)
+    out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H) if need_out else None
     return out, ((z_t, w, query, key, rp, alpha, ys, mb) if save else None)
 
 
@@ -316,7 +318,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     sender and receiver rows) and returns (grad_R, grad_W) of its edges."""
     L, H, A = P.lmax, P.H, P.A
     if saved is None:
-        _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True)
+        _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True, need_out=False)
     z_t, w, q, k, rp, alpha, ys, mb = saved
     gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16)
     go = [P.mm_grad(gm[m], P.d_N[m]) for m in range(L + 1)]
@@ -345,6 +347,19 @@ def _gm_blocks(t, n: int, L: int, C: int):
     return [flat[n * C * l * l:n * C * (l + 1) ** 2].view(n, 2 * l + 1, C) for l in range(L + 1)]
 
 
+# HBM left free when chunk intermediates are kept for the backward: chunks
+# whose intermediates (~28 KB per edge at C = 128, L = 2) would cut into it
+# are recomputed in the backward instead
+KEEP_RESERVE_BYTES = 40 << 30
+
+
+def _free_bytes(device) -> int:
+    """Device memory a new tensor can take: the driver's free memory plus what
+    torch's caching allocator holds unused."""
+    free, _total = torch.cuda.mem_get_info(device)
+    return free + torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+
+
 class _TeceFused(torch.autograd.Function):
     """The whole TECE convolution with the radial MLP as one operator, for
     frozen parameters: inputs x_lc [rows, K, C] (node features, l layout,
@@ -352,7 +367,10 @@ class _TeceFused(torch.autograd.Function):
     receiver sums [N, K C], group-major, in feature-row order.  The backward
     is written out (recomputing each chunk's forward when there is more than
     one), so GEMM operands go between kernels and GEMMs in the mixing
-    precision without casts, and all chunks add their grad_x into one buffer."""
+    precision without casts, and all chunks add their grad_x into one buffer.
+    With several chunks, each chunk's intermediates are kept for the backward
+    while that leaves ``KEEP_RESERVE_BYTES`` of HBM free; only the chunks
+    beyond that are recomputed."""
 
     @staticmethod
     def forward(ctx, x_lc, R, W, P: _FusedParams, plan: ops.EdgePlan, rs, rd, dst, node_map, chunks):
@@ -364,9 +382,14 @@ class _TeceFused(torch.autograd.Function):
             Nn = plan.n_nodes
             out = torch.empty(Nn, (L + 1) ** 2 * C, dtype=x_lc.dtype, device=x_lc.device)
             full = _gm_blocks(out, Nn, L, C)
+            keep = any(ctx.needs_input_grad[:3])
+            ctx.saved_chunks = []
             for n0, n1, e0, e1 in chunks:
-                oc, _ = _fused_chunk_fwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
-                                         sub_plan(plan, n0, n1, e0, e1), None, False)
+                oc, saved = _fused_chunk_fwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
+                                             sub_plan(plan, n0, n1, e0, e1), None, keep)
+                if saved is not None and _free_bytes(x_lc.device) < KEEP_RESERVE_BYTES:
+                    saved, keep = None, False   # no room: this and later chunks are recomputed
+                ctx.saved_chunks.append(saved)
                 rows_c = node_map[n0:n1].long()
                 for l, blk in enumerate(_gm_blocks(oc, n1 - n0, L, C)):
                     full[l].index_copy_(0, rows_c, blk)
@@ -387,11 +410,13 @@ class _TeceFused(torch.autograd.Function):
             return gx, gR, gW, None, None, None, None, None, None, None
         gR, gW = torch.empty_like(R), torch.empty_like(W)
         full = _gm_blocks(g_out, plan.n_nodes, L, C)
-        for n0, n1, e0, e1 in chunks:
+        for i, (n0, n1, e0, e1) in enumerate(chunks):
             rows_c = node_map[n0:n1].long()
             g_c = torch.cat([f.index_select(0, rows_c).reshape(-1) for f in full]).view(n1 - n0, -1)
+            saved, ctx.saved_chunks[i] = ctx.saved_chunks[i], None
             gR_c, gW_c = _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
-                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0, None, g_c, gx)
+                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0, saved, g_c, gx)
+            del saved
             gR[e0:e1] = gR_c
             gW[e0:e1] = gW_c
         return gx, gR, gW, None, None, None, None, None, None, None

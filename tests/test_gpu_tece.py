@@ -473,11 +473,20 @@ def test_tece_receiver_chunks(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-@pytest.mark.parametrize("chunk_edges", [None, 700])
-def test_tece_fused_operator_matches_oracle(cuda, dtype, chunk_edges):
+@pytest.mark.parametrize("chunk_edges,keep", [(None, "all"), (700, "all"), (700, "none"), (700, "some")])
+def test_tece_fused_operator_matches_oracle(cuda, dtype, chunk_edges, keep, monkeypatch):
     """Frozen parameters (as every calculator sets them) run the TECE layers
     on the fused operator (_TeceFused: hand-written backward, one grad_x
-    buffer), in one piece and in receiver chunks of ~700 edges."""
+    buffer), in one piece and in receiver chunks of ~700 edges whose
+    intermediates are all kept, all recomputed, or kept for the first two
+    chunks only (the HBM reserve reached)."""
+    if keep == "none":
+        monkeypatch.setattr(pt, "KEEP_RESERVE_BYTES", 1 << 62)
+    elif keep == "some":
+        calls = iter(range(10 ** 6))
+        monkeypatch.setattr(pt, "_free_bytes", lambda device: (1 << 62) if next(calls) % 1000 < 2 else 0)
+    else:
+        monkeypatch.setattr(pt, "KEEP_RESERVE_BYTES", 0)
     got, want = _model_pair([structures.bcc_fe(reps=(3, 3, 2), seed=10)], cuda, dtype, seed=2,
                             chunk_edges=chunk_edges, num_channel=64, num_head=2, frozen=True)
     _check(got, want, dtype)

@@ -95,6 +95,9 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     if name.startswith("radial_mlp_out"):
         E, n_out = info
         return s * (E * (64 + n_out) + 64 * n_out)
+    if name.startswith("rows_accumulate"):
+        n_rows, width, n_out = info
+        return s * width * (n_rows + 2 * n_out) + 4 * (n_rows + n_out)
     if name.startswith("seg_linear"):
         x_numel, y_numel, w_numel = info
         return s * (x_numel + y_numel + w_numel)

@@ -317,6 +317,18 @@ int tace_nl_batch_count(const double* pos, int64_t n_atoms, int32_t n_structs, c
 int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, const void* plan, int64_t n_bins,
                        const void* workspace, int64_t workspace_bytes, int32_t mode, const int32_t* rowptr,
                        int32_t* src, int32_t* shifts, void* stream);
+/* Segmented row sum added into out: for each segment s < n_segments,
+ * out[target[s], :] += sum over k in [rowptr[s], rowptr[s+1]) of
+ * rows[slot[k], :] (slot NULL: rows[k]; target NULL: target[s] = s), rows of
+ * `width` values, summed in slot order (deterministic, no atomics).  A target
+ * row may appear in at most one segment of a call.  It sums the per-edge
+ * grad_x rows of the TECE rotate-in backward over each receiver (receiver
+ * CSR) and each sender (a sender CSR) -- the index_add of
+ * oam_2026_07_05.py:769-771's gather, run backwards.  rowptr, slot and target
+ * are trusted device arrays (values within [0, n_rows) and [0, n_out_rows)). */
+int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                         const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
+                         int64_t n_out_rows, void* stream);
 /* exclusive prefix sum: out[0] = 0, out[i+1] = out[i] + counts[i], i < n */
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream);
 

@@ -106,6 +106,33 @@ static void launch_seg_rowsum(const T* cbuf, const int* s_rowptr, const int* s_s
                        row, sg);
 }
 
+// out[target[s], :] += sum over k in [rowptr[s], rowptr[s+1]) of
+// rows[slot ? slot[k] : k, :] -- a segmented row sum in fixed (slot) order,
+// added into out; target = null means target[s] = s.  One workgroup per
+// segment; V values per thread (vector loads).  A target row must not occur
+// in two segments of one launch.
+template <typename T, int V>
+__global__ __launch_bounds__(256) void k_rows_accumulate(const T* __restrict__ rows, int64_t width,
+                                                         const int* __restrict__ rowptr, const int* __restrict__ slot,
+                                                         const int* __restrict__ target, int n_seg,
+                                                         T* __restrict__ out) {
+  typedef T vec __attribute__((ext_vector_type(V)));
+  const int sg = blockIdx.x;
+  if (sg >= n_seg) return;
+  const int b = rowptr[sg], e = rowptr[sg + 1];
+  if (b == e) return;
+  const int64_t t = target ? (int64_t)target[sg] : (int64_t)sg;
+  for (int64_t j = (int64_t)threadIdx.x * V; j < width; j += 256 * V) {
+    vec acc = (vec)(T(0));
+    for (int k = b; k < e; ++k) {
+      const int64_t r = slot ? (int64_t)slot[k] : (int64_t)k;
+      acc += __builtin_nontemporal_load((const vec*)(rows + r * width + j));
+    }
+    vec* o = (vec*)(out + t * width + j);
+    *o = *o + acc;
+  }
+}
+
 // gy = sum of the per-part grad_y partials, in part order
 template <typename T>
 __global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, int nparts, int64_t n,
@@ -1048,6 +1075,38 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
     hipLaunchKernelGGL((k_nlb_edges<true, false>), dim3((n + 255) / 256), dim3(256), 0, s, pos, n, B, abin, aimg,
                        bstart, batoms, nullptr, rowptr, src, shifts);
   return check_launch("tace_nl_batch_fill");
+}
+
+int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                         const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
+                         int64_t n_out_rows, void* stream) {
+  if (n_rows < 0 || width <= 0 || n_segments < 0 || n_segments > INT32_MAX || n_out_rows < 0)
+    return fail("tace_rows_accumulate: bad sizes");
+  if (n_segments == 0) return 0;
+  if (!rowptr || !out || (n_rows > 0 && !rows)) return fail("tace_rows_accumulate: null pointer");
+  if (!target && n_segments > n_out_rows) return fail("tace_rows_accumulate: more segments than output rows");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g((unsigned)n_segments), b(256);
+  const int esz = dtype == TACE_F64 ? 8 : 4;
+  const bool vec = (width * esz) % 16 == 0 && ((uintptr_t)rows & 15) == 0 && ((uintptr_t)out & 15) == 0;
+  if (dtype == TACE_F32) {
+    if (vec)
+      hipLaunchKernelGGL((k_rows_accumulate<float, 4>), g, b, 0, s, (const float*)rows, width, rowptr, slot, target,
+                         (int)n_segments, (float*)out);
+    else
+      hipLaunchKernelGGL((k_rows_accumulate<float, 1>), g, b, 0, s, (const float*)rows, width, rowptr, slot, target,
+                         (int)n_segments, (float*)out);
+  } else if (dtype == TACE_F64) {
+    if (vec)
+      hipLaunchKernelGGL((k_rows_accumulate<double, 2>), g, b, 0, s, (const double*)rows, width, rowptr, slot, target,
+                         (int)n_segments, (double*)out);
+    else
+      hipLaunchKernelGGL((k_rows_accumulate<double, 1>), g, b, 0, s, (const double*)rows, width, rowptr, slot,
+                         target, (int)n_segments, (double*)out);
+  } else {
+    return fail("tace_rows_accumulate: dtype must be TACE_F32 or TACE_F64");
+  }
+  return check_launch("tace_rows_accumulate");
 }
 
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream) {

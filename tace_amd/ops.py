@@ -572,6 +572,36 @@ def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: 
     return gxs, gxd, gW, gwr
 
 
+def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor, slot: Optional[torch.Tensor] = None,
+                    target: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[target[s]] += sum of rows[slot[k]], k in [rowptr[s], rowptr[s+1])
+    (``tace_rows_accumulate``: fixed order, no atomics); returns out."""
+    n_seg = rowptr.numel() - 1
+    dt = out.dtype
+    _req(out, "out", dt)
+    _req(rows, "rows", dt, (rows.shape[0], out.shape[1]))
+    _req(rowptr, "rowptr", torch.int32, (n_seg + 1,))
+    if slot is not None:
+        _req(slot, "slot", torch.int32, (rows.shape[0],))
+    if target is not None:
+        _req(target, "target", torch.int32, (n_seg,))
+    tok = _t0("rows_accumulate")
+    N.check(N.lib().tace_rows_accumulate(N.dtype_code(dt), rows.data_ptr(), rows.shape[0], out.shape[1],
+                                         rowptr.data_ptr(), N.ptr(slot), N.ptr(target), n_seg, out.data_ptr(),
+                                         out.shape[0], N.stream_ptr(out.device)), "tace_rows_accumulate")
+    _t1(tok, (rows.shape[0], out.shape[1], min(n_seg, out.shape[0])))
+    return out
+
+
+def sender_csr(rows_src: torch.Tensor, n_rows: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(rowptr int32 [n_rows+1], slot int32 [E]): the edges grouped by sender
+    row, in edge order within a sender."""
+    slot = torch.argsort(rows_src, stable=True).to(torch.int32)
+    rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=rows_src.device)
+    rp[1:] = torch.cumsum(torch.bincount(rows_src, minlength=n_rows), 0)
+    return rp.to(torch.int32), slot
+
+
 def _pad4(lst):
     return [N.ptr(t) for t in lst] + [None] * (4 - len(lst))
 

@@ -313,9 +313,12 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     return out, ((z_t, w, query, key, rp, alpha, ys, mb) if save else None)
 
 
-def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, dst_out, saved, g_out, gx):
-    """Backward of one chunk: adds its grad_x into ``gx`` (index_add over the
-    sender and receiver rows) and returns (grad_R, grad_W) of its edges."""
+def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, dst_out, recv_rows, saved,
+                     g_out, gx):
+    """Backward of one chunk: adds its grad_x into ``gx`` (per-edge rows
+    summed over the receiver CSR -- receivers at feature rows ``recv_rows``
+    -- and over a sender CSR, in fixed order) and returns (grad_R, grad_W)
+    of its edges."""
     L, H, A = P.lmax, P.H, P.A
     if saved is None:
         _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True, need_out=False)
@@ -334,8 +337,12 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     del gq, gk
     gR = torch.mm(grp, P.rp_N)
     gxs, gxd, gW_in, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True)
-    gx.index_add_(0, rs, gxs).index_add_(0, rd, gxd)
-    del gxs, gxd
+    Nr, E = x_lc.shape[0], rs.shape[0]
+    g2 = gx.view(Nr, -1)
+    ops.rows_accumulate(g2, gxd.view(E, -1), plan.rowptr, plan.eid, recv_rows)
+    del gxd
+    ops.rows_accumulate(g2, gxs.view(E, -1), *ops.sender_csr(rs, Nr))
+    del gxs
     gh = torch.mm(gw, P.mlp_WT_scaled)
     gR += ops.launch_mlp_hidden_bwd(z_t, gh, P.mlp_flat, R.shape[1])
     return gR, gW.add_(gW_in)
@@ -367,7 +374,9 @@ class _TeceFused(torch.autograd.Function):
     receiver sums [N, K C], group-major, in feature-row order.  The backward
     is written out (recomputing each chunk's forward when there is more than
     one), so GEMM operands go between kernels and GEMMs in the mixing
-    precision without casts, and all chunks add their grad_x into one buffer.
+    precision without casts, and all chunks add their grad_x into one buffer
+    by segmented sums in a fixed order (no atomics: the forces repeat bit for
+    bit).
     With several chunks, each chunk's intermediates are kept for the backward
     while that leaves ``KEEP_RESERVE_BYTES`` of HBM free; only the chunks
     beyond that are recomputed."""
@@ -405,7 +414,8 @@ class _TeceFused(torch.autograd.Function):
         g_out = g_out.contiguous()
         gx = torch.zeros_like(x_lc)
         if chunks is None:
-            gR, gW = _fused_chunk_bwd(P, x_lc, R, W, rs, rd, plan, node_map, dst, ctx.saved_chunk, g_out, gx)
+            gR, gW = _fused_chunk_bwd(P, x_lc, R, W, rs, rd, plan, node_map, dst, node_map, ctx.saved_chunk, g_out,
+                                      gx)
             ctx.saved_chunk = None
             return gx, gR, gW, None, None, None, None, None, None, None
         gR, gW = torch.empty_like(R), torch.empty_like(W)
@@ -415,7 +425,8 @@ class _TeceFused(torch.autograd.Function):
             g_c = torch.cat([f.index_select(0, rows_c).reshape(-1) for f in full]).view(n1 - n0, -1)
             saved, ctx.saved_chunks[i] = ctx.saved_chunks[i], None
             gR_c, gW_c = _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
-                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0, saved, g_c, gx)
+                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0,
+                                          node_map[n0:n1].contiguous(), saved, g_c, gx)
             del saved
             gR[e0:e1] = gR_c
             gW[e0:e1] = gW_c

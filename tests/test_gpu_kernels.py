@@ -510,3 +510,34 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts
     (gw_want,) = torch.autograd.grad(ref, wr, go)
     (gw,) = torch.autograd.grad(lin(xg, sp, alpha), lin.weight, go.to(cuda))
     close(gw, gw_want, dtype, "seg linear grad w")
+
+
+# ------------------------------------------------------ segmented row sums ----
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("width", [1152, 37])
+def test_rows_accumulate_matches_index_add(cuda, dtype, width):
+    """tace_rows_accumulate (fixed-order segmented sums added into out) against
+    index_add_: receiver-CSR segments with target rows, a sender CSR over all
+    rows (empty segments included), and rows whose width is not a multiple
+    of the vector length."""
+    g = torch.Generator().manual_seed(width)
+    E, Nr = 900, 120
+    rows = torch.randn(E, width, generator=g, dtype=torch.float64)
+    base = torch.randn(Nr, width, generator=g, dtype=torch.float64)
+    src = torch.randint(0, Nr - 7, (E,), generator=g)          # rows >= Nr-7 get nothing
+    want = base.clone().index_add_(0, src, rows)
+    rp, slot = ops.sender_csr(src.to(cuda), Nr)
+    got = ops.rows_accumulate(base.to(dtype).to(cuda), rows.to(dtype).to(cuda), rp, slot)
+    close(got, want, dtype, "sender segments")
+    # receiver-grouped segments written to permuted target rows
+    counts = torch.randint(0, 15, (Nr,), generator=g)
+    counts[3] = 0
+    Eg = int(counts.sum())
+    rows2 = torch.randn(Eg, width, generator=g, dtype=torch.float64)
+    rowptr = torch.zeros(Nr + 1, dtype=torch.int64)
+    rowptr[1:] = torch.cumsum(counts, 0)
+    target = torch.randperm(Nr, generator=g)
+    want2 = base.clone().index_add_(0, torch.repeat_interleave(target, counts), rows2)
+    got2 = ops.rows_accumulate(base.to(dtype).to(cuda), rows2.to(dtype).to(cuda), rowptr.to(torch.int32).to(cuda),
+                               None, target.to(torch.int32).to(cuda))
+    close(got2, want2, dtype, "receiver segments")

@@ -492,6 +492,15 @@ def test_tece_fused_operator_matches_oracle(cuda, dtype, chunk_edges, keep, monk
     _check(got, want, dtype)
 
 
+def test_tece_fused_forces_repeat_bit_for_bit(cuda):
+    """No atomics on the fused path: two evaluations give identical forces."""
+    st = [structures.bcc_fe(reps=(3, 3, 2), seed=10)]
+    kw = dict(seed=2, chunk_edges=700, num_channel=64, num_head=2, frozen=True)
+    a, _ = _model_pair(st, cuda, torch.float32, **kw)
+    b, _ = _model_pair(st, cuda, torch.float32, **kw)
+    assert torch.equal(a["forces"], b["forces"]) and torch.equal(a["energy"], b["energy"])
+
+
 @pytest.mark.parametrize("chunk_edges", [None, 700])
 def test_tece_fused_bf16_mixing_equals_operator_path(cuda, chunk_edges):
     """bf16 channel mixing: the fused operator (bf16 GEMM operands stored by

@@ -70,8 +70,8 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         E, K, C, H = info
         return s * E * (2 * K * C + 2 * H + H) + s * H
     if name.startswith("tece_score_bwd"):
-        E, K, C, H = info
-        return s * E * (4 * K * C + 4 * H + H) + s * H
+        E, K, C, H, b16 = info
+        return s * E * (2 * K * C + 4 * H + H) + (2 if b16 else s) * E * 2 * K * C + s * H
     if name.startswith("graph_softmax_fwd"):
         E, H, n = info
         return s * E * H * 2 + 4 * (E + n + 1)
@@ -82,16 +82,30 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         n, E, C, K, H = info
         return s * (E * (K * C + H + K * K) + n * K * C) + 4 * (E + 2 * n + 1)
     if name.startswith("tece_rotate_out_bwd"):
-        n, E, C, K, H = info
-        return s * (E * (2 * K * C + 2 * H + 2 * K * K) + n * K * C) + 8 * E
+        n, E, C, K, H, b16 = info
+        return s * (E * (K * C + 2 * H + 2 * K * K) + n * K * C) + (2 if b16 else s) * E * K * C + 8 * E
     if name.startswith("edge_rotate_in_fwd"):
-        E, K, C, has_w = info
+        E, K, C, has_w, b16 = info
         nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
-        return s * E * (4 * K * C + K * K + (2 * nc * C + 2 * K * C if has_w else 0)) + 16 * E
+        so = 2 if b16 else s
+        # x_src, x_dst and W read; m_src, m_dst (and w read, m_w written) out
+        return s * E * (2 * K * C + K * K + (2 * nc * C if has_w else 0)) + so * E * (2 * K * C + (2 * K * C if has_w else 0)) \
+            + 16 * E
     if name.startswith("edge_rotate_in_bwd"):
         E, K, C, has_w = info
         nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
-        return s * E * (8 * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
+        # x_src, x_dst, g_m_src, g_m_dst, W read; per-edge grad_x rows and g_W
+        # written; with radial weights also g_m_w and w read, g_w written
+        return s * E * (6 * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
+    if name.startswith("tece_edge_ace_fwd") or name.startswith("tece_edge_ace_bwd"):
+        E, A, L, b16 = info
+        n, P = L + 1, len(ops.edge_ace_paths(L))
+        ys = E * ((P * n * A + n * A + (n * (L + 1) + n) * A) + L * 4 * n * A)   # y0 [E, .], y_m [2E, 2nA]
+        os_ = E * (n * A + L * 2 * n * A)                                       # o0 [E, nA], o_m [2E, nA]
+        so = 2 if b16 else s
+        if name.startswith("tece_edge_ace_fwd"):
+            return s * ys + so * os_
+        return s * (ys + os_) + so * ys
     if name.startswith("radial_mlp_out"):
         E, n_out = info
         return s * (E * (64 + n_out) + 64 * n_out)

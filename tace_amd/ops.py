@@ -460,7 +460,7 @@ def launch_score_bwd(q, k, rp, tscale, gs, lmax: int, H: int, bf16_out: bool = F
                                         tscale.data_ptr(), gs.data_ptr(), E, lmax, C, H, _block_array(gq),
                                         _block_array(gk), grp.data_ptr(), N.stream_ptr(rp.device)),
             "tace_tece_score_bwd")
-    _t1(tok, (E, (lmax + 1) ** 2, C, H))
+    _t1(tok, (E, (lmax + 1) ** 2, C, H, bf16_out))
     return gq, gk, grp
 
 
@@ -521,7 +521,7 @@ def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax
                                              W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
                                              plan.n_nodes, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
                                              gW.data_ptr(), N.stream_ptr(W.device)), "tace_tece_rotate_out_bwd")
-    _t1(tok, (plan.n_nodes, E, C, K, H))
+    _t1(tok, (plan.n_nodes, E, C, K, H, bf16_out))
     return gm, ga, gW
 
 
@@ -546,7 +546,7 @@ def launch_rotate_in_fwd(x, W, rows_src, rows_dst, wr, lmax: int, bf16_out: bool
                                             rows_src.data_ptr(), rows_dst.data_ptr(), N.ptr(wr), Nr, E, lmax, C,
                                             _block_array(ms), _block_array(md), _block_array(mw) if mw else None,
                                             N.stream_ptr(x.device)), "tace_edge_rotate_in_fwd")
-    _t1(tok, (E, K, C, wr is not None))
+    _t1(tok, (E, K, C, wr is not None, bf16_out))
     return ms, md, mw
 
 
@@ -619,7 +619,7 @@ def launch_edge_ace_fwd(ys, lmax: int, A: int, bf16_out: bool = False):
     tok = _t0("tece_edge_ace_fwd")
     N.check(N.lib().tace_tece_edge_ace_fwd(_tece_code(dt, bf16_out), *_pad4(list(ys)), E, lmax, A, *_pad4(outs),
                                            N.stream_ptr(y0.device)), "tace_tece_edge_ace_fwd")
-    _t1(tok, (E, A, lmax))
+    _t1(tok, (E, A, lmax, bf16_out))
     return outs
 
 
@@ -632,7 +632,7 @@ def launch_edge_ace_bwd(ys, gos, lmax: int, A: int, bf16_out: bool = False):
     tok = _t0("tece_edge_ace_bwd")
     N.check(N.lib().tace_tece_edge_ace_bwd(_tece_code(dt, bf16_out), *_pad4(list(ys)), *_pad4(list(gos)), E, lmax, A,
                                            *_pad4(gys), N.stream_ptr(ys[0].device)), "tace_tece_edge_ace_bwd")
-    _t1(tok, (E, A, lmax))
+    _t1(tok, (E, A, lmax, bf16_out))
     return gys
 
 

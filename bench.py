@@ -1,20 +1,23 @@
 """Benchmark: TACE energy + conservative forces on the 12,288-atom water box.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                    [--workload water12k|fe101k]
+                    [--workload water12k|fcc1024|ragged128|fe101k] [--kernels]
 
 One step = one MD-step evaluation on one GPU: GPU cell-list neighbour list
 from positions resident in HBM, the model forward (edge featurisation, 3
 interaction + product layers, readout) and the backward for F = -dE/dr.
 Workload: 4,096 H2O, 49.7 A periodic cube, r_c = 6,
 Cartesian-TACE architecture C=128, L=3, nu=3, 3 layers, random-init weights
-(seed 0), float32.  Prints one JSON line on stdout.  ``--workload fe101k``
-measures the TECE configuration instead (bcc Fe
-37^3 cells, 101,306 atoms, r_c = 5, C=128, L=2, 4 heads, 2 layers).
+(seed 0), float32.  Prints one JSON line on stdout.  The other configurations
+have their own workloads: ``fcc1024`` (configs[1], 1,024-atom FCC alloy),
+``ragged128`` (configs[3], 128 random crystals, 89 species, with stress) and
+``fe101k`` (configs[4], TECE: bcc Fe 37^3 cells, 101,306 atoms, r_c = 5, C=128,
+L=2, 4 heads, 2 layers, bf16 channel mixing).
 
 ``roofline`` is for the kernel with the largest share of the timed region,
 bracketed with HIP events on the stream it runs on; its algorithmic bytes
-per launch follow the formulas in DESIGN.md.  ``cpu_baseline`` times the
+per launch follow ``algorithmic_bytes`` below (each operand read or written
+once).  ``cpu_baseline`` times the
 CPU oracle (a restatement of the reference algorithm) on a bounded sample of
 the same workload on this host.
 """
@@ -200,7 +203,7 @@ def workloads(args):
         dt_fs=1.0, species=list(structures.MPTRJ_ELEMENTS), targets=["energy", "forces", "stress"],
         structs=lambda: structures.ragged_batch(128, seed=0),
         cfg=lambda a: configs.model_cfg("ragged128", list(structures.MPTRJ_ELEMENTS), a),
-        describe=lambda nat: f"128 random triclinic crystals, {nat} atoms (configs[3]), E+F+S, per-crystal GPU NL "
+        describe=lambda nat: f"128 random triclinic crystals, {nat} atoms (configs[3]), E+F+S, batched GPU NL "
                              f"every step",
         arch=dict(channels=256, L=3, correlation=3, layers=2, cutoff=6.0, species=89),
         cpu_slice=lambda: (structures.ragged_batch(3, nmin=8, nmax=40, seed=1), "3-crystal ragged slice"))
@@ -244,7 +247,7 @@ def main():
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; runs on more than one GPU are not part of it "
-              "(see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "(the one-GPU line is the per-GPU share of a spatially decomposed run).", file=sys.stderr)
         sys.exit(2)
 
     from tace_amd import data, model as pm, ops

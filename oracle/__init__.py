@@ -18,6 +18,7 @@ installed, so e3nn's published algorithms are restated here:
 * ``neighbours.py`` brute-force periodic neighbour list (matscipy ``ijSd``
                     semantics) in float64 numpy.
 
-Parity pins (what fixes each part independently of this code) are listed in
-DESIGN.md and exercised by ``tests/test_oracle_pins.py``.
+The parity pins (what fixes each part independently of this code: closed
+forms, independent implementations, invariances, finite differences) are the
+tests of ``tests/test_oracle_pins.py`` and ``tests/test_oracle_tece_pins.py``.
 """

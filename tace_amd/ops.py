@@ -190,21 +190,47 @@ def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cuto
 
 
 # ------------------------------------------------------ edge tensor product ----
+def launch_edge_tp_fwd(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0, node_map=None):
+    Nn, E = plan.n_nodes, plan.n_edges
+    dt = x.dtype
+    _req(x, "x", dt, (Nn, C * var.d1))
+    _req(y, "y", dt, (E, var.d2))
+    _req(w, "w", dt, (E, C * var.npath))
+    out = torch.empty(Nn, C * var.dout, dtype=dt, device=x.device)
+    tok = _t0("edge_tp_fwd:" + var.key)
+    N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                     plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), N.ptr(node_map), Nn,
+                                     E, C, layout, out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
+    _t1(tok, (Nn, E, C))
+    return out
+
+
+def launch_edge_tp_bwd(x, y, w, gout, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0, node_map=None,
+                       need_x: bool = True):
+    """(grad_x or None, grad_y, grad_w) of ``launch_edge_tp_fwd``."""
+    _req(gout, "g_out", x.dtype, (plan.n_nodes, C * var.dout))
+    gx = torch.empty_like(x) if need_x else None
+    gy = torch.empty_like(y)
+    gw = torch.empty_like(w)
+    s_rowptr, s_slot = plan.sender_csr() if need_x else (None, None)
+    n_ws = N.lib().tace_edge_tp_workspace_elems(var.vid, plan.n_edges, C, int(need_x))
+    if n_ws < 0:
+        N.check(int(n_ws), "tace_edge_tp_workspace_elems")
+    ws = torch.empty(max(n_ws, 1), dtype=x.dtype, device=x.device)
+    tok = _t0("edge_tp_bwd:" + var.key)
+    N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                     gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
+                                     N.ptr(node_map), plan.n_nodes, plan.n_edges, C, layout, N.ptr(s_rowptr),
+                                     N.ptr(s_slot), ws.data_ptr(), ws.numel(), N.ptr(gx), gy.data_ptr(),
+                                     gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
+    _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
+    return gx, gy, gw
+
+
 class _EdgeTP(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int, node_map):
-        Nn, E = plan.n_nodes, plan.n_edges
-        dt = x.dtype
-        _req(x, "x", dt, (Nn, C * var.d1))
-        _req(y, "y", dt, (E, var.d2))
-        _req(w, "w", dt, (E, C * var.npath))
-        out = torch.empty(Nn, C * var.dout, dtype=dt, device=x.device)
-        tok = _t0("edge_tp_fwd:" + var.key)
-        N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
-                                         plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
-                                         N.ptr(node_map), Nn, E, C, layout, out.data_ptr(),
-                                         N.stream_ptr(x.device)), "tace_edge_tp_fwd")
-        _t1(tok, (Nn, E, C))
+        out = launch_edge_tp_fwd(x, y, w, plan, var, C, layout, node_map)
         ctx.save_for_backward(x, y, w)
         ctx.plan, ctx.var, ctx.C, ctx.layout, ctx.node_map = plan, var, C, layout, node_map
         return out
@@ -212,26 +238,8 @@ class _EdgeTP(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gout):
         x, y, w = ctx.saved_tensors
-        plan, var, C = ctx.plan, ctx.var, ctx.C
-        gout = gout.contiguous()
-        need_x = ctx.needs_input_grad[0]
-        gx = torch.empty_like(x) if need_x else None
-        gy = torch.empty_like(y)
-        gw = torch.empty_like(w)
-        s_rowptr, s_slot = plan.sender_csr() if need_x else (None, None)
-        n_ws = N.lib().tace_edge_tp_workspace_elems(var.vid, plan.n_edges, C, int(need_x))
-        if n_ws < 0:
-            N.check(int(n_ws), "tace_edge_tp_workspace_elems")
-        ws = torch.empty(max(n_ws, 1), dtype=x.dtype, device=x.device)
-        tok = _t0("edge_tp_bwd:" + var.key)
-        N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
-                                         gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
-                                         plan.src.data_ptr(), N.ptr(ctx.node_map), plan.n_nodes, plan.n_edges, C,
-                                         ctx.layout,
-                                         N.ptr(s_rowptr),
-                                         N.ptr(s_slot), ws.data_ptr(), ws.numel(), N.ptr(gx),
-                                         gy.data_ptr(), gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
-        _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
+        gx, gy, gw = launch_edge_tp_bwd(x, y, w, gout.contiguous(), ctx.plan, ctx.var, ctx.C, ctx.layout,
+                                        ctx.node_map, ctx.needs_input_grad[0])
         return gx, gy, gw, None, None, None, None, None
 
 
@@ -303,20 +311,38 @@ LAYOUT_IN1_GROUPED, LAYOUT_OUT_GROUPED, LAYOUT_IN2_GROUPED = 1, 2, 4
 LAYOUT_ALL_GROUPED = 7
 
 
+def launch_uuu_fwd(x1, x2, w, var: TpVariant, C: int, layout: int = 0):
+    Nn = x1.shape[0]
+    dt = x1.dtype
+    _req(x1, "x1", dt, (Nn, C * var.d1))
+    _req(x2, "x2", dt, (Nn, C * var.d2))
+    if w is not None:
+        _req(w, "w", dt, (Nn, C * var.npath))
+    out = torch.empty(Nn, C * var.dout, dtype=dt, device=x1.device)
+    tok = _t0("uuu_fwd:" + var.key)
+    N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), N.ptr(w), Nn, C, layout,
+                                 out.data_ptr(), N.stream_ptr(x1.device)), "tace_uuu_fwd")
+    _t1(tok, (Nn, C))
+    return out
+
+
+def launch_uuu_bwd(x1, x2, w, gout, var: TpVariant, C: int, layout: int = 0):
+    """(grad_x1, grad_x2, grad_w or None) of ``launch_uuu_fwd``."""
+    _req(gout, "g_out", x1.dtype, (x1.shape[0], C * var.dout))
+    g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
+    gw = torch.empty_like(w) if w is not None else None
+    tok = _t0("uuu_bwd:" + var.key)
+    N.check(N.lib().tace_uuu_bwd(var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(), N.ptr(w),
+                                 gout.data_ptr(), x1.shape[0], C, layout, g1.data_ptr(), g2.data_ptr(), N.ptr(gw),
+                                 N.stream_ptr(x1.device)), "tace_uuu_bwd")
+    _t1(tok, (x1.shape[0], C))
+    return g1, g2, gw
+
+
 class _UUU(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x1, x2, w, var: TpVariant, C: int, layout: int):
-        Nn = x1.shape[0]
-        dt = x1.dtype
-        _req(x1, "x1", dt, (Nn, C * var.d1))
-        _req(x2, "x2", dt, (Nn, C * var.d2))
-        if w is not None:
-            _req(w, "w", dt, (Nn, C * var.npath))
-        out = torch.empty(Nn, C * var.dout, dtype=dt, device=x1.device)
-        tok = _t0("uuu_fwd:" + var.key)
-        N.check(N.lib().tace_uuu_fwd(var.vid, N.dtype_code(dt), x1.data_ptr(), x2.data_ptr(), N.ptr(w), Nn, C,
-                                     layout, out.data_ptr(), N.stream_ptr(x1.device)), "tace_uuu_fwd")
-        _t1(tok, (Nn, C))
+        out = launch_uuu_fwd(x1, x2, w, var, C, layout)
         ctx.save_for_backward(x1, x2, w)
         ctx.var, ctx.C, ctx.layout = var, C, layout
         return out
@@ -324,14 +350,7 @@ class _UUU(torch.autograd.Function):
     @staticmethod
     def backward(ctx, gout):
         x1, x2, w = ctx.saved_tensors
-        gout = gout.contiguous()
-        g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
-        gw = torch.empty_like(w) if w is not None else None
-        tok = _t0("uuu_bwd:" + ctx.var.key)
-        N.check(N.lib().tace_uuu_bwd(ctx.var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(), N.ptr(w),
-                                     gout.data_ptr(), x1.shape[0], ctx.C, ctx.layout, g1.data_ptr(), g2.data_ptr(),
-                                     N.ptr(gw), N.stream_ptr(x1.device)), "tace_uuu_bwd")
-        _t1(tok, (x1.shape[0], ctx.C))
+        g1, g2, gw = launch_uuu_bwd(x1, x2, w, gout.contiguous(), ctx.var, ctx.C, ctx.layout)
         return g1, g2, gw, None, None, None
 
 

@@ -22,7 +22,7 @@ from typing import Optional, Sequence
 
 import torch
 
-from . import ops
+from . import library, ops
 from .model import e3nn_to_gm, gm_to_e3nn
 from .so3 import Irrep, Irreps, generate_paths
 from .tece import TeceConvolution
@@ -66,8 +66,9 @@ class e3nnHipScatterTensorProduct(torch.nn.Module):
         ops.find_variant(self.key)  # raises if this variant is not compiled in
 
     def forward(self, x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, edge_index: torch.Tensor) -> torch.Tensor:
-        plan = ops.EdgePlan.from_edge_index(edge_index, x.shape[0])
-        return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C)
+        # a registered custom operator (tace_amd.library): traceable by
+        # make_fx / torch.export, backward included
+        return library.uvu_scatter(x, y, w, edge_index, self.key, self.C)
 
 
 class e3nnHipUuuTensorProduct(torch.nn.Module):
@@ -90,7 +91,7 @@ class e3nnHipUuuTensorProduct(torch.nn.Module):
         # ws [N, paths*C]: the per-node weights of the trainable (bilinear-gate)
         # product; only the variants compiled as weighted accept them (the ABI
         # rejects a mismatch)
-        return ops.uuu_tp(x, y, ops.find_variant(self.key), self.C, 0, ws)
+        return library.uuu(x, y, ws, self.key, self.C)
 
 
 class HipTeceConvolution(TeceConvolution):

@@ -16,13 +16,17 @@ needs from the operators in the ``fused_tp`` slots.
 * ``tace_amd::uuu(x1, x2, w, key, channels)``: the uuu product of
   ``uuuTensorProduct.fused_tp`` (``fused.py:90-95``), ``w`` the optional
   per-node path weights; backward ``tace_amd::uuu_backward``.
+* ``tace_amd::receiver_csr``, ``tece_rotate_in``, ``tece_score``,
+  ``tece_softmax``, ``tece_edge_ace``, ``tece_rotate_out`` (each with a
+  ``*_backward``): the kernels of the TECE convolution slot
+  (``HipTeceConvolution``), edge features as lists of SO(2) blocks.
 
 Operators run the library's kernels; there is no CPU implementation.
 """
 
 from __future__ import annotations
 
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
 import torch
 
@@ -112,3 +116,238 @@ def _uuu_backward(ctx, grad_out):
 
 
 uuu.register_autograd(_uuu_backward, setup_context=_uuu_setup)
+
+
+# ------------------------------------------------------------------ TECE ----
+# The kernels of the TECE convolution slot (HipTeceConvolution, replacing
+# OAM20260705Convolution, tace/models/_e3nn/archive/oam_2026_07_05.py:756-823).
+# Edge features are lists of SO(2) blocks (block 0 [E, (L+1) ch], block m
+# [2E, (L+1-m) ch]).  Gradients that do not reach an output arrive as None
+# and are taken as zeros.
+
+def _zeros_for(grads, like):
+    return [g.contiguous() if g is not None else torch.zeros_like(t) for g, t in zip(grads, like)]
+
+
+@torch.library.custom_op("tace_amd::receiver_csr", mutates_args=(), device_types="cuda")
+def receiver_csr(edge_index: Tensor, n_nodes: int) -> Tuple[Tensor, Tensor]:
+    """(rowptr int32 [n_nodes+1], eid int32 [E]): the edges of each receiver
+    (edge_index[1]) in edge order."""
+    dst = edge_index[1]
+    rp = torch.zeros(n_nodes + 1, dtype=torch.int64, device=dst.device)
+    rp[1:] = torch.cumsum(torch.bincount(dst, minlength=n_nodes), 0)
+    return rp.to(torch.int32), torch.argsort(dst, stable=True).to(torch.int32)
+
+
+@receiver_csr.register_fake
+def _receiver_csr_fake(edge_index, n_nodes):
+    return (edge_index.new_empty(n_nodes + 1, dtype=torch.int32),
+            edge_index.new_empty(edge_index.shape[1], dtype=torch.int32))
+
+
+def _plan(rowptr, eid, src=None) -> ops.EdgePlan:
+    n = rowptr.shape[0] - 1
+    return ops.EdgePlan(n, eid.shape[0], rowptr, src if src is not None else eid, eid)
+
+
+@torch.library.custom_op("tace_amd::tece_rotate_in", mutates_args=(), device_types="cuda")
+def tece_rotate_in(x: Tensor, wigner: Tensor, rows_src: Tensor, rows_dst: Tensor, radial_w: Tensor,
+                   lmax: int) -> List[Tensor]:
+    ms, md, mw = ops.launch_rotate_in_fwd(x.contiguous(), wigner.contiguous(), rows_src.contiguous(),
+                                          rows_dst.contiguous(), radial_w.contiguous(), lmax)
+    return ms + md + mw
+
+
+@tece_rotate_in.register_fake
+def _tece_rotate_in_fake(x, wigner, rows_src, rows_dst, radial_w, lmax):
+    E, C = wigner.shape[0], x.shape[2]
+    mk = lambda ch: [x.new_empty(shp) for shp in ops.so2_block_shapes(E, lmax, ch)]
+    return mk(C) + mk(C) + mk(2 * C)
+
+
+@torch.library.custom_op("tace_amd::tece_rotate_in_backward", mutates_args=(), device_types="cuda")
+def tece_rotate_in_backward(x: Tensor, wigner: Tensor, rows_src: Tensor, rows_dst: Tensor, radial_w: Tensor,
+                            grads: List[Tensor], lmax: int) -> Tuple[Tensor, Tensor, Tensor]:
+    n = lmax + 1
+    g = [t.contiguous() for t in grads]
+    gxs, gxd, gW, gwr = ops.launch_rotate_in_bwd(x.contiguous(), wigner.contiguous(), rows_src.contiguous(),
+                                                 rows_dst.contiguous(), radial_w.contiguous(), g[:n], g[n:2 * n],
+                                                 g[2 * n:], True)
+    gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
+    return gx, gW, gwr
+
+
+@tece_rotate_in_backward.register_fake
+def _tece_rotate_in_backward_fake(x, wigner, rows_src, rows_dst, radial_w, grads, lmax):
+    return torch.empty_like(x), torch.empty_like(wigner), torch.empty_like(radial_w)
+
+
+def _rotate_in_setup(ctx, inputs, output):
+    x, wigner, rows_src, rows_dst, radial_w, lmax = inputs
+    ctx.save_for_backward(x, wigner, rows_src, rows_dst, radial_w)
+    ctx.lmax = lmax
+    ctx.like = [o.detach() for o in output]
+
+
+def _rotate_in_backward(ctx, grads):
+    x, wigner, rows_src, rows_dst, radial_w = ctx.saved_tensors
+    gx, gW, gwr = tece_rotate_in_backward(x, wigner, rows_src, rows_dst, radial_w, _zeros_for(grads, ctx.like),
+                                          ctx.lmax)
+    return gx, gW, None, None, gwr, None
+
+
+tece_rotate_in.register_autograd(_rotate_in_backward, setup_context=_rotate_in_setup)
+
+
+@torch.library.custom_op("tace_amd::tece_score", mutates_args=(), device_types="cuda")
+def tece_score(q: List[Tensor], k: List[Tensor], radial_proj: Tensor, tscale: Tensor, lmax: int,
+               heads: int) -> Tensor:
+    return ops.launch_score_fwd([t.contiguous() for t in q], [t.contiguous() for t in k], radial_proj.contiguous(),
+                                tscale.contiguous(), lmax, heads)
+
+
+@tece_score.register_fake
+def _tece_score_fake(q, k, radial_proj, tscale, lmax, heads):
+    return radial_proj.new_empty(radial_proj.shape[0], heads)
+
+
+@torch.library.custom_op("tace_amd::tece_score_backward", mutates_args=(), device_types="cuda")
+def tece_score_backward(q: List[Tensor], k: List[Tensor], radial_proj: Tensor, tscale: Tensor, grad: Tensor,
+                        lmax: int, heads: int) -> List[Tensor]:
+    gq, gk, grp = ops.launch_score_bwd([t.contiguous() for t in q], [t.contiguous() for t in k],
+                                       radial_proj.contiguous(), tscale.contiguous(), grad.contiguous(), lmax, heads)
+    return gq + gk + [grp]
+
+
+@tece_score_backward.register_fake
+def _tece_score_backward_fake(q, k, radial_proj, tscale, grad, lmax, heads):
+    return [torch.empty_like(t) for t in q] + [torch.empty_like(t) for t in k] + [torch.empty_like(radial_proj)]
+
+
+def _score_setup(ctx, inputs, output):
+    q, k, radial_proj, tscale, lmax, heads = inputs
+    ctx.save_for_backward(*q, *k, radial_proj, tscale)
+    ctx.lmax, ctx.heads = lmax, heads
+
+
+def _score_backward(ctx, grad):
+    *qk, rp, tscale = ctx.saved_tensors
+    n = ctx.lmax + 1
+    out = tece_score_backward(list(qk[:n]), list(qk[n:]), rp, tscale, grad, ctx.lmax, ctx.heads)
+    return out[:n], out[n:2 * n], out[2 * n], None, None, None
+
+
+tece_score.register_autograd(_score_backward, setup_context=_score_setup)
+
+
+@torch.library.custom_op("tace_amd::tece_softmax", mutates_args=(), device_types="cuda")
+def tece_softmax(score: Tensor, rowptr: Tensor, eid: Tensor) -> Tensor:
+    return ops.launch_softmax_fwd(score.contiguous(), _plan(rowptr, eid))
+
+
+@tece_softmax.register_fake
+def _tece_softmax_fake(score, rowptr, eid):
+    return torch.empty_like(score)
+
+
+@torch.library.custom_op("tace_amd::tece_softmax_backward", mutates_args=(), device_types="cuda")
+def tece_softmax_backward(alpha: Tensor, grad: Tensor, rowptr: Tensor, eid: Tensor) -> Tensor:
+    return ops.launch_softmax_bwd(alpha.contiguous(), grad.contiguous(), _plan(rowptr, eid))
+
+
+@tece_softmax_backward.register_fake
+def _tece_softmax_backward_fake(alpha, grad, rowptr, eid):
+    return torch.empty_like(alpha)
+
+
+def _softmax_setup(ctx, inputs, output):
+    score, rowptr, eid = inputs
+    ctx.save_for_backward(output, rowptr, eid)
+
+
+def _softmax_backward(ctx, grad):
+    alpha, rowptr, eid = ctx.saved_tensors
+    return tece_softmax_backward(alpha, grad, rowptr, eid), None, None
+
+
+tece_softmax.register_autograd(_softmax_backward, setup_context=_softmax_setup)
+
+
+@torch.library.custom_op("tace_amd::tece_edge_ace", mutates_args=(), device_types="cuda")
+def tece_edge_ace(ys: List[Tensor], lmax: int, hidden: int) -> List[Tensor]:
+    return ops.launch_edge_ace_fwd([t.contiguous() for t in ys], lmax, hidden)
+
+
+@tece_edge_ace.register_fake
+def _tece_edge_ace_fake(ys, lmax, hidden):
+    E, n = ys[0].shape[0], lmax + 1
+    return [ys[0].new_empty(E if m == 0 else 2 * E, n * hidden) for m in range(lmax + 1)]
+
+
+@torch.library.custom_op("tace_amd::tece_edge_ace_backward", mutates_args=(), device_types="cuda")
+def tece_edge_ace_backward(ys: List[Tensor], grads: List[Tensor], lmax: int, hidden: int) -> List[Tensor]:
+    return ops.launch_edge_ace_bwd([t.contiguous() for t in ys], [g.contiguous() for g in grads], lmax, hidden)
+
+
+@tece_edge_ace_backward.register_fake
+def _tece_edge_ace_backward_fake(ys, grads, lmax, hidden):
+    return [torch.empty_like(y) for y in ys]
+
+
+def _edge_ace_setup(ctx, inputs, output):
+    ys, lmax, hidden = inputs
+    ctx.save_for_backward(*ys)
+    ctx.lmax, ctx.hidden = lmax, hidden
+    ctx.like = [o.detach() for o in output]
+
+
+def _edge_ace_backward(ctx, grads):
+    ys = list(ctx.saved_tensors)
+    return tece_edge_ace_backward(ys, _zeros_for(grads, ctx.like), ctx.lmax, ctx.hidden), None, None
+
+
+tece_edge_ace.register_autograd(_edge_ace_backward, setup_context=_edge_ace_setup)
+
+
+@torch.library.custom_op("tace_amd::tece_rotate_out", mutates_args=(), device_types="cuda")
+def tece_rotate_out(m: List[Tensor], alpha: Tensor, wigner: Tensor, rowptr: Tensor, eid: Tensor, dst: Tensor,
+                    lmax: int, heads: int) -> Tensor:
+    """Receiver sums [N, (L+1)^2 C], group-major, rows = node ids (dst: the
+    receiver of each edge, int64, for the backward)."""
+    return ops.launch_rotate_out_fwd([t.contiguous() for t in m], alpha.contiguous(), wigner.contiguous(),
+                                     _plan(rowptr, eid), None, lmax, heads)
+
+
+@tece_rotate_out.register_fake
+def _tece_rotate_out_fake(m, alpha, wigner, rowptr, eid, dst, lmax, heads):
+    C = m[0].shape[1] // (lmax + 1)
+    return alpha.new_empty(rowptr.shape[0] - 1, (lmax + 1) ** 2 * C)
+
+
+@torch.library.custom_op("tace_amd::tece_rotate_out_backward", mutates_args=(), device_types="cuda")
+def tece_rotate_out_backward(m: List[Tensor], alpha: Tensor, wigner: Tensor, grad: Tensor, dst: Tensor,
+                             rowptr: Tensor, eid: Tensor, lmax: int, heads: int) -> List[Tensor]:
+    gm, ga, gW = ops.launch_rotate_out_bwd([t.contiguous() for t in m], alpha.contiguous(), wigner.contiguous(),
+                                           grad.contiguous(), dst.contiguous(), None, _plan(rowptr, eid), lmax, heads)
+    return gm + [ga, gW]
+
+
+@tece_rotate_out_backward.register_fake
+def _tece_rotate_out_backward_fake(m, alpha, wigner, grad, dst, rowptr, eid, lmax, heads):
+    return [torch.empty_like(t) for t in m] + [torch.empty_like(alpha), torch.empty_like(wigner)]
+
+
+def _rotate_out_setup(ctx, inputs, output):
+    m, alpha, wigner, rowptr, eid, dst, lmax, heads = inputs
+    ctx.save_for_backward(*m, alpha, wigner, rowptr, eid, dst)
+    ctx.lmax, ctx.heads = lmax, heads
+
+
+def _rotate_out_backward(ctx, grad):
+    *m, alpha, wigner, rowptr, eid, dst = ctx.saved_tensors
+    out = tece_rotate_out_backward(list(m), alpha, wigner, grad, dst, rowptr, eid, ctx.lmax, ctx.heads)
+    k = ctx.lmax + 1
+    return out[:k], out[k], out[k + 1], None, None, None, None, None
+
+
+tece_rotate_out.register_autograd(_rotate_out_backward, setup_context=_rotate_out_setup)

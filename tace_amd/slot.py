@@ -121,10 +121,23 @@ class HipTeceConvolution(TeceConvolution):
         if cutoff is not None:
             raise NotImplementedError("HipTeceConvolution: per-edge cutoff rescaling (apply_cutoff=False) is not "
                                       "on the MI355X path")
-        Nn, C, L = x.shape[0], self.C, self.lmax
+        Nn, C, L, H = x.shape[0], self.C, self.lmax, self.H
+        n = L + 1
         irreps = Irreps([(C, Irrep(l, (-1) ** l)) for l in range(L + 1)])
         x_lc = self.node_components(e3nn_to_gm(x.contiguous(), irreps))
-        plan = ops.EdgePlan.from_edge_index(edge_index, Nn)
+        # the kernels as registered custom operators (tace_amd.library), so
+        # the reference's make_fx / torch.export path traces this module
+        rowptr, eid = library.receiver_csr(edge_index, Nn)
         src, dst = edge_index[0], edge_index[1]
-        out = self.edges(x_lc, w, src, dst, plan, None, dst, wigner, radial_basis)
+        blocks = library.tece_rotate_in(x_lc, wigner, src, dst, w, L)
+        ms, md, mw = blocks[:n], blocks[n:2 * n], blocks[2 * n:]
+        key = self.key_proj.blocks(ms, self.mixing)
+        query = self.query_proj.blocks(md, self.mixing)
+        rp = self.radial_proj(radial_basis)
+        T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
+        score = library.tece_score(query, key, rp, (T * self.attention_scale).detach(), L, H)
+        alpha = library.tece_softmax(score, rowptr, eid)
+        o = library.tece_edge_ace(self._shared_input_gemms(mw), L, self.A)
+        m = self.linear_down.blocks(o, self.mixing)
+        out = library.tece_rotate_out(m, alpha, wigner, rowptr, eid, dst, L, H)
         return gm_to_e3nn(out, irreps)

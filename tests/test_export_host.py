@@ -52,3 +52,30 @@ def test_uuu_slot_traces_to_custom_ops():
     g = make_fx(fn, tracing_mode="symbolic")(torch.empty(N, 8 * 9, device="meta"))
     targets = [str(n.target) for n in g.graph.nodes if n.op == "call_function"]
     assert "tace_amd.uuu.default" in targets and "tace_amd.uuu_backward.default" in targets
+
+
+def test_tece_slot_traces_to_custom_ops():
+    """The TECE convolution slot: all its kernels trace as custom operators,
+    with their backward operators under a traced autograd.grad."""
+    lmax, C, H, A, nr = 2, 16, 2, 8, 8
+    conv = slot.HipTeceConvolution(lmax, lmax, C, H, True, A, None, nr, "w1", True, True, True).to("meta")
+    for prm in conv.parameters():
+        prm.requires_grad_(False)
+    N, E, K = 13, 57, (lmax + 1) ** 2
+
+    def fn(x, w, edge_index, wigner, R):
+        x = x.detach().requires_grad_(True)
+        w = w.detach().requires_grad_(True)
+        R = R.detach().requires_grad_(True)
+        out = conv(x, w, edge_index, None, wigner, wigner.transpose(1, 2), R)
+        return torch.autograd.grad((out * out).sum(), [x, w, R])
+
+    args = (torch.empty(N, K * C, device="meta"), torch.empty(E, conv.weight_numel, device="meta"),
+            torch.empty(2, E, dtype=torch.int64, device="meta"), torch.empty(E, K, K, device="meta"),
+            torch.empty(E, nr, device="meta"))
+    g = make_fx(fn, tracing_mode="symbolic", _allow_non_fake_inputs=True)(*args)
+    targets = {str(n.target) for n in g.graph.nodes if n.op == "call_function"}
+    for op in ("receiver_csr", "tece_rotate_in", "tece_score", "tece_softmax", "tece_edge_ace", "tece_rotate_out"):
+        assert f"tace_amd.{op}.default" in targets, op
+    for op in ("tece_rotate_in", "tece_score", "tece_softmax", "tece_edge_ace", "tece_rotate_out"):
+        assert f"tace_amd.{op}_backward.default" in targets, op

@@ -66,3 +66,48 @@ def test_exported_uuu_slot_with_gradient(cuda):
     other = torch.randn(35, 16 * 16, generator=g, dtype=torch.float64).to(cuda)
     for a, b in zip(ep.module()(other), fn(other)):
         assert ((a - b).abs().max() / b.abs().max()).item() < 1e-12
+
+
+def test_exported_tece_slot_with_gradients(cuda):
+    """The TECE convolution slot (frozen parameters, random weights) traced
+    with its gradients to x, the radial weights and the radial basis,
+    exported with dynamic node / edge counts and run on another graph."""
+    from oracle import tece as ot
+    lmax, C, H, A, nr = 2, 32, 2, 16, 8
+    K = (lmax + 1) ** 2
+    torch.manual_seed(3)
+    conv = slot.HipTeceConvolution(lmax, lmax, C, H, True, A, None, nr, "w1", True, True, True).double()
+    with torch.no_grad():
+        for prm in conv.parameters():
+            prm.copy_(0.5 * torch.randn_like(prm))
+    conv = conv.to(cuda)
+    for prm in conv.parameters():
+        prm.requires_grad_(False)
+
+    def fn(x, w, edge_index, wigner, R):
+        x = x.detach().requires_grad_(True)
+        w = w.detach().requires_grad_(True)
+        R = R.detach().requires_grad_(True)
+        out = conv(x, w, edge_index, None, wigner, wigner.transpose(1, 2), R)
+        gx, gw, gR = torch.autograd.grad((out * out).sum(), [x, w, R])
+        return out.detach(), gx, gw, gR
+
+    g = torch.Generator().manual_seed(4)
+
+    def graph(N, E):
+        x = torch.randn(N, K * C, generator=g, dtype=torch.float64).to(cuda)
+        w = torch.randn(E, conv.weight_numel, generator=g, dtype=torch.float64).to(cuda)
+        ei = torch.randint(0, N, (2, E), generator=g).to(cuda)
+        v = torch.randn(E, 3, generator=g, dtype=torch.float64)
+        W, _ = ot.edge_wigner(v / v.norm(dim=1, keepdim=True) * 2.0, lmax, lmax)
+        R = torch.randn(E, nr, generator=g, dtype=torch.float64).to(cuda)
+        return x, w, ei, W.to(cuda).contiguous(), R
+
+    sample = graph(30, 260)
+    traced = make_fx(fn, tracing_mode="symbolic", _allow_non_fake_inputs=True)(*sample)
+    n, e = torch.export.Dim("num_nodes", min=2), torch.export.Dim("num_edges", min=2)
+    ep = torch.export.export(traced, sample, dynamic_shapes=({0: n}, {0: e}, {1: e}, {0: e}, {0: e}), strict=False)
+    other = graph(47, 511)
+    for a, b in zip(ep.module()(*other), fn(*other)):
+        assert a.shape == b.shape
+        assert ((a - b).abs().max() / b.abs().max()).item() < 1e-10

@@ -16,6 +16,9 @@ needs from the operators in the ``fused_tp`` slots.
 * ``tace_amd::uuu(x1, x2, w, key, channels)``: the uuu product of
   ``uuuTensorProduct.fused_tp`` (``fused.py:90-95``), ``w`` the optional
   per-node path weights; backward ``tace_amd::uuu_backward``.
+* The uvu and uuu backward operators are differentiable themselves (double
+  backward for training with a force loss): their backward is written with
+  the forward and backward operators.
 * ``tace_amd::receiver_csr``, ``tece_rotate_in``, ``tece_score``,
   ``tece_softmax``, ``tece_edge_ace``, ``tece_rotate_out`` (each with a
   ``*_backward``): the kernels of the TECE convolution slot
@@ -77,6 +80,36 @@ def _uvu_backward(ctx, grad_out):
 uvu_scatter.register_autograd(_uvu_backward, setup_context=_uvu_setup)
 
 
+# Double backward (training with a force loss, create_graph=True).  The
+# product is trilinear in (x, y, w) and its backward (gx, gy, gw) is
+# multilinear in (x, y, w, g) with each output free of its own operand:
+# gx(y, w, g), gy(x, w, g), gw(x, y, g).  For upstream gradients (ax, ay, aw)
+# of (gx, gy, gw):
+#   d/dg = TP(ax, y, w) + TP(x, ay, w) + TP(x, y, aw)
+#   d/dx = gx-part of bwd(x, ay, w, g) + of bwd(x, y, aw, g)
+#   d/dy = gy-part of bwd(ax, y, w, g) + of bwd(x, y, aw, g)
+#   d/dw = gw-part of bwd(ax, y, w, g) + of bwd(x, ay, w, g)
+# -- the forward and backward operators again (themselves differentiable).
+def _uvu_bwd_setup(ctx, inputs, output):
+    x, y, w, edge_index, grad_out, key, channels = inputs
+    ctx.save_for_backward(x, y, w, edge_index, grad_out)
+    ctx.key, ctx.channels = key, channels
+
+
+def _uvu_bwd_backward(ctx, ax, ay, aw):
+    x, y, w, ei, g = ctx.saved_tensors
+    key, C = ctx.key, ctx.channels
+    zx, zy, zw = (a if a is not None else torch.zeros_like(t) for a, t in ((ax, x), (ay, y), (aw, w)))
+    gg = uvu_scatter(zx, y, w, ei, key, C) + uvu_scatter(x, zy, w, ei, key, C) + uvu_scatter(x, y, zw, ei, key, C)
+    bx = uvu_scatter_backward(zx, y, w, ei, g, key, C)   # (., gy, gw) with x -> ax
+    by = uvu_scatter_backward(x, zy, w, ei, g, key, C)   # (gx, ., gw) with y -> ay
+    bw = uvu_scatter_backward(x, y, zw, ei, g, key, C)   # (gx, gy, .) with w -> aw
+    return by[0] + bw[0], bx[1] + bw[1], bx[2] + by[2], None, gg, None, None
+
+
+uvu_scatter_backward.register_autograd(_uvu_bwd_backward, setup_context=_uvu_bwd_setup)
+
+
 # ------------------------------------------------------------------- uuu ----
 @torch.library.custom_op("tace_amd::uuu", mutates_args=(), device_types="cuda")
 def uuu(x1: Tensor, x2: Tensor, w: Optional[Tensor], key: str, channels: int) -> Tensor:
@@ -116,6 +149,38 @@ def _uuu_backward(ctx, grad_out):
 
 
 uuu.register_autograd(_uuu_backward, setup_context=_uuu_setup)
+
+
+# Double backward of the uuu product: (g1, g2, gw) are multilinear in
+# (x1, x2, w, g) with g1 free of x1, g2 free of x2 and gw free of w (the same
+# scheme as the uvu one above).  Identical inputs pass the same tensor twice;
+# autograd adds the two contributions.
+def _uuu_bwd_setup(ctx, inputs, output):
+    x1, x2, w, grad_out, key, channels = inputs
+    ctx.save_for_backward(x1, x2, w, grad_out)
+    ctx.key, ctx.channels, ctx.has_w = key, channels, w is not None
+
+
+def _uuu_bwd_backward(ctx, a1, a2, aw):
+    x1, x2, w, g = ctx.saved_tensors
+    key, C = ctx.key, ctx.channels
+    z1 = a1 if a1 is not None else torch.zeros_like(x1)
+    z2 = a2 if a2 is not None else torch.zeros_like(x2)
+    gg = uuu(z1, x2, w, key, C) + uuu(x1, z2, w, key, C)
+    b1 = uuu_backward(z1, x2, w, g, key, C)   # (., g2, gw) with x1 -> a1
+    b2 = uuu_backward(x1, z2, w, g, key, C)   # (g1, ., gw) with x2 -> a2
+    d1, d2 = b2[0], b1[1]
+    dw = None
+    if ctx.has_w:
+        dw = b1[2] + b2[2]
+        if aw is not None and aw.numel():
+            gg = gg + uuu(x1, x2, aw, key, C)
+            bw = uuu_backward(x1, x2, aw, g, key, C)
+            d1, d2 = d1 + bw[0], d2 + bw[1]
+    return d1, d2, dw, gg, None, None
+
+
+uuu_backward.register_autograd(_uuu_bwd_backward, setup_context=_uuu_bwd_setup)
 
 
 # ------------------------------------------------------------------ TECE ----

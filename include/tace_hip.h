@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 12
+#define TACE_HIP_ABI_VERSION 13
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -160,10 +160,11 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  * (tace/models/linear.py:377-482) on species-sorted, group-major node
  * features: every output block, species and instruction of one linear (or of
  * its input gradient) in one launch.  The work is a table of n_tiles output
- * tiles of tile x tile elements (tile = 128: float32 on MFMA; 64: float32 or
- * float64 on FMA), each inside one output block and one species' rows:
+ * tiles of tile_rows x tile_cols elements (128 x 128: float32 on MFMA;
+ * 64 x 64: float32 or float64 on FMA), each inside one output block and one
+ * species' rows:
  *   tiles    int64 [n_tiles, 8]: out_base (element offset of the tile's first
- *            row in y), rows (1..tile), n (block width = row stride), c0 (first
+ *            row in y), rows (1..tile_rows), n (block width = row stride), c0 (first
  *            column), bias_off (offset into bias, -1 none), cb, ce (its
  *            contributions [cb, ce)), unused;
  *   contribs int64 [*, 4]: x_base (offset of the tile's first row in x), k
@@ -176,9 +177,9 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
  * device memory and are trusted: the host builds them from the layout
  * (tace_amd.ops.SegLinearPlan) and checks every offset against the array
  * sizes before upload. */
-int tace_seg_linear(int dtype, int32_t tile, const void* x, void* y, const void* w, const void* bias,
-                    const int64_t* tiles, int64_t n_tiles, const int64_t* contribs, const double* scales,
-                    double alpha, void* stream);
+int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y, const void* w,
+                    const void* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
+                    const double* scales, double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"

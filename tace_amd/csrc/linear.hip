@@ -118,25 +118,28 @@ __global__ __launch_bounds__(256) void k_seg_linear(const T* __restrict__ x, T* 
   }
 }
 
-// float32 on MFMA: 128 x 128 tiles, 4 waves of 64 x 64 (4 x 4 blocks of
-// v_mfma_f32_16x16x4f32), in chunks of 32 k.  A stages through LDS
-// k-contiguous (As[row][k]); since the sum over k is order free, in MFMA step s
-// lane l supplies A[row][4 (l/16) + s] of a 16-k half, so it reads its four k
-// values of a fragment as one 16-byte LDS load.  B keeps the layout of its
-// source: k-contiguous (Bt[col][k], one 16-byte read per fragment) for the
-// input gradient, whose W^T rows are W's k-contiguous rows, and
-// column-contiguous (Bn[k][col], four 4-byte reads) for the forward, whose W
-// [k, n] rows run along the columns -- every global load is then a 16-byte
-// load from one base with constant offsets, and no staging store transposes.
-// The next chunk's global loads are issued before the current chunk's MFMAs
-// and land in registers, so memory latency overlaps the matrix work.  Tiles
-// are taken XCD-grouped: workgroup b runs tile (b % 8) * per + b / 8, so XCD k
-// works through a contiguous stretch of the table (the column tiles of one
-// row tile, the row tiles of one species' weight) and shares them in its L2.
-constexpr int MT = 128, MK = 32, MPAD = 4, NPAD = 4;
+// float32 on MFMA: 4 waves in a 2 x 2 grid, each owning WM x WN blocks of
+// 16 x 16 (v_mfma_f32_16x16x4f32), so a tile is (32 WM) x (32 WN); the
+// library runs 128 x 128 (4, 4) at 2 waves per SIMD.  (256 x 128 and 128 x 256
+// tiles halve the weight or input re-reads of config 4's linears but need
+// ~350 registers per lane, 1 wave per SIMD, and measured 12-20% slower.)  A stages through LDS k-contiguous (As[row][k]) in chunks of 32
+// k; since the sum over k is order free, in MFMA step s lane l supplies
+// A[row][4 (l/16) + s] of a 16-k half, so it reads its four k values of a
+// fragment as one 16-byte LDS load.  B keeps the layout of its source:
+// k-contiguous (Bt[col][k], one 16-byte read per fragment) for the input
+// gradient, whose W^T rows are W's k-contiguous rows, and column-contiguous
+// (Bn[k][col], four 4-byte reads) for the forward, whose W [k, n] rows run
+// along the columns -- every global load is a 16-byte load and no staging
+// store transposes.  The next chunk's global loads are issued before the
+// current chunk's MFMAs and land in registers, so memory latency overlaps the
+// matrix work.  Tiles are taken XCD-grouped: workgroup b runs tile (b % 8) *
+// per + b / 8, so XCD k works through a contiguous stretch of the table (the
+// column tiles of one row tile, the row tiles of one species' weight) and
+// shares them in its L2.
+constexpr int MK = 32, MPAD = 4, NPAD = 4;
 typedef float f4 __attribute__((ext_vector_type(4)));
 
-// one 16-byte load of p[0..3], or the in-bounds elements (ok[e]) and zeros
+// one 16-byte load of p[0..3], or the first lim (< 4) elements and zeros
 __device__ __forceinline__ f4 seg_ld4(const float* p, bool vec, bool any, int lim) {
   if (vec) return *(const f4*)p;
   f4 v = f4{0.f, 0.f, 0.f, 0.f};
@@ -148,39 +151,71 @@ __device__ __forceinline__ f4 seg_ld4(const float* p, bool vec, bool any, int li
   return v;
 }
 
-// A and W^T: thread -> row (or column) t/2, k k0 + 16 (t&1) .. +15 of a
-// k-contiguous matrix with `valid` rows and row stride k
-__device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k, int k0, bool valid, bool vec,
-                                           int t, f4* v) {
-  const int r = t >> 1, kk = k0 + (t & 1) * 16;
-  const float* p = base + (int64_t)r * k + kk;
+// R rows x 32 k of a k-contiguous matrix (row stride k, `nrows` valid rows):
+// thread t holds rows t/2 + 128 rr (rr < R/128), k k0 + 16 (t&1) .. +15 --
+// one base address per row, four 16-byte loads at constant offsets
+template <int R>
+__device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k, int k0, int nrows, bool vec, int t,
+                                           f4* v) {
+  const int kk = k0 + 16 * (t & 1);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int left = k - (kk + 4 * q);
-    v[q] = seg_ld4(p + 4 * q, valid && vec && left >= 4, valid && left > 0, left);
+  for (int rr = 0; rr < R / 128; ++rr) {
+    const int r = (t >> 1) + 128 * rr;
+    const float* p = base + (int64_t)r * k + kk;
+    const bool ok = r < nrows;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int left = k - (kk + 4 * q);
+      v[4 * rr + q] = seg_ld4(p + 4 * q, ok && vec && left >= 4, ok && left > 0, left);
+    }
   }
 }
 
-// W [k, n]: thread -> k row k0 + t%32, columns c0 + 4 (t/32) + 32 q .. +3
-__device__ __forceinline__ void seg_load_n(const float* __restrict__ wb, int k, int n, int c0, int k0, bool vec,
-                                           int t, f4* v) {
-  const int kk = k0 + (t & 31), cc = c0 + 4 * (t >> 5);
-  const float* p = wb + (int64_t)kk * n + cc;
+template <int R>
+__device__ __forceinline__ void seg_store_k(float* lds, int stride, int t, const f4* v, float sc) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int left = n - (cc + 32 * q);
-    v[q] = seg_ld4(p + 32 * q, kk < k && vec && left >= 4, kk < k && left > 0, left);
-  }
+  for (int rr = 0; rr < R / 128; ++rr)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *(f4*)&lds[((t >> 1) + 128 * rr) * stride + 16 * (t & 1) + 4 * q] = v[4 * rr + q] * sc;
 }
 
+// 32 k rows x Cn columns of W [k, n] (columns c0 ..): thread t holds k row
+// t % 32 and columns 4 (t/32) + 32 q + 128 cc (q < 4, cc < Cn/128)
+template <int Cn>
+__device__ __forceinline__ void seg_load_n(const float* __restrict__ wb, int k, int n, int c0, int k0, bool vec, int t,
+                                           f4* v) {
+  const int kk = k0 + (t & 31), cb = c0 + 4 * (t >> 5);
+  const float* p = wb + (int64_t)kk * n + cb;
+#pragma unroll
+  for (int cc = 0; cc < Cn / 128; ++cc)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int left = n - (cb + 32 * q + 128 * cc);
+      v[4 * cc + q] = seg_ld4(p + 32 * q + 128 * cc, kk < k && vec && left >= 4, kk < k && left > 0, left);
+    }
+}
+
+template <int Cn>
+__device__ __forceinline__ void seg_store_n(float* lds, int t, const f4* v, float sc) {
+#pragma unroll
+  for (int cc = 0; cc < Cn / 128; ++cc)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *(f4*)&lds[(t & 31) * (Cn + NPAD) + 4 * (t >> 5) + 32 * q + 128 * cc] = v[4 * cc + q] * sc;
+}
+
+template <int WM, int WN>
 __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict__ x, float* __restrict__ y,
                                                          const float* __restrict__ w, const float* __restrict__ bias,
                                                          const int64_t* __restrict__ tiles,
                                                          const int64_t* __restrict__ contribs,
                                                          const double* __restrict__ scales, float alpha,
                                                          int n_tiles, int per) {
-  __shared__ float As[MT][MK + MPAD];
-  __shared__ float Bs[MT * (MK + MPAD)];   // Bt[MT][MK + MPAD] or Bn[MK][MT + NPAD]
+  constexpr int TR = 32 * WM, TC = 32 * WN, BT = MK + MPAD;
+  constexpr int BS = (TC * BT > MK * (TC + NPAD)) ? TC * BT : MK * (TC + NPAD);
+  __shared__ float As[TR * BT];
+  __shared__ float Bs[BS];   // Bt[TC][MK + MPAD] or Bn[MK][TC + NPAD]
   const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
   if (tile >= n_tiles) return;
   const int64_t* td = tiles + 8 * (int64_t)tile;
@@ -189,16 +224,14 @@ __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict
   const int64_t bias_off = td[4];
   const int cb = (int)td[5], ce = (int)td[6];
   const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int wr = (wv >> 1) * 64, wc = (wv & 1) * 64;   // the wave's quadrant
-  const int fr = lane & 15, fg = lane >> 4;            // fragment row/col, k group
-  const int sr = t >> 1, sk = (t & 1) * 16;            // staging slot of A / Bt
-  const int nk = t & 31, nc = 4 * (t >> 5);            // staging slot of Bn
-  constexpr int BT = MK + MPAD, BN = MT + NPAD;
-  f4 acc[4][4];
+  const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 16 * WN;   // the wave's block of the tile
+  const int fr = lane & 15, fg = lane >> 4;                        // fragment row/col, k group
+  constexpr int NA = TR / 32, NB = TC / 32;   // f4 per thread per chunk
+  f4 acc[WM][WN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
 
   for (int c = cb; c < ce; ++c) {
     const int64_t* cd = contribs + 4 * (int64_t)c;
@@ -210,60 +243,53 @@ __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict
     const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
     const bool wvec = ((((uintptr_t)wb) & 15) == 0) && (((trans ? k : n) & 3) == 0) && ((c0 & 3) == 0);
     const float* __restrict__ wt = wb + (int64_t)c0 * k;   // W^T tile rows (trans)
-    const bool arow = sr < rows, brow = c0 + sr < n;
-    f4 a[4], b[4];
-    seg_load_k(xa, k, 0, arow, xvec, t, a);
-    if (trans) seg_load_k(wt, k, 0, brow, wvec, t, b);
-    else seg_load_n(wb, k, n, c0, 0, wvec, t, b);
+    f4 a[NA], b[NB];
+    seg_load_k<TR>(xa, k, 0, rows, xvec, t, a);
+    if (trans) seg_load_k<TC>(wt, k, 0, n - c0, wvec, t, b);
+    else seg_load_n<TC>(wb, k, n, c0, 0, wvec, t, b);
     for (int k0 = 0; k0 < k; k0 += MK) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) *(f4*)&As[sr][sk + 4 * q] = a[q];
-      if (trans) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) *(f4*)&Bs[sr * BT + sk + 4 * q] = b[q] * sc;
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) *(f4*)&Bs[nk * BN + nc + 32 * q] = b[q] * sc;
-      }
+      seg_store_k<TR>(As, BT, t, a, 1.f);
+      if (trans) seg_store_k<TC>(Bs, BT, t, b, sc);
+      else seg_store_n<TC>(Bs, t, b, sc);
       __syncthreads();
       if (k0 + MK < k) {   // next chunk in flight during this chunk's MFMAs
-        seg_load_k(xa, k, k0 + MK, arow, xvec, t, a);
-        if (trans) seg_load_k(wt, k, k0 + MK, brow, wvec, t, b);
-        else seg_load_n(wb, k, n, c0, k0 + MK, wvec, t, b);
+        seg_load_k<TR>(xa, k, k0 + MK, rows, xvec, t, a);
+        if (trans) seg_load_k<TC>(wt, k, k0 + MK, n - c0, wvec, t, b);
+        else seg_load_n<TC>(wb, k, n, c0, k0 + MK, wvec, t, b);
       }
 #pragma unroll
       for (int h = 0; h < MK; h += 16) {
-        f4 af[4], bf[4];
+        f4 af[WM], bf[WN];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *(const f4*)&As[wr + 16 * i + fr][h + 4 * fg];
+        for (int i = 0; i < WM; ++i) af[i] = *(const f4*)&As[(wr + 16 * i + fr) * BT + h + 4 * fg];
         if (trans) {
 #pragma unroll
-          for (int j = 0; j < 4; ++j) bf[j] = *(const f4*)&Bs[(wc + 16 * j + fr) * BT + h + 4 * fg];
+          for (int j = 0; j < WN; ++j) bf[j] = *(const f4*)&Bs[(wc + 16 * j + fr) * BT + h + 4 * fg];
         } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
+          for (int j = 0; j < WN; ++j)
 #pragma unroll
-            for (int s = 0; s < 4; ++s) bf[j][s] = Bs[(h + 4 * fg + s) * BN + wc + 16 * j + fr];
+            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = Bs[(h + 4 * fg + s2) * (TC + NPAD) + wc + 16 * j + fr];
         }
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
+        for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
+          for (int i = 0; i < WM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < WN; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s2], bf[j][s2], acc[i][j], 0, 0, 0);
       }
       __syncthreads();
     }
   }
   // D lane l, register q of block (i, j) = tile row wr + 16 i + 4 (l/16) + q, column wc + 16 j + l%16
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < WN; ++j) {
     const int col = c0 + wc + 16 * j + fr;
     if (col >= n) continue;
     const float bv = bias_off >= 0 ? bias[bias_off + col] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = wr + 16 * i + 4 * fg + q;
@@ -274,20 +300,23 @@ __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict
 
 }  // namespace
 
-extern "C" int tace_seg_linear(int dtype, int32_t tile, const void* x, void* y, const void* w, const void* bias,
-                               const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
-                               const double* scales, double alpha, void* stream) {
+extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y,
+                               const void* w, const void* bias, const int64_t* tiles, int64_t n_tiles,
+                               const int64_t* contribs, const double* scales, double alpha, void* stream) {
   if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear: bad tile count");
-  if (!((dtype == TACE_F32 && (tile == 128 || tile == 64)) || (dtype == TACE_F64 && tile == 64)))
-    return tace_fail_msg("tace_seg_linear: tile edge must be 128 or 64 (float32) or 64 (float64)");
+  const int tr = tile_rows, tc = tile_cols;
+  const bool mfma = dtype == TACE_F32 && tr == 128 && tc == 128;
+  if (!(mfma || ((dtype == TACE_F32 || dtype == TACE_F64) && tr == 64 && tc == 64)))
+    return tace_fail_msg("tace_seg_linear: tiles must be 128x128 (float32) or 64x64");
   if (n_tiles == 0) return 0;
   if (!x || !y || !w || !tiles || !contribs || !scales) return tace_fail_msg("tace_seg_linear: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)n_tiles), block(256);
-  if (dtype == TACE_F32 && tile == MT) {
+  if (mfma) {
     const int per = (int)((n_tiles + 7) / 8);
-    hipLaunchKernelGGL(k_seg_linear_mfma, dim3((unsigned)(8 * per)), block, 0, s, (const float*)x, (float*)y,
-                       (const float*)w, (const float*)bias, tiles, contribs, scales, (float)alpha, (int)n_tiles, per);
+    const dim3 g8((unsigned)(8 * per));
+    hipLaunchKernelGGL((k_seg_linear_mfma<4, 4>), g8, block, 0, s, (const float*)x, (float*)y, (const float*)w,
+                       (const float*)bias, tiles, contribs, scales, (float)alpha, (int)n_tiles, per);
   } else if (dtype == TACE_F32)
     hipLaunchKernelGGL(k_seg_linear<float>, grid, block, 0, s, (const float*)x, (float*)y, (const float*)w,
                        (const float*)bias, tiles, contribs, scales, (float)alpha);

@@ -154,7 +154,7 @@ class _LinearLayout:
         """``tace_seg_linear`` tables of the forward ("fwd": x -> out, bias
         added) or the input gradient ("bwd": g_out -> g_x, W^T) over species
         ranges ``rr`` of Z rows; the last few are cached."""
-        tile = SEG_LINEAR_TILE_F32 if x.dtype == torch.float32 else 64
+        tile = (128, 128) if x.dtype == torch.float32 and SEG_LINEAR_TILE_F32 == 128 else (64, 64)
         key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile)
         plan = self._seg.get(key)
         if plan is not None:

@@ -871,18 +871,19 @@ class SegLinearPlan:
     ranges: [(species or None, a, b)] node ranges (species-sorted rows; None =
     the shared weight).  w_stride / b_stride: elements per species of weight /
     bias.  x_numel / y_numel / w_numel / b_numel: sizes every offset is
-    checked against before the tables go to the device.  tile: the tile edge
-    (128: float32 MFMA kernel, 64: FMA kernel)."""
+    checked against before the tables go to the device.  tile: (rows, cols)
+    of the output tiles (float32 MFMA kernel: (128, 128); FMA kernel:
+    (64, 64))."""
 
     def __init__(self, Z, out_blocks, ins, ranges, w_stride, b_stride, x_numel, y_numel, w_numel, b_numel, device,
-                 tile: int = 64):
-        TM = tile
-        self.tile = tile
+                 tile: Tuple[int, int] = (64, 64)):
+        TM, TN = tile
+        self.tile = tuple(tile)
         tiles, contribs, scales = [], [], []
         nc = 0
         for ob, (s_o, n, d, boff) in enumerate(out_blocks):
             mine = [c for c in ins if c[0] == ob]
-            c0s = np.arange(0, n, TM, dtype=np.int64)
+            c0s = np.arange(0, n, TN, dtype=np.int64)
             for (sp, a, b) in ranges:
                 if b <= a:
                     continue
@@ -916,7 +917,7 @@ class SegLinearPlan:
         s = np.concatenate(scales) if scales else np.zeros(0, dtype=np.float64)
         # every access of every tile inside its array
         if len(t):
-            last_col = np.minimum(t[:, 3] + TM, t[:, 2])
+            last_col = np.minimum(t[:, 3] + TN, t[:, 2])
             if (t[:, 0] + (t[:, 1] - 1) * t[:, 2] + last_col).max() > y_numel:
                 raise ValueError("seg linear plan: output tile out of range")
             if (t[:, 4] >= 0).any() and (t[:, 4] + t[:, 2])[t[:, 4] >= 0].max() > b_numel:
@@ -949,7 +950,8 @@ def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional
         if bias.numel() != plan.b_numel:
             raise ValueError("seg linear: bias size differs from the plan's")
     tok = _t0("seg_linear")
-    N.check(N.lib().tace_seg_linear(N.dtype_code(dt), plan.tile, x.data_ptr(), y.data_ptr(), w.data_ptr(),
+    N.check(N.lib().tace_seg_linear(N.dtype_code(dt), plan.tile[0], plan.tile[1], x.data_ptr(), y.data_ptr(),
+                                    w.data_ptr(),
                                     None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(), plan.n_tiles,
                                     plan.contribs.data_ptr(), plan.scales.data_ptr(), float(alpha),
                                     N.stream_ptr(x.device)), "tace_seg_linear")

@@ -465,7 +465,9 @@ def _element_linear_reference(x, W, b, irreps_in, irreps_out, species, alpha):
 
 
 SEG_CASES = [("8x0e+5x0e+6x1o+4x1o+3x2e", "70x0e+6x1o+65x2e+2x3o", [0, 1, 17, 64, 65, 3, 130, 0]),
-             ("64x0e+36x0e+132x1o+20x2e", "260x0e+68x1o+40x2e", [140, 0, 3, 290, 1])]
+             ("64x0e+36x0e+132x1o+20x2e", "260x0e+68x1o+40x2e", [140, 0, 3, 290, 1]),
+             # long k into 256-wide blocks, and back (1100-wide gradient blocks)
+             ("1100x0e+300x1o", "256x0e+256x1o", [0, 300, 7, 129])]
 
 
 @pytest.mark.parametrize("dtype,tile", [(torch.float64, 64), (torch.float32, 128), (torch.float32, 64)])

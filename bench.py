@@ -57,6 +57,16 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         n, E, C, need_x = info
         return s * (E * (2 * var.npath * C + 2 * var.d2) + n * C * (var.d1 * (2 if need_x else 1) + var.dout)) \
             + 4 * (E + n + 1)
+    if name.startswith("edge_rtp_fwd"):
+        # h instead of w: x, y, h read (the last radial layer's 64 x W weights
+        # once), out written
+        n, E, C = info
+        return s * (E * (64 + var.d2) + n * C * (var.d1 + var.dout) + 64 * var.npath * C) + 4 * (E + n + 1)
+    if name.startswith("edge_rtp_bwd"):
+        # x, y, h, g_out read; g_w, g_y (and g_x) written
+        n, E, C, need_x = info
+        return s * (E * (64 + var.npath * C + 2 * var.d2) + n * C * (var.d1 * (2 if need_x else 1) + var.dout)
+                    + 64 * var.npath * C) + 4 * (E + n + 1)
     if name.startswith("uuu_fwd"):
         n, C = info
         return s * n * C * (var.d1 + var.d2 + var.dout)

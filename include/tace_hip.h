@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 13
+#define TACE_HIP_ABI_VERSION 14
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -96,6 +96,33 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
+
+/* The same product with the radial MLP's last layer folded in (float32):
+ * w[e, p*C + u] = alpha * sum_k h[e, k] w_last[k, p*C + u] -- the last
+ * mlpLinear of the radial network (tace/models/mlp.py:136-191) feeding the
+ * weights of the edge product (tace/models/_e3nn/fused.py:218-271) -- is made
+ * inside the kernel on MFMA and never stored.  h [E, 64] (the last hidden
+ * activations, 16-byte aligned), w_last [64, C*npath]; C a multiple of 64;
+ * slot_rows: n_edges int32 of scratch (the sender's feature row of every
+ * receiver-sorted slot, filled by the call); the other arguments and
+ * layouts as in tace_edge_tp_fwd.  out equals
+ * tace_edge_tp_fwd with w from that layer, up to the order in which each
+ * receiver's edges are summed (fixed: results repeat bit for bit). */
+int tace_edge_rtp_fwd(int vid, const float* x, const float* y, const float* h, const float* w_last, float alpha,
+                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, int32_t* slot_rows,
+                      float* out, void* stream);
+/* Gradients of sum(gout * out) as in tace_edge_tp_bwd: gy [E, d2], gw [E,
+ * C*npath] = grad of the per-edge weights w (the caller forms the h gradient
+ * as alpha * gw @ w_last^T), gx [N, C*d1] (NULL to skip); the weights are
+ * recomputed on MFMA.  `workspace` holds at least
+ * tace_edge_rtp_workspace_elems(vid, E, C, gx != NULL) floats. */
+int64_t tace_edge_rtp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx);
+int tace_edge_rtp_bwd(int vid, const float* x, const float* y, const float* h, const float* w_last, float alpha,
+                      const float* gout, const int32_t* rowptr, const int32_t* eid, const int32_t* src,
+                      const int32_t* node_map, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                      const int32_t* s_rowptr, const int32_t* s_slot, int32_t* slot_rows, float* workspace,
+                      int64_t workspace_elems, float* gx, float* gy, float* gw, void* stream);
 
 /* out[n] = uuu(x1[n], x2[n]); x1 [N, C*d1], x2 [N, C*d2], out [N, C*dout].
  * Weighted variants (the bilinear-gate products, second operand = hidden

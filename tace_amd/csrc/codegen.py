@@ -324,6 +324,374 @@ class Variant:
         L.append("}")
         return "\n".join(L)
 
+    # ------------------------------------------------- radial-fused uvu ----
+    # The same products with the radial MLP's last layer folded in: the
+    # per-edge weights w[e, p, u] = alpha sum_k h[e, k] Wl[k, p C + u] (64
+    # hidden features, fp32) are made on MFMA inside the kernel and never go
+    # through HBM.  A workgroup of 8 wavefronts owns 64 channels of one part
+    # and walks the 16-edge blocks of a range of receivers; its wavefronts
+    # split the work by unit, so matrix cores and vector ALUs run side by side
+    # on every SIMD:
+    #  * producers (wavefronts 0-3): wavefront v makes the weights of channels
+    #    16 v .. 16 v + 15 for the 16 edges of block k + 1
+    #    (v_mfma_f32_16x16x4f32; the B fragments of Wl stay in registers for
+    #    the workgroup's life) into an LDS tile [16][P][64], and stages the
+    #    block's y rows;
+    #  * consumers (wavefronts 4-7): wavefront 4 + v takes edges 4 v .. 4 v + 3
+    #    of block k with one lane per channel, as the unfused kernels do --
+    #    edge ids, senders and y are uniform over the wavefront, x rows are
+    #    read 256 bytes at a time (prefetched one block ahead) and the weights
+    #    come from the tile.
+    # Tiles are double-buffered: one barrier per block.  One part per in1
+    # block, with all of the block's paths, so a grad-x row block comes from
+    # one part.
+    def rtp_parts(self) -> List[int]:
+        return [b for b in range(len(self.in1)) if any(pb[0] == b for pb in self.path_blocks)]
+
+    def _rtp_signature(self, kind: str, q: int) -> List[str]:
+        if kind == "fwd":
+            return [f"template <bool IN1_GM, bool OUT_GM>\n__device__ __forceinline__ void f_{self.name}_rfwd{q}(",
+                    "    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ h,",
+                    "    const float* __restrict__ Wl, float alpha,",
+                    "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+                    "    const int* __restrict__ map, const int* __restrict__ srow, float* __restrict__ out,",
+                    "    int n_nodes, int C, int n_begin, int n_end, int c0, float* __restrict__ tile,",
+                    "    float* __restrict__ ytile, float* __restrict__ red) {"]
+        return [f"template <bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__device__ __forceinline__ void f_{self.name}_rbwd{q}(",
+                "    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ h,",
+                "    const float* __restrict__ Wl, float alpha, const float* __restrict__ gout,",
+                "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+                "    const int* __restrict__ map, const int* __restrict__ srow, float* __restrict__ cbuf,",
+                "    float* __restrict__ gy, float* __restrict__ gw, int n_nodes, int C, int n_begin, int n_end,",
+                "    int c0, float* __restrict__ tile, float* __restrict__ ytile) {"]
+
+    def _rtp_head(self, L: List[str], paths: Sequence[int]) -> None:
+        P = len(paths)
+        L += [f"  constexpr int RTP_ROW = {P * 64}, RTP_TILE = 16 * RTP_ROW;",
+              "  typedef float T;",
+              "  const int lane = (int)threadIdx.x & 63;",
+              "  const int wv = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);",
+              "  const bool prod = wv < 4;",
+              "  const int cw = prod ? wv : wv - 4;  // producer: channel group; consumer: edge group",
+              "  const int lrow = lane & 15, lgrp = lane >> 4;",
+              "  const int u = c0 + lane;  // consumer lane's channel",
+              "  const size_t N = (size_t)n_nodes;",
+              f"  const size_t WW = (size_t)C * {len(self.paths)};",
+              f"  float wf[{P}][16];",
+              "  if (prod) {"]
+        for pi, p in enumerate(paths):
+            L.append("#pragma unroll")
+            L.append(f"    for (int s = 0; s < 16; ++s) wf[{pi}][s] = "
+                     f"Wl[(size_t)(16 * lgrp + s) * WW + (size_t){p} * C + c0 + 16 * cw + lrow];")
+        L.append("  }")
+
+    def _rtp_load(self, L: List[str], cur: str, av: str, yv: str, ind: str) -> None:
+        """Producer: A fragment (h rows) and this thread's y value of block `cur`."""
+        L += [f"{ind}{{",
+              f"{ind}  const int ea = {cur}.b0 + lrow;",
+              f"{ind}  const bool oka = ea < {cur}.end;",
+              f"{ind}  rtp_a_frag(h, oka ? (eid ? eid[ea] : ea) : 0, oka, lgrp, {av});",
+              f"{ind}  const int t = (int)threadIdx.x, ey = {cur}.b0 + (t >> 4), jy = t & 15;",
+              f"{ind}  {yv} = ey < {cur}.end && jy < {self.D2} ? y[(size_t)(eid ? eid[ey] : ey) * {self.D2} + jy] : 0.0f;",
+              f"{ind}}}"]
+
+    def _rtp_produce(self, L: List[str], paths: Sequence[int], buf: str, av: str, yv: str, ind: str) -> None:
+        """Producer: weights of the block whose A fragment is `av` into tile
+        buffer `buf`; its y values (`yv`, one per thread) into ytile."""
+        P = len(paths)
+        L += [f"{ind}{{",
+              f"{ind}  float* __restrict__ tb = tile + ({buf}) * RTP_TILE;",
+              f"{ind}  ytile[({buf}) * 256 + (int)threadIdx.x] = {yv};",
+              f"{ind}  rtp_f4 acc[{P}];"]
+        for pi in range(P):
+            L.append(f"{ind}  acc[{pi}] = rtp_f4{{0.0f, 0.0f, 0.0f, 0.0f}};")
+        L.append("#pragma unroll")
+        L.append(f"{ind}  for (int s = 0; s < 16; ++s) {{")
+        for pi in range(P):
+            L.append(f"{ind}    acc[{pi}] = __builtin_amdgcn_mfma_f32_16x16x4f32({av}[s], wf[{pi}][s], acc[{pi}], 0, 0, 0);")
+        L.append(f"{ind}  }}")
+        L.append("#pragma unroll")
+        L.append(f"{ind}  for (int r = 0; r < 4; ++r) {{")
+        for pi in range(P):
+            L.append(f"{ind}    tb[(4 * lgrp + r) * RTP_ROW + {pi * 64} + 16 * cw + lrow] = alpha * acc[{pi}][r];")
+        L.append(f"{ind}  }}")
+        L.append(f"{ind}}}")
+
+    def _rtp_xload(self, L: List[str], b: int, cur: str, pre: str, ind: str, decl: bool) -> None:
+        """Consumer: x rows of its 4 edges of block `cur` into registers {pre}{rr}_{m}."""
+        for rr in range(4):
+            L.append(f"{ind}{{")
+            L.append(f"{ind}  const int e = {cur}.b0 + 4 * cw + {rr};")
+            L.append(f"{ind}  const int s = e < {cur}.end ? srow[e] : -1;")
+            for m in range(self.d1[b]):
+                L.append(f"{ind}  {pre}{rr}_{m} = s >= 0 ? {self._ld_x('s', b, m)} : T(0);")
+            L.append(f"{ind}}}")
+
+    def _rtp_edge_operands(self, L: List[str], b: int, paths: Sequence[int], rr: int) -> None:
+        used_y = sorted({self.off2[self.path_blocks[p][1]] + j for p in paths for (_, j, _, _) in self.cg[p]})
+        L += [f"          const int e = cur.b0 + 4 * cw + {rr};",
+              "          const int ed = eid ? eid[e] : e;"]
+        for m in range(self.d1[b]):
+            L.append(f"          const T x{b}_{m} = xc{rr}_{m};")
+        for j in used_y:
+            L.append(f"          const T y{j} = yb[(e - cur.b0) * 16 + {j}];")
+        L.append("          const float* __restrict__ wrow = tb + (e - cur.b0) * RTP_ROW + lane;")
+        for pi, p in enumerate(paths):
+            L.append(f"          const T w{p} = wrow[{pi * 64}];")
+
+    def _rtp_fwd_edge(self, L: List[str], paths: Sequence[int]) -> None:
+        for (b1, b2, ps, pairs) in self._block_pairs(paths):
+            o2 = self.off2[b2]
+            L.append("          {")
+            for (i, j) in pairs:
+                L.append(f"            const T q{i}_{j} = x{b1}_{i} * y{o2 + j};")
+            for p in ps:
+                byk = {}
+                for (i, j, k, c) in self.cg[p]:
+                    byk.setdefault(k, []).append((i, j, c))
+                for k in range(self.dout[p]):
+                    if k in byk:
+                        t = " + ".join(f"{_lit(c)} * q{i}_{j}" for i, j, c in byk[k])
+                        L.append(f"            a{self.offo[p] + k} += w{p} * ({t});")
+            L.append("          }")
+
+    def _rtp_bwd_edge(self, L: List[str], b: int, paths: Sequence[int]) -> None:
+        for m in range(self.d1[b]):
+            L.append(f"          T hx{b}_{m} = T(0);")
+        L += [f"          T hy{j} = T(0);" for j in range(16)]
+        for p in paths:
+            b1, b2 = self.path_blocks[p]
+            o, o2 = self.offo[p], self.off2[b2]
+            L.append("          {")
+            byjk, byik = {}, {}
+            for (i, j, k, c) in self.cg[p]:
+                byjk.setdefault((j, k), []).append((i, c))
+                byik.setdefault((i, k), []).append((j, c))
+            used_i = sorted({i for (i, j, k, c) in self.cg[p]})
+            L += [f"            T psi{i} = T(0);" for i in used_i]
+            for (j, k), ic in sorted(byjk.items()):
+                L.append(f"            {{ const T t = y{o2 + j} * g{o + k};")
+                L += [f"              psi{i} += {_lit(c)} * t;" for i, c in ic]
+                L.append("            }")
+            L.append(f"            __builtin_nontemporal_store("
+                     f"{' + '.join(f'x{b1}_{i} * psi{i}' for i in used_i)}, &gw[(size_t)ed * WW + (size_t){p} * C + u]);")
+            L.append("            if (NEED_GX) {")
+            L += [f"              hx{b1}_{i} += w{p} * psi{i};" for i in used_i]
+            L.append("            }")
+            used_k = sorted({k for (i, j, k, c) in self.cg[p]})
+            L += [f"            const T a{k} = w{p} * g{o + k};" for k in used_k]
+            for (i, k), jc in sorted(byik.items()):
+                L.append(f"            {{ const T z = x{b1}_{i} * a{k};")
+                L += [f"              hy{o2 + j} += {_lit(c)} * z;" for j, c in jc]
+                L.append("            }")
+            L.append("          }")
+        L.append("          if (NEED_GX) {")
+        L.append("            float* __restrict__ cb = cbuf + (size_t)e * DX;")
+        for m in range(self.d1[b]):
+            e3, gm = self._row_addr(b, m)
+            L.append(f"            __builtin_nontemporal_store(hx{b}_{m}, &cb[IN1_GM ? ({gm}) : ({e3})]);")
+        L.append("          }")
+        L.append("          const T v = reduce16_lanes(hy0, hy1, hy2, hy3, hy4, hy5, hy6, hy7, hy8, hy9, hy10, hy11, "
+                 "hy12, hy13, hy14, hy15);")
+        L.append("          const int jj = rev4(lane);")
+        L.append(f"          if (lane < 16 && jj < {self.D2}) gy[(size_t)ed * {self.D2} + jj] = v;")
+
+    def _rtp_out_store(self, L: List[str], paths: Sequence[int], ind: str, node: str, val) -> None:
+        accs = [self.offo[p] + k for p in paths for k in range(self.dout[p])]
+        for idx, k in enumerate(accs):
+            p = next(pp for pp in paths if self.offo[pp] <= k < self.offo[pp] + self.dout[pp])
+            e3, gm = self._addr("out", p, k - self.offo[p])
+            e3, gm = e3.replace("(size_t)n ", f"(size_t){node} "), gm.replace("(size_t)n ", f"(size_t){node} ")
+            L.append(f"{ind}out[OUT_GM ? ({gm}) : ({e3})] = {val(idx, k)};")
+
+    def _rtp_body(self, L: List[str], b: int, paths: Sequence[int], kind: str) -> None:
+        """Producer and consumer loops over the same block sequence, one
+        barrier per block in each (the wavefronts of a role never run the
+        other role's loop, so the two keep separate registers)."""
+        accs = [self.offo[p] + k for p in paths for k in range(self.dout[p])]
+        NA = len(accs)
+        red_sum = lambda idx, k: (f"rb[{idx} * 64 + lane] + rb[({NA} + {idx}) * 64 + lane] + "
+                                  f"rb[({2 * NA} + {idx}) * 64 + lane] + rb[({3 * NA} + {idx}) * 64 + lane]")
+        if kind == "fwd":
+            # receivers without edges: zeros (no block visits them)
+            L.append("  if (!prod) {")
+            L.append("    for (int n0 = n_begin + cw; n0 < n_end; n0 += 4) {")
+            L.append("      if (rowptr[n0] == rowptr[n0 + 1]) {")
+            L.append("        const int nz = map ? map[n0] : n0;")
+            self._rtp_out_store(L, paths, "        ", "nz", lambda idx, k: "0.0f")
+            L.append("      }")
+            L.append("    }")
+            L.append("  }")
+        L.append("  RtpCur cur;")
+        L.append("  if (!rtp_seek(cur, rowptr, n_begin, n_end)) return;")
+        L.append("  RtpCur nxt = cur;")
+        # ---- producers: the operands of block k + 2 are loaded while the
+        # MFMAs of block k + 1 run
+        L.append("  if (prod) {")
+        L.append("    float av[16], an[16], yv = 0.0f, yn = 0.0f;")
+        self._rtp_load(L, "cur", "av", "yv", "    ")
+        L.append("    bool m1 = rtp_next(nxt, rowptr, n_end);  // nxt = block 1")
+        L.append("    if (m1) {")
+        self._rtp_load(L, "nxt", "an", "yn", "      ")
+        L.append("    }")
+        self._rtp_produce(L, paths, "0", "av", "yv", "    ")
+        L.append("    __syncthreads();")
+        L.append("    for (int k = 0;; ++k) {")
+        L.append("      const bool more = m1;  // block k + 1 exists")
+        L.append("      if (more) {")
+        L.append("#pragma unroll")
+        L.append("        for (int s = 0; s < 16; ++s) av[s] = an[s];")
+        L.append("        yv = yn;")
+        L.append("        m1 = rtp_next(nxt, rowptr, n_end);  // nxt = block k + 2")
+        L.append("        if (m1) {")
+        self._rtp_load(L, "nxt", "an", "yn", "          ")
+        L.append("        }")
+        self._rtp_produce(L, paths, "(k + 1) & 1", "av", "yv", "        ")
+        L.append("      }")
+        L.append("      __syncthreads();")
+        L.append("      if (!more) break;")
+        L.append("    }")
+        L.append("    return;")
+        L.append("  }")
+        # ---- consumers
+        for rr in range(4):
+            for m in range(self.d1[b]):
+                L.append(f"  T xc{rr}_{m} = T(0), xn{rr}_{m} = T(0);")
+        self._rtp_xload(L, b, "cur", "xc", "  ", False)
+        if kind == "fwd":
+            L += [f"  T a{k} = T(0);" for k in accs]
+            L.append("  int rp = 0, pend_n = -1;  // receiver whose 4 partial sums wait in red[rp ^ 1]")
+        else:
+            for p in paths:
+                for k in range(self.dout[p]):
+                    L.append(f"  T g{self.offo[p] + k} = T(0);")
+        L.append("  __syncthreads();")
+        L.append("  for (int k = 0;; ++k) {")
+        L.append("    const bool more = rtp_next(nxt, rowptr, n_end);  // nxt = block k + 1")
+        L.append("    const float* __restrict__ tb = tile + (k & 1) * RTP_TILE;")
+        L.append("    const float* __restrict__ yb = ytile + (k & 1) * 256;")
+        L.append("    const int n = map ? map[cur.n0] : cur.n0;  // feature row of the receiver")
+        if kind == "fwd":
+            # the previous receiver's totals, summed in a fixed order
+            L.append("    if (pend_n >= 0) {")
+            L.append("      const float* __restrict__ rb = red + (rp ^ 1) * " + str(4 * NA * 64) + ";")
+            L.append("      if (cw == 0) {")
+            self._rtp_out_store(L, paths, "        ", "pend_n", red_sum)
+            L.append("      }")
+            L.append("      pend_n = -1;")
+            L.append("    }")
+        else:
+            L.append("    if (cur.b0 == cur.beg) {  // first block of the receiver: its output gradient")
+            for p in paths:
+                for k in range(self.dout[p]):
+                    e3, gm = self._addr("out", p, k)
+                    L.append(f"      g{self.offo[p] + k} = gout[OUT_GM ? ({gm}) : ({e3})];")
+            L.append("    }")
+        L.append("    if (more) {")
+        self._rtp_xload(L, b, "nxt", "xn", "      ", False)
+        L.append("    }")
+        for rr in range(4):
+            L.append(f"    if (cur.b0 + 4 * cw + {rr} < cur.end) {{")
+            L.append("        {")
+            self._rtp_edge_operands(L, b, paths, rr)
+            if kind == "fwd":
+                self._rtp_fwd_edge(L, paths)
+            else:
+                self._rtp_bwd_edge(L, b, paths)
+            L.append("        }")
+            L.append("    }")
+        if kind == "fwd":
+            L.append("    if (cur.b0 + 16 >= cur.end) {  // last block of the receiver: partial sums -> red")
+            L.append("      float* __restrict__ rb = red + rp * " + str(4 * NA * 64) + ";")
+            for idx, k in enumerate(accs):
+                L.append(f"      rb[({NA} * cw + {idx}) * 64 + lane] = a{k};")
+                L.append(f"      a{k} = T(0);")
+            L.append("      pend_n = n;")
+            L.append("      rp ^= 1;")
+            L.append("    }")
+        for rr in range(4):
+            for m in range(self.d1[b]):
+                L.append(f"    xc{rr}_{m} = xn{rr}_{m};")
+        L.append("    __syncthreads();")
+        L.append("    if (!more) break;")
+        L.append("    cur = nxt;")
+        L.append("  }")
+        if kind == "fwd":
+            L.append("  if (pend_n >= 0 && cw == 0) {")
+            L.append("    const float* __restrict__ rb = red + (rp ^ 1) * " + str(4 * NA * 64) + ";")
+            self._rtp_out_store(L, paths, "    ", "pend_n", red_sum)
+            L.append("  }")
+
+    def emit_rtp_fwd(self, b: int) -> str:
+        paths = self._part_paths([b])
+        L = self._rtp_signature("fwd", self.rtp_parts().index(b))
+        self._rtp_head(L, paths)
+        self._rtp_body(L, b, paths, "fwd")
+        L.append("}")
+        return "\n".join(L)
+
+    def emit_rtp_bwd(self, b: int) -> str:
+        """Part of in1 block b: per edge e (slot of receiver n), channel u and
+        path p, with g = grad of out[n] and w from the MFMA tile,
+          psi_i = sum_{j,k} c^p_ijk y_j g_pk,  gw_p = sum_i x_i psi_i,
+          hx_i += w_p psi_i  (-> cbuf row of slot e),
+          hy_j += sum_{i,k} c^p_ijk x_i (w_p g_pk)  (summed over the
+        wavefront's 64 channels into this slot's grad_y partial)."""
+        paths = self._part_paths([b])
+        L = self._rtp_signature("bwd", self.rtp_parts().index(b))
+        self._rtp_head(L, paths)
+        L.append(f"  const size_t DX = (size_t)C * {self.D1};")
+        self._rtp_body(L, b, paths, "bwd")
+        L.append("}")
+        return "\n".join(L)
+
+    def _rtp_lds(self) -> Tuple[int, int]:
+        """(tile floats, red floats) of the largest part: two tile buffers; two
+        buffers of the 4 consumers' partial sums."""
+        tiles, reds = [], []
+        for b in self.rtp_parts():
+            ps = self._part_paths([b])
+            tiles.append(2 * 16 * 64 * len(ps))
+            reds.append(2 * 4 * 64 * sum(self.dout[p] for p in ps))
+        return max(tiles), max(reds)
+
+    def emit_rtp_wrappers(self) -> str:
+        parts = self.rtp_parts()
+        nq = len(parts)
+        nt, nr = self._rtp_lds()
+        a_f = "x, y, h, Wl, alpha, rowptr, eid, src, map, srow, out, n_nodes, C, nb, ne, c0, tile, ytile, red"
+        a_b = "x, y, h, Wl, alpha, gout, rowptr, eid, src, map, srow, cbuf, gy, gw, n_nodes, C, nb, ne, c0, tile, ytile"
+        head = ["  int ph, nb, ne;",
+                f"  if (!rtp_slot(n_nodes, {nq} * (C >> 6), per_range, &ph, &nb, &ne)) return;",
+                f"  const int q = ph % {nq}, c0 = (ph / {nq}) * 64;"]
+        L = [f"template <bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) RTP_OCC void k_{self.name}_rfwd(",
+             "    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ h,",
+             "    const float* __restrict__ Wl, float alpha,",
+             "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+             "    const int* __restrict__ map, const int* __restrict__ srow, float* __restrict__ out, int n_nodes,",
+             "    int C, int per_range) {",
+             f"  __shared__ float tile[{nt}];",
+             "  __shared__ float ytile[512];",
+             f"  __shared__ float red[{nr}];"]
+        L += head
+        for qq in range(nq):
+            L.append(f"  {'if' if qq == 0 else 'else if'} (q == {qq}) f_{self.name}_rfwd{qq}<IN1_GM, OUT_GM>({a_f});")
+        L.append("}")
+        L += [f"template <bool NEED_GX, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) RTP_OCC void k_{self.name}_rbwd(",
+              "    const float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ h,",
+              "    const float* __restrict__ Wl, float alpha, const float* __restrict__ gout,",
+              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
+              "    const int* __restrict__ map, const int* __restrict__ srow, float* __restrict__ cbuf,",
+              "    float* __restrict__ gyp, float* __restrict__ gw, int n_nodes, int n_edges, int C, int per_range) {",
+              f"  __shared__ float tile[{nt}];",
+              "  __shared__ float ytile[512];"]
+        L += head
+        L.append(f"  float* __restrict__ gy = gyp + (size_t)ph * n_edges * {self.D2};")
+        for qq in range(nq):
+            L.append(f"  {'if' if qq == 0 else 'else if'} (q == {qq}) f_{self.name}_rbwd{qq}<NEED_GX, IN1_GM, OUT_GM>({a_b});")
+        L.append("}")
+        return "\n".join(L)
+
     def _row_addr(self, b: int, m: int) -> Tuple[str, str]:
         """Position of (block b, component m, channel u) inside one grad-x row
         of C*D1 values: e3nn order, or group-major order within the row (each
@@ -474,8 +842,10 @@ class Variant:
     def emit(self) -> str:
         if self.kind == "uvu":
             nq = len(self.parts())
+            rp = self.rtp_parts()
             return "\n\n".join([self.emit_uvu_fwd(q) for q in range(nq)] + [self.emit_uvu_bwd(q) for q in range(nq)]
-                               + [self.emit_uvu_wrappers()])
+                               + [self.emit_uvu_wrappers()] + [self.emit_rtp_fwd(b) for b in rp]
+                               + [self.emit_rtp_bwd(b) for b in rp] + [self.emit_rtp_wrappers()])
         return self.emit_uuu_fwd() + "\n\n" + self.emit_uuu_bwd()
 
 
@@ -610,6 +980,10 @@ _UVU_FWD_SIG = ("const void*, const void*, const void*, const int*, const int*, 
                 "int, hipStream_t")
 _UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, const int*, "
                 "void*, void*, void*, int, int, int, int, hipStream_t")
+_RTP_FWD_SIG = ("const float*, const float*, const float*, const float*, float, const int*, const int*, const int*, "
+                "const int*, const int*, float*, int, int, int, int, hipStream_t")
+_RTP_BWD_SIG = ("const float*, const float*, const float*, const float*, float, const float*, const int*, const int*, "
+                "const int*, const int*, const int*, float*, float*, float*, int, int, int, int, int, hipStream_t")
 _UUU_FWD_SIG = "const void*, const void*, const void*, void*, int, int, int, hipStream_t"
 _UUU_BWD_SIG = "const void*, const void*, const void*, const void*, void*, void*, void*, int, int, int, hipStream_t"
 _TYPEDEFS = [
@@ -617,6 +991,8 @@ _TYPEDEFS = [
     f"typedef void (*UvuBwd)({_UVU_BWD_SIG});",
     f"typedef void (*UuuFwd)({_UUU_FWD_SIG});",
     f"typedef void (*UuuBwd)({_UUU_BWD_SIG});",
+    f"typedef void (*RtpFwd)({_RTP_FWD_SIG});",
+    f"typedef void (*RtpBwd)({_RTP_BWD_SIG});",
 ]
 
 
@@ -650,6 +1026,24 @@ def _launchers(v: Variant) -> List[str]:
                 for gx in (True, False):
                     out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, E, C);")
             out.append("}")
+            if tag == "f":
+                # radial-fused kernels (float32 only): grid from rtp_slot, 4 wavefronts of 16 channels
+                nq = len(v.rtp_parts())
+                launch = (f"const int nph = {nq} * (C / 64), nr = (n + per_range - 1) / per_range; "
+                          "const dim3 g((unsigned)(8 * ((nr + 7) / 8) * nph)), b(512);")
+                out.append(f"void L_{v.name}_rfwd(const float* x, const float* y, const float* h, const float* Wl, float alpha, const int* rp, const int* eid, const int* src, const int* map, const int* srow, float* o, int n, int flags, int C, int per_range, hipStream_t s) {{")
+                out.append("  if (n <= 0) return;")
+                out.append("  " + launch)
+                for f in range(4):
+                    out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_rfwd<{_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, x, y, h, Wl, alpha, rp, eid, src, map, srow, o, n, C, per_range);")
+                out.append("}")
+                out.append(f"void L_{v.name}_rbwd(const float* x, const float* y, const float* h, const float* Wl, float alpha, const float* go, const int* rp, const int* eid, const int* src, const int* map, const int* srow, float* cb, float* gy, float* gw, int n, int E, int flags, int C, int per_range, hipStream_t s) {{")
+                out.append("  if (n <= 0) return;")
+                out.append("  " + launch)
+                for f in range(4):
+                    for gx in (True, False):
+                        out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_rbwd<{_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, x, y, h, Wl, alpha, go, rp, eid, src, map, srow, cb, gy, gw, n, E, C, per_range);")
+                out.append("}")
         else:
             out.append(f"void L_{v.name}_fwd_{tag}(const void* x1, const void* x2, const void* w, void* o, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
@@ -688,11 +1082,14 @@ def emit_all(gen_dir: str) -> List[str]:
            "  int nparts;                     // uvu: part kernels per launch = grad_y partials",
            "  int nseg; int seg[8][2];        // group-major grad-x row segments (offset / C, length / C)",
            "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
-           "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;", "};"]
+           "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;",
+           "  int rnparts;                    // uvu: radial-fused parts (grad_y partials: rnparts * C / 64)",
+           "  RtpFwd rfwd; RtpBwd rbwd;       // uvu: radial-fused kernels (float32)", "};"]
     for v in vs:
         if v.kind == "uvu":
             reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
                     (("fwd", _UVU_FWD_SIG), ("bwd", _UVU_BWD_SIG)) for t in ("f", "d")]
+            reg += [f"void L_{v.name}_rfwd({_RTP_FWD_SIG});", f"void L_{v.name}_rbwd({_RTP_BWD_SIG});"]
         else:
             reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
                     (("fwd", _UUU_FWD_SIG), ("bwd", _UUU_BWD_SIG)) for t in ("f", "d")]
@@ -706,10 +1103,11 @@ def emit_all(gen_dir: str) -> List[str]:
                 f"{int(v.weighted)}")
         if v.kind == "uvu":
             reg.append(f"  {{{head}, {len(v.parts())}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
-                       f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr}},")
+                       f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr, {len(v.rtp_parts())}, L_{n}_rfwd, "
+                       f"L_{n}_rbwd}},")
         else:
             reg.append(f"  {{{head}, 0, 0, {seg}, nullptr, nullptr, nullptr, nullptr, "
-                       f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d}},")
+                       f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d, 0, nullptr, nullptr}},")
     reg.append("};")
     reg.append(f"static const int kNumVariants = {len(vs)};")
     _write(os.path.join(gen_dir, "registry.inc"), reg)

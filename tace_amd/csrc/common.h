@@ -62,3 +62,85 @@ __device__ __forceinline__ int tp_part_node(int n_nodes, int nparts, int* q) {
   const int n = (int)(blockIdx.x & 7) * per + i / nparts;
   return n < n_nodes ? n : -1;
 }
+
+// Work of one persistent workgroup of the radial-fused tensor products: slot
+// `ph` (part x channel quarter-block) and receivers [*n_begin, *n_end).  The
+// grid is 8 * rpx * nph workgroups: XCD k takes the contiguous receiver ranges
+// k*rpx .. k*rpx+rpx-1 of `per_range` receivers and, for each range, its nph
+// slots in consecutive workgroups, so the range's senders are read into that
+// XCD's L2 once for all slots.  Returns false for padding workgroups (the
+// decision is uniform over the workgroup).
+__device__ __forceinline__ bool rtp_slot(int n_nodes, int nph, int per_range, int* ph, int* n_begin, int* n_end) {
+  const int rpx = (int)(gridDim.x >> 3) / nph;
+  const int i = (int)(blockIdx.x >> 3);
+  *ph = i % nph;
+  const int64_t b = ((int64_t)(blockIdx.x & 7) * rpx + i / nph) * per_range;
+  if (b >= n_nodes) return false;
+  *n_begin = (int)b;
+  *n_end = (int)(b + per_range < n_nodes ? b + per_range : n_nodes);
+  return true;
+}
+
+// Cursor over the 16-edge blocks of a workgroup's receivers (receivers
+// without edges have no blocks).  Uniform over the workgroup.
+struct RtpCur {
+  int n0, beg, end, b0;
+};
+
+// first block at receiver >= n0; false (cursor unchanged) if there is none
+__device__ __forceinline__ bool rtp_seek(RtpCur& c, const int* __restrict__ rowptr, int n0, int n_end) {
+  for (; n0 < n_end; ++n0) {
+    const int b = rowptr[n0], e = rowptr[n0 + 1];
+    if (e > b) {
+      c.n0 = n0;
+      c.beg = b;
+      c.end = e;
+      c.b0 = b;
+      return true;
+    }
+  }
+  return false;
+}
+
+// the block after c; false (cursor unchanged) at the end of the range
+__device__ __forceinline__ bool rtp_next(RtpCur& c, const int* __restrict__ rowptr, int n_end) {
+  if (c.b0 + 16 < c.end) {
+    c.b0 += 16;
+    return true;
+  }
+  return rtp_seek(c, rowptr, c.n0 + 1, n_end);
+}
+
+typedef float rtp_f4 __attribute__((ext_vector_type(4)));
+#ifndef RTP_OCC
+#define RTP_OCC __attribute__((amdgpu_waves_per_eu(2, 2)))
+#endif
+
+// A fragment of the radial-layer MFMA (v_mfma_f32_16x16x4f32, k permuted so
+// that lane group g of k-step s holds k = 16 g + s): h[row][16 g .. 16 g + 15]
+// of the edge in row (64 hidden features per edge), zeros for rows past the
+// receiver's edges.
+__device__ __forceinline__ void rtp_a_frag(const float* __restrict__ h, int ed, bool ok, int g, float* a) {
+  if (ok) {
+    const rtp_f4* hp = reinterpret_cast<const rtp_f4*>(h + (size_t)ed * 64 + 16 * g);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const rtp_f4 t = hp[v];
+      a[4 * v] = t[0]; a[4 * v + 1] = t[1]; a[4 * v + 2] = t[2]; a[4 * v + 3] = t[3];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < 16; ++s) a[s] = 0.0f;
+  }
+}
+
+// Sum of 16 per-lane values over each 16-lane row of the wavefront (15
+// shuffles): lane l returns the row total of component rev4(l & 15).
+__device__ __forceinline__ float reduce16_row(float* v) {
+  const int lane = (int)threadIdx.x & 63;
+  tr_step<float, 8>(v, lane, 1);
+  tr_step<float, 4>(v, lane, 2);
+  tr_step<float, 2>(v, lane, 4);
+  tr_step<float, 1>(v, lane, 8);
+  return v[0];
+}

@@ -777,6 +777,119 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
   return check_launch("tace_edge_tp_bwd");
 }
 
+// ---------------------------------------------- radial-fused edge products --
+// Receivers per persistent workgroup: about 2048 workgroups in all (8 per CU
+// over the launch), at least one receiver each.
+static int rtp_per_range(int64_t n_nodes, int nph) {
+  const int64_t ranges = 2048 / nph > 8 ? 2048 / nph : 8;
+  const int64_t per = (n_nodes + ranges - 1) / ranges;
+  return per > 0 ? (int)per : 1;
+}
+
+// slot_rows[k] = feature row of the sender of receiver-sorted slot k
+__global__ __launch_bounds__(256) void k_slot_rows(const int32_t* __restrict__ eid, const int32_t* __restrict__ src,
+                                                   const int32_t* __restrict__ node_map, int64_t E,
+                                                   int32_t* __restrict__ out) {
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= E) return;
+  const int32_t s = src[eid ? eid[k] : k];
+  out[k] = node_map ? node_map[s] : s;
+}
+
+static void launch_slot_rows(const int32_t* eid, const int32_t* src, const int32_t* node_map, int64_t E, int32_t* out,
+                             hipStream_t s) {
+  if (E > 0)
+    hipLaunchKernelGGL(k_slot_rows, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s, eid, src, node_map, E, out);
+}
+
+static int rtp_checks(const char* who, int vid, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                      const float* h) {
+  char msg[200];
+  if (tp_common_checks(who, vid, n_nodes, n_edges, channels, layout)) return -1;
+  if (!kVariants[vid].rfwd) {
+    snprintf(msg, sizeof(msg), "%s: variant %s has no radial-fused kernels", who, kVariants[vid].key);
+    return fail(msg);
+  }
+  if (channels % 64 != 0) {
+    snprintf(msg, sizeof(msg), "%s: channels must be a multiple of 64 (got %d)", who, (int)channels);
+    return fail(msg);
+  }
+  if (((uintptr_t)h & 15) != 0) {
+    snprintf(msg, sizeof(msg), "%s: h must be 16-byte aligned", who);
+    return fail(msg);
+  }
+  return 0;
+}
+
+int tace_edge_rtp_fwd(int vid, const float* x, const float* y, const float* h, const float* w_last, float alpha,
+                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, int32_t* slot_rows,
+                      float* out, void* stream) {
+  if (rtp_checks("tace_edge_rtp_fwd", vid, n_nodes, n_edges, channels, layout, h)) return -1;
+  if ((!out && n_nodes) || !rowptr || !w_last || (n_edges && (!x || !y || !h || !src || !slot_rows)))
+    return fail("tace_edge_rtp_fwd: null pointer");
+  const TpVariant& v = kVariants[vid];
+  const int nph = v.rnparts * (channels / 64);
+  hipStream_t s = (hipStream_t)stream;
+  launch_slot_rows(eid, src, node_map, n_edges, slot_rows, s);
+  v.rfwd(x, y, h, w_last, alpha, rowptr, eid, src, node_map, slot_rows, out, (int)n_nodes, layout, channels,
+         rtp_per_range(n_nodes, nph), s);
+  return check_launch("tace_edge_rtp_fwd");
+}
+
+int64_t tace_edge_rtp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0 || !kVariants[vid].rfwd)
+    return fail("tace_edge_rtp_workspace_elems: bad variant id");
+  if (n_edges < 0 || channels <= 0 || channels % 64 != 0) return fail("tace_edge_rtp_workspace_elems: bad sizes");
+  const TpVariant& v = kVariants[vid];
+  const int64_t nph = (int64_t)v.rnparts * (channels / 64);
+  int64_t n = need_gx ? n_edges * (int64_t)channels * v.d1 : 0;
+  if (nph > 1) n += nph * n_edges * v.d2;
+  return n;
+}
+
+int tace_edge_rtp_bwd(int vid, const float* x, const float* y, const float* h, const float* w_last, float alpha,
+                      const float* gout, const int32_t* rowptr, const int32_t* eid, const int32_t* src,
+                      const int32_t* node_map, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                      const int32_t* s_rowptr, const int32_t* s_slot, int32_t* slot_rows, float* workspace,
+                      int64_t workspace_elems, float* gx, float* gy, float* gw, void* stream) {
+  if (rtp_checks("tace_edge_rtp_bwd", vid, n_nodes, n_edges, channels, layout, h)) return -1;
+  if (!rowptr || !w_last || (n_edges && (!x || !y || !h || !gout || !src || !gy || !gw || !slot_rows)))
+    return fail("tace_edge_rtp_bwd: null pointer");
+  const TpVariant& v = kVariants[vid];
+  const int nph = v.rnparts * (channels / 64);
+  const int64_t row = (int64_t)channels * v.d1;
+  const int64_t cb_elems = gx ? n_edges * row : 0;
+  const int64_t need = cb_elems + (nph > 1 ? (int64_t)nph * n_edges * v.d2 : 0);
+  if (gx && !s_rowptr) return fail("tace_edge_rtp_bwd: grad_x needs the sender CSR");
+  if (n_edges && ((gx && !s_slot) || (need && !workspace)))
+    return fail("tace_edge_rtp_bwd: null sender CSR or workspace");
+  if (workspace_elems < need) return fail("tace_edge_rtp_bwd: workspace smaller than tace_edge_rtp_workspace_elems()");
+  RowSegs sg;
+  memset(&sg, 0, sizeof(sg));
+  if (layout & TACE_LAYOUT_IN1_GROUPED) {
+    sg.n = v.nseg;
+    for (int g = 0; g < v.nseg; ++g) {
+      sg.off[g] = (int64_t)v.seg[g][0] * channels;
+      sg.len[g] = (int64_t)v.seg[g][1] * channels;
+    }
+  }
+  hipStream_t s = (hipStream_t)stream;
+  // workspace = [grad_x rows of every slot | grad_y partial of every (part, 64 channels)]
+  float* cbuf = gx && n_edges ? workspace : nullptr;
+  float* gyp = nph > 1 ? workspace + cb_elems : gy;
+  const int64_t ny = n_edges * v.d2;
+  launch_slot_rows(eid, src, node_map, n_edges, slot_rows, s);
+  v.rbwd(x, y, h, w_last, alpha, gout, rowptr, eid, src, node_map, slot_rows, cbuf, gyp, gw, (int)n_nodes,
+         (int)n_edges, layout, channels, rtp_per_range(n_nodes, nph), s);
+  if (nph > 1 && ny)
+    hipLaunchKernelGGL(k_sum_parts<float>, dim3((unsigned)((ny + 255) / 256)), dim3(256), 0, s, (const float*)gyp,
+                       nph, ny, gy);
+  if (gx && n_nodes)
+    launch_seg_rowsum<float>(cbuf, s_rowptr, s_slot, node_map, gx, (int)n_nodes, row, sg, channels, s);
+  return check_launch("tace_edge_rtp_bwd");
+}
+
 static bool uuu_layout_ok(int32_t layout) {
   return layout == 0 || layout == TACE_LAYOUT_OUT_GROUPED ||
          layout == (TACE_LAYOUT_IN1_GROUPED | TACE_LAYOUT_OUT_GROUPED) ||

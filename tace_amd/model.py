@@ -113,6 +113,15 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 # per-species linears over at least this many species ranges run as one
 # segmented-GEMM launch (tace_seg_linear); fewer, larger ranges stay one
 # library GEMM per instruction and species
+# the interaction's radial last layer inside the edge-product kernels
+# (ops.edge_rtp_scatter; float32, C % 64 == 0).  Off: on the 12k-atom water
+# box the fused kernels take 12.6 ms (forward) and 23.3 ms (backward) per
+# layer against 8.2 ms and 8.5 ms for the last layer's own MFMA kernel plus
+# the product kernels -- the weight slice each wavefront keeps for its MFMAs
+# (112 registers at 7 paths) leaves the product math 1-2 wavefronts per SIMD,
+# too few to keep the vector ALUs busy.
+RADIAL_FUSED_TP = False
+
 SEG_LINEAR_MIN_RANGES = 3
 # tile edge of the float32 segmented GEMM: 128 = MFMA kernel, 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128
@@ -315,9 +324,19 @@ class MLP(torch.nn.Module):
     def forward(self, x):
         if not self.fused:
             return self.mlp(x)
+        return ops.radial_mlp_out(self.hidden(x), *self.last_layer())
+
+    def hidden(self, x):
+        """The last hidden activations [E, 64] (fused MLPs only)."""
         lins = [m for m in self.mlp if isinstance(m, mlpLinear)]
-        h = ops.radial_mlp_hidden(x, [m.weight * m.alpha for m in lins[:-1]])
-        return ops.radial_mlp_out(h, lins[-1].weight, lins[-1].alpha)
+        return ops.radial_mlp_hidden(x, [m.weight * m.alpha for m in lins[:-1]])
+
+    def last_layer(self):
+        """(weight [64, n_out], alpha) of the last linear layer: the MLP's
+        output is alpha * hidden(x) @ weight.  The weight is a constant here,
+        as in ``forward``: gradients flow to the hidden activations only."""
+        last = [m for m in self.mlp if isinstance(m, mlpLinear)][-1]
+        return last.weight.detach(), float(last.alpha)
 
 
 # ------------------------------------------------------------------ blocks ----
@@ -340,6 +359,11 @@ class O3ScatterTensorProduct(torch.nn.Module):
 
     def forward(self, x, y, w, plan: ops.EdgePlan, layout: int = 0, node_map=None):
         return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C, layout, node_map)
+
+    def radial_fused(self, x, y, h, W, alpha: float, plan: ops.EdgePlan, layout: int = 0, node_map=None):
+        """forward(x, y, alpha * h @ W, ...) with the radial last layer inside
+        the product kernels (``ops.edge_rtp_scatter``)."""
+        return ops.edge_rtp_scatter(x, y, h, W, alpha, plan, ops.find_variant(self.key), self.C, layout, node_map)
 
 
 class uuuTensorProduct(torch.nn.Module):
@@ -448,8 +472,12 @@ class O3CgtpInteraction(torch.nn.Module):
         """x: group-major node features in species-sorted row order."""
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
-        w = self.edge_info(R)
-        m = self.rejector(x, Y, w, plan, ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED, sp.node_map)
+        lay = ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED
+        if RADIAL_FUSED_TP and self.edge_info.fused and ops.rtp_supported(x.dtype, self.rejector.C, 64):
+            m = self.rejector.radial_fused(x, Y, self.edge_info.hidden(R), *self.edge_info.last_layer(), plan, lay,
+                                           sp.node_map)
+        else:
+            m = self.rejector(x, Y, self.edge_info(R), plan, lay, sp.node_map)
         # linear_down(m) / avg_num_neighbors, the division in the GEMM scale
         m = self.linear_down(m, alpha=1.0 / self.avg_num_neighbors)
         m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))

@@ -254,6 +254,91 @@ def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int
     return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout), node_map)
 
 
+# ------------------------------------------ radial-fused edge tensor product ----
+def rtp_supported(dtype, C: int, hidden: int) -> bool:
+    """Whether the radial-fused kernels take this product: float32, channels a
+    multiple of 64, 64 hidden features in front of the radial last layer."""
+    return dtype == torch.float32 and C % 64 == 0 and hidden == 64
+
+
+def launch_edge_rtp_fwd(x, y, h, W, alpha: float, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0,
+                        node_map=None):
+    """``launch_edge_tp_fwd`` with w = alpha h @ W made inside the kernel."""
+    Nn, E = plan.n_nodes, plan.n_edges
+    f32 = torch.float32
+    _req(x, "x", f32, (Nn, C * var.d1))
+    _req(y, "y", f32, (E, var.d2))
+    _req(h, "h", f32, (E, 64))
+    _req(W, "w_last", f32, (64, C * var.npath))
+    out = torch.empty(Nn, C * var.dout, dtype=f32, device=x.device)
+    rows = torch.empty(max(E, 1), dtype=torch.int32, device=x.device)
+    tok = _t0("edge_rtp_fwd:" + var.key)
+    N.check(N.lib().tace_edge_rtp_fwd(var.vid, x.data_ptr(), y.data_ptr(), h.data_ptr(), W.data_ptr(), float(alpha),
+                                      plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), N.ptr(node_map),
+                                      Nn, E, C, layout, rows.data_ptr(), out.data_ptr(), N.stream_ptr(x.device)),
+            "tace_edge_rtp_fwd")
+    _t1(tok, (Nn, E, C))
+    return out
+
+
+def launch_edge_rtp_bwd(x, y, h, W, alpha: float, gout, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0,
+                        node_map=None, need_x: bool = True):
+    """(grad_x or None, grad_y, grad_w) of ``launch_edge_rtp_fwd``; grad_w is
+    the gradient of the per-edge weights alpha h @ W."""
+    E = plan.n_edges
+    _req(gout, "g_out", torch.float32, (plan.n_nodes, C * var.dout))
+    gx = torch.empty_like(x) if need_x else None
+    gy = torch.empty_like(y)
+    gw = torch.empty(E, C * var.npath, dtype=torch.float32, device=x.device)
+    s_rowptr, s_slot = plan.sender_csr() if need_x else (None, None)
+    n_ws = N.lib().tace_edge_rtp_workspace_elems(var.vid, E, C, int(need_x))
+    if n_ws < 0:
+        N.check(int(n_ws), "tace_edge_rtp_workspace_elems")
+    ws = torch.empty(max(n_ws, 1), dtype=torch.float32, device=x.device)
+    rows = torch.empty(max(E, 1), dtype=torch.int32, device=x.device)
+    tok = _t0("edge_rtp_bwd:" + var.key)
+    N.check(N.lib().tace_edge_rtp_bwd(var.vid, x.data_ptr(), y.data_ptr(), h.data_ptr(), W.data_ptr(), float(alpha),
+                                      gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
+                                      N.ptr(node_map), plan.n_nodes, E, C, layout, N.ptr(s_rowptr), N.ptr(s_slot),
+                                      rows.data_ptr(), ws.data_ptr(), ws.numel(), N.ptr(gx), gy.data_ptr(),
+                                      gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_rtp_bwd")
+    _t1(tok, (plan.n_nodes, E, C, need_x))
+    return gx, gy, gw
+
+
+class _EdgeRTP(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, h, W, alpha: float, plan: EdgePlan, var: TpVariant, C: int, layout: int, node_map):
+        out = launch_edge_rtp_fwd(x, y, h, W, alpha, plan, var, C, layout, node_map)
+        ctx.save_for_backward(x, y, h, W)
+        ctx.alpha, ctx.plan, ctx.var, ctx.C, ctx.layout, ctx.node_map = alpha, plan, var, C, layout, node_map
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x, y, h, W = ctx.saved_tensors
+        gx, gy, gw = launch_edge_rtp_bwd(x, y, h, W, ctx.alpha, gout.contiguous(), ctx.plan, ctx.var, ctx.C,
+                                         ctx.layout, ctx.node_map, ctx.needs_input_grad[0])
+        gh = torch.mm(gw, W.t()).mul_(ctx.alpha) if ctx.needs_input_grad[2] else None
+        gW = torch.mm(h.t(), gw).mul_(ctx.alpha) if ctx.needs_input_grad[3] else None
+        return gx, gy, gh, gW, None, None, None, None, None, None
+
+
+def edge_rtp_scatter(x, y, h, W, alpha: float, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0,
+                     node_map: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``edge_tp_scatter(x, y, alpha * h @ W, ...)`` with the radial MLP's last
+    layer (``mlp.py:136-191``) made on MFMA inside the product kernels: the
+    per-edge weights never go through HBM, in the forward or the backward.
+    h [E, 64] (last hidden activations), W [64, C * npath]; float32, C a
+    multiple of 64 (``rtp_supported``)."""
+    if node_map is not None:
+        _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    if not rtp_supported(x.dtype, C, h.shape[-1]):
+        raise ValueError("edge_rtp_scatter: needs float32, channels a multiple of 64 and 64 hidden features")
+    return _EdgeRTP.apply(x.contiguous(), y.contiguous(), h.contiguous(), W.contiguous(), float(alpha), plan, var, C,
+                          int(layout), node_map)
+
+
 # ------------------------------------------------------------ edge vectors ----
 class _EdgeVectors(torch.autograd.Function):
     @staticmethod

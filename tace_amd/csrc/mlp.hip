@@ -109,80 +109,83 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
 // ------------------------------------------------------------- last layer --
 // out[e, n] = alpha sum_k h[e, k] W[k, n] with K = 64 (the wide, linear last
 // layer: E ~ 1e6 edges x N ~ 3e3 weights, output-write and fp32-MFMA bound).
-// Each wavefront owns 64 output columns and keeps their 64 x 64 slice of W in
-// registers as v_mfma_f32_16x16x4f32 B fragments for its whole life; it then
-// streams 16-edge blocks: A fragments from h (one 64-byte row segment per
-// lane), 16 k-steps x 4 column blocks of MFMA, and the 16 x 64 result tile
-// stored straight from the accumulators.  K is permuted inside each step
-// (lane group q of step s holds k = 16 q + s) so that a lane's A values are
-// one contiguous row segment.  Workgroups (4 waves = 256 columns) that share
-// an edge chunk are placed on one XCD (blockIdx round-robins over the 8
-// XCDs), so the chunk's h rows are read from HBM about once.
+// Each wavefront owns 64 output columns (two 32-column blocks) and keeps
+// their 64 x 64 slice of W in registers as v_mfma_f32_32x32x2f32 B fragments
+// for its whole life; it then streams 32-edge blocks: A fragments from h (one
+// 128-byte row segment per lane), 32 k-steps x 2 column blocks of MFMA, and
+// the two 32 x 32 result tiles stored straight from the accumulators -- in
+// the 32 x 32 output layout every store instruction writes two whole
+// 128-byte row segments, so no transpose through LDS is needed; the stores
+// are non-temporal (the output is streamed once to HBM).  K is permuted
+// inside each step (lane half q of step s holds k = 32 q + s) so that a
+// lane's A values are one contiguous row segment.  Workgroups (4 waves = 256
+// columns) that share an edge chunk are placed on one XCD (blockIdx
+// round-robins over the 8 XCDs), so the chunk's h rows are read from HBM
+// about once.
 typedef float f4_t __attribute__((ext_vector_type(4)));
+typedef float f16_t __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ void load_a_frag(const float* __restrict__ h, int64_t er, int64_t E, int q, float* a) {
+__device__ __forceinline__ void load_a_frag32(const float* __restrict__ h, int64_t er, int64_t E, int q, float* a) {
   if (er < E) {
-    const f4_t* hp = reinterpret_cast<const f4_t*>(h + er * 64 + 16 * q);
+    const f4_t* hp = reinterpret_cast<const f4_t*>(h + er * 64 + 32 * q);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
+    for (int v = 0; v < 8; ++v) {
       const f4_t t = hp[v];
       a[4 * v] = t[0]; a[4 * v + 1] = t[1]; a[4 * v + 2] = t[2]; a[4 * v + 3] = t[3];
     }
   } else {
 #pragma unroll
-    for (int s = 0; s < 16; ++s) a[s] = 0.0f;
+    for (int s = 0; s < 32; ++s) a[s] = 0.0f;
   }
 }
 
 __global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h, const float* __restrict__ Wm,
                                                      int64_t E, int N, float alpha, int n_col_tiles,
                                                      int64_t n_chunks, int edges_per_chunk, float* __restrict__ out) {
-  // per wave: the 16 x 64 result tile, transposed through LDS so that every
-  // store is one 256-byte row segment (row stride 65 floats: no bank conflicts)
-  __shared__ float tile[4][16][65];
   const int b = (int)blockIdx.x;
   const int64_t chunk = (int64_t)(b & 7) + 8 * (int64_t)((b >> 3) / n_col_tiles);
   const int ct = (b >> 3) % n_col_tiles;
   if (chunk >= n_chunks) return;
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
-  const int i = lane & 15, q = lane >> 4;
+  const int i = lane & 31, q = lane >> 5;
   const int col0 = ct * 256 + wave * 64;
-  float bf[16][4];
+  // B fragments: lane (i, q) of step s holds W[32 q + s][col0 + 32 cb + i]
+  float bf[32][2];
 #pragma unroll
-  for (int s = 0; s < 16; ++s)
+  for (int s = 0; s < 32; ++s)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int c = col0 + 16 * cb + i;
-      bf[s][cb] = c < N ? Wm[(int64_t)(16 * q + s) * N + c] : 0.0f;
+    for (int cb = 0; cb < 2; ++cb) {
+      const int c = col0 + 32 * cb + i;
+      bf[s][cb] = c < N ? Wm[(int64_t)(32 * q + s) * N + c] : 0.0f;
     }
   const int64_t e_begin = chunk * edges_per_chunk;
   const int64_t e_end = e_begin + edges_per_chunk < E ? e_begin + edges_per_chunk : E;
-  const bool col_ok = col0 + lane < N;
-  float a[16], an[16];
-  load_a_frag(h, e_begin + i, E, q, a);
-  for (int64_t e0 = e_begin; e0 < e_end; e0 += 16) {
+  float a[32], an[32];
+  load_a_frag32(h, e_begin + i, E, q, a);
+  for (int64_t e0 = e_begin; e0 < e_end; e0 += 32) {
     // next block's A fragment in flight during this block's MFMAs
-    load_a_frag(h, e0 + 16 < e_end ? e0 + 16 + i : E, E, q, an);
-    f4_t acc[4];
+    load_a_frag32(h, e0 + 32 < e_end ? e0 + 32 + i : E, E, q, an);
+    f16_t acc[2];
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) acc[cb] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-    for (int s = 0; s < 16; ++s)
+      for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], bf[s][cb], acc[cb], 0, 0, 0);
+    for (int s = 0; s < 32; ++s)
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < 2; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], bf[s][cb], acc[cb], 0, 0, 0);
+    // accumulator r of lane (i, q): row 8 (r / 4) + 4 q + r % 4, column i
 #pragma unroll
-      for (int r = 0; r < 4; ++r) tile[wave][4 * q + r][16 * cb + i] = alpha * acc[cb][r];
-    __builtin_amdgcn_wave_barrier();
+    for (int cb = 0; cb < 2; ++cb) {
+      const int c = col0 + 32 * cb + i;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int64_t row = e0 + r;
-      if (row < E && col_ok) out[row * N + col0 + lane] = tile[wave][r][lane];
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = e0 + 8 * (r >> 2) + 4 * q + (r & 3);
+        if (row < e_end && c < N) __builtin_nontemporal_store(alpha * acc[cb][r], out + row * N + c);
+      }
     }
-    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int s = 0; s < 16; ++s) a[s] = an[s];
+    for (int s = 0; s < 32; ++s) a[s] = an[s];
   }
 }
 

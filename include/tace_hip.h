@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 14
+#define TACE_HIP_ABI_VERSION 15
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -135,8 +135,15 @@ int tace_edge_rtp_bwd(int vid, const float* x, const float* y, const float* h, c
  * IN1_GROUPED|OUT_GROUPED|IN2_GROUPED. */
 int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void* w, int64_t n_nodes, int32_t channels,
                  int32_t layout, void* out, void* stream);
+/* Gradients g1 [N, C*d1], g2 [N, C*d2] (and gw for weighted variants) of
+ * sum(gout * out).  Variants with many x1 blocks run their backward in parts
+ * (one per group of x1 blocks) whose g2 partials go to `workspace` (at least
+ * tace_uuu_workspace_elems(vid, N, C) elements; 0 for one part, then
+ * workspace may be NULL) and are summed in a fixed order. */
+int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels);
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
-                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* stream);
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* workspace,
+                 int64_t workspace_elems, void* stream);
 
 /* ---- edge featurisation --------------------------------------------------
  * vec [E, 3] edge vectors; r = |vec| + 1e-9;

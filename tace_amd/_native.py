@@ -42,7 +42,9 @@ _SIGS = {
     "tace_edge_vec_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_edge_vec_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_uuu_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp]),
-    "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp]),
+    "tace_uuu_workspace_elems": (_c_i64, [_c_int, _c_i64, _c_i32]),
+    "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i64,
+                              _vp]),
     "tace_edge_basis_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_edge_basis_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32,
                                      _vp, _vp]),

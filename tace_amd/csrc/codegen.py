@@ -781,61 +781,102 @@ class Variant:
         L.append("}")
         return "\n".join(L)
 
+    def uuu_parts(self, cap: int = 40) -> List[List[int]]:
+        """in1 blocks split into consecutive parts of at most ``cap`` x
+        components per channel (one block per part at least): the backward
+        runs one part per thread so that x, grad_x and the part's output
+        gradients fit in registers at several wavefronts per SIMD.  A part owns
+        its blocks' grad_x rows; grad_x2 is summed over the parts' partials.
+        Products with few output components (<= 128 per channel) stay whole:
+        their registers fit, and the parts would only re-read x2."""
+        if self.DO <= 128:
+            return [[b for b in range(len(self.in1)) if any(pb[0] == b for pb in self.path_blocks)]]
+        out, cur, acc = [], [], 0
+        for b in range(len(self.in1)):
+            if not any(pb[0] == b for pb in self.path_blocks):
+                continue
+            if cur and acc + self.d1[b] > cap:
+                out.append(cur)
+                cur, acc = [], 0
+            cur.append(b)
+            acc += self.d1[b]
+        if cur:
+            out.append(cur)
+        return out
+
     def emit_uuu_bwd(self) -> str:
         P = len(self.paths)
+        parts = self.uuu_parts()
+        nq = len(parts)
         L = []
+        for q, blocks in enumerate(parts):
+            L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__device__ __forceinline__ void f_{self.name}_bwd{q}(")
+            L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ w,")
+            L.append("    const T* __restrict__ gout, T* __restrict__ g1, T* __restrict__ g2, T* __restrict__ gw,")
+            L.append("    size_t n, int u, size_t N, int C) {")
+            for bb in blocks:
+                for m in range(self.d1[bb]):
+                    L.append(f"  const T x{bb}_{m} = {self._ld('x1', 'in1', bb, m, 'IN1_GM')};")
+                    L.append(f"  T hx{bb}_{m} = T(0);")
+            for bb, d in enumerate(self.d2):
+                for m in range(d):
+                    L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
+                    L.append(f"  T hy{bb}_{m} = T(0);")
+            if self.weighted:
+                L.append(f"  const size_t wo = n * {P} * (size_t)C + u;")
+            for p in range(P):
+                b1, b2 = self.path_blocks[p]
+                if b1 not in blocks:
+                    continue
+                d = self.dout[p]
+                L.append("  {")
+                for k in range(d):
+                    L.append(f"    const T o{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
+                if self.weighted:
+                    # grad of the weight: sum_k gout_k t_k with t the unweighted path output
+                    L.append("    if (gw) {")
+                    tsum = []
+                    for k in range(d):
+                        terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
+                        if terms:
+                            tsum.append(f"o{k} * ({' + '.join(terms)})")
+                    L.append(f"      gw[wo + (size_t){p} * C] = {' + '.join(tsum) if tsum else 'T(0)'};")
+                    L.append("    }")
+                    L.append(f"    const T wp = w[wo + (size_t){p} * C];")
+                    for k in range(d):
+                        L.append(f"    const T g{k} = wp * o{k};")
+                else:
+                    for k in range(d):
+                        L.append(f"    const T g{k} = o{k};")
+                for (i, j, k, c) in self.cg[p]:
+                    L.append(f"    hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * g{k});")
+                    L.append(f"    hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * g{k});")
+                L.append("  }")
+            for bb in blocks:
+                for m in range(self.d1[bb]):
+                    e3, gm = self._addr("in1", bb, m)
+                    L.append(f"  g1[IN1_GM ? ({gm}) : ({e3})] = hx{bb}_{m};")
+            for bb, d in enumerate(self.d2):
+                for m in range(d):
+                    e3, gm = self._addr("in2", bb, m)
+                    L.append(f"  g2[IN2_GM ? ({gm}) : ({e3})] = hy{bb}_{m};")
+            L.append("}")
+        # one launch runs every part: consecutive workgroups = the parts of the
+        # same 256 (node, channel) pairs, so they share x2 in L2; part q writes
+        # grad_x2 partial q (g2 itself when there is one part)
         L.append(f"template <typename T, bool IN1_GM, bool OUT_GM, bool IN2_GM>\n__global__ __launch_bounds__(256) void k_{self.name}_bwd(")
         L.append("    const T* __restrict__ x1, const T* __restrict__ x2, const T* __restrict__ w,")
-        L.append("    const T* __restrict__ gout, T* __restrict__ g1, T* __restrict__ g2, T* __restrict__ gw,")
+        L.append("    const T* __restrict__ gout, T* __restrict__ g1, T* __restrict__ g2p, T* __restrict__ gw,")
         L.append("    int n_nodes, int C) {")
-        L.append("  const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;")
+        L.append(f"  const int q = (int)(blockIdx.x % {nq});")
+        L.append(f"  const size_t t = (size_t)(blockIdx.x / {nq}) * 256 + threadIdx.x;")
         L.append("  const size_t n = t / (size_t)C; const int u = (int)(t % (size_t)C);")
         L.append("  const size_t N = (size_t)n_nodes;")
         L.append("  if (n >= N) return;")
-        for bb, d in enumerate(self.d1):
-            for m in range(d):
-                L.append(f"  const T x{bb}_{m} = {self._ld('x1', 'in1', bb, m, 'IN1_GM')};")
-                L.append(f"  T hx{bb}_{m} = T(0);")
-        for bb, d in enumerate(self.d2):
-            for m in range(d):
-                L.append(f"  const T y{bb}_{m} = {self._ld('x2', 'in2', bb, m, 'IN2_GM')};")
-                L.append(f"  T hy{bb}_{m} = T(0);")
-        if self.weighted:
-            L.append(f"  const size_t wo = n * {P} * (size_t)C + u;")
-        for p in range(P):
-            b1, b2 = self.path_blocks[p]
-            d = self.dout[p]
-            L.append("  {")
-            for k in range(d):
-                L.append(f"    const T o{k} = {self._ld('gout', 'out', p, k, 'OUT_GM')};")
-            if self.weighted:
-                # grad of the weight: sum_k gout_k t_k with t the unweighted path output
-                L.append("    if (gw) {")
-                tsum = []
-                for k in range(d):
-                    terms = [f"{_lit(c)} * (x{b1}_{i} * y{b2}_{j})" for (i, j, kk, c) in self.cg[p] if kk == k]
-                    if terms:
-                        tsum.append(f"o{k} * ({' + '.join(terms)})")
-                L.append(f"      gw[wo + (size_t){p} * C] = {' + '.join(tsum) if tsum else 'T(0)'};")
-                L.append("    }")
-                L.append(f"    const T wp = w[wo + (size_t){p} * C];")
-                for k in range(d):
-                    L.append(f"    const T g{k} = wp * o{k};")
-            else:
-                for k in range(d):
-                    L.append(f"    const T g{k} = o{k};")
-            for (i, j, k, c) in self.cg[p]:
-                L.append(f"    hx{b1}_{i} += {_lit(c)} * (y{b2}_{j} * g{k});")
-                L.append(f"    hy{b2}_{j} += {_lit(c)} * (x{b1}_{i} * g{k});")
-            L.append("  }")
-        for bb, d in enumerate(self.d1):
-            for m in range(d):
-                e3, gm = self._addr("in1", bb, m)
-                L.append(f"  g1[IN1_GM ? ({gm}) : ({e3})] = hx{bb}_{m};")
-        for bb, d in enumerate(self.d2):
-            for m in range(d):
-                e3, gm = self._addr("in2", bb, m)
-                L.append(f"  g2[IN2_GM ? ({gm}) : ({e3})] = hy{bb}_{m};")
+        L.append(f"  T* __restrict__ g2 = g2p + (size_t)q * N * C * {self.D2};")
+        for q in range(nq):
+            L.append(f"  {'if' if q == 0 else 'else if'} (q == {q}) f_{self.name}_bwd{q}<T, IN1_GM, OUT_GM, IN2_GM>("
+                     "x1, x2, w, gout, g1, g2, gw, n, u, N, C);")
         L.append("}")
         return "\n".join(L)
 
@@ -1053,7 +1094,7 @@ def _launchers(v: Variant) -> List[str]:
             out.append("}")
             out.append(f"void L_{v.name}_bwd_{tag}(const void* x1, const void* x2, const void* w, const void* go, void* g1, void* g2, void* gw, int n, int C, int flags, hipStream_t s) {{")
             out.append("  const size_t tot = (size_t)n * C; if (tot == 0) return;")
-            out.append("  const dim3 g((unsigned)((tot + 255) / 256)), b(256);")
+            out.append(f"  const dim3 g((unsigned)((tot + 255) / 256 * {len(v.uuu_parts())})), b(256);")
             for f in UUU_LAYOUTS:
                 out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(f & 1)}, {_b(f & 2)}, {_b(f & 4)}>), g, b, 0, s, (const {T}*)x1, (const {T}*)x2, (const {T}*)w, (const {T}*)go, ({T}*)g1, ({T}*)g2, ({T}*)gw, n, C);")
             out.append("}")
@@ -1084,7 +1125,8 @@ def emit_all(gen_dir: str) -> List[str]:
            "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
            "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;",
            "  int rnparts;                    // uvu: radial-fused parts (grad_y partials: rnparts * C / 64)",
-           "  RtpFwd rfwd; RtpBwd rbwd;       // uvu: radial-fused kernels (float32)", "};"]
+           "  RtpFwd rfwd; RtpBwd rbwd;       // uvu: radial-fused kernels (float32)",
+           "  int unparts;                    // uuu: backward parts (grad_x2 partials when > 1)", "};"]
     for v in vs:
         if v.kind == "uvu":
             reg += [f"void L_{v.name}_{k}_{t}({sig});" for k, sig in
@@ -1104,10 +1146,11 @@ def emit_all(gen_dir: str) -> List[str]:
         if v.kind == "uvu":
             reg.append(f"  {{{head}, {len(v.parts())}, {len(segs)}, {seg}, L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, "
                        f"L_{n}_bwd_d, nullptr, nullptr, nullptr, nullptr, {len(v.rtp_parts())}, L_{n}_rfwd, "
-                       f"L_{n}_rbwd}},")
+                       f"L_{n}_rbwd, 0}},")
         else:
             reg.append(f"  {{{head}, 0, 0, {seg}, nullptr, nullptr, nullptr, nullptr, "
-                       f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d, 0, nullptr, nullptr}},")
+                       f"L_{n}_fwd_f, L_{n}_fwd_d, L_{n}_bwd_f, L_{n}_bwd_d, 0, nullptr, nullptr, "
+                       f"{len(v.uuu_parts())}}},")
     reg.append("};")
     reg.append(f"static const int kNumVariants = {len(vs)};")
     _write(os.path.join(gen_dir, "registry.inc"), reg)

@@ -917,25 +917,47 @@ int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void*
   return check_launch("tace_uuu_fwd");
 }
 
+int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels) {
+  if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_workspace_elems: bad variant id");
+  if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_workspace_elems: bad sizes");
+  const TpVariant& v = kVariants[vid];
+  return v.unparts > 1 ? (int64_t)v.unparts * n_nodes * channels * v.d2 : 0;
+}
+
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
-                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* stream) {
+                 int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* workspace,
+                 int64_t workspace_elems, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
   if (!uuu_layout_ok(layout)) return fail("tace_uuu_bwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
   if (n_nodes && (!x1 || !x2 || !gout || !g1 || !g2)) return fail("tace_uuu_bwd: null pointer");
-  if ((size_t)n_nodes * channels > (size_t)UINT32_MAX * 128) return fail("tace_uuu_bwd: too many nodes");
   const TpVariant& v = kVariants[vid];
+  if (((size_t)n_nodes * channels + 255) / 256 * v.unparts > (size_t)UINT32_MAX) return fail("tace_uuu_bwd: too many nodes");
   if (n_nodes && v.weighted != (w != nullptr))
     return fail(v.weighted ? "tace_uuu_bwd: this product is weighted: w is required"
                            : "tace_uuu_bwd: this product has no path weights: w must be null");
   if (n_nodes && w && !gw) return fail("tace_uuu_bwd: weighted products need gw");
+  const int64_t ny = n_nodes * (int64_t)channels * v.d2;
+  const int64_t need = v.unparts > 1 ? (int64_t)v.unparts * ny : 0;
+  if (need && !workspace) return fail("tace_uuu_bwd: null workspace");
+  if (workspace_elems < need) return fail("tace_uuu_bwd: workspace smaller than tace_uuu_workspace_elems()");
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == TACE_F32)
-    v.ubwd_f(x1, x2, w, gout, g1, g2, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
-  else if (dtype == TACE_F64)
-    v.ubwd_d(x1, x2, w, gout, g1, g2, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
-  else
+  // parts > 1: each part writes its grad_x2 partial into the workspace; the
+  // partials are summed into g2 in a fixed order
+  void* g2p = v.unparts > 1 ? workspace : g2;
+  const unsigned nb = (unsigned)((ny + 255) / 256);
+  if (dtype == TACE_F32) {
+    v.ubwd_f(x1, x2, w, gout, g1, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
+    if (v.unparts > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)g2p, v.unparts, ny, (float*)g2);
+  } else if (dtype == TACE_F64) {
+    v.ubwd_d(x1, x2, w, gout, g1, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
+    if (v.unparts > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)g2p, v.unparts, ny,
+                         (double*)g2);
+  } else {
     return fail("tace_uuu_bwd: dtype must be TACE_F32 or TACE_F64");
+  }
   return check_launch("tace_uuu_bwd");
 }
 

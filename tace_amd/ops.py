@@ -416,10 +416,14 @@ def launch_uuu_bwd(x1, x2, w, gout, var: TpVariant, C: int, layout: int = 0):
     _req(gout, "g_out", x1.dtype, (x1.shape[0], C * var.dout))
     g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
     gw = torch.empty_like(w) if w is not None else None
+    n_ws = N.lib().tace_uuu_workspace_elems(var.vid, x1.shape[0], C)
+    if n_ws < 0:
+        N.check(int(n_ws), "tace_uuu_workspace_elems")
+    ws = torch.empty(n_ws, dtype=x1.dtype, device=x1.device) if n_ws else None
     tok = _t0("uuu_bwd:" + var.key)
     N.check(N.lib().tace_uuu_bwd(var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(), N.ptr(w),
                                  gout.data_ptr(), x1.shape[0], C, layout, g1.data_ptr(), g2.data_ptr(), N.ptr(gw),
-                                 N.stream_ptr(x1.device)), "tace_uuu_bwd")
+                                 N.ptr(ws), int(n_ws), N.stream_ptr(x1.device)), "tace_uuu_bwd")
     _t1(tok, (x1.shape[0], C))
     return g1, g2, gw
 

@@ -131,6 +131,8 @@ def _uuu_cases():
         out.append((full, full, [0]))
         out.append((nu2_ls, full, full))
         out.append((nu2_ls, full, [0]))
+    # a product whose backward runs in parts with summed grad_x2 partials
+    out.append((nu2_ls, full, [0, 1, 2]))
     return out
 
 

@@ -173,8 +173,8 @@ int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const
  * the caller.  weights: the n_layers matrices packed row-major
  * [n_in x 64 | 64 x 64 | ...] with their scale folded in.  Outputs: h
  * [E, 64] (the last hidden activations, row-major) and the saved
- * pre-activations z_t [n_layers, 64, E] (feature-major) that the backward
- * reads.
+ * pre-activations z_t [n_layers, E, 64] (edge-major) that the backward
+ * reads.  float32 runs on fp32 MFMA, float64 per edge on the vector ALUs.
  *   tace_radial_mlp_bwd: g_radial [E, n_in] from g_h [E, 64] (weights are
  *   constants: no weight gradient). */
 #define TACE_MLP_WIDTH 64

@@ -11,8 +11,16 @@
 // Layouts: radial [E, n_in]; weights packed [n_in x 64 | 64 x 64 | ...]
 // (row-major, scale folded in); the last hidden activations h [E, 64]
 // row-major (the A operand of the last layer's GEMM); the saved
-// pre-activations feature-major, z_t [n_layers, 64, E] (consecutive edges =
-// consecutive addresses).
+// pre-activations edge-major, z_t [n_layers, E, 64].
+//
+// float32 runs the layers on MFMA (k_mlp_fwd_mfma / k_mlp_bwd_mfma): per
+// 32-edge block a wavefront multiplies [32 x K] activations by the [K x 64]
+// weights with v_mfma_f32_32x32x2f32 (weights staged once per workgroup in
+// LDS), applies SiLU (or its derivative) to the accumulators and passes the
+// result to the next layer through a per-wavefront LDS tile (the accumulator
+// layout holds a column per lane, the A operand needs a row); z_t and h are
+// stored straight from the accumulators, two 128-byte row segments per
+// store.  The per-thread kernels below stay for float64.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -49,7 +57,7 @@ __global__ __launch_bounds__(256) void k_mlp_fwd(const T* __restrict__ radial, i
   for (int l = 0;; ++l) {
 #pragma unroll
     for (int j = 0; j < W; ++j) {
-      z_t[((int64_t)l * W + j) * E + e] = z[j];
+      z_t[((int64_t)l * E + e) * W + j] = z[j];
       a_[j] = z[j] * sigm(z[j]);
     }
     if (l + 1 == n_layers) break;
@@ -81,7 +89,7 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
   for (int l = n_layers - 1; l >= 0; --l) {
 #pragma unroll
     for (int j = 0; j < W; ++j) {
-      const T zv = z_t[((int64_t)l * W + j) * E + e];
+      const T zv = z_t[((int64_t)l * E + e) * W + j];
       const T s = sigm(zv);
       g[j] *= s * (T(1) + zv * (T(1) - s));
     }
@@ -106,6 +114,173 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
   }
 }
 
+// ------------------------------------------------- hidden layers on MFMA --
+typedef float f16_t __attribute__((ext_vector_type(16)));
+constexpr int TSTRIDE = 68;  // LDS tile row stride (16-byte aligned rows)
+
+// accumulator r of lane (i, q) in the 32 x 32 output layout: row
+// 8 (r / 4) + 4 q + r % 4, column i
+__device__ __forceinline__ int acc_row(int r, int q) { return 8 * (r >> 2) + 4 * q + (r & 3); }
+
+// the [32 x 64] accumulator pair -> LDS tile -> A fragment (lane (i, q) of
+// k-step s holds row i, k = 32 q + s)
+__device__ __forceinline__ void tile_to_afrag(const f16_t* acc, float* __restrict__ T, int i, int q, float* a) {
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) T[acc_row(r, q) * TSTRIDE + 32 * cb + i] = acc[cb][r];
+  __builtin_amdgcn_wave_barrier();
+  typedef float f4v __attribute__((ext_vector_type(4)));
+  const f4v* tp = reinterpret_cast<const f4v*>(T + i * TSTRIDE + 32 * q);
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {
+    const f4v t = tp[v];
+    a[4 * v] = t[0]; a[4 * v + 1] = t[1]; a[4 * v + 2] = t[2]; a[4 * v + 3] = t[3];
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ float silu_f(float z) { return z * (1.0f / (1.0f + expf(-z))); }
+__device__ __forceinline__ float dsilu_f(float z) {
+  const float s = 1.0f / (1.0f + expf(-z));
+  return s * (1.0f + z * (1.0f - s));
+}
+
+// LDS: weights [K0p x 64 | (n_layers - 1) x 64 x 64] (K0p = n_in rounded up to
+// even, zero rows past n_in), then one tile [32 x TSTRIDE] per wavefront
+__global__ __launch_bounds__(256) void k_mlp_fwd_mfma(const float* __restrict__ radial, int64_t E, int n_in,
+                                                      int n_layers, const float* __restrict__ wg,
+                                                      float* __restrict__ h, float* __restrict__ z_t) {
+  extern __shared__ float smem[];
+  const int K0p = (n_in + 1) & ~1, S0 = K0p >> 1;
+  const int nw = K0p * 64 + (n_layers - 1) * 4096;
+  for (int t = (int)threadIdx.x; t < nw; t += 256)
+    smem[t] = t < K0p * 64 ? ((t >> 6) < n_in ? wg[t] : 0.0f) : wg[t - (K0p - n_in) * 64];
+  __syncthreads();
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6, i = lane & 31, q = lane >> 5;
+  float* __restrict__ T = smem + nw + wave * 32 * TSTRIDE;
+  const int64_t nblk = (E + 31) / 32;
+  for (int64_t blk = (int64_t)blockIdx.x * 4 + wave; blk < nblk; blk += (int64_t)gridDim.x * 4) {
+    const int64_t e0 = blk * 32, er = e0 + i;
+    f16_t acc[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
+    // first layer: A = radial rows, lane half q holds k = S0 q + s
+    for (int s = 0; s < S0; ++s) {
+      const int k = S0 * q + s;
+      const float av = er < E && k < n_in ? radial[er * n_in + k] : 0.0f;
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+        acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(av, smem[k * 64 + 32 * cb + i], acc[cb], 0, 0, 0);
+    }
+    for (int l = 0;; ++l) {
+      // acc holds z_l: save it, activate
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t e = e0 + acc_row(r, q);
+          const float z = acc[cb][r];
+          if (e < E) z_t[((int64_t)l * E + e) * 64 + 32 * cb + i] = z;
+          acc[cb][r] = silu_f(z);
+        }
+      if (l + 1 == n_layers) break;
+      float a[32];
+      tile_to_afrag(acc, T, i, q, a);
+      const float* __restrict__ Wl = smem + K0p * 64 + l * 4096;
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 32; ++s)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], Wl[(32 * q + s) * 64 + 32 * cb + i], acc[cb], 0, 0, 0);
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t e = e0 + acc_row(r, q);
+        if (e < E) h[e * 64 + 32 * cb + i] = acc[cb][r];
+      }
+  }
+}
+
+// LDS: transposed weights WT_0 [64 x 32] (columns past n_in zero) then
+// WT_l [64 x 64] for l = 1 .. n_layers - 1 (WT_l[j][k] = W_l[k][j]), then the
+// tiles
+__global__ __launch_bounds__(256) void k_mlp_bwd_mfma(const float* __restrict__ z_t, const float* __restrict__ gh,
+                                                      int64_t E, int n_in, int n_layers,
+                                                      const float* __restrict__ wg, float* __restrict__ g_radial) {
+  extern __shared__ float smem[];
+  const int nw = 64 * 32 + (n_layers - 1) * 4096;
+  for (int t = (int)threadIdx.x; t < nw; t += 256) {
+    float v;
+    if (t < 64 * 32) {
+      const int j = t >> 5, k = t & 31;
+      v = k < n_in ? wg[k * 64 + j] : 0.0f;
+    } else {
+      const int u = t - 64 * 32, l = u >> 12, j = (u >> 6) & 63, k = u & 63;
+      v = wg[n_in * 64 + l * 4096 + k * 64 + j];
+    }
+    smem[t] = v;
+  }
+  __syncthreads();
+  const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6, i = lane & 31, q = lane >> 5;
+  float* __restrict__ T = smem + nw + wave * 32 * TSTRIDE;
+  const int64_t nblk = (E + 31) / 32;
+  for (int64_t blk = (int64_t)blockIdx.x * 4 + wave; blk < nblk; blk += (int64_t)gridDim.x * 4) {
+    const int64_t e0 = blk * 32;
+    f16_t g[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t e = e0 + acc_row(r, q);
+        g[cb][r] = e < E ? gh[e * 64 + 32 * cb + i] : 0.0f;
+      }
+    for (int l = n_layers - 1;; --l) {
+      // g_z = g_a silu'(z_l)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t e = e0 + acc_row(r, q);
+          const float z = e < E ? z_t[((int64_t)l * E + e) * 64 + 32 * cb + i] : 0.0f;
+          g[cb][r] *= dsilu_f(z);
+        }
+      float a[32];
+      tile_to_afrag(g, T, i, q, a);
+      if (l == 0) {
+        f16_t acc = {};
+#pragma unroll
+        for (int s = 0; s < 32; ++s)
+          acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], smem[(32 * q + s) * 32 + i], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t e = e0 + acc_row(r, q);
+          if (e < E && i < n_in) g_radial[e * n_in + i] = acc[r];
+        }
+        break;
+      }
+      const float* __restrict__ WT = smem + 64 * 32 + (l - 1) * 4096;
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) g[cb][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 32; ++s)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          g[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], WT[(32 * q + s) * 64 + 32 * cb + i], g[cb], 0, 0, 0);
+    }
+  }
+}
+
 // ------------------------------------------------------------- last layer --
 // out[e, n] = alpha sum_k h[e, k] W[k, n] with K = 64 (the wide, linear last
 // layer: E ~ 1e6 edges x N ~ 3e3 weights, output-write and fp32-MFMA bound).
@@ -123,7 +298,6 @@ __global__ __launch_bounds__(256) void k_mlp_bwd(const T* __restrict__ z_t, cons
 // round-robins over the 8 XCDs), so the chunk's h rows are read from HBM
 // about once.
 typedef float f4_t __attribute__((ext_vector_type(4)));
-typedef float f16_t __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ void load_a_frag32(const float* __restrict__ h, int64_t er, int64_t E, int q, float* a) {
   if (er < E) {
@@ -189,6 +363,28 @@ __global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h
   }
 }
 
+size_t mlp_fwd_lds_bytes(int n_in, int n_layers) {
+  return sizeof(float) * ((size_t)((n_in + 1) & ~1) * 64 + (size_t)(n_layers - 1) * 4096 + 4 * 32 * TSTRIDE);
+}
+
+size_t mlp_bwd_lds_bytes(int n_layers) {
+  return sizeof(float) * ((size_t)64 * 32 + (size_t)(n_layers - 1) * 4096 + 4 * 32 * TSTRIDE);
+}
+
+// 4 wavefronts per workgroup, one 32-edge block per wavefront and pass
+dim3 mlp_mfma_grid(int64_t E) {
+  const int64_t wgs = ((E + 31) / 32 + 3) / 4;
+  return dim3((unsigned)(wgs < 2048 ? (wgs > 0 ? wgs : 1) : 2048));
+}
+
+// dynamic LDS above the 64 KB default (the limit is per kernel and process)
+int mlp_lds_attr(const void* fn, size_t bytes) {
+  if (bytes <= 65536) return 0;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) != hipSuccess)
+    return tace_fail_msg("radial MLP: cannot raise the kernel's dynamic LDS limit");
+  return 0;
+}
+
 int mlp_checks(const char* who, int64_t E, int32_t n_in, int32_t n_layers) {
   char msg[160];
   if (E < 0 || n_in < 1 || n_in > TACE_MLP_MAX_IN || n_layers < 1 || n_layers > TACE_MLP_MAX_LAYERS) {
@@ -210,10 +406,12 @@ int tace_radial_mlp_fwd(int dtype, const void* radial, int64_t n_edges, int32_t 
   if (!radial || !weights || !h || !z_t) return tace_fail_msg("tace_radial_mlp_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges + 255) / 256)), b(256);
-  if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_mlp_fwd<float>, g, b, 0, s, (const float*)radial, n_edges, n_in, n_layers,
-                       (const float*)weights, (float*)h, (float*)z_t);
-  else if (dtype == TACE_F64)
+  if (dtype == TACE_F32) {
+    const size_t lds = mlp_fwd_lds_bytes(n_in, n_layers);
+    if (mlp_lds_attr((const void*)k_mlp_fwd_mfma, lds)) return -1;
+    hipLaunchKernelGGL(k_mlp_fwd_mfma, mlp_mfma_grid(n_edges), b, lds, s, (const float*)radial, n_edges, n_in,
+                       n_layers, (const float*)weights, (float*)h, (float*)z_t);
+  } else if (dtype == TACE_F64)
     hipLaunchKernelGGL(k_mlp_fwd<double>, g, b, 0, s, (const double*)radial, n_edges, n_in, n_layers,
                        (const double*)weights, (double*)h, (double*)z_t);
   else
@@ -228,10 +426,12 @@ int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h, int64_t n_e
   if (!z_t || !g_h || !weights || !g_radial) return tace_fail_msg("tace_radial_mlp_bwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)((n_edges + 255) / 256)), b(256);
-  if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_mlp_bwd<float>, g, b, 0, s, (const float*)z_t, (const float*)g_h, n_edges, n_in,
-                       n_layers, (const float*)weights, (float*)g_radial);
-  else if (dtype == TACE_F64)
+  if (dtype == TACE_F32) {
+    const size_t lds = mlp_bwd_lds_bytes(n_layers);
+    if (mlp_lds_attr((const void*)k_mlp_bwd_mfma, lds)) return -1;
+    hipLaunchKernelGGL(k_mlp_bwd_mfma, mlp_mfma_grid(n_edges), b, lds, s, (const float*)z_t, (const float*)g_h,
+                       n_edges, n_in, n_layers, (const float*)weights, (float*)g_radial);
+  } else if (dtype == TACE_F64)
     hipLaunchKernelGGL(k_mlp_bwd<double>, g, b, 0, s, (const double*)z_t, (const double*)g_h, n_edges,
                        n_in, n_layers, (const double*)weights, (double*)g_radial);
   else

@@ -868,7 +868,7 @@ def launch_mlp_hidden_fwd(radial, weights, n_layers: int):
     _req(radial, "radial", dt, (E, n_in))
     _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
     h = torch.empty(E, width, dtype=dt, device=radial.device)
-    z_t = torch.empty(n_layers, width, E, dtype=dt, device=radial.device)
+    z_t = torch.empty(n_layers, E, width, dtype=dt, device=radial.device)
     tok = _t0("radial_mlp_fwd")
     N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers, weights.data_ptr(),
                                         h.data_ptr(), z_t.data_ptr(), N.stream_ptr(radial.device)),
@@ -878,7 +878,7 @@ def launch_mlp_hidden_fwd(radial, weights, n_layers: int):
 
 
 def launch_mlp_hidden_bwd(z_t, gh, weights, n_in: int) -> torch.Tensor:
-    n_layers, _, E = z_t.shape
+    n_layers, E, _ = z_t.shape
     _req(gh, "g_h", z_t.dtype, (E, 64))
     g = torch.empty(E, n_in, dtype=z_t.dtype, device=z_t.device)
     tok = _t0("radial_mlp_bwd")

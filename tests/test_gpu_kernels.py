@@ -402,7 +402,8 @@ def var_out_ls(var, in1, lmax):
 
 # ------------------------------------------------------------ radial MLP ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-@pytest.mark.parametrize("dims", [[8, 64, 64, 64, 2944], [8, 64, 64, 64, 1536], [10, 64, 96], [8, 64, 64, 64, 64, 7]])
+@pytest.mark.parametrize("dims", [[8, 64, 64, 64, 2944], [8, 64, 64, 64, 1536], [10, 64, 96], [8, 64, 64, 64, 64, 7],
+                                  [7, 64, 64, 30]])
 def test_radial_mlp_matches_oracle(cuda, dtype, dims):
     """Fused width-64 hidden layers + last-layer GEMM against the oracle MLP (same weights)."""
     from tace_amd import model as pm

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 15
+#define TACE_HIP_ABI_VERSION 16
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -171,18 +171,18 @@ int tace_edge_vec_bwd(int dtype, const void* g_vec, const int32_t* rowptr, const
  * [E, n_in], h_l = silu(h_(l-1) W_l) for l = 1..n_layers, every hidden width
  * TACE_MLP_WIDTH; the last (wide, linear) layer of the MLP is a GEMM left to
  * the caller.  weights: the n_layers matrices packed row-major
- * [n_in x 64 | 64 x 64 | ...] with their scale folded in.  Outputs: h
- * [E, 64] (the last hidden activations, row-major) and the saved
- * pre-activations z_t [n_layers, E, 64] (edge-major) that the backward
- * reads.  float32 runs on fp32 MFMA, float64 per edge on the vector ALUs.
- *   tace_radial_mlp_bwd: g_radial [E, n_in] from g_h [E, 64] (weights are
- *   constants: no weight gradient). */
+ * [n_in x 64 | 64 x 64 | ...] with their scale folded in.  Output: h [E, 64]
+ * (the last hidden activations, row-major).  float32 runs on fp32 MFMA,
+ * float64 per edge on the vector ALUs.
+ *   tace_radial_mlp_bwd: g_radial [E, n_in] from g_h [E, 64], recomputing the
+ *   pre-activations from radial (nothing is saved between the two; weights
+ *   are constants: no weight gradient). */
 #define TACE_MLP_WIDTH 64
 #define TACE_MLP_MAX_IN 32
 #define TACE_MLP_MAX_LAYERS 4
 int tace_radial_mlp_fwd(int dtype, const void* radial, int64_t n_edges, int32_t n_in, int32_t n_layers,
-                        const void* weights, void* h, void* z_t, void* stream);
-int tace_radial_mlp_bwd(int dtype, const void* z_t, const void* g_h, int64_t n_edges, int32_t n_in,
+                        const void* weights, void* h, void* stream);
+int tace_radial_mlp_bwd(int dtype, const void* radial, const void* g_h, int64_t n_edges, int32_t n_in,
                         int32_t n_layers, const void* weights, void* g_radial, void* stream);
 /* the last (linear) layer in float32: out [E, n_out] = alpha h [E, 64] @
  * weight [64, n_out] (row-major; h 16-byte aligned), on fp32 MFMA. */

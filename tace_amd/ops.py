@@ -860,30 +860,30 @@ def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, row
     return tuple(blocks)
 
 
-def launch_mlp_hidden_fwd(radial, weights, n_layers: int):
-    """Hidden layers of the radial MLP: (h [E, 64], saved pre-activations z_t)."""
+def launch_mlp_hidden_fwd(radial, weights, n_layers: int) -> torch.Tensor:
+    """Hidden layers of the radial MLP: the last hidden activations h [E, 64]
+    (the backward recomputes the rest from ``radial``)."""
     E, n_in = radial.shape
     dt = radial.dtype
     width = 64
     _req(radial, "radial", dt, (E, n_in))
     _req(weights, "weights", dt, (n_in * width + (n_layers - 1) * width * width,))
     h = torch.empty(E, width, dtype=dt, device=radial.device)
-    z_t = torch.empty(n_layers, E, width, dtype=dt, device=radial.device)
     tok = _t0("radial_mlp_fwd")
     N.check(N.lib().tace_radial_mlp_fwd(N.dtype_code(dt), radial.data_ptr(), E, n_in, n_layers, weights.data_ptr(),
-                                        h.data_ptr(), z_t.data_ptr(), N.stream_ptr(radial.device)),
-            "tace_radial_mlp_fwd")
+                                        h.data_ptr(), N.stream_ptr(radial.device)), "tace_radial_mlp_fwd")
     _t1(tok, (E, n_in, n_layers))
-    return h, z_t
+    return h
 
 
-def launch_mlp_hidden_bwd(z_t, gh, weights, n_in: int) -> torch.Tensor:
-    n_layers, E, _ = z_t.shape
-    _req(gh, "g_h", z_t.dtype, (E, 64))
-    g = torch.empty(E, n_in, dtype=z_t.dtype, device=z_t.device)
+def launch_mlp_hidden_bwd(radial, gh, weights, n_layers: int) -> torch.Tensor:
+    """grad of ``radial`` from the grad of the last hidden activations."""
+    E, n_in = radial.shape
+    _req(gh, "g_h", radial.dtype, (E, 64))
+    g = torch.empty(E, n_in, dtype=radial.dtype, device=radial.device)
     tok = _t0("radial_mlp_bwd")
-    N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(z_t.dtype), z_t.data_ptr(), gh.data_ptr(), E, n_in, n_layers,
-                                        weights.data_ptr(), g.data_ptr(), N.stream_ptr(z_t.device)),
+    N.check(N.lib().tace_radial_mlp_bwd(N.dtype_code(radial.dtype), radial.data_ptr(), gh.data_ptr(), E, n_in,
+                                        n_layers, weights.data_ptr(), g.data_ptr(), N.stream_ptr(radial.device)),
             "tace_radial_mlp_bwd")
     _t1(tok, (E, n_in, n_layers))
     return g
@@ -892,15 +892,15 @@ def launch_mlp_hidden_bwd(z_t, gh, weights, n_in: int) -> torch.Tensor:
 class _RadialMlp(torch.autograd.Function):
     @staticmethod
     def forward(ctx, radial, weights, n_layers: int):
-        h, z_t = launch_mlp_hidden_fwd(radial, weights, n_layers)
-        ctx.save_for_backward(z_t, weights)
-        ctx.n_in = radial.shape[1]
+        h = launch_mlp_hidden_fwd(radial, weights, n_layers)
+        ctx.save_for_backward(radial, weights)
+        ctx.n_layers = n_layers
         return h
 
     @staticmethod
     def backward(ctx, gh):
-        z_t, weights = ctx.saved_tensors
-        return launch_mlp_hidden_bwd(z_t, gh.contiguous(), weights, ctx.n_in), None, None
+        radial, weights = ctx.saved_tensors
+        return launch_mlp_hidden_bwd(radial, gh.contiguous(), weights, ctx.n_layers), None, None
 
 
 def launch_mlp_out_f32(h, W, alpha: float) -> torch.Tensor:

@@ -292,7 +292,7 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     receiver sums (None without ``need_out``: a recompute for the backward)
     and, with ``save``, what the backward needs."""
     L, H, A = P.lmax, P.H, P.A
-    h, z_t = ops.launch_mlp_hidden_fwd(R, P.mlp_flat, P.mlp_layers)
+    h = ops.launch_mlp_hidden_fwd(R, P.mlp_flat, P.mlp_layers)
     if h.dtype == torch.float32:
         w = ops.launch_mlp_out_f32(h, P.mlp_W, P.mlp_alpha)
     else:
@@ -310,7 +310,7 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     mb = [P.mm(o[m], P.d_T[m], P.d_b if m == 0 else None) for m in range(L + 1)]
     del o
     out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H) if need_out else None
-    return out, ((z_t, w, query, key, rp, alpha, ys, mb) if save else None)
+    return out, ((w, query, key, rp, alpha, ys, mb) if save else None)
 
 
 def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, dst_out, recv_rows, saved,
@@ -322,7 +322,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     L, H, A = P.lmax, P.H, P.A
     if saved is None:
         _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True, need_out=False)
-    z_t, w, q, k, rp, alpha, ys, mb = saved
+    w, q, k, rp, alpha, ys, mb = saved
     gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16)
     go = [P.mm_grad(gm[m], P.d_N[m]) for m in range(L + 1)]
     del gm
@@ -344,7 +344,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     ops.rows_accumulate(g2, gxs.view(E, -1), *ops.sender_csr(rs, Nr))
     del gxs
     gh = torch.mm(gw, P.mlp_WT_scaled)
-    gR += ops.launch_mlp_hidden_bwd(z_t, gh, P.mlp_flat, R.shape[1])
+    gR += ops.launch_mlp_hidden_bwd(R, gh, P.mlp_flat, P.mlp_layers)
     return gR, gW.add_(gW_in)
 
 

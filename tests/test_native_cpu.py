@@ -91,3 +91,30 @@ def test_generated_contraction_order_matches_oracle(in1, lmax):
     np.testing.assert_allclose(gx, gx_o.numpy(), rtol=1e-11, atol=1e-11)
     np.testing.assert_allclose(gw.reshape(E, -1), gw_o.numpy(), rtol=1e-11, atol=1e-11)
     np.testing.assert_allclose(gy, gy_o.numpy(), rtol=1e-11, atol=1e-11)
+
+
+def test_kernel_parts_partition_the_paths():
+    """The part splits of the generated kernels: every path in exactly one
+    part; a part of the radial-fused uvu kernels and of the uuu backward
+    holds whole in1 blocks (so each grad-x row block comes from one part);
+    the uuu backward's parts respect their component cap and only products
+    with many outputs are split; the registry records the part counts the
+    launchers size their grids and workspaces with."""
+    reg = open(os.path.join(ROOT, "tace_amd", "csrc", "gen", "registry.inc")).read()
+    for v in codegen.all_variants():
+        if v.kind == "uvu":
+            parts = [v._part_paths([b]) for b in v.rtp_parts()]
+            assert sorted(p for ps in parts for p in ps) == list(range(len(v.paths))), v.name
+            assert f"{len(v.rtp_parts())}, L_{v.name}_rfwd, L_{v.name}_rbwd" in reg, v.name
+        else:
+            parts = v.uuu_parts()
+            blocks = [b for bs in parts for b in bs]
+            assert len(blocks) == len(set(blocks)), v.name
+            covered = sorted(p for p in range(len(v.paths)) if v.path_blocks[p][0] in blocks)
+            assert covered == list(range(len(v.paths))), v.name
+            if v.DO <= 128:
+                assert len(parts) == 1, v.name
+            else:
+                for bs in parts:
+                    assert len(bs) == 1 or sum(v.d1[b] for b in bs) <= 40, (v.name, bs)
+            assert reg.count(f"L_{v.name}_bwd_d, 0, nullptr, nullptr, {len(parts)}}}") == 1, v.name

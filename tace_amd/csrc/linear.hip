@@ -118,25 +118,9 @@ __global__ __launch_bounds__(256) void k_seg_linear(const T* __restrict__ x, T* 
   }
 }
 
-// float32 on MFMA: 4 waves in a 2 x 2 grid, each owning WM x WN blocks of
-// 16 x 16 (v_mfma_f32_16x16x4f32), so a tile is (32 WM) x (32 WN); the
-// library runs 128 x 128 (4, 4) at 2 waves per SIMD.  (256 x 128 and 128 x 256
-// tiles halve the weight or input re-reads of config 4's linears but need
-// ~350 registers per lane, 1 wave per SIMD, and measured 12-20% slower.)  A stages through LDS k-contiguous (As[row][k]) in chunks of 32
-// k; since the sum over k is order free, in MFMA step s lane l supplies
-// A[row][4 (l/16) + s] of a 16-k half, so it reads its four k values of a
-// fragment as one 16-byte LDS load.  B keeps the layout of its source:
-// k-contiguous (Bt[col][k], one 16-byte read per fragment) for the input
-// gradient, whose W^T rows are W's k-contiguous rows, and column-contiguous
-// (Bn[k][col], four 4-byte reads) for the forward, whose W [k, n] rows run
-// along the columns -- every global load is a 16-byte load and no staging
-// store transposes.  The next chunk's global loads are issued before the
-// current chunk's MFMAs and land in registers, so memory latency overlaps the
-// matrix work.  Tiles are taken XCD-grouped: workgroup b runs tile (b % 8) *
-// per + b / 8, so XCD k works through a contiguous stretch of the table (the
-// column tiles of one row tile, the row tiles of one species' weight) and
-// shares them in its L2.
-constexpr int MK = 32, MPAD = 4, NPAD = 4;
+// Global loads of the float32 MFMA path (k_seg_linear_bf16x3 below): every
+// load is a 16-byte load, and the next 32-k chunk's loads are issued before
+// the current chunk's MFMAs, so memory latency overlaps the matrix work.
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 // one 16-byte load of p[0..3], or the first lim (< 4) elements and zeros
@@ -171,51 +155,119 @@ __device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k
   }
 }
 
-template <int R>
-__device__ __forceinline__ void seg_store_k(float* lds, int stride, int t, const f4* v, float sc) {
+// float32 as three bfloat16 terms on the bf16 MFMA (v_mfma_f32_16x16x32_bf16,
+// 2.3 PFLOP/s against 0.15 for the float32 MFMA).  Each operand v is split
+// with round-to-nearest-even into v0 = bf16(v), v1 = bf16(v - v0), v2 =
+// bf16(v - v0 - v1).  The split is exact, v = v0 + v1 + v2: v - v0 is exact
+// in float32 and holds at most 16 significant bits, |v1| <= 2^-8 |v|, and
+// v - v0 - v1 holds at most 8, which bf16 keeps (exponent range aside).  A
+// product is the six terms a_i b_j with i + j <= 2; the three left out
+// (a1 b2, a2 b1, a2 b2) total at most ~2^-23 |a b|, the size of float32's own
+// rounding of a product, and every kept term is exact in the float32
+// accumulator's multiply, so the sums carry the rounding of a float32 GEMM.
+// The terms are added smallest first.
+//
+// A tile is 128 x 128: 4 waves in a 2 x 2 grid, each owning 4 x 4 blocks of
+// 16 x 16.  Tiles are taken XCD-grouped: workgroup b runs tile (b % 8) * per
+// + b / 8, so XCD k works through a contiguous stretch of the table (the
+// column tiles of one row tile, the row tiles of one species' weight) and
+// shares them in its L2.  The split happens once per element at the LDS
+// store, into three planes stored k-contiguous (rows of 32 k + 8 pad:
+// 80-byte rows, so the 16 rows of a fragment read fall on distinct banks),
+// and an MFMA fragment (8 k of one row) is one 16-byte LDS read.  The
+// forward's W [k, n] is loaded two k rows per thread and stored transposed as
+// (k, k + 1) pairs.
+constexpr int SB_K = 32, SB_STR = SB_K + 8;
+typedef __bf16 sb_bf8 __attribute__((ext_vector_type(8)));
+
+typedef __bf16 sb_bf2 __attribute__((ext_vector_type(2)));
+typedef float sb_f2 __attribute__((ext_vector_type(2)));
+
+// two values -> their three terms as packed bf16 pairs (h[p] = plane p of
+// (v.x, v.y), low half v.x); the float -> bf16 conversions round to nearest
+// even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ void sb_split2(sb_f2 v, unsigned* h) {
 #pragma unroll
-  for (int rr = 0; rr < R / 128; ++rr)
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *(f4*)&lds[((t >> 1) + 128 * rr) * stride + 16 * (t & 1) + 4 * q] = v[4 * rr + q] * sc;
+  for (int p = 0; p < 3; ++p) {
+    const sb_bf2 b = __builtin_convertvector(v, sb_bf2);
+    h[p] = __builtin_bit_cast(unsigned, b);
+    if (p < 2) v -= sb_f2{__uint_as_float(h[p] << 16), __uint_as_float(h[p] & 0xffff0000u)};
+  }
 }
 
-// 32 k rows x Cn columns of W [k, n] (columns c0 ..): thread t holds k row
-// t % 32 and columns 4 (t/32) + 32 q + 128 cc (q < 4, cc < Cn/128)
-template <int Cn>
-__device__ __forceinline__ void seg_load_n(const float* __restrict__ wb, int k, int n, int c0, int k0, bool vec, int t,
-                                           f4* v) {
-  const int kk = k0 + (t & 31), cb = c0 + 4 * (t >> 5);
-  const float* p = wb + (int64_t)kk * n + cb;
+// rows of 16 k (four f4 of one row, k-contiguous) -> planes p[row][kofs ..]
+__device__ __forceinline__ void sb_store_k16(unsigned short* lds, int plane, int off, const f4* v, float sc) {
+  typedef unsigned u4v __attribute__((ext_vector_type(4)));
+  u4v o[3][2];
 #pragma unroll
-  for (int cc = 0; cc < Cn / 128; ++cc)
+  for (int q = 0; q < 4; ++q)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int left = n - (cb + 32 * q + 128 * cc);
-      v[4 * cc + q] = seg_ld4(p + 32 * q + 128 * cc, kk < k && vec && left >= 4, kk < k && left > 0, left);
+    for (int e = 0; e < 2; ++e) {
+      unsigned h[3];
+      sb_split2(sb_f2{v[q][2 * e], v[q][2 * e + 1]} * sc, h);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) o[p][q >> 1][2 * (q & 1) + e] = h[p];
     }
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    *(u4v*)&lds[p * plane + off] = o[p][0];
+    *(u4v*)&lds[p * plane + off + 8] = o[p][1];
+  }
 }
 
-template <int Cn>
-__device__ __forceinline__ void seg_store_n(float* lds, int t, const f4* v, float sc) {
+// 32 k rows x 128 columns of W [k, n] from column c0: thread t holds k rows
+// k0 + 2 (t/16) and the next, columns 4 (t%16) + 64 q (q < 2) -- v[2 q + r]
+// for row 2 (t/16) + r
+__device__ __forceinline__ void sb_load_n(const float* __restrict__ wb, int k, int n, int c0, int k0, bool vec, int t,
+                                          f4* v) {
+  const int cb = c0 + 4 * (t & 15);
 #pragma unroll
-  for (int cc = 0; cc < Cn / 128; ++cc)
+  for (int r = 0; r < 2; ++r) {
+    const int kk = k0 + 2 * (t >> 4) + r;
+    const float* p = wb + (int64_t)kk * n + cb;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *(f4*)&lds[(t & 31) * (Cn + NPAD) + 4 * (t >> 5) + 32 * q + 128 * cc] = v[4 * cc + q] * sc;
+    for (int q = 0; q < 2; ++q) {
+      const int left = n - (cb + 64 * q);
+      v[2 * q + r] = seg_ld4(p + 64 * q, kk < k && vec && left >= 4, kk < k && left > 0, left);
+    }
+  }
 }
 
-template <int WM, int WN>
-__global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict__ x, float* __restrict__ y,
-                                                         const float* __restrict__ w, const float* __restrict__ bias,
-                                                         const int64_t* __restrict__ tiles,
-                                                         const int64_t* __restrict__ contribs,
-                                                         const double* __restrict__ scales, float alpha,
-                                                         int n_tiles, int per) {
-  constexpr int TR = 32 * WM, TC = 32 * WN, BT = MK + MPAD;
-  constexpr int BS = (TC * BT > MK * (TC + NPAD)) ? TC * BT : MK * (TC + NPAD);
-  __shared__ float As[TR * BT];
-  __shared__ float Bs[BS];   // Bt[TC][MK + MPAD] or Bn[MK][TC + NPAD]
+// Lane t writes its four columns 4 (t%16) + e in the order e = (e' + r) & 3,
+// r = (t/4) & 3, so that a store instruction (fixed e') spreads the 16 lanes
+// of a row group over distinct banks instead of four.
+__device__ __forceinline__ void sb_store_n(unsigned short* lds, int plane, int t, const f4* v, float sc) {
+  const int kp = 2 * (t >> 4), r = (t >> 2) & 3;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    f4 u0, u1;   // v rotated left by r
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const f4 x0 = v[2 * q], x1 = v[2 * q + 1];
+      u0[e] = r == 0 ? x0[e] : r == 1 ? x0[(e + 1) & 3] : r == 2 ? x0[(e + 2) & 3] : x0[(e + 3) & 3];
+      u1[e] = r == 0 ? x1[e] : r == 1 ? x1[(e + 1) & 3] : r == 2 ? x1[(e + 2) & 3] : x1[(e + 3) & 3];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      unsigned h[3];   // (k, k + 1) of one column
+      sb_split2(sb_f2{u0[e], u1[e]} * sc, h);
+      const int col = 4 * (t & 15) + 64 * q + ((e + r) & 3);
+#pragma unroll
+      for (int p = 0; p < 3; ++p) *(unsigned*)&lds[p * plane + col * SB_STR + kp] = h[p];
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restrict__ x, float* __restrict__ y,
+                                                           const float* __restrict__ w,
+                                                           const float* __restrict__ bias,
+                                                           const int64_t* __restrict__ tiles,
+                                                           const int64_t* __restrict__ contribs,
+                                                           const double* __restrict__ scales, float alpha,
+                                                           int n_tiles, int per) {
+  constexpr int WM = 4, WN = 4, TR = 128, TC = 128, PL = 128 * SB_STR;   // plane size (bf16)
+  __shared__ __attribute__((aligned(16))) unsigned short As[3 * PL];
+  __shared__ __attribute__((aligned(16))) unsigned short Bs[3 * PL];
   const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
   if (tile >= n_tiles) return;
   const int64_t* td = tiles + 8 * (int64_t)tile;
@@ -224,14 +276,14 @@ __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict
   const int64_t bias_off = td[4];
   const int cb = (int)td[5], ce = (int)td[6];
   const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
-  const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 16 * WN;   // the wave's block of the tile
-  const int fr = lane & 15, fg = lane >> 4;                        // fragment row/col, k group
-  constexpr int NA = TR / 32, NB = TC / 32;   // f4 per thread per chunk
+  const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 16 * WN;
+  const int fr = lane & 15, fg = lane >> 4;
   f4 acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  const int soff = (t >> 1) * SB_STR + 16 * (t & 1);   // this thread's k16 run of a k-contiguous plane
 
   for (int c = cb; c < ce; ++c) {
     const int64_t* cd = contribs + 4 * (int64_t)c;
@@ -242,47 +294,47 @@ __global__ __launch_bounds__(256) void k_seg_linear_mfma(const float* __restrict
     const float sc = (float)scales[c];
     const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
     const bool wvec = ((((uintptr_t)wb) & 15) == 0) && (((trans ? k : n) & 3) == 0) && ((c0 & 3) == 0);
-    const float* __restrict__ wt = wb + (int64_t)c0 * k;   // W^T tile rows (trans)
-    f4 a[NA], b[NB];
-    seg_load_k<TR>(xa, k, 0, rows, xvec, t, a);
-    if (trans) seg_load_k<TC>(wt, k, 0, n - c0, wvec, t, b);
-    else seg_load_n<TC>(wb, k, n, c0, 0, wvec, t, b);
-    for (int k0 = 0; k0 < k; k0 += MK) {
-      seg_store_k<TR>(As, BT, t, a, 1.f);
-      if (trans) seg_store_k<TC>(Bs, BT, t, b, sc);
-      else seg_store_n<TC>(Bs, t, b, sc);
-      __syncthreads();
-      if (k0 + MK < k) {   // next chunk in flight during this chunk's MFMAs
-        seg_load_k<TR>(xa, k, k0 + MK, rows, xvec, t, a);
-        if (trans) seg_load_k<TC>(wt, k, k0 + MK, n - c0, wvec, t, b);
-        else seg_load_n<TC>(wb, k, n, c0, k0 + MK, wvec, t, b);
-      }
+    const float* __restrict__ wt = wb + (int64_t)c0 * k;
+    f4 a[4], b[4];
+    auto load = [&](int kc, f4* a, f4* b) {
+      seg_load_k<TR>(xa, k, kc, rows, xvec, t, a);
+      if (trans) seg_load_k<TC>(wt, k, kc, n - c0, wvec, t, b);
+      else sb_load_n(wb, k, n, c0, kc, wvec, t, b);
+    };
+    auto stage = [&](const f4* a, const f4* b) {
+      sb_store_k16(As, PL, soff, a, 1.f);
+      if (trans) sb_store_k16(Bs, PL, soff, b, sc);
+      else sb_store_n(Bs, PL, t, b, sc);
+    };
+    auto mma = [&]() {
+      sb_bf8 af[3][WM];
 #pragma unroll
-      for (int h = 0; h < MK; h += 16) {
-        f4 af[WM], bf[WN];
+      for (int p = 0; p < 3; ++p)
 #pragma unroll
-        for (int i = 0; i < WM; ++i) af[i] = *(const f4*)&As[(wr + 16 * i + fr) * BT + h + 4 * fg];
-        if (trans) {
+        for (int i = 0; i < WM; ++i) af[p][i] = *(const sb_bf8*)&As[p * PL + (wr + 16 * i + fr) * SB_STR + 8 * fg];
 #pragma unroll
-          for (int j = 0; j < WN; ++j) bf[j] = *(const f4*)&Bs[(wc + 16 * j + fr) * BT + h + 4 * fg];
-        } else {
+      for (int j = 0; j < WN; ++j) {
+        sb_bf8 bf[3];
 #pragma unroll
-          for (int j = 0; j < WN; ++j)
+        for (int p = 0; p < 3; ++p) bf[p] = *(const sb_bf8*)&Bs[p * PL + (wc + 16 * j + fr) * SB_STR + 8 * fg];
+        // (i, j) terms a_i b_j, smallest first: 11, 02, 20, 01, 10, 00
+        constexpr int TA[6] = {1, 0, 2, 0, 1, 0}, TB[6] = {1, 2, 0, 1, 0, 0};
 #pragma unroll
-            for (int s2 = 0; s2 < 4; ++s2) bf[j][s2] = Bs[(h + 4 * fg + s2) * (TC + NPAD) + wc + 16 * j + fr];
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 4; ++s2)
+        for (int u = 0; u < 6; ++u)
 #pragma unroll
           for (int i = 0; i < WM; ++i)
-#pragma unroll
-            for (int j = 0; j < WN; ++j)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][s2], bf[j][s2], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[TA[u]][i], bf[TB[u]], acc[i][j], 0, 0, 0);
       }
+    };
+    load(0, a, b);
+    for (int k0 = 0; k0 < k; k0 += SB_K) {
+      stage(a, b);
+      __syncthreads();
+      if (k0 + SB_K < k) load(k0 + SB_K, a, b);   // next chunk in flight during this chunk's MFMAs
+      mma();
       __syncthreads();
     }
   }
-  // D lane l, register q of block (i, j) = tile row wr + 16 i + 4 (l/16) + q, column wc + 16 j + l%16
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
     const int col = c0 + wc + 16 * j + fr;
@@ -315,7 +367,7 @@ extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, 
   if (mfma) {
     const int per = (int)((n_tiles + 7) / 8);
     const dim3 g8((unsigned)(8 * per));
-    hipLaunchKernelGGL((k_seg_linear_mfma<4, 4>), g8, block, 0, s, (const float*)x, (float*)y, (const float*)w,
+    hipLaunchKernelGGL(k_seg_linear_bf16x3, g8, block, 0, s, (const float*)x, (float*)y, (const float*)w,
                        (const float*)bias, tiles, contribs, scales, (float)alpha, (int)n_tiles, per);
   } else if (dtype == TACE_F32)
     hipLaunchKernelGGL(k_seg_linear<float>, grid, block, 0, s, (const float*)x, (float*)y, (const float*)w,

@@ -123,7 +123,8 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 RADIAL_FUSED_TP = False
 
 SEG_LINEAR_MIN_RANGES = 3
-# tile edge of the float32 segmented GEMM: 128 = MFMA kernel, 64 = FMA kernel
+# tile edge of the float32 segmented GEMM: 128 = MFMA kernel (float32 as three
+# bf16 terms), 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128
 
 

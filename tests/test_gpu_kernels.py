@@ -517,6 +517,49 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts
     close(gw, gw_want, dtype, "seg linear grad w")
 
 
+def test_seg_linear_f32_error_matches_float32_gemm(cuda):
+    """The float32 segmented GEMM (three-term bfloat16 split on the bf16
+    MFMA) against the float64 truth of the same float32 inputs, next to the
+    error of a float32 CPU GEMM of those inputs: long k (2048, 1100) so that
+    the rounding of the sums dominates, inputs spanning 2^-20 .. 2^20 so that
+    a split that dropped the third term (a 16-bit significand) would be off by
+    ~2^-17 instead of ~2^-24.  The forward and the input gradient."""
+    from tace_amd import model as pm
+    counts = [300, 5, 130]
+    irr_in, irr_out = "2048x0e+1100x1o", "256x0e+192x1o"
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).float()
+    g = torch.Generator().manual_seed(11)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S, bias=False)
+
+    def spread(shape):
+        return (torch.randn(shape, generator=g, dtype=torch.float64)
+                * torch.exp2(torch.randint(-20, 21, shape, generator=g).double())).float()
+    with torch.no_grad():
+        lin.weight.copy_(spread(lin.weight.shape))
+    x, go = spread((Z, lin.lay.dim_in)), spread((Z, lin.lay.dim_out))
+    w64 = lin.weight.detach().double()
+    xr = x.double().requires_grad_(True)
+    want = _element_linear_reference(xr, w64, torch.zeros(S, 256, dtype=torch.float64), irr_in, irr_out, species, 1.0)
+    (gx_want,) = torch.autograd.grad(want, xr, go.double())
+    xc = x.clone().requires_grad_(True)
+    cpu = _element_linear_reference(xc, lin.weight.detach(), torch.zeros(S, 256), irr_in, irr_out, species, 1.0)
+    (gx_cpu,) = torch.autograd.grad(cpu, xc, go)
+    sp = pm.SpeciesPlan(attrs.to(cuda))
+    xg = x.to(cuda).requires_grad_(True)
+    got = lin.to(cuda)(xg, sp, 1.0)
+    (gx,) = torch.autograd.grad(got, xg, go.to(cuda))
+
+    def err(a, b):   # max |a - b| over the row's scale, per output row block
+        a, b = a.detach().double().cpu(), b.detach().double()
+        return ((a - b).abs().amax(1) / b.abs().amax(1).clamp_min(1e-300)).max().item()
+    for what, gpu, ref, truth in (("fwd", got, cpu, want), ("grad x", gx, gx_cpu, gx_want)):
+        e_gpu, e_cpu = err(gpu, truth), err(ref, truth)
+        print(f"seg linear {what}: rel err {e_gpu:.3e} (float32 CPU GEMM {e_cpu:.3e})")
+        assert e_gpu < 4 * e_cpu + 1e-7, f"{what}: {e_gpu:.3e} vs float32 GEMM {e_cpu:.3e}"
+
+
 # ------------------------------------------------------ segmented row sums ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("width", [1152, 37])

@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include "../../include/tace_hip.h"
+#include "bf16x3.h"
 
 int tace_fail_msg(const char* msg);   // tace_hip.hip
 int tace_check_launch(const char* what);
@@ -156,16 +157,9 @@ __device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k
 }
 
 // float32 as three bfloat16 terms on the bf16 MFMA (v_mfma_f32_16x16x32_bf16,
-// 2.3 PFLOP/s against 0.15 for the float32 MFMA).  Each operand v is split
-// with round-to-nearest-even into v0 = bf16(v), v1 = bf16(v - v0), v2 =
-// bf16(v - v0 - v1).  The split is exact, v = v0 + v1 + v2: v - v0 is exact
-// in float32 and holds at most 16 significant bits, |v1| <= 2^-8 |v|, and
-// v - v0 - v1 holds at most 8, which bf16 keeps (exponent range aside).  A
-// product is the six terms a_i b_j with i + j <= 2; the three left out
-// (a1 b2, a2 b1, a2 b2) total at most ~2^-23 |a b|, the size of float32's own
-// rounding of a product, and every kept term is exact in the float32
-// accumulator's multiply, so the sums carry the rounding of a float32 GEMM.
-// The terms are added smallest first.
+// 2.3 PFLOP/s against 0.15 for the float32 MFMA): both operands split into
+// three bf16 terms, six products per pair (bf16x3.h: the split is exact and
+// the sums carry the rounding of a float32 GEMM).
 //
 // A tile is 128 x 128: 4 waves in a 2 x 2 grid, each owning 4 x 4 blocks of
 // 16 x 16.  Tiles are taken XCD-grouped: workgroup b runs tile (b % 8) * per
@@ -178,23 +172,6 @@ __device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k
 // forward's W [k, n] is loaded two k rows per thread and stored transposed as
 // (k, k + 1) pairs.
 constexpr int SB_K = 32, SB_STR = SB_K + 8;
-typedef __bf16 sb_bf8 __attribute__((ext_vector_type(8)));
-
-typedef __bf16 sb_bf2 __attribute__((ext_vector_type(2)));
-typedef float sb_f2 __attribute__((ext_vector_type(2)));
-
-// two values -> their three terms as packed bf16 pairs (h[p] = plane p of
-// (v.x, v.y), low half v.x); the float -> bf16 conversions round to nearest
-// even (v_cvt_pk_bf16_f32)
-__device__ __forceinline__ void sb_split2(sb_f2 v, unsigned* h) {
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    const sb_bf2 b = __builtin_convertvector(v, sb_bf2);
-    h[p] = __builtin_bit_cast(unsigned, b);
-    if (p < 2) v -= sb_f2{__uint_as_float(h[p] << 16), __uint_as_float(h[p] & 0xffff0000u)};
-  }
-}
-
 // rows of 16 k (four f4 of one row, k-contiguous) -> planes p[row][kofs ..]
 __device__ __forceinline__ void sb_store_k16(unsigned short* lds, int plane, int off, const f4* v, float sc) {
   typedef unsigned u4v __attribute__((ext_vector_type(4)));
@@ -204,7 +181,7 @@ __device__ __forceinline__ void sb_store_k16(unsigned short* lds, int plane, int
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       unsigned h[3];
-      sb_split2(sb_f2{v[q][2 * e], v[q][2 * e + 1]} * sc, h);
+      bx3_split2(bx3_f2{v[q][2 * e], v[q][2 * e + 1]} * sc, h);
 #pragma unroll
       for (int p = 0; p < 3; ++p) o[p][q >> 1][2 * (q & 1) + e] = h[p];
     }
@@ -250,7 +227,7 @@ __device__ __forceinline__ void sb_store_n(unsigned short* lds, int plane, int t
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       unsigned h[3];   // (k, k + 1) of one column
-      sb_split2(sb_f2{u0[e], u1[e]} * sc, h);
+      bx3_split2(bx3_f2{u0[e], u1[e]} * sc, h);
       const int col = 4 * (t & 15) + 64 * q + ((e + r) & 3);
 #pragma unroll
       for (int p = 0; p < 3; ++p) *(unsigned*)&lds[p * plane + col * SB_STR + kp] = h[p];
@@ -307,23 +284,21 @@ __global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restri
       else sb_store_n(Bs, PL, t, b, sc);
     };
     auto mma = [&]() {
-      sb_bf8 af[3][WM];
+      bx3_bf8 af[3][WM];
 #pragma unroll
       for (int p = 0; p < 3; ++p)
 #pragma unroll
-        for (int i = 0; i < WM; ++i) af[p][i] = *(const sb_bf8*)&As[p * PL + (wr + 16 * i + fr) * SB_STR + 8 * fg];
+        for (int i = 0; i < WM; ++i) af[p][i] = *(const bx3_bf8*)&As[p * PL + (wr + 16 * i + fr) * SB_STR + 8 * fg];
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        sb_bf8 bf[3];
+        bx3_bf8 bf[3];
 #pragma unroll
-        for (int p = 0; p < 3; ++p) bf[p] = *(const sb_bf8*)&Bs[p * PL + (wc + 16 * j + fr) * SB_STR + 8 * fg];
-        // (i, j) terms a_i b_j, smallest first: 11, 02, 20, 01, 10, 00
-        constexpr int TA[6] = {1, 0, 2, 0, 1, 0}, TB[6] = {1, 2, 0, 1, 0, 0};
+        for (int p = 0; p < 3; ++p) bf[p] = *(const bx3_bf8*)&Bs[p * PL + (wc + 16 * j + fr) * SB_STR + 8 * fg];
 #pragma unroll
-        for (int u = 0; u < 6; ++u)
+        for (int u = 0; u < 6; ++u)   // the six terms a_i b_j, smallest first
 #pragma unroll
           for (int i = 0; i < WM; ++i)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[TA[u]][i], bf[TB[u]], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[BX3_TA[u]][i], bf[BX3_TB[u]], acc[i][j], 0, 0, 0);
       }
     };
     load(0, a, b);

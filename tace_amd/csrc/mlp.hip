@@ -21,6 +21,8 @@
 // layout holds a column per lane, the A operand needs a row); h is stored
 // straight from the accumulators, two 128-byte row segments per store.  The per-thread kernels below stay for float64.
 #include <hip/hip_runtime.h>
+
+#include "bf16x3.h"
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -329,20 +331,22 @@ __global__ __launch_bounds__(256) void k_mlp_bwd_mfma(const float* __restrict__ 
 
 // ------------------------------------------------------------- last layer --
 // out[e, n] = alpha sum_k h[e, k] W[k, n] with K = 64 (the wide, linear last
-// layer: E ~ 1e6 edges x N ~ 3e3 weights, output-write and fp32-MFMA bound).
-// Each wavefront owns 64 output columns (two 32-column blocks) and keeps
-// their 64 x 64 slice of W in registers as v_mfma_f32_32x32x2f32 B fragments
-// for its whole life; it then streams 32-edge blocks: A fragments from h (one
-// 128-byte row segment per lane), 32 k-steps x 2 column blocks of MFMA, and
-// the two 32 x 32 result tiles stored straight from the accumulators -- in
-// the 32 x 32 output layout every store instruction writes two whole
-// 128-byte row segments, so no transpose through LDS is needed; the stores
-// are non-temporal (the output is streamed once to HBM).  K is permuted
-// inside each step (lane half q of step s holds k = 32 q + s) so that a
-// lane's A values are one contiguous row segment.  Workgroups (4 waves = 256
-// columns) that share an edge chunk are placed on one XCD (blockIdx
-// round-robins over the 8 XCDs), so the chunk's h rows are read from HBM
-// about once.
+// layer: E ~ 1e6 edges x N ~ 3e3 weights, output-write bound).  float32 runs
+// on the bf16 MFMA (v_mfma_f32_32x32x16_bf16) with both operands split into
+// three bf16 terms (bf16x3.h: exact split, six products, float32 rounding).
+// Each wavefront owns 64 output columns (two 32-column blocks) and keeps the
+// three terms of their 64 x 64 slice of W in registers as B fragments for its
+// whole life; it then streams 32-edge blocks: A from h (one 128-byte row
+// segment per lane, split once), 4 k-steps x 2 column blocks x 6 terms of
+// MFMA, and the two 32 x 32 result tiles stored straight from the
+// accumulators -- in the 32 x 32 output layout every store instruction writes
+// two whole 128-byte row segments, so no transpose through LDS is needed; the
+// stores are non-temporal (the output is streamed once to HBM).  K is
+// permuted (lane half q of step s holds k = 32 q + 8 s .. + 7) so that a
+// lane's A values are one contiguous row segment; B uses the same k for the
+// same lane and item.  Workgroups (4 waves = 256 columns) that share an edge
+// chunk are placed on one XCD (blockIdx round-robins over the 8 XCDs), so the
+// chunk's h rows are read from HBM about once.
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void load_a_frag32(const float* __restrict__ h, int64_t er, int64_t E, int q, float* a) {
@@ -369,31 +373,40 @@ __global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h
   const int lane = (int)threadIdx.x & 63, wave = (int)threadIdx.x >> 6;
   const int i = lane & 31, q = lane >> 5;
   const int col0 = ct * 256 + wave * 64;
-  // B fragments: lane (i, q) of step s holds W[32 q + s][col0 + 32 cb + i]
-  float bf[32][2];
+  // B fragments: lane (i, q) of step s, item j holds W[32 q + 8 s + j][col0 + 32 cb + i]
+  bx3_bf8 bw[4][2][3];
 #pragma unroll
-  for (int s = 0; s < 32; ++s)
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int c = col0 + 32 * cb + i;
-      bf[s][cb] = c < N ? Wm[(int64_t)(32 * q + s) * N + c] : 0.0f;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = c < N ? Wm[(int64_t)(32 * q + 8 * s + j) * N + c] : 0.0f;
+      bx3_split8(v, bw[s][cb]);
     }
   const int64_t e_begin = chunk * edges_per_chunk;
   const int64_t e_end = e_begin + edges_per_chunk < E ? e_begin + edges_per_chunk : E;
-  float a[32], an[32];
+  float a[32];
   load_a_frag32(h, e_begin + i, E, q, a);
   for (int64_t e0 = e_begin; e0 < e_end; e0 += 32) {
+    bx3_bf8 at[4][3];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) bx3_split8(a + 8 * s, at[s]);
     // next block's A fragment in flight during this block's MFMAs
-    load_a_frag32(h, e0 + 32 < e_end ? e0 + 32 + i : E, E, q, an);
+    load_a_frag32(h, e0 + 32 < e_end ? e0 + 32 + i : E, E, q, a);
     f16_t acc[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
 #pragma unroll
-    for (int s = 0; s < 32; ++s)
+    for (int u = 0; u < 6; ++u)
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[s], bf[s][cb], acc[cb], 0, 0, 0);
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[s][BX3_TA[u]], bw[s][cb][BX3_TB[u]], acc[cb], 0, 0, 0);
     // accumulator r of lane (i, q): row 8 (r / 4) + 4 q + r % 4, column i
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -404,8 +417,6 @@ __global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h
         if (row < e_end && c < N) __builtin_nontemporal_store(alpha * acc[cb][r], out + row * N + c);
       }
     }
-#pragma unroll
-    for (int s = 0; s < 32; ++s) a[s] = an[s];
   }
 }
 

@@ -308,8 +308,9 @@ class mlpLinear(torch.nn.Module):
 class MLP(torch.nn.Module):
     """Radial MLP (``mlp.py:136-191``): alpha = gain/sqrt(h_in), SiLU between
     layers.  Width-64 hidden layers run in one HIP kernel per direction
-    (``ops.radial_mlp_hidden``) and the wide last layer on an fp32-MFMA kernel
-    (``ops.radial_mlp_out``), the weights as constants: the inference path
+    (``ops.radial_mlp_hidden``) and the wide last layer on a float32 MFMA
+    kernel (three-term bf16 split, ``ops.radial_mlp_out``), the weights as
+    constants: the inference path
     freezes parameters."""
 
     def __init__(self, dims):

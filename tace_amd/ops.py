@@ -904,7 +904,8 @@ class _RadialMlp(torch.autograd.Function):
 
 
 def launch_mlp_out_f32(h, W, alpha: float) -> torch.Tensor:
-    """alpha h @ W on the fp32-MFMA kernel (h [E, 64], W [64, n_out])."""
+    """alpha h @ W in float32 on the bf16 MFMA, both operands split into three
+    bf16 terms (h [E, 64], W [64, n_out])."""
     E = h.shape[0]
     _req(h, "h", torch.float32, (E, 64))
     _req(W, "weight", torch.float32, (64, W.shape[1]))

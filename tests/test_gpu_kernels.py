@@ -560,6 +560,32 @@ def test_seg_linear_f32_error_matches_float32_gemm(cuda):
         assert e_gpu < 4 * e_cpu + 1e-7, f"{what}: {e_gpu:.3e} vs float32 GEMM {e_cpu:.3e}"
 
 
+def test_mlp_out_f32_error_matches_float32_gemm(cuda):
+    """The radial MLP's last layer (three-term bfloat16 split on the bf16
+    MFMA) against the float64 truth of the same float32 inputs, next to a
+    float32 CPU GEMM's error: inputs spanning 2^-20 .. 2^20, so that a split
+    that dropped its third term (a 16-bit significand) would be off by ~2^-17
+    instead of ~2^-24; a ragged edge count (not a multiple of 32 or of the
+    1024-edge chunk) and a width that is not a multiple of 32 or 256."""
+    g = torch.Generator().manual_seed(3)
+    E, N = 2 * 1024 + 77, 600
+
+    def spread(shape):
+        return (torch.randn(shape, generator=g, dtype=torch.float64)
+                * torch.exp2(torch.randint(-20, 21, shape, generator=g).double())).float()
+    h, W = spread((E, 64)), spread((64, N))
+    alpha = 0.37
+    truth = alpha * (h.double() @ W.double())
+    cpu = alpha * (h @ W)
+    got = ops.launch_mlp_out_f32(h.to(cuda), W.to(cuda), alpha).double().cpu()
+
+    def err(a):   # per-row max error over the row's scale
+        return ((a.double() - truth).abs().amax(1) / truth.abs().amax(1).clamp_min(1e-300)).max().item()
+    e_gpu, e_cpu = err(got), err(cpu)
+    print(f"mlp out: rel err {e_gpu:.3e} (float32 CPU GEMM {e_cpu:.3e})")
+    assert e_gpu < 4 * e_cpu + 1e-8, f"{e_gpu:.3e} vs float32 GEMM {e_cpu:.3e}"
+
+
 # ------------------------------------------------------ segmented row sums ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("width", [1152, 37])

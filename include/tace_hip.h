@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 16
+#define TACE_HIP_ABI_VERSION 17
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -185,9 +185,16 @@ int tace_radial_mlp_fwd(int dtype, const void* radial, int64_t n_edges, int32_t 
 int tace_radial_mlp_bwd(int dtype, const void* radial, const void* g_h, int64_t n_edges, int32_t n_in,
                         int32_t n_layers, const void* weights, void* g_radial, void* stream);
 /* the last (linear) layer in float32: out [E, n_out] = alpha h [E, 64] @
- * weight [64, n_out] (row-major; h 16-byte aligned), on fp32 MFMA. */
+ * weight [64, n_out] (row-major; h 16-byte aligned), on the bf16 MFMA with
+ * both operands split exactly into three bf16 terms (float32 rounding).
+ *   tace_radial_mlp_out_bwd_f32: its input gradient (the backward of the
+ *   last Linear of mlp.py:136-191), g_h [E, 64] = alpha g_out [E, n_out] @
+ *   weight^T, the same way (g_out and weight 16-byte aligned when n_out is a
+ *   multiple of 4; weights are constants: no weight gradient). */
 int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
                             float* out, void* stream);
+int tace_radial_mlp_out_bwd_f32(const float* g_out, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
+                                float* g_h, void* stream);
 
 /* ---- per-species (element) linears
  * tace_seg_linear replaces the per-element o3.Linear of e3nnElementLinear

@@ -70,6 +70,7 @@ _SIGS = {
     "tace_radial_mlp_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_radial_mlp_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_radial_mlp_out_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
+    "tace_radial_mlp_out_bwd_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
     "tace_seg_linear": (_c_int, [_c_int, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_dbl, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),

@@ -420,6 +420,103 @@ __global__ __launch_bounds__(256) void k_mlp_out_f32(const float* __restrict__ h
   }
 }
 
+// The last layer's input gradient: g_h[e, c] = alpha sum_n g[e, n] W[c, n]
+// (c < 64; g [E, N] is the gradient of the layer's output).  float32 on the
+// bf16 MFMA (v_mfma_f32_32x32x16_bf16) with the exact three-term split of
+// bf16x3.h.  One wavefront per 32 edges and all 64 columns (two 32-column
+// blocks), four per workgroup; they stream N in 32-wide slabs: lane (i, q)
+// reads g[e0 + i][k0 + 16 q .. + 15] (each row's 128-byte slab segment over
+// the two lane halves), and the workgroup splits the slab of W (64 x 32, from
+// L2) once into three bf16 planes in LDS, from which lane (i, q) reads
+// W[32 cb + i][same k] -- step s item j of both operands is k = k0 + 16 q +
+// 8 s + j.  The next slab's loads are issued before the current slab's
+// MFMAs.  Read-bound on g.
+__device__ __forceinline__ void mlp_ld16(const float* __restrict__ row, int k, int N, bool ok, bool vec, float* v) {
+  if (ok && vec && k + 16 <= N) {
+    const f4_t* p = reinterpret_cast<const f4_t*>(row + k);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const f4_t t = p[u];
+      v[4 * u] = t[0]; v[4 * u + 1] = t[1]; v[4 * u + 2] = t[2]; v[4 * u + 3] = t[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = (ok && k + j < N) ? row[k + j] : 0.0f;
+  }
+}
+
+__device__ __forceinline__ void mlp_ld8(const float* __restrict__ row, int k, int N, bool vec, float* v) {
+  if (vec && k + 8 <= N) {
+    const f4_t* p = reinterpret_cast<const f4_t*>(row + k);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const f4_t t = p[u];
+      v[4 * u] = t[0]; v[4 * u + 1] = t[1]; v[4 * u + 2] = t[2]; v[4 * u + 3] = t[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = k + j < N ? row[k + j] : 0.0f;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_mlp_out_bwd_f32(const float* __restrict__ g, const float* __restrict__ Wm,
+                                                         int64_t E, int N, float alpha, float* __restrict__ gh) {
+  constexpr int BSTR = 40;                       // bf16 per LDS row: 32 k + 8 pad (80 bytes)
+  __shared__ __attribute__((aligned(16))) unsigned short Bp[3 * 64 * BSTR];   // term p, column c, k
+  const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int i = lane & 31, q = lane >> 5;
+  const int64_t e0 = ((int64_t)blockIdx.x * 4 + wave) * 32;
+  const int64_t er = e0 + i;
+  const bool rok = er < E;
+  const bool vec = (N & 3) == 0;
+  const float* __restrict__ grow = g + (rok ? er : 0) * (int64_t)N;
+  // the slab's W[c][k0 + kk .. + 7] for c = t / 4, kk = 8 (t % 4), split once per workgroup
+  const int wc = t >> 2, wk = 8 * (t & 3);
+  const float* __restrict__ wrow = Wm + (int64_t)wc * N;
+  f16_t acc[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
+  float a[16], w[8];
+  mlp_ld16(grow, 16 * q, N, rok, vec, a);
+  mlp_ld8(wrow, wk, N, vec, w);
+  for (int k0 = 0; k0 < N; k0 += 32) {
+    bx3_bf8 wt[3];
+    bx3_split8(w, wt);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) *(bx3_bf8*)&Bp[(p * 64 + wc) * BSTR + wk] = wt[p];
+    bx3_bf8 at[2][3];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) bx3_split8(a + 8 * s, at[s]);
+    __syncthreads();
+    if (k0 + 32 < N) {   // next slab in flight during this slab's MFMAs
+      mlp_ld16(grow, k0 + 32 + 16 * q, N, rok, vec, a);
+      mlp_ld8(wrow, k0 + 32 + wk, N, vec, w);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        bx3_bf8 bt[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) bt[p] = *(const bx3_bf8*)&Bp[(p * 64 + 32 * cb + i) * BSTR + 16 * q + 8 * s];
+#pragma unroll
+        for (int u = 0; u < 6; ++u)
+          acc[cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(at[s][BX3_TA[u]], bt[BX3_TB[u]], acc[cb], 0, 0, 0);
+      }
+    __syncthreads();
+  }
+  // accumulator r of lane (i, q): row 8 (r / 4) + 4 q + r % 4, column 32 cb + i
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = e0 + 8 * (r >> 2) + 4 * q + (r & 3);
+      if (row < E) gh[row * 64 + 32 * cb + i] = alpha * acc[cb][r];
+    }
+}
+
 size_t mlp_lds_bytes(int n_in, int n_layers) {
   return sizeof(float) * ((size_t)mlp_lds_weights(n_in, n_layers) + 4 * 32 * TSTRIDE);
 }
@@ -526,6 +623,20 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
   hipLaunchKernelGGL(k_mlp_out_f32, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, h, weight, n_edges, n_out,
                      alpha, n_col_tiles, n_chunks, edges_per_chunk, out);
   return tace_check_launch("tace_radial_mlp_out_f32");
+}
+
+int tace_radial_mlp_out_bwd_f32(const float* g_out, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
+                                float* g_h, void* stream) {
+  if (n_edges < 0 || n_out <= 0) return tace_fail_msg("tace_radial_mlp_out_bwd_f32: bad sizes");
+  if (n_edges == 0) return 0;
+  if (!g_out || !weight || !g_h) return tace_fail_msg("tace_radial_mlp_out_bwd_f32: null pointer");
+  if ((n_out & 3) == 0 && ((((uintptr_t)g_out) | ((uintptr_t)weight)) & 15) != 0)
+    return tace_fail_msg("tace_radial_mlp_out_bwd_f32: g_out and weight must be 16-byte aligned");
+  const int64_t n_wg = (n_edges + 127) / 128;
+  if (n_wg > INT32_MAX) return tace_fail_msg("tace_radial_mlp_out_bwd_f32: too many edges");
+  hipLaunchKernelGGL(k_mlp_out_bwd_f32, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, g_out, weight,
+                     n_edges, n_out, alpha, g_h);
+  return tace_check_launch("tace_radial_mlp_out_bwd_f32");
 }
 
 }  // extern "C"

@@ -917,6 +917,20 @@ def launch_mlp_out_f32(h, W, alpha: float) -> torch.Tensor:
     return out
 
 
+def launch_mlp_out_bwd_f32(g, W, alpha: float) -> torch.Tensor:
+    """alpha g @ W^T (g [E, n_out], W [64, n_out]): the last layer's input
+    gradient, in float32 on the bf16 MFMA (three-term split)."""
+    E, n = g.shape
+    _req(g, "g_out", torch.float32, (E, n))
+    _req(W, "weight", torch.float32, (64, n))
+    gh = torch.empty(E, 64, dtype=torch.float32, device=g.device)
+    tok = _t0("radial_mlp_out_bwd")
+    N.check(N.lib().tace_radial_mlp_out_bwd_f32(g.data_ptr(), W.data_ptr(), E, n, float(alpha), gh.data_ptr(),
+                                                N.stream_ptr(g.device)), "tace_radial_mlp_out_bwd_f32")
+    _t1(tok, (E, n))
+    return gh
+
+
 class _MlpOut(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, W, alpha: float):
@@ -928,7 +942,7 @@ class _MlpOut(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         (W,) = ctx.saved_tensors
-        return torch.mm(g, W.t()).mul_(ctx.alpha), None, None
+        return launch_mlp_out_bwd_f32(g.contiguous(), W, ctx.alpha), None, None
 
 
 def radial_mlp_out(h: torch.Tensor, W: torch.Tensor, alpha: float) -> torch.Tensor:

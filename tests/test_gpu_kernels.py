@@ -566,7 +566,8 @@ def test_mlp_out_f32_error_matches_float32_gemm(cuda):
     float32 CPU GEMM's error: inputs spanning 2^-20 .. 2^20, so that a split
     that dropped its third term (a 16-bit significand) would be off by ~2^-17
     instead of ~2^-24; a ragged edge count (not a multiple of 32 or of the
-    1024-edge chunk) and a width that is not a multiple of 32 or 256."""
+    1024-edge chunk) and a width that is not a multiple of 32 or 256; then
+    the input gradient the same way."""
     g = torch.Generator().manual_seed(3)
     E, N = 2 * 1024 + 77, 600
 
@@ -584,6 +585,16 @@ def test_mlp_out_f32_error_matches_float32_gemm(cuda):
     e_gpu, e_cpu = err(got), err(cpu)
     print(f"mlp out: rel err {e_gpu:.3e} (float32 CPU GEMM {e_cpu:.3e})")
     assert e_gpu < 4 * e_cpu + 1e-8, f"{e_gpu:.3e} vs float32 GEMM {e_cpu:.3e}"
+    # the input gradient g_h = alpha g @ W^T (tace_radial_mlp_out_bwd_f32),
+    # widths with a partial last 32-slab (600) and not a multiple of 4 (601)
+    for n in (600, 601):
+        Wn, gn = spread((64, n)), spread((E, n))
+        truth = alpha * (gn.double() @ Wn.double().t())
+        cpu = alpha * (gn @ Wn.t())
+        got = ops.launch_mlp_out_bwd_f32(gn.to(cuda), Wn.to(cuda), alpha).double().cpu()
+        e_gpu, e_cpu = err(got), err(cpu)
+        print(f"mlp out grad h (n_out {n}): rel err {e_gpu:.3e} (float32 CPU GEMM {e_cpu:.3e})")
+        assert e_gpu < 4 * e_cpu + 1e-8, f"grad h, n_out {n}: {e_gpu:.3e} vs float32 GEMM {e_cpu:.3e}"
 
 
 # ------------------------------------------------------ segmented row sums ----

@@ -110,9 +110,6 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------- linears ----
-# per-species linears over at least this many species ranges run as one
-# segmented-GEMM launch (tace_seg_linear); fewer, larger ranges stay one
-# library GEMM per instruction and species
 # the interaction's radial last layer inside the edge-product kernels
 # (ops.edge_rtp_scatter; float32, C % 64 == 0).  Off: on the 12k-atom water
 # box the fused kernels take 12.6 ms (forward) and 23.3 ms (backward) per
@@ -122,7 +119,13 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 # too few to keep the vector ALUs busy.
 RADIAL_FUSED_TP = False
 
-SEG_LINEAR_MIN_RANGES = 3
+# per-species linears over at least this many species ranges run as one
+# segmented-GEMM launch (tace_seg_linear, float32 on the bf16x3 MFMA kernel);
+# fewer run one library GEMM per instruction and species.  At 1 every
+# per-species linear takes the segmented kernel: on the 2-species water box it
+# measured 72.3 against 72.7 ms/step with library GEMMs, on 1-species bcc Fe
+# 375.8 against 379.3 ms/step.
+SEG_LINEAR_MIN_RANGES = 1
 # tile edge of the float32 segmented GEMM: 128 = MFMA kernel (float32 as three
 # bf16 terms), 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 17
+#define TACE_HIP_ABI_VERSION 18
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -96,6 +96,27 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
+
+/* tace_edge_tp_bwd for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight MD/serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference: it exists for those callers.
+ * Same arguments, results and rules as tace_edge_tp_bwd, without the
+ * workspace: the per-slot grad_x rows and grad_y partials go to a library-owned
+ * device array of TACE_NOALLOC_SCRATCH_BYTES per GPU (held until the process
+ * ends; its address is looked up once per device on the first call with that
+ * device current).  A call whose workspace (tace_edge_tp_workspace_elems x
+ * element size) exceeds it fails with an error before any device work.  The
+ * call allocates nothing.  Every call on one GPU shares that GPU's array:
+ * calls that overlap in time on one GPU (e.g. on two streams, or from two
+ * threads) race and give wrong results -- serialise them.  Devices with an
+ * index >= TACE_NOALLOC_MAX_DEVICES are refused. */
+#define TACE_NOALLOC_SCRATCH_BYTES (64ll << 20)
+#define TACE_NOALLOC_MAX_DEVICES 64
+int tace_edge_tp_bwd_noalloc(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                             const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                             int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                             const int32_t* s_rowptr, const int32_t* s_slot, void* gx, void* gy, void* gw,
+                             void* stream);
 
 /* The same product with the radial MLP's last layer folded in (float32):
  * w[e, p*C + u] = alpha * sum_k h[e, k] w_last[k, p*C + u] -- the last

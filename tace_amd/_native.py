@@ -34,6 +34,8 @@ _SIGS = {
                                   _c_i32, _vp, _vp]),
     "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                   _c_i32, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp]),
+    "tace_edge_tp_bwd_noalloc": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
+                                          _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tace_edge_rtp_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
                                    _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_edge_rtp_workspace_elems": (_c_i64, [_c_int, _c_i64, _c_i32, _c_i32]),

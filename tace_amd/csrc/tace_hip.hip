@@ -17,6 +17,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/tace_hip.h"
 
 namespace {
@@ -775,6 +777,72 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                                 channels, s);
   }
   return check_launch("tace_edge_tp_bwd");
+}
+
+// ------------------------------------------ allocation-free edge-TP backward --
+// The workspace of tace_edge_tp_bwd (per-slot grad_x rows and per-part grad_y
+// partials) taken from a file-scope device array instead of a caller buffer.
+// Each GPU holds its own copy of `scratch` for the life of the process; host
+// code never uses the array's name as an address: the per-device address
+// comes from hipGetSymbolAddress once per device (noalloc_scratch below).
+static __device__ __align__(256) unsigned char scratch[TACE_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[TACE_NOALLOC_MAX_DEVICES];
+
+// address of the current device's `scratch`, looked up on the first call per
+// device (with that device current) and kept; nullptr after fail()
+static void* noalloc_scratch(const char* who) {
+  char msg[200];
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= TACE_NOALLOC_MAX_DEVICES) {
+    snprintf(msg, sizeof(msg), "%s: no usable current device (%s)", who,
+             e != hipSuccess ? hipGetErrorString(e) : "device index out of range");
+    fail(msg);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      snprintf(msg, sizeof(msg), "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, dev,
+               hipGetErrorString(e));
+      fail(msg);
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+int tace_edge_tp_bwd_noalloc(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                             const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                             int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                             const int32_t* s_rowptr, const int32_t* s_slot, void* gx, void* gy, void* gw,
+                             void* stream) {
+  if (tp_common_checks("tace_edge_tp_bwd_noalloc", vid, n_nodes, n_edges, channels, layout)) return -1;
+  if (dtype != TACE_F32 && dtype != TACE_F64)
+    return fail("tace_edge_tp_bwd_noalloc: dtype must be TACE_F32 or TACE_F64");
+  const int64_t elems = tace_edge_tp_workspace_elems(vid, n_edges, channels, gx != nullptr);
+  if (elems < 0) return -1;
+  const int64_t es = dtype == TACE_F32 ? 4 : 8;
+  if (elems > TACE_NOALLOC_SCRATCH_BYTES / es) {
+    char msg[240];
+    snprintf(msg, sizeof(msg),
+             "tace_edge_tp_bwd_noalloc: needs %lld bytes of scratch (E=%lld, C=%d), above the %lld-byte maximum; "
+             "use tace_edge_tp_bwd with a caller workspace",
+             (long long)(elems * es), (long long)n_edges, (int)channels, (long long)TACE_NOALLOC_SCRATCH_BYTES);
+    return fail(msg);
+  }
+  void* ws = nullptr;
+  if (elems > 0 && !(ws = noalloc_scratch("tace_edge_tp_bwd_noalloc"))) return -1;
+  // every scratch element the kernels read is written earlier in the same
+  // call (all grad_x row segments of every slot by the parts, every grad_y
+  // partial), so nothing needs clearing between calls
+  return tace_edge_tp_bwd(vid, dtype, x, y, w, gout, rowptr, eid, src, node_map, n_nodes, n_edges, channels, layout,
+                          s_rowptr, s_slot, ws, elems, gx, gy, gw, stream);
 }
 
 // ---------------------------------------------- radial-fused edge products --

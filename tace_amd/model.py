@@ -25,7 +25,6 @@ from __future__ import annotations
 import collections
 import copy
 import math
-from types import SimpleNamespace
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -120,12 +119,14 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
 RADIAL_FUSED_TP = False
 
 # per-species linears over at least this many species ranges run as one
-# segmented-GEMM launch (tace_seg_linear, float32 on the bf16x3 MFMA kernel);
-# fewer run one library GEMM per instruction and species.  At 1 every
-# per-species linear takes the segmented kernel: on the 2-species water box it
-# measured 72.3 against 72.7 ms/step with library GEMMs, on 1-species bcc Fe
-# 375.8 against 379.3 ms/step.
-SEG_LINEAR_MIN_RANGES = 1
+# segmented-GEMM launch (tace_seg_linear); fewer run one library GEMM per
+# instruction and species.  float32 (the bf16x3 MFMA kernel): every
+# per-species linear takes the segmented kernel -- on the 2-species water box
+# it measured 72.3 against 72.7 ms/step with library GEMMs, on 1-species bcc Fe
+# 375.8 against 379.3 ms/step.  float64 runs the segmented launch on a 64x64
+# FMA tile kernel, which only pays for itself once the library path needs
+# many small GEMMs (several species).
+SEG_LINEAR_MIN_RANGES = {torch.float32: 1, torch.float64: 3}
 # tile edge of the float32 segmented GEMM: 128 = MFMA kernel (float32 as three
 # bf16 terms), 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128
@@ -204,7 +205,7 @@ class _LinearFn(torch.autograd.Function):
         shared = weight.dim() == 1
         rr = [(None, 0, Z)] if shared else ranges
         rr = [r for r in rr if r[2] > r[1]]
-        ctx.seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES
+        ctx.seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES.get(x.dtype, 1)
         ctx.save_for_backward(x, weight, bias)
         ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
         if ctx.seg:
@@ -900,20 +901,88 @@ def _atomic_virials(vec, edge_forces, edge_index, lattice, batch, n_nodes):
     return av, torch.where(st.abs() < 1e10, st, torch.zeros_like(st))
 
 
+# ------------------------------------------------------------ caller API ----
+# target properties whose first derivative this path computes (the
+# first-derivative rows of the reference's PROPERTY table,
+# tace/dataset/quantity.py), and the compute_* switches it honours
+_FIRST_DERIVATIVE = ("forces", "stress", "virials", "edge_forces", "atomic_virials", "atomic_stresses")
+_SUPPORTED_FLAGS = frozenset("compute_" + p for p in ("energy", "node_energy") + _FIRST_DERIVATIVE)
+
+
+class ComputeFlags:
+    """The reference's ``ComputeFlag`` (``tace/dataset/quantity.py:917-922``):
+    one boolean ``compute_<property>`` per property, False unless set.
+    Callers switch outputs on and off through it (``interface/torchsim/
+    torchsim.py:131-137``, ``interface/lammps/mliap.py:25-34``)."""
+
+    def __init__(self, **on: bool):
+        for k, v in on.items():
+            setattr(self, k, bool(v))
+
+    def __getattr__(self, name: str) -> bool:
+        if name.startswith("compute_"):
+            return False
+        raise AttributeError(name)
+
+    def enabled(self) -> List[str]:
+        return sorted(k for k, v in vars(self).items() if v)
+
+    def __repr__(self) -> str:
+        return f"ComputeFlags({', '.join(self.enabled())})"
+
+
+class TorchElement:
+    """The model's element table, as ``TorchElement``
+    (``tace/dataset/element.py:41-64``): sorted atomic numbers, ``z2idx`` and
+    ``z2onehot`` (an atomic number outside the table raises in ``one_hot``)."""
+
+    def __init__(self, zs: Sequence[int]):
+        self.zs = sorted(int(z) for z in zs)
+        self.num_elements = len(self.zs)
+        self.lookup_table = torch.full((max(self.zs) + 1,), -1, dtype=torch.int64)
+        self.lookup_table[torch.tensor(self.zs, dtype=torch.int64)] = torch.arange(self.num_elements)
+
+    def z2idx(self, z: torch.Tensor) -> torch.Tensor:
+        return self.lookup_table[z]
+
+    def z2onehot(self, zs: torch.Tensor) -> torch.Tensor:
+        idx = self.lookup_table.to(zs.device)[zs]
+        return torch.nn.functional.one_hot(idx, num_classes=self.num_elements)
+
+    def __len__(self) -> int:
+        return len(self.zs)
+
+
+def _opt(data, key: str):
+    """data[key] or None, for plain dicts and torch_geometric batches alike."""
+    return data[key] if key in data else None
+
+
 class TensorModel(torch.nn.Module):
     """``TensorModel`` (``tace/models/adapter.py:23-452``) for energy, forces,
-    stress/virials: ``forward(data) -> {energy, node_energy, forces, stress, virials}``."""
+    stress/virials, edge forces and per-atom virials/stresses:
+    ``forward(data) -> {energy, node_energy, forces, virials, stress,
+    edge_forces, atomic_virials, atomic_stresses}`` (None where not computed).
+    Which derivatives are taken follows ``flags`` (set from the target
+    properties, ``adapter.py:410-426``, and overridable by the caller) and
+    ``compute_first_derivative`` (``adapter.py:95``)."""
 
     def __init__(self, readout_fn: TACE):
         super().__init__()
         self.readout_fn = readout_fn
         self.fidelity_idx = 0
         self.lmp = False
-        # switches the reference's callers set (adapter.py flags; the LAMMPS
-        # EdgeForcesWrapper, interface/lammps/mliap.py:25-34, turns on
-        # compute_edge_forces and sets lmp)
-        self.flags = SimpleNamespace(compute_forces=True, compute_stress=False, compute_virials=False,
-                                     compute_edge_forces=False)
+        self._set_target_property()
+
+    def _set_target_property(self) -> None:
+        """``adapter.py:410-431``: flags and derivative switches from the
+        target properties (no second-derivative targets on this path)."""
+        tp = self.get_target_property()
+        self.flags = ComputeFlags(**{f"compute_{k}": True for k in tp})
+        self.compute_first_derivative = any(p in _FIRST_DERIVATIVE for p in tp)
+        self.compute_second_derivative = False
+        self.retain_graph = False
+        self.create_graph = False
 
     # getters used by the ASE / TorchSim / LAMMPS callers (adapter.py:386-452)
     def get_cutoff(self) -> float:
@@ -921,6 +990,9 @@ class TensorModel(torch.nn.Module):
 
     def get_atomic_numbers(self):
         return [int(z) for z in self.readout_fn.atomic_numbers.cpu().tolist()]
+
+    def get_torch_element(self) -> TorchElement:
+        return TorchElement(self.get_atomic_numbers())
 
     def get_model_dtype(self):
         return self.readout_fn.cutoff.dtype
@@ -943,6 +1015,16 @@ class TensorModel(torch.nn.Module):
 
     def reset_target_property(self, target_property):
         self.readout_fn.target_property = list(target_property)
+        self._set_target_property()
+
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        """``load_state_dict`` that also takes a reference checkpoint as saved
+        (``lightning/lit_model.py:597-610`` calls it on the model
+        ``create_model`` built): keys of e3nn's internal modules are dropped
+        and matrix-form weights (``TACE_USE_MATRIX_WEIGHT=1``,
+        ``linear.py:322-327, 417-425``) are concatenated into the flat form."""
+        sd = _reference_state_dict(self.state_dict(), state_dict)
+        return super().load_state_dict(sd, strict=strict, assign=assign)
 
     @staticmethod
     def _ghost_owners(lmp_data, nlocal: int, nghosts: int, like: torch.Tensor) -> torch.Tensor:
@@ -986,7 +1068,7 @@ class TensorModel(torch.nn.Module):
         ei = data["edge_index"]
         if ei.numel() and int(ei[1].max()) >= nlocal:
             raise ValueError("LAMMPS mode: every edge's receiver (edge_index[1]) must be a local atom")
-        owner = self._ghost_owners(data.get("lmp_data"), nlocal, nghosts, vec)
+        owner = self._ghost_owners(_opt(data, "lmp_data"), nlocal, nghosts, vec)
         ei = torch.stack([owner[ei[0]], ei[1]])
         attrs = data["node_attrs"][:nlocal]
         d = dict(node_attrs=attrs, edge_index=ei, batch=data["batch"][:nlocal], ptr=data["ptr"])
@@ -1002,15 +1084,25 @@ class TensorModel(torch.nn.Module):
     def forward(self, data: Dict[str, torch.Tensor]) -> Dict[str, Optional[torch.Tensor]]:
         if self.lmp or ("edge_vector" in data and "natoms" in data):
             return self._forward_lammps(data)
-        tp = set(self.get_target_property())
-        want_f = "forces" in tp
-        want_s = bool({"stress", "virials"} & tp)
-        want_e = bool({"edge_forces", "atomic_virials", "atomic_stresses"} & tp)
+        fl = self.flags
+        unsupported = [k for k in fl.enabled() if k not in _SUPPORTED_FLAGS]
+        if unsupported:
+            raise NotImplementedError(f"{unsupported} are not computed on the MI355X path")
+        # adapter.py:69-87: the gradient inputs follow the flags
+        want_f = fl.compute_forces
+        want_s = fl.compute_stress or fl.compute_virials
+        want_e = fl.compute_edge_forces or fl.compute_atomic_virials or fl.compute_atomic_stresses
+        if (want_f or want_s or want_e) and not self.compute_first_derivative:
+            raise RuntimeError("flags request derivatives but compute_first_derivative is False")
+        dt = self.get_model_dtype()
         pos = data["positions"]
         if not pos.is_cuda:
             raise RuntimeError("tace_amd.TensorModel runs on the GPU only (positions are on %s)" % pos.device)
-        pos = pos.detach().requires_grad_(want_f or want_s or want_e)
-        lattice, batch = data["lattice"], data["batch"]
+        pos = pos.detach().to(dt).requires_grad_(want_f or want_s or want_e)
+        lattice, batch = data["lattice"].to(dt), data["batch"]
+        shifts = data["edge_shifts"]
+        if shifts.dtype != dt:
+            shifts = shifts.to(dt)
         num_graphs = data["ptr"].numel() - 1
         inputs = [pos] if want_f else []
         if want_s:
@@ -1023,17 +1115,18 @@ class TensorModel(torch.nn.Module):
         else:
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
-        plan = data.get("_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
+        plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
         # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
         # +1e-9 of the length is applied in the edge-basis kernel
-        dst32 = data.get("_dst32")
+        dst32 = _opt(data, "_dst32")
         if dst32 is None:
             dst32 = ei[1].to(torch.int32)
         egraph = None if num_graphs == 1 else batch[ei[0]].to(torch.int32)
-        vec = ops.edge_vectors(pos_s, lat_s, data["edge_shifts"], plan, dst32, egraph)
+        vec = ops.edge_vectors(pos_s, lat_s, shifts, plan, dst32, egraph)
         E, e_node = self.readout_fn.energy(data, plan, vec)
-        out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, stress=None,
-                                                      virials=None)
+        out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, virials=None,
+                                                      stress=None, edge_forces=None, atomic_virials=None,
+                                                      atomic_stresses=None)
         if want_e:
             inputs.append(vec)
         if inputs:
@@ -1063,19 +1156,57 @@ _E3NN_INTERNAL = ("output_mask", "_compiled", ".tp.", ".sc.", ".act_gates.", ".m
                   "._bias_mask", ".cut.")
 
 
+def _reference_state_dict(own: Dict[str, torch.Tensor], state_dict: Dict[str, torch.Tensor]) -> Dict[str, torch.Tensor]:
+    """A reference ``state_dict`` mapped onto this model's keys.
+
+    * Matrix-form weights (``TACE_USE_MATRIX_WEIGHT=1``): ``e3nnLinear``
+      stores one ``weight.<i>`` of shape ``path_shape`` per o3.Linear
+      instruction and ``e3nnElementLinear`` one of shape ``(num_elements,
+      *path_shape)`` (``tace/models/linear.py:322-327, 417-425``); the flat
+      weight is their concatenation in instruction order, per element
+      (``linear.py:351-356, 444-456``).  The element bias of that form is
+      ``(num_elements * bias_numel,)`` viewed per element (``linear.py:426-427,
+      457-461``).
+    * Keys that only e3nn's internal modules register (output masks,
+      compiled-graph constants) are dropped.
+    Everything else is passed through for ``load_state_dict`` to judge."""
+    sd = dict(state_dict)
+    for k, ref in own.items():
+        if k in sd:
+            v = sd[k]
+            if k.endswith(".bias") and ref.dim() == 2 and v.dim() == 1 and v.numel() == ref.numel():
+                sd[k] = v.reshape(ref.shape)
+            continue
+        if not k.endswith(".weight") or f"{k}.0" not in sd:
+            continue
+        parts, i = [], 0
+        while f"{k}.{i}" in sd:
+            parts.append(sd.pop(f"{k}.{i}"))
+            i += 1
+        if ref.dim() == 1:
+            flat = torch.cat([p.reshape(-1) for p in parts])
+        else:
+            flat = torch.cat([p.reshape(ref.shape[0], -1) for p in parts], dim=-1)
+        if flat.shape != ref.shape:
+            raise RuntimeError(f"matrix-form weights of {k} concatenate to {tuple(flat.shape)}, "
+                               f"expected {tuple(ref.shape)}")
+        sd[k] = flat
+    return {k: v for k, v in sd.items() if k in own or not any(t in k for t in _E3NN_INTERNAL)}
+
+
 def load_reference_state_dict(model: torch.nn.Module, state_dict: Dict[str, torch.Tensor]):
     """``load_state_dict(strict=True)`` semantics for every parameter and buffer
-    this model owns; keys that only e3nn's internal modules register in a
-    reference checkpoint (masks, compiled-graph constants) are ignored."""
+    this model owns, from a reference checkpoint in either weight form; keys
+    that only e3nn's internal modules register are ignored."""
     own = model.state_dict()
-    extra = [k for k in state_dict if k not in own]
-    unknown = [k for k in extra if not any(t in k for t in _E3NN_INTERNAL)]
+    sd = _reference_state_dict(own, state_dict)
+    unknown = [k for k in sd if k not in own]
     if unknown:
         raise RuntimeError(f"unexpected keys in state_dict: {unknown[:8]}")
-    missing = [k for k in own if k not in state_dict]
+    missing = [k for k in own if k not in sd]
     if missing:
         raise RuntimeError(f"missing keys in state_dict: {missing[:8]}")
-    model.load_state_dict({k: v for k, v in state_dict.items() if k in own}, strict=True)
+    torch.nn.Module.load_state_dict(model, sd, strict=True)
     return model
 
 

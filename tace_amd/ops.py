@@ -319,7 +319,10 @@ class _EdgeRTP(torch.autograd.Function):
         x, y, h, W = ctx.saved_tensors
         gx, gy, gw = launch_edge_rtp_bwd(x, y, h, W, ctx.alpha, gout.contiguous(), ctx.plan, ctx.var, ctx.C,
                                          ctx.layout, ctx.node_map, ctx.needs_input_grad[0])
-        gh = torch.mm(gw, W.t()).mul_(ctx.alpha) if ctx.needs_input_grad[2] else None
+        gh = None
+        if ctx.needs_input_grad[2]:
+            gh = (launch_mlp_out_bwd_f32(gw, W, ctx.alpha) if gw.shape[1] % 4 == 0
+                  else torch.mm(gw, W.t()).mul_(ctx.alpha))
         gW = torch.mm(h.t(), gw).mul_(ctx.alpha) if ctx.needs_input_grad[3] else None
         return gx, gy, gh, gW, None, None, None, None, None, None
 

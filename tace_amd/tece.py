@@ -343,7 +343,10 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     del gxd
     ops.rows_accumulate(g2, gxs.view(E, -1), *ops.sender_csr(rs, Nr))
     del gxs
-    gh = torch.mm(gw, P.mlp_WT_scaled)
+    if gw.dtype == torch.float32 and gw.shape[1] % 4 == 0:
+        gh = ops.launch_mlp_out_bwd_f32(gw, P.mlp_W, P.mlp_alpha)
+    else:
+        gh = torch.mm(gw, P.mlp_WT_scaled)
     gR += ops.launch_mlp_hidden_bwd(R, gh, P.mlp_flat, P.mlp_layers)
     return gR, gW.add_(gW_in)
 

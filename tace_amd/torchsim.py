@@ -51,14 +51,12 @@ class TACETorchSimCalc(torch.nn.Module):
         self.neighbor_list_fn = neighbor_list_fn
         self._memory_scales_with = "n_atoms_x_density"
         model = model.to(device=self._device, dtype=dtype)
-        # the properties to compute (the reference sets model.flags; this
-        # model derives forces / stress from its target list)
-        tp = list(target_property) if target_property is not None else ["energy"]
-        if compute_forces and "forces" not in tp:
-            tp.append("forces")
-        if compute_stress and "stress" not in tp:
-            tp.append("stress")
-        model.reset_target_property(tp)
+        if target_property:  # load_tace(..., target_property=...), lit_model.py:639-661
+            model.reset_target_property(list(target_property))
+        # torchsim.py:131-137: the caller's switches override the targets'
+        model.flags.compute_forces = self._compute_forces
+        model.flags.compute_stress = self._compute_stress
+        model.compute_first_derivative = self._compute_forces or self._compute_stress
         model.reset_fidelity_idx(fidelity_idx)
         model.eval()
         for param in model.parameters():
@@ -66,7 +64,7 @@ class TACETorchSimCalc(torch.nn.Module):
         self.model = model
         self._dtype = model.get_model_dtype()
         self.r_max = model.get_cutoff()
-        self._z_list = model.get_atomic_numbers()
+        self.torch_element = model.get_torch_element()
         self.atomic_numbers_in_init = atomic_numbers is not None
         self.system_idx_in_init = system_idx is not None
         if (atomic_numbers is not None and system_idx is not None
@@ -103,12 +101,10 @@ class TACETorchSimCalc(torch.nn.Module):
         self.ptr = torch.cat([counts.new_zeros(1), counts.cumsum(0)])
 
     def _setup_node_attrs(self, atomic_numbers: torch.Tensor) -> None:
-        table = torch.full((int(max(self._z_list)) + 1,), -1, dtype=torch.int64, device=atomic_numbers.device)
-        table[torch.tensor(self._z_list, device=atomic_numbers.device)] = torch.arange(
-            len(self._z_list), device=atomic_numbers.device)
-        if int(atomic_numbers.max()) >= table.numel() or bool((table[atomic_numbers] < 0).any()):
+        zs = self.torch_element.zs
+        if int(atomic_numbers.max()) > max(zs) or bool((self.torch_element.z2idx(atomic_numbers.cpu()) < 0).any()):
             raise ValueError("atomic number outside the model's element table")
-        self.node_attrs = torch.nn.functional.one_hot(table[atomic_numbers], len(self._z_list)).to(self._dtype)
+        self.node_attrs = self.torch_element.z2onehot(atomic_numbers).to(self._dtype)
 
     def _graph(self, state) -> Dict[str, torch.Tensor]:
         cell = state.row_vector_cell.to(self._device)

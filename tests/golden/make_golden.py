@@ -37,7 +37,18 @@ def cases():
         # config-5 architecture (TECE) on a 128-atom bcc Fe slice
         "fe128_tece": dict(structs=lambda: [structures.bcc_fe(reps=(4, 4, 4), seed=3)], preset="tece", stress=False,
                            over={}),
+        # config-4 architecture (89-species embedding over the MPTrj elements,
+        # 256 channels, L = 3, nu = 3, 2 layers, r_c = 6) on four small
+        # random triclinic crystals, with stress
+        "ragged89_c256": dict(structs=lambda: _ragged(4, (8, 40), seed=5), preset="ragged128", stress=True,
+                              over={}, zs=list(structures.MPTRJ_ELEMENTS)),
     }
+
+
+def _ragged(n_structs, size_range, seed):
+    rng = np.random.default_rng(seed)
+    return [structures.random_crystal(rng, int(rng.integers(size_range[0], size_range[1] + 1)),
+                                      structures.MPTRJ_ELEMENTS) for _ in range(n_structs)]
 
 
 def weight_checksum(model) -> np.ndarray:
@@ -50,7 +61,7 @@ def build(name, spec, weight_seed=0):
     structs = spec["structs"]()
     rc = configs.PRESETS[spec["preset"]]["cutoff"]
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc) for s in structs]
-    zs = sorted({int(z) for s in structs for z in s["numbers"]})
+    zs = spec.get("zs") or sorted({int(z) for s in structs for z in s["numbers"]})
     nat = sum(len(s["positions"]) for s in structs)
     avg = sum(e[0].shape[1] for e in edges) / nat
     cfg = configs.model_cfg(spec["preset"], zs, avg, **spec["over"])

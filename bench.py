@@ -39,6 +39,10 @@ sys.path.insert(0, ROOT)
 
 METRIC = "atom-steps/sec (E+F, fp32) at 12k atoms; % HBM/MFMA roofline"
 HBM_PEAK_GBS = 8000.0
+FP32_PEAK_TFS = 157.3    # MI355X dense fp32 (matrix and vector)
+BF16_PEAK_TFS = 2500.0   # MI355X dense bf16 MFMA
+# float32 GEMMs on the bf16 MFMA: six bf16 products per float32 product
+BF16X3_PRODUCTS = 6
 DT_FS = 0.5  # water with H
 
 
@@ -126,7 +130,7 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         n_rows, width, n_out = info
         return s * width * (n_rows + 2 * n_out) + 4 * (n_rows + n_out)
     if name.startswith("seg_linear"):
-        x_numel, y_numel, w_numel = info
+        x_numel, y_numel, w_numel, _flops = info
         return s * (x_numel + y_numel + w_numel)
     if name.startswith("edge_basis_fwd"):
         (E,) = info
@@ -150,6 +154,36 @@ def measured_traffic(workload: str, entry: str):
             if name.strip() == entry:
                 return float(val)
     return None
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def mfma_roofline(summ, wall_ms: float):
+    """MFMA-bound kernel with the largest share: the segmented per-species GEMM
+    (the product basis's Coef contractions and the element-aware linears), on
+    the bf16 MFMA with float32 split into three bf16 terms.  ``achieved`` is
+    its algorithmic float32 flops (tile rows x columns x k, summed over the
+    tile table) over its HIP-event time, against the fp32 peak;
+    ``bf16_pipe_frac`` counts the six bf16 products per float32 product
+    against the bf16 peak."""
+    if "seg_linear" not in summ:
+        return None
+    cnt, tot_ms, infos = summ["seg_linear"]
+    flops = sum(i[3] for i in infos)
+    tfs = flops / (tot_ms * 1e-3) / 1e12
+    return dict(kernel="seg_linear (k_seg_linear_bf16x3)", bound="mfma", achieved=round(tfs, 1),
+                peak=FP32_PEAK_TFS, unit="TFLOP/s", frac=round(tfs / FP32_PEAK_TFS, 4),
+                bf16_pipe_frac=round(BF16X3_PRODUCTS * tfs / BF16_PEAK_TFS, 4),
+                flops_per_step=None, launches=cnt, avg_launch_us=round(tot_ms / cnt * 1e3, 1),
+                share_of_step=round(tot_ms / wall_ms, 3))
 
 
 def cpu_baseline(wl, reps=3):
@@ -180,7 +214,7 @@ def cpu_baseline(wl, reps=3):
     for _ in range(reps):
         om.compute(m, graph()[1], forces=True, stress=stress)
     dt = time.perf_counter() - t0
-    return dict(value=n * reps / dt, unit="atom-steps/s", cores=threads, kind="port",
+    return dict(value=n * reps / dt, unit="atom-steps/s", cores=threads, kind="port", cpu=_cpu_model(),
                 sample=f"{n}-atom {what} (same model, float32), "
                        f"{reps} timed {'E+F+S' if stress else 'E+F'} steps incl. brute-force NL after 1 warm-up; "
                        f"{dt:.1f} s")
@@ -306,17 +340,42 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] warm-up done, E = {out['energy'].sum().item():.6f}; timing {args.steps} steps")
 
+    # timed region: K steps; a HIP event pair per step (current stream) gives
+    # the median, the wall clock around all K the throughput
     ops.TIMER = ops.KernelTimer()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for i in range(args.steps):
+        ev[i][0].record()
         out = step()
+        ev[i][1].record()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     timer, ops.TIMER = ops.TIMER, None
     ms = dt / args.steps * 1e3
+    step_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    med = step_ms[len(step_ms) // 2] if len(step_ms) % 2 else 0.5 * sum(step_ms[len(step_ms) // 2 - 1:][:2])
     summ = timer.summary()
-    log(f"[bench] {ms:.2f} ms/step")
+    log(f"[bench] {ms:.2f} ms/step (median {med:.2f}, min {step_ms[0]:.2f}, max {step_ms[-1]:.2f})")
+
+    # model only: the same forward + force backward on a graph built once
+    if single:
+        g_fixed = data.resident_graph(pos64, s["cell"], s["pbc"], attrs, rc)
+    else:
+        g_fixed = data.gpu_graph(structs, cfg["atomic_numbers"], rc, dtype=torch.float32, device=dev)
+    model(g_fixed)
+    mev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        mev[i][0].record()
+        model(g_fixed)
+        mev[i][1].record()
+    torch.cuda.synchronize()
+    model_ms = sorted(a.elapsed_time(b) for a, b in mev)
+    model_med = model_ms[len(model_ms) // 2]
+    del g_fixed
+    log(f"[bench] model only (graph built once): median {model_med:.2f} ms/step")
 
     # dominant native kernel -> roofline
     name, (cnt, tot_ms, infos) = max(summ.items(), key=lambda kv: kv[1][1])
@@ -327,8 +386,13 @@ def main():
     traffic = measured_traffic(args.workload, name)
     roof = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
+                traffic_source=(f"profiles/{args.workload}_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                f"copy-calibrated)" if traffic is not None else None),
                 algorithmic_bytes=round(byts / cnt),
                 avg_launch_us=round(tot_ms / cnt * 1e3, 1), share_of_step=round(tot_ms / (dt * 1e3), 3))
+    roof_mfma = mfma_roofline(summ, dt * 1e3)
+    if roof_mfma is not None:
+        roof_mfma["flops_per_step"] = round(sum(i[3] for i in summ["seg_linear"][2]) / args.steps)
     if args.kernels:
         for k, (c, t, _) in sorted(summ.items(), key=lambda kv: -kv[1][1]):
             log(f"  {t / args.steps:8.3f} ms/step  {c // args.steps:3d} launches/step  {k}")
@@ -339,7 +403,9 @@ def main():
                data="synthetic",
                config=dict(workload=wl["describe"](nat), atoms=nat, edges=int(E0), **wl["arch"],
                            parallelism="single GPU"),
+               ms_per_step_median=round(med, 3), model_only_ms_per_step=round(model_med, 3),
                ns_per_day=round(1e3 / ms * 86400 * wl["dt_fs"] * 1e-6, 4), dt_fs=wl["dt_fs"], roofline=roof,
+               roofline_mfma=roof_mfma,
                peak_mem_gb=round(torch.cuda.max_memory_allocated(dev) / 2 ** 30, 1))
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")

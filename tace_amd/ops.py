@@ -1038,6 +1038,12 @@ class SegLinearPlan:
                 raise ValueError("seg linear plan: weight out of range")
         self.n_tiles = len(t)
         self.x_numel, self.y_numel, self.w_numel, self.b_numel = x_numel, y_numel, w_numel, b_numel
+        # multiply-adds x 2 of the whole launch (rows x valid columns x summed k
+        # of every tile): the algorithmic flops of the GEMMs, padding excluded
+        self.flops = 0
+        if len(t) and len(c):
+            ksum = np.concatenate([[0], np.cumsum(c[:, 1])])
+            self.flops = int(2 * (t[:, 1] * np.minimum(TN, t[:, 2] - t[:, 3]) * (ksum[t[:, 6]] - ksum[t[:, 5]])).sum())
         self.tiles = torch.from_numpy(np.ascontiguousarray(t)).to(device)
         self.contribs = torch.from_numpy(np.ascontiguousarray(c) if len(c) else np.zeros((1, 4), np.int64)).to(device)
         self.scales = torch.from_numpy(s if len(s) else np.zeros(1)).to(device)
@@ -1062,7 +1068,7 @@ def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional
                                     None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(), plan.n_tiles,
                                     plan.contribs.data_ptr(), plan.scales.data_ptr(), float(alpha),
                                     N.stream_ptr(x.device)), "tace_seg_linear")
-    _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel))
+    _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
     return y
 
 

@@ -55,12 +55,17 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     from tace_amd import ops
 
     if name.startswith("edge_tp_fwd"):
-        n, E, C = info
-        return s * (E * (var.npath * C + var.d2) + n * C * (var.d1 + var.dout)) + 4 * (E + n + 1)
+        # with edge pairs (a 4th item) the weights are one row per pair
+        n, E, C = info[:3]
+        rows = info[3] if len(info) > 3 else E
+        return s * (rows * var.npath * C + E * var.d2 + n * C * (var.d1 + var.dout)) + 4 * (E + n + 1) \
+            + (4 * E if len(info) > 3 else 0)
     if name.startswith("edge_tp_bwd"):
-        n, E, C, need_x = info
-        return s * (E * (2 * var.npath * C + 2 * var.d2) + n * C * (var.d1 * (2 if need_x else 1) + var.dout)) \
-            + 4 * (E + n + 1)
+        n, E, C, need_x = info[:4]
+        rows = info[4] if len(info) > 4 else E
+        return s * (rows * var.npath * C + E * (var.npath * C + 2 * var.d2)
+                    + n * C * (var.d1 * (2 if need_x else 1) + var.dout)) + 4 * (E + n + 1) \
+            + (4 * E if len(info) > 4 else 0)
     if name.startswith("edge_rtp_fwd"):
         # h instead of w: x, y, h read (the last radial layer's 64 x W weights
         # once), out written

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 18
+#define TACE_HIP_ABI_VERSION 20
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -96,6 +96,22 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
                      int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream);
+
+/* The same products with the weight rows indexed through w_rows (int32 [E],
+ * by edge id; NULL = the edge id itself): edge e uses w[w_rows[e]] and
+ * w has as many rows as w_rows names.  The two directions of an edge (i -> j
+ * with shift S, j -> i with -S) have one length, so the radial MLP's weights
+ * (tace/models/_e3nn/inter.py:166-183) are the same for both and can be made
+ * once per pair (tace_edge_pairs).  gw stays per edge: [E, C*npath]. */
+int tace_edge_tp_fwd_rows(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
+                          const int32_t* eid, const int32_t* src, const int32_t* node_map, const int32_t* w_rows,
+                          int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, void* out,
+                          void* stream);
+int tace_edge_tp_bwd_rows(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                          const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                          const int32_t* w_rows, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                          const int32_t* s_rowptr, const int32_t* s_slot, void* workspace, int64_t workspace_elems,
+                          void* gx, void* gy, void* gw, void* stream);
 
 /* tace_edge_tp_bwd for callers that cannot allocate device memory (code under
  * HIP graph capture, tight MD/serving loops, harnesses that forbid
@@ -216,6 +232,12 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
                             float* out, void* stream);
 int tace_radial_mlp_out_bwd_f32(const float* g_out, const float* weight, int64_t n_edges, int32_t n_out, float alpha,
                                 float* g_h, void* stream);
+/* the same for weight rows shared by edge pairs: g_h [n_rows, 64] = alpha
+ * (g_out[rows_a[r]] + g_out[rows_b[r]]) @ weight^T, the sum in float32
+ * (rows_b[r] < 0: g_out[rows_a[r]] alone); g_out [E, n_out] per edge. */
+int tace_radial_mlp_out_bwd_pairs_f32(const float* g_out, const int32_t* rows_a, const int32_t* rows_b,
+                                      int64_t n_rows, int32_t n_out, float alpha, const float* weight, float* g_h,
+                                      void* stream);
 
 /* ---- per-species (element) linears
  * tace_seg_linear replaces the per-element o3.Linear of e3nnElementLinear
@@ -242,6 +264,28 @@ int tace_radial_mlp_out_bwd_f32(const float* g_out, const float* weight, int64_t
 int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y, const void* w,
                     const void* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                     const double* scales, double alpha, void* stream);
+/* The float32 128 x 128 case with the weights split ahead of time (they are
+ * constants at inference; the same e3nnElementLinear forward and input
+ * gradient, linear.py:377-482).
+ *   tace_bf16x3_split_blocks writes, for n_blocks weight blocks (int64 [n, 6]:
+ *   src_off, cols, k, transpose, dst_off, unused; double scales[n]), the three
+ *   bf16 terms of scale * B (the exact split of float32 into three bf16, round
+ *   to nearest even) into planes[p * plane_stride + dst_off + c k_pad + kk]
+ *   for column c < cols and kk < k_pad = ceil8(k), with B[kk][c] =
+ *   w[src_off + kk cols + c] (transpose = 1: the forward's W [k, n]) or
+ *   w[src_off + c k + kk] (transpose = 0: W [n, k] applied transposed, the
+ *   input gradient), and zeros for kk >= k.
+ *   tace_seg_linear_presplit then runs the tile table of tace_seg_linear with
+ *   each contribution's w_off pointing at its block in the planes (16-byte
+ *   aligned, plane_stride a multiple of 8); trans and the scales are unused
+ *   (folded into the planes).  The products and their order are those of
+ *   tace_seg_linear's float32 128 x 128 kernel, so the outputs are the same
+ *   bits. */
+int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, const double* scales, int64_t n_blocks,
+                             uint16_t* planes, int64_t plane_stride, void* stream);
+int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
+                             const float* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
+                             double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"
@@ -392,6 +436,19 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream);
+/* Edge pairs of a neighbour list in receiver-CSR form (rowptr, eid as for
+ * the tensor products; src [E] senders, shifts [E, 3] int32 periodic shifts,
+ * by edge id): the reverse of edge e (i -> j, S) is the edge j -> i with
+ * shift -S (the full list of dataset/neighbour_list.py:195-298 holds both).
+ * Each pair gets one row, numbered in order of its lower edge id; an edge
+ * without a reverse gets a row of its own.  Outputs: w_rows [E] (the row of
+ * every edge), row_edges [E] and row_partner [E] (for the first n_rows rows:
+ * the lower edge id and its partner, -1 for none).  work: TACE_EDGE_PAIRS_WORK(E)
+ * int32; n_rows is left in work[3 E]. */
+#define TACE_EDGE_PAIRS_WORK(E) (3 * (E) + 2 * (((E) + 1023) / 1024) + 4)
+int tace_edge_pairs(const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* shifts,
+                    int64_t n_nodes, int64_t n_edges, int32_t* work, int32_t* w_rows, int32_t* row_edges,
+                    int32_t* row_partner, void* stream);
 /* exclusive prefix sum: out[0] = 0, out[i+1] = out[i] + counts[i], i < n */
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream);
 

@@ -34,6 +34,12 @@ _SIGS = {
                                   _c_i32, _vp, _vp]),
     "tace_edge_tp_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                   _c_i32, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp]),
+    "tace_edge_tp_fwd_rows": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
+                                       _c_i32, _c_i32, _vp, _vp]),
+    "tace_edge_tp_bwd_rows": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
+                                       _c_i32, _c_i32, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp, _vp]),
+    "tace_edge_pairs": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp]),
+    "tace_radial_mlp_out_bwd_pairs_f32": (_c_int, [_vp, _vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp, _vp]),
     "tace_edge_tp_bwd_noalloc": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
                                           _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tace_edge_rtp_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
@@ -74,6 +80,8 @@ _SIGS = {
     "tace_radial_mlp_out_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
     "tace_radial_mlp_out_bwd_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
     "tace_seg_linear": (_c_int, [_c_int, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_dbl, _vp]),
+    "tace_bf16x3_split_blocks": (_c_int, [_vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp]),
+    "tace_seg_linear_presplit": (_c_int, [_vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_dbl, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

@@ -42,7 +42,7 @@ def generate():
 
 def _compile(src: str, force: bool) -> str:
     obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
-    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(ROOT, "include", "tace_hip.h")]
+    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(CSRC, "bf16x3.h"), os.path.join(ROOT, "include", "tace_hip.h")]
     deps += glob.glob(os.path.join(GEN, "*.inc"))
     if not force and os.path.exists(obj) and os.path.getmtime(obj) >= max(os.path.getmtime(d) for d in deps):
         return obj

@@ -19,6 +19,16 @@ typedef unsigned bx3_u4 __attribute__((ext_vector_type(4)));
 __device__ constexpr int BX3_TA[6] = {1, 0, 2, 0, 1, 0};
 __device__ constexpr int BX3_TB[6] = {1, 2, 0, 1, 0, 0};
 
+// scale * v rounded to float32 before the split.  The empty asm makes the
+// products opaque, so the compiler cannot contract them into the split's
+// first subtraction (an FMA there would split the unrounded product, and two
+// kernels could then disagree in the last bits).
+__device__ __forceinline__ bx3_f2 bx3_scale2(bx3_f2 v, float s) {
+  float a = v.x * s, b = v.y * s;
+  asm volatile("" : "+v"(a), "+v"(b));
+  return bx3_f2{a, b};
+}
+
 // two values -> their three terms as packed bf16 pairs (h[p] = term p of
 // (v.x, v.y), low half v.x); float -> bf16 rounds to nearest even
 // (v_cvt_pk_bf16_f32)

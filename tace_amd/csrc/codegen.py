@@ -132,6 +132,7 @@ class Variant:
         L.append("  int ed = e < end ? (eid ? eid[e] : e) : 0;")
         L.append("  int s = e < end ? src[ed] : 0;")
         L.append("  if (map) s = map[s];")
+        L.append("  int wr = e < end && wmap ? wmap[ed] : ed;  // weight row of the edge")
         for (b, m) in xs:
             L.append(f"  T x{b}_{m} = T(0);")
         L += [f"  T w{p} = T(0);" for p in paths]
@@ -139,16 +140,17 @@ class Variant:
         L.append("  if (e < end) {")
         for (b, m) in xs:
             L.append(f"    x{b}_{m} = {self._ld_x('s', b, m)};")
-        L += [f"    w{p} = __builtin_nontemporal_load(&w[(size_t)ed * WW + (size_t){p} * C + u]);" for p in paths]
+        L += [f"    w{p} = __builtin_nontemporal_load(&w[(size_t)wr * WW + (size_t){p} * C + u]);" for p in paths]
         L += [f"    y{j} = y[(size_t)ed * {self.D2} + {j}];" for j in range(self.D2)]
         L.append("  }")
         L.append("  for (; e < end; ++e) {")
         L.append("    const int en = e + 1 < end ? e + 1 : e;")
         L.append("    const int edn = eid ? eid[en] : en;")
         L.append("    const int sn = map ? map[src[edn]] : src[edn];")
+        L.append("    const int wrn = wmap ? wmap[edn] : edn;")
         for (b, m) in xs:
             L.append(f"    const T xn{b}_{m} = {self._ld_x('sn', b, m)};")
-        L += [f"    const T wn{p} = __builtin_nontemporal_load(&w[(size_t)edn * WW + (size_t){p} * C + u]);" for p in paths]
+        L += [f"    const T wn{p} = __builtin_nontemporal_load(&w[(size_t)wrn * WW + (size_t){p} * C + u]);" for p in paths]
         L += [f"    const T yn{j} = y[(size_t)edn * {self.D2} + {j}];" for j in range(self.D2)]
 
     def _edge_rotate(self, L: List[str], blocks: Sequence[int], paths: Sequence[int]) -> None:
@@ -158,6 +160,7 @@ class Variant:
         L += [f"    w{p} = wn{p};" for p in paths]
         L += [f"    y{j} = yn{j};" for j in range(self.D2)]
         L.append("    ed = edn;")
+        L.append("    wr = wrn;")
         L.append("  }")
 
     def emit_uvu_fwd(self, q: int) -> str:
@@ -170,7 +173,8 @@ class Variant:
         L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__device__ __forceinline__ void f_{self.name}_fwd{q}(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C, int n0) {",
+             "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ out, int n_nodes, int C,",
+             "    int n0) {",
              "  const int u = (int)threadIdx.x;",
              "  if (u >= C) return;",
              "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
@@ -221,8 +225,8 @@ class Variant:
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const T* __restrict__ gout,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    const int* __restrict__ map, T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw,",
-             "    int n_nodes, int C, int n0, T (*red)[8][16]) {",
+             "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ cbuf, T* __restrict__ gy,",
+             "    T* __restrict__ gw, int n_nodes, int C, int n0, T (*red)[8][16]) {",
              "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
              "  const int lane = (int)threadIdx.x & 63, wv = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;",
              "  const bool act = (int)threadIdx.x < C;",
@@ -297,12 +301,12 @@ class Variant:
         compute-heavy parts share the CUs instead of running one after the
         other.  Part q of the backward writes grad_y partial q."""
         nq = len(self.parts())
-        a_f = "x, y, w, rowptr, eid, src, map, out, n_nodes, C, n0"
-        a_b = "x, y, w, gout, rowptr, eid, src, map, cbuf, gy + (size_t)q * n_edges * %d, gw, n_nodes, C, n0, red" % self.D2
+        a_f = "x, y, w, rowptr, eid, src, map, wmap, out, n_nodes, C, n0"
+        a_b = "x, y, w, gout, rowptr, eid, src, map, wmap, cbuf, gy + (size_t)q * n_edges * %d, gw, n_nodes, C, n0, red" % self.D2
         L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-             "    const int* __restrict__ map, T* __restrict__ out, int n_nodes, int C) {",
+             "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ out, int n_nodes, int C) {",
              "  int q;",
              f"  const int n0 = tp_part_node(n_nodes, {nq}, &q);",
              "  if (n0 < 0) return;"]
@@ -313,8 +317,8 @@ class Variant:
               "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
               "    const T* __restrict__ gout,",
               "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
-              "    const int* __restrict__ map, T* __restrict__ cbuf, T* __restrict__ gy, T* __restrict__ gw,",
-              "    int n_nodes, int n_edges, int C) {",
+              "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ cbuf, T* __restrict__ gy,",
+              "    T* __restrict__ gw, int n_nodes, int n_edges, int C) {",
               "  __shared__ T red[2][8][16];",
               "  int q;",
               f"  const int n0 = tp_part_node(n_nodes, {nq}, &q);",
@@ -1017,10 +1021,10 @@ def emit_wigner_cg(lmax_all: int = 3) -> str:
 
 
 # -------------------------------------------------------------------- main ----
-_UVU_FWD_SIG = ("const void*, const void*, const void*, const int*, const int*, const int*, const int*, void*, int, int, "
-                "int, hipStream_t")
+_UVU_FWD_SIG = ("const void*, const void*, const void*, const int*, const int*, const int*, const int*, const int*, "
+                "void*, int, int, int, hipStream_t")
 _UVU_BWD_SIG = ("const void*, const void*, const void*, const void*, const int*, const int*, const int*, const int*, "
-                "void*, void*, void*, int, int, int, int, hipStream_t")
+                "const int*, void*, void*, void*, int, int, int, int, hipStream_t")
 _RTP_FWD_SIG = ("const float*, const float*, const float*, const float*, float, const int*, const int*, const int*, "
                 "const int*, const int*, float*, int, int, int, int, hipStream_t")
 _RTP_BWD_SIG = ("const float*, const float*, const float*, const float*, float, const float*, const int*, const int*, "
@@ -1054,18 +1058,18 @@ def _launchers(v: Variant) -> List[str]:
             # grid: parts x receivers padded to a multiple of 8 (tp_part_node); block: one lane per channel
             nq = len(v.parts())
             launch = f"const dim3 g((unsigned)((n + 7) / 8 * 8 * {nq})), b((unsigned)((C + 63) / 64 * 64));"
-            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, const int* map, void* o, int n, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_fwd_{tag}(const void* x, const void* y, const void* w, const int* rp, const int* eid, const int* src, const int* map, const int* wmap, void* o, int n, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
             for f in range(4):
-                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, map, ({T}*)o, n, C);")
+                out.append(f"  if (flags == {f}) hipLaunchKernelGGL((k_{v.name}_fwd<{T}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, rp, eid, src, map, wmap, ({T}*)o, n, C);")
             out.append("}")
-            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, void* cb, void* gy, void* gw, int n, int E, int flags, int C, hipStream_t s) {{")
+            out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, const int* wmap, void* cb, void* gy, void* gw, int n, int E, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
             out.append("  " + launch)
             for f in range(4):
                 for gx in (True, False):
-                    out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, E, C);")
+                    out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, wmap, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, E, C);")
             out.append("}")
             if tag == "f":
                 # radial-fused kernels (float32 only): grid from rtp_slot, 4 wavefronts of 16 channels

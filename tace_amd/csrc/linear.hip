@@ -173,6 +173,7 @@ __device__ __forceinline__ void seg_load_k(const float* __restrict__ base, int k
 // (k, k + 1) pairs.
 constexpr int SB_K = 32, SB_STR = SB_K + 8;
 // rows of 16 k (four f4 of one row, k-contiguous) -> planes p[row][kofs ..]
+template <bool SCALED>
 __device__ __forceinline__ void sb_store_k16(unsigned short* lds, int plane, int off, const f4* v, float sc) {
   typedef unsigned u4v __attribute__((ext_vector_type(4)));
   u4v o[3][2];
@@ -181,7 +182,8 @@ __device__ __forceinline__ void sb_store_k16(unsigned short* lds, int plane, int
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       unsigned h[3];
-      bx3_split2(bx3_f2{v[q][2 * e], v[q][2 * e + 1]} * sc, h);
+      const bx3_f2 u = bx3_f2{v[q][2 * e], v[q][2 * e + 1]};
+      bx3_split2(SCALED ? bx3_scale2(u, sc) : u, h);
 #pragma unroll
       for (int p = 0; p < 3; ++p) o[p][q >> 1][2 * (q & 1) + e] = h[p];
     }
@@ -227,7 +229,7 @@ __device__ __forceinline__ void sb_store_n(unsigned short* lds, int plane, int t
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       unsigned h[3];   // (k, k + 1) of one column
-      bx3_split2(bx3_f2{u0[e], u1[e]} * sc, h);
+      bx3_split2(bx3_scale2(bx3_f2{u0[e], u1[e]}, sc), h);
       const int col = 4 * (t & 15) + 64 * q + ((e + r) & 3);
 #pragma unroll
       for (int p = 0; p < 3; ++p) *(unsigned*)&lds[p * plane + col * SB_STR + kp] = h[p];
@@ -279,8 +281,8 @@ __global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restri
       else sb_load_n(wb, k, n, c0, kc, wvec, t, b);
     };
     auto stage = [&](const f4* a, const f4* b) {
-      sb_store_k16(As, PL, soff, a, 1.f);
-      if (trans) sb_store_k16(Bs, PL, soff, b, sc);
+      sb_store_k16<false>(As, PL, soff, a, 1.f);
+      if (trans) sb_store_k16<true>(Bs, PL, soff, b, sc);
       else sb_store_n(Bs, PL, t, b, sc);
     };
     auto mma = [&]() {
@@ -325,7 +327,176 @@ __global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restri
   }
 }
 
+// ---- the same GEMM with the weights split ahead of time ------------------
+// The weights of the per-species linears are constants at inference, so their
+// three bf16 terms (with the contribution's scale folded in) are made once,
+// by k_split_blocks, into three planes laid out the way the LDS tile holds
+// them: per weight block, column-major runs of k_pad = ceil8(k) bf16 (zeros
+// past k), column c of the block at w_off + c k_pad of each plane.  The GEMM
+// then stages B with plain 16-byte copies -- no split, no transposition, no
+// scale -- which removes most of the kernel's VALU work and the transposed
+// LDS stores.
+
+// 128 columns x 32 k of one contribution's B: thread t stages column t / 2,
+// k k0 + 16 (t & 1) .. + 15, of each plane (two 16-byte loads per plane; a
+// k_pad run is a multiple of 8, so each load is wholly inside or outside it)
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void sbs_load(const unsigned short* __restrict__ wp, int64_t pstride, int kpad, int ncols,
+                                         int k0, int t, u4v* v) {
+  const int col = t >> 1, kk = k0 + 16 * (t & 1);
+  const unsigned short* p = wp + (int64_t)col * kpad + kk;
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bool ok = col < ncols && kk + 8 * h < kpad;
+      v[2 * pl + h] = ok ? *(const u4v*)(p + pl * pstride + 8 * h) : u4v{0u, 0u, 0u, 0u};
+    }
+}
+
+__device__ __forceinline__ void sbs_store(unsigned short* lds, int plane, int off, const u4v* v) {
+#pragma unroll
+  for (int pl = 0; pl < 3; ++pl) {
+    *(u4v*)&lds[pl * plane + off] = v[2 * pl];
+    *(u4v*)&lds[pl * plane + off + 8] = v[2 * pl + 1];
+  }
+}
+
+__global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict__ x, float* __restrict__ y,
+                                                         const unsigned short* __restrict__ wsp, int64_t pstride,
+                                                         const float* __restrict__ bias,
+                                                         const int64_t* __restrict__ tiles,
+                                                         const int64_t* __restrict__ contribs, float alpha,
+                                                         int n_tiles, int per) {
+  constexpr int WM = 4, WN = 4, TR = 128, PL = 128 * SB_STR;   // plane size (bf16)
+  __shared__ __attribute__((aligned(16))) unsigned short As[3 * PL];
+  __shared__ __attribute__((aligned(16))) unsigned short Bs[3 * PL];
+  const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (tile >= n_tiles) return;
+  const int64_t* td = tiles + 8 * (int64_t)tile;
+  const int64_t out_base = td[0];
+  const int rows = (int)td[1], n = (int)td[2], c0 = (int)td[3];
+  const int64_t bias_off = td[4];
+  const int cb = (int)td[5], ce = (int)td[6];
+  const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 16 * WN;
+  const int fr = lane & 15, fg = lane >> 4;
+  f4 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  const int soff = (t >> 1) * SB_STR + 16 * (t & 1);   // this thread's k16 run of a k-contiguous plane
+
+  for (int c = cb; c < ce; ++c) {
+    const int64_t* cd = contribs + 4 * (int64_t)c;
+    const float* __restrict__ xa = x + cd[0];
+    const int k = (int)cd[1];
+    const int kpad = (k + 7) & ~7;
+    const unsigned short* __restrict__ wp = wsp + cd[2] + (int64_t)c0 * kpad;
+    const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
+    f4 a[4];
+    u4v b[6];
+    auto load = [&](int kc) {
+      seg_load_k<TR>(xa, k, kc, rows, xvec, t, a);
+      sbs_load(wp, pstride, kpad, n - c0, kc, t, b);
+    };
+    auto mma = [&]() {
+      bx3_bf8 af[3][WM];
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int i = 0; i < WM; ++i) af[p][i] = *(const bx3_bf8*)&As[p * PL + (wr + 16 * i + fr) * SB_STR + 8 * fg];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        bx3_bf8 bf[3];
+#pragma unroll
+        for (int p = 0; p < 3; ++p) bf[p] = *(const bx3_bf8*)&Bs[p * PL + (wc + 16 * j + fr) * SB_STR + 8 * fg];
+#pragma unroll
+        for (int u = 0; u < 6; ++u)   // the six terms a_i b_j, smallest first
+#pragma unroll
+          for (int i = 0; i < WM; ++i)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[BX3_TA[u]][i], bf[BX3_TB[u]], acc[i][j], 0, 0, 0);
+      }
+    };
+    load(0);
+    for (int k0 = 0; k0 < k; k0 += SB_K) {
+      sb_store_k16<false>(As, PL, soff, a, 1.f);
+      sbs_store(Bs, PL, soff, b);
+      __syncthreads();
+      if (k0 + SB_K < k) load(k0 + SB_K);   // next chunk in flight during this chunk's MFMAs
+      mma();
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int col = c0 + wc + 16 * j + fr;
+    if (col >= n) continue;
+    const float bv = bias_off >= 0 ? bias[bias_off + col] : 0.f;
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int r = wr + 16 * i + 4 * fg + q;
+        if (r < rows) y[out_base + (int64_t)r * n + col] = alpha * (acc[i][j][q] + bv);
+      }
+  }
+}
+
+// Per block (6 x int64): src_off, cols, k, transpose, dst_off, unused; one
+// double scale.  dst column c, k index kk < k_pad of plane p = term p of
+// scale * (transpose ? w[src_off + kk cols + c] : w[src_off + c k + kk]),
+// zero for kk >= k.  blockIdx.y picks the block, the x dimension strides
+// over its cols x k_pad elements.
+__global__ __launch_bounds__(256) void k_split_blocks(const float* __restrict__ w, const int64_t* __restrict__ blocks,
+                                                      const double* __restrict__ scales,
+                                                      unsigned short* __restrict__ out, int64_t pstride) {
+  const int64_t* bd = blocks + 6 * (int64_t)blockIdx.y;
+  const int64_t src = bd[0], dst = bd[4];
+  const int cols = (int)bd[1], k = (int)bd[2];
+  const bool tr = bd[3] != 0;
+  const int kpad = (k + 7) & ~7;
+  const float sc = (float)scales[blockIdx.y];
+  const int64_t total = (int64_t)cols * kpad;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int c = (int)(e / kpad), kk = (int)(e - (int64_t)c * kpad);
+    float v = 0.f;
+    if (kk < k) v = bx3_scale2(bx3_f2{tr ? w[src + (int64_t)kk * cols + c] : w[src + (int64_t)c * k + kk], 0.f}, sc).x;
+    unsigned h[3];
+    bx3_split2(bx3_f2{v, 0.f}, h);
+#pragma unroll
+    for (int p = 0; p < 3; ++p) out[p * pstride + dst + e] = (unsigned short)(h[p] & 0xffffu);
+  }
+}
+
 }  // namespace
+
+extern "C" int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, const double* scales,
+                                        int64_t n_blocks, uint16_t* planes, int64_t plane_stride, void* stream) {
+  if (n_blocks < 0 || n_blocks > 65535) return tace_fail_msg("tace_bf16x3_split_blocks: 0..65535 blocks");
+  if (n_blocks == 0) return 0;
+  if (!w || !blocks || !scales || !planes) return tace_fail_msg("tace_bf16x3_split_blocks: null pointer");
+  if (plane_stride < 0) return tace_fail_msg("tace_bf16x3_split_blocks: bad plane stride");
+  hipLaunchKernelGGL(k_split_blocks, dim3(64, (unsigned)n_blocks), dim3(256), 0, (hipStream_t)stream, w, blocks,
+                     scales, (unsigned short*)planes, plane_stride);
+  return tace_check_launch("tace_bf16x3_split_blocks");
+}
+
+extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
+                                        const float* bias, const int64_t* tiles, int64_t n_tiles,
+                                        const int64_t* contribs, double alpha, void* stream) {
+  if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit: bad tile count");
+  if (n_tiles == 0) return 0;
+  if (!x || !y || !w_planes || !tiles || !contribs) return tace_fail_msg("tace_seg_linear_presplit: null pointer");
+  if ((((uintptr_t)w_planes) & 15) != 0 || (plane_stride & 7) != 0)
+    return tace_fail_msg("tace_seg_linear_presplit: planes must be 16-byte aligned with a stride that is a multiple of 8");
+  const int per = (int)((n_tiles + 7) / 8);
+  hipLaunchKernelGGL(k_seg_linear_bx3s, dim3((unsigned)(8 * per)), dim3(256), 0, (hipStream_t)stream, x, y,
+                     (const unsigned short*)w_planes, plane_stride, bias, tiles, contribs, (float)alpha,
+                     (int)n_tiles, per);
+  return tace_check_launch("tace_seg_linear_presplit");
+}
 
 extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y,
                                const void* w, const void* bias, const int64_t* tiles, int64_t n_tiles,

@@ -459,8 +459,14 @@ __device__ __forceinline__ void mlp_ld8(const float* __restrict__ row, int k, in
   }
 }
 
+// PAIRS: output row e is the gradient of a weight row shared by two edges
+// (the two directions of a pair have the same length, hence the same radial
+// weights): g row = g[ra[e]] + g[rb[e]] (rb[e] < 0: g[ra[e]] alone), summed
+// in float32 before the split.
+template <bool PAIRS>
 __global__ __launch_bounds__(256) void k_mlp_out_bwd_f32(const float* __restrict__ g, const float* __restrict__ Wm,
-                                                         int64_t E, int N, float alpha, float* __restrict__ gh) {
+                                                         int64_t E, int N, float alpha, float* __restrict__ gh,
+                                                         const int* __restrict__ ra, const int* __restrict__ rb) {
   constexpr int BSTR = 40;                       // bf16 per LDS row: 32 k + 8 pad (80 bytes)
   __shared__ __attribute__((aligned(16))) unsigned short Bp[3 * 64 * BSTR];   // term p, column c, k
   const int t = (int)threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -469,7 +475,9 @@ __global__ __launch_bounds__(256) void k_mlp_out_bwd_f32(const float* __restrict
   const int64_t er = e0 + i;
   const bool rok = er < E;
   const bool vec = (N & 3) == 0;
-  const float* __restrict__ grow = g + (rok ? er : 0) * (int64_t)N;
+  const float* __restrict__ grow = g + (PAIRS ? (rok ? (int64_t)ra[er] : 0) : (rok ? er : 0)) * (int64_t)N;
+  const int rbe = PAIRS && rok ? rb[er] : -1;
+  const float* __restrict__ grow2 = g + (rbe >= 0 ? (int64_t)rbe : 0) * (int64_t)N;
   // the slab's W[c][k0 + kk .. + 7] for c = t / 4, kk = 8 (t % 4), split once per workgroup
   const int wc = t >> 2, wk = 8 * (t & 3);
   const float* __restrict__ wrow = Wm + (int64_t)wc * N;
@@ -478,20 +486,26 @@ __global__ __launch_bounds__(256) void k_mlp_out_bwd_f32(const float* __restrict
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
-  float a[16], w[8];
+  float a[16], w[8], a2[16];
   mlp_ld16(grow, 16 * q, N, rok, vec, a);
+  if (PAIRS) mlp_ld16(grow2, 16 * q, N, rbe >= 0, vec, a2);
   mlp_ld8(wrow, wk, N, vec, w);
   for (int k0 = 0; k0 < N; k0 += 32) {
     bx3_bf8 wt[3];
     bx3_split8(w, wt);
 #pragma unroll
     for (int p = 0; p < 3; ++p) *(bx3_bf8*)&Bp[(p * 64 + wc) * BSTR + wk] = wt[p];
+    if (PAIRS) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) a[j] += a2[j];
+    }
     bx3_bf8 at[2][3];
 #pragma unroll
     for (int s = 0; s < 2; ++s) bx3_split8(a + 8 * s, at[s]);
     __syncthreads();
     if (k0 + 32 < N) {   // next slab in flight during this slab's MFMAs
       mlp_ld16(grow, k0 + 32 + 16 * q, N, rok, vec, a);
+      if (PAIRS) mlp_ld16(grow2, k0 + 32 + 16 * q, N, rbe >= 0, vec, a2);
       mlp_ld8(wrow, k0 + 32 + wk, N, vec, w);
     }
 #pragma unroll
@@ -634,9 +648,25 @@ int tace_radial_mlp_out_bwd_f32(const float* g_out, const float* weight, int64_t
     return tace_fail_msg("tace_radial_mlp_out_bwd_f32: g_out and weight must be 16-byte aligned");
   const int64_t n_wg = (n_edges + 127) / 128;
   if (n_wg > INT32_MAX) return tace_fail_msg("tace_radial_mlp_out_bwd_f32: too many edges");
-  hipLaunchKernelGGL(k_mlp_out_bwd_f32, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, g_out, weight,
-                     n_edges, n_out, alpha, g_h);
+  hipLaunchKernelGGL(k_mlp_out_bwd_f32<false>, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, g_out,
+                     weight, n_edges, n_out, alpha, g_h, nullptr, nullptr);
   return tace_check_launch("tace_radial_mlp_out_bwd_f32");
+}
+
+int tace_radial_mlp_out_bwd_pairs_f32(const float* g_out, const int32_t* rows_a, const int32_t* rows_b,
+                                      int64_t n_rows, int32_t n_out, float alpha, const float* weight, float* g_h,
+                                      void* stream) {
+  if (n_rows < 0 || n_out <= 0) return tace_fail_msg("tace_radial_mlp_out_bwd_pairs_f32: bad sizes");
+  if (n_rows == 0) return 0;
+  if (!g_out || !rows_a || !rows_b || !weight || !g_h)
+    return tace_fail_msg("tace_radial_mlp_out_bwd_pairs_f32: null pointer");
+  if ((n_out & 3) == 0 && ((((uintptr_t)g_out) | ((uintptr_t)weight)) & 15) != 0)
+    return tace_fail_msg("tace_radial_mlp_out_bwd_pairs_f32: g_out and weight must be 16-byte aligned");
+  const int64_t n_wg = (n_rows + 127) / 128;
+  if (n_wg > INT32_MAX) return tace_fail_msg("tace_radial_mlp_out_bwd_pairs_f32: too many rows");
+  hipLaunchKernelGGL(k_mlp_out_bwd_f32<true>, dim3((unsigned)n_wg), dim3(256), 0, (hipStream_t)stream, g_out,
+                     weight, n_rows, n_out, alpha, g_h, (const int*)rows_a, (const int*)rows_b);
+  return tace_check_launch("tace_radial_mlp_out_bwd_pairs_f32");
 }
 
 }  // extern "C"

@@ -368,6 +368,114 @@ __global__ void k_nl_bin(const double* __restrict__ pos, int n, NlGeom g, int* _
   atomicAdd(bcount + lin, 1);
 }
 
+// ---- edge pairs: the two directions of an edge ---------------------------
+// partner[e] = id of the reverse of edge e (sender i -> receiver j, shift S):
+// the edge j -> i with shift -S, looked up among receiver i's edges; -1 when
+// the list has none.  One wavefront per receiver j walks its edges; for each,
+// the 64 lanes test 64 of receiver i's edges at a time (coalesced reads) and
+// a ballot picks the match.
+__global__ __launch_bounds__(64) void k_edge_partner(const int* __restrict__ rowptr, const int* __restrict__ eid,
+                                                     const int* __restrict__ src, const int* __restrict__ shifts,
+                                                     int* __restrict__ partner) {
+  const int j = (int)blockIdx.x, lane = (int)threadIdx.x;
+  const int end = rowptr[j + 1];
+  for (int k = rowptr[j]; k < end; ++k) {
+    const int e = eid ? eid[k] : k;
+    const int i = src[e];
+    const int sx = -shifts[3 * e], sy = -shifts[3 * e + 1], sz = -shifts[3 * e + 2];
+    int found = -1;
+    const int b2 = rowptr[i], e2end = rowptr[i + 1];
+    for (int k2 = b2; k2 < e2end && found < 0; k2 += 64) {
+      const int kk = k2 + lane;
+      bool hit = false;
+      int e2 = 0;
+      if (kk < e2end) {
+        e2 = eid ? eid[kk] : kk;
+        hit = src[e2] == j && shifts[3 * e2] == sx && shifts[3 * e2 + 1] == sy && shifts[3 * e2 + 2] == sz;
+      }
+      const unsigned long long m = __ballot(hit);
+      if (m) found = __shfl(e2, __ffsll((long long)m) - 1);
+    }
+    if (lane == 0) partner[e] = found;
+  }
+}
+
+// Exclusive scan of m ints in three launches (1024 elements per block):
+// block sums, a scan of the sums (k_scan), then each block's own scan plus
+// its offset.  out[m] = total.
+__device__ __forceinline__ int block_excl_scan256(int v, int* sh) {
+  const int t = (int)threadIdx.x;
+  sh[t] = v;
+  __syncthreads();
+  for (int o = 1; o < 256; o <<= 1) {
+    const int u = t >= o ? sh[t - o] : 0;
+    __syncthreads();
+    sh[t] += u;
+    __syncthreads();
+  }
+  const int incl = sh[t];
+  __syncthreads();
+  return incl - v;
+}
+
+__global__ __launch_bounds__(256) void k_scan_sums(const int* __restrict__ cnt, int m, int* __restrict__ sums) {
+  __shared__ int sh[256];
+  const int base = (int)blockIdx.x * 1024 + 4 * (int)threadIdx.x;
+  int v = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v += base + q < m ? cnt[base + q] : 0;
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) sums[blockIdx.x] = sh[0];
+}
+
+__global__ __launch_bounds__(256) void k_scan_apply(const int* __restrict__ cnt, int m,
+                                                    const int* __restrict__ offs, int* __restrict__ out) {
+  __shared__ int sh[256];
+  const int base = (int)blockIdx.x * 1024 + 4 * (int)threadIdx.x;
+  int v[4], tot = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    v[q] = base + q < m ? cnt[base + q] : 0;
+    tot += v[q];
+  }
+  int run = offs[blockIdx.x] + block_excl_scan256(tot, sh);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    if (base + q < m) out[base + q] = run;
+    run += v[q];
+  }
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 255) out[m] = run;
+}
+
+// owner[e] = 1 when e carries its pair's row (the lower id of a pair, or an
+// edge without a partner)
+__global__ void k_edge_owner(const int* __restrict__ partner, int E, int* __restrict__ owner) {
+  const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (e < E) owner[e] = (partner[e] < 0 || partner[e] > e) ? 1 : 0;
+}
+
+// rank = exclusive scan of owner: w_rows[e] = the row of e's pair;
+// row_edges[r] / row_partner[r] = the owner edge of row r and its partner
+__global__ void k_edge_rows(const int* __restrict__ partner, const int* __restrict__ rank, int E,
+                            int* __restrict__ w_rows, int* __restrict__ row_edges, int* __restrict__ row_partner) {
+  const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (e >= E) return;
+  const int p = partner[e];
+  if (p < 0 || p > e) {
+    const int r = rank[e];
+    w_rows[e] = r;
+    row_edges[r] = e;
+    row_partner[r] = p;
+  } else {
+    w_rows[e] = rank[p];
+  }
+}
+
 // exclusive scan of cnt[0..m) into out[0..m]; single block of 1024 threads
 __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ cnt, int m, int* __restrict__ out) {
   __shared__ long long part[1024];
@@ -701,21 +809,29 @@ static int tp_common_checks(const char* who, int vid, int64_t n_nodes, int64_t n
   return 0;
 }
 
-int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
-                     const int32_t* eid, const int32_t* src, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
-                     int32_t channels, int32_t layout, void* out, void* stream) {
+int tace_edge_tp_fwd_rows(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
+                          const int32_t* eid, const int32_t* src, const int32_t* node_map, const int32_t* w_rows,
+                          int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout, void* out,
+                          void* stream) {
   if (tp_common_checks("tace_edge_tp_fwd", vid, n_nodes, n_edges, channels, layout)) return -1;
   if ((!x && n_edges) || (!out && n_nodes) || !rowptr || (n_edges && (!y || !w || !src)))
     return fail("tace_edge_tp_fwd: null pointer");
   const TpVariant& v = kVariants[vid];
   hipStream_t s = (hipStream_t)stream;
   if (dtype == TACE_F32)
-    v.fwd_f(x, y, w, rowptr, eid, src, node_map, out, (int)n_nodes, layout, channels, s);
+    v.fwd_f(x, y, w, rowptr, eid, src, node_map, w_rows, out, (int)n_nodes, layout, channels, s);
   else if (dtype == TACE_F64)
-    v.fwd_d(x, y, w, rowptr, eid, src, node_map, out, (int)n_nodes, layout, channels, s);
+    v.fwd_d(x, y, w, rowptr, eid, src, node_map, w_rows, out, (int)n_nodes, layout, channels, s);
   else
     return fail("tace_edge_tp_fwd: dtype must be TACE_F32 or TACE_F64");
   return check_launch("tace_edge_tp_fwd");
+}
+
+int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const void* w, const int32_t* rowptr,
+                     const int32_t* eid, const int32_t* src, const int32_t* node_map, int64_t n_nodes, int64_t n_edges,
+                     int32_t channels, int32_t layout, void* out, void* stream) {
+  return tace_edge_tp_fwd_rows(vid, dtype, x, y, w, rowptr, eid, src, node_map, nullptr, n_nodes, n_edges, channels,
+                               layout, out, stream);
 }
 
 int64_t tace_edge_tp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx) {
@@ -732,6 +848,15 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
                      int64_t n_nodes, int64_t n_edges,
                      int32_t channels, int32_t layout, const int32_t* s_rowptr, const int32_t* s_slot,
                      void* workspace, int64_t workspace_elems, void* gx, void* gy, void* gw, void* stream) {
+  return tace_edge_tp_bwd_rows(vid, dtype, x, y, w, gout, rowptr, eid, src, node_map, nullptr, n_nodes, n_edges,
+                               channels, layout, s_rowptr, s_slot, workspace, workspace_elems, gx, gy, gw, stream);
+}
+
+int tace_edge_tp_bwd_rows(int vid, int dtype, const void* x, const void* y, const void* w, const void* gout,
+                          const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* node_map,
+                          const int32_t* w_rows, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
+                          const int32_t* s_rowptr, const int32_t* s_slot, void* workspace, int64_t workspace_elems,
+                          void* gx, void* gy, void* gw, void* stream) {
   if (tp_common_checks("tace_edge_tp_bwd", vid, n_nodes, n_edges, channels, layout)) return -1;
   if (!rowptr || (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)))
     return fail("tace_edge_tp_bwd: null pointer");
@@ -761,14 +886,16 @@ int tace_edge_tp_bwd(int vid, int dtype, const void* x, const void* y, const voi
   const int64_t ny = n_edges * v.d2;
   const unsigned nb = (unsigned)((ny + 255) / 256);
   if (dtype == TACE_F32) {
-    v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout, channels, s);
+    v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, w_rows, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout,
+            channels, s);
     if (v.nparts > 1 && ny)
       hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)gyp, v.nparts, ny, (float*)gy);
     if (gx && n_nodes)
       launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, node_map, (float*)gx, (int)n_nodes, row, sg,
                                channels, s);
   } else {
-    v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout, channels, s);
+    v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, w_rows, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout,
+            channels, s);
     if (v.nparts > 1 && ny)
       hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)gyp, v.nparts, ny,
                          (double*)gy);
@@ -1310,6 +1437,35 @@ int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t wi
     return fail("tace_rows_accumulate: dtype must be TACE_F32 or TACE_F64");
   }
   return check_launch("tace_rows_accumulate");
+}
+
+int tace_edge_pairs(const int32_t* rowptr, const int32_t* eid, const int32_t* src, const int32_t* shifts,
+                    int64_t n_nodes, int64_t n_edges, int32_t* work, int32_t* w_rows, int32_t* row_edges,
+                    int32_t* row_partner, void* stream) {
+  if (n_nodes < 0 || n_edges < 0 || n_nodes > INT32_MAX - 1 || n_edges > INT32_MAX / 4 - 64)
+    return fail("tace_edge_pairs: bad sizes");
+  if (!rowptr || (n_edges && (!src || !shifts || !work || !w_rows || !row_edges || !row_partner)))
+    return fail("tace_edge_pairs: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  int* partner = work;
+  int* owner = work + n_edges;
+  int* rank = work + 2 * n_edges;   // n_edges + 1: rank[n_edges] = number of rows
+  int* sums = work + 3 * n_edges + 1;   // block sums of the scan and their scan
+  if (n_edges == 0) {
+    hipLaunchKernelGGL(k_fill<int>, dim3(1), dim3(256), 0, s, rank, (size_t)1, 0);
+    return check_launch("tace_edge_pairs");
+  }
+  if (n_nodes > 0)
+    hipLaunchKernelGGL(k_edge_partner, dim3((unsigned)n_nodes), dim3(64), 0, s, rowptr, eid, src, shifts, partner);
+  const unsigned nb = (unsigned)((n_edges + 255) / 256);
+  hipLaunchKernelGGL(k_edge_owner, dim3(nb), dim3(256), 0, s, partner, (int)n_edges, owner);
+  const int nblk = (int)((n_edges + 1023) / 1024);
+  hipLaunchKernelGGL(k_scan_sums, dim3((unsigned)nblk), dim3(256), 0, s, owner, (int)n_edges, sums);
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, sums, nblk, sums + nblk);
+  hipLaunchKernelGGL(k_scan_apply, dim3((unsigned)nblk), dim3(256), 0, s, owner, (int)n_edges, sums + nblk, rank);
+  hipLaunchKernelGGL(k_edge_rows, dim3(nb), dim3(256), 0, s, partner, rank, (int)n_edges, w_rows, row_edges,
+                     row_partner);
+  return check_launch("tace_edge_pairs");
 }
 
 int tace_scan_i32(const int32_t* counts, int64_t n, int32_t* out, void* stream) {

@@ -65,7 +65,7 @@ def device_graph(p64: torch.Tensor, sizes: Sequence[int], cells, pbcs, cutoff: f
     counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
     dst = torch.repeat_interleave(torch.arange(n_tot, device=p64.device), counts, output_size=E)
     return dict(edge_index=torch.stack([src.to(torch.int64), dst]), edge_shifts=shifts,
-                _edge_plan=EdgePlan(n_tot, E, rowptr, src, None), _dst32=dst.to(torch.int32))
+                _edge_plan=EdgePlan(n_tot, E, rowptr, src, None), _dst32=dst.to(torch.int32), _shifts32=shifts)
 
 
 def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float, dtype=torch.float32,
@@ -104,6 +104,7 @@ def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cut
              batch=torch.zeros(n, dtype=torch.int64, device=dev),
              ptr=torch.tensor([0, n], dtype=torch.int64, device=dev))
     d["_edge_plan"] = EdgePlan(n, int(src.shape[0]), rowptr, src, None)
+    d["_shifts32"] = sh
     return d
 
 

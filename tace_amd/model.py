@@ -130,6 +130,12 @@ SEG_LINEAR_MIN_RANGES = {torch.float32: 1, torch.float64: 3}
 # tile edge of the float32 segmented GEMM: 128 = MFMA kernel (float32 as three
 # bf16 terms), 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128
+# the 128 MFMA kernel reads weights split into bf16 terms once per weight
+# version (tace_seg_linear_presplit) instead of splitting them in every launch
+SEG_LINEAR_PRESPLIT = True
+# radial MLP of the cgtp interactions once per edge pair (both directions of
+# an edge have the same length), when the graph's periodic shifts are known
+PAIR_RADIAL = True
 
 
 class _LinearLayout:
@@ -162,6 +168,43 @@ class _LinearLayout:
         self.read = {i for (i, *_r) in self.ins}
         self.written = {o for (_, o, *_r) in self.ins}
         self._seg = collections.OrderedDict()
+        self._split = {}
+        # pre-split weight planes (tace_bf16x3_split_blocks): per instruction
+        # the block's offset in one species' planes, its columns and k; per
+        # direction ("fwd": B = W, "bwd": B = W^T)
+        self.split_blocks = {}
+        for kind in ("fwd", "bwd"):
+            blocks, acc = [], 0
+            for (i, o, off, mi, mo, pw) in self.ins:
+                cols, k = (mo, mi) if kind == "fwd" else (mi, mo)
+                blocks.append((acc, cols, k))
+                acc += cols * ((k + 7) // 8 * 8)
+            self.split_blocks[kind] = (blocks, acc)
+
+    def split_weights(self, kind: str, weight: torch.Tensor) -> Tuple[torch.Tensor, int]:
+        """The three bf16 terms of every (species, instruction) weight block
+        with its path weight folded in, in the column layout of
+        ``tace_seg_linear_presplit`` ("fwd": B = W, "bwd": B = W^T); returns
+        (planes int16 [3 * stride], plane stride).  Cached until the weight
+        changes (its version counter or storage)."""
+        w = weight.detach()
+        key = (w.data_ptr(), w._version, tuple(w.shape), str(w.device))
+        hit = self._split.get(kind)
+        if hit is not None and hit[0] == key:
+            return hit[1], hit[2]
+        blocks, per = self.split_blocks[kind]
+        S = 1 if w.dim() == 1 else w.shape[0]
+        stride = (S * per + 63) // 64 * 64
+        tab, sc = [], []
+        for sp in range(S):
+            for (dst, cols, k), (i, o, off, mi, mo, pw) in zip(blocks, self.ins):
+                tab.append((sp * self.weight_numel + off, cols, k, 1 if kind == "fwd" else 0, sp * per + dst, 0))
+                sc.append(pw)
+        planes = ops.bf16x3_split_blocks(w.contiguous().view(-1), tab, sc, stride)
+        # the entry keeps the weight alive, so no other tensor can take its
+        # address (and version) while the planes are cached
+        self._split[kind] = (key, planes, stride, w)
+        return planes, stride
 
     def seg_plan(self, kind: str, rr, Z: int, x: torch.Tensor, weight: torch.Tensor,
                  bias: Optional[torch.Tensor]) -> ops.SegLinearPlan:
@@ -169,7 +212,8 @@ class _LinearLayout:
         added) or the input gradient ("bwd": g_out -> g_x, W^T) over species
         ranges ``rr`` of Z rows; the last few are cached."""
         tile = (128, 128) if x.dtype == torch.float32 and SEG_LINEAR_TILE_F32 == 128 else (64, 64)
-        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile)
+        presplit = tile == (128, 128) and SEG_LINEAR_PRESPLIT
+        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile, presplit)
         plan = self._seg.get(key)
         if plan is not None:
             self._seg.move_to_end(key)
@@ -183,8 +227,16 @@ class _LinearLayout:
             outs = [(s, m, d, None) for (s, m, d) in self.gin.blocks]
             ins = [(i, self.gout.blocks[o][0], mo, off, True, pw) for (i, o, off, mi, mo, pw) in self.ins]
             xn, yn = Z * self.dim_out, Z * self.dim_in
-        plan = ops.SegLinearPlan(Z, outs, ins, rr, self.weight_numel, self.bias_numel, xn, yn, weight.numel(),
-                                 0 if bias is None else bias.numel(), x.device, tile)
+        if presplit:
+            # weight offsets into the pre-split planes instead of the flat weight
+            blocks, per = self.split_blocks[kind]
+            ins = [(a, b, k, blocks[j][0], tr, pw) for j, (a, b, k, _off, tr, pw) in enumerate(ins)]
+            S = 1 if weight.dim() == 1 else weight.shape[0]
+            plan = ops.SegLinearPlan(Z, outs, ins, rr, per, self.bias_numel, xn, yn, S * per,
+                                     0 if bias is None else bias.numel(), x.device, tile, split_weights=True)
+        else:
+            plan = ops.SegLinearPlan(Z, outs, ins, rr, self.weight_numel, self.bias_numel, xn, yn, weight.numel(),
+                                     0 if bias is None else bias.numel(), x.device, tile)
         self._seg[key] = plan
         if len(self._seg) > 16:
             self._seg.popitem(last=False)
@@ -210,7 +262,10 @@ class _LinearFn(torch.autograd.Function):
         ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
         if ctx.seg:
             # all species and instructions in one segmented-GEMM launch
-            return ops.seg_linear(x, out, weight, bias, lay.seg_plan("fwd", rr, Z, x, weight, bias), alpha)
+            plan = lay.seg_plan("fwd", rr, Z, x, weight, bias)
+            if plan.split_weights:
+                return ops.seg_linear_presplit(x, out, *lay.split_weights("fwd", weight), bias, plan, alpha)
+            return ops.seg_linear(x, out, weight, bias, plan, alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
             for (sp, a, b) in rr:
@@ -238,7 +293,11 @@ class _LinearFn(torch.autograd.Function):
         gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
         gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
         if ctx.seg and gx is not None:
-            ops.seg_linear(gout, gx, weight, None, lay.seg_plan("bwd", rr, x.shape[0], x, weight, None), alpha)
+            plan = lay.seg_plan("bwd", rr, x.shape[0], x, weight, None)
+            if plan.split_weights:
+                ops.seg_linear_presplit(gout, gx, *lay.split_weights("bwd", weight), None, plan, alpha)
+            else:
+                ops.seg_linear(gout, gx, weight, None, plan, alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
             for (sp, a, b) in rr:
@@ -366,6 +425,13 @@ class O3ScatterTensorProduct(torch.nn.Module):
     def forward(self, x, y, w, plan: ops.EdgePlan, layout: int = 0, node_map=None):
         return ops.edge_tp_scatter(x, y, w, plan, ops.find_variant(self.key), self.C, layout, node_map)
 
+    def paired(self, x, y, h, W, alpha: float, plan: ops.EdgePlan, pairs: ops.EdgePairs, layout: int = 0,
+               node_map=None):
+        """forward(x, y, alpha * h @ W, ...) with the weights made once per edge
+        pair (``ops.edge_tp_scatter_pairs``; h holds the pairs' rows)."""
+        return ops.edge_tp_scatter_pairs(x, y, h, W, alpha, plan, pairs, ops.find_variant(self.key), self.C, layout,
+                                         node_map)
+
     def radial_fused(self, x, y, h, W, alpha: float, plan: ops.EdgePlan, layout: int = 0, node_map=None):
         """forward(x, y, alpha * h @ W, ...) with the radial last layer inside
         the product kernels (``ops.edge_rtp_scatter``)."""
@@ -479,7 +545,13 @@ class O3CgtpInteraction(torch.nn.Module):
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = self.linear_up(x)
         lay = ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED
-        if RADIAL_FUSED_TP and self.edge_info.fused and ops.rtp_supported(x.dtype, self.rejector.C, 64):
+        pairs = plan._pairs if PAIR_RADIAL else None
+        if pairs is not None and self.edge_info.fused:
+            # the radial weights depend on the edge length only: made once per
+            # edge pair and read by both directions
+            h = self.edge_info.hidden(R.index_select(0, pairs.row_edges))
+            m = self.rejector.paired(x, Y, h, *self.edge_info.last_layer(), plan, pairs, lay, sp.node_map)
+        elif RADIAL_FUSED_TP and self.edge_info.fused and ops.rtp_supported(x.dtype, self.rejector.C, 64):
             m = self.rejector.radial_fused(x, Y, self.edge_info.hidden(R), *self.edge_info.last_layer(), plan, lay,
                                            sp.node_map)
         else:
@@ -1116,6 +1188,9 @@ class TensorModel(torch.nn.Module):
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
         plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
+        if PAIR_RADIAL and plan.n_edges:
+            sh32 = _opt(data, "_shifts32")
+            plan.edge_pairs(sh32 if sh32 is not None else shifts)
         # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
         # +1e-9 of the length is applied in the edge-basis kernel
         dst32 = _opt(data, "_dst32")

@@ -116,6 +116,7 @@ class EdgePlan:
     src: torch.Tensor              # int32 [E], sender of edge id
     eid: Optional[torch.Tensor]    # int32 [E] or None
     _sender: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+    _pairs: Optional["EdgePairs"] = None
 
     def sender_csr(self) -> Tuple[torch.Tensor, torch.Tensor]:
         """(s_rowptr int32 [N+1], s_slot int32 [E]): receiver-sorted slots grouped
@@ -128,6 +129,13 @@ class EdgePlan:
             rp[1:] = torch.cumsum(counts, 0)
             self._sender = (rp.to(torch.int32).contiguous(), order)
         return self._sender
+
+    def edge_pairs(self, shifts: torch.Tensor) -> "EdgePairs":
+        """The edge pairs of this list (``tace_edge_pairs``), from the integer
+        periodic shifts [E, 3] (edge-id order); cached on the plan."""
+        if self._pairs is None:
+            self._pairs = edge_pairs(self, shifts)
+        return self._pairs
 
     @staticmethod
     def from_edge_index(edge_index: torch.Tensor, n_nodes: int) -> "EdgePlan":
@@ -146,6 +154,40 @@ class EdgePlan:
         else:
             eid = torch.argsort(dst, stable=True).to(torch.int32).contiguous()
         return EdgePlan(n_nodes, E, rowptr.to(torch.int32).contiguous(), src.to(torch.int32).contiguous(), eid)
+
+
+@dataclass
+class EdgePairs:
+    """The two directions of every edge (``tace_edge_pairs``): ``w_rows``
+    (int32 [E], by edge id) the row of each edge's pair, ``row_edges`` /
+    ``row_partner`` (int32 [n_rows]) the lower edge id of each row and its
+    reverse (-1: none).  A weight that depends on the edge length only is made
+    once per row."""
+
+    n_rows: int
+    w_rows: torch.Tensor
+    row_edges: torch.Tensor
+    row_partner: torch.Tensor
+
+
+def edge_pairs(plan: EdgePlan, shifts: torch.Tensor) -> EdgePairs:
+    E = plan.n_edges
+    sh = shifts if shifts.dtype == torch.int32 else torch.round(shifts).to(torch.int32)
+    _req(sh.contiguous(), "shifts", torch.int32, (E, 3))
+    sh = sh.contiguous()
+    dev = plan.rowptr.device
+    work = torch.empty(3 * E + 2 * ((E + 1023) // 1024) + 4, dtype=torch.int32, device=dev)  # TACE_EDGE_PAIRS_WORK
+    w_rows = torch.empty(E, dtype=torch.int32, device=dev)
+    row_edges = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+    row_partner = torch.empty(max(E, 1), dtype=torch.int32, device=dev)
+    tok = _t0("edge_pairs")
+    N.check(N.lib().tace_edge_pairs(plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr() if E else None,
+                                    sh.data_ptr() if E else None, plan.n_nodes, E, work.data_ptr(), w_rows.data_ptr(),
+                                    row_edges.data_ptr(), row_partner.data_ptr(), N.stream_ptr(dev)),
+            "tace_edge_pairs")
+    _t1(tok, (E,))
+    n_rows = int(work[3 * E].item())
+    return EdgePairs(n_rows, w_rows, row_edges[:n_rows], row_partner[:n_rows])
 
 
 # ------------------------------------------------------- edge featurisation ----
@@ -190,40 +232,48 @@ def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cuto
 
 
 # ------------------------------------------------------ edge tensor product ----
-def launch_edge_tp_fwd(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0, node_map=None):
+def launch_edge_tp_fwd(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0, node_map=None,
+                       pairs: Optional[EdgePairs] = None):
+    """``pairs``: w has one row per edge pair (``EdgePairs.n_rows``), edge e
+    reads row ``pairs.w_rows[e]``."""
     Nn, E = plan.n_nodes, plan.n_edges
     dt = x.dtype
     _req(x, "x", dt, (Nn, C * var.d1))
     _req(y, "y", dt, (E, var.d2))
-    _req(w, "w", dt, (E, C * var.npath))
+    _req(w, "w", dt, (E if pairs is None else pairs.n_rows, C * var.npath))
     out = torch.empty(Nn, C * var.dout, dtype=dt, device=x.device)
     tok = _t0("edge_tp_fwd:" + var.key)
-    N.check(N.lib().tace_edge_tp_fwd(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
-                                     plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(), N.ptr(node_map), Nn,
-                                     E, C, layout, out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
-    _t1(tok, (Nn, E, C))
+    N.check(N.lib().tace_edge_tp_fwd_rows(var.vid, N.dtype_code(dt), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                          plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
+                                          N.ptr(node_map), None if pairs is None else pairs.w_rows.data_ptr(), Nn,
+                                          E, C, layout, out.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_fwd")
+    _t1(tok, (Nn, E, C) if pairs is None else (Nn, E, C, pairs.n_rows))
     return out
 
 
 def launch_edge_tp_bwd(x, y, w, gout, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0, node_map=None,
-                       need_x: bool = True):
-    """(grad_x or None, grad_y, grad_w) of ``launch_edge_tp_fwd``."""
+                       need_x: bool = True, pairs: Optional[EdgePairs] = None):
+    """(grad_x or None, grad_y, grad_w) of ``launch_edge_tp_fwd``; with
+    ``pairs`` grad_w is per edge ([E, C*npath]), not per weight row."""
     _req(gout, "g_out", x.dtype, (plan.n_nodes, C * var.dout))
     gx = torch.empty_like(x) if need_x else None
     gy = torch.empty_like(y)
-    gw = torch.empty_like(w)
+    gw = torch.empty(plan.n_edges, w.shape[1], dtype=w.dtype, device=w.device)
     s_rowptr, s_slot = plan.sender_csr() if need_x else (None, None)
     n_ws = N.lib().tace_edge_tp_workspace_elems(var.vid, plan.n_edges, C, int(need_x))
     if n_ws < 0:
         N.check(int(n_ws), "tace_edge_tp_workspace_elems")
     ws = torch.empty(max(n_ws, 1), dtype=x.dtype, device=x.device)
     tok = _t0("edge_tp_bwd:" + var.key)
-    N.check(N.lib().tace_edge_tp_bwd(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
-                                     gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid), plan.src.data_ptr(),
-                                     N.ptr(node_map), plan.n_nodes, plan.n_edges, C, layout, N.ptr(s_rowptr),
-                                     N.ptr(s_slot), ws.data_ptr(), ws.numel(), N.ptr(gx), gy.data_ptr(),
-                                     gw.data_ptr(), N.stream_ptr(x.device)), "tace_edge_tp_bwd")
-    _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x))
+    N.check(N.lib().tace_edge_tp_bwd_rows(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
+                                          gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
+                                          plan.src.data_ptr(), N.ptr(node_map),
+                                          None if pairs is None else pairs.w_rows.data_ptr(), plan.n_nodes,
+                                          plan.n_edges, C, layout, N.ptr(s_rowptr), N.ptr(s_slot), ws.data_ptr(),
+                                          ws.numel(), N.ptr(gx), gy.data_ptr(), gw.data_ptr(),
+                                          N.stream_ptr(x.device)), "tace_edge_tp_bwd")
+    _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x) if pairs is None
+        else (plan.n_nodes, plan.n_edges, C, need_x, pairs.n_rows))
     return gx, gy, gw
 
 
@@ -252,6 +302,55 @@ def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int
     if node_map is not None:
         _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
     return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout), node_map)
+
+
+class _PairRadialTP(torch.autograd.Function):
+    """The radial MLP's last layer (w = alpha h @ W, one row per edge pair)
+    and the edge product that reads w through ``pairs.w_rows``, as one
+    operator: the backward turns the per-edge grad_w into the gradient of the
+    pair rows' h directly (the two edges' rows summed in float32 inside the
+    last layer's input-gradient kernel), so no per-pair grad_w is formed."""
+
+    @staticmethod
+    def forward(ctx, x, y, h, W, alpha: float, plan: EdgePlan, pairs: EdgePairs, var: TpVariant, C: int,
+                layout: int, node_map):
+        w = radial_mlp_out(h, W, alpha)
+        out = launch_edge_tp_fwd(x, y, w, plan, var, C, layout, node_map, pairs)
+        ctx.save_for_backward(x, y, w, W)
+        ctx.alpha, ctx.plan, ctx.pairs, ctx.var, ctx.C, ctx.layout, ctx.node_map = (alpha, plan, pairs, var, C,
+                                                                                   layout, node_map)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x, y, w, W = ctx.saved_tensors
+        pairs = ctx.pairs
+        gx, gy, gw = launch_edge_tp_bwd(x, y, w, gout.contiguous(), ctx.plan, ctx.var, ctx.C, ctx.layout,
+                                        ctx.node_map, ctx.needs_input_grad[0], pairs)
+        gh = None
+        if ctx.needs_input_grad[2]:
+            if gw.dtype == torch.float32:
+                gh = launch_mlp_out_bwd_pairs_f32(gw, pairs, W, ctx.alpha)
+            else:
+                ra = pairs.row_edges.long()
+                rb = pairs.row_partner.long()
+                g = gw.index_select(0, ra)
+                has = rb >= 0
+                g[has] += gw.index_select(0, rb[has])
+                gh = torch.mm(g, W.t()).mul_(ctx.alpha)
+        return gx, gy, gh, None, None, None, None, None, None, None, None
+
+
+def edge_tp_scatter_pairs(x, y, h, W, alpha: float, plan: EdgePlan, pairs: EdgePairs, var: TpVariant, C: int,
+                          layout: int = 0, node_map: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``edge_tp_scatter(x, y, w, ...)`` with w = alpha h @ W made once per
+    edge pair (h [n_rows, 64], the radial MLP's last hidden activations of the
+    pairs' lower edges) and read by both edges of each pair (``pairs.w_rows``).
+    Gradients: x, y and h (W is a constant, as in ``radial_mlp_out``)."""
+    if node_map is not None:
+        _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    return _PairRadialTP.apply(x.contiguous(), y.contiguous(), h.contiguous(), W.detach().contiguous(), float(alpha),
+                               plan, pairs, var, C, int(layout), node_map)
 
 
 # ------------------------------------------ radial-fused edge tensor product ----
@@ -934,6 +1033,22 @@ def launch_mlp_out_bwd_f32(g, W, alpha: float) -> torch.Tensor:
     return gh
 
 
+def launch_mlp_out_bwd_pairs_f32(g, pairs: EdgePairs, W, alpha: float) -> torch.Tensor:
+    """alpha (g[row_edges] + g[row_partner]) @ W^T per pair row: the last
+    layer's input gradient for weights shared by the two edges of a pair."""
+    E, n = g.shape
+    _req(g, "g_out", torch.float32, (E, n))
+    _req(W, "weight", torch.float32, (64, n))
+    gh = torch.empty(pairs.n_rows, 64, dtype=torch.float32, device=g.device)
+    tok = _t0("radial_mlp_out_bwd")
+    N.check(N.lib().tace_radial_mlp_out_bwd_pairs_f32(g.data_ptr(), pairs.row_edges.data_ptr(),
+                                                      pairs.row_partner.data_ptr(), pairs.n_rows, n, float(alpha),
+                                                      W.data_ptr(), gh.data_ptr(), N.stream_ptr(g.device)),
+            "tace_radial_mlp_out_bwd_pairs_f32")
+    _t1(tok, (E, n))
+    return gh
+
+
 class _MlpOut(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, W, alpha: float):
@@ -983,9 +1098,14 @@ class SegLinearPlan:
     (64, 64))."""
 
     def __init__(self, Z, out_blocks, ins, ranges, w_stride, b_stride, x_numel, y_numel, w_numel, b_numel, device,
-                 tile: Tuple[int, int] = (64, 64)):
+                 tile: Tuple[int, int] = (64, 64), split_weights: bool = False):
         TM, TN = tile
         self.tile = tuple(tile)
+        # split_weights: w_off / w_stride / w_numel index the pre-split planes
+        # (one plane), where a contribution's block is n columns of ceil8(k)
+        self.split_weights = bool(split_weights)
+        if self.split_weights and self.tile != (128, 128):
+            raise ValueError("pre-split weights run on the 128 x 128 float32 MFMA tiles")
         tiles, contribs, scales = [], [], []
         nc = 0
         for ob, (s_o, n, d, boff) in enumerate(out_blocks):
@@ -1034,8 +1154,11 @@ class SegLinearPlan:
             n_c = np.repeat(t[:, 2], t[:, 6] - t[:, 5])
             if (c[:, 0] + rows_c * c[:, 1]).max() > x_numel:
                 raise ValueError("seg linear plan: input tile out of range")
-            if (c[:, 2] + c[:, 1] * n_c).max() > w_numel:
+            kw = (c[:, 1] + 7) // 8 * 8 if self.split_weights else c[:, 1]
+            if (c[:, 2] + kw * n_c).max() > w_numel:
                 raise ValueError("seg linear plan: weight out of range")
+            if self.split_weights and (c[:, 2] % 8).any():
+                raise ValueError("seg linear plan: pre-split weight blocks must start on 8-element boundaries")
         self.n_tiles = len(t)
         self.x_numel, self.y_numel, self.w_numel, self.b_numel = x_numel, y_numel, w_numel, b_numel
         # multiply-adds x 2 of the whole launch (rows x valid columns x summed k
@@ -1068,6 +1191,54 @@ def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional
                                     None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(), plan.n_tiles,
                                     plan.contribs.data_ptr(), plan.scales.data_ptr(), float(alpha),
                                     N.stream_ptr(x.device)), "tace_seg_linear")
+    _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
+    return y
+
+
+def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int) -> torch.Tensor:
+    """``tace_bf16x3_split_blocks``: the three bf16 terms of scale x each
+    weight block, column-major runs of ceil8(k) (table rows: src_off, cols, k,
+    transpose, dst_off, 0); returns int16 planes [3 * plane_stride]."""
+    _req(w, "weight", torch.float32)
+    tab = np.asarray(blocks, dtype=np.int64).reshape(-1, 6)
+    if len(tab):
+        kpad = (tab[:, 2] + 7) // 8 * 8
+        if (tab[:, 0] + tab[:, 1] * tab[:, 2]).max() > w.numel():
+            raise ValueError("bf16x3 split: source block out of range")
+        if (tab[:, 4] + tab[:, 1] * kpad).max() > plane_stride:
+            raise ValueError("bf16x3 split: destination block out of range")
+    planes = torch.zeros(3 * plane_stride, dtype=torch.int16, device=w.device)
+    tb = torch.from_numpy(np.ascontiguousarray(tab)).to(w.device)
+    sc = torch.tensor(list(scales), dtype=torch.float64, device=w.device)
+    for b0 in range(0, len(tab), 65535):
+        b1 = min(len(tab), b0 + 65535)
+        N.check(N.lib().tace_bf16x3_split_blocks(w.data_ptr(), tb[b0:b1].data_ptr(), sc[b0:b1].data_ptr(), b1 - b0,
+                                                 planes.data_ptr(), plane_stride, N.stream_ptr(w.device)),
+                "tace_bf16x3_split_blocks")
+    return planes
+
+
+def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, plane_stride: int,
+                        bias: Optional[torch.Tensor], plan: SegLinearPlan, alpha: float) -> torch.Tensor:
+    """Runs a ``split_weights`` plan (``tace_seg_linear_presplit``) with the
+    weight planes of ``bf16x3_split_blocks``; returns y."""
+    if not plan.split_weights:
+        raise ValueError("seg linear: the plan indexes flat weights, not pre-split planes")
+    for t, nm, n in ((x, "x", plan.x_numel), (y, "y", plan.y_numel)):
+        _req(t, nm, torch.float32)
+        if t.numel() != n:
+            raise ValueError(f"seg linear: {nm} has {t.numel()} elements, the plan was built for {n}")
+    if planes.dtype != torch.int16 or planes.numel() != 3 * plane_stride or plane_stride < plan.w_numel:
+        raise ValueError("seg linear: weight planes do not match the plan")
+    if bias is not None:
+        _req(bias, "bias", torch.float32)
+        if bias.numel() != plan.b_numel:
+            raise ValueError("seg linear: bias size differs from the plan's")
+    tok = _t0("seg_linear")
+    N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride,
+                                             None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(),
+                                             plan.n_tiles, plan.contribs.data_ptr(), float(alpha),
+                                             N.stream_ptr(x.device)), "tace_seg_linear_presplit")
     _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
     return y
 

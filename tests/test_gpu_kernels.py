@@ -473,9 +473,10 @@ SEG_CASES = [("8x0e+5x0e+6x1o+4x1o+3x2e", "70x0e+6x1o+65x2e+2x3o", [0, 1, 17, 64
              ("1100x0e+300x1o", "256x0e+256x1o", [0, 300, 7, 129])]
 
 
-@pytest.mark.parametrize("dtype,tile", [(torch.float64, 64), (torch.float32, 128), (torch.float32, 64)])
+@pytest.mark.parametrize("dtype,tile,presplit", [(torch.float64, 64, False), (torch.float32, 128, True),
+                                                (torch.float32, 128, False), (torch.float32, 64, False)])
 @pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
-def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts, monkeypatch):
+def test_seg_linear_matches_reference(cuda, dtype, tile, presplit, irr_in, irr_out, counts, monkeypatch):
     """One-launch per-species linear (tace_seg_linear) against an independent
     per-node restatement: several inputs into one output block (two 0e, two
     1o), a 65-wide block (two column tiles, one partial), an output block no
@@ -485,6 +486,7 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts
     gradient."""
     from tace_amd import model as pm
     monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", tile)
+    monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", presplit)
     S, Z = len(counts), sum(counts)
     species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
     attrs = torch.nn.functional.one_hot(species, S).to(dtype)
@@ -515,6 +517,39 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, irr_in, irr_out, counts
     (gw_want,) = torch.autograd.grad(ref, wr, go)
     (gw,) = torch.autograd.grad(lin(xg, sp, alpha), lin.weight, go.to(cuda))
     close(gw, gw_want, dtype, "seg linear grad w")
+
+
+@pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
+def test_seg_linear_presplit_equals_in_kernel_split(cuda, irr_in, irr_out, counts, monkeypatch):
+    """The pre-split weight planes (tace_bf16x3_split_blocks +
+    tace_seg_linear_presplit) give the same bits as the kernel that splits
+    the weights in every launch: the same bf16 terms, the same products in
+    the same order.  After an in-place weight update the planes are rebuilt."""
+    from tace_amd import model as pm
+    monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", 128)
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).float().to(cuda)
+    g = torch.Generator().manual_seed(9)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) * 3.0)
+        lin.bias.copy_(torch.randn(lin.bias.shape, generator=g))
+    lin = lin.to(cuda)
+    sp = pm.SpeciesPlan(attrs)
+    x = torch.randn(Z, lin.lay.dim_in, generator=g).to(cuda).requires_grad_(True)
+    go = torch.randn(Z, lin.lay.dim_out, generator=g).to(cuda)
+    for step in range(2):
+        outs = {}
+        for presplit in (False, True):
+            monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", presplit)
+            y = lin(x, sp, 0.9)
+            (gx,) = torch.autograd.grad(y, x, go)
+            outs[presplit] = (y.detach(), gx)
+        assert torch.equal(outs[True][0], outs[False][0]), f"forward differs (step {step})"
+        assert torch.equal(outs[True][1], outs[False][1]), f"input gradient differs (step {step})"
+        with torch.no_grad():
+            lin.weight.mul_(-0.5)   # a new weight version: the cached planes must be rebuilt
 
 
 def test_seg_linear_f32_error_matches_float32_gemm(cuda):

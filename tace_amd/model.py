@@ -25,6 +25,7 @@ from __future__ import annotations
 import collections
 import copy
 import math
+import random
 from typing import Dict, List, Optional, Sequence, Tuple
 
 import torch
@@ -43,8 +44,13 @@ class SpeciesPlan:
     one contiguous row range.  ``perm[r]`` = node stored in row r,
     ``node_map[n]`` (int32) = row of node n (what the edge kernels take)."""
 
-    def __init__(self, attrs: torch.Tensor):
+    def __init__(self, attrs: torch.Tensor, exchange=None, pairs: Optional[ops.EdgePairs] = None):
         self.attrs = attrs
+        # LAMMPS ML-IAP data whose forward_exchange fills ghost rows before
+        # every interaction layer >= 1 (several domains), or None
+        self.exchange = exchange
+        # edge pairs whose radial weights are made once (None: per edge)
+        self.pairs = pairs
         species = attrs.argmax(dim=-1)
         self.perm = torch.argsort(species, stable=True)
         inv = torch.empty_like(self.perm)
@@ -106,6 +112,39 @@ def gm_to_e3nn(x: torch.Tensor, irreps) -> torch.Tensor:
     Z = x.shape[0]
     cols = [lay.block(x, b).view(Z, d, m).transpose(1, 2).reshape(Z, m * d) for b, (s, m, d) in enumerate(lay.blocks)]
     return torch.cat(cols, dim=1)
+
+
+class _GhostExchangeFn(torch.autograd.Function):
+    """``GhostExchange`` (``tace/models/lammps.py:82-102``) on this model's
+    node features (group-major rows in species order): every row goes out in
+    LAMMPS atom order and e3nn's mul_ir layout, ``forward_exchange`` replaces
+    the ghost rows by their owners' rows (possibly from another domain), and
+    the backward's ``reverse_exchange`` sums ghost-row gradients into their
+    owners."""
+
+    @staticmethod
+    def forward(ctx, x, irreps, sp: "SpeciesPlan", lmp_data):
+        rows = gm_to_e3nn(x, irreps).index_select(0, sp.inv).contiguous()
+        out = torch.empty_like(rows)
+        lmp_data.forward_exchange(rows, out, rows.shape[1])
+        ctx.irreps, ctx.sp, ctx.lmp = irreps, sp, lmp_data
+        return e3nn_to_gm(out.index_select(0, sp.perm), irreps)
+
+    @staticmethod
+    def backward(ctx, g):
+        rows = gm_to_e3nn(g.contiguous(), ctx.irreps).index_select(0, ctx.sp.inv).contiguous()
+        gin = torch.empty_like(rows)
+        ctx.lmp.reverse_exchange(rows, gin, rows.shape[1])
+        return e3nn_to_gm(gin.index_select(0, ctx.sp.perm), ctx.irreps), None, None, None
+
+
+def _exchange_ghosts(x: torch.Tensor, irreps, sp: "SpeciesPlan", layer: int) -> torch.Tensor:
+    """``handle_lammps`` (``tace/models/lammps.py:105-134``, called after
+    linear_up at ``_e3nn/inter.py:228``): no exchange in layer 0 (ghost
+    features come from their own embedding), the owners' rows from layer 1."""
+    if sp.exchange is None or layer == 0:
+        return x
+    return _GhostExchangeFn.apply(x, irreps, sp, sp.exchange)
 
 
 # ---------------------------------------------------------------- linears ----
@@ -543,9 +582,9 @@ class O3CgtpInteraction(torch.nn.Module):
     def forward(self, x, sp: SpeciesPlan, R, Y, plan: ops.EdgePlan):
         """x: group-major node features in species-sorted row order."""
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
-        x = self.linear_up(x)
+        x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
         lay = ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED
-        pairs = plan._pairs if PAIR_RADIAL else None
+        pairs = sp.pairs
         if pairs is not None and self.edge_info.fused:
             # the radial weights depend on the edge length only: made once per
             # edge pair and read by both directions
@@ -603,7 +642,7 @@ class TeceInteraction(torch.nn.Module):
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
         from . import tece
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
-        x = self.linear_up(x)
+        x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
         if tece.FUSED and tece.fused_supported(self.rejector, self.edge_info):
             msg = tece.tece_fused(self.rejector, self.edge_info, x, sp.node_map, R, plan, src, dst, wigner,
                                   self.chunk_edges)
@@ -921,12 +960,17 @@ class TACE(torch.nn.Module):
             dtype=torch.get_default_dtype()))
         self.scale_shift.register_buffer("shift", torch.zeros(len(stats), len(zs), dtype=torch.get_default_dtype()))
 
-    def energy(self, data, plan: ops.EdgePlan, edge_vector):
+    def energy(self, data, plan: ops.EdgePlan, edge_vector, exchange=None, pairs: Optional[ops.EdgePairs] = None):
         """Energy branch of ``readout_fn`` (``tace.py:356-418``) + ``ScaleShift``
-        (``blocks.py:289-379``), fidelity 0."""
+        (``blocks.py:289-379``), fidelity 0.  ``exchange``: LAMMPS ML-IAP data
+        for the per-layer ghost exchange (several domains).  ``pairs``: make
+        the radial weights once per edge pair (the energy and its gradients
+        with respect to positions and cell are unchanged; the gradient with
+        respect to each edge vector is not split between the two directions,
+        so callers that want per-edge gradients pass None)."""
         attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
         num_graphs = ptr.numel() - 1
-        sp = SpeciesPlan(attrs)
+        sp = SpeciesPlan(attrs, exchange, pairs)
         x = self.representation(attrs, plan, edge_vector, sp, data["edge_index"])
         e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
@@ -1099,26 +1143,31 @@ class TensorModel(torch.nn.Module):
         return super().load_state_dict(sd, strict=strict, assign=assign)
 
     @staticmethod
-    def _ghost_owners(lmp_data, nlocal: int, nghosts: int, like: torch.Tensor) -> torch.Tensor:
-        """Local atom that each of the nlocal + nghosts LAMMPS atoms stands for:
-        one width-1 ``forward_exchange`` of the local indices
-        (``models/lammps.py:82-102`` semantics: ghost rows are copied from
-        their owners)."""
+    def _ghost_owners(lmp_data, nlocal: int, nghosts: int, like: torch.Tensor) -> Optional[torch.Tensor]:
+        """Local atom that each of the nlocal + nghosts LAMMPS atoms stands
+        for, from one width-2 ``forward_exchange`` of (local index, a random
+        token of this call) (``models/lammps.py:82-102`` semantics: ghost rows
+        are copied from their owners).  None when some ghost's row carries
+        another token: it is owned by another domain, and the model then runs
+        the per-layer exchange instead."""
         ntotal = nlocal + nghosts
         ids = torch.arange(ntotal, device=like.device)
         if nghosts == 0:
             return ids
         if lmp_data is None or not hasattr(lmp_data, "forward_exchange"):
             raise RuntimeError("LAMMPS mode with ghost atoms needs lmp_data with forward_exchange")
-        col = torch.zeros(ntotal, 1, dtype=like.dtype, device=like.device)
+        token = 1.0 + random.random()
+        col = torch.zeros(ntotal, 2, dtype=like.dtype, device=like.device)
         col[:nlocal, 0] = torch.arange(nlocal, device=like.device, dtype=like.dtype)
+        col[:nlocal, 1] = token
         out = torch.empty_like(col)
-        lmp_data.forward_exchange(col, out, 1)
+        lmp_data.forward_exchange(col, out, 2)
+        if bool((out[nlocal:, 1] != token).any()):
+            return None
         owner = out[:, 0].round().long()
         owner[:nlocal] = ids[:nlocal]
         if bool(((owner < 0) | (owner >= nlocal)).any()):
-            raise RuntimeError("ghost exchange returned owners outside the local atoms (a multi-domain run: the "
-                               "MI355X path covers one LAMMPS domain)")
+            raise RuntimeError("ghost exchange returned owners outside the local atoms")
         return owner
 
     def _forward_lammps(self, data: Dict[str, torch.Tensor]) -> Dict[str, Optional[torch.Tensor]]:
@@ -1127,10 +1176,13 @@ class TensorModel(torch.nn.Module):
         ``edge_index`` = [neighbour j, local i] over nlocal + nghosts atoms
         (``natoms``); returns the local energies and ``edge_forces`` =
         dE/d(edge_vector).  A ghost atom's features equal its owner's in every
-        layer (the reference's per-layer ghost exchange), so each ghost sender
-        is replaced by its owner and the graph is the periodic one on the
-        local atoms; the gradients the exchange's reverse pass would sum into
-        the owners are summed there by the sender CSR."""
+        layer >= 1 (the reference's per-layer ghost exchange).  When every
+        ghost is owned by this domain, each ghost sender is replaced by its
+        owner and the graph is the periodic one on the local atoms (the sender
+        CSR sums what the exchange's reverse pass would); otherwise the model
+        runs on all nlocal + nghosts rows and exchanges the ghost rows through
+        ``lmp_data`` before every interaction layer >= 1, as the reference
+        does (``_e3nn/inter.py:228``, ``models/lammps.py:105-134``)."""
         nlocal, nghosts = (int(v) for v in data["natoms"])
         vec = data["edge_vector"]
         if not vec.is_cuda:
@@ -1140,12 +1192,22 @@ class TensorModel(torch.nn.Module):
         ei = data["edge_index"]
         if ei.numel() and int(ei[1].max()) >= nlocal:
             raise ValueError("LAMMPS mode: every edge's receiver (edge_index[1]) must be a local atom")
-        owner = self._ghost_owners(_opt(data, "lmp_data"), nlocal, nghosts, vec)
-        ei = torch.stack([owner[ei[0]], ei[1]])
-        attrs = data["node_attrs"][:nlocal]
-        d = dict(node_attrs=attrs, edge_index=ei, batch=data["batch"][:nlocal], ptr=data["ptr"])
-        plan = ops.EdgePlan.from_edge_index(ei, nlocal)
-        E, e_node = self.readout_fn.energy(d, plan, vec)
+        lmp_data = _opt(data, "lmp_data")
+        owner = self._ghost_owners(lmp_data, nlocal, nghosts, vec)
+        if owner is not None:
+            ei = torch.stack([owner[ei[0]], ei[1]])
+            n = nlocal
+            exchange = None
+        else:
+            n = nlocal + nghosts
+            exchange = lmp_data
+        attrs = data["node_attrs"][:n]
+        d = dict(node_attrs=attrs, edge_index=ei, batch=torch.zeros(n, dtype=torch.int64, device=vec.device),
+                 ptr=torch.tensor([0, n], dtype=torch.int64, device=vec.device))
+        plan = ops.EdgePlan.from_edge_index(ei, n)
+        _, e_node = self.readout_fn.energy(d, plan, vec, exchange)
+        e_node = e_node[:nlocal]
+        E = e_node.sum().view(1)
         out: Dict[str, Optional[torch.Tensor]] = dict(energy=E.detach(), node_energy=e_node.detach(), forces=None,
                                                       stress=None, virials=None, edge_forces=None)
         if self.flags.compute_edge_forces:
@@ -1188,9 +1250,10 @@ class TensorModel(torch.nn.Module):
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
         plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
-        if PAIR_RADIAL and plan.n_edges:
+        pairs = None
+        if PAIR_RADIAL and plan.n_edges and not want_e:
             sh32 = _opt(data, "_shifts32")
-            plan.edge_pairs(sh32 if sh32 is not None else shifts)
+            pairs = plan.edge_pairs(sh32 if sh32 is not None else shifts)
         # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
         # +1e-9 of the length is applied in the edge-basis kernel
         dst32 = _opt(data, "_dst32")
@@ -1198,7 +1261,7 @@ class TensorModel(torch.nn.Module):
             dst32 = ei[1].to(torch.int32)
         egraph = None if num_graphs == 1 else batch[ei[0]].to(torch.int32)
         vec = ops.edge_vectors(pos_s, lat_s, shifts, plan, dst32, egraph)
-        E, e_node = self.readout_fn.energy(data, plan, vec)
+        E, e_node = self.readout_fn.energy(data, plan, vec, pairs=pairs)
         out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, virials=None,
                                                       stress=None, edge_forces=None, atomic_virials=None,
                                                       atomic_stresses=None)

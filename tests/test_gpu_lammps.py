@@ -148,3 +148,38 @@ def test_atomic_virials_sum_to_the_virial(cuda):
                        d64["batch"], d64["ptr"], 2)
     (gv,) = torch.autograd.grad(E0.sum(), vec)
     assert (out["edge_forces"].cpu() - gv).abs().max().item() < 1e-8
+
+
+
+@pytest.mark.parametrize("preset", ["si64", "tece"])
+def test_lammps_two_domains_match_single_domain(cuda, tmp_path, preset):
+    """The periodic cell split into two LAMMPS domains (x < L/2 and the rest),
+    each with its own ghosts, run by two processes (one per domain, as MPI
+    ranks would be) on the one GPU with the per-layer ghost exchange over a
+    gloo stand-in for LAMMPS's communication: the two local energies add up
+    to the oracle's energy and every edge's dE/d(edge vector) equals the
+    oracle's (float64 bars)."""
+    import os
+    import socket
+    import sys
+
+    import torch.multiprocessing as mp
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import _lammps_domains as ld
+
+    setup = ld.setup(preset)
+    with socket.socket() as sk:
+        sk.bind(("127.0.0.1", 0))
+        port = sk.getsockname()[1]
+    mp.spawn(ld.worker, args=(port, str(tmp_path), preset), nprocs=2, join=True)
+    ei, vec, E0, gv0, dom = setup["ei"], setup["vec"], setup["E0"], setup["gv0"], setup["dom"]
+    E = 0.0
+    for d in (0, 1):
+        r = np.load(tmp_path / f"dom{d}.npz")
+        E += float(r["energy"][0])
+        mine = (dom[ei[1]] == d).nonzero().squeeze(1).numpy()
+        assert (r["mine"] == mine).all()
+        assert np.abs(r["edge_forces"] - gv0.numpy()[mine]).max() < 1e-8
+        assert int(r["n_ghost_foreign"][0]) > 0   # the exchange really crossed domains
+    assert abs(E - float(E0[0])) < 1e-10 * abs(float(E0[0])), (E, E0)

@@ -616,7 +616,8 @@ class TACE(torch.nn.Module):
         return E, e_base_node + e_node
 
 
-def compute(model: TACE, data: Dict[str, torch.Tensor], forces: bool = True, stress: bool = False):
+def compute(model: TACE, data: Dict[str, torch.Tensor], forces: bool = True, stress: bool = False,
+            create_graph: bool = False):
     """``TensorModel.forward`` restated (``tace/models/adapter.py:32-174, 278-384``):
     edge vectors from (strained) positions, E, F = -dE/dr, S = -V/|det L| with
     V = -dE/d(eps) (``compute_symmetric_displacement``, ``models/utils.py:50-79``)."""
@@ -638,9 +639,12 @@ def compute(model: TACE, data: Dict[str, torch.Tensor], forces: bool = True, str
     vec = pos_s[dst] - pos_s[src] + torch.einsum("ni,nij->nj", data["edge_shifts"], lat_s[batch[src]])
     length = (vec ** 2).sum(dim=1, keepdim=True).sqrt() + 1e-9
     E, e_node = model.energy(data["node_attrs"], data["edge_index"], vec, length, batch, ptr, num_graphs)
-    out = {"energy": E.detach(), "node_energy": e_node.detach()}
+    # create_graph: keep the graph of the derivatives (training with a force
+    # loss, adapter.py:95-104), energies not detached
+    out = {"energy": E if create_graph else E.detach(), "node_energy": e_node if create_graph else e_node.detach()}
     if forces or stress:
-        grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True)
+        grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True,
+                                    create_graph=create_graph, retain_graph=create_graph)
         out["forces"] = -grads[0] if grads[0] is not None else torch.zeros_like(pos)
         if stress:
             V = -grads[1] if grads[1] is not None else torch.zeros_like(lattice)

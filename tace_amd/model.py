@@ -361,6 +361,37 @@ class _LinearFn(torch.autograd.Function):
         return gx, gw, gb, None, None, None
 
 
+def _linear_autograd(x, weight, bias, lay: _LinearLayout, ranges, alpha: float) -> torch.Tensor:
+    """``_LinearFn`` as plain torch operations (differentiable to any order):
+    per output block and species range, the sum over its instructions of
+    pw * x_block @ W, plus the bias on 0e blocks, times alpha; group-major out."""
+    Z = x.shape[0]
+    shared = weight.dim() == 1
+    rr = [(None, 0, Z)] if shared else [r for r in ranges if r[2] > r[1]]
+    if Z == 0 or not rr:
+        return x.new_zeros(Z, lay.dim_out)
+    boffs = {o: (boff, m) for (o, boff, m) in lay.bias_blocks}
+    flat = []
+    for o, (_s, m_o, d_o) in enumerate(lay.gout.blocks):
+        parts = []
+        for (sp, a, b) in rr:
+            acc = None
+            for (i, oo, off, mi, mo, pw) in lay.ins:
+                if oo != o:
+                    continue
+                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
+                t = torch.mm(lay.gin.block(x, i, a, b), W) * pw
+                acc = t if acc is None else acc + t
+            if acc is None:
+                acc = x.new_zeros((b - a) * d_o, m_o)
+            if bias is not None and o in boffs:
+                boff, m = boffs[o]
+                acc = acc + (bias if shared else bias[sp])[boff:boff + m]
+            parts.append(acc)
+        flat.append((torch.cat(parts, 0) if len(parts) > 1 else parts[0]).reshape(-1))
+    return (torch.cat(flat) * alpha).view(Z, lay.dim_out)
+
+
 class e3nnLinear(torch.nn.Module):
     """Parameters ``weight`` [numel] ~ N(0,1), ``bias`` [#0e] zeros
     (``linear.py:282-374``); group-major input and output."""
@@ -373,6 +404,8 @@ class e3nnLinear(torch.nn.Module):
         self.bias = torch.nn.Parameter(torch.zeros(self.lay.bias_numel)) if bias and self.lay.bias_numel else None
 
     def forward(self, x, alpha: float = 1.0):
+        if ops.MODE.double:
+            return _linear_autograd(x.contiguous(), self.weight, self.bias, self.lay, None, float(alpha))
         return _LinearFn.apply(x.contiguous(), self.weight, self.bias, self.lay, None, float(alpha))
 
 
@@ -391,6 +424,8 @@ class e3nnElementLinear(torch.nn.Module):
                      if bias and self.lay.bias_numel else None)
 
     def forward(self, x: torch.Tensor, sp: SpeciesPlan, alpha: float = 1.0) -> torch.Tensor:
+        if ops.MODE.double:
+            return _linear_autograd(x.contiguous(), self.weight, self.bias, self.lay, sp.ranges, float(alpha))
         return _LinearFn.apply(x.contiguous(), self.weight, self.bias, self.lay, sp.ranges, float(alpha))
 
 
@@ -426,7 +461,7 @@ class MLP(torch.nn.Module):
         self.fused = len(dims) >= 3 and all(h == 64 for h in dims[1:-1]) and dims[0] <= 32 and len(dims) - 2 <= 4
 
     def forward(self, x):
-        if not self.fused:
+        if not self.fused or ops.MODE.double:
             return self.mlp(x)
         return ops.radial_mlp_out(self.hidden(x), *self.last_layer())
 
@@ -536,6 +571,18 @@ class _GateFn(torch.autograd.Function):
         return gx, None, None, None
 
 
+def _gate(x: torch.Tensor, lin: GMLayout, lout: GMLayout, C: int) -> torch.Tensor:
+    """``_GateFn``; inside ``ops.differentiable_twice`` as plain torch operations."""
+    if not ops.MODE.double:
+        return _GateFn.apply(x, lin, lout, C)
+    Z = x.shape[0]
+    ng = len(lout.blocks)
+    g = torch.sigmoid(lin.block(x, 0).view(Z, -1)[:, :ng * C]) * SIGMOID_CST
+    out = [(src * g[:, k * C:(k + 1) * C].unsqueeze(1)).reshape(-1)
+           for k, src in enumerate(_gated_blocks(x, lin, lout, C))]
+    return torch.cat(out).view(Z, lout.dim)
+
+
 def _gated_blocks(x: torch.Tensor, lin: GMLayout, lout: GMLayout, C: int) -> List[torch.Tensor]:
     """[Z, 2l+1, C] views of the gated irreps inside the gate's input."""
     Z = x.shape[0]
@@ -585,7 +632,9 @@ class O3CgtpInteraction(torch.nn.Module):
         x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
         lay = ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED
         pairs = sp.pairs
-        if pairs is not None and self.edge_info.fused:
+        if ops.MODE.double:
+            m = self.rejector(x, Y, self.edge_info(R), plan, lay, sp.node_map)
+        elif pairs is not None and self.edge_info.fused:
             # the radial weights depend on the edge length only: made once per
             # edge pair and read by both directions
             h = self.edge_info.hidden(R.index_select(0, pairs.row_edges))
@@ -597,7 +646,7 @@ class O3CgtpInteraction(torch.nn.Module):
             m = self.rejector(x, Y, self.edge_info(R), plan, lay, sp.node_map)
         # linear_down(m) / avg_num_neighbors, the division in the GEMM scale
         m = self.linear_down(m, alpha=1.0 / self.avg_num_neighbors)
-        m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))
+        m = self.linear_nonlinearity(_gate(m, *self._gate_lay, self.C))
         return m, sc
 
 
@@ -641,6 +690,9 @@ class TeceInteraction(torch.nn.Module):
 
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
         from . import tece
+        if ops.MODE.double:
+            raise NotImplementedError("the TECE convolution is differentiable once on the MI355X path: "
+                                      "no create_graph / training-mode forces through it")
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
         if tece.FUSED and tece.fused_supported(self.rejector, self.edge_info):
@@ -651,7 +703,7 @@ class TeceInteraction(torch.nn.Module):
         else:
             msg = self._chunked(x, sp, R, plan, src, dst, wigner)
         m = self.linear_down(msg)
-        m = self.linear_nonlinearity(_GateFn.apply(m, *self._gate_lay, self.C))
+        m = self.linear_nonlinearity(_gate(m, *self._gate_lay, self.C))
         return m, sc
 
 
@@ -1250,8 +1302,19 @@ class TensorModel(torch.nn.Module):
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
         plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
+        # adapter.py:95-104: training (or create_graph) keeps the graph of the
+        # derivatives, so that a loss on forces / stress can be differentiated
+        # with respect to the parameters; the operators then take their
+        # twice-differentiable form
+        cg = bool(self.training or self.create_graph)
+        with ops.differentiable_twice(cg):
+            return self._forward_graph(data, pos, lattice, batch, shifts, num_graphs, inputs, pos_s, lat_s, ei, plan,
+                                       want_f, want_s, want_e, cg)
+
+    def _forward_graph(self, data, pos, lattice, batch, shifts, num_graphs, inputs, pos_s, lat_s, ei, plan,
+                       want_f: bool, want_s: bool, want_e: bool, cg: bool):
         pairs = None
-        if PAIR_RADIAL and plan.n_edges and not want_e:
+        if PAIR_RADIAL and plan.n_edges and not want_e and not cg:
             sh32 = _opt(data, "_shifts32")
             pairs = plan.edge_pairs(sh32 if sh32 is not None else shifts)
         # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
@@ -1268,7 +1331,8 @@ class TensorModel(torch.nn.Module):
         if want_e:
             inputs.append(vec)
         if inputs:
-            grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True)
+            grads = torch.autograd.grad(E, inputs, grad_outputs=torch.ones_like(E), allow_unused=True,
+                                        retain_graph=cg or self.retain_graph, create_graph=cg)
             k = 0
             if want_f:
                 out["forces"] = -grads[0] if grads[0] is not None else torch.zeros_like(pos)
@@ -1284,8 +1348,9 @@ class TensorModel(torch.nn.Module):
                 out["edge_forces"] = ef
                 out["atomic_virials"], out["atomic_stresses"] = _atomic_virials(vec.detach(), ef, ei, lattice, batch,
                                                                                 pos.shape[0])
-        out["energy"] = out["energy"].detach()
-        out["node_energy"] = out["node_energy"].detach()
+        if not cg:
+            out["energy"] = out["energy"].detach()
+            out["node_energy"] = out["node_energy"].detach()
         return out
 
 

@@ -14,6 +14,9 @@ raises if the native library is missing -- there is no CPU path.
 
 from __future__ import annotations
 
+import contextlib
+import threading
+
 import ctypes
 import math
 from dataclasses import dataclass
@@ -50,6 +53,33 @@ class KernelTimer:
 
 
 TIMER = None
+
+
+class _Mode(threading.local):
+    """Per-thread switch of the operators' autograd form (see ``differentiable_twice``)."""
+
+    double = False
+
+
+MODE = _Mode()
+
+
+@contextlib.contextmanager
+def differentiable_twice(on: bool = True):
+    """Inside this context the model's operators take a form whose backward is
+    itself differentiable: the edge and node tensor products on the HIP
+    kernels through operators whose backward is written with the forward and
+    backward operators (``_EdgeTPD``, ``_UUUD``), everything else (edge
+    vectors, radial basis and harmonics, radial MLP, linears, gate) as plain
+    torch operations.  This is what training with a force loss needs
+    (``create_graph=True`` in ``tace/models/adapter.py:95-104``); outside it the
+    inference operators run (first-order backward, frozen radial weights)."""
+    prev = MODE.double
+    MODE.double = bool(on)
+    try:
+        yield
+    finally:
+        MODE.double = prev
 
 
 def _t0(name):
@@ -225,8 +255,48 @@ class _EdgeBasis(torch.autograd.Function):
         return gvec, None, None, None, None, None
 
 
+def spherical_harmonics(u: torch.Tensor, lmax: int) -> torch.Tensor:
+    """e3nn's real spherical harmonics of the rows of u [E, 3], component
+    normalisation, polar axis y, m = -l..l within each l (the closed forms the
+    edge-basis kernel evaluates), as torch operations: [E, (lmax + 1)^2]."""
+    x, y, z = u[:, 0], u[:, 1], u[:, 2]
+    out = [torch.ones_like(x)]
+    if lmax >= 1:
+        s3 = math.sqrt(3.0)
+        out += [s3 * x, s3 * y, s3 * z]
+    if lmax >= 2:
+        s15, s5 = math.sqrt(15.0), math.sqrt(5.0)
+        y2, xz2 = y * y, x * x + z * z
+        q = [s15 * x * z, s15 * x * y, s5 * (y2 - 0.5 * xz2), s15 * y * z, 0.5 * s15 * (z * z - x * x)]
+        out += q
+    if lmax >= 3:
+        c42, c7, c168 = math.sqrt(42.0) / 6.0, math.sqrt(7.0), math.sqrt(168.0) / 8.0
+        t = 4.0 * y2 - xz2
+        out += [c42 * (q[0] * z + q[4] * x), c7 * q[0] * y, c168 * t * x, 0.5 * c7 * y * (2.0 * y2 - 3.0 * xz2),
+                c168 * t * z, c7 * q[4] * y, c42 * (q[4] * z - q[0] * x)]
+    if lmax > 3:
+        raise ValueError("spherical harmonics up to l = 3")
+    return torch.stack(out, dim=1)
+
+
+def _edge_basis_autograd(vec, bessel_w, prefactor: float, cutoff: float, p: int, lmax: int):
+    """The edge-basis kernel's arithmetic as torch operations: length + 1e-9
+    (adapter.py:347), j0 Bessel x C2 polynomial cutoff (radial.py:43-84,
+    437-472), harmonics of vec / length (representation.py:321-324)."""
+    r = torch.sqrt((vec * vec).sum(dim=1, keepdim=True)) + 1e-9
+    x = r / cutoff
+    c1, c2, c3 = (p + 1.0) * (p + 2.0) / 2.0, p * (p + 2.0), p * (p + 1.0) / 2.0
+    xp = x ** p
+    env = 1.0 - c1 * xp + c2 * (xp * x) - c3 * (xp * x * x)
+    env = torch.where(r < cutoff, env, torch.zeros_like(env))
+    R = prefactor * (torch.sin(bessel_w * r) / r) * env
+    return R, spherical_harmonics(vec / r, lmax)
+
+
 def edge_basis(vec: torch.Tensor, bessel_w: torch.Tensor, prefactor: float, cutoff: float, p: int,
                lmax: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    if MODE.double:
+        return _edge_basis_autograd(vec, bessel_w, float(prefactor), float(cutoff), int(p), int(lmax))
     return _EdgeBasis.apply(vec.contiguous(), bessel_w.contiguous(), float(prefactor), float(cutoff), int(p),
                             int(lmax))
 
@@ -293,6 +363,46 @@ class _EdgeTP(torch.autograd.Function):
         return gx, gy, gw, None, None, None, None, None
 
 
+# Double backward of the edge product.  out = TP(x, y, w) is trilinear and its
+# backward (gx, gy, gw) is multilinear in (x, y, w, g) with gx(y, w, g),
+# gy(x, w, g), gw(x, y, g).  For upstream gradients (ax, ay, aw):
+#   d/dg = TP(ax, y, w) + TP(x, ay, w) + TP(x, y, aw)
+#   d/dx = gx of bwd(x, ay, w, g) + gx of bwd(x, y, aw, g)
+#   d/dy = gy of bwd(ax, y, w, g) + gy of bwd(x, y, aw, g)
+#   d/dw = gw of bwd(ax, y, w, g) + gw of bwd(x, ay, w, g)
+# -- the same two operators again, so every order is differentiable.
+class _EdgeTPD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int, node_map):
+        ctx.save_for_backward(x, y, w)
+        ctx.args = (plan, var, C, layout, node_map)
+        return launch_edge_tp_fwd(x, y, w, plan, var, C, layout, node_map)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, y, w = ctx.saved_tensors
+        gx, gy, gw = _EdgeTPBwdD.apply(x, y, w, g.contiguous(), *ctx.args)
+        return gx, gy, gw, None, None, None, None, None
+
+
+class _EdgeTPBwdD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, y, w, g, plan: EdgePlan, var: TpVariant, C: int, layout: int, node_map):
+        ctx.save_for_backward(x, y, w, g)
+        ctx.args = (plan, var, C, layout, node_map)
+        return launch_edge_tp_bwd(x, y, w, g, plan, var, C, layout, node_map, True)
+
+    @staticmethod
+    def backward(ctx, ax, ay, aw):
+        x, y, w, g = ctx.saved_tensors
+        a = ctx.args
+        zx, zy, zw = (t.contiguous() if t is not None else torch.zeros_like(r) for t, r in ((ax, x), (ay, y), (aw, w)))
+        F, B = _EdgeTPD.apply, _EdgeTPBwdD.apply
+        gg = F(zx, y, w, *a) + F(x, zy, w, *a) + F(x, y, zw, *a)
+        bx, by, bw = B(zx, y, w, g, *a), B(x, zy, w, g, *a), B(x, y, zw, g, *a)
+        return by[0] + bw[0], bx[1] + bw[1], bx[2] + by[2], gg, None, None, None, None, None
+
+
 def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int = 0,
                     node_map: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Fused uvu tensor product + receiver scatter.  ``layout``: combination of
@@ -301,6 +411,8 @@ def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int
     features are stored in another order than the edges index (None: same)."""
     if node_map is not None:
         _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
+    if MODE.double:
+        return _EdgeTPD.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout), node_map)
     return _EdgeTP.apply(x.contiguous(), y.contiguous(), w.contiguous(), plan, var, C, int(layout), node_map)
 
 
@@ -485,6 +597,10 @@ def edge_vectors(pos, lattice, shifts, plan: EdgePlan, dst: torch.Tensor, edge_g
     """vec[e] = pos[dst] - pos[src] + shifts[e] . lattice[edge_graph[e]]
     (``tace/models/adapter.py:334-340``) with a deterministic CSR backward.
     ``dst`` int32 [E] in edge-id order; ``edge_graph`` int32 [E] or None (one graph)."""
+    if MODE.double:
+        # adapter.py:334-340 as torch operations (differentiable to any order)
+        L = lattice[edge_graph.long()] if edge_graph is not None else lattice[0].expand(plan.n_edges, 3, 3)
+        return pos[dst.long()] - pos[plan.src.long()] + torch.einsum("ei,eij->ej", shifts.to(pos.dtype), L)
     if dst.dtype != torch.int32:
         dst = dst.to(torch.int32)
     if edge_graph is not None and edge_graph.dtype != torch.int32:
@@ -545,11 +661,60 @@ class _UUU(torch.autograd.Function):
         return g1, g2, gw, None, None, None
 
 
+# Double backward of the node product: (g1, g2, gw) are multilinear in
+# (x1, x2, w, g) with g1 free of x1, g2 free of x2 and gw free of w (the scheme
+# of the edge product above).  Identical inputs pass one tensor twice and
+# autograd adds the two contributions.
+class _UUUD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x1, x2, w, var: TpVariant, C: int, layout: int):
+        ctx.save_for_backward(x1, x2, w)
+        ctx.args = (var, C, layout)
+        return launch_uuu_fwd(x1, x2, w, var, C, layout)
+
+    @staticmethod
+    def backward(ctx, g):
+        x1, x2, w = ctx.saved_tensors
+        g1, g2, gw = _UUUBwdD.apply(x1, x2, w, g.contiguous(), *ctx.args)
+        return g1, g2, (gw if w is not None else None), None, None, None
+
+
+class _UUUBwdD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x1, x2, w, g, var: TpVariant, C: int, layout: int):
+        ctx.save_for_backward(x1, x2, w, g)
+        ctx.args = (var, C, layout)
+        g1, g2, gw = launch_uuu_bwd(x1, x2, w, g, var, C, layout)
+        return g1, g2, gw if gw is not None else x1.new_zeros(0)
+
+    @staticmethod
+    def backward(ctx, a1, a2, aw):
+        x1, x2, w, g = ctx.saved_tensors
+        a = ctx.args
+        z1 = a1.contiguous() if a1 is not None else torch.zeros_like(x1)
+        z2 = a2.contiguous() if a2 is not None else torch.zeros_like(x2)
+        F, B = _UUUD.apply, _UUUBwdD.apply
+        gg = F(z1, x2, w, *a) + F(x1, z2, w, *a)
+        b1, b2 = B(z1, x2, w, g, *a), B(x1, z2, w, g, *a)
+        d1, d2, dw = b2[0], b1[1], None
+        if w is not None:
+            dw = b1[2] + b2[2]
+            if aw is not None and aw.numel():
+                zw = aw.contiguous()
+                gg = gg + F(x1, x2, zw, *a)
+                bw = B(x1, x2, zw, g, *a)
+                d1, d2 = d1 + bw[0], d2 + bw[1]
+        return d1, d2, dw, gg, None, None, None
+
+
 def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0, w: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``layout`` = 0 (e3nn operands), LAYOUT_OUT_GROUPED, IN1|OUT or
     IN1|OUT|IN2 (LAYOUT_ALL_GROUPED): the group-major layout of
     ``include/tace_hip.h`` for x1 / out / x2.  ``w`` [N, npath*C]: per-node
     path weights (bilinear-gate product basis)."""
+    if MODE.double:
+        return _UUUD.apply(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(), var, C,
+                           int(layout))
     return _UUU.apply(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(), var, C, int(layout))
 
 

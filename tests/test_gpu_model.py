@@ -38,7 +38,7 @@ def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, **over):
         torch.set_default_dtype(prev)
     pm.load_reference_state_dict(gpu.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
                                                   for k, v in ref.state_dict().items()})
-    gpu = gpu.to(cuda)
+    gpu = gpu.to(cuda).eval()   # inference, as the calculators set it
     if not stress:
         gpu.reset_target_property(["energy", "forces"])
     dg = data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda)
@@ -96,7 +96,7 @@ def test_gpu_neighbour_list_feeds_model(cuda):
     cfg = configs.model_cfg("fcc1024", sorted(set(s["numbers"].tolist())), edges[0][0].shape[1] / len(s["numbers"]),
                             num_channel=32)
     torch.manual_seed(1)
-    gpu = pm.create_model(cfg).double().to(cuda)
+    gpu = pm.create_model(cfg).double().to(cuda).eval()
     gpu.reset_target_property(["energy", "forces"])
     a = gpu(data.collate([s], edges, cfg["atomic_numbers"], dtype=torch.float64, device=cuda))
     g = data.gpu_graph([s], cfg["atomic_numbers"], 5.0, dtype=torch.float64, device=cuda)
@@ -117,7 +117,7 @@ def test_batched_gpu_neighbour_list_feeds_model(cuda):
     nat = sum(len(s["positions"]) for s in structs)
     cfg = configs.model_cfg("si64", zs, sum(e[0].shape[1] for e in edges) / nat, num_channel=16)
     torch.manual_seed(4)
-    gpu = pm.create_model(cfg).double().to(cuda)
+    gpu = pm.create_model(cfg).double().to(cuda).eval()
     a = gpu(data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float64, device=cuda))
     g = data.gpu_graph(structs, cfg["atomic_numbers"], 5.0, dtype=torch.float64, device=cuda)
     assert g["edge_index"].shape[1] == sum(e[0].shape[1] for e in edges)

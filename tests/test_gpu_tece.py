@@ -409,7 +409,7 @@ def _model_pair(structs, cuda, dtype, seed=0, chunk_edges=None, mixing=None, fro
         torch.set_default_dtype(prev)
     pm.load_reference_state_dict(gpu.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
                                                   for k, v in ref.state_dict().items()})
-    gpu = gpu.to(cuda)
+    gpu = gpu.to(cuda).eval()   # inference (training mode would ask for create_graph)
     gpu.reset_target_property(["energy", "forces"])
     if mixing is not None:
         assert pm.set_tece_channel_mixing(gpu, mixing) > 0

@@ -690,12 +690,12 @@ class TeceInteraction(torch.nn.Module):
 
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
         from . import tece
-        if ops.MODE.double:
-            raise NotImplementedError("the TECE convolution is differentiable once on the MI355X path: "
-                                      "no create_graph / training-mode forces through it")
         sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
         x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
-        if tece.FUSED and tece.fused_supported(self.rejector, self.edge_info):
+        if ops.MODE.double:
+            # training: the whole convolution as torch operations (twice differentiable)
+            msg = self.rejector(x, self.edge_info(R), plan, sp.node_map, src, dst, wigner, R)
+        elif tece.FUSED and tece.fused_supported(self.rejector, self.edge_info):
             msg = tece.tece_fused(self.rejector, self.edge_info, x, sp.node_map, R, plan, src, dst, wigner,
                                   self.chunk_edges)
         elif plan.n_edges <= self.chunk_edges:

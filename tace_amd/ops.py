@@ -746,9 +746,76 @@ class _EdgeWigner(torch.autograd.Function):
         return gv, None
 
 
+def _edge_frame_autograd(vec: torch.Tensor) -> torch.Tensor:
+    """The edge-frame kernel's rotation R [E, 3, 3] (R @ vec/|vec| = +y) as
+    torch operations: quaternion charts q+ = (1+y, -z, 0, x), q- = (-z, 1-y,
+    x, 0) (w, x, y, z), normalised with eps^2 = 1e-14 inside the root, q+
+    flipped onto q-'s hemisphere, nlerp with the C-infinity step of (y+1)/2
+    (rotation_matrix.py:16-88)."""
+    def nrm(t):
+        return torch.sqrt((t * t).sum(-1, keepdim=True) + 1e-14)
+
+    u = vec / nrm(vec)
+    x, y, z = u.unbind(-1)
+    zero = torch.zeros_like(x)
+    qp = torch.stack([1.0 + y, -z, zero, x], -1)
+    qp = qp / nrm(qp)
+    qn = torch.stack([-z, 1.0 - y, x, zero], -1)
+    qn = qn / nrm(qn)
+    s = 0.5 * (y + 1.0)
+    tiny = torch.finfo(vec.dtype).eps
+    sa = torch.where(s < tiny, torch.full_like(s, tiny), s)
+    sb = torch.where(1.0 - s < tiny, torch.full_like(s, tiny), 1.0 - s)
+    a, b = torch.exp(-1.0 / sa), torch.exp(-1.0 / sb)
+    t = torch.where(s <= 0.0, torch.zeros_like(s), torch.where(s >= 1.0, torch.ones_like(s), a / (a + b)))
+    qp = torch.where((qn * qp).sum(-1, keepdim=True) < 0.0, -qp, qp)
+    t = t.unsqueeze(-1)
+    q = (1.0 - t) * qn + t * qp
+    q = q / nrm(q)
+    w, a, b, c = q.unbind(-1)
+    R = [[1 - 2 * (b * b + c * c), 2 * (a * b - w * c), 2 * (a * c + w * b)],
+         [2 * (a * b + w * c), 1 - 2 * (a * a + c * c), 2 * (b * c - w * a)],
+         [2 * (a * c - w * b), 2 * (b * c + w * a), 1 - 2 * (a * a + b * b)]]
+    return torch.stack([torch.stack(r, -1) for r in R], -2)
+
+
+def so2_m_rows(lmax: int) -> List[int]:
+    """e3nn component (l^2 + l + m) of every row of the SO(2) m layout
+    (mmax = lmax): m = 0 for l = 0..lmax, then per m the +m and the -m rows."""
+    rows = [l * l + l for l in range(lmax + 1)]
+    for m in range(1, lmax + 1):
+        rows += [l * l + l + m for l in range(m, lmax + 1)] + [l * l + l - m for l in range(m, lmax + 1)]
+    return rows
+
+
+def _edge_wigner_autograd(vec: torch.Tensor, lmax: int) -> torch.Tensor:
+    """The Wigner kernel as torch operations: D^0 = 1, D^1 = R, D^l = (2l+1)
+    C^T (R (x) D^(l-1)) C with C = W3j(1, l-1, l) (wigner.py:330-357), the
+    block-diagonal matrix's rows in the m layout."""
+    from .so3 import wigner_3j
+
+    R = _edge_frame_autograd(vec)
+    E = vec.shape[0]
+    blocks = [R.new_ones(E, 1, 1)]
+    if lmax >= 1:
+        blocks.append(R)
+    for l in range(2, lmax + 1):
+        cg = torch.as_tensor(wigner_3j(1, l - 1, l), dtype=R.dtype, device=R.device)
+        u = torch.einsum("abm,eac,ebd->emcd", cg, R, blocks[l - 1])
+        blocks.append((2 * l + 1) * torch.einsum("emcd,cdn->emn", u, cg))
+    K = (lmax + 1) ** 2
+    D = torch.block_diag(*[torch.ones(2 * l + 1, 2 * l + 1) for l in range(lmax + 1)]).to(R.device) > 0
+    full = R.new_zeros(E, K, K)
+    full = full.masked_scatter(D.unsqueeze(0).expand(E, K, K),
+                               torch.cat([b.reshape(E, -1) for b in blocks], dim=1).reshape(-1))
+    return full[:, so2_m_rows(lmax), :]
+
+
 def edge_wigner(vec: torch.Tensor, lmax: int) -> torch.Tensor:
     """Edge-frame Wigner matrices [E, K, K] (rows in the SO(2) m layout,
     columns e3nn components); the inverse rotation is the transpose."""
+    if MODE.double:
+        return _edge_wigner_autograd(vec, int(lmax))
     return _EdgeWigner.apply(vec.contiguous(), int(lmax))
 
 

@@ -22,6 +22,8 @@ import torch
 
 from . import ops
 
+_SIGMOID_CST = 1.8467055342154763   # e3nn normalize2mom(sigmoid) (tace/models/mlp.py:43)
+
 # frozen parameters run the convolution on the fused operator (_TeceFused);
 # False keeps the per-operator autograd path (the reference for its tests)
 FUSED = True
@@ -194,12 +196,119 @@ class TeceConvolution(torch.nn.Module):
         m = self.linear_down.blocks(o, self.mixing)
         return ops.tece_rotate_out(m, alpha, wigner, plan, out_map, dst_out, self.lmax, self.H)
 
+    # ---- the convolution as torch operations (training: twice differentiable) --
+    def _expand(self, full: bool) -> torch.Tensor:
+        """Row -> component map of the radial weights (full=False, one per (m,
+        l), shared by +m and -m rows) and of the gates (full=True, lmax+1 per m)
+        (``so2_expand_index``, ``SO2Gate``)."""
+        idx, off, n = [], 0, self.lmax + 1
+        for m in range(self.mmax + 1):
+            k = n if full else n - m
+            r = list(range(off, off + k))
+            idx += r + (r if m > 0 else [])
+            off += k
+        return torch.tensor(idx, dtype=torch.long)
+
+    def _edge_ace_autograd(self, u, v, coefs):
+        """u + g u + complex edge-ACE product (``oam_2026_07_05.py:782-790``,
+        ``uuuSO2TensorProduct`` 312-516) on [E, rows, A] m-layout features
+        (m = 0: n real rows; m > 0: n rows of the +m, then n of the -m part),
+        per path weights ``coefs`` [E, P n A] in ``ops.edge_ace_paths`` order;
+        each output m scaled by 1/sqrt(its number of paths)."""
+        E, n, A = u.shape[0], self.lmax + 1, self.A
+
+        def split(x):
+            return [x[:, :n]] + [x[:, n + 2 * n * (m - 1):n + 2 * n * m].reshape(E, 2, n, A)
+                                 for m in range(1, self.mmax + 1)]
+        us, vs = split(u), split(v)
+        by_m3 = {}
+        for j, (m3, m1, m2, is_sum) in enumerate(ops.edge_ace_paths(self.lmax)):
+            by_m3.setdefault(m3, []).append((j, m1, m2, is_sum))
+        outs = []
+        for m3 in range(self.mmax + 1):
+            ps = by_m3[m3]
+            re, im = 0.0, 0.0
+            for (j, m1, m2, is_sum) in ps:
+                w = coefs[:, j * n * A:(j + 1) * n * A].reshape(E, n, A)
+                a, b = us[m1], vs[m2]
+                if m1 == 0 and m2 == 0:
+                    zr, zi = a * b, None
+                elif m2 == 0:
+                    zr, zi = a[:, 0] * b, a[:, 1] * b
+                elif m1 == 0:
+                    zr, zi = a * b[:, 0], a * b[:, 1]
+                elif is_sum:
+                    zr, zi = a[:, 0] * b[:, 0] - a[:, 1] * b[:, 1], a[:, 0] * b[:, 1] + a[:, 1] * b[:, 0]
+                else:
+                    zr, zi = a[:, 0] * b[:, 0] + a[:, 1] * b[:, 1], a[:, 1] * b[:, 0] - a[:, 0] * b[:, 1]
+                re = re + zr * w
+                if m3 > 0:
+                    im = im + zi * w
+            sc = 1.0 / math.sqrt(len(ps))
+            outs.append(re * sc)
+            if m3 > 0:
+                outs.append(im * sc)
+        return torch.cat(outs, dim=1)
+
+    def _score_autograd(self, q, k, R):
+        """Radial-rotary complex QK score [E, H] (``oam_2026_07_05.py:699-754``)
+        on [E, K, C] m-layout query / key; the temperature is differentiated."""
+        E, H, Ch, n = q.shape[0], self.H, self.Ch, self.lmax + 1
+        rp = self.radial_proj(R)
+        bias, phase = rp[:, :H], math.pi * torch.tanh(rp[:, H:])
+        s = (q[:, :n].reshape(E, n, H, Ch) * k[:, :n].reshape(E, n, H, Ch)).sum(dim=(1, 3))
+        off = n
+        for m in range(1, self.mmax + 1):
+            nm = n - m
+            qm = q[:, off:off + 2 * nm].reshape(E, 2, nm, H, Ch)
+            km = k[:, off:off + 2 * nm].reshape(E, 2, nm, H, Ch)
+            off += 2 * nm
+            c, sn = torch.cos(m * phase).view(E, 1, H, 1), torch.sin(m * phase).view(E, 1, H, 1)
+            s = s + (qm[:, 0] * (c * km[:, 0] - sn * km[:, 1]) + qm[:, 1] * (sn * km[:, 0] + c * km[:, 1])).sum(
+                dim=(1, 3))
+        T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
+        return s * (self.attention_scale * T) + bias
+
+    def _forward_autograd(self, x_gm, w, node_map, src, dst, wigner, R):
+        """The whole convolution as torch operations (the per-edge kernels'
+        arithmetic; ``oam_2026_07_05.py:756-823``): what training with a force
+        loss differentiates twice.  Same inputs and output as ``forward``."""
+        Nn, E, C, K = x_gm.shape[0], w.shape[0], self.C, self.K
+        rows = node_map.long()
+        x_lc = self.node_components(x_gm)
+        rs, rd = rows[src], rows[dst]
+        m = torch.bmm(wigner, torch.cat((x_lc[rs], x_lc[rd]), dim=-1))
+        key, query = self.key_proj(m[:, :, :C]), self.query_proj(m[:, :, C:])
+        score = self._score_autograd(query, key, R)
+        dev = w.device
+        m = w.view(E, self.num_components, 2 * C).index_select(1, self._expand(False).to(dev)) * m
+        coefs = torch.sigmoid(self.linear_coefs(m).squeeze(-1)) * _SIGMOID_CST
+        v = self.linear_glu(m)
+        u = self.linear_up(m)
+        gate, u = u[:, :self.num_gates], u[:, self.num_gates:self.num_gates + self.rows_full]
+        g = (torch.sigmoid(gate) * _SIGMOID_CST).index_select(1, self._expand(True).to(dev))
+        m = self.linear_down(u + g * u + self._edge_ace_autograd(u, v, coefs))
+        # graph softmax over each receiver's in-edges (softmax.py:100-112):
+        # exp(s - max) / (sum exp(s - max) + 1e-16), the max not differentiated
+        H = self.H
+        mx = torch.full((Nn, H), -math.inf, dtype=score.dtype, device=dev).scatter_reduce(
+            0, rd.view(-1, 1).expand(-1, H), score.detach(), reduce="amax", include_self=True)
+        ex = torch.exp(score - mx[rd])
+        alpha = ex / (torch.zeros(Nn, H, dtype=score.dtype, device=dev).index_add(0, rd, ex) + 1e-16)[rd]
+        m = (m.view(E, K, H, self.Ch) * alpha.view(E, 1, H, 1)).view(E, K, C)
+        m = torch.bmm(wigner.transpose(1, 2), m)
+        out = torch.zeros(Nn, K, C, dtype=m.dtype, device=dev).index_add(0, rd, m)
+        # [rows, K, C] (l layout) -> group-major C x (0..lmax)
+        return torch.cat([out[:, l * l:(l + 1) ** 2].reshape(-1) for l in range(self.lmax + 1)]).view(Nn, K * C)
+
     def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):
         """x_gm: node features, group-major C x (0..lmax) in feature-row order;
         w: radial weights [E, weight_numel]; node_map[n] = feature row of node
         n; src/dst: edge endpoints (node ids); wigner [E, K, K] from
         ``ops.edge_wigner``; R: radial basis [E, num_radial].  Returns the
         receiver sums, group-major, in feature-row order."""
+        if ops.MODE.double:
+            return self._forward_autograd(x_gm, w, node_map, src, dst, wigner, R)
         rows = node_map.long()
         return self.edges(self.node_components(x_gm), w, rows[src], rows[dst], plan, node_map, dst, wigner, R)
 

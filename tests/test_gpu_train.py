@@ -5,9 +5,10 @@ its derivatives (``tace/models/adapter.py:95-104``), so a loss on energies,
 forces and stress can be differentiated with respect to the parameters: the
 double backward of force-matching training (``lightning/lit_model.py:150``).
 The tensor products run on the HIP kernels through operators whose backward
-is differentiable again; the gradients of such a loss with respect to every
-parameter must equal torch autograd through the CPU oracle (float64, 1e-10
-relative), and the forces of the training path those of the inference path.
+is differentiable again, the TECE convolution as torch operations; the
+gradients of such a loss with respect to every parameter must equal torch
+autograd through the CPU oracle (float64, 1e-10 relative), and the forces of
+the training path those of the inference path.
 """
 
 import numpy as np
@@ -115,12 +116,61 @@ def test_training_and_inference_forces_agree(cuda):
     assert (a["forces"].detach() - b["forces"]).abs().max().item() <= 1e-11 * max(b["forces"].abs().max().item(), 1.0)
 
 
-def test_tece_refuses_create_graph(cuda):
-    """The TECE convolution is first-order on this path: training mode raises
-    instead of returning gradients that would miss the second derivatives."""
-    s = structures.bcc_fe(reps=(2, 2, 2), seed=1)
-    ref, gpu, d64, dg = _pair([s], "tece", cuda, seed=2, num_channel=16)
+def _perturb_tece(module, seed):
+    """Random radial phase / bias and temperatures (zero / fixed at init), so
+    that the rotary and temperature terms carry gradients."""
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in module.named_parameters():
+            if "radial_proj" in name:
+                p.copy_(0.7 * torch.randn(p.shape, generator=g, dtype=p.dtype))
+            elif "temperature_logit" in name:
+                p.copy_(torch.randn(p.shape, generator=g, dtype=p.dtype))
+
+
+def test_tece_force_loss_parameter_gradients_match_oracle(cuda):
+    """Config-5 architecture (TECE edge cluster expansion with radial rotary
+    attention, bilinear-gate product basis) on a distorted bcc Fe slice: the
+    gradients of an energy + force loss with respect to every parameter,
+    including the radial projection and the attention temperatures."""
+    s = structures.bcc_fe(reps=(2, 2, 2), seed=4)
+    rc = configs.PRESETS["tece"]["cutoff"]
+    edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc)]
+    cfg = configs.model_cfg("tece", [26], edges[0][0].shape[1] / len(s["positions"]), num_channel=16, num_head=2,
+                            edge_ace_hidden=8)
+    torch.manual_seed(6)
+    ref = om.TACE(cfg).double()
+    _perturb_tece(ref, 9)
+    torch.set_default_dtype(torch.float64)
+    try:
+        gpu = pm.create_model(cfg)
+    finally:
+        torch.set_default_dtype(torch.float32)
+    pm.load_reference_state_dict(gpu.readout_fn, ref.state_dict())
+    gpu = gpu.to(cuda)
     gpu.reset_target_property(["energy", "forces"])
+    d64 = data.collate([s], edges, cfg["atomic_numbers"], dtype=torch.float64)
+    dg = data.collate([s], edges, cfg["atomic_numbers"], dtype=torch.float64, device=cuda)
+    # the training path's energies and forces equal the inference kernels'
+    gpu.eval()
+    inf = gpu(dg)
     gpu.train()
-    with pytest.raises(NotImplementedError):
-        gpu(dg)
+    out = gpu(dg)
+    assert (out["energy"].detach() - inf["energy"]).abs().max().item() <= 1e-11 * inf["energy"].abs().max().item()
+    assert (out["forces"].detach() - inf["forces"]).abs().max().item() <= 1e-11 * max(inf["forces"].abs().max().item(),
+                                                                                    1.0)
+    loss = _loss(out, False, seed=13)
+    names = [n for n, p in gpu.readout_fn.named_parameters() if p.requires_grad]
+    own = dict(gpu.readout_fn.named_parameters())
+    grads = torch.autograd.grad(loss, [own[n] for n in names])
+    want = om.compute(ref, d64, forces=True, create_graph=True)
+    rp = dict(ref.named_parameters())
+    wgrads = torch.autograd.grad(_loss(want, False, seed=13), [rp[n] for n in names], allow_unused=True)
+    checked = 0
+    for n, gg, gw in zip(names, grads, wgrads):
+        gw = torch.zeros_like(rp[n]) if gw is None else gw
+        scale = gw.abs().max().item()
+        err = (gg.cpu() - gw).abs().max().item()
+        assert err <= 1e-10 * max(scale, 1e-30) + 1e-14, (n, err, scale)
+        checked += ("temperature_logit" in n or "radial_proj" in n) and scale > 0
+    assert checked >= 2   # the rotary and temperature parameters have gradients

@@ -106,3 +106,69 @@ def test_mode_is_restored():
             assert not ops.MODE.double
         assert ops.MODE.double
     assert not ops.MODE.double
+
+
+def test_edge_wigner_matches_the_oracle_frames():
+    """The torch edge frames / Wigner blocks of the training path against the
+    oracle's restatement, including edges along +-y (the chart blend's ends)."""
+    from oracle import tece as ot
+    g = torch.Generator().manual_seed(3)
+    v = torch.randn(200, 3, generator=g, dtype=torch.float64) * 2.0
+    v[0] = torch.tensor([0.0, 1.5, 0.0], dtype=torch.float64)
+    v[1] = torch.tensor([0.0, -2.0, 0.0], dtype=torch.float64)
+    v[2] = torch.tensor([1e-3, -2.0, 0.0], dtype=torch.float64)
+    for lmax in (1, 2, 3):
+        a = ops._edge_wigner_autograd(v, lmax)
+        b, _ = ot.edge_wigner(v, lmax, lmax)
+        assert (a - b).abs().max().item() < 1e-12, lmax
+
+
+def test_tece_convolution_autograd_matches_the_oracle():
+    """The training path's torch TECE convolution on group-major, permuted
+    feature rows against the oracle's convolution on a random graph: output
+    and the gradients of a scalar function of it (inputs and parameters)."""
+    from oracle import tece as ot
+    from tace_amd import tece as pt
+    lmax, C, H, A, nr = 2, 8, 2, 4, 8
+    K = (lmax + 1) ** 2
+    g = torch.Generator().manual_seed(4)
+    torch.manual_seed(5)
+    ref = ot.TeceConvolution(lmax, lmax, C, H, A, nr).double()
+    with torch.no_grad():
+        for name, p in ref.named_parameters():
+            if "radial_proj" in name:
+                p.copy_(0.7 * torch.randn(p.shape, generator=g, dtype=p.dtype))
+            elif "temperature_logit" in name:
+                p.copy_(torch.randn(p.shape, generator=g, dtype=p.dtype))
+    torch.set_default_dtype(torch.float64)
+    try:
+        conv = pt.TeceConvolution(lmax, lmax, C, H, A, nr)
+    finally:
+        torch.set_default_dtype(torch.float32)
+    conv.load_state_dict(ref.state_dict(), strict=False)
+    N, E = 12, 60
+    src = torch.randint(0, N, (E,), generator=g)
+    dst = torch.randint(0, N, (E,), generator=g)
+    vec = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    x_l = torch.randn(N, K, C, generator=g, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(E, conv.weight_numel, generator=g, dtype=torch.float64, requires_grad=True)
+    R = torch.randn(E, nr, generator=g, dtype=torch.float64)
+    W, Wi = ot.edge_wigner(vec, lmax, lmax)
+    want = ref(x_l, w, torch.stack([src, dst]), W, Wi, R)
+    # group-major rows in a permuted order (row perm^-1[n] holds node n)
+    perm = torch.randperm(N, generator=g)
+    node_map = torch.empty_like(perm)
+    node_map[perm] = torch.arange(N)
+    x_rows = x_l[perm]
+    x_gm = torch.cat([x_rows[:, l * l:(l + 1) ** 2].reshape(-1) for l in range(lmax + 1)]).view(N, K * C)
+    got = conv._forward_autograd(x_gm, w, node_map.to(torch.int32), src, dst, ops._edge_wigner_autograd(vec, lmax), R)
+    got_l = torch.cat([got.reshape(-1)[N * C * l * l:N * C * (l + 1) ** 2].view(N, 2 * l + 1, C)
+                       for l in range(lmax + 1)], dim=1)[node_map]
+    assert (got_l - want).abs().max().item() < 1e-12 * max(1.0, want.abs().max().item())
+    probe = torch.randn(N, K, C, generator=g, dtype=torch.float64)
+    own = dict(conv.named_parameters())
+    names = [n for n, _ in ref.named_parameters()]
+    ga = torch.autograd.grad((got_l * probe).sum(), [x_l, w] + [own[n] for n in names])
+    gb = torch.autograd.grad((want * probe).sum(), [x_l, w] + [dict(ref.named_parameters())[n] for n in names])
+    for a, b in zip(ga, gb):
+        assert (a - b).abs().max().item() < 1e-11 * max(1.0, b.abs().max().item())

@@ -40,41 +40,42 @@ Tensor = torch.Tensor
 
 # ------------------------------------------------------------------- uvu ----
 @torch.library.custom_op("tace_amd::uvu_scatter", mutates_args=(), device_types="cuda")
-def uvu_scatter(x: Tensor, y: Tensor, w: Tensor, edge_index: Tensor, key: str, channels: int) -> Tensor:
+def uvu_scatter(x: Tensor, y: Tensor, w: Tensor, edge_index: Tensor, key: str, channels: int,
+                layout: int = 0) -> Tensor:
     plan = ops.EdgePlan.from_edge_index(edge_index, x.shape[0])
     return ops.launch_edge_tp_fwd(x.contiguous(), y.contiguous(), w.contiguous(), plan, ops.find_variant(key),
-                                  channels)
+                                  channels, layout)
 
 
 @uvu_scatter.register_fake
-def _uvu_scatter_fake(x, y, w, edge_index, key, channels):
+def _uvu_scatter_fake(x, y, w, edge_index, key, channels, layout=0):
     return x.new_empty(x.shape[0], channels * ops.find_variant(key).dout)
 
 
 @torch.library.custom_op("tace_amd::uvu_scatter_backward", mutates_args=(), device_types="cuda")
 def uvu_scatter_backward(x: Tensor, y: Tensor, w: Tensor, edge_index: Tensor, grad_out: Tensor, key: str,
-                         channels: int) -> Tuple[Tensor, Tensor, Tensor]:
+                         channels: int, layout: int = 0) -> Tuple[Tensor, Tensor, Tensor]:
     plan = ops.EdgePlan.from_edge_index(edge_index, x.shape[0])
     gx, gy, gw = ops.launch_edge_tp_bwd(x.contiguous(), y.contiguous(), w.contiguous(), grad_out.contiguous(), plan,
-                                        ops.find_variant(key), channels)
+                                        ops.find_variant(key), channels, layout)
     return gx, gy, gw
 
 
 @uvu_scatter_backward.register_fake
-def _uvu_scatter_backward_fake(x, y, w, edge_index, grad_out, key, channels):
+def _uvu_scatter_backward_fake(x, y, w, edge_index, grad_out, key, channels, layout=0):
     return torch.empty_like(x), torch.empty_like(y), torch.empty_like(w)
 
 
 def _uvu_setup(ctx, inputs, output):
-    x, y, w, edge_index, key, channels = inputs
+    x, y, w, edge_index, key, channels, layout = inputs
     ctx.save_for_backward(x, y, w, edge_index)
-    ctx.key, ctx.channels = key, channels
+    ctx.key, ctx.channels, ctx.layout = key, channels, layout
 
 
 def _uvu_backward(ctx, grad_out):
     x, y, w, edge_index = ctx.saved_tensors
-    gx, gy, gw = uvu_scatter_backward(x, y, w, edge_index, grad_out, ctx.key, ctx.channels)
-    return gx, gy, gw, None, None, None
+    gx, gy, gw = uvu_scatter_backward(x, y, w, edge_index, grad_out, ctx.key, ctx.channels, ctx.layout)
+    return gx, gy, gw, None, None, None, None
 
 
 uvu_scatter.register_autograd(_uvu_backward, setup_context=_uvu_setup)
@@ -91,20 +92,21 @@ uvu_scatter.register_autograd(_uvu_backward, setup_context=_uvu_setup)
 #   d/dw = gw-part of bwd(ax, y, w, g) + of bwd(x, ay, w, g)
 # -- the forward and backward operators again (themselves differentiable).
 def _uvu_bwd_setup(ctx, inputs, output):
-    x, y, w, edge_index, grad_out, key, channels = inputs
+    x, y, w, edge_index, grad_out, key, channels, layout = inputs
     ctx.save_for_backward(x, y, w, edge_index, grad_out)
-    ctx.key, ctx.channels = key, channels
+    ctx.key, ctx.channels, ctx.layout = key, channels, layout
 
 
 def _uvu_bwd_backward(ctx, ax, ay, aw):
     x, y, w, ei, g = ctx.saved_tensors
-    key, C = ctx.key, ctx.channels
+    key, C, lay = ctx.key, ctx.channels, ctx.layout
     zx, zy, zw = (a if a is not None else torch.zeros_like(t) for a, t in ((ax, x), (ay, y), (aw, w)))
-    gg = uvu_scatter(zx, y, w, ei, key, C) + uvu_scatter(x, zy, w, ei, key, C) + uvu_scatter(x, y, zw, ei, key, C)
-    bx = uvu_scatter_backward(zx, y, w, ei, g, key, C)   # (., gy, gw) with x -> ax
-    by = uvu_scatter_backward(x, zy, w, ei, g, key, C)   # (gx, ., gw) with y -> ay
-    bw = uvu_scatter_backward(x, y, zw, ei, g, key, C)   # (gx, gy, .) with w -> aw
-    return by[0] + bw[0], bx[1] + bw[1], bx[2] + by[2], None, gg, None, None
+    gg = (uvu_scatter(zx, y, w, ei, key, C, lay) + uvu_scatter(x, zy, w, ei, key, C, lay)
+          + uvu_scatter(x, y, zw, ei, key, C, lay))
+    bx = uvu_scatter_backward(zx, y, w, ei, g, key, C, lay)   # (., gy, gw) with x -> ax
+    by = uvu_scatter_backward(x, zy, w, ei, g, key, C, lay)   # (gx, ., gw) with y -> ay
+    bw = uvu_scatter_backward(x, y, zw, ei, g, key, C, lay)   # (gx, gy, .) with w -> aw
+    return by[0] + bw[0], bx[1] + bw[1], bx[2] + by[2], None, gg, None, None, None
 
 
 uvu_scatter_backward.register_autograd(_uvu_bwd_backward, setup_context=_uvu_bwd_setup)
@@ -112,40 +114,40 @@ uvu_scatter_backward.register_autograd(_uvu_bwd_backward, setup_context=_uvu_bwd
 
 # ------------------------------------------------------------------- uuu ----
 @torch.library.custom_op("tace_amd::uuu", mutates_args=(), device_types="cuda")
-def uuu(x1: Tensor, x2: Tensor, w: Optional[Tensor], key: str, channels: int) -> Tensor:
+def uuu(x1: Tensor, x2: Tensor, w: Optional[Tensor], key: str, channels: int, layout: int = 0) -> Tensor:
     return ops.launch_uuu_fwd(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(),
-                              ops.find_variant(key), channels)
+                              ops.find_variant(key), channels, layout)
 
 
 @uuu.register_fake
-def _uuu_fake(x1, x2, w, key, channels):
+def _uuu_fake(x1, x2, w, key, channels, layout=0):
     return x1.new_empty(x1.shape[0], channels * ops.find_variant(key).dout)
 
 
 @torch.library.custom_op("tace_amd::uuu_backward", mutates_args=(), device_types="cuda")
 def uuu_backward(x1: Tensor, x2: Tensor, w: Optional[Tensor], grad_out: Tensor, key: str,
-                 channels: int) -> Tuple[Tensor, Tensor, Tensor]:
+                 channels: int, layout: int = 0) -> Tuple[Tensor, Tensor, Tensor]:
     g1, g2, gw = ops.launch_uuu_bwd(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(),
-                                    grad_out.contiguous(), ops.find_variant(key), channels)
+                                    grad_out.contiguous(), ops.find_variant(key), channels, layout)
     # a weightless product returns an empty weight gradient (schema: tensors only)
     return g1, g2, gw if gw is not None else x1.new_empty(0)
 
 
 @uuu_backward.register_fake
-def _uuu_backward_fake(x1, x2, w, grad_out, key, channels):
+def _uuu_backward_fake(x1, x2, w, grad_out, key, channels, layout=0):
     return torch.empty_like(x1), torch.empty_like(x2), torch.empty_like(w) if w is not None else x1.new_empty(0)
 
 
 def _uuu_setup(ctx, inputs, output):
-    x1, x2, w, key, channels = inputs
+    x1, x2, w, key, channels, layout = inputs
     ctx.save_for_backward(x1, x2, w)
-    ctx.key, ctx.channels, ctx.has_w = key, channels, w is not None
+    ctx.key, ctx.channels, ctx.has_w, ctx.layout = key, channels, w is not None, layout
 
 
 def _uuu_backward(ctx, grad_out):
     x1, x2, w = ctx.saved_tensors
-    g1, g2, gw = uuu_backward(x1, x2, w, grad_out, ctx.key, ctx.channels)
-    return g1, g2, gw if ctx.has_w else None, None, None
+    g1, g2, gw = uuu_backward(x1, x2, w, grad_out, ctx.key, ctx.channels, ctx.layout)
+    return g1, g2, gw if ctx.has_w else None, None, None, None
 
 
 uuu.register_autograd(_uuu_backward, setup_context=_uuu_setup)
@@ -156,31 +158,112 @@ uuu.register_autograd(_uuu_backward, setup_context=_uuu_setup)
 # scheme as the uvu one above).  Identical inputs pass the same tensor twice;
 # autograd adds the two contributions.
 def _uuu_bwd_setup(ctx, inputs, output):
-    x1, x2, w, grad_out, key, channels = inputs
+    x1, x2, w, grad_out, key, channels, layout = inputs
     ctx.save_for_backward(x1, x2, w, grad_out)
-    ctx.key, ctx.channels, ctx.has_w = key, channels, w is not None
+    ctx.key, ctx.channels, ctx.has_w, ctx.layout = key, channels, w is not None, layout
 
 
 def _uuu_bwd_backward(ctx, a1, a2, aw):
     x1, x2, w, g = ctx.saved_tensors
-    key, C = ctx.key, ctx.channels
+    key, C, lay = ctx.key, ctx.channels, ctx.layout
     z1 = a1 if a1 is not None else torch.zeros_like(x1)
     z2 = a2 if a2 is not None else torch.zeros_like(x2)
-    gg = uuu(z1, x2, w, key, C) + uuu(x1, z2, w, key, C)
-    b1 = uuu_backward(z1, x2, w, g, key, C)   # (., g2, gw) with x1 -> a1
-    b2 = uuu_backward(x1, z2, w, g, key, C)   # (g1, ., gw) with x2 -> a2
+    gg = uuu(z1, x2, w, key, C, lay) + uuu(x1, z2, w, key, C, lay)
+    b1 = uuu_backward(z1, x2, w, g, key, C, lay)   # (., g2, gw) with x1 -> a1
+    b2 = uuu_backward(x1, z2, w, g, key, C, lay)   # (g1, ., gw) with x2 -> a2
     d1, d2 = b2[0], b1[1]
     dw = None
     if ctx.has_w:
         dw = b1[2] + b2[2]
         if aw is not None and aw.numel():
-            gg = gg + uuu(x1, x2, aw, key, C)
-            bw = uuu_backward(x1, x2, aw, g, key, C)
+            gg = gg + uuu(x1, x2, aw, key, C, lay)
+            bw = uuu_backward(x1, x2, aw, g, key, C, lay)
             d1, d2 = d1 + bw[0], d2 + bw[1]
-    return d1, d2, dw, gg, None, None
+    return d1, d2, dw, gg, None, None, None
 
 
 uuu_backward.register_autograd(_uuu_bwd_backward, setup_context=_uuu_bwd_setup)
+
+
+# ------------------------------------------------------- per-species linear ----
+# ``e3nnElementLinear`` (tace/models/linear.py:377-481) for the exported model:
+# features in node order (group-major), the species of every node as an int64
+# tensor.  Inside the operator the rows are grouped by species and the
+# segmented GEMM runs (what the eager model does once per forward with its
+# species plan); the operator's backward gives the input gradient (exported
+# models are evaluated with frozen parameters).
+_LIN_LAYOUTS = {}
+
+
+def _lin_layout(irreps_in: str, irreps_out: str):
+    from .model import _LinearLayout
+    key = (irreps_in, irreps_out)
+    if key not in _LIN_LAYOUTS:
+        _LIN_LAYOUTS[key] = _LinearLayout(irreps_in, irreps_out)
+    return _LIN_LAYOUTS[key]
+
+
+def _gm_take(x: Tensor, gm, idx: Tensor) -> Tensor:
+    """Rows ``idx`` of group-major features (every block gathered by node)."""
+    Z = x.shape[0]
+    flat = x.reshape(-1)
+    out = [flat[Z * s:Z * (s + m * d)].view(Z, d * m).index_select(0, idx).reshape(-1) for (s, m, d) in gm.blocks]
+    return torch.cat(out).view(idx.shape[0], -1)
+
+
+def _element_linear_sorted(x, weight, bias, species, irreps_in, irreps_out, alpha):
+    from .model import SpeciesPlan, _LinearFn
+    lay = _lin_layout(irreps_in, irreps_out)
+    sp = SpeciesPlan(torch.nn.functional.one_hot(species, weight.shape[0]).to(x.dtype))
+    xs = _gm_take(x, lay.gin, sp.perm).contiguous()
+    return lay, sp, xs
+
+
+@torch.library.custom_op("tace_amd::element_linear", mutates_args=(), device_types="cuda")
+def element_linear(x: Tensor, weight: Tensor, bias: Optional[Tensor], species: Tensor, irreps_in: str,
+                   irreps_out: str, alpha: float) -> Tensor:
+    from .model import _LinearFn
+    lay, sp, xs = _element_linear_sorted(x, weight, bias, species, irreps_in, irreps_out, alpha)
+    ys = _LinearFn.apply(xs, weight, bias, lay, sp.ranges, alpha)
+    return _gm_take(ys, lay.gout, sp.inv)
+
+
+@element_linear.register_fake
+def _element_linear_fake(x, weight, bias, species, irreps_in, irreps_out, alpha):
+    return x.new_empty(x.shape[0], _lin_layout(irreps_in, irreps_out).dim_out)
+
+
+@torch.library.custom_op("tace_amd::element_linear_backward", mutates_args=(), device_types="cuda")
+def element_linear_backward(x: Tensor, weight: Tensor, species: Tensor, grad_out: Tensor, irreps_in: str,
+                            irreps_out: str, alpha: float) -> Tensor:
+    from .model import _LinearFn
+    lay, sp, xs = _element_linear_sorted(x, weight, None, species, irreps_in, irreps_out, alpha)
+    gs = _gm_take(grad_out.contiguous(), lay.gout, sp.perm)
+    with torch.enable_grad():
+        xs = xs.detach().requires_grad_(True)
+        ys = _LinearFn.apply(xs, weight.detach(), None, lay, sp.ranges, alpha)
+        (gx,) = torch.autograd.grad(ys, xs, gs)
+    return _gm_take(gx, lay.gin, sp.inv)
+
+
+@element_linear_backward.register_fake
+def _element_linear_backward_fake(x, weight, species, grad_out, irreps_in, irreps_out, alpha):
+    return torch.empty_like(x)
+
+
+def _element_linear_setup(ctx, inputs, output):
+    x, weight, bias, species, irreps_in, irreps_out, alpha = inputs
+    ctx.save_for_backward(x, weight, species)
+    ctx.args = (irreps_in, irreps_out, alpha)
+
+
+def _element_linear_bwd(ctx, grad_out):
+    x, weight, species = ctx.saved_tensors
+    gx = element_linear_backward(x, weight, species, grad_out, *ctx.args)
+    return gx, None, None, None, None, None, None
+
+
+element_linear.register_autograd(_element_linear_bwd, setup_context=_element_linear_setup)
 
 
 # ------------------------------------------------------------------ TECE ----

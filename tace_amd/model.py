@@ -44,7 +44,8 @@ class SpeciesPlan:
     one contiguous row range.  ``perm[r]`` = node stored in row r,
     ``node_map[n]`` (int32) = row of node n (what the edge kernels take)."""
 
-    def __init__(self, attrs: torch.Tensor, exchange=None, pairs: Optional[ops.EdgePairs] = None):
+    def __init__(self, attrs: torch.Tensor, exchange=None, pairs: Optional[ops.EdgePairs] = None,
+                 natural: bool = False):
         self.attrs = attrs
         # LAMMPS ML-IAP data whose forward_exchange fills ghost rows before
         # every interaction layer >= 1 (several domains), or None
@@ -52,6 +53,13 @@ class SpeciesPlan:
         # edge pairs whose radial weights are made once (None: per edge)
         self.pairs = pairs
         species = attrs.argmax(dim=-1)
+        self.species = species
+        if natural:
+            # export mode: rows stay in node order; the per-species linears
+            # group them inside their operator (tace_amd::element_linear)
+            self.perm = self.inv = torch.arange(attrs.shape[0], device=attrs.device)
+            self.node_map, self.ranges = None, None
+            return
         self.perm = torch.argsort(species, stable=True)
         inv = torch.empty_like(self.perm)
         inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
@@ -424,6 +432,10 @@ class e3nnElementLinear(torch.nn.Module):
                      if bias and self.lay.bias_numel else None)
 
     def forward(self, x: torch.Tensor, sp: SpeciesPlan, alpha: float = 1.0) -> torch.Tensor:
+        if ops.MODE.export:
+            from . import library
+            return library.element_linear(x.contiguous(), self.weight, self.bias, sp.species, str(self.irreps_in),
+                                          str(self.irreps_out), float(alpha))
         if ops.MODE.double:
             return _linear_autograd(x.contiguous(), self.weight, self.bias, self.lay, sp.ranges, float(alpha))
         return _LinearFn.apply(x.contiguous(), self.weight, self.bias, self.lay, sp.ranges, float(alpha))
@@ -1022,7 +1034,7 @@ class TACE(torch.nn.Module):
         so callers that want per-edge gradients pass None)."""
         attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
         num_graphs = ptr.numel() - 1
-        sp = SpeciesPlan(attrs, exchange, pairs)
+        sp = SpeciesPlan(attrs, exchange, pairs, natural=ops.MODE.export)
         x = self.representation(attrs, plan, edge_vector, sp, data["edge_index"])
         e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
@@ -1301,20 +1313,23 @@ class TensorModel(torch.nn.Module):
         else:
             pos_s, lat_s = pos, lattice
         ei = data["edge_index"]
-        plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
+        if ops.MODE.export:
+            plan = ops.TracedEdges(ei, pos.shape[0])
+        else:
+            plan = _opt(data, "_edge_plan") or ops.EdgePlan.from_edge_index(ei, pos.shape[0])
         # adapter.py:95-104: training (or create_graph) keeps the graph of the
         # derivatives, so that a loss on forces / stress can be differentiated
         # with respect to the parameters; the operators then take their
         # twice-differentiable form
         cg = bool(self.training or self.create_graph)
-        with ops.differentiable_twice(cg):
+        with ops.differentiable_twice(cg or ops.MODE.export):
             return self._forward_graph(data, pos, lattice, batch, shifts, num_graphs, inputs, pos_s, lat_s, ei, plan,
                                        want_f, want_s, want_e, cg)
 
     def _forward_graph(self, data, pos, lattice, batch, shifts, num_graphs, inputs, pos_s, lat_s, ei, plan,
                        want_f: bool, want_s: bool, want_e: bool, cg: bool):
         pairs = None
-        if PAIR_RADIAL and plan.n_edges and not want_e and not cg:
+        if PAIR_RADIAL and not ops.MODE.export and plan.n_edges and not want_e and not cg:
             sh32 = _opt(data, "_shifts32")
             pairs = plan.edge_pairs(sh32 if sh32 is not None else shifts)
         # prepare_graph (adapter.py:334-347) on the HIP edge-vector kernel; the
@@ -1322,7 +1337,7 @@ class TensorModel(torch.nn.Module):
         dst32 = _opt(data, "_dst32")
         if dst32 is None:
             dst32 = ei[1].to(torch.int32)
-        egraph = None if num_graphs == 1 else batch[ei[0]].to(torch.int32)
+        egraph = None if (num_graphs == 1 and not ops.MODE.export) else batch[ei[0]].to(torch.int32)
         vec = ops.edge_vectors(pos_s, lat_s, shifts, plan, dst32, egraph)
         E, e_node = self.readout_fn.energy(data, plan, vec, pairs=pairs)
         out: Dict[str, Optional[torch.Tensor]] = dict(energy=E, node_energy=e_node, forces=None, virials=None,

@@ -56,9 +56,11 @@ TIMER = None
 
 
 class _Mode(threading.local):
-    """Per-thread switch of the operators' autograd form (see ``differentiable_twice``)."""
+    """Per-thread switch of the operators' autograd form (see ``differentiable_twice``
+    and ``export_mode``)."""
 
     double = False
+    export = False
 
 
 MODE = _Mode()
@@ -80,6 +82,33 @@ def differentiable_twice(on: bool = True):
         yield
     finally:
         MODE.double = prev
+
+
+@contextlib.contextmanager
+def export_mode():
+    """The model as a graph that ``make_fx`` / ``torch.export`` can trace with
+    symbolic node and edge counts: the operators of ``differentiable_twice``,
+    with the kernels reached only through the ``torch.library`` operators of
+    ``tace_amd.library`` (tensor products, per-species linears), no host-side
+    plans (species order, receiver CSR, edge pairs are made inside those
+    operators) and features in node order."""
+    prev = (MODE.double, MODE.export)
+    MODE.double, MODE.export = True, True
+    try:
+        yield
+    finally:
+        MODE.double, MODE.export = prev
+
+
+class TracedEdges:
+    """The edge list where an ``EdgePlan`` would be (export mode): the
+    operators build their receiver CSR from ``edge_index`` themselves."""
+
+    def __init__(self, edge_index: torch.Tensor, n_nodes):
+        self.edge_index = edge_index
+        self.n_nodes = n_nodes
+        self.src = edge_index[0]
+        self.n_edges = edge_index.shape[1]
 
 
 def _t0(name):
@@ -409,6 +438,11 @@ def edge_tp_scatter(x, y, w, plan: EdgePlan, var: TpVariant, C: int, layout: int
     LAYOUT_IN1_GROUPED (x, grad x) and LAYOUT_OUT_GROUPED (output, grad output).
     ``node_map`` (int32 [N]): row of node n in x and in the output when the
     features are stored in another order than the edges index (None: same)."""
+    if MODE.export:
+        from . import library
+        if node_map is not None:
+            raise ValueError("export mode keeps the features in node order (node_map None)")
+        return library.uvu_scatter(x, y, w, plan.edge_index, var.key, C, int(layout))
     if node_map is not None:
         _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
     if MODE.double:
@@ -712,6 +746,9 @@ def uuu_tp(x1, x2, var: TpVariant, C: int, layout: int = 0, w: Optional[torch.Te
     IN1|OUT|IN2 (LAYOUT_ALL_GROUPED): the group-major layout of
     ``include/tace_hip.h`` for x1 / out / x2.  ``w`` [N, npath*C]: per-node
     path weights (bilinear-gate product basis)."""
+    if MODE.export:
+        from . import library
+        return library.uuu(x1, x2, w, var.key, C, int(layout))
     if MODE.double:
         return _UUUD.apply(x1.contiguous(), x2.contiguous(), None if w is None else w.contiguous(), var, C,
                            int(layout))

@@ -274,9 +274,12 @@ class TeceConvolution(torch.nn.Module):
         arithmetic; ``oam_2026_07_05.py:756-823``): what training with a force
         loss differentiates twice.  Same inputs and output as ``forward``."""
         Nn, E, C, K = x_gm.shape[0], w.shape[0], self.C, self.K
-        rows = node_map.long()
         x_lc = self.node_components(x_gm)
-        rs, rd = rows[src], rows[dst]
+        if node_map is None:   # features in node order
+            rs, rd = src, dst
+        else:
+            rows = node_map.long()
+            rs, rd = rows[src], rows[dst]
         m = torch.bmm(wigner, torch.cat((x_lc[rs], x_lc[rd]), dim=-1))
         key, query = self.key_proj(m[:, :, :C]), self.query_proj(m[:, :, C:])
         score = self._score_autograd(query, key, R)

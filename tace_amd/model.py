@@ -52,6 +52,7 @@ class SpeciesPlan:
         self.exchange = exchange
         # edge pairs whose radial weights are made once (None: per edge)
         self.pairs = pairs
+        self._pair_radial = None
         species = attrs.argmax(dim=-1)
         self.species = species
         if natural:
@@ -72,6 +73,13 @@ class SpeciesPlan:
             if c:
                 self.ranges.append((s, acc, acc + c))
             acc += c
+
+    def pair_radial(self, R: torch.Tensor) -> torch.Tensor:
+        """R's rows of the edge pairs' lower edges (the radial MLP's input),
+        gathered once per forward for all interaction layers."""
+        if self._pair_radial is None or self._pair_radial[0] is not R:
+            self._pair_radial = (R, R.index_select(0, self.pairs.row_edges))
+        return self._pair_radial[1]
 
 
 # ------------------------------------------------------------ feature layout ----
@@ -177,6 +185,11 @@ SEG_LINEAR_MIN_RANGES = {torch.float32: 1, torch.float64: 3}
 # tile edge of the float32 segmented GEMM: 128 = MFMA kernel (float32 as three
 # bf16 terms), 64 = FMA kernel
 SEG_LINEAR_TILE_F32 = 128
+# float32 shared-weight linears (e3nnLinear) with at least this many
+# instructions run as one segmented-GEMM launch too (None: one library GEMM
+# per instruction).  Water box: 62.4 against 63.0 ms/step model time (89
+# library launches per step replaced by 28 segmented ones)
+SEG_LINEAR_SHARED_MIN_INS = 1
 # the 128 MFMA kernel reads weights split into bf16 terms once per weight
 # version (tace_seg_linear_presplit) instead of splitting them in every launch
 SEG_LINEAR_PRESPLIT = True
@@ -305,6 +318,8 @@ class _LinearFn(torch.autograd.Function):
         rr = [(None, 0, Z)] if shared else ranges
         rr = [r for r in rr if r[2] > r[1]]
         ctx.seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES.get(x.dtype, 1)
+        if shared and x.dtype == torch.float32 and SEG_LINEAR_SHARED_MIN_INS is not None:
+            ctx.seg = len(lay.ins) >= SEG_LINEAR_SHARED_MIN_INS and Z > 0
         ctx.save_for_backward(x, weight, bias)
         ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
         if ctx.seg:
@@ -649,7 +664,7 @@ class O3CgtpInteraction(torch.nn.Module):
         elif pairs is not None and self.edge_info.fused:
             # the radial weights depend on the edge length only: made once per
             # edge pair and read by both directions
-            h = self.edge_info.hidden(R.index_select(0, pairs.row_edges))
+            h = self.edge_info.hidden(sp.pair_radial(R))
             m = self.rejector.paired(x, Y, h, *self.edge_info.last_layer(), plan, pairs, lay, sp.node_map)
         elif RADIAL_FUSED_TP and self.edge_info.fused and ops.rtp_supported(x.dtype, self.rejector.C, 64):
             m = self.rejector.radial_fused(x, Y, self.edge_info.hidden(R), *self.edge_info.last_layer(), plan, lay,

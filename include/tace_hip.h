@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 20
+#define TACE_HIP_ABI_VERSION 21
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -268,13 +268,20 @@ int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void*
  * constants at inference; the same e3nnElementLinear forward and input
  * gradient, linear.py:377-482).
  *   tace_bf16x3_split_blocks writes, for n_blocks weight blocks (int64 [n, 6]:
- *   src_off, cols, k, transpose, dst_off, unused; double scales[n]), the three
+ *   src_off, cols, k, transpose, dst_off, layout; double scales[n]), the three
  *   bf16 terms of scale * B (the exact split of float32 into three bf16, round
- *   to nearest even) into planes[p * plane_stride + dst_off + c k_pad + kk]
- *   for column c < cols and kk < k_pad = ceil8(k), with B[kk][c] =
- *   w[src_off + kk cols + c] (transpose = 1: the forward's W [k, n]) or
- *   w[src_off + c k + kk] (transpose = 0: W [n, k] applied transposed, the
- *   input gradient), and zeros for kk >= k.
+ *   to nearest even), with B[kk][c] = w[src_off + kk cols + c] (transpose = 1:
+ *   the forward's W [k, n]) or w[src_off + c k + kk] (transpose = 0: W [n, k]
+ *   applied transposed, the input gradient) and zeros past k and cols:
+ *     layout 0: term p into planes[p * plane_stride + dst_off + c k_pad + kk]
+ *               for column c < cols and kk < k_pad = ceil8(k);
+ *     layout 1 (MFMA fragment order, for tace_seg_linear_presplit_ks): one
+ *               buffer, per 16-column block cb and 32-k step s (nks =
+ *               ceil(k / 32) steps per column block, ceil16(cols) columns)
+ *               the three terms as runs of 512: element (c, kk) of term p at
+ *               planes[dst_off + ((cb nks + s) 3 + p) 512 + (((kk % 32) / 8)
+ *               16 + c % 16) 8 + kk % 8], cb = c / 16, s = kk / 32;
+ *               plane_stride is unused.
  *   tace_seg_linear_presplit then runs the tile table of tace_seg_linear with
  *   each contribution's w_off pointing at its block in the planes (16-byte
  *   aligned, plane_stride a multiple of 8); trans and the scales are unused
@@ -286,6 +293,21 @@ int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, const double
 int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
                              const float* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                              double alpha, void* stream);
+/* The same linears' tiles with one contribution of k <= 128 (the input
+ * gradients of the product-basis contractions, linear.py:377-482, and any
+ * block with no contribution), as n_tasks row tiles of up to 128 rows, each
+ * over a column range, with the weights split in MFMA fragment order
+ * (tace_bf16x3_split_blocks layout 1):
+ *   tasks int64 [n_tasks, 10]: out_base (offset of the tile's row 0, column 0
+ *         in y), rows (1..128), n (block width = row stride of y), cb, ce (its
+ *         columns [cb, ce), ce <= n), bias_off (-1 none), x_base (offset of
+ *         the tile's row 0 in x), k (0..128, the row stride of x; 0: no
+ *         contribution), w_off (the block's offset in w_frag), unused.
+ * y[tile] = alpha (x[rows, :k] @ B + bias[bias_off + cols]), the same bits as
+ * tace_seg_linear_presplit gives for the same tile.  Trusted tables, checked
+ * by the host (tace_amd.ops.SegLinearPlan). */
+int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+                                const int64_t* tasks, int64_t n_tasks, double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"

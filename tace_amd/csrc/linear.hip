@@ -444,11 +444,243 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
   }
 }
 
-// Per block (6 x int64): src_off, cols, k, transpose, dst_off, unused; one
-// double scale.  dst column c, k index kk < k_pad of plane p = term p of
-// scale * (transpose ? w[src_off + kk cols + c] : w[src_off + c k + kk]),
-// zero for kk >= k.  blockIdx.y picks the block, the x dimension strides
-// over its cols x k_pad elements.
+// ---- short k, wide n: the input-gradient shape ---------------------------
+// The input gradients of the product-basis contractions are [rows, k = 128]
+// x [128, n] with n up to ~5,400 columns per output block.  A 128 x 128 tile
+// of the kernel above does four 32-k steps after staging A and B through LDS
+// with two barriers per step, then writes its outputs one float per lane.
+// Here a workgroup owns one 128-row tile of one contribution with k <= 128
+// and a range of columns:
+//  * A is split once into the three bf16 planes in LDS (k-contiguous rows of
+//    128 + 8 bf16: 272-byte rows, so the 16 rows of a fragment read fall on
+//    distinct banks); one barrier, none after it;
+//  * eight wavefronts in two groups of four take the range's 128-column tiles
+//    alternately; a wavefront owns all 128 rows of 32 columns, so each B
+//    fragment is loaded by one wavefront only;
+//  * B comes from weights pre-split in MFMA fragment order (k_split_blocks,
+//    layout 1): the three terms of one 16-column x 32-k fragment are three
+//    contiguous 1 KB runs in lane order, so a fragment is one fully
+//    coalesced 16-byte load per lane.  Loaded one 32-k step ahead, and across
+//    the end of a column tile: the next tile's first step is in flight before
+//    this tile's stores, so no wait covers them.  The loads are unconditional
+//    (the column block clamped into the weight block);
+//  * the MFMA runs with the operands swapped (B fragments as the row operand),
+//    so a lane holds 4 consecutive columns of one output row: one 16-byte
+//    store per 16 x 16 block.
+// The number of 32-k steps is a template parameter (1..4).  Per output element
+// the products and their order are those of k_seg_linear_bx3s (k steps in
+// order, the six terms smallest first, each a sum over the same 32 products),
+// so the two kernels give the same bits.
+//
+// Task table (10 x int64): out_base (element offset of the tile's row 0,
+// column 0 in y), rows (<= 128), n (block width = row stride of y), [cb, ce)
+// (the columns, ce <= n), bias_off (-1 none), x_base (element offset of the
+// tile's row 0 in x), k (0..128, the row stride of x; 0 = no contribution:
+// the tile is alpha * bias or zero), w_off (the block's offset in the
+// fragment-order weights), unused.
+constexpr int KS_KMAX = 128, KS_STR = KS_KMAX + 8, KS_PL = 128 * KS_STR;
+
+struct KsTask {
+  int64_t out_base, bias_off;
+  int rows, n, cb, ce, nks, nb16;
+  const unsigned short* wf;
+};
+
+// B fragments (three terms, column blocks 2 wq and 2 wq + 1 of column tile c)
+// of step ks into d; the column block clamped to the weight block's last
+__device__ __forceinline__ void ks_load_b(const KsTask& T, int c, int ks, int wq, int lane, u4v (&d)[3][2]) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int jb = min((c >> 4) + 2 * wq + j, T.nb16 - 1);
+    const unsigned short* p = T.wf + ((int64_t)(jb * T.nks + ks) * 3) * 512 + 8 * lane;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) d[pl][j] = *(const u4v*)(p + pl * 512);
+  }
+}
+
+// step KS of a column tile: MFMAs on cur while the next step's fragments
+// (or the next tile's first) load into nxt
+template <int NKS, int KS>
+__device__ __forceinline__ void ks_step(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
+                                        int lane, int fr, int fg, f4 (&acc)[8][2], const u4v (&cur)[3][2],
+                                        u4v (&nxt)[3][2]) {
+  if (KS + 1 < NKS) ks_load_b(T, c, KS + 1, wq, lane, nxt);
+  else ks_load_b(T, c + 256, 0, wq, lane, nxt);
+  // the loads go out before this step's MFMAs (the scheduler would sink them
+  // to the end of the step, where nothing hides their latency)
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ip = 0; ip < 4; ++ip) {   // row blocks in pairs: four independent accumulators per term
+    bx3_bf8 af[2][3];
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl)
+        af[ii][pl] = *(const bx3_bf8*)&As[pl * KS_PL + (32 * ip + 16 * ii + fr) * KS_STR + 32 * KS + 8 * fg];
+#pragma unroll
+    for (int u = 0; u < 6; ++u)   // the six terms a_i b_j, smallest first
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[2 * ip + ii][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bx3_bf8, cur[BX3_TB[u]][j]), af[ii][BX3_TA[u]], acc[2 * ip + ii][j], 0, 0, 0);
+  }
+  // keep the next step's LDS reads out of this one
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// steps KS.. of a column tile; step KS reads buffer (KS + PAR) & 1
+template <int NKS, int PAR, int KS>
+__device__ __forceinline__ void ks_steps(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
+                                         int lane, int fr, int fg, f4 (&acc)[8][2], u4v (&b0)[3][2],
+                                         u4v (&b1)[3][2]) {
+  if constexpr (KS < NKS) {
+    if constexpr (((KS + PAR) & 1) == 0) ks_step<NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+    else ks_step<NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b1, b0);
+    ks_steps<NKS, PAR, KS + 1>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+  }
+}
+
+// this wavefront's 128 x 32 part of column tile c
+template <int NKS, int PAR>
+__device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, const KsTask& T, float* __restrict__ y,
+                                        const float* __restrict__ bias, float alpha, bool vst, int c, int wq,
+                                        int lane, int fr, int fg, u4v (&b0)[3][2], u4v (&b1)[3][2]) {
+  // the bias of this lane's 8 columns, loaded before the MFMAs: a load
+  // waited for in the stores would wait for the B fragments loaded after it
+  f4 bv[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) bv[j] = f4{0.f, 0.f, 0.f, 0.f};
+  if (T.bias_off >= 0) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[j][q] = bias[T.bias_off + min(c + 32 * wq + 16 * j + 4 * fg + q, T.ce - 1)];
+  }
+  f4 acc[8][2];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  ks_steps<NKS, PAR, 0>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+  // acc[i][j][q] = out[row 16 i + fr][column c + 32 wq + 16 j + 4 fg + q].
+  // Lanes fr and fr ^ 8 trade one block, so that a store writes 8 whole rows
+  // of the 32 columns (128 contiguous bytes each) instead of 16 half rows:
+  // lane fr < 8 keeps j = 0 of row fr and takes j = 0 of row fr + 8; lane
+  // fr >= 8 keeps j = 1 of row fr and takes j = 1 of row fr - 8.
+  const bool lo = fr < 8;
+  const int jl = lo ? 0 : 1;   // this lane's 16-column half, in both stores
+  const int col = c + 32 * wq + 16 * jl + 4 * fg;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f4 v0 = alpha * (acc[i][0] + bv[0]), v1 = alpha * (acc[i][1] + bv[1]);
+    const f4 give = lo ? v1 : v0;
+    f4 got;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) got[q] = __shfl_xor(give[q], 8);
+    const f4 s0 = lo ? v0 : got, s1 = lo ? got : v1;   // rows 16 i + (fr & 7), + 8
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int r = 16 * i + 8 * h + (fr & 7);
+      if (r >= T.rows || col >= T.ce) continue;
+      const f4 v = h ? s1 : s0;
+      float* dst = y + T.out_base + (int64_t)r * T.n + col;
+      if (vst) {
+        *(f4*)dst = v;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (col + q < T.ce) dst[q] = v[q];
+      }
+    }
+  }
+}
+
+template <int NKS>
+__device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As, const KsTask& T,
+                                           float* __restrict__ y, const float* __restrict__ bias, float alpha, int grp,
+                                           int wq, int lane, int fr, int fg) {
+  int c0 = T.cb + 128 * grp;
+  if (c0 >= T.ce) return;
+  // 16-byte stores when every 4-column group of every row is 16-byte aligned
+  // (ce and cb are then multiples of 4 too)
+  const bool vst = ((T.n & 3) == 0) && ((T.out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
+  u4v b0[3][2], b1[3][2];
+  if (NKS > 0) ks_load_b(T, c0, 0, wq, lane, b0);
+  for (; c0 < T.ce; c0 += 512) {
+    ks_tile<NKS, 0>(As, T, y, bias, alpha, vst, c0, wq, lane, fr, fg, b0, b1);
+    if (c0 + 256 < T.ce) ks_tile<NKS, NKS & 1>(As, T, y, bias, alpha, vst, c0 + 256, wq, lane, fr, fg, b0, b1);
+  }
+}
+
+__global__ __launch_bounds__(512) void k_seg_linear_ks(const float* __restrict__ x, float* __restrict__ y,
+                                                       const unsigned short* __restrict__ wfrag,
+                                                       const float* __restrict__ bias,
+                                                       const int64_t* __restrict__ tasks, float alpha, int n_tasks,
+                                                       int per) {
+  __shared__ __attribute__((aligned(16))) unsigned short As[3 * KS_PL];
+  const int task = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (task >= n_tasks) return;
+  const int64_t* td = tasks + 10 * (int64_t)task;
+  KsTask T;
+  T.out_base = td[0];
+  T.rows = (int)td[1];
+  T.n = (int)td[2];
+  T.cb = (int)td[3];
+  T.ce = (int)td[4];
+  T.bias_off = td[5];
+  const int64_t x_base = td[6];
+  const int k = (int)td[7];
+  T.wf = wfrag + td[8];
+  T.nks = (k + 31) >> 5;
+  T.nb16 = (T.n + 15) >> 4;
+  const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int grp = wv >> 2, wq = wv & 3;
+  const int fr = lane & 15, fg = lane >> 4;
+
+  // A: rows x k of x (row stride k) -> planes, zeros past rows and past k
+  // (up to the next multiple of 32)
+  {
+    const float* __restrict__ xa = x + x_base;
+    const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
+    const int kq = T.nks * 4;   // 8-k units per row
+    for (int u = t; u < 128 * kq; u += 512) {
+      const int r = u / kq, kk = (u - r * kq) * 8;
+      const bool ok = r < T.rows;
+      const float* p = xa + (int64_t)r * k + kk;
+      const f4 a0 = seg_ld4(p, ok && xvec && kk + 4 <= k, ok && kk < k, k - kk);
+      const f4 a1 = seg_ld4(p + 4, ok && xvec && kk + 8 <= k, ok && kk + 4 < k, k - kk - 4);
+      const float v[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      bx3_bf8 tt[3];
+      bx3_split8(v, tt);
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl) *(bx3_bf8*)&As[pl * KS_PL + r * KS_STR + kk] = tt[pl];
+    }
+  }
+  __syncthreads();
+
+  switch (T.nks) {
+    case 1: ks_columns<1>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
+    case 2: ks_columns<2>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
+    case 3: ks_columns<3>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
+    case 4: ks_columns<4>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
+    default: ks_columns<0>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;   // k = 0: bias or zeros
+  }
+}
+
+// Per block (6 x int64): src_off, cols, k, transpose, dst_off, layout; one
+// double scale.  B[kk][c] = scale * (transpose ? w[src_off + kk cols + c] :
+// w[src_off + c k + kk]), zero past k (and past cols).
+//  layout 0: column c, k index kk < k_pad = ceil8(k) of term p at
+//            out[p * pstride + dst_off + c k_pad + kk];
+//  layout 1: MFMA fragment order for k_seg_linear_ks, one buffer: per
+//            16-column block cb and 32-k step s (nks = ceil(k / 32) steps),
+//            the three terms as 512-element runs in lane order, element
+//            (c, kk) of term p at out[dst_off + ((cb nks + s) 3 + p) 512 +
+//            (((kk % 32) / 8) 16 + c % 16) 8 + kk % 8], cb = c / 16, s = kk /
+//            32, over ceil16(cols) columns.
+// blockIdx.y picks the block, the x dimension strides over its elements.
 __global__ __launch_bounds__(256) void k_split_blocks(const float* __restrict__ w, const int64_t* __restrict__ blocks,
                                                       const double* __restrict__ scales,
                                                       unsigned short* __restrict__ out, int64_t pstride) {
@@ -456,17 +688,27 @@ __global__ __launch_bounds__(256) void k_split_blocks(const float* __restrict__ 
   const int64_t src = bd[0], dst = bd[4];
   const int cols = (int)bd[1], k = (int)bd[2];
   const bool tr = bd[3] != 0;
-  const int kpad = (k + 7) & ~7;
+  const bool frag = bd[5] == 1;
+  const int kpad = frag ? (k + 31) & ~31 : (k + 7) & ~7;
+  const int ccols = frag ? (cols + 15) & ~15 : cols;
   const float sc = (float)scales[blockIdx.y];
-  const int64_t total = (int64_t)cols * kpad;
+  const int64_t total = (int64_t)ccols * kpad;
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
     const int c = (int)(e / kpad), kk = (int)(e - (int64_t)c * kpad);
     float v = 0.f;
-    if (kk < k) v = bx3_scale2(bx3_f2{tr ? w[src + (int64_t)kk * cols + c] : w[src + (int64_t)c * k + kk], 0.f}, sc).x;
+    if (kk < k && c < cols)
+      v = bx3_scale2(bx3_f2{tr ? w[src + (int64_t)kk * cols + c] : w[src + (int64_t)c * k + kk], 0.f}, sc).x;
     unsigned h[3];
     bx3_split2(bx3_f2{v, 0.f}, h);
+    if (frag) {
+      const int64_t run = ((int64_t)(c >> 4) * (kpad >> 5) + (kk >> 5)) * 3;
+      const int64_t lane_el = (int64_t)((((kk & 31) >> 3) << 4) + (c & 15)) * 8 + (kk & 7);
 #pragma unroll
-    for (int p = 0; p < 3; ++p) out[p * pstride + dst + e] = (unsigned short)(h[p] & 0xffffu);
+      for (int p = 0; p < 3; ++p) out[dst + (run + p) * 512 + lane_el] = (unsigned short)(h[p] & 0xffffu);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 3; ++p) out[p * pstride + dst + e] = (unsigned short)(h[p] & 0xffffu);
+    }
   }
 }
 
@@ -496,6 +738,19 @@ extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t
                      (const unsigned short*)w_planes, plane_stride, bias, tiles, contribs, (float)alpha,
                      (int)n_tiles, per);
   return tace_check_launch("tace_seg_linear_presplit");
+}
+
+extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+                                           const int64_t* tasks, int64_t n_tasks, double alpha, void* stream) {
+  if (n_tasks < 0 || n_tasks > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_ks: bad task count");
+  if (n_tasks == 0) return 0;
+  if (!x || !y || !w_frag || !tasks) return tace_fail_msg("tace_seg_linear_presplit_ks: null pointer");
+  if ((((uintptr_t)w_frag) & 15) != 0)
+    return tace_fail_msg("tace_seg_linear_presplit_ks: the fragment-order weights must be 16-byte aligned");
+  const int per = (int)((n_tasks + 7) / 8);
+  hipLaunchKernelGGL(k_seg_linear_ks, dim3((unsigned)(8 * per)), dim3(512), 0, (hipStream_t)stream, x, y,
+                     (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
+  return tace_check_launch("tace_seg_linear_presplit_ks");
 }
 
 extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y,

@@ -233,37 +233,54 @@ class _LinearLayout:
         # the block's offset in one species' planes, its columns and k; per
         # direction ("fwd": B = W, "bwd": B = W^T)
         self.split_blocks = {}
+        # the same in MFMA fragment order (layout 1) for the instructions with
+        # k <= 128 (tace_seg_linear_presplit_ks); offset -1 for the others
+        self.frag_blocks = {}
         for kind in ("fwd", "bwd"):
-            blocks, acc = [], 0
+            blocks, acc, fblocks, facc = [], 0, [], 0
             for (i, o, off, mi, mo, pw) in self.ins:
                 cols, k = (mo, mi) if kind == "fwd" else (mi, mo)
                 blocks.append((acc, cols, k))
                 acc += cols * ((k + 7) // 8 * 8)
+                if k <= 128:
+                    fblocks.append((facc, cols, k))
+                    facc += 3 * ((cols + 15) // 16 * 16) * ((k + 31) // 32 * 32)
+                else:
+                    fblocks.append((-1, cols, k))
             self.split_blocks[kind] = (blocks, acc)
+            self.frag_blocks[kind] = (fblocks, facc)
 
-    def split_weights(self, kind: str, weight: torch.Tensor) -> Tuple[torch.Tensor, int]:
+    def split_weights(self, kind: str, weight: torch.Tensor, frag: bool = False) -> Tuple[torch.Tensor, int]:
         """The three bf16 terms of every (species, instruction) weight block
         with its path weight folded in, in the column layout of
         ``tace_seg_linear_presplit`` ("fwd": B = W, "bwd": B = W^T); returns
-        (planes int16 [3 * stride], plane stride).  Cached until the weight
+        (planes int16 [3 * stride], plane stride).  ``frag``: the blocks with
+        k <= 128 in the MFMA fragment order of ``tace_seg_linear_presplit_ks``
+        instead (one buffer; the stride is its size).  Cached until the weight
         changes (its version counter or storage)."""
         w = weight.detach()
         key = (w.data_ptr(), w._version, tuple(w.shape), str(w.device))
-        hit = self._split.get(kind)
+        ck = (kind, frag)
+        hit = self._split.get(ck)
         if hit is not None and hit[0] == key:
             return hit[1], hit[2]
-        blocks, per = self.split_blocks[kind]
+        blocks, per = (self.frag_blocks if frag else self.split_blocks)[kind]
         S = 1 if w.dim() == 1 else w.shape[0]
-        stride = (S * per + 63) // 64 * 64
+        # never empty: a plan whose short-k tasks are all zero blocks still
+        # passes a valid pointer
+        stride = max(64, (S * per + 63) // 64 * 64)
         tab, sc = [], []
         for sp in range(S):
             for (dst, cols, k), (i, o, off, mi, mo, pw) in zip(blocks, self.ins):
-                tab.append((sp * self.weight_numel + off, cols, k, 1 if kind == "fwd" else 0, sp * per + dst, 0))
+                if dst < 0:
+                    continue
+                tab.append((sp * self.weight_numel + off, cols, k, 1 if kind == "fwd" else 0, sp * per + dst,
+                            1 if frag else 0))
                 sc.append(pw)
-        planes = ops.bf16x3_split_blocks(w.contiguous().view(-1), tab, sc, stride)
+        planes = ops.bf16x3_split_blocks(w.contiguous().view(-1), tab, sc, stride, frag=frag)
         # the entry keeps the weight alive, so no other tensor can take its
         # address (and version) while the planes are cached
-        self._split[kind] = (key, planes, stride, w)
+        self._split[ck] = (key, planes, stride, w)
         return planes, stride
 
     def seg_plan(self, kind: str, rr, Z: int, x: torch.Tensor, weight: torch.Tensor,
@@ -290,10 +307,12 @@ class _LinearLayout:
         if presplit:
             # weight offsets into the pre-split planes instead of the flat weight
             blocks, per = self.split_blocks[kind]
-            ins = [(a, b, k, blocks[j][0], tr, pw) for j, (a, b, k, _off, tr, pw) in enumerate(ins)]
+            fblocks, fper = self.frag_blocks[kind]
+            ins = [(a, b, k, blocks[j][0], tr, pw, fblocks[j][0]) for j, (a, b, k, _off, tr, pw) in enumerate(ins)]
             S = 1 if weight.dim() == 1 else weight.shape[0]
             plan = ops.SegLinearPlan(Z, outs, ins, rr, per, self.bias_numel, xn, yn, S * per,
-                                     0 if bias is None else bias.numel(), x.device, tile, split_weights=True)
+                                     0 if bias is None else bias.numel(), x.device, tile, split_weights=True,
+                                     frag=(fper, S * fper))
         else:
             plan = ops.SegLinearPlan(Z, outs, ins, rr, self.weight_numel, self.bias_numel, xn, yn, weight.numel(),
                                      0 if bias is None else bias.numel(), x.device, tile)
@@ -326,7 +345,8 @@ class _LinearFn(torch.autograd.Function):
             # all species and instructions in one segmented-GEMM launch
             plan = lay.seg_plan("fwd", rr, Z, x, weight, bias)
             if plan.split_weights:
-                return ops.seg_linear_presplit(x, out, *lay.split_weights("fwd", weight), bias, plan, alpha)
+                fr = lay.split_weights("fwd", weight, frag=True)[0] if plan.n_ks else None
+                return ops.seg_linear_presplit(x, out, *lay.split_weights("fwd", weight), bias, plan, alpha, frag=fr)
             return ops.seg_linear(x, out, weight, bias, plan, alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
@@ -357,7 +377,8 @@ class _LinearFn(torch.autograd.Function):
         if ctx.seg and gx is not None:
             plan = lay.seg_plan("bwd", rr, x.shape[0], x, weight, None)
             if plan.split_weights:
-                ops.seg_linear_presplit(gout, gx, *lay.split_weights("bwd", weight), None, plan, alpha)
+                fr = lay.split_weights("bwd", weight, frag=True)[0] if plan.n_ks else None
+                ops.seg_linear_presplit(gout, gx, *lay.split_weights("bwd", weight), None, plan, alpha, frag=fr)
             else:
                 ops.seg_linear(gout, gx, weight, None, plan, alpha)
         done = set()

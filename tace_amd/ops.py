@@ -1350,6 +1350,14 @@ def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> tor
 
 
 # ------------------------------------------------------ per-species linears ----
+# output blocks of at least this many columns whose tiles have one
+# contribution with k <= 128 (or none) go to tace_seg_linear_presplit_ks
+# (pre-split plans only; None: every tile to the tile kernel)
+SEG_KS_MIN_N = 256
+# columns per tace_seg_linear_presplit_ks task
+SEG_KS_CHUNK = 1024
+
+
 class SegLinearPlan:
     """Device tables of ``tace_seg_linear`` for one direction of one
     per-species linear over one set of species row ranges.
@@ -1367,7 +1375,8 @@ class SegLinearPlan:
     (64, 64))."""
 
     def __init__(self, Z, out_blocks, ins, ranges, w_stride, b_stride, x_numel, y_numel, w_numel, b_numel, device,
-                 tile: Tuple[int, int] = (64, 64), split_weights: bool = False):
+                 tile: Tuple[int, int] = (64, 64), split_weights: bool = False,
+                 frag: Optional[Tuple[int, int]] = None):
         TM, TN = tile
         self.tile = tuple(tile)
         # split_weights: w_off / w_stride / w_numel index the pre-split planes
@@ -1375,10 +1384,18 @@ class SegLinearPlan:
         self.split_weights = bool(split_weights)
         if self.split_weights and self.tile != (128, 128):
             raise ValueError("pre-split weights run on the 128 x 128 float32 MFMA tiles")
-        tiles, contribs, scales = [], [], []
+        tiles, contribs, scales, tasks = [], [], [], []
         nc = 0
+        # frag: (per-species stride, size) of the fragment-order weights that
+        # the short-k tasks read; an instruction's offset there is its 7th item
+        # (-1: not split that way)
+        self.frag_numel = frag[1] if frag is not None else 0
         for ob, (s_o, n, d, boff) in enumerate(out_blocks):
             mine = [c for c in ins if c[0] == ob]
+            if (self.split_weights and frag is not None and SEG_KS_MIN_N is not None and n >= SEG_KS_MIN_N
+                    and len(mine) <= 1 and all(c[2] <= 128 and c[6] >= 0 for c in mine)):
+                tasks += self._ks_tasks(Z, s_o, n, d, boff, mine, ranges, frag[0], b_stride)
+                continue
             c0s = np.arange(0, n, TN, dtype=np.int64)
             for (sp, a, b) in ranges:
                 if b <= a:
@@ -1401,7 +1418,7 @@ class SegLinearPlan:
                 tiles.append(t)
                 if k_each:
                     c = np.zeros((T, k_each, 4), dtype=np.int64)
-                    for j, (_, s_i, k, w_off, trans, sc) in enumerate(mine):
+                    for j, (_, s_i, k, w_off, trans, sc, *_f) in enumerate(mine):
                         c[:, j, 0] = Z * s_i + R.ravel() * k
                         c[:, j, 1] = k
                         c[:, j, 2] = w_off + (0 if sp is None else sp * w_stride)
@@ -1439,6 +1456,47 @@ class SegLinearPlan:
         self.tiles = torch.from_numpy(np.ascontiguousarray(t)).to(device)
         self.contribs = torch.from_numpy(np.ascontiguousarray(c) if len(c) else np.zeros((1, 4), np.int64)).to(device)
         self.scales = torch.from_numpy(s if len(s) else np.zeros(1)).to(device)
+        # short-k tasks (tace_seg_linear_presplit_ks), checked like the tiles
+        k_t = np.asarray(tasks, dtype=np.int64).reshape(-1, 10)
+        if len(k_t):
+            if (k_t[:, 0] + (k_t[:, 1] - 1) * k_t[:, 2] + k_t[:, 4]).max() > y_numel:
+                raise ValueError("seg linear plan: output task out of range")
+            if (k_t[:, 0] < 0).any() or (k_t[:, 4] > k_t[:, 2]).any() or (k_t[:, 3] >= k_t[:, 4]).any():
+                raise ValueError("seg linear plan: bad task columns")
+            hb = k_t[:, 5] >= 0
+            if hb.any() and (k_t[hb, 5] + k_t[hb, 4]).max() > b_numel:
+                raise ValueError("seg linear plan: bias out of range")
+            hk = k_t[:, 7] > 0
+            if hk.any():
+                if (k_t[hk, 6] + k_t[hk, 1] * k_t[hk, 7]).max() > x_numel:
+                    raise ValueError("seg linear plan: input task out of range")
+                fsz = 3 * ((k_t[hk, 2] + 15) // 16 * 16) * ((k_t[hk, 7] + 31) // 32 * 32)
+                if (k_t[hk, 8] + fsz).max() > self.frag_numel or (k_t[hk, 8] % 8).any():
+                    raise ValueError("seg linear plan: fragment-order weights of a task out of range")
+            self.flops += int(2 * (k_t[:, 1] * (k_t[:, 4] - k_t[:, 3]) * k_t[:, 7]).sum())
+        self.n_ks = len(k_t)
+        self.ks_tasks = torch.from_numpy(np.ascontiguousarray(k_t) if len(k_t) else np.zeros((1, 10), np.int64)).to(device)
+
+    def _ks_tasks(self, Z, s_o, n, d, boff, mine, ranges, f_stride, b_stride):
+        """Tasks of one output block (one contribution with k <= 128, or
+        none): column chunk-major, so that the workgroups running at one time
+        on an XCD share a chunk's weight columns in its L2."""
+        out = []
+        for cb in range(0, n, SEG_KS_CHUNK):
+            ce = min(n, cb + SEG_KS_CHUNK)
+            for (sp, a, b) in ranges:
+                if b <= a:
+                    continue
+                for r0 in range(a * d, b * d, 128):
+                    rows = min(b * d - r0, 128)
+                    bo = -1 if boff is None else boff + (0 if sp is None else sp * b_stride)
+                    if mine:
+                        s_i, k, f_off = mine[0][1], mine[0][2], mine[0][6]
+                        out.append((Z * s_o + r0 * n, rows, n, cb, ce, bo, Z * s_i + r0 * k, k,
+                                    f_off + (0 if sp is None else sp * f_stride), 0))
+                    else:
+                        out.append((Z * s_o + r0 * n, rows, n, cb, ce, bo, 0, 0, 0, 0))
+        return out
 
 
 def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], plan: SegLinearPlan,
@@ -1464,19 +1522,26 @@ def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional
     return y
 
 
-def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int) -> torch.Tensor:
+def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int, frag: bool = False) -> torch.Tensor:
     """``tace_bf16x3_split_blocks``: the three bf16 terms of scale x each
-    weight block, column-major runs of ceil8(k) (table rows: src_off, cols, k,
-    transpose, dst_off, 0); returns int16 planes [3 * plane_stride]."""
+    weight block (table rows: src_off, cols, k, transpose, dst_off, layout),
+    column-major runs of ceil8(k) into int16 planes [3 * plane_stride]
+    (layout 0), or with ``frag`` in MFMA fragment order into one int16 buffer
+    [plane_stride] (layout 1)."""
     _req(w, "weight", torch.float32)
     tab = np.asarray(blocks, dtype=np.int64).reshape(-1, 6)
     if len(tab):
-        kpad = (tab[:, 2] + 7) // 8 * 8
+        if (tab[:, 5] != (1 if frag else 0)).any():
+            raise ValueError("bf16x3 split: every block must have the requested layout")
+        if frag:
+            size = 3 * ((tab[:, 1] + 15) // 16 * 16) * ((tab[:, 2] + 31) // 32 * 32)
+        else:
+            size = tab[:, 1] * ((tab[:, 2] + 7) // 8 * 8)
         if (tab[:, 0] + tab[:, 1] * tab[:, 2]).max() > w.numel():
             raise ValueError("bf16x3 split: source block out of range")
-        if (tab[:, 4] + tab[:, 1] * kpad).max() > plane_stride:
+        if (tab[:, 4] + size).max() > plane_stride:
             raise ValueError("bf16x3 split: destination block out of range")
-    planes = torch.zeros(3 * plane_stride, dtype=torch.int16, device=w.device)
+    planes = torch.zeros((1 if frag else 3) * plane_stride, dtype=torch.int16, device=w.device)
     tb = torch.from_numpy(np.ascontiguousarray(tab)).to(w.device)
     sc = torch.tensor(list(scales), dtype=torch.float64, device=w.device)
     for b0 in range(0, len(tab), 65535):
@@ -1488,9 +1553,12 @@ def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int) -> t
 
 
 def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, plane_stride: int,
-                        bias: Optional[torch.Tensor], plan: SegLinearPlan, alpha: float) -> torch.Tensor:
+                        bias: Optional[torch.Tensor], plan: SegLinearPlan, alpha: float,
+                        frag: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Runs a ``split_weights`` plan (``tace_seg_linear_presplit``) with the
-    weight planes of ``bf16x3_split_blocks``; returns y."""
+    weight planes of ``bf16x3_split_blocks``, and its short-k tasks
+    (``tace_seg_linear_presplit_ks``) with the fragment-order weights
+    ``frag``; returns y."""
     if not plan.split_weights:
         raise ValueError("seg linear: the plan indexes flat weights, not pre-split planes")
     for t, nm, n in ((x, "x", plan.x_numel), (y, "y", plan.y_numel)):
@@ -1504,10 +1572,17 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, 
         if bias.numel() != plan.b_numel:
             raise ValueError("seg linear: bias size differs from the plan's")
     tok = _t0("seg_linear")
-    N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride,
-                                             None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(),
-                                             plan.n_tiles, plan.contribs.data_ptr(), float(alpha),
-                                             N.stream_ptr(x.device)), "tace_seg_linear_presplit")
+    st = N.stream_ptr(x.device)
+    b_ptr = None if bias is None else bias.data_ptr()
+    N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride, b_ptr,
+                                             plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
+                                             float(alpha), st), "tace_seg_linear_presplit")
+    if plan.n_ks:
+        if frag is None or frag.dtype != torch.int16 or frag.numel() < plan.frag_numel:
+            raise ValueError("seg linear: the plan's short-k tasks need its fragment-order weights")
+        N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
+                                                    plan.ks_tasks.data_ptr(), plan.n_ks, float(alpha), st),
+                "tace_seg_linear_presplit_ks")
     _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
     return y
 

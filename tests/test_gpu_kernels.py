@@ -470,7 +470,13 @@ def _element_linear_reference(x, W, b, irreps_in, irreps_out, species, alpha):
 SEG_CASES = [("8x0e+5x0e+6x1o+4x1o+3x2e", "70x0e+6x1o+65x2e+2x3o", [0, 1, 17, 64, 65, 3, 130, 0]),
              ("64x0e+36x0e+132x1o+20x2e", "260x0e+68x1o+40x2e", [140, 0, 3, 290, 1]),
              # long k into 256-wide blocks, and back (1100-wide gradient blocks)
-             ("1100x0e+300x1o", "256x0e+256x1o", [0, 300, 7, 129])]
+             ("1100x0e+300x1o", "256x0e+256x1o", [0, 300, 7, 129]),
+             # short k into wide blocks (the short-k task kernel: k 128, 100,
+             # 20 and 8 into 300, 1100, 260 and 40 columns; a 513-wide block
+             # no instruction writes), and back (k 100 and 64 into 1100 and
+             # 300 columns)
+             ("128x0e+100x1o+20x2e+8x3o", "300x0e+1100x1o+260x2e+40x3o+513x3e", [0, 300, 7, 129, 1]),
+             ("1100x0e+300x1o", "100x0e+64x1o", [130, 0, 5, 256])]
 
 
 @pytest.mark.parametrize("dtype,tile,presplit", [(torch.float64, 64, False), (torch.float32, 128, True),

@@ -321,7 +321,7 @@ def tece_rotate_in_backward(x: Tensor, wigner: Tensor, rows_src: Tensor, rows_ds
     gxs, gxd, gW, gwr = ops.launch_rotate_in_bwd(x.contiguous(), wigner.contiguous(), rows_src.contiguous(),
                                                  rows_dst.contiguous(), radial_w.contiguous(), g[:n], g[n:2 * n],
                                                  g[2 * n:], True)
-    gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
+    gx = ops.scatter_add_rows(ops.scatter_add_rows(torch.zeros_like(x), rows_src, gxs), rows_dst, gxd)
     return gx, gW, gwr
 
 

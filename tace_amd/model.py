@@ -1110,7 +1110,7 @@ def _atomic_virials(vec, edge_forces, edge_index, lattice, batch, n_nodes):
     symmetrised and negated; stresses = -virials / cell volume."""
     ev = edge_forces.unsqueeze(-1) * vec.unsqueeze(-2)  # [E, 3, 3], f_i r_j
     av = torch.zeros(n_nodes, 3, 3, dtype=vec.dtype, device=vec.device)
-    av.index_add_(0, edge_index[0], ev).index_add_(0, edge_index[1], ev)
+    ops.scatter_add_rows(ops.scatter_add_rows(av, edge_index[0], ev), edge_index[1], ev)
     av = -0.5 * (av + av.transpose(-1, -2)) / 2
     vol = torch.linalg.det(lattice).abs()
     st = -av / vol[batch].view(-1, 1, 1)

@@ -622,8 +622,8 @@ class _EdgeVectors(torch.autograd.Function):
             if ctx.edge_graph is None:
                 glat = outer.sum(0).view(1, 3, 3)
             else:
-                glat = torch.zeros(ctx.nlat, 9, dtype=g.dtype, device=g.device).index_add_(
-                    0, ctx.edge_graph.long(), outer).view(-1, 3, 3)
+                glat = scatter_add_rows(torch.zeros(ctx.nlat, 9, dtype=g.dtype, device=g.device),
+                                        ctx.edge_graph.long(), outer).view(-1, 3, 3)
         return gpos, glat, None, None, None, None
 
 
@@ -1072,6 +1072,22 @@ def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor,
     return out
 
 
+def scatter_add_rows(out: torch.Tensor, index: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """out[index[e]] += src[e] (rows of any trailing shape).  On the GPU
+    every row's terms are summed in edge order by ``tace_rows_accumulate``
+    over a CSR of ``index`` (no atomics: the same bits on every run); on the
+    CPU ``index_add_``.  Returns out."""
+    E = src.shape[0]
+    if E == 0:
+        return out
+    if not src.is_cuda or (torch.is_grad_enabled() and src.requires_grad):
+        # CPU, or a sum that must stay differentiable
+        return out.index_add_(0, index, src)
+    n = out.shape[0]
+    rp, slot = sender_csr(index.long(), n)
+    return rows_accumulate(out.view(n, -1), src.reshape(E, -1).contiguous(), rp, slot).view(out.shape)
+
+
 def sender_csr(rows_src: torch.Tensor, n_rows: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """(rowptr int32 [n_rows+1], slot int32 [E]): the edges grouped by sender
     row, in edge order within a sender."""
@@ -1213,7 +1229,7 @@ class _EdgeRotateIn(torch.autograd.Function):
                                                  ctx.needs_input_grad[2])
         gx = None
         if ctx.needs_input_grad[0]:
-            gx = torch.zeros_like(x).index_add_(0, rows_src, gxs).index_add_(0, rows_dst, gxd)
+            gx = scatter_add_rows(scatter_add_rows(torch.zeros_like(x), rows_src, gxs), rows_dst, gxd)
         return gx, gW, gwr, None, None, None
 
 

@@ -501,6 +501,17 @@ def test_tece_fused_forces_repeat_bit_for_bit(cuda):
     assert torch.equal(a["forces"], b["forces"]) and torch.equal(a["energy"], b["energy"])
 
 
+def test_tece_trainable_forces_repeat_bit_for_bit(cuda):
+    """Trainable parameters (the per-operator autograd path): grad_x of the
+    rotate-in operator and the lattice gradient are summed per row in a fixed
+    order, so two evaluations give identical forces and stress."""
+    st = [structures.bcc_fe(reps=(3, 3, 2), seed=10)]
+    kw = dict(seed=2, num_channel=64, num_head=2, frozen=False)
+    a, _ = _model_pair(st, cuda, torch.float32, **kw)
+    b, _ = _model_pair(st, cuda, torch.float32, **kw)
+    assert torch.equal(a["forces"], b["forces"]) and torch.equal(a["energy"], b["energy"])
+
+
 @pytest.mark.parametrize("chunk_edges", [None, 700])
 def test_tece_fused_bf16_mixing_equals_operator_path(cuda, chunk_edges):
     """bf16 channel mixing: the fused operator (bf16 GEMM operands stored by

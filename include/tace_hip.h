@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 21
+#define TACE_HIP_ABI_VERSION 22
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -295,19 +295,21 @@ int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes,
                              double alpha, void* stream);
 /* The same linears' tiles with one contribution of k <= 128 (the input
  * gradients of the product-basis contractions, linear.py:377-482, and any
- * block with no contribution), as n_tasks row tiles of up to 128 rows, each
- * over a column range, with the weights split in MFMA fragment order
- * (tace_bf16x3_split_blocks layout 1):
+ * block with no contribution), as n_tasks row tiles of up to task_rows rows
+ * (the compiled tile height, tace_seg_linear_ks_rows(); any other value is
+ * refused), each over a column range, with the weights split in MFMA fragment
+ * order (tace_bf16x3_split_blocks layout 1):
  *   tasks int64 [n_tasks, 10]: out_base (offset of the tile's row 0, column 0
- *         in y), rows (1..128), n (block width = row stride of y), cb, ce (its
+ *         in y), rows (1..task_rows), n (block width = row stride of y), cb, ce (its
  *         columns [cb, ce), ce <= n), bias_off (-1 none), x_base (offset of
  *         the tile's row 0 in x), k (0..128, the row stride of x; 0: no
  *         contribution), w_off (the block's offset in w_frag), unused.
  * y[tile] = alpha (x[rows, :k] @ B + bias[bias_off + cols]), the same bits as
  * tace_seg_linear_presplit gives for the same tile.  Trusted tables, checked
  * by the host (tace_amd.ops.SegLinearPlan). */
+int32_t tace_seg_linear_ks_rows(void);
 int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
-                                const int64_t* tasks, int64_t n_tasks, double alpha, void* stream);
+                                const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"

@@ -449,14 +449,14 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 // x [128, n] with n up to ~5,400 columns per output block.  A 128 x 128 tile
 // of the kernel above does four 32-k steps after staging A and B through LDS
 // with two barriers per step, then writes its outputs one float per lane.
-// Here a workgroup owns one 128-row tile of one contribution with k <= 128
+// Here a workgroup owns one KS_ROWS-row tile of one contribution with k <= 128
 // and a range of columns:
 //  * A is split once into the three bf16 planes in LDS (k-contiguous rows of
 //    128 + 8 bf16: 272-byte rows, so the 16 rows of a fragment read fall on
 //    distinct banks); one barrier, none after it;
-//  * eight wavefronts in two groups of four take the range's 128-column tiles
-//    alternately; a wavefront owns all 128 rows of 32 columns, so each B
-//    fragment is loaded by one wavefront only;
+//  * KS_GROUPS groups of four wavefronts take the range's 128-column tiles in
+//    turn; a wavefront owns all KS_ROWS rows of 32 columns, so each B fragment
+//    is loaded by one wavefront only;
 //  * B comes from weights pre-split in MFMA fragment order (k_split_blocks,
 //    layout 1): the three terms of one 16-column x 32-k fragment are three
 //    contiguous 1 KB runs in lane order, so a fragment is one fully
@@ -473,12 +473,16 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 // so the two kernels give the same bits.
 //
 // Task table (10 x int64): out_base (element offset of the tile's row 0,
-// column 0 in y), rows (<= 128), n (block width = row stride of y), [cb, ce)
+// column 0 in y), rows (<= KS_ROWS), n (block width = row stride of y), [cb, ce)
 // (the columns, ce <= n), bias_off (-1 none), x_base (element offset of the
 // tile's row 0 in x), k (0..128, the row stride of x; 0 = no contribution:
 // the tile is alpha * bias or zero), w_off (the block's offset in the
 // fragment-order weights), unused.
-constexpr int KS_KMAX = 128, KS_STR = KS_KMAX + 8, KS_PL = 128 * KS_STR;
+// rows per task (16-row MFMA blocks: KS_RB), groups of four wavefronts per
+// workgroup and the column stride between one group's consecutive tiles
+constexpr int KS_ROWS = 128, KS_RB = KS_ROWS / 16;
+constexpr int KS_KMAX = 128, KS_STR = KS_KMAX + 8, KS_PL = KS_ROWS * KS_STR;
+constexpr int KS_GROUPS = 2, KS_THREADS = 256 * KS_GROUPS, KS_CSTEP = 128 * KS_GROUPS;
 
 struct KsTask {
   int64_t out_base, bias_off;
@@ -502,15 +506,15 @@ __device__ __forceinline__ void ks_load_b(const KsTask& T, int c, int ks, int wq
 // (or the next tile's first) load into nxt
 template <int NKS, int KS>
 __device__ __forceinline__ void ks_step(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
-                                        int lane, int fr, int fg, f4 (&acc)[8][2], const u4v (&cur)[3][2],
+                                        int lane, int fr, int fg, f4 (&acc)[KS_RB][2], const u4v (&cur)[3][2],
                                         u4v (&nxt)[3][2]) {
   if (KS + 1 < NKS) ks_load_b(T, c, KS + 1, wq, lane, nxt);
-  else ks_load_b(T, c + 256, 0, wq, lane, nxt);
+  else ks_load_b(T, c + KS_CSTEP, 0, wq, lane, nxt);
   // the loads go out before this step's MFMAs (the scheduler would sink them
   // to the end of the step, where nothing hides their latency)
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int ip = 0; ip < 4; ++ip) {   // row blocks in pairs: four independent accumulators per term
+  for (int ip = 0; ip < KS_RB / 2; ++ip) {   // row blocks in pairs: four independent accumulators per term
     bx3_bf8 af[2][3];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
@@ -533,7 +537,7 @@ __device__ __forceinline__ void ks_step(const unsigned short* __restrict__ As, c
 // steps KS.. of a column tile; step KS reads buffer (KS + PAR) & 1
 template <int NKS, int PAR, int KS>
 __device__ __forceinline__ void ks_steps(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
-                                         int lane, int fr, int fg, f4 (&acc)[8][2], u4v (&b0)[3][2],
+                                         int lane, int fr, int fg, f4 (&acc)[KS_RB][2], u4v (&b0)[3][2],
                                          u4v (&b1)[3][2]) {
   if constexpr (KS < NKS) {
     if constexpr (((KS + PAR) & 1) == 0) ks_step<NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
@@ -558,9 +562,9 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
 #pragma unroll
       for (int q = 0; q < 4; ++q) bv[j][q] = bias[T.bias_off + min(c + 32 * wq + 16 * j + 4 * fg + q, T.ce - 1)];
   }
-  f4 acc[8][2];
+  f4 acc[KS_RB][2];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < KS_RB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
   ks_steps<NKS, PAR, 0>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
@@ -573,7 +577,7 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
   const int jl = lo ? 0 : 1;   // this lane's 16-column half, in both stores
   const int col = c + 32 * wq + 16 * jl + 4 * fg;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < KS_RB; ++i) {
     const f4 v0 = alpha * (acc[i][0] + bv[0]), v1 = alpha * (acc[i][1] + bv[1]);
     const f4 give = lo ? v1 : v0;
     f4 got;
@@ -608,13 +612,14 @@ __device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As
   const bool vst = ((T.n & 3) == 0) && ((T.out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
   u4v b0[3][2], b1[3][2];
   if (NKS > 0) ks_load_b(T, c0, 0, wq, lane, b0);
-  for (; c0 < T.ce; c0 += 512) {
+  for (; c0 < T.ce; c0 += 2 * KS_CSTEP) {
     ks_tile<NKS, 0>(As, T, y, bias, alpha, vst, c0, wq, lane, fr, fg, b0, b1);
-    if (c0 + 256 < T.ce) ks_tile<NKS, NKS & 1>(As, T, y, bias, alpha, vst, c0 + 256, wq, lane, fr, fg, b0, b1);
+    if (c0 + KS_CSTEP < T.ce)
+      ks_tile<NKS, NKS & 1>(As, T, y, bias, alpha, vst, c0 + KS_CSTEP, wq, lane, fr, fg, b0, b1);
   }
 }
 
-__global__ __launch_bounds__(512) void k_seg_linear_ks(const float* __restrict__ x, float* __restrict__ y,
+__global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __restrict__ x, float* __restrict__ y,
                                                        const unsigned short* __restrict__ wfrag,
                                                        const float* __restrict__ bias,
                                                        const int64_t* __restrict__ tasks, float alpha, int n_tasks,
@@ -645,7 +650,7 @@ __global__ __launch_bounds__(512) void k_seg_linear_ks(const float* __restrict__
     const float* __restrict__ xa = x + x_base;
     const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
     const int kq = T.nks * 4;   // 8-k units per row
-    for (int u = t; u < 128 * kq; u += 512) {
+    for (int u = t; u < KS_ROWS * kq; u += KS_THREADS) {
       const int r = u / kq, kk = (u - r * kq) * 8;
       const bool ok = r < T.rows;
       const float* p = xa + (int64_t)r * k + kk;
@@ -740,15 +745,19 @@ extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t
   return tace_check_launch("tace_seg_linear_presplit");
 }
 
+extern "C" int32_t tace_seg_linear_ks_rows(void) { return KS_ROWS; }
+
 extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
-                                           const int64_t* tasks, int64_t n_tasks, double alpha, void* stream) {
+                                           const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha,
+                                           void* stream) {
+  if (task_rows != KS_ROWS) return tace_fail_msg("tace_seg_linear_presplit_ks: tasks must have the compiled row count");
   if (n_tasks < 0 || n_tasks > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_ks: bad task count");
   if (n_tasks == 0) return 0;
   if (!x || !y || !w_frag || !tasks) return tace_fail_msg("tace_seg_linear_presplit_ks: null pointer");
   if ((((uintptr_t)w_frag) & 15) != 0)
     return tace_fail_msg("tace_seg_linear_presplit_ks: the fragment-order weights must be 16-byte aligned");
   const int per = (int)((n_tasks + 7) / 8);
-  hipLaunchKernelGGL(k_seg_linear_ks, dim3((unsigned)(8 * per)), dim3(512), 0, (hipStream_t)stream, x, y,
+  hipLaunchKernelGGL(k_seg_linear_ks, dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream, x, y,
                      (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
   return tace_check_launch("tace_seg_linear_presplit_ks");
 }

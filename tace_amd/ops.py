@@ -1491,6 +1491,7 @@ class SegLinearPlan:
                     raise ValueError("seg linear plan: fragment-order weights of a task out of range")
             self.flops += int(2 * (k_t[:, 1] * (k_t[:, 4] - k_t[:, 3]) * k_t[:, 7]).sum())
         self.n_ks = len(k_t)
+        self.ks_rows = N.lib().tace_seg_linear_ks_rows() if len(k_t) else 0
         self.ks_tasks = torch.from_numpy(np.ascontiguousarray(k_t) if len(k_t) else np.zeros((1, 10), np.int64)).to(device)
 
     def _ks_tasks(self, Z, s_o, n, d, boff, mine, ranges, f_stride, b_stride):
@@ -1498,13 +1499,14 @@ class SegLinearPlan:
         none): column chunk-major, so that the workgroups running at one time
         on an XCD share a chunk's weight columns in its L2."""
         out = []
+        R = N.lib().tace_seg_linear_ks_rows()   # the compiled task height
         for cb in range(0, n, SEG_KS_CHUNK):
             ce = min(n, cb + SEG_KS_CHUNK)
             for (sp, a, b) in ranges:
                 if b <= a:
                     continue
-                for r0 in range(a * d, b * d, 128):
-                    rows = min(b * d - r0, 128)
+                for r0 in range(a * d, b * d, R):
+                    rows = min(b * d - r0, R)
                     bo = -1 if boff is None else boff + (0 if sp is None else sp * b_stride)
                     if mine:
                         s_i, k, f_off = mine[0][1], mine[0][2], mine[0][6]
@@ -1597,7 +1599,8 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, 
         if frag is None or frag.dtype != torch.int16 or frag.numel() < plan.frag_numel:
             raise ValueError("seg linear: the plan's short-k tasks need its fragment-order weights")
         N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
-                                                    plan.ks_tasks.data_ptr(), plan.n_ks, float(alpha), st),
+                                                    plan.ks_tasks.data_ptr(), plan.n_ks, plan.ks_rows, float(alpha),
+                                                    st),
                 "tace_seg_linear_presplit_ks")
     _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
     return y

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 22
+#define TACE_HIP_ABI_VERSION 23
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -460,6 +460,19 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream);
+/* The TECE SO(2) linears under bf16 channel mixing
+ * (oam_2026_07_05.py:138-247, SO2_m0_Linear / SO2_m_Linear per m block, and
+ * their input gradients with the transposed weights):
+ *   out[i, j] = sum_k a[i, k] B[k, j] (+ bias[j])   for i < m, j < n
+ * a bf16 [m, k] with row stride lda (elements, >= k), out float32 [m, n] with
+ * row stride ldo (>= n), bias float32 [n] or NULL; products of bf16 values
+ * summed in float32.  B [k, n] bf16 is passed in MFMA fragment order: per
+ * 16-column block cb < ceil(n / 16) and 32-k step s < ceil(k / 32), the 512
+ * values B[32 s + 8 g + e][16 cb + f] (f < 16, g < 4, e < 8; zeros past k and
+ * n) at b_frag[(cb ceil(k / 32) + s) 512 + (16 g + f) 8 + e], 16-byte
+ * aligned.  0 < k <= 2048. */
+int tace_so2_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b_frag, const float* bias, float* out,
+                       int64_t ldo, int64_t m, int32_t n, int32_t k, void* stream);
 /* Edge pairs of a neighbour list in receiver-CSR form (rowptr, eid as for
  * the tensor products; src [E] senders, shifts [E, 3] int32 periodic shifts,
  * by edge id): the reverse of edge e (i -> j, S) is the edge j -> i with

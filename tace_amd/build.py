@@ -55,7 +55,8 @@ def _compile(src: str, force: bool) -> str:
 
 def build(verbose: bool = True, force: bool = True, jobs: int = 0) -> str:
     t0 = time.time()
-    srcs = [os.path.join(CSRC, n) for n in ("tace_hip.hip", "tece.hip", "mlp.hip", "linear.hip")] + generate()
+    srcs = [os.path.join(CSRC, n) for n in ("tace_hip.hip", "tece.hip", "mlp.hip", "linear.hip", "so2_gemm.hip")] \
+        + generate()
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     jobs = jobs or min(16, os.cpu_count() or 4)

@@ -1051,6 +1051,40 @@ def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: 
     return gxs, gxd, gW, gwr
 
 
+def bf16_fragment_order(B: torch.Tensor) -> torch.Tensor:
+    """B [k, n] bfloat16 -> the MFMA fragment order of ``tace_so2_gemm_bf16``:
+    per 16-column block and 32-k step, 512 values in lane order (lane 16 g + f
+    holds B[32 s + 8 g + e][16 cb + f], e < 8), zeros past k and n."""
+    if B.dim() != 2 or B.dtype != torch.bfloat16:
+        raise ValueError("bf16_fragment_order: B must be a 2-D bfloat16 matrix")
+    k, n = B.shape
+    nks, nb = (k + 31) // 32, (n + 15) // 16
+    P = B.new_zeros(32 * nks, 16 * nb)
+    P[:k, :n] = B
+    return P.view(nks, 4, 8, nb, 16).permute(3, 0, 1, 4, 2).contiguous().view(-1)
+
+
+def so2_gemm_bf16(a: torch.Tensor, b_frag: torch.Tensor, n: int, k: int,
+                  bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``tace_so2_gemm_bf16``: a [m, k] bfloat16 @ B [k, n] (given in fragment
+    order, ``bf16_fragment_order``) with float32 sums (+ bias [n] float32);
+    returns float32 [m, n]."""
+    if not a.is_cuda or a.dim() != 2 or a.dtype != torch.bfloat16 or a.shape[1] != k or a.stride(1) != 1:
+        raise ValueError("so2 gemm: a must be a bfloat16 GPU matrix [m, k] with unit column stride")
+    nks, nb = (k + 31) // 32, (n + 15) // 16
+    if b_frag.dtype != torch.bfloat16 or b_frag.numel() != nks * nb * 512 or not b_frag.is_contiguous():
+        raise ValueError("so2 gemm: the weight is not in the fragment order of a [k, n] matrix")
+    if bias is not None:
+        _req(bias, "bias", torch.float32, (n,))
+    m = a.shape[0]
+    out = torch.empty(m, n, dtype=torch.float32, device=a.device)
+    tok = _t0("so2_gemm_bf16")
+    N.check(N.lib().tace_so2_gemm_bf16(a.data_ptr(), a.stride(0), b_frag.data_ptr(), N.ptr(bias), out.data_ptr(), n,
+                                       m, n, k, N.stream_ptr(a.device)), "tace_so2_gemm_bf16")
+    _t1(tok, (m, n, k))
+    return out
+
+
 def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor, slot: Optional[torch.Tensor] = None,
                     target: Optional[torch.Tensor] = None) -> torch.Tensor:
     """out[target[s]] += sum of rows[slot[k]], k in [rowptr[s], rowptr[s+1])

@@ -338,6 +338,14 @@ def sub_plan(plan: ops.EdgePlan, n0: int, n1: int, e0: int, e1: int) -> ops.Edge
 
 
 # ----------------------------------------------------------- fused operator --
+# bf16 channel mixing: the SO(2) GEMMs with a bias (the m = 0 blocks) on
+# tace_so2_gemm_bf16, bias in the epilogue (False: torch.addmm, which copies
+# the bias into the output and accumulates onto it).  The others stay on the
+# library GEMM: with the whole k of a row tile in LDS, tiles of k > 384 are 32
+# rows or fewer and re-read B too often (measured: k = 1152, n = 768 at 2.7x
+# the library's time, while the three biased shapes gain 7.5 ms per fe101k step)
+SO2_GEMM = True
+
 class _FusedParams:
     """Everything the fused TECE operator needs from the frozen modules,
     prepared once per forward: the SO(2) linears as W^T (forward GEMM
@@ -383,18 +391,33 @@ class _FusedParams:
         self.mlp_W = lins[-1].weight.detach().to(dtype).contiguous()
         self.mlp_alpha = float(lins[-1].alpha)
         self.mlp_WT_scaled = (lins[-1].weight * lins[-1].alpha).detach().to(dtype).t().contiguous()
+        # fragment-order copies of the bf16 GEMM operands (by id of the operand;
+        # each entry keeps its operand alive)
+        self._frag = {}
+
+    def _so2(self, x, B, b=None):
+        """x @ B (+ b) on ``tace_so2_gemm_bf16`` (bf16 operands, float32 sums,
+        bias in the epilogue); B's fragment-order copy is made on first use."""
+        f = self._frag.get(id(B))
+        if f is None:
+            f = self._frag[id(B)] = (ops.bf16_fragment_order(B), B)
+        return ops.so2_gemm_bf16(x, f[0], B.shape[1], B.shape[0], b)
 
     def mm(self, x, WT, b=None):
         """x @ WT (+ b): bf16 operands with float32 accumulation and output
         under bf16 mixing, else in the features' precision."""
         if self.bf16:
+            if SO2_GEMM and b is not None and x.dtype == torch.bfloat16:
+                return self._so2(x, WT, b)
             if b is None:
                 return torch.mm(x, WT, out_dtype=torch.float32)
             return torch.addmm(b, x, WT, out_dtype=torch.float32)
         return torch.mm(x, WT) if b is None else torch.addmm(b, x, WT)
 
     def mm_grad(self, g, WN):
-        return torch.mm(g, WN, out_dtype=torch.float32) if self.bf16 else torch.mm(g, WN)
+        if self.bf16:
+            return torch.mm(g, WN, out_dtype=torch.float32)
+        return torch.mm(g, WN)
 
 
 def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, save: bool,

@@ -667,3 +667,26 @@ def test_rows_accumulate_matches_index_add(cuda, dtype, width):
     got2 = ops.rows_accumulate(base.to(dtype).to(cuda), rows2.to(dtype).to(cuda), rowptr.to(torch.int32).to(cuda),
                                None, target.to(torch.int32).to(cuda))
     close(got2, want2, dtype, "receiver segments")
+
+
+# ------------------------------------------- TECE SO(2) GEMM under bf16 mixing ----
+@pytest.mark.parametrize("m,k,n,bias,pad", [(5000, 96, 384, True, 0), (3000, 384, 384, True, 0),
+                                            (2500, 768, 1152, True, 0), (2100, 1152, 768, False, 0),
+                                            (4099, 256, 256, False, 0), (777, 100, 70, True, 0),
+                                            (1500, 128, 96, False, 24), (33, 512, 192, False, 8)])
+def test_so2_gemm_bf16_matches_float32_product(cuda, m, k, n, bias, pad):
+    """``tace_so2_gemm_bf16`` against the float32 product of the same bf16
+    values (exact products, so only the order of the float32 sums differs):
+    the SO(2) linear shapes of the TECE layer, k and n tails, rows past the
+    last full tile, a row stride above k."""
+    from tace_amd import ops
+    g = torch.Generator().manual_seed(k + n)
+    a_full = torch.randn(m, k + pad, generator=g).to(torch.bfloat16).to(cuda)
+    a = a_full[:, :k]
+    B = torch.randn(k, n, generator=g).to(torch.bfloat16).to(cuda)
+    b = torch.randn(n, generator=g).to(cuda) if bias else None
+    got = ops.so2_gemm_bf16(a, ops.bf16_fragment_order(B), n, k, b)
+    want = a.float() @ B.float() + (b if bias else 0.0)
+    scale = (a.float().abs() @ B.float().abs()).amax(1, keepdim=True) + 1e-30
+    err = ((got - want).abs() / scale).max().item()
+    assert got.shape == (m, n) and err < 2e-6, err

@@ -118,3 +118,24 @@ def test_kernel_parts_partition_the_paths():
                 for bs in parts:
                     assert len(bs) == 1 or sum(v.d1[b] for b in bs) <= 40, (v.name, bs)
             assert reg.count(f"L_{v.name}_bwd_d, 0, nullptr, nullptr, {len(parts)}}}") == 1, v.name
+
+
+def test_bf16_fragment_order_layout():
+    """``ops.bf16_fragment_order``: element (k, n) of B lands at the lane and
+    slot of the MFMA B operand the header states (per 16-column block cb and
+    32-k step s: offset (cb nks + s) 512 + (16 g + f) 8 + e for k = 32 s + 8 g
+    + e, n = 16 cb + f), zeros past k and n."""
+    import torch
+    from tace_amd import ops
+    k, n = 70, 37
+    B = (torch.arange(k * n, dtype=torch.float32).view(k, n) % 251 + 1).to(torch.bfloat16)
+    f = ops.bf16_fragment_order(B)
+    nks, nb = 3, 3
+    assert f.numel() == nks * nb * 512
+    for kk in range(32 * nks):
+        for nn in range(16 * nb):
+            s, g, e = kk // 32, (kk % 32) // 8, kk % 8
+            cb, fl = nn // 16, nn % 16
+            v = f[(cb * nks + s) * 512 + (16 * g + fl) * 8 + e]
+            want = B[kk, nn] if kk < k and nn < n else torch.tensor(0, dtype=torch.bfloat16)
+            assert v == want, (kk, nn)

@@ -10,8 +10,8 @@
 // chunk, K and N = 96..1152.  A library GEMM tiles them like square GEMMs and
 // adds a bias by first copying it into the output and then accumulating with
 // beta = 1.  Here:
-//  * a workgroup of four wavefronts owns RT = 16 RB rows of A (RT = 128, 64, 32
-//    or 16 by K, so that the A tile stays under 64 KB of LDS): the rows are
+//  * a workgroup of eight wavefronts owns RT = 16 RB rows of A (RT = 128, 64
+//    or 32 by K; the A tile takes up to ~132 KB of LDS): the rows are
 //    copied once into LDS (k-contiguous rows of ceil32(K) + 8 bf16, so the 16
 //    rows of a fragment read fall on distinct banks) behind one barrier;
 //  * the wavefronts take the output's 32-column strips in turn, each strip all
@@ -36,7 +36,7 @@ typedef float gf4 __attribute__((ext_vector_type(4)));
 typedef unsigned gu4 __attribute__((ext_vector_type(4)));
 typedef __bf16 gbf8 __attribute__((ext_vector_type(8)));
 
-constexpr int G_THREADS = 256;
+constexpr int G_THREADS = 512, G_WAVES = G_THREADS / 64, G_SSTEP = 32 * G_WAVES;
 
 struct GJob {
   const unsigned short* a;    // A tile row 0
@@ -185,16 +185,16 @@ __global__ __launch_bounds__(G_THREADS) void k_so2_gemm_bf16(const unsigned shor
   __syncthreads();
 
   const bool vst = ((ldo & 3) == 0) && ((((uintptr_t)J.out) & 15) == 0);
-  // 32-column strips c = 32 (wv + 4 s)
+  // 32-column strips c = 32 (wv + G_WAVES s)
   int c = 32 * wv;
   if (c >= N) return;
   gu4 b0[2], b1[2];
   g_load_b(J, c, 0, lane, b0);
-  for (; c < N; c += 256) {
-    g_strip<RB, 0>(As, J, c, c + 128, vst, lane, fr, fg, b0, b1);
-    if (c + 128 < N) {
-      if (J.nks & 1) g_strip<RB, 1>(As, J, c + 128, c + 256, vst, lane, fr, fg, b0, b1);
-      else g_strip<RB, 0>(As, J, c + 128, c + 256, vst, lane, fr, fg, b0, b1);
+  for (; c < N; c += 2 * G_SSTEP) {
+    g_strip<RB, 0>(As, J, c, c + G_SSTEP, vst, lane, fr, fg, b0, b1);
+    if (c + G_SSTEP < N) {
+      if (J.nks & 1) g_strip<RB, 1>(As, J, c + G_SSTEP, c + 2 * G_SSTEP, vst, lane, fr, fg, b0, b1);
+      else g_strip<RB, 0>(As, J, c + G_SSTEP, c + 2 * G_SSTEP, vst, lane, fr, fg, b0, b1);
     }
   }
 }
@@ -216,15 +216,18 @@ extern "C" int tace_so2_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t
     const int64_t tiles = (m + 16 * (RB) - 1) / (16 * (RB));                                                          \
     if (tiles > 0x7fffffff) return tace_fail_msg("tace_so2_gemm_bf16: too many rows");                              \
     const size_t lds = (size_t)16 * (RB) * (32 * nks + 8) * 2;                                                        \
+    if (lds > 65536 &&                                                                                               \
+        hipFuncSetAttribute((const void*)k_so2_gemm_bf16<RB>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds)   \
+            != hipSuccess)                                                                                           \
+      return tace_fail_msg("tace_so2_gemm_bf16: cannot reserve the LDS tile");                                       \
     hipLaunchKernelGGL(k_so2_gemm_bf16<RB>, dim3((unsigned)tiles), dim3(G_THREADS), lds, s,                         \
                        (const unsigned short*)a, lda, (const unsigned short*)b_frag, bias, out, ldo, m, (int)n,     \
                        (int)k);                                                                                      \
   } while (0)
-  // rows per workgroup by k: the A tile stays under 64 KB of LDS
-  if (k <= 184) SO2_G(8);
-  else if (k <= 376) SO2_G(4);
-  else if (k <= 984) SO2_G(2);
-  else SO2_G(1);
+  // rows per workgroup by k: the A tile takes at most ~132 KB of LDS
+  if (k <= 376) SO2_G(8);
+  else if (k <= 1016) SO2_G(4);
+  else SO2_G(2);
 #undef SO2_G
   return tace_check_launch("tace_so2_gemm_bf16");
 }

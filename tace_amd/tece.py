@@ -338,13 +338,21 @@ def sub_plan(plan: ops.EdgePlan, n0: int, n1: int, e0: int, e1: int) -> ops.Edge
 
 
 # ----------------------------------------------------------- fused operator --
-# bf16 channel mixing: the SO(2) GEMMs with a bias (the m = 0 blocks) on
-# tace_so2_gemm_bf16, bias in the epilogue (False: torch.addmm, which copies
-# the bias into the output and accumulates onto it).  The others stay on the
-# library GEMM: with the whole k of a row tile in LDS, tiles of k > 384 are 32
-# rows or fewer and re-read B too often (measured: k = 1152, n = 768 at 2.7x
-# the library's time, while the three biased shapes gain 7.5 ms per fe101k step)
+# bf16 channel mixing: SO(2) GEMMs on tace_so2_gemm_bf16 (bias in the
+# epilogue) where it measured faster than the library GEMM on fe101k
+# (_so2_route); False: torch.mm / addmm (addmm copies the bias into the output
+# and accumulates onto it)
 SO2_GEMM = True
+SO2_GEMM_ALL = False
+
+
+def _so2_route(k: int, n: int, bias: bool) -> bool:
+    """The shapes [rows, k] x [k, n] that tace_so2_gemm_bf16 runs faster
+    than the library (fe101k, per step): every biased one (k 768 -> 1152:
+    21.3 -> 16.5 ms, 384 -> 384: 12.7 -> 7.5, 96 -> 384: 5.1 -> 2.1), k <= 128
+    (0.2-0.5 ms each) and 192 -> 512 (6.7 -> 6.1).  The library keeps 256 ->
+    256 (8.6 vs 9.6), 512 -> 192, 1152 -> 768 (10.6 vs 16.6) and the rest."""
+    return SO2_GEMM_ALL or bias or k <= 128 or (k <= 192 and n >= 512)
 
 class _FusedParams:
     """Everything the fused TECE operator needs from the frozen modules,
@@ -407,7 +415,7 @@ class _FusedParams:
         """x @ WT (+ b): bf16 operands with float32 accumulation and output
         under bf16 mixing, else in the features' precision."""
         if self.bf16:
-            if SO2_GEMM and b is not None and x.dtype == torch.bfloat16:
+            if SO2_GEMM and x.dtype == torch.bfloat16 and _so2_route(WT.shape[0], WT.shape[1], b is not None):
                 return self._so2(x, WT, b)
             if b is None:
                 return torch.mm(x, WT, out_dtype=torch.float32)
@@ -416,6 +424,8 @@ class _FusedParams:
 
     def mm_grad(self, g, WN):
         if self.bf16:
+            if SO2_GEMM and g.dtype == torch.bfloat16 and _so2_route(WN.shape[0], WN.shape[1], False):
+                return self._so2(g, WN)
             return torch.mm(g, WN, out_dtype=torch.float32)
         return torch.mm(g, WN)
 

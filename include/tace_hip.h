@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 23
+#define TACE_HIP_ABI_VERSION 24
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -293,21 +293,22 @@ int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, const double
 int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
                              const float* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                              double alpha, void* stream);
-/* The same linears' tiles with one contribution of k <= 128 (the input
+/* The same linears' tiles with one contribution of k <= 256 (the input
  * gradients of the product-basis contractions, linear.py:377-482, and any
- * block with no contribution), as n_tasks row tiles of up to task_rows rows
- * (the compiled tile height, tace_seg_linear_ks_rows(); any other value is
- * refused), each over a column range, with the weights split in MFMA fragment
- * order (tace_bf16x3_split_blocks layout 1):
+ * block with no contribution), as n_tasks row tiles of up to task_rows rows,
+ * each over a column range, with the weights split in MFMA fragment order
+ * (tace_bf16x3_split_blocks layout 1).  task_rows is 128 (every task's k <=
+ * 128) or 64 (k <= 256): tace_seg_linear_ks_rows(k) gives the height for k
+ * (0: not supported); one call takes tasks of one height:
  *   tasks int64 [n_tasks, 10]: out_base (offset of the tile's row 0, column 0
  *         in y), rows (1..task_rows), n (block width = row stride of y), cb, ce (its
  *         columns [cb, ce), ce <= n), bias_off (-1 none), x_base (offset of
- *         the tile's row 0 in x), k (0..128, the row stride of x; 0: no
+ *         the tile's row 0 in x), k (0..256, the row stride of x; 0: no
  *         contribution), w_off (the block's offset in w_frag), unused.
  * y[tile] = alpha (x[rows, :k] @ B + bias[bias_off + cols]), the same bits as
  * tace_seg_linear_presplit gives for the same tile.  Trusted tables, checked
  * by the host (tace_amd.ops.SegLinearPlan). */
-int32_t tace_seg_linear_ks_rows(void);
+int32_t tace_seg_linear_ks_rows(int32_t k);
 int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
                                 const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha, void* stream);
 

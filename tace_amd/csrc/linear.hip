@@ -449,13 +449,13 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 // x [128, n] with n up to ~5,400 columns per output block.  A 128 x 128 tile
 // of the kernel above does four 32-k steps after staging A and B through LDS
 // with two barriers per step, then writes its outputs one float per lane.
-// Here a workgroup owns one KS_ROWS-row tile of one contribution with k <= 128
-// and a range of columns:
+// Here a workgroup owns one R-row tile of one contribution with k <= KM (R =
+// 128 for k <= 128, R = 64 for k <= 256) and a range of columns:
 //  * A is split once into the three bf16 planes in LDS (k-contiguous rows of
 //    128 + 8 bf16: 272-byte rows, so the 16 rows of a fragment read fall on
 //    distinct banks); one barrier, none after it;
 //  * KS_GROUPS groups of four wavefronts take the range's 128-column tiles in
-//    turn; a wavefront owns all KS_ROWS rows of 32 columns, so each B fragment
+//    turn; a wavefront owns all R rows of 32 columns, so each B fragment
 //    is loaded by one wavefront only;
 //  * B comes from weights pre-split in MFMA fragment order (k_split_blocks,
 //    layout 1): the three terms of one 16-column x 32-k fragment are three
@@ -467,22 +467,26 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 //  * the MFMA runs with the operands swapped (B fragments as the row operand),
 //    so a lane holds 4 consecutive columns of one output row: one 16-byte
 //    store per 16 x 16 block.
-// The number of 32-k steps is a template parameter (1..4).  Per output element
+// The number of 32-k steps is a template parameter (1..KM / 32).  Per output element
 // the products and their order are those of k_seg_linear_bx3s (k steps in
 // order, the six terms smallest first, each a sum over the same 32 products),
 // so the two kernels give the same bits.
 //
 // Task table (10 x int64): out_base (element offset of the tile's row 0,
-// column 0 in y), rows (<= KS_ROWS), n (block width = row stride of y), [cb, ce)
+// column 0 in y), rows (<= R), n (block width = row stride of y), [cb, ce)
 // (the columns, ce <= n), bias_off (-1 none), x_base (element offset of the
-// tile's row 0 in x), k (0..128, the row stride of x; 0 = no contribution:
+// tile's row 0 in x), k (0..KM, the row stride of x; 0 = no contribution:
 // the tile is alpha * bias or zero), w_off (the block's offset in the
 // fragment-order weights), unused.
-// rows per task (16-row MFMA blocks: KS_RB), groups of four wavefronts per
-// workgroup and the column stride between one group's consecutive tiles
-constexpr int KS_ROWS = 128, KS_RB = KS_ROWS / 16;
-constexpr int KS_KMAX = 128, KS_STR = KS_KMAX + 8, KS_PL = KS_ROWS * KS_STR;
+// Two instantiations: R = 128 rows per task for k <= 128, R = 64 for k <= 256
+// (the A planes take 3 R (KM + 8) bf16 of LDS, ~100 KB either way).  Groups of
+// four wavefronts per workgroup and the column stride between one group's
+// consecutive tiles:
 constexpr int KS_GROUPS = 2, KS_THREADS = 256 * KS_GROUPS, KS_CSTEP = 128 * KS_GROUPS;
+template <int R, int KM>
+struct KsShape {
+  static constexpr int RB = R / 16, STR = KM + 8, PL = R * STR;
+};
 
 struct KsTask {
   int64_t out_base, bias_off;
@@ -504,23 +508,24 @@ __device__ __forceinline__ void ks_load_b(const KsTask& T, int c, int ks, int wq
 
 // step KS of a column tile: MFMAs on cur while the next step's fragments
 // (or the next tile's first) load into nxt
-template <int NKS, int KS>
+template <int R, int KM, int NKS, int KS>
 __device__ __forceinline__ void ks_step(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
-                                        int lane, int fr, int fg, f4 (&acc)[KS_RB][2], const u4v (&cur)[3][2],
+                                        int lane, int fr, int fg, f4 (&acc)[R / 16][2], const u4v (&cur)[3][2],
                                         u4v (&nxt)[3][2]) {
   if (KS + 1 < NKS) ks_load_b(T, c, KS + 1, wq, lane, nxt);
   else ks_load_b(T, c + KS_CSTEP, 0, wq, lane, nxt);
   // the loads go out before this step's MFMAs (the scheduler would sink them
   // to the end of the step, where nothing hides their latency)
   __builtin_amdgcn_sched_barrier(0);
+  typedef KsShape<R, KM> S;
 #pragma unroll
-  for (int ip = 0; ip < KS_RB / 2; ++ip) {   // row blocks in pairs: four independent accumulators per term
+  for (int ip = 0; ip < S::RB / 2; ++ip) {   // row blocks in pairs: four independent accumulators per term
     bx3_bf8 af[2][3];
 #pragma unroll
     for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
       for (int pl = 0; pl < 3; ++pl)
-        af[ii][pl] = *(const bx3_bf8*)&As[pl * KS_PL + (32 * ip + 16 * ii + fr) * KS_STR + 32 * KS + 8 * fg];
+        af[ii][pl] = *(const bx3_bf8*)&As[pl * S::PL + (32 * ip + 16 * ii + fr) * S::STR + 32 * KS + 8 * fg];
 #pragma unroll
     for (int u = 0; u < 6; ++u)   // the six terms a_i b_j, smallest first
 #pragma unroll
@@ -535,19 +540,19 @@ __device__ __forceinline__ void ks_step(const unsigned short* __restrict__ As, c
 }
 
 // steps KS.. of a column tile; step KS reads buffer (KS + PAR) & 1
-template <int NKS, int PAR, int KS>
+template <int R, int KM, int NKS, int PAR, int KS>
 __device__ __forceinline__ void ks_steps(const unsigned short* __restrict__ As, const KsTask& T, int c, int wq,
-                                         int lane, int fr, int fg, f4 (&acc)[KS_RB][2], u4v (&b0)[3][2],
+                                         int lane, int fr, int fg, f4 (&acc)[R / 16][2], u4v (&b0)[3][2],
                                          u4v (&b1)[3][2]) {
   if constexpr (KS < NKS) {
-    if constexpr (((KS + PAR) & 1) == 0) ks_step<NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
-    else ks_step<NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b1, b0);
-    ks_steps<NKS, PAR, KS + 1>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+    if constexpr (((KS + PAR) & 1) == 0) ks_step<R, KM, NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+    else ks_step<R, KM, NKS, KS>(As, T, c, wq, lane, fr, fg, acc, b1, b0);
+    ks_steps<R, KM, NKS, PAR, KS + 1>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
   }
 }
 
 // this wavefront's 128 x 32 part of column tile c
-template <int NKS, int PAR>
+template <int R, int KM, int NKS, int PAR>
 __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, const KsTask& T, float* __restrict__ y,
                                         const float* __restrict__ bias, float alpha, bool vst, int c, int wq,
                                         int lane, int fr, int fg, u4v (&b0)[3][2], u4v (&b1)[3][2]) {
@@ -562,12 +567,13 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
 #pragma unroll
       for (int q = 0; q < 4; ++q) bv[j][q] = bias[T.bias_off + min(c + 32 * wq + 16 * j + 4 * fg + q, T.ce - 1)];
   }
-  f4 acc[KS_RB][2];
+  constexpr int RB = R / 16;
+  f4 acc[RB][2];
 #pragma unroll
-  for (int i = 0; i < KS_RB; ++i)
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
-  ks_steps<NKS, PAR, 0>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
+  ks_steps<R, KM, NKS, PAR, 0>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
   // acc[i][j][q] = out[row 16 i + fr][column c + 32 wq + 16 j + 4 fg + q].
   // Lanes fr and fr ^ 8 trade one block, so that a store writes 8 whole rows
   // of the 32 columns (128 contiguous bytes each) instead of 16 half rows:
@@ -577,7 +583,7 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
   const int jl = lo ? 0 : 1;   // this lane's 16-column half, in both stores
   const int col = c + 32 * wq + 16 * jl + 4 * fg;
 #pragma unroll
-  for (int i = 0; i < KS_RB; ++i) {
+  for (int i = 0; i < RB; ++i) {
     const f4 v0 = alpha * (acc[i][0] + bv[0]), v1 = alpha * (acc[i][1] + bv[1]);
     const f4 give = lo ? v1 : v0;
     f4 got;
@@ -601,7 +607,7 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
   }
 }
 
-template <int NKS>
+template <int R, int KM, int NKS>
 __device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As, const KsTask& T,
                                            float* __restrict__ y, const float* __restrict__ bias, float alpha, int grp,
                                            int wq, int lane, int fr, int fg) {
@@ -613,18 +619,20 @@ __device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As
   u4v b0[3][2], b1[3][2];
   if (NKS > 0) ks_load_b(T, c0, 0, wq, lane, b0);
   for (; c0 < T.ce; c0 += 2 * KS_CSTEP) {
-    ks_tile<NKS, 0>(As, T, y, bias, alpha, vst, c0, wq, lane, fr, fg, b0, b1);
+    ks_tile<R, KM, NKS, 0>(As, T, y, bias, alpha, vst, c0, wq, lane, fr, fg, b0, b1);
     if (c0 + KS_CSTEP < T.ce)
-      ks_tile<NKS, NKS & 1>(As, T, y, bias, alpha, vst, c0 + KS_CSTEP, wq, lane, fr, fg, b0, b1);
+      ks_tile<R, KM, NKS, NKS & 1>(As, T, y, bias, alpha, vst, c0 + KS_CSTEP, wq, lane, fr, fg, b0, b1);
   }
 }
 
+template <int R, int KM>
 __global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __restrict__ x, float* __restrict__ y,
                                                        const unsigned short* __restrict__ wfrag,
                                                        const float* __restrict__ bias,
                                                        const int64_t* __restrict__ tasks, float alpha, int n_tasks,
                                                        int per) {
-  __shared__ __attribute__((aligned(16))) unsigned short As[3 * KS_PL];
+  typedef KsShape<R, KM> S;
+  __shared__ __attribute__((aligned(16))) unsigned short As[3 * S::PL];
   const int task = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
   if (task >= n_tasks) return;
   const int64_t* td = tasks + 10 * (int64_t)task;
@@ -650,7 +658,7 @@ __global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __res
     const float* __restrict__ xa = x + x_base;
     const bool xvec = ((((uintptr_t)xa) & 15) == 0) && ((k & 3) == 0);
     const int kq = T.nks * 4;   // 8-k units per row
-    for (int u = t; u < KS_ROWS * kq; u += KS_THREADS) {
+    for (int u = t; u < R * kq; u += KS_THREADS) {
       const int r = u / kq, kk = (u - r * kq) * 8;
       const bool ok = r < T.rows;
       const float* p = xa + (int64_t)r * k + kk;
@@ -660,18 +668,24 @@ __global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __res
       bx3_bf8 tt[3];
       bx3_split8(v, tt);
 #pragma unroll
-      for (int pl = 0; pl < 3; ++pl) *(bx3_bf8*)&As[pl * KS_PL + r * KS_STR + kk] = tt[pl];
+      for (int pl = 0; pl < 3; ++pl) *(bx3_bf8*)&As[pl * S::PL + r * S::STR + kk] = tt[pl];
     }
   }
   __syncthreads();
 
+#define KS_C(n) ks_columns<R, KM, (n) <= KM / 32 ? (n) : 0>(As, T, y, bias, alpha, grp, wq, lane, fr, fg)
   switch (T.nks) {
-    case 1: ks_columns<1>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
-    case 2: ks_columns<2>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
-    case 3: ks_columns<3>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
-    case 4: ks_columns<4>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;
-    default: ks_columns<0>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;   // k = 0: bias or zeros
+    case 1: KS_C(1); break;
+    case 2: KS_C(2); break;
+    case 3: KS_C(3); break;
+    case 4: KS_C(4); break;
+    case 5: KS_C(5); break;
+    case 6: KS_C(6); break;
+    case 7: KS_C(7); break;
+    case 8: KS_C(8); break;
+    default: ks_columns<R, KM, 0>(As, T, y, bias, alpha, grp, wq, lane, fr, fg); break;   // k = 0: bias or zeros
   }
+#undef KS_C
 }
 
 // Per block (6 x int64): src_off, cols, k, transpose, dst_off, layout; one
@@ -745,20 +759,25 @@ extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t
   return tace_check_launch("tace_seg_linear_presplit");
 }
 
-extern "C" int32_t tace_seg_linear_ks_rows(void) { return KS_ROWS; }
+extern "C" int32_t tace_seg_linear_ks_rows(int32_t k) { return k < 0 ? 0 : k <= 128 ? 128 : k <= 256 ? 64 : 0; }
 
 extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
                                            const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha,
                                            void* stream) {
-  if (task_rows != KS_ROWS) return tace_fail_msg("tace_seg_linear_presplit_ks: tasks must have the compiled row count");
+  if (task_rows != 128 && task_rows != 64)
+    return tace_fail_msg("tace_seg_linear_presplit_ks: tasks of 128 rows (k <= 128) or 64 rows (k <= 256)");
   if (n_tasks < 0 || n_tasks > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_ks: bad task count");
   if (n_tasks == 0) return 0;
   if (!x || !y || !w_frag || !tasks) return tace_fail_msg("tace_seg_linear_presplit_ks: null pointer");
   if ((((uintptr_t)w_frag) & 15) != 0)
     return tace_fail_msg("tace_seg_linear_presplit_ks: the fragment-order weights must be 16-byte aligned");
   const int per = (int)((n_tasks + 7) / 8);
-  hipLaunchKernelGGL(k_seg_linear_ks, dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream, x, y,
-                     (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
+  if (task_rows == 128)
+    hipLaunchKernelGGL((k_seg_linear_ks<128, 128>), dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream,
+                       x, y, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
+  else
+    hipLaunchKernelGGL((k_seg_linear_ks<64, 256>), dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream,
+                       x, y, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
   return tace_check_launch("tace_seg_linear_presplit_ks");
 }
 

@@ -234,7 +234,7 @@ class _LinearLayout:
         # direction ("fwd": B = W, "bwd": B = W^T)
         self.split_blocks = {}
         # the same in MFMA fragment order (layout 1) for the instructions with
-        # k <= 128 (tace_seg_linear_presplit_ks); offset -1 for the others
+        # k <= 256 (tace_seg_linear_presplit_ks); offset -1 for the others
         self.frag_blocks = {}
         for kind in ("fwd", "bwd"):
             blocks, acc, fblocks, facc = [], 0, [], 0
@@ -242,7 +242,7 @@ class _LinearLayout:
                 cols, k = (mo, mi) if kind == "fwd" else (mi, mo)
                 blocks.append((acc, cols, k))
                 acc += cols * ((k + 7) // 8 * 8)
-                if k <= 128:
+                if k <= 256:
                     fblocks.append((facc, cols, k))
                     facc += 3 * ((cols + 15) // 16 * 16) * ((k + 31) // 32 * 32)
                 else:
@@ -255,7 +255,7 @@ class _LinearLayout:
         with its path weight folded in, in the column layout of
         ``tace_seg_linear_presplit`` ("fwd": B = W, "bwd": B = W^T); returns
         (planes int16 [3 * stride], plane stride).  ``frag``: the blocks with
-        k <= 128 in the MFMA fragment order of ``tace_seg_linear_presplit_ks``
+        k <= 256 in the MFMA fragment order of ``tace_seg_linear_presplit_ks``
         instead (one buffer; the stride is its size).  Cached until the weight
         changes (its version counter or storage)."""
         w = weight.detach()

@@ -1401,7 +1401,7 @@ def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> tor
 
 # ------------------------------------------------------ per-species linears ----
 # output blocks of at least this many columns whose tiles have one
-# contribution with k <= 128 (or none) go to tace_seg_linear_presplit_ks
+# contribution with k <= 256 (or none) go to tace_seg_linear_presplit_ks
 # (pre-split plans only; None: every tile to the tile kernel)
 SEG_KS_MIN_N = 256
 # columns per tace_seg_linear_presplit_ks task
@@ -1443,7 +1443,7 @@ class SegLinearPlan:
         for ob, (s_o, n, d, boff) in enumerate(out_blocks):
             mine = [c for c in ins if c[0] == ob]
             if (self.split_weights and frag is not None and SEG_KS_MIN_N is not None and n >= SEG_KS_MIN_N
-                    and len(mine) <= 1 and all(c[2] <= 128 and c[6] >= 0 for c in mine)):
+                    and len(mine) <= 1 and all(c[2] <= 256 and c[6] >= 0 for c in mine)):
                 tasks += self._ks_tasks(Z, s_o, n, d, boff, mine, ranges, frag[0], b_stride)
                 continue
             c0s = np.arange(0, n, TN, dtype=np.int64)
@@ -1525,15 +1525,33 @@ class SegLinearPlan:
                     raise ValueError("seg linear plan: fragment-order weights of a task out of range")
             self.flops += int(2 * (k_t[:, 1] * (k_t[:, 4] - k_t[:, 3]) * k_t[:, 7]).sum())
         self.n_ks = len(k_t)
-        self.ks_rows = N.lib().tace_seg_linear_ks_rows() if len(k_t) else 0
-        self.ks_tasks = torch.from_numpy(np.ascontiguousarray(k_t) if len(k_t) else np.zeros((1, 10), np.int64)).to(device)
+        # one launch per task height (128 rows: k <= 128, 64 rows: k <= 256)
+        self.ks_groups = []
+        if len(k_t):
+            by_k = {int(k): self._ks_rows(int(k)) for k in np.unique(k_t[:, 7])}
+            hts = np.array([by_k[int(k)] for k in k_t[:, 7]], dtype=np.int64)
+            for R in (128, 64):
+                sel = k_t[hts == R]
+                if len(sel):
+                    if (sel[:, 1] > R).any():
+                        raise ValueError("seg linear plan: a task is taller than its kernel's tile")
+                    self.ks_groups.append((R, len(sel), torch.from_numpy(np.ascontiguousarray(sel)).to(device)))
+
+    @staticmethod
+    def _ks_rows(k: int) -> int:
+        """Task height of ``tace_seg_linear_presplit_ks`` for contributions of
+        width k (k = 0: a block without contribution, 128 rows)."""
+        R = N.lib().tace_seg_linear_ks_rows(int(k))
+        if R <= 0:
+            raise ValueError(f"seg linear plan: no short-k task kernel for k = {k}")
+        return R
 
     def _ks_tasks(self, Z, s_o, n, d, boff, mine, ranges, f_stride, b_stride):
         """Tasks of one output block (one contribution with k <= 128, or
         none): column chunk-major, so that the workgroups running at one time
         on an XCD share a chunk's weight columns in its L2."""
         out = []
-        R = N.lib().tace_seg_linear_ks_rows()   # the compiled task height
+        R = self._ks_rows(mine[0][2] if mine else 0)   # the task height for this k
         for cb in range(0, n, SEG_KS_CHUNK):
             ce = min(n, cb + SEG_KS_CHUNK)
             for (sp, a, b) in ranges:
@@ -1632,10 +1650,10 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, 
     if plan.n_ks:
         if frag is None or frag.dtype != torch.int16 or frag.numel() < plan.frag_numel:
             raise ValueError("seg linear: the plan's short-k tasks need its fragment-order weights")
-        N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
-                                                    plan.ks_tasks.data_ptr(), plan.n_ks, plan.ks_rows, float(alpha),
-                                                    st),
-                "tace_seg_linear_presplit_ks")
+        for R, n_t, tasks in plan.ks_groups:
+            N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
+                                                        tasks.data_ptr(), n_t, R, float(alpha), st),
+                    "tace_seg_linear_presplit_ks")
     _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))
     return y
 

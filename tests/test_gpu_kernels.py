@@ -476,7 +476,9 @@ SEG_CASES = [("8x0e+5x0e+6x1o+4x1o+3x2e", "70x0e+6x1o+65x2e+2x3o", [0, 1, 17, 64
              # no instruction writes), and back (k 100 and 64 into 1100 and
              # 300 columns)
              ("128x0e+100x1o+20x2e+8x3o", "300x0e+1100x1o+260x2e+40x3o+513x3e", [0, 300, 7, 129, 1]),
-             ("1100x0e+300x1o", "100x0e+64x1o", [130, 0, 5, 256])]
+             ("1100x0e+300x1o", "100x0e+64x1o", [130, 0, 5, 256]),
+             # the 64-row task kernel: k 200 and 256 into 300 and 700 columns
+             ("200x0e+256x1o", "300x0e+700x1o", [70, 0, 3, 140])]
 
 
 @pytest.mark.parametrize("dtype,tile,presplit", [(torch.float64, 64, False), (torch.float32, 128, True),

@@ -2,7 +2,8 @@
 // (tace/models/_e3nn/archive/oam_2026_07_05.py:547-823):
 //   * edge-frame Wigner matrices in the SO(2) "m layout" from the edge vector
 //     (tace/models/o2/rotation_matrix.py:74-88, tace/models/o2/wigner.py:231-357),
-//     forward and the exact backward to the edge vector (dual numbers);
+//     forward and the exact backward to the edge vector (reverse mode through
+//     the D^l recursion, dual numbers for the frame);
 //   * the radial-rotary complex QK score (oam_2026_07_05.py:699-754);
 //   * the graph softmax over each receiver's in-edges (tace/models/softmax.py:100-112),
 //     walked along the receiver CSR (no atomics);
@@ -220,18 +221,78 @@ __device__ void wigner_m(const S& vx, const S& vy, const S& vz, S* W) {
   }
 }
 
+// Adjoint of wig_next: given gD = dE/dD, accumulate dE/dR into gR and dE/dP
+// into gP (U is linear in R and in P, D linear in U); one row m of U at a time.
 template <typename T, int L>
-__global__ __launch_bounds__(64) void k_wigner_fwd(const T* __restrict__ vec, int64_t E, T* __restrict__ W) {
-  constexpr int K = (L + 1) * (L + 1);
-  const int64_t e = (int64_t)blockIdx.x * 64 + threadIdx.x;
-  if (e >= E) return;
-  T w[K * K];
-  wigner_m<T, T, L>(vec[3 * e], vec[3 * e + 1], vec[3 * e + 2], w);
-  T* o = W + e * K * K;
+__device__ void wig_next_adj(const T* R, const T* P, const T* gD, T* gR, T* gP) {
+  constexpr int dp = 2 * L - 1, dn = 2 * L + 1;
+  const double* cg = WigCG<L>::v;
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) o[i] = w[i];
+  for (int m = 0; m < dn; ++m) {
+    T gU[3][dp];
+#pragma unroll
+    for (int c = 0; c < 3; ++c)
+#pragma unroll
+      for (int d = 0; d < dp; ++d) {
+        T acc = T(0);
+#pragma unroll
+        for (int n = 0; n < dn; ++n) {
+          const double k = cg[(c * dp + d) * dn + n];
+          if (k != 0.0) acc += T(k) * gD[m * dn + n];
+        }
+        gU[c][d] = T(2 * L + 1) * acc;
+      }
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < dp; ++b) {
+        const double k = cg[(a * dp + b) * dn + m];
+        if (k != 0.0) {
+#pragma unroll
+          for (int c = 0; c < 3; ++c)
+#pragma unroll
+            for (int d = 0; d < dp; ++d) {
+              gR[a * 3 + c] += T(k) * gU[c][d] * P[b * dp + d];
+              gP[b * dp + d] += T(k) * R[a * 3 + c] * gU[c][d];
+            }
+        }
+      }
+  }
 }
 
+// Forward: one edge per lane; a wavefront's 64 matrices go through LDS (row
+// stride K*K+1 words, odd or padded, so the per-lane writes hit distinct banks)
+// and leave as one contiguous, coalesced run. Matrices too large for 64 KB of
+// LDS are stored per lane.
+template <typename T, int L>
+__global__ __launch_bounds__(64) void k_wigner_fwd(const T* __restrict__ vec, int64_t E, T* __restrict__ W) {
+  constexpr int K = (L + 1) * (L + 1), KK = K * K;
+  constexpr int KP = (KK % 2) ? KK : KK + 1;
+  constexpr bool STAGE = 64 * KP * sizeof(T) <= 65536;
+  const int64_t e0 = (int64_t)blockIdx.x * 64;
+  const int64_t e = e0 + threadIdx.x;
+  T w[KK];
+  if (e < E) wigner_m<T, T, L>(vec[3 * e], vec[3 * e + 1], vec[3 * e + 2], w);
+  if constexpr (STAGE) {
+    __shared__ T st[64 * KP];
+#pragma unroll
+    for (int i = 0; i < KK; ++i) st[threadIdx.x * KP + i] = w[i];
+    __syncthreads();
+    const int nv = E - e0 < 64 ? (int)(E - e0) : 64;
+    T* o = W + e0 * KK;
+    for (int idx = threadIdx.x; idx < nv * KK; idx += 64) o[idx] = st[(idx / KK) * KP + idx % KK];
+  } else {
+    if (e >= E) return;
+    T* o = W + e * KK;
+#pragma unroll
+    for (int i = 0; i < KK; ++i) o[i] = w[i];
+  }
+}
+
+// Backward, reverse mode: the incoming gradient is read on the diagonal blocks
+// only (the others multiply constant zeros), pulled back through the D^l
+// recursion to the frame R, and R's dual parts (forward mode over the three
+// vector components) take it to the edge vector.
 template <typename T, int L>
 __global__ __launch_bounds__(64) void k_wigner_bwd(const T* __restrict__ vec, const T* __restrict__ gW, int64_t E,
                                                    T* __restrict__ gv) {
@@ -240,14 +301,44 @@ __global__ __launch_bounds__(64) void k_wigner_bwd(const T* __restrict__ vec, co
   if (e >= E) return;
   Dual3<T> x(vec[3 * e]), y(vec[3 * e + 1]), z(vec[3 * e + 2]);
   x.d[0] = T(1); y.d[1] = T(1); z.d[2] = T(1);
-  Dual3<T> w[K * K];
-  wigner_m<T, Dual3<T>, L>(x, y, z, w);
+  Dual3<T> Rd[9];
+  edge_frame<T>(x, y, z, Rd);
+  T R[9], gR[9];
+#pragma unroll
+  for (int k = 0; k < 9; ++k) { R[k] = Rd[k].v; gR[k] = T(0); }
+  T gD2[25], gD3[49];
   const T* g = gW + e * K * K;
+#pragma unroll
+  for (int r = 0; r < K; ++r) {
+    const int src = m_row<L>(r);
+    int l = 0;
+    while ((l + 1) * (l + 1) <= src) ++l;
+    const int i = src - l * l;
+#pragma unroll
+    for (int j = 0; j < 2 * l + 1; ++j) {
+      const T v = g[r * K + l * l + j];
+      if (l == 1) gR[i * 3 + j] += v;
+      else if (l == 2) gD2[i * 5 + j] = v;
+      else if (l == 3) gD3[i * 7 + j] = v;
+    }
+  }
+  if constexpr (L >= 3) {
+    T D2[25];
+    wig_next<T, T, 2>(R, R, D2);
+    wig_next_adj<T, 3>(R, D2, gD3, gR, gD2);
+  }
+  if constexpr (L >= 2) {
+    T gP[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) gP[k] = T(0);
+    wig_next_adj<T, 2>(R, R, gD2, gR, gP);
+#pragma unroll
+    for (int k = 0; k < 9; ++k) gR[k] += gP[k];
+  }
   T a0 = 0, a1 = 0, a2 = 0;
 #pragma unroll
-  for (int i = 0; i < K * K; ++i) {
-    const T gi = g[i];
-    a0 += gi * w[i].d[0]; a1 += gi * w[i].d[1]; a2 += gi * w[i].d[2];
+  for (int k = 0; k < 9; ++k) {
+    a0 += gR[k] * Rd[k].d[0]; a1 += gR[k] * Rd[k].d[1]; a2 += gR[k] * Rd[k].d[2];
   }
   gv[3 * e] = a0; gv[3 * e + 1] = a1; gv[3 * e + 2] = a2;
 }

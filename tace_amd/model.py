@@ -787,6 +787,43 @@ class TeceInteraction(torch.nn.Module):
         return torch.cat(blocks).view(x.shape[0], -1)
 
 
+class _SplitUpFn(torch.autograd.Function):
+    """``CgtpACE._split_up_torch`` with a one-pass backward: the gradient of
+    ``linear_up``'s output is written block by block into one uninitialised
+    tensor (every element is covered: the path weights' SiLU gradient, then
+    the node and base halves of each doubled block), instead of autograd's
+    zero-filled full-size gradient per slice and their sums."""
+
+    @staticmethod
+    def forward(ctx, u, mod):
+        ctx.mod = mod
+        ctx.save_for_backward(u)
+        return mod._split_up_torch(u)
+
+    @staticmethod
+    def backward(ctx, g_node, g_base, g_ws):
+        (u,) = ctx.saved_tensors
+        mod = ctx.mod
+        Z, C, lay = u.shape[0], mod.C, mod._up_lay
+        gu = torch.empty_like(u)
+        g0 = lay.block(gu, 0)
+        if g_ws is None:
+            g0.zero_()
+        else:
+            g0.copy_(torch.ops.aten.silu_backward(g_ws, lay.block(u, 0)))
+        off = 0
+        for b, (mul, ir) in enumerate(mod.double):
+            f = lay.block(gu, b + 1).view(Z, ir.dim, mul)
+            n = Z * ir.dim * C
+            for half, g in ((f[:, :, :C], g_node), (f[:, :, C:], g_base)):
+                if g is None:
+                    half.zero_()
+                else:
+                    half.copy_(g.reshape(-1)[off:off + n].view(Z, ir.dim, C))
+            off += n
+        return gu, None
+
+
 class CgtpACE(torch.nn.Module):
     """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``): nu-chain of uuu products
     and per-species coefficient linears, evaluated on species-sorted nodes."""
@@ -845,6 +882,11 @@ class CgtpACE(torch.nn.Module):
         """linear_up output -> (node features, base features + ones, path weights),
         all group-major (``prod.py:178-214``)."""
         u = self.linear_up(x)
+        if not ops.MODE.double:
+            return _SplitUpFn.apply(u, self)
+        return self._split_up_torch(u)
+
+    def _split_up_torch(self, u):
         Z, C = u.shape[0], self.C
         ws = torch.nn.functional.silu(self._up_lay.block(u, 0))
         node, base = [], []

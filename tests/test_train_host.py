@@ -172,3 +172,29 @@ def test_tece_convolution_autograd_matches_the_oracle():
     gb = torch.autograd.grad((want * probe).sum(), [x_l, w] + [dict(ref.named_parameters())[n] for n in names])
     for a, b in zip(ga, gb):
         assert (a - b).abs().max().item() < 1e-11 * max(1.0, b.abs().max().item())
+
+
+def test_bilinear_split_backward_equals_autograd_of_the_slices():
+    """The bilinear-gate product basis splits linear_up's output into path
+    weights (SiLU), node and base features (prod.py:178-214); its one-pass
+    backward gives the bits of autograd through the slices, also with an
+    output left unused."""
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    try:
+        torch.manual_seed(0)
+        m = pm.CgtpACE(0, 2, "16x0e+16x1o+16x2e", 16, 2, 2, 2, 3, bilinear=True)
+    finally:
+        torch.set_default_dtype(prev)
+    u = torch.randn(7, m._up_lay.dim, dtype=torch.float64, requires_grad=True)
+    gs = None
+    for keep in (3, 2):
+        a = m._split_up_torch(u)
+        b = pm._SplitUpFn.apply(u, m)
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+        if gs is None:
+            gs = [torch.randn_like(o) for o in a]
+        ga = torch.autograd.grad(a[:keep], u, gs[:keep])[0]
+        gb = torch.autograd.grad(b[:keep], u, gs[:keep])[0]
+        assert torch.equal(ga, gb), keep

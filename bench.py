@@ -191,7 +191,7 @@ def mfma_roofline(summ, wall_ms: float):
     cnt, tot_ms, infos = summ["seg_linear"]
     flops = sum(i[3] for i in infos)
     tfs = flops / (tot_ms * 1e-3) / 1e12
-    return dict(kernel="seg_linear (k_seg_linear_bx3s + k_seg_linear_ks)", bound="mfma", achieved=round(tfs, 1),
+    return dict(kernel="seg_linear (k_seg_linear_bx3f + k_seg_linear_ks)", bound="mfma", achieved=round(tfs, 1),
                 peak=FP32_PEAK_TFS, unit="TFLOP/s", frac=round(tfs / FP32_PEAK_TFS, 4),
                 bf16_pipe_frac=round(BF16X3_PRODUCTS * tfs / BF16_PEAK_TFS, 4),
                 flops_per_step=None, launches=cnt, avg_launch_us=round(tot_ms / cnt * 1e3, 1),

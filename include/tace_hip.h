@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 24
+#define TACE_HIP_ABI_VERSION 25
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -275,7 +275,8 @@ int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void*
  *   applied transposed, the input gradient) and zeros past k and cols:
  *     layout 0: term p into planes[p * plane_stride + dst_off + c k_pad + kk]
  *               for column c < cols and kk < k_pad = ceil8(k);
- *     layout 1 (MFMA fragment order, for tace_seg_linear_presplit_ks): one
+ *     layout 1 (MFMA fragment order, for tace_seg_linear_presplit_ks and
+ *               tace_seg_linear_presplit_frag): one
  *               buffer, per 16-column block cb and 32-k step s (nks =
  *               ceil(k / 32) steps per column block, ceil16(cols) columns)
  *               the three terms as runs of 512: element (c, kk) of term p at
@@ -309,6 +310,17 @@ int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes,
  * tace_seg_linear_presplit gives for the same tile.  Trusted tables, checked
  * by the host (tace_amd.ops.SegLinearPlan). */
 int32_t tace_seg_linear_ks_rows(int32_t k);
+/* The tile table of tace_seg_linear_presplit (same tiles and contributions,
+ * any k) with each contribution's w_off pointing at its block in weights
+ * split in MFMA fragment order (tace_bf16x3_split_blocks layout 1, 16-byte
+ * aligned): B is read from there one 32-k step ahead instead of being staged
+ * in LDS.  aligned != 0 promises that every contribution's x offset and k are
+ * multiples of 4 (16-byte rows of x; with x 16-byte aligned the kernel then
+ * loads A without per-element tails).  The same bits as
+ * tace_seg_linear_presplit for the same tiles. */
+int tace_seg_linear_presplit_frag(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+                                  const int64_t* tiles, int64_t n_tiles, const int64_t* contribs, int32_t aligned,
+                                  double alpha, void* stream);
 int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
                                 const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha, void* stream);
 

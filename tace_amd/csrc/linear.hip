@@ -444,6 +444,239 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
   }
 }
 
+// ---- the tile kernel with B in fragment order ----------------------------
+// k_seg_linear_bx3s stages A and B through LDS with two barriers per 32-k
+// step; LDS traffic (48 KB of plane stores and 96 KB of fragment reads per
+// step and workgroup) then takes about as long as the MFMAs.  Here:
+//  * B fragments come straight from the weights pre-split in MFMA fragment
+//    order (k_split_blocks layout 1, as the task kernel reads them): one
+//    coalesced 16-byte load per lane and fragment, one step ahead;
+//  * A (128 rows x 32 k) is loaded two steps ahead and split into the three
+//    planes in LDS, double buffered: step s + 1's planes are written after
+//    step s's MFMAs, and one barrier per step separates them;
+//  * every load is unconditional (past the last step it repeats that step):
+//    a load under a branch makes the compiler wait for all loads at the
+//    join, the prefetches included;
+//  * the MFMA runs with the operands swapped (B fragments as the row
+//    operand), so a lane holds 4 consecutive columns of one output row, and
+//    the stores trade blocks between lanes fr and fr ^ 8 as the task kernel's
+//    do (8 whole rows of 32 columns per store).
+// Tiles, contributions and the XCD-grouped tile order are those of
+// k_seg_linear_bx3s; contribution column 2 is the block's offset in the
+// fragment-order weights.  Per output element the products and their order
+// are those of k_seg_linear_bx3s (contributions and k steps in order, the six
+// terms smallest first, each a sum over the same 32 products), so the two
+// kernels give the same bits.
+struct FtLoad {   // the contribution and step whose operands load next
+  const float* xa;
+  const unsigned short* wf;
+  int c, s, k, nks;
+  bool xvec;
+};
+
+__device__ __forceinline__ void ft_open(FtLoad& L, const float* __restrict__ x, const unsigned short* __restrict__ wfrag,
+                                        const int64_t* __restrict__ contribs, int c) {
+  const int64_t* cd = contribs + 4 * (int64_t)c;
+  L.c = c;
+  L.s = 0;
+  L.xa = x + cd[0];
+  L.k = (int)cd[1];
+  L.nks = (L.k + 31) >> 5;
+  L.wf = wfrag + cd[2];
+  L.xvec = ((((uintptr_t)L.xa) & 15) == 0) && ((L.k & 3) == 0);
+}
+
+// A (128 rows x 32 k) of step L.s as seg_load_k<128> holds it, but rows past
+// nrows repeat the last row (their outputs are not stored).  VEC (every
+// contribution 16-byte aligned with k % 4 == 0): four unconditional 16-byte
+// loads, a run past k read from the row's start and zeroed -- no branch, so
+// the compiler's wait for this step's B (issued before) is exact.
+template <bool VEC>
+__device__ __forceinline__ void ft_load_a(const FtLoad& L, int nrows, int t, f4* v) {
+  const int kk = 32 * L.s + 16 * (t & 1);
+  const int r = min(t >> 1, nrows - 1);
+  const float* row = L.xa + (int64_t)r * L.k;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int left = L.k - (kk + 4 * q);
+    if constexpr (VEC) {
+      const f4 u = *(const f4*)(left >= 4 ? row + kk + 4 * q : row);
+      v[q] = left >= 4 ? u : f4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      v[q] = seg_ld4(row + kk + 4 * q, false, left > 0, left);
+    }
+  }
+}
+
+// B fragments (three terms) of column blocks jb0 .. jb0 + 3 (clamped to the
+// block's last) at step L.s
+__device__ __forceinline__ void ft_load_b(const FtLoad& L, int jb0, int nb16, int lane, u4v (&d)[3][4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int jb = min(jb0 + j, nb16 - 1);
+    const unsigned short* p = L.wf + ((int64_t)(jb * L.nks + L.s) * 3) * 512 + 8 * lane;
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) d[pl][j] = *(const u4v*)(p + pl * 512);
+  }
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_seg_linear_bx3f(
+    const float* __restrict__ x, float* __restrict__ y,
+                                                         const unsigned short* __restrict__ wfrag,
+                                                         const float* __restrict__ bias,
+                                                         const int64_t* __restrict__ tiles,
+                                                         const int64_t* __restrict__ contribs, float alpha,
+                                                         int n_tiles, int per) {
+  constexpr int WM = 4, TR = 128, PL = 128 * SB_STR;   // plane size (bf16)
+  __shared__ __attribute__((aligned(16))) unsigned short As[2][3 * PL];
+  const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (tile >= n_tiles) return;
+  const int64_t* td = tiles + 8 * (int64_t)tile;
+  const int64_t out_base = td[0];
+  const int rows = (int)td[1], n = (int)td[2], c0 = (int)td[3];
+  const int64_t bias_off = td[4];
+  const int cb = (int)td[5], ce = (int)td[6];
+  const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 64;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int nb16 = (n + 15) >> 4, jb0 = (c0 + wc) >> 4;
+  const int soff = (t >> 1) * SB_STR + 16 * (t & 1);   // this thread's k16 run of a k-contiguous plane
+
+  f4 acc[WM][4];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // skip contributions without k steps
+  int c = cb;
+  FtLoad L;
+  while (c < ce) {
+    ft_open(L, x, wfrag, contribs, c);
+    if (L.nks > 0) break;
+    ++c;
+  }
+  if (c < ce) {
+    // the steps of all contributions, in order.  A loads two steps ahead of
+    // the MFMAs (cursor LA; A(j) in register set j & 1), B one step ahead
+    // (cursor LB): x streams from HBM, the weights from L2
+    FtLoad LA = L, LB = L;
+    bool moreA = true, moreB = true;
+    // C to the step after the one it names; after the last step C stays
+    // there (more = false), so the loads below never need a condition
+    auto advance = [&](FtLoad& C, bool& more) {
+      if (C.s + 1 < C.nks) {
+        ++C.s;
+        return;
+      }
+      for (int cc = C.c + 1; cc < ce; ++cc) {
+        FtLoad D;
+        ft_open(D, x, wfrag, contribs, cc);
+        if (D.nks > 0) {
+          C = D;
+          return;
+        }
+      }
+      more = false;
+    };
+    f4 a0[4], a1[4];
+    u4v b0[3][4], b1[3][4];
+    ft_load_a<VEC>(LA, rows, t, a0);
+    advance(LA, moreA);
+    ft_load_b(LB, jb0, nb16, lane, b0);
+    advance(LB, moreB);
+    ft_load_a<VEC>(LA, rows, t, a1);   // (a repeat of the last step when there is no next)
+    advance(LA, moreA);
+    sb_store_k16<false>(As[0], PL, soff, a0, 1.f);
+    __syncthreads();
+    // step g: MFMAs on LDS buffer `buf` (= g & 1) and fragments cur while A(g
+    // + 2) loads into al and B(g + 1) into nxt; then A(g + 1) (in as) split
+    // into the other buffer
+    auto step = [&](int buf, const u4v (&cur)[3][4], u4v (&nxt)[3][4], f4 (&al)[4], const f4 (&as)[4]) {
+      const bool have = moreB;
+      // B before A: vector loads complete in issue order, so waiting for
+      // this step's B (issued last step) does not wait for the A issued
+      // after it.  Unconditional (repeats past the last step): a load under
+      // a branch makes the compiler wait for every load at the join
+      ft_load_b(LB, jb0, nb16, lane, nxt);
+      advance(LB, moreB);
+      ft_load_a<VEC>(LA, rows, t, al);
+      advance(LA, moreA);
+      __builtin_amdgcn_sched_barrier(0);
+      const unsigned short* Ab = As[buf];
+#pragma unroll
+      for (int ip = 0; ip < WM / 2; ++ip) {
+        bx3_bf8 af[2][3];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int pl = 0; pl < 3; ++pl)
+            af[ii][pl] = *(const bx3_bf8*)&Ab[pl * PL + (wr + 32 * ip + 16 * ii + fr) * SB_STR + 8 * fg];
+#pragma unroll
+        for (int u = 0; u < 6; ++u)   // the six terms a_i b_j, smallest first
+#pragma unroll
+          for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              acc[2 * ip + ii][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  __builtin_bit_cast(bx3_bf8, cur[BX3_TB[u]][j]), af[ii][BX3_TA[u]], acc[2 * ip + ii][j], 0, 0, 0);
+      }
+      // the next A's split after the MFMAs (interleaving it measured slower)
+      __builtin_amdgcn_sched_barrier(0);
+      sb_store_k16<false>(As[buf ^ 1], PL, soff, as, 1.f);
+      __syncthreads();
+      return have;
+    };
+    while (step(0, b0, b1, a0, a1) && step(1, b1, b0, a1, a0)) {
+    }
+  }
+
+  // the bias of this lane's 16 columns (no loads are outstanding here)
+  f4 bv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bv[j] = f4{0.f, 0.f, 0.f, 0.f};
+    if (bias_off >= 0) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[j][q] = bias[bias_off + min(c0 + wc + 16 * j + 4 * fg + q, n - 1)];
+    }
+  }
+  // acc[i][j][q] = out[row wr + 16 i + fr][column c0 + wc + 16 j + 4 fg + q];
+  // per pair of blocks (2 jp, 2 jp + 1) lanes fr and fr ^ 8 trade one block,
+  // so a store writes 8 whole rows of 32 columns
+  const bool vst = ((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
+  const bool lo = fr < 8;
+  const int jl = lo ? 0 : 1;
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp) {
+    const int col = c0 + wc + 32 * jp + 16 * jl + 4 * fg;
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      const f4 v0 = alpha * (acc[i][2 * jp] + bv[2 * jp]), v1 = alpha * (acc[i][2 * jp + 1] + bv[2 * jp + 1]);
+      const f4 give = lo ? v1 : v0;
+      f4 got;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) got[q] = __shfl_xor(give[q], 8);
+      const f4 s0 = lo ? v0 : got, s1 = lo ? got : v1;   // rows 16 i + (fr & 7), + 8
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = wr + 16 * i + 8 * h + (fr & 7);
+        if (r >= rows || col >= n) continue;
+        const f4 v = h ? s1 : s0;
+        float* dst = y + out_base + (int64_t)r * n + col;
+        if (vst) {
+          *(f4*)dst = v;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (col + q < n) dst[q] = v[q];
+        }
+      }
+    }
+  }
+}
+
 // ---- short k, wide n: the input-gradient shape ---------------------------
 // The input gradients of the product-basis contractions are [rows, k = 128]
 // x [128, n] with n up to ~5,400 columns per output block.  A 128 x 128 tile
@@ -757,6 +990,25 @@ extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t
                      (const unsigned short*)w_planes, plane_stride, bias, tiles, contribs, (float)alpha,
                      (int)n_tiles, per);
   return tace_check_launch("tace_seg_linear_presplit");
+}
+
+extern "C" int tace_seg_linear_presplit_frag(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+                                             const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
+                                             int32_t aligned, double alpha, void* stream) {
+  if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_frag: bad tile count");
+  if (n_tiles == 0) return 0;
+  if (!x || !y || !w_frag || !tiles || !contribs) return tace_fail_msg("tace_seg_linear_presplit_frag: null pointer");
+  if ((((uintptr_t)w_frag) & 15) != 0)
+    return tace_fail_msg("tace_seg_linear_presplit_frag: fragment-order weights must be 16-byte aligned");
+  const int per = (int)((n_tiles + 7) / 8);
+  const dim3 g((unsigned)(8 * per)), b(256);
+  if (aligned && (((uintptr_t)x) & 15) == 0)
+    hipLaunchKernelGGL(k_seg_linear_bx3f<true>, g, b, 0, (hipStream_t)stream, x, y, (const unsigned short*)w_frag,
+                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
+  else
+    hipLaunchKernelGGL(k_seg_linear_bx3f<false>, g, b, 0, (hipStream_t)stream, x, y, (const unsigned short*)w_frag,
+                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
+  return tace_check_launch("tace_seg_linear_presplit_frag");
 }
 
 extern "C" int32_t tace_seg_linear_ks_rows(int32_t k) { return k < 0 ? 0 : k <= 128 ? 128 : k <= 256 ? 64 : 0; }

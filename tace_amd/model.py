@@ -233,8 +233,8 @@ class _LinearLayout:
         # the block's offset in one species' planes, its columns and k; per
         # direction ("fwd": B = W, "bwd": B = W^T)
         self.split_blocks = {}
-        # the same in MFMA fragment order (layout 1) for the instructions with
-        # k <= 256 (tace_seg_linear_presplit_ks); offset -1 for the others
+        # the same in MFMA fragment order (layout 1: tace_seg_linear_presplit_ks
+        # and tace_seg_linear_presplit_frag)
         self.frag_blocks = {}
         for kind in ("fwd", "bwd"):
             blocks, acc, fblocks, facc = [], 0, [], 0
@@ -242,11 +242,8 @@ class _LinearLayout:
                 cols, k = (mo, mi) if kind == "fwd" else (mi, mo)
                 blocks.append((acc, cols, k))
                 acc += cols * ((k + 7) // 8 * 8)
-                if k <= 256:
-                    fblocks.append((facc, cols, k))
-                    facc += 3 * ((cols + 15) // 16 * 16) * ((k + 31) // 32 * 32)
-                else:
-                    fblocks.append((-1, cols, k))
+                fblocks.append((facc, cols, k))
+                facc += 3 * ((cols + 15) // 16 * 16) * ((k + 31) // 32 * 32)
             self.split_blocks[kind] = (blocks, acc)
             self.frag_blocks[kind] = (fblocks, facc)
 
@@ -254,10 +251,11 @@ class _LinearLayout:
         """The three bf16 terms of every (species, instruction) weight block
         with its path weight folded in, in the column layout of
         ``tace_seg_linear_presplit`` ("fwd": B = W, "bwd": B = W^T); returns
-        (planes int16 [3 * stride], plane stride).  ``frag``: the blocks with
-        k <= 256 in the MFMA fragment order of ``tace_seg_linear_presplit_ks``
-        instead (one buffer; the stride is its size).  Cached until the weight
-        changes (its version counter or storage)."""
+        (planes int16 [3 * stride], plane stride).  ``frag``: the blocks in
+        the MFMA fragment order of ``tace_seg_linear_presplit_ks`` and
+        ``tace_seg_linear_presplit_frag`` instead (one buffer; the stride is
+        its size).  Cached until the weight changes (its version counter or
+        storage)."""
         w = weight.detach()
         key = (w.data_ptr(), w._version, tuple(w.shape), str(w.device))
         ck = (kind, frag)
@@ -290,7 +288,7 @@ class _LinearLayout:
         ranges ``rr`` of Z rows; the last few are cached."""
         tile = (128, 128) if x.dtype == torch.float32 and SEG_LINEAR_TILE_F32 == 128 else (64, 64)
         presplit = tile == (128, 128) and SEG_LINEAR_PRESPLIT
-        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile, presplit)
+        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile, presplit, ops.SEG_TILE_FRAG)
         plan = self._seg.get(key)
         if plan is not None:
             self._seg.move_to_end(key)
@@ -345,8 +343,9 @@ class _LinearFn(torch.autograd.Function):
             # all species and instructions in one segmented-GEMM launch
             plan = lay.seg_plan("fwd", rr, Z, x, weight, bias)
             if plan.split_weights:
-                fr = lay.split_weights("fwd", weight, frag=True)[0] if plan.n_ks else None
-                return ops.seg_linear_presplit(x, out, *lay.split_weights("fwd", weight), bias, plan, alpha, frag=fr)
+                fr = lay.split_weights("fwd", weight, frag=True)[0] if plan.n_ks or plan.tile_frag else None
+                pl = (None, 0) if plan.tile_frag else lay.split_weights("fwd", weight)
+                return ops.seg_linear_presplit(x, out, *pl, bias, plan, alpha, frag=fr)
             return ops.seg_linear(x, out, weight, bias, plan, alpha)
         done = set()
         for (i, o, off, mi, mo, pw) in lay.ins:
@@ -377,8 +376,9 @@ class _LinearFn(torch.autograd.Function):
         if ctx.seg and gx is not None:
             plan = lay.seg_plan("bwd", rr, x.shape[0], x, weight, None)
             if plan.split_weights:
-                fr = lay.split_weights("bwd", weight, frag=True)[0] if plan.n_ks else None
-                ops.seg_linear_presplit(gout, gx, *lay.split_weights("bwd", weight), None, plan, alpha, frag=fr)
+                fr = lay.split_weights("bwd", weight, frag=True)[0] if plan.n_ks or plan.tile_frag else None
+                pl = (None, 0) if plan.tile_frag else lay.split_weights("bwd", weight)
+                ops.seg_linear_presplit(gout, gx, *pl, None, plan, alpha, frag=fr)
             else:
                 ops.seg_linear(gout, gx, weight, None, plan, alpha)
         done = set()

@@ -1406,6 +1406,10 @@ def radial_mlp_hidden(radial: torch.Tensor, mats: Sequence[torch.Tensor]) -> tor
 SEG_KS_MIN_N = 256
 # columns per tace_seg_linear_presplit_ks task
 SEG_KS_CHUNK = 1024
+# pre-split plans' tiles read the weights in fragment order
+# (tace_seg_linear_presplit_frag) when every instruction has a
+# fragment-order block; False: the planes of tace_seg_linear_presplit
+SEG_TILE_FRAG = True
 
 
 class SegLinearPlan:
@@ -1440,6 +1444,10 @@ class SegLinearPlan:
         # the short-k tasks read; an instruction's offset there is its 7th item
         # (-1: not split that way)
         self.frag_numel = frag[1] if frag is not None else 0
+        # the tiles read B in fragment order too (tace_seg_linear_presplit_frag)
+        # when every instruction has a fragment-order block
+        self.tile_frag = bool(self.split_weights and frag is not None and SEG_TILE_FRAG
+                              and all(len(c) > 6 and c[6] >= 0 for c in ins))
         for ob, (s_o, n, d, boff) in enumerate(out_blocks):
             mine = [c for c in ins if c[0] == ob]
             if (self.split_weights and frag is not None and SEG_KS_MIN_N is not None and n >= SEG_KS_MIN_N
@@ -1471,7 +1479,10 @@ class SegLinearPlan:
                     for j, (_, s_i, k, w_off, trans, sc, *_f) in enumerate(mine):
                         c[:, j, 0] = Z * s_i + R.ravel() * k
                         c[:, j, 1] = k
-                        c[:, j, 2] = w_off + (0 if sp is None else sp * w_stride)
+                        if self.tile_frag:
+                            c[:, j, 2] = _f[0] + (0 if sp is None else sp * frag[0])
+                        else:
+                            c[:, j, 2] = w_off + (0 if sp is None else sp * w_stride)
                         c[:, j, 3] = int(trans)
                     contribs.append(c.reshape(-1, 4))
                     scales.append(np.tile(np.array([m[5] for m in mine], dtype=np.float64), T))
@@ -1490,12 +1501,20 @@ class SegLinearPlan:
             n_c = np.repeat(t[:, 2], t[:, 6] - t[:, 5])
             if (c[:, 0] + rows_c * c[:, 1]).max() > x_numel:
                 raise ValueError("seg linear plan: input tile out of range")
-            kw = (c[:, 1] + 7) // 8 * 8 if self.split_weights else c[:, 1]
-            if (c[:, 2] + kw * n_c).max() > w_numel:
-                raise ValueError("seg linear plan: weight out of range")
+            if self.tile_frag:
+                fsz = 3 * ((n_c + 15) // 16 * 16) * ((c[:, 1] + 31) // 32 * 32)
+                if (c[:, 2] + fsz).max() > self.frag_numel:
+                    raise ValueError("seg linear plan: fragment-order weight out of range")
+            else:
+                kw = (c[:, 1] + 7) // 8 * 8 if self.split_weights else c[:, 1]
+                if (c[:, 2] + kw * n_c).max() > w_numel:
+                    raise ValueError("seg linear plan: weight out of range")
             if self.split_weights and (c[:, 2] % 8).any():
                 raise ValueError("seg linear plan: pre-split weight blocks must start on 8-element boundaries")
         self.n_tiles = len(t)
+        # every contribution's x rows start on a 16-byte boundary (offsets and
+        # k multiples of 4): the fragment-order tiles' aligned A loads
+        self.tile_aligned = bool(len(c) == 0 or (((c[:, 0] % 4) == 0) & ((c[:, 1] % 4) == 0)).all())
         self.x_numel, self.y_numel, self.w_numel, self.b_numel = x_numel, y_numel, w_numel, b_numel
         # multiply-adds x 2 of the whole launch (rows x valid columns x summed k
         # of every tile): the algorithmic flops of the GEMMs, padding excluded
@@ -1622,11 +1641,13 @@ def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int, frag
     return planes
 
 
-def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, plane_stride: int,
+def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: Optional[torch.Tensor], plane_stride: int,
                         bias: Optional[torch.Tensor], plan: SegLinearPlan, alpha: float,
                         frag: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Runs a ``split_weights`` plan (``tace_seg_linear_presplit``) with the
-    weight planes of ``bf16x3_split_blocks``, and its short-k tasks
+    """Runs a ``split_weights`` plan: its tiles with the weight planes of
+    ``bf16x3_split_blocks`` (``tace_seg_linear_presplit``; planes may be None
+    when the plan's tiles read the fragment-order weights instead,
+    ``tace_seg_linear_presplit_frag``), and its short-k tasks
     (``tace_seg_linear_presplit_ks``) with the fragment-order weights
     ``frag``; returns y."""
     if not plan.split_weights:
@@ -1635,7 +1656,11 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, 
         _req(t, nm, torch.float32)
         if t.numel() != n:
             raise ValueError(f"seg linear: {nm} has {t.numel()} elements, the plan was built for {n}")
-    if planes.dtype != torch.int16 or planes.numel() != 3 * plane_stride or plane_stride < plan.w_numel:
+    if (plan.n_ks or plan.tile_frag) and (frag is None or frag.dtype != torch.int16
+                                          or frag.numel() < plan.frag_numel):
+        raise ValueError("seg linear: the plan needs its fragment-order weights")
+    if not plan.tile_frag and (planes is None or planes.dtype != torch.int16 or planes.numel() != 3 * plane_stride
+                               or plane_stride < plan.w_numel):
         raise ValueError("seg linear: weight planes do not match the plan")
     if bias is not None:
         _req(bias, "bias", torch.float32)
@@ -1644,12 +1669,16 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: torch.Tensor, 
     tok = _t0("seg_linear")
     st = N.stream_ptr(x.device)
     b_ptr = None if bias is None else bias.data_ptr()
-    N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride, b_ptr,
-                                             plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
-                                             float(alpha), st), "tace_seg_linear_presplit")
+    if plan.tile_frag:
+        N.check(N.lib().tace_seg_linear_presplit_frag(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
+                                                      plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
+                                                      int(plan.tile_aligned), float(alpha), st),
+                "tace_seg_linear_presplit_frag")
+    else:
+        N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride, b_ptr,
+                                                 plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
+                                                 float(alpha), st), "tace_seg_linear_presplit")
     if plan.n_ks:
-        if frag is None or frag.dtype != torch.int16 or frag.numel() < plan.frag_numel:
-            raise ValueError("seg linear: the plan's short-k tasks need its fragment-order weights")
         for R, n_t, tasks in plan.ks_groups:
             N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
                                                         tasks.data_ptr(), n_t, R, float(alpha), st),

@@ -530,9 +530,11 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, presplit, irr_in, irr_o
 @pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
 def test_seg_linear_presplit_equals_in_kernel_split(cuda, irr_in, irr_out, counts, monkeypatch):
     """The pre-split weight planes (tace_bf16x3_split_blocks +
-    tace_seg_linear_presplit) give the same bits as the kernel that splits
-    the weights in every launch: the same bf16 terms, the same products in
-    the same order.  After an in-place weight update the planes are rebuilt."""
+    tace_seg_linear_presplit) and the fragment-order weights
+    (tace_seg_linear_presplit_frag, with B read from global memory) give the
+    same bits as the kernel that splits the weights in every launch: the same
+    bf16 terms, the same products in the same order.  After an in-place
+    weight update the planes are rebuilt."""
     from tace_amd import model as pm
     monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", 128)
     S, Z = len(counts), sum(counts)
@@ -549,13 +551,15 @@ def test_seg_linear_presplit_equals_in_kernel_split(cuda, irr_in, irr_out, count
     go = torch.randn(Z, lin.lay.dim_out, generator=g).to(cuda)
     for step in range(2):
         outs = {}
-        for presplit in (False, True):
+        for presplit, tfrag in ((False, False), (True, False), (True, True)):
             monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", presplit)
+            monkeypatch.setattr(ops, "SEG_TILE_FRAG", tfrag)
             y = lin(x, sp, 0.9)
             (gx,) = torch.autograd.grad(y, x, go)
-            outs[presplit] = (y.detach(), gx)
-        assert torch.equal(outs[True][0], outs[False][0]), f"forward differs (step {step})"
-        assert torch.equal(outs[True][1], outs[False][1]), f"input gradient differs (step {step})"
+            outs[(presplit, tfrag)] = (y.detach(), gx)
+        for key in ((True, False), (True, True)):
+            assert torch.equal(outs[key][0], outs[(False, False)][0]), f"forward differs {key} (step {step})"
+            assert torch.equal(outs[key][1], outs[(False, False)][1]), f"input gradient differs {key} (step {step})"
         with torch.no_grad():
             lin.weight.mul_(-0.5)   # a new weight version: the cached planes must be rebuilt
 

@@ -610,7 +610,11 @@ class _EdgeVectors(torch.autograd.Function):
         plan = ctx.plan
         g = g.contiguous()
         gpos = glat = None
-        if ctx.needs_input_grad[0]:
+        if ctx.needs_input_grad[0] and plan.n_edges == 0:
+            # no edge: every receiver and sender sum is empty (and the empty
+            # per-edge tensors have no device pointer for the kernel)
+            gpos = torch.zeros(plan.n_nodes, 3, dtype=g.dtype, device=g.device)
+        elif ctx.needs_input_grad[0]:
             s_rowptr, s_slot = plan.sender_csr()
             gpos = torch.empty(plan.n_nodes, 3, dtype=g.dtype, device=g.device)
             N.check(N.lib().tace_edge_vec_bwd(N.dtype_code(g.dtype), g.data_ptr(), plan.rowptr.data_ptr(),

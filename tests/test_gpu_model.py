@@ -19,12 +19,13 @@ pytestmark = pytest.mark.gpu
 BARS = {torch.float64: (1e-10, 1e-8, 1e-8), torch.float32: (1e-5, 1e-4, 1e-4)}
 
 
-def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, **over):
+def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, avg=None, keep=None, **over):
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS[preset]["cutoff"])
              for s in structs]
     zs = sorted({int(z) for s in structs for z in s["numbers"]})
     nat = sum(len(s["positions"]) for s in structs)
-    avg = sum(e[0].shape[1] for e in edges) / nat
+    if avg is None:
+        avg = sum(e[0].shape[1] for e in edges) / nat
     cfg = configs.model_cfg(preset, zs, avg, **over)
     torch.manual_seed(seed)
     ref = om.TACE(cfg).double()
@@ -43,6 +44,8 @@ def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, **over):
         gpu.reset_target_property(["energy", "forces"])
     dg = data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda)
     got = gpu(dg)
+    if keep is not None:
+        keep.update(model=gpu, cfg=cfg)
     return got, want
 
 
@@ -78,6 +81,56 @@ def test_water_slice(cuda, dtype):
     """Config 3 architecture (C=128, L=3, 3 layers, r_c=6) on 64 molecules."""
     got, want = _run_pair([structures.water_box(n_side=4, box=12.425, seed=3)], "water12k", cuda, dtype)
     _check(got, want, dtype)
+
+
+def _edge_cases():
+    box = np.eye(3) * 20.0
+    single = dict(positions=np.zeros((1, 3)), cell=box, numbers=np.array([14]), pbc=(True,) * 3)
+    apart = dict(positions=np.array([[1.0, 1.0, 1.0], [8.5, 1.2, 0.9]]), cell=box, numbers=np.array([14, 14]),
+                 pbc=(True,) * 3)
+    dimer = dict(positions=np.array([[1.0, 1.0, 1.0], [3.2, 1.3, 0.8]]), cell=box, numbers=np.array([14, 14]),
+                 pbc=(True,) * 3)
+    return single, apart, dimer
+
+
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_batch_with_isolated_atoms_and_edgeless_structures(cuda, dtype):
+    """The readout's batch rules (tace/models/_e3nn/tace.py:356-418) in one
+    ragged batch with stress: a single atom without neighbours (scale and
+    shift 0), two atoms beyond the cutoff (no edges, scale and shift kept), a
+    close dimer and a crystal, against the oracle at the model bars."""
+    single, apart, dimer = _edge_cases()
+    structs = [structures.si_diamond(seed=4), single, apart, dimer]
+    keep = {}
+    got, want = _run_pair(structs, "si64", cuda, dtype, stress=True, keep=keep)
+    # the same batch through the batched GPU neighbour search (what the calculators run)
+    cfg = keep["cfg"]
+    g2 = keep["model"](data.gpu_graph(structs, cfg["atomic_numbers"], configs.PRESETS["si64"]["cutoff"],
+                                      dtype=dtype, device=cuda))
+    tol = 1e-12 if dtype == torch.float64 else 1e-5
+    for k in ("energy", "forces", "stress"):
+        d = (g2[k] - got[k]).abs().max().item()
+        assert d <= tol * max(got[k].abs().max().item(), 1.0), (k, d)
+    e_rel, f_abs, s_abs = BARS[dtype]
+    E, E0 = got["energy"].double().cpu(), want["energy"]
+    assert ((E - E0).abs() <= e_rel * E0.abs().clamp_min(1.0)).all(), (E, E0)
+    F, F0 = got["forces"].double().cpu(), want["forces"]
+    assert (F - F0).abs().max().item() < f_abs
+    assert F[64:66].abs().max().item() == 0.0   # the single atom and the pair beyond the cutoff feel no force
+    S, S0 = got["stress"].double().cpu(), want["stress"]
+    assert (S - S0).abs().max().item() < s_abs
+    assert S[1:3].abs().max().item() == 0.0
+
+
+def test_batch_without_any_edge(cuda):
+    """A batch whose structures have no edge at all (every kernel launch
+    with zero edges): energies equal the oracle's, forces and stress zero."""
+    single, apart, _ = _edge_cases()
+    got, want = _run_pair([single, apart], "si64", cuda, torch.float64, stress=True, avg=28.0)
+    E, E0 = got["energy"].double().cpu(), want["energy"]
+    assert ((E - E0).abs() <= 1e-10 * E0.abs().clamp_min(1.0)).all(), (E, E0)
+    assert got["forces"].abs().max().item() == 0.0 and want["forces"].abs().max().item() == 0.0
+    assert got["stress"].abs().max().item() == 0.0
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])

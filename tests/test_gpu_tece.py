@@ -461,6 +461,22 @@ def test_tece_two_species_batch(cuda, dtype):
     _check(got, want, dtype)
 
 
+@pytest.mark.parametrize("frozen,chunk_edges", [(True, None), (True, 700), (False, None)])
+def test_tece_batch_with_isolated_atoms(cuda, frozen, chunk_edges):
+    """A TECE batch holding a single Fe atom without neighbours (scale and
+    shift 0) and two Fe atoms beyond the cutoff (no edges) beside a bcc
+    slice: nodes that receive and send nothing, on the fused operator (in one
+    piece and in receiver chunks) and on the per-operator path."""
+    box = np.eye(3) * 20.0
+    single = dict(positions=np.zeros((1, 3)), cell=box, numbers=np.array([26]), pbc=(True,) * 3)
+    apart = dict(positions=np.array([[1.0, 1.0, 1.0], [8.5, 1.2, 0.9]]), cell=box, numbers=np.array([26, 26]),
+                 pbc=(True,) * 3)
+    got, want = _model_pair([structures.bcc_fe(reps=(3, 3, 2), seed=10), single, apart], cuda, torch.float64,
+                            seed=2, chunk_edges=chunk_edges, num_channel=64, num_head=2, frozen=frozen)
+    _check(got, want, torch.float64)
+    assert got["forces"][-3:].abs().max().item() == 0.0
+
+
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 def test_tece_receiver_chunks(cuda, dtype):
     """The receiver-chunked convolution (activation checkpointing per chunk, used

@@ -22,6 +22,9 @@ def _batch():
     rng = np.random.default_rng(21)
     structs = [structures.random_crystal(rng, int(rng.integers(3, 24)), [1, 8, 14, 26]) for _ in range(5)]
     structs.append(structures.si_diamond(seed=2))
+    # a single atom without neighbours: the readout's isolated-atom rule
+    structs.append(dict(positions=np.array([[0.5, 0.5, 0.5]]), cell=np.eye(3) * 20.0, numbers=np.array([14]),
+                        pbc=(True,) * 3))
     return structs
 
 

@@ -69,10 +69,17 @@ CASES = [
     # a ragged batch of triclinic crystals with stress
     ("ragged128", lambda: [structures.random_crystal(np.random.default_rng(5 + i), 10 + 4 * i, [3, 8, 14])
                            for i in range(2)], True, dict(num_channel=16, num_layers=2)),
+    # a crystal, a single atom without neighbours and two atoms beyond the cutoff, with stress
+    ("si64", lambda: [structures.si_diamond(seed=2),
+                      dict(positions=np.zeros((1, 3)), cell=np.eye(3) * 20.0, numbers=np.array([14]),
+                           pbc=(True,) * 3),
+                      dict(positions=np.array([[1.0, 1.0, 1.0], [8.5, 1.2, 0.9]]), cell=np.eye(3) * 20.0,
+                           numbers=np.array([14, 14]), pbc=(True,) * 3)], True, dict(num_channel=16)),
 ]
 
 
-@pytest.mark.parametrize("preset,make,stress,over", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("preset,make,stress,over", CASES,
+                         ids=[c[0] for c in CASES[:-1]] + ["si64_isolated_atoms"])
 def test_force_loss_parameter_gradients_match_oracle(cuda, preset, make, stress, over):
     structs = make()
     ref, gpu, d64, dg = _pair(structs, preset, cuda, seed=3, **over)

@@ -396,6 +396,19 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
                             const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows, int64_t n_edges,
                             int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst, void* g_wigner,
                             void* g_radial_w, void* stream);
+/* tace_edge_rotate_in_bwd_runs: tace_edge_rotate_in_bwd for edges in
+ * receiver-CSR order, 4 (lmax+1)^2 channels values of at most 64 KB: the
+ * receiver rows of the four edges a workgroup holds (positions 4 b .. 4 b + 3)
+ * are summed per run of equal rows_dst in edge order and written once, at the
+ * run's first position of g_x_dst_runs [E, K, C]; the other positions are not
+ * written.  tace_rows_accumulate_runs (run = 4) then sums them per receiver:
+ * the receiver half of the index_add of oam_2026_07_05.py:769-771's gather,
+ * run backwards, with a quarter of the per-edge rows. */
+int tace_edge_rotate_in_bwd_runs(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                                 const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
+                                 const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows,
+                                 int64_t n_edges, int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst_runs,
+                                 void* g_wigner, void* g_radial_w, void* stream);
 int tace_tece_score_fwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
                         const void* tscale, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
                         void* score, void* stream);
@@ -473,6 +486,12 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream);
+/* tace_rows_accumulate over the CSR positions themselves (slot NULL) that
+ * only reads each segment's first position and the multiples of `run`
+ * inside it: the run sums tace_edge_rotate_in_bwd_runs writes (run = 4). */
+int tace_rows_accumulate_runs(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                              const int32_t* target, int64_t n_segments, int32_t run, void* out, int64_t n_out_rows,
+                              void* stream);
 /* The TECE SO(2) linears under bf16 channel mixing
  * (oam_2026_07_05.py:138-247, SO2_m0_Linear / SO2_m_Linear per m block, and
  * their input gradients with the transposed weights):

@@ -71,6 +71,8 @@ _SIGS = {
                                          _vp, _vp]),
     "tace_edge_rotate_in_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
                                          _c_i32, _vp, _vp, _vp, _vp, _vp]),
+    "tace_edge_rotate_in_bwd_runs": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
+                                              _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp]),
     "tace_tece_edge_ace_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp,
                                         _vp]),
     "tace_tece_edge_ace_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,
@@ -94,6 +96,8 @@ _SIGS = {
     "tace_nl_batch_count": (_c_int, [_vp, _c_i64, _c_i32, _vp, _c_i64, _vp, _c_i64, _c_i32, _vp, _vp]),
     "tace_nl_batch_fill": (_c_int, [_vp, _c_i64, _c_i32, _vp, _c_i64, _vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp]),
     "tace_rows_accumulate": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp]),
+    "tace_rows_accumulate_runs": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i32, _vp, _c_i64,
+                                           _vp]),
     "tace_scan_i32": (_c_int, [_vp, _c_i64, _vp, _vp]),
 }
 

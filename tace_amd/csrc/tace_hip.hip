@@ -117,7 +117,7 @@ template <typename T, int V>
 __global__ __launch_bounds__(256) void k_rows_accumulate(const T* __restrict__ rows, int64_t width,
                                                          const int* __restrict__ rowptr, const int* __restrict__ slot,
                                                          const int* __restrict__ target, int n_seg,
-                                                         T* __restrict__ out) {
+                                                         T* __restrict__ out, int run) {
   typedef T vec __attribute__((ext_vector_type(V)));
   const int sg = blockIdx.x;
   if (sg >= n_seg) return;
@@ -126,7 +126,9 @@ __global__ __launch_bounds__(256) void k_rows_accumulate(const T* __restrict__ r
   const int64_t t = target ? (int64_t)target[sg] : (int64_t)sg;
   for (int64_t j = (int64_t)threadIdx.x * V; j < width; j += 256 * V) {
     vec acc = (vec)(T(0));
-    for (int k = b; k < e; ++k) {
+    // run > 1: only the segment's first position and the multiples of run
+    // inside it hold rows (the other positions are parts of those runs)
+    for (int k = b; k < e; k = run > 1 ? (k / run + 1) * run : k + 1) {
       const int64_t r = slot ? (int64_t)slot[k] : (int64_t)k;
       acc += __builtin_nontemporal_load((const vec*)(rows + r * width + j));
     }
@@ -1407,9 +1409,27 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
   return check_launch("tace_nl_batch_fill");
 }
 
+static int rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                           const int32_t* slot, const int32_t* target, int64_t n_segments, int32_t run, void* out,
+                           int64_t n_out_rows, void* stream);
+
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream) {
+  return rows_accumulate(dtype, rows, n_rows, width, rowptr, slot, target, n_segments, 1, out, n_out_rows, stream);
+}
+
+int tace_rows_accumulate_runs(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                              const int32_t* target, int64_t n_segments, int32_t run, void* out, int64_t n_out_rows,
+                              void* stream) {
+  if (run < 1 || run > 1024) return fail("tace_rows_accumulate_runs: run must be 1..1024");
+  return rows_accumulate(dtype, rows, n_rows, width, rowptr, nullptr, target, n_segments, run, out, n_out_rows,
+                         stream);
+}
+
+static int rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
+                           const int32_t* slot, const int32_t* target, int64_t n_segments, int32_t run, void* out,
+                           int64_t n_out_rows, void* stream) {
   if (n_rows < 0 || width <= 0 || n_segments < 0 || n_segments > INT32_MAX || n_out_rows < 0)
     return fail("tace_rows_accumulate: bad sizes");
   if (n_segments == 0) return 0;
@@ -1422,17 +1442,17 @@ int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t wi
   if (dtype == TACE_F32) {
     if (vec)
       hipLaunchKernelGGL((k_rows_accumulate<float, 4>), g, b, 0, s, (const float*)rows, width, rowptr, slot, target,
-                         (int)n_segments, (float*)out);
+                         (int)n_segments, (float*)out, (int)run);
     else
       hipLaunchKernelGGL((k_rows_accumulate<float, 1>), g, b, 0, s, (const float*)rows, width, rowptr, slot, target,
-                         (int)n_segments, (float*)out);
+                         (int)n_segments, (float*)out, (int)run);
   } else if (dtype == TACE_F64) {
     if (vec)
       hipLaunchKernelGGL((k_rows_accumulate<double, 2>), g, b, 0, s, (const double*)rows, width, rowptr, slot, target,
-                         (int)n_segments, (double*)out);
+                         (int)n_segments, (double*)out, (int)run);
     else
       hipLaunchKernelGGL((k_rows_accumulate<double, 1>), g, b, 0, s, (const double*)rows, width, rowptr, slot,
-                         target, (int)n_segments, (double*)out);
+                         target, (int)n_segments, (double*)out, (int)run);
   } else {
     return fail("tace_rows_accumulate: dtype must be TACE_F32 or TACE_F64");
   }

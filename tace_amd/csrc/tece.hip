@@ -633,17 +633,15 @@ __device__ __forceinline__ void store_lane_sums(const T* p, int n, T* out, int l
 //   channels C..2C-1 (per edge; the caller sums them into the rows);
 //   g_W[e, r, k] = sum over the 2C channels of g[e,r,c] x[row(e,c), k, c];
 //   g_w[e, comp, c] = sum of g_mw[e,r,c] m[e,r,c] over the rows r of comp.
-template <typename T, int L, int NS>
-__global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, const T* __restrict__ W,
-                                                   const int64_t* __restrict__ rows_src,
-                                                   const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
-                                                   const Blk<const T> gms, const Blk<const T> gmd,
-                                                   const Blk<const T> gmw, int64_t n_rows, int64_t E, int C,
-                                                   T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
-                                                   T* __restrict__ gwr) {
+template <typename T, int L, int NS, bool RUNS>
+__device__ __forceinline__ void rotin_bwd_edge(const T* __restrict__ x, const T* __restrict__ W,
+                                               const int64_t* __restrict__ rows_src,
+                                               const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
+                                               const Blk<const T>& gms, const Blk<const T>& gmd,
+                                               const Blk<const T>& gmw, int64_t n_rows, int64_t E, int C, int64_t e,
+                                               T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
+                                               T* __restrict__ gwr, T* __restrict__ lrow) {
   constexpr int K = (L + 1) * (L + 1), P = (K * K + 15) / 16 * 16, NC = (L + 1) * (L + 2) / 2;
-  const int64_t e = wave_edge();
-  if (e >= E) return;
   const int lane = (int)threadIdx.x & 63;
   const T* w = W + e * K * K;
   const int64_t rs = rows_src[e], rd = rows_dst[e];
@@ -685,13 +683,15 @@ __global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, cons
           for (int q = 0; q < NC; ++q) gwr[(e * NC + q) * C2 + c] = gc[q];
         }
       }
-      T* gx = src ? gxs : gxd;
 #pragma unroll
       for (int kk = 0; kk < K; ++kk) {
         T a = 0;
 #pragma unroll
         for (int r = 0; r < K; ++r) a += w[r * K + kk] * g[r];
-        gx[(e * K + kk) * C + cc] = a;
+        if (RUNS && !src)
+          lrow[kk * C + cc] = a;
+        else
+          (src ? gxs : gxd)[(e * K + kk) * C + cc] = a;
       }
 #pragma unroll
       for (int r = 0; r < K; ++r)
@@ -700,6 +700,48 @@ __global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, cons
     }
   }
   store_lane_sums<T, P>(p, K * K, gW + e * K * K, lane);
+}
+
+// One edge per wavefront (4 per workgroup).
+// RUNS (edges in receiver-CSR order, dynamic LDS of 4 K C values): the four
+// edges of a workgroup put their receiver rows in LDS, and each run of edges
+// with the same receiver row writes one row, the run's sum in edge order, at
+// the run's first position; positions inside a run are left unwritten.  A
+// run starts at a receiver's first edge or at a multiple of 4, which is what
+// tace_rows_accumulate_runs reads (run = 4).
+template <typename T, int L, int NS, bool RUNS>
+__global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, const T* __restrict__ W,
+                                                   const int64_t* __restrict__ rows_src,
+                                                   const int64_t* __restrict__ rows_dst, const T* __restrict__ wr,
+                                                   const Blk<const T> gms, const Blk<const T> gmd,
+                                                   const Blk<const T> gmw, int64_t n_rows, int64_t E, int C,
+                                                   T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
+                                                   T* __restrict__ gwr) {
+  constexpr int K = (L + 1) * (L + 1);
+  extern __shared__ __attribute__((aligned(16))) unsigned char rb_raw[];
+  const int64_t e = wave_edge();
+  if (!RUNS && e >= E) return;
+  if (e < E) rotin_bwd_edge<T, L, NS, RUNS>(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, n_rows, E, C, e, gxs, gxd, gW,
+                                            gwr, (T*)rb_raw + (threadIdx.x >> 6) * K * C);
+  if constexpr (RUNS) {
+    __syncthreads();
+    const T* rows = (const T*)rb_raw;
+    const int64_t e0 = (int64_t)blockIdx.x * 4;
+    const int KC = K * C;
+    int64_t rd[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) rd[w] = e0 + w < E ? rows_dst[e0 + w] : -2;
+    for (int w = 0; w < 4 && e0 + w < E; ++w) {
+      if (w > 0 && rd[w] == rd[w - 1]) continue;   // inside a run
+      int w1 = w + 1;
+      while (w1 < 4 && rd[w1] == rd[w]) ++w1;
+      for (int i = (int)threadIdx.x; i < KC; i += 256) {
+        T v = rows[w * KC + i];
+        for (int u = w + 1; u < w1; ++u) v += rows[u * KC + i];
+        gxd[(e0 + w) * KC + i] = v;
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------- edge ACE --
@@ -1241,7 +1283,7 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
   const dim3 g = wave_grid(n_edges), b(256);
 #define RI_B(TT, LL)                                                                                          \
   TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                       \
-    hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,     \
+    hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS, false>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src,     \
                        rows_dst, (const TT*)radial_w, blocks_of<const TT>(g_m_src, lmax),                   \
                        blocks_of<const TT>(g_m_dst, lmax), blocks_of<const TT>(g_m_w, lmax), n_rows, n_edges,  \
                        channels, (TT*)g_x_src, (TT*)g_x_dst, (TT*)g_wigner, (TT*)g_radial_w))
@@ -1254,6 +1296,37 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
   }
 #undef RI_B
   return tace_check_launch("tace_edge_rotate_in_bwd");
+}
+
+int tace_edge_rotate_in_bwd_runs(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
+                                 const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
+                                 const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows,
+                                 int64_t n_edges, int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst_runs,
+                                 void* g_wigner, void* g_radial_w, void* stream) {
+  if (rotin_checks("tace_edge_rotate_in_bwd_runs", n_rows, n_edges, lmax, channels)) return -1;
+  const size_t es = dtype == TACE_F64 ? 8 : 4;
+  const size_t lds = (size_t)4 * (lmax + 1) * (lmax + 1) * channels * es;
+  if (lds > 65536) return tace_fail_msg("tace_edge_rotate_in_bwd_runs: 4 (lmax+1)^2 channels values exceed 64 KB of LDS");
+  if (n_edges == 0) return 0;
+  if (!x || !wigner || !rows_src || !rows_dst || !g_x_src || !g_x_dst_runs || !g_wigner || (g_m_w && !radial_w))
+    return tace_fail_msg("tace_edge_rotate_in_bwd_runs: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g = wave_grid(n_edges), b(256);
+#define RI_BR(TT, LL)                                                                                            \
+  TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                         \
+    hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS, true>), g, b, lds, s, (const TT*)x, (const TT*)wigner, rows_src, \
+                       rows_dst, (const TT*)radial_w, blocks_of<const TT>(g_m_src, lmax),                     \
+                       blocks_of<const TT>(g_m_dst, lmax), blocks_of<const TT>(g_m_w, lmax), n_rows, n_edges,    \
+                       channels, (TT*)g_x_src, (TT*)g_x_dst_runs, (TT*)g_wigner, (TT*)g_radial_w))
+  if (dtype == TACE_F32) {
+    if (lmax == 1) { RI_BR(float, 1) } else if (lmax == 2) { RI_BR(float, 2) } else { RI_BR(float, 3) }
+  } else if (dtype == TACE_F64) {
+    if (lmax == 1) { RI_BR(double, 1) } else if (lmax == 2) { RI_BR(double, 2) } else { RI_BR(double, 3) }
+  } else {
+    return tace_fail_msg("tace_edge_rotate_in_bwd_runs: dtype must be TACE_F32 or TACE_F64");
+  }
+#undef RI_BR
+  return tace_check_launch("tace_edge_rotate_in_bwd_runs");
 }
 
 int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, const int32_t* eid, int64_t n_nodes,

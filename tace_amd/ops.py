@@ -1033,9 +1033,25 @@ def launch_rotate_in_fwd(x, W, rows_src, rows_dst, wr, lmax: int, bf16_out: bool
     return ms, md, mw
 
 
-def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: bool):
+# the rotate-in backward's receiver rows as run sums of each workgroup's four
+# edges (tace_edge_rotate_in_bwd_runs) where the edges are in receiver-CSR
+# order and 4 K C values fit in 64 KB of LDS
+ROTIN_RUNS = 4
+
+
+def rotate_in_runs_ok(x: torch.Tensor) -> bool:
+    """Whether ``launch_rotate_in_bwd(..., runs=True)`` takes node features x [rows, K, C]."""
+    K, C = x.shape[1], x.shape[2]
+    return 4 * K * C * x.element_size() <= 65536
+
+
+def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: bool, runs: bool = False):
     """Per-edge grad_x rows of the senders / receivers [E, K, C] each, g_wigner
-    and (need_gwr) g_radial_w; gmw None = no gradient reaches m_w."""
+    and (need_gwr) g_radial_w; gmw None = no gradient reaches m_w.  runs
+    (edges in receiver-CSR order, ``rotate_in_runs_ok``): the receiver rows
+    come as run sums at the runs' first positions
+    (``tace_edge_rotate_in_bwd_runs``), for ``rows_accumulate(...,
+    run=ROTIN_RUNS)``."""
     Nr, K, C = x.shape
     E = W.shape[0]
     gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
@@ -1044,13 +1060,16 @@ def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: 
     gwr = None
     if wr is not None and need_gwr:
         gwr = torch.empty_like(wr) if gmw is not None else torch.zeros_like(wr)
+    if runs and not rotate_in_runs_ok(x):
+        raise ValueError("rotate-in backward by runs: 4 K C values exceed 64 KB")
+    name = "tace_edge_rotate_in_bwd_runs" if runs else "tace_edge_rotate_in_bwd"
     tok = _t0("edge_rotate_in_bwd")
-    N.check(N.lib().tace_edge_rotate_in_bwd(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
-                                            rows_dst.data_ptr(), N.ptr(wr), _block_array(gms), _block_array(gmd),
-                                            _block_array(gmw) if gmw is not None else None, Nr, E,
-                                            (int(math.isqrt(K)) - 1), C, gxs.data_ptr(), gxd.data_ptr(),
-                                            gW.data_ptr(), N.ptr(gwr) if gmw is not None else None,
-                                            N.stream_ptr(x.device)), "tace_edge_rotate_in_bwd")
+    N.check(getattr(N.lib(), name)(N.dtype_code(x.dtype), x.data_ptr(), W.data_ptr(), rows_src.data_ptr(),
+                                   rows_dst.data_ptr(), N.ptr(wr), _block_array(gms), _block_array(gmd),
+                                   _block_array(gmw) if gmw is not None else None, Nr, E,
+                                   (int(math.isqrt(K)) - 1), C, gxs.data_ptr(), gxd.data_ptr(),
+                                   gW.data_ptr(), N.ptr(gwr) if gmw is not None else None,
+                                   N.stream_ptr(x.device)), name)
     _t1(tok, (E, K, C, gmw is not None))
     return gxs, gxd, gW, gwr
 
@@ -1090,9 +1109,11 @@ def so2_gemm_bf16(a: torch.Tensor, b_frag: torch.Tensor, n: int, k: int,
 
 
 def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor, slot: Optional[torch.Tensor] = None,
-                    target: Optional[torch.Tensor] = None) -> torch.Tensor:
+                    target: Optional[torch.Tensor] = None, run: int = 1) -> torch.Tensor:
     """out[target[s]] += sum of rows[slot[k]], k in [rowptr[s], rowptr[s+1])
-    (``tace_rows_accumulate``: fixed order, no atomics); returns out."""
+    (``tace_rows_accumulate``: fixed order, no atomics); returns out.  run >
+    1 (slot None): only each segment's first position and the multiples of
+    run inside it are read (``tace_rows_accumulate_runs``)."""
     n_seg = rowptr.numel() - 1
     dt = out.dtype
     _req(out, "out", dt)
@@ -1102,10 +1123,17 @@ def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor,
         _req(slot, "slot", torch.int32, (rows.shape[0],))
     if target is not None:
         _req(target, "target", torch.int32, (n_seg,))
+    if run != 1 and slot is not None:
+        raise ValueError("rows_accumulate: run sums are read at CSR positions (slot must be None)")
     tok = _t0("rows_accumulate")
-    N.check(N.lib().tace_rows_accumulate(N.dtype_code(dt), rows.data_ptr(), rows.shape[0], out.shape[1],
-                                         rowptr.data_ptr(), N.ptr(slot), N.ptr(target), n_seg, out.data_ptr(),
-                                         out.shape[0], N.stream_ptr(out.device)), "tace_rows_accumulate")
+    if run != 1:
+        N.check(N.lib().tace_rows_accumulate_runs(N.dtype_code(dt), rows.data_ptr(), rows.shape[0], out.shape[1],
+                                                  rowptr.data_ptr(), N.ptr(target), n_seg, int(run), out.data_ptr(),
+                                                  out.shape[0], N.stream_ptr(out.device)), "tace_rows_accumulate_runs")
+    else:
+        N.check(N.lib().tace_rows_accumulate(N.dtype_code(dt), rows.data_ptr(), rows.shape[0], out.shape[1],
+                                             rowptr.data_ptr(), N.ptr(slot), N.ptr(target), n_seg, out.data_ptr(),
+                                             out.shape[0], N.stream_ptr(out.device)), "tace_rows_accumulate")
     _t1(tok, (rows.shape[0], out.shape[1], min(n_seg, out.shape[0])))
     return out
 

@@ -481,10 +481,13 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     gmd = [P.mm_grad(gq[m], P.q_N[m]) for m in range(L + 1)]
     del gq, gk
     gR = torch.mm(grp, P.rp_N)
-    gxs, gxd, gW_in, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True)
+    # edges in receiver-CSR order: the receiver rows come as run sums of each
+    # workgroup's four edges, a quarter of the rows to write and read back
+    runs = ops.ROTIN_RUNS if plan.eid is None and ops.rotate_in_runs_ok(x_lc) else 1
+    gxs, gxd, gW_in, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True, runs=runs > 1)
     Nr, E = x_lc.shape[0], rs.shape[0]
     g2 = gx.view(Nr, -1)
-    ops.rows_accumulate(g2, gxd.view(E, -1), plan.rowptr, plan.eid, recv_rows)
+    ops.rows_accumulate(g2, gxd.view(E, -1), plan.rowptr, plan.eid, recv_rows, run=runs)
     del gxd
     ops.rows_accumulate(g2, gxs.view(E, -1), *ops.sender_csr(rs, Nr))
     del gxs

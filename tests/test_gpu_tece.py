@@ -253,6 +253,52 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
     close(gx2, gx2_o, dtype, "grad x (weighted only)")
 
 
+@pytest.mark.parametrize("dtype,lmax,C", [(torch.float32, 2, 128), (torch.float32, 1, 64), (torch.float32, 3, 256),
+                                          (torch.float32, 2, 48), (torch.float64, 2, 64), (torch.float64, 1, 128)])
+def test_rotate_in_bwd_runs_equal_per_edge_rows(cuda, dtype, lmax, C):
+    """tace_edge_rotate_in_bwd_runs + tace_rows_accumulate_runs against
+    tace_edge_rotate_in_bwd + tace_rows_accumulate on edges in receiver-CSR
+    order: the sender rows, g_wigner and g_radial_w are the same bits (the
+    same per-edge code); the receiver sums added to a non-zero g_x equal the
+    per-edge rows' sums up to float rounding (runs of a workgroup's four
+    edges summed first).  Receivers with no edge, one edge, and runs that
+    start inside and at the edges of a workgroup; feature rows in another
+    order than the receivers."""
+    g = torch.Generator().manual_seed(lmax * 1000 + C)
+    N, E = 90, 2003
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    ei = _random_graph(N, E, g)
+    ei = ei[:, torch.argsort(ei[1], stable=True)]
+    counts = torch.bincount(ei[1], minlength=N)
+    rowptr = torch.zeros(N + 1, dtype=torch.int32)
+    rowptr[1:] = torch.cumsum(counts, 0).to(torch.int32)
+    node_map = torch.randperm(N, generator=g).to(torch.int32)
+    dv = lambda t: t.to(dtype).to(cuda)
+    x = dv(torch.randn(N, K, C, generator=g, dtype=torch.float64))
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = dv(W)
+    wr = dv(torch.randn(E, nc * 2 * C, generator=g, dtype=torch.float64))
+
+    def blocks(width):
+        return [dv(torch.randn(E * (1 if m == 0 else 2), (lmax + 1 - m) * width, generator=g, dtype=torch.float64))
+                for m in range(lmax + 1)]
+    gms, gmd, gmw = blocks(C), blocks(C), blocks(2 * C)
+    rs, rd = node_map[ei[0]].long().to(cuda), node_map[ei[1]].long().to(cuda)
+    assert ops.rotate_in_runs_ok(x)
+    base = dv(torch.randn(N, K, C, generator=g, dtype=torch.float64))
+    rp, nm = rowptr.to(cuda), node_map.to(cuda)
+    a = ops.launch_rotate_in_bwd(x, W, rs, rd, wr, gms, gmd, gmw, True)
+    b = ops.launch_rotate_in_bwd(x, W, rs, rd, wr, gms, gmd, gmw, True, runs=True)
+    for i, what in ((0, "sender rows"), (2, "g_wigner"), (3, "g_radial_w")):
+        assert torch.equal(a[i], b[i]), what
+    want, got = base.clone(), base.clone()
+    ops.rows_accumulate(want.view(N, -1), a[1].view(E, -1), rp, None, nm)
+    ops.rows_accumulate(got.view(N, -1), b[1].view(E, -1), rp, None, nm, run=ops.ROTIN_RUNS)
+    close(got, want, dtype, "receiver sums", tol=1e-13 if dtype == torch.float64 else 1e-6)
+    idle = node_map[(counts == 0).nonzero().flatten()].long().to(cuda)
+    assert idle.numel() >= 2 and torch.equal(got[idle], base[idle])
+
+
 # ------------------------------------------------------------- edge ACE ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("lmax,A", [(2, 32), (1, 16), (3, 8), (2, 20)])

@@ -87,6 +87,22 @@ def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float,
     return dict(positions=p64.to(dtype), node_attrs=attrs, lattice=lat, batch=batch, ptr=ptr.to(device), **g)
 
 
+_CELLS: Dict = {}
+
+
+def _device_cell(cell, dtype, device) -> torch.Tensor:
+    """The lattice [1, 3, 3] on the device, kept per (values, dtype, device):
+    an MD run passes the same cell every step.  Callers must not write to it."""
+    a = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(3, 3))
+    key = (a.tobytes(), str(dtype), str(device))
+    t = _CELLS.get(key)
+    if t is None:
+        if len(_CELLS) > 64:
+            _CELLS.clear()
+        t = _CELLS[key] = torch.as_tensor(a, dtype=dtype, device=device).view(1, 3, 3)
+    return t
+
+
 def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cutoff: float,
                    dtype=torch.float32) -> Dict[str, torch.Tensor]:
     """One periodic structure already resident on the GPU (float64 positions)
@@ -98,11 +114,13 @@ def resident_graph(pos64: torch.Tensor, cell, pbc, node_attrs: torch.Tensor, cut
     rowptr, src, sh = neighbour_list(pos64, cell, pbc, cutoff)
     counts = (rowptr[1:] - rowptr[:-1]).to(torch.int64)
     dst = torch.repeat_interleave(torch.arange(n, device=dev), counts, output_size=int(src.shape[0]))
+    # ptr [0, n] by a fill kernel, the lattice from a cache (host-to-device
+    # copies of pageable memory wait for the GPU to go idle)
+    ptr = torch.zeros(2, dtype=torch.int64, device=dev)
+    ptr[1:] = n
     d = dict(positions=pos64.to(dtype), node_attrs=node_attrs,
              edge_index=torch.stack([src.to(torch.int64), dst]), edge_shifts=sh.to(dtype),
-             lattice=torch.as_tensor(np.asarray(cell), dtype=dtype, device=dev).view(1, 3, 3),
-             batch=torch.zeros(n, dtype=torch.int64, device=dev),
-             ptr=torch.tensor([0, n], dtype=torch.int64, device=dev))
+             lattice=_device_cell(cell, dtype, dev), batch=torch.zeros(n, dtype=torch.int64, device=dev), ptr=ptr)
     d["_edge_plan"] = EdgePlan(n, int(src.shape[0]), rowptr, src, None)
     d["_shifts32"] = sh
     return d

@@ -44,6 +44,10 @@ class SpeciesPlan:
     one contiguous row range.  ``perm[r]`` = node stored in row r,
     ``node_map[n]`` (int32) = row of node n (what the edge kernels take)."""
 
+    # (attrs, its version, natural, the plan's fields) of the last plan made
+    # (the reference keeps attrs alive, so its identity cannot be reused)
+    _last = None
+
     def __init__(self, attrs: torch.Tensor, exchange=None, pairs: Optional[ops.EdgePairs] = None,
                  natural: bool = False):
         self.attrs = attrs
@@ -53,6 +57,14 @@ class SpeciesPlan:
         # edge pairs whose radial weights are made once (None: per edge)
         self.pairs = pairs
         self._pair_radial = None
+        # the same node_attrs tensor as the last plan's, unchanged (an MD run
+        # passes it every step): its order and species ranges again, without
+        # reading the species counts back to the host
+        last = SpeciesPlan._last
+        if (last is not None and last[0] is attrs and last[1] == attrs._version and last[2] == natural
+                and not attrs.requires_grad):
+            self.species, self.perm, self.inv, self.node_map, self.ranges = last[3]
+            return
         species = attrs.argmax(dim=-1)
         self.species = species
         if natural:
@@ -60,19 +72,22 @@ class SpeciesPlan:
             # group them inside their operator (tace_amd::element_linear)
             self.perm = self.inv = torch.arange(attrs.shape[0], device=attrs.device)
             self.node_map, self.ranges = None, None
-            return
-        self.perm = torch.argsort(species, stable=True)
-        inv = torch.empty_like(self.perm)
-        inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
-        self.inv = inv
-        self.node_map = inv.to(torch.int32)
-        counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
-        self.ranges = []
-        acc = 0
-        for s, c in enumerate(counts):
-            if c:
-                self.ranges.append((s, acc, acc + c))
-            acc += c
+        else:
+            self.perm = torch.argsort(species, stable=True)
+            inv = torch.empty_like(self.perm)
+            inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
+            self.inv = inv
+            self.node_map = inv.to(torch.int32)
+            counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
+            self.ranges = []
+            acc = 0
+            for s, c in enumerate(counts):
+                if c:
+                    self.ranges.append((s, acc, acc + c))
+                acc += c
+        if not attrs.requires_grad:
+            SpeciesPlan._last = (attrs, attrs._version, natural,
+                                 (self.species, self.perm, self.inv, self.node_map, self.ranges))
 
     def pair_radial(self, R: torch.Tensor) -> torch.Tensor:
         """R's rows of the edge pairs' lower edges (the radial MLP's input),
@@ -1047,10 +1062,22 @@ class Representation(torch.nn.Module):
             self.products.append(prod)
             irreps = prod.irreps_out
 
+    def _basis_scalars(self):
+        """(prefactor, cutoff, p) of the radial basis as Python numbers, read
+        from the buffers once and again only after a buffer is replaced or
+        written (reading a device scalar stops the host until the GPU idles)."""
+        rb = self.radial_basis
+        bufs = (rb.radial_fn.prefactor, rb.cutoff_fn.cutoff, rb.cutoff_fn.p)
+        key = tuple((id(b), b._version) if torch.is_tensor(b) else (None, b) for b in bufs)
+        cached = getattr(self, "_basis_cache", None)
+        if cached is None or cached[0] != key or any(c is not b for c, b in zip(cached[2], bufs)):
+            self._basis_cache = (key, (float(bufs[0]), float(bufs[1]), int(bufs[2])), bufs)
+        return self._basis_cache[1]
+
     def edge_features(self, edge_vector: torch.Tensor):
         rb = self.radial_basis
-        return ops.edge_basis(edge_vector, rb.radial_fn.bessel_weights.to(edge_vector.dtype),
-                              float(rb.radial_fn.prefactor), float(rb.cutoff_fn.cutoff), int(rb.cutoff_fn.p),
+        pref, cut, p = self._basis_scalars()
+        return ops.edge_basis(edge_vector, rb.radial_fn.bessel_weights.to(edge_vector.dtype), pref, cut, p,
                               self.lmax)
 
     def forward(self, attrs, plan: ops.EdgePlan, edge_vector, sp: SpeciesPlan, edge_index=None):

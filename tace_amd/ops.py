@@ -183,9 +183,12 @@ class EdgePlan:
         if self._sender is None:
             slot_src = self.src.long() if self.eid is None else self.src.long()[self.eid.long()]
             order = torch.argsort(slot_src, stable=True).to(torch.int32).contiguous()
-            counts = torch.bincount(slot_src, minlength=self.n_nodes)
-            rp = torch.zeros(self.n_nodes + 1, dtype=torch.int64, device=self.src.device)
-            rp[1:] = torch.cumsum(counts, 0)
+            # counts by index_add_ (integer sums: exact in any order; bincount
+            # would read the largest index back to the host)
+            dev = self.src.device
+            rp = torch.zeros(self.n_nodes + 1, dtype=torch.int64, device=dev)
+            rp[1:].index_add_(0, slot_src, torch.ones_like(slot_src))
+            rp = torch.cumsum(rp, 0)
             self._sender = (rp.to(torch.int32).contiguous(), order)
         return self._sender
 

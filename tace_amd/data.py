@@ -73,18 +73,22 @@ def gpu_graph(structs: List[Dict], atomic_numbers: Sequence[int], cutoff: float,
     """Batch built on the GPU (``device_graph``) from host structures; the
     result carries its receiver CSR plan."""
     sizes = [len(s["positions"]) for s in structs]
-    p64 = torch.as_tensor(np.concatenate([np.asarray(s["positions"], dtype=np.float64).reshape(-1, 3)
-                                          for s in structs]), device=device)
+    dev = torch.device(device)
+    up = lambda t: t.to(dev)
+    p64 = up(torch.from_numpy(np.concatenate([np.asarray(s["positions"], dtype=np.float64).reshape(-1, 3)
+                                              for s in structs])))
     g = device_graph(p64, sizes, [s["cell"] for s in structs], [s["pbc"] for s in structs], cutoff)
     sizes_t = torch.tensor(sizes, dtype=torch.int64)
-    batch = torch.repeat_interleave(torch.arange(len(structs)), sizes_t).to(device)
+    batch = up(torch.repeat_interleave(torch.arange(len(structs)), sizes_t))
     ptr = torch.zeros(len(structs) + 1, dtype=torch.int64)
     ptr[1:] = torch.cumsum(sizes_t, 0)
-    attrs = torch.cat([one_hot(s["numbers"], atomic_numbers, dtype) for s in structs]).to(device)
-    lat = torch.as_tensor(np.stack([np.asarray(s["cell"], dtype=np.float64).reshape(3, 3) for s in structs]),
-                          dtype=dtype, device=device)
+    attrs_h = torch.cat([one_hot(s["numbers"], atomic_numbers, dtype) for s in structs])
+    lat = up(torch.from_numpy(np.stack([np.asarray(s["cell"], dtype=np.float64).reshape(3, 3)
+                                        for s in structs])).to(dtype))
     g["edge_shifts"] = g["edge_shifts"].to(dtype)
-    return dict(positions=p64.to(dtype), node_attrs=attrs, lattice=lat, batch=batch, ptr=ptr.to(device), **g)
+    # per-species node counts (columns of node_attrs), known here on the host
+    g["_species_counts"] = attrs_h.sum(0).to(torch.int64).tolist()
+    return dict(positions=p64.to(dtype), node_attrs=up(attrs_h), lattice=lat, batch=batch, ptr=up(ptr), **g)
 
 
 _CELLS: Dict = {}

@@ -49,7 +49,9 @@ class SpeciesPlan:
     _last = None
 
     def __init__(self, attrs: torch.Tensor, exchange=None, pairs: Optional[ops.EdgePairs] = None,
-                 natural: bool = False):
+                 natural: bool = False, counts: Optional[List[int]] = None):
+        """counts: the number of nodes of each species (attrs column), when
+        the caller knows them on the host; else they are read back from attrs."""
         self.attrs = attrs
         # LAMMPS ML-IAP data whose forward_exchange fills ghost rows before
         # every interaction layer >= 1 (several domains), or None
@@ -78,7 +80,8 @@ class SpeciesPlan:
             inv[self.perm] = torch.arange(len(self.perm), device=self.perm.device)
             self.inv = inv
             self.node_map = inv.to(torch.int32)
-            counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
+            if counts is None or len(counts) != attrs.shape[1]:
+                counts = torch.bincount(species, minlength=attrs.shape[1]).tolist()
             self.ranges = []
             acc = 0
             for s, c in enumerate(counts):
@@ -1139,7 +1142,7 @@ class TACE(torch.nn.Module):
         so callers that want per-edge gradients pass None)."""
         attrs, batch, ptr = data["node_attrs"], data["batch"], data["ptr"]
         num_graphs = ptr.numel() - 1
-        sp = SpeciesPlan(attrs, exchange, pairs, natural=ops.MODE.export)
+        sp = SpeciesPlan(attrs, exchange, pairs, natural=ops.MODE.export, counts=_opt(data, "_species_counts"))
         x = self.representation(attrs, plan, edge_vector, sp, data["edge_index"])
         e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order

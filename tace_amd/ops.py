@@ -218,18 +218,39 @@ class EdgePlan:
         return EdgePlan(n_nodes, E, rowptr.to(torch.int32).contiguous(), src.to(torch.int32).contiguous(), eid)
 
 
-@dataclass
 class EdgePairs:
     """The two directions of every edge (``tace_edge_pairs``): ``w_rows``
     (int32 [E], by edge id) the row of each edge's pair, ``row_edges`` /
     ``row_partner`` (int32 [n_rows]) the lower edge id of each row and its
     reverse (-1: none).  A weight that depends on the edge length only is made
-    once per row."""
+    once per row.
 
-    n_rows: int
-    w_rows: torch.Tensor
-    row_edges: torch.Tensor
-    row_partner: torch.Tensor
+    The row count is made on the GPU; it is copied to pinned host memory
+    without waiting, and the host waits for that copy only when ``n_rows``
+    (or a row array) is first needed, by which time the GPU has later work
+    queued and does not run dry."""
+
+    def __init__(self, n_rows, w_rows: torch.Tensor, row_edges: torch.Tensor, row_partner: torch.Tensor):
+        # n_rows: an int, or (pinned host int32 [1], event recorded after its copy)
+        self._n = n_rows
+        self.w_rows = w_rows
+        self._row_edges, self._row_partner = row_edges, row_partner
+
+    @property
+    def n_rows(self) -> int:
+        if not isinstance(self._n, int):
+            host, ev = self._n
+            ev.synchronize()
+            self._n = int(host[0])
+        return self._n
+
+    @property
+    def row_edges(self) -> torch.Tensor:
+        return self._row_edges[:self.n_rows]
+
+    @property
+    def row_partner(self) -> torch.Tensor:
+        return self._row_partner[:self.n_rows]
 
 
 def edge_pairs(plan: EdgePlan, shifts: torch.Tensor) -> EdgePairs:
@@ -248,8 +269,11 @@ def edge_pairs(plan: EdgePlan, shifts: torch.Tensor) -> EdgePairs:
                                     row_edges.data_ptr(), row_partner.data_ptr(), N.stream_ptr(dev)),
             "tace_edge_pairs")
     _t1(tok, (E,))
-    n_rows = int(work[3 * E].item())
-    return EdgePairs(n_rows, w_rows, row_edges[:n_rows], row_partner[:n_rows])
+    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    host.copy_(work[3 * E:3 * E + 1], non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record(torch.cuda.current_stream(dev))
+    return EdgePairs((host, ev), w_rows, row_edges, row_partner)
 
 
 # ------------------------------------------------------- edge featurisation ----
@@ -1161,9 +1185,11 @@ def sender_csr(rows_src: torch.Tensor, n_rows: int) -> Tuple[torch.Tensor, torch
     """(rowptr int32 [n_rows+1], slot int32 [E]): the edges grouped by sender
     row, in edge order within a sender."""
     slot = torch.argsort(rows_src, stable=True).to(torch.int32)
+    # counts by index_add_ (exact integer sums; bincount reads the largest
+    # index back to the host)
     rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=rows_src.device)
-    rp[1:] = torch.cumsum(torch.bincount(rows_src, minlength=n_rows), 0)
-    return rp.to(torch.int32), slot
+    rp[1:].index_add_(0, rows_src, torch.ones_like(rows_src))
+    return torch.cumsum(rp, 0).to(torch.int32), slot
 
 
 def _pad4(lst):

@@ -118,11 +118,14 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
         return s * E * (2 * K * C + K * K + (2 * nc * C if has_w else 0)) + so * E * (2 * K * C + (2 * K * C if has_w else 0)) \
             + 16 * E
     if name.startswith("edge_rotate_in_bwd"):
-        E, K, C, has_w = info
+        E, K, C, has_w = info[:4]
+        runs = len(info) > 4 and info[4]
         nc = (int(math.isqrt(K)) * (int(math.isqrt(K)) + 1)) // 2
-        # x_src, x_dst, g_m_src, g_m_dst, W read; per-edge grad_x rows and g_W
-        # written; with radial weights also g_m_w and w read, g_w written
-        return s * E * (6 * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
+        # x_src, x_dst, g_m_src, g_m_dst, W read; per-edge sender grad_x rows
+        # and g_W written, receiver grad_x rows per edge or (runs) one per run
+        # of a workgroup's four edges, counted as a quarter row per edge; with
+        # radial weights also g_m_w and w read, g_w written
+        return s * E * ((5.25 if runs else 6) * K * C + 2 * K * K + (2 * K * C + 4 * nc * C if has_w else 0)) + 16 * E
     if name.startswith("tece_edge_ace_fwd") or name.startswith("tece_edge_ace_bwd"):
         E, A, L, b16 = info
         n, P = L + 1, len(ops.edge_ace_paths(L))

@@ -1097,7 +1097,7 @@ def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: 
                                    (int(math.isqrt(K)) - 1), C, gxs.data_ptr(), gxd.data_ptr(),
                                    gW.data_ptr(), N.ptr(gwr) if gmw is not None else None,
                                    N.stream_ptr(x.device)), name)
-    _t1(tok, (E, K, C, gmw is not None))
+    _t1(tok, (E, K, C, gmw is not None, bool(runs)))
     return gxs, gxd, gW, gwr
 
 

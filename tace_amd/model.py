@@ -750,9 +750,11 @@ class TeceInteraction(torch.nn.Module):
         self.C = C
         self._gate_lay = (GMLayout(self.linear_down.irreps_out), GMLayout(self.gated))
         # edges per receiver chunk: above this the convolution runs chunk by
-        # chunk and recomputes its per-edge intermediates (~100 KB per edge at
-        # C=128) in the backward instead of keeping them
-        self.chunk_edges = 1 << 18
+        # chunk (the fused operator keeps a chunk's intermediates for the
+        # backward while HBM allows, else recomputes them).  At the 101k-atom
+        # bcc Fe box: 2^18 -> 333, 2^19 -> 321, 2^20 -> 317 ms/step (171, 180,
+        # 196 GB peak); 2^21: 316 ms at 230 GB
+        self.chunk_edges = 1 << 20
 
     def forward(self, x, sp: SpeciesPlan, R, plan: ops.EdgePlan, src, dst, wigner):
         from . import tece

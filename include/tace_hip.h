@@ -300,7 +300,9 @@ int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes,
  * each over a column range, with the weights split in MFMA fragment order
  * (tace_bf16x3_split_blocks layout 1).  task_rows is 128 (every task's k <=
  * 128) or 64 (k <= 256): tace_seg_linear_ks_rows(k) gives the height for k
- * (0: not supported); one call takes tasks of one height:
+ * (0: not supported); one call takes tasks of one height.  A task whose k
+ * exceeds its height's limit (128 for 128-row tasks, 256 for 64-row tasks)
+ * gets NaN in every output of its tile:
  *   tasks int64 [n_tasks, 10]: out_base (offset of the tile's row 0, column 0
  *         in y), rows (1..task_rows), n (block width = row stride of y), cb, ce (its
  *         columns [cb, ce), ce <= n), bias_off (-1 none), x_base (offset of
@@ -486,6 +488,16 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream);
+/* Per-graph sums of node rows: out[g, :] = sum over k in [ptr[g], ptr[g+1])
+ * of values[k, :] (rows of `width` values, 0 < width <= 4096; out is
+ * overwritten), in a fixed order that depends only on the graph's size, so
+ * the same bits on every run.  Replaces the atomics of scatter_sum(x, batch)
+ * (tace/utils/torch_scatter.py:43-62) for the graph energies
+ * (tace/models/_e3nn/tace.py:364, 416) and for the backward of the strain
+ * gather sym[batch] (tace/models/utils.py:50-79).  ptr is a trusted device
+ * array of n_graphs + 1 non-decreasing offsets within [0, n_rows]. */
+int tace_graph_sum(int dtype, const void* values, int64_t n_rows, int64_t width, const int64_t* ptr,
+                   int64_t n_graphs, void* out, void* stream);
 /* tace_rows_accumulate over the CSR positions themselves (slot NULL) that
  * only reads each segment's first position and the multiples of `run`
  * inside it: the run sums tace_edge_rotate_in_bwd_runs writes (run = 4). */

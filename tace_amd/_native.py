@@ -96,6 +96,7 @@ _SIGS = {
     "tace_nl_batch_count": (_c_int, [_vp, _c_i64, _c_i32, _vp, _c_i64, _vp, _c_i64, _c_i32, _vp, _vp]),
     "tace_nl_batch_fill": (_c_int, [_vp, _c_i64, _c_i32, _vp, _c_i64, _vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp]),
     "tace_rows_accumulate": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp]),
+    "tace_graph_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
     "tace_rows_accumulate_runs": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i32, _vp, _c_i64,
                                            _vp]),
     "tace_scan_i32": (_c_int, [_vp, _c_i64, _vp, _vp]),

@@ -884,6 +884,15 @@ __global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __res
   const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
   const int grp = wv >> 2, wq = wv & 3;
   const int fr = lane & 15, fg = lane >> 4;
+  if (k < 0 || k > KM) {
+    // outside this instantiation's k range: NaN outputs instead of a product
+    // of a truncated A tile (the host table builder never makes such tasks)
+    for (int u = t; u < T.rows * (T.ce - T.cb); u += KS_THREADS) {
+      const int r = u / (T.ce - T.cb), c = T.cb + (u - r * (T.ce - T.cb));
+      y[T.out_base + (int64_t)r * T.n + c] = __builtin_nanf("");
+    }
+    return;
+  }
 
   // A: rows x k of x (row stride k) -> planes, zeros past rows and past k
   // (up to the next multiple of 32)

@@ -126,7 +126,7 @@ __device__ __forceinline__ void g_strip(const unsigned short* __restrict__ As, c
       if (r >= J.rows || col >= J.n) continue;
       const gf4 v = h ? s1 : s0;
       float* dst = J.out + (int64_t)r * J.ldo + col;
-      if (vst) {
+      if (vst && col + 4 <= J.n) {
         *(gf4*)dst = v;
       } else {
 #pragma unroll

@@ -137,6 +137,29 @@ __global__ __launch_bounds__(256) void k_rows_accumulate(const T* __restrict__ r
   }
 }
 
+// out[g, j] = sum of v[k, j] over the rows k in [ptr[g], ptr[g+1]): one
+// workgroup per graph, thread t sums rows ptr[g] + t + 256 i in order, then a
+// fixed tree over the 256 partial sums -- the same bits on every run.
+template <typename T>
+__global__ __launch_bounds__(256) void k_graph_sum(const T* __restrict__ v, int64_t width,
+                                                   const int64_t* __restrict__ ptr, T* __restrict__ out) {
+  __shared__ T sh[256];
+  const int g = (int)blockIdx.x, t = (int)threadIdx.x;
+  const int64_t b = ptr[g], e = ptr[g + 1];
+  for (int64_t j = 0; j < width; ++j) {
+    T acc = T(0);
+    for (int64_t k = b + t; k < e; k += 256) acc += v[k * width + j];
+    sh[t] = acc;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+      if (t < o) sh[t] += sh[t + o];
+      __syncthreads();
+    }
+    if (t == 0) out[(int64_t)g * width + j] = sh[0];
+    __syncthreads();
+  }
+}
+
 // gy = sum of the per-part grad_y partials, in part order
 template <typename T>
 __global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, int nparts, int64_t n,
@@ -454,11 +477,21 @@ __global__ __launch_bounds__(256) void k_scan_apply(const int* __restrict__ cnt,
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == 255) out[m] = run;
 }
 
+// The partner of e when the pairing is mutual, else -1: a zero-shift self
+// edge finds itself, and of duplicated edges only the first pair is mutual;
+// every other copy keeps a row of its own.
+__device__ __forceinline__ int mutual_partner(const int* __restrict__ partner, int e) {
+  const int p = partner[e];
+  return (p >= 0 && p != e && partner[p] == e) ? p : -1;
+}
+
 // owner[e] = 1 when e carries its pair's row (the lower id of a pair, or an
 // edge without a partner)
 __global__ void k_edge_owner(const int* __restrict__ partner, int E, int* __restrict__ owner) {
   const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-  if (e < E) owner[e] = (partner[e] < 0 || partner[e] > e) ? 1 : 0;
+  if (e >= E) return;
+  const int p = mutual_partner(partner, e);
+  owner[e] = (p < 0 || p > e) ? 1 : 0;
 }
 
 // rank = exclusive scan of owner: w_rows[e] = the row of e's pair;
@@ -467,7 +500,7 @@ __global__ void k_edge_rows(const int* __restrict__ partner, const int* __restri
                             int* __restrict__ w_rows, int* __restrict__ row_edges, int* __restrict__ row_partner) {
   const int e = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (e >= E) return;
-  const int p = partner[e];
+  const int p = mutual_partner(partner, e);
   if (p < 0 || p > e) {
     const int r = rank[e];
     w_rows[e] = r;
@@ -1417,6 +1450,24 @@ int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t wi
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream) {
   return rows_accumulate(dtype, rows, n_rows, width, rowptr, slot, target, n_segments, 1, out, n_out_rows, stream);
+}
+
+int tace_graph_sum(int dtype, const void* values, int64_t n_rows, int64_t width, const int64_t* ptr,
+                   int64_t n_graphs, void* out, void* stream) {
+  if (n_rows < 0 || width <= 0 || width > 4096 || n_graphs < 0 || n_graphs > INT32_MAX)
+    return fail("tace_graph_sum: bad sizes (0 < width <= 4096)");
+  if (n_graphs == 0) return 0;
+  if (!ptr || !out || (n_rows > 0 && !values)) return fail("tace_graph_sum: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    hipLaunchKernelGGL(k_graph_sum<float>, dim3((unsigned)n_graphs), dim3(256), 0, s, (const float*)values, width, ptr,
+                       (float*)out);
+  else if (dtype == TACE_F64)
+    hipLaunchKernelGGL(k_graph_sum<double>, dim3((unsigned)n_graphs), dim3(256), 0, s, (const double*)values, width,
+                       ptr, (double*)out);
+  else
+    return fail("tace_graph_sum: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_graph_sum");
 }
 
 int tace_rows_accumulate_runs(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,

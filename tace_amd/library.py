@@ -38,6 +38,49 @@ from . import ops
 Tensor = torch.Tensor
 
 
+# ------------------------------------------------------------ per graph ----
+# Per-graph sums of node rows and their transpose (the gather of per-graph
+# rows to the nodes), each the other's backward: the energy sum and the strain
+# displacement of stress (``scatter_sum(..., batch)``, tace/models/_e3nn/tace.py:364, 416;
+# ``sym[batch]``, tace/models/utils.py:50-79) in a fixed order.
+@torch.library.custom_op("tace_amd::graph_sum", mutates_args=(), device_types="cuda")
+def graph_sum(values: Tensor, ptr: Tensor, batch: Tensor) -> Tensor:
+    return ops._graph_sum(values, ptr)
+
+
+@graph_sum.register_fake
+def _graph_sum_fake(values, ptr, batch):
+    return values.new_empty((ptr.shape[0] - 1,) + tuple(values.shape[1:]))
+
+
+@torch.library.custom_op("tace_amd::graph_gather", mutates_args=(), device_types="cuda")
+def graph_gather(values: Tensor, ptr: Tensor, batch: Tensor) -> Tensor:
+    return values.index_select(0, batch)
+
+
+@graph_gather.register_fake
+def _graph_gather_fake(values, ptr, batch):
+    return values.new_empty((batch.shape[0],) + tuple(values.shape[1:]))
+
+
+def _graph_setup(ctx, inputs, output):
+    ctx.save_for_backward(inputs[1], inputs[2])
+
+
+def _graph_sum_backward(ctx, g):
+    ptr, batch = ctx.saved_tensors
+    return graph_gather(g, ptr, batch), None, None
+
+
+def _graph_gather_backward(ctx, g):
+    ptr, batch = ctx.saved_tensors
+    return graph_sum(g, ptr, batch), None, None
+
+
+graph_sum.register_autograd(_graph_sum_backward, setup_context=_graph_setup)
+graph_gather.register_autograd(_graph_gather_backward, setup_context=_graph_setup)
+
+
 # ------------------------------------------------------------------- uvu ----
 @torch.library.custom_op("tace_amd::uvu_scatter", mutates_args=(), device_types="cuda")
 def uvu_scatter(x: Tensor, y: Tensor, w: Tensor, edge_index: Tensor, key: str, channels: int,

@@ -1158,8 +1158,10 @@ class TACE(torch.nn.Module):
         e_node = e_node * torch.where(isolated, torch.zeros_like(scale), scale)
         shift = (attrs * self.scale_shift.shift[0]).sum(-1)
         e_node = e_node + torch.where(isolated, torch.zeros_like(shift), shift)
-        zeros = torch.zeros(num_graphs, dtype=attrs.dtype, device=attrs.device)
-        E = zeros.index_add(0, batch, e_base) + zeros.index_add(0, batch, e_node)
+        # scatter_sum of the base and the model energies (tace.py:364, 416), per
+        # graph in node order
+        sums = ops.graph_sum(torch.stack([e_base, e_node], 1), ptr, batch)
+        E = sums[:, 0] + sums[:, 1]
         return E, e_base + e_node
 
 
@@ -1417,7 +1419,7 @@ class TensorModel(torch.nn.Module):
             # compute_symmetric_displacement (tace/models/utils.py:50-79)
             disp = torch.zeros(num_graphs, 3, 3, dtype=pos.dtype, device=pos.device, requires_grad=True)
             sym = 0.5 * (disp + disp.transpose(-1, -2))
-            pos_s = pos + torch.einsum("be,bec->bc", pos, sym[batch])
+            pos_s = pos + torch.einsum("be,bec->bc", pos, ops.graph_gather(sym, data["ptr"], batch))
             lat_s = lattice + torch.matmul(lattice, sym)
             inputs.append(disp)
         else:

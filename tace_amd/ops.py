@@ -1165,6 +1165,77 @@ def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor,
     return out
 
 
+def _graph_sum(values: torch.Tensor, ptr: torch.Tensor) -> torch.Tensor:
+    """[N, w] rows -> [B, w] sums over the contiguous node ranges of ``ptr``
+    [B + 1], each range summed in node order (``tace_rows_accumulate``)."""
+    v = values.reshape(values.shape[0], -1).contiguous()
+    _req(v, "values", v.dtype)
+    p = ptr if ptr.dtype == torch.int64 else ptr.to(torch.int64)
+    p = p.contiguous()
+    _req(p, "ptr", torch.int64, (p.numel(),))
+    out = torch.empty(p.numel() - 1, v.shape[1], dtype=v.dtype, device=v.device)
+    tok = _t0("graph_sum")
+    N.check(N.lib().tace_graph_sum(N.dtype_code(v.dtype), v.data_ptr(), v.shape[0], v.shape[1], p.data_ptr(),
+                                   out.shape[0], out.data_ptr(), N.stream_ptr(v.device)), "tace_graph_sum")
+    _t1(tok, (v.shape[0], v.shape[1], out.shape[0]))
+    return out.reshape((p.numel() - 1,) + tuple(values.shape[1:]))
+
+
+class _GraphSum(torch.autograd.Function):
+    """Per-graph sums of node rows in a fixed order (``scatter_sum(..., batch)``
+    of ``tace/utils/torch_scatter.py:43-62`` without atomics); backward: the
+    graph's gradient gathered to its nodes (``_GraphGather``)."""
+
+    @staticmethod
+    def forward(ctx, values, ptr, batch):
+        ctx.save_for_backward(ptr, batch)
+        return _graph_sum(values, ptr)
+
+    @staticmethod
+    def backward(ctx, g):
+        ptr, batch = ctx.saved_tensors
+        return _GraphGather.apply(g, ptr, batch), None, None
+
+
+class _GraphGather(torch.autograd.Function):
+    """values[batch] for per-graph rows; backward: per-graph sums in a fixed
+    order (``_GraphSum``), so both directions are repeatable bit for bit."""
+
+    @staticmethod
+    def forward(ctx, values, ptr, batch):
+        ctx.save_for_backward(ptr, batch)
+        return values.index_select(0, batch)
+
+    @staticmethod
+    def backward(ctx, g):
+        ptr, batch = ctx.saved_tensors
+        return _GraphSum.apply(g, ptr, batch), None, None
+
+
+def graph_sum(values: torch.Tensor, ptr: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
+    """Sum of node rows ``values`` [N, ...] per graph ([B, ...]); the nodes of
+    graph b are rows ptr[b]..ptr[b+1]-1 and ``batch`` [N] their graph
+    (collated batches hold both).  The same bits on every run, differentiable
+    (twice as well)."""
+    if MODE.export:
+        from . import library
+        return library.graph_sum(values, ptr, batch)
+    if not values.is_cuda:
+        return torch.zeros((ptr.numel() - 1,) + tuple(values.shape[1:]), dtype=values.dtype,
+                           device=values.device).index_add(0, batch, values)
+    return _GraphSum.apply(values, ptr, batch)
+
+
+def graph_gather(values: torch.Tensor, ptr: torch.Tensor, batch: torch.Tensor) -> torch.Tensor:
+    """``values[batch]`` for per-graph rows, with a fixed-order backward."""
+    if MODE.export:
+        from . import library
+        return library.graph_gather(values, ptr, batch)
+    if not values.is_cuda:
+        return values.index_select(0, batch)
+    return _GraphGather.apply(values, ptr, batch)
+
+
 def scatter_add_rows(out: torch.Tensor, index: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
     """out[index[e]] += src[e] (rows of any trailing shape).  On the GPU
     every row's terms are summed in edge order by ``tace_rows_accumulate``
@@ -1615,6 +1686,8 @@ class SegLinearPlan:
                 if len(sel):
                     if (sel[:, 1] > R).any():
                         raise ValueError("seg linear plan: a task is taller than its kernel's tile")
+                    if (sel[:, 7] > (128 if R == 128 else 256)).any():
+                        raise ValueError("seg linear plan: a task's k exceeds its kernel's limit")
                     self.ks_groups.append((R, len(sel), torch.from_numpy(np.ascontiguousarray(sel)).to(device)))
 
     @staticmethod

@@ -696,3 +696,24 @@ def test_so2_gemm_bf16_matches_float32_product(cuda, m, k, n, bias, pad):
     scale = (a.float().abs() @ B.float().abs()).amax(1, keepdim=True) + 1e-30
     err = ((got - want).abs() / scale).max().item()
     assert got.shape == (m, n) and err < 2e-6, err
+
+
+@pytest.mark.parametrize("n,ldo", [(6, 8), (70, 76), (33, 40)])
+def test_so2_gemm_bf16_padded_output_rows_untouched(cuda, n, ldo):
+    """Through the C ABI with an output row stride above n: columns n..ldo-1
+    of every row (a strided view's neighbours) keep their sentinel."""
+    from tace_amd import _native as N
+    m, k = 300, 96
+    g = torch.Generator().manual_seed(n)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16).to(cuda)
+    B = torch.randn(k, n, generator=g).to(torch.bfloat16).to(cuda)
+    bias = torch.randn(n, generator=g).to(cuda)
+    bf = ops.bf16_fragment_order(B)
+    out = torch.full((m, ldo), 12345.0, dtype=torch.float32, device=cuda)
+    N.check(N.lib().tace_so2_gemm_bf16(a.data_ptr(), k, bf.data_ptr(), bias.data_ptr(), out.data_ptr(), ldo, m, n, k,
+                                       N.stream_ptr(a.device)), "tace_so2_gemm_bf16")
+    torch.cuda.synchronize()
+    assert bool((out[:, n:] == 12345.0).all()), "the kernel wrote past column n"
+    want = a.float() @ B.float() + bias
+    scale = (a.float().abs() @ B.float().abs()).amax(1, keepdim=True) + 1e-30
+    assert ((out[:, :n] - want).abs() / scale).max().item() < 2e-6

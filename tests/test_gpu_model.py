@@ -179,3 +179,58 @@ def test_batched_gpu_neighbour_list_feeds_model(cuda):
     assert (a["energy"] - b["energy"]).abs().max().item() < 1e-10 * a["energy"].abs().max().item()
     assert (a["forces"] - b["forces"]).abs().max().item() < 1e-10
     assert (a["stress"] - b["stress"]).abs().max().item() < 1e-10
+
+
+@pytest.mark.parametrize("which", ["water", "ragged"])
+def test_energies_forces_stress_repeat_bit_for_bit(cuda, which):
+    """Every reduction on the path runs in a fixed order (receiver and sender
+    CSR sums, per-graph sums of the energies and of the strain gradient), so
+    repeated evaluations give the same bits: a water box and a ragged batch
+    with stress, float32."""
+    if which == "water":
+        structs, preset, over = [structures.water_box(n_side=6, box=49.7 / 16 * 6, seed=7)], "water12k", {}
+    else:
+        rng = np.random.default_rng(9)
+        structs = [structures.random_crystal(rng, int(rng.integers(8, 60)), [1, 8, 14, 26, 29]) for _ in range(12)]
+        preset, over = "ragged128", dict(num_channel=32)
+    zs = sorted({int(z) for s in structs for z in s["numbers"]})
+    rc = configs.PRESETS[preset]["cutoff"]
+    cfg = configs.model_cfg(preset, zs, 40.0, **over)
+    torch.manual_seed(2)
+    gpu = pm.create_model(cfg).to(cuda).eval()
+    if which == "water":
+        gpu.reset_target_property(["energy", "forces"])
+    g = data.gpu_graph(structs, cfg["atomic_numbers"], rc, dtype=torch.float32, device=cuda)
+    runs = [gpu(g) for _ in range(3)]
+    keys = ["energy", "forces"] + (["stress"] if which == "ragged" else [])
+    for r in runs[1:]:
+        for k in keys:
+            assert torch.equal(r[k], runs[0][k]), k
+
+
+def test_graph_sum_and_gather(cuda):
+    """``ops.graph_sum`` (``tace_graph_sum``) against float64 sums, with empty
+    graphs and graphs of one and of several thousand nodes; ``graph_gather``
+    and the two backward directions against torch's index_add / index_select."""
+    from tace_amd import ops
+    counts = torch.tensor([0, 1, 5000, 0, 37, 300, 1])
+    ptr = torch.zeros(len(counts) + 1, dtype=torch.int64)
+    ptr[1:] = torch.cumsum(counts, 0)
+    batch = torch.repeat_interleave(torch.arange(len(counts)), counts)
+    g = torch.Generator().manual_seed(3)
+    for dtype, w in ((torch.float32, 2), (torch.float64, 9), (torch.float32, 1)):
+        v = torch.randn(int(ptr[-1]), w, generator=g, dtype=torch.float64)
+        want = torch.zeros(len(counts), w, dtype=torch.float64).index_add_(0, batch, v)
+        vg = v.to(dtype).to(cuda).requires_grad_(True)
+        got = ops.graph_sum(vg, ptr.to(cuda), batch.to(cuda))
+        tol = 1e-12 if dtype == torch.float64 else 1e-5
+        assert (got.double().cpu() - want).abs().max().item() <= tol * max(1.0, want.abs().max().item())
+        assert torch.equal(got, ops.graph_sum(vg, ptr.to(cuda), batch.to(cuda)))
+        up = torch.randn(len(counts), w, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+        (gv,) = torch.autograd.grad(got, vg, up)
+        assert torch.equal(gv, up.index_select(0, batch.to(cuda)))
+        per = up.clone().requires_grad_(True)
+        gat = ops.graph_gather(per, ptr.to(cuda), batch.to(cuda))
+        assert torch.equal(gat, up.index_select(0, batch.to(cuda)))
+        (gp,) = torch.autograd.grad(gat, per, vg.detach())
+        assert (gp.double().cpu() - want).abs().max().item() <= tol * max(1.0, want.abs().max().item())

@@ -101,3 +101,52 @@ def test_pair_rows_equal_expanded_weights(cuda, dtype):
     tol = 1e-5 if dtype == torch.float32 else 1e-12
     err = ((gh - rh).abs().max() / rh.abs().max()).item()
     assert err < tol, err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+def test_self_and_duplicate_edges_get_their_own_rows(cuda, dtype):
+    """A zero-shift self edge i -> i finds itself as its reverse, and a
+    duplicated edge shares its reverse with the original: only mutual pairs
+    share a row, every other edge gets its own, and the pair-row product
+    still equals the product with the weights expanded to every edge."""
+    s = structures.si_diamond(seed=4)
+    plan, sh = _nl(s, 5.0, cuda)
+    rp = plan.rowptr.cpu().numpy()
+    dst = np.repeat(np.arange(plan.n_nodes), np.diff(rp))
+    src = plan.src.cpu().numpy()
+    S = sh.cpu().numpy()
+    # extra edges: 3 -> 3 with S = 0, and copies of edges 10 and 25
+    src2 = np.concatenate([src, [3, src[10], src[25]]])
+    dst2 = np.concatenate([dst, [3, dst[10], dst[25]]])
+    S2 = np.concatenate([S, [[0, 0, 0], S[10], S[25]]]).astype(S.dtype)
+    order = np.argsort(dst2, kind="stable")
+    ei = torch.as_tensor(np.stack([src2[order], dst2[order]]), device=cuda)
+    sh2 = torch.as_tensor(S2[order], device=cuda)
+    sub = ops.EdgePlan.from_edge_index(ei, plan.n_nodes)
+    pairs = sub.edge_pairs(sh2)
+    E = sub.n_edges
+    ra, rb = pairs.row_edges.cpu().numpy(), pairs.row_partner.cpu().numpy()
+    rows = pairs.w_rows.cpu().numpy()
+    # the self edge and the two copies are unpaired (each original keeps its reverse)
+    assert int((rb < 0).sum()) == 3 and pairs.n_rows == (E + 3) // 2
+    assert sorted(set(rows.tolist())) == list(range(pairs.n_rows))
+    owners = np.concatenate([ra, rb[rb >= 0]])
+    assert sorted(owners.tolist()) == list(range(E))
+    assert (rows[ra] == np.arange(pairs.n_rows)).all() and (rows[rb[rb >= 0]] == np.nonzero(rb >= 0)[0]).all()
+    # the product through the pair rows equals the per-edge product
+    C = 64
+    var = ops.find_variant(ops.variant_key("uvu", [0, 1, 2], [0, 1, 2], [0, 1, 2]))
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(plan.n_nodes, C * var.d1, generator=g, dtype=dtype).to(cuda).requires_grad_(True)
+    y = torch.randn(E, var.d2, generator=g, dtype=dtype).to(cuda).requires_grad_(True)
+    h = torch.randn(pairs.n_rows, 64, generator=g, dtype=dtype).to(cuda).requires_grad_(True)
+    W = torch.randn(64, C * var.npath, generator=g, dtype=dtype).to(cuda)
+    out = ops.edge_tp_scatter_pairs(x, y, h, W, 0.125, sub, pairs, var, C)
+    w_all = ops.radial_mlp_out(h.index_select(0, pairs.w_rows), W, 0.125)
+    ref = ops.edge_tp_scatter(x, y, w_all, sub, var, C)
+    go = torch.randn(out.shape, generator=g, dtype=dtype).to(cuda)
+    grads = torch.autograd.grad(out, [x, y, h], go)
+    refs = torch.autograd.grad(ref, [x, y, h], go)
+    tol = 1e-5 if dtype == torch.float32 else 1e-12
+    for a, b in zip((out,) + grads, (ref,) + refs):
+        assert ((a - b).abs().max() / b.abs().max()).item() < tol

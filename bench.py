@@ -153,6 +153,24 @@ def algorithmic_bytes(name: str, info, var, s: int) -> float:
     return float("nan")
 
 
+def section8d_bytes(name: str, info, var, s: int) -> float:
+    """The per-edge algorithmic bytes of an edge-TP launch as the hot-path
+    measurement contract defines them (every per-edge operand counted per
+    edge, the weights included; int32 CSR src + perm = 8 B per edge):
+      forward   s [E (W + d_Y) + N (d_x + d_out)] + 8 E
+      backward  s [E (2 W + 2 d_Y) + N (2 d_x + d_out)] + 8 E
+                (without grad_x, as in layer 0: N (d_x + d_out))
+    with W = P C, d_x = d1 C, d_out = dout C per node, d_Y = d2."""
+    n, E, C = info[:3]
+    W, dY, dx, do = var.npath * C, var.d2, var.d1 * C, var.dout * C
+    if name.startswith("edge_tp_fwd"):
+        return s * (E * (W + dY) + n * (dx + do)) + 8 * E
+    if name.startswith("edge_tp_bwd"):
+        need_x = info[3]
+        return s * (E * (2 * W + 2 * dY) + n * ((2 if need_x else 1) * dx + do)) + 8 * E
+    return float("nan")
+
+
 def measured_traffic(workload: str, entry: str):
     """HBM bytes per call of ``entry`` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
     summary committed under profiles/ for this workload (None when not measured)."""
@@ -201,8 +219,27 @@ def mfma_roofline(summ, wall_ms: float):
                 share_of_step=round(tot_ms / wall_ms, 3))
 
 
-def cpu_baseline(wl, reps=3):
-    """CPU oracle on a bounded slice of the workload's structure (same model, float32)."""
+def _lscpu() -> dict:
+    """Model name, sockets, cores and threads of this host (lscpu)."""
+    import subprocess
+    out = {}
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        return out
+    want = {"Model name": "model", "Vendor ID": "vendor", "CPU family": "family", "Model": "model_id",
+            "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket", "Thread(s) per core": "threads_per_core",
+            "CPU(s)": "cpus", "CPU max MHz": "max_mhz"}
+    for line in txt.splitlines():
+        if ":" in line:
+            k, v = line.split(":", 1)
+            if k.strip() in want:
+                out[want[k.strip()]] = v.strip()
+    return out
+
+
+def cpu_baseline(wl, reps=3, dtype=torch.float32):
+    """CPU oracle on a bounded slice of the workload's structure (same model)."""
     from oracle import model as om
     from oracle import neighbours as onl
     from tace_amd import data
@@ -215,13 +252,13 @@ def cpu_baseline(wl, reps=3):
 
     def graph():
         edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc) for s in structs]
-        return edges, data.collate(structs, edges, cfg["atomic_numbers"], dtype=torch.float32)
+        return edges, data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype)
 
     n = sum(len(s["numbers"]) for s in structs)
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], rc) for s in structs]
     cfg = wl["cfg"](sum(e[0].shape[1] for e in edges) / n)
     torch.manual_seed(0)
-    m = om.TACE(cfg).float()
+    m = om.TACE(cfg).to(dtype)
     for prm in m.parameters():  # frozen, as in the reference calculators
         prm.requires_grad_(False)
     om.compute(m, graph()[1], forces=True, stress=stress)  # warm-up
@@ -229,8 +266,10 @@ def cpu_baseline(wl, reps=3):
     for _ in range(reps):
         om.compute(m, graph()[1], forces=True, stress=stress)
     dt = time.perf_counter() - t0
+    prec = "float32" if dtype == torch.float32 else "float64"
     return dict(value=n * reps / dt, unit="atom-steps/s", cores=threads, kind="port", cpu=_cpu_model(),
-                sample=f"{n}-atom {what} (same model, float32), "
+                precision=prec,
+                sample=f"{n}-atom {what} (same model, {prec}), "
                        f"{reps} timed {'E+F+S' if stress else 'E+F'} steps incl. brute-force NL after 1 warm-up; "
                        f"{dt:.1f} s")
 
@@ -392,21 +431,63 @@ def main():
     del g_fixed
     log(f"[bench] model only (graph built once): median {model_med:.2f} ms/step")
 
-    # dominant native kernel -> roofline
+    # dominant native entry point -> roofline
     # the matrix-core GEMMs have their own roofline (roofline_mfma)
+    phases = timer.phases()
     hbm_kernels = {k: v for k, v in summ.items() if k not in MFMA_KERNELS}
     name, (cnt, tot_ms, infos) = max(hbm_kernels.items(), key=lambda kv: kv[1][1])
     key = name.split(":", 1)[1] if ":" in name else None
     var = ops.find_variant(key) if key else None
-    byts = sum(algorithmic_bytes(name, i, var, 4) for i in infos)
-    achieved = byts / (tot_ms * 1e-3) / 1e9
     traffic = measured_traffic(args.workload, name)
-    roof = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
-                frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
-                traffic_source=(f"profiles/{args.workload}_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
-                                f"copy-calibrated)" if traffic is not None else None),
-                algorithmic_bytes=round(byts / cnt),
-                avg_launch_us=round(tot_ms / cnt * 1e3, 1), share_of_step=round(tot_ms / (dt * 1e3), 3))
+    src = (f"profiles/{args.workload}_hbm_traffic.md (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)")
+    if name.startswith("edge_tp_") and name in phases:
+        # the edge-TP backward: its product kernel alone (HIP events around
+        # the kernel inside the entry point, tace_mark_phase_event), by the
+        # per-edge bytes; the entry point (kernel + grad_y and grad_x sums) and
+        # the bytes with the weights counted once per edge pair beside it
+        k_cnt, k_ms = phases[name]
+        b8d = sum(section8d_bytes(name, i, var, 4) for i in infos)
+        bpair = sum(algorithmic_bytes(name, i, var, 4) for i in infos)
+        kern = b8d / (k_ms * 1e-3) / 1e9
+        entry = b8d / (tot_ms * 1e-3) / 1e9
+        roof = dict(kernel=f"{name} (product kernel k_uvu_*_bwd alone)", bound="hbm", achieved=round(kern, 1),
+                    peak=HBM_PEAK_GBS, unit="GB/s", frac=round(kern / HBM_PEAK_GBS, 4),
+                    traffic=measured_traffic(args.workload, name + " kernel"),
+                    traffic_source=src, algorithmic_bytes=round(b8d / cnt),
+                    bytes_definition="per edge: s[E(2W+2dY) + N(2dx+dout)] + 8E",
+                    avg_launch_us=round(k_ms / k_cnt * 1e3, 1), share_of_step=round(k_ms / (dt * 1e3), 3),
+                    entry_point=dict(what="tace_edge_tp_bwd: kernel + grad_y part sum + grad_x sender sum",
+                                     achieved=round(entry, 1), frac=round(entry / HBM_PEAK_GBS, 4),
+                                     avg_launch_us=round(tot_ms / cnt * 1e3, 1), traffic=traffic,
+                                     traffic_over_algorithmic=(round(traffic / (b8d / cnt), 3)
+                                                               if traffic is not None else None)),
+                    pair_rows=dict(what="weights counted once per edge pair (the model's pair-shared radial "
+                                        "weights), entry point time",
+                                   algorithmic_bytes=round(bpair / cnt),
+                                   frac=round(bpair / (tot_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)))
+    else:
+        byts = sum(algorithmic_bytes(name, i, var, 4) for i in infos)
+        achieved = byts / (tot_ms * 1e-3) / 1e9
+        roof = dict(kernel=name, bound="hbm", achieved=round(achieved, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(achieved / HBM_PEAK_GBS, 4), traffic=traffic,
+                    traffic_source=src if traffic is not None else None,
+                    algorithmic_bytes=round(byts / cnt),
+                    avg_launch_us=round(tot_ms / cnt * 1e3, 1), share_of_step=round(tot_ms / (dt * 1e3), 3))
+    # every edge / scatter kernel of the step: all edge-TP entry points (their
+    # grad_y and grad_x sums included) against the per-edge bytes
+    agg_b, agg_ms = 0.0, 0.0
+    for k, (c, t, inf) in summ.items():
+        if k.startswith("edge_tp_fwd") or k.startswith("edge_tp_bwd"):
+            v = ops.find_variant(k.split(":", 1)[1])
+            agg_b += sum(section8d_bytes(k, i, v, 4) for i in inf)
+            agg_ms += t
+    if agg_ms > 0:
+        a = agg_b / (agg_ms * 1e-3) / 1e9
+        roof["aggregate_edge_scatter"] = dict(
+            what="all edge-TP forward and backward entry points of the step (every layer; grad_y / grad_x sums "
+                 "included), per-edge bytes", bytes_per_step=round(agg_b / args.steps),
+            ms_per_step=round(agg_ms / args.steps, 3), achieved=round(a, 1), frac=round(a / HBM_PEAK_GBS, 4),
+            target_frac=0.60)
     roof_mfma = mfma_roofline(summ, dt * 1e3)
     if roof_mfma is not None:
         roof_mfma["flops_per_step"] = round(sum(i[3] for i in summ["seg_linear"][2]) / args.steps)
@@ -427,6 +508,9 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] CPU baseline (oracle) ...")
         res["cpu_baseline"] = cpu_baseline(wl)
+        res["cpu_baseline"]["fp64"] = {k: v for k, v in cpu_baseline(wl, dtype=torch.float64).items()
+                                       if k in ("value", "unit", "precision", "sample")}
+        res["cpu_baseline"]["host"] = _lscpu()
     print(json.dumps(res), flush=True)
 
 

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 25
+#define TACE_HIP_ABI_VERSION 26
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -53,6 +53,13 @@ extern "C" {
 
 const char* tace_last_error(void);
 int tace_abi_version(void);
+/* Measurement hook (no counterpart in the reference; for profilers that
+ * bracket an entry point with events): the next tace_edge_tp_bwd,
+ * tace_edge_tp_bwd_rows or tace_edge_tp_bwd_noalloc call made on this host
+ * thread records `hip_event` (a hipEvent_t) on its stream right after its
+ * product kernel, before the grad_y and grad_x sums, and the mark is then
+ * cleared.  NULL clears a pending mark.  Returns 0. */
+int tace_mark_phase_event(void* hip_event);
 
 /* ---- tensor-product variants -------------------------------------------
  * A variant is keyed by "kind|in1 ls|in2 ls|out ls", e.g.

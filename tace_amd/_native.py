@@ -25,6 +25,7 @@ _vp, _cp = ctypes.c_void_p, ctypes.c_char_p
 _SIGS = {
     "tace_last_error": (_cp, []),
     "tace_abi_version": (_c_int, []),
+    "tace_mark_phase_event": (_c_int, [_vp]),
     "tace_tp_num_variants": (_c_int, []),
     "tace_tp_variant_key": (_cp, [_c_int]),
     "tace_tp_find": (_c_int, [_cp]),

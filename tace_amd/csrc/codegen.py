@@ -213,10 +213,12 @@ class Variant:
           gw_p    = sum_i x_i psi_i
           hx_i   += w_p psi_i                            -> cbuf row of slot e
           hy_j   += sum_{i,k} c^p_ijk x_i (w_p g_pk)     -> summed over channels
-        grad_y is reduced over the 64 lanes of each wavefront (transposing
-        butterfly, 17 shuffles for 16 values) and over the workgroup's
-        wavefronts through LDS in a fixed order into this part's partial
-        (``gy`` points at it): deterministic, no atomics."""
+        A workgroup is one wavefront: channel group ``cg`` (channels 64 cg ..
+        64 cg + 63) of one receiver and part.  grad_y is reduced over its 64
+        lanes (transposing butterfly, 17 shuffles for 16 values) into the
+        (part, channel group) partial ``gy`` points at; ``k_sum_parts`` adds
+        the partials in a fixed order: deterministic, no atomics and no
+        barrier inside the edge loop."""
         P = len(self.paths)
         blocks = self.parts()[q]
         paths = self._part_paths(blocks)
@@ -226,11 +228,11 @@ class Variant:
              "    const T* __restrict__ gout,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
              "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ cbuf, T* __restrict__ gy,",
-             "    T* __restrict__ gw, int n_nodes, int C, int n0, T (*red)[8][16]) {",
+             "    T* __restrict__ gw, int n_nodes, int C, int n0, int cg) {",
              "  const int n = map ? map[n0] : n0;  // feature row of the receiver",
-             "  const int lane = (int)threadIdx.x & 63, wv = (int)threadIdx.x >> 6, nw = (int)blockDim.x >> 6;",
-             "  const bool act = (int)threadIdx.x < C;",
-             "  const int u = act ? (int)threadIdx.x : C - 1;",
+             "  const int lane = (int)threadIdx.x & 63;",
+             "  const bool act = 64 * cg + lane < C;",
+             "  const int u = act ? 64 * cg + lane : C - 1;  // this lane's channel",
              "  const size_t N = (size_t)n_nodes;",
              "  const int beg = rowptr[n0], end = rowptr[n0 + 1];",
              f"  const size_t WW = (size_t)C * {P}, DX = (size_t)C * {self.D1};"]
@@ -279,18 +281,7 @@ class Variant:
         L.append("    }")
         L.append("    const T v = reduce16_lanes(hy0, hy1, hy2, hy3, hy4, hy5, hy6, hy7, hy8, hy9, hy10, hy11, hy12, hy13, hy14, hy15);")
         L.append("    const int jj = rev4(lane);")
-        prev = ""
-        L.append("    if (nw == 1) {")
-        L.append(f"      if (lane < 16 && jj < {self.D2}) gy[(size_t)ed * {self.D2} + jj] = {prev}v;")
-        L.append("    } else {")
-        L.append("      if (lane < 16) red[e & 1][wv][jj] = v;")
-        L.append("      __syncthreads();")
-        L.append(f"      if (wv == 0 && lane < 16 && jj < {self.D2}) {{")
-        L.append("        T acc = red[e & 1][0][jj];")
-        L.append("        for (int r = 1; r < nw; ++r) acc += red[e & 1][r][jj];")
-        L.append(f"        gy[(size_t)ed * {self.D2} + jj] = {prev}acc;")
-        L.append("      }")
-        L.append("    }")
+        L.append(f"    if (lane < 16 && jj < {self.D2}) gy[(size_t)ed * {self.D2} + jj] = v;")
         self._edge_rotate(L, blocks, paths)
         L.append("}")
         return "\n".join(L)
@@ -299,10 +290,12 @@ class Variant:
         """One launch runs every part: the workgroups of one receiver's parts
         are neighbours on the same XCD (tp_part_node), so memory-heavy and
         compute-heavy parts share the CUs instead of running one after the
-        other.  Part q of the backward writes grad_y partial q."""
+        other.  The backward runs a wavefront per (part q, channel group cg)
+        that writes grad_y partial q * ceil(C / 64) + cg."""
         nq = len(self.parts())
         a_f = "x, y, w, rowptr, eid, src, map, wmap, out, n_nodes, C, n0"
-        a_b = "x, y, w, gout, rowptr, eid, src, map, wmap, cbuf, gy + (size_t)q * n_edges * %d, gw, n_nodes, C, n0, red" % self.D2
+        a_b = ("x, y, w, gout, rowptr, eid, src, map, wmap, cbuf, gy + (size_t)(q * ncg + cg) * n_edges * %d, gw, "
+               "n_nodes, C, n0, cg" % self.D2)
         L = [f"template <typename T, bool IN1_GM, bool OUT_GM>\n__global__ __launch_bounds__(512) void k_{self.name}_fwd(",
              "    const T* __restrict__ x, const T* __restrict__ y, const T* __restrict__ w,",
              "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
@@ -319,10 +312,13 @@ class Variant:
               "    const int* __restrict__ rowptr, const int* __restrict__ eid, const int* __restrict__ src,",
               "    const int* __restrict__ map, const int* __restrict__ wmap, T* __restrict__ cbuf, T* __restrict__ gy,",
               "    T* __restrict__ gw, int n_nodes, int n_edges, int C) {",
-              "  __shared__ T red[2][8][16];",
+              "  // one wavefront per (receiver, part, channel group of 64)",
+              "  const int ncg = (C + 63) >> 6;",
               "  int q;",
-              f"  const int n0 = tp_part_node(n_nodes, {nq}, &q);",
-              "  if (n0 < 0) return;"]
+              f"  const int n0 = tp_part_node(n_nodes, {nq} * ncg, &q);",
+              "  if (n0 < 0) return;",
+              "  const int cg = q % ncg;",
+              "  q /= ncg;"]
         for q in range(nq):
             L.append(f"  {'if' if q == 0 else 'else if'} (q == {q}) f_{self.name}_bwd{q}<T, NEED_GX, IN1_GM, OUT_GM>({a_b});")
         L.append("}")
@@ -1066,7 +1062,7 @@ def _launchers(v: Variant) -> List[str]:
             out.append("}")
             out.append(f"void L_{v.name}_bwd_{tag}(const void* x, const void* y, const void* w, const void* go, const int* rp, const int* eid, const int* src, const int* map, const int* wmap, void* cb, void* gy, void* gw, int n, int E, int flags, int C, hipStream_t s) {{")
             out.append("  if (n <= 0) return;")
-            out.append("  " + launch)
+            out.append(f"  const dim3 g((unsigned)((n + 7) / 8 * 8 * {nq} * ((C + 63) / 64))), b(64);")
             for f in range(4):
                 for gx in (True, False):
                     out.append(f"  if (flags == {f} && {'cb' if gx else '!cb'}) hipLaunchKernelGGL((k_{v.name}_bwd<{T}, {_b(gx)}, {_b(f & 1)}, {_b(f & 2)}>), g, b, 0, s, (const {T}*)x, (const {T}*)y, (const {T}*)w, (const {T}*)go, rp, eid, src, map, wmap, ({T}*)cb, ({T}*)gy, ({T}*)gw, n, E, C);")
@@ -1124,7 +1120,7 @@ def emit_all(gen_dir: str) -> List[str]:
            "struct TpVariant {",
            "  const char* key; int kind; int npath; int d1; int d2; int dout;",
            "  int weighted;                   // uuu: per-node path weights required",
-           "  int nparts;                     // uvu: part kernels per launch = grad_y partials",
+           "  int nparts;                     // uvu: part kernels per launch (grad_y partials: nparts * ceil(C / 64))",
            "  int nseg; int seg[8][2];        // group-major grad-x row segments (offset / C, length / C)",
            "  UvuFwd fwd_f, fwd_d; UvuBwd bwd_f, bwd_d;",
            "  UuuFwd ufwd_f, ufwd_d; UuuBwd ubwd_f, ubwd_d;",

@@ -24,6 +24,9 @@
 namespace {
 
 thread_local char g_err[512] = "";
+// tace_mark_phase_event: recorded after the next edge-TP backward's product
+// kernel on this host thread, then cleared
+thread_local hipEvent_t g_phase_event = nullptr;
 
 int fail(const char* msg) {
   snprintf(g_err, sizeof(g_err), "%s", msg);
@@ -40,6 +43,11 @@ int check_launch(const char* what) {
 }
 
 }  // namespace
+
+extern "C" int tace_mark_phase_event(void* hip_event) {
+  g_phase_event = (hipEvent_t)hip_event;
+  return 0;
+}
 
 // error helpers shared with the other translation units of the library
 int tace_fail_msg(const char* msg) { return fail(msg); }
@@ -869,12 +877,17 @@ int tace_edge_tp_fwd(int vid, int dtype, const void* x, const void* y, const voi
                                layout, out, stream);
 }
 
+// grad_y partials of one edge-TP backward launch: one per (part, channel
+// group of 64); summed by k_sum_parts when there is more than one
+static int tp_bwd_partials(const TpVariant& v, int channels) { return v.nparts * ((channels + 63) / 64); }
+
 int64_t tace_edge_tp_workspace_elems(int vid, int64_t n_edges, int32_t channels, int32_t need_gx) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 0) return fail("tace_edge_tp_workspace_elems: bad variant id");
   if (n_edges < 0 || channels <= 0) return fail("tace_edge_tp_workspace_elems: bad sizes");
   const TpVariant& v = kVariants[vid];
   int64_t n = need_gx ? n_edges * (int64_t)channels * v.d1 : 0;
-  if (v.nparts > 1) n += (int64_t)v.nparts * n_edges * v.d2;
+  const int np = tp_bwd_partials(v, channels);
+  if (np > 1) n += (int64_t)np * n_edges * v.d2;
   return n;
 }
 
@@ -892,13 +905,18 @@ int tace_edge_tp_bwd_rows(int vid, int dtype, const void* x, const void* y, cons
                           const int32_t* w_rows, int64_t n_nodes, int64_t n_edges, int32_t channels, int32_t layout,
                           const int32_t* s_rowptr, const int32_t* s_slot, void* workspace, int64_t workspace_elems,
                           void* gx, void* gy, void* gw, void* stream) {
+  const hipEvent_t phase = g_phase_event;   // one-shot, cleared on every path
+  g_phase_event = nullptr;
   if (tp_common_checks("tace_edge_tp_bwd", vid, n_nodes, n_edges, channels, layout)) return -1;
   if (!rowptr || (n_edges && (!x || !y || !w || !gout || !src || !gy || !gw)))
     return fail("tace_edge_tp_bwd: null pointer");
   const TpVariant& v = kVariants[vid];
   const int64_t row = (int64_t)channels * v.d1;
   const int64_t cb_elems = gx ? n_edges * row : 0;
-  const int64_t need = cb_elems + (v.nparts > 1 ? (int64_t)v.nparts * n_edges * v.d2 : 0);
+  const int np = tp_bwd_partials(v, channels);
+  if ((n_nodes + 7) / 8 * 8 * (int64_t)np > (int64_t)INT32_MAX)
+    return fail("tace_edge_tp_bwd: too many receivers for one launch");
+  const int64_t need = cb_elems + (np > 1 ? (int64_t)np * n_edges * v.d2 : 0);
   if (gx && !s_rowptr) return fail("tace_edge_tp_bwd: grad_x needs the sender CSR");
   if (n_edges && ((gx && !s_slot) || (need && !workspace))) return fail("tace_edge_tp_bwd: null sender CSR or workspace");
   if (workspace_elems < need) return fail("tace_edge_tp_bwd: workspace smaller than tace_edge_tp_workspace_elems()");
@@ -917,22 +935,24 @@ int tace_edge_tp_bwd_rows(int vid, int dtype, const void* x, const void* y, cons
   // workspace = [grad_x rows of every slot | grad_y partial of every part]
   // cbuf == nullptr selects the kernels without grad_x
   void* cbuf = gx && n_edges ? workspace : nullptr;
-  void* gyp = v.nparts > 1 ? (void*)((char*)workspace + cb_elems * es) : gy;
+  void* gyp = np > 1 ? (void*)((char*)workspace + cb_elems * es) : gy;
   const int64_t ny = n_edges * v.d2;
   const unsigned nb = (unsigned)((ny + 255) / 256);
   if (dtype == TACE_F32) {
     v.bwd_f(x, y, w, gout, rowptr, eid, src, node_map, w_rows, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout,
             channels, s);
-    if (v.nparts > 1 && ny)
-      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)gyp, v.nparts, ny, (float*)gy);
+    if (phase) hipEventRecord(phase, s);
+    if (np > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)gyp, np, ny, (float*)gy);
     if (gx && n_nodes)
       launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, node_map, (float*)gx, (int)n_nodes, row, sg,
                                channels, s);
   } else {
     v.bwd_d(x, y, w, gout, rowptr, eid, src, node_map, w_rows, cbuf, gyp, gw, (int)n_nodes, (int)n_edges, layout,
             channels, s);
-    if (v.nparts > 1 && ny)
-      hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)gyp, v.nparts, ny,
+    if (phase) hipEventRecord(phase, s);
+    if (np > 1 && ny)
+      hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)gyp, np, ny,
                          (double*)gy);
     if (gx && n_nodes)
       launch_seg_rowsum<double>((const double*)cbuf, s_rowptr, s_slot, node_map, (double*)gx, (int)n_nodes, row, sg,

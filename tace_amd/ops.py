@@ -31,25 +31,43 @@ from . import _native as N
 class KernelTimer:
     """Optional HIP-event bracketing of every native launch, on the stream the
     kernel runs on (torch's current stream).  ``ops.TIMER = KernelTimer()``
-    enables it; ``summary()`` returns {name: (launches, total_ms)}."""
+    enables it; ``summary()`` returns {name: (launches, total_ms, infos)} and
+    ``phases()`` {name: (launches, first phase ms)} for the entry points that
+    mark a phase event (the edge-TP backward: its product kernel alone)."""
 
     def __init__(self):
         self.events = {}
+        self.mid = {}
 
     def start(self, name):
         e0 = torch.cuda.Event(enable_timing=True)
         e0.record()
         return name, e0
 
-    def stop(self, tok, info=None):
+    def mark_phase(self, tok):
+        """Arms ``tace_mark_phase_event`` for the next entry point call."""
+        if tok is None:
+            return None
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()   # creates the underlying event; the library records it again
+        N.lib().tace_mark_phase_event(ctypes.c_void_p(e.cuda_event))
+        return e
+
+    def stop(self, tok, info=None, mid=None):
         name, e0 = tok
         e1 = torch.cuda.Event(enable_timing=True)
         e1.record()
         self.events.setdefault(name, []).append((e0, e1, info))
+        if mid is not None:
+            self.mid.setdefault(name, []).append((e0, mid))
 
     def summary(self):
         torch.cuda.synchronize()
         return {k: (len(v), sum(a.elapsed_time(b) for a, b, _ in v), [i for _, _, i in v]) for k, v in self.events.items()}
+
+    def phases(self):
+        torch.cuda.synchronize()
+        return {k: (len(v), sum(a.elapsed_time(b) for a, b in v)) for k, v in self.mid.items()}
 
 
 TIMER = None
@@ -391,6 +409,7 @@ def launch_edge_tp_bwd(x, y, w, gout, plan: EdgePlan, var: TpVariant, C: int, la
         N.check(int(n_ws), "tace_edge_tp_workspace_elems")
     ws = torch.empty(max(n_ws, 1), dtype=x.dtype, device=x.device)
     tok = _t0("edge_tp_bwd:" + var.key)
+    mid = TIMER.mark_phase(tok) if tok is not None else None
     N.check(N.lib().tace_edge_tp_bwd_rows(var.vid, N.dtype_code(x.dtype), x.data_ptr(), y.data_ptr(), w.data_ptr(),
                                           gout.data_ptr(), plan.rowptr.data_ptr(), N.ptr(plan.eid),
                                           plan.src.data_ptr(), N.ptr(node_map),
@@ -398,8 +417,9 @@ def launch_edge_tp_bwd(x, y, w, gout, plan: EdgePlan, var: TpVariant, C: int, la
                                           plan.n_edges, C, layout, N.ptr(s_rowptr), N.ptr(s_slot), ws.data_ptr(),
                                           ws.numel(), N.ptr(gx), gy.data_ptr(), gw.data_ptr(),
                                           N.stream_ptr(x.device)), "tace_edge_tp_bwd")
-    _t1(tok, (plan.n_nodes, plan.n_edges, C, need_x) if pairs is None
-        else (plan.n_nodes, plan.n_edges, C, need_x, pairs.n_rows))
+    if tok is not None:
+        TIMER.stop(tok, (plan.n_nodes, plan.n_edges, C, need_x) if pairs is None
+                   else (plan.n_nodes, plan.n_edges, C, need_x, pairs.n_rows), mid)
     return gx, gy, gw
 
 

@@ -22,14 +22,22 @@ needs from the operators in the ``fused_tp`` slots.
 * ``tace_amd::receiver_csr``, ``tece_rotate_in``, ``tece_score``,
   ``tece_softmax``, ``tece_edge_ace``, ``tece_rotate_out`` (each with a
   ``*_backward``): the kernels of the TECE convolution slot
-  (``HipTeceConvolution``), edge features as lists of SO(2) blocks.
+  (``HipTeceConvolution``) and of exported TECE programs, edge features as
+  lists of SO(2) blocks.
+* ``tace_amd::graph_sum`` / ``graph_gather``: fixed-order per-graph sums
+  (energies, the strain gradient) and their transpose.
+* ``tace_amd::lammps_forward_exchange`` / ``lammps_reverse_exchange``: the
+  per-layer ghost exchange of exported LAMMPS programs
+  (``tace/models/lammps.py:38-80``), through ``use_lammps_data``.
 
 Operators run the library's kernels; there is no CPU implementation.
 """
 
 from __future__ import annotations
 
-from typing import List, Optional, Tuple
+import threading
+from contextlib import contextmanager
+from typing import Any, Iterator, List, Optional, Tuple
 
 import torch
 
@@ -79,6 +87,70 @@ def _graph_gather_backward(ctx, g):
 
 graph_sum.register_autograd(_graph_sum_backward, setup_context=_graph_setup)
 graph_gather.register_autograd(_graph_gather_backward, setup_context=_graph_setup)
+
+
+# ------------------------------------------------------- LAMMPS exchange ----
+# The per-layer ghost exchange of an exported LAMMPS program
+# (tace/models/lammps.py:13-80: ``use_lammps_mliap_data`` and the
+# lammps_forward_exchange / lammps_reverse_exchange operators).  A program has
+# no Python object to hold LAMMPS's ML-IAP data, so the caller makes it current
+# for the call (``use_lammps_data``) and the operators read it from there.
+_LAMMPS_DATA = threading.local()
+
+
+@contextmanager
+def use_lammps_data(data: Any) -> Iterator[None]:
+    """Makes ``data`` (LAMMPS KOKKOS ML-IAP data: forward_exchange /
+    reverse_exchange) the exchange target of the exported program's operators
+    on this thread for the duration of the block."""
+    prev = getattr(_LAMMPS_DATA, "data", None)
+    _LAMMPS_DATA.data = data
+    try:
+        yield
+    finally:
+        _LAMMPS_DATA.data = prev
+
+
+def _lammps_data():
+    data = getattr(_LAMMPS_DATA, "data", None)
+    if data is None:
+        raise RuntimeError("LAMMPS ghost exchange called outside use_lammps_data(...)")
+    return data
+
+
+@torch.library.custom_op("tace_amd::lammps_forward_exchange", mutates_args=(), device_types="cuda")
+def lammps_forward_exchange(rows: Tensor) -> Tensor:
+    """Ghost rows replaced by their owners' rows (rows in LAMMPS atom order)."""
+    flat = rows.reshape(rows.shape[0], -1).contiguous()
+    out = torch.empty_like(flat)
+    _lammps_data().forward_exchange(flat, out, out.shape[1])
+    return out.view(rows.shape)
+
+
+@lammps_forward_exchange.register_fake
+def _lammps_forward_exchange_fake(rows):
+    return torch.empty_like(rows)
+
+
+@torch.library.custom_op("tace_amd::lammps_reverse_exchange", mutates_args=(), device_types="cuda")
+def lammps_reverse_exchange(grad: Tensor) -> Tensor:
+    """The transpose: ghost-row gradients summed into their owners' rows."""
+    flat = grad.reshape(grad.shape[0], -1).contiguous()
+    out = torch.empty_like(flat)
+    _lammps_data().reverse_exchange(flat, out, out.shape[1])
+    return out.view(grad.shape)
+
+
+@lammps_reverse_exchange.register_fake
+def _lammps_reverse_exchange_fake(grad):
+    return torch.empty_like(grad)
+
+
+def _lammps_forward_exchange_backward(ctx, g):
+    return lammps_reverse_exchange(g)
+
+
+lammps_forward_exchange.register_autograd(_lammps_forward_exchange_backward)
 
 
 # ------------------------------------------------------------------- uvu ----

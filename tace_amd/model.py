@@ -172,12 +172,23 @@ class _GhostExchangeFn(torch.autograd.Function):
         return e3nn_to_gm(gin.index_select(0, ctx.sp.perm), ctx.irreps), None, None, None
 
 
+# the ghost exchange of an exported LAMMPS program: the tace_amd::
+# lammps_forward_exchange operator on the LAMMPS data the caller makes current
+# (library.use_lammps_data), as AOTI_LAMMPS_GHOST_EXCHANGE marks it in
+# tace/models/lammps.py:12, 126-130
+LAMMPS_PROGRAM_EXCHANGE = object()
+
+
 def _exchange_ghosts(x: torch.Tensor, irreps, sp: "SpeciesPlan", layer: int) -> torch.Tensor:
     """``handle_lammps`` (``tace/models/lammps.py:105-134``, called after
     linear_up at ``_e3nn/inter.py:228``): no exchange in layer 0 (ghost
     features come from their own embedding), the owners' rows from layer 1."""
     if sp.exchange is None or layer == 0:
         return x
+    if sp.exchange is LAMMPS_PROGRAM_EXCHANGE:
+        # export mode: rows in node (LAMMPS atom) order
+        from . import library
+        return e3nn_to_gm(library.lammps_forward_exchange(gm_to_e3nn(x, irreps)), irreps)
     return _GhostExchangeFn.apply(x, irreps, sp, sp.exchange)
 
 
@@ -1359,28 +1370,36 @@ class TensorModel(torch.nn.Module):
         runs on all nlocal + nghosts rows and exchanges the ghost rows through
         ``lmp_data`` before every interaction layer >= 1, as the reference
         does (``_e3nn/inter.py:228``, ``models/lammps.py:105-134``)."""
-        nlocal, nghosts = (int(v) for v in data["natoms"])
         vec = data["edge_vector"]
         if not vec.is_cuda:
             raise RuntimeError("tace_amd.TensorModel runs on the GPU only (edge_vector is on %s)" % vec.device)
         if not vec.requires_grad:
             vec = vec.detach().requires_grad_(True)
         ei = data["edge_index"]
-        if ei.numel() and int(ei[1].max()) >= nlocal:
-            raise ValueError("LAMMPS mode: every edge's receiver (edge_index[1]) must be a local atom")
-        lmp_data = _opt(data, "lmp_data")
-        owner = self._ghost_owners(lmp_data, nlocal, nghosts, vec)
-        if owner is not None:
-            ei = torch.stack([owner[ei[0]], ei[1]])
-            n = nlocal
-            exchange = None
+        if ops.MODE.export:
+            # exported program (LAMMPS AOTI inputs, tace/models/compile/aot.py:35-43):
+            # nlocal from batch, every row of node_attrs a node, the ghost
+            # exchange through the operator in every layer >= 1
+            nlocal, n = data["batch"].shape[0], data["node_attrs"].shape[0]
+            exchange = LAMMPS_PROGRAM_EXCHANGE
+            plan = ops.TracedEdges(ei, n)
         else:
-            n = nlocal + nghosts
-            exchange = lmp_data
+            nlocal, nghosts = (int(v) for v in data["natoms"])
+            if ei.numel() and int(ei[1].max()) >= nlocal:
+                raise ValueError("LAMMPS mode: every edge's receiver (edge_index[1]) must be a local atom")
+            lmp_data = _opt(data, "lmp_data")
+            owner = self._ghost_owners(lmp_data, nlocal, nghosts, vec)
+            if owner is not None:
+                ei = torch.stack([owner[ei[0]], ei[1]])
+                n = nlocal
+                exchange = None
+            else:
+                n = nlocal + nghosts
+                exchange = lmp_data
+            plan = ops.EdgePlan.from_edge_index(ei, n)
         attrs = data["node_attrs"][:n]
         d = dict(node_attrs=attrs, edge_index=ei, batch=torch.zeros(n, dtype=torch.int64, device=vec.device),
-                 ptr=torch.tensor([0, n], dtype=torch.int64, device=vec.device))
-        plan = ops.EdgePlan.from_edge_index(ei, n)
+                 ptr=torch.arange(2, dtype=torch.int64, device=vec.device) * n)
         _, e_node = self.readout_fn.energy(d, plan, vec, exchange)
         e_node = e_node[:nlocal]
         E = e_node.sum().view(1)

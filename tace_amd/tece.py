@@ -304,12 +304,32 @@ class TeceConvolution(torch.nn.Module):
         # [rows, K, C] (l layout) -> group-major C x (0..lmax)
         return torch.cat([out[:, l * l:(l + 1) ** 2].reshape(-1) for l in range(self.lmax + 1)]).view(Nn, K * C)
 
+    def _forward_library(self, x_gm, w, plan, src, dst, wigner, R):
+        """Export mode: the kernels as ``tace_amd::`` operators (opaque nodes
+        of the traced program, each with its registered backward), features in
+        node order, edges in any order (``plan``: ``ops.TracedEdges``)."""
+        from . import library
+        Nn, L, H, n = x_gm.shape[0], self.lmax, self.H, self.lmax + 1
+        rowptr, eid = library.receiver_csr(plan.edge_index, Nn)
+        blocks = library.tece_rotate_in(self.node_components(x_gm), wigner, src, dst, w, L)
+        ms, md, mw = blocks[:n], blocks[n:2 * n], blocks[2 * n:]
+        key = self.key_proj.blocks(ms, self.mixing)
+        query = self.query_proj.blocks(md, self.mixing)
+        T = self.tmin + (self.tmax - self.tmin) * torch.sigmoid(self.temperature_logit)
+        score = library.tece_score(query, key, self.radial_proj(R), (T * self.attention_scale).detach(), L, H)
+        alpha = library.tece_softmax(score, rowptr, eid)
+        o = library.tece_edge_ace(self._shared_input_gemms(mw), L, self.A)
+        m = self.linear_down.blocks(o, self.mixing)
+        return library.tece_rotate_out(m, alpha, wigner, rowptr, eid, dst, L, H)
+
     def forward(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):
         """x_gm: node features, group-major C x (0..lmax) in feature-row order;
         w: radial weights [E, weight_numel]; node_map[n] = feature row of node
         n; src/dst: edge endpoints (node ids); wigner [E, K, K] from
         ``ops.edge_wigner``; R: radial basis [E, num_radial].  Returns the
         receiver sums, group-major, in feature-row order."""
+        if ops.MODE.export:
+            return self._forward_library(x_gm, w, plan, src, dst, wigner, R)
         if ops.MODE.double:
             return self._forward_autograd(x_gm, w, node_map, src, dst, wigner, R)
         rows = node_map.long()

@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import neighbours as onl
-from tace_amd import configs, data, export, model as pm, structures
+from tace_amd import configs, data, export, model as pm, ops, structures
 
 pytestmark = pytest.mark.gpu
 
@@ -60,8 +60,8 @@ def test_exported_model_matches_eager(cuda, tmp_path, preset, over):
 
 
 def test_exported_tece_model_matches_eager(cuda, tmp_path):
-    """The config-5 TECE architecture (its convolution as torch operations in
-    the program, the tensor products and per-species linears as operators)."""
+    """The config-5 TECE architecture: the convolution's kernels, the tensor
+    products and the per-species linears as operators in the program."""
     s = structures.bcc_fe(reps=(2, 2, 2), seed=5)
     m, cfg = _model("tece", [26], 40.0, cuda, seed=2, num_channel=16, num_head=2, edge_ace_hidden=8)
     m.reset_target_property(["energy", "forces"])
@@ -69,4 +69,31 @@ def test_exported_tece_model_matches_eager(cuda, tmp_path):
     loaded = export.load_program(path)
     for st in (s, structures.bcc_fe(reps=(3, 2, 2), seed=6)):
         g = _graph([st], cfg, cuda)
+        ops.TIMER = ops.KernelTimer()
+        try:
+            got = loaded(g)
+            launched = set(ops.TIMER.summary())
+        finally:
+            ops.TIMER = None
+        _compare(got, m(g), loaded.output_keys)
+        # the program runs the convolution's kernels, forward and backward
+        for k in ("edge_rotate_in_fwd", "edge_rotate_in_bwd", "tece_rotate_out_fwd", "tece_rotate_out_bwd"):
+            assert k in launched, k
+
+
+def test_exported_model_takes_other_graph_counts(cuda, tmp_path):
+    """A program exported on a two-graph batch runs batches of three graphs
+    and of one (dynamic graph count, ``_graph_dynamic_shapes``,
+    tace/models/compile/aot.py:513-530), with stress."""
+    rng = np.random.default_rng(3)
+    zs = [3, 8, 14]
+    mk = lambda k: [structures.random_crystal(rng, int(rng.integers(5, 12)), zs) for _ in range(k)]
+    sample, other, single = mk(2), mk(3), mk(1)
+    m, cfg = _model("si64", zs, 30.0, cuda, seed=4, num_channel=16)
+    m.reset_target_property(["energy", "forces", "stress"])
+    path = export.save_program(m, _graph(sample, cfg, cuda), str(tmp_path / "multi.pt2"))
+    loaded = export.load_program(path)
+    assert loaded.get_cutoff() == cfg["cutoff"] and loaded.get_atomic_numbers() == cfg["atomic_numbers"]
+    for structs in (sample, other, single):
+        g = _graph(structs, cfg, cuda)
         _compare(loaded(g), m(g), loaded.output_keys)

@@ -1433,6 +1433,128 @@ def edge_rotate_in(x: torch.Tensor, W: torch.Tensor, rows_src: torch.Tensor, row
     return tuple(blocks)
 
 
+# ---- TECE rotate-in / rotate-out, twice differentiable (training) ----------
+# Both are multilinear: rotate-in m_s = W x_src, m_d = W x_dst, m_w = w (.)
+# [m_s | m_d] in (x, W, w), rotate-out out = sum_e W_e^T (alpha_e m_e) in (m,
+# alpha, W), and every gradient of their backward is free of its own operand
+# (grad_x(W, w, g), grad_W(x, w, g), grad_w(x, W, g)).  So the backward of the
+# backward is made of the forward and backward operators again, as for the
+# edge tensor product: for upstream gradients (a_x, a_W, a_w) of the backward's
+# outputs, d/dg = f(a_x, W, w) + f(x, a_W, w) + f(x, W, a_w); d/dx = the x part
+# of bwd(x, a_W, w, g) + of bwd(x, W, a_w, g); and so on.  Rotate-in's m_s and
+# m_d do not depend on w, so the a_w terms use m_w and its gradient alone.
+def _rot_in_zero_sd(blocks, n):
+    return [torch.zeros_like(t) for t in blocks[:2 * n]] + list(blocks[2 * n:])
+
+
+class _RotInD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W, wr, rows_src, rows_dst, lmax: int):
+        ms, md, mw = launch_rotate_in_fwd(x, W, rows_src, rows_dst, wr, lmax)
+        ctx.save_for_backward(x, W, wr, rows_src, rows_dst)
+        ctx.lmax = lmax
+        ctx.like = [(t.shape, t.dtype) for t in ms + md + mw]
+        return tuple(ms + md + mw)
+
+    @staticmethod
+    def backward(ctx, *g):
+        x, W, wr, rs, rd = ctx.saved_tensors
+        g = [t.contiguous() if t is not None else torch.zeros(shp, dtype=dt, device=x.device)
+             for t, (shp, dt) in zip(g, ctx.like)]
+        gx, gW, gwr = _RotInBwdD.apply(x, W, wr, rs, rd, ctx.lmax, *g)
+        return gx, gW, gwr, None, None, None
+
+
+class _RotInBwdD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W, wr, rs, rd, lmax: int, *g):
+        n = lmax + 1
+        gxs, gxd, gW, gwr = launch_rotate_in_bwd(x, W, rs, rd, wr, list(g[:n]), list(g[n:2 * n]),
+                                                 list(g[2 * n:]), True)
+        Nr, K, C = x.shape
+        gx = scatter_add_rows(scatter_add_rows(torch.zeros_like(x), rs, gxs), rd, gxd)
+        ctx.save_for_backward(x, W, wr, rs, rd, *g)
+        ctx.lmax = lmax
+        return gx, gW, gwr
+
+    @staticmethod
+    def backward(ctx, ax, aW, aw):
+        x, W, wr, rs, rd, *g = ctx.saved_tensors
+        L, n = ctx.lmax, ctx.lmax + 1
+        zx = ax if ax is not None else torch.zeros_like(x)
+        zW = aW if aW is not None else torch.zeros_like(W)
+        zw = aw if aw is not None else torch.zeros_like(wr)
+        fwd = lambda a, b, c: _RotInD.apply(a.contiguous(), b.contiguous(), c.contiguous(), rs, rd, L)
+        bwd = lambda a, b, c, gg: _RotInBwdD.apply(a.contiguous(), b.contiguous(), c.contiguous(), rs, rd, L, *gg)
+        f1, f2, f3 = fwd(zx, W, wr), fwd(x, zW, wr), fwd(x, W, zw)
+        dg = [a + b + (c if k >= 2 * n else 0.0) for k, (a, b, c) in enumerate(zip(f1, f2, f3))]
+        gw_only = _rot_in_zero_sd(g, n)
+        b1 = bwd(zx, W, wr, g)          # W and w parts with x -> a_x
+        b2 = bwd(x, zW, wr, g)          # x and w parts with W -> a_W
+        b3 = bwd(x, W, zw, gw_only)     # x and W parts with w -> a_w (m_w only)
+        return (b2[0] + b3[0], b1[1] + b3[1], b1[2] + b2[2], None, None, None) + tuple(dg)
+
+
+def edge_rotate_in_twice(x, W, rows_src, rows_dst, lmax: int, radial_w):
+    """``edge_rotate_in`` (radial weights required) whose backward is
+    differentiable again (training with a force loss)."""
+    out = _RotInD.apply(x.contiguous(), W.contiguous(), radial_w.contiguous(), rows_src.long().contiguous(),
+                        rows_dst.long().contiguous(), int(lmax))
+    n = lmax + 1
+    return [list(out[i * n:(i + 1) * n]) for i in range(3)]
+
+
+class _RotOutD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, H: int, *m):
+        out = launch_rotate_out_fwd(list(m), alpha, W, plan, node_map, lmax, H)
+        ctx.save_for_backward(alpha, W, node_map, dst, *m)
+        ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        alpha, W, node_map, dst, *m = ctx.saved_tensors
+        out = _RotOutBwdD.apply(alpha, W, gout.contiguous(), ctx.plan, node_map, dst, ctx.lmax, ctx.H, *m)
+        ga, gW, gm = out[0], out[1], out[2:]
+        return (ga, gW, None, None, None, None, None) + tuple(gm)
+
+
+class _RotOutBwdD(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, alpha, W, gout, plan: EdgePlan, node_map, dst, lmax: int, H: int, *m):
+        gm, ga, gW = launch_rotate_out_bwd(list(m), alpha, W, gout, dst, node_map, plan, lmax, H)
+        ctx.save_for_backward(alpha, W, gout, node_map, dst, *m)
+        ctx.plan, ctx.lmax, ctx.H = plan, lmax, H
+        return (ga, gW) + tuple(gm)
+
+    @staticmethod
+    def backward(ctx, aa, aW, *am):
+        alpha, W, gout, node_map, dst, *m = ctx.saved_tensors
+        plan, L, H = ctx.plan, ctx.lmax, ctx.H
+        za = aa if aa is not None else torch.zeros_like(alpha)
+        zW = aW if aW is not None else torch.zeros_like(W)
+        zm = [a if a is not None else torch.zeros_like(t) for a, t in zip(am, m)]
+        fwd = lambda a, b, mm: _RotOutD.apply(a.contiguous(), b.contiguous(), plan, node_map, dst, L, H,
+                                              *[t.contiguous() for t in mm])
+        bwd = lambda a, b, mm: _RotOutBwdD.apply(a.contiguous(), b.contiguous(), gout, plan, node_map, dst, L, H,
+                                                 *[t.contiguous() for t in mm])
+        dg = fwd(alpha, W, zm) + fwd(za, W, m) + fwd(alpha, zW, m)
+        b_m = bwd(alpha, W, zm)    # alpha and W parts with m -> a_m
+        b_a = bwd(za, W, m)        # m and W parts with alpha -> a_alpha
+        b_W = bwd(alpha, zW, m)    # m and alpha parts with W -> a_W
+        ga = b_m[0] + b_W[0]
+        gW = b_m[1] + b_a[1]
+        gm = [p + q for p, q in zip(b_a[2:], b_W[2:])]
+        return (ga, gW, dg, None, None, None, None, None) + tuple(gm)
+
+
+def tece_rotate_out_twice(m, alpha, W, plan: EdgePlan, node_map, dst, lmax: int, heads: int) -> torch.Tensor:
+    """``tece_rotate_out`` whose backward is differentiable again."""
+    return _RotOutD.apply(alpha.contiguous(), W.contiguous(), plan, node_map, dst.long().contiguous(), int(lmax),
+                          int(heads), *[t.contiguous() for t in m])
+
+
 def launch_mlp_hidden_fwd(radial, weights, n_layers: int) -> torch.Tensor:
     """Hidden layers of the radial MLP: the last hidden activations h [E, 64]
     (the backward recomputes the rest from ``radial``)."""

@@ -27,6 +27,9 @@ _SIGMOID_CST = 1.8467055342154763   # e3nn normalize2mom(sigmoid) (tace/models/m
 # frozen parameters run the convolution on the fused operator (_TeceFused);
 # False keeps the per-operator autograd path (the reference for its tests)
 FUSED = True
+# training (twice differentiable): rotate-in and rotate-out on their kernels
+# (_forward_train); False runs the whole convolution as torch operations
+TRAIN_ON_KERNELS = True
 
 class _MixedLinear(torch.autograd.Function):
     """y = x W^T (+ b) with x and W rounded to bfloat16 and fp32 accumulation
@@ -304,6 +307,34 @@ class TeceConvolution(torch.nn.Module):
         # [rows, K, C] (l layout) -> group-major C x (0..lmax)
         return torch.cat([out[:, l * l:(l + 1) ** 2].reshape(-1) for l in range(self.lmax + 1)]).view(Nn, K * C)
 
+    def _forward_train(self, x_gm, w, plan: ops.EdgePlan, node_map, src, dst, wigner, R):
+        """Training (twice differentiable): the rotate-in and the rotate-out
+        (gathers, rotations, radial weighting, attention weighting and
+        receiver sums) on their HIP kernels through operators whose backward is
+        differentiable again; score, graph softmax, gate, edge-ACE and the SO(2)
+        linears as torch operations (``_forward_autograd``'s)."""
+        Nn, E, C = x_gm.shape[0], w.shape[0], self.C
+        L, H, n = self.lmax, self.H, self.lmax + 1
+        rows = node_map.long() if node_map is not None else None
+        rs, rd = (src, dst) if rows is None else (rows[src], rows[dst])
+        ms, md, mw = ops.edge_rotate_in_twice(self.node_components(x_gm), wigner, rs, rd, L, w)
+        key = ops.so2_from_blocks(self.key_proj.blocks(ms, self.mixing), L)
+        query = ops.so2_from_blocks(self.query_proj.blocks(md, self.mixing), L)
+        score = self._score_autograd(query, key, R)
+        m = ops.so2_from_blocks(mw, L)
+        coefs = torch.sigmoid(self.linear_coefs(m).squeeze(-1)) * _SIGMOID_CST
+        v = self.linear_glu(m)
+        u = self.linear_up(m)
+        gate, u = u[:, :self.num_gates], u[:, self.num_gates:self.num_gates + self.rows_full]
+        g = (torch.sigmoid(gate) * _SIGMOID_CST).index_select(1, self._expand(True).to(w.device))
+        m = self.linear_down(u + g * u + self._edge_ace_autograd(u, v, coefs))
+        # graph softmax over each receiver's in-edges (softmax.py:100-112)
+        mx = torch.full((Nn, H), -math.inf, dtype=score.dtype, device=w.device).scatter_reduce(
+            0, rd.view(-1, 1).expand(-1, H), score.detach(), reduce="amax", include_self=True)
+        ex = torch.exp(score - mx[rd])
+        alpha = ex / (torch.zeros(Nn, H, dtype=score.dtype, device=w.device).index_add(0, rd, ex) + 1e-16)[rd]
+        return ops.tece_rotate_out_twice(ops.so2_to_blocks(m, L), alpha, wigner, plan, node_map, dst, L, H)
+
     def _forward_library(self, x_gm, w, plan, src, dst, wigner, R):
         """Export mode: the kernels as ``tace_amd::`` operators (opaque nodes
         of the traced program, each with its registered backward), features in
@@ -331,6 +362,8 @@ class TeceConvolution(torch.nn.Module):
         if ops.MODE.export:
             return self._forward_library(x_gm, w, plan, src, dst, wigner, R)
         if ops.MODE.double:
+            if TRAIN_ON_KERNELS and isinstance(plan, ops.EdgePlan):
+                return self._forward_train(x_gm, w, plan, node_map, src, dst, wigner, R)
             return self._forward_autograd(x_gm, w, node_map, src, dst, wigner, R)
         rows = node_map.long()
         return self.edges(self.node_components(x_gm), w, rows[src], rows[dst], plan, node_map, dst, wigner, R)

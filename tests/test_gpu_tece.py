@@ -691,3 +691,41 @@ def test_tece_bf16_channel_mixing_error(cuda):
           f"({f_rel:.3e} of max |F|)", flush=True)
     # measured on MI355X: energy 1.0e-7 relative, forces 3.6e-4 of max |F|
     assert e_rel < 1e-5 and f_rel < 2e-3, (e_rel, f_abs, f_rel)
+
+
+def test_rotate_in_out_second_derivatives(cuda):
+    """The twice-differentiable rotate-in and rotate-out of training
+    (``ops.edge_rotate_in_twice`` / ``tece_rotate_out_twice``): first and
+    second derivatives against central finite differences (float64
+    ``gradcheck`` / ``gradgradcheck``) on a small graph with unsorted edges."""
+    lmax, C, H = 2, 4, 2
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    g = torch.Generator().manual_seed(4)
+    Nn, E = 5, 11
+    dst = torch.randint(0, Nn, (E,), generator=g)
+    src = torch.randint(0, Nn, (E,), generator=g)
+    vec = torch.randn(E, 3, generator=g, dtype=torch.float64)
+    W = ops._edge_wigner_autograd(vec.to(cuda), lmax).detach()
+    x = torch.randn(Nn, K, C, generator=g, dtype=torch.float64).to(cuda)
+    w = torch.randn(E, nc * 2 * C, generator=g, dtype=torch.float64).to(cuda)
+    rs, rd = src.to(cuda), dst.to(cuda)
+
+    def rin(x, W, w):
+        ms, md, mw = ops.edge_rotate_in_twice(x, W, rs, rd, lmax, w)
+        return tuple(ms + md + mw)
+
+    args = (x.requires_grad_(True), W.clone().requires_grad_(True), w.requires_grad_(True))
+    assert torch.autograd.gradcheck(rin, args, atol=1e-8)
+    assert torch.autograd.gradgradcheck(rin, args, atol=1e-8)
+
+    plan = ops.EdgePlan.from_edge_index(torch.stack([rs, rd]), Nn)
+    m = [torch.randn(shp, generator=g, dtype=torch.float64).to(cuda).requires_grad_(True)
+         for shp in ops.so2_block_shapes(E, lmax, C)]
+    alpha = torch.rand(E, H, generator=g, dtype=torch.float64).to(cuda).requires_grad_(True)
+
+    def rout(alpha, W, *m):
+        return ops.tece_rotate_out_twice(list(m), alpha, W, plan, None, rd, lmax, H)
+
+    args = (alpha, W.clone().requires_grad_(True), *m)
+    assert torch.autograd.gradcheck(rout, args, atol=1e-8)
+    assert torch.autograd.gradgradcheck(rout, args, atol=1e-8)

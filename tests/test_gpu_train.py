@@ -4,8 +4,9 @@ In training mode (or with ``create_graph``) ``TensorModel`` keeps the graph of
 its derivatives (``tace/models/adapter.py:95-104``), so a loss on energies,
 forces and stress can be differentiated with respect to the parameters: the
 double backward of force-matching training (``lightning/lit_model.py:150``).
-The tensor products run on the HIP kernels through operators whose backward
-is differentiable again, the TECE convolution as torch operations; the
+The tensor products and the TECE convolution's rotate-in and rotate-out run
+on the HIP kernels through operators whose backward is differentiable again;
+the
 gradients of such a loss with respect to every parameter must equal torch
 autograd through the CPU oracle (float64, 1e-10 relative), and the forces of
 the training path those of the inference path.
@@ -17,7 +18,7 @@ import torch
 
 from oracle import model as om
 from oracle import neighbours as onl
-from tace_amd import configs, data, model as pm, structures
+from tace_amd import configs, data, model as pm, ops, structures
 
 pytestmark = pytest.mark.gpu
 
@@ -162,7 +163,15 @@ def test_tece_force_loss_parameter_gradients_match_oracle(cuda):
     gpu.eval()
     inf = gpu(dg)
     gpu.train()
-    out = gpu(dg)
+    ops.TIMER = ops.KernelTimer()
+    try:
+        out = gpu(dg)
+        fwd_launched = set(ops.TIMER.summary())
+    finally:
+        ops.TIMER = None
+    # the convolution's rotate-in / rotate-out kernels in training, forward and force backward
+    for k in ("edge_rotate_in_fwd", "edge_rotate_in_bwd", "tece_rotate_out_fwd", "tece_rotate_out_bwd"):
+        assert k in fwd_launched, k
     assert (out["energy"].detach() - inf["energy"]).abs().max().item() <= 1e-11 * inf["energy"].abs().max().item()
     assert (out["forces"].detach() - inf["forces"]).abs().max().item() <= 1e-11 * max(inf["forces"].abs().max().item(),
                                                                                     1.0)

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 26
+#define TACE_HIP_ABI_VERSION 28
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -495,6 +495,14 @@ int tace_nl_batch_fill(const double* pos, int64_t n_atoms, int32_t n_structs, co
 int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t width, const int32_t* rowptr,
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream);
+/* A narrow linear map of rows: out[r, j] = bias[j] + sum_i x[r, i] m[i, j]
+ * for r < n_rows, x [n_rows, k], m [k, n] row-major, bias [n] or NULL, out
+ * [n_rows, n] (1 <= k, n <= 64), summed in i order.  The TECE radial
+ * projection radial_proj(R) (oam_2026_07_05.py:678-682, 699-754: [E, num_radial]
+ * -> [E, 2 H]) and its input gradient (m = the weight untransposed), which a
+ * library GEMM runs as one launch per call at 8 x 8 sizes. */
+int tace_narrow_linear(int dtype, const void* x, int64_t n_rows, int32_t k, const void* m, const void* bias,
+                       int32_t n, void* out, void* stream);
 /* Per-graph sums of node rows: out[g, :] = sum over k in [ptr[g], ptr[g+1])
  * of values[k, :] (rows of `width` values, 0 < width <= 4096; out is
  * overwritten), in a fixed order that depends only on the graph's size, so
@@ -524,6 +532,13 @@ int tace_rows_accumulate_runs(int dtype, const void* rows, int64_t n_rows, int64
  * aligned.  0 < k <= 2048. */
 int tace_so2_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b_frag, const float* bias, float* out,
                        int64_t ldo, int64_t m, int32_t n, int32_t k, void* stream);
+/* The same product for large k (0 < k <= 65536): a 128-row x 256-column
+ * output tile per workgroup with A staged through LDS in 64-k steps, so B is
+ * read once per 128 rows whatever k (tace_so2_gemm_bf16 holds all of a row
+ * tile's k in LDS, 32-128 rows).  Same arguments and layout; float32 sums of
+ * the same bf16 products in k order. */
+int tace_so2_gemm_bf16_kt(const uint16_t* a, int64_t lda, const uint16_t* b_frag, const float* bias, float* out,
+                          int64_t ldo, int64_t m, int32_t n, int32_t k, void* stream);
 /* Edge pairs of a neighbour list in receiver-CSR form (rowptr, eid as for
  * the tensor products; src [E] senders, shifts [E, 3] int32 periodic shifts,
  * by edge id): the reverse of edge e (i -> j, S) is the edge j -> i with

@@ -87,6 +87,7 @@ _SIGS = {
     "tace_seg_linear_presplit": (_c_int, [_vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_dbl, _vp]),
     "tace_seg_linear_ks_rows": (_c_i32, [_c_i32]),
     "tace_so2_gemm_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp]),
+    "tace_so2_gemm_bf16_kt": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp]),
     "tace_seg_linear_presplit_ks": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_dbl, _vp]),
     "tace_seg_linear_presplit_frag": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_dbl, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
@@ -98,6 +99,7 @@ _SIGS = {
     "tace_nl_batch_fill": (_c_int, [_vp, _c_i64, _c_i32, _vp, _c_i64, _vp, _c_i64, _c_i32, _vp, _vp, _vp, _vp]),
     "tace_rows_accumulate": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp]),
     "tace_graph_sum": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp]),
+    "tace_narrow_linear": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _vp, _c_i32, _vp, _vp]),
     "tace_rows_accumulate_runs": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _c_i32, _vp, _c_i64,
                                            _vp]),
     "tace_scan_i32": (_c_int, [_vp, _c_i64, _vp, _vp]),

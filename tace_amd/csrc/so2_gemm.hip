@@ -199,7 +199,223 @@ __global__ __launch_bounds__(G_THREADS) void k_so2_gemm_bf16(const unsigned shor
   }
 }
 
+// ---- k-tiled variant: the large-k shapes ------------------------------------
+// With all of a tile's k in LDS, k >= 256 leaves room for 32-64 rows only, and
+// every such row tile re-reads all of B from L2.  Here a workgroup of four
+// wavefronts owns a 128-row x 256-column output tile; A goes through LDS in
+// 64-k stages (double-buffered, the next stage loaded into registers during
+// this stage's MFMAs, one barrier per stage); wavefront w keeps the 128 x 64
+// accumulator block of columns 64 w .. 64 w + 63 (32 MFMA blocks) and reads
+// its B fragments from the fragment-order weight one 32-k step ahead.  Tiles
+// are numbered row-tile-major and handed to the XCDs in contiguous ranges, so
+// the column tiles of one row tile (same A rows) share an XCD's L2.
+constexpr int KT_ROWS = 128, KT_COLS = 256, KT_KS = 64, KT_STR = KT_KS + 8;   // LDS row: 144 bytes
+constexpr int KT_THREADS = 256;
+
+struct KtJob {
+  const unsigned short* a;
+  const unsigned short* bf;
+  const float* bias;
+  float* out;
+  int64_t lda, ldo;
+  int rows, n, k, nks, nb16, c0;
+};
+
+// 128 x 64 of A (k0 .. k0 + 63) into registers.  AVEC (16-byte aligned rows,
+// k % 64 == 0): every load unconditional and unmasked, at a clamped address --
+// rows past the tile repeat its last row (their outputs are not stored); the
+// prefetch past the last stage repeats it (never read).  A load under a branch, or
+// one whose value a select may discard, lets the compiler move it into a
+// branch, and at the join it waits for every outstanding load, the
+// prefetches included.  Otherwise: zeros past the rows and past k.
+template <bool AVEC>
+__device__ __forceinline__ void kt_load_a(const KtJob& J, int k0, int t, gu4 (&r)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int u = t + KT_THREADS * q, row = u >> 3, kk = k0 + ((u & 7) << 3);
+    if (AVEC) {
+      r[q] = *(const gu4*)(J.a + (int64_t)min(row, J.rows - 1) * J.lda + min(kk, J.k - 8));
+    } else {
+      gu4 v = gu4{0u, 0u, 0u, 0u};
+      if (row < J.rows) {
+        const unsigned short* p = J.a + (int64_t)row * J.lda + kk;
+        unsigned short e[8];
+#pragma unroll
+        for (int z = 0; z < 8; ++z) e[z] = kk + z < J.k ? p[z] : (unsigned short)0;
+        v = gu4{e[0] | ((unsigned)e[1] << 16), e[2] | ((unsigned)e[3] << 16), e[4] | ((unsigned)e[5] << 16),
+                e[6] | ((unsigned)e[7] << 16)};
+      }
+      r[q] = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void kt_store_a(unsigned short* __restrict__ As, int t, const gu4 (&r)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int u = t + KT_THREADS * q;
+    *(gu4*)&As[(u >> 3) * KT_STR + ((u & 7) << 3)] = r[q];
+  }
+}
+
+// B fragments of the wavefront's four 16-column blocks at 32-k step ks (the
+// column block clamped to the last one: its outputs are not stored)
+__device__ __forceinline__ void kt_load_b(const KtJob& J, int cw, int ks, int lane, gu4 (&d)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int jb = min((cw >> 4) + j, J.nb16 - 1);
+    d[j] = *(const gu4*)(J.bf + ((int64_t)jb * J.nks + ks) * 512 + 8 * lane);
+  }
+}
+
+template <bool AVEC>
+__global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned short* __restrict__ a, int64_t lda,
+                                                             const unsigned short* __restrict__ bfrag,
+                                                             const float* __restrict__ bias, float* __restrict__ out,
+                                                             int64_t ldo, int64_t M, int N, int K, int n_rt, int n_ct,
+                                                             int per) {
+  __shared__ __attribute__((aligned(16))) unsigned short As[2][KT_ROWS * KT_STR];
+  const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  if (tile >= n_rt * n_ct) return;
+  const int rt = tile / n_ct, ct = tile - rt * n_ct;
+  const int64_t row0 = (int64_t)rt * KT_ROWS;
+  KtJob J;
+  J.a = a + row0 * lda;
+  J.bf = bfrag;
+  J.bias = bias;
+  J.out = out + row0 * ldo;
+  J.lda = lda;
+  J.ldo = ldo;
+  J.rows = (int)min((int64_t)KT_ROWS, M - row0);
+  J.n = N;
+  J.k = K;
+  J.nks = (K + 31) >> 5;
+  J.nb16 = (N + 15) >> 4;
+  J.c0 = ct * KT_COLS;
+  const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int fr = lane & 15, fg = lane >> 4;
+  const int cw = J.c0 + 64 * wv;          // the wavefront's first column
+  const bool has_cols = cw < N;           // otherwise it only stages A
+  const int n_st = (J.nks + 1) >> 1;      // 64-k stages
+
+  gf4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = gf4{0.f, 0.f, 0.f, 0.f};
+
+  gu4 ra[4];
+  kt_load_a<AVEC>(J, 0, t, ra);
+  kt_store_a(As[0], t, ra);
+  __syncthreads();
+  if (has_cols) {
+    gu4 b0[4], b1[4];
+    kt_load_b(J, cw, 0, lane, b0);
+    for (int st = 0; st < n_st; ++st) {
+      const unsigned short* __restrict__ Ab = As[st & 1];
+      const int ks0 = 2 * st;
+      // every load unconditional: past the last stage / step they repeat it
+      kt_load_a<AVEC>(J, min(st + 1, n_st - 1) * KT_KS, t, ra);
+      kt_load_b(J, cw, min(ks0 + 1, J.nks - 1), lane, b1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const gbf8 af = *(const gbf8*)&Ab[(16 * i + fr) * KT_STR + 8 * fg];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf8, b0[j]), af, acc[i][j], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      kt_load_b(J, cw, min(ks0 + 2, J.nks - 1), lane, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (AVEC || ks0 + 1 < J.nks) {   // AVEC: k % 64 == 0, every stage has both steps
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const gbf8 af = *(const gbf8*)&Ab[(16 * i + fr) * KT_STR + 32 + 8 * fg];
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] =
+                __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(gbf8, b1[j]), af, acc[i][j], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      kt_store_a(As[(st + 1) & 1], t, ra);
+      __syncthreads();
+    }
+  } else {
+    for (int st = 0; st < n_st; ++st) {
+      kt_load_a<AVEC>(J, min(st + 1, n_st - 1) * KT_KS, t, ra);
+      kt_store_a(As[(st + 1) & 1], t, ra);
+      __syncthreads();
+    }
+  }
+  if (!has_cols) return;
+
+  // epilogue: acc[i][j][q] = out[row 16 i + fr][column cw + 16 j + 4 fg + q];
+  // per pair of column blocks (j, j + 1) lanes fr and fr ^ 8 trade one block
+  // so that each 16-byte store writes whole 128-byte row segments
+  const bool lo = fr < 8;
+  const bool vst = ((J.ldo & 3) == 0) && ((((uintptr_t)J.out) & 15) == 0);
+#pragma unroll
+  for (int jp = 0; jp < 2; ++jp) {
+    const int cb = cw + 32 * jp;
+    gf4 bv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        bv[j][q] = J.bias ? J.bias[min(cb + 16 * j + 4 * fg + q, N - 1)] : 0.f;
+    const int col = cb + (lo ? 0 : 16) + 4 * fg;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const gf4 v0 = acc[i][2 * jp] + bv[0], v1 = acc[i][2 * jp + 1] + bv[1];
+      const gf4 give = lo ? v1 : v0;
+      gf4 got;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) got[q] = __shfl_xor(give[q], 8);
+      const gf4 s0 = lo ? v0 : got, s1 = lo ? got : v1;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 16 * i + 8 * h + (fr & 7);
+        if (r >= J.rows || col >= N) continue;
+        const gf4 v = h ? s1 : s0;
+        float* dst = J.out + (int64_t)r * J.ldo + col;
+        if (vst && col + 4 <= N) {
+          *(gf4*)dst = v;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (col + q < N) dst[q] = v[q];
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
+
+extern "C" int tace_so2_gemm_bf16_kt(const uint16_t* a, int64_t lda, const uint16_t* b_frag, const float* bias,
+                                     float* out, int64_t ldo, int64_t m, int32_t n, int32_t k, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0 || k > 65536 || lda < k || ldo < n)
+    return tace_fail_msg("tace_so2_gemm_bf16_kt: bad sizes (0 < n, 0 < k <= 65536, lda >= k, ldo >= n)");
+  if (m == 0) return 0;
+  if (!a || !b_frag || !out) return tace_fail_msg("tace_so2_gemm_bf16_kt: null pointer");
+  if ((((uintptr_t)b_frag) & 15) != 0)
+    return tace_fail_msg("tace_so2_gemm_bf16_kt: the fragment-order weight must be 16-byte aligned");
+  const int64_t n_rt = (m + KT_ROWS - 1) / KT_ROWS, n_ct = (n + KT_COLS - 1) / KT_COLS;
+  if (n_rt * n_ct > 0x7fffffffll / 2) return tace_fail_msg("tace_so2_gemm_bf16_kt: too many rows");
+  const int64_t per = (n_rt * n_ct + 7) / 8;
+  const bool avec = ((((uintptr_t)a) & 15) == 0) && ((lda & 7) == 0) && ((k & 63) == 0);
+  if (avec)
+    hipLaunchKernelGGL(k_so2_gemm_kt<true>, dim3((unsigned)(8 * per)), dim3(KT_THREADS), 0, (hipStream_t)stream,
+                       (const unsigned short*)a, lda, (const unsigned short*)b_frag, bias, out, ldo, m, (int)n, (int)k,
+                       (int)n_rt, (int)n_ct, (int)per);
+  else
+    hipLaunchKernelGGL(k_so2_gemm_kt<false>, dim3((unsigned)(8 * per)), dim3(KT_THREADS), 0, (hipStream_t)stream,
+                       (const unsigned short*)a, lda, (const unsigned short*)b_frag, bias, out, ldo, m, (int)n, (int)k,
+                       (int)n_rt, (int)n_ct, (int)per);
+  return tace_check_launch("tace_so2_gemm_bf16_kt");
+}
 
 extern "C" int tace_so2_gemm_bf16(const uint16_t* a, int64_t lda, const uint16_t* b_frag, const float* bias, float* out,
                                   int64_t ldo, int64_t m, int32_t n, int32_t k, void* stream) {

@@ -168,6 +168,23 @@ __global__ __launch_bounds__(256) void k_graph_sum(const T* __restrict__ v, int6
   }
 }
 
+// out[r, j] = bias[j] + sum_i x[r, i] m[i, j] for narrow matrices (k, n <= 64):
+// one thread per output element; the row's k inputs come from L1 / L2 (n
+// threads share a row), m and bias are a few hundred bytes that stay in L1
+template <typename T>
+__global__ __launch_bounds__(256) void k_narrow_linear(const T* __restrict__ x, int64_t n_rows, int k,
+                                                       const T* __restrict__ m, const T* __restrict__ bias, int n,
+                                                       T* __restrict__ out) {
+  const int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (id >= n_rows * n) return;
+  const int64_t r = id / n;
+  const int j = (int)(id - r * n);
+  T acc = bias ? bias[j] : T(0);
+  const T* xr = x + r * k;
+  for (int i = 0; i < k; ++i) acc += xr[i] * m[(int64_t)i * n + j];
+  out[id] = acc;
+}
+
 // gy = sum of the per-part grad_y partials, in part order
 template <typename T>
 __global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, int nparts, int64_t n,
@@ -568,71 +585,6 @@ __global__ void k_nl_sortbins(const int* __restrict__ bstart, int nbins, int* __
   }
 }
 
-// For receiver a: every source b and shift S with |r_a - r_b + S.cell|^2 < rc^2,
-// (b, S) != (a, 0).  The distance is evaluated exactly as the brute-force
-// oracle does for edge (i=b, j=a, S): d = r_a - r_b, v = d + S0 c0 + S1 c1 + S2 c2.
-template <bool FILL>
-__global__ __launch_bounds__(64) void k_nl_edges(const double* __restrict__ pos, int n, NlGeom g,
-                                                 const int* __restrict__ abin, const int* __restrict__ aimg,
-                                                 const int* __restrict__ bstart, const int* __restrict__ batoms,
-                                                 int* __restrict__ counts, const int* __restrict__ rowptr,
-                                                 int* __restrict__ src, int* __restrict__ shift) {
-#pragma clang fp contract(off)
-  const int a = blockIdx.x * blockDim.x + threadIdx.x;
-  if (a >= n) return;
-  const double ax = pos[3 * a], ay = pos[3 * a + 1], az = pos[3 * a + 2];
-  const int lin = abin[a];
-  const int ba[3] = {lin / (g.nb[1] * g.nb[2]), (lin / g.nb[2]) % g.nb[1], lin % g.nb[2]};
-  const int oa[3] = {aimg[3 * a], aimg[3 * a + 1], aimg[3 * a + 2]};
-  int cnt = 0;
-  const int base = FILL ? rowptr[a] : 0;
-  int lo[3], hi[3];
-  for (int k = 0; k < 3; ++k) {
-    lo[k] = ba[k] - g.reach[k];
-    hi[k] = ba[k] + g.reach[k];
-    if (!g.pbc[k]) {
-      lo[k] = lo[k] < 0 ? 0 : lo[k];
-      hi[k] = hi[k] >= g.nb[k] ? g.nb[k] - 1 : hi[k];
-    }
-  }
-  for (int bx = lo[0]; bx <= hi[0]; ++bx) {
-    const int wx = ((bx % g.nb[0]) + g.nb[0]) % g.nb[0];
-    const int sx = (bx - wx) / g.nb[0];
-    for (int by = lo[1]; by <= hi[1]; ++by) {
-      const int wy = ((by % g.nb[1]) + g.nb[1]) % g.nb[1];
-      const int sy = (by - wy) / g.nb[1];
-      for (int bz = lo[2]; bz <= hi[2]; ++bz) {
-        const int wz = ((bz % g.nb[2]) + g.nb[2]) % g.nb[2];
-        const int sz = (bz - wz) / g.nb[2];
-        const int bl = (wx * g.nb[1] + wy) * g.nb[2] + wz;
-        for (int q = bstart[bl]; q < bstart[bl + 1]; ++q) {
-          const int b = batoms[q];
-          const int S0 = aimg[3 * b] - oa[0] - sx;
-          const int S1 = aimg[3 * b + 1] - oa[1] - sy;
-          const int S2 = aimg[3 * b + 2] - oa[2] - sz;
-          if (b == a && S0 == 0 && S1 == 0 && S2 == 0) continue;
-          const double d0 = ax - pos[3 * b], d1 = ay - pos[3 * b + 1], d2 = az - pos[3 * b + 2];
-          const double s0 = (double)S0, s1 = (double)S1, s2 = (double)S2;
-          const double v0 = d0 + s0 * g.cell[0] + s1 * g.cell[3] + s2 * g.cell[6];
-          const double v1 = d1 + s0 * g.cell[1] + s1 * g.cell[4] + s2 * g.cell[7];
-          const double v2 = d2 + s0 * g.cell[2] + s1 * g.cell[5] + s2 * g.cell[8];
-          const double r2 = v0 * v0 + v1 * v1 + v2 * v2;
-          if (r2 < g.rc2) {
-            if (FILL) {
-              const int slot = base + cnt;
-              src[slot] = b;
-              shift[3 * slot] = S0;
-              shift[3 * slot + 1] = S1;
-              shift[3 * slot + 2] = S2;
-            }
-            ++cnt;
-          }
-        }
-      }
-    }
-  }
-  if (!FILL) counts[a] = cnt;
-}
 
 // ------------------------------------------------- batched neighbours --
 // Many structures in one pass.  The host-built plan table holds per structure
@@ -700,7 +652,7 @@ __global__ void k_nlb_rank(const int* __restrict__ abin, int n, const int* __res
 }
 
 // is source b (with periodic shift S) within the cutoff of receiver a?  The
-// same arithmetic as k_nl_edges (no contraction), the self image excluded.
+// brute-force oracle's arithmetic (no contraction), the self image excluded.
 static __device__ __forceinline__ bool nl_pair(const double* __restrict__ pos, const int* __restrict__ aimg,
                                                const NlGeom& g, int a, double ax, double ay, double az,
                                                const int* oa, int sx, int sy, int sz, int b, int* S) {
@@ -716,6 +668,87 @@ static __device__ __forceinline__ bool nl_pair(const double* __restrict__ pos, c
   const double v2 = d2 + s0 * g.cell[2] + s1 * g.cell[5] + s2 * g.cell[8];
   const double r2 = v0 * v0 + v1 * v1 + v2 * v2;
   return r2 < g.rc2;
+}
+
+// For receiver a: every source b and shift S with |r_a - r_b + S.cell|^2 < rc^2,
+// (b, S) != (a, 0) (nl_pair: the distance exactly as the brute-force oracle
+// evaluates it for edge (i=b, j=a, S)).  WAVE = false: one thread per receiver;
+// WAVE = true: one wavefront per receiver (four per workgroup), the 64 lanes
+// over each bin's candidates, counts by ballot and fill slots by the rank of
+// the lane's hit among the wave's hits, so the edge order is the serial one.
+// A structure of n atoms gives only n / 64 wavefronts with a thread per
+// receiver; below NL_WAVE_MAX atoms the wavefront form fills the GPU.
+constexpr int NL_WAVE_MAX = 32768;
+
+template <bool FILL, bool WAVE>
+__global__ __launch_bounds__(256) void k_nl_edges(const double* __restrict__ pos, int n, NlGeom g,
+                                                  const int* __restrict__ abin, const int* __restrict__ aimg,
+                                                  const int* __restrict__ bstart, const int* __restrict__ batoms,
+                                                  int* __restrict__ counts, const int* __restrict__ rowptr,
+                                                  int* __restrict__ src, int* __restrict__ shift) {
+  const int lane = WAVE ? (int)(threadIdx.x & 63) : 0;
+  const int a = WAVE ? (int)(blockIdx.x * 4 + (threadIdx.x >> 6)) : (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (a >= n) return;
+  const double ax = pos[3 * a], ay = pos[3 * a + 1], az = pos[3 * a + 2];
+  const int lin = abin[a];
+  const int ba[3] = {lin / (g.nb[1] * g.nb[2]), (lin / g.nb[2]) % g.nb[1], lin % g.nb[2]};
+  const int oa[3] = {aimg[3 * a], aimg[3 * a + 1], aimg[3 * a + 2]};
+  int cnt = 0;
+  const int base = FILL ? rowptr[a] : 0;
+  int lo[3], hi[3];
+  for (int k = 0; k < 3; ++k) {
+    lo[k] = ba[k] - g.reach[k];
+    hi[k] = ba[k] + g.reach[k];
+    if (!g.pbc[k]) {
+      lo[k] = lo[k] < 0 ? 0 : lo[k];
+      hi[k] = hi[k] >= g.nb[k] ? g.nb[k] - 1 : hi[k];
+    }
+  }
+  for (int bx = lo[0]; bx <= hi[0]; ++bx) {
+    const int wx = ((bx % g.nb[0]) + g.nb[0]) % g.nb[0];
+    const int sx = (bx - wx) / g.nb[0];
+    for (int by = lo[1]; by <= hi[1]; ++by) {
+      const int wy = ((by % g.nb[1]) + g.nb[1]) % g.nb[1];
+      const int sy = (by - wy) / g.nb[1];
+      for (int bz = lo[2]; bz <= hi[2]; ++bz) {
+        const int wz = ((bz % g.nb[2]) + g.nb[2]) % g.nb[2];
+        const int sz = (bz - wz) / g.nb[2];
+        const int bl = (wx * g.nb[1] + wy) * g.nb[2] + wz;
+        const int q1 = bstart[bl + 1];
+        for (int q0 = bstart[bl]; q0 < q1; q0 += (WAVE ? 64 : 1)) {
+          const int q = q0 + lane;
+          int S[3] = {0, 0, 0};
+          int b = 0;
+          bool hit = false;
+          if (q < q1) {
+            b = batoms[q];
+            hit = nl_pair(pos, aimg, g, a, ax, ay, az, oa, sx, sy, sz, b, S);
+          }
+          if (WAVE) {
+            const unsigned long long m = __ballot(hit);
+            if (FILL && hit) {
+              const int slot = base + cnt + __popcll(m & ((1ull << lane) - 1ull));
+              src[slot] = b;
+              shift[3 * slot] = S[0];
+              shift[3 * slot + 1] = S[1];
+              shift[3 * slot + 2] = S[2];
+            }
+            cnt += __popcll(m);
+          } else if (hit) {
+            if (FILL) {
+              const int slot = base + cnt;
+              src[slot] = b;
+              shift[3 * slot] = S[0];
+              shift[3 * slot + 1] = S[1];
+              shift[3 * slot + 2] = S[2];
+            }
+            ++cnt;
+          }
+        }
+      }
+    }
+  }
+  if (!FILL && lane == 0) counts[a] = cnt;
 }
 
 // WAVE = false: one thread per receiver (large structures: enough receivers
@@ -1313,8 +1346,12 @@ int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const 
   hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bcount, (int)nbins, bstart);
   hipLaunchKernelGGL(k_nl_scatter, ga, ba, 0, s, abin, n, bstart, bfill, batoms);
   hipLaunchKernelGGL(k_nl_sortbins, dim3((unsigned)((nbins + 255) / 256)), dim3(256), 0, s, bstart, (int)nbins, batoms);
-  hipLaunchKernelGGL((k_nl_edges<false>), dim3((n + 63) / 64), dim3(64), 0, s, pos, n, g, abin, aimg, bstart, batoms,
-                     counts, nullptr, nullptr, nullptr);
+  if (n < NL_WAVE_MAX)
+    hipLaunchKernelGGL((k_nl_edges<false, true>), dim3((n + 3) / 4), dim3(256), 0, s, pos, n, g, abin, aimg, bstart,
+                       batoms, counts, nullptr, nullptr, nullptr);
+  else
+    hipLaunchKernelGGL((k_nl_edges<false, false>), dim3((n + 255) / 256), dim3(256), 0, s, pos, n, g, abin, aimg,
+                       bstart, batoms, counts, nullptr, nullptr, nullptr);
   return check_launch("tace_nl_count");
 }
 
@@ -1334,8 +1371,12 @@ int tace_nl_fill(const double* pos, int64_t n_atoms, const double* cell, const i
   const int* bstart = bcount + nbins;
   const int* bfill = bstart + nbins + 1;
   const int* batoms = bfill + nbins;
-  hipLaunchKernelGGL((k_nl_edges<true>), dim3((n + 63) / 64), dim3(64), 0, s, pos, n, g, abin, aimg, bstart, batoms,
-                     nullptr, rowptr, src, shifts);
+  if (n < NL_WAVE_MAX)
+    hipLaunchKernelGGL((k_nl_edges<true, true>), dim3((n + 3) / 4), dim3(256), 0, s, pos, n, g, abin, aimg, bstart,
+                       batoms, nullptr, rowptr, src, shifts);
+  else
+    hipLaunchKernelGGL((k_nl_edges<true, false>), dim3((n + 255) / 256), dim3(256), 0, s, pos, n, g, abin, aimg,
+                       bstart, batoms, nullptr, rowptr, src, shifts);
   return check_launch("tace_nl_fill");
 }
 
@@ -1470,6 +1511,25 @@ int tace_rows_accumulate(int dtype, const void* rows, int64_t n_rows, int64_t wi
                          const int32_t* slot, const int32_t* target, int64_t n_segments, void* out,
                          int64_t n_out_rows, void* stream) {
   return rows_accumulate(dtype, rows, n_rows, width, rowptr, slot, target, n_segments, 1, out, n_out_rows, stream);
+}
+
+int tace_narrow_linear(int dtype, const void* x, int64_t n_rows, int32_t k, const void* m, const void* bias,
+                       int32_t n, void* out, void* stream) {
+  if (n_rows < 0 || k <= 0 || k > 64 || n <= 0 || n > 64) return fail("tace_narrow_linear: bad sizes (k, n in 1..64)");
+  if (n_rows == 0) return 0;
+  if (!x || !m || !out) return fail("tace_narrow_linear: null pointer");
+  if (n_rows * n / 256 + 1 > (int64_t)UINT32_MAX) return fail("tace_narrow_linear: too many rows");
+  const dim3 g((unsigned)((n_rows * n + 255) / 256)), b(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == TACE_F32)
+    hipLaunchKernelGGL(k_narrow_linear<float>, g, b, 0, s, (const float*)x, n_rows, (int)k, (const float*)m,
+                       (const float*)bias, (int)n, (float*)out);
+  else if (dtype == TACE_F64)
+    hipLaunchKernelGGL(k_narrow_linear<double>, g, b, 0, s, (const double*)x, n_rows, (int)k, (const double*)m,
+                       (const double*)bias, (int)n, (double*)out);
+  else
+    return fail("tace_narrow_linear: dtype must be TACE_F32 or TACE_F64");
+  return check_launch("tace_narrow_linear");
 }
 
 int tace_graph_sum(int dtype, const void* values, int64_t n_rows, int64_t width, const int64_t* ptr,

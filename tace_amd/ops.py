@@ -1135,10 +1135,11 @@ def bf16_fragment_order(B: torch.Tensor) -> torch.Tensor:
 
 
 def so2_gemm_bf16(a: torch.Tensor, b_frag: torch.Tensor, n: int, k: int,
-                  bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+                  bias: Optional[torch.Tensor] = None, ktiled: bool = False) -> torch.Tensor:
     """``tace_so2_gemm_bf16``: a [m, k] bfloat16 @ B [k, n] (given in fragment
     order, ``bf16_fragment_order``) with float32 sums (+ bias [n] float32);
-    returns float32 [m, n]."""
+    returns float32 [m, n].  ktiled: the k-tiled kernel
+    (``tace_so2_gemm_bf16_kt``, for large k)."""
     if not a.is_cuda or a.dim() != 2 or a.dtype != torch.bfloat16 or a.shape[1] != k or a.stride(1) != 1:
         raise ValueError("so2 gemm: a must be a bfloat16 GPU matrix [m, k] with unit column stride")
     nks, nb = (k + 31) // 32, (n + 15) // 16
@@ -1149,8 +1150,9 @@ def so2_gemm_bf16(a: torch.Tensor, b_frag: torch.Tensor, n: int, k: int,
     m = a.shape[0]
     out = torch.empty(m, n, dtype=torch.float32, device=a.device)
     tok = _t0("so2_gemm_bf16")
-    N.check(N.lib().tace_so2_gemm_bf16(a.data_ptr(), a.stride(0), b_frag.data_ptr(), N.ptr(bias), out.data_ptr(), n,
-                                       m, n, k, N.stream_ptr(a.device)), "tace_so2_gemm_bf16")
+    fn = "tace_so2_gemm_bf16_kt" if ktiled else "tace_so2_gemm_bf16"
+    N.check(getattr(N.lib(), fn)(a.data_ptr(), a.stride(0), b_frag.data_ptr(), N.ptr(bias), out.data_ptr(), n, m, n, k,
+                                 N.stream_ptr(a.device)), fn)
     _t1(tok, (m, n, k))
     return out
 
@@ -1182,6 +1184,25 @@ def rows_accumulate(out: torch.Tensor, rows: torch.Tensor, rowptr: torch.Tensor,
                                              rowptr.data_ptr(), N.ptr(slot), N.ptr(target), n_seg, out.data_ptr(),
                                              out.shape[0], N.stream_ptr(out.device)), "tace_rows_accumulate")
     _t1(tok, (rows.shape[0], out.shape[1], min(n_seg, out.shape[0])))
+    return out
+
+
+def narrow_linear(x: torch.Tensor, m: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x [rows, k] @ m [k, n] (+ bias [n]) for k, n <= 64 (``tace_narrow_linear``;
+    no autograd: the fused TECE operator's radial projection and its input
+    gradient)."""
+    dt = x.dtype
+    rows, k = x.shape
+    _req(x, "x", dt)
+    _req(m, "m", dt, (k, m.shape[1]))
+    n = m.shape[1]
+    if bias is not None:
+        _req(bias, "bias", dt, (n,))
+    out = torch.empty(rows, n, dtype=dt, device=x.device)
+    tok = _t0("narrow_linear")
+    N.check(N.lib().tace_narrow_linear(N.dtype_code(dt), x.data_ptr(), rows, k, m.data_ptr(), N.ptr(bias), n,
+                                       out.data_ptr(), N.stream_ptr(x.device)), "tace_narrow_linear")
+    _t1(tok, (rows, k, n))
     return out
 
 

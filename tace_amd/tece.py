@@ -391,21 +391,51 @@ def sub_plan(plan: ops.EdgePlan, n0: int, n1: int, e0: int, e1: int) -> ops.Edge
 
 
 # ----------------------------------------------------------- fused operator --
-# bf16 channel mixing: SO(2) GEMMs on tace_so2_gemm_bf16 (bias in the
-# epilogue) where it measured faster than the library GEMM on fe101k
+# bf16 channel mixing: SO(2) GEMMs on tace_so2_gemm_bf16 / _kt (bias in the
+# epilogue) where they measured faster than the library GEMM on fe101k
 # (_so2_route); False: torch.mm / addmm (addmm copies the bias into the output
-# and accumulates onto it)
+# and accumulates onto it); SO2_GEMM_ALL: every shape on the hand-written ones
 SO2_GEMM = True
 SO2_GEMM_ALL = False
 
 
-def _so2_route(k: int, n: int, bias: bool) -> bool:
-    """The shapes [rows, k] x [k, n] that tace_so2_gemm_bf16 runs faster
-    than the library (fe101k, per step): every biased one (k 768 -> 1152:
-    21.3 -> 16.5 ms, 384 -> 384: 12.7 -> 7.5, 96 -> 384: 5.1 -> 2.1), k <= 128
-    (0.2-0.5 ms each) and 192 -> 512 (6.7 -> 6.1).  The library keeps 256 ->
-    256 (8.6 vs 9.6), 512 -> 192, 1152 -> 768 (10.6 vs 16.6) and the rest."""
-    return SO2_GEMM_ALL or bias or k <= 128 or (k <= 192 and n >= 512)
+# kernel per SO(2) GEMM shape (k, n, biased) under bf16 mixing: "kt" =
+# tace_so2_gemm_bf16_kt (A through LDS in 64-k stages, 128 x 256 tiles), "lds"
+# = tace_so2_gemm_bf16 (a row tile's whole k in LDS), None = the library
+# (torch.mm / addmm).  Measured per call on the fe101k chunk shapes (2^20
+# edges: block 0 has 1 M rows, blocks m > 0 2 M), library / lds / kt in ms:
+#   biased:   384->384 1.22 / 0.77 / 0.72, 768->1152 3.90 / 3.06 / 2.52,
+#             96->384 0.90 / 0.37 / 0.74
+#   1 M rows: 384->96 0.30 / 0.33 / 0.25, 1152->768 2.03 / 3.24 / 2.14,
+#             384->384 0.64 / 0.71 / 0.62
+#   2 M rows: 256->256 0.68 / 0.89 / 0.65, 512->192 0.82 / 1.07 / 0.78,
+#             96->256 0.56 / 0.55 / 0.76, 256->96 0.45 / 0.47 / 0.38,
+#             192->512 1.21 / 1.19 / 1.23, 128->128 0.31 / 0.33 / 0.33,
+#             256->192 0.59 / 0.78 / 0.54, 96->128 0.33 / 0.30 / 0.51,
+#             128->96 0.35 / 0.29 / 0.28, 192->256 0.65 / 0.76 / 0.59
+# (the library's bias costs a copy of the broadcast bias into the output plus
+# a beta = 1 pass; k = 96 is not a multiple of 64, so the k-tiled kernel takes
+# its slower general path).  Every shape takes a hand-written kernel: where
+# the library is ahead (1152->768, 128->128) it is by 4-5%.
+_SO2_TABLE = {
+    (384, 384, True): "kt", (768, 1152, True): "kt", (96, 384, True): "lds",
+    (384, 96, False): "kt", (1152, 768, False): "kt", (384, 384, False): "kt",
+    (256, 256, False): "kt", (512, 192, False): "kt", (96, 256, False): "lds", (256, 96, False): "kt",
+    (192, 512, False): "lds", (128, 128, False): "kt", (256, 192, False): "kt", (96, 128, False): "lds",
+    (128, 96, False): "kt", (192, 256, False): "kt",
+}
+
+
+def _so2_route(k: int, n: int, bias: bool):
+    """Kernel for the SO(2) GEMM [rows, k] x [k, n] (+ bias): "kt", "lds" or
+    None (the library); see _SO2_TABLE."""
+    if SO2_GEMM_ALL:
+        return "kt" if k >= 256 else "lds"
+    key = (k, n, bool(bias))
+    if key in _SO2_TABLE:
+        return _SO2_TABLE[key]
+    return "kt" if k % 64 == 0 else "lds"
+
 
 class _FusedParams:
     """Everything the fused TECE operator needs from the frozen modules,
@@ -456,20 +486,22 @@ class _FusedParams:
         # each entry keeps its operand alive)
         self._frag = {}
 
-    def _so2(self, x, B, b=None):
-        """x @ B (+ b) on ``tace_so2_gemm_bf16`` (bf16 operands, float32 sums,
-        bias in the epilogue); B's fragment-order copy is made on first use."""
+    def _so2(self, x, B, b=None, kernel="lds"):
+        """x @ B (+ b) on ``tace_so2_gemm_bf16`` or, kernel "kt", its k-tiled
+        variant (bf16 operands, float32 sums, bias in the epilogue); B's
+        fragment-order copy is made on first use."""
         f = self._frag.get(id(B))
         if f is None:
             f = self._frag[id(B)] = (ops.bf16_fragment_order(B), B)
-        return ops.so2_gemm_bf16(x, f[0], B.shape[1], B.shape[0], b)
+        return ops.so2_gemm_bf16(x, f[0], B.shape[1], B.shape[0], b, ktiled=kernel == "kt")
 
     def mm(self, x, WT, b=None):
         """x @ WT (+ b): bf16 operands with float32 accumulation and output
         under bf16 mixing, else in the features' precision."""
         if self.bf16:
-            if SO2_GEMM and x.dtype == torch.bfloat16 and _so2_route(WT.shape[0], WT.shape[1], b is not None):
-                return self._so2(x, WT, b)
+            r = _so2_route(WT.shape[0], WT.shape[1], b is not None) if SO2_GEMM else None
+            if r is not None and x.dtype == torch.bfloat16:
+                return self._so2(x, WT, b, r)
             if b is None:
                 return torch.mm(x, WT, out_dtype=torch.float32)
             return torch.addmm(b, x, WT, out_dtype=torch.float32)
@@ -477,8 +509,9 @@ class _FusedParams:
 
     def mm_grad(self, g, WN):
         if self.bf16:
-            if SO2_GEMM and g.dtype == torch.bfloat16 and _so2_route(WN.shape[0], WN.shape[1], False):
-                return self._so2(g, WN)
+            r = _so2_route(WN.shape[0], WN.shape[1], False) if SO2_GEMM else None
+            if r is not None and g.dtype == torch.bfloat16:
+                return self._so2(g, WN, None, r)
             return torch.mm(g, WN, out_dtype=torch.float32)
         return torch.mm(g, WN)
 
@@ -500,7 +533,7 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     key = [P.mm(ms[m], P.k_T[m], P.k_b if m == 0 else None) for m in range(L + 1)]
     query = [P.mm(md[m], P.q_T[m], P.q_b if m == 0 else None) for m in range(L + 1)]
     del ms, md
-    rp = torch.addmm(P.rp_b, R, P.rp_T)
+    rp = ops.narrow_linear(R, P.rp_T, P.rp_b)
     alpha = ops.launch_softmax_fwd(ops.launch_score_fwd(query, key, rp, P.tscale, L, H), plan)
     ys = [P.mm(mw[m], P.s_T[m], P.s_b if m == 0 else None) for m in range(L + 1)]
     del mw
@@ -533,7 +566,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     gms = [P.mm_grad(gk[m], P.k_N[m]) for m in range(L + 1)]
     gmd = [P.mm_grad(gq[m], P.q_N[m]) for m in range(L + 1)]
     del gq, gk
-    gR = torch.mm(grp, P.rp_N)
+    gR = ops.narrow_linear(grp, P.rp_N)
     # edges in receiver-CSR order: the receiver rows come as run sums of each
     # workgroup's four edges, a quarter of the rows to write and read back
     runs = ops.ROTIN_RUNS if plan.eid is None and ops.rotate_in_runs_ok(x_lc) else 1

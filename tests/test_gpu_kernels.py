@@ -676,30 +676,34 @@ def test_rows_accumulate_matches_index_add(cuda, dtype, width):
 
 
 # ------------------------------------------- TECE SO(2) GEMM under bf16 mixing ----
+@pytest.mark.parametrize("ktiled", [False, True])
 @pytest.mark.parametrize("m,k,n,bias,pad", [(5000, 96, 384, True, 0), (3000, 384, 384, True, 0),
                                             (2500, 768, 1152, True, 0), (2100, 1152, 768, False, 0),
                                             (4099, 256, 256, False, 0), (777, 100, 70, True, 0),
-                                            (1500, 128, 96, False, 24), (33, 512, 192, False, 8)])
-def test_so2_gemm_bf16_matches_float32_product(cuda, m, k, n, bias, pad):
-    """``tace_so2_gemm_bf16`` against the float32 product of the same bf16
-    values (exact products, so only the order of the float32 sums differs):
-    the SO(2) linear shapes of the TECE layer, k and n tails, rows past the
-    last full tile, a row stride above k."""
+                                            (1500, 128, 96, False, 24), (33, 512, 192, False, 8),
+                                            (300, 1000, 300, True, 4), (129, 40, 257, False, 0)])
+def test_so2_gemm_bf16_matches_float32_product(cuda, m, k, n, bias, pad, ktiled):
+    """``tace_so2_gemm_bf16`` and its k-tiled variant against the float32
+    product of the same bf16 values (exact products, so only the order of the
+    float32 sums differs): the SO(2) linear shapes of the TECE layer, k and n
+    tails (k not a multiple of 32 or 64, n past a 256-column tile), rows past
+    the last full tile, a row stride above k."""
     from tace_amd import ops
     g = torch.Generator().manual_seed(k + n)
     a_full = torch.randn(m, k + pad, generator=g).to(torch.bfloat16).to(cuda)
     a = a_full[:, :k]
     B = torch.randn(k, n, generator=g).to(torch.bfloat16).to(cuda)
     b = torch.randn(n, generator=g).to(cuda) if bias else None
-    got = ops.so2_gemm_bf16(a, ops.bf16_fragment_order(B), n, k, b)
+    got = ops.so2_gemm_bf16(a, ops.bf16_fragment_order(B), n, k, b, ktiled=ktiled)
     want = a.float() @ B.float() + (b if bias else 0.0)
     scale = (a.float().abs() @ B.float().abs()).amax(1, keepdim=True) + 1e-30
     err = ((got - want).abs() / scale).max().item()
     assert got.shape == (m, n) and err < 2e-6, err
 
 
+@pytest.mark.parametrize("fn", ["tace_so2_gemm_bf16", "tace_so2_gemm_bf16_kt"])
 @pytest.mark.parametrize("n,ldo", [(6, 8), (70, 76), (33, 40)])
-def test_so2_gemm_bf16_padded_output_rows_untouched(cuda, n, ldo):
+def test_so2_gemm_bf16_padded_output_rows_untouched(cuda, n, ldo, fn):
     """Through the C ABI with an output row stride above n: columns n..ldo-1
     of every row (a strided view's neighbours) keep their sentinel."""
     from tace_amd import _native as N
@@ -710,10 +714,24 @@ def test_so2_gemm_bf16_padded_output_rows_untouched(cuda, n, ldo):
     bias = torch.randn(n, generator=g).to(cuda)
     bf = ops.bf16_fragment_order(B)
     out = torch.full((m, ldo), 12345.0, dtype=torch.float32, device=cuda)
-    N.check(N.lib().tace_so2_gemm_bf16(a.data_ptr(), k, bf.data_ptr(), bias.data_ptr(), out.data_ptr(), ldo, m, n, k,
-                                       N.stream_ptr(a.device)), "tace_so2_gemm_bf16")
+    N.check(getattr(N.lib(), fn)(a.data_ptr(), k, bf.data_ptr(), bias.data_ptr(), out.data_ptr(), ldo, m, n, k,
+                                 N.stream_ptr(a.device)), fn)
     torch.cuda.synchronize()
     assert bool((out[:, n:] == 12345.0).all()), "the kernel wrote past column n"
     want = a.float() @ B.float() + bias
     scale = (a.float().abs() @ B.float().abs()).amax(1, keepdim=True) + 1e-30
     assert ((out[:, :n] - want).abs() / scale).max().item() < 2e-6
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("k,n,bias", [(8, 8, True), (8, 8, False), (1, 64, True), (64, 3, False)])
+def test_narrow_linear_matches_torch(cuda, dtype, k, n, bias):
+    """``tace_narrow_linear`` (the TECE radial projection and its input
+    gradient) against a float64 product, rows not a multiple of the block."""
+    g = torch.Generator().manual_seed(k * 100 + n)
+    x = torch.randn(1037, k, generator=g, dtype=torch.float64)
+    m = torch.randn(k, n, generator=g, dtype=torch.float64)
+    b = torch.randn(n, generator=g, dtype=torch.float64) if bias else None
+    got = ops.narrow_linear(x.to(dtype).to(cuda), m.to(dtype).to(cuda), None if b is None else b.to(dtype).to(cuda))
+    want = x @ m + (b if bias else 0.0)
+    close(got, want, dtype, "narrow linear")

@@ -1157,7 +1157,9 @@ class TACE(torch.nn.Module):
         num_graphs = ptr.numel() - 1
         sp = SpeciesPlan(attrs, exchange, pairs, natural=ops.MODE.export, counts=_opt(data, "_species_counts"))
         x = self.representation(attrs, plan, edge_vector, sp, data["edge_index"])
-        e_base = (attrs @ self.atomic_energy_layer.atomic_energy.T)[:, 0]
+        # E0(Z_n) (OneHotToAtomicEnergy, blocks.py:250-286) as a masked row sum (a
+        # [N, S] x [S, 1] product would be a library GEMM launch)
+        e_base = (attrs * self.atomic_energy_layer.atomic_energy[0]).sum(-1)
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
         num_nodes = ptr[1:] - ptr[:-1]
         ei = data["edge_index"]
@@ -1438,8 +1440,10 @@ class TensorModel(torch.nn.Module):
             # compute_symmetric_displacement (tace/models/utils.py:50-79)
             disp = torch.zeros(num_graphs, 3, 3, dtype=pos.dtype, device=pos.device, requires_grad=True)
             sym = 0.5 * (disp + disp.transpose(-1, -2))
-            pos_s = pos + torch.einsum("be,bec->bc", pos, ops.graph_gather(sym, data["ptr"], batch))
-            lat_s = lattice + torch.matmul(lattice, sym)
+            # r + r . sym(eps), L + L . sym(eps) as broadcast products and sums over
+            # the 3-long axis (batched 3 x 3 products would be library GEMM launches)
+            pos_s = pos + (pos.unsqueeze(-1) * ops.graph_gather(sym, data["ptr"], batch)).sum(1)
+            lat_s = lattice + (lattice.unsqueeze(-1) * sym.unsqueeze(1)).sum(2)
             inputs.append(disp)
         else:
             pos_s, lat_s = pos, lattice

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 28
+#define TACE_HIP_ABI_VERSION 29
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -182,12 +182,18 @@ int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void*
 /* Gradients g1 [N, C*d1], g2 [N, C*d2] (and gw for weighted variants) of
  * sum(gout * out).  Variants with many x1 blocks run their backward in parts
  * (one per group of x1 blocks) whose g2 partials go to `workspace` (at least
- * tace_uuu_workspace_elems(vid, N, C) elements; 0 for one part, then
- * workspace may be NULL) and are summed in a fixed order. */
-int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels);
+ * tace_uuu_workspace_elems(vid, N, C, accumulate) elements; 0 for one part
+ * without accumulate bit 1, then workspace may be NULL) and are summed in a
+ * fixed order.  accumulate bit 0 adds grad_x1 to what g1 holds, bit 1 adds
+ * grad_x2 to what g2 holds (instead of overwriting them): the gradient sums of
+ * a tensor that other operators read too.  An accumulated gradient is staged
+ * in the workspace and added after the product kernel, grad_x1 first, so g1
+ * and g2 may be the same array when both bits are set and x1 and x2 are in
+ * one layout (the product of a tensor with itself). */
+int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels, int32_t accumulate);
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
                  int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* workspace,
-                 int64_t workspace_elems, void* stream);
+                 int64_t workspace_elems, int32_t accumulate, void* stream);
 
 /* ---- edge featurisation --------------------------------------------------
  * vec [E, 3] edge vectors; r = |vec| + 1e-9;
@@ -263,13 +269,20 @@ int tace_radial_mlp_out_bwd_pairs_f32(const float* g_out, const int32_t* rows_a,
  *            matrix in w), trans (0: W is [k, n] row-major; 1: W is [n, k]
  *            row-major and W^T is applied -- the input gradient);
  *   scales   double [*]: the contribution's path weight.
- * y[tile] = alpha (sum_c scale_c x_c[rows] @ W_c + bias[bias_off + cols]).
- * Every tile element is written; tiles must not overlap.  The tables live in
+ * y[tile] = addend[tile] + alpha (sum_c scale_c x_c[rows] @ W_c +
+ * bias[bias_off + cols]), addend optional (null: no term) and either y itself
+ * (y += ..., the gradient sums of a tensor read by several linears) or an
+ * array of y's size that does not overlap y.  The entry points below take
+ * addend the same way; their MFMA kernels (tace_seg_linear_presplit_frag and
+ * tace_seg_linear_presplit_ks) start each sum from addend / alpha, so there
+ * the result equals the formula up to float32 rounding and alpha must not be
+ * 0 when addend is given.  Every tile element is written; tiles must not
+ * overlap.  The tables live in
  * device memory and are trusted: the host builds them from the layout
  * (tace_amd.ops.SegLinearPlan) and checks every offset against the array
  * sizes before upload. */
-int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y, const void* w,
-                    const void* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
+int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y, const void* addend,
+                    const void* w, const void* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                     const double* scales, double alpha, void* stream);
 /* The float32 128 x 128 case with the weights split ahead of time (they are
  * constants at inference; the same e3nnElementLinear forward and input
@@ -298,8 +311,8 @@ int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void*
  *   bits. */
 int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, const double* scales, int64_t n_blocks,
                              uint16_t* planes, int64_t plane_stride, void* stream);
-int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
-                             const float* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
+int tace_seg_linear_presplit(const float* x, float* y, const float* addend, const uint16_t* w_planes,
+                             int64_t plane_stride, const float* bias, const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                              double alpha, void* stream);
 /* The same linears' tiles with one contribution of k <= 256 (the input
  * gradients of the product-basis contractions, linear.py:377-482, and any
@@ -315,7 +328,7 @@ int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes,
  *         columns [cb, ce), ce <= n), bias_off (-1 none), x_base (offset of
  *         the tile's row 0 in x), k (0..256, the row stride of x; 0: no
  *         contribution), w_off (the block's offset in w_frag), unused.
- * y[tile] = alpha (x[rows, :k] @ B + bias[bias_off + cols]), the same bits as
+ * y[tile] = addend[tile] + alpha (x[rows, :k] @ B + bias[bias_off + cols]), the same bits as
  * tace_seg_linear_presplit gives for the same tile.  Trusted tables, checked
  * by the host (tace_amd.ops.SegLinearPlan). */
 int32_t tace_seg_linear_ks_rows(int32_t k);
@@ -327,10 +340,12 @@ int32_t tace_seg_linear_ks_rows(int32_t k);
  * multiples of 4 (16-byte rows of x; with x 16-byte aligned the kernel then
  * loads A without per-element tails).  The same bits as
  * tace_seg_linear_presplit for the same tiles. */
-int tace_seg_linear_presplit_frag(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+int tace_seg_linear_presplit_frag(const float* x, float* y, const float* addend, const uint16_t* w_frag,
+                                  const float* bias,
                                   const int64_t* tiles, int64_t n_tiles, const int64_t* contribs, int32_t aligned,
                                   double alpha, void* stream);
-int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+int tace_seg_linear_presplit_ks(const float* x, float* y, const float* addend, const uint16_t* w_frag,
+                                const float* bias,
                                 const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)

@@ -51,9 +51,9 @@ _SIGS = {
     "tace_edge_vec_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_edge_vec_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp]),
     "tace_uuu_fwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp]),
-    "tace_uuu_workspace_elems": (_c_i64, [_c_int, _c_i64, _c_i32]),
+    "tace_uuu_workspace_elems": (_c_i64, [_c_int, _c_i64, _c_i32, _c_i32]),
     "tace_uuu_bwd": (_c_int, [_c_int, _c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i64,
-                              _vp]),
+                              _c_i32, _vp]),
     "tace_edge_basis_fwd": (_c_int, [_c_int, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_edge_basis_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _c_dbl, _c_dbl, _c_i32, _c_i32,
                                      _vp, _vp]),
@@ -82,14 +82,14 @@ _SIGS = {
     "tace_radial_mlp_bwd": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp]),
     "tace_radial_mlp_out_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
     "tace_radial_mlp_out_bwd_f32": (_c_int, [_vp, _vp, _c_i64, _c_i32, ctypes.c_float, _vp, _vp]),
-    "tace_seg_linear": (_c_int, [_c_int, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_dbl, _vp]),
+    "tace_seg_linear": (_c_int, [_c_int, _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_dbl, _vp]),
     "tace_bf16x3_split_blocks": (_c_int, [_vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp]),
-    "tace_seg_linear_presplit": (_c_int, [_vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_dbl, _vp]),
+    "tace_seg_linear_presplit": (_c_int, [_vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _c_i64, _vp, _c_dbl, _vp]),
     "tace_seg_linear_ks_rows": (_c_i32, [_c_i32]),
     "tace_so2_gemm_bf16": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp]),
     "tace_so2_gemm_bf16_kt": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp]),
-    "tace_seg_linear_presplit_ks": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_dbl, _vp]),
-    "tace_seg_linear_presplit_frag": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_dbl, _vp]),
+    "tace_seg_linear_presplit_ks": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_dbl, _vp]),
+    "tace_seg_linear_presplit_frag": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_dbl, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

@@ -18,8 +18,10 @@
 // tile's first row in x), k (width of that input block = row stride), w_off
 // (element offset of its weight matrix), trans (0: B = W [k, n] row-major;
 // 1: B = W^T with W [n, k] row-major -- the input-gradient direction).
-// Output: y[tile] = alpha * (sum_c scale_c x_c[tile rows] @ B_c + bias), every
-// element of every tile written (no accumulation into y).
+// Output: y[tile] = addend[tile] + alpha * (sum_c scale_c x_c[tile rows] @ B_c
+// + bias), every element of every tile written once.  addend is optional (null:
+// no term) and may be y itself (y += ...): each element is read before it is
+// written, by the lane that writes it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -37,7 +39,7 @@ constexpr int TM = 64, TN = 64, TK = 16, PAD = 4;
 // tx*4..tx*4+3 of the tile.  A and B stage through LDS k-major (As[k][row],
 // Bs[k][col]) so the inner product reads one 4-vector of each per k.
 template <typename T>
-__global__ __launch_bounds__(256) void k_seg_linear(const T* __restrict__ x, T* __restrict__ y,
+__global__ __launch_bounds__(256) void k_seg_linear(const T* __restrict__ x, T* y, const T* addend,
                                                     const T* __restrict__ w, const T* __restrict__ bias,
                                                     const int64_t* __restrict__ tiles,
                                                     const int64_t* __restrict__ contribs,
@@ -114,7 +116,9 @@ __global__ __launch_bounds__(256) void k_seg_linear(const T* __restrict__ x, T* 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int col = c0 + tx * 4 + j;
-      if (col < n) y[out_base + (int64_t)r * n + col] = alpha * (acc[i][j] + bv[j]);
+      if (col >= n) continue;
+      const int64_t o = out_base + (int64_t)r * n + col;
+      y[o] = alpha * (acc[i][j] + bv[j]) + (addend ? addend[o] : T(0));
     }
   }
 }
@@ -134,6 +138,27 @@ __device__ __forceinline__ f4 seg_ld4(const float* p, bool vec, bool any, int li
       if (e < lim) v[e] = p[e];
   }
   return v;
+}
+
+// The MFMA kernels start each output's sum from addend / alpha (so that
+// alpha (sum + bias) = addend + alpha (products + bias) up to rounding): the
+// addend is read into the accumulators before the first MFMA, its loads in
+// flight with the tile's first operand loads, instead of a load-add-store
+// round trip per output row in the epilogue.  Rows past `rows` and columns
+// past `ce` start from zero (they are not stored).
+__device__ __forceinline__ f4 addend_init(const float* __restrict__ a, int64_t o, bool rok, int col, int ce,
+                                          bool vec, float inv_alpha) {
+  f4 v = f4{0.f, 0.f, 0.f, 0.f};
+  if (rok) {
+    if (vec && col + 4 <= ce) {
+      v = *(const f4*)(a + o);
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (col + q < ce) v[q] = a[o + q];
+    }
+  }
+  return inv_alpha == 1.f ? v : v * inv_alpha;
 }
 
 // R rows x 32 k of a k-contiguous matrix (row stride k, `nrows` valid rows):
@@ -237,8 +262,8 @@ __device__ __forceinline__ void sb_store_n(unsigned short* lds, int plane, int t
   }
 }
 
-__global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restrict__ x, float* __restrict__ y,
-                                                           const float* __restrict__ w,
+__global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restrict__ x, float* y,
+                                                           const float* addend, const float* __restrict__ w,
                                                            const float* __restrict__ bias,
                                                            const int64_t* __restrict__ tiles,
                                                            const int64_t* __restrict__ contribs,
@@ -322,7 +347,9 @@ __global__ __launch_bounds__(256) void k_seg_linear_bf16x3(const float* __restri
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = wr + 16 * i + 4 * fg + q;
-        if (r < rows) y[out_base + (int64_t)r * n + col] = alpha * (acc[i][j][q] + bv);
+        if (r >= rows) continue;
+        const int64_t o = out_base + (int64_t)r * n + col;
+        y[o] = alpha * (acc[i][j][q] + bv) + (addend ? addend[o] : 0.f);
       }
   }
 }
@@ -362,7 +389,7 @@ __device__ __forceinline__ void sbs_store(unsigned short* lds, int plane, int of
   }
 }
 
-__global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict__ x, float* __restrict__ y,
+__global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict__ x, float* y, const float* addend,
                                                          const unsigned short* __restrict__ wsp, int64_t pstride,
                                                          const float* __restrict__ bias,
                                                          const int64_t* __restrict__ tiles,
@@ -439,7 +466,9 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int r = wr + 16 * i + 4 * fg + q;
-        if (r < rows) y[out_base + (int64_t)r * n + col] = alpha * (acc[i][j][q] + bv);
+        if (r >= rows) continue;
+        const int64_t o = out_base + (int64_t)r * n + col;
+        y[o] = alpha * (acc[i][j][q] + bv) + (addend ? addend[o] : 0.f);
       }
   }
 }
@@ -522,7 +551,7 @@ __device__ __forceinline__ void ft_load_b(const FtLoad& L, int jb0, int nb16, in
 
 template <bool VEC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_seg_linear_bx3f(
-    const float* __restrict__ x, float* __restrict__ y,
+    const float* __restrict__ x, float* y, const float* addend,
                                                          const unsigned short* __restrict__ wfrag,
                                                          const float* __restrict__ bias,
                                                          const int64_t* __restrict__ tiles,
@@ -544,10 +573,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int soff = (t >> 1) * SB_STR + 16 * (t & 1);   // this thread's k16 run of a k-contiguous plane
 
   f4 acc[WM][4];
+  if (addend) {
+    const bool avec = ((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)addend) & 15) == 0);
+    const float ia = 1.f / alpha;
 #pragma unroll
-  for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 4; ++j) {
+        const int r = wr + 16 * i + fr, col = c0 + wc + 16 * j + 4 * fg;
+        acc[i][j] = addend_init(addend, out_base + (int64_t)r * n + col, r < rows, col, n, avec, ia);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // skip contributions without k steps
   int c = cb;
@@ -725,6 +766,7 @@ struct KsTask {
   int64_t out_base, bias_off;
   int rows, n, cb, ce, nks, nb16;
   const unsigned short* wf;
+  const float* addend;   // added to the outputs (null: none; may be y)
 };
 
 // B fragments (three terms, column blocks 2 wq and 2 wq + 1 of column tile c)
@@ -786,7 +828,7 @@ __device__ __forceinline__ void ks_steps(const unsigned short* __restrict__ As, 
 
 // this wavefront's 128 x 32 part of column tile c
 template <int R, int KM, int NKS, int PAR>
-__device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, const KsTask& T, float* __restrict__ y,
+__device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, const KsTask& T, float* y,
                                         const float* __restrict__ bias, float alpha, bool vst, int c, int wq,
                                         int lane, int fr, int fg, u4v (&b0)[3][2], u4v (&b1)[3][2]) {
   // the bias of this lane's 8 columns, loaded before the MFMAs: a load
@@ -802,10 +844,22 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
   }
   constexpr int RB = R / 16;
   f4 acc[RB][2];
+  if (T.addend) {
+    const bool avec = ((T.n & 3) == 0) && ((T.out_base & 3) == 0) && ((((uintptr_t)T.addend) & 15) == 0);
+    const float ia = 1.f / alpha;
 #pragma unroll
-  for (int i = 0; i < RB; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < 2; ++j) {
+        const int r = 16 * i + fr, col = c + 32 * wq + 16 * j + 4 * fg;
+        acc[i][j] = addend_init(T.addend, T.out_base + (int64_t)r * T.n + col, r < T.rows, col, T.ce, avec, ia);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+  }
   ks_steps<R, KM, NKS, PAR, 0>(As, T, c, wq, lane, fr, fg, acc, b0, b1);
   // acc[i][j][q] = out[row 16 i + fr][column c + 32 wq + 16 j + 4 fg + q].
   // Lanes fr and fr ^ 8 trade one block, so that a store writes 8 whole rows
@@ -842,7 +896,7 @@ __device__ __forceinline__ void ks_tile(const unsigned short* __restrict__ As, c
 
 template <int R, int KM, int NKS>
 __device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As, const KsTask& T,
-                                           float* __restrict__ y, const float* __restrict__ bias, float alpha, int grp,
+                                           float* y, const float* __restrict__ bias, float alpha, int grp,
                                            int wq, int lane, int fr, int fg) {
   int c0 = T.cb + 128 * grp;
   if (c0 >= T.ce) return;
@@ -859,7 +913,8 @@ __device__ __forceinline__ void ks_columns(const unsigned short* __restrict__ As
 }
 
 template <int R, int KM>
-__global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __restrict__ x, float* __restrict__ y,
+__global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __restrict__ x, float* y,
+                                                       const float* addend,
                                                        const unsigned short* __restrict__ wfrag,
                                                        const float* __restrict__ bias,
                                                        const int64_t* __restrict__ tasks, float alpha, int n_tasks,
@@ -879,6 +934,7 @@ __global__ __launch_bounds__(KS_THREADS) void k_seg_linear_ks(const float* __res
   const int64_t x_base = td[6];
   const int k = (int)td[7];
   T.wf = wfrag + td[8];
+  T.addend = addend;
   T.nks = (k + 31) >> 5;
   T.nb16 = (T.n + 15) >> 4;
   const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
@@ -986,9 +1042,9 @@ extern "C" int tace_bf16x3_split_blocks(const float* w, const int64_t* blocks, c
   return tace_check_launch("tace_bf16x3_split_blocks");
 }
 
-extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t* w_planes, int64_t plane_stride,
-                                        const float* bias, const int64_t* tiles, int64_t n_tiles,
-                                        const int64_t* contribs, double alpha, void* stream) {
+extern "C" int tace_seg_linear_presplit(const float* x, float* y, const float* addend, const uint16_t* w_planes,
+                                        int64_t plane_stride, const float* bias, const int64_t* tiles,
+                                        int64_t n_tiles, const int64_t* contribs, double alpha, void* stream) {
   if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit: bad tile count");
   if (n_tiles == 0) return 0;
   if (!x || !y || !w_planes || !tiles || !contribs) return tace_fail_msg("tace_seg_linear_presplit: null pointer");
@@ -996,33 +1052,38 @@ extern "C" int tace_seg_linear_presplit(const float* x, float* y, const uint16_t
     return tace_fail_msg("tace_seg_linear_presplit: planes must be 16-byte aligned with a stride that is a multiple of 8");
   const int per = (int)((n_tiles + 7) / 8);
   hipLaunchKernelGGL(k_seg_linear_bx3s, dim3((unsigned)(8 * per)), dim3(256), 0, (hipStream_t)stream, x, y,
-                     (const unsigned short*)w_planes, plane_stride, bias, tiles, contribs, (float)alpha,
+                     addend, (const unsigned short*)w_planes, plane_stride, bias, tiles, contribs, (float)alpha,
                      (int)n_tiles, per);
   return tace_check_launch("tace_seg_linear_presplit");
 }
 
-extern "C" int tace_seg_linear_presplit_frag(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+extern "C" int tace_seg_linear_presplit_frag(const float* x, float* y, const float* addend, const uint16_t* w_frag,
+                                             const float* bias,
                                              const int64_t* tiles, int64_t n_tiles, const int64_t* contribs,
                                              int32_t aligned, double alpha, void* stream) {
   if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_frag: bad tile count");
   if (n_tiles == 0) return 0;
   if (!x || !y || !w_frag || !tiles || !contribs) return tace_fail_msg("tace_seg_linear_presplit_frag: null pointer");
+  if (addend && alpha == 0.0) return tace_fail_msg("tace_seg_linear_presplit_frag: an addend needs alpha != 0");
   if ((((uintptr_t)w_frag) & 15) != 0)
     return tace_fail_msg("tace_seg_linear_presplit_frag: fragment-order weights must be 16-byte aligned");
   const int per = (int)((n_tiles + 7) / 8);
   const dim3 g((unsigned)(8 * per)), b(256);
   if (aligned && (((uintptr_t)x) & 15) == 0)
-    hipLaunchKernelGGL(k_seg_linear_bx3f<true>, g, b, 0, (hipStream_t)stream, x, y, (const unsigned short*)w_frag,
+    hipLaunchKernelGGL(k_seg_linear_bx3f<true>, g, b, 0, (hipStream_t)stream, x, y, addend,
+                       (const unsigned short*)w_frag,
                        bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
   else
-    hipLaunchKernelGGL(k_seg_linear_bx3f<false>, g, b, 0, (hipStream_t)stream, x, y, (const unsigned short*)w_frag,
+    hipLaunchKernelGGL(k_seg_linear_bx3f<false>, g, b, 0, (hipStream_t)stream, x, y, addend,
+                       (const unsigned short*)w_frag,
                        bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
   return tace_check_launch("tace_seg_linear_presplit_frag");
 }
 
 extern "C" int32_t tace_seg_linear_ks_rows(int32_t k) { return k < 0 ? 0 : k <= 128 ? 128 : k <= 256 ? 64 : 0; }
 
-extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const uint16_t* w_frag, const float* bias,
+extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const float* addend, const uint16_t* w_frag,
+                                           const float* bias,
                                            const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha,
                                            void* stream) {
   if (task_rows != 128 && task_rows != 64)
@@ -1030,20 +1091,21 @@ extern "C" int tace_seg_linear_presplit_ks(const float* x, float* y, const uint1
   if (n_tasks < 0 || n_tasks > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_ks: bad task count");
   if (n_tasks == 0) return 0;
   if (!x || !y || !w_frag || !tasks) return tace_fail_msg("tace_seg_linear_presplit_ks: null pointer");
+  if (addend && alpha == 0.0) return tace_fail_msg("tace_seg_linear_presplit_ks: an addend needs alpha != 0");
   if ((((uintptr_t)w_frag) & 15) != 0)
     return tace_fail_msg("tace_seg_linear_presplit_ks: the fragment-order weights must be 16-byte aligned");
   const int per = (int)((n_tasks + 7) / 8);
   if (task_rows == 128)
     hipLaunchKernelGGL((k_seg_linear_ks<128, 128>), dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream,
-                       x, y, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
+                       x, y, addend, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
   else
     hipLaunchKernelGGL((k_seg_linear_ks<64, 256>), dim3((unsigned)(8 * per)), dim3(KS_THREADS), 0, (hipStream_t)stream,
-                       x, y, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
+                       x, y, addend, (const unsigned short*)w_frag, bias, tasks, (float)alpha, (int)n_tasks, per);
   return tace_check_launch("tace_seg_linear_presplit_ks");
 }
 
 extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, const void* x, void* y,
-                               const void* w, const void* bias, const int64_t* tiles, int64_t n_tiles,
+                               const void* addend, const void* w, const void* bias, const int64_t* tiles, int64_t n_tiles,
                                const int64_t* contribs, const double* scales, double alpha, void* stream) {
   if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear: bad tile count");
   const int tr = tile_rows, tc = tile_cols;
@@ -1057,13 +1119,16 @@ extern "C" int tace_seg_linear(int dtype, int32_t tile_rows, int32_t tile_cols, 
   if (mfma) {
     const int per = (int)((n_tiles + 7) / 8);
     const dim3 g8((unsigned)(8 * per));
-    hipLaunchKernelGGL(k_seg_linear_bf16x3, g8, block, 0, s, (const float*)x, (float*)y, (const float*)w,
+    hipLaunchKernelGGL(k_seg_linear_bf16x3, g8, block, 0, s, (const float*)x, (float*)y, (const float*)addend,
+                       (const float*)w,
                        (const float*)bias, tiles, contribs, scales, (float)alpha, (int)n_tiles, per);
   } else if (dtype == TACE_F32)
-    hipLaunchKernelGGL(k_seg_linear<float>, grid, block, 0, s, (const float*)x, (float*)y, (const float*)w,
+    hipLaunchKernelGGL(k_seg_linear<float>, grid, block, 0, s, (const float*)x, (float*)y, (const float*)addend,
+                       (const float*)w,
                        (const float*)bias, tiles, contribs, scales, (float)alpha);
   else if (dtype == TACE_F64)
-    hipLaunchKernelGGL(k_seg_linear<double>, grid, block, 0, s, (const double*)x, (double*)y, (const double*)w,
+    hipLaunchKernelGGL(k_seg_linear<double>, grid, block, 0, s, (const double*)x, (double*)y,
+                       (const double*)addend, (const double*)w,
                        (const double*)bias, tiles, contribs, scales, alpha);
   else
     return tace_fail_msg("tace_seg_linear: dtype must be TACE_F32 or TACE_F64");

@@ -185,15 +185,16 @@ __global__ __launch_bounds__(256) void k_narrow_linear(const T* __restrict__ x, 
   out[id] = acc;
 }
 
-// gy = sum of the per-part grad_y partials, in part order
+// gy = sum of the per-part grad_y partials, in part order (added to what out
+// holds when accumulate != 0)
 template <typename T>
 __global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, int nparts, int64_t n,
-                                                   T* __restrict__ out) {
+                                                   T* __restrict__ out, int accumulate = 0) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n) return;
   T acc = parts[i];
   for (int q = 1; q < nparts; ++q) acc += parts[(size_t)q * n + i];
-  out[i] = acc;
+  out[i] = accumulate ? out[i] + acc : acc;
 }
 
 // ------------------------------------------------------------ edge vectors --
@@ -1200,16 +1201,28 @@ int tace_uuu_fwd(int vid, int dtype, const void* x1, const void* x2, const void*
   return check_launch("tace_uuu_fwd");
 }
 
-int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels) {
+// Workspace of the backward: grad_x2 partials when there are several parts
+// or when grad_x2 is added to g2 (accumulate bit 1), then grad_x1 when it is
+// added to g1 (bit 0); the sums into g1 / g2 run after the product kernel.
+static int64_t uuu_ws_g1_offset(const TpVariant& v, int64_t n_nodes, int32_t channels, int32_t accumulate) {
+  return (v.unparts > 1 || (accumulate & 2)) ? (int64_t)v.unparts * n_nodes * channels * v.d2 : 0;
+}
+
+static int64_t uuu_ws_elems(const TpVariant& v, int64_t n_nodes, int32_t channels, int32_t accumulate) {
+  return uuu_ws_g1_offset(v, n_nodes, channels, accumulate) +
+         ((accumulate & 1) ? n_nodes * (int64_t)channels * v.d1 : 0);
+}
+
+int64_t tace_uuu_workspace_elems(int vid, int64_t n_nodes, int32_t channels, int32_t accumulate) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_workspace_elems: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_workspace_elems: bad sizes");
-  const TpVariant& v = kVariants[vid];
-  return v.unparts > 1 ? (int64_t)v.unparts * n_nodes * channels * v.d2 : 0;
+  if (accumulate & ~3) return fail("tace_uuu_workspace_elems: accumulate takes bits 0 and 1 only");
+  return uuu_ws_elems(kVariants[vid], n_nodes, channels, accumulate);
 }
 
 int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void* w, const void* gout, int64_t n_nodes,
                  int32_t channels, int32_t layout, void* g1, void* g2, void* gw, void* workspace,
-                 int64_t workspace_elems, void* stream) {
+                 int64_t workspace_elems, int32_t accumulate, void* stream) {
   if (vid < 0 || vid >= kNumVariants || kVariants[vid].kind != 1) return fail("tace_uuu_bwd: bad variant id");
   if (channels <= 0 || n_nodes < 0) return fail("tace_uuu_bwd: bad sizes");
   if (!uuu_layout_ok(layout)) return fail("tace_uuu_bwd: layout must be 0, OUT, IN1|OUT or IN1|OUT|IN2 (GROUPED)");
@@ -1220,24 +1233,44 @@ int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void*
     return fail(v.weighted ? "tace_uuu_bwd: this product is weighted: w is required"
                            : "tace_uuu_bwd: this product has no path weights: w must be null");
   if (n_nodes && w && !gw) return fail("tace_uuu_bwd: weighted products need gw");
+  if (accumulate & ~3) return fail("tace_uuu_bwd: accumulate takes bits 0 and 1 only");
+  if (g1 == g2 && n_nodes &&
+      (accumulate != 3 || !(layout & TACE_LAYOUT_IN1_GROUPED) != !(layout & TACE_LAYOUT_IN2_GROUPED) || v.d1 != v.d2))
+    return fail("tace_uuu_bwd: g1 and g2 may be one array only when both accumulate into it, in one layout");
   const int64_t ny = n_nodes * (int64_t)channels * v.d2;
-  const int64_t need = v.unparts > 1 ? (int64_t)v.unparts * ny : 0;
+  const int64_t need = uuu_ws_elems(v, n_nodes, channels, accumulate);
   if (need && !workspace) return fail("tace_uuu_bwd: null workspace");
   if (workspace_elems < need) return fail("tace_uuu_bwd: workspace smaller than tace_uuu_workspace_elems()");
   hipStream_t s = (hipStream_t)stream;
-  // parts > 1: each part writes its grad_x2 partial into the workspace; the
-  // partials are summed into g2 in a fixed order
-  void* g2p = v.unparts > 1 ? workspace : g2;
-  const unsigned nb = (unsigned)((ny + 255) / 256);
+  // parts > 1 (or grad_x2 accumulated): each part writes its grad_x2 partial
+  // into the workspace, and the partials are summed into g2 in a fixed order;
+  // grad_x1 accumulated: the kernel writes it into the workspace too, and it
+  // is added to g1 first (so g1 == g2 receives grad_x1, then grad_x2)
+  const int64_t off1 = uuu_ws_g1_offset(v, n_nodes, channels, accumulate);
+  const bool ws2 = off1 > 0;
+  const int acc1 = accumulate & 1, acc2 = (accumulate >> 1) & 1;
+  const int64_t n1 = n_nodes * (int64_t)channels * v.d1;
+  const unsigned nb = (unsigned)((ny + 255) / 256), nb1 = (unsigned)((n1 + 255) / 256);
   if (dtype == TACE_F32) {
-    v.ubwd_f(x1, x2, w, gout, g1, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
-    if (v.unparts > 1 && ny)
-      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)g2p, v.unparts, ny, (float*)g2);
+    float* wsf = (float*)workspace;
+    void* g1k = acc1 ? (void*)(wsf + off1) : g1;
+    void* g2p = ws2 ? workspace : g2;
+    v.ubwd_f(x1, x2, w, gout, g1k, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
+    if (acc1 && n1)
+      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb1), dim3(256), 0, s, (const float*)g1k, 1, n1, (float*)g1, 1);
+    if (ws2 && ny)
+      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)g2p, v.unparts, ny, (float*)g2,
+                         acc2);
   } else if (dtype == TACE_F64) {
-    v.ubwd_d(x1, x2, w, gout, g1, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
-    if (v.unparts > 1 && ny)
+    double* wsd = (double*)workspace;
+    void* g1k = acc1 ? (void*)(wsd + off1) : g1;
+    void* g2p = ws2 ? workspace : g2;
+    v.ubwd_d(x1, x2, w, gout, g1k, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
+    if (acc1 && n1)
+      hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb1), dim3(256), 0, s, (const double*)g1k, 1, n1, (double*)g1, 1);
+    if (ws2 && ny)
       hipLaunchKernelGGL(k_sum_parts<double>, dim3(nb), dim3(256), 0, s, (const double*)g2p, v.unparts, ny,
-                         (double*)g2);
+                         (double*)g2, acc2);
   } else {
     return fail("tace_uuu_bwd: dtype must be TACE_F32 or TACE_F64");
   }

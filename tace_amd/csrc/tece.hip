@@ -612,6 +612,82 @@ __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, cons
   }
 }
 
+// The same forward for float32 features and an even channel count, two
+// adjacent channels per lane: 8-byte feature and radial-weight loads and
+// 4-byte (bf16) or 8-byte (float32) stores, half the memory instructions of
+// the kernel above.  Each output row sums over its own l block of the
+// block-diagonal Wigner matrix only: the other entries are zeros, whose
+// products the kernel above adds (fma(0, x, a) = a), so the sums are the same
+// bits.  Needs x and radial_w 8-byte aligned and the output blocks aligned to
+// two elements.
+template <int L>
+__device__ __forceinline__ constexpr int m_l(int r) {   // l of m-layout row r
+  if (r <= L) return r;
+  int off = L + 1;
+  for (int m = 1; m <= L; ++m) {
+    const int n = L + 1 - m;
+    if (r < off + 2 * n) return m + (r - off < n ? r - off : r - off - n);
+    off += 2 * n;
+  }
+  return 0;
+}
+
+__device__ __forceinline__ constexpr int l_of(int k) {   // l of l-layout component k
+  int l = 0;
+  while ((l + 1) * (l + 1) <= k) ++l;
+  return l;
+}
+
+__device__ __forceinline__ void st_pair(float* p, float a, float b) { *(float2*)p = make_float2(a, b); }
+__device__ __forceinline__ void st_pair(bf16_t* p, float a, float b) {
+  *(uint32_t*)p = (uint32_t)out_cvt<bf16_t>(a) | ((uint32_t)out_cvt<bf16_t>(b) << 16);
+}
+
+template <typename TO, int L, int NP>
+__global__ __launch_bounds__(256) void k_rotin_fwd_pairs(const float* __restrict__ x, const float* __restrict__ W,
+                                                         const int64_t* __restrict__ rows_src,
+                                                         const int64_t* __restrict__ rows_dst,
+                                                         const float* __restrict__ wr, int64_t n_rows, int64_t E,
+                                                         int C, const Blk<TO> ms, const Blk<TO> md,
+                                                         const Blk<TO> mw) {
+  constexpr int K = (L + 1) * (L + 1), NC = (L + 1) * (L + 2) / 2;
+  const int64_t e = wave_edge();
+  if (e >= E) return;
+  const int lane = (int)threadIdx.x & 63;
+  const float* w = W + e * K * K;
+  const int64_t rs = rows_src[e], rd = rows_dst[e];
+  const int C2 = 2 * C;
+#pragma unroll
+  for (int j = 0; j < NP; ++j) {
+    const int c = 2 * (lane + 64 * j);
+    if (c < C2) {
+      const bool src = c < C;
+      const int64_t row = src ? rs : rd;
+      const int cc = src ? c : c - C;
+      const bool ok = row >= 0 && row < n_rows;
+      float2 xk[K];
+#pragma unroll
+      for (int kk = 0; kk < K; ++kk)
+        xk[kk] = ok ? *(const float2*)(x + (row * K + kk) * C + cc) : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int r = 0; r < K; ++r) {
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < K; ++kk) {
+          if (l_of(kk) != m_l<L>(r)) continue;   // constant after unrolling
+          a0 += w[r * K + kk] * xk[kk].x;
+          a1 += w[r * K + kk] * xk[kk].y;
+        }
+        st_pair(erow<L>(src ? ms : md, e, r, C) + cc, a0, a1);
+        if (wr) {
+          const float2 wv = *(const float2*)(wr + (e * NC + m_comp<L>(r)) * C2 + c);
+          st_pair(erow<L>(mw, e, r, C2) + c, wv.x * a0, wv.y * a1);
+        }
+      }
+    }
+  }
+}
+
 // Sums p[0..P) over the 64 lanes in groups of 16 (reduce16_lanes) and stores
 // the totals at out[0..n).
 template <typename T, int P>
@@ -1252,6 +1328,29 @@ int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const 
     return tace_fail_msg("tace_edge_rotate_in_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
+  // float32 features, even channel count, 8-byte aligned x / radial_w and
+  // outputs aligned to two elements: two channels per lane
+  const size_t oal = dtype == TACE_F32_BF16 ? 4 : 8;
+  bool pairs = (dtype == TACE_F32 || dtype == TACE_F32_BF16) && (channels & 1) == 0 && channels <= 512 &&
+               ((uintptr_t)x & 7) == 0 && ((uintptr_t)radial_w & 7) == 0;
+  for (int m = 0; pairs && m <= lmax; ++m)
+    pairs = ((uintptr_t)m_src[m] % oal) == 0 && ((uintptr_t)m_dst[m] % oal) == 0 &&
+            (!radial_w || ((uintptr_t)m_w[m] % oal) == 0);
+  if (pairs) {
+#define RI_P(TO, LL)                                                                                          \
+  TACE_SLOTS_DISPATCH(channels, NP,                                                                           \
+    hipLaunchKernelGGL((k_rotin_fwd_pairs<TO, LL, NP>), g, b, 0, s, (const float*)x, (const float*)wigner,     \
+                       rows_src, rows_dst, (const float*)radial_w, n_rows, n_edges, channels,                  \
+                       blocks_of<TO>(m_src, lmax), blocks_of<TO>(m_dst, lmax),                                 \
+                       blocks_of<TO>(radial_w ? m_w : nullptr, lmax)))
+    if (dtype == TACE_F32) {
+      if (lmax == 1) { RI_P(float, 1) } else if (lmax == 2) { RI_P(float, 2) } else { RI_P(float, 3) }
+    } else {
+      if (lmax == 1) { RI_P(bf16_t, 1) } else if (lmax == 2) { RI_P(bf16_t, 2) } else { RI_P(bf16_t, 3) }
+    }
+#undef RI_P
+    return tace_check_launch("tace_edge_rotate_in_fwd");
+  }
 #define RI_F(TT, TO, LL)                                                                                    \
   TACE_SLOTS_DISPATCH(2 * channels, NS,                                                                     \
     hipLaunchKernelGGL((k_rotin_fwd<TT, TO, LL, NS>), g, b, 0, s, (const TT*)x, (const TT*)wigner, rows_src, \

@@ -349,49 +349,80 @@ class _LinearLayout:
         return plan
 
 
+def _linear_route(x: torch.Tensor, weight: torch.Tensor, lay: "_LinearLayout", ranges):
+    """(non-empty species ranges, whether the segmented-GEMM kernel runs) of
+    one linear on x: shared weights take the whole row range."""
+    Z = x.shape[0]
+    shared = weight.dim() == 1
+    rr = [(None, 0, Z)] if shared else ranges
+    rr = [r for r in rr if r[2] > r[1]]
+    seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES.get(x.dtype, 1)
+    if shared and x.dtype == torch.float32 and SEG_LINEAR_SHARED_MIN_INS is not None:
+        seg = len(lay.ins) >= SEG_LINEAR_SHARED_MIN_INS and Z > 0
+    return rr, seg
+
+
+def _linear_apply(x, weight, bias, lay: "_LinearLayout", rr, seg: bool, alpha: float, kind: str = "fwd",
+                  out: Optional[torch.Tensor] = None, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One direction of an e3nn linear on group-major rows: ``kind`` "fwd"
+    (x -> out = alpha (x W + bias)) or "bwd" (g_out -> g_x = alpha g_out W^T,
+    no bias), plus ``addend`` when given (``out`` itself for out += ..., or a
+    separate tensor).  Per instruction and species range one GEMM, or all of
+    them in one segmented-GEMM launch (``seg``)."""
+    fwd = kind == "fwd"
+    gin, gout_l = (lay.gin, lay.gout) if fwd else (lay.gout, lay.gin)
+    dim = lay.dim_out if fwd else lay.dim_in
+    Z = x.shape[0]
+    if out is None:
+        out = x.new_empty(Z, dim)
+    if not fwd:
+        bias = None
+    shared = weight.dim() == 1
+    if seg:
+        plan = lay.seg_plan(kind, rr, Z, x, weight, bias)
+        if plan.split_weights:
+            fr = lay.split_weights(kind, weight, frag=True)[0] if plan.n_ks or plan.tile_frag else None
+            pl = (None, 0) if plan.tile_frag else lay.split_weights(kind, weight)
+            return ops.seg_linear_presplit(x, out, *pl, bias, plan, alpha, frag=fr, addend=addend)
+        return ops.seg_linear(x, out, weight, bias, plan, alpha, addend=addend)
+    acc = addend is not None
+    if acc and addend.data_ptr() != out.data_ptr():
+        out.copy_(addend)
+    done = set()
+    for (i, o, off, mi, mo, pw) in lay.ins:
+        src, dst = (i, o) if fwd else (o, i)
+        for (sp, a, b) in rr:
+            W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
+            gout_l.block(out, dst, a, b).addmm_(gin.block(x, src, a, b), W if fwd else W.t(),
+                                                beta=1.0 if acc or (dst, sp) in done else 0.0, alpha=pw * alpha)
+            done.add((dst, sp))
+    if not acc:
+        hit = lay.written if fwd else lay.read
+        for o in range(len(gout_l.blocks)):
+            if o not in hit:
+                gout_l.block(out, o).zero_()
+    if bias is not None:
+        for (o, boff, m) in lay.bias_blocks:
+            for (sp, a, b) in rr:
+                bv = (bias if shared else bias[sp])[boff:boff + m]
+                lay.gout.block(out, o, a, b).add_(bv, alpha=alpha)
+    return out
+
+
 class _LinearFn(torch.autograd.Function):
     """e3nn ``o3.Linear`` on group-major features: per instruction and species
     range one GEMM written in place into the output (``addmm_``, path weight
-    and ``alpha`` in the GEMM's scale), bias added to the 0e blocks.
-    ``weight`` [numel] (shared) or [S, numel] with ``ranges`` = [(species, a,
-    b)] over species-sorted rows.  out = alpha * (linear(x) + bias)."""
+    and ``alpha`` in the GEMM's scale), bias added to the 0e blocks, or all
+    of them in one segmented-GEMM launch.  ``weight`` [numel] (shared) or
+    [S, numel] with ``ranges`` = [(species, a, b)] over species-sorted rows.
+    out = alpha * (linear(x) + bias)."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, lay: _LinearLayout, ranges, alpha: float):
-        Z = x.shape[0]
-        out = x.new_empty(Z, lay.dim_out)
-        shared = weight.dim() == 1
-        rr = [(None, 0, Z)] if shared else ranges
-        rr = [r for r in rr if r[2] > r[1]]
-        ctx.seg = not shared and len(rr) >= SEG_LINEAR_MIN_RANGES.get(x.dtype, 1)
-        if shared and x.dtype == torch.float32 and SEG_LINEAR_SHARED_MIN_INS is not None:
-            ctx.seg = len(lay.ins) >= SEG_LINEAR_SHARED_MIN_INS and Z > 0
+        rr, seg = _linear_route(x, weight, lay, ranges)
         ctx.save_for_backward(x, weight, bias)
-        ctx.lay, ctx.rr, ctx.alpha = lay, rr, alpha
-        if ctx.seg:
-            # all species and instructions in one segmented-GEMM launch
-            plan = lay.seg_plan("fwd", rr, Z, x, weight, bias)
-            if plan.split_weights:
-                fr = lay.split_weights("fwd", weight, frag=True)[0] if plan.n_ks or plan.tile_frag else None
-                pl = (None, 0) if plan.tile_frag else lay.split_weights("fwd", weight)
-                return ops.seg_linear_presplit(x, out, *pl, bias, plan, alpha, frag=fr)
-            return ops.seg_linear(x, out, weight, bias, plan, alpha)
-        done = set()
-        for (i, o, off, mi, mo, pw) in lay.ins:
-            for (sp, a, b) in rr:
-                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
-                lay.gout.block(out, o, a, b).addmm_(lay.gin.block(x, i, a, b), W,
-                                                    beta=1.0 if (o, sp) in done else 0.0, alpha=pw * alpha)
-                done.add((o, sp))
-        for o in range(len(lay.gout.blocks)):
-            if o not in lay.written:
-                lay.gout.block(out, o).zero_()
-        if bias is not None:
-            for (o, boff, m) in lay.bias_blocks:
-                for (sp, a, b) in rr:
-                    bv = (bias if shared else bias[sp])[boff:boff + m]
-                    lay.gout.block(out, o, a, b).add_(bv, alpha=alpha)
-        return out
+        ctx.lay, ctx.rr, ctx.alpha, ctx.seg = lay, rr, alpha, seg
+        return _linear_apply(x, weight, bias, lay, rr, seg, alpha)
 
     @staticmethod
     def backward(ctx, gout):
@@ -399,33 +430,16 @@ class _LinearFn(torch.autograd.Function):
         lay, rr, alpha = ctx.lay, ctx.rr, ctx.alpha
         gout = gout.contiguous()
         shared = weight.dim() == 1
-        gx = torch.empty_like(x) if ctx.needs_input_grad[0] else None
+        gx = None
+        if ctx.needs_input_grad[0]:
+            gx = _linear_apply(gout, weight, None, lay, rr, ctx.seg, alpha, kind="bwd")
         gw = torch.zeros_like(weight) if ctx.needs_input_grad[1] else None
         gb = torch.zeros_like(bias) if bias is not None and ctx.needs_input_grad[2] else None
-        if ctx.seg and gx is not None:
-            plan = lay.seg_plan("bwd", rr, x.shape[0], x, weight, None)
-            if plan.split_weights:
-                fr = lay.split_weights("bwd", weight, frag=True)[0] if plan.n_ks or plan.tile_frag else None
-                pl = (None, 0) if plan.tile_frag else lay.split_weights("bwd", weight)
-                ops.seg_linear_presplit(gout, gx, *pl, None, plan, alpha, frag=fr)
-            else:
-                ops.seg_linear(gout, gx, weight, None, plan, alpha)
-        done = set()
-        for (i, o, off, mi, mo, pw) in lay.ins:
-            for (sp, a, b) in rr:
-                G = lay.gout.block(gout, o, a, b)
-                W = (weight if shared else weight[sp])[off:off + mi * mo].view(mi, mo)
-                if gx is not None and not ctx.seg:
-                    lay.gin.block(gx, i, a, b).addmm_(G, W.t(), beta=1.0 if (i, sp) in done else 0.0,
-                                                      alpha=pw * alpha)
-                    done.add((i, sp))
-                if gw is not None:
+        if gw is not None:
+            for (i, o, off, mi, mo, pw) in lay.ins:
+                for (sp, a, b) in rr:
                     tgt = (gw if shared else gw[sp])[off:off + mi * mo].view(mi, mo)
-                    tgt.addmm_(lay.gin.block(x, i, a, b).t(), G, alpha=pw * alpha)
-        if gx is not None and not ctx.seg:
-            for i in range(len(lay.gin.blocks)):
-                if i not in lay.read:
-                    lay.gin.block(gx, i).zero_()
+                    tgt.addmm_(lay.gin.block(x, i, a, b).t(), lay.gout.block(gout, o, a, b), alpha=pw * alpha)
         if gb is not None:
             for (o, boff, m) in lay.bias_blocks:
                 for (sp, a, b) in rr:
@@ -705,8 +719,13 @@ class O3CgtpInteraction(torch.nn.Module):
 
     def forward(self, x, sp: SpeciesPlan, R, Y, plan: ops.EdgePlan):
         """x: group-major node features in species-sorted row order."""
-        sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
-        x = _exchange_ghosts(self.linear_up(x), self.linear_up.irreps_out, sp, self.layer)
+        if hasattr(self, "resnetBB") and not (ops.MODE.double or ops.MODE.export) \
+                and _frozen(self.linear_up, self.resnetBB):
+            up, sc = _SharedInputLinearsFn.apply(x.contiguous(), self.linear_up, None, self.resnetBB, sp.ranges)
+        else:
+            sc = self.resnetBB(x, sp) if hasattr(self, "resnetBB") else None
+            up = self.linear_up(x)
+        x = _exchange_ghosts(up, self.linear_up.irreps_out, sp, self.layer)
         lay = ops.LAYOUT_IN1_GROUPED | ops.LAYOUT_OUT_GROUPED
         pairs = sp.pairs
         if ops.MODE.double:
@@ -855,6 +874,103 @@ class _SplitUpFn(torch.autograd.Function):
         return gu, None
 
 
+def _frozen(*mods: torch.nn.Module) -> bool:
+    """No parameter of these modules takes a gradient (the inference path)."""
+    return not any(p.requires_grad for m in mods for p in m.parameters())
+
+
+class _SharedInputLinearsFn(torch.autograd.Function):
+    """Two linears of one input as one autograd node (the interaction's
+    linear_up and its resnet linear, ``inter.py:212-227``): the second's input
+    gradient is added to the first's in its GEMM epilogue instead of autograd
+    summing two gradient tensors."""
+
+    @staticmethod
+    def forward(ctx, x, lin_a, ranges_a, lin_b, ranges_b):
+        ra = _linear_route(x, lin_a.weight, lin_a.lay, ranges_a)
+        rb = _linear_route(x, lin_b.weight, lin_b.lay, ranges_b)
+        ctx.args = (lin_a, ra, lin_b, rb)
+        return (_linear_apply(x, lin_a.weight, lin_a.bias, lin_a.lay, *ra, 1.0),
+                _linear_apply(x, lin_b.weight, lin_b.bias, lin_b.lay, *rb, 1.0))
+
+    @staticmethod
+    def backward(ctx, ga, gb):
+        lin_a, ra, lin_b, rb = ctx.args
+        gx = None
+        if ga is not None:
+            gx = _linear_apply(ga.contiguous(), lin_a.weight, None, lin_a.lay, *ra, 1.0, kind="bwd")
+        if gb is not None:
+            gx = _linear_apply(gb.contiguous(), lin_b.weight, None, lin_b.lay, *rb, 1.0, kind="bwd", out=gx,
+                               addend=gx)
+        return gx, None, None, None, None
+
+
+class _ProductBasisFn(torch.autograd.Function):
+    """``CgtpACE.forward`` (``prod.py:216-266``) without path weights as one
+    autograd node: out = linear(sum_nu coefs[nu - 1](f_nu)) + sc with f_1 = x,
+    f_nu = uuu(f_{nu-1}, x).  The coefficient linears add into one buffer in
+    their GEMM epilogues; in the backward each f_nu's gradient through its
+    coefficient linear is added in that GEMM's epilogue to the one through
+    the next product, and the products' gradients of x are added to g_x in
+    their part sums (the uuu backward's accumulate mode)."""
+
+    @staticmethod
+    def forward(ctx, x, sc, mod: "CgtpACE", sp):
+        ranges = None if mod.agnostic else sp.ranges
+        routes = []
+
+        def coef(k, inp, acc=None):
+            L = mod.coefs[k]
+            r = _linear_route(inp, L.weight, L.lay, ranges)
+            routes.append(r)
+            return _linear_apply(inp, L.weight, L.bias, L.lay, *r, 1.0, out=acc, addend=acc)
+
+        outs = coef(0, x)
+        feats, x1s = x, []
+        for nu in range(2, mod.correlation + 1):
+            ace = mod.aces[nu - 2]
+            f = ops.launch_uuu_fwd(feats, x, None, ops.find_variant(ace.key), ace.C, ops.LAYOUT_ALL_GROUPED)
+            x1s.append(feats)
+            coef(nu - 1, f, outs)
+            feats = f
+        L = mod.linear
+        fr = _linear_route(outs, L.weight, L.lay, None)
+        ctx.routes, ctx.final, ctx.mod, ctx.has_sc = routes, fr, mod, sc is not None
+        ctx.save_for_backward(x, *x1s[1:])
+        return _linear_apply(outs, L.weight, L.bias, L.lay, *fr, 1.0, addend=sc)
+
+    @staticmethod
+    def backward(ctx, g):
+        mod = ctx.mod
+        x, *fs = ctx.saved_tensors   # fs: f_2 .. f_{correlation-1}
+        g = g.contiguous()
+        L = mod.linear
+        g_outs = _linear_apply(g, L.weight, None, L.lay, *ctx.final, 1.0, kind="bwd")
+
+        def coef_bwd(k):
+            C = mod.coefs[k]
+            return _linear_apply(g_outs, C.weight, None, C.lay, *ctx.routes[k], 1.0, kind="bwd")
+
+        g_x = coef_bwd(0)
+        if mod.correlation >= 2:
+            g_f = coef_bwd(mod.correlation - 1)
+            for nu in range(mod.correlation, 2, -1):
+                ace = mod.aces[nu - 2]
+                # the gradient of f_{nu-1} through this product (new), then
+                # through its coefficient linear (added in the GEMM epilogue)
+                g_prev, _, _ = ops.launch_uuu_bwd(fs[nu - 3], x, None, g_f, ops.find_variant(ace.key), ace.C,
+                                                  ops.LAYOUT_ALL_GROUPED, acc2=g_x)
+                C = mod.coefs[nu - 2]
+                _linear_apply(g_outs, C.weight, None, C.lay, *ctx.routes[nu - 2], 1.0, kind="bwd", out=g_prev,
+                              addend=g_prev)
+                g_f = g_prev
+            # f_2 = uuu(x, x): both of its gradients into g_x
+            ace = mod.aces[0]
+            ops.launch_uuu_bwd(x, x, None, g_f, ops.find_variant(ace.key), ace.C, ops.LAYOUT_ALL_GROUPED, acc1=g_x,
+                               acc2=g_x)
+        return g_x, (g if ctx.has_sc else None), None, None
+
+
 class CgtpACE(torch.nn.Module):
     """``CgtpACE`` (``tace/models/_e3nn/prod.py:20-266``): nu-chain of uuu products
     and per-species coefficient linears, evaluated on species-sorted nodes."""
@@ -930,6 +1046,8 @@ class CgtpACE(torch.nn.Module):
 
     def forward(self, x, sp: SpeciesPlan, sc):
         """x: group-major node features in species-sorted row order."""
+        if not (self.bilinear or ops.MODE.double or ops.MODE.export) and _frozen(self):
+            return _ProductBasisFn.apply(x.contiguous(), None if sc is None else sc.contiguous(), self, sp)
         ws = base = None
         if self.bilinear:
             x, base, ws = self._split_up(x)

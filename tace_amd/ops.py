@@ -714,19 +714,28 @@ def launch_uuu_fwd(x1, x2, w, var: TpVariant, C: int, layout: int = 0):
     return out
 
 
-def launch_uuu_bwd(x1, x2, w, gout, var: TpVariant, C: int, layout: int = 0):
-    """(grad_x1, grad_x2, grad_w or None) of ``launch_uuu_fwd``."""
+def launch_uuu_bwd(x1, x2, w, gout, var: TpVariant, C: int, layout: int = 0,
+                   acc1: Optional[torch.Tensor] = None, acc2: Optional[torch.Tensor] = None):
+    """(grad_x1, grad_x2, grad_w or None) of ``launch_uuu_fwd``.  ``acc1`` /
+    ``acc2``: tensors shaped like x1 / x2 that the gradient is added to in
+    place (and returned) instead of a new tensor; both may be one tensor when
+    x1 and x2 are (then it receives both gradients)."""
     _req(gout, "g_out", x1.dtype, (x1.shape[0], C * var.dout))
-    g1, g2 = torch.empty_like(x1), torch.empty_like(x2)
+    for a, x, nm in ((acc1, x1, "acc1"), (acc2, x2, "acc2")):
+        if a is not None:
+            _req(a, nm, x.dtype, tuple(x.shape))
+    g1 = acc1 if acc1 is not None else torch.empty_like(x1)
+    g2 = acc2 if acc2 is not None else torch.empty_like(x2)
+    accumulate = (1 if acc1 is not None else 0) | (2 if acc2 is not None else 0)
     gw = torch.empty_like(w) if w is not None else None
-    n_ws = N.lib().tace_uuu_workspace_elems(var.vid, x1.shape[0], C)
+    n_ws = N.lib().tace_uuu_workspace_elems(var.vid, x1.shape[0], C, accumulate)
     if n_ws < 0:
         N.check(int(n_ws), "tace_uuu_workspace_elems")
     ws = torch.empty(n_ws, dtype=x1.dtype, device=x1.device) if n_ws else None
     tok = _t0("uuu_bwd:" + var.key)
     N.check(N.lib().tace_uuu_bwd(var.vid, N.dtype_code(x1.dtype), x1.data_ptr(), x2.data_ptr(), N.ptr(w),
                                  gout.data_ptr(), x1.shape[0], C, layout, g1.data_ptr(), g2.data_ptr(), N.ptr(gw),
-                                 N.ptr(ws), int(n_ws), N.stream_ptr(x1.device)), "tace_uuu_bwd")
+                                 N.ptr(ws), int(n_ws), accumulate, N.stream_ptr(x1.device)), "tace_uuu_bwd")
     _t1(tok, (x1.shape[0], C))
     return g1, g2, gw
 
@@ -1885,10 +1894,27 @@ class SegLinearPlan:
         return out
 
 
+def _addend_ptr(addend: Optional[torch.Tensor], y: torch.Tensor):
+    """Device pointer of the term added to every output (None: no term):
+    y itself (y += ...) or a tensor of y's dtype and size apart from y."""
+    if addend is None:
+        return None
+    if addend.dtype != y.dtype or addend.numel() != y.numel() or not addend.is_contiguous() \
+            or addend.device != y.device:
+        raise ValueError("seg linear: the addend must be a contiguous tensor of the output's dtype, size and device")
+    if addend.data_ptr() != y.data_ptr():
+        a0, a1 = addend.data_ptr(), addend.data_ptr() + addend.numel() * addend.element_size()
+        y0, y1 = y.data_ptr(), y.data_ptr() + y.numel() * y.element_size()
+        if a0 < y1 and y0 < a1:
+            raise ValueError("seg linear: the addend overlaps the output without being it")
+    return addend.data_ptr()
+
+
 def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor], plan: SegLinearPlan,
-               alpha: float) -> torch.Tensor:
+               alpha: float, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Runs ``plan`` (``tace_seg_linear``) from x into y (every element of y
-    that a tile covers is overwritten); returns y."""
+    that a tile covers is overwritten, with ``addend`` added: y itself for
+    y += ..., or a separate tensor); returns y."""
     dt = x.dtype
     for t, nm, n in ((x, "x", plan.x_numel), (y, "y", plan.y_numel), (w, "weight", plan.w_numel)):
         _req(t, nm, dt)
@@ -1900,7 +1926,7 @@ def seg_linear(x: torch.Tensor, y: torch.Tensor, w: torch.Tensor, bias: Optional
             raise ValueError("seg linear: bias size differs from the plan's")
     tok = _t0("seg_linear")
     N.check(N.lib().tace_seg_linear(N.dtype_code(dt), plan.tile[0], plan.tile[1], x.data_ptr(), y.data_ptr(),
-                                    w.data_ptr(),
+                                    _addend_ptr(addend, y), w.data_ptr(),
                                     None if bias is None else bias.data_ptr(), plan.tiles.data_ptr(), plan.n_tiles,
                                     plan.contribs.data_ptr(), plan.scales.data_ptr(), float(alpha),
                                     N.stream_ptr(x.device)), "tace_seg_linear")
@@ -1940,13 +1966,13 @@ def bf16x3_split_blocks(w: torch.Tensor, blocks, scales, plane_stride: int, frag
 
 def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: Optional[torch.Tensor], plane_stride: int,
                         bias: Optional[torch.Tensor], plan: SegLinearPlan, alpha: float,
-                        frag: Optional[torch.Tensor] = None) -> torch.Tensor:
+                        frag: Optional[torch.Tensor] = None, addend: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Runs a ``split_weights`` plan: its tiles with the weight planes of
     ``bf16x3_split_blocks`` (``tace_seg_linear_presplit``; planes may be None
     when the plan's tiles read the fragment-order weights instead,
     ``tace_seg_linear_presplit_frag``), and its short-k tasks
     (``tace_seg_linear_presplit_ks``) with the fragment-order weights
-    ``frag``; returns y."""
+    ``frag``; ``addend`` as in ``seg_linear``; returns y."""
     if not plan.split_weights:
         raise ValueError("seg linear: the plan indexes flat weights, not pre-split planes")
     for t, nm, n in ((x, "x", plan.x_numel), (y, "y", plan.y_numel)):
@@ -1966,18 +1992,20 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: Optional[torch
     tok = _t0("seg_linear")
     st = N.stream_ptr(x.device)
     b_ptr = None if bias is None else bias.data_ptr()
+    a_ptr = _addend_ptr(addend, y)
     if plan.tile_frag:
-        N.check(N.lib().tace_seg_linear_presplit_frag(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
+        N.check(N.lib().tace_seg_linear_presplit_frag(x.data_ptr(), y.data_ptr(), a_ptr, frag.data_ptr(), b_ptr,
                                                       plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
                                                       int(plan.tile_aligned), float(alpha), st),
                 "tace_seg_linear_presplit_frag")
     else:
-        N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), planes.data_ptr(), plane_stride, b_ptr,
+        N.check(N.lib().tace_seg_linear_presplit(x.data_ptr(), y.data_ptr(), a_ptr, planes.data_ptr(), plane_stride,
+                                                 b_ptr,
                                                  plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
                                                  float(alpha), st), "tace_seg_linear_presplit")
     if plan.n_ks:
         for R, n_t, tasks in plan.ks_groups:
-            N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), frag.data_ptr(), b_ptr,
+            N.check(N.lib().tace_seg_linear_presplit_ks(x.data_ptr(), y.data_ptr(), a_ptr, frag.data_ptr(), b_ptr,
                                                         tasks.data_ptr(), n_t, R, float(alpha), st),
                     "tace_seg_linear_presplit_ks")
     _t1(tok, (plan.x_numel, plan.y_numel, plan.w_numel, plan.flops))

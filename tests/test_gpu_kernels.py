@@ -159,6 +159,50 @@ def test_uuu_matches_oracle(cuda, dtype, in1, in2, outl):
     close(g2, g2o, dtype, "g2")
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("case", ["one_part", "parts", "identical"])
+def test_uuu_backward_accumulate_adds_to_given_gradients(cuda, dtype, case):
+    """tace_uuu_bwd's accumulate bits add grad_x1 / grad_x2 to what g1 / g2
+    hold (the same bits as the overwriting call plus a separate add); with
+    both bits and one array for g1 and g2 (a product of a tensor with
+    itself) the array receives both gradients."""
+    C, Nn, L = 64, 37, 3
+    full = list(range(L + 1))
+    nu2 = om.UUUTP(_irreps(full, 1), _irreps(full, 1), [(1, (l, (-1) ** l)) for l in full], True)
+    nu2_ls = [ir[0] for _, ir in nu2.out]
+    in1, outl = {"one_part": (full, full), "parts": (nu2_ls, [0, 1, 2]), "identical": (full, full)}[case]
+    var = ops.find_variant(ops.variant_key("uuu", in1, full, outl))
+    lay = ops.LAYOUT_ALL_GROUPED
+    g = torch.Generator().manual_seed(11)
+    mk = lambda n: torch.randn(Nn, n, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    d1 = sum(C * (2 * l + 1) for l in in1)
+    d2 = sum(C * (2 * l + 1) for l in full)
+    x1, x2 = mk(d1), mk(d2)
+    if case == "identical":
+        x1 = x2
+    go = mk(C * var.dout)
+    g1, g2, _ = ops.launch_uuu_bwd(x1, x2, None, go, var, C, lay)
+    if case == "identical":
+        a = mk(d2)
+        want = (a + g1) + g2
+        got = a.clone()
+        r1, r2, _ = ops.launch_uuu_bwd(x1, x2, None, go, var, C, lay, acc1=got, acc2=got)
+        assert r1.data_ptr() == r2.data_ptr() == got.data_ptr()
+        assert torch.equal(got, want)
+        return
+    a1, a2 = mk(d1), mk(d2)
+    for acc in ((True, False), (False, True), (True, True)):
+        t1 = a1.clone() if acc[0] else None
+        t2 = a2.clone() if acc[1] else None
+        r1, r2, _ = ops.launch_uuu_bwd(x1, x2, None, go, var, C, lay, acc1=t1, acc2=t2)
+        assert torch.equal(r1, a1 + g1 if acc[0] else g1), acc
+        assert torch.equal(r2, a2 + g2 if acc[1] else g2), acc
+        if acc[0]:
+            assert r1.data_ptr() == t1.data_ptr()
+        if acc[1]:
+            assert r2.data_ptr() == t2.data_ptr()
+
+
 # ------------------------------------------------------------ neighbours ----
 def _nl_cases():
     rng = np.random.default_rng(11)
@@ -525,6 +569,52 @@ def test_seg_linear_matches_reference(cuda, dtype, tile, presplit, irr_in, irr_o
     (gw_want,) = torch.autograd.grad(ref, wr, go)
     (gw,) = torch.autograd.grad(lin(xg, sp, alpha), lin.weight, go.to(cuda))
     close(gw, gw_want, dtype, "seg linear grad w")
+
+
+@pytest.mark.parametrize("dtype,tile,presplit,tfrag", [(torch.float64, 64, False, False),
+                                                      (torch.float32, 128, True, True),
+                                                      (torch.float32, 128, True, False),
+                                                      (torch.float32, 128, False, False),
+                                                      (torch.float32, 64, False, False)])
+@pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
+def test_seg_linear_addend(cuda, dtype, tile, presplit, tfrag, irr_in, irr_out, counts, monkeypatch):
+    """Every segmented-linear kernel (FMA tiles, the MFMA tile kernels with
+    weights split in the launch, pre-split or in fragment order, and the
+    short-k tasks) adds the addend to each output, forward and input
+    gradient: into a separate output and in place (y += ...), equal to the
+    separate sum up to rounding (the MFMA kernels start their sums from the
+    addend instead of adding it at the end)."""
+    from tace_amd import model as pm
+    monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", tile)
+    monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", presplit)
+    monkeypatch.setattr(ops, "SEG_TILE_FRAG", tfrag)
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).to(dtype).to(cuda)
+    g = torch.Generator().manual_seed(21)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S).to(dtype)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(lin.weight.shape, generator=g, dtype=dtype))
+        lin.bias.copy_(torch.randn(lin.bias.shape, generator=g, dtype=dtype))
+    lin = lin.to(cuda)
+    sp = pm.SpeciesPlan(attrs)
+    for kind, din, dout in (("fwd", lin.lay.dim_in, lin.lay.dim_out), ("bwd", lin.lay.dim_out, lin.lay.dim_in)):
+        x = torch.randn(Z, din, generator=g, dtype=dtype).to(cuda)
+        add = torch.randn(Z, dout, generator=g, dtype=dtype).to(cuda)
+        rr, seg = pm._linear_route(x, lin.weight, lin.lay, sp.ranges)
+        bias = lin.bias if kind == "fwd" else None
+        y0 = pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind)
+        want = add + y0
+        y1 = pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind, addend=add)
+        y2 = add.clone()
+        pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind, out=y2, addend=y2)
+        for got, nm in ((y1, "separate"), (y2, "in place")):
+            close(got, want, dtype, f"{kind} {nm}")
+        if seg:   # the kernels take the addend as y itself or apart from y
+            buf = torch.zeros(Z * dout + 1, dtype=dtype, device=cuda)
+            with pytest.raises(ValueError, match="overlaps"):
+                pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind, out=buf[1:].view(Z, dout),
+                                 addend=buf[:-1].view(Z, dout))
 
 
 @pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)

@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 BARS = {torch.float64: (1e-10, 1e-8, 1e-8), torch.float32: (1e-5, 1e-4, 1e-4)}
 
 
-def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, avg=None, keep=None, **over):
+def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, avg=None, keep=None, frozen=True, **over):
     edges = [onl.neighbour_list(s["positions"], s["cell"], s["pbc"], configs.PRESETS[preset]["cutoff"])
              for s in structs]
     zs = sorted({int(z) for s in structs for z in s["numbers"]})
@@ -40,6 +40,9 @@ def _run_pair(structs, preset, cuda, dtype, seed=0, stress=False, avg=None, keep
     pm.load_reference_state_dict(gpu.readout_fn, {k: (v.to(dtype) if v.is_floating_point() else v)
                                                   for k, v in ref.state_dict().items()})
     gpu = gpu.to(cuda).eval()   # inference, as the calculators set it
+    if frozen:   # the calculators freeze the parameters too
+        for prm in gpu.parameters():
+            prm.requires_grad_(False)
     if not stress:
         gpu.reset_target_property(["energy", "forces"])
     dg = data.collate(structs, edges, cfg["atomic_numbers"], dtype=dtype, device=cuda)
@@ -70,9 +73,13 @@ def test_si64_energy_forces_stress(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-def test_fcc_alloy_slice(cuda, dtype):
-    """Config 2 architecture (C=128, L=3, 2 layers) on a 4x4x2 slice (128 atoms, 4 species)."""
-    got, want = _run_pair([structures.fcc_alloy(reps=(4, 4, 2), seed=2)], "fcc1024", cuda, dtype)
+@pytest.mark.parametrize("frozen", [True, False])
+def test_fcc_alloy_slice(cuda, dtype, frozen):
+    """Config 2 architecture (C=128, L=3, 2 layers) on a 4x4x2 slice (128 atoms, 4 species);
+    frozen parameters run the product basis and the interaction's input linears
+    as single autograd nodes with gradient sums in the kernel epilogues,
+    trainable ones as one node per operator."""
+    got, want = _run_pair([structures.fcc_alloy(reps=(4, 4, 2), seed=2)], "fcc1024", cuda, dtype, frozen=frozen)
     _check(got, want, dtype)
 
 
@@ -198,6 +205,8 @@ def test_energies_forces_stress_repeat_bit_for_bit(cuda, which):
     cfg = configs.model_cfg(preset, zs, 40.0, **over)
     torch.manual_seed(2)
     gpu = pm.create_model(cfg).to(cuda).eval()
+    for prm in gpu.parameters():
+        prm.requires_grad_(False)
     if which == "water":
         gpu.reset_target_property(["energy", "forces"])
     g = data.gpu_graph(structs, cfg["atomic_numbers"], rc, dtype=torch.float32, device=cuda)

@@ -253,6 +253,37 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
     close(gx2, gx2_o, dtype, "grad x (weighted only)")
 
 
+@pytest.mark.parametrize("bf16_out", [False, True])
+@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 64), (3, 48), (2, 256)])
+def test_rotate_in_fwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, lmax, C):
+    """The float32 rotate-in forward with two channels per lane (x, radial
+    weights and outputs aligned) gives the bits of the one-channel kernel,
+    which runs on the same values when x is not 8-byte aligned: each row
+    summed over its Wigner l block only adds none of the zero entries'
+    products that change a sum; bf16 outputs round the same way."""
+    g = torch.Generator().manual_seed(lmax * 77 + C)
+    N, E = 60, 999
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    ei = _random_graph(N, E, g)
+    x = torch.randn(N, K, C, generator=g)
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = W.float().to(cuda)
+    wr = torch.randn(E, nc * 2 * C, generator=g).to(cuda)
+    rs, rd = ei[0].to(cuda), ei[1].to(cuda)
+    rs[5], rd[7] = -1, N + 3   # rows outside the features read as zeros
+    xa = x.to(cuda)
+    buf = torch.empty(x.numel() + 1, device=cuda)
+    xu = buf[1:].view(N, K, C)   # 4 bytes past an aligned allocation
+    xu.copy_(xa)
+    assert xa.data_ptr() % 8 == 0 and xu.data_ptr() % 8 == 4
+    for r in (wr, None):
+        a = ops.launch_rotate_in_fwd(xa, W, rs, rd, r, lmax, bf16_out)
+        b = ops.launch_rotate_in_fwd(xu, W, rs, rd, r, lmax, bf16_out)
+        for ta, tb in zip(a, b):
+            for pa, pb in zip(ta, tb):
+                assert torch.equal(pa, pb)
+
+
 @pytest.mark.parametrize("dtype,lmax,C", [(torch.float32, 2, 128), (torch.float32, 1, 64), (torch.float32, 3, 256),
                                           (torch.float32, 2, 48), (torch.float64, 2, 64), (torch.float64, 1, 128)])
 def test_rotate_in_bwd_runs_equal_per_edge_rows(cuda, dtype, lmax, C):

@@ -42,7 +42,8 @@ def generate():
 
 def _compile(src: str, force: bool) -> str:
     obj = os.path.join(OBJ, os.path.splitext(os.path.basename(src))[0] + ".o")
-    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(CSRC, "bf16x3.h"), os.path.join(ROOT, "include", "tace_hip.h")]
+    deps = [src, os.path.join(CSRC, "common.h"), os.path.join(CSRC, "bf16x3.h"), os.path.join(CSRC, "tece_common.h"),
+            os.path.join(ROOT, "include", "tace_hip.h")]
     deps += glob.glob(os.path.join(GEN, "*.inc"))
     if not force and os.path.exists(obj) and os.path.getmtime(obj) >= max(os.path.getmtime(d) for d in deps):
         return obj
@@ -55,8 +56,10 @@ def _compile(src: str, force: bool) -> str:
 
 def build(verbose: bool = True, force: bool = True, jobs: int = 0) -> str:
     t0 = time.time()
-    srcs = [os.path.join(CSRC, n) for n in ("tace_hip.hip", "tece.hip", "mlp.hip", "linear.hip", "so2_gemm.hip")] \
-        + generate()
+    # the longest translation units first
+    srcs = [os.path.join(CSRC, n) for n in ("tece_rotin.hip", "tece_rotout.hip", "tece_ace.hip", "linear.hip",
+                                            "tace_hip.hip", "tece_score.hip", "tece_wigner.hip", "mlp.hip",
+                                            "so2_gemm.hip")] + generate()
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     jobs = jobs or min(16, os.cpu_count() or 4)

@@ -8,8 +8,10 @@ temperature, edge-ACE, graph softmax, radial phase, gate_m0).  The edge
 frames, the gather + rotation into the edge frame with the radial weighting,
 the rotary QK score, the graph softmax, the gate + complex edge-ACE product
 and the attention-weighted inverse rotation + receiver sum run on the HIP
-kernels of ``csrc/tece.hip``; the SO(2) linears are dense GEMMs (hipBLASLt
-through torch), those sharing an input stacked into one GEMM per m.  Node
+kernels of ``csrc/tece_*.hip``; the SO(2) linears are GEMMs on the bf16 MFMA
+kernels of ``csrc/so2_gemm.hip`` under bf16 channel mixing (torch GEMMs in
+float32 / float64 otherwise), those sharing an input stacked into one GEMM per
+m.  Node
 features come and go in the model's group-major, species-sorted layout.
 """
 

@@ -45,6 +45,25 @@ def _vectors(E, g):
     return torch.cat([d, special])
 
 
+def _wigner_block_mask(lmax):
+    """[K, K] bool: row r of the m layout (m = 0 rows l = 0..L, then per m the
+    +m rows and the -m rows, l = m..L) and column k of the l layout share an l."""
+    row_l = list(range(lmax + 1))
+    for m in range(1, lmax + 1):
+        row_l += list(range(m, lmax + 1)) * 2
+    col_l = [l for l in range(lmax + 1) for _ in range(2 * l + 1)]
+    return torch.tensor(row_l)[:, None] == torch.tensor(col_l)[None, :]
+
+
+def _check_block_grad(gW, gW_o, lmax, dtype):
+    """A rotate-in / rotate-out gradient of the Wigner matrix on its l blocks
+    (against the dense reference) and zeros off them (the kernels read the
+    blocks only)."""
+    mask = _wigner_block_mask(lmax).to(gW.device)
+    close(gW * mask, gW_o * mask.to(gW_o.device), dtype, "grad W (l blocks)")
+    assert torch.equal(gW * ~mask, torch.zeros_like(gW)), "grad W off the l blocks"
+
+
 def _random_graph(N, E, g):
     src = torch.randint(0, N, (E,), generator=g)
     dst = torch.randint(0, N - 2, (E,), generator=g)  # the last two nodes receive nothing
@@ -186,7 +205,39 @@ def test_rotate_out_matches_oracle(cuda, dtype, lmax, H, C):
     gm, ga, gW = torch.autograd.grad((out * gout).sum(), [a, b, w])
     close(gm, gm_o, dtype, "grad m")
     close(ga, ga_o, dtype, "grad alpha")
-    close(gW, gW_o, dtype, "grad W")
+    _check_block_grad(gW, gW_o, lmax, dtype)
+
+
+@pytest.mark.parametrize("bf16_out", [False, True])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (1, 2, 64), (2, 1, 256), (2, 8, 64), (1, 3, 96)])
+def test_rotate_out_bwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, lmax, H, C):
+    """The float32 rotate-out backward with two channels per lane against the
+    one-channel kernel (which runs when g_out is not 8-byte aligned): g_m the
+    same bits, g_alpha and g_wigner equal up to float rounding, g_wigner zero
+    off the l blocks."""
+    g = torch.Generator().manual_seed(lmax * 13 + H + C)
+    N, E = 80, 1501
+    K = (lmax + 1) ** 2
+    ei = _random_graph(N, E, g)
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
+    node_map = torch.randperm(N, generator=g).to(torch.int32).to(cuda)
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = W.float().to(cuda)
+    m = [t.float().to(cuda) for t in ops.so2_to_blocks(torch.randn(E, K, C, generator=g), lmax)]
+    al = torch.rand(E, H, generator=g).to(cuda)
+    go = torch.randn(N, K * C, generator=g).to(cuda)
+    buf = torch.empty(go.numel() + 1, device=cuda)
+    gou = buf[1:].view(N, K * C)
+    gou.copy_(go)
+    dst = ei[1].to(cuda)
+    a = ops.launch_rotate_out_bwd(m, al, W, go, dst, node_map, plan, lmax, H, bf16_out)
+    b = ops.launch_rotate_out_bwd(m, al, W, gou, dst, node_map, plan, lmax, H, bf16_out)
+    for pa, pb in zip(a[0], b[0]):
+        assert torch.equal(pa, pb), "g_m"
+    close(a[1], b[1], torch.float32, "g_alpha")
+    close(a[2], b[2], torch.float32, "g_wigner")
+    off = ~_wigner_block_mask(lmax).to(cuda)
+    assert not a[2][:, off].any() and not b[2][:, off].any()
 
 
 # ----------------------------------------------------------- rotate in ----
@@ -212,7 +263,7 @@ def test_rotate_in_matches_oracle(cuda, dtype, lmax, C):
     close(m, m_o, dtype, "m")
     gx, gW = torch.autograd.grad((m * gm.to(dtype).to(cuda)).sum(), [a, w])
     close(gx, gx_o, dtype, "grad x")
-    close(gW, gW_o, dtype, "grad W")
+    _check_block_grad(gW, gW_o, lmax, dtype)
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
@@ -242,7 +293,7 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
     loss = (ms * dv(gs)).sum() + (md * dv(gd)).sum() + (mw * dv(gw)).sum()
     gx, gW, gwr = torch.autograd.grad(loss, [a, w, r])
     close(gx, gx_o, dtype, "grad x")
-    close(gW, gW_o, dtype, "grad W")
+    _check_block_grad(gW, gW_o, lmax, dtype)
     close(gwr, gwr_o, dtype, "grad radial w")
     # only the weighted output used: the src/dst gradients are absent
     ms, md, mw = ops.edge_rotate_in(a, w, ei[0].to(cuda), ei[1].to(cuda), lmax, r)
@@ -282,6 +333,50 @@ def test_rotate_in_fwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, lm
         for ta, tb in zip(a, b):
             for pa, pb in zip(ta, tb):
                 assert torch.equal(pa, pb)
+
+
+@pytest.mark.parametrize("runs", [False, True])
+@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 64), (2, 48), (2, 256)])
+def test_rotate_in_bwd_channel_pairs_equal_one_channel_kernel(cuda, runs, lmax, C):
+    """The float32 rotate-in backward with two channels per lane against the
+    one-channel kernel (which runs when x is not 8-byte aligned): the same
+    bits for the per-edge grad_x rows and g_radial_w, g_wigner equal up to
+    float rounding (two channels summed per lane first) and zero off the l
+    blocks in both."""
+    g = torch.Generator().manual_seed(lmax * 31 + C + int(runs))
+    N, E = 70, 1203
+    K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2
+    ei = _random_graph(N, E, g)
+    ei = ei[:, torch.argsort(ei[1], stable=True)]
+    dv = lambda t: t.float().to(cuda)
+    x = dv(torch.randn(N, K, C, generator=g))
+    buf = torch.empty(x.numel() + 1, device=cuda)
+    xu = buf[1:].view(N, K, C)
+    xu.copy_(x)
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = dv(W)
+    wr = dv(torch.randn(E, nc * 2 * C, generator=g))
+
+    def blocks(width):
+        return [dv(torch.randn(E * (1 if m == 0 else 2), (lmax + 1 - m) * width, generator=g)) for m in range(lmax + 1)]
+    gms, gmd, gmw = blocks(C), blocks(C), blocks(2 * C)
+    rs, rd = ei[0].to(cuda), ei[1].to(cuda)
+    if runs and not ops.rotate_in_runs_ok(x):
+        pytest.skip("4 K C values exceed 64 KB of LDS")
+    a = ops.launch_rotate_in_bwd(x, W, rs, rd, wr, gms, gmd, gmw, True, runs=runs)
+    b = ops.launch_rotate_in_bwd(xu, W, rs, rd, wr, gms, gmd, gmw, True, runs=runs)
+    assert torch.equal(a[0], b[0]), "sender rows"
+    if runs:   # receiver rows at the runs' first positions only
+        first = torch.ones(E, dtype=torch.bool)
+        first[1:] = ei[1][1:] != ei[1][:-1]
+        first[::4] = True
+        assert torch.equal(a[1][first.to(cuda)], b[1][first.to(cuda)]), "receiver run rows"
+    else:
+        assert torch.equal(a[1], b[1]), "receiver rows"
+    assert torch.equal(a[3], b[3]), "g_radial_w"
+    close(a[2], b[2], torch.float32, "g_wigner")
+    off = ~_wigner_block_mask(lmax).to(cuda)
+    assert not a[2][:, off].any() and not b[2][:, off].any()
 
 
 @pytest.mark.parametrize("dtype,lmax,C", [(torch.float32, 2, 128), (torch.float32, 1, 64), (torch.float32, 3, 256),

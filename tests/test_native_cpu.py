@@ -42,6 +42,18 @@ def test_channel_limit_and_layout_checks():
     assert rc < 0 and b"layout" in lib.tace_last_error()
 
 
+@pytest.mark.parametrize("C,H,ok", [(48, 1, False), (96, 16, False), (128, 4, True), (192, 1, True), (160, 1, False)])
+def test_rotate_out_head_width_check(C, H, ok):
+    """The head sums of the rotate-out and score kernels add a head's lanes
+    with power-of-two shuffles: a per-head width must divide 64 or be a
+    multiple of 64, and other widths are refused before any device work (an
+    accepted call gets as far as its null-pointer check)."""
+    lib = _native.lib()
+    rc = lib.tace_tece_rotate_out_bwd(0, None, None, None, None, None, None, 10, 5, 2, C, H, None, None, None, None)
+    assert rc < 0
+    assert (b"null pointer" in lib.tace_last_error()) == ok, lib.tace_last_error()
+
+
 @pytest.mark.parametrize("in1,lmax", [([0], 2), ([0, 1, 2, 3], 3), ([0, 1, 2], 2)])
 def test_generated_contraction_order_matches_oracle(in1, lmax):
     """CPU restatement of the contractions the generated edge kernels perform

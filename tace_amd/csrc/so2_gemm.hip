@@ -127,7 +127,7 @@ __device__ __forceinline__ void g_strip(const unsigned short* __restrict__ As, c
       const gf4 v = h ? s1 : s0;
       float* dst = J.out + (int64_t)r * J.ldo + col;
       if (vst && col + 4 <= J.n) {
-        *(gf4*)dst = v;
+        __builtin_nontemporal_store(v, (gf4*)dst);   // streamed: keep L2 for B
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -250,6 +250,13 @@ __device__ __forceinline__ void kt_load_a(const KtJob& J, int k0, int t, gu4 (&r
   }
 }
 
+// AVEC with this thread's four row pointers made once (row clamped, k offset
+// of its 8-element run included): a stage's load is pointer + k0
+__device__ __forceinline__ void kt_load_a_p(const unsigned short* const (&ap)[4], int k0, gu4 (&r)[4]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r[q] = *(const gu4*)(ap[q] + k0);
+}
+
 __device__ __forceinline__ void kt_store_a(unsigned short* __restrict__ As, int t, const gu4 (&r)[4]) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -292,7 +299,7 @@ __global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned sh
   J.nks = (K + 31) >> 5;
   J.nb16 = (N + 15) >> 4;
   J.c0 = ct * KT_COLS;
-  const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int t = (int)threadIdx.x, lane = t & 63, wv = __builtin_amdgcn_readfirstlane(t >> 6);
   const int fr = lane & 15, fg = lane >> 4;
   const int cw = J.c0 + 64 * wv;          // the wavefront's first column
   const bool has_cols = cw < N;           // otherwise it only stages A
@@ -304,8 +311,18 @@ __global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned sh
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = gf4{0.f, 0.f, 0.f, 0.f};
 
+  const unsigned short* ap[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int u = t + KT_THREADS * q;
+    ap[q] = J.a + (int64_t)min(u >> 3, J.rows - 1) * J.lda + ((u & 7) << 3);
+  }
+  auto load_a = [&](int k0, gu4 (&r)[4]) {
+    if constexpr (AVEC) kt_load_a_p(ap, k0, r);
+    else kt_load_a<AVEC>(J, k0, t, r);
+  };
   gu4 ra[4];
-  kt_load_a<AVEC>(J, 0, t, ra);
+  load_a(0, ra);
   kt_store_a(As[0], t, ra);
   __syncthreads();
   if (has_cols) {
@@ -315,7 +332,7 @@ __global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned sh
       const unsigned short* __restrict__ Ab = As[st & 1];
       const int ks0 = 2 * st;
       // every load unconditional: past the last stage / step they repeat it
-      kt_load_a<AVEC>(J, min(st + 1, n_st - 1) * KT_KS, t, ra);
+      load_a(min(st + 1, n_st - 1) * KT_KS, ra);
       kt_load_b(J, cw, min(ks0 + 1, J.nks - 1), lane, b1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -344,7 +361,7 @@ __global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned sh
     }
   } else {
     for (int st = 0; st < n_st; ++st) {
-      kt_load_a<AVEC>(J, min(st + 1, n_st - 1) * KT_KS, t, ra);
+      load_a(min(st + 1, n_st - 1) * KT_KS, ra);
       kt_store_a(As[(st + 1) & 1], t, ra);
       __syncthreads();
     }
@@ -381,7 +398,7 @@ __global__ __launch_bounds__(KT_THREADS, 2) void k_so2_gemm_kt(const unsigned sh
         const gf4 v = h ? s1 : s0;
         float* dst = J.out + (int64_t)r * J.ldo + col;
         if (vst && col + 4 <= N) {
-          *(gf4*)dst = v;
+          __builtin_nontemporal_store(v, (gf4*)dst);   // streamed: keep L2 for A and B
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)

@@ -191,6 +191,23 @@ __device__ __forceinline__ void stv(T* p, const T (&o)[V]) {
     *p = o[0];
 }
 
+// one converted output element as a streamed (non-temporal) store
+template <typename TO, typename T>
+__device__ __forceinline__ void st_nt(TO* p, T v) {
+  __builtin_nontemporal_store(out_cvt<TO>(v), p);
+}
+
+// the same into global memory as streamed (non-temporal) stores: per-edge
+// outputs read once by a later kernel, so L2 stays with the gathered rows
+typedef float tece_f2_t __attribute__((ext_vector_type(2)));
+template <typename T, int V>
+__device__ __forceinline__ void stv_nt(T* p, const T (&o)[V]) {
+  if constexpr (V == 2)
+    __builtin_nontemporal_store(tece_f2_t{o[0], o[1]}, (tece_f2_t*)p);
+  else
+    __builtin_nontemporal_store(o[0], p);
+}
+
 // ---------------------------------------------------------- C ABI helpers --
 // block arrays: lmax+1 pointers (block 0, then m = 1..lmax); entries past
 // lmax are ignored

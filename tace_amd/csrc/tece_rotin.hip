@@ -67,9 +67,12 @@ __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, cons
 // the kernel above, whose sums (over each row's l block, in the same order)
 // it gives bit for bit.  Needs x and radial_w 8-byte aligned and the output
 // blocks aligned to two elements.
-__device__ __forceinline__ void st_pair(float* p, float a, float b) { *(float2*)p = make_float2(a, b); }
+// (streamed: the outputs go to the GEMMs, L2 is left to the gathered rows)
+__device__ __forceinline__ void st_pair(float* p, float a, float b) {
+  __builtin_nontemporal_store(tece_f2_t{a, b}, (tece_f2_t*)p);
+}
 __device__ __forceinline__ void st_pair(bf16_t* p, float a, float b) {
-  *(uint32_t*)p = (uint32_t)out_cvt<bf16_t>(a) | ((uint32_t)out_cvt<bf16_t>(b) << 16);
+  __builtin_nontemporal_store((uint32_t)out_cvt<bf16_t>(a) | ((uint32_t)out_cvt<bf16_t>(b) << 16), (uint32_t*)p);
 }
 
 template <typename TO, int L, int NP>
@@ -210,7 +213,7 @@ __device__ __forceinline__ void rotin_bwd_edge(const T* __restrict__ x, const T*
         }
         if (gwr) {
 #pragma unroll
-          for (int q = 0; q < NC; ++q) stv<T, V>(gwr + (e * NC + q) * C2 + c, gc[q]);
+          for (int q = 0; q < NC; ++q) stv_nt<T, V>(gwr + (e * NC + q) * C2 + c, gc[q]);
         }
       }
 #pragma unroll
@@ -230,7 +233,7 @@ __device__ __forceinline__ void rotin_bwd_edge(const T* __restrict__ x, const T*
         if (RUNS && !src)
           stv<T, V>(lrow + kk * C + cc, a);
         else
-          stv<T, V>((src ? gxs : gxd) + (e * K + kk) * C + cc, a);
+          stv_nt<T, V>((src ? gxs : gxd) + (e * K + kk) * C + cc, a);
       }
 #pragma unroll
       for (int r = 0; r < K; ++r)

@@ -92,8 +92,8 @@ __global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const B
 #pragma unroll
       for (int r = 0; r <= L; ++r) {
         const T qv = erow<L>(q, e, r, C)[c], kv = erow<L>(k, e, r, C)[c];
-        erow<L>(gq, e, r, C)[c] = out_cvt<TO>(G * kv);
-        erow<L>(gk, e, r, C)[c] = out_cvt<TO>(G * qv);
+        st_nt<TO>(&erow<L>(gq, e, r, C)[c], G * kv);
+        st_nt<TO>(&erow<L>(gk, e, r, C)[c], G * qv);
       }
 #pragma unroll
       for (int m = 1; m <= L; ++m) {
@@ -107,10 +107,10 @@ __global__ __launch_bounds__(256) void k_score_bwd(const Blk<const T> q, const B
           const T kr = erow<L>(k, e, ir, C)[c], ki = erow<L>(k, e, ii, C)[c];
           A += qr * kr + qi * ki;
           B += qi * kr - qr * ki;
-          erow<L>(gq, e, ir, C)[c] = out_cvt<TO>(G * (cs * kr - sn * ki));
-          erow<L>(gq, e, ii, C)[c] = out_cvt<TO>(G * (cs * ki + sn * kr));
-          erow<L>(gk, e, ir, C)[c] = out_cvt<TO>(G * (cs * qr + sn * qi));
-          erow<L>(gk, e, ii, C)[c] = out_cvt<TO>(G * (cs * qi - sn * qr));
+          st_nt<TO>(&erow<L>(gq, e, ir, C)[c], G * (cs * kr - sn * ki));
+          st_nt<TO>(&erow<L>(gq, e, ii, C)[c], G * (cs * ki + sn * kr));
+          st_nt<TO>(&erow<L>(gk, e, ir, C)[c], G * (cs * qr + sn * qi));
+          st_nt<TO>(&erow<L>(gk, e, ii, C)[c], G * (cs * qi - sn * qr));
         }
         d[0] += T(m) * (cs * B - sn * A);
       }

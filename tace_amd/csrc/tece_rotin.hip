@@ -61,28 +61,52 @@ __global__ __launch_bounds__(256) void k_rotin_fwd(const T* __restrict__ x, cons
   }
 }
 
-// The same forward for float32 features and an even channel count, two
-// adjacent channels per lane: 8-byte feature and radial-weight loads and
-// 4-byte (bf16) or 8-byte (float32) stores, half the memory instructions of
-// the kernel above, whose sums (over each row's l block, in the same order)
-// it gives bit for bit.  Needs x and radial_w 8-byte aligned and the output
-// blocks aligned to two elements.
-// (streamed: the outputs go to the GEMMs, L2 is left to the gathered rows)
-__device__ __forceinline__ void st_pair(float* p, float a, float b) {
-  __builtin_nontemporal_store(tece_f2_t{a, b}, (tece_f2_t*)p);
+// The same forward for float32 features with VC = 2 or 4 adjacent channels
+// per lane (the channel count a multiple of VC): 8- or 16-byte feature and
+// radial-weight loads and 4- or 8-byte (bf16) / 8- or 16-byte (float32)
+// stores, a half or a quarter of the memory instructions of the kernel above
+// (whose sums, over each row's l block in the same order, it gives bit for
+// bit).  Needs x and radial_w aligned to VC floats and the output blocks to
+// VC elements.  The stores are streamed (non-temporal): the outputs go to the
+// GEMMs, L2 is left to the gathered rows.
+template <int VC> struct RotinVec;
+template <> struct RotinVec<2> { typedef float f __attribute__((ext_vector_type(2))); typedef uint32_t h; };
+template <> struct RotinVec<4> {
+  typedef float f __attribute__((ext_vector_type(4)));
+  typedef uint32_t h __attribute__((ext_vector_type(2)));
+};
+
+template <int VC>
+__device__ __forceinline__ void st_vec(float* p, const float (&a)[VC]) {
+  typename RotinVec<VC>::f v;
+#pragma unroll
+  for (int i = 0; i < VC; ++i) v[i] = a[i];
+  __builtin_nontemporal_store(v, (typename RotinVec<VC>::f*)p);
 }
-__device__ __forceinline__ void st_pair(bf16_t* p, float a, float b) {
-  __builtin_nontemporal_store((uint32_t)out_cvt<bf16_t>(a) | ((uint32_t)out_cvt<bf16_t>(b) << 16), (uint32_t*)p);
+template <int VC>
+__device__ __forceinline__ void st_vec(bf16_t* p, const float (&a)[VC]) {
+  uint32_t w[VC / 2];
+#pragma unroll
+  for (int i = 0; i < VC / 2; ++i)
+    w[i] = (uint32_t)out_cvt<bf16_t>(a[2 * i]) | ((uint32_t)out_cvt<bf16_t>(a[2 * i + 1]) << 16);
+  if constexpr (VC == 2) {
+    __builtin_nontemporal_store(w[0], (uint32_t*)p);
+  } else {
+    typename RotinVec<VC>::h v;
+    v[0] = w[0];
+    v[1] = w[1];
+    __builtin_nontemporal_store(v, (typename RotinVec<VC>::h*)p);
+  }
 }
 
-template <typename TO, int L, int NP>
-__global__ __launch_bounds__(256) void k_rotin_fwd_pairs(const float* __restrict__ x, const float* __restrict__ W,
-                                                         const int64_t* __restrict__ rows_src,
-                                                         const int64_t* __restrict__ rows_dst,
-                                                         const float* __restrict__ wr, int64_t n_rows, int64_t E,
-                                                         int C, const Blk<TO> ms, const Blk<TO> md,
-                                                         const Blk<TO> mw) {
+template <typename TO, int L, int NP, int VC>
+__global__ __launch_bounds__(256) void k_rotin_fwd_vec(const float* __restrict__ x, const float* __restrict__ W,
+                                                       const int64_t* __restrict__ rows_src,
+                                                       const int64_t* __restrict__ rows_dst,
+                                                       const float* __restrict__ wr, int64_t n_rows, int64_t E, int C,
+                                                       const Blk<TO> ms, const Blk<TO> md, const Blk<TO> mw) {
   constexpr int K = (L + 1) * (L + 1), NC = (L + 1) * (L + 2) / 2;
+  typedef typename RotinVec<VC>::f fv;
   const int64_t e = wave_edge();
   if (e >= E) return;
   const int lane = (int)threadIdx.x & 63;
@@ -91,30 +115,41 @@ __global__ __launch_bounds__(256) void k_rotin_fwd_pairs(const float* __restrict
   const int C2 = 2 * C;
 #pragma unroll
   for (int j = 0; j < NP; ++j) {
-    const int c = 2 * (lane + 64 * j);
+    const int c = VC * (lane + 64 * j);
     if (c < C2) {
       const bool src = c < C;
       const int64_t row = src ? rs : rd;
       const int cc = src ? c : c - C;
       const bool ok = row >= 0 && row < n_rows;
-      float2 xk[K];
+      fv xk[K];
 #pragma unroll
-      for (int kk = 0; kk < K; ++kk)
-        xk[kk] = ok ? *(const float2*)(x + (row * K + kk) * C + cc) : make_float2(0.f, 0.f);
+      for (int kk = 0; kk < K; ++kk) {
+        if (ok) {
+          xk[kk] = *(const fv*)(x + (row * K + kk) * C + cc);
+        } else {
+#pragma unroll
+          for (int i = 0; i < VC; ++i) xk[kk][i] = 0.f;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < K; ++r) {
-        float a0 = 0.f, a1 = 0.f;
+        float a[VC];
+#pragma unroll
+        for (int i = 0; i < VC; ++i) a[i] = 0.f;
 #pragma unroll
         for (int d = 0; d < 2 * L + 1; ++d) {   // the columns of row r's block
           const int l = m_l<L>(r);
           if (d > 2 * l) continue;   // constant after unrolling
-          a0 += w[r * K + l * l + d] * xk[l * l + d].x;
-          a1 += w[r * K + l * l + d] * xk[l * l + d].y;
+#pragma unroll
+          for (int i = 0; i < VC; ++i) a[i] += w[r * K + l * l + d] * xk[l * l + d][i];
         }
-        st_pair(erow<L>(src ? ms : md, e, r, C) + cc, a0, a1);
+        st_vec<VC>(erow<L>(src ? ms : md, e, r, C) + cc, a);
         if (wr) {
-          const float2 wv = *(const float2*)(wr + (e * NC + m_comp<L>(r)) * C2 + c);
-          st_pair(erow<L>(mw, e, r, C2) + c, wv.x * a0, wv.y * a1);
+          const fv wv = *(const fv*)(wr + (e * NC + m_comp<L>(r)) * C2 + c);
+          float b[VC];
+#pragma unroll
+          for (int i = 0; i < VC; ++i) b[i] = wv[i] * a[i];
+          st_vec<VC>(erow<L>(mw, e, r, C2) + c, b);
         }
       }
     }
@@ -334,27 +369,35 @@ int tace_edge_rotate_in_fwd(int dtype, const void* x, const void* wigner, const 
     return tace_fail_msg("tace_edge_rotate_in_fwd: null pointer");
   hipStream_t s = (hipStream_t)stream;
   const dim3 g = wave_grid(n_edges), b(256);
-  // float32 features, even channel count, 8-byte aligned x / radial_w and
-  // outputs aligned to two elements: two channels per lane
-  const size_t oal = dtype == TACE_F32_BF16 ? 4 : 8;
-  bool pairs = (dtype == TACE_F32 || dtype == TACE_F32_BF16) && (channels & 1) == 0 && channels <= 512 &&
-               ((uintptr_t)x & 7) == 0 && ((uintptr_t)radial_w & 7) == 0;
-  for (int m = 0; pairs && m <= lmax; ++m)
-    pairs = ((uintptr_t)m_src[m] % oal) == 0 && ((uintptr_t)m_dst[m] % oal) == 0 &&
-            (!radial_w || ((uintptr_t)m_w[m] % oal) == 0);
-  if (pairs) {
-#define RI_P(TO, LL)                                                                                          \
-  TACE_SLOTS_DISPATCH(channels, NP,                                                                           \
-    hipLaunchKernelGGL((k_rotin_fwd_pairs<TO, LL, NP>), g, b, 0, s, (const float*)x, (const float*)wigner,     \
+  // float32 features: VC = 4 (or 2) channels per lane when the channel count
+  // is a multiple of VC, x and radial_w are aligned to VC floats and the
+  // outputs to VC elements
+  auto aligned = [&](int vc) {
+    if (!(dtype == TACE_F32 || dtype == TACE_F32_BF16) || channels % vc || channels > 512) return false;
+    const size_t xal = 4 * (size_t)vc, oal = (dtype == TACE_F32_BF16 ? 2 : 4) * (size_t)vc;
+    if (((uintptr_t)x % xal) || ((uintptr_t)radial_w % xal)) return false;
+    for (int m = 0; m <= lmax; ++m)
+      if (((uintptr_t)m_src[m] % oal) || ((uintptr_t)m_dst[m] % oal) || (radial_w && ((uintptr_t)m_w[m] % oal)))
+        return false;
+    return true;
+  };
+  const int vc = aligned(4) ? 4 : aligned(2) ? 2 : 1;
+  if (vc > 1) {
+#define RI_V(TO, LL, VCC)                                                                                     \
+  TACE_SLOTS_DISPATCH(2 * channels / (VCC), NP,                                                              \
+    hipLaunchKernelGGL((k_rotin_fwd_vec<TO, LL, NP, VCC>), g, b, 0, s, (const float*)x, (const float*)wigner,  \
                        rows_src, rows_dst, (const float*)radial_w, n_rows, n_edges, channels,                  \
                        blocks_of<TO>(m_src, lmax), blocks_of<TO>(m_dst, lmax),                                 \
                        blocks_of<TO>(radial_w ? m_w : nullptr, lmax)))
+#define RI_VL(TO, VCC)                                                                                        \
+  if (lmax == 1) { RI_V(TO, 1, VCC) } else if (lmax == 2) { RI_V(TO, 2, VCC) } else { RI_V(TO, 3, VCC) }
     if (dtype == TACE_F32) {
-      if (lmax == 1) { RI_P(float, 1) } else if (lmax == 2) { RI_P(float, 2) } else { RI_P(float, 3) }
+      if (vc == 4) { RI_VL(float, 4) } else { RI_VL(float, 2) }
     } else {
-      if (lmax == 1) { RI_P(bf16_t, 1) } else if (lmax == 2) { RI_P(bf16_t, 2) } else { RI_P(bf16_t, 3) }
+      if (vc == 4) { RI_VL(bf16_t, 4) } else { RI_VL(bf16_t, 2) }
     }
-#undef RI_P
+#undef RI_VL
+#undef RI_V
     return tace_check_launch("tace_edge_rotate_in_fwd");
   }
 #define RI_F(TT, TO, LL)                                                                                    \

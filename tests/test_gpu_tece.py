@@ -305,13 +305,13 @@ def test_rotate_in_weighted_matches_oracle(cuda, dtype, lmax, C):
 
 
 @pytest.mark.parametrize("bf16_out", [False, True])
-@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 64), (3, 48), (2, 256)])
+@pytest.mark.parametrize("lmax,C", [(2, 128), (1, 64), (3, 48), (2, 256), (2, 50)])
 def test_rotate_in_fwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, lmax, C):
-    """The float32 rotate-in forward with two channels per lane (x, radial
-    weights and outputs aligned) gives the bits of the one-channel kernel,
-    which runs on the same values when x is not 8-byte aligned: each row
-    summed over its Wigner l block only adds none of the zero entries'
-    products that change a sum; bf16 outputs round the same way."""
+    """The float32 rotate-in forward with four channels per lane (two when
+    the channel count is not a multiple of 4; x, radial weights and outputs
+    aligned) gives the bits of the one-channel kernel, which runs on the same
+    values when x is not 8-byte aligned: each row summed over its Wigner l
+    block in the same order; bf16 outputs round the same way."""
     g = torch.Generator().manual_seed(lmax * 77 + C)
     N, E = 60, 999
     K, nc = (lmax + 1) ** 2, (lmax + 1) * (lmax + 2) // 2

@@ -240,6 +240,36 @@ def test_rotate_out_bwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, l
     assert not a[2][:, off].any() and not b[2][:, off].any()
 
 
+@pytest.mark.parametrize("bf16_out", [False, True])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (1, 2, 64), (2, 1, 256), (3, 4, 64), (2, 32, 64)])
+def test_score_channel_vectors_equal_one_channel_kernel(cuda, bf16_out, lmax, H, C):
+    """The float32 score kernels with four (or two) channels per lane against
+    the one-channel kernels (which run when a query block is not 8-byte
+    aligned): equal up to float rounding (a lane's channels summed first;
+    the compiler may contract a channel's products differently)."""
+    g = torch.Generator().manual_seed(lmax * 5 + H + C)
+    E = 1001
+    q = [t.to(cuda) for t in ops.so2_to_blocks(torch.randn(E, (lmax + 1) ** 2, C, generator=g), lmax)]
+    k = [t.to(cuda) for t in ops.so2_to_blocks(torch.randn(E, (lmax + 1) ** 2, C, generator=g), lmax)]
+    rp = torch.randn(E, 2 * H, generator=g).to(cuda)
+    ts = torch.rand(H, generator=g).to(cuda) + 0.5
+    gs = torch.randn(E, H, generator=g).to(cuda)
+    buf = torch.empty(q[0].numel() + 1, device=cuda)
+    q0u = buf[1:].view(q[0].shape)
+    q0u.copy_(q[0])
+    qu = [q0u] + q[1:]
+    s_a = ops.launch_score_fwd(q, k, rp, ts, lmax, H)
+    s_b = ops.launch_score_fwd(qu, k, rp, ts, lmax, H)
+    close(s_a, s_b, torch.float32, "score")
+    a = ops.launch_score_bwd(q, k, rp, ts, gs, lmax, H, bf16_out)
+    b = ops.launch_score_bwd(qu, k, rp, ts, gs, lmax, H, bf16_out)
+    tol = 1e-2 if bf16_out else None   # bf16 outputs: one rounding step apart at most
+    for i in (0, 1):
+        for pa, pb in zip(a[i], b[i]):
+            close(pa.float(), pb.float(), torch.float32, "g_q" if i == 0 else "g_k", tol=tol)
+    close(a[2], b[2], torch.float32, "g_radial_proj")
+
+
 # ----------------------------------------------------------- rotate in ----
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
 @pytest.mark.parametrize("lmax,C", [(2, 128), (1, 32), (2, 48), (3, 64), (2, 512)])

@@ -336,6 +336,8 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a device copy of 1 GiB five times (reference for the HBM byte counters)")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        ap.error("--steps must be at least 1 and --warmup at least 0")
     if args.calibrate_copy:
         a = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0").fill_(1.0)
         b = torch.empty_like(a)
@@ -390,10 +392,12 @@ def main():
             return model(data.gpu_graph(structs, cfg["atomic_numbers"], rc, dtype=torch.float32, device=dev))
 
     log(f"[bench] {args.workload}: {nat} atoms, {E0} edges (avg {avg:.1f}), warm-up {args.warmup}")
+    out = None
     for _ in range(args.warmup):
         out = step()
     torch.cuda.synchronize()
-    log(f"[bench] warm-up done, E = {out['energy'].sum().item():.6f}; timing {args.steps} steps")
+    e_w = "n/a" if out is None else f"{out['energy'].sum().item():.6f}"
+    log(f"[bench] warm-up done, E = {e_w}; timing {args.steps} steps")
 
     # timed region: K steps; a HIP event pair per step (current stream) gives
     # the median, the wall clock around all K the throughput

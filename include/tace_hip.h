@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 29
+#define TACE_HIP_ABI_VERSION 30
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -347,6 +347,21 @@ int tace_seg_linear_presplit_frag(const float* x, float* y, const float* addend,
 int tace_seg_linear_presplit_ks(const float* x, float* y, const float* addend, const uint16_t* w_frag,
                                 const float* bias,
                                 const int64_t* tasks, int64_t n_tasks, int32_t task_rows, double alpha, void* stream);
+/* tace_seg_linear_presplit_frag with k split over `splits` (2..64)
+ * workgroups per tile, for launches with too few tiles to fill the GPU (the
+ * small systems' per-species linears, linear.py:377-482): every tile has at
+ * most one contribution (a tile with more gets NaN in every output); work
+ * item tile * splits + s sums 32-k steps [s nks / splits, (s + 1) nks /
+ * splits) of it into partials[(tile splits + s) 16384 ..] (a 128 x 128 tile,
+ * row stride 128; partial_elems >= n_tiles splits 16384 floats, 16-byte
+ * aligned, no other use during the call), and a second kernel writes y[tile]
+ * = alpha (addend / alpha + partial_0 + ... + partial_{splits-1} + bias),
+ * the partials in split order: every run gives the same bits, which differ
+ * from the unsplit kernel's by float32 summation order. */
+int tace_seg_linear_presplit_frag_split(const float* x, float* y, const float* addend, const uint16_t* w_frag,
+                                        const float* bias, const int64_t* tiles, int64_t n_tiles,
+                                        const int64_t* contribs, int32_t aligned, int32_t splits, float* partials,
+                                        int64_t partial_elems, double alpha, void* stream);
 
 /* ---- TECE radial-rotary edge attention (config 5)
  * K = (lmax+1)^2 edge-frame components with mmax = lmax; the "m layout"

@@ -90,6 +90,8 @@ _SIGS = {
     "tace_so2_gemm_bf16_kt": (_c_int, [_vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp]),
     "tace_seg_linear_presplit_ks": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_dbl, _vp]),
     "tace_seg_linear_presplit_frag": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_dbl, _vp]),
+    "tace_seg_linear_presplit_frag_split": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i32, _c_i32, _vp,
+                                                     _c_i64, _c_dbl, _vp]),
     "tace_nl_workspace_bytes": (_c_i64, [_c_i64, _vp, _vp, _c_dbl]),
     "tace_nl_count": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _c_i64, _vp, _vp]),
     "tace_nl_fill": (_c_int, [_vp, _c_i64, _vp, _vp, _c_dbl, _vp, _vp, _vp, _vp, _vp]),

@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void k_seg_linear_bx3s(const float* __restrict
 struct FtLoad {   // the contribution and step whose operands load next
   const float* xa;
   const unsigned short* wf;
-  int c, s, k, nks;
+  int c, s, k, nks, send;   // steps s .. send - 1 of the contribution's nks
   bool xvec;
 };
 
@@ -511,6 +511,7 @@ __device__ __forceinline__ void ft_open(FtLoad& L, const float* __restrict__ x, 
   L.xa = x + cd[0];
   L.k = (int)cd[1];
   L.nks = (L.k + 31) >> 5;
+  L.send = L.nks;
   L.wf = wfrag + cd[2];
   L.xvec = ((((uintptr_t)L.xa) & 15) == 0) && ((L.k & 3) == 0);
 }
@@ -549,23 +550,34 @@ __device__ __forceinline__ void ft_load_b(const FtLoad& L, int jb0, int nb16, in
   }
 }
 
-template <bool VEC>
+//
+// SPLIT (split k, for launches with too few tiles to fill the chip): work
+// item vi = tile * splits + sp sums steps [sp nks / splits, (sp + 1) nks /
+// splits) of the tile's first contribution into its own 128 x 128 partial
+// tile, partials + 16384 vi (row stride 128), with no addend, bias or alpha;
+// k_seg_split_sum adds the partials up (NaN for a tile with more than one
+// contribution).
+template <bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_seg_linear_bx3f(
     const float* __restrict__ x, float* y, const float* addend,
                                                          const unsigned short* __restrict__ wfrag,
                                                          const float* __restrict__ bias,
                                                          const int64_t* __restrict__ tiles,
                                                          const int64_t* __restrict__ contribs, float alpha,
-                                                         int n_tiles, int per) {
+                                                         int n_tiles, int per, int splits,
+                                                         float* __restrict__ partials) {
   constexpr int WM = 4, TR = 128, PL = 128 * SB_STR;   // plane size (bf16)
   __shared__ __attribute__((aligned(16))) unsigned short As[2][3 * PL];
-  const int tile = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  const int vi = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+  const int tile = SPLIT ? vi / splits : vi;
   if (tile >= n_tiles) return;
   const int64_t* td = tiles + 8 * (int64_t)tile;
   const int64_t out_base = td[0];
   const int rows = (int)td[1], n = (int)td[2], c0 = (int)td[3];
-  const int64_t bias_off = td[4];
-  const int cb = (int)td[5], ce = (int)td[6];
+  const int64_t bias_off = SPLIT ? -1 : td[4];
+  const int cb = (int)td[5];
+  int ce = (int)td[6];
+  if constexpr (SPLIT) ce = min(ce, cb + 1);   // k_seg_split_sum writes NaN for a tile with more
   const int t = (int)threadIdx.x, lane = t & 63, wv = t >> 6;
   const int wr = (wv >> 1) * 16 * WM, wc = (wv & 1) * 64;
   const int fr = lane & 15, fg = lane >> 4;
@@ -573,7 +585,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int soff = (t >> 1) * SB_STR + 16 * (t & 1);   // this thread's k16 run of a k-contiguous plane
 
   f4 acc[WM][4];
-  if (addend) {
+  if (!SPLIT && addend) {
     const bool avec = ((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)addend) & 15) == 0);
     const float ia = 1.f / alpha;
 #pragma unroll
@@ -595,7 +607,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   FtLoad L;
   while (c < ce) {
     ft_open(L, x, wfrag, contribs, c);
-    if (L.nks > 0) break;
+    if constexpr (SPLIT) {
+      const int sp = vi - tile * splits;
+      L.s = (int)((int64_t)sp * L.nks / splits);
+      L.send = (int)((int64_t)(sp + 1) * L.nks / splits);
+    }
+    if (L.send > L.s) break;
     ++c;
   }
   if (c < ce) {
@@ -607,14 +624,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // C to the step after the one it names; after the last step C stays
     // there (more = false), so the loads below never need a condition
     auto advance = [&](FtLoad& C, bool& more) {
-      if (C.s + 1 < C.nks) {
+      if (C.s + 1 < C.send) {
         ++C.s;
+        return;
+      }
+      if constexpr (SPLIT) {   // one contribution
+        more = false;
         return;
       }
       for (int cc = C.c + 1; cc < ce; ++cc) {
         FtLoad D;
         ft_open(D, x, wfrag, contribs, cc);
-        if (D.nks > 0) {
+        if (D.send > 0) {
           C = D;
           return;
         }
@@ -686,7 +707,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // acc[i][j][q] = out[row wr + 16 i + fr][column c0 + wc + 16 j + 4 fg + q];
   // per pair of blocks (2 jp, 2 jp + 1) lanes fr and fr ^ 8 trade one block,
   // so a store writes 8 whole rows of 32 columns
-  const bool vst = ((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
+  const bool vst = SPLIT || (((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0));
+  const float osc = SPLIT ? 1.f : alpha;
   const bool lo = fr < 8;
   const int jl = lo ? 0 : 1;
 #pragma unroll
@@ -694,7 +716,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int col = c0 + wc + 32 * jp + 16 * jl + 4 * fg;
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
-      const f4 v0 = alpha * (acc[i][2 * jp] + bv[2 * jp]), v1 = alpha * (acc[i][2 * jp + 1] + bv[2 * jp + 1]);
+      const f4 v0 = osc * (acc[i][2 * jp] + bv[2 * jp]), v1 = osc * (acc[i][2 * jp + 1] + bv[2 * jp + 1]);
       const f4 give = lo ? v1 : v0;
       f4 got;
 #pragma unroll
@@ -705,7 +727,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int r = wr + 16 * i + 8 * h + (fr & 7);
         if (r >= rows || col >= n) continue;
         const f4 v = h ? s1 : s0;
-        float* dst = y + out_base + (int64_t)r * n + col;
+        float* dst = SPLIT ? partials + 16384 * (int64_t)vi + 128 * r + (col - c0) : y + out_base + (int64_t)r * n + col;
         if (vst) {
           *(f4*)dst = v;
         } else {
@@ -715,6 +737,46 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+  }
+}
+
+// The partial tiles of k_seg_linear_bx3f<*, true> added up, 16 workgroups
+// per tile (8 rows each, a thread per 4 columns of a row): y = alpha
+// (addend / alpha + partial_0 + ... + partial_{splits-1} + bias), the partials
+// in split order (a fixed order, so every run gives the same bits); NaN in
+// every output of a tile with more than one contribution (the split kernel
+// sums only its first).  The addend may be y itself: each element is read
+// and then written by the same thread.
+__global__ __launch_bounds__(256) void k_seg_split_sum(float* y, const float* addend, const float* __restrict__ bias,
+                                                       const int64_t* __restrict__ tiles,
+                                                       const float* __restrict__ partials, int splits, float alpha) {
+  const int tile = (int)(blockIdx.x >> 4);
+  const int64_t* td = tiles + 8 * (int64_t)tile;
+  const int64_t out_base = td[0], bias_off = td[4];
+  const int rows = (int)td[1], n = (int)td[2], c0 = (int)td[3];
+  const int r = 8 * (int)(blockIdx.x & 15) + ((int)threadIdx.x >> 5), cc = 4 * ((int)threadIdx.x & 31), col = c0 + cc;
+  if (r >= rows || col >= n) return;
+  const bool bad = td[6] - td[5] > 1;
+  const bool vec = ((n & 3) == 0) && ((out_base & 3) == 0) && ((((uintptr_t)y) & 15) == 0);
+  const bool avec = vec && ((((uintptr_t)addend) & 15) == 0);
+  const int64_t o = out_base + (int64_t)r * n + col;
+  f4 acc = addend ? addend_init(addend, o, true, col, n, avec, 1.f / alpha) : f4{0.f, 0.f, 0.f, 0.f};
+  const float* __restrict__ P = partials + (int64_t)tile * splits * 16384 + 128 * r + cc;
+#pragma unroll 4
+  for (int s = 0; s < splits; ++s) acc += *(const f4*)(P + (int64_t)s * 16384);
+  f4 b = f4{0.f, 0.f, 0.f, 0.f};
+  if (bias_off >= 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (col + q < n) b[q] = bias[bias_off + col + q];
+  }
+  const f4 out = bad ? f4{NAN, NAN, NAN, NAN} : alpha * (acc + b);
+  if (vec && col + 4 <= n) {
+    *(f4*)(y + o) = out;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (col + q < n) y[o + q] = out[q];
   }
 }
 
@@ -1070,14 +1132,48 @@ extern "C" int tace_seg_linear_presplit_frag(const float* x, float* y, const flo
   const int per = (int)((n_tiles + 7) / 8);
   const dim3 g((unsigned)(8 * per)), b(256);
   if (aligned && (((uintptr_t)x) & 15) == 0)
-    hipLaunchKernelGGL(k_seg_linear_bx3f<true>, g, b, 0, (hipStream_t)stream, x, y, addend,
+    hipLaunchKernelGGL((k_seg_linear_bx3f<true, false>), g, b, 0, (hipStream_t)stream, x, y, addend,
                        (const unsigned short*)w_frag,
-                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
+                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per, 1, nullptr);
   else
-    hipLaunchKernelGGL(k_seg_linear_bx3f<false>, g, b, 0, (hipStream_t)stream, x, y, addend,
+    hipLaunchKernelGGL((k_seg_linear_bx3f<false, false>), g, b, 0, (hipStream_t)stream, x, y, addend,
                        (const unsigned short*)w_frag,
-                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per);
+                       bias, tiles, contribs, (float)alpha, (int)n_tiles, per, 1, nullptr);
   return tace_check_launch("tace_seg_linear_presplit_frag");
+}
+
+extern "C" int tace_seg_linear_presplit_frag_split(const float* x, float* y, const float* addend,
+                                                   const uint16_t* w_frag, const float* bias, const int64_t* tiles,
+                                                   int64_t n_tiles, const int64_t* contribs, int32_t aligned,
+                                                   int32_t splits, float* partials, int64_t partial_elems,
+                                                   double alpha, void* stream) {
+  if (n_tiles < 0 || n_tiles > 0x7ffffff0) return tace_fail_msg("tace_seg_linear_presplit_frag_split: bad tile count");
+  if (splits < 2 || splits > 64) return tace_fail_msg("tace_seg_linear_presplit_frag_split: 2..64 splits");
+  if (n_tiles * splits > 0x7ffffff0 || n_tiles > 0x7ffffff)
+    return tace_fail_msg("tace_seg_linear_presplit_frag_split: too many work items");
+  if (n_tiles == 0) return 0;
+  if (!x || !y || !w_frag || !tiles || !contribs || !partials)
+    return tace_fail_msg("tace_seg_linear_presplit_frag_split: null pointer");
+  if (addend && alpha == 0.0) return tace_fail_msg("tace_seg_linear_presplit_frag_split: an addend needs alpha != 0");
+  if ((((uintptr_t)w_frag) & 15) != 0 || (((uintptr_t)partials) & 15) != 0)
+    return tace_fail_msg("tace_seg_linear_presplit_frag_split: weights and partials must be 16-byte aligned");
+  if (partial_elems < n_tiles * splits * 16384)
+    return tace_fail_msg("tace_seg_linear_presplit_frag_split: partials hold fewer than n_tiles * splits * 16384 floats");
+  const int64_t items = n_tiles * splits;
+  const int per = (int)((items + 7) / 8);
+  const dim3 g((unsigned)(8 * per)), b(256);
+  if (aligned && (((uintptr_t)x) & 15) == 0)
+    hipLaunchKernelGGL((k_seg_linear_bx3f<true, true>), g, b, 0, (hipStream_t)stream, x, y, addend,
+                       (const unsigned short*)w_frag, bias, tiles, contribs, (float)alpha, (int)n_tiles, per,
+                       (int)splits, partials);
+  else
+    hipLaunchKernelGGL((k_seg_linear_bx3f<false, true>), g, b, 0, (hipStream_t)stream, x, y, addend,
+                       (const unsigned short*)w_frag, bias, tiles, contribs, (float)alpha, (int)n_tiles, per,
+                       (int)splits, partials);
+  if (int rc = tace_check_launch("tace_seg_linear_presplit_frag_split")) return rc;
+  hipLaunchKernelGGL(k_seg_split_sum, dim3((unsigned)(16 * n_tiles)), dim3(256), 0, (hipStream_t)stream, y, addend, bias,
+                     tiles, (const float*)partials, (int)splits, (float)alpha);
+  return tace_check_launch("tace_seg_linear_presplit_frag_split");
 }
 
 extern "C" int32_t tace_seg_linear_ks_rows(int32_t k) { return k < 0 ? 0 : k <= 128 ? 128 : k <= 256 ? 64 : 0; }

@@ -629,8 +629,12 @@ int tace_radial_mlp_out_f32(const float* h, const float* weight, int64_t n_edges
   if (n_edges == 0) return 0;
   if (!h || !weight || !out) return tace_fail_msg("tace_radial_mlp_out_f32: null pointer");
   if (((uintptr_t)h & 15) != 0) return tace_fail_msg("tace_radial_mlp_out_f32: h must be 16-byte aligned");
-  const int edges_per_chunk = 1024;
+  // 1,024 edges per chunk, fewer (down to 128) when that leaves fewer than
+  // 2,048 workgroups: small systems still fill the GPU
   const int n_col_tiles = (n_out + 255) / 256;
+  int edges_per_chunk = 1024;
+  while (edges_per_chunk > 128 && n_col_tiles * ((n_edges + edges_per_chunk - 1) / edges_per_chunk) < 2048)
+    edges_per_chunk >>= 1;
   const int64_t n_chunks = (n_edges + edges_per_chunk - 1) / edges_per_chunk;
   const int64_t n_wg = n_col_tiles * ((n_chunks + 7) / 8) * 8;
   if (n_wg > INT32_MAX) return tace_fail_msg("tace_radial_mlp_out_f32: too many edges");

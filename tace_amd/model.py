@@ -317,7 +317,8 @@ class _LinearLayout:
         ranges ``rr`` of Z rows; the last few are cached."""
         tile = (128, 128) if x.dtype == torch.float32 and SEG_LINEAR_TILE_F32 == 128 else (64, 64)
         presplit = tile == (128, 128) and SEG_LINEAR_PRESPLIT
-        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile, presplit, ops.SEG_TILE_FRAG)
+        key = (kind, tuple(rr), Z, str(x.device), bias is not None, weight.numel(), tile, presplit, ops.SEG_TILE_FRAG,
+               ops.SEG_SPLIT_SLOTS, ops.SEG_SPLIT_MIN_STEPS, ops.SEG_SPLIT_MAX_TILES)
         plan = self._seg.get(key)
         if plan is not None:
             self._seg.move_to_end(key)

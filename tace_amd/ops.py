@@ -1714,6 +1714,32 @@ SEG_KS_CHUNK = 1024
 # (tace_seg_linear_presplit_frag) when every instruction has a
 # fragment-order block; False: the planes of tace_seg_linear_presplit
 SEG_TILE_FRAG = True
+# fragment-order tile launches of at most SEG_SPLIT_MAX_TILES tiles (too
+# few to fill the GPU) may split each tile's k over several workgroups
+# (tace_seg_linear_presplit_frag_split): SEG_SPLIT_SLOTS is the number of
+# tile workgroups the GPU runs at once (two per CU; None: never split), a
+# split takes at least SEG_SPLIT_MIN_STEPS 32-k steps.  Measured: the
+# 1,024-atom alloy's model step 3.24 -> 2.90 ms; the ragged batch's 342-tile
+# launches were slower split (uneven tile heights), hence the tile limit
+SEG_SPLIT_SLOTS = 512
+SEG_SPLIT_MIN_STEPS = 8
+SEG_SPLIT_MAX_TILES = 192
+
+
+def seg_split_count(n_tiles: int, nks_min: int, nks_max: int) -> int:
+    """Splits per tile (1: none) for n_tiles tiles of nks_min .. nks_max
+    32-k steps: the fewest time units by a model in which the launch runs in
+    rounds of SEG_SPLIT_SLOTS workgroups, a workgroup takes one unit per step
+    plus one, and the partial sums' launch takes two."""
+    if SEG_SPLIT_SLOTS is None or n_tiles <= 0 or n_tiles > SEG_SPLIT_MAX_TILES:
+        return 1
+    slots = int(SEG_SPLIT_SLOTS)
+    best, best_c = 1, -(-n_tiles // slots) * (nks_max + 1)
+    for S in range(2, min(64, nks_min // max(1, SEG_SPLIT_MIN_STEPS)) + 1):
+        c = -(-n_tiles * S // slots) * (-(-nks_max // S) + 1) + 2
+        if c < best_c:
+            best, best_c = S, c
+    return best
 
 
 class SegLinearPlan:
@@ -1819,6 +1845,12 @@ class SegLinearPlan:
         # every contribution's x rows start on a 16-byte boundary (offsets and
         # k multiples of 4): the fragment-order tiles' aligned A loads
         self.tile_aligned = bool(len(c) == 0 or (((c[:, 0] % 4) == 0) & ((c[:, 1] % 4) == 0)).all())
+        # k split over `splits` workgroups per tile when the tiles are too few
+        # to fill the GPU (fragment-order tiles with one contribution each)
+        self.splits = 1
+        if self.tile_frag and len(t) and ((t[:, 6] - t[:, 5]) == 1).all():
+            nks = (c[t[:, 5], 1] + 31) // 32
+            self.splits = seg_split_count(len(t), int(nks.min()), int(nks.max()))
         self.x_numel, self.y_numel, self.w_numel, self.b_numel = x_numel, y_numel, w_numel, b_numel
         # multiply-adds x 2 of the whole launch (rows x valid columns x summed k
         # of every tile): the algorithmic flops of the GEMMs, padding excluded
@@ -1993,7 +2025,15 @@ def seg_linear_presplit(x: torch.Tensor, y: torch.Tensor, planes: Optional[torch
     st = N.stream_ptr(x.device)
     b_ptr = None if bias is None else bias.data_ptr()
     a_ptr = _addend_ptr(addend, y)
-    if plan.tile_frag:
+    if plan.tile_frag and plan.splits > 1:
+        pe = plan.n_tiles * plan.splits * 16384
+        partials = torch.empty(pe, dtype=torch.float32, device=x.device)
+        N.check(N.lib().tace_seg_linear_presplit_frag_split(x.data_ptr(), y.data_ptr(), a_ptr, frag.data_ptr(), b_ptr,
+                                                            plan.tiles.data_ptr(), plan.n_tiles,
+                                                            plan.contribs.data_ptr(), int(plan.tile_aligned),
+                                                            plan.splits, partials.data_ptr(), pe, float(alpha), st),
+                "tace_seg_linear_presplit_frag_split")
+    elif plan.tile_frag:
         N.check(N.lib().tace_seg_linear_presplit_frag(x.data_ptr(), y.data_ptr(), a_ptr, frag.data_ptr(), b_ptr,
                                                       plan.tiles.data_ptr(), plan.n_tiles, plan.contribs.data_ptr(),
                                                       int(plan.tile_aligned), float(alpha), st),

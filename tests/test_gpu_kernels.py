@@ -627,6 +627,7 @@ def test_seg_linear_presplit_equals_in_kernel_split(cuda, irr_in, irr_out, count
     weight update the planes are rebuilt."""
     from tace_amd import model as pm
     monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", 128)
+    monkeypatch.setattr(ops, "SEG_SPLIT_SLOTS", None)   # split k sums in another order
     S, Z = len(counts), sum(counts)
     species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
     attrs = torch.nn.functional.one_hot(species, S).float().to(cuda)
@@ -652,6 +653,107 @@ def test_seg_linear_presplit_equals_in_kernel_split(cuda, irr_in, irr_out, count
             assert torch.equal(outs[key][1], outs[(False, False)][1]), f"input gradient differs {key} (step {step})"
         with torch.no_grad():
             lin.weight.mul_(-0.5)   # a new weight version: the cached planes must be rebuilt
+
+
+@pytest.mark.parametrize("irr_in,irr_out,counts", SEG_CASES)
+def test_seg_linear_split_k(cuda, irr_in, irr_out, counts, monkeypatch):
+    """The fragment-order tile kernel with each tile's k split over several
+    workgroups (tace_seg_linear_presplit_frag_split: partial tiles, then
+    their sum in split order with addend and bias) against the unsplit
+    kernel, forward and input gradient, with and without an addend (in
+    place): equal up to float32 summation order, the same bits on a repeat;
+    tiles with two contributions stay unsplit."""
+    from tace_amd import model as pm
+    monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", 128)
+    monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", True)
+    monkeypatch.setattr(ops, "SEG_TILE_FRAG", True)
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).float().to(cuda)
+    g = torch.Generator().manual_seed(31)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(lin.weight.shape, generator=g))
+        lin.bias.copy_(torch.randn(lin.bias.shape, generator=g))
+    lin = lin.to(cuda)
+    sp = pm.SpeciesPlan(attrs)
+    n_split = 0
+    for kind, din, dout in (("fwd", lin.lay.dim_in, lin.lay.dim_out), ("bwd", lin.lay.dim_out, lin.lay.dim_in)):
+        x = torch.randn(Z, din, generator=g).to(cuda)
+        add = torch.randn(Z, dout, generator=g).to(cuda)
+        rr, seg = pm._linear_route(x, lin.weight, lin.lay, sp.ranges)
+        bias = lin.bias if kind == "fwd" else None
+        res = {}
+        for target, steps in ((None, 8), (4096, 1)):
+            monkeypatch.setattr(ops, "SEG_SPLIT_SLOTS", target)
+            monkeypatch.setattr(ops, "SEG_SPLIT_MIN_STEPS", steps)
+            if seg:
+                n_split += lin.lay.seg_plan(kind, rr, Z, x, lin.weight, bias).splits > 1
+            y = pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind)
+            y_again = pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind)
+            assert torch.equal(y, y_again), (kind, target)
+            y_acc = add.clone()
+            pm._linear_apply(x, lin.weight, bias, lin.lay, rr, seg, 0.8, kind=kind, out=y_acc, addend=y_acc)
+            res[target] = (y, y_acc)
+        close(res[4096][0], res[None][0], torch.float32, f"{kind} split k")
+        close(res[4096][1], res[None][1], torch.float32, f"{kind} split k, addend in place")
+    # every case but the first (two inputs into one output block in both
+    # directions) has a direction with one contribution per tile
+    if irr_in != SEG_CASES[0][0]:
+        assert n_split > 0
+
+
+def test_seg_linear_split_k_rejects_tiles_with_two_contributions(cuda, monkeypatch):
+    """A tile with two contributions handed to the split-k entry point gets
+    NaN in every output (the plan never splits such tiles); the other tiles
+    of the launch are right."""
+    from tace_amd import _native as N
+    from tace_amd import model as pm
+    monkeypatch.setattr(pm, "SEG_LINEAR_TILE_F32", 128)
+    monkeypatch.setattr(pm, "SEG_LINEAR_PRESPLIT", True)
+    monkeypatch.setattr(ops, "SEG_TILE_FRAG", True)
+    monkeypatch.setattr(ops, "SEG_SPLIT_SLOTS", None)
+    irr_in, irr_out, counts = "40x0e+72x0e+16x1o", "64x0e+32x1o", [150, 20]
+    S, Z = len(counts), sum(counts)
+    species = torch.repeat_interleave(torch.arange(S), torch.tensor(counts))
+    attrs = torch.nn.functional.one_hot(species, S).float().to(cuda)
+    g = torch.Generator().manual_seed(4)
+    lin = pm.e3nnElementLinear(irr_in, irr_out, S)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(lin.weight.shape, generator=g))
+    lin = lin.to(cuda)
+    sp = pm.SpeciesPlan(attrs)
+    x = torch.randn(Z, lin.lay.dim_in, generator=g).to(cuda)
+    rr, seg = pm._linear_route(x, lin.weight, lin.lay, sp.ranges)
+    assert seg
+    plan = lin.lay.seg_plan("fwd", rr, Z, x, lin.weight, None)
+    assert plan.tile_frag and plan.splits == 1 and plan.n_ks == 0
+    want = pm._linear_apply(x, lin.weight, None, lin.lay, rr, seg, 1.0, kind="fwd")
+    frag = lin.lay.split_weights("fwd", lin.weight, frag=True)[0]
+    t = plan.tiles.cpu().numpy()
+    multi = (t[:, 6] - t[:, 5]) > 1
+    assert multi.any() and (~multi).any()
+    y = torch.zeros_like(want)
+    pe = plan.n_tiles * 2 * 16384
+    partials = torch.empty(pe, device=cuda)
+    N.check(N.lib().tace_seg_linear_presplit_frag_split(x.data_ptr(), y.data_ptr(), None, frag.data_ptr(), None,
+                                                        plan.tiles.data_ptr(), plan.n_tiles,
+                                                        plan.contribs.data_ptr(), int(plan.tile_aligned), 2,
+                                                        partials.data_ptr(), pe, 1.0, N.stream_ptr(cuda)),
+            "split k")
+    torch.cuda.synchronize()
+    yf = y.view(-1)
+    for (ob, rows, n, c0, _b, cb, ce, _u) in t.tolist():
+        idx = ob + torch.arange(rows, device=cuda)[:, None] * n + c0 + torch.arange(min(128, n - c0), device=cuda)
+        if ce - cb > 1:
+            assert torch.isnan(yf[idx]).all()
+        else:
+            close(yf[idx], want.view(-1)[idx], torch.float32, "one-contribution tile")
+    with pytest.raises(RuntimeError, match="partials hold fewer"):
+        N.check(N.lib().tace_seg_linear_presplit_frag_split(x.data_ptr(), y.data_ptr(), None, frag.data_ptr(), None,
+                                                            plan.tiles.data_ptr(), plan.n_tiles,
+                                                            plan.contribs.data_ptr(), 1, 2, partials.data_ptr(),
+                                                            pe - 1, 1.0, N.stream_ptr(cuda)), "split k")
 
 
 def test_seg_linear_f32_error_matches_float32_gemm(cuda):

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 30
+#define TACE_HIP_ABI_VERSION 31
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -434,8 +434,13 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
                             const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
                             const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows, int64_t n_edges,
                             int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst, void* g_wigner,
-                            void* g_radial_w, void* stream);
-/* tace_edge_rotate_in_bwd_runs: tace_edge_rotate_in_bwd for edges in
+                            void* g_radial_w, int32_t accumulate_wigner, void* stream);
+/* accumulate_wigner != 0: g_wigner[e] += this gradient on the Wigner
+ * matrix's l blocks, the entries off the blocks left as they are (the
+ * caller's zeros, as tace_tece_rotate_out_bwd writes them), so the two
+ * rotations' Wigner gradients sum without another pass; 0: g_wigner is
+ * written, zeros off the blocks.
+ * tace_edge_rotate_in_bwd_runs: tace_edge_rotate_in_bwd for edges in
  * receiver-CSR order, 4 (lmax+1)^2 channels values of at most 64 KB: the
  * receiver rows of the four edges a workgroup holds (positions 4 b .. 4 b + 3)
  * are summed per run of equal rows_dst in edge order and written once, at the
@@ -447,7 +452,7 @@ int tace_edge_rotate_in_bwd_runs(int dtype, const void* x, const void* wigner, c
                                  const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
                                  const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows,
                                  int64_t n_edges, int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst_runs,
-                                 void* g_wigner, void* g_radial_w, void* stream);
+                                 void* g_wigner, void* g_radial_w, int32_t accumulate_wigner, void* stream);
 int tace_tece_score_fwd(int dtype, const void* const* q, const void* const* k, const void* radial_proj,
                         const void* tscale, int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads,
                         void* score, void* stream);

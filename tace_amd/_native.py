@@ -71,9 +71,9 @@ _SIGS = {
     "tace_edge_rotate_in_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp, _vp,
                                          _vp, _vp]),
     "tace_edge_rotate_in_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32,
-                                         _c_i32, _vp, _vp, _vp, _vp, _vp]),
+                                         _c_i32, _vp, _vp, _vp, _vp, _c_i32, _vp]),
     "tace_edge_rotate_in_bwd_runs": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64,
-                                              _c_i32, _c_i32, _vp, _vp, _vp, _vp, _vp]),
+                                              _c_i32, _c_i32, _vp, _vp, _vp, _vp, _c_i32, _vp]),
     "tace_tece_edge_ace_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _vp, _vp, _vp, _vp,
                                         _vp]),
     "tace_tece_edge_ace_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32,

@@ -177,7 +177,7 @@ __device__ __forceinline__ void rotin_bwd_edge(const T* __restrict__ x, const T*
                                                const Blk<const T>& gms, const Blk<const T>& gmd,
                                                const Blk<const T>& gmw, int64_t n_rows, int64_t E, int C, int64_t e,
                                                T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
-                                               T* __restrict__ gwr, T* __restrict__ lrow) {
+                                               T* __restrict__ gwr, T* __restrict__ lrow, bool accW) {
   constexpr int K = (L + 1) * (L + 1), NB = wig_nb<L>(), P = (NB + 15) / 16 * 16, NC = (L + 1) * (L + 2) / 2;
   const int lane = (int)threadIdx.x & 63;
   const T* w = W + e * K * K;
@@ -294,9 +294,11 @@ __device__ __forceinline__ void rotin_bwd_edge(const T* __restrict__ x, const T*
       int r = 0;
       while (r + 1 < K && wig_row_off<L>(r + 1) <= i) ++r;
       const int l = m_l<L>(r);
-      gW[e * K * K + r * K + l * l + (i - wig_row_off<L>(r))] = t;
+      T* dst = gW + e * K * K + r * K + l * l + (i - wig_row_off<L>(r));
+      *dst = accW ? *dst + t : t;
     }
   }
+  if (accW) return;   // the entries off the blocks hold the caller's zeros
   for (int i = lane; i < K * K; i += 64) {
     const int r = i / K, kk = i - r * K;
     if (l_of(kk) != m_l<L>(r)) gW[e * K * K + i] = T(0);
@@ -317,14 +319,14 @@ __global__ __launch_bounds__(256) void k_rotin_bwd(const T* __restrict__ x, cons
                                                    const Blk<const T> gms, const Blk<const T> gmd,
                                                    const Blk<const T> gmw, int64_t n_rows, int64_t E, int C,
                                                    T* __restrict__ gxs, T* __restrict__ gxd, T* __restrict__ gW,
-                                                   T* __restrict__ gwr) {
+                                                   T* __restrict__ gwr, bool accW) {
   constexpr int K = (L + 1) * (L + 1);
   extern __shared__ __attribute__((aligned(16))) unsigned char rb_raw[];
   const int64_t e = wave_edge();
   if (!RUNS && e >= E) return;
   if (e < E)
     rotin_bwd_edge<T, L, NS, V, RUNS>(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, n_rows, E, C, e, gxs, gxd, gW,
-                                      gwr, (T*)rb_raw + (threadIdx.x >> 6) * K * C);
+                                      gwr, (T*)rb_raw + (threadIdx.x >> 6) * K * C, accW);
   if constexpr (RUNS) {
     __syncthreads();
     const T* rows = (const T*)rb_raw;
@@ -439,7 +441,8 @@ static int tace_edge_rotate_in_bwd_impl(int dtype, const void* x, const void* wi
                                         const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
                                         const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows,
                                         int64_t n_edges, int32_t lmax, int32_t channels, void* g_x_src,
-                                        void* g_x_dst, void* g_wigner, void* g_radial_w, bool runs, void* stream) {
+                                        void* g_x_dst, void* g_wigner, void* g_radial_w, bool runs, bool acc_wigner,
+                                        void* stream) {
   const char* who = runs ? "tace_edge_rotate_in_bwd_runs" : "tace_edge_rotate_in_bwd";
   if (rotin_checks(who, n_rows, n_edges, lmax, channels)) return -1;
   const size_t es = dtype == TACE_F64 ? 8 : 4;
@@ -463,7 +466,7 @@ static int tace_edge_rotate_in_bwd_impl(int dtype, const void* x, const void* wi
     hipLaunchKernelGGL((k_rotin_bwd<TT, LL, NS, VV, RR>), g, b, lds, s, (const TT*)x, (const TT*)wigner,        \
                        rows_src, rows_dst, (const TT*)radial_w, blocks_of<const TT>(g_m_src, lmax),             \
                        blocks_of<const TT>(g_m_dst, lmax), blocks_of<const TT>(g_m_w, lmax), n_rows, n_edges,    \
-                       channels, (TT*)g_x_src, (TT*)g_x_dst, (TT*)g_wigner, (TT*)g_radial_w))
+                       channels, (TT*)g_x_src, (TT*)g_x_dst, (TT*)g_wigner, (TT*)g_radial_w, acc_wigner))
 #define RI_BL(TT, VV, RR, SLOTS)                                                                                  \
   if (lmax == 1) { RI_B(TT, 1, VV, RR, SLOTS) } else if (lmax == 2) { RI_B(TT, 2, VV, RR, SLOTS) }             \
   else { RI_B(TT, 3, VV, RR, SLOTS) }
@@ -476,7 +479,7 @@ static int tace_edge_rotate_in_bwd_impl(int dtype, const void* x, const void* wi
   hipLaunchKernelGGL((k_rotin_bwd<float, LL, NSP, 2, RR>), g, b, lds, s, (const float*)x, (const float*)wigner, \
                      rows_src, rows_dst, (const float*)radial_w, blocks_of<const float>(g_m_src, lmax),          \
                      blocks_of<const float>(g_m_dst, lmax), blocks_of<const float>(g_m_w, lmax), n_rows, n_edges,  \
-                     channels, (float*)g_x_src, (float*)g_x_dst, (float*)g_wigner, (float*)g_radial_w);
+                     channels, (float*)g_x_src, (float*)g_x_dst, (float*)g_wigner, (float*)g_radial_w, acc_wigner);
   if (pairs) {
     // channel pairs: lmax <= 2 and channels <= 512 (rotin_bwd_pairs)
     if (runs) { RI_BP(true) } else { RI_BP(false) }
@@ -500,20 +503,20 @@ int tace_edge_rotate_in_bwd(int dtype, const void* x, const void* wigner, const 
                             const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
                             const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows, int64_t n_edges,
                             int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst, void* g_wigner,
-                            void* g_radial_w, void* stream) {
+                            void* g_radial_w, int32_t accumulate_wigner, void* stream) {
   return tace_edge_rotate_in_bwd_impl(dtype, x, wigner, rows_src, rows_dst, radial_w, g_m_src, g_m_dst, g_m_w,
                                       n_rows, n_edges, lmax, channels, g_x_src, g_x_dst, g_wigner, g_radial_w,
-                                      false, stream);
+                                      false, accumulate_wigner != 0, stream);
 }
 
 int tace_edge_rotate_in_bwd_runs(int dtype, const void* x, const void* wigner, const int64_t* rows_src,
                                  const int64_t* rows_dst, const void* radial_w, const void* const* g_m_src,
                                  const void* const* g_m_dst, const void* const* g_m_w, int64_t n_rows,
                                  int64_t n_edges, int32_t lmax, int32_t channels, void* g_x_src, void* g_x_dst_runs,
-                                 void* g_wigner, void* g_radial_w, void* stream) {
+                                 void* g_wigner, void* g_radial_w, int32_t accumulate_wigner, void* stream) {
   return tace_edge_rotate_in_bwd_impl(dtype, x, wigner, rows_src, rows_dst, radial_w, g_m_src, g_m_dst, g_m_w,
                                       n_rows, n_edges, lmax, channels, g_x_src, g_x_dst_runs, g_wigner, g_radial_w,
-                                      true, stream);
+                                      true, accumulate_wigner != 0, stream);
 }
 
 }  // extern "C"

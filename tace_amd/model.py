@@ -1282,9 +1282,15 @@ class TACE(torch.nn.Module):
         e_node = self.energy_readouts[0](x)[:, 0].index_select(0, sp.inv)  # back to node order
         num_nodes = ptr[1:] - ptr[:-1]
         ei = data["edge_index"]
-        num_edges = torch.zeros(num_graphs, dtype=torch.int64, device=attrs.device)
-        if ei.numel():
-            num_edges = num_edges.index_add(0, batch[ei[1]], torch.ones_like(ei[1]))
+        if isinstance(plan, ops.EdgePlan) and plan.n_nodes == attrs.shape[0]:
+            # edges per graph from the receiver CSR (graph g's receivers are
+            # nodes ptr[g] .. ptr[g+1]-1): no per-edge atomics on a few counters
+            rp = plan.rowptr.long()
+            num_edges = rp[ptr[1:]] - rp[ptr[:-1]]
+        else:
+            num_edges = torch.zeros(num_graphs, dtype=torch.int64, device=attrs.device)
+            if ei.numel():
+                num_edges = num_edges.index_add(0, batch[ei[1]], torch.ones_like(ei[1]))
         isolated = ((num_nodes == 1) & (num_edges == 0))[batch]
         scale = (attrs * self.scale_shift.scale[0]).sum(-1)
         e_node = e_node * torch.where(isolated, torch.zeros_like(scale), scale)

@@ -1046,7 +1046,9 @@ def launch_rotate_out_fwd(m, alpha, W, plan: EdgePlan, node_map, lmax: int, H: i
 
 
 def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax: int, H: int,
-                          bf16_out: bool = False):
+                          bf16_out: bool = False, gW_out: Optional[torch.Tensor] = None):
+    """(g_m, g_alpha, g_wigner) of the rotate-out; g_wigner into ``gW_out``
+    when given (a contiguous tensor of W's shape)."""
     E, dt = W.shape[0], W.dtype
     K = (lmax + 1) ** 2
     C = m[0].shape[1] // (lmax + 1)
@@ -1054,7 +1056,10 @@ def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax
     _req(dst, "dst", torch.int64, (E,))
     odt = torch.bfloat16 if bf16_out else dt
     gm = [torch.empty(t.shape, dtype=odt, device=t.device) for t in m]
-    ga, gW = torch.empty_like(alpha), torch.empty_like(W)
+    ga = torch.empty_like(alpha)
+    if gW_out is not None:
+        _req(gW_out, "gW_out", dt, tuple(W.shape))
+    gW = torch.empty_like(W) if gW_out is None else gW_out
     tok = _t0("tece_rotate_out_bwd")
     N.check(N.lib().tace_tece_rotate_out_bwd(_tece_code(dt, bf16_out), _block_array(m), alpha.data_ptr(),
                                              W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
@@ -1101,18 +1106,22 @@ def rotate_in_runs_ok(x: torch.Tensor) -> bool:
     return 4 * K * C * x.element_size() <= 65536
 
 
-def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: bool, runs: bool = False):
+def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: bool, runs: bool = False,
+                         gW_acc: Optional[torch.Tensor] = None):
     """Per-edge grad_x rows of the senders / receivers [E, K, C] each, g_wigner
     and (need_gwr) g_radial_w; gmw None = no gradient reaches m_w.  runs
     (edges in receiver-CSR order, ``rotate_in_runs_ok``): the receiver rows
     come as run sums at the runs' first positions
     (``tace_edge_rotate_in_bwd_runs``), for ``rows_accumulate(...,
-    run=ROTIN_RUNS)``."""
+    run=ROTIN_RUNS)``.  gW_acc: a Wigner gradient with zeros off the l blocks
+    (the rotate-out backward's) that g_wigner is added into and returned as."""
     Nr, K, C = x.shape
     E = W.shape[0]
     gxs = torch.empty(E, K, C, dtype=x.dtype, device=x.device)
     gxd = torch.empty_like(gxs)
-    gW = torch.empty_like(W)
+    if gW_acc is not None:
+        _req(gW_acc, "gW_acc", W.dtype, tuple(W.shape))
+    gW = torch.empty_like(W) if gW_acc is None else gW_acc
     gwr = None
     if wr is not None and need_gwr:
         gwr = torch.empty_like(wr) if gmw is not None else torch.zeros_like(wr)
@@ -1125,7 +1134,7 @@ def launch_rotate_in_bwd(x, W, rows_src, rows_dst, wr, gms, gmd, gmw, need_gwr: 
                                    _block_array(gmw) if gmw is not None else None, Nr, E,
                                    (int(math.isqrt(K)) - 1), C, gxs.data_ptr(), gxd.data_ptr(),
                                    gW.data_ptr(), N.ptr(gwr) if gmw is not None else None,
-                                   N.stream_ptr(x.device)), name)
+                                   int(gW_acc is not None), N.stream_ptr(x.device)), name)
     _t1(tok, (E, K, C, gmw is not None, bool(runs)))
     return gxs, gxd, gW, gwr
 

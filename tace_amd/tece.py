@@ -547,16 +547,19 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
 
 
 def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, dst_out, recv_rows, saved,
-                     g_out, gx):
+                     g_out, gx, gR_out=None, gW_out=None):
     """Backward of one chunk: adds its grad_x into ``gx`` (per-edge rows
     summed over the receiver CSR -- receivers at feature rows ``recv_rows``
     -- and over a sender CSR, in fixed order) and returns (grad_R, grad_W)
-    of its edges."""
+    of its edges, written into ``gR_out`` / ``gW_out`` when given."""
     L, H, A = P.lmax, P.H, P.A
     if saved is None:
         _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True, need_out=False)
     w, q, k, rp, alpha, ys, mb = saved
-    gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16)
+    # the two rotations' Wigner gradients: the rotate-out's written (zeros
+    # off the l blocks), the rotate-in's added on the blocks
+    gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16,
+                                                gW_out=gW_out)
     go = [P.mm_grad(gm[m], P.d_N[m]) for m in range(L + 1)]
     del gm
     gys = ops.launch_edge_ace_bwd(ys, go, L, A, P.bf16)
@@ -572,7 +575,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     # edges in receiver-CSR order: the receiver rows come as run sums of each
     # workgroup's four edges, a quarter of the rows to write and read back
     runs = ops.ROTIN_RUNS if plan.eid is None and ops.rotate_in_runs_ok(x_lc) else 1
-    gxs, gxd, gW_in, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True, runs=runs > 1)
+    gxs, gxd, gW, gw = ops.launch_rotate_in_bwd(x_lc, W, rs, rd, w, gms, gmd, gmw, True, runs=runs > 1, gW_acc=gW)
     Nr, E = x_lc.shape[0], rs.shape[0]
     g2 = gx.view(Nr, -1)
     ops.rows_accumulate(g2, gxd.view(E, -1), plan.rowptr, plan.eid, recv_rows, run=runs)
@@ -583,8 +586,8 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
         gh = ops.launch_mlp_out_bwd_f32(gw, P.mlp_W, P.mlp_alpha)
     else:
         gh = torch.mm(gw, P.mlp_WT_scaled)
-    gR += ops.launch_mlp_hidden_bwd(R, gh, P.mlp_flat, P.mlp_layers)
-    return gR, gW.add_(gW_in)
+    gR = torch.add(gR, ops.launch_mlp_hidden_bwd(R, gh, P.mlp_flat, P.mlp_layers), out=gR_out)
+    return gR, gW
 
 
 def _gm_blocks(t, n: int, L: int, C: int):
@@ -663,12 +666,10 @@ class _TeceFused(torch.autograd.Function):
             rows_c = node_map[n0:n1].long()
             g_c = torch.cat([f.index_select(0, rows_c).reshape(-1) for f in full]).view(n1 - n0, -1)
             saved, ctx.saved_chunks[i] = ctx.saved_chunks[i], None
-            gR_c, gW_c = _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
-                                          sub_plan(plan, n0, n1, e0, e1), None, dst[e0:e1] - n0,
-                                          node_map[n0:n1].contiguous(), saved, g_c, gx)
+            _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1], sub_plan(plan, n0, n1, e0, e1),
+                             None, dst[e0:e1] - n0, node_map[n0:n1].contiguous(), saved, g_c, gx,
+                             gR_out=gR[e0:e1], gW_out=gW[e0:e1])
             del saved
-            gR[e0:e1] = gR_c
-            gW[e0:e1] = gW_c
         return gx, gR, gW, None, None, None, None, None, None, None
 
 

@@ -453,6 +453,16 @@ def test_rotate_in_bwd_runs_equal_per_edge_rows(cuda, dtype, lmax, C):
     close(got, want, dtype, "receiver sums", tol=1e-13 if dtype == torch.float64 else 1e-6)
     idle = node_map[(counts == 0).nonzero().flatten()].long().to(cuda)
     assert idle.numel() >= 2 and torch.equal(got[idle], base[idle])
+    # accumulate mode (accumulate_wigner = 1): g_wigner added on the l blocks
+    # into a given gradient with zeros off them; the other outputs unchanged
+    blk = _wigner_block_mask(lmax).to(cuda)
+    prior = dv(torch.randn(E, K, K, generator=g, dtype=torch.float64)) * blk
+    for runs in (False, True):
+        acc = prior.clone()
+        c = ops.launch_rotate_in_bwd(x, W, rs, rd, wr, gms, gmd, gmw, True, runs=runs, gW_acc=acc)
+        assert c[2].data_ptr() == acc.data_ptr()
+        assert torch.equal(acc, prior + a[2]), runs
+        assert torch.equal(c[0], a[0]) and torch.equal(c[3], a[3]), runs
 
 
 # ------------------------------------------------------------- edge ACE ----

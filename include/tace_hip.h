@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define TACE_HIP_ABI_VERSION 31
+#define TACE_HIP_ABI_VERSION 32
 #define TACE_MAX_CHANNELS 512
 #define TACE_F32 0
 #define TACE_F64 1
@@ -471,9 +471,15 @@ int tace_graph_softmax_fwd(int dtype, const void* score, const int32_t* rowptr, 
                            int32_t heads, void* alpha, void* stream);
 int tace_graph_softmax_bwd(int dtype, const void* alpha, const void* g_alpha, const int32_t* rowptr,
                            const int32_t* eid, int64_t n_nodes, int32_t heads, void* g_score, void* stream);
+/* tace_tece_rotate_out_fwd writes out with out_rows rows (0: n_nodes; other
+ * values need node_map, each of the n_nodes receivers going to row
+ * node_map[n] < out_rows): a receiver chunk's sums go straight into the
+ * whole batch's output.  tace_tece_rotate_out_bwd reads g_out with n_nodes
+ * rows the same way (the whole batch's, with a chunk's edges and dst). */
 int tace_tece_rotate_out_fwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
                              const int32_t* rowptr, const int32_t* eid, const int32_t* node_map, int64_t n_nodes,
-                             int32_t lmax, int32_t channels, int32_t heads, void* out, void* stream);
+                             int64_t out_rows, int32_t lmax, int32_t channels, int32_t heads, void* out,
+                             void* stream);
 int tace_tece_rotate_out_bwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
                              const void* g_out, const int64_t* dst, const int32_t* node_map, int64_t n_nodes,
                              int64_t n_edges, int32_t lmax, int32_t channels, int32_t heads, const void* const* g_m,

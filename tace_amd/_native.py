@@ -64,8 +64,8 @@ _SIGS = {
                                      _vp, _vp]),
     "tace_graph_softmax_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
     "tace_graph_softmax_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _vp, _vp]),
-    "tace_tece_rotate_out_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i32, _c_i32, _c_i32,
-                                          _vp, _vp]),
+    "tace_tece_rotate_out_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
+                                          _c_i32, _vp, _vp]),
     "tace_tece_rotate_out_bwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32,
                                           _c_i32, _vp, _vp, _vp, _vp]),
     "tace_edge_rotate_in_fwd": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_i64, _c_i32, _c_i32, _vp, _vp,

@@ -13,13 +13,14 @@
 // --------------------------------------------------- rotate out + scatter --
 // out[n, k, c] = sum_{e -> n} sum_r W[e, r, k] alpha[e, c / Ch] m[e, r, c]
 // (r in column k's l block: the Wigner matrix's blocks only are read)
-// written group-major (block l of the batch = [N, 2l+1, C] at N*C*l^2) at
-// feature row map[n].  One workgroup per receiver, one lane per channel.
+// written group-major (block l of the output = [NN, 2l+1, C] at NN*C*l^2, NN
+// output rows) at feature row map[n].  One workgroup per receiver, one lane
+// per channel.
 template <typename T, int L>
 __global__ __launch_bounds__(512) void k_rotout_fwd(const Blk<const T> m, const T* __restrict__ alpha,
                                                     const T* __restrict__ W, const int* __restrict__ rowptr,
                                                     const int* __restrict__ eid, const int* __restrict__ map,
-                                                    int N, int C, int H, T* __restrict__ out) {
+                                                    int N, int64_t NN, int C, int H, T* __restrict__ out) {
   constexpr int K = (L + 1) * (L + 1);
   const int n0 = blockIdx.x;
   const int c = threadIdx.x;
@@ -45,7 +46,6 @@ __global__ __launch_bounds__(512) void k_rotout_fwd(const Blk<const T> m, const 
       }
   }
   const int n = map ? map[n0] : n0;
-  const int64_t NN = N;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     int l = 0;
@@ -177,9 +177,12 @@ static int rotout_checks(const char* who, int64_t N, int32_t lmax, int32_t C, in
 
 int tace_tece_rotate_out_fwd(int dtype, const void* const* m, const void* alpha, const void* wigner,
                              const int32_t* rowptr,
-                             const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int32_t lmax,
-                             int32_t channels, int32_t heads, void* out, void* stream) {
+                             const int32_t* eid, const int32_t* node_map, int64_t n_nodes, int64_t out_rows,
+                             int32_t lmax, int32_t channels, int32_t heads, void* out, void* stream) {
   if (rotout_checks("tace_tece_rotate_out_fwd", n_nodes, lmax, channels, heads)) return -1;
+  if (out_rows == 0) out_rows = n_nodes;
+  if (out_rows < 0 || (out_rows != n_nodes && !node_map))
+    return tace_fail_msg("tace_tece_rotate_out_fwd: out_rows other than n_nodes needs a node_map");
   if (n_nodes == 0) return 0;
   if (!rowptr || !out) return tace_fail_msg("tace_tece_rotate_out_fwd: null pointer");
   if (!m) return tace_fail_msg("tace_tece_rotate_out_fwd: null block array");
@@ -187,7 +190,7 @@ int tace_tece_rotate_out_fwd(int dtype, const void* const* m, const void* alpha,
   const dim3 g((unsigned)n_nodes), b((unsigned)((channels + 63) / 64 * 64));
 #define ROT_F(TT, LL)                                                                                           \
   hipLaunchKernelGGL((k_rotout_fwd<TT, LL>), g, b, 0, s, blocks_of<const TT>(m, lmax), (const TT*)alpha,      \
-                     (const TT*)wigner, rowptr, eid, node_map, (int)n_nodes, channels, heads, (TT*)out)
+                     (const TT*)wigner, rowptr, eid, node_map, (int)n_nodes, out_rows, channels, heads, (TT*)out)
   if (dtype == TACE_F32) {
     if (lmax == 1) ROT_F(float, 1); else if (lmax == 2) ROT_F(float, 2); else ROT_F(float, 3);
   } else if (dtype == TACE_F64) {

@@ -199,15 +199,8 @@ class EdgePlan:
         """(s_rowptr int32 [N+1], s_slot int32 [E]): receiver-sorted slots grouped
         by sender, stable -- the fixed order of the grad_x segmented sum."""
         if self._sender is None:
-            slot_src = self.src.long() if self.eid is None else self.src.long()[self.eid.long()]
-            order = torch.argsort(slot_src, stable=True).to(torch.int32).contiguous()
-            # counts by index_add_ (integer sums: exact in any order; bincount
-            # would read the largest index back to the host)
-            dev = self.src.device
-            rp = torch.zeros(self.n_nodes + 1, dtype=torch.int64, device=dev)
-            rp[1:].index_add_(0, slot_src, torch.ones_like(slot_src))
-            rp = torch.cumsum(rp, 0)
-            self._sender = (rp.to(torch.int32).contiguous(), order)
+            slot_src = self.src if self.eid is None else self.src[self.eid.long()]
+            self._sender = group_by_key(slot_src, self.n_nodes)
         return self._sender
 
     def edge_pairs(self, shifts: torch.Tensor) -> "EdgePairs":
@@ -1026,7 +1019,11 @@ def launch_softmax_bwd(a, ga, plan: EdgePlan) -> torch.Tensor:
     return gs
 
 
-def launch_rotate_out_fwd(m, alpha, W, plan: EdgePlan, node_map, lmax: int, H: int) -> torch.Tensor:
+def launch_rotate_out_fwd(m, alpha, W, plan: EdgePlan, node_map, lmax: int, H: int,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Receiver sums [n_nodes, K C] (group-major, rows node_map[n]); with
+    ``out`` (a whole batch's output, any row count, node_map required) the
+    sums of plan's receivers go into its rows node_map[n]."""
     E, dt = W.shape[0], W.dtype
     K = (lmax + 1) ** 2
     C = m[0].shape[1] // (lmax + 1)
@@ -1035,24 +1032,33 @@ def launch_rotate_out_fwd(m, alpha, W, plan: EdgePlan, node_map, lmax: int, H: i
     _req(W, "wigner", dt, (E, K, K))
     if node_map is not None:
         _req(node_map, "node_map", torch.int32, (plan.n_nodes,))
-    out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=W.device)
+    if out is None:
+        out = torch.empty(plan.n_nodes, K * C, dtype=dt, device=W.device)
+    else:
+        if node_map is None:
+            raise ValueError("rotate-out into a given output needs the receivers' rows (node_map)")
+        _req(out, "out", dt, (out.shape[0], K * C))
     tok = _t0("tece_rotate_out_fwd")
     N.check(N.lib().tace_tece_rotate_out_fwd(N.dtype_code(dt), _block_array(m), alpha.data_ptr(), W.data_ptr(),
                                              plan.rowptr.data_ptr(), N.ptr(plan.eid), N.ptr(node_map), plan.n_nodes,
-                                             lmax, C, H, out.data_ptr(), N.stream_ptr(W.device)),
+                                             out.shape[0], lmax, C, H, out.data_ptr(), N.stream_ptr(W.device)),
             "tace_tece_rotate_out_fwd")
     _t1(tok, (plan.n_nodes, E, C, K, H))
     return out
 
 
 def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax: int, H: int,
-                          bf16_out: bool = False, gW_out: Optional[torch.Tensor] = None):
+                          bf16_out: bool = False, gW_out: Optional[torch.Tensor] = None,
+                          g_rows: Optional[int] = None):
     """(g_m, g_alpha, g_wigner) of the rotate-out; g_wigner into ``gW_out``
-    when given (a contiguous tensor of W's shape)."""
+    when given (a contiguous tensor of W's shape).  ``g_rows``: the row count
+    of gout when it is not plan.n_nodes (a whole batch's gradient read at
+    rows node_map[dst[e]] for a chunk's edges)."""
     E, dt = W.shape[0], W.dtype
     K = (lmax + 1) ** 2
     C = m[0].shape[1] // (lmax + 1)
-    _req(gout, "g_out", dt, (plan.n_nodes, K * C))
+    n_rows = plan.n_nodes if g_rows is None else int(g_rows)
+    _req(gout, "g_out", dt, (n_rows, K * C))
     _req(dst, "dst", torch.int64, (E,))
     odt = torch.bfloat16 if bf16_out else dt
     gm = [torch.empty(t.shape, dtype=odt, device=t.device) for t in m]
@@ -1063,7 +1069,7 @@ def launch_rotate_out_bwd(m, alpha, W, gout, dst, node_map, plan: EdgePlan, lmax
     tok = _t0("tece_rotate_out_bwd")
     N.check(N.lib().tace_tece_rotate_out_bwd(_tece_code(dt, bf16_out), _block_array(m), alpha.data_ptr(),
                                              W.data_ptr(), gout.data_ptr(), dst.data_ptr(), N.ptr(node_map),
-                                             plan.n_nodes, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
+                                             n_rows, E, lmax, C, H, _block_array(gm), ga.data_ptr(),
                                              gW.data_ptr(), N.stream_ptr(W.device)), "tace_tece_rotate_out_bwd")
     _t1(tok, (plan.n_nodes, E, C, K, H, bf16_out))
     return gm, ga, gW
@@ -1311,15 +1317,25 @@ def scatter_add_rows(out: torch.Tensor, index: torch.Tensor, src: torch.Tensor) 
     return rows_accumulate(out.view(n, -1), src.reshape(E, -1).contiguous(), rp, slot).view(out.shape)
 
 
+def group_by_key(keys: torch.Tensor, n_keys: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(rowptr int32 [n_keys+1], order int32 [E]) of keys in [0, n_keys): the
+    positions grouped by key, in position order within a key (a stable sort
+    of 32-bit keys, half the radix passes of 64-bit ones), and each key's
+    range from a binary search of the sorted keys (no atomics, no host
+    synchronisation)."""
+    if n_keys >= 2 ** 31:
+        raise ValueError("group_by_key: more than 2^31 keys")
+    k32 = keys.to(torch.int32)
+    srt, order = torch.sort(k32, stable=True)
+    bounds = torch.arange(n_keys + 1, dtype=torch.int32, device=keys.device)
+    rp = torch.searchsorted(srt, bounds, out_int32=True)
+    return rp.contiguous(), order.to(torch.int32).contiguous()
+
+
 def sender_csr(rows_src: torch.Tensor, n_rows: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """(rowptr int32 [n_rows+1], slot int32 [E]): the edges grouped by sender
     row, in edge order within a sender."""
-    slot = torch.argsort(rows_src, stable=True).to(torch.int32)
-    # counts by index_add_ (exact integer sums; bincount reads the largest
-    # index back to the host)
-    rp = torch.zeros(n_rows + 1, dtype=torch.int64, device=rows_src.device)
-    rp[1:].index_add_(0, rows_src, torch.ones_like(rows_src))
-    return torch.cumsum(rp, 0).to(torch.int32), slot
+    return group_by_key(rows_src, n_rows)
 
 
 def _pad4(lst):

@@ -519,10 +519,11 @@ class _FusedParams:
 
 
 def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, out_map, save: bool,
-                     need_out: bool = True):
+                     need_out: bool = True, out=None):
     """One receiver chunk of the convolution (the sequence of
     ``TeceConvolution.edges`` with the radial MLP in front).  Returns the
-    receiver sums (None without ``need_out``: a recompute for the backward)
+    receiver sums (None without ``need_out``: a recompute for the backward;
+    written into the whole batch's ``out`` at rows ``out_map`` when given)
     and, with ``save``, what the backward needs."""
     L, H, A = P.lmax, P.H, P.A
     h = ops.launch_mlp_hidden_fwd(R, P.mlp_flat, P.mlp_layers)
@@ -542,7 +543,7 @@ def _fused_chunk_fwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     o = ops.launch_edge_ace_fwd(ys, L, A, P.bf16)
     mb = [P.mm(o[m], P.d_T[m], P.d_b if m == 0 else None) for m in range(L + 1)]
     del o
-    out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H) if need_out else None
+    out = ops.launch_rotate_out_fwd(mb, alpha, W, plan, out_map, L, H, out=out) if need_out else None
     return out, ((w, query, key, rp, alpha, ys, mb) if save else None)
 
 
@@ -551,7 +552,8 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     """Backward of one chunk: adds its grad_x into ``gx`` (per-edge rows
     summed over the receiver CSR -- receivers at feature rows ``recv_rows``
     -- and over a sender CSR, in fixed order) and returns (grad_R, grad_W)
-    of its edges, written into ``gR_out`` / ``gW_out`` when given."""
+    of its edges, written into ``gR_out`` / ``gW_out`` when given.  g_out
+    is the whole batch's output gradient, read at rows out_map[dst_out[e]]."""
     L, H, A = P.lmax, P.H, P.A
     if saved is None:
         _, saved = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, out_map, True, need_out=False)
@@ -559,7 +561,7 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
     # the two rotations' Wigner gradients: the rotate-out's written (zeros
     # off the l blocks), the rotate-in's added on the blocks
     gm, g_alpha, gW = ops.launch_rotate_out_bwd(mb, alpha, W, g_out, dst_out, out_map, plan, L, H, P.bf16,
-                                                gW_out=gW_out)
+                                                gW_out=gW_out, g_rows=g_out.shape[0])
     go = [P.mm_grad(gm[m], P.d_N[m]) for m in range(L + 1)]
     del gm
     gys = ops.launch_edge_ace_bwd(ys, go, L, A, P.bf16)
@@ -588,12 +590,6 @@ def _fused_chunk_bwd(P: _FusedParams, x_lc, R, W, rs, rd, plan: ops.EdgePlan, ou
         gh = torch.mm(gw, P.mlp_WT_scaled)
     gR = torch.add(gR, ops.launch_mlp_hidden_bwd(R, gh, P.mlp_flat, P.mlp_layers), out=gR_out)
     return gR, gW
-
-
-def _gm_blocks(t, n: int, L: int, C: int):
-    """[n, (L+1)^2 C] group-major rows -> per-l views [n, 2l+1, C]."""
-    flat = t.view(-1)
-    return [flat[n * C * l * l:n * C * (l + 1) ** 2].view(n, 2 * l + 1, C) for l in range(L + 1)]
 
 
 # HBM left free when chunk intermediates are kept for the backward: chunks
@@ -631,19 +627,17 @@ class _TeceFused(torch.autograd.Function):
             out, ctx.saved_chunk = _fused_chunk_fwd(P, x_lc, R, W, rs, rd, plan, node_map, True)
         else:
             Nn = plan.n_nodes
+            # every chunk's receiver sums straight into their rows of the output
             out = torch.empty(Nn, (L + 1) ** 2 * C, dtype=x_lc.dtype, device=x_lc.device)
-            full = _gm_blocks(out, Nn, L, C)
             keep = any(ctx.needs_input_grad[:3])
             ctx.saved_chunks = []
             for n0, n1, e0, e1 in chunks:
-                oc, saved = _fused_chunk_fwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
-                                             sub_plan(plan, n0, n1, e0, e1), None, keep)
+                _, saved = _fused_chunk_fwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1],
+                                            sub_plan(plan, n0, n1, e0, e1), node_map[n0:n1].contiguous(), keep,
+                                            out=out)
                 if saved is not None and _free_bytes(x_lc.device) < KEEP_RESERVE_BYTES:
                     saved, keep = None, False   # no room: this and later chunks are recomputed
                 ctx.saved_chunks.append(saved)
-                rows_c = node_map[n0:n1].long()
-                for l, blk in enumerate(_gm_blocks(oc, n1 - n0, L, C)):
-                    full[l].index_copy_(0, rows_c, blk)
             ctx.saved_chunk = None
         ctx.save_for_backward(x_lc, R, W, rs, rd, dst, node_map)
         return out
@@ -652,7 +646,6 @@ class _TeceFused(torch.autograd.Function):
     def backward(ctx, g_out):
         x_lc, R, W, rs, rd, dst, node_map = ctx.saved_tensors
         P, plan, chunks = ctx.P, ctx.plan, ctx.chunks
-        L, C = P.lmax, P.C
         g_out = g_out.contiguous()
         gx = torch.zeros_like(x_lc)
         if chunks is None:
@@ -661,13 +654,12 @@ class _TeceFused(torch.autograd.Function):
             ctx.saved_chunk = None
             return gx, gR, gW, None, None, None, None, None, None, None
         gR, gW = torch.empty_like(R), torch.empty_like(W)
-        full = _gm_blocks(g_out, plan.n_nodes, L, C)
         for i, (n0, n1, e0, e1) in enumerate(chunks):
-            rows_c = node_map[n0:n1].long()
-            g_c = torch.cat([f.index_select(0, rows_c).reshape(-1) for f in full]).view(n1 - n0, -1)
             saved, ctx.saved_chunks[i] = ctx.saved_chunks[i], None
+            # the output gradient of the chunk's receivers read in place
+            # (rows node_map[dst[e]] of the whole batch's)
             _fused_chunk_bwd(P, x_lc, R[e0:e1], W[e0:e1], rs[e0:e1], rd[e0:e1], sub_plan(plan, n0, n1, e0, e1),
-                             None, dst[e0:e1] - n0, node_map[n0:n1].contiguous(), saved, g_c, gx,
+                             node_map, dst[e0:e1], node_map[n0:n1].contiguous(), saved, g_out, gx,
                              gR_out=gR[e0:e1], gW_out=gW[e0:e1])
             del saved
         return gx, gR, gW, None, None, None, None, None, None, None

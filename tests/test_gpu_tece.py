@@ -662,14 +662,19 @@ def test_tece_bcc_fe_slice(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
-def test_tece_two_species_batch(cuda, dtype):
-    """Two graphs, two species (species-sorted rows, per-species resnet), C=32."""
+@pytest.mark.parametrize("frozen,chunk_edges", [(False, None), (True, 700)])
+def test_tece_two_species_batch(cuda, dtype, frozen, chunk_edges):
+    """Two graphs, two species (species-sorted rows, per-species resnet), C=32:
+    on the per-operator path, and on the fused operator in receiver chunks
+    whose sums go straight to (and whose output gradient is read from) the
+    feature rows of the whole batch, which are not in node order here."""
     a = structures.bcc_fe(reps=(2, 2, 3), seed=8)
     b = structures.bcc_fe(reps=(3, 2, 2), seed=9)
     nb = np.array(b["numbers"]).copy()
     nb[::3] = 28
     b = dict(b, numbers=nb)
-    got, want = _model_pair([a, b], cuda, dtype, seed=4, num_channel=32, edge_ace_hidden=16, num_head=2)
+    got, want = _model_pair([a, b], cuda, dtype, seed=4, num_channel=32, edge_ace_hidden=16, num_head=2,
+                            frozen=frozen, chunk_edges=chunk_edges)
     _check(got, want, dtype)
 
 

@@ -54,3 +54,23 @@ def test_so2_block_layout_round_trip():
         k = n - 1
         assert torch.equal(b[1][2 * 2].view(k, ch), x[2, n:n + k])
         assert torch.equal(b[1][2 * 2 + 1].view(k, ch), x[2, n + k:n + 2 * k])
+
+
+def test_group_by_key_is_a_stable_counting_sort():
+    """ops.group_by_key (the sender CSR of the grad_x sums) against a
+    brute-force grouping: per key, the positions holding it in increasing
+    order, and the key ranges; keys that never occur (empty ranges), all
+    positions on one key, no positions."""
+    g = torch.Generator().manual_seed(3)
+    cases = [(torch.randint(0, 40, (3000,), generator=g), 40), (torch.full((17,), 5, dtype=torch.int64), 9),
+             (torch.zeros(0, dtype=torch.int64), 4), (torch.randint(0, 3, (1,), generator=g), 3)]
+    for keys, n in cases:
+        rp, order = ops.group_by_key(keys, n)
+        assert rp.dtype == torch.int32 and order.dtype == torch.int32 and rp.shape == (n + 1,)
+        kl = keys.tolist()
+        want = [i for k in range(n) for i in range(len(kl)) if kl[i] == k]
+        assert order.tolist() == want
+        starts = [0]
+        for k in range(n):
+            starts.append(starts[-1] + kl.count(k))
+        assert rp.tolist() == starts

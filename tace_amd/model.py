@@ -855,23 +855,21 @@ class _SplitUpFn(torch.autograd.Function):
     def backward(ctx, g_node, g_base, g_ws):
         (u,) = ctx.saved_tensors
         mod = ctx.mod
-        Z, C, lay = u.shape[0], mod.C, mod._up_lay
+        C, lay = mod.C, mod._up_lay
         gu = torch.empty_like(u)
         g0 = lay.block(gu, 0)
         if g_ws is None:
             g0.zero_()
         else:
-            g0.copy_(torch.ops.aten.silu_backward(g_ws, lay.block(u, 0)))
-        off = 0
-        for b, (mul, ir) in enumerate(mod.double):
-            f = lay.block(gu, b + 1).view(Z, ir.dim, mul)
-            n = Z * ir.dim * C
-            for half, g in ((f[:, :, :C], g_node), (f[:, :, C:], g_base)):
-                if g is None:
-                    half.zero_()
-                else:
-                    half.copy_(g.reshape(-1)[off:off + n].view(Z, ir.dim, C))
-            off += n
+            torch.ops.aten.silu_backward.grad_input(g_ws.contiguous().view(g0.shape), lay.block(u, 0), grad_input=g0)
+        # the node and base halves of every doubled block in one strided copy each
+        dbl = mod._doubled_rows(gu)
+        R = dbl.shape[0]
+        for half, g in ((dbl[:, :C], g_node), (dbl[:, C:], g_base)):
+            if g is None:
+                half.zero_()
+            else:
+                half.copy_(g.reshape(-1)[:R * C].view(R, C))
         return gu, None
 
 
@@ -1035,15 +1033,27 @@ class CgtpACE(torch.nn.Module):
         return self._split_up_torch(u)
 
     def _split_up_torch(self, u):
+        """The doubled blocks follow the path weights in ``u`` and the node
+        blocks follow each other in the group-major output in the same order,
+        so every doubled block's rows [Z (2l+1), 2C] together are one [R, 2C]
+        matrix whose halves are the node and base features: one strided copy
+        each (and a block of ones after the base features)."""
         Z, C = u.shape[0], self.C
         ws = torch.nn.functional.silu(self._up_lay.block(u, 0))
-        node, base = [], []
-        for b, (mul, ir) in enumerate(self.double):
-            f = self._up_lay.block(u, b + 1).view(Z, ir.dim, mul)
-            node.append(f[:, :, :C].reshape(-1))
-            base.append(f[:, :, C:].reshape(-1))
-        base.append(u.new_ones(Z * C))
-        return torch.cat(node).view(Z, -1), torch.cat(base).view(Z, -1), ws
+        dbl = self._doubled_rows(u)
+        node = dbl[:, :C].contiguous().view(Z, -1)
+        R = dbl.shape[0]
+        base = u.new_empty(Z, (R // Z + 1) * C)
+        bf = base.view(-1)
+        bf[:R * C].view(R, C).copy_(dbl[:, C:])
+        bf[R * C:].fill_(1.0)
+        return node, base, ws
+
+    def _doubled_rows(self, u):
+        """All doubled blocks of ``linear_up``'s output as one [Z sum(2l+1), 2C] view."""
+        Z, C = u.shape[0], self.C
+        s0 = self._up_lay.blocks[1][0]
+        return u.view(-1)[Z * s0:].view(-1, 2 * C)
 
     def forward(self, x, sp: SpeciesPlan, sc):
         """x: group-major node features in species-sorted row order."""

@@ -96,8 +96,36 @@ class SpeciesPlan:
         """R's rows of the edge pairs' lower edges (the radial MLP's input),
         gathered once per forward for all interaction layers."""
         if self._pair_radial is None or self._pair_radial[0] is not R:
-            self._pair_radial = (R, R.index_select(0, self.pairs.row_edges))
+            if ops.MODE.double or ops.MODE.export or not _RowGatherFn.fits(R):
+                rows = R.index_select(0, self.pairs.row_edges)
+            else:
+                rows = _RowGatherFn.apply(R, self.pairs.row_edges)
+            self._pair_radial = (R, rows)
         return self._pair_radial[1]
+
+
+class _RowGatherFn(torch.autograd.Function):
+    """R[rows] for distinct rows, moved as 16-byte elements (a row of 8
+    float32 is two of them instead of eight 4-byte gathers); the backward
+    writes each row's gradient back to its row (distinct rows: no sums) and
+    zeros elsewhere."""
+
+    @staticmethod
+    def fits(R: torch.Tensor) -> bool:
+        return R.dim() == 2 and R.is_contiguous() and (R.shape[1] * R.element_size()) % 16 == 0
+
+    @staticmethod
+    def forward(ctx, R, rows):
+        ctx.save_for_backward(rows)
+        ctx.shape = R.shape
+        return R.view(torch.complex128).index_select(0, rows).view(R.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        (rows,) = ctx.saved_tensors
+        gR = g.new_zeros(ctx.shape)
+        gR.view(torch.complex128).index_copy_(0, rows.long(), g.contiguous().view(torch.complex128))
+        return gR, None
 
 
 # ------------------------------------------------------------ feature layout ----
@@ -657,9 +685,12 @@ class _GateFn(torch.autograd.Function):
             go = lout.block(gout, k).view(Z, -1, C)
             gk = g[:, k * C:(k + 1) * C]
             torch.mul(go, gk.unsqueeze(1), out=dsts[k])
-            torch.sum(go * srcs[k], dim=1, out=gg[:, k * C:(k + 1) * C])
-        # d/dz [CST * sigmoid(z)] = g * (1 - g / CST)
-        X0g[:, :ng * C] = gg * g * (1.0 - g / SIGMOID_CST)
+            if go.shape[1] == 1:
+                torch.mul(go[:, 0], srcs[k][:, 0], out=gg[:, k * C:(k + 1) * C])
+            else:
+                torch.sum(go * srcs[k], dim=1, out=gg[:, k * C:(k + 1) * C])
+        # d/dz [CST * sigmoid(z)] = g * (1 - g / CST) = g - g^2 / CST
+        torch.mul(gg, torch.addcmul(g, g, g, value=-1.0 / SIGMOID_CST), out=X0g[:, :ng * C])
         return gx, None, None, None
 
 

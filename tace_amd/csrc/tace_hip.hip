@@ -197,6 +197,32 @@ __global__ __launch_bounds__(256) void k_sum_parts(const T* __restrict__ parts, 
   out[i] = accumulate ? out[i] + acc : acc;
 }
 
+// the same, four float32 per thread (n % 4 == 0, 16-byte aligned arrays):
+// the same sums in the same order, a quarter of the memory instructions
+typedef float sp_f4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void k_sum_parts4(const float* __restrict__ parts, int nparts, int64_t n,
+                                                    float* __restrict__ out, int accumulate) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  sp_f4 acc = *(const sp_f4*)(parts + i);
+  for (int q = 1; q < nparts; ++q) acc += *(const sp_f4*)(parts + (size_t)q * n + i);
+  if (accumulate) acc = *(const sp_f4*)(out + i) + acc;
+  *(sp_f4*)(out + i) = acc;
+}
+
+// k_sum_parts for float32, on four elements per thread where the sizes and
+// alignment allow
+static void sum_parts_f32(const float* parts, int nparts, int64_t n, float* out, int accumulate, hipStream_t s) {
+  if (n <= 0) return;
+  if ((n & 3) == 0 && ((((uintptr_t)parts) | ((uintptr_t)out)) & 15) == 0) {
+    hipLaunchKernelGGL(k_sum_parts4, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, parts, nparts, n, out,
+                       accumulate);
+  } else {
+    hipLaunchKernelGGL(k_sum_parts<float>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, parts, nparts, n,
+                       out, accumulate);
+  }
+}
+
 // ------------------------------------------------------------ edge vectors --
 // vec[e] = pos[dst] - pos[src] + S[e] . lat[eb[e]]   (adapter.py:334-340)
 template <typename T>
@@ -977,7 +1003,7 @@ int tace_edge_tp_bwd_rows(int vid, int dtype, const void* x, const void* y, cons
             channels, s);
     if (phase) hipEventRecord(phase, s);
     if (np > 1 && ny)
-      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)gyp, np, ny, (float*)gy);
+      sum_parts_f32((const float*)gyp, np, ny, (float*)gy, 0, s);
     if (gx && n_nodes)
       launch_seg_rowsum<float>((const float*)cbuf, s_rowptr, s_slot, node_map, (float*)gx, (int)n_nodes, row, sg,
                                channels, s);
@@ -1167,8 +1193,7 @@ int tace_edge_rtp_bwd(int vid, const float* x, const float* y, const float* h, c
   v.rbwd(x, y, h, w_last, alpha, gout, rowptr, eid, src, node_map, slot_rows, cbuf, gyp, gw, (int)n_nodes,
          (int)n_edges, layout, channels, rtp_per_range(n_nodes, nph), s);
   if (nph > 1 && ny)
-    hipLaunchKernelGGL(k_sum_parts<float>, dim3((unsigned)((ny + 255) / 256)), dim3(256), 0, s, (const float*)gyp,
-                       nph, ny, gy);
+    sum_parts_f32((const float*)gyp, nph, ny, gy, 0, s);
   if (gx && n_nodes)
     launch_seg_rowsum<float>(cbuf, s_rowptr, s_slot, node_map, gx, (int)n_nodes, row, sg, channels, s);
   return check_launch("tace_edge_rtp_bwd");
@@ -1257,10 +1282,9 @@ int tace_uuu_bwd(int vid, int dtype, const void* x1, const void* x2, const void*
     void* g2p = ws2 ? workspace : g2;
     v.ubwd_f(x1, x2, w, gout, g1k, g2p, w ? gw : nullptr, (int)n_nodes, channels, layout, s);
     if (acc1 && n1)
-      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb1), dim3(256), 0, s, (const float*)g1k, 1, n1, (float*)g1, 1);
+      sum_parts_f32((const float*)g1k, 1, n1, (float*)g1, 1, s);
     if (ws2 && ny)
-      hipLaunchKernelGGL(k_sum_parts<float>, dim3(nb), dim3(256), 0, s, (const float*)g2p, v.unparts, ny, (float*)g2,
-                         acc2);
+      sum_parts_f32((const float*)g2p, v.unparts, ny, (float*)g2, acc2, s);
   } else if (dtype == TACE_F64) {
     double* wsd = (double*)workspace;
     void* g1k = acc1 ? (void*)(wsd + off1) : g1;

@@ -208,6 +208,51 @@ def test_rotate_out_matches_oracle(cuda, dtype, lmax, H, C):
     _check_block_grad(gW, gW_o, lmax, dtype)
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+@pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (1, 2, 32)])
+def test_rotate_out_receiver_chunks_into_batch_rows(cuda, dtype, lmax, H, C):
+    """Receiver chunks of one rotate-out: each chunk's forward writes its
+    receivers' sums straight into the whole batch's output (out_rows, rows
+    node_map[n]) and its backward reads the whole batch's g_out at rows
+    node_map[dst[e]]; together they give the bits of one call over the batch
+    (the same per-receiver and per-edge arithmetic), receivers without edges
+    included."""
+    g = torch.Generator().manual_seed(lmax * 7 + H + C)
+    N, E = 90, 1200
+    K = (lmax + 1) ** 2
+    ei = _random_graph(N, E, g)
+    ei = ei[:, torch.argsort(ei[1], stable=True)]   # receiver-grouped edges, as the chunks need
+    plan = ops.EdgePlan.from_edge_index(ei.to(cuda), N)
+    node_map = torch.randperm(N, generator=g).to(torch.int32).to(cuda)
+    W, _ = ot.edge_wigner(_vectors(E - 10, g), lmax, lmax)
+    W = W.to(dtype).to(cuda)
+    m = [t.to(dtype).to(cuda) for t in ops.so2_to_blocks(torch.randn(E, K, C, generator=g, dtype=torch.float64),
+                                                         lmax)]
+    al = torch.rand(E, H, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    go = torch.randn(N, K * C, generator=g, dtype=torch.float64).to(dtype).to(cuda)
+    dst = ei[1].to(cuda)
+    whole = ops.launch_rotate_out_fwd(m, al, W, plan, node_map, lmax, H)
+    gm, ga, gW = ops.launch_rotate_out_bwd(m, al, W, go, dst, node_map, plan, lmax, H)
+    rp = plan.rowptr.cpu().tolist()
+    out = torch.full_like(whole, float("nan"))
+    for n0, n1 in ((0, 31), (31, 32), (32, 77), (77, N)):
+        e0, e1 = rp[n0], rp[n1]
+        sub = pt.sub_plan(plan, n0, n1, e0, e1)
+        mc = [t[e0:e1] if i == 0 else t.view(E, 2, -1)[e0:e1].reshape(2 * (e1 - e0), -1)
+              for i, t in enumerate(m)]
+        ops.launch_rotate_out_fwd(mc, al[e0:e1].contiguous(), W[e0:e1].contiguous(), sub,
+                                  node_map[n0:n1].contiguous(), lmax, H, out=out)
+        c = ops.launch_rotate_out_bwd(mc, al[e0:e1].contiguous(), W[e0:e1].contiguous(), go, dst[e0:e1].contiguous(),
+                                      node_map, sub, lmax, H, g_rows=N)
+        for i, (a, b) in enumerate(zip(c[0], gm)):
+            want = b[e0:e1] if i == 0 else b.view(E, 2, -1)[e0:e1].reshape(2 * (e1 - e0), -1)
+            assert torch.equal(a, want), ("g_m", i, n0)
+        assert torch.equal(c[1], ga[e0:e1]) and torch.equal(c[2], gW[e0:e1]), n0
+    assert torch.equal(out, whole)
+    with pytest.raises(ValueError, match="node_map"):
+        ops.launch_rotate_out_fwd(m, al, W, plan, None, lmax, H, out=out)
+
+
 @pytest.mark.parametrize("bf16_out", [False, True])
 @pytest.mark.parametrize("lmax,H,C", [(2, 4, 128), (1, 2, 64), (2, 1, 256), (2, 8, 64), (1, 3, 96)])
 def test_rotate_out_bwd_channel_pairs_equal_one_channel_kernel(cuda, bf16_out, lmax, H, C):

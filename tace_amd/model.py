@@ -112,7 +112,8 @@ class _RowGatherFn(torch.autograd.Function):
 
     @staticmethod
     def fits(R: torch.Tensor) -> bool:
-        return R.dim() == 2 and R.is_contiguous() and (R.shape[1] * R.element_size()) % 16 == 0
+        return (R.dim() == 2 and R.is_contiguous() and (R.shape[1] * R.element_size()) % 16 == 0
+                and (R.storage_offset() * R.element_size()) % 16 == 0)
 
     @staticmethod
     def forward(ctx, R, rows):

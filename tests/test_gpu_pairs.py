@@ -25,12 +25,14 @@ def _nl(s, rc, cuda):
     return ops.EdgePlan(len(s["positions"]), E, rowptr, src, None), sh
 
 
-@pytest.mark.parametrize("which", ["si", "water", "tiny_cell"])
+@pytest.mark.parametrize("which", ["si", "water", "dense", "tiny_cell"])
 def test_pairs_match_the_edge_set(cuda, which):
     if which == "si":
         s, rc = structures.si_diamond(seed=3), 5.0
     elif which == "water":
         s, rc = structures.water_box(n_side=4, box=49.7 / 16 * 4, seed=5), 6.0
+    elif which == "dense":   # ~250 edges per receiver: several 64-edge runs, several 128-candidate rounds
+        s, rc = structures.water_box(n_side=4, box=49.7 / 16 * 4, seed=6), 8.5
     else:   # self-images: edges i -> i with S != 0
         s, rc = structures.bcc_fe(reps=(1, 1, 1), seed=2), 5.0
     plan, sh = _nl(s, rc, cuda)

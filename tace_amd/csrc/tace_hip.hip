@@ -596,23 +596,6 @@ __global__ void k_nl_scatter(const int* __restrict__ abin, int n, const int* __r
   batoms[bstart[b] + slot] = i;
 }
 
-// deterministic order inside each bin: insertion sort of atom ids
-__global__ void k_nl_sortbins(const int* __restrict__ bstart, int nbins, int* __restrict__ batoms) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nbins) return;
-  const int s = bstart[b], e = bstart[b + 1];
-  for (int i = s + 1; i < e; ++i) {
-    const int v = batoms[i];
-    int j = i - 1;
-    while (j >= s && batoms[j] > v) {
-      batoms[j + 1] = batoms[j];
-      --j;
-    }
-    batoms[j + 1] = v;
-  }
-}
-
-
 // ------------------------------------------------- batched neighbours --
 // Many structures in one pass.  The host-built plan table holds per structure
 // its NlGeom, then struct_ptr[ns+1] (first atom of each structure) and
@@ -665,8 +648,8 @@ __global__ void k_nlb_bin(const double* __restrict__ pos, int n, NlBatch B, int*
 
 // Deterministic bin contents without a sort: atom i goes to the slot of its
 // rank (by id) among the atoms k_nl_scatter put into its bin in arbitrary
-// order -- batoms ends up ascending in every bin, as k_nl_sortbins leaves it,
-// with a thread per atom instead of a serial sort per bin.
+// order -- batoms ends up ascending in every bin, with a thread per atom
+// instead of a serial sort per bin (single structures and batches alike).
 __global__ void k_nlb_rank(const int* __restrict__ abin, int n, const int* __restrict__ bstart,
                            const int* __restrict__ unsorted, int* __restrict__ batoms) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1373,8 +1356,9 @@ int64_t tace_nl_workspace_bytes(int64_t n_atoms, const double* cell, const int32
   if (!cell || !pbc) return fail("tace_nl_workspace_bytes: null pointer");
   if (nl_geometry(cell, pbc, cutoff, &g)) return -1;
   const int64_t nbins = (int64_t)g.nb[0] * g.nb[1] * g.nb[2];
-  // abin[n], aimg[3n], bcount[nbins], bstart[nbins+1], bfill[nbins], batoms[n]
-  return (int64_t)sizeof(int32_t) * (n_atoms * 5 + nbins * 3 + 1);
+  // abin[n], aimg[3n], bcount[nbins], bstart[nbins+1], bfill[nbins], batoms[n],
+  // unsorted[n] (the bin contents before the ranking; tace_nl_count only)
+  return (int64_t)sizeof(int32_t) * (n_atoms * 6 + nbins * 3 + 1);
 }
 
 int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const int32_t* pbc, double cutoff,
@@ -1386,7 +1370,7 @@ int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const 
   if (n_atoms == 0) return 0;
   if (!pos || !workspace || !counts) return fail("tace_nl_count: null pointer");
   const int64_t nbins = (int64_t)g.nb[0] * g.nb[1] * g.nb[2];
-  if (workspace_bytes < (int64_t)sizeof(int32_t) * (n_atoms * 5 + nbins * 3 + 1))
+  if (workspace_bytes < (int64_t)sizeof(int32_t) * (n_atoms * 6 + nbins * 3 + 1))
     return fail("tace_nl_count: workspace too small");
   hipStream_t s = (hipStream_t)stream;
   const int n = (int)n_atoms;
@@ -1396,13 +1380,14 @@ int tace_nl_count(const double* pos, int64_t n_atoms, const double* cell, const 
   int* bstart = bcount + nbins;
   int* bfill = bstart + nbins + 1;
   int* batoms = bfill + nbins;
+  int* unsorted = batoms + n;
   launch_fill<int>(bcount, (size_t)nbins, 0, s);
   launch_fill<int>(bfill, (size_t)nbins, 0, s);
   const dim3 ga((n + 255) / 256), ba(256);
   hipLaunchKernelGGL(k_nl_bin, ga, ba, 0, s, pos, n, g, abin, aimg, bcount);
   hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bcount, (int)nbins, bstart);
-  hipLaunchKernelGGL(k_nl_scatter, ga, ba, 0, s, abin, n, bstart, bfill, batoms);
-  hipLaunchKernelGGL(k_nl_sortbins, dim3((unsigned)((nbins + 255) / 256)), dim3(256), 0, s, bstart, (int)nbins, batoms);
+  hipLaunchKernelGGL(k_nl_scatter, ga, ba, 0, s, abin, n, bstart, bfill, unsorted);
+  hipLaunchKernelGGL(k_nlb_rank, ga, ba, 0, s, abin, n, bstart, unsorted, batoms);
   if (n < NL_WAVE_MAX)
     hipLaunchKernelGGL((k_nl_edges<false, true>), dim3((n + 3) / 4), dim3(256), 0, s, pos, n, g, abin, aimg, bstart,
                        batoms, counts, nullptr, nullptr, nullptr);
